@@ -1,0 +1,470 @@
+"""TEST INFRASTRUCTURE ONLY -- CPU oracle driver.
+
+Only tests/, ``__graft_entry__.smoke()`` and bench.py's ``cpu_baseline`` leg
+may import this module, and only as the checker (or the timed CPU baseline).
+The product never imports it.
+
+Contents:
+
+* ``neighbor_graph``: the C restatement of the reference's periodic
+  neighbour graph (``neighbor_oracle.c``).
+* ``compact_radial_tables``: numpy restatement of the compact radial model's
+  tabulation (``libsymmetrix/source/compact_radial.cpp``):
+  Bessel features with polynomial cutoff ``:227-267``, SiLU MLP
+  ``multilayer_perceptron.cpp:78-140``, knot derivatives ``:326-370``.
+* ``MaceOracle``: the C++ restatement of ``MACECPU`` (``mace_oracle.cpp``)
+  built from a model JSON dict, in float32 or float64.
+* ``reduce``: atom forces and stress from directed edge forces
+  (``mace_kokkos_evaluate.cpp:87-106, 156-186``), and the Voigt order of
+  ``calculator.py:3821-3894``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = None
+
+
+def build() -> str:
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return os.path.join(_HERE, "liboracle.so")
+
+
+def _lib():
+    global _LIB
+    if _LIB is None:
+        path = os.path.join(_HERE, "liboracle.so")
+        if not os.path.exists(path):
+            build()
+        lib = ctypes.CDLL(path)
+        lib.oracle_neighbor_last_error.restype = ctypes.c_char_p
+        lib.oracle_mace_last_error.restype = ctypes.c_char_p
+        for name in ("oracle_mace_create_f32", "oracle_mace_create_f64"):
+            getattr(lib, name).restype = ctypes.c_void_p
+            getattr(lib, name).argtypes = [ctypes.c_void_p]
+        for name in ("oracle_mace_destroy_f32", "oracle_mace_destroy_f64"):
+            getattr(lib, name).argtypes = [ctypes.c_void_p]
+        _LIB = lib
+    return _LIB
+
+
+def _ptr(a, ctype):
+    return a.ctypes.data_as(ctypes.POINTER(ctype))
+
+
+# ---------------------------------------------------------------------------
+# neighbour graph
+# ---------------------------------------------------------------------------
+
+
+def neighbor_graph(positions, cell, inverse_cell, cutoff):
+    """Receiver-major periodic neighbour graph in the reference's edge order.
+
+    Returns dict(num_neigh, receiver_offsets, sources, shifts, fractional_xyz).
+    Raises ValueError for inputs the reference rejects.
+    """
+    lib = _lib()
+    pos = np.ascontiguousarray(positions, dtype=np.float64).reshape(-1, 3)
+    c = np.ascontiguousarray(cell, dtype=np.float64).reshape(9)
+    ic = np.ascontiguousarray(inverse_cell, dtype=np.float64).reshape(9)
+    n = pos.shape[0]
+    num_neigh = np.zeros(n, dtype=np.int32)
+    offsets = np.zeros(n + 1, dtype=np.int32)
+    total = ctypes.c_longlong(0)
+    status = lib.oracle_neighbor_count(
+        _ptr(pos, ctypes.c_double), ctypes.c_int(n), _ptr(c, ctypes.c_double),
+        _ptr(ic, ctypes.c_double), ctypes.c_double(cutoff), _ptr(num_neigh, ctypes.c_int),
+        _ptr(offsets, ctypes.c_int), ctypes.byref(total))
+    if status != 0:
+        raise ValueError(lib.oracle_neighbor_last_error().decode())
+    e = total.value
+    sources = np.zeros(e, dtype=np.int32)
+    shifts = np.zeros((e, 3), dtype=np.int32)
+    frac = np.zeros((e, 3), dtype=np.float64)
+    status = lib.oracle_neighbor_fill(
+        _ptr(pos, ctypes.c_double), ctypes.c_int(n), _ptr(c, ctypes.c_double),
+        _ptr(ic, ctypes.c_double), ctypes.c_double(cutoff), _ptr(offsets, ctypes.c_int),
+        _ptr(sources, ctypes.c_int), _ptr(shifts, ctypes.c_int), _ptr(frac, ctypes.c_double))
+    if status != 0:
+        raise ValueError(lib.oracle_neighbor_last_error().decode())
+    return {
+        "num_neigh": num_neigh,
+        "receiver_offsets": offsets,
+        "sources": sources,
+        "shifts": shifts,
+        "fractional_xyz": frac,
+    }
+
+
+# ---------------------------------------------------------------------------
+# compact radial tabulation
+# ---------------------------------------------------------------------------
+
+
+def _silu_mlp(features, weights, scale, penultimate=False):
+    x = features
+    for w in weights[:-1]:
+        z = x @ w.T
+        x = scale * z / (1.0 + np.exp(-z))
+    if penultimate:
+        return x
+    return x @ weights[-1].T
+
+
+def spline_derivatives(values, h):
+    """Knot derivatives by the reference's tridiagonal rule
+    (compact_radial.cpp:326-370): not-a-knot-like left end, zero derivative at
+    the right end."""
+    values = np.asarray(values, dtype=np.float64)
+    n = values.shape[-1]
+    unknowns = n - 2
+    out = np.zeros_like(values)
+    flat = values.reshape(-1, n)
+    res = out.reshape(-1, n)
+    for f in range(flat.shape[0]):
+        v = flat[f]
+        lower = np.zeros(unknowns)
+        diag = np.full(unknowns, 4.0)
+        upper = np.zeros(unknowns)
+        rhs = np.zeros(unknowns)
+        left = 2.0 * (-v[0] + 2.0 * v[1] - v[2]) / h
+        upper[0] = 2.0
+        rhs[0] = 3.0 * (v[2] - v[0]) / h - left
+        for node in range(2, n - 1):
+            row = node - 1
+            lower[row] = 1.0
+            if node + 1 <= n - 2:
+                upper[row] = 1.0
+            rhs[row] = 3.0 * (v[node + 1] - v[node - 1]) / h
+        for row in range(1, unknowns):
+            factor = lower[row] / diag[row - 1]
+            diag[row] -= factor * upper[row - 1]
+            rhs[row] -= factor * rhs[row - 1]
+        sol = np.zeros(unknowns)
+        sol[-1] = rhs[-1] / diag[-1]
+        for row in range(unknowns - 2, -1, -1):
+            sol[row] = (rhs[row] - upper[row] * sol[row + 1]) / diag[row]
+        d = np.zeros(n)
+        d[1 : n - 1] = sol
+        d[0] = d[2] + left
+        d[-1] = 0.0
+        res[f] = d
+    return out
+
+
+def spline_derivatives_fast(values, h):
+    """Vectorised form of ``spline_derivatives`` over many functions (same
+    elimination, same operation order per function)."""
+    v = np.asarray(values, dtype=np.float64)
+    n = v.shape[-1]
+    u = n - 2
+    left = 2.0 * (-v[..., 0] + 2.0 * v[..., 1] - v[..., 2]) / h
+    diag = np.full(u, 4.0)
+    upper = np.zeros(u)
+    lower = np.zeros(u)
+    upper[0] = 2.0
+    for node in range(2, n - 1):
+        row = node - 1
+        lower[row] = 1.0
+        if node + 1 <= n - 2:
+            upper[row] = 1.0
+    rhs = np.empty(v.shape[:-1] + (u,))
+    rhs[..., 0] = 3.0 * (v[..., 2] - v[..., 0]) / h - left
+    for node in range(2, n - 1):
+        rhs[..., node - 1] = 3.0 * (v[..., node + 1] - v[..., node - 1]) / h
+    for row in range(1, u):
+        factor = lower[row] / diag[row - 1]
+        diag[row] -= factor * upper[row - 1]
+        rhs[..., row] -= factor * rhs[..., row - 1]
+    sol = np.empty_like(rhs)
+    sol[..., -1] = rhs[..., -1] / diag[-1]
+    for row in range(u - 2, -1, -1):
+        sol[..., row] = (rhs[..., row] - upper[row] * sol[..., row + 1]) / diag[row]
+    d = np.zeros_like(v)
+    d[..., 1 : n - 1] = sol
+    d[..., 0] = d[..., 2] + left
+    d[..., -1] = 0.0
+    return d
+
+
+def compact_radial_grid(model):
+    cr = model["compact_radial"]
+    grid_min = float(cr["spline_grid_min"])
+    points = int(cr["num_spline_points"])
+    h = (float(model["r_cut"]) - grid_min) / (points - 1)
+    return grid_min, h, points
+
+
+def radial_features(model, type_i, type_j):
+    """Bessel x polynomial-cutoff features on the spline knots
+    (compact_radial.cpp:227-267), shape (knots, num_bessel)."""
+    cr = model["compact_radial"]
+    grid_min, h, points = compact_radial_grid(model)
+    w = np.asarray(cr["basis"]["weights"], dtype=np.float64)
+    pref = float(cr["basis"]["prefactor"])
+    rmax = float(cr["cutoff"]["r_max"])
+    p = int(cr["cutoff"]["p"])
+    if cr["distance_transform"]["type"] != "none":
+        raise NotImplementedError("only distance_transform 'none' is restated")
+    r = grid_min + np.arange(points) * h
+    scaled = r / rmax
+    cut = np.where(
+        r < rmax,
+        1.0
+        - ((p + 1.0) * (p + 2.0) / 2.0) * scaled**p
+        + p * (p + 2.0) * scaled ** (p + 1)
+        - (p * (p + 1.0) / 2.0) * scaled ** (p + 2),
+        0.0,
+    )
+    return pref * np.sin(w[None, :] * r[:, None]) / r[:, None] * cut[:, None]
+
+
+def _network(model, name):
+    net = model["compact_radial"]["networks"][name]
+    shape = net["shape"]
+    weights = [
+        np.asarray(w, dtype=np.float64).reshape(shape[i + 1], shape[i])
+        for i, w in enumerate(net["weights"])
+    ]
+    return weights, float(net["activation_scale"])
+
+
+def compact_radial_tables(model, type_i, type_j, name):
+    """Nodal values and derivatives (functions, knots) of network ``name`` for
+    the unordered pair (type_i, type_j)."""
+    _, h, _ = compact_radial_grid(model)
+    feats = radial_features(model, type_i, type_j)
+    weights, scale = _network(model, name)
+    values = _silu_mlp(feats, weights, scale).T.copy()  # (functions, knots)
+    return values, spline_derivatives_fast(values, h)
+
+
+# ---------------------------------------------------------------------------
+# MACE oracle
+# ---------------------------------------------------------------------------
+
+
+class _Spec(ctypes.Structure):
+    _fields_ = [
+        ("num_elements", ctypes.c_int), ("channels", ctypes.c_int), ("l_max", ctypes.c_int),
+        ("L_max", ctypes.c_int), ("r_cut", ctypes.c_double), ("num_active", ctypes.c_int),
+        ("type_to_active", ctypes.c_void_p), ("spline_nodes", ctypes.c_int),
+        ("spline_h", ctypes.c_double), ("spline_x0", ctypes.c_double),
+        ("r0_values", ctypes.c_void_p), ("r0_derivs", ctypes.c_void_p),
+        ("r1_values", ctypes.c_void_p), ("r1_derivs", ctypes.c_void_p),
+        ("H0", ctypes.c_void_p), ("A0W", ctypes.c_void_p), ("m0_offsets", ctypes.c_void_p),
+        ("m0_degree", ctypes.c_void_p), ("m0_index", ctypes.c_void_p),
+        ("m0_coef", ctypes.c_void_p), ("H1W", ctypes.c_void_p), ("num_paths", ctypes.c_int),
+        ("num_terms", ctypes.c_int), ("path_l", ctypes.c_void_p), ("path_l1", ctypes.c_void_p),
+        ("path_l2", ctypes.c_void_p), ("term_lme", ctypes.c_void_p),
+        ("term_row", ctypes.c_void_p), ("term_cg", ctypes.c_void_p), ("A1W", ctypes.c_void_p),
+        ("m1_terms", ctypes.c_int), ("m1_degree", ctypes.c_void_p),
+        ("m1_index", ctypes.c_void_p), ("m1_coef", ctypes.c_void_p), ("H2M0", ctypes.c_void_p),
+        ("H2M1", ctypes.c_void_p), ("readout_q", ctypes.c_void_p),
+        ("readout_hidden", ctypes.c_int), ("readout_w1", ctypes.c_void_p),
+        ("readout_w2", ctypes.c_void_p), ("readout_scale", ctypes.c_double),
+        ("atomic_energies", ctypes.c_void_p),
+    ]
+
+
+def _monomial_arrays(monomial_lists):
+    deg, idx = [], []
+    for m in monomial_lists:
+        if not 1 <= len(m) <= 3:
+            raise NotImplementedError("oracle restates polynomials of degree 1..3")
+        deg.append(len(m))
+        idx.append(list(m) + [0] * (3 - len(m)))
+    return np.asarray(deg, dtype=np.int32), np.asarray(idx, dtype=np.int32).reshape(-1, 3)
+
+
+class MaceOracle:
+    """CPU restatement of MACECPU for one model and a set of active types."""
+
+    def __init__(self, model: dict, active_types, precision="float32"):
+        if model.get("symmetrix_format_version") != 4 or model.get("h1_affine_mode") != "m0_composite":
+            raise NotImplementedError("the oracle restates format 4 / m0_composite models")
+        if model.get("has_zbl") or model.get("A0_scaled") or model.get("A1_scaled"):
+            raise NotImplementedError("ZBL and A0/A1 scaling are not restated")
+        self.precision = precision
+        self.model = model
+        ne = int(model["num_elements"])
+        C = int(model["num_channels"])
+        lmax, Lmax = int(model["l_max"]), int(model["L_max"])
+        nlm, nLM = (lmax + 1) ** 2, (Lmax + 1) ** 2
+        self.C, self.lmax, self.Lmax = C, lmax, Lmax
+        active = sorted(set(int(t) for t in active_types))
+        self.active = active
+        t2a = np.full(ne, -1, dtype=np.int32)
+        for a, t in enumerate(active):
+            t2a[t] = a
+        grid_min, h, points = compact_radial_grid(model)
+        r0v, r0d, r1v, r1d = [], [], [], []
+        for ai in range(len(active)):
+            for aj in range(ai, len(active)):
+                v, d = compact_radial_tables(model, active[ai], active[aj], "R0")
+                r0v.append(v)
+                r0d.append(d)
+                v, d = compact_radial_tables(model, active[ai], active[aj], "R1")
+                r1v.append(v)
+                r1d.append(d)
+        keep = {}
+
+        def arr(a, dtype=np.float64):
+            a = np.ascontiguousarray(a, dtype=dtype)
+            keep[id(a)] = a
+            return a.ctypes.data
+
+        m0_lists, m0_coef_blocks, m0_off = [], [], [0]
+        for LM in range(nLM):
+            monos = model["M0_monomials"][str(LM)]
+            m0_lists.extend(monos)
+            m0_off.append(m0_off[-1] + len(monos))
+        m0_deg, m0_idx = _monomial_arrays(m0_lists)
+        m0_coef = np.zeros((ne, C, m0_off[-1]))
+        for a in range(ne):
+            wa = model["M0_weights"][str(a)]
+            for LM in range(nLM):
+                block = np.asarray([wa[str(LM)][str(k)] for k in range(C)], dtype=np.float64)
+                m0_coef[a, :, m0_off[LM] : m0_off[LM + 1]] = block
+        m1_deg, m1_idx = _monomial_arrays(model["M1_monomials"])
+        m1_coef = np.asarray(
+            [[model["M1_weights"][str(a)][str(k)] for k in range(C)] for a in range(ne)],
+            dtype=np.float64,
+        )
+        a1 = [np.ascontiguousarray(w, dtype=np.float64) for w in model["A1_weights"]]
+        self._a1 = a1
+        a1_ptrs = (ctypes.c_void_p * len(a1))(*[w.ctypes.data for w in a1])
+        self._a1_ptrs = a1_ptrs
+        spec = _Spec(
+            num_elements=ne, channels=C, l_max=lmax, L_max=Lmax, r_cut=float(model["r_cut"]),
+            num_active=len(active), type_to_active=arr(t2a, np.int32), spline_nodes=points,
+            spline_h=h, spline_x0=grid_min, r0_values=arr(np.stack(r0v)),
+            r0_derivs=arr(np.stack(r0d)), r1_values=arr(np.stack(r1v)),
+            r1_derivs=arr(np.stack(r1d)), H0=arr(model["H0_weights"]),
+            A0W=arr(np.asarray(model["A0_weights"], dtype=np.float64)),
+            m0_offsets=arr(m0_off, np.int32), m0_degree=arr(m0_deg, np.int32),
+            m0_index=arr(m0_idx, np.int32), m0_coef=arr(m0_coef), H1W=arr(model["H1_weights"]),
+            num_paths=len(model["Phi1_l"]), num_terms=len(model["Phi1_lme"]),
+            path_l=arr(model["Phi1_l"], np.int32), path_l1=arr(model["Phi1_l1"], np.int32),
+            path_l2=arr(model["Phi1_l2"], np.int32), term_lme=arr(model["Phi1_lme"], np.int32),
+            term_row=arr(model["Phi1_lelm1lm2"], np.int32),
+            term_cg=arr(model["Phi1_clebsch_gordan"]),
+            A1W=ctypes.cast(a1_ptrs, ctypes.c_void_p).value, m1_terms=len(m1_deg),
+            m1_degree=arr(m1_deg, np.int32), m1_index=arr(m1_idx, np.int32),
+            m1_coef=arr(m1_coef), H2M0=arr(np.asarray(model["H2_weights_for_M0"])),
+            H2M1=arr(model["H2_weights_for_M1"]), readout_q=arr(model["readout_1_weights_for_M0"]),
+            readout_hidden=int(model.get("readout_2_hidden_size", 16)),
+            readout_w1=arr(model["readout_2_weights_1"]),
+            readout_w2=arr(model["readout_2_weights_2"]),
+            readout_scale=float(model["readout_2_scale_factor"]),
+            atomic_energies=arr(model["atomic_energies"]),
+        )
+        lib = _lib()
+        suffix = "f32" if precision == "float32" else "f64"
+        self._destroy = getattr(lib, f"oracle_mace_destroy_{suffix}")
+        self._compute = getattr(lib, f"oracle_mace_compute_{suffix}")
+        handle = getattr(lib, f"oracle_mace_create_{suffix}")(ctypes.byref(spec))
+        del keep
+        if not handle:
+            raise ValueError(lib.oracle_mace_last_error().decode())
+        self._handle = handle
+
+    def __del__(self):
+        if getattr(self, "_handle", None):
+            self._destroy(self._handle)
+            self._handle = None
+
+    def compute(self, node_types, num_neigh, neigh_indices, neigh_types, xyz, r, num_threads=0):
+        """Node energies (N,) and directed edge forces (E, 3), both float64."""
+        types = np.ascontiguousarray(node_types, dtype=np.int32)
+        nn = np.ascontiguousarray(num_neigh, dtype=np.int32)
+        idx = np.ascontiguousarray(neigh_indices, dtype=np.int32)
+        nt = np.ascontiguousarray(neigh_types, dtype=np.int32)
+        xyz = np.ascontiguousarray(xyz, dtype=np.float64).reshape(-1, 3)
+        r = np.ascontiguousarray(r, dtype=np.float64)
+        n = len(types)
+        energies = np.zeros(n)
+        forces = np.zeros((len(r), 3))
+        status = self._compute(
+            ctypes.c_void_p(self._handle), ctypes.c_int(n), _ptr(types, ctypes.c_int),
+            _ptr(nn, ctypes.c_int), _ptr(idx, ctypes.c_int), _ptr(nt, ctypes.c_int),
+            _ptr(xyz, ctypes.c_double), _ptr(r, ctypes.c_double), _ptr(energies, ctypes.c_double),
+            _ptr(forces, ctypes.c_double), ctypes.c_int(num_threads))
+        if status != 0:
+            raise RuntimeError(_lib().oracle_mace_last_error().decode())
+        return energies, forces
+
+
+def reduce(num_neigh, neigh_indices, forces, xyz, volume):
+    """Atom forces (N, 3) and the 3x3 stress from directed edge forces."""
+    lib = _lib()
+    nn = np.ascontiguousarray(num_neigh, dtype=np.int32)
+    idx = np.ascontiguousarray(neigh_indices, dtype=np.int32)
+    f = np.ascontiguousarray(forces, dtype=np.float64)
+    x = np.ascontiguousarray(xyz, dtype=np.float64)
+    n = len(nn)
+    atom = np.zeros((n, 3))
+    stress = np.zeros(9)
+    lib.oracle_reduce(ctypes.c_int(n), _ptr(nn, ctypes.c_int), _ptr(idx, ctypes.c_int),
+                      _ptr(f, ctypes.c_double), _ptr(x, ctypes.c_double), ctypes.c_double(volume),
+                      _ptr(atom, ctypes.c_double), _ptr(stress, ctypes.c_double))
+    return atom, stress.reshape(3, 3)
+
+
+def voigt(stress):
+    """3x3 -> (xx, yy, zz, yz, xz, xy), symmetrised (ASE's convention)."""
+    s = np.asarray(stress).reshape(3, 3)
+    return np.array([s[0, 0], s[1, 1], s[2, 2], 0.5 * (s[1, 2] + s[2, 1]),
+                     0.5 * (s[0, 2] + s[2, 0]), 0.5 * (s[0, 1] + s[1, 0])])
+
+
+def graph_inputs(structure, cutoff, atomic_numbers):
+    """Neighbour graph (oracle order) and edge geometry of a periodic structure.
+
+    Returns dict with node_types, num_neigh, neigh_indices, neigh_types, xyz, r.
+    """
+    cell = np.asarray(structure.cell, dtype=np.float64)
+    inv = np.linalg.inv(cell)
+    g = neighbor_graph(structure.positions, cell, inv, cutoff)
+    lookup = {int(z): i for i, z in enumerate(atomic_numbers)}
+    types = np.array([lookup[int(z)] for z in structure.numbers], dtype=np.int32)
+    receivers = np.repeat(np.arange(len(types)), g["num_neigh"])
+    xyz = (
+        structure.positions[g["sources"]] - structure.positions[receivers]
+        + g["shifts"].astype(np.float64) @ cell
+    )
+    r = np.linalg.norm(xyz, axis=1)
+    return {
+        "node_types": types,
+        "num_neigh": g["num_neigh"],
+        "neigh_indices": g["sources"],
+        "neigh_types": types[g["sources"]],
+        "xyz": xyz,
+        "r": r,
+        "receivers": receivers,
+        "graph": g,
+    }
+
+
+def evaluate(oracle: MaceOracle, structure, cutoff, num_threads=0):
+    """Energy, atom forces and Voigt stress of a periodic structure."""
+    gi = graph_inputs(structure, cutoff, oracle.model["atomic_numbers"])
+    energies, forces = oracle.compute(gi["node_types"], gi["num_neigh"], gi["neigh_indices"],
+                                      gi["neigh_types"], gi["xyz"], gi["r"], num_threads)
+    atom, stress = reduce(gi["num_neigh"], gi["neigh_indices"], forces, gi["xyz"],
+                          abs(np.linalg.det(structure.cell)))
+    return {
+        "energy": float(np.sum(energies, dtype=np.float64)),
+        "energies": energies,
+        "forces": atom,
+        "stress": voigt(stress),
+        "stress_3x3": stress,
+        "directed_forces": forces,
+        "inputs": gi,
+    }
