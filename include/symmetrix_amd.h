@@ -1,0 +1,173 @@
+/*
+ * symmetrix_amd.h -- C ABI of the MI355X-native MACE evaluator.
+ *
+ * Drop-in boundary for the model-evaluation path of Symmetrix-XL: every entry
+ * point below replaces one method of the reference's native evaluator class
+ * MACEKokkosFloat, which the reference binds to Python with pybind11
+ * (symmetrix/source/cpp/mace_kokkos.cpp) and calls from its ASE calculator
+ * (symmetrix/source/symmetrix/calculator.py) and LAMMPS pair style
+ * (pair_symmetrix/pair_symmetrix_mace.cpp).  The cited line of each function
+ * is the reference interface it stands in for.
+ *
+ * Conventions (kept from the reference, mace_kokkos.hpp and
+ * jit_host_plugin_abi.h:109-110):
+ *   - plain pointers and sizes only; arrays are C-contiguous; host pointers
+ *     unless a function name ends in _device;
+ *   - node types are model element indices (not atomic numbers);
+ *   - edges are receiver-major, contiguous per receiver; edge vector
+ *     xyz = r_source - r_receiver (+ periodic shift . cell);
+ *   - directed forces are f_e = -dE/dxyz_e (reference node_forces);
+ *   - atom forces F_a = sum_{src=a} f_e - sum_{recv=a} f_e; stress
+ *     sigma = -(1/V) sum_e f_e (x) xyz_e, row-major 3x3;
+ *   - graph preparation returns a generation token; a stale token is an
+ *     error (mace_kokkos_evaluate.cpp:326-334);
+ *   - every function returns SXL_OK (0) or an error code and never throws;
+ *     the message of the last error on the calling thread is sxl_last_error();
+ *   - one evaluator owns one HIP stream and device memory and is not
+ *     thread-safe; calls return after their device work has completed unless
+ *     stated otherwise.
+ */
+#ifndef SYMMETRIX_AMD_H
+#define SYMMETRIX_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SXL_OK 0
+#define SXL_INVALID_ARGUMENT 1 /* std::invalid_argument in the reference  */
+#define SXL_OUT_OF_RANGE 2     /* std::out_of_range                        */
+#define SXL_LENGTH_ERROR 3     /* std::length_error (int32 cardinality)     */
+#define SXL_RUNTIME_ERROR 4    /* std::runtime_error, device failures      */
+#define SXL_LOGIC_ERROR 5      /* std::logic_error                          */
+#define SXL_ALLOCATION_ERROR 6 /* host or device allocation failure         */
+
+typedef struct sxl_evaluator sxl_evaluator;
+
+typedef struct {
+    int num_elements;
+    int num_channels;
+    int l_max;
+    int L_max;
+    int num_paths;
+    int spline_points;
+    double r_cut;
+} sxl_model_info_t;
+
+typedef struct {
+    int64_t device_bytes;
+    int num_nodes;
+    int64_t num_edges;
+    int graph_builds;
+    int evaluations;
+    double last_evaluation_ms; /* host time to enqueue and run one evaluation */
+} sxl_stats_t;
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* sxl_last_error(void);
+
+/* Load a format-4 compact MACE JSON for FP32 evaluation on the current HIP
+ * device.  Replaces MACEKokkosFloat(filename, head)
+ * (symmetrix/source/cpp/mace_kokkos.cpp:262-264). */
+int sxl_create(const char* model_path, const char* head, sxl_evaluator** out);
+void sxl_destroy(sxl_evaluator* evaluator);
+
+/* Model metadata: r_cut, l_max, L_max, ... properties (mace_kokkos.cpp:2762). */
+int sxl_model_info(const sxl_evaluator* evaluator, sxl_model_info_t* out);
+/* atomic_numbers / atomic_energies properties: num_elements entries. */
+int sxl_atomic_numbers(const sxl_evaluator* evaluator, int* out);
+int sxl_atomic_energies(const sxl_evaluator* evaluator, double* out);
+
+/* Receiver-major CSR from the caller.  Replaces
+ * _prepare_factorized_graph(num_nodes, node_types, num_neigh, neigh_indices,
+ * neigh_types) (mace_kokkos.cpp:1561-1579). */
+int sxl_prepare_graph(sxl_evaluator* evaluator, int num_nodes, const int* node_types, const int* num_neigh,
+                      const int* neigh_indices, const int* neigh_types, uint64_t* generation);
+
+/* Periodic neighbour graph built on the device at `cutoff` (model cutoff plus
+ * skin).  cell and inverse_cell are row-major 3x3 (rows are lattice vectors).
+ * Replaces _prepare_periodic_factorized_graph(node_types, positions, cell,
+ * inverse_cell, neighbor_cutoff) (mace_kokkos.cpp:1580-1603). */
+int sxl_prepare_periodic_graph(sxl_evaluator* evaluator, int num_nodes, const int* node_types,
+                               const double* positions, const double* cell, const double* inverse_cell,
+                               double cutoff, uint64_t* generation, int64_t* num_edges);
+int sxl_prepare_periodic_graph_device(sxl_evaluator* evaluator, int num_nodes, const int* node_types,
+                                      const double* d_positions, const double* cell,
+                                      const double* inverse_cell, double cutoff, uint64_t* generation,
+                                      int64_t* num_edges);
+
+/* Copies of the prepared periodic graph (any output may be NULL): num_neigh
+ * [N], receiver_offsets [N+1], sources [E], shifts [E][3], fractional_xyz
+ * [E][3].  Outputs of the reference's build_periodic_neighbor_graph_kokkos
+ * (libsymmetrix/source/neighbor_graph_kokkos.cpp:38-405). */
+int sxl_graph_arrays(sxl_evaluator* evaluator, uint64_t generation, int* num_neigh, int* receiver_offsets,
+                     int* sources, int* shifts, double* fractional_xyz);
+
+/* New cell for the prepared periodic graph (_update_factorized_cell). */
+int sxl_update_cell(sxl_evaluator* evaluator, uint64_t generation, const double* cell,
+                    const double* inverse_cell);
+
+/* Evaluate energies and forces at new positions of a prepared periodic graph.
+ * Replaces _compute_prepared_factorized_positions(generation, positions)
+ * (mace_kokkos.cpp:1828-1836). */
+int sxl_compute_prepared_positions(sxl_evaluator* evaluator, uint64_t generation, const double* positions);
+int sxl_compute_prepared_positions_device(sxl_evaluator* evaluator, uint64_t generation,
+                                          const double* d_positions);
+
+/* Evaluate with caller-provided edge vectors xyz [E][3] and lengths r [E].
+ * Replaces _compute_prepared_factorized(generation, xyz, r)
+ * (mace_kokkos.cpp:1817-1827). */
+int sxl_compute_prepared(sxl_evaluator* evaluator, uint64_t generation, const double* xyz, const double* r);
+
+/* One-shot: prepare the CSR graph and evaluate.  Replaces
+ * compute_node_energies_forces(num_nodes, node_types, num_neigh,
+ * neigh_indices, neigh_types, xyz, r) (mace_kokkos.cpp:2169-2203). */
+int sxl_compute_node_energies_forces(sxl_evaluator* evaluator, int num_nodes, const int* node_types,
+                                     const int* num_neigh, const int* neigh_indices, const int* neigh_types,
+                                     const double* xyz, const double* r);
+
+/* Largest displacement of positions since the periodic graph was built (for
+ * skin-based neighbour reuse, calculator.py:2851-2898). */
+int sxl_max_displacement(sxl_evaluator* evaluator, uint64_t generation, const double* positions,
+                         int positions_on_device, double* out);
+
+/* node_energies property, N doubles (mace_kokkos.cpp:2086-2093). */
+int sxl_node_energies(const sxl_evaluator* evaluator, double* out, int num_nodes);
+/* node_forces property, directed edge forces [E][3] (mace_kokkos.cpp:2094-2101). */
+int sxl_node_forces(const sxl_evaluator* evaluator, double* out, int64_t num_edges);
+/* _reduce_atom_forces: [N][3] (mace_kokkos.cpp:2103-2133). */
+int sxl_reduce_atom_forces(sxl_evaluator* evaluator, uint64_t generation, double* out);
+/* _reduce_stress(volume): 3x3 row-major (mace_kokkos.cpp:2134-2154). */
+int sxl_reduce_stress(sxl_evaluator* evaluator, uint64_t generation, double volume, double* out9);
+/* Sum of node energies in double (calculator.py:3831-3834). */
+int sxl_total_energy(sxl_evaluator* evaluator, uint64_t generation, double* out);
+
+/* Device pointers of the last evaluation's results, valid until the next
+ * call: atom forces [N][3] and totals [10] = (energy, stress row-major); the
+ * totals hold the stress of the last sxl_reduce_stress volume. */
+int sxl_device_results(const sxl_evaluator* evaluator, const double** atom_forces, const double** totals);
+
+int sxl_graph_size(const sxl_evaluator* evaluator, int* num_nodes, int64_t* num_edges, uint64_t* generation);
+
+/* Model-free periodic neighbour graph on the device.  Replaces
+ * build_periodic_neighbor_graph_kokkos(positions, cell, inverse_cell, cutoff)
+ * (libsymmetrix/source/neighbor_graph_kokkos.cpp:38-405), whose Python
+ * binding is _kokkos_periodic_neighbor_graph.  Build, then copy the arrays
+ * (sized by num_edges) with sxl_neighbor_graph_copy, then free. */
+typedef struct sxl_graph sxl_graph;
+int sxl_neighbor_graph_build(const double* positions, int num_nodes, const double* cell,
+                             const double* inverse_cell, double cutoff, sxl_graph** out, int64_t* num_edges);
+int sxl_neighbor_graph_copy(const sxl_graph* graph, int* num_neigh, int* receiver_offsets, int* sources,
+                            int* shifts, double* fractional_xyz);
+void sxl_neighbor_graph_free(sxl_graph* graph);
+int sxl_stats(const sxl_evaluator* evaluator, sxl_stats_t* out);
+/* Waits for all device work of the evaluator. */
+int sxl_synchronize(const sxl_evaluator* evaluator);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SYMMETRIX_AMD_H */

@@ -1,0 +1,330 @@
+// C ABI of the evaluator (include/symmetrix_amd.h): exception-free wrappers.
+#include "../../include/symmetrix_amd.h"
+
+#include <algorithm>
+#include <cmath>
+#include <memory>
+#include <new>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "evaluator.hpp"
+
+struct sxl_evaluator {
+    sxl::Evaluator impl;
+    sxl_evaluator(const char* path, const char* head) : impl(path, head ? head : "") {}
+};
+
+struct sxl_graph {
+    sxl::PeriodicGraph graph;
+};
+
+namespace {
+
+thread_local std::string g_error;
+
+template <class F>
+int guarded(F&& f)
+{
+    try {
+        f();
+        g_error.clear();
+        return SXL_OK;
+    } catch (const std::bad_alloc& e) {
+        g_error = e.what();
+        return SXL_ALLOCATION_ERROR;
+    } catch (const std::out_of_range& e) {
+        g_error = e.what();
+        return SXL_OUT_OF_RANGE;
+    } catch (const std::length_error& e) {
+        g_error = e.what();
+        return SXL_LENGTH_ERROR;
+    } catch (const std::invalid_argument& e) {
+        g_error = e.what();
+        return SXL_INVALID_ARGUMENT;
+    } catch (const std::logic_error& e) {
+        g_error = e.what();
+        return SXL_LOGIC_ERROR;
+    } catch (const std::exception& e) {
+        g_error = e.what();
+        return SXL_RUNTIME_ERROR;
+    } catch (...) {
+        g_error = "unknown error";
+        return SXL_RUNTIME_ERROR;
+    }
+}
+
+int null_handle()
+{
+    g_error = "null evaluator handle or output pointer";
+    return SXL_INVALID_ARGUMENT;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* sxl_last_error(void) { return g_error.c_str(); }
+
+int sxl_create(const char* model_path, const char* head, sxl_evaluator** out)
+{
+    if (!model_path || !out) return null_handle();
+    *out = nullptr;
+    return guarded([&] { *out = new sxl_evaluator(model_path, head); });
+}
+
+void sxl_destroy(sxl_evaluator* evaluator) { delete evaluator; }
+
+int sxl_model_info(const sxl_evaluator* ev, sxl_model_info_t* out)
+{
+    if (!ev || !out) return null_handle();
+    return guarded([&] {
+        const sxl::HostModel& m = ev->impl.model();
+        out->num_elements = m.num_elements;
+        out->num_channels = m.channels;
+        out->l_max = m.l_max;
+        out->L_max = m.L_max;
+        out->num_paths = m.num_paths();
+        out->spline_points = m.spline_points;
+        out->r_cut = m.r_cut;
+    });
+}
+
+int sxl_atomic_numbers(const sxl_evaluator* ev, int* out)
+{
+    if (!ev || !out) return null_handle();
+    return guarded([&] {
+        const auto& v = ev->impl.model().atomic_numbers;
+        for (std::size_t i = 0; i < v.size(); ++i) out[i] = v[i];
+    });
+}
+
+int sxl_atomic_energies(const sxl_evaluator* ev, double* out)
+{
+    if (!ev || !out) return null_handle();
+    return guarded([&] {
+        const auto& v = ev->impl.model().atomic_energies;
+        for (std::size_t i = 0; i < v.size(); ++i) out[i] = v[i];
+    });
+}
+
+int sxl_prepare_graph(sxl_evaluator* ev, int num_nodes, const int* node_types, const int* num_neigh,
+                      const int* neigh_indices, const int* neigh_types, uint64_t* generation)
+{
+    if (!ev || !generation || (num_nodes > 0 && (!node_types || !num_neigh))) return null_handle();
+    return guarded([&] {
+        *generation = ev->impl.prepare_graph(num_nodes, node_types, num_neigh, neigh_indices, neigh_types);
+    });
+}
+
+static int prepare_periodic(sxl_evaluator* ev, int num_nodes, const int* node_types, const double* positions,
+                            bool device, const double* cell, const double* inverse_cell, double cutoff,
+                            uint64_t* generation, int64_t* num_edges)
+{
+    if (!ev || !generation || !cell || !inverse_cell || (num_nodes > 0 && (!node_types || !positions)))
+        return null_handle();
+    return guarded([&] {
+        *generation = ev->impl.prepare_periodic_graph(num_nodes, node_types, positions, device, cell, inverse_cell,
+                                                      cutoff);
+        if (num_edges) *num_edges = ev->impl.num_edges();
+    });
+}
+
+int sxl_prepare_periodic_graph(sxl_evaluator* ev, int num_nodes, const int* node_types, const double* positions,
+                               const double* cell, const double* inverse_cell, double cutoff, uint64_t* generation,
+                               int64_t* num_edges)
+{
+    return prepare_periodic(ev, num_nodes, node_types, positions, false, cell, inverse_cell, cutoff, generation,
+                            num_edges);
+}
+
+int sxl_prepare_periodic_graph_device(sxl_evaluator* ev, int num_nodes, const int* node_types,
+                                      const double* d_positions, const double* cell, const double* inverse_cell,
+                                      double cutoff, uint64_t* generation, int64_t* num_edges)
+{
+    return prepare_periodic(ev, num_nodes, node_types, d_positions, true, cell, inverse_cell, cutoff, generation,
+                            num_edges);
+}
+
+int sxl_graph_arrays(sxl_evaluator* ev, uint64_t generation, int* num_neigh, int* receiver_offsets, int* sources,
+                     int* shifts, double* fractional_xyz)
+{
+    if (!ev) return null_handle();
+    return guarded(
+        [&] { ev->impl.graph_arrays(generation, num_neigh, receiver_offsets, sources, shifts, fractional_xyz); });
+}
+
+int sxl_update_cell(sxl_evaluator* ev, uint64_t generation, const double* cell, const double* inverse_cell)
+{
+    if (!ev || !cell || !inverse_cell) return null_handle();
+    return guarded([&] { ev->impl.update_cell(generation, cell, inverse_cell); });
+}
+
+int sxl_compute_prepared_positions(sxl_evaluator* ev, uint64_t generation, const double* positions)
+{
+    if (!ev || (!positions && ev->impl.num_nodes() > 0)) return null_handle();
+    return guarded([&] { ev->impl.compute_positions(generation, positions, false); });
+}
+
+int sxl_compute_prepared_positions_device(sxl_evaluator* ev, uint64_t generation, const double* d_positions)
+{
+    if (!ev || (!d_positions && ev->impl.num_nodes() > 0)) return null_handle();
+    return guarded([&] { ev->impl.compute_positions(generation, d_positions, true); });
+}
+
+int sxl_compute_prepared(sxl_evaluator* ev, uint64_t generation, const double* xyz, const double* r)
+{
+    if (!ev || ((!xyz || !r) && ev->impl.num_edges() > 0)) return null_handle();
+    return guarded([&] { ev->impl.compute_xyz(generation, xyz, r, false); });
+}
+
+int sxl_compute_node_energies_forces(sxl_evaluator* ev, int num_nodes, const int* node_types, const int* num_neigh,
+                                     const int* neigh_indices, const int* neigh_types, const double* xyz,
+                                     const double* r)
+{
+    if (!ev) return null_handle();
+    return guarded([&] {
+        const uint64_t g = ev->impl.prepare_graph(num_nodes, node_types, num_neigh, neigh_indices, neigh_types);
+        ev->impl.compute_xyz(g, xyz, r, false);
+    });
+}
+
+int sxl_max_displacement(sxl_evaluator* ev, uint64_t generation, const double* positions, int on_device,
+                         double* out)
+{
+    if (!ev || !out) return null_handle();
+    return guarded([&] { *out = ev->impl.max_displacement(generation, positions, on_device != 0); });
+}
+
+int sxl_node_energies(const sxl_evaluator* ev, double* out, int num_nodes)
+{
+    if (!ev || (!out && num_nodes > 0)) return null_handle();
+    return guarded([&] {
+        if (num_nodes != ev->impl.num_nodes()) throw std::invalid_argument("node energy extent mismatch");
+        ev->impl.node_energies(out);
+    });
+}
+
+int sxl_node_forces(const sxl_evaluator* ev, double* out, int64_t num_edges)
+{
+    if (!ev || (!out && num_edges > 0)) return null_handle();
+    return guarded([&] {
+        if (num_edges != ev->impl.num_edges()) throw std::invalid_argument("directed force extent mismatch");
+        ev->impl.node_forces(out);
+    });
+}
+
+int sxl_reduce_atom_forces(sxl_evaluator* ev, uint64_t generation, double* out)
+{
+    if (!ev || (!out && ev->impl.num_nodes() > 0)) return null_handle();
+    return guarded([&] { ev->impl.atom_forces(generation, out); });
+}
+
+int sxl_reduce_stress(sxl_evaluator* ev, uint64_t generation, double volume, double* out9)
+{
+    if (!ev || !out9) return null_handle();
+    return guarded([&] { ev->impl.stress(generation, volume, out9); });
+}
+
+int sxl_total_energy(sxl_evaluator* ev, uint64_t generation, double* out)
+{
+    if (!ev || !out) return null_handle();
+    return guarded([&] { *out = ev->impl.total_energy(generation); });
+}
+
+int sxl_device_results(const sxl_evaluator* ev, const double** atom_forces, const double** totals)
+{
+    if (!ev) return null_handle();
+    return guarded([&] {
+        if (atom_forces) *atom_forces = ev->impl.device_atom_forces();
+        if (totals) *totals = ev->impl.device_totals();
+    });
+}
+
+int sxl_graph_size(const sxl_evaluator* ev, int* num_nodes, int64_t* num_edges, uint64_t* generation)
+{
+    if (!ev) return null_handle();
+    return guarded([&] {
+        if (num_nodes) *num_nodes = ev->impl.num_nodes();
+        if (num_edges) *num_edges = ev->impl.num_edges();
+        if (generation) *generation = ev->impl.generation();
+    });
+}
+
+int sxl_stats(const sxl_evaluator* ev, sxl_stats_t* out)
+{
+    if (!ev || !out) return null_handle();
+    return guarded([&] {
+        const sxl::EvaluatorStats& s = ev->impl.stats();
+        out->device_bytes = static_cast<int64_t>(s.device_bytes);
+        out->num_nodes = ev->impl.num_nodes();
+        out->num_edges = ev->impl.num_edges();
+        out->graph_builds = s.graph_builds;
+        out->evaluations = s.evaluations;
+        out->last_evaluation_ms = s.last_evaluation_ms;
+    });
+}
+
+int sxl_neighbor_graph_build(const double* positions, int num_nodes, const double* cell, const double* inverse_cell,
+                             double cutoff, sxl_graph** out, int64_t* num_edges)
+{
+    if (!out || !cell || !inverse_cell || (num_nodes > 0 && !positions)) return null_handle();
+    *out = nullptr;
+    return guarded([&] {
+        sxl::validate_periodic_inputs(num_nodes, cell, inverse_cell, cutoff);
+        for (long long i = 0; i < 3LL * num_nodes; ++i)
+            if (!std::isfinite(positions[i])) throw std::invalid_argument("neighbor graph positions must be finite");
+        hipStream_t stream = nullptr;
+        if (hipStreamCreateWithFlags(&stream, hipStreamNonBlocking) != hipSuccess)
+            throw std::runtime_error("stream creation failed");
+        auto graph = std::make_unique<sxl_graph>();
+        try {
+            sxl::DeviceBuffer d_pos;
+            d_pos.reserve(std::max(num_nodes, 1) * 3 * sizeof(double));
+            if (num_nodes > 0 &&
+                hipMemcpy(d_pos.as<double>(), positions, num_nodes * 3 * sizeof(double), hipMemcpyHostToDevice) !=
+                    hipSuccess)
+                throw std::runtime_error("position upload failed");
+            sxl::build_periodic_graph(d_pos.as<double>(), num_nodes, cell, inverse_cell, cutoff, stream, graph->graph);
+        } catch (...) {
+            (void)hipStreamDestroy(stream);
+            throw;
+        }
+        (void)hipStreamDestroy(stream);
+        if (num_edges) *num_edges = graph->graph.num_edges;
+        *out = graph.release();
+    });
+}
+
+int sxl_neighbor_graph_copy(const sxl_graph* g, int* num_neigh, int* receiver_offsets, int* sources, int* shifts,
+                            double* fractional_xyz)
+{
+    if (!g) return null_handle();
+    return guarded([&] {
+        const int N = g->graph.num_nodes;
+        const long long E = g->graph.num_edges;
+        std::vector<int> first(N + 1);
+        auto copy = [](void* dst, const void* src, size_t bytes) {
+            if (bytes && hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost) != hipSuccess)
+                throw std::runtime_error("graph copy failed");
+        };
+        copy(first.data(), g->graph.first.as<int>(), (N + 1) * sizeof(int));
+        if (receiver_offsets) std::copy(first.begin(), first.end(), receiver_offsets);
+        if (num_neigh)
+            for (int i = 0; i < N; ++i) num_neigh[i] = first[i + 1] - first[i];
+        if (sources) copy(sources, g->graph.sources.as<int>(), E * sizeof(int));
+        if (shifts) copy(shifts, g->graph.shifts.as<int>(), E * 3 * sizeof(int));
+        if (fractional_xyz) copy(fractional_xyz, g->graph.fractional_xyz.as<double>(), E * 3 * sizeof(double));
+    });
+}
+
+void sxl_neighbor_graph_free(sxl_graph* graph) { delete graph; }
+
+int sxl_synchronize(const sxl_evaluator* ev)
+{
+    if (!ev) return null_handle();
+    return guarded([&] { ev->impl.synchronize(); });
+}
+
+}  // extern "C"

@@ -1,0 +1,909 @@
+// MI355X MACE evaluator host code (see evaluator.hpp).
+#include "evaluator.hpp"
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <limits>
+#include <map>
+#include <numeric>
+#include <stdexcept>
+#include <thread>
+
+#include "r1_shapes.inc"
+
+namespace sxl {
+
+namespace {
+
+void hip_check(hipError_t err, const char* what)
+{
+    if (err != hipSuccess)
+        throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(err));
+}
+
+// Copies a host vector into a device buffer and waits, so the (often
+// temporary) host vector may be released as soon as this returns.
+template <class T>
+void upload(DeviceBuffer& buf, const std::vector<T>& host, hipStream_t s)
+{
+    buf.reserve(std::max<std::size_t>(host.size() * sizeof(T), sizeof(T)));
+    if (!host.empty()) {
+        hip_check(hipMemcpyAsync(buf.as<void>(), host.data(), host.size() * sizeof(T),
+                                 hipMemcpyHostToDevice, s),
+                  "upload");
+        hip_check(hipStreamSynchronize(s), "upload");
+    }
+}
+
+std::vector<float> to_float(const double* p, std::size_t n)
+{
+    std::vector<float> out(n);
+    for (std::size_t i = 0; i < n; ++i) out[i] = static_cast<float>(p[i]);
+    return out;
+}
+
+std::vector<float> transpose(const double* p, int rows, int cols)
+{
+    std::vector<float> out(static_cast<std::size_t>(rows) * cols);
+    for (int r = 0; r < rows; ++r)
+        for (int c = 0; c < cols; ++c)
+            out[static_cast<std::size_t>(c) * rows + r] = static_cast<float>(p[static_cast<std::size_t>(r) * cols + c]);
+    return out;
+}
+
+// Monomial tables -> packed (deg | i0 << 4 | i1 << 10 | i2 << 16)
+std::vector<int> pack_terms(const std::vector<int>& degree, const std::vector<int>& index)
+{
+    std::vector<int> out(degree.size());
+    for (std::size_t t = 0; t < degree.size(); ++t)
+        out[t] = degree[t] | (index[3 * t] << 4) | (index[3 * t + 1] << 10) | (index[3 * t + 2] << 16);
+    return out;
+}
+
+// Compiled R1 shape: validates the JSON path list against the compiled one and
+// scatters the JSON CG coefficients onto the compiled term slots.
+template <class S>
+std::vector<float> shape_cg(const HostModel& m)
+{
+    if (m.num_paths() != S::NP)
+        throw std::invalid_argument("Phi1 path list does not match the compiled (l_max, L_max) shape.");
+    for (int p = 0; p < S::NP; ++p)
+        if (m.Phi1_l[p] != S::path_lo[p] || m.Phi1_l1[p] != S::path_l1[p] ||
+            m.Phi1_l2[p] != S::path_l2[p])
+            throw std::invalid_argument(
+                "Phi1 path list does not match the compiled (l_max, L_max) shape.");
+    std::map<std::pair<int, int>, int> slot;
+    for (int t = 0; t < S::NT; ++t) slot[{S::term_row[t], S::term_lme[t]}] = t;
+    std::vector<double> cg(S::NT, 0.0);
+    for (std::size_t j = 0; j < m.Phi1_cg.size(); ++j) {
+        auto it = slot.find({m.Phi1_row[j], m.Phi1_lme[j]});
+        if (it == slot.end()) {
+            if (m.Phi1_cg[j] == 0.0) continue;
+            throw std::invalid_argument(
+                "Phi1 coupling term outside the compiled CG sparsity of this shape.");
+        }
+        cg[it->second] += m.Phi1_cg[j];
+    }
+    return std::vector<float>(cg.begin(), cg.end());
+}
+
+struct ShapeInfo {
+    int nlme;
+    std::vector<int> num_e, lme_off;
+};
+
+template <class S>
+ShapeInfo shape_info()
+{
+    ShapeInfo s;
+    s.nlme = S::NLME;
+    s.num_e.assign(S::num_e, S::num_e + S::LMAX + 1);
+    s.lme_off.assign(S::lme_off, S::lme_off + S::LMAX + 1);
+    return s;
+}
+
+}  // namespace
+
+DeviceBuffer::~DeviceBuffer() { release(); }
+
+void DeviceBuffer::release()
+{
+    if (ptr_) (void)hipFree(ptr_);
+    ptr_ = nullptr;
+    bytes_ = 0;
+}
+
+void DeviceBuffer::reserve(std::size_t bytes)
+{
+    if (bytes <= bytes_) return;
+    release();
+    void* p = nullptr;
+    hipError_t err = hipMalloc(&p, bytes);
+    if (err != hipSuccess) {
+        (void)hipGetLastError();
+        throw std::runtime_error("device allocation of " + std::to_string(bytes) +
+                                 " bytes failed: " + hipGetErrorString(err));
+    }
+    ptr_ = p;
+    bytes_ = bytes;
+}
+
+Evaluator::Evaluator(const std::string& model_path, const std::string& head)
+    : model_(HostModel::load(model_path, head))
+{
+    int devices = 0;
+    if (hipGetDeviceCount(&devices) != hipSuccess || devices == 0) {
+        (void)hipGetLastError();
+        throw std::runtime_error("no HIP device is available");
+    }
+    hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "stream create");
+    C_ = model_.channels;
+    nlm_ = model_.num_lm;
+    nLM_ = model_.num_LM;
+    ShapeInfo info;
+    if (model_.l_max == 2 && model_.L_max == 1)
+        info = shape_info<R1Shape<2, 1>>();
+    else if (model_.l_max == 3 && model_.L_max == 1)
+        info = shape_info<R1Shape<3, 1>>();
+    else if (model_.l_max == 3 && model_.L_max == 2)
+        info = shape_info<R1Shape<3, 2>>();
+    else
+        throw std::invalid_argument("no compiled kernels for (l_max, L_max) = (" +
+                                    std::to_string(model_.l_max) + ", " + std::to_string(model_.L_max) +
+                                    "); compiled shapes: (2,1), (3,1), (3,2)");
+    nlme_ = info.nlme;
+    num_e_ = info.num_e;
+    lme_off_ = info.lme_off;
+    if (C_ % 32 != 0 || C_ > 1024)
+        throw std::invalid_argument("channel count must be a multiple of 32 and at most 1024");
+    // one workgroup of C threads per receiver, at most 256 threads
+    if (C_ > 256) throw std::invalid_argument("channel counts above 256 are not supported yet");
+    grid_.x0 = model_.grid_min;
+    grid_.h = model_.spline_h;
+    grid_.intervals = model_.spline_points - 1;
+    grid_.r_cut = model_.r_cut;
+    upload_static_tables();
+    hip_check(hipStreamSynchronize(stream_), "model upload");
+}
+
+Evaluator::~Evaluator()
+{
+    if (stream_) (void)hipStreamSynchronize(stream_);
+    // buffers free themselves; the stream goes last
+    A0_.release();
+    if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+void Evaluator::upload_static_tables()
+{
+    const HostModel& m = model_;
+    const int L1 = m.L_max + 1;
+    upload(h1w_, to_float(m.H1W.data(), m.H1W.size()), stream_);
+    std::vector<float> h1wt;
+    for (int l = 0; l < L1; ++l) {
+        auto t = transpose(m.H1W.data() + static_cast<std::size_t>(l) * C_ * C_, C_, C_);
+        h1wt.insert(h1wt.end(), t.begin(), t.end());
+    }
+    upload(h1wt_, h1wt, stream_);
+    a1w_.clear();
+    a1wt_.clear();
+    for (int l = 0; l <= m.l_max; ++l) {
+        a1w_.push_back(std::make_unique<DeviceBuffer>());
+        a1wt_.push_back(std::make_unique<DeviceBuffer>());
+        upload(*a1w_[l], to_float(m.A1W[l].data(), m.A1W[l].size()), stream_);
+        upload(*a1wt_[l], transpose(m.A1W[l].data(), num_e_[l] * C_, C_), stream_);
+    }
+    upload(h2m1_, to_float(m.H2M1.data(), m.H2M1.size()), stream_);
+    upload(q_, to_float(m.readout_q.data(), m.readout_q.size()), stream_);
+    upload(w1_, to_float(m.readout_w1.data(), m.readout_w1.size()), stream_);
+    upload(w2_, to_float(m.readout_w2.data(), m.readout_w2.size()), stream_);
+    std::vector<float> cg;
+    if (m.l_max == 2 && m.L_max == 1)
+        cg = shape_cg<R1Shape<2, 1>>(m);
+    else if (m.l_max == 3 && m.L_max == 1)
+        cg = shape_cg<R1Shape<3, 1>>(m);
+    else
+        cg = shape_cg<R1Shape<3, 2>>(m);
+    upload(cg_, cg, stream_);
+    upload(p0_offsets_, m.m0_offsets, stream_);
+    upload(p0_packed_, pack_terms(m.m0_degree, m.m0_index), stream_);
+    p0_terms_ = m.m0_offsets.back();
+    std::vector<int> off1 = {0, static_cast<int>(m.m1_degree.size())};
+    upload(p1_offsets_, off1, stream_);
+    upload(p1_packed_, pack_terms(m.m1_degree, m.m1_index), stream_);
+    p1_terms_ = static_cast<int>(m.m1_degree.size());
+}
+
+// Radial spline tables and per-type weights of the active element types
+// (reference MACECPU::prepare_active_types, mace.cpp:118-213, with H0 and
+// A0_W folded into the layer-0 splines per ordered pair as the reference's
+// device path does, mace_kokkos_factorized_lifecycle.cpp:3990-4046).
+void Evaluator::prepare_active_types(const std::vector<int>& node_types)
+{
+    std::vector<int> types(node_types.begin(), node_types.end());
+    std::sort(types.begin(), types.end());
+    types.erase(std::unique(types.begin(), types.end()), types.end());
+    if (types.empty()) throw std::invalid_argument("MACE compact radial cache requires at least one active type.");
+    for (int t : types)
+        if (t < 0 || t >= model_.num_elements) throw std::out_of_range("MACE active type index is out of range.");
+    if (types == active_types_) return;
+    const HostModel& m = model_;
+    const int na = static_cast<int>(types.size());
+    if (na * na > 0xffff) throw std::invalid_argument("too many active element types");
+    const int P = m.spline_points, NI = P - 1, NL = m.l_max + 1, NP = m.num_paths();
+    const double h = m.spline_h;
+    // nodal tables per unordered pair
+    const int npairs = na * (na + 1) / 2;
+    std::vector<std::vector<double>> r0v(npairs), r0d(npairs), r1v(npairs), r1d(npairs);
+    std::vector<std::pair<int, int>> pair_types;
+    for (int a = 0; a < na; ++a)
+        for (int b = a; b < na; ++b) pair_types.push_back({a, b});
+    auto tabulate = [&](int p) {
+        const int ti = types[pair_types[p].first], tj = types[pair_types[p].second];
+        m.radial_tables(m.R0, ti, tj, r0v[p], r0d[p]);
+        m.radial_tables(m.R1, ti, tj, r1v[p], r1d[p]);
+    };
+    const int nthreads = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+    {
+        std::vector<std::thread> pool;
+        for (int w = 0; w < nthreads; ++w)
+            pool.emplace_back([&, w] {
+                for (int p = w; p < npairs; p += nthreads) tabulate(p);
+            });
+        for (auto& t : pool) t.join();
+    }
+    auto hermite = [&](const std::vector<double>& v, const std::vector<double>& d, int fn, int iv,
+                       double* c4) {
+        const double v0 = v[static_cast<std::size_t>(fn) * P + iv], v1 = v[static_cast<std::size_t>(fn) * P + iv + 1];
+        const double d0 = d[static_cast<std::size_t>(fn) * P + iv], d1 = d[static_cast<std::size_t>(fn) * P + iv + 1];
+        c4[0] = v0;
+        c4[1] = d0;
+        c4[2] = (-3.0 * v0 - 2.0 * h * d0 + 3.0 * v1 - h * d1) / (h * h);
+        c4[3] = (2.0 * v0 + h * d0 - 2.0 * v1 + h * d1) / (h * h * h);
+    };
+    // R1 table: [pair_u][iv][q][p][k]
+    std::vector<float> r1(static_cast<std::size_t>(npairs) * NI * 4 * NP * C_);
+    for (int pu = 0; pu < npairs; ++pu)
+        for (int iv = 0; iv < NI; ++iv)
+            for (int p = 0; p < NP; ++p)
+                for (int k = 0; k < C_; ++k) {
+                    double c4[4];
+                    hermite(r1v[pu], r1d[pu], p * C_ + k, iv, c4);
+                    for (int q = 0; q < 4; ++q)
+                        r1[((((static_cast<std::size_t>(pu) * NI + iv) * 4 + q) * NP + p) * C_) + k] =
+                            static_cast<float>(c4[q]);
+                }
+    // R0 folded: [pair_o][iv][q][l][k'] = sum_k c[iv][q][l*C+k] H0[tj][k] A0W[ti][l][k][k']
+    std::vector<float> r0f(static_cast<std::size_t>(na) * na * NI * 4 * NL * C_);
+    auto fold = [&](int po) {
+        const int ai = po / na, aj = po % na;
+        const int ti = types[ai], tj = types[aj];
+        const int pu = ai <= aj ? ai * (2 * na - ai - 1) / 2 + aj : aj * (2 * na - aj - 1) / 2 + ai;
+        std::vector<double> u(C_), out(C_);
+        for (int iv = 0; iv < NI; ++iv)
+            for (int q = 0; q < 4; ++q)
+                for (int l = 0; l < NL; ++l) {
+                    for (int k = 0; k < C_; ++k) {
+                        double c4[4];
+                        hermite(r0v[pu], r0d[pu], l * C_ + k, iv, c4);
+                        u[k] = c4[q] * m.H0[static_cast<std::size_t>(tj) * C_ + k];
+                    }
+                    std::fill(out.begin(), out.end(), 0.0);
+                    const double* W = m.A0W.data() + (static_cast<std::size_t>(ti) * NL + l) * C_ * C_;
+                    for (int k = 0; k < C_; ++k) {
+                        const double uk = u[k];
+                        const double* w = W + static_cast<std::size_t>(k) * C_;
+                        for (int ko = 0; ko < C_; ++ko) out[ko] += uk * w[ko];
+                    }
+                    float* dst = r0f.data() + ((((static_cast<std::size_t>(po) * NI + iv) * 4 + q) * NL + l) * C_);
+                    for (int ko = 0; ko < C_; ++ko) dst[ko] = static_cast<float>(out[ko]);
+                }
+    };
+    {
+        std::vector<std::thread> pool;
+        for (int w = 0; w < nthreads; ++w)
+            pool.emplace_back([&, w] {
+                for (int po = w; po < na * na; po += nthreads) fold(po);
+            });
+        for (auto& t : pool) t.join();
+    }
+    upload(r1_, r1, stream_);
+    upload(r0f_, r0f, stream_);
+    // per active type tables
+    std::vector<int> type_active(m.num_elements, -1);
+    for (int a = 0; a < na; ++a) type_active[types[a]] = a;
+    upload(type_active_, type_active, stream_);
+    std::vector<float> p0c, p1c, h2m0;
+    std::vector<double> e0;
+    const std::size_t T0 = p0_terms_, T1 = p1_terms_;
+    for (int a = 0; a < na; ++a) {
+        const int t = types[a];
+        auto c0 = to_float(m.m0_coef.data() + static_cast<std::size_t>(t) * T0 * C_, T0 * C_);
+        p0c.insert(p0c.end(), c0.begin(), c0.end());
+        auto c1 = to_float(m.m1_coef.data() + static_cast<std::size_t>(t) * T1 * C_, T1 * C_);
+        p1c.insert(p1c.end(), c1.begin(), c1.end());
+        auto hm = to_float(m.H2M0.data() + static_cast<std::size_t>(t) * C_ * C_,
+                           static_cast<std::size_t>(C_) * C_);
+        h2m0.insert(h2m0.end(), hm.begin(), hm.end());
+        e0.push_back(m.atomic_energies[t]);
+    }
+    upload(p0_coef_, p0c, stream_);
+    upload(p1_coef_, p1c, stream_);
+    upload(h2m0_, h2m0, stream_);
+    upload(e0_, e0, stream_);
+    hip_check(hipStreamSynchronize(stream_), "active type upload");
+    active_types_ = types;
+}
+
+void Evaluator::check_generation(std::uint64_t generation) const
+{
+    if (generation == 0 || generation != generation_)
+        throw std::invalid_argument("stale or unknown graph generation token");
+}
+
+void Evaluator::allocate_workspace()
+{
+    const std::size_t N = std::max(num_nodes_, 1);
+    const std::size_t E = std::max<long long>(num_edges_, 1);
+    const std::size_t f = sizeof(float);
+    A0_.reserve(N * nlm_ * C_ * f);
+    M0_.reserve(N * nLM_ * C_ * f);
+    H1_.reserve(N * nLM_ * C_ * f);
+    Phi1_.reserve(N * nlme_ * C_ * f);
+    A1_.reserve(N * nlm_ * C_ * f);
+    A1adj_.reserve(N * nlm_ * C_ * f);
+    direct_.reserve(N * C_ * f);
+    H1adj_.reserve(N * nLM_ * C_ * f);
+    msg_.reserve(E * nLM_ * C_ * f);
+    energies_.reserve(N * sizeof(double));
+    forces_.reserve(E * 3 * sizeof(double));
+    atom_forces_.reserve(N * 3 * sizeof(double));
+    partials_.reserve(static_cast<std::size_t>(reduce_totals_partials(num_nodes_, static_cast<int>(num_edges_))) *
+                      10 * sizeof(double));
+    totals_.reserve(16 * sizeof(double));
+    xyz_.reserve(E * 3 * sizeof(double));
+    r_.reserve(E * sizeof(double));
+}
+
+// Shared tail of both graph preparations: receivers, source-major transpose,
+// edge pair indices, workspace.
+void Evaluator::finish_graph(const int* host_neigh_types)
+{
+    const int N = num_nodes_;
+    const int E = static_cast<int>(num_edges_);
+    receiver_.reserve(std::max(E, 1) * sizeof(int));
+    hip_check(launch_receivers(N, first_.as<int>(), receiver_.as<int>(), stream_), "receivers");
+    // transpose: count -> scan -> fill -> sort each source segment ascending
+    DeviceBuffer counts, offsets64;
+    counts.reserve((N + 1) * sizeof(int));
+    offsets64.reserve((N + 1) * sizeof(long long));
+    scratch_.reserve(scan_scratch_size(N + 1) * sizeof(long long));
+    hip_check(hipMemsetAsync(counts.as<void>(), 0, (N + 1) * sizeof(int), stream_), "memset");
+    hip_check(launch_transpose_count(E, source_.as<int>(), counts.as<int>(), stream_), "transpose");
+    hip_check(launch_exclusive_scan_i32(counts.as<int>(), N, offsets64.as<long long>(),
+                                        scratch_.as<long long>(), stream_),
+              "scan");
+    tfirst_.reserve((N + 1) * sizeof(int));
+    hip_check(launch_narrow_offsets(offsets64.as<long long>(), N, tfirst_.as<int>(), nullptr, stream_),
+              "narrow");
+    tedge_.reserve(std::max(E, 1) * sizeof(int));
+    hip_check(hipMemsetAsync(counts.as<void>(), 0, (N + 1) * sizeof(int), stream_), "memset");
+    hip_check(launch_transpose_fill(E, source_.as<int>(), tfirst_.as<int>(), counts.as<int>(),
+                                    tedge_.as<int>(), stream_),
+              "transpose fill");
+    hip_check(launch_sort_segments(N, tfirst_.as<int>(), tedge_.as<int>(), stream_), "sort");
+    // edge pair indices
+    edge_pair_.reserve(std::max(E, 1) * sizeof(int));
+    if (host_neigh_types) {
+        // caller-provided source types (prepare_graph): computed on the host
+        std::vector<int> ta(model_.num_elements, -1);
+        for (std::size_t a = 0; a < active_types_.size(); ++a) ta[active_types_[a]] = static_cast<int>(a);
+        const int na = static_cast<int>(active_types_.size());
+        std::vector<int> pairs(E);
+        std::size_t e = 0;
+        std::vector<int> first(N + 1);
+        hip_check(hipMemcpyAsync(first.data(), first_.as<int>(), (N + 1) * sizeof(int), hipMemcpyDeviceToHost,
+                                 stream_),
+                  "copy");
+        hip_check(hipStreamSynchronize(stream_), "sync");
+        for (int i = 0; i < N; ++i) {
+            const int a = ta[host_types_[i]];
+            for (int j = first[i]; j < first[i + 1]; ++j, ++e) {
+                const int t = host_neigh_types[e];
+                if (t < 0 || t >= model_.num_elements) throw std::out_of_range("MACE radial type index is out of range.");
+                const int b = ta[t];
+                if (b < 0) throw std::runtime_error("MACE radial cache is not prepared for an active type.");
+                const int po = a * na + b;
+                const int pu = a <= b ? a * (2 * na - a - 1) / 2 + b : b * (2 * na - b - 1) / 2 + a;
+                pairs[e] = po | (pu << 16);
+            }
+        }
+        upload(edge_pair_, pairs, stream_);
+    } else {
+        hip_check(launch_edge_pairs(E, receiver_.as<int>(), source_.as<int>(), node_types_.as<int>(),
+                                    type_active_.as<int>(), static_cast<int>(active_types_.size()),
+                                    edge_pair_.as<int>(), stream_),
+                  "edge pairs");
+    }
+    allocate_workspace();
+    hip_check(hipStreamSynchronize(stream_), "graph preparation");
+    ++generation_;
+    evaluated_generation_ = 0;
+    reduced_ = false;
+    stats_.graph_builds += 1;
+    stats_.last_num_nodes = N;
+    stats_.last_num_edges = E;
+}
+
+std::uint64_t Evaluator::prepare_graph(int num_nodes, const int* node_types, const int* num_neigh,
+                                       const int* neigh_indices, const int* neigh_types)
+{
+    if (num_nodes < 0 || num_nodes >= std::numeric_limits<int>::max())
+        throw std::length_error("MACE graph atom count exceeds the 32-bit CSR limit.");
+    std::vector<int> types(node_types, node_types + num_nodes);
+    long long E = 0;
+    std::vector<int> first(num_nodes + 1, 0);
+    for (int i = 0; i < num_nodes; ++i) {
+        if (num_neigh[i] < 0) throw std::invalid_argument("num_neigh must be non-negative.");
+        E += num_neigh[i];
+        if (E > std::numeric_limits<int>::max())
+            throw std::length_error("MACE graph directed-edge count exceeds the 32-bit topology limit.");
+        first[i + 1] = static_cast<int>(E);
+    }
+    for (long long e = 0; e < E; ++e)
+        if (neigh_indices[e] < 0 || neigh_indices[e] >= num_nodes)
+            throw std::out_of_range("neighbour index out of range.");
+    prepare_active_types(types);
+    host_types_ = types;
+    num_nodes_ = num_nodes;
+    num_edges_ = E;
+    periodic_ = false;
+    upload(node_types_, types, stream_);
+    upload(first_, first, stream_);
+    std::vector<int> src(neigh_indices, neigh_indices + E);
+    upload(source_, src, stream_);
+    finish_graph(neigh_types);
+    return generation_;
+}
+
+void validate_periodic_inputs(int num_nodes, const double* cell, const double* inverse_cell, double cutoff)
+{
+    if (!std::isfinite(cutoff) || !(cutoff > 0.0))
+        throw std::invalid_argument("neighbor graph cutoff must be finite and positive");
+    if (num_nodes < 0 || num_nodes >= std::numeric_limits<int>::max())
+        throw std::length_error("neighbor graph exceeds 32-bit node indexing");
+    for (int i = 0; i < 9; ++i)
+        if (!std::isfinite(cell[i]) || !std::isfinite(inverse_cell[i]))
+            throw std::invalid_argument("neighbor graph cell must be finite");
+    for (int row = 0; row < 3; ++row)
+        for (int column = 0; column < 3; ++column) {
+            double product = 0.0;
+            for (int inner = 0; inner < 3; ++inner) product += cell[3 * row + inner] * inverse_cell[3 * inner + column];
+            if (std::abs(product - (row == column ? 1.0 : 0.0)) > 1e-9)
+                throw std::invalid_argument("neighbor graph cell and inverse cell are inconsistent");
+        }
+}
+
+void build_periodic_graph(const double* d_positions, int num_nodes, const double* cell, const double* inverse_cell,
+                          double cutoff, hipStream_t stream, PeriodicGraph& out)
+{
+    validate_periodic_inputs(num_nodes, cell, inverse_cell, cutoff);
+    const int N = num_nodes;
+    NeighborPlan plan;
+    plan.num_nodes = N;
+    std::memcpy(plan.cell, cell, sizeof(plan.cell));
+    std::memcpy(plan.inverse_cell, inverse_cell, sizeof(plan.inverse_cell));
+    plan.cutoff_squared = cutoff * cutoff;
+    for (int axis = 0; axis < 3; ++axis) {
+        double inverse_norm_squared = 0.0;
+        for (int component = 0; component < 3; ++component) {
+            const double v = inverse_cell[3 * component + axis];
+            inverse_norm_squared += v * v;
+        }
+        if (!(inverse_norm_squared > 0.0)) throw std::invalid_argument("neighbor graph cell must be invertible");
+        const double face_height = 1.0 / std::sqrt(inverse_norm_squared);
+        const double bins = std::floor(face_height / cutoff);
+        if (bins >= static_cast<double>(std::numeric_limits<int>::max()))
+            throw std::length_error("neighbor graph bin extent exceeds 32-bit indexing");
+        plan.bins[axis] = std::max(1, static_cast<int>(bins));
+        const double reach = std::ceil(cutoff * std::sqrt(inverse_norm_squared) * plan.bins[axis]) + 1.0;
+        if (reach >= static_cast<double>(std::numeric_limits<int>::max() / 2))
+            throw std::length_error("neighbor graph stencil exceeds 32-bit indexing");
+        plan.reach[axis] = std::max(1, static_cast<int>(reach));
+    }
+    const std::size_t num_bins_size =
+        static_cast<std::size_t>(plan.bins[0]) * plan.bins[1] * static_cast<std::size_t>(plan.bins[2]);
+    if (num_bins_size >= static_cast<std::size_t>(std::numeric_limits<int>::max()))
+        throw std::length_error("neighbor graph bin count exceeds 32-bit indexing");
+    const int num_bins = static_cast<int>(num_bins_size);
+    DeviceBuffer wp, wf, wrap, atom_bins, bin_sizes, bin_off64, bin_offsets, bin_atoms, counts, offsets, scratch;
+    wp.reserve(std::max(N, 1) * 3 * sizeof(double));
+    wf.reserve(std::max(N, 1) * 3 * sizeof(double));
+    wrap.reserve(std::max(N, 1) * 3 * sizeof(int));
+    atom_bins.reserve(std::max(N, 1) * sizeof(int));
+    bin_sizes.reserve((num_bins + 1) * sizeof(int));
+    bin_off64.reserve((num_bins + 1) * sizeof(long long));
+    bin_offsets.reserve((num_bins + 1) * sizeof(int));
+    bin_atoms.reserve(std::max(N, 1) * sizeof(int));
+    counts.reserve(std::max(N, 1) * sizeof(long long));
+    offsets.reserve((N + 1) * sizeof(long long));
+    scratch.reserve(scan_scratch_size(std::max(num_bins, N) + 1) * sizeof(long long));
+    hip_check(hipMemsetAsync(bin_sizes.as<void>(), 0, (num_bins + 1) * sizeof(int), stream), "memset");
+    hip_check(launch_neighbor_bins(plan, d_positions, wp.as<double>(), wf.as<double>(), wrap.as<int>(),
+                                   atom_bins.as<int>(), bin_sizes.as<int>(), stream),
+              "bins");
+    hip_check(launch_exclusive_scan_i32(bin_sizes.as<int>(), num_bins, bin_off64.as<long long>(),
+                                        scratch.as<long long>(), stream),
+              "bin scan");
+    hip_check(launch_narrow_offsets(bin_off64.as<long long>(), num_bins, bin_offsets.as<int>(), nullptr, stream),
+              "narrow");
+    // cursors start at the bin offsets
+    hip_check(hipMemcpyAsync(bin_sizes.as<int>(), bin_offsets.as<int>(), num_bins * sizeof(int),
+                             hipMemcpyDeviceToDevice, stream),
+              "cursors");
+    hip_check(launch_neighbor_fill_bins(plan, atom_bins.as<int>(), bin_offsets.as<int>(), bin_sizes.as<int>(),
+                                        bin_atoms.as<int>(), stream),
+              "fill bins");
+    hip_check(launch_sort_segments(num_bins, bin_offsets.as<int>(), bin_atoms.as<int>(), stream), "sort bins");
+    hip_check(launch_neighbor_edges(plan, wp.as<double>(), wf.as<double>(), wrap.as<int>(), atom_bins.as<int>(),
+                                    bin_offsets.as<int>(), bin_atoms.as<int>(), nullptr, counts.as<long long>(),
+                                    nullptr, nullptr, nullptr, stream),
+              "count edges");
+    hip_check(launch_exclusive_scan_i64(counts.as<long long>(), N, offsets.as<long long>(), scratch.as<long long>(),
+                                        stream),
+              "edge scan");
+    long long total = 0;
+    hip_check(hipMemcpyAsync(&total, offsets.as<long long>() + N, sizeof(long long), hipMemcpyDeviceToHost, stream),
+              "copy");
+    hip_check(hipStreamSynchronize(stream), "edge count");
+    if (total > std::numeric_limits<int>::max())
+        throw std::length_error("neighbor graph exceeds 32-bit edge indexing");
+    const int E = static_cast<int>(total);
+    out.first.reserve((N + 1) * sizeof(int));
+    hip_check(launch_narrow_offsets(offsets.as<long long>(), N, out.first.as<int>(), nullptr, stream), "narrow");
+    out.sources.reserve(std::max(E, 1) * sizeof(int));
+    out.shifts.reserve(std::max(E, 1) * 3 * sizeof(int));
+    out.fractional_xyz.reserve(std::max(E, 1) * 3 * sizeof(double));
+    hip_check(launch_neighbor_edges(plan, wp.as<double>(), wf.as<double>(), wrap.as<int>(), atom_bins.as<int>(),
+                                    bin_offsets.as<int>(), bin_atoms.as<int>(), offsets.as<long long>(), nullptr,
+                                    out.sources.as<int>(), out.shifts.as<int>(), out.fractional_xyz.as<double>(),
+                                    stream),
+              "fill edges");
+    hip_check(hipStreamSynchronize(stream), "graph build");
+    out.num_nodes = N;
+    out.num_edges = E;
+}
+
+std::uint64_t Evaluator::prepare_periodic_graph(int num_nodes, const int* node_types, const double* positions,
+                                                bool device_positions, const double* cell,
+                                                const double* inverse_cell, double cutoff)
+{
+    validate_periodic_inputs(num_nodes, cell, inverse_cell, cutoff);
+    std::vector<int> types(node_types, node_types + num_nodes);
+    prepare_active_types(types);
+    const int N = num_nodes;
+    positions_.reserve(std::max(N, 1) * 3 * sizeof(double));
+    if (N > 0)
+        hip_check(hipMemcpyAsync(positions_.as<double>(), positions, N * 3 * sizeof(double),
+                                 device_positions ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, stream_),
+                  "positions");
+    ref_positions_.reserve(std::max(N, 1) * 3 * sizeof(double));
+    if (N > 0)
+        hip_check(hipMemcpyAsync(ref_positions_.as<double>(), positions_.as<double>(), N * 3 * sizeof(double),
+                                 hipMemcpyDeviceToDevice, stream_),
+                  "positions");
+    build_periodic_graph(positions_.as<double>(), N, cell, inverse_cell, cutoff, stream_, pgraph_);
+    const int E = static_cast<int>(pgraph_.num_edges);
+    first_.reserve((N + 1) * sizeof(int));
+    hip_check(hipMemcpyAsync(first_.as<int>(), pgraph_.first.as<int>(), (N + 1) * sizeof(int),
+                             hipMemcpyDeviceToDevice, stream_),
+              "copy");
+    source_.reserve(std::max(E, 1) * sizeof(int));
+    if (E > 0)
+        hip_check(hipMemcpyAsync(source_.as<int>(), pgraph_.sources.as<int>(), E * sizeof(int),
+                                 hipMemcpyDeviceToDevice, stream_),
+                  "copy");
+    host_types_ = types;
+    num_nodes_ = N;
+    num_edges_ = E;
+    periodic_ = true;
+    std::memcpy(cell_, cell, sizeof(cell_));
+    std::memcpy(inverse_cell_, inverse_cell, sizeof(inverse_cell_));
+    upload(node_types_, types, stream_);
+    std::vector<double> cellv(cell, cell + 9);
+    upload(cell_dev_, cellv, stream_);
+    finish_graph(nullptr);
+    return generation_;
+}
+
+void Evaluator::update_cell(std::uint64_t generation, const double* cell, const double* inverse_cell)
+{
+    check_generation(generation);
+    if (!periodic_) throw std::invalid_argument("update_cell requires a periodic graph");
+    std::memcpy(cell_, cell, sizeof(cell_));
+    std::memcpy(inverse_cell_, inverse_cell, sizeof(inverse_cell_));
+    std::vector<double> cellv(cell, cell + 9);
+    upload(cell_dev_, cellv, stream_);
+}
+
+void Evaluator::graph_arrays(std::uint64_t generation, int* num_neigh, int* receiver_offsets, int* sources,
+                             int* shifts, double* fractional_xyz) const
+{
+    check_generation(generation);
+    const int N = num_nodes_;
+    const long long E = num_edges_;
+    std::vector<int> first(N + 1);
+    hip_check(hipMemcpyAsync(first.data(), first_.as<int>(), (N + 1) * sizeof(int), hipMemcpyDeviceToHost, stream_),
+              "copy");
+    if (sources && E)
+        hip_check(hipMemcpyAsync(sources, source_.as<int>(), E * sizeof(int), hipMemcpyDeviceToHost, stream_), "copy");
+    if (periodic_) {
+        if (shifts && E)
+            hip_check(hipMemcpyAsync(shifts, pgraph_.shifts.as<int>(), E * 3 * sizeof(int), hipMemcpyDeviceToHost,
+                                     stream_),
+                      "copy");
+        if (fractional_xyz && E)
+            hip_check(hipMemcpyAsync(fractional_xyz, pgraph_.fractional_xyz.as<double>(), E * 3 * sizeof(double),
+                                     hipMemcpyDeviceToHost, stream_),
+                      "copy");
+    }
+    hip_check(hipStreamSynchronize(stream_), "graph copy");
+    if (receiver_offsets) std::copy(first.begin(), first.end(), receiver_offsets);
+    if (num_neigh)
+        for (int i = 0; i < N; ++i) num_neigh[i] = first[i + 1] - first[i];
+}
+
+void Evaluator::compute_positions(std::uint64_t generation, const double* positions, bool device_positions)
+{
+    check_generation(generation);
+    if (!periodic_) throw std::invalid_argument("positions require a periodic graph; use edge vectors instead");
+    const int N = num_nodes_;
+    if (N > 0 && positions != positions_.as<double>())
+        hip_check(hipMemcpyAsync(positions_.as<double>(), positions, N * 3 * sizeof(double),
+                                 device_positions ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, stream_),
+                  "positions");
+    hip_check(launch_edge_geometry(static_cast<int>(num_edges_), receiver_.as<int>(), source_.as<int>(),
+                                   pgraph_.shifts.as<int>(), positions_.as<double>(), cell_dev_.as<double>(),
+                                   xyz_.as<double>(), r_.as<double>(), stream_),
+              "edge geometry");
+    evaluate();
+}
+
+void Evaluator::compute_xyz(std::uint64_t generation, const double* xyz, const double* r, bool device_arrays)
+{
+    check_generation(generation);
+    const long long E = num_edges_;
+    const hipMemcpyKind kind = device_arrays ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+    if (E > 0) {
+        hip_check(hipMemcpyAsync(xyz_.as<double>(), xyz, E * 3 * sizeof(double), kind, stream_), "xyz");
+        hip_check(hipMemcpyAsync(r_.as<double>(), r, E * sizeof(double), kind, stream_), "r");
+    }
+    evaluate();
+}
+
+double Evaluator::max_displacement(std::uint64_t generation, const double* positions, bool device_positions)
+{
+    check_generation(generation);
+    if (!periodic_) throw std::invalid_argument("displacements require a periodic graph");
+    const int N = num_nodes_;
+    if (N > 0 && positions != positions_.as<double>())
+        hip_check(hipMemcpyAsync(positions_.as<double>(), positions, N * 3 * sizeof(double),
+                                 device_positions ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, stream_),
+                  "positions");
+    hip_check(launch_max_displacement(N, positions_.as<double>(), ref_positions_.as<double>(),
+                                      totals_.as<double>() + 12, stream_),
+              "displacement");
+    double d2 = 0.0;
+    hip_check(hipMemcpyAsync(&d2, totals_.as<double>() + 12, sizeof(double), hipMemcpyDeviceToHost, stream_),
+              "copy");
+    hip_check(hipStreamSynchronize(stream_), "displacement");
+    return std::sqrt(d2);
+}
+
+void Evaluator::evaluate()
+{
+    const auto t0 = std::chrono::steady_clock::now();
+    const int N = num_nodes_;
+    const int E = static_cast<int>(num_edges_);
+    LayerArgs la;
+    la.graph.num_nodes = N;
+    la.graph.num_edges = E;
+    la.graph.node_types = node_types_.as<int>();
+    la.graph.type_active = type_active_.as<int>();
+    la.graph.num_active = static_cast<int>(active_types_.size());
+    la.graph.first = first_.as<int>();
+    la.graph.receiver = receiver_.as<int>();
+    la.graph.source = source_.as<int>();
+    la.graph.tfirst = tfirst_.as<int>();
+    la.graph.tedge = tedge_.as<int>();
+    la.graph.edge_pair = edge_pair_.as<int>();
+    la.graph.xyz = xyz_.as<double>();
+    la.graph.r = r_.as<double>();
+    la.grid = grid_;
+    la.C = C_;
+    la.l_max = model_.l_max;
+    la.L_max = model_.L_max;
+    la.node_offset = 0;
+    la.node_count = N;
+    hipStream_t s = stream_;
+    PolyTable p0{p0_terms_, p0_offsets_.as<int>(), p0_packed_.as<int>(), p0_coef_.as<float>()};
+    PolyTable p1{p1_terms_, p1_offsets_.as<int>(), p1_packed_.as<int>(), p1_coef_.as<float>()};
+    const long long nodeLM = static_cast<long long>(nLM_) * C_;
+    const long long nodelm = static_cast<long long>(nlm_) * C_;
+    const long long nodelme = static_cast<long long>(nlme_) * C_;
+
+    if (E > 0 || N > 0) {
+        // layer 0: A0 (folded H0, A0_W), M0, H1
+        hip_check(launch_a0_forward(la, r0f_.as<float>(), A0_.as<float>(), s), "A0 forward");
+        hip_check(launch_m0_forward(la, p0, A0_.as<float>(), M0_.as<float>(), s), "M0 forward");
+        for (int l = 0; l <= model_.L_max; ++l) {
+            GemmArgs g;
+            g.nodes = N;
+            g.rows_per_node = 2 * l + 1;
+            g.K = C_;
+            g.Ncols = C_;
+            g.a = {M0_.as<float>() + l * l * C_, nodeLM, C_};
+            g.B = h1w_.as<float>() + static_cast<std::size_t>(l) * C_ * C_;
+            g.c = {H1_.as<float>() + l * l * C_, nodeLM, C_};
+            hip_check(launch_gemm(g, s), "H1 gemm");
+        }
+        // layer 1: Phi1 -> A1
+        hip_check(launch_r1_forward(la, r1_.as<float>(), cg_.as<float>(), H1_.as<float>(), Phi1_.as<float>(), s),
+                  "R1 forward");
+        for (int l = 0; l <= model_.l_max; ++l) {
+            GemmArgs g;
+            g.nodes = N;
+            g.rows_per_node = 2 * l + 1;
+            g.K = num_e_[l] * C_;
+            g.Ncols = C_;
+            g.a = {Phi1_.as<float>() + static_cast<long long>(lme_off_[l]) * C_, nodelme,
+                   static_cast<long long>(num_e_[l]) * C_};
+            g.B = a1w_[l]->as<float>();
+            g.c = {A1_.as<float>() + l * l * C_, nodelm, C_};
+            if (num_e_[l] > 0) hip_check(launch_gemm(g, s), "A1 gemm");
+        }
+        // readout and its reverse down to A1_adj
+        ReadoutArgs ra;
+        ra.num_nodes = N;
+        ra.C = C_;
+        ra.num_lm = nlm_;
+        ra.num_LM = nLM_;
+        ra.hidden = model_.readout_hidden;
+        ra.node_types = node_types_.as<int>();
+        ra.type_active = type_active_.as<int>();
+        ra.A1 = A1_.as<float>();
+        ra.M0 = M0_.as<float>();
+        ra.p1 = p1;
+        ra.H2M0 = h2m0_.as<float>();
+        ra.H2M1 = h2m1_.as<float>();
+        ra.q = q_.as<float>();
+        ra.W1 = w1_.as<float>();
+        ra.W2 = w2_.as<float>();
+        ra.scale = static_cast<float>(model_.readout_scale);
+        ra.E0 = e0_.as<double>();
+        ra.energies = energies_.as<double>();
+        ra.direct = direct_.as<float>();
+        ra.A1_adj = A1adj_.as<float>();
+        hip_check(launch_readout(ra, s), "readout");
+        // dPhi1 = A1_adj A1_W^T  (into the Phi1 buffer, no longer needed)
+        float* dPhi1 = Phi1_.as<float>();
+        for (int l = 0; l <= model_.l_max; ++l) {
+            if (num_e_[l] == 0) continue;
+            GemmArgs g;
+            g.nodes = N;
+            g.rows_per_node = 2 * l + 1;
+            g.K = C_;
+            g.Ncols = num_e_[l] * C_;
+            g.a = {A1adj_.as<float>() + l * l * C_, nodelm, C_};
+            g.B = a1wt_[l]->as<float>();
+            g.c = {dPhi1 + static_cast<long long>(lme_off_[l]) * C_, nodelme, static_cast<long long>(num_e_[l]) * C_};
+            hip_check(launch_gemm(g, s), "A1 reverse gemm");
+        }
+        hip_check(launch_r1_reverse(la, r1_.as<float>(), cg_.as<float>(), H1_.as<float>(), dPhi1,
+                                    forces_.as<double>(), msg_.as<float>(), s),
+                  "R1 reverse");
+        hip_check(launch_gather_messages(la, msg_.as<float>(), H1adj_.as<float>(), s), "H1 adjoint gather");
+        // M0_adj = H1_adj H1_W^T (+ direct scalar adjoint), into the M0 buffer
+        float* M0adj = M0_.as<float>();
+        for (int l = 0; l <= model_.L_max; ++l) {
+            GemmArgs g;
+            g.nodes = N;
+            g.rows_per_node = 2 * l + 1;
+            g.K = C_;
+            g.Ncols = C_;
+            g.a = {H1adj_.as<float>() + l * l * C_, nodeLM, C_};
+            g.B = h1wt_.as<float>() + static_cast<std::size_t>(l) * C_ * C_;
+            g.c = {M0adj + l * l * C_, nodeLM, C_};
+            hip_check(launch_gemm(g, s), "H1 reverse gemm");
+        }
+        hip_check(launch_add_direct(N, C_, nLM_, direct_.as<float>(), M0adj, s), "direct adjoint");
+        // A0_adj into the A1 buffer (no longer needed)
+        float* A0adj = A1_.as<float>();
+        hip_check(launch_m0_reverse(la, p0, A0_.as<float>(), M0adj, A0adj, s), "M0 reverse");
+        hip_check(launch_a0_reverse(la, r0f_.as<float>(), A0adj, forces_.as<double>(), s), "A0 reverse");
+    }
+    hip_check(launch_atom_forces(N, first_.as<int>(), tfirst_.as<int>(), tedge_.as<int>(), forces_.as<double>(),
+                                 atom_forces_.as<double>(), s),
+              "atom forces");
+    // the evaluation (and any copy from caller-owned host arrays) has completed
+    // when this returns
+    hip_check(hipStreamSynchronize(s), "evaluation");
+    evaluated_generation_ = generation_;
+    reduced_ = false;
+    stats_.evaluations += 1;
+    stats_.last_evaluation_ms =
+        std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+}
+
+void Evaluator::reduce(double volume)
+{
+    if (evaluated_generation_ != generation_)
+        throw std::invalid_argument("results require a completed evaluation of the current graph");
+    if (reduced_ && reduced_volume_ == volume) return;
+    if (!std::isfinite(volume) || !(volume > 0.0))
+        throw std::invalid_argument("Stress reduction requires a positive finite volume.");
+    const int np = reduce_totals_partials(num_nodes_, static_cast<int>(num_edges_));
+    hip_check(launch_reduce_totals(num_nodes_, static_cast<int>(num_edges_), energies_.as<double>(),
+                                   forces_.as<double>(), xyz_.as<double>(), 1.0 / volume, partials_.as<double>(), np,
+                                   totals_.as<double>(), stream_),
+              "totals");
+    reduced_ = true;
+    reduced_volume_ = volume;
+}
+
+void Evaluator::synchronize() const { hip_check(hipStreamSynchronize(stream_), "synchronize"); }
+
+void Evaluator::node_energies(double* out) const
+{
+    if (evaluated_generation_ != generation_) throw std::invalid_argument("no completed evaluation");
+    if (num_nodes_ > 0)
+        hip_check(hipMemcpyAsync(out, energies_.as<double>(), num_nodes_ * sizeof(double), hipMemcpyDeviceToHost,
+                                 stream_),
+                  "copy");
+    synchronize();
+}
+
+void Evaluator::node_forces(double* out) const
+{
+    if (evaluated_generation_ != generation_) throw std::invalid_argument("no completed evaluation");
+    if (num_edges_ > 0)
+        hip_check(hipMemcpyAsync(out, forces_.as<double>(), num_edges_ * 3 * sizeof(double), hipMemcpyDeviceToHost,
+                                 stream_),
+                  "copy");
+    synchronize();
+}
+
+void Evaluator::atom_forces(std::uint64_t generation, double* out)
+{
+    check_generation(generation);
+    if (evaluated_generation_ != generation_)
+        throw std::invalid_argument("Atom-force reduction requires the current completed graph.");
+    if (num_nodes_ > 0)
+        hip_check(hipMemcpyAsync(out, atom_forces_.as<double>(), num_nodes_ * 3 * sizeof(double),
+                                 hipMemcpyDeviceToHost, stream_),
+                  "copy");
+    synchronize();
+}
+
+void Evaluator::stress(std::uint64_t generation, double volume, double* out9)
+{
+    check_generation(generation);
+    reduce(volume);
+    hip_check(hipMemcpyAsync(out9, totals_.as<double>() + 1, 9 * sizeof(double), hipMemcpyDeviceToHost, stream_),
+              "copy");
+    synchronize();
+}
+
+double Evaluator::total_energy(std::uint64_t generation)
+{
+    check_generation(generation);
+    reduce(reduced_ ? reduced_volume_ : 1.0);
+    double e = 0.0;
+    hip_check(hipMemcpyAsync(&e, totals_.as<double>(), sizeof(double), hipMemcpyDeviceToHost, stream_), "copy");
+    synchronize();
+    return e;
+}
+
+}  // namespace sxl

@@ -1,0 +1,163 @@
+// MI355X MACE evaluator: owns the device copy of a model and of one prepared
+// graph, and runs the energy + force evaluation on one HIP stream.
+//
+// The public surface mirrors the reference evaluator's prepared-graph API
+// (symmetrix/source/cpp/mace_kokkos.cpp:1561-1840, 2086-2203;
+// libsymmetrix/source/mace_kokkos.hpp:339-460): prepare a graph and receive a
+// generation token, set geometry (positions or edge vectors) for that token,
+// evaluate, then read node energies, directed edge forces, reduced atom
+// forces and the stress.  A stale token is rejected
+// (mace_kokkos_evaluate.cpp:326-334).  One evaluator is not thread-safe.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "kernels.hpp"
+#include "model.hpp"
+
+namespace sxl {
+
+class DeviceBuffer {
+public:
+    DeviceBuffer() = default;
+    DeviceBuffer(const DeviceBuffer&) = delete;
+    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+    ~DeviceBuffer();
+    void reserve(std::size_t bytes);  // grow-only
+    void release();
+    template <class T>
+    T* as() const { return static_cast<T*>(ptr_); }
+    std::size_t bytes() const { return bytes_; }
+
+private:
+    void* ptr_ = nullptr;
+    std::size_t bytes_ = 0;
+};
+
+// Periodic neighbour graph on the device (reference
+// build_periodic_neighbor_graph_kokkos, neighbor_graph_kokkos.cpp:38-405).
+struct PeriodicGraph {
+    int num_nodes = 0;
+    long long num_edges = 0;
+    DeviceBuffer first;           // [N+1] int
+    DeviceBuffer sources;         // [E] int
+    DeviceBuffer shifts;          // [E][3] int
+    DeviceBuffer fractional_xyz;  // [E][3] double
+};
+
+// Builds the graph of N positions (device pointer) with the given cell.
+// Validates inputs like the reference and throws on failure.
+void build_periodic_graph(const double* d_positions, int num_nodes, const double* cell,
+                          const double* inverse_cell, double cutoff, hipStream_t stream,
+                          PeriodicGraph& out);
+void validate_periodic_inputs(int num_nodes, const double* cell, const double* inverse_cell,
+                              double cutoff);
+
+struct EvaluatorStats {
+    std::size_t device_bytes = 0;
+    int last_num_nodes = 0;
+    int last_num_edges = 0;
+    int active_edges = 0;
+    double last_evaluation_ms = 0.0;
+    int graph_builds = 0;
+    int evaluations = 0;
+};
+
+class Evaluator {
+public:
+    Evaluator(const std::string& model_path, const std::string& head);
+    ~Evaluator();
+
+    const HostModel& model() const { return model_; }
+    hipStream_t stream() const { return stream_; }
+
+    // --- graphs -------------------------------------------------------------
+    // Receiver-major CSR given by the caller (neighbour lists of the caller,
+    // e.g. a LAMMPS full list): neigh_types are model element indices.
+    std::uint64_t prepare_graph(int num_nodes, const int* node_types, const int* num_neigh,
+                                const int* neigh_indices, const int* neigh_types);
+    // Periodic graph built on the device with cutoff + skin.  Positions are
+    // host or device pointers (device_positions).
+    std::uint64_t prepare_periodic_graph(int num_nodes, const int* node_types, const double* positions,
+                                         bool device_positions, const double* cell,
+                                         const double* inverse_cell, double cutoff);
+    void update_cell(std::uint64_t generation, const double* cell, const double* inverse_cell);
+    long long num_edges() const { return num_edges_; }
+    int num_nodes() const { return num_nodes_; }
+    std::uint64_t generation() const { return generation_; }
+    // Copies of the prepared periodic graph (host pointers, may be null).
+    void graph_arrays(std::uint64_t generation, int* num_neigh, int* receiver_offsets, int* sources,
+                      int* shifts, double* fractional_xyz) const;
+
+    // --- geometry + evaluation ----------------------------------------------
+    void compute_positions(std::uint64_t generation, const double* positions, bool device_positions);
+    void compute_xyz(std::uint64_t generation, const double* xyz, const double* r, bool device_arrays);
+    // Largest displacement (Angstrom) of positions from those of the last
+    // periodic graph build, on the device (for neighbour-list skin reuse).
+    double max_displacement(std::uint64_t generation, const double* positions, bool device_positions);
+
+    // --- results -------------------------------------------------------------
+    void node_energies(double* out) const;            // [N]
+    void node_forces(double* out) const;              // [E][3] directed, -dE/dxyz
+    void atom_forces(std::uint64_t generation, double* out);              // [N][3]
+    void stress(std::uint64_t generation, double volume, double* out9);   // 3x3 row-major
+    double total_energy(std::uint64_t generation);
+    // device pointers of the results (valid until the next call)
+    const double* device_atom_forces() const { return atom_forces_.as<double>(); }
+    const double* device_totals() const { return totals_.as<double>(); }
+    void synchronize() const;
+
+    const EvaluatorStats& stats() const { return stats_; }
+
+private:
+    void check_generation(std::uint64_t generation) const;
+    void prepare_active_types(const std::vector<int>& node_types);
+    void upload_static_tables();
+    void finish_graph(const int* host_neigh_types);
+    void allocate_workspace();
+    void evaluate();
+    void reduce(double volume);
+
+    HostModel model_;
+    hipStream_t stream_ = nullptr;
+    EvaluatorStats stats_;
+
+    // shape
+    int C_ = 0, nlm_ = 0, nLM_ = 0, nlme_ = 0;
+    std::vector<int> num_e_, lme_off_;
+
+    // model tables on the device
+    std::vector<int> active_types_;
+    DeviceBuffer type_active_, r0f_, r1_, p0_coef_, p0_packed_, p0_offsets_, p1_coef_, p1_packed_,
+        p1_offsets_, h2m0_, e0_;
+    DeviceBuffer h1w_, h1wt_, h2m1_, q_, w1_, w2_, cg_;
+    std::vector<std::unique_ptr<DeviceBuffer>> a1w_, a1wt_;
+    int p0_terms_ = 0, p1_terms_ = 0;
+    SplineGrid grid_;
+
+    // graph
+    std::uint64_t generation_ = 0;
+    std::uint64_t evaluated_generation_ = 0;
+    bool periodic_ = false;
+    int num_nodes_ = 0;
+    long long num_edges_ = 0;
+    std::vector<int> host_types_;
+    double cell_[9] = {}, inverse_cell_[9] = {};
+    PeriodicGraph pgraph_;
+    DeviceBuffer node_types_, first_, receiver_, source_, tfirst_, tedge_, edge_pair_, ref_positions_,
+        positions_, cell_dev_;
+    DeviceBuffer xyz_, r_;
+
+    // workspace
+    DeviceBuffer A0_, M0_, H1_, Phi1_, A1_, A1adj_, direct_, H1adj_, msg_, energies_, forces_,
+        atom_forces_, partials_, totals_, scratch_;
+    bool reduced_ = false;
+    double reduced_volume_ = 0.0;
+};
+
+}  // namespace sxl

@@ -1,0 +1,413 @@
+// Device graph construction: periodic cell-binned neighbour search, scans,
+// the receiver array and the deterministic source-major transpose.
+//
+// The neighbour search follows the reference's device algorithm
+// (libsymmetrix/source/neighbor_graph_kokkos.cpp:117-402): wrap to fractional
+// [0,1), bin, sort each bin ascending, and for every receiver walk the
+// dz -> dy -> dx stencil and each bin's atoms in ascending order, skipping the
+// self image and keeping d^2 <= cutoff^2.  Floating-point contraction is off
+// in this file (and the build passes -ffp-contract=off), so the double
+// arithmetic rounds exactly like the CPU restatement and the edge list is
+// bit-identical to it.
+#pragma clang fp contract(off)
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "kernels.hpp"
+
+namespace sxl {
+namespace {
+
+__device__ __forceinline__ int floor_div(int numerator, int denominator)
+{
+    const int quotient = numerator / denominator;
+    const int remainder = numerator % denominator;
+    return quotient - ((remainder != 0 && remainder < 0) ? 1 : 0);
+}
+
+__global__ void bins_kernel(NeighborPlan p, const double* __restrict__ pos, double* __restrict__ wp,
+                            double* __restrict__ wf, int* __restrict__ wrap, int* __restrict__ atom_bins,
+                            int* __restrict__ bin_sizes)
+{
+    const int atom = blockIdx.x * blockDim.x + threadIdx.x;
+    if (atom >= p.num_nodes) return;
+    double fractional[3];
+    for (int axis = 0; axis < 3; ++axis) {
+        double value = 0.0;
+        for (int component = 0; component < 3; ++component)
+            value += pos[3 * static_cast<size_t>(atom) + component] * p.inverse_cell[3 * component + axis];
+        const int w = static_cast<int>(floor(value));
+        value -= w;
+        fractional[axis] = value;
+        wf[3 * static_cast<size_t>(atom) + axis] = value;
+        wrap[3 * static_cast<size_t>(atom) + axis] = w;
+    }
+    for (int component = 0; component < 3; ++component) {
+        double value = 0.0;
+        for (int axis = 0; axis < 3; ++axis) value += fractional[axis] * p.cell[3 * axis + component];
+        wp[3 * static_cast<size_t>(atom) + component] = value;
+    }
+    const int x = min(p.bins[0] - 1, static_cast<int>(fractional[0] * p.bins[0]));
+    const int y = min(p.bins[1] - 1, static_cast<int>(fractional[1] * p.bins[1]));
+    const int z = min(p.bins[2] - 1, static_cast<int>(fractional[2] * p.bins[2]));
+    const int bin = static_cast<int>((static_cast<size_t>(z) * p.bins[1] + y) * p.bins[0] + x);
+    atom_bins[atom] = bin;
+    atomicAdd(&bin_sizes[bin], 1);
+}
+
+__global__ void fill_bins_kernel(int n, const int* __restrict__ atom_bins, int* __restrict__ cursors,
+                                 int* __restrict__ bin_atoms)
+{
+    const int atom = blockIdx.x * blockDim.x + threadIdx.x;
+    if (atom >= n) return;
+    const int index = atomicAdd(&cursors[atom_bins[atom]], 1);
+    bin_atoms[index] = atom;
+}
+
+__global__ void edges_kernel(NeighborPlan p, const double* __restrict__ wp,
+                             const double* __restrict__ wf, const int* __restrict__ wrap,
+                             const int* __restrict__ atom_bins, const int* __restrict__ bin_offsets,
+                             const int* __restrict__ bin_atoms, const long long* __restrict__ offsets,
+                             long long* __restrict__ counts, int* __restrict__ sources,
+                             int* __restrict__ shifts, double* __restrict__ frac)
+{
+    const int receiver = blockIdx.x * blockDim.x + threadIdx.x;
+    if (receiver >= p.num_nodes) return;
+    const bool fill = offsets != nullptr;
+    const int bx = p.bins[0], by = p.bins[1], bz = p.bins[2];
+    const int receiver_bin = atom_bins[receiver];
+    const int receiver_x = receiver_bin % bx;
+    const int receiver_y = (receiver_bin / bx) % by;
+    const int receiver_z = static_cast<int>(static_cast<size_t>(receiver_bin) /
+                                            (static_cast<size_t>(bx) * static_cast<size_t>(by)));
+    long long local = 0;
+    const long long out0 = fill ? offsets[receiver] : 0;
+    double rp[3];
+    for (int c = 0; c < 3; ++c) rp[c] = wp[3 * static_cast<size_t>(receiver) + c];
+    for (int dz = -p.reach[2]; dz <= p.reach[2]; ++dz) {
+        const int raw_z = receiver_z + dz;
+        const int shift_z = floor_div(raw_z, bz);
+        const int source_z = raw_z - shift_z * bz;
+        for (int dy = -p.reach[1]; dy <= p.reach[1]; ++dy) {
+            const int raw_y = receiver_y + dy;
+            const int shift_y = floor_div(raw_y, by);
+            const int source_y = raw_y - shift_y * by;
+            for (int dx = -p.reach[0]; dx <= p.reach[0]; ++dx) {
+                const int raw_x = receiver_x + dx;
+                const int shift_x = floor_div(raw_x, bx);
+                const int source_x = raw_x - shift_x * bx;
+                const int source_bin = static_cast<int>(
+                    (static_cast<size_t>(source_z) * by + source_y) * bx + source_x);
+                const int image[3] = {shift_x, shift_y, shift_z};
+                for (int index = bin_offsets[source_bin]; index < bin_offsets[source_bin + 1]; ++index) {
+                    const int source = bin_atoms[index];
+                    if (source == receiver && shift_x == 0 && shift_y == 0 && shift_z == 0) continue;
+                    double distance_squared = 0.0;
+                    for (int component = 0; component < 3; ++component) {
+                        double displacement = wp[3 * static_cast<size_t>(source) + component] - rp[component];
+                        for (int axis = 0; axis < 3; ++axis)
+                            displacement += image[axis] * p.cell[3 * axis + component];
+                        distance_squared += displacement * displacement;
+                    }
+                    if (distance_squared > p.cutoff_squared) continue;
+                    if (fill) {
+                        const size_t edge = static_cast<size_t>(out0 + local);
+                        sources[edge] = source;
+                        for (int axis = 0; axis < 3; ++axis) {
+                            shifts[3 * edge + axis] = image[axis] - wrap[3 * static_cast<size_t>(source) + axis] +
+                                                      wrap[3 * static_cast<size_t>(receiver) + axis];
+                            frac[3 * edge + axis] = wf[3 * static_cast<size_t>(source) + axis] -
+                                                    wf[3 * static_cast<size_t>(receiver) + axis] + image[axis];
+                        }
+                    }
+                    ++local;
+                }
+            }
+        }
+    }
+    if (!fill) counts[receiver] = local;
+}
+
+// ---- scans ---------------------------------------------------------------
+constexpr int kScanThreads = 256;
+constexpr int kScanItems = 4;
+constexpr int kScanSpan = kScanThreads * kScanItems;
+
+template <typename In>
+__global__ void __launch_bounds__(kScanThreads) scan_blocks_kernel(const In* __restrict__ in, int n,
+                                                                   long long* __restrict__ out,
+                                                                   long long* __restrict__ block_sums)
+{
+    __shared__ long long s[kScanThreads];
+    const int t = threadIdx.x;
+    const size_t base = static_cast<size_t>(blockIdx.x) * kScanSpan + static_cast<size_t>(t) * kScanItems;
+    long long v[kScanItems];
+    long long local = 0;
+    for (int q = 0; q < kScanItems; ++q) {
+        const size_t idx = base + q;
+        v[q] = idx < static_cast<size_t>(n) ? static_cast<long long>(in[idx]) : 0;
+        local += v[q];
+    }
+    s[t] = local;
+    __syncthreads();
+    for (int off = 1; off < kScanThreads; off <<= 1) {
+        const long long add = t >= off ? s[t - off] : 0;
+        __syncthreads();
+        s[t] += add;
+        __syncthreads();
+    }
+    long long run = s[t] - local;  // exclusive prefix of this thread
+    for (int q = 0; q < kScanItems; ++q) {
+        const size_t idx = base + q;
+        if (idx < static_cast<size_t>(n)) out[idx] = run;
+        run += v[q];
+    }
+    if (t == kScanThreads - 1) block_sums[blockIdx.x] = s[t];
+}
+
+// exclusive scan of block sums in place (one workgroup, sequential chunks);
+// writes the grand total to *total
+__global__ void __launch_bounds__(kScanThreads) scan_sums_kernel(long long* __restrict__ sums, int nb,
+                                                                 long long* __restrict__ total)
+{
+    __shared__ long long s[kScanThreads];
+    __shared__ long long carry;
+    const int t = threadIdx.x;
+    if (t == 0) carry = 0;
+    __syncthreads();
+    for (int base = 0; base < nb; base += kScanThreads) {
+        const int idx = base + t;
+        const long long v = idx < nb ? sums[idx] : 0;
+        s[t] = v;
+        __syncthreads();
+        for (int off = 1; off < kScanThreads; off <<= 1) {
+            const long long add = t >= off ? s[t - off] : 0;
+            __syncthreads();
+            s[t] += add;
+            __syncthreads();
+        }
+        if (idx < nb) sums[idx] = carry + s[t] - v;
+        __syncthreads();
+        if (t == kScanThreads - 1) carry += s[t];
+        __syncthreads();
+    }
+    if (t == 0) *total = carry;
+}
+
+__global__ void scan_add_kernel(long long* __restrict__ out, int n, const long long* __restrict__ sums)
+{
+    const size_t idx = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= static_cast<size_t>(n)) return;
+    out[idx] += sums[idx / kScanSpan];
+}
+
+template <typename In>
+hipError_t exclusive_scan(const In* in, int n, long long* out, long long* scratch, hipStream_t s)
+{
+    // out has n+1 entries; out[n] = total
+    const int nb = n > 0 ? (n + kScanSpan - 1) / kScanSpan : 0;
+    if (nb > 0) {
+        scan_blocks_kernel<In><<<nb, kScanThreads, 0, s>>>(in, n, out, scratch);
+        scan_sums_kernel<<<1, kScanThreads, 0, s>>>(scratch, nb, out + n);
+        scan_add_kernel<<<(n + 255) / 256, 256, 0, s>>>(out, n, scratch);
+    } else {
+        hipError_t err = hipMemsetAsync(out, 0, sizeof(long long), s);
+        if (err != hipSuccess) return err;
+    }
+    return hipGetLastError();
+}
+
+__global__ void narrow_kernel(const long long* __restrict__ offsets, int n, int* __restrict__ out,
+                              int* __restrict__ counts)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i > n) return;
+    out[i] = static_cast<int>(offsets[i]);
+    if (counts && i < n) counts[i] = static_cast<int>(offsets[i + 1] - offsets[i]);
+}
+
+__global__ void receivers_kernel(int n, const int* __restrict__ first, int* __restrict__ receiver)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    for (int e = first[i]; e < first[i + 1]; ++e) receiver[e] = i;
+}
+
+__global__ void transpose_count_kernel(int E, const int* __restrict__ source, int* __restrict__ counts)
+{
+    const int e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    atomicAdd(&counts[source[e]], 1);
+}
+
+__global__ void transpose_fill_kernel(int E, const int* __restrict__ source, const int* __restrict__ tfirst,
+                                      int* __restrict__ cursors, int* __restrict__ tedge)
+{
+    const int e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    const int s = source[e];
+    const int slot = atomicAdd(&cursors[s], 1);
+    tedge[tfirst[s] + slot] = e;
+}
+
+// insertion sort of each segment (ascending): makes atomic fill orders canonical
+__global__ void sort_segments_kernel(int nseg, const int* __restrict__ offsets, int* __restrict__ values)
+{
+    const int sgm = blockIdx.x * blockDim.x + threadIdx.x;
+    if (sgm >= nseg) return;
+    const int begin = offsets[sgm], end = offsets[sgm + 1];
+    for (int index = begin + 1; index < end; ++index) {
+        const int v = values[index];
+        int ins = index;
+        while (ins > begin && values[ins - 1] > v) {
+            values[ins] = values[ins - 1];
+            --ins;
+        }
+        values[ins] = v;
+    }
+}
+
+__global__ void max_displacement_kernel(int n, const double* __restrict__ a, const double* __restrict__ b,
+                                        unsigned long long* __restrict__ out)
+{
+    __shared__ double s[256];
+    const int t = threadIdx.x;
+    double m = 0.0;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + t; i < static_cast<size_t>(n);
+         i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+        const double dx = a[3 * i] - b[3 * i], dy = a[3 * i + 1] - b[3 * i + 1],
+                     dz = a[3 * i + 2] - b[3 * i + 2];
+        const double d2 = dx * dx + dy * dy + dz * dz;
+        m = d2 > m ? d2 : m;
+        if (d2 != d2) m = __longlong_as_double(0x7ff0000000000000LL);  // non-finite input: infinite
+    }
+    s[t] = m;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if (t < w) s[t] = s[t + w] > s[t] ? s[t + w] : s[t];
+        __syncthreads();
+    }
+    if (t == 0) atomicMax(out, static_cast<unsigned long long>(__double_as_longlong(s[0])));
+}
+
+__global__ void edge_pairs_kernel(int E, const int* __restrict__ receiver, const int* __restrict__ source,
+                                  const int* __restrict__ node_types, const int* __restrict__ type_active,
+                                  int n, int* __restrict__ edge_pair)
+{
+    const int e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    const int a = type_active[node_types[receiver[e]]];
+    const int b = type_active[node_types[source[e]]];
+    const int ordered = a * n + b;
+    const int unordered = a <= b ? a * (2 * n - a - 1) / 2 + b : b * (2 * n - b - 1) / 2 + a;
+    edge_pair[e] = ordered | (unordered << 16);
+}
+
+}  // namespace
+
+hipError_t launch_edge_pairs(int num_edges, const int* receiver, const int* source, const int* node_types,
+                             const int* type_active, int num_active, int* edge_pair, hipStream_t s)
+{
+    if (num_edges <= 0) return hipSuccess;
+    edge_pairs_kernel<<<(num_edges + 255) / 256, 256, 0, s>>>(num_edges, receiver, source, node_types,
+                                                              type_active, num_active, edge_pair);
+    return hipGetLastError();
+}
+
+hipError_t launch_neighbor_bins(const NeighborPlan& p, const double* positions, double* wrapped_positions,
+                                double* wrapped_fractional, int* wrap_shifts, int* atom_bins,
+                                int* bin_sizes, hipStream_t s)
+{
+    if (p.num_nodes <= 0) return hipSuccess;
+    bins_kernel<<<(p.num_nodes + 255) / 256, 256, 0, s>>>(p, positions, wrapped_positions,
+                                                          wrapped_fractional, wrap_shifts, atom_bins,
+                                                          bin_sizes);
+    return hipGetLastError();
+}
+
+hipError_t launch_neighbor_fill_bins(const NeighborPlan& p, const int* atom_bins, const int* bin_offsets,
+                                     int* bin_cursors, int* bin_atoms, hipStream_t s)
+{
+    (void)bin_offsets;
+    if (p.num_nodes <= 0) return hipSuccess;
+    fill_bins_kernel<<<(p.num_nodes + 255) / 256, 256, 0, s>>>(p.num_nodes, atom_bins, bin_cursors,
+                                                               bin_atoms);
+    return hipGetLastError();
+}
+
+hipError_t launch_neighbor_edges(const NeighborPlan& p, const double* wrapped_positions,
+                                 const double* wrapped_fractional, const int* wrap_shifts,
+                                 const int* atom_bins, const int* bin_offsets, const int* bin_atoms,
+                                 const long long* edge_offsets, long long* edge_counts, int* sources,
+                                 int* shifts, double* fractional_xyz, hipStream_t s)
+{
+    if (p.num_nodes <= 0) return hipSuccess;
+    edges_kernel<<<(p.num_nodes + 127) / 128, 128, 0, s>>>(
+        p, wrapped_positions, wrapped_fractional, wrap_shifts, atom_bins, bin_offsets, bin_atoms,
+        edge_offsets, edge_counts, sources, shifts, fractional_xyz);
+    return hipGetLastError();
+}
+
+std::size_t scan_scratch_size(int n) { return static_cast<std::size_t>(n / kScanSpan + 2); }
+
+hipError_t launch_exclusive_scan_i32(const int* in, int n, long long* out, long long* scratch,
+                                     hipStream_t s)
+{
+    return exclusive_scan<int>(in, n, out, scratch, s);
+}
+
+hipError_t launch_exclusive_scan_i64(const long long* in, int n, long long* out, long long* scratch,
+                                     hipStream_t s)
+{
+    return exclusive_scan<long long>(in, n, out, scratch, s);
+}
+
+hipError_t launch_narrow_offsets(const long long* offsets, int n, int* out_offsets, int* out_counts,
+                                 hipStream_t s)
+{
+    narrow_kernel<<<(n + 1 + 255) / 256, 256, 0, s>>>(offsets, n, out_offsets, out_counts);
+    return hipGetLastError();
+}
+
+hipError_t launch_receivers(int num_nodes, const int* first, int* receiver, hipStream_t s)
+{
+    if (num_nodes <= 0) return hipSuccess;
+    receivers_kernel<<<(num_nodes + 255) / 256, 256, 0, s>>>(num_nodes, first, receiver);
+    return hipGetLastError();
+}
+
+hipError_t launch_transpose_count(int num_edges, const int* source, int* counts, hipStream_t s)
+{
+    if (num_edges <= 0) return hipSuccess;
+    transpose_count_kernel<<<(num_edges + 255) / 256, 256, 0, s>>>(num_edges, source, counts);
+    return hipGetLastError();
+}
+
+hipError_t launch_transpose_fill(int num_edges, const int* source, const int* tfirst, int* cursors,
+                                 int* tedge, hipStream_t s)
+{
+    if (num_edges <= 0) return hipSuccess;
+    transpose_fill_kernel<<<(num_edges + 255) / 256, 256, 0, s>>>(num_edges, source, tfirst, cursors,
+                                                                  tedge);
+    return hipGetLastError();
+}
+
+hipError_t launch_sort_segments(int num_segments, const int* offsets, int* values, hipStream_t s)
+{
+    if (num_segments <= 0) return hipSuccess;
+    sort_segments_kernel<<<(num_segments + 127) / 128, 128, 0, s>>>(num_segments, offsets, values);
+    return hipGetLastError();
+}
+
+hipError_t launch_max_displacement(int n, const double* a, const double* b, double* out, hipStream_t s)
+{
+    hipError_t err = hipMemsetAsync(out, 0, sizeof(double), s);
+    if (err != hipSuccess || n <= 0) return err;
+    const int blocks = std::min((n + 255) / 256, 1024);
+    max_displacement_kernel<<<blocks, 256, 0, s>>>(n, a, b, reinterpret_cast<unsigned long long*>(out));
+    return hipGetLastError();
+}
+
+}  // namespace sxl

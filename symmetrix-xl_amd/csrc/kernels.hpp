@@ -1,0 +1,195 @@
+// Launch interface between the host evaluator and the gfx950 kernels.
+//
+// Data layout in HBM (channels fastest everywhere, so a workgroup whose
+// threads own channels reads and writes whole 128-byte lines):
+//   node features   A0, A1, A0_adj, A1_adj  [N][num_lm][C]
+//                   M0, H1, M0_adj, H1_adj  [N][num_LM][C]
+//                   Phi1, dPhi1             [N][num_lme][C]
+//   edge geometry   xyz [E][3] f64, r [E] f64
+//   directed forces f   [E][3] f64
+//   H1 messages     msg [E][num_LM][C] (H1-adjoint contributions per edge)
+//   spline tables   R0 folded per ordered active pair:
+//                     [pair_o][interval][4][l_max+1][C]
+//                   R1 per unordered active pair:
+//                     [pair_u][interval][4][num_paths][C]
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace sxl {
+
+struct EdgeGraph {
+    int num_nodes = 0;
+    int num_edges = 0;
+    const int* node_types = nullptr;   // [N] model element index
+    const int* type_active = nullptr;  // [num_elements] active index or -1
+    int num_active = 0;
+    const int* first = nullptr;        // [N+1] receiver offsets
+    const int* receiver = nullptr;     // [E]
+    const int* source = nullptr;       // [E]
+    const int* tfirst = nullptr;       // [N+1] source-major offsets
+    const int* tedge = nullptr;        // [E] edge ids grouped by source, ascending
+    const int* edge_pair = nullptr;    // [E] ordered pair | unordered pair << 16 (active types)
+    const double* xyz = nullptr;       // [E][3]
+    const double* r = nullptr;         // [E]
+};
+
+struct SplineGrid {
+    double x0 = 0.0;
+    double h = 0.0;
+    int intervals = 0;  // knots - 1
+    double r_cut = 0.0;
+};
+
+struct PolyTable {
+    int num_terms = 0;
+    const int* offsets = nullptr;  // [outputs+1]
+    const int* packed = nullptr;   // [terms] deg | i0<<4 | i1<<10 | i2<<16
+    const float* coef = nullptr;   // [active_type][terms][C]
+};
+
+struct GemmRows {
+    const float* ptr = nullptr;
+    long long node_stride = 0;  // floats between consecutive nodes
+    long long row_stride = 0;   // floats between consecutive rows of one node
+};
+
+struct GemmOut {
+    float* ptr = nullptr;
+    long long node_stride = 0;
+    long long row_stride = 0;
+};
+
+// out(node, m) = in(node, m) @ B (K x Ncols row-major)
+struct GemmArgs {
+    int nodes = 0;
+    int rows_per_node = 0;
+    int K = 0;
+    int Ncols = 0;
+    GemmRows a;
+    const float* B = nullptr;
+    GemmOut c;
+};
+
+hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream);
+
+struct LayerArgs {
+    EdgeGraph graph;
+    SplineGrid grid;
+    int C = 0;
+    int l_max = 0, L_max = 0;
+    int node_offset = 0;  // first receiver handled by this launch
+    int node_count = 0;   // receivers handled by this launch
+};
+
+// Layer 0: A0[i] = sum_j R0f_{pair(i,j)}(r) Y(r_hat)   (H0 and A0_W folded in)
+hipError_t launch_a0_forward(const LayerArgs& a, const float* r0f, float* A0, hipStream_t s);
+// M0 = P0(A0) per (node, LM, channel)
+hipError_t launch_m0_forward(const LayerArgs& a, const PolyTable& p0, const float* A0, float* M0,
+                             hipStream_t s);
+// Layer 1 forward: Phi1[i] = sum_j sum_terms cg R1 Y H1[src]
+hipError_t launch_r1_forward(const LayerArgs& a, const float* r1, const float* cg, const float* H1,
+                             float* Phi1, hipStream_t s);
+
+struct ReadoutArgs {
+    int num_nodes = 0;
+    int C = 0;
+    int num_lm = 0;
+    int num_LM = 0;
+    int hidden = 0;
+    const int* node_types = nullptr;
+    const int* type_active = nullptr;
+    const float* A1 = nullptr;      // [N][num_lm][C]
+    const float* M0 = nullptr;      // [N][num_LM][C] (scalar block = LM 0)
+    PolyTable p1;
+    const float* H2M0 = nullptr;    // [active][C][C]
+    const float* H2M1 = nullptr;    // [C][C]
+    const float* q = nullptr;       // [C]
+    const float* W1 = nullptr;      // [hidden][C]
+    const float* W2 = nullptr;      // [hidden]
+    float scale = 1.0f;
+    const double* E0 = nullptr;     // [active]
+    double* energies = nullptr;     // [N]
+    float* direct = nullptr;        // [N][C]
+    float* A1_adj = nullptr;        // [N][num_lm][C]
+};
+hipError_t launch_readout(const ReadoutArgs& a, hipStream_t s);
+
+// Layer 1 reverse: directed forces (stored) and per-edge H1-adjoint messages.
+hipError_t launch_r1_reverse(const LayerArgs& a, const float* r1, const float* cg, const float* H1,
+                             const float* dPhi1, double* forces, float* msg, hipStream_t s);
+// H1_adj[s] = sum over edges with source s of msg[e]
+hipError_t launch_gather_messages(const LayerArgs& a, const float* msg, float* H1_adj,
+                                  hipStream_t s);
+// M0_adj[:, LM 0, :] += direct
+hipError_t launch_add_direct(int nodes, int C, int num_LM, const float* direct, float* M0_adj,
+                             hipStream_t s);
+// A0_adj = sum_LM M0_adj[LM] dP0_LM/dA0
+hipError_t launch_m0_reverse(const LayerArgs& a, const PolyTable& p0, const float* A0,
+                             const float* M0_adj, float* A0_adj, hipStream_t s);
+// Layer 0 reverse: forces += -(dE/dxyz) through R0f and Y
+hipError_t launch_a0_reverse(const LayerArgs& a, const float* r0f, const float* A0_adj,
+                             double* forces, hipStream_t s);
+
+// Geometry from positions: xyz = pos[src] - pos[recv] + shift . cell
+hipError_t launch_edge_geometry(int num_edges, const int* receiver, const int* source,
+                                const int* shifts, const double* positions, const double* cell,
+                                double* xyz, double* r, hipStream_t s);
+
+// Reductions (deterministic, f64)
+hipError_t launch_atom_forces(int num_nodes, const int* first, const int* tfirst, const int* tedge,
+                              const double* forces, double* atom_forces, hipStream_t s);
+// partial sums per block then one final pass: out[0] = sum energies, out[1..9] = stress
+hipError_t launch_reduce_totals(int num_nodes, int num_edges, const double* energies,
+                                const double* forces, const double* xyz, double inv_volume,
+                                double* partials, int num_partials, double* out, hipStream_t s);
+int reduce_totals_partials(int num_nodes, int num_edges);
+
+// Neighbour graph construction (bit-identical to the reference's device
+// algorithm); see neighbor.hip.
+struct NeighborPlan {
+    int num_nodes = 0;
+    int bins[3] = {1, 1, 1};
+    int reach[3] = {1, 1, 1};
+    double cell[9] = {};
+    double inverse_cell[9] = {};
+    double cutoff_squared = 0.0;
+};
+hipError_t launch_neighbor_bins(const NeighborPlan& p, const double* positions,
+                                double* wrapped_positions, double* wrapped_fractional,
+                                int* wrap_shifts, int* atom_bins, int* bin_sizes, hipStream_t s);
+hipError_t launch_neighbor_fill_bins(const NeighborPlan& p, const int* atom_bins,
+                                     const int* bin_offsets, int* bin_cursors, int* bin_atoms,
+                                     hipStream_t s);
+hipError_t launch_neighbor_edges(const NeighborPlan& p, const double* wrapped_positions,
+                                 const double* wrapped_fractional, const int* wrap_shifts,
+                                 const int* atom_bins, const int* bin_offsets, const int* bin_atoms,
+                                 const long long* edge_offsets, long long* edge_counts, int* sources,
+                                 int* shifts, double* fractional_xyz, hipStream_t s);
+
+// Exclusive scans (int -> int64 offsets), scratch of scan_scratch_size() int64
+std::size_t scan_scratch_size(int n);
+hipError_t launch_exclusive_scan_i32(const int* in, int n, long long* out, long long* scratch,
+                                     hipStream_t s);
+hipError_t launch_exclusive_scan_i64(const long long* in, int n, long long* out, long long* scratch,
+                                     hipStream_t s);
+// int64 offsets -> int32 offsets and counts
+hipError_t launch_narrow_offsets(const long long* offsets, int n, int* out_offsets, int* out_counts,
+                                 hipStream_t s);
+// receiver ids per edge, and the source-major transpose (deterministic order)
+hipError_t launch_receivers(int num_nodes, const int* first, int* receiver, hipStream_t s);
+hipError_t launch_transpose_count(int num_edges, const int* source, int* counts, hipStream_t s);
+hipError_t launch_transpose_fill(int num_edges, const int* source, const int* tfirst, int* cursors,
+                                 int* tedge, hipStream_t s);
+hipError_t launch_sort_segments(int num_segments, const int* offsets, int* values, hipStream_t s);
+hipError_t launch_max_displacement(int n, const double* a, const double* b, double* out,
+                                   hipStream_t s);
+// edge_pair[e] = ordered | unordered << 16 from the active indices of the
+// receiver and source element types
+hipError_t launch_edge_pairs(int num_edges, const int* receiver, const int* source,
+                             const int* node_types, const int* type_active, int num_active,
+                             int* edge_pair, hipStream_t s);
+
+}  // namespace sxl

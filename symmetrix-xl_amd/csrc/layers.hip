@@ -1,0 +1,1028 @@
+// gfx950 kernels of the MACE energy + force evaluation.
+//
+// Edge stages are receiver-owned: one workgroup per receiver, one thread per
+// channel.  The edges of the receiver are processed in tiles: in a tile
+// prologue one thread per edge forms the edge's geometry (spline interval,
+// harmonics, their gradients, and for the second interaction the products
+// cg_t * Y[lm1_t]) into LDS; the channel threads then stream the tile's edges,
+// evaluating the radial splines from the coefficient tables and accumulating
+// into registers.  No graph-wide edge state is materialised in the forward
+// pass; the reverse pass writes the directed force of each edge and, for the
+// second interaction, the edge's H1-adjoint contribution (gathered per source
+// afterwards in a fixed order, so results are run-to-run deterministic).
+//
+// Reference semantics (libsymmetrix/source/mace.cpp): compute_A0_streamed
+// :1355-1403, compute_M0 :1638-1662, compute_Phi1_streamed :2022-2083,
+// compute_M1/H2/readouts and reverse_H2/M1 :2460-2657,
+// reverse_Phi1_streamed :2198-2302, reverse_M0 :1664-1688,
+// reverse_A0_streamed :1485-1559; reductions mace_kokkos_evaluate.cpp:48-291.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "device_math.hpp"
+#include "kernels.hpp"
+#include "r1_shapes.inc"
+
+namespace sxl {
+namespace {
+
+constexpr int kMaxWaves = 4;  // 256 threads
+
+__device__ __forceinline__ int receiver_of_block(const LayerArgs& a)
+{
+    return a.node_offset + xcd_contiguous(blockIdx.x, a.node_count);
+}
+
+// ---------------------------------------------------------------------------
+// Layer 0 forward: A0[i, lm, k] = sum_j R0f_{pair}(r_ij)[l, k] Y_lm(r_ij)
+// ---------------------------------------------------------------------------
+template <int LMAX>
+__global__ void __launch_bounds__(256) a0_forward_kernel(LayerArgs a, const float* __restrict__ r0f,
+                                                          float* __restrict__ A0)
+{
+    constexpr int NLM = (LMAX + 1) * (LMAX + 1);
+    constexpr int NL = LMAX + 1;
+    constexpr int TE = 64;
+    __shared__ float s_Y[TE][NLM];
+    __shared__ float s_x[TE];
+    __shared__ int s_iv[TE];
+    __shared__ int s_pair[TE];
+
+    const int i = receiver_of_block(a);
+    const int k = threadIdx.x;
+    const int C = a.C;
+    const EdgeGraph& g = a.graph;
+    float acc[NLM];
+#pragma unroll
+    for (int lm = 0; lm < NLM; ++lm) acc[lm] = 0.0f;
+    const int e0 = g.first[i], e1 = g.first[i + 1];
+    const size_t interval_stride = static_cast<size_t>(4) * NL * C;
+    const size_t pair_stride = static_cast<size_t>(a.grid.intervals) * interval_stride;
+    for (int base = e0; base < e1; base += TE) {
+        const int n = min(TE, e1 - base);
+        __syncthreads();
+        if (threadIdx.x < n) {
+            const int t = threadIdx.x;
+            const int e = base + t;
+            const double rr = g.r[e];
+            int iv = -1;
+            if (rr < a.grid.r_cut) {
+                float x, Y[NLM], dir[3];
+                spline_point(rr, a.grid, iv, x);
+                edge_harmonics<LMAX, false>(g.xyz + 3 * static_cast<size_t>(e), rr, Y, nullptr,
+                                            nullptr, nullptr, dir);
+                s_x[t] = x;
+                s_pair[t] = g.edge_pair[e] & 0xffff;
+#pragma unroll
+                for (int lm = 0; lm < NLM; ++lm) s_Y[t][lm] = Y[lm];
+            }
+            s_iv[t] = iv;
+        }
+        __syncthreads();
+        if (k < C) {
+            for (int j = 0; j < n; ++j) {
+                const int iv = s_iv[j];
+                if (iv < 0) continue;
+                const float x = s_x[j];
+                const float* c = r0f + s_pair[j] * pair_stride + iv * interval_stride + k;
+#pragma unroll
+                for (int l = 0; l <= LMAX; ++l) {
+                    const float c0 = c[(0 * NL + l) * C];
+                    const float c1 = c[(1 * NL + l) * C];
+                    const float c2 = c[(2 * NL + l) * C];
+                    const float c3 = c[(3 * NL + l) * C];
+                    const float R = c0 + x * (c1 + x * (c2 + x * c3));
+#pragma unroll
+                    for (int lm = l * l; lm < (l + 1) * (l + 1); ++lm) acc[lm] += R * s_Y[j][lm];
+                }
+            }
+        }
+    }
+    if (k < C) {
+        float* out = A0 + static_cast<size_t>(i) * NLM * C + k;
+#pragma unroll
+        for (int lm = 0; lm < NLM; ++lm) out[lm * C] = acc[lm];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Symmetric contraction polynomials.  Each thread owns one channel; its
+// inputs live in an LDS column so that runtime monomial indices address LDS,
+// not registers.
+// ---------------------------------------------------------------------------
+// coef: this channel's coefficients, term stride C; x: LDS column, stride xs
+__device__ __forceinline__ float poly_value(const PolyTable& p, const float* __restrict__ coef,
+                                            int C, int begin, int end, const float* x, int xs)
+{
+    float f = 0.0f;
+    for (int t = begin; t < end; ++t) {
+        const int pk = p.packed[t];
+        const int deg = pk & 15;
+        float v = coef[static_cast<size_t>(t) * C] * x[((pk >> 4) & 63) * xs];
+        if (deg > 1) v *= x[((pk >> 10) & 63) * xs];
+        if (deg > 2) v *= x[((pk >> 16) & 63) * xs];
+        f += v;
+    }
+    return f;
+}
+
+// g[v] += lambda * dP/dx_v  (LDS column, owner thread only)
+__device__ __forceinline__ void poly_gradient(const PolyTable& p, const float* __restrict__ coef,
+                                              int C, int begin, int end, const float* x, float* g,
+                                              float lambda, int xs)
+{
+    for (int t = begin; t < end; ++t) {
+        const int pk = p.packed[t];
+        const int deg = pk & 15;
+        const int i0 = ((pk >> 4) & 63) * xs;
+        const float c = coef[static_cast<size_t>(t) * C] * lambda;
+        if (deg == 1) {
+            g[i0] += c;
+        } else if (deg == 2) {
+            const int i1 = ((pk >> 10) & 63) * xs;
+            const float x0 = x[i0], x1 = x[i1];
+            g[i0] += c * x1;
+            g[i1] += c * x0;
+        } else {
+            const int i1 = ((pk >> 10) & 63) * xs;
+            const int i2 = ((pk >> 16) & 63) * xs;
+            const float x0 = x[i0], x1 = x[i1], x2 = x[i2];
+            g[i0] += c * x1 * x2;
+            g[i1] += c * x0 * x2;
+            g[i2] += c * x0 * x1;
+        }
+    }
+}
+
+__global__ void __launch_bounds__(256) m0_forward_kernel(LayerArgs a, PolyTable p,
+                                                          const float* __restrict__ A0,
+                                                          float* __restrict__ M0)
+{
+    extern __shared__ float s_mem[];
+    const int i = a.node_offset + xcd_contiguous(blockIdx.x, a.node_count);
+    const int k = threadIdx.x;
+    const int C = a.C;
+    if (k >= C) return;
+    const int nlm = (a.l_max + 1) * (a.l_max + 1);
+    const int nLM = (a.L_max + 1) * (a.L_max + 1);
+    const int stride = blockDim.x;
+    float* x = s_mem + k;
+    const float* in = A0 + static_cast<size_t>(i) * nlm * C + k;
+    for (int lm = 0; lm < nlm; ++lm) x[lm * stride] = in[lm * C];
+    const int at = a.graph.type_active[a.graph.node_types[i]];
+    const float* coef = p.coef + static_cast<size_t>(at) * p.num_terms * C + k;
+    float* out = M0 + static_cast<size_t>(i) * nLM * C + k;
+    for (int LM = 0; LM < nLM; ++LM)
+        out[LM * C] = poly_value(p, coef, C, p.offsets[LM], p.offsets[LM + 1], x, stride);
+}
+
+__global__ void __launch_bounds__(256) m0_reverse_kernel(LayerArgs a, PolyTable p,
+                                                          const float* __restrict__ A0,
+                                                          const float* __restrict__ M0_adj,
+                                                          float* __restrict__ A0_adj)
+{
+    extern __shared__ float s_mem[];
+    const int i = a.node_offset + xcd_contiguous(blockIdx.x, a.node_count);
+    const int k = threadIdx.x;
+    const int C = a.C;
+    if (k >= C) return;
+    const int nlm = (a.l_max + 1) * (a.l_max + 1);
+    const int nLM = (a.L_max + 1) * (a.L_max + 1);
+    const int stride = blockDim.x;
+    float* x = s_mem + k;
+    float* gsum = s_mem + static_cast<size_t>(nlm) * stride + k;
+    const float* in = A0 + static_cast<size_t>(i) * nlm * C + k;
+    for (int lm = 0; lm < nlm; ++lm) {
+        x[lm * stride] = in[lm * C];
+        gsum[lm * stride] = 0.0f;
+    }
+    const int at = a.graph.type_active[a.graph.node_types[i]];
+    const float* coef = p.coef + static_cast<size_t>(at) * p.num_terms * C + k;
+    const float* lam = M0_adj + static_cast<size_t>(i) * nLM * C + k;
+    for (int LM = 0; LM < nLM; ++LM)
+        poly_gradient(p, coef, C, p.offsets[LM], p.offsets[LM + 1], x, gsum, lam[LM * C], stride);
+    float* out = A0_adj + static_cast<size_t>(i) * nlm * C + k;
+    for (int lm = 0; lm < nlm; ++lm) out[lm * C] = gsum[lm * stride];
+}
+
+// ---------------------------------------------------------------------------
+// Layer 1 forward: Phi1[i, lme, k] = sum_j sum_t cg_t Y_{lm1_t} R1_{p_t}(r)[k] H1[src, lm2_t, k]
+// ---------------------------------------------------------------------------
+template <class S>
+__global__ void __launch_bounds__(256) r1_forward_kernel(LayerArgs a, const float* __restrict__ r1,
+                                                          const float* __restrict__ cg,
+                                                          const float* __restrict__ H1,
+                                                          float* __restrict__ Phi1)
+{
+    constexpr int NLM = (S::LMAX + 1) * (S::LMAX + 1);
+    constexpr int NLMS = (S::LLMAX + 1) * (S::LLMAX + 1);
+    constexpr int NP = S::NP;
+    constexpr int NT = S::NT;
+    constexpr int TE = 32;
+    __shared__ float s_cgY[TE][(NT + 3) / 4 * 4];
+    __shared__ float s_x[TE];
+    __shared__ int s_iv[TE];
+    __shared__ int s_pair[TE];
+    __shared__ int s_src[TE];
+
+    const int i = receiver_of_block(a);
+    const int k = threadIdx.x;
+    const int C = a.C;
+    const EdgeGraph& g = a.graph;
+    float acc[S::NLME];
+#pragma unroll
+    for (int q = 0; q < S::NLME; ++q) acc[q] = 0.0f;
+    const int e0 = g.first[i], e1 = g.first[i + 1];
+    const size_t interval_stride = static_cast<size_t>(4) * NP * C;
+    const size_t pair_stride = static_cast<size_t>(a.grid.intervals) * interval_stride;
+    for (int base = e0; base < e1; base += TE) {
+        const int n = min(TE, e1 - base);
+        __syncthreads();
+        if (threadIdx.x < n) {
+            const int t = threadIdx.x;
+            const int e = base + t;
+            const double rr = g.r[e];
+            int iv = -1;
+            if (rr < a.grid.r_cut) {
+                float x, Y[NLM], dir[3];
+                spline_point(rr, a.grid, iv, x);
+                edge_harmonics<S::LMAX, false>(g.xyz + 3 * static_cast<size_t>(e), rr, Y, nullptr,
+                                               nullptr, nullptr, dir);
+                s_x[t] = x;
+                s_pair[t] = g.edge_pair[e] >> 16;
+                s_src[t] = g.source[e];
+#pragma unroll
+                for (int q = 0; q < NT; ++q) s_cgY[t][q] = cg[q] * Y[S::term_lm1[q]];
+            }
+            s_iv[t] = iv;
+        }
+        __syncthreads();
+        if (k < C) {
+            for (int j = 0; j < n; ++j) {
+                const int iv = s_iv[j];
+                if (iv < 0) continue;
+                const float x = s_x[j];
+                const float* c = r1 + s_pair[j] * pair_stride + iv * interval_stride + k;
+                float R[NP];
+#pragma unroll
+                for (int p = 0; p < NP; ++p) {
+                    const float c0 = c[(0 * NP + p) * C];
+                    const float c1 = c[(1 * NP + p) * C];
+                    const float c2 = c[(2 * NP + p) * C];
+                    const float c3 = c[(3 * NP + p) * C];
+                    R[p] = c0 + x * (c1 + x * (c2 + x * c3));
+                }
+                const float* hs = H1 + static_cast<size_t>(s_src[j]) * NLMS * C + k;
+                float H[NLMS];
+#pragma unroll
+                for (int q = 0; q < NLMS; ++q) H[q] = hs[q * C];
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+                    acc[S::term_lme[t]] += s_cgY[j][t] * (R[S::term_p[t]] * H[S::term_lm2[t]]);
+            }
+        }
+    }
+    if (k < C) {
+        float* out = Phi1 + static_cast<size_t>(i) * S::NLME * C + k;
+#pragma unroll
+        for (int q = 0; q < S::NLME; ++q) out[q * C] = acc[q];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Layer 1 reverse.  With dPhi1 of the receiver in registers, per edge:
+//   s[p,lm2] = sum_t cg_t Y_lm1 dPhi1[lme_t]          (t in path p, source lm2)
+//   msg[lm2] = sum_p R_p s[p,lm2]                      -> H1 adjoint of the source
+//   A        = sum_{p,lm2} R'_p H[lm2] s[p,lm2]
+//   U[lm1]   = sum_t cg_t R_p H[lm2_t] dPhi1[lme_t]
+//   f_edge   = -sum_k (r_hat A + sum_lm1 dY[lm1] U[lm1])
+// ---------------------------------------------------------------------------
+template <class S>
+__global__ void __launch_bounds__(256) r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
+                                                         const float* __restrict__ cg,
+                                                         const float* __restrict__ H1,
+                                                         const float* __restrict__ dPhi1,
+                                                         double* __restrict__ forces,
+                                                         float* __restrict__ msg)
+{
+    constexpr int NLM = (S::LMAX + 1) * (S::LMAX + 1);
+    constexpr int NLMS = (S::LLMAX + 1) * (S::LLMAX + 1);
+    constexpr int NP = S::NP;
+    constexpr int NT = S::NT;
+    constexpr int TE = 16;
+    __shared__ float s_cgY[TE][(NT + 3) / 4 * 4];
+    __shared__ float s_dY[TE][3][NLM];
+    __shared__ float s_dir[TE][3];
+    __shared__ float s_x[TE];
+    __shared__ int s_iv[TE];
+    __shared__ int s_pair[TE];
+    __shared__ int s_src[TE];
+    __shared__ float s_f[TE][kMaxWaves][3];
+
+    const int i = receiver_of_block(a);
+    const int k = threadIdx.x;
+    const int C = a.C;
+    const int wave = threadIdx.x >> 6;
+    const int nwaves = blockDim.x >> 6;
+    const EdgeGraph& g = a.graph;
+    float dphi[S::NLME];
+    if (k < C) {
+        const float* in = dPhi1 + static_cast<size_t>(i) * S::NLME * C + k;
+#pragma unroll
+        for (int q = 0; q < S::NLME; ++q) dphi[q] = in[q * C];
+    } else {
+#pragma unroll
+        for (int q = 0; q < S::NLME; ++q) dphi[q] = 0.0f;
+    }
+    const int e0 = g.first[i], e1 = g.first[i + 1];
+    const size_t interval_stride = static_cast<size_t>(4) * NP * C;
+    const size_t pair_stride = static_cast<size_t>(a.grid.intervals) * interval_stride;
+    for (int base = e0; base < e1; base += TE) {
+        const int n = min(TE, e1 - base);
+        __syncthreads();
+        if (threadIdx.x < n) {
+            const int t = threadIdx.x;
+            const int e = base + t;
+            const double rr = g.r[e];
+            int iv = -1;
+            if (rr < a.grid.r_cut) {
+                float x, Y[NLM], dx[NLM], dy[NLM], dz[NLM], dir[3];
+                spline_point(rr, a.grid, iv, x);
+                edge_harmonics<S::LMAX, true>(g.xyz + 3 * static_cast<size_t>(e), rr, Y, dx, dy, dz,
+                                              dir);
+                s_x[t] = x;
+                s_pair[t] = g.edge_pair[e] >> 16;
+                s_src[t] = g.source[e];
+                s_dir[t][0] = dir[0];
+                s_dir[t][1] = dir[1];
+                s_dir[t][2] = dir[2];
+#pragma unroll
+                for (int lm = 0; lm < NLM; ++lm) {
+                    s_dY[t][0][lm] = dx[lm];
+                    s_dY[t][1][lm] = dy[lm];
+                    s_dY[t][2][lm] = dz[lm];
+                }
+#pragma unroll
+                for (int q = 0; q < NT; ++q) s_cgY[t][q] = cg[q] * Y[S::term_lm1[q]];
+            }
+            s_iv[t] = iv;
+        }
+        __syncthreads();
+        for (int j = 0; j < n; ++j) {
+            const int iv = s_iv[j];
+            if (iv < 0) continue;
+            float fx = 0.0f, fy = 0.0f, fz = 0.0f;
+            if (k < C) {
+                const float x = s_x[j];
+                const float* c = r1 + s_pair[j] * pair_stride + iv * interval_stride + k;
+                float R[NP], dR[NP];
+#pragma unroll
+                for (int p = 0; p < NP; ++p) {
+                    const float c0 = c[(0 * NP + p) * C];
+                    const float c1 = c[(1 * NP + p) * C];
+                    const float c2 = c[(2 * NP + p) * C];
+                    const float c3 = c[(3 * NP + p) * C];
+                    R[p] = c0 + x * (c1 + x * (c2 + x * c3));
+                    dR[p] = c1 + x * (2.0f * c2 + 3.0f * x * c3);
+                }
+                const int src = s_src[j];
+                const float* hs = H1 + static_cast<size_t>(src) * NLMS * C + k;
+                float H[NLMS];
+#pragma unroll
+                for (int q = 0; q < NLMS; ++q) H[q] = hs[q * C];
+                float s[NP][NLMS];
+                float U[NLM];
+#pragma unroll
+                for (int p = 0; p < NP; ++p)
+#pragma unroll
+                    for (int q = 0; q < NLMS; ++q) s[p][q] = 0.0f;
+#pragma unroll
+                for (int lm = 0; lm < NLM; ++lm) U[lm] = 0.0f;
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    const int p = S::term_p[t];
+                    const int q = S::term_lm2[t];
+                    const float d = dphi[S::term_lme[t]];
+                    s[p][q] += s_cgY[j][t] * d;
+                    U[S::term_lm1[t]] += cg[t] * (R[p] * H[q] * d);
+                }
+                float m[NLMS];
+#pragma unroll
+                for (int q = 0; q < NLMS; ++q) m[q] = 0.0f;
+                float A = 0.0f;
+#pragma unroll
+                for (int p = 0; p < NP; ++p) {
+                    const int l2 = S::path_l2[p];
+#pragma unroll
+                    for (int q = 0; q < NLMS; ++q) {
+                        if (q < l2 * l2 || q >= (l2 + 1) * (l2 + 1)) continue;
+                        m[q] += R[p] * s[p][q];
+                        A += dR[p] * H[q] * s[p][q];
+                    }
+                }
+                float* mo = msg + (static_cast<size_t>(base + j) * NLMS) * C + k;
+#pragma unroll
+                for (int q = 0; q < NLMS; ++q) mo[q * C] = m[q];
+                float gx = 0.0f, gy = 0.0f, gz = 0.0f;
+#pragma unroll
+                for (int lm = 0; lm < NLM; ++lm) {
+                    gx += s_dY[j][0][lm] * U[lm];
+                    gy += s_dY[j][1][lm] * U[lm];
+                    gz += s_dY[j][2][lm] * U[lm];
+                }
+                fx = -(s_dir[j][0] * A + gx);
+                fy = -(s_dir[j][1] * A + gy);
+                fz = -(s_dir[j][2] * A + gz);
+            }
+            fx = wave_sum(fx);
+            fy = wave_sum(fy);
+            fz = wave_sum(fz);
+            if ((threadIdx.x & 63) == 0) {
+                s_f[j][wave][0] = fx;
+                s_f[j][wave][1] = fy;
+                s_f[j][wave][2] = fz;
+            }
+        }
+        __syncthreads();
+        if (threadIdx.x < n) {
+            const int t = threadIdx.x;
+            double f[3] = {0.0, 0.0, 0.0};
+            if (s_iv[t] >= 0)
+                for (int w = 0; w < nwaves; ++w)
+                    for (int c = 0; c < 3; ++c) f[c] += static_cast<double>(s_f[t][w][c]);
+            double* out = forces + 3 * static_cast<size_t>(base + t);
+            out[0] = f[0];
+            out[1] = f[1];
+            out[2] = f[2];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Layer 0 reverse: f_ij += -sum_{lm,k} A0_adj[i,lm,k] (r_hat R0f' Y_lm + R0f dY_lm)
+// ---------------------------------------------------------------------------
+template <int LMAX>
+__global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const float* __restrict__ r0f,
+                                                          const float* __restrict__ A0_adj,
+                                                          double* __restrict__ forces)
+{
+    constexpr int NLM = (LMAX + 1) * (LMAX + 1);
+    constexpr int NL = LMAX + 1;
+    constexpr int TE = 32;
+    __shared__ float s_Y[TE][NLM];
+    __shared__ float s_dY[TE][3][NLM];
+    __shared__ float s_dir[TE][3];
+    __shared__ float s_x[TE];
+    __shared__ int s_iv[TE];
+    __shared__ int s_pair[TE];
+    __shared__ float s_f[TE][kMaxWaves][3];
+
+    const int i = receiver_of_block(a);
+    const int k = threadIdx.x;
+    const int C = a.C;
+    const int wave = threadIdx.x >> 6;
+    const int nwaves = blockDim.x >> 6;
+    const EdgeGraph& g = a.graph;
+    float adj[NLM];
+    if (k < C) {
+        const float* in = A0_adj + static_cast<size_t>(i) * NLM * C + k;
+#pragma unroll
+        for (int lm = 0; lm < NLM; ++lm) adj[lm] = in[lm * C];
+    } else {
+#pragma unroll
+        for (int lm = 0; lm < NLM; ++lm) adj[lm] = 0.0f;
+    }
+    const int e0 = g.first[i], e1 = g.first[i + 1];
+    const size_t interval_stride = static_cast<size_t>(4) * NL * C;
+    const size_t pair_stride = static_cast<size_t>(a.grid.intervals) * interval_stride;
+    for (int base = e0; base < e1; base += TE) {
+        const int n = min(TE, e1 - base);
+        __syncthreads();
+        if (threadIdx.x < n) {
+            const int t = threadIdx.x;
+            const int e = base + t;
+            const double rr = g.r[e];
+            int iv = -1;
+            if (rr < a.grid.r_cut) {
+                float x, Y[NLM], dx[NLM], dy[NLM], dz[NLM], dir[3];
+                spline_point(rr, a.grid, iv, x);
+                edge_harmonics<LMAX, true>(g.xyz + 3 * static_cast<size_t>(e), rr, Y, dx, dy, dz,
+                                           dir);
+                s_x[t] = x;
+                s_pair[t] = g.edge_pair[e] & 0xffff;
+                s_dir[t][0] = dir[0];
+                s_dir[t][1] = dir[1];
+                s_dir[t][2] = dir[2];
+#pragma unroll
+                for (int lm = 0; lm < NLM; ++lm) {
+                    s_Y[t][lm] = Y[lm];
+                    s_dY[t][0][lm] = dx[lm];
+                    s_dY[t][1][lm] = dy[lm];
+                    s_dY[t][2][lm] = dz[lm];
+                }
+            }
+            s_iv[t] = iv;
+        }
+        __syncthreads();
+        for (int j = 0; j < n; ++j) {
+            const int iv = s_iv[j];
+            if (iv < 0) continue;
+            float fx = 0.0f, fy = 0.0f, fz = 0.0f;
+            if (k < C) {
+                const float x = s_x[j];
+                const float* c = r0f + s_pair[j] * pair_stride + iv * interval_stride + k;
+                float A = 0.0f, gx = 0.0f, gy = 0.0f, gz = 0.0f;
+#pragma unroll
+                for (int l = 0; l <= LMAX; ++l) {
+                    const float c0 = c[(0 * NL + l) * C];
+                    const float c1 = c[(1 * NL + l) * C];
+                    const float c2 = c[(2 * NL + l) * C];
+                    const float c3 = c[(3 * NL + l) * C];
+                    const float R = c0 + x * (c1 + x * (c2 + x * c3));
+                    const float dR = c1 + x * (2.0f * c2 + 3.0f * x * c3);
+                    float yl = 0.0f, ax = 0.0f, ay = 0.0f, az = 0.0f;
+#pragma unroll
+                    for (int lm = l * l; lm < (l + 1) * (l + 1); ++lm) {
+                        yl += s_Y[j][lm] * adj[lm];
+                        ax += s_dY[j][0][lm] * adj[lm];
+                        ay += s_dY[j][1][lm] * adj[lm];
+                        az += s_dY[j][2][lm] * adj[lm];
+                    }
+                    A += dR * yl;
+                    gx += R * ax;
+                    gy += R * ay;
+                    gz += R * az;
+                }
+                fx = -(s_dir[j][0] * A + gx);
+                fy = -(s_dir[j][1] * A + gy);
+                fz = -(s_dir[j][2] * A + gz);
+            }
+            fx = wave_sum(fx);
+            fy = wave_sum(fy);
+            fz = wave_sum(fz);
+            if ((threadIdx.x & 63) == 0) {
+                s_f[j][wave][0] = fx;
+                s_f[j][wave][1] = fy;
+                s_f[j][wave][2] = fz;
+            }
+        }
+        __syncthreads();
+        if (threadIdx.x < n && s_iv[threadIdx.x] >= 0) {
+            const int t = threadIdx.x;
+            double f[3] = {0.0, 0.0, 0.0};
+            for (int w = 0; w < nwaves; ++w)
+                for (int c = 0; c < 3; ++c) f[c] += static_cast<double>(s_f[t][w][c]);
+            double* out = forces + 3 * static_cast<size_t>(base + t);
+            out[0] += f[0];
+            out[1] += f[1];
+            out[2] += f[2];
+        }
+    }
+}
+
+// H1_adj[s, lm2, k] = sum over edges e with source s (ascending e) of msg[e, lm2, k]
+__global__ void __launch_bounds__(256) gather_messages_kernel(LayerArgs a,
+                                                               const float* __restrict__ msg,
+                                                               float* __restrict__ H1_adj)
+{
+    const int s = a.node_offset + xcd_contiguous(blockIdx.x, a.node_count);
+    const int k = threadIdx.x;
+    const int C = a.C;
+    if (k >= C) return;
+    const int nLM = (a.L_max + 1) * (a.L_max + 1);
+    const EdgeGraph& g = a.graph;
+    float acc[16];
+    for (int q = 0; q < nLM; ++q) acc[q] = 0.0f;
+    for (int t = g.tfirst[s]; t < g.tfirst[s + 1]; ++t) {
+        const int e = g.tedge[t];
+        if (!(g.r[e] < a.grid.r_cut)) continue;
+        const float* m = msg + static_cast<size_t>(e) * nLM * C + k;
+        for (int q = 0; q < nLM; ++q) acc[q] += m[q * C];
+    }
+    float* out = H1_adj + static_cast<size_t>(s) * nLM * C + k;
+    for (int q = 0; q < nLM; ++q) out[q * C] = acc[q];
+}
+
+__global__ void add_direct_kernel(int nodes, int C, int nLM, const float* __restrict__ direct,
+                                  float* __restrict__ M0_adj)
+{
+    const size_t idx = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (idx >= static_cast<size_t>(nodes) * C) return;
+    const size_t i = idx / C, k = idx % C;
+    M0_adj[i * nLM * C + k] += direct[idx];
+}
+
+// ---------------------------------------------------------------------------
+// Node readout: M1 = P1(A1), H2 = T_z^T x + W^T M1, E = E0 + q.x + MLP(H2),
+// then the reverse down to A1_adj and the direct scalar adjoint
+// (m0_composite basis, reference mace.cpp:2460-2657).
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) readout_kernel(ReadoutArgs a)
+{
+    extern __shared__ float s_mem[];
+    const int i = xcd_contiguous(blockIdx.x, a.num_nodes);
+    const int k = threadIdx.x;
+    const int C = a.C;
+    const int stride = blockDim.x;
+    const int nlm = a.num_lm;
+    float* x = s_mem + k;                                     // [nlm][stride]
+    float* grad = s_mem + static_cast<size_t>(nlm) * stride + k;  // [nlm][stride]
+    float* vec = s_mem + static_cast<size_t>(2 * nlm) * stride;   // 4 vectors of stride
+    float* s_xs = vec;
+    float* s_m1 = vec + stride;
+    float* s_h2 = vec + 2 * stride;
+    float* s_tmp = vec + 3 * stride;
+    float* s_hid = vec + 4 * stride;  // 2 * 64
+    const bool ok = k < C;
+    const int at = a.type_active[a.node_types[i]];
+    float m1 = 0.0f;
+    if (ok) {
+        const float* in = a.A1 + static_cast<size_t>(i) * nlm * C + k;
+        for (int lm = 0; lm < nlm; ++lm) {
+            x[lm * stride] = in[lm * C];
+            grad[lm * stride] = 0.0f;
+        }
+        const float* coef = a.p1.coef + static_cast<size_t>(at) * a.p1.num_terms * C + k;
+        m1 = poly_value(a.p1, coef, C, 0, a.p1.num_terms, x, stride);
+        poly_gradient(a.p1, coef, C, 0, a.p1.num_terms, x, grad, 1.0f, stride);
+        s_xs[k] = a.M0[static_cast<size_t>(i) * a.num_LM * C + k];
+        s_m1[k] = m1;
+    }
+    __syncthreads();
+    // H2[k] = sum_in T[in][k] xs[in] + W[in][k] m1[in]
+    float h2 = 0.0f;
+    if (ok) {
+        const float* T = a.H2M0 + static_cast<size_t>(at) * C * C + k;
+        const float* W = a.H2M1 + k;
+        for (int in = 0; in < C; ++in) h2 += T[static_cast<size_t>(in) * C] * s_xs[in];
+        for (int in = 0; in < C; ++in) h2 += W[static_cast<size_t>(in) * C] * s_m1[in];
+        s_h2[k] = h2;
+        s_tmp[k] = a.q[k] * s_xs[k];
+    }
+    __syncthreads();
+    // hidden layer of readout_2 (SiLU x scale), one thread per hidden unit
+    float* s_act = s_hid;
+    float* s_gh = s_hid + 64;
+    if (threadIdx.x < a.hidden) {
+        const int h = threadIdx.x;
+        float z = 0.0f;
+        const float* w1 = a.W1 + static_cast<size_t>(h) * C;
+        for (int c = 0; c < C; ++c) z += w1[c] * s_h2[c];
+        const float sig = 1.0f / (1.0f + expf(-z));
+        const float act = a.scale * z * sig;
+        const float dact = a.scale * sig + a.scale * z * sig * (1.0f - sig);
+        s_act[h] = a.W2[h] * act;
+        s_gh[h] = a.W2[h] * dact;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double e = a.E0[at];
+        float e1 = 0.0f;
+        for (int c = 0; c < C; ++c) e1 += s_tmp[c];
+        float e2 = 0.0f;
+        for (int h = 0; h < a.hidden; ++h) e2 += s_act[h];
+        a.energies[i] = e + static_cast<double>(e1) + static_cast<double>(e2);
+    }
+    // H2_adj[k] = sum_h W2[h] dact[h] W1[h][k]
+    if (ok) {
+        float g2 = 0.0f;
+        for (int h = 0; h < a.hidden; ++h) g2 += s_gh[h] * a.W1[static_cast<size_t>(h) * C + k];
+        s_tmp[k] = g2;  // s_tmp reused after the energy sum (synchronised below)
+    }
+    __syncthreads();
+    if (ok) {
+        // direct[k] = q[k] + sum_o T[k][o] H2_adj[o];  M1_adj[k] = sum_o W[k][o] H2_adj[o]
+        const float* T = a.H2M0 + static_cast<size_t>(at) * C * C + static_cast<size_t>(k) * C;
+        const float* W = a.H2M1 + static_cast<size_t>(k) * C;
+        float d = a.q[k], m1adj = 0.0f;
+        for (int o = 0; o < C; ++o) {
+            const float g2 = s_tmp[o];
+            d += T[o] * g2;
+            m1adj += W[o] * g2;
+        }
+        a.direct[static_cast<size_t>(i) * C + k] = d;
+        float* out = a.A1_adj + static_cast<size_t>(i) * nlm * C + k;
+        for (int lm = 0; lm < nlm; ++lm) out[lm * C] = grad[lm * stride] * m1adj;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// fp32 MFMA GEMM over per-node row blocks.  64x64 output tile per 256-thread
+// workgroup, 2x2 waves of v_mfma_f32_32x32x2f32, K staged through LDS in
+// chunks of 32.  Requires K % 32 == 0.
+// ---------------------------------------------------------------------------
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+__global__ void __launch_bounds__(256) gemm_kernel(GemmArgs g)
+{
+    constexpr int BM = 64, BN = 64, BK = 32;
+    __shared__ float As[BM][BK + 1];
+    __shared__ float Bs[BK][BN + 1];
+    const int M = g.nodes * g.rows_per_node;
+    const int row0 = blockIdx.x * BM;
+    const int col0 = blockIdx.y * BN;
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lr = t >> 2, lc = (t & 3) * 8;
+    const int arow_index = row0 + lr;
+    const float* arow = nullptr;
+    if (arow_index < M) {
+        const int node = arow_index / g.rows_per_node;
+        const int m = arow_index - node * g.rows_per_node;
+        arow = g.a.ptr + node * g.a.node_stride + m * g.a.row_stride;
+    }
+    const int br = t >> 3, bc = (t & 7) * 8;
+    floatx16 acc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+    for (int k0 = 0; k0 < g.K; k0 += BK) {
+        if (arow) {
+            const float4 v0 = *reinterpret_cast<const float4*>(arow + k0 + lc);
+            const float4 v1 = *reinterpret_cast<const float4*>(arow + k0 + lc + 4);
+            As[lr][lc + 0] = v0.x, As[lr][lc + 1] = v0.y, As[lr][lc + 2] = v0.z, As[lr][lc + 3] = v0.w;
+            As[lr][lc + 4] = v1.x, As[lr][lc + 5] = v1.y, As[lr][lc + 6] = v1.z, As[lr][lc + 7] = v1.w;
+        } else {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) As[lr][lc + q] = 0.0f;
+        }
+        const float* brow = g.B + static_cast<size_t>(k0 + br) * g.Ncols;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int col = col0 + bc + q;
+            Bs[br][bc + q] = col < g.Ncols ? brow[col] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 2) {
+            const float av = As[wm * 32 + (lane & 31)][kk + (lane >> 5)];
+            const float bv = Bs[kk + (lane >> 5)][wn * 32 + (lane & 31)];
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc, 0, 0, 0);
+        }
+        __syncthreads();
+    }
+    const int col = col0 + wn * 32 + (lane & 31);
+    if (col >= g.Ncols) return;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const int row = row0 + wm * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        if (row < M) {
+            const int node = row / g.rows_per_node;
+            const int m = row - node * g.rows_per_node;
+            float* out = g.c.ptr + node * g.c.node_stride + m * g.c.row_stride;
+            out[col] = acc[v];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// geometry and reductions
+// ---------------------------------------------------------------------------
+__global__ void edge_geometry_kernel(int E, const int* __restrict__ receiver,
+                                     const int* __restrict__ source, const int* __restrict__ shifts,
+                                     const double* __restrict__ pos, const double* __restrict__ cell,
+                                     double* __restrict__ xyz, double* __restrict__ r)
+{
+    const int e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    const int i = receiver[e], j = source[e];
+    const double s0 = shifts[3 * static_cast<size_t>(e)], s1 = shifts[3 * static_cast<size_t>(e) + 1],
+                 s2 = shifts[3 * static_cast<size_t>(e) + 2];
+    double v[3];
+    for (int c = 0; c < 3; ++c)
+        v[c] = pos[3 * static_cast<size_t>(j) + c] - pos[3 * static_cast<size_t>(i) + c] +
+               s0 * cell[c] + s1 * cell[3 + c] + s2 * cell[6 + c];
+    xyz[3 * static_cast<size_t>(e)] = v[0];
+    xyz[3 * static_cast<size_t>(e) + 1] = v[1];
+    xyz[3 * static_cast<size_t>(e) + 2] = v[2];
+    r[e] = sqrt(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]);
+}
+
+// F_a = sum_{e: src=a} f_e - sum_{e: recv=a} f_e, each sum in ascending edge order
+__global__ void atom_forces_kernel(int N, const int* __restrict__ first, const int* __restrict__ tfirst,
+                                   const int* __restrict__ tedge, const double* __restrict__ f,
+                                   double* __restrict__ out)
+{
+    const int a = blockIdx.x * blockDim.x + threadIdx.x;
+    if (a >= N) return;
+    double fs[3] = {0.0, 0.0, 0.0}, fr[3] = {0.0, 0.0, 0.0};
+    for (int t = tfirst[a]; t < tfirst[a + 1]; ++t) {
+        const size_t e = tedge[t];
+        fs[0] += f[3 * e], fs[1] += f[3 * e + 1], fs[2] += f[3 * e + 2];
+    }
+    for (int e = first[a]; e < first[a + 1]; ++e) {
+        fr[0] += f[3 * static_cast<size_t>(e)], fr[1] += f[3 * static_cast<size_t>(e) + 1],
+            fr[2] += f[3 * static_cast<size_t>(e) + 2];
+    }
+    out[3 * static_cast<size_t>(a)] = fs[0] - fr[0];
+    out[3 * static_cast<size_t>(a) + 1] = fs[1] - fr[1];
+    out[3 * static_cast<size_t>(a) + 2] = fs[2] - fr[2];
+}
+
+constexpr int kReduceThreads = 256;
+constexpr int kReduceItems = 4;  // items per thread per block
+
+// partials[b][0] = sum of energies of block b's nodes, [1..9] = -(1/V) f (x) xyz
+__global__ void __launch_bounds__(kReduceThreads) totals_partial_kernel(
+    int N, int E, const double* __restrict__ energies, const double* __restrict__ f,
+    const double* __restrict__ xyz, double inv_volume, double* __restrict__ partials)
+{
+    __shared__ double s[kReduceThreads][10];
+    const int t = threadIdx.x;
+    double acc[10];
+    for (int c = 0; c < 10; ++c) acc[c] = 0.0;
+    const size_t span = static_cast<size_t>(kReduceThreads) * kReduceItems;
+    const size_t b0 = static_cast<size_t>(blockIdx.x) * span;
+    for (int q = 0; q < kReduceItems; ++q) {
+        const size_t idx = b0 + static_cast<size_t>(q) * kReduceThreads + t;
+        if (idx < static_cast<size_t>(N)) acc[0] += energies[idx];
+        if (idx < static_cast<size_t>(E)) {
+            for (int c = 0; c < 9; ++c)
+                acc[1 + c] += -inv_volume * f[3 * idx + c / 3] * xyz[3 * idx + c % 3];
+        }
+    }
+    for (int c = 0; c < 10; ++c) s[t][c] = acc[c];
+    __syncthreads();
+    for (int w = kReduceThreads / 2; w > 0; w >>= 1) {
+        if (t < w)
+            for (int c = 0; c < 10; ++c) s[t][c] += s[t + w][c];
+        __syncthreads();
+    }
+    if (t < 10) partials[static_cast<size_t>(blockIdx.x) * 10 + t] = s[0][t];
+}
+
+__global__ void totals_final_kernel(int num_partials, const double* __restrict__ partials,
+                                    double* __restrict__ out)
+{
+    const int c = threadIdx.x;
+    if (c >= 10) return;
+    double acc = 0.0;
+    for (int b = 0; b < num_partials; ++b) acc += partials[static_cast<size_t>(b) * 10 + c];
+    out[c] = acc;
+}
+
+inline int node_threads(int C) { return ((C + 63) / 64) * 64; }
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream)
+{
+    const int M = g.nodes * g.rows_per_node;
+    if (M <= 0 || g.Ncols <= 0) return hipSuccess;
+    if (g.K % 32 != 0) return hipErrorInvalidValue;
+    dim3 grid((M + 63) / 64, (g.Ncols + 63) / 64);
+    gemm_kernel<<<grid, 256, 0, stream>>>(g);
+    return hipGetLastError();
+}
+
+hipError_t launch_a0_forward(const LayerArgs& a, const float* r0f, float* A0, hipStream_t s)
+{
+    if (a.node_count <= 0) return hipSuccess;
+    const int threads = node_threads(a.C);
+    switch (a.l_max) {
+    case 2: a0_forward_kernel<2><<<a.node_count, threads, 0, s>>>(a, r0f, A0); break;
+    case 3: a0_forward_kernel<3><<<a.node_count, threads, 0, s>>>(a, r0f, A0); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_a0_reverse(const LayerArgs& a, const float* r0f, const float* A0_adj,
+                             double* forces, hipStream_t s)
+{
+    if (a.node_count <= 0) return hipSuccess;
+    const int threads = node_threads(a.C);
+    switch (a.l_max) {
+    case 2: a0_reverse_kernel<2><<<a.node_count, threads, 0, s>>>(a, r0f, A0_adj, forces); break;
+    case 3: a0_reverse_kernel<3><<<a.node_count, threads, 0, s>>>(a, r0f, A0_adj, forces); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_m0_forward(const LayerArgs& a, const PolyTable& p0, const float* A0, float* M0,
+                             hipStream_t s)
+{
+    if (a.node_count <= 0) return hipSuccess;
+    const int threads = node_threads(a.C);
+    const int nlm = (a.l_max + 1) * (a.l_max + 1);
+    const size_t shmem = sizeof(float) * nlm * threads;
+    m0_forward_kernel<<<a.node_count, threads, shmem, s>>>(a, p0, A0, M0);
+    return hipGetLastError();
+}
+
+hipError_t launch_m0_reverse(const LayerArgs& a, const PolyTable& p0, const float* A0,
+                             const float* M0_adj, float* A0_adj, hipStream_t s)
+{
+    if (a.node_count <= 0) return hipSuccess;
+    const int threads = node_threads(a.C);
+    const int nlm = (a.l_max + 1) * (a.l_max + 1);
+    const size_t shmem = sizeof(float) * 2 * nlm * threads;
+    m0_reverse_kernel<<<a.node_count, threads, shmem, s>>>(a, p0, A0, M0_adj, A0_adj);
+    return hipGetLastError();
+}
+
+hipError_t launch_r1_forward(const LayerArgs& a, const float* r1, const float* cg, const float* H1,
+                             float* Phi1, hipStream_t s)
+{
+    if (a.node_count <= 0) return hipSuccess;
+    const int threads = node_threads(a.C);
+    if (a.l_max == 2 && a.L_max == 1)
+        r1_forward_kernel<R1Shape<2, 1>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, Phi1);
+    else if (a.l_max == 3 && a.L_max == 1)
+        r1_forward_kernel<R1Shape<3, 1>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, Phi1);
+    else if (a.l_max == 3 && a.L_max == 2)
+        r1_forward_kernel<R1Shape<3, 2>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, Phi1);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_r1_reverse(const LayerArgs& a, const float* r1, const float* cg, const float* H1,
+                             const float* dPhi1, double* forces, float* msg, hipStream_t s)
+{
+    if (a.node_count <= 0) return hipSuccess;
+    const int threads = node_threads(a.C);
+    if (threads > 256) return hipErrorInvalidValue;
+    if (a.l_max == 2 && a.L_max == 1)
+        r1_reverse_kernel<R1Shape<2, 1>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, dPhi1,
+                                                                          forces, msg);
+    else if (a.l_max == 3 && a.L_max == 1)
+        r1_reverse_kernel<R1Shape<3, 1>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, dPhi1,
+                                                                          forces, msg);
+    else if (a.l_max == 3 && a.L_max == 2)
+        r1_reverse_kernel<R1Shape<3, 2>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, dPhi1,
+                                                                          forces, msg);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_gather_messages(const LayerArgs& a, const float* msg, float* H1_adj, hipStream_t s)
+{
+    if (a.node_count <= 0) return hipSuccess;
+    gather_messages_kernel<<<a.node_count, node_threads(a.C), 0, s>>>(a, msg, H1_adj);
+    return hipGetLastError();
+}
+
+hipError_t launch_add_direct(int nodes, int C, int num_LM, const float* direct, float* M0_adj,
+                             hipStream_t s)
+{
+    const size_t n = static_cast<size_t>(nodes) * C;
+    if (n == 0) return hipSuccess;
+    add_direct_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(nodes, C, num_LM, direct,
+                                                                            M0_adj);
+    return hipGetLastError();
+}
+
+hipError_t launch_readout(const ReadoutArgs& a, hipStream_t s)
+{
+    if (a.num_nodes <= 0) return hipSuccess;
+    const int threads = std::max(node_threads(a.C), 64);
+    const size_t shmem = sizeof(float) * (static_cast<size_t>(2 * a.num_lm + 4) * threads + 128);
+    readout_kernel<<<a.num_nodes, threads, shmem, s>>>(a);
+    return hipGetLastError();
+}
+
+hipError_t launch_edge_geometry(int num_edges, const int* receiver, const int* source,
+                                const int* shifts, const double* positions, const double* cell,
+                                double* xyz, double* r, hipStream_t s)
+{
+    if (num_edges <= 0) return hipSuccess;
+    edge_geometry_kernel<<<(num_edges + 255) / 256, 256, 0, s>>>(num_edges, receiver, source, shifts,
+                                                                 positions, cell, xyz, r);
+    return hipGetLastError();
+}
+
+hipError_t launch_atom_forces(int num_nodes, const int* first, const int* tfirst, const int* tedge,
+                              const double* forces, double* atom_forces, hipStream_t s)
+{
+    if (num_nodes <= 0) return hipSuccess;
+    atom_forces_kernel<<<(num_nodes + 255) / 256, 256, 0, s>>>(num_nodes, first, tfirst, tedge, forces,
+                                                               atom_forces);
+    return hipGetLastError();
+}
+
+int reduce_totals_partials(int num_nodes, int num_edges)
+{
+    const long long n = std::max<long long>(std::max(num_nodes, num_edges), 1);
+    const long long span = static_cast<long long>(kReduceThreads) * kReduceItems;
+    return static_cast<int>((n + span - 1) / span);
+}
+
+hipError_t launch_reduce_totals(int num_nodes, int num_edges, const double* energies,
+                                const double* forces, const double* xyz, double inv_volume,
+                                double* partials, int num_partials, double* out, hipStream_t s)
+{
+    totals_partial_kernel<<<num_partials, kReduceThreads, 0, s>>>(num_nodes, num_edges, energies, forces,
+                                                                  xyz, inv_volume, partials);
+    totals_final_kernel<<<1, 64, 0, s>>>(num_partials, partials, out);
+    return hipGetLastError();
+}
+
+}  // namespace sxl

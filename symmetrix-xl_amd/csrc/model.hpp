@@ -1,0 +1,80 @@
+// Host-side MACE model: format-version-4 compact JSON loader and the compact
+// radial tabulation.
+//
+// Loader semantics follow the reference's MACECPU::load_from_json
+// (libsymmetrix/source/mace.cpp:2659-2959) and the format-4 H1 affine
+// validation (h1_affine_schema.hpp:168-258) for the "m0_composite" basis;
+// the radial tabulation follows CompactRadialModel
+// (compact_radial.cpp:110-420).  Unsupported options (ZBL, A0/A1 density
+// scaling, field coupling, first-interaction residual, Agnesi transform,
+// pair-spline radial form) are rejected with an error, never ignored.
+#pragma once
+
+#include <string>
+#include <vector>
+
+namespace sxl {
+
+struct RadialNetwork {
+    std::vector<int> shape;
+    std::vector<std::vector<double>> weights;  // [layer] row-major [out][in]
+    double activation_scale = 1.0;
+};
+
+struct HostModel {
+    int num_elements = 0;
+    int channels = 0;
+    int l_max = 0, L_max = 0;
+    int num_lm = 0, num_LM = 0;
+    double r_cut = 0.0;
+    std::vector<int> atomic_numbers;
+    std::vector<double> atomic_energies;
+    std::string selected_head;
+    std::vector<std::string> available_heads;
+
+    // compact radial model
+    double grid_min = 0.0, spline_h = 0.0;
+    int spline_points = 0;
+    std::vector<double> bessel_weights;
+    double bessel_prefactor = 0.0;
+    double cutoff_rmax = 0.0;
+    int cutoff_p = 0;
+    RadialNetwork R0, R1;
+
+    std::vector<double> H0;   // [ne][C]
+    std::vector<double> A0W;  // [ne][l_max+1][C][C]  ([in][out])
+
+    // symmetric contraction M0: terms of all LM, grouped by LM
+    std::vector<int> m0_offsets;  // [num_LM+1]
+    std::vector<int> m0_degree;   // [T]
+    std::vector<int> m0_index;    // [T][3]
+    std::vector<double> m0_coef;  // [ne][T][C]
+
+    std::vector<double> H1W;  // [L_max+1][C][C]
+
+    std::vector<int> Phi1_l, Phi1_l1, Phi1_l2, Phi1_lme, Phi1_row;
+    std::vector<double> Phi1_cg;
+    std::vector<std::vector<double>> A1W;  // [l] -> [num_e[l]*C][C]
+
+    std::vector<int> m1_degree, m1_index;  // [T1], [T1][3]
+    std::vector<double> m1_coef;           // [ne][T1][C]
+
+    std::vector<double> H2M0;  // [ne][C][C]  ([in][out])
+    std::vector<double> H2M1;  // [C][C]
+    std::vector<double> readout_q;  // [C]
+    int readout_hidden = 16;
+    std::vector<double> readout_w1;  // [hidden][C]
+    std::vector<double> readout_w2;  // [hidden]
+    double readout_scale = 1.0;
+
+    static HostModel load(const std::string& path, const std::string& head);
+
+    // Nodal values and derivatives, [function][knot], of one radial network
+    // for the unordered element pair (type_i, type_j).
+    void radial_tables(const RadialNetwork& net, int type_i, int type_j,
+                       std::vector<double>& values, std::vector<double>& derivs) const;
+
+    int num_paths() const { return static_cast<int>(Phi1_l.size()); }
+};
+
+}  // namespace sxl

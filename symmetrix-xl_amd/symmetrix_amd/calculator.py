@@ -1,0 +1,136 @@
+"""Energy / forces / stress calculator with neighbour-list skin reuse.
+
+Counterpart of the reference's ASE calculator ``Symmetrix``
+(``symmetrix/source/symmetrix/calculator.py:539-757, 2838-3093, 3821-4021``)
+for the model-evaluation path: the neighbour graph is built on the device at
+cutoff + skin and reused while no atom has moved more than skin/2 since the
+build (``calculator.py:2851-2898``); every call evaluates at the current
+positions; energy is the FP64 sum of node energies, forces are reduced from
+the directed edge forces, stress is -(1/V) sum f (x) xyz in Voigt order
+(``calculator.py:3821-3894``).
+
+ASE is optional: ``calculate`` accepts an ``ase.Atoms`` or any object with
+``positions``, ``numbers`` and ``cell`` (e.g. ``synthetic.Structure``).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from .mace import MACEKokkosFloat
+
+
+def _arrays(atoms):
+    if hasattr(atoms, "get_positions"):
+        positions = np.asarray(atoms.get_positions(), dtype=np.float64)
+        numbers = np.asarray(atoms.get_atomic_numbers())
+        cell = np.asarray(atoms.get_cell(), dtype=np.float64)
+        pbc = np.asarray(atoms.get_pbc(), dtype=bool)
+    else:
+        positions = np.asarray(atoms.positions, dtype=np.float64)
+        numbers = np.asarray(atoms.numbers)
+        cell = np.asarray(atoms.cell, dtype=np.float64)
+        pbc = np.asarray(getattr(atoms, "pbc", (True, True, True)), dtype=bool)
+    return positions, numbers, cell, pbc
+
+
+def full_3x3_to_voigt_6_stress(stress):
+    s = np.asarray(stress).reshape(3, 3)
+    return np.array([s[0, 0], s[1, 1], s[2, 2], 0.5 * (s[1, 2] + s[2, 1]), 0.5 * (s[0, 2] + s[2, 0]),
+                     0.5 * (s[0, 1] + s[1, 0])])
+
+
+class Symmetrix:
+    """MACE calculator on one MI355X (reference ``symmetrix.Symmetrix``)."""
+
+    implemented_properties = ["energy", "free_energy", "energies", "forces", "stress"]
+
+    def __init__(self, model_file, dtype="float32", use_kokkos=True, streamed_edges="direct",
+                 neighbor_skin=0.5, head=None, **unused):
+        if dtype not in ("float32", np.float32):
+            raise ValueError("the MI355X evaluator computes in float32 (dtype='float32')")
+        if streamed_edges not in ("direct", "generic", True):
+            raise ValueError(f"unsupported streamed_edges mode {streamed_edges!r}")
+        if not (neighbor_skin >= 0.0):
+            raise ValueError("neighbor_skin must be non-negative")
+        self.evaluator = MACEKokkosFloat(model_file, head or "")
+        self.cutoff = float(self.evaluator.r_cut)
+        self.neighbor_skin = float(neighbor_skin)
+        self._type_of_z = {z: i for i, z in enumerate(self.evaluator.atomic_numbers)}
+        self._cache = None
+        self.results = {}
+        self.neighbor_rebuild_count = 0
+        self.calculation_count = 0
+
+    # ---- neighbour cache -----------------------------------------------------
+    def _node_types(self, numbers):
+        try:
+            return np.array([self._type_of_z[int(z)] for z in numbers], dtype=np.int32)
+        except KeyError as err:
+            raise ValueError(f"atomic number {err.args[0]} is not supported by the model") from None
+
+    def _geometry(self, atoms):
+        positions, numbers, cell, pbc = _arrays(atoms)
+        if np.all(pbc):
+            return positions, numbers, cell, True
+        if np.any(pbc):
+            raise NotImplementedError("mixed periodic boundary conditions are not supported")
+        # isolated system: a cubic box larger than the extent plus twice the
+        # neighbour cutoff has no periodic image within the cutoff
+        reach = self.cutoff + self.neighbor_skin
+        lo = positions.min(axis=0) if len(positions) else np.zeros(3)
+        hi = positions.max(axis=0) if len(positions) else np.zeros(3)
+        side = float(np.max(hi - lo)) + 2.0 * reach + 1.0
+        return positions - lo + reach, numbers, np.eye(3) * side, False
+
+    def _needs_rebuild(self, positions, numbers, cell):
+        c = self._cache
+        if c is None or len(numbers) != len(c["numbers"]) or np.any(numbers != c["numbers"]):
+            return True
+        if not np.array_equal(cell, c["cell"]):
+            return True
+        moved = self.evaluator._max_displacement(c["generation"], positions)
+        return not (moved <= 0.5 * self.neighbor_skin)
+
+    def _prepare(self, atoms):
+        positions, numbers, cell, periodic = self._geometry(atoms)
+        if self._needs_rebuild(positions, numbers, cell):
+            types = self._node_types(numbers)
+            info = self.evaluator._prepare_periodic_factorized_graph(
+                types, positions, cell, np.linalg.inv(cell), self.cutoff + self.neighbor_skin)
+            self._cache = {"generation": info["generation"], "numbers": numbers.copy(), "cell": cell.copy(),
+                           "num_edges": info["num_edges"]}
+            self.neighbor_rebuild_count += 1
+        return positions, cell, periodic
+
+    # ---- evaluation -----------------------------------------------------------------
+    def calculate(self, atoms=None, properties=("energy", "forces", "stress"), system_changes=None):
+        positions, cell, periodic = self._prepare(atoms)
+        gen = self._cache["generation"]
+        ev = self.evaluator
+        ev._compute_prepared_factorized_positions(gen, positions)
+        energy = ev._total_energy(gen)
+        results = {
+            "energy": energy,
+            "free_energy": energy,
+            "energies": ev.node_energies,
+            "forces": ev._reduce_atom_forces(len(positions), execution_graph_generation=gen),
+        }
+        if "stress" in properties and periodic:
+            volume = abs(float(np.linalg.det(cell)))
+            results["stress"] = full_3x3_to_voigt_6_stress(ev._reduce_stress(volume, None, gen))
+        self.results = results
+        self.calculation_count += 1
+        return results
+
+    def get_potential_energy(self, atoms=None, force_consistent=False):
+        return self.calculate(atoms, ("energy",))["energy"]
+
+    def get_forces(self, atoms=None):
+        return self.calculate(atoms, ("forces",))["forces"]
+
+    def get_stress(self, atoms=None):
+        return self.calculate(atoms, ("stress",))["stress"]
+
+    def get_property(self, name, atoms=None, allow_calculation=True):
+        return self.calculate(atoms)[name]

@@ -1,0 +1,311 @@
+"""Python face of the evaluator, mirroring the reference's native class.
+
+``MACEKokkosFloat`` keeps the method names, argument meaning and result
+layout of the reference's pybind11 class of the same name
+(``symmetrix/source/cpp/mace_kokkos.cpp:1561-1840, 2086-2203, 2762``) for the
+model-evaluation path, so callers written against the reference run
+unchanged.  All work runs in ``libsymmetrix_amd.so`` on the GPU; nothing here
+computes model quantities.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import _native
+from ._native import c_double_p, c_i64, c_int_p, c_u64, check, library
+
+
+def _i32(a, n=None, name="array"):
+    a = np.ascontiguousarray(a, dtype=np.int32).reshape(-1)
+    if n is not None and a.size != n:
+        raise ValueError(f"{name} must hold {n} values, got {a.size}")
+    return a
+
+
+def _f64(a, n=None, name="array"):
+    a = np.ascontiguousarray(a, dtype=np.float64).reshape(-1)
+    if n is not None and a.size != n:
+        raise ValueError(f"{name} must hold {n} values, got {a.size}")
+    return a
+
+
+def _p(a, ctype):
+    return a.ctypes.data_as(ctypes.POINTER(ctype))
+
+
+class MACEKokkosFloat:
+    """FP32 MACE evaluator on one MI355X (reference class ``MACEKokkosFloat``)."""
+
+    streamed_edges_mode = "direct"
+
+    def __init__(self, filename, head: str = ""):
+        lib = library()
+        handle = ctypes.c_void_p()
+        check(lib.sxl_create(str(filename).encode(), (head or "").encode(), ctypes.byref(handle)))
+        self._h = handle
+        info = _native.ModelInfo()
+        check(lib.sxl_model_info(self._h, ctypes.byref(info)))
+        self._info = info
+        z = np.zeros(info.num_elements, dtype=np.int32)
+        check(lib.sxl_atomic_numbers(self._h, _p(z, ctypes.c_int)))
+        e0 = np.zeros(info.num_elements, dtype=np.float64)
+        check(lib.sxl_atomic_energies(self._h, _p(e0, ctypes.c_double)))
+        self._atomic_numbers = [int(v) for v in z]
+        self._atomic_energies = [float(v) for v in e0]
+        self._generation = 0
+        self._evaluated = False
+
+    def close(self):
+        if getattr(self, "_h", None):
+            library().sxl_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ---- model metadata ----------------------------------------------------
+    @property
+    def atomic_numbers(self):
+        return list(self._atomic_numbers)
+
+    @property
+    def atomic_energies(self):
+        return list(self._atomic_energies)
+
+    @property
+    def r_cut(self):
+        return self._info.r_cut
+
+    @property
+    def l_max(self):
+        return self._info.l_max
+
+    @property
+    def L_max(self):
+        return self._info.L_max
+
+    @property
+    def num_channels(self):
+        return self._info.num_channels
+
+    @property
+    def num_elements(self):
+        return self._info.num_elements
+
+    # ---- graphs --------------------------------------------------------------
+    def _prepare_factorized_graph(self, num_nodes, node_types, num_neigh, neigh_indices, neigh_types):
+        types = _i32(node_types, num_nodes, "node_types")
+        nn = _i32(num_neigh, num_nodes, "num_neigh")
+        e = int(nn.sum())
+        idx = _i32(neigh_indices, e, "neigh_indices")
+        nt = _i32(neigh_types, e, "neigh_types")
+        gen = c_u64(0)
+        check(library().sxl_prepare_graph(self._h, int(num_nodes), _p(types, ctypes.c_int),
+                                          _p(nn, ctypes.c_int), _p(idx, ctypes.c_int),
+                                          _p(nt, ctypes.c_int), ctypes.byref(gen)))
+        self._generation = int(gen.value)
+        self._evaluated = False
+        return self._generation
+
+    def _prepare_periodic_factorized_graph(self, node_types, positions, cell, inverse_cell, neighbor_cutoff):
+        types = _i32(node_types)
+        n = types.size
+        pos = _f64(positions, 3 * n, "positions")
+        c = _f64(cell, 9, "cell")
+        ic = _f64(inverse_cell, 9, "inverse_cell")
+        gen = c_u64(0)
+        ne = c_i64(0)
+        check(library().sxl_prepare_periodic_graph(self._h, n, _p(types, ctypes.c_int), _p(pos, ctypes.c_double),
+                                                   _p(c, ctypes.c_double), _p(ic, ctypes.c_double),
+                                                   float(neighbor_cutoff), ctypes.byref(gen), ctypes.byref(ne)))
+        self._generation = int(gen.value)
+        self._evaluated = False
+        return {"generation": self._generation, "num_edges": int(ne.value)}
+
+    def _prepare_periodic_factorized_graph_device(self, node_types, positions_ptr, cell, inverse_cell,
+                                                  neighbor_cutoff):
+        """As ``_prepare_periodic_factorized_graph`` with positions already on
+        the device (an integer device address, e.g. ``tensor.data_ptr()``)."""
+        types = _i32(node_types)
+        c = _f64(cell, 9, "cell")
+        ic = _f64(inverse_cell, 9, "inverse_cell")
+        gen = c_u64(0)
+        ne = c_i64(0)
+        check(library().sxl_prepare_periodic_graph_device(
+            self._h, types.size, _p(types, ctypes.c_int), ctypes.c_void_p(int(positions_ptr)),
+            _p(c, ctypes.c_double), _p(ic, ctypes.c_double), float(neighbor_cutoff), ctypes.byref(gen),
+            ctypes.byref(ne)))
+        self._generation = int(gen.value)
+        self._evaluated = False
+        return {"generation": self._generation, "num_edges": int(ne.value)}
+
+    def _update_factorized_cell(self, generation, cell, inverse_cell):
+        c = _f64(cell, 9, "cell")
+        ic = _f64(inverse_cell, 9, "inverse_cell")
+        check(library().sxl_update_cell(self._h, c_u64(int(generation)), _p(c, ctypes.c_double),
+                                        _p(ic, ctypes.c_double)))
+
+    def _graph_size(self):
+        n = ctypes.c_int(0)
+        e = c_i64(0)
+        g = c_u64(0)
+        check(library().sxl_graph_size(self._h, ctypes.byref(n), ctypes.byref(e), ctypes.byref(g)))
+        return int(n.value), int(e.value), int(g.value)
+
+    def _periodic_graph_arrays(self, generation):
+        """The prepared periodic graph: num_neigh, receiver_offsets, sources,
+        shifts, fractional_xyz (reference neighbour-graph output layout)."""
+        n, e, _ = self._graph_size()
+        num_neigh = np.zeros(n, dtype=np.int32)
+        offsets = np.zeros(n + 1, dtype=np.int32)
+        sources = np.zeros(e, dtype=np.int32)
+        shifts = np.zeros((e, 3), dtype=np.int32)
+        frac = np.zeros((e, 3), dtype=np.float64)
+        check(library().sxl_graph_arrays(self._h, c_u64(int(generation)), _p(num_neigh, ctypes.c_int),
+                                         _p(offsets, ctypes.c_int), _p(sources, ctypes.c_int),
+                                         _p(shifts, ctypes.c_int), _p(frac, ctypes.c_double)))
+        return {"num_neigh": num_neigh, "receiver_offsets": offsets, "sources": sources, "shifts": shifts,
+                "fractional_xyz": frac}
+
+    # ---- evaluation -----------------------------------------------------------
+    def _compute_prepared_factorized_positions(self, generation, positions):
+        n, _, _ = self._graph_size()
+        pos = _f64(positions, 3 * n, "positions")
+        check(library().sxl_compute_prepared_positions(self._h, c_u64(int(generation)), _p(pos, ctypes.c_double)))
+        self._evaluated = True
+
+    def _compute_prepared_factorized_positions_device(self, generation, positions_ptr):
+        check(library().sxl_compute_prepared_positions_device(self._h, c_u64(int(generation)),
+                                                              ctypes.c_void_p(int(positions_ptr))))
+        self._evaluated = True
+
+    def _compute_prepared_factorized(self, generation, xyz, r):
+        _, e, _ = self._graph_size()
+        x = _f64(xyz, 3 * e, "xyz")
+        rr = _f64(r, e, "r")
+        check(library().sxl_compute_prepared(self._h, c_u64(int(generation)), _p(x, ctypes.c_double),
+                                             _p(rr, ctypes.c_double)))
+        self._evaluated = True
+
+    def compute_node_energies_forces(self, num_nodes, node_types, num_neigh, neigh_indices, neigh_types, xyz, r,
+                                     execution_graph_generation=0):
+        """Evaluate energies and directed forces (reference
+        ``compute_node_energies_forces``, mace_kokkos.cpp:2169-2203).  With a
+        nonzero generation the prepared graph of that token is reused."""
+        if execution_graph_generation:
+            self._compute_prepared_factorized(execution_graph_generation, xyz, r)
+            return
+        types = _i32(node_types, num_nodes, "node_types")
+        nn = _i32(num_neigh, num_nodes, "num_neigh")
+        e = int(nn.sum())
+        idx = _i32(neigh_indices, e, "neigh_indices")
+        nt = _i32(neigh_types, e, "neigh_types")
+        x = _f64(xyz, 3 * e, "xyz")
+        rr = _f64(r, e, "r")
+        check(library().sxl_compute_node_energies_forces(
+            self._h, int(num_nodes), _p(types, ctypes.c_int), _p(nn, ctypes.c_int), _p(idx, ctypes.c_int),
+            _p(nt, ctypes.c_int), _p(x, ctypes.c_double), _p(rr, ctypes.c_double)))
+        _, _, self._generation = self._graph_size()
+        self._evaluated = True
+
+    def _max_displacement(self, generation, positions):
+        n, _, _ = self._graph_size()
+        pos = _f64(positions, 3 * n, "positions")
+        out = ctypes.c_double(0.0)
+        check(library().sxl_max_displacement(self._h, c_u64(int(generation)),
+                                             ctypes.cast(pos.ctypes.data, ctypes.c_void_p), 0,
+                                             ctypes.byref(out)))
+        return float(out.value)
+
+    # ---- results ----------------------------------------------------------------
+    @property
+    def node_energies(self):
+        n, _, _ = self._graph_size()
+        out = np.zeros(n, dtype=np.float64)
+        check(library().sxl_node_energies(self._h, _p(out, ctypes.c_double), n))
+        return out
+
+    @property
+    def node_forces(self):
+        _, e, _ = self._graph_size()
+        out = np.zeros(3 * e, dtype=np.float64)
+        check(library().sxl_node_forces(self._h, _p(out, ctypes.c_double), e))
+        return out
+
+    def _reduce_atom_forces(self, num_nodes, receivers=None, sources=None, execution_graph_generation=0):
+        gen = int(execution_graph_generation) or self._generation
+        out = np.zeros((int(num_nodes), 3), dtype=np.float64)
+        n, _, _ = self._graph_size()
+        if n != int(num_nodes):
+            raise ValueError("Atom-force reduction extents are inconsistent.")
+        check(library().sxl_reduce_atom_forces(self._h, c_u64(gen), _p(out, ctypes.c_double)))
+        return out
+
+    def _reduce_stress(self, volume, xyz=None, execution_graph_generation=0):
+        gen = int(execution_graph_generation) or self._generation
+        out = np.zeros(9, dtype=np.float64)
+        check(library().sxl_reduce_stress(self._h, c_u64(gen), float(volume), _p(out, ctypes.c_double)))
+        return out.reshape(3, 3)
+
+    def _total_energy(self, execution_graph_generation=0):
+        gen = int(execution_graph_generation) or self._generation
+        out = ctypes.c_double(0.0)
+        check(library().sxl_total_energy(self._h, c_u64(gen), ctypes.byref(out)))
+        return float(out.value)
+
+    def _device_results(self):
+        """Device addresses of (atom forces [N][3], totals [10]) of the last
+        evaluation (valid until the next call)."""
+        f = ctypes.c_void_p()
+        t = ctypes.c_void_p()
+        check(library().sxl_device_results(self._h, ctypes.byref(f), ctypes.byref(t)))
+        return f.value, t.value
+
+    def _synchronize(self):
+        check(library().sxl_synchronize(self._h))
+
+    @property
+    def stats(self):
+        s = _native.Stats()
+        check(library().sxl_stats(self._h, ctypes.byref(s)))
+        return {name: getattr(s, name) for name, _ in _native.Stats._fields_}
+
+
+def periodic_neighbor_graph(positions, cell, inverse_cell, cutoff):
+    """Periodic neighbour graph on the device in the reference's edge order
+    (reference ``_kokkos_periodic_neighbor_graph``): dict of num_neigh,
+    receiver_offsets, sources, shifts, fractional_xyz."""
+    lib = library()
+    pos = np.ascontiguousarray(positions, dtype=np.float64).reshape(-1, 3)
+    n = pos.shape[0]
+    c = _f64(cell, 9, "cell")
+    ic = _f64(inverse_cell, 9, "inverse_cell")
+    handle = ctypes.c_void_p()
+    ne = c_i64(0)
+    check(lib.sxl_neighbor_graph_build(_p(pos, ctypes.c_double), n, _p(c, ctypes.c_double),
+                                       _p(ic, ctypes.c_double), float(cutoff), ctypes.byref(handle),
+                                       ctypes.byref(ne)))
+    try:
+        e = int(ne.value)
+        num_neigh = np.zeros(n, dtype=np.int32)
+        offsets = np.zeros(n + 1, dtype=np.int32)
+        sources = np.zeros(e, dtype=np.int32)
+        shifts = np.zeros((e, 3), dtype=np.int32)
+        frac = np.zeros((e, 3), dtype=np.float64)
+        check(lib.sxl_neighbor_graph_copy(handle, _p(num_neigh, ctypes.c_int), _p(offsets, ctypes.c_int),
+                                          _p(sources, ctypes.c_int), _p(shifts, ctypes.c_int),
+                                          _p(frac, ctypes.c_double)))
+    finally:
+        lib.sxl_neighbor_graph_free(handle)
+    return {"num_neigh": num_neigh, "receiver_offsets": offsets, "sources": sources, "shifts": shifts,
+            "fractional_xyz": frac}
+
+
+# reference binding name (symmetrix._kokkos_periodic_neighbor_graph)
+_kokkos_periodic_neighbor_graph = periodic_neighbor_graph
