@@ -684,11 +684,13 @@ __global__ void __launch_bounds__(256) readout_kernel(ReadoutArgs a)
         for (int h = 0; h < a.hidden; ++h) e2 += s_act[h];
         a.energies[i] = e + static_cast<double>(e1) + static_cast<double>(e2);
     }
-    // H2_adj[k] = sum_h W2[h] dact[h] W1[h][k]
+    // H2_adj[k] = sum_h W2[h] dact[h] W1[h][k], into s_h2: H2 is dead after the
+    // hidden layer (synchronised above), while thread 0 may still be reading
+    // s_tmp for the energy
     if (ok) {
         float g2 = 0.0f;
         for (int h = 0; h < a.hidden; ++h) g2 += s_gh[h] * a.W1[static_cast<size_t>(h) * C + k];
-        s_tmp[k] = g2;  // s_tmp reused after the energy sum (synchronised below)
+        s_h2[k] = g2;
     }
     __syncthreads();
     if (ok) {
@@ -697,7 +699,7 @@ __global__ void __launch_bounds__(256) readout_kernel(ReadoutArgs a)
         const float* W = a.H2M1 + static_cast<size_t>(k) * C;
         float d = a.q[k], m1adj = 0.0f;
         for (int o = 0; o < C; ++o) {
-            const float g2 = s_tmp[o];
+            const float g2 = s_h2[o];
             d += T[o] * g2;
             m1adj += W[o] * g2;
         }
