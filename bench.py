@@ -1,0 +1,314 @@
+"""Benchmark: microseconds per atom for one complete energy + forces + stress
+call of the medium-shape MACE on 5,000-atom SrTiO3.
+
+A step is one call of the evaluation path with the positions already resident
+in HBM: the neighbour-reuse check (max displacement vs skin/2 on the device),
+edge geometry, the full forward and reverse pass, atom forces, and the energy
+and stress reductions (energy and stress copied to the host; atom forces stay
+on the device).  W untimed warmup steps, then K steps timed as one block
+between device synchronisations.  Prints one JSON line.
+
+Extra fields beside the contract's: the median per-step time, the
+host-boundary rate (host positions in, host forces out, through the
+calculator), per-stage device times from HIP events recorded on the
+evaluator's stream during the timed steps, the roofline of the dominant
+kernel and the CPU baseline (the oracle's OpenMP restatement on this host).
+"""
+
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (os.path.join(ROOT, "symmetrix-xl_amd"), ROOT):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+METRIC = "µs/atom per E+F+stress call (FP32, 1 MI355X) at 5k atoms; max atoms tiled"
+PUBLISHED_US_PER_ATOM = 1.922  # reference, RTX 5090, 5,000-atom SrTiO3
+FP32_PEAK_TFLOPS = 157.3
+HBM_PEAK_GBS = 8000.0
+
+
+class HipMemory:
+    """Device buffers through the HIP runtime (plumbing for resident inputs)."""
+
+    def __init__(self):
+        self.lib = ctypes.CDLL("libamdhip64.so")
+        self.lib.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+        self.lib.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+        self.lib.hipFree.argtypes = [ctypes.c_void_p]
+        self.lib.hipDeviceSynchronize.argtypes = []
+
+    def upload(self, array):
+        a = np.ascontiguousarray(array)
+        ptr = ctypes.c_void_p()
+        if self.lib.hipMalloc(ctypes.byref(ptr), a.nbytes) != 0:
+            raise RuntimeError("hipMalloc failed")
+        if self.lib.hipMemcpy(ptr, a.ctypes.data_as(ctypes.c_void_p), a.nbytes, 1) != 0:  # HostToDevice
+            raise RuntimeError("hipMemcpy failed")
+        return ptr.value
+
+    def synchronize(self):
+        if self.lib.hipDeviceSynchronize() != 0:
+            raise RuntimeError("hipDeviceSynchronize failed")
+
+    def free(self, ptr):
+        self.lib.hipFree(ctypes.c_void_p(ptr))
+
+
+def workload_model(preset, seed):
+    from symmetrix_amd import synthetic
+
+    cache = os.environ.get("SXL_BENCH_CACHE", "/tmp")
+    path = os.path.join(cache, f"sxl_{preset}_seed{seed}.json")
+    if not os.path.exists(path):
+        tmp = path + f".{os.getpid()}.tmp"
+        synthetic.write_model(tmp, preset, seed)
+        os.replace(tmp, path)
+    return path
+
+
+def essential_flops(model_info, num_active_edges, num_nodes, m0_degrees, m1_degrees):
+    """Formulation-minimal FLOPs per stage (FMA = 2) of one evaluation.
+
+    Per active edge (C channels, lmax edge harmonics, P paths, R_nz nonzero CG
+    rows): A0 forward 6(lmax+1)C + 2 n_lm C; A0 reverse 10(lmax+1)C + 4 n_lm C;
+    R1 forward 6PC + 2 R_nz C + C sum_p(2 l1_p + 1); R1 reverse
+    10PC + 7 R_nz C + C sum_p(2 l1_p + 1).  Node stages count their dense
+    products (2 flops per multiply-add).
+    """
+    from symmetrix_amd import irreps
+
+    C, lmax, Lmax = model_info["C"], model_info["lmax"], model_info["Lmax"]
+    nlm, nLM = (lmax + 1) ** 2, (Lmax + 1) ** 2
+    tables = irreps.phi1_tables(lmax, Lmax)
+    paths = tables["paths"]
+    P = len(paths)
+    rows_nz = len({t["row"] for t in tables["terms"]})
+    sum_l1 = sum(2 * l1 + 1 for l1, _, _ in paths)
+    num_e = tables["num_e"]
+    nlme = sum((2 * l + 1) * num_e[l] for l in range(lmax + 1))
+    E, N = num_active_edges, num_nodes
+    per_edge = {
+        "a0_forward": 6 * (lmax + 1) * C + 2 * nlm * C,
+        "a0_reverse": 10 * (lmax + 1) * C + 4 * nlm * C,
+        "r1_forward": 6 * P * C + 2 * rows_nz * C + C * sum_l1,
+        "r1_reverse": 10 * P * C + 7 * rows_nz * C + C * sum_l1,
+    }
+    out = {k: v * E for k, v in per_edge.items()}
+    out["h1_gemm"] = 2 * N * nLM * C * C
+    out["h1_reverse_gemm"] = 2 * N * nLM * C * C
+    out["a1_gemm"] = 2 * N * nlme * C * C
+    out["a1_reverse_gemm"] = 2 * N * nlme * C * C
+    out["m0_forward"] = 2 * N * C * m0_degrees
+    out["m0_reverse"] = 4 * N * C * m0_degrees
+    out["readout"] = N * (6 * C * m1_degrees + 8 * C * C)
+    return out, per_edge
+
+
+def polynomial_degree_sum(lmax, out_lmax, correlation=3):
+    """Sum of monomial degrees of the generated symmetric contraction."""
+    from symmetrix_amd import irreps
+
+    total = 0
+    for out_l in range(out_lmax + 1):
+        for monomials, _ in irreps.equivariant_polynomials(lmax, out_l, correlation):
+            total += sum(len(m) for m in monomials)
+    return total
+
+
+def cpu_baseline(model_path, structure, cutoff, threads, calls):
+    from oracle import oracle
+    from symmetrix_amd import synthetic
+
+    with open(model_path) as f:
+        model = json.load(f)
+    types = synthetic.node_types(structure, model["atomic_numbers"])
+    orc = oracle.MaceOracle(model, np.unique(types), "float32")
+    gi = oracle.graph_inputs(structure, cutoff, model["atomic_numbers"])
+    volume = structure.volume
+
+    def call():
+        e, f = orc.compute(gi["node_types"], gi["num_neigh"], gi["neigh_indices"], gi["neigh_types"],
+                           gi["xyz"], gi["r"], threads)
+        oracle.reduce(gi["num_neigh"], gi["neigh_indices"], f, gi["xyz"], volume)
+        return float(np.sum(e))
+
+    call()  # warmup
+    times = []
+    for _ in range(calls):
+        t0 = time.perf_counter()
+        call()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times) / len(structure) * 1e6, times
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--preset", default="medium")
+    ap.add_argument("--cells", type=int, default=10, help="SrTiO3 supercell edge (5 n^3 atoms)")
+    ap.add_argument("--sigma", type=float, default=0.05)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--skin", type=float, default=0.5)
+    ap.add_argument("--cpu-calls", type=int, default=2, help="timed oracle calls for cpu_baseline (0: skip)")
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--host-steps", type=int, default=5, help="host-boundary calculator steps (0: skip)")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py runs on one GPU only: this build has no multi-GPU path "
+              "(sharding is described in DESIGN.md); use --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    from symmetrix_amd import MACEKokkosFloat, Symmetrix, synthetic
+
+    t_setup = time.perf_counter()
+    model_path = workload_model(args.preset, args.seed)
+    structure = synthetic.srtio3_supercell(args.cells, sigma=args.sigma, seed=args.seed)
+    N = len(structure)
+    ev = MACEKokkosFloat(model_path)
+    cutoff = ev.r_cut + args.skin
+    types = synthetic.node_types(structure, ev.atomic_numbers)
+    hip = HipMemory()
+    d_pos = hip.upload(structure.positions.astype(np.float64))
+    cell = structure.cell
+    inv = np.linalg.inv(cell)
+    volume = structure.volume
+    info = ev._prepare_periodic_factorized_graph_device(types, d_pos, cell, inv, cutoff)
+    gen = info["generation"]
+    graph = ev._periodic_graph_arrays(gen)
+    receivers = np.repeat(np.arange(N), graph["num_neigh"])
+    xyz = (structure.positions[graph["sources"]] - structure.positions[receivers]
+           + graph["shifts"].astype(np.float64) @ cell)
+    r = np.linalg.norm(xyz, axis=1)
+    active_edges = int(np.count_nonzero(r < ev.r_cut))
+    setup_s = time.perf_counter() - t_setup
+    print(f"[bench] {N} atoms, {info['num_edges']} edges ({active_edges} within r_cut), setup {setup_s:.1f} s",
+          file=sys.stderr, flush=True)
+
+    rebuilds = 0
+
+    def step():
+        nonlocal gen, rebuilds
+        moved = ev._max_displacement_device(gen, d_pos)
+        if not moved <= 0.5 * args.skin:
+            gen = ev._prepare_periodic_factorized_graph_device(types, d_pos, cell, inv, cutoff)["generation"]
+            rebuilds += 1
+        ev._compute_prepared_factorized_positions_device(gen, d_pos)
+        stress = ev._reduce_stress(volume, None, gen)
+        energy = ev._total_energy(gen)
+        return energy, stress
+
+    for _ in range(args.warmup):
+        step()
+    ev._set_profiling(True)
+    hip.synchronize()
+    per_step = []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        ts = time.perf_counter()
+        energy, stress = step()
+        per_step.append(time.perf_counter() - ts)
+    hip.synchronize()
+    elapsed = time.perf_counter() - t0
+    stages = ev._stage_times()
+    ms_per_step = elapsed / args.steps * 1e3
+    value = ms_per_step * 1e3 / N
+    median_us = statistics.median(per_step) * 1e6 / N
+    print(f"[bench] {ms_per_step:.3f} ms/step = {value:.4f} us/atom (median {median_us:.4f}), E={energy:.6f}",
+          file=sys.stderr, flush=True)
+
+    # roofline of the dominant kernel (largest average device time per launch)
+    model_info = {"C": ev.num_channels, "lmax": ev.l_max, "Lmax": ev.L_max}
+    m0_deg = polynomial_degree_sum(ev.l_max, ev.L_max)
+    m1_deg = polynomial_degree_sum(ev.l_max, 0)
+    flops, per_edge = essential_flops(model_info, active_edges, N, m0_deg, m1_deg)
+    stage_avg = {k: (ms / c if c else 0.0) for k, (ms, c) in stages.items()}
+    dominant = max(stage_avg, key=stage_avg.get)
+    avg_ms = stage_avg[dominant]
+    achieved = flops.get(dominant, 0.0) / (avg_ms * 1e-3) / 1e12 if avg_ms > 0 else 0.0
+    roofline = {
+        "bound": "mfma",
+        "achieved": round(achieved, 3),
+        "peak": FP32_PEAK_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
+        "traffic": None,
+        "kernel": dominant,
+        "kernel_avg_ms": round(avg_ms, 4),
+        "algorithmic_flops_per_launch": flops.get(dominant, 0.0),
+        "flops_per_active_edge": per_edge.get(dominant),
+        "active_edges": active_edges,
+    }
+    total_flops = sum(flops.values())
+
+    # host-boundary rate (PCIe-inclusive; never `value`)
+    host_us = None
+    if args.host_steps > 0:
+        calc = Symmetrix(model_path, neighbor_skin=args.skin)
+        calc.calculate(structure)
+        t = time.perf_counter()
+        for _ in range(args.host_steps):
+            calc.calculate(structure)
+        host_us = (time.perf_counter() - t) / args.host_steps / N * 1e6
+        del calc
+
+    cpu = None
+    if args.cpu_calls > 0:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        us, times = cpu_baseline(model_path, structure, cutoff, threads, args.cpu_calls)
+        cpu = {
+            "value": round(us, 3),
+            "unit": "us/atom",
+            "cores": threads,
+            "kind": "port",
+            "sample": f"full {N}-atom workload, 1 warmup + median of {args.cpu_calls} oracle calls "
+                      f"(OpenMP restatement of the reference CPU path, compute + reductions, "
+                      f"neighbour list reused), {sum(times):.1f} s timed",
+        }
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 5),
+        "unit": "us/atom",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": False,
+        "scaling": "strong",
+        "vs_baseline": round(value / PUBLISHED_US_PER_ATOM, 4),
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {
+            "workload": f"medium-shape random-init MACE ({args.preset}: 128x0e+128x1o, lmax 3, correlation 3, "
+                        f"89-element embedding) on SrTiO3 {args.cells}^3 ({N} atoms, sigma {args.sigma} A, "
+                        f"seed {args.seed}), cutoff {ev.r_cut} + {args.skin} A skin, E+F+stress",
+            "atoms": N,
+            "edges": int(info["num_edges"]),
+            "active_edges": active_edges,
+        },
+        "median_us_per_atom": round(median_us, 5),
+        "host_boundary_us_per_atom": None if host_us is None else round(host_us, 5),
+        "stage_ms": {k: round(v, 4) for k, v in stage_avg.items()},
+        "essential_gflop_per_call": round(total_flops / 1e9, 3),
+        "neighbor_rebuilds_timed": rebuilds,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    hip.free(d_pos)
+
+
+if __name__ == "__main__":
+    main()

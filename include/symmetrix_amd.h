@@ -163,6 +163,17 @@ int sxl_neighbor_graph_copy(const sxl_graph* graph, int* num_neigh, int* receive
                             int* shifts, double* fractional_xyz);
 void sxl_neighbor_graph_free(sxl_graph* graph);
 int sxl_stats(const sxl_evaluator* evaluator, sxl_stats_t* out);
+/* Stage profiling: with enable != 0 every evaluation records HIP events
+ * around each stage on the evaluator's stream (counters reset).  The
+ * accumulated device time (ms) and count of each stage are read with
+ * sxl_stage_times (arrays of sxl_num_stages() entries); sxl_stage_name gives
+ * the stage names (kernel families).  Counterpart of the reference's
+ * factorized_last_evaluation_ms timing fields (mace_kokkos.hpp:1425-1455). */
+int sxl_set_profiling(sxl_evaluator* evaluator, int enable);
+int sxl_num_stages(void);
+const char* sxl_stage_name(int stage);
+int sxl_stage_times(const sxl_evaluator* evaluator, double* ms, int* counts);
+
 /* Waits for all device work of the evaluator. */
 int sxl_synchronize(const sxl_evaluator* evaluator);
 

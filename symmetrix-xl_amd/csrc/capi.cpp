@@ -321,6 +321,22 @@ int sxl_neighbor_graph_copy(const sxl_graph* g, int* num_neigh, int* receiver_of
 
 void sxl_neighbor_graph_free(sxl_graph* graph) { delete graph; }
 
+int sxl_set_profiling(sxl_evaluator* ev, int enable)
+{
+    if (!ev) return null_handle();
+    return guarded([&] { ev->impl.set_profiling(enable != 0); });
+}
+
+int sxl_num_stages(void) { return sxl::kNumStages; }
+
+const char* sxl_stage_name(int stage) { return sxl::stage_name(stage); }
+
+int sxl_stage_times(const sxl_evaluator* ev, double* ms, int* counts)
+{
+    if (!ev) return null_handle();
+    return guarded([&] { ev->impl.stage_times(ms, counts); });
+}
+
 int sxl_synchronize(const sxl_evaluator* ev)
 {
     if (!ev) return null_handle();

@@ -106,6 +106,15 @@ ShapeInfo shape_info()
 
 }  // namespace
 
+const char* stage_name(int stage)
+{
+    static const char* names[kNumStages] = {
+        "edge_geometry", "a0_forward", "m0_forward", "h1_gemm", "r1_forward", "a1_gemm", "readout",
+        "a1_reverse_gemm", "r1_reverse", "h1_adjoint_gather", "h1_reverse_gemm", "m0_reverse", "a0_reverse",
+        "atom_forces"};
+    return stage >= 0 && stage < kNumStages ? names[stage] : "";
+}
+
 DeviceBuffer::~DeviceBuffer() { release(); }
 
 void DeviceBuffer::release()
@@ -168,9 +177,38 @@ Evaluator::Evaluator(const std::string& model_path, const std::string& head)
     hip_check(hipStreamSynchronize(stream_), "model upload");
 }
 
+void Evaluator::set_profiling(bool enable)
+{
+    if (enable && events_.empty()) {
+        events_.resize(2 * kNumStages);
+        for (auto& e : events_) hip_check(hipEventCreate(&e), "event create");
+    }
+    profiling_ = enable;
+    for (int i = 0; i < kNumStages; ++i) {
+        stage_ms_[i] = 0.0;
+        stage_count_[i] = 0;
+    }
+}
+
+void Evaluator::stage_times(double* ms, int* counts) const
+{
+    for (int i = 0; i < kNumStages; ++i) {
+        if (ms) ms[i] = stage_ms_[i];
+        if (counts) counts[i] = stage_count_[i];
+    }
+}
+
+void Evaluator::mark(int stage, bool end)
+{
+    if (!profiling_) return;
+    hip_check(hipEventRecord(events_[2 * stage + (end ? 1 : 0)], stream_), "event record");
+    if (end) stage_used_[stage] = true;
+}
+
 Evaluator::~Evaluator()
 {
     if (stream_) (void)hipStreamSynchronize(stream_);
+    for (auto& e : events_) (void)hipEventDestroy(e);
     // buffers free themselves; the stream goes last
     A0_.release();
     if (stream_) (void)hipStreamDestroy(stream_);
@@ -664,10 +702,13 @@ void Evaluator::compute_positions(std::uint64_t generation, const double* positi
         hip_check(hipMemcpyAsync(positions_.as<double>(), positions, N * 3 * sizeof(double),
                                  device_positions ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, stream_),
                   "positions");
+    for (int i = 0; i < kNumStages; ++i) stage_used_[i] = false;
+    mark(kStageGeometry, false);
     hip_check(launch_edge_geometry(static_cast<int>(num_edges_), receiver_.as<int>(), source_.as<int>(),
                                    pgraph_.shifts.as<int>(), positions_.as<double>(), cell_dev_.as<double>(),
                                    xyz_.as<double>(), r_.as<double>(), stream_),
               "edge geometry");
+    mark(kStageGeometry, true);
     evaluate();
 }
 
@@ -680,6 +721,7 @@ void Evaluator::compute_xyz(std::uint64_t generation, const double* xyz, const d
         hip_check(hipMemcpyAsync(xyz_.as<double>(), xyz, E * 3 * sizeof(double), kind, stream_), "xyz");
         hip_check(hipMemcpyAsync(r_.as<double>(), r, E * sizeof(double), kind, stream_), "r");
     }
+    for (int i = 0; i < kNumStages; ++i) stage_used_[i] = false;
     evaluate();
 }
 
@@ -736,8 +778,13 @@ void Evaluator::evaluate()
 
     if (E > 0 || N > 0) {
         // layer 0: A0 (folded H0, A0_W), M0, H1
+        mark(kStageA0Forward, false);
         hip_check(launch_a0_forward(la, r0f_.as<float>(), A0_.as<float>(), s), "A0 forward");
+        mark(kStageA0Forward, true);
+        mark(kStageM0Forward, false);
         hip_check(launch_m0_forward(la, p0, A0_.as<float>(), M0_.as<float>(), s), "M0 forward");
+        mark(kStageM0Forward, true);
+        mark(kStageH1Gemm, false);
         for (int l = 0; l <= model_.L_max; ++l) {
             GemmArgs g;
             g.nodes = N;
@@ -749,9 +796,13 @@ void Evaluator::evaluate()
             g.c = {H1_.as<float>() + l * l * C_, nodeLM, C_};
             hip_check(launch_gemm(g, s), "H1 gemm");
         }
+        mark(kStageH1Gemm, true);
         // layer 1: Phi1 -> A1
+        mark(kStageR1Forward, false);
         hip_check(launch_r1_forward(la, r1_.as<float>(), cg_.as<float>(), H1_.as<float>(), Phi1_.as<float>(), s),
                   "R1 forward");
+        mark(kStageR1Forward, true);
+        mark(kStageA1Gemm, false);
         for (int l = 0; l <= model_.l_max; ++l) {
             GemmArgs g;
             g.nodes = N;
@@ -764,6 +815,7 @@ void Evaluator::evaluate()
             g.c = {A1_.as<float>() + l * l * C_, nodelm, C_};
             if (num_e_[l] > 0) hip_check(launch_gemm(g, s), "A1 gemm");
         }
+        mark(kStageA1Gemm, true);
         // readout and its reverse down to A1_adj
         ReadoutArgs ra;
         ra.num_nodes = N;
@@ -786,7 +838,10 @@ void Evaluator::evaluate()
         ra.energies = energies_.as<double>();
         ra.direct = direct_.as<float>();
         ra.A1_adj = A1adj_.as<float>();
+        mark(kStageReadout, false);
         hip_check(launch_readout(ra, s), "readout");
+        mark(kStageReadout, true);
+        mark(kStageA1ReverseGemm, false);
         // dPhi1 = A1_adj A1_W^T  (into the Phi1 buffer, no longer needed)
         float* dPhi1 = Phi1_.as<float>();
         for (int l = 0; l <= model_.l_max; ++l) {
@@ -801,10 +856,16 @@ void Evaluator::evaluate()
             g.c = {dPhi1 + static_cast<long long>(lme_off_[l]) * C_, nodelme, static_cast<long long>(num_e_[l]) * C_};
             hip_check(launch_gemm(g, s), "A1 reverse gemm");
         }
+        mark(kStageA1ReverseGemm, true);
+        mark(kStageR1Reverse, false);
         hip_check(launch_r1_reverse(la, r1_.as<float>(), cg_.as<float>(), H1_.as<float>(), dPhi1,
                                     forces_.as<double>(), msg_.as<float>(), s),
                   "R1 reverse");
+        mark(kStageR1Reverse, true);
+        mark(kStageGather, false);
         hip_check(launch_gather_messages(la, msg_.as<float>(), H1adj_.as<float>(), s), "H1 adjoint gather");
+        mark(kStageGather, true);
+        mark(kStageH1ReverseGemm, false);
         // M0_adj = H1_adj H1_W^T (+ direct scalar adjoint), into the M0 buffer
         float* M0adj = M0_.as<float>();
         for (int l = 0; l <= model_.L_max; ++l) {
@@ -819,17 +880,32 @@ void Evaluator::evaluate()
             hip_check(launch_gemm(g, s), "H1 reverse gemm");
         }
         hip_check(launch_add_direct(N, C_, nLM_, direct_.as<float>(), M0adj, s), "direct adjoint");
+        mark(kStageH1ReverseGemm, true);
         // A0_adj into the A1 buffer (no longer needed)
         float* A0adj = A1_.as<float>();
+        mark(kStageM0Reverse, false);
         hip_check(launch_m0_reverse(la, p0, A0_.as<float>(), M0adj, A0adj, s), "M0 reverse");
+        mark(kStageM0Reverse, true);
+        mark(kStageA0Reverse, false);
         hip_check(launch_a0_reverse(la, r0f_.as<float>(), A0adj, forces_.as<double>(), s), "A0 reverse");
+        mark(kStageA0Reverse, true);
     }
+    mark(kStageAtomForces, false);
     hip_check(launch_atom_forces(N, first_.as<int>(), tfirst_.as<int>(), tedge_.as<int>(), forces_.as<double>(),
                                  atom_forces_.as<double>(), s),
               "atom forces");
+    mark(kStageAtomForces, true);
     // the evaluation (and any copy from caller-owned host arrays) has completed
     // when this returns
     hip_check(hipStreamSynchronize(s), "evaluation");
+    if (profiling_)
+        for (int i = 0; i < kNumStages; ++i) {
+            if (!stage_used_[i]) continue;
+            float ms = 0.0f;
+            hip_check(hipEventElapsedTime(&ms, events_[2 * i], events_[2 * i + 1]), "event time");
+            stage_ms_[i] += ms;
+            stage_count_[i] += 1;
+        }
     evaluated_generation_ = generation_;
     reduced_ = false;
     stats_.evaluations += 1;

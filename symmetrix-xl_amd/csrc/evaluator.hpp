@@ -68,6 +68,27 @@ struct EvaluatorStats {
     int evaluations = 0;
 };
 
+// Stages of one evaluation, timed with HIP events on the evaluator's stream
+// when profiling is enabled.
+enum Stage {
+    kStageGeometry = 0,
+    kStageA0Forward,
+    kStageM0Forward,
+    kStageH1Gemm,
+    kStageR1Forward,
+    kStageA1Gemm,
+    kStageReadout,
+    kStageA1ReverseGemm,
+    kStageR1Reverse,
+    kStageGather,
+    kStageH1ReverseGemm,
+    kStageM0Reverse,
+    kStageA0Reverse,
+    kStageAtomForces,
+    kNumStages
+};
+const char* stage_name(int stage);
+
 class Evaluator {
 public:
     Evaluator(const std::string& model_path, const std::string& head);
@@ -114,6 +135,10 @@ public:
 
     const EvaluatorStats& stats() const { return stats_; }
 
+    // Per-stage device time (ms) accumulated over profiled evaluations.
+    void set_profiling(bool enable);
+    void stage_times(double* ms, int* counts) const;
+
 private:
     void check_generation(std::uint64_t generation) const;
     void prepare_active_types(const std::vector<int>& node_types);
@@ -158,6 +183,13 @@ private:
         atom_forces_, partials_, totals_, scratch_;
     bool reduced_ = false;
     double reduced_volume_ = 0.0;
+
+    bool profiling_ = false;
+    std::vector<hipEvent_t> events_;  // [stage][begin, end]
+    double stage_ms_[kNumStages] = {};
+    int stage_count_[kNumStages] = {};
+    bool stage_used_[kNumStages] = {};
+    void mark(int stage, bool end);
 };
 
 }  // namespace sxl

@@ -88,6 +88,10 @@ SIGNATURES = {
     "sxl_neighbor_graph_copy": (ctypes.c_int, [ctypes.c_void_p, c_int_p, c_int_p, c_int_p, c_int_p,
                                                c_double_p]),
     "sxl_neighbor_graph_free": (None, [ctypes.c_void_p]),
+    "sxl_set_profiling": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
+    "sxl_num_stages": (ctypes.c_int, []),
+    "sxl_stage_name": (ctypes.c_char_p, [ctypes.c_int]),
+    "sxl_stage_times": (ctypes.c_int, [ctypes.c_void_p, c_double_p, c_int_p]),
 }
 
 _lib = None

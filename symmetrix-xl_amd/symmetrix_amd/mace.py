@@ -223,6 +223,12 @@ class MACEKokkosFloat:
                                              ctypes.byref(out)))
         return float(out.value)
 
+    def _max_displacement_device(self, generation, positions_ptr):
+        out = ctypes.c_double(0.0)
+        check(library().sxl_max_displacement(self._h, c_u64(int(generation)), ctypes.c_void_p(int(positions_ptr)),
+                                             1, ctypes.byref(out)))
+        return float(out.value)
+
     # ---- results ----------------------------------------------------------------
     @property
     def node_energies(self):
@@ -269,6 +275,18 @@ class MACEKokkosFloat:
 
     def _synchronize(self):
         check(library().sxl_synchronize(self._h))
+
+    def _set_profiling(self, enable=True):
+        check(library().sxl_set_profiling(self._h, 1 if enable else 0))
+
+    def _stage_times(self):
+        """{stage: (accumulated device ms, count)} of profiled evaluations."""
+        lib = library()
+        n = lib.sxl_num_stages()
+        ms = np.zeros(n, dtype=np.float64)
+        counts = np.zeros(n, dtype=np.int32)
+        check(lib.sxl_stage_times(self._h, _p(ms, ctypes.c_double), _p(counts, ctypes.c_int)))
+        return {lib.sxl_stage_name(i).decode(): (float(ms[i]), int(counts[i])) for i in range(n)}
 
     @property
     def stats(self):
