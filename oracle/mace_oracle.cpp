@@ -851,6 +851,63 @@ int oracle_mace_compute_f64(void* h, int N, const int* types, const int* num_nei
                            num_threads);
 }
 
+// Harmonics of edge vectors as the oracle forms them in compute():
+// Y [n][num_lm] and dY/d(x,y,z) [n][3][num_lm], double precision.
+void oracle_harmonics(int lmax, long long n, const double* xyz, double* Y, double* dY)
+{
+    const int nlm = (lmax + 1) * (lmax + 1);
+    for (long long e = 0; e < n; ++e) {
+        const double ex = xyz[3 * e], ey = xyz[3 * e + 1], ez = xyz[3 * e + 2];
+        const double rr = std::sqrt(ex * ex + ey * ey + ez * ez);
+        double v[16], gx[16], gy[16], gz[16];
+        double* Ye = Y + e * nlm;
+        double* Ge = dY + e * 3 * nlm;
+        if (rr == 0.0) {
+            for (int lm = 0; lm < nlm; ++lm) {
+                Ye[lm] = lm == 0 ? 1.0 : 0.0;
+                Ge[lm] = Ge[nlm + lm] = Ge[2 * nlm + lm] = 0.0;
+            }
+            continue;
+        }
+        const double u0 = ez / rr, u1 = ex / rr, u2 = ey / rr;
+        real_harmonics<double>(lmax, u0, u1, u2, v, gx, gy, gz);
+        const double norm = 3.5449077018110318;
+        for (int l = 0; l <= lmax; ++l)
+            for (int lm = l * l; lm < (l + 1) * (l + 1); ++lm) {
+                Ye[lm] = norm * v[lm];
+                Ge[lm] = norm * (gy[lm] - l * v[lm] * u1) / rr;
+                Ge[nlm + lm] = norm * (gz[lm] - l * v[lm] * u2) / rr;
+                Ge[2 * nlm + lm] = norm * (gx[lm] - l * v[lm] * u0) / rr;
+            }
+    }
+}
+
+// The oracle's cubic Hermite spline set (double): values and derivatives of
+// nfn functions at n points.  values/derivs are nodal [nfn][nodes].
+void oracle_spline_eval(double h, double x0, int nodes, int nfn, const double* values, const double* derivs,
+                        long long n, const double* r, double* out_value, double* out_deriv)
+{
+    SplineSet<double> sp;
+    sp.build(h, x0, nodes, nfn, values, derivs);
+    for (long long e = 0; e < n; ++e) {
+        int iv;
+        double x;
+        sp.point(r[e], iv, x);
+        const double* c = sp.coef(iv);
+        for (int f = 0; f < nfn; ++f) {
+            out_value[e * nfn + f] = c[f] + c[nfn + f] * x + c[2 * nfn + f] * x * x + c[3 * nfn + f] * x * x * x;
+            out_deriv[e * nfn + f] = c[nfn + f] + 2.0 * c[2 * nfn + f] * x + 3.0 * c[3 * nfn + f] * x * x;
+        }
+    }
+}
+
+// The oracle's polynomial (value and gradient) of monomials of degree 1..3.
+double oracle_poly_eval(int num_terms, const int* degree, const int* index, const double* coef, int nvar,
+                        const double* x, double* grad)
+{
+    return Oracle<double>::poly(coef, degree, index, 0, num_terms, x, grad, nvar);
+}
+
 // Atom forces F_a = sum_{e: src=a} f_e - sum_{e: recv=a} f_e and stress
 // sigma[3a+b] = -(1/V) sum_e f_e[a] xyz_e[b]
 // (mace_kokkos_evaluate.cpp:87-106, 156-186), serial in edge order.

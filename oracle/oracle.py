@@ -401,6 +401,46 @@ class MaceOracle:
         return energies, forces
 
 
+def harmonics(lmax, xyz):
+    """The oracle's harmonics Y (n, num_lm) and gradients dY (n, 3, num_lm)."""
+    x = np.ascontiguousarray(xyz, dtype=np.float64).reshape(-1, 3)
+    nlm = (lmax + 1) ** 2
+    Y = np.zeros((len(x), nlm))
+    dY = np.zeros((len(x), 3, nlm))
+    _lib().oracle_harmonics(ctypes.c_int(lmax), ctypes.c_longlong(len(x)), _ptr(x, ctypes.c_double),
+                            _ptr(Y, ctypes.c_double), _ptr(dY, ctypes.c_double))
+    return Y, dY
+
+
+def spline_eval(h, x0, values, derivs, r):
+    """The oracle's Hermite spline set at points r: values, derivatives (n, nfn)."""
+    v = np.ascontiguousarray(values, dtype=np.float64)
+    d = np.ascontiguousarray(derivs, dtype=np.float64)
+    nfn, nodes = v.shape
+    rr = np.ascontiguousarray(r, dtype=np.float64)
+    out_v = np.zeros((len(rr), nfn))
+    out_d = np.zeros((len(rr), nfn))
+    _lib().oracle_spline_eval(ctypes.c_double(h), ctypes.c_double(x0), ctypes.c_int(nodes), ctypes.c_int(nfn),
+                              _ptr(v, ctypes.c_double), _ptr(d, ctypes.c_double), ctypes.c_longlong(len(rr)),
+                              _ptr(rr, ctypes.c_double), _ptr(out_v, ctypes.c_double),
+                              _ptr(out_d, ctypes.c_double))
+    return out_v, out_d
+
+
+def poly_eval(monomials, coefficients, x):
+    """The oracle's polynomial value and gradient."""
+    deg, idx = _monomial_arrays(monomials)
+    c = np.ascontiguousarray(coefficients, dtype=np.float64)
+    xv = np.ascontiguousarray(x, dtype=np.float64)
+    g = np.zeros(len(xv))
+    lib = _lib()
+    lib.oracle_poly_eval.restype = ctypes.c_double
+    f = lib.oracle_poly_eval(ctypes.c_int(len(deg)), _ptr(deg, ctypes.c_int), _ptr(idx, ctypes.c_int),
+                             _ptr(c, ctypes.c_double), ctypes.c_int(len(xv)), _ptr(xv, ctypes.c_double),
+                             _ptr(g, ctypes.c_double))
+    return f, g
+
+
 def reduce(num_neigh, neigh_indices, forces, xyz, volume):
     """Atom forces (N, 3) and the 3x3 stress from directed edge forces."""
     lib = _lib()

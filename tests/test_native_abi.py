@@ -1,0 +1,90 @@
+"""The C-ABI library without a GPU: it loads, exports exactly the entry points
+declared in include/symmetrix_amd.h, and reports loader errors (which happen
+before any device work) with the reference's error classes."""
+
+import ctypes
+import json
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "symmetrix_amd.h")
+
+
+def declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(sxl_[a-z_0-9]+)\s*\(", text))
+
+
+def test_library_exports_every_declared_symbol():
+    from symmetrix_amd import _native
+
+    lib = _native.library()
+    names = declared()
+    assert len(names) >= 30
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(_native.SIGNATURES) == names
+
+
+def test_stage_names():
+    from symmetrix_amd import _native
+
+    lib = _native.library()
+    n = lib.sxl_num_stages()
+    names = [lib.sxl_stage_name(i).decode() for i in range(n)]
+    assert "r1_reverse" in names and "a0_forward" in names and len(set(names)) == n
+
+
+def _create(path):
+    from symmetrix_amd import _native
+
+    h = ctypes.c_void_p()
+    status = _native.library().sxl_create(path.encode(), b"", ctypes.byref(h))
+    return status, _native.library().sxl_last_error().decode()
+
+
+def test_missing_model_file_is_invalid_argument():
+    status, msg = _create("/nonexistent/model.json")
+    assert status == 1 and "cannot open model file" in msg
+
+
+@pytest.mark.parametrize(
+    "change, message",
+    [
+        ({"symmetrix_format_version": 2}, "format version 4"),
+        ({"h1_affine_mode": "other"}, "h1_affine_mode"),
+        ({"has_zbl": True}, "ZBL"),
+        ({"radial_representation": "pair-splines"}, "compact radial"),
+        ({"l_max": 5}, "L_max <= l_max <= 3"),
+        ({"readout_1_weights": [0.0]}, "old-basis"),
+    ],
+)
+def test_model_validation_errors(tmp_path, change, message):
+    from symmetrix_amd import synthetic
+
+    model = json.loads(synthetic.model_json(synthetic.random_mace_model("tiny", seed=0)))
+    model.update(change)
+    path = tmp_path / "m.json"
+    path.write_text(json.dumps(model))
+    status, msg = _create(str(path))
+    assert status == 1, msg
+    assert message in msg
+
+
+def test_malformed_json(tmp_path):
+    path = tmp_path / "m.json"
+    path.write_text('{"num_elements": 1, ')
+    status, msg = _create(str(path))
+    assert status == 1 and "parse error" in msg
+
+
+def test_null_arguments_are_rejected():
+    from symmetrix_amd import _native
+
+    lib = _native.library()
+    assert lib.sxl_create(None, None, None) == 1
+    assert lib.sxl_stats(None, None) == 1

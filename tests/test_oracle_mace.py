@@ -1,0 +1,133 @@
+"""The MACE oracle end to end (CPU): forces and stress against finite
+differences of its own energy (the reference method,
+symmetrix/test/test_mace.py:687-750, rtol 1e-4 / atol 1e-6 in FP64), global
+invariances, FP32 vs FP64 (reference test_mace_streamed_edges.py:556, atol
+3e-5), and skin-masked vs exact graphs (reference :4592-4675).
+"""
+
+import json
+
+import numpy as np
+import pytest
+
+
+@pytest.fixture(scope="module")
+def tiny():
+    from symmetrix_amd import synthetic
+
+    return json.loads(synthetic.model_json(synthetic.random_mace_model("tiny", seed=0)))
+
+
+@pytest.fixture(scope="module")
+def structure():
+    from symmetrix_amd import synthetic
+
+    return synthetic.srtio3_supercell(2, sigma=0.1, seed=3)
+
+
+def make(oracle_lib, model, structure, precision="float64"):
+    from symmetrix_amd import synthetic
+
+    types = synthetic.node_types(structure, model["atomic_numbers"])
+    return oracle_lib.MaceOracle(model, np.unique(types), precision)
+
+
+def energy(oracle_lib, orc, model, s, skin=0.5):
+    return oracle_lib.evaluate(orc, s, model["r_cut"] + skin)["energy"]
+
+
+def test_forces_match_finite_differences(oracle_lib, tiny, structure):
+    orc = make(oracle_lib, tiny, structure)
+    base = oracle_lib.evaluate(orc, structure, tiny["r_cut"] + 0.5)
+    h = 1e-4
+    for atom, axis in [(0, 0), (5, 1), (17, 2), (33, 0)]:
+        sp, sm = structure.copy(), structure.copy()
+        sp.positions[atom, axis] += h
+        sm.positions[atom, axis] -= h
+        fd = -(energy(oracle_lib, orc, tiny, sp) - energy(oracle_lib, orc, tiny, sm)) / (2 * h)
+        assert base["forces"][atom, axis] == pytest.approx(fd, rel=1e-4, abs=1e-6)
+
+
+def test_directed_forces_are_edge_gradients(oracle_lib, tiny, structure):
+    orc = make(oracle_lib, tiny, structure)
+    res = oracle_lib.evaluate(orc, structure, tiny["r_cut"] + 0.5)
+    gi = res["inputs"]
+    h = 1e-5
+    for e in [0, 7, 123]:
+        for axis in range(3):
+            xp, xm = gi["xyz"].copy(), gi["xyz"].copy()
+            xp[e, axis] += h
+            xm[e, axis] -= h
+            ep = orc.compute(gi["node_types"], gi["num_neigh"], gi["neigh_indices"], gi["neigh_types"], xp,
+                             np.linalg.norm(xp, axis=1))[0].sum()
+            em = orc.compute(gi["node_types"], gi["num_neigh"], gi["neigh_indices"], gi["neigh_types"], xm,
+                             np.linalg.norm(xm, axis=1))[0].sum()
+            assert res["directed_forces"][e, axis] == pytest.approx(-(ep - em) / (2 * h), rel=1e-4, abs=1e-7)
+
+
+def test_stress_matches_strain_derivative(oracle_lib, tiny, structure):
+    orc = make(oracle_lib, tiny, structure)
+    base = oracle_lib.evaluate(orc, structure, tiny["r_cut"] + 0.5)
+    eps = 1e-5
+    for i, j in [(0, 0), (1, 1), (0, 2), (1, 2)]:
+        def strained(e):
+            F = np.eye(3)
+            F[i, j] += e / 2
+            F[j, i] += e / 2
+            s = structure.copy()
+            s.positions = structure.positions @ F.T
+            s.cell = structure.cell @ F.T
+            return s
+
+        fd = (energy(oracle_lib, orc, tiny, strained(eps)) - energy(oracle_lib, orc, tiny, strained(-eps))) / (2 * eps)
+        assert base["stress_3x3"][i, j] == pytest.approx(fd / structure.volume, rel=1e-4, abs=1e-8)
+    s = base["stress_3x3"]
+    np.testing.assert_allclose(s, s.T, atol=1e-9)
+
+
+def test_forces_sum_to_zero_and_translation_invariance(oracle_lib, tiny, structure):
+    orc = make(oracle_lib, tiny, structure)
+    base = oracle_lib.evaluate(orc, structure, tiny["r_cut"] + 0.5)
+    np.testing.assert_allclose(base["forces"].sum(axis=0), 0.0, atol=1e-10)
+    moved = structure.copy()
+    moved.positions = moved.positions + np.array([0.31, -1.7, 2.2])
+    assert energy(oracle_lib, orc, tiny, moved) == pytest.approx(base["energy"], abs=1e-9)
+
+
+def test_rotation_invariance(oracle_lib, tiny, structure):
+    # energy invariant and forces covariant under a global rotation of atoms and
+    # cell: pins harmonics, coupling tables and polynomial equivariance together
+    from symmetrix_amd import irreps
+
+    orc = make(oracle_lib, tiny, structure)
+    base = oracle_lib.evaluate(orc, structure, tiny["r_cut"] + 0.5)
+    R = irreps.random_rotation(9)
+    rot = structure.copy()
+    rot.positions = structure.positions @ R.T
+    rot.cell = structure.cell @ R.T
+    res = oracle_lib.evaluate(orc, rot, tiny["r_cut"] + 0.5)
+    assert res["energy"] == pytest.approx(base["energy"], abs=1e-9)
+    np.testing.assert_allclose(res["forces"], base["forces"] @ R.T, atol=1e-10)
+    np.testing.assert_allclose(res["stress_3x3"], R @ base["stress_3x3"] @ R.T, atol=1e-10)
+
+
+def test_float32_matches_float64(oracle_lib, tiny, structure):
+    r64 = oracle_lib.evaluate(make(oracle_lib, tiny, structure, "float64"), structure, tiny["r_cut"] + 0.5)
+    r32 = oracle_lib.evaluate(make(oracle_lib, tiny, structure, "float32"), structure, tiny["r_cut"] + 0.5)
+    np.testing.assert_allclose(r32["energies"], r64["energies"], atol=3e-5)
+    np.testing.assert_allclose(r32["directed_forces"], r64["directed_forces"], atol=3e-5)
+
+
+def test_skin_masked_graph_equals_exact_graph(oracle_lib, tiny, structure):
+    orc = make(oracle_lib, tiny, structure)
+    exact = oracle_lib.evaluate(orc, structure, tiny["r_cut"])
+    skin = oracle_lib.evaluate(orc, structure, tiny["r_cut"] + 0.7)
+    assert skin["energy"] == pytest.approx(exact["energy"], abs=1e-10)
+    np.testing.assert_allclose(skin["forces"], exact["forces"], atol=1e-12)
+
+
+def test_rejects_unsupported_models(oracle_lib, tiny, structure):
+    bad = dict(tiny)
+    bad["has_zbl"] = True
+    with pytest.raises(NotImplementedError):
+        make(oracle_lib, bad, structure)
