@@ -55,6 +55,16 @@ class HipMemory:
             raise RuntimeError("hipMemcpy failed")
         return ptr.value
 
+    def alloc(self, nbytes):
+        ptr = ctypes.c_void_p()
+        if self.lib.hipMalloc(ctypes.byref(ptr), nbytes) != 0:
+            raise RuntimeError("hipMalloc failed")
+        return ptr.value
+
+    def copy_device(self, dst, src, nbytes):
+        if self.lib.hipMemcpy(ctypes.c_void_p(dst), ctypes.c_void_p(src), nbytes, 3) != 0:  # DeviceToDevice
+            raise RuntimeError("hipMemcpy failed")
+
     def synchronize(self):
         if self.lib.hipDeviceSynchronize() != 0:
             raise RuntimeError("hipDeviceSynchronize failed")
@@ -163,7 +173,22 @@ def main():
     ap.add_argument("--cpu-calls", type=int, default=2, help="timed oracle calls for cpu_baseline (0: skip)")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--host-steps", type=int, default=5, help="host-boundary calculator steps (0: skip)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run 3 device-to-device copies of MIB MiB (the known-size kernel that "
+                         "scales FETCH_SIZE / WRITE_SIZE counters to bytes), then exit")
     args = ap.parse_args()
+
+    if args.copy_calibration > 0:
+        hip = HipMemory()
+        nbytes = args.copy_calibration << 20
+        src, dst = hip.alloc(nbytes), hip.alloc(nbytes)
+        for _ in range(3):
+            hip.copy_device(dst, src, nbytes)
+        hip.synchronize()
+        print(json.dumps({"copy_calibration_bytes": nbytes, "copies": 3}), flush=True)
+        hip.free(src)
+        hip.free(dst)
+        return
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py runs on one GPU only: this build has no multi-GPU path "

@@ -13,11 +13,11 @@ namespace sxl {
 constexpr float kShNorm = 3.5449077018110318f;
 
 // Real harmonics (orthonormal, no Condon-Shortley phase) of the permuted unit
-// direction u = (z, x, y)/r, as homogeneous polynomials of degree l, and the
-// gradients of those polynomials with respect to u.
-template <int LMAX, bool GRAD>
-__device__ __forceinline__ void harmonic_forms(float x, float y, float z, float* v, float* gx,
-                                               float* gy, float* gz)
+// direction u = (z, x, y)/r, block l, as homogeneous polynomials of degree l,
+// and the gradients of those polynomials with respect to u.
+template <int L, bool GRAD>
+__device__ __forceinline__ void harmonic_block(float x, float y, float z, float* v, float* gx, float* gy,
+                                               float* gz)
 {
     constexpr float c00 = 0.28209479177387814f;
     constexpr float c1 = 0.4886025119029199f;
@@ -28,64 +28,88 @@ __device__ __forceinline__ void harmonic_forms(float x, float y, float z, float*
     constexpr float c32 = 2.890611442640554f;
     constexpr float c31 = 0.4570457994644658f;
     constexpr float c30 = 0.3731763325901154f;
-    v[0] = c00;
-    if (GRAD) gx[0] = gy[0] = gz[0] = 0.0f;
-    if constexpr (LMAX >= 1) {
-        v[1] = c1 * y;
-        v[2] = c1 * z;
-        v[3] = c1 * x;
+    if constexpr (L == 0) {
+        v[0] = c00;
+        if (GRAD) gx[0] = gy[0] = gz[0] = 0.0f;
+    } else if constexpr (L == 1) {
+        v[0] = c1 * y;
+        v[1] = c1 * z;
+        v[2] = c1 * x;
         if (GRAD) {
-            gx[1] = 0.0f, gy[1] = c1, gz[1] = 0.0f;
-            gx[2] = 0.0f, gy[2] = 0.0f, gz[2] = c1;
-            gx[3] = c1, gy[3] = 0.0f, gz[3] = 0.0f;
+            gx[0] = 0.0f, gy[0] = c1, gz[0] = 0.0f;
+            gx[1] = 0.0f, gy[1] = 0.0f, gz[1] = c1;
+            gx[2] = c1, gy[2] = 0.0f, gz[2] = 0.0f;
+        }
+    } else if constexpr (L == 2) {
+        const float xx = x * x, yy = y * y, zz = z * z;
+        v[0] = c2a * x * y;
+        v[1] = c2a * y * z;
+        v[2] = c20 * (2.0f * zz - xx - yy);
+        v[3] = c2a * x * z;
+        v[4] = c22 * (xx - yy);
+        if (GRAD) {
+            gx[0] = c2a * y, gy[0] = c2a * x, gz[0] = 0.0f;
+            gx[1] = 0.0f, gy[1] = c2a * z, gz[1] = c2a * y;
+            gx[2] = -2.0f * c20 * x, gy[2] = -2.0f * c20 * y, gz[2] = 4.0f * c20 * z;
+            gx[3] = c2a * z, gy[3] = 0.0f, gz[3] = c2a * x;
+            gx[4] = 2.0f * c22 * x, gy[4] = -2.0f * c22 * y, gz[4] = 0.0f;
+        }
+    } else {
+        static_assert(L == 3, "harmonic blocks up to l = 3");
+        const float xx = x * x, yy = y * y, zz = z * z;
+        v[0] = c33 * y * (3.0f * xx - yy);
+        v[1] = c32 * x * y * z;
+        v[2] = c31 * y * (4.0f * zz - xx - yy);
+        v[3] = c30 * z * (2.0f * zz - 3.0f * xx - 3.0f * yy);
+        v[4] = c31 * x * (4.0f * zz - xx - yy);
+        v[5] = 0.5f * c32 * z * (xx - yy);
+        v[6] = c33 * x * (xx - 3.0f * yy);
+        if (GRAD) {
+            gx[0] = 6.0f * c33 * x * y, gy[0] = 3.0f * c33 * (xx - yy), gz[0] = 0.0f;
+            gx[1] = c32 * y * z, gy[1] = c32 * x * z, gz[1] = c32 * x * y;
+            gx[2] = -2.0f * c31 * x * y, gy[2] = c31 * (4.0f * zz - xx - 3.0f * yy),
+            gz[2] = 8.0f * c31 * y * z;
+            gx[3] = -6.0f * c30 * x * z, gy[3] = -6.0f * c30 * y * z,
+            gz[3] = c30 * (6.0f * zz - 3.0f * xx - 3.0f * yy);
+            gx[4] = c31 * (4.0f * zz - 3.0f * xx - yy), gy[4] = -2.0f * c31 * x * y,
+            gz[4] = 8.0f * c31 * x * z;
+            gx[5] = c32 * x * z, gy[5] = -c32 * y * z, gz[5] = 0.5f * c32 * (xx - yy);
+            gx[6] = 3.0f * c33 * (xx - yy), gy[6] = -6.0f * c33 * x * y, gz[6] = 0.0f;
         }
     }
-    if constexpr (LMAX >= 2) {
-        const float xx = x * x, yy = y * y, zz = z * z;
-        v[4] = c2a * x * y;
-        v[5] = c2a * y * z;
-        v[6] = c20 * (2.0f * zz - xx - yy);
-        v[7] = c2a * x * z;
-        v[8] = c22 * (xx - yy);
-        if (GRAD) {
-            gx[4] = c2a * y, gy[4] = c2a * x, gz[4] = 0.0f;
-            gx[5] = 0.0f, gy[5] = c2a * z, gz[5] = c2a * y;
-            gx[6] = -2.0f * c20 * x, gy[6] = -2.0f * c20 * y, gz[6] = 4.0f * c20 * z;
-            gx[7] = c2a * z, gy[7] = 0.0f, gz[7] = c2a * x;
-            gx[8] = 2.0f * c22 * x, gy[8] = -2.0f * c22 * y, gz[8] = 0.0f;
-        }
-    }
-    if constexpr (LMAX >= 3) {
-        const float xx = x * x, yy = y * y, zz = z * z;
-        v[9] = c33 * y * (3.0f * xx - yy);
-        v[10] = c32 * x * y * z;
-        v[11] = c31 * y * (4.0f * zz - xx - yy);
-        v[12] = c30 * z * (2.0f * zz - 3.0f * xx - 3.0f * yy);
-        v[13] = c31 * x * (4.0f * zz - xx - yy);
-        v[14] = 0.5f * c32 * z * (xx - yy);
-        v[15] = c33 * x * (xx - 3.0f * yy);
-        if (GRAD) {
-            gx[9] = 6.0f * c33 * x * y, gy[9] = 3.0f * c33 * (xx - yy), gz[9] = 0.0f;
-            gx[10] = c32 * y * z, gy[10] = c32 * x * z, gz[10] = c32 * x * y;
-            gx[11] = -2.0f * c31 * x * y, gy[11] = c31 * (4.0f * zz - xx - 3.0f * yy),
-            gz[11] = 8.0f * c31 * y * z;
-            gx[12] = -6.0f * c30 * x * z, gy[12] = -6.0f * c30 * y * z,
-            gz[12] = c30 * (6.0f * zz - 3.0f * xx - 3.0f * yy);
-            gx[13] = c31 * (4.0f * zz - 3.0f * xx - yy), gy[13] = -2.0f * c31 * x * y,
-            gz[13] = 8.0f * c31 * x * z;
-            gx[14] = c32 * x * z, gy[14] = -c32 * y * z, gz[14] = 0.5f * c32 * (xx - yy);
-            gx[15] = 3.0f * c33 * (xx - yy), gy[15] = -6.0f * c33 * x * y, gz[15] = 0.0f;
+}
+
+// Block l of the MACE harmonics of the unit direction u (Cartesian) and, with
+// GRAD, their gradients d/d(x,y,z) for |r| = 1/ir; written to Y[lm] and
+// dY{x,y,z}[lm], lm = l^2 .. (l+1)^2 - 1.
+template <int L, bool GRAD>
+__device__ __forceinline__ void harmonic_block_out(float ux, float uy, float uz, float ir, float* Y,
+                                                   float* dYx, float* dYy, float* dYz)
+{
+    constexpr int M = 2 * L + 1;
+    float v[M], g0[M], g1[M], g2[M];
+    // permuted direction (z, x, y)
+    harmonic_block<L, GRAD>(uz, ux, uy, v, g0, g1, g2);
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        Y[L * L + m] = kShNorm * v[m];
+        if constexpr (GRAD) {
+            const float lv = static_cast<float>(L) * v[m];
+            // d/dx <- d/du1, d/dy <- d/du2, d/dz <- d/du0
+            dYx[L * L + m] = kShNorm * (g1[m] - lv * ux) * ir;
+            dYy[L * L + m] = kShNorm * (g2[m] - lv * uy) * ir;
+            dYz[L * L + m] = kShNorm * (g0[m] - lv * uz) * ir;
         }
     }
 }
 
 // MACE harmonics Y[lm] of an edge vector (x,y,z) with length r, and
-// optionally dY/d(x,y,z) (unpermuted Cartesian components).
+// optionally dY/d(x,y,z) (unpermuted Cartesian components).  The outputs may
+// point into LDS: each l block is stored as soon as it is formed.
 template <int LMAX, bool GRAD>
 __device__ __forceinline__ void edge_harmonics(const double* xyz, double r, float* Y, float* dYx,
                                                float* dYy, float* dYz, float* dir)
 {
-    constexpr int NLM = (LMAX + 1) * (LMAX + 1);
     const double inv = 1.0 / r;
     const float ux = static_cast<float>(xyz[0] * inv);
     const float uy = static_cast<float>(xyz[1] * inv);
@@ -93,23 +117,11 @@ __device__ __forceinline__ void edge_harmonics(const double* xyz, double r, floa
     dir[0] = ux;
     dir[1] = uy;
     dir[2] = uz;
-    float v[NLM], g0[NLM], g1[NLM], g2[NLM];
-    // permuted direction (z, x, y)
-    harmonic_forms<LMAX, GRAD>(uz, ux, uy, v, g0, g1, g2);
     const float ir = static_cast<float>(inv);
-#pragma unroll
-    for (int l = 0; l <= LMAX; ++l)
-#pragma unroll
-        for (int lm = l * l; lm < (l + 1) * (l + 1); ++lm) {
-            Y[lm] = kShNorm * v[lm];
-            if constexpr (GRAD) {
-                const float lv = static_cast<float>(l) * v[lm];
-                // d/dx <- d/du1, d/dy <- d/du2, d/dz <- d/du0
-                dYx[lm] = kShNorm * (g1[lm] - lv * ux) * ir;
-                dYy[lm] = kShNorm * (g2[lm] - lv * uy) * ir;
-                dYz[lm] = kShNorm * (g0[lm] - lv * uz) * ir;
-            }
-        }
+    harmonic_block_out<0, GRAD>(ux, uy, uz, ir, Y, dYx, dYy, dYz);
+    if constexpr (LMAX >= 1) harmonic_block_out<1, GRAD>(ux, uy, uz, ir, Y, dYx, dYy, dYz);
+    if constexpr (LMAX >= 2) harmonic_block_out<2, GRAD>(ux, uy, uz, ir, Y, dYx, dYy, dYz);
+    if constexpr (LMAX >= 3) harmonic_block_out<3, GRAD>(ux, uy, uz, ir, Y, dYx, dYy, dYz);
 }
 
 // Cubic Hermite evaluation point (reference cubic_spline_set.cpp:32-47),
@@ -147,6 +159,70 @@ __device__ __forceinline__ float wave_sum(float v)
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
     return v;
+}
+
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_moved(float v)
+{
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xf, false));
+}
+
+// Sum over the 64 lanes of a wave with DPP moves (quad permutes, row
+// mirrors, row broadcasts), returned wave-uniform.  Fixed combination order,
+// so the result is run-to-run identical.
+__device__ __forceinline__ float wave_sum_dpp(float v)
+{
+    v += dpp_moved<0xb1>(v);         // quad_perm [1,0,3,2]
+    v += dpp_moved<0x4e>(v);         // quad_perm [2,3,0,1]
+    v += dpp_moved<0x141>(v);        // row_half_mirror
+    v += dpp_moved<0x140>(v);        // row_mirror
+    v += dpp_moved<0x142, 0xa>(v);   // row_bcast:15 into rows 1 and 3
+    v += dpp_moved<0x143, 0xc>(v);   // row_bcast:31 into rows 2 and 3
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ float uniform(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+}
+
+// Raw (untyped) buffer resource over [base, base + bytes); gfx9 word 3.
+// Loads beyond `bytes` return zero and stores beyond it are dropped.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+
+typedef float float4v __attribute__((ext_vector_type(4)));
+
+// The raw buffer builtins move untyped 32-bit words (unsigned int); the
+// float views are bit casts, never value conversions.
+__device__ __forceinline__ float4v load4(__amdgpu_buffer_rsrc_t r, int voffset, int soffset)
+{
+    return __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(r, voffset, soffset, 0));
+}
+
+__device__ __forceinline__ float load1(__amdgpu_buffer_rsrc_t r, int voffset, int soffset)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voffset, soffset, 0));
+}
+
+__device__ __forceinline__ void store1(float v, __amdgpu_buffer_rsrc_t r, int voffset, int soffset)
+{
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned int, v), r, voffset, soffset, 0);
+}
+
+// Cubic of one interval, c = (c0, c1, c2, c3) in local coordinate x.
+__device__ __forceinline__ float cubic(const float4v& c, float x)
+{
+    return fmaf(x, fmaf(x, fmaf(x, c.w, c.z), c.y), c.x);
+}
+
+__device__ __forceinline__ float cubic_slope(const float4v& c, float x, float x3)
+{
+    return fmaf(x, fmaf(x3, c.w, c.z + c.z), c.y);
 }
 
 __device__ __forceinline__ int unordered_pair(int a, int b, int n)

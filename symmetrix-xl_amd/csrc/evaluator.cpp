@@ -301,7 +301,7 @@ void Evaluator::prepare_active_types(const std::vector<int>& node_types)
         c4[2] = (-3.0 * v0 - 2.0 * h * d0 + 3.0 * v1 - h * d1) / (h * h);
         c4[3] = (2.0 * v0 + h * d0 - 2.0 * v1 + h * d1) / (h * h * h);
     };
-    // R1 table: [pair_u][iv][q][p][k]
+    // R1 table: [pair_u][iv][p][k][q]
     std::vector<float> r1(static_cast<std::size_t>(npairs) * NI * 4 * NP * C_);
     for (int pu = 0; pu < npairs; ++pu)
         for (int iv = 0; iv < NI; ++iv)
@@ -310,10 +310,10 @@ void Evaluator::prepare_active_types(const std::vector<int>& node_types)
                     double c4[4];
                     hermite(r1v[pu], r1d[pu], p * C_ + k, iv, c4);
                     for (int q = 0; q < 4; ++q)
-                        r1[((((static_cast<std::size_t>(pu) * NI + iv) * 4 + q) * NP + p) * C_) + k] =
+                        r1[(((static_cast<std::size_t>(pu) * NI + iv) * NP + p) * C_ + k) * 4 + q] =
                             static_cast<float>(c4[q]);
                 }
-    // R0 folded: [pair_o][iv][q][l][k'] = sum_k c[iv][q][l*C+k] H0[tj][k] A0W[ti][l][k][k']
+    // R0 folded: [pair_o][iv][l][k'][q] = sum_k c[iv][q][l*C+k] H0[tj][k] A0W[ti][l][k][k']
     std::vector<float> r0f(static_cast<std::size_t>(na) * na * NI * 4 * NL * C_);
     auto fold = [&](int po) {
         const int ai = po / na, aj = po % na;
@@ -335,8 +335,8 @@ void Evaluator::prepare_active_types(const std::vector<int>& node_types)
                         const double* w = W + static_cast<std::size_t>(k) * C_;
                         for (int ko = 0; ko < C_; ++ko) out[ko] += uk * w[ko];
                     }
-                    float* dst = r0f.data() + ((((static_cast<std::size_t>(po) * NI + iv) * 4 + q) * NL + l) * C_);
-                    for (int ko = 0; ko < C_; ++ko) dst[ko] = static_cast<float>(out[ko]);
+                    float* dst = r0f.data() + (((static_cast<std::size_t>(po) * NI + iv) * NL + l) * C_) * 4 + q;
+                    for (int ko = 0; ko < C_; ++ko) dst[4 * ko] = static_cast<float>(out[ko]);
                 }
     };
     {

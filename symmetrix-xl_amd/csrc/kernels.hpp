@@ -9,9 +9,11 @@
 //   directed forces f   [E][3] f64
 //   H1 messages     msg [E][num_LM][C] (H1-adjoint contributions per edge)
 //   spline tables   R0 folded per ordered active pair:
-//                     [pair_o][interval][4][l_max+1][C]
+//                     [pair_o][interval][l_max+1][C][4]
 //                   R1 per unordered active pair:
-//                     [pair_u][interval][4][num_paths][C]
+//                     [pair_u][interval][num_paths][C][4]
+//                   (the 4 cubic coefficients of one channel are one 16-byte
+//                   load; a wave reads 1 KiB contiguous per path)
 #pragma once
 
 #include <hip/hip_runtime.h>

@@ -35,6 +35,38 @@ __device__ __forceinline__ int receiver_of_block(const LayerArgs& a)
 }
 
 // ---------------------------------------------------------------------------
+// Edge tiles.  Wave 0 of the workgroup stages up to 64 edges of the receiver:
+// the edges within r_cut are compacted (ballot + lane prefix count) into LDS
+// slots with their spline row, local coordinate and harmonics; the channel
+// loops then run over the active slots only.  Spline rows are addressed
+// through buffer resources built from wave-uniform (scalar) row bases, so a
+// coefficient load costs no vector address arithmetic.
+// ---------------------------------------------------------------------------
+constexpr int kTile = 64;
+
+struct TileSlot {
+    bool active;
+    int slot;
+};
+
+// Ballot-compacts the edges [base, base + n) of the tile; lanes 0..63 of wave 0.
+__device__ __forceinline__ TileSlot compact_edge(const EdgeGraph& g, const SplineGrid& grid, int base,
+                                                 int n, int t, double& rr, int* count)
+{
+    bool on = false;
+    rr = 0.0;
+    if (t < n) {
+        rr = g.r[base + t];
+        on = rr < grid.r_cut;
+    }
+    const unsigned long long mask = __ballot(on);
+    const int slot = __builtin_amdgcn_mbcnt_hi(static_cast<unsigned>(mask >> 32),
+                                               __builtin_amdgcn_mbcnt_lo(static_cast<unsigned>(mask), 0));
+    if (t == 0) *count = __popcll(mask);
+    return {on, slot};
+}
+
+// ---------------------------------------------------------------------------
 // Layer 0 forward: A0[i, lm, k] = sum_j R0f_{pair}(r_ij)[l, k] Y_lm(r_ij)
 // ---------------------------------------------------------------------------
 template <int LMAX>
@@ -43,59 +75,50 @@ __global__ void __launch_bounds__(256) a0_forward_kernel(LayerArgs a, const floa
 {
     constexpr int NLM = (LMAX + 1) * (LMAX + 1);
     constexpr int NL = LMAX + 1;
-    constexpr int TE = 64;
-    __shared__ float s_Y[TE][NLM];
-    __shared__ float s_x[TE];
-    __shared__ int s_iv[TE];
-    __shared__ int s_pair[TE];
+    __shared__ float s_Y[kTile][NLM];
+    __shared__ float s_x[kTile];
+    __shared__ int s_row[kTile];
+    __shared__ int s_count;
 
     const int i = receiver_of_block(a);
     const int k = threadIdx.x;
     const int C = a.C;
     const EdgeGraph& g = a.graph;
+    const int voff = min(k, C - 1) * 16;
+    const int row_bytes = NL * C * 16;
     float acc[NLM];
 #pragma unroll
     for (int lm = 0; lm < NLM; ++lm) acc[lm] = 0.0f;
     const int e0 = g.first[i], e1 = g.first[i + 1];
-    const size_t interval_stride = static_cast<size_t>(4) * NL * C;
-    const size_t pair_stride = static_cast<size_t>(a.grid.intervals) * interval_stride;
-    for (int base = e0; base < e1; base += TE) {
-        const int n = min(TE, e1 - base);
+    for (int base = e0; base < e1; base += kTile) {
         __syncthreads();
-        if (threadIdx.x < n) {
+        if (threadIdx.x < 64) {
             const int t = threadIdx.x;
-            const int e = base + t;
-            const double rr = g.r[e];
-            int iv = -1;
-            if (rr < a.grid.r_cut) {
+            double rr;
+            const TileSlot ts = compact_edge(g, a.grid, base, min(kTile, e1 - base), t, rr, &s_count);
+            if (ts.active) {
+                const int e = base + t;
+                int iv;
                 float x, Y[NLM], dir[3];
                 spline_point(rr, a.grid, iv, x);
                 edge_harmonics<LMAX, false>(g.xyz + 3 * static_cast<size_t>(e), rr, Y, nullptr,
                                             nullptr, nullptr, dir);
-                s_x[t] = x;
-                s_pair[t] = g.edge_pair[e] & 0xffff;
+                s_x[ts.slot] = x;
+                s_row[ts.slot] = (g.edge_pair[e] & 0xffff) * a.grid.intervals + iv;
 #pragma unroll
-                for (int lm = 0; lm < NLM; ++lm) s_Y[t][lm] = Y[lm];
+                for (int lm = 0; lm < NLM; ++lm) s_Y[ts.slot][lm] = Y[lm];
             }
-            s_iv[t] = iv;
         }
         __syncthreads();
-        if (k < C) {
-            for (int j = 0; j < n; ++j) {
-                const int iv = s_iv[j];
-                if (iv < 0) continue;
-                const float x = s_x[j];
-                const float* c = r0f + s_pair[j] * pair_stride + iv * interval_stride + k;
+        const int count = uniform(s_count);
+        for (int j = 0; j < count; ++j) {
+            const float x = uniform(s_x[j]);
+            const auto rs = buffer_rsrc(r0f + static_cast<size_t>(uniform(s_row[j])) * NL * C * 4, row_bytes);
 #pragma unroll
-                for (int l = 0; l <= LMAX; ++l) {
-                    const float c0 = c[(0 * NL + l) * C];
-                    const float c1 = c[(1 * NL + l) * C];
-                    const float c2 = c[(2 * NL + l) * C];
-                    const float c3 = c[(3 * NL + l) * C];
-                    const float R = c0 + x * (c1 + x * (c2 + x * c3));
+            for (int l = 0; l <= LMAX; ++l) {
+                const float R = cubic(load4(rs, voff, l * C * 16), x);
 #pragma unroll
-                    for (int lm = l * l; lm < (l + 1) * (l + 1); ++lm) acc[lm] += R * s_Y[j][lm];
-                }
+                for (int lm = l * l; lm < (l + 1) * (l + 1); ++lm) acc[lm] = fmaf(R, s_Y[j][lm], acc[lm]);
             }
         }
     }
@@ -219,68 +242,60 @@ __global__ void __launch_bounds__(256) r1_forward_kernel(LayerArgs a, const floa
     constexpr int NLMS = (S::LLMAX + 1) * (S::LLMAX + 1);
     constexpr int NP = S::NP;
     constexpr int NT = S::NT;
-    constexpr int TE = 32;
-    __shared__ float s_cgY[TE][(NT + 3) / 4 * 4];
-    __shared__ float s_x[TE];
-    __shared__ int s_iv[TE];
-    __shared__ int s_pair[TE];
-    __shared__ int s_src[TE];
+    constexpr int NPQ = S::NPQ;
+    __shared__ float s_cgY[kTile][(NT + 3) / 4 * 4];
+    __shared__ float s_x[kTile];
+    __shared__ int s_row[kTile];
+    __shared__ int s_src[kTile];
+    __shared__ int s_count;
 
     const int i = receiver_of_block(a);
     const int k = threadIdx.x;
     const int C = a.C;
     const EdgeGraph& g = a.graph;
+    const int kk = min(k, C - 1);
+    const int row_bytes = NP * C * 16;
+    const int h_bytes = NLMS * C * 4;
     float acc[S::NLME];
 #pragma unroll
     for (int q = 0; q < S::NLME; ++q) acc[q] = 0.0f;
     const int e0 = g.first[i], e1 = g.first[i + 1];
-    const size_t interval_stride = static_cast<size_t>(4) * NP * C;
-    const size_t pair_stride = static_cast<size_t>(a.grid.intervals) * interval_stride;
-    for (int base = e0; base < e1; base += TE) {
-        const int n = min(TE, e1 - base);
+    for (int base = e0; base < e1; base += kTile) {
         __syncthreads();
-        if (threadIdx.x < n) {
+        if (threadIdx.x < 64) {
             const int t = threadIdx.x;
-            const int e = base + t;
-            const double rr = g.r[e];
-            int iv = -1;
-            if (rr < a.grid.r_cut) {
+            double rr;
+            const TileSlot ts = compact_edge(g, a.grid, base, min(kTile, e1 - base), t, rr, &s_count);
+            if (ts.active) {
+                const int e = base + t;
+                int iv;
                 float x, Y[NLM], dir[3];
                 spline_point(rr, a.grid, iv, x);
                 edge_harmonics<S::LMAX, false>(g.xyz + 3 * static_cast<size_t>(e), rr, Y, nullptr,
                                                nullptr, nullptr, dir);
-                s_x[t] = x;
-                s_pair[t] = g.edge_pair[e] >> 16;
-                s_src[t] = g.source[e];
+                s_x[ts.slot] = x;
+                s_row[ts.slot] = (g.edge_pair[e] >> 16) * a.grid.intervals + iv;
+                s_src[ts.slot] = g.source[e];
 #pragma unroll
-                for (int q = 0; q < NT; ++q) s_cgY[t][q] = cg[q] * Y[S::term_lm1[q]];
+                for (int q = 0; q < NT; ++q) s_cgY[ts.slot][q] = cg[q] * Y[S::term_lm1[q]];
             }
-            s_iv[t] = iv;
         }
         __syncthreads();
-        if (k < C) {
-            for (int j = 0; j < n; ++j) {
-                const int iv = s_iv[j];
-                if (iv < 0) continue;
-                const float x = s_x[j];
-                const float* c = r1 + s_pair[j] * pair_stride + iv * interval_stride + k;
-                float R[NP];
+        const int count = uniform(s_count);
+        for (int j = 0; j < count; ++j) {
+            const float x = uniform(s_x[j]);
+            const auto rs = buffer_rsrc(r1 + static_cast<size_t>(uniform(s_row[j])) * NP * C * 4, row_bytes);
+            const auto hs = buffer_rsrc(H1 + static_cast<size_t>(uniform(s_src[j])) * NLMS * C, h_bytes);
+            float R[NP], H[NLMS], RH[NPQ];
 #pragma unroll
-                for (int p = 0; p < NP; ++p) {
-                    const float c0 = c[(0 * NP + p) * C];
-                    const float c1 = c[(1 * NP + p) * C];
-                    const float c2 = c[(2 * NP + p) * C];
-                    const float c3 = c[(3 * NP + p) * C];
-                    R[p] = c0 + x * (c1 + x * (c2 + x * c3));
-                }
-                const float* hs = H1 + static_cast<size_t>(s_src[j]) * NLMS * C + k;
-                float H[NLMS];
+            for (int p = 0; p < NP; ++p) R[p] = cubic(load4(rs, kk * 16, p * C * 16), x);
 #pragma unroll
-                for (int q = 0; q < NLMS; ++q) H[q] = hs[q * C];
+            for (int q = 0; q < NLMS; ++q) H[q] = load1(hs, kk * 4, q * C * 4);
 #pragma unroll
-                for (int t = 0; t < NT; ++t)
-                    acc[S::term_lme[t]] += s_cgY[j][t] * (R[S::term_p[t]] * H[S::term_lm2[t]]);
-            }
+            for (int pq = 0; pq < NPQ; ++pq) RH[pq] = R[S::pq_p[pq]] * H[S::pq_lm2[pq]];
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+                acc[S::term_lme[t]] = fmaf(s_cgY[j][t], RH[S::tr_pq[S::term_tr[t]]], acc[S::term_lme[t]]);
         }
     }
     if (k < C) {
@@ -291,15 +306,20 @@ __global__ void __launch_bounds__(256) r1_forward_kernel(LayerArgs a, const floa
 }
 
 // ---------------------------------------------------------------------------
-// Layer 1 reverse.  With dPhi1 of the receiver in registers, per edge:
-//   s[p,lm2] = sum_t cg_t Y_lm1 dPhi1[lme_t]          (t in path p, source lm2)
-//   msg[lm2] = sum_p R_p s[p,lm2]                      -> H1 adjoint of the source
-//   A        = sum_{p,lm2} R'_p H[lm2] s[p,lm2]
-//   U[lm1]   = sum_t cg_t R_p H[lm2_t] dPhi1[lme_t]
-//   f_edge   = -sum_k (r_hat A + sum_lm1 dY[lm1] U[lm1])
+// Layer 1 reverse.  Per receiver and channel, the CG contraction of dPhi1 is
+// taken once: G[p, lm2, lm1] = sum_{t in (p, lm2, lm1)} cg_t dPhi1[lme_t].
+// Per edge:
+//   s[p,lm2]  = sum_lm1 Y_lm1 G[p,lm2,lm1]
+//   msg[lm2]  = sum_p R_p s[p,lm2]                   -> H1 adjoint of the source
+//   A         = sum_p R'_p sum_lm2 H[lm2] s[p,lm2]
+//   U[lm1]    = sum_{p,lm2} R_p H[lm2] G[p,lm2,lm1]
+//   f_edge    = -sum_k (r_hat A + sum_lm1 dY[lm1] U[lm1])
+// When G does not fit the register budget (many triples) the terms are
+// contracted per edge instead, with dPhi1 in registers.
 // ---------------------------------------------------------------------------
 template <class S>
-__global__ void __launch_bounds__(256) r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S::NTR <= 96 ? 3 : 1)))
+r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
                                                          const float* __restrict__ cg,
                                                          const float* __restrict__ H1,
                                                          const float* __restrict__ dPhi1,
@@ -310,155 +330,164 @@ __global__ void __launch_bounds__(256) r1_reverse_kernel(LayerArgs a, const floa
     constexpr int NLMS = (S::LLMAX + 1) * (S::LLMAX + 1);
     constexpr int NP = S::NP;
     constexpr int NT = S::NT;
-    constexpr int TE = 16;
-    __shared__ float s_cgY[TE][(NT + 3) / 4 * 4];
-    __shared__ float s_dY[TE][3][NLM];
-    __shared__ float s_dir[TE][3];
-    __shared__ float s_x[TE];
-    __shared__ int s_iv[TE];
-    __shared__ int s_pair[TE];
-    __shared__ int s_src[TE];
-    __shared__ float s_f[TE][kMaxWaves][3];
+    constexpr int NPQ = S::NPQ;
+    constexpr bool kFactored = S::NTR <= 96;
+    constexpr int NG = kFactored ? S::NTR : S::NLME;
+    constexpr int NCGY = kFactored ? 1 : (NT + 3) / 4 * 4;
+    __shared__ float s_Y[kTile][NLM];
+    __shared__ float s_dY[kTile][3][NLM];
+    __shared__ float s_geo[kTile][4];  // r_hat, local spline coordinate
+    __shared__ float s_cgY[kTile][NCGY];
+    __shared__ int s_row[kTile];
+    __shared__ int s_src[kTile];
+    __shared__ int s_eid[kTile];
+    __shared__ float s_f[kTile][kMaxWaves][3];
+    __shared__ int s_count;
 
     const int i = receiver_of_block(a);
     const int k = threadIdx.x;
     const int C = a.C;
     const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
     const int nwaves = blockDim.x >> 6;
     const EdgeGraph& g = a.graph;
-    float dphi[S::NLME];
+    const int kk = min(k, C - 1);
+    const int row_bytes = NP * C * 16;
+    const int h_bytes = NLMS * C * 4;
+    // G (factored) or dPhi1 (per-term); zero on lanes beyond C
+    float G[NG];
+#pragma unroll
+    for (int q = 0; q < NG; ++q) G[q] = 0.0f;
     if (k < C) {
         const float* in = dPhi1 + static_cast<size_t>(i) * S::NLME * C + k;
+        if constexpr (kFactored) {
+            float d[S::NLME];
 #pragma unroll
-        for (int q = 0; q < S::NLME; ++q) dphi[q] = in[q * C];
-    } else {
+            for (int q = 0; q < S::NLME; ++q) d[q] = in[q * C];
 #pragma unroll
-        for (int q = 0; q < S::NLME; ++q) dphi[q] = 0.0f;
+            for (int t = 0; t < NT; ++t) G[S::term_tr[t]] = fmaf(cg[t], d[S::term_lme[t]], G[S::term_tr[t]]);
+        } else {
+#pragma unroll
+            for (int q = 0; q < S::NLME; ++q) G[q] = in[q * C];
+        }
     }
     const int e0 = g.first[i], e1 = g.first[i + 1];
-    const size_t interval_stride = static_cast<size_t>(4) * NP * C;
-    const size_t pair_stride = static_cast<size_t>(a.grid.intervals) * interval_stride;
-    for (int base = e0; base < e1; base += TE) {
-        const int n = min(TE, e1 - base);
+    for (int base = e0; base < e1; base += kTile) {
         __syncthreads();
-        if (threadIdx.x < n) {
+        if (threadIdx.x < 64) {
             const int t = threadIdx.x;
+            double rr;
+            const int n = min(kTile, e1 - base);
+            const TileSlot ts = compact_edge(g, a.grid, base, n, t, rr, &s_count);
             const int e = base + t;
-            const double rr = g.r[e];
-            int iv = -1;
-            if (rr < a.grid.r_cut) {
-                float x, Y[NLM], dx[NLM], dy[NLM], dz[NLM], dir[3];
+            if (ts.active) {
+                int iv;
+                float x;
+                const int sl = ts.slot;
                 spline_point(rr, a.grid, iv, x);
-                edge_harmonics<S::LMAX, true>(g.xyz + 3 * static_cast<size_t>(e), rr, Y, dx, dy, dz,
-                                              dir);
-                s_x[t] = x;
-                s_pair[t] = g.edge_pair[e] >> 16;
-                s_src[t] = g.source[e];
-                s_dir[t][0] = dir[0];
-                s_dir[t][1] = dir[1];
-                s_dir[t][2] = dir[2];
+                edge_harmonics<S::LMAX, true>(g.xyz + 3 * static_cast<size_t>(e), rr, s_Y[sl], s_dY[sl][0],
+                                              s_dY[sl][1], s_dY[sl][2], s_geo[sl]);
+                s_geo[sl][3] = x;
+                s_row[sl] = (g.edge_pair[e] >> 16) * a.grid.intervals + iv;
+                s_src[sl] = g.source[e];
+                s_eid[sl] = e;
+                if constexpr (!kFactored) {
 #pragma unroll
-                for (int lm = 0; lm < NLM; ++lm) {
-                    s_dY[t][0][lm] = dx[lm];
-                    s_dY[t][1][lm] = dy[lm];
-                    s_dY[t][2][lm] = dz[lm];
+                    for (int q = 0; q < NT; ++q) s_cgY[sl][q] = cg[q] * s_Y[sl][S::term_lm1[q]];
                 }
-#pragma unroll
-                for (int q = 0; q < NT; ++q) s_cgY[t][q] = cg[q] * Y[S::term_lm1[q]];
+            } else if (t < n) {
+                double* out = forces + 3 * static_cast<size_t>(e);
+                out[0] = 0.0;
+                out[1] = 0.0;
+                out[2] = 0.0;
             }
-            s_iv[t] = iv;
         }
         __syncthreads();
-        for (int j = 0; j < n; ++j) {
-            const int iv = s_iv[j];
-            if (iv < 0) continue;
-            float fx = 0.0f, fy = 0.0f, fz = 0.0f;
-            if (k < C) {
-                const float x = s_x[j];
-                const float* c = r1 + s_pair[j] * pair_stride + iv * interval_stride + k;
-                float R[NP], dR[NP];
+        const int count = uniform(s_count);
+        for (int j = 0; j < count; ++j) {
+            const float x = uniform(s_geo[j][3]);
+            const auto rs = buffer_rsrc(r1 + static_cast<size_t>(uniform(s_row[j])) * NP * C * 4, row_bytes);
+            const auto hs = buffer_rsrc(H1 + static_cast<size_t>(uniform(s_src[j])) * NLMS * C, h_bytes);
+            float R[NP], dR[NP], H[NLMS];
 #pragma unroll
-                for (int p = 0; p < NP; ++p) {
-                    const float c0 = c[(0 * NP + p) * C];
-                    const float c1 = c[(1 * NP + p) * C];
-                    const float c2 = c[(2 * NP + p) * C];
-                    const float c3 = c[(3 * NP + p) * C];
-                    R[p] = c0 + x * (c1 + x * (c2 + x * c3));
-                    dR[p] = c1 + x * (2.0f * c2 + 3.0f * x * c3);
+            for (int p = 0; p < NP; ++p) {
+                const float4v c = load4(rs, kk * 16, p * C * 16);
+                R[p] = cubic(c, x);
+                dR[p] = cubic_slope(c, x, 3.0f * x);
+            }
+#pragma unroll
+            for (int q = 0; q < NLMS; ++q) H[q] = load1(hs, kk * 4, q * C * 4);
+            float sp[NPQ], U[NLM], RH[NPQ];
+#pragma unroll
+            for (int pq = 0; pq < NPQ; ++pq) {
+                sp[pq] = 0.0f;
+                RH[pq] = R[S::pq_p[pq]] * H[S::pq_lm2[pq]];
+            }
+#pragma unroll
+            for (int lm = 0; lm < NLM; ++lm) U[lm] = 0.0f;
+            if constexpr (kFactored) {
+#pragma unroll
+                for (int tr = 0; tr < S::NTR; ++tr) {
+                    sp[S::tr_pq[tr]] = fmaf(s_Y[j][S::tr_lm1[tr]], G[tr], sp[S::tr_pq[tr]]);
+                    U[S::tr_lm1[tr]] = fmaf(RH[S::tr_pq[tr]], G[tr], U[S::tr_lm1[tr]]);
                 }
-                const int src = s_src[j];
-                const float* hs = H1 + static_cast<size_t>(src) * NLMS * C + k;
-                float H[NLMS];
-#pragma unroll
-                for (int q = 0; q < NLMS; ++q) H[q] = hs[q * C];
-                float s[NP][NLMS];
-                float U[NLM];
-#pragma unroll
-                for (int p = 0; p < NP; ++p)
-#pragma unroll
-                    for (int q = 0; q < NLMS; ++q) s[p][q] = 0.0f;
-#pragma unroll
-                for (int lm = 0; lm < NLM; ++lm) U[lm] = 0.0f;
+            } else {
 #pragma unroll
                 for (int t = 0; t < NT; ++t) {
-                    const int p = S::term_p[t];
-                    const int q = S::term_lm2[t];
-                    const float d = dphi[S::term_lme[t]];
-                    s[p][q] += s_cgY[j][t] * d;
-                    U[S::term_lm1[t]] += cg[t] * (R[p] * H[q] * d);
+                    const int pq = S::tr_pq[S::term_tr[t]];
+                    const float d = G[S::term_lme[t]];
+                    sp[pq] = fmaf(s_cgY[j][t], d, sp[pq]);
+                    U[S::term_lm1[t]] = fmaf(cg[t], RH[pq] * d, U[S::term_lm1[t]]);
                 }
-                float m[NLMS];
-#pragma unroll
-                for (int q = 0; q < NLMS; ++q) m[q] = 0.0f;
-                float A = 0.0f;
-#pragma unroll
-                for (int p = 0; p < NP; ++p) {
-                    const int l2 = S::path_l2[p];
-#pragma unroll
-                    for (int q = 0; q < NLMS; ++q) {
-                        if (q < l2 * l2 || q >= (l2 + 1) * (l2 + 1)) continue;
-                        m[q] += R[p] * s[p][q];
-                        A += dR[p] * H[q] * s[p][q];
-                    }
-                }
-                float* mo = msg + (static_cast<size_t>(base + j) * NLMS) * C + k;
-#pragma unroll
-                for (int q = 0; q < NLMS; ++q) mo[q * C] = m[q];
-                float gx = 0.0f, gy = 0.0f, gz = 0.0f;
-#pragma unroll
-                for (int lm = 0; lm < NLM; ++lm) {
-                    gx += s_dY[j][0][lm] * U[lm];
-                    gy += s_dY[j][1][lm] * U[lm];
-                    gz += s_dY[j][2][lm] * U[lm];
-                }
-                fx = -(s_dir[j][0] * A + gx);
-                fy = -(s_dir[j][1] * A + gy);
-                fz = -(s_dir[j][2] * A + gz);
             }
-            fx = wave_sum(fx);
-            fy = wave_sum(fy);
-            fz = wave_sum(fz);
-            if ((threadIdx.x & 63) == 0) {
+            float m[NLMS], ap[NP];
+#pragma unroll
+            for (int q = 0; q < NLMS; ++q) m[q] = 0.0f;
+#pragma unroll
+            for (int p = 0; p < NP; ++p) ap[p] = 0.0f;
+#pragma unroll
+            for (int pq = 0; pq < NPQ; ++pq) {
+                m[S::pq_lm2[pq]] = fmaf(R[S::pq_p[pq]], sp[pq], m[S::pq_lm2[pq]]);
+                ap[S::pq_p[pq]] = fmaf(H[S::pq_lm2[pq]], sp[pq], ap[S::pq_p[pq]]);
+            }
+            float A = 0.0f;
+#pragma unroll
+            for (int p = 0; p < NP; ++p) A = fmaf(dR[p], ap[p], A);
+            const int e = uniform(s_eid[j]);
+            if (k < C) {
+                const auto ms = buffer_rsrc(msg + static_cast<size_t>(e) * NLMS * C, h_bytes);
+#pragma unroll
+                for (int q = 0; q < NLMS; ++q) store1(m[q], ms, k * 4, q * C * 4);
+            }
+            float gx = 0.0f, gy = 0.0f, gz = 0.0f;
+#pragma unroll
+            for (int lm = 0; lm < NLM; ++lm) {
+                gx = fmaf(s_dY[j][0][lm], U[lm], gx);
+                gy = fmaf(s_dY[j][1][lm], U[lm], gy);
+                gz = fmaf(s_dY[j][2][lm], U[lm], gz);
+            }
+            const float fx = wave_sum_dpp(-fmaf(s_geo[j][0], A, gx));
+            const float fy = wave_sum_dpp(-fmaf(s_geo[j][1], A, gy));
+            const float fz = wave_sum_dpp(-fmaf(s_geo[j][2], A, gz));
+            if (lane == 0) {
                 s_f[j][wave][0] = fx;
                 s_f[j][wave][1] = fy;
                 s_f[j][wave][2] = fz;
             }
         }
         __syncthreads();
-        if (threadIdx.x < n) {
+        if (threadIdx.x < count) {
             const int t = threadIdx.x;
             double f[3] = {0.0, 0.0, 0.0};
-            if (s_iv[t] >= 0)
-                for (int w = 0; w < nwaves; ++w)
-                    for (int c = 0; c < 3; ++c) f[c] += static_cast<double>(s_f[t][w][c]);
-            double* out = forces + 3 * static_cast<size_t>(base + t);
+            for (int w = 0; w < nwaves; ++w)
+                for (int c = 0; c < 3; ++c) f[c] += static_cast<double>(s_f[t][w][c]);
+            double* out = forces + 3 * static_cast<size_t>(s_eid[t]);
             out[0] = f[0];
             out[1] = f[1];
             out[2] = f[2];
         }
     }
 }
-
 // ---------------------------------------------------------------------------
 // Layer 0 reverse: f_ij += -sum_{lm,k} A0_adj[i,lm,k] (r_hat R0f' Y_lm + R0f dY_lm)
 // ---------------------------------------------------------------------------
@@ -469,21 +498,23 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
 {
     constexpr int NLM = (LMAX + 1) * (LMAX + 1);
     constexpr int NL = LMAX + 1;
-    constexpr int TE = 32;
-    __shared__ float s_Y[TE][NLM];
-    __shared__ float s_dY[TE][3][NLM];
-    __shared__ float s_dir[TE][3];
-    __shared__ float s_x[TE];
-    __shared__ int s_iv[TE];
-    __shared__ int s_pair[TE];
-    __shared__ float s_f[TE][kMaxWaves][3];
+    __shared__ float s_Y[kTile][NLM];
+    __shared__ float s_dY[kTile][3][NLM];
+    __shared__ float s_geo[kTile][4];
+    __shared__ int s_row[kTile];
+    __shared__ int s_eid[kTile];
+    __shared__ float s_f[kTile][kMaxWaves][3];
+    __shared__ int s_count;
 
     const int i = receiver_of_block(a);
     const int k = threadIdx.x;
     const int C = a.C;
     const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
     const int nwaves = blockDim.x >> 6;
     const EdgeGraph& g = a.graph;
+    const int voff = min(k, C - 1) * 16;
+    const int row_bytes = NL * C * 16;
     float adj[NLM];
     if (k < C) {
         const float* in = A0_adj + static_cast<size_t>(i) * NLM * C + k;
@@ -494,86 +525,65 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
         for (int lm = 0; lm < NLM; ++lm) adj[lm] = 0.0f;
     }
     const int e0 = g.first[i], e1 = g.first[i + 1];
-    const size_t interval_stride = static_cast<size_t>(4) * NL * C;
-    const size_t pair_stride = static_cast<size_t>(a.grid.intervals) * interval_stride;
-    for (int base = e0; base < e1; base += TE) {
-        const int n = min(TE, e1 - base);
+    for (int base = e0; base < e1; base += kTile) {
         __syncthreads();
-        if (threadIdx.x < n) {
+        if (threadIdx.x < 64) {
             const int t = threadIdx.x;
-            const int e = base + t;
-            const double rr = g.r[e];
-            int iv = -1;
-            if (rr < a.grid.r_cut) {
-                float x, Y[NLM], dx[NLM], dy[NLM], dz[NLM], dir[3];
+            double rr;
+            const TileSlot ts = compact_edge(g, a.grid, base, min(kTile, e1 - base), t, rr, &s_count);
+            if (ts.active) {
+                const int e = base + t;
+                int iv;
+                float x;
+                const int sl = ts.slot;
                 spline_point(rr, a.grid, iv, x);
-                edge_harmonics<LMAX, true>(g.xyz + 3 * static_cast<size_t>(e), rr, Y, dx, dy, dz,
-                                           dir);
-                s_x[t] = x;
-                s_pair[t] = g.edge_pair[e] & 0xffff;
-                s_dir[t][0] = dir[0];
-                s_dir[t][1] = dir[1];
-                s_dir[t][2] = dir[2];
-#pragma unroll
-                for (int lm = 0; lm < NLM; ++lm) {
-                    s_Y[t][lm] = Y[lm];
-                    s_dY[t][0][lm] = dx[lm];
-                    s_dY[t][1][lm] = dy[lm];
-                    s_dY[t][2][lm] = dz[lm];
-                }
+                edge_harmonics<LMAX, true>(g.xyz + 3 * static_cast<size_t>(e), rr, s_Y[sl], s_dY[sl][0],
+                                           s_dY[sl][1], s_dY[sl][2], s_geo[sl]);
+                s_geo[sl][3] = x;
+                s_row[sl] = (g.edge_pair[e] & 0xffff) * a.grid.intervals + iv;
+                s_eid[sl] = e;
             }
-            s_iv[t] = iv;
         }
         __syncthreads();
-        for (int j = 0; j < n; ++j) {
-            const int iv = s_iv[j];
-            if (iv < 0) continue;
-            float fx = 0.0f, fy = 0.0f, fz = 0.0f;
-            if (k < C) {
-                const float x = s_x[j];
-                const float* c = r0f + s_pair[j] * pair_stride + iv * interval_stride + k;
-                float A = 0.0f, gx = 0.0f, gy = 0.0f, gz = 0.0f;
+        const int count = uniform(s_count);
+        for (int j = 0; j < count; ++j) {
+            const float x = uniform(s_geo[j][3]);
+            const float x3 = 3.0f * x;
+            const auto rs = buffer_rsrc(r0f + static_cast<size_t>(uniform(s_row[j])) * NL * C * 4, row_bytes);
+            float A = 0.0f, gx = 0.0f, gy = 0.0f, gz = 0.0f;
 #pragma unroll
-                for (int l = 0; l <= LMAX; ++l) {
-                    const float c0 = c[(0 * NL + l) * C];
-                    const float c1 = c[(1 * NL + l) * C];
-                    const float c2 = c[(2 * NL + l) * C];
-                    const float c3 = c[(3 * NL + l) * C];
-                    const float R = c0 + x * (c1 + x * (c2 + x * c3));
-                    const float dR = c1 + x * (2.0f * c2 + 3.0f * x * c3);
-                    float yl = 0.0f, ax = 0.0f, ay = 0.0f, az = 0.0f;
+            for (int l = 0; l <= LMAX; ++l) {
+                const float4v c = load4(rs, voff, l * C * 16);
+                float yl = 0.0f, ax = 0.0f, ay = 0.0f, az = 0.0f;
 #pragma unroll
-                    for (int lm = l * l; lm < (l + 1) * (l + 1); ++lm) {
-                        yl += s_Y[j][lm] * adj[lm];
-                        ax += s_dY[j][0][lm] * adj[lm];
-                        ay += s_dY[j][1][lm] * adj[lm];
-                        az += s_dY[j][2][lm] * adj[lm];
-                    }
-                    A += dR * yl;
-                    gx += R * ax;
-                    gy += R * ay;
-                    gz += R * az;
+                for (int lm = l * l; lm < (l + 1) * (l + 1); ++lm) {
+                    yl = fmaf(s_Y[j][lm], adj[lm], yl);
+                    ax = fmaf(s_dY[j][0][lm], adj[lm], ax);
+                    ay = fmaf(s_dY[j][1][lm], adj[lm], ay);
+                    az = fmaf(s_dY[j][2][lm], adj[lm], az);
                 }
-                fx = -(s_dir[j][0] * A + gx);
-                fy = -(s_dir[j][1] * A + gy);
-                fz = -(s_dir[j][2] * A + gz);
+                const float R = cubic(c, x);
+                A = fmaf(cubic_slope(c, x, x3), yl, A);
+                gx = fmaf(R, ax, gx);
+                gy = fmaf(R, ay, gy);
+                gz = fmaf(R, az, gz);
             }
-            fx = wave_sum(fx);
-            fy = wave_sum(fy);
-            fz = wave_sum(fz);
-            if ((threadIdx.x & 63) == 0) {
+            const float fx = wave_sum_dpp(-fmaf(s_geo[j][0], A, gx));
+            const float fy = wave_sum_dpp(-fmaf(s_geo[j][1], A, gy));
+            const float fz = wave_sum_dpp(-fmaf(s_geo[j][2], A, gz));
+            if (lane == 0) {
                 s_f[j][wave][0] = fx;
                 s_f[j][wave][1] = fy;
                 s_f[j][wave][2] = fz;
             }
         }
         __syncthreads();
-        if (threadIdx.x < n && s_iv[threadIdx.x] >= 0) {
+        if (threadIdx.x < count) {
             const int t = threadIdx.x;
             double f[3] = {0.0, 0.0, 0.0};
             for (int w = 0; w < nwaves; ++w)
                 for (int c = 0; c < 3; ++c) f[c] += static_cast<double>(s_f[t][w][c]);
-            double* out = forces + 3 * static_cast<size_t>(base + t);
+            double* out = forces + 3 * static_cast<size_t>(s_eid[t]);
             out[0] += f[0];
             out[1] += f[1];
             out[2] += f[2];
@@ -582,26 +592,48 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
 }
 
 // H1_adj[s, lm2, k] = sum over edges e with source s (ascending e) of msg[e, lm2, k]
+template <int NLMS>
 __global__ void __launch_bounds__(256) gather_messages_kernel(LayerArgs a,
-                                                               const float* __restrict__ msg,
-                                                               float* __restrict__ H1_adj)
+                                                              const float* __restrict__ msg,
+                                                              float* __restrict__ H1_adj)
 {
     const int s = a.node_offset + xcd_contiguous(blockIdx.x, a.node_count);
     const int k = threadIdx.x;
     const int C = a.C;
     if (k >= C) return;
-    const int nLM = (a.L_max + 1) * (a.L_max + 1);
     const EdgeGraph& g = a.graph;
-    float acc[16];
-    for (int q = 0; q < nLM; ++q) acc[q] = 0.0f;
-    for (int t = g.tfirst[s]; t < g.tfirst[s + 1]; ++t) {
+    float acc[NLMS];
+#pragma unroll
+    for (int q = 0; q < NLMS; ++q) acc[q] = 0.0f;
+    const int t0 = g.tfirst[s], t1 = g.tfirst[s + 1];
+    const size_t row = static_cast<size_t>(NLMS) * C;
+    int t = t0;
+    // edges in groups of four: all loads of a group are issued before the adds
+    for (; t + 4 <= t1; t += 4) {
+        float v[4][NLMS];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int e = g.tedge[t + u];
+            const bool on = g.r[e] < a.grid.r_cut;
+            const float* m = msg + e * row + k;
+#pragma unroll
+            for (int q = 0; q < NLMS; ++q) v[u][q] = on ? m[q * C] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int q = 0; q < NLMS; ++q) acc[q] += v[u][q];
+    }
+    for (; t < t1; ++t) {
         const int e = g.tedge[t];
         if (!(g.r[e] < a.grid.r_cut)) continue;
-        const float* m = msg + static_cast<size_t>(e) * nLM * C + k;
-        for (int q = 0; q < nLM; ++q) acc[q] += m[q * C];
+        const float* m = msg + e * row + k;
+#pragma unroll
+        for (int q = 0; q < NLMS; ++q) acc[q] += m[q * C];
     }
-    float* out = H1_adj + static_cast<size_t>(s) * nLM * C + k;
-    for (int q = 0; q < nLM; ++q) out[q * C] = acc[q];
+    float* out = H1_adj + static_cast<size_t>(s) * NLMS * C + k;
+#pragma unroll
+    for (int q = 0; q < NLMS; ++q) out[q * C] = acc[q];
 }
 
 __global__ void add_direct_kernel(int nodes, int C, int nLM, const float* __restrict__ direct,
@@ -802,25 +834,34 @@ __global__ void edge_geometry_kernel(int E, const int* __restrict__ receiver,
     r[e] = sqrt(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]);
 }
 
-// F_a = sum_{e: src=a} f_e - sum_{e: recv=a} f_e, each sum in ascending edge order
-__global__ void atom_forces_kernel(int N, const int* __restrict__ first, const int* __restrict__ tfirst,
-                                   const int* __restrict__ tedge, const double* __restrict__ f,
-                                   double* __restrict__ out)
+// F_a = sum_{e: src=a} f_e - sum_{e: recv=a} f_e.  One wave per atom; lane l
+// sums edges l, l+64, ... of each list, then a fixed butterfly combines the
+// lanes, so the result does not depend on scheduling.
+__global__ void __launch_bounds__(256) atom_forces_kernel(int N, const int* __restrict__ first,
+                                                          const int* __restrict__ tfirst,
+                                                          const int* __restrict__ tedge,
+                                                          const double* __restrict__ f,
+                                                          double* __restrict__ out)
 {
-    const int a = blockIdx.x * blockDim.x + threadIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int a = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (a >= N) return;
-    double fs[3] = {0.0, 0.0, 0.0}, fr[3] = {0.0, 0.0, 0.0};
-    for (int t = tfirst[a]; t < tfirst[a + 1]; ++t) {
+    double acc[3] = {0.0, 0.0, 0.0};
+    for (int t = tfirst[a] + lane; t < tfirst[a + 1]; t += 64) {
         const size_t e = tedge[t];
-        fs[0] += f[3 * e], fs[1] += f[3 * e + 1], fs[2] += f[3 * e + 2];
+        acc[0] += f[3 * e], acc[1] += f[3 * e + 1], acc[2] += f[3 * e + 2];
     }
-    for (int e = first[a]; e < first[a + 1]; ++e) {
-        fr[0] += f[3 * static_cast<size_t>(e)], fr[1] += f[3 * static_cast<size_t>(e) + 1],
-            fr[2] += f[3 * static_cast<size_t>(e) + 2];
+    for (int e = first[a] + lane; e < first[a + 1]; e += 64) {
+        acc[0] -= f[3 * static_cast<size_t>(e)], acc[1] -= f[3 * static_cast<size_t>(e) + 1],
+            acc[2] -= f[3 * static_cast<size_t>(e) + 2];
     }
-    out[3 * static_cast<size_t>(a)] = fs[0] - fr[0];
-    out[3 * static_cast<size_t>(a) + 1] = fs[1] - fr[1];
-    out[3 * static_cast<size_t>(a) + 2] = fs[2] - fr[2];
+    for (int off = 32; off > 0; off >>= 1)
+        for (int c = 0; c < 3; ++c) acc[c] += __shfl_xor(acc[c], off, 64);
+    if (lane == 0) {
+        out[3 * static_cast<size_t>(a)] = acc[0];
+        out[3 * static_cast<size_t>(a) + 1] = acc[1];
+        out[3 * static_cast<size_t>(a) + 2] = acc[2];
+    }
 }
 
 constexpr int kReduceThreads = 256;
@@ -855,14 +896,24 @@ __global__ void __launch_bounds__(kReduceThreads) totals_partial_kernel(
     if (t < 10) partials[static_cast<size_t>(blockIdx.x) * 10 + t] = s[0][t];
 }
 
-__global__ void totals_final_kernel(int num_partials, const double* __restrict__ partials,
-                                    double* __restrict__ out)
+__global__ void __launch_bounds__(256) totals_final_kernel(int num_partials,
+                                                         const double* __restrict__ partials,
+                                                         double* __restrict__ out)
 {
-    const int c = threadIdx.x;
-    if (c >= 10) return;
-    double acc = 0.0;
-    for (int b = 0; b < num_partials; ++b) acc += partials[static_cast<size_t>(b) * 10 + c];
-    out[c] = acc;
+    __shared__ double s[256][10];
+    const int t = threadIdx.x;
+    double acc[10];
+    for (int c = 0; c < 10; ++c) acc[c] = 0.0;
+    for (int b = t; b < num_partials; b += 256)
+        for (int c = 0; c < 10; ++c) acc[c] += partials[static_cast<size_t>(b) * 10 + c];
+    for (int c = 0; c < 10; ++c) s[t][c] = acc[c];
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if (t < w)
+            for (int c = 0; c < 10; ++c) s[t][c] += s[t + w][c];
+        __syncthreads();
+    }
+    if (t < 10) out[t] = s[0][t];
 }
 
 inline int node_threads(int C) { return ((C + 63) / 64) * 64; }
@@ -968,7 +1019,12 @@ hipError_t launch_r1_reverse(const LayerArgs& a, const float* r1, const float* c
 hipError_t launch_gather_messages(const LayerArgs& a, const float* msg, float* H1_adj, hipStream_t s)
 {
     if (a.node_count <= 0) return hipSuccess;
-    gather_messages_kernel<<<a.node_count, node_threads(a.C), 0, s>>>(a, msg, H1_adj);
+    const dim3 grid(a.node_count), block(node_threads(a.C));
+    switch (a.L_max) {
+    case 1: gather_messages_kernel<4><<<grid, block, 0, s>>>(a, msg, H1_adj); break;
+    case 2: gather_messages_kernel<9><<<grid, block, 0, s>>>(a, msg, H1_adj); break;
+    default: gather_messages_kernel<1><<<grid, block, 0, s>>>(a, msg, H1_adj); break;
+    }
     return hipGetLastError();
 }
 
@@ -1005,8 +1061,8 @@ hipError_t launch_atom_forces(int num_nodes, const int* first, const int* tfirst
                               const double* forces, double* atom_forces, hipStream_t s)
 {
     if (num_nodes <= 0) return hipSuccess;
-    atom_forces_kernel<<<(num_nodes + 255) / 256, 256, 0, s>>>(num_nodes, first, tfirst, tedge, forces,
-                                                               atom_forces);
+    atom_forces_kernel<<<(num_nodes + 3) / 4, 256, 0, s>>>(num_nodes, first, tfirst, tedge, forces,
+                                                           atom_forces);
     return hipGetLastError();
 }
 
@@ -1023,7 +1079,7 @@ hipError_t launch_reduce_totals(int num_nodes, int num_edges, const double* ener
 {
     totals_partial_kernel<<<num_partials, kReduceThreads, 0, s>>>(num_nodes, num_edges, energies, forces,
                                                                   xyz, inv_volume, partials);
-    totals_final_kernel<<<1, 64, 0, s>>>(num_partials, partials, out);
+    totals_final_kernel<<<1, 256, 0, s>>>(num_partials, partials, out);
     return hipGetLastError();
 }
 
