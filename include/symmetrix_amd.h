@@ -63,6 +63,9 @@ typedef struct {
     int graph_builds;
     int evaluations;
     double last_evaluation_ms; /* host time to enqueue and run one evaluation */
+    int tiled_evaluations;     /* evaluations that ran the tiled plan */
+    int tile_receivers;        /* receivers per tile of the prepared graph, 0 = untiled */
+    int num_tiles;
 } sxl_stats_t;
 
 /* Message of the last failed call on this thread ("" if none). */
@@ -173,6 +176,22 @@ int sxl_set_profiling(sxl_evaluator* evaluator, int enable);
 int sxl_num_stages(void);
 const char* sxl_stage_name(int stage);
 int sxl_stage_times(const sxl_evaluator* evaluator, double* ms, int* counts);
+
+/* Tiled ("fixed workspace") execution for capacity runs: receivers are
+ * processed in tiles with one reused work arena; graph-wide state is H1, its
+ * adjoint and two per-node scalar blocks.  With allow != 0 the plan of the
+ * next prepared graph is tiled when the receiver limit (if set) is below the
+ * node count, or when the untiled work arrays would not fit the free device
+ * memory (tiles of 32768 receivers).  Both setters invalidate the prepared
+ * graph: prepare again afterwards.  Replace MACEKokkos::set_allow_fixed_workspace
+ * (libsymmetrix/source/mace_kokkos_runtime.cpp:3992-4000; Python
+ * _set_allow_fixed_workspace, symmetrix/source/cpp/mace_kokkos.cpp:444-447)
+ * and set_dual_layer_workspace_receiver_limit_for_testing
+ * (mace_kokkos_runtime.cpp:2771-2781; Python binding mace_kokkos.cpp:439-441);
+ * a limit <= 0 is rejected like the reference's. */
+int sxl_set_allow_fixed_workspace(sxl_evaluator* evaluator, int allow);
+int sxl_allow_fixed_workspace(const sxl_evaluator* evaluator, int* allow);
+int sxl_set_workspace_receiver_limit(sxl_evaluator* evaluator, int receivers);
 
 /* Waits for all device work of the evaluator. */
 int sxl_synchronize(const sxl_evaluator* evaluator);

@@ -257,13 +257,34 @@ int sxl_stats(const sxl_evaluator* ev, sxl_stats_t* out)
     if (!ev || !out) return null_handle();
     return guarded([&] {
         const sxl::EvaluatorStats& s = ev->impl.stats();
-        out->device_bytes = static_cast<int64_t>(s.device_bytes);
         out->num_nodes = ev->impl.num_nodes();
         out->num_edges = ev->impl.num_edges();
         out->graph_builds = s.graph_builds;
         out->evaluations = s.evaluations;
         out->last_evaluation_ms = s.last_evaluation_ms;
+        out->device_bytes = static_cast<int64_t>(sxl::device_bytes_in_use());
+        out->tiled_evaluations = s.tiled_evaluations;
+        out->tile_receivers = s.tile_receivers;
+        out->num_tiles = s.num_tiles;
     });
+}
+
+int sxl_set_allow_fixed_workspace(sxl_evaluator* ev, int allow)
+{
+    if (!ev) return null_handle();
+    return guarded([&] { ev->impl.set_allow_fixed_workspace(allow != 0); });
+}
+
+int sxl_allow_fixed_workspace(const sxl_evaluator* ev, int* allow)
+{
+    if (!ev || !allow) return null_handle();
+    return guarded([&] { *allow = ev->impl.allow_fixed_workspace() ? 1 : 0; });
+}
+
+int sxl_set_workspace_receiver_limit(sxl_evaluator* ev, int receivers)
+{
+    if (!ev) return null_handle();
+    return guarded([&] { ev->impl.set_workspace_receiver_limit(receivers); });
 }
 
 int sxl_neighbor_graph_build(const double* positions, int num_nodes, const double* cell, const double* inverse_cell,

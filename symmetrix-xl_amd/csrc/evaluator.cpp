@@ -2,6 +2,7 @@
 #include "evaluator.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <chrono>
 #include <cmath>
 #include <cstring>
@@ -115,11 +116,20 @@ const char* stage_name(int stage)
     return stage >= 0 && stage < kNumStages ? names[stage] : "";
 }
 
+namespace {
+std::atomic<std::size_t> g_device_bytes{0};
+}
+
+std::size_t device_bytes_in_use() { return g_device_bytes.load(); }
+
 DeviceBuffer::~DeviceBuffer() { release(); }
 
 void DeviceBuffer::release()
 {
-    if (ptr_) (void)hipFree(ptr_);
+    if (ptr_) {
+        (void)hipFree(ptr_);
+        g_device_bytes -= bytes_;
+    }
     ptr_ = nullptr;
     bytes_ = 0;
 }
@@ -137,6 +147,7 @@ void DeviceBuffer::reserve(std::size_t bytes)
     }
     ptr_ = p;
     bytes_ = bytes;
+    g_device_bytes += bytes;
 }
 
 Evaluator::Evaluator(const std::string& model_path, const std::string& head)
@@ -386,15 +397,25 @@ void Evaluator::allocate_workspace()
     const std::size_t N = std::max(num_nodes_, 1);
     const std::size_t E = std::max<long long>(num_edges_, 1);
     const std::size_t f = sizeof(float);
-    A0_.reserve(N * nlm_ * C_ * f);
-    M0_.reserve(N * nLM_ * C_ * f);
+    // receiver-indexed work arrays span one tile (the whole graph untiled)
+    const std::size_t NT = tile_receivers_ > 0 ? static_cast<std::size_t>(tile_receivers_) : N;
+    std::size_t ET = E;
+    if (tile_receivers_ > 0) {
+        ET = 1;
+        for (int t = 0; t < num_tiles_; ++t)
+            ET = std::max<std::size_t>(ET, tile_first_edge_[t + 1] - tile_first_edge_[t]);
+        M0s_.reserve(N * C_ * f);
+    }
+    A0_.reserve(NT * nlm_ * C_ * f);
+    M0_.reserve(NT * nLM_ * C_ * f);
+    Phi1_.reserve(NT * nlme_ * C_ * f);
+    A1_.reserve(NT * nlm_ * C_ * f);
+    A1adj_.reserve(NT * nlm_ * C_ * f);
+    msg_.reserve(ET * nLM_ * C_ * f);
+    // graph-wide
     H1_.reserve(N * nLM_ * C_ * f);
-    Phi1_.reserve(N * nlme_ * C_ * f);
-    A1_.reserve(N * nlm_ * C_ * f);
-    A1adj_.reserve(N * nlm_ * C_ * f);
-    direct_.reserve(N * C_ * f);
     H1adj_.reserve(N * nLM_ * C_ * f);
-    msg_.reserve(E * nLM_ * C_ * f);
+    direct_.reserve(N * C_ * f);
     energies_.reserve(N * sizeof(double));
     forces_.reserve(E * 3 * sizeof(double));
     atom_forces_.reserve(N * 3 * sizeof(double));
@@ -403,6 +424,89 @@ void Evaluator::allocate_workspace()
     totals_.reserve(16 * sizeof(double));
     xyz_.reserve(E * 3 * sizeof(double));
     r_.reserve(E * sizeof(double));
+}
+
+// Execution plan of the prepared graph.  With fixed workspace allowed, the
+// graph is tiled when a receiver limit below N is set, or when the untiled
+// work arrays would not fit the free device memory (tiles of
+// kDefaultTileReceivers).  For a tiled plan: the edge range of each tile and
+// the runs of the source-major edge lists per tile (for the H1 adjoint).
+void Evaluator::plan_tiles()
+{
+    tile_receivers_ = 0;
+    num_tiles_ = 0;
+    tile_first_edge_.clear();
+    tile_run_offsets_.clear();
+    const int N = num_nodes_;
+    if (!allow_fixed_workspace_ || N == 0) return;
+    int T = receiver_limit_;
+    if (T <= 0) {
+        const std::size_t per_node = static_cast<std::size_t>(C_) * sizeof(float) * (3 * nlm_ + nLM_ + nlme_);
+        const std::size_t per_edge = static_cast<std::size_t>(nLM_) * C_ * sizeof(float);
+        const std::size_t untiled = per_node * N + per_edge * static_cast<std::size_t>(num_edges_);
+        std::size_t free_bytes = 0, total_bytes = 0;
+        hip_check(hipMemGetInfo(&free_bytes, &total_bytes), "memory info");
+        const std::size_t held = A0_.bytes() + M0_.bytes() + Phi1_.bytes() + A1_.bytes() + A1adj_.bytes() +
+                                 msg_.bytes();
+        if (untiled > (free_bytes + held) / 10 * 9) T = kDefaultTileReceivers;
+    }
+    if (T <= 0 || T >= N) return;
+    tile_receivers_ = T;
+    num_tiles_ = (N + T - 1) / T;
+    std::vector<int> first(N + 1);
+    hip_check(hipMemcpyAsync(first.data(), first_.as<int>(), (N + 1) * sizeof(int), hipMemcpyDeviceToHost, stream_),
+              "copy");
+    hip_check(hipStreamSynchronize(stream_), "sync");
+    tile_first_edge_.resize(num_tiles_ + 1);
+    for (int t = 0; t <= num_tiles_; ++t) tile_first_edge_[t] = first[std::min(N, t * T)];
+    // runs: count per tile, scan on the host, fill
+    DeviceBuffer per_source, per_tile, offsets;
+    per_source.reserve(static_cast<std::size_t>(N) * sizeof(int));
+    per_tile.reserve(static_cast<std::size_t>(num_tiles_) * sizeof(int));
+    hip_check(hipMemsetAsync(per_tile.as<void>(), 0, num_tiles_ * sizeof(int), stream_), "memset");
+    hip_check(launch_tile_runs_count(N, tfirst_.as<int>(), tedge_.as<int>(), receiver_.as<int>(), T,
+                                     per_source.as<int>(), per_tile.as<int>(), stream_),
+              "tile runs");
+    std::vector<int> counts(num_tiles_);
+    hip_check(hipMemcpyAsync(counts.data(), per_tile.as<int>(), num_tiles_ * sizeof(int), hipMemcpyDeviceToHost,
+                             stream_),
+              "copy");
+    hip_check(hipStreamSynchronize(stream_), "sync");
+    tile_run_offsets_.assign(num_tiles_ + 1, 0);
+    for (int t = 0; t < num_tiles_; ++t) tile_run_offsets_[t + 1] = tile_run_offsets_[t] + counts[t];
+    const int runs = tile_run_offsets_[num_tiles_];
+    run_source_.reserve(std::max(runs, 1) * sizeof(int));
+    run_start_.reserve(std::max(runs, 1) * sizeof(int));
+    run_length_.reserve(std::max(runs, 1) * sizeof(int));
+    upload(offsets, tile_run_offsets_, stream_);
+    hip_check(hipMemsetAsync(per_tile.as<void>(), 0, num_tiles_ * sizeof(int), stream_), "memset");
+    hip_check(launch_tile_runs_fill(N, tfirst_.as<int>(), tedge_.as<int>(), receiver_.as<int>(), T,
+                                    offsets.as<int>(), per_tile.as<int>(), run_source_.as<int>(),
+                                    run_start_.as<int>(), run_length_.as<int>(), stream_),
+              "tile runs");
+    hip_check(hipStreamSynchronize(stream_), "tile plan");
+}
+
+void Evaluator::invalidate_graph()
+{
+    hip_check(hipStreamSynchronize(stream_), "synchronize");
+    ++generation_;
+    evaluated_generation_ = 0;
+    reduced_ = false;
+}
+
+void Evaluator::set_allow_fixed_workspace(bool allow)
+{
+    if (allow == allow_fixed_workspace_) return;
+    invalidate_graph();
+    allow_fixed_workspace_ = allow;
+}
+
+void Evaluator::set_workspace_receiver_limit(int receivers)
+{
+    if (receivers <= 0) throw std::invalid_argument("Dual-layer workspace receiver limit must be positive.");
+    invalidate_graph();
+    receiver_limit_ = receivers;
 }
 
 // Shared tail of both graph preparations: receivers, source-major transpose,
@@ -465,6 +569,7 @@ void Evaluator::finish_graph(const int* host_neigh_types)
                                     edge_pair_.as<int>(), stream_),
                   "edge pairs");
     }
+    plan_tiles();
     allocate_workspace();
     hip_check(hipStreamSynchronize(stream_), "graph preparation");
     ++generation_;
@@ -473,6 +578,8 @@ void Evaluator::finish_graph(const int* host_neigh_types)
     stats_.graph_builds += 1;
     stats_.last_num_nodes = N;
     stats_.last_num_edges = E;
+    stats_.tile_receivers = tile_receivers_;
+    stats_.num_tiles = num_tiles_;
 }
 
 std::uint64_t Evaluator::prepare_graph(int num_nodes, const int* node_types, const int* num_neigh,
@@ -746,6 +853,10 @@ double Evaluator::max_displacement(std::uint64_t generation, const double* posit
 
 void Evaluator::evaluate()
 {
+    if (tile_receivers_ > 0) {
+        evaluate_tiled();
+        return;
+    }
     const auto t0 = std::chrono::steady_clock::now();
     const int N = num_nodes_;
     const int E = static_cast<int>(num_edges_);
@@ -818,7 +929,10 @@ void Evaluator::evaluate()
         mark(kStageA1Gemm, true);
         // readout and its reverse down to A1_adj
         ReadoutArgs ra;
+        ra.node_offset = 0;
         ra.num_nodes = N;
+        ra.local_base = 0;
+        ra.m0_stride = nodeLM;
         ra.C = C_;
         ra.num_lm = nlm_;
         ra.num_LM = nLM_;
@@ -909,6 +1023,180 @@ void Evaluator::evaluate()
     evaluated_generation_ = generation_;
     reduced_ = false;
     stats_.evaluations += 1;
+    stats_.last_evaluation_ms =
+        std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+}
+
+// Tiled evaluation (reference compute_dual_layer_tiled,
+// mace_kokkos_evaluate.cpp:754-1238): three sweeps over receiver tiles with
+// one reused arena.
+//   1. A0 -> M0 -> H1 (graph-wide), keeping the scalar M0 block graph-wide;
+//   2. Phi1 -> A1 -> readout (energies, direct adjoint) -> dPhi1 -> R1
+//      reverse (directed forces, per-edge messages) -> H1 adjoint += the
+//      tile's messages, run by run;
+//   3. M0 adjoint = H1 adjoint H1_W^T + direct -> A0 (recomputed) -> A0
+//      adjoint -> A0 reverse (directed forces +=).
+// Each tile's edges are its receivers' contiguous CSR range.
+void Evaluator::evaluate_tiled()
+{
+    const auto t0 = std::chrono::steady_clock::now();
+    const int N = num_nodes_;
+    const int E = static_cast<int>(num_edges_);
+    const int T = tile_receivers_;
+    LayerArgs la;
+    la.graph.num_nodes = N;
+    la.graph.num_edges = E;
+    la.graph.node_types = node_types_.as<int>();
+    la.graph.type_active = type_active_.as<int>();
+    la.graph.num_active = static_cast<int>(active_types_.size());
+    la.graph.first = first_.as<int>();
+    la.graph.receiver = receiver_.as<int>();
+    la.graph.source = source_.as<int>();
+    la.graph.tfirst = tfirst_.as<int>();
+    la.graph.tedge = tedge_.as<int>();
+    la.graph.edge_pair = edge_pair_.as<int>();
+    la.graph.xyz = xyz_.as<double>();
+    la.graph.r = r_.as<double>();
+    la.grid = grid_;
+    la.C = C_;
+    la.l_max = model_.l_max;
+    la.L_max = model_.L_max;
+    hipStream_t s = stream_;
+    PolyTable p0{p0_terms_, p0_offsets_.as<int>(), p0_packed_.as<int>(), p0_coef_.as<float>()};
+    PolyTable p1{p1_terms_, p1_offsets_.as<int>(), p1_packed_.as<int>(), p1_coef_.as<float>()};
+    const long long nodeLM = static_cast<long long>(nLM_) * C_;
+    const long long nodelm = static_cast<long long>(nlm_) * C_;
+    const long long nodelme = static_cast<long long>(nlme_) * C_;
+    auto tile = [&](int t) {
+        la.node_offset = t * T;
+        la.node_count = std::min(T, N - t * T);
+        la.local_base = la.node_offset;
+        la.edge_base = tile_first_edge_[t];
+    };
+    auto h1_gemms = [&](const float* in, long long in_stride, const float* W, float* out, long long out_stride,
+                        const char* what) {
+        for (int l = 0; l <= model_.L_max; ++l) {
+            GemmArgs g;
+            g.nodes = la.node_count;
+            g.rows_per_node = 2 * l + 1;
+            g.K = C_;
+            g.Ncols = C_;
+            g.a = {in + l * l * C_, in_stride, C_};
+            g.B = W + static_cast<std::size_t>(l) * C_ * C_;
+            g.c = {out + l * l * C_, out_stride, C_};
+            hip_check(launch_gemm(g, s), what);
+        }
+    };
+    float* H1 = H1_.as<float>();
+    float* H1adj = H1adj_.as<float>();
+    float* M0s = M0s_.as<float>();
+    hip_check(hipMemsetAsync(H1adj, 0, static_cast<std::size_t>(N) * nodeLM * sizeof(float), s), "memset");
+    // sweep 1
+    for (int t = 0; t < num_tiles_; ++t) {
+        tile(t);
+        hip_check(launch_a0_forward(la, r0f_.as<float>(), A0_.as<float>(), s), "A0 forward");
+        hip_check(launch_m0_forward(la, p0, A0_.as<float>(), M0_.as<float>(), s), "M0 forward");
+        h1_gemms(M0_.as<float>(), nodeLM, h1w_.as<float>(), H1 + la.node_offset * nodeLM, nodeLM, "H1 gemm");
+        hip_check(hipMemcpy2DAsync(M0s + static_cast<std::size_t>(la.node_offset) * C_, C_ * sizeof(float),
+                                   M0_.as<float>(), nodeLM * sizeof(float), C_ * sizeof(float), la.node_count,
+                                   hipMemcpyDeviceToDevice, s),
+                  "M0 scalar block");
+    }
+    // sweep 2
+    ReadoutArgs ra;
+    ra.C = C_;
+    ra.num_lm = nlm_;
+    ra.num_LM = nLM_;
+    ra.hidden = model_.readout_hidden;
+    ra.node_types = node_types_.as<int>();
+    ra.type_active = type_active_.as<int>();
+    ra.A1 = A1_.as<float>();
+    ra.M0 = M0s;
+    ra.m0_stride = C_;
+    ra.p1 = p1;
+    ra.H2M0 = h2m0_.as<float>();
+    ra.H2M1 = h2m1_.as<float>();
+    ra.q = q_.as<float>();
+    ra.W1 = w1_.as<float>();
+    ra.W2 = w2_.as<float>();
+    ra.scale = static_cast<float>(model_.readout_scale);
+    ra.E0 = e0_.as<double>();
+    ra.energies = energies_.as<double>();
+    ra.direct = direct_.as<float>();
+    ra.A1_adj = A1adj_.as<float>();
+    float* dPhi1 = Phi1_.as<float>();
+    for (int t = 0; t < num_tiles_; ++t) {
+        tile(t);
+        hip_check(launch_r1_forward(la, r1_.as<float>(), cg_.as<float>(), H1, Phi1_.as<float>(), s), "R1 forward");
+        for (int l = 0; l <= model_.l_max; ++l) {
+            if (num_e_[l] == 0) continue;
+            GemmArgs g;
+            g.nodes = la.node_count;
+            g.rows_per_node = 2 * l + 1;
+            g.K = num_e_[l] * C_;
+            g.Ncols = C_;
+            g.a = {Phi1_.as<float>() + static_cast<long long>(lme_off_[l]) * C_, nodelme,
+                   static_cast<long long>(num_e_[l]) * C_};
+            g.B = a1w_[l]->as<float>();
+            g.c = {A1_.as<float>() + l * l * C_, nodelm, C_};
+            hip_check(launch_gemm(g, s), "A1 gemm");
+        }
+        ra.node_offset = la.node_offset;
+        ra.num_nodes = la.node_count;
+        ra.local_base = la.local_base;
+        hip_check(launch_readout(ra, s), "readout");
+        for (int l = 0; l <= model_.l_max; ++l) {
+            if (num_e_[l] == 0) continue;
+            GemmArgs g;
+            g.nodes = la.node_count;
+            g.rows_per_node = 2 * l + 1;
+            g.K = C_;
+            g.Ncols = num_e_[l] * C_;
+            g.a = {A1adj_.as<float>() + l * l * C_, nodelm, C_};
+            g.B = a1wt_[l]->as<float>();
+            g.c = {dPhi1 + static_cast<long long>(lme_off_[l]) * C_, nodelme, static_cast<long long>(num_e_[l]) * C_};
+            hip_check(launch_gemm(g, s), "A1 reverse gemm");
+        }
+        hip_check(launch_r1_reverse(la, r1_.as<float>(), cg_.as<float>(), H1, dPhi1, forces_.as<double>(),
+                                    msg_.as<float>(), s),
+                  "R1 reverse");
+        TileRuns runs;
+        runs.count = tile_run_offsets_[t + 1] - tile_run_offsets_[t];
+        runs.source = run_source_.as<int>() + tile_run_offsets_[t];
+        runs.start = run_start_.as<int>() + tile_run_offsets_[t];
+        runs.length = run_length_.as<int>() + tile_run_offsets_[t];
+        hip_check(launch_gather_tile_runs(la, runs, msg_.as<float>(), H1adj, s), "H1 adjoint gather");
+    }
+    // sweep 3
+    float* M0adj = M0_.as<float>();
+    float* A0adj = A1_.as<float>();
+    for (int t = 0; t < num_tiles_; ++t) {
+        tile(t);
+        h1_gemms(H1adj + la.node_offset * nodeLM, nodeLM, h1wt_.as<float>(), M0adj, nodeLM, "H1 reverse gemm");
+        hip_check(launch_add_direct(la.node_count, C_, nLM_, direct_.as<float>() + static_cast<std::size_t>(la.node_offset) * C_,
+                                    M0adj, s),
+                  "direct adjoint");
+        hip_check(launch_a0_forward(la, r0f_.as<float>(), A0_.as<float>(), s), "A0 forward");
+        hip_check(launch_m0_reverse(la, p0, A0_.as<float>(), M0adj, A0adj, s), "M0 reverse");
+        hip_check(launch_a0_reverse(la, r0f_.as<float>(), A0adj, forces_.as<double>(), s), "A0 reverse");
+    }
+    mark(kStageAtomForces, false);
+    hip_check(launch_atom_forces(N, first_.as<int>(), tfirst_.as<int>(), tedge_.as<int>(), forces_.as<double>(),
+                                 atom_forces_.as<double>(), s),
+              "atom forces");
+    mark(kStageAtomForces, true);
+    hip_check(hipStreamSynchronize(s), "evaluation");
+    if (profiling_ && stage_used_[kStageAtomForces]) {
+        float ms = 0.0f;
+        hip_check(hipEventElapsedTime(&ms, events_[2 * kStageAtomForces], events_[2 * kStageAtomForces + 1]),
+                  "event time");
+        stage_ms_[kStageAtomForces] += ms;
+        stage_count_[kStageAtomForces] += 1;
+    }
+    evaluated_generation_ = generation_;
+    reduced_ = false;
+    stats_.evaluations += 1;
+    stats_.tiled_evaluations += 1;
     stats_.last_evaluation_ms =
         std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
 }

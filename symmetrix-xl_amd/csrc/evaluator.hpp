@@ -58,15 +58,24 @@ void build_periodic_graph(const double* d_positions, int num_nodes, const double
 void validate_periodic_inputs(int num_nodes, const double* cell, const double* inverse_cell,
                               double cutoff);
 
+// Bytes of device memory held by this library's buffers (all evaluators).
+std::size_t device_bytes_in_use();
+
 struct EvaluatorStats {
-    std::size_t device_bytes = 0;
     int last_num_nodes = 0;
     int last_num_edges = 0;
     int active_edges = 0;
     double last_evaluation_ms = 0.0;
     int graph_builds = 0;
     int evaluations = 0;
+    int tiled_evaluations = 0;
+    int tile_receivers = 0;  // receivers per tile of the prepared graph, 0 = untiled plan
+    int num_tiles = 0;
 };
+
+// Receivers per tile chosen by the planner when tiled execution is allowed
+// and the untiled workspace does not fit (reference mace_kokkos.hpp:542).
+constexpr int kDefaultTileReceivers = 32768;
 
 // Stages of one evaluation, timed with HIP events on the evaluator's stream
 // when profiling is enabled.
@@ -135,6 +144,16 @@ public:
 
     const EvaluatorStats& stats() const { return stats_; }
 
+    // --- execution plan --------------------------------------------------------
+    // Tiled ("fixed workspace") execution: receivers are processed in tiles
+    // with a reused per-tile arena; graph-wide state is H1, its adjoint, the
+    // scalar M0 block and the direct adjoint.  Both setters invalidate the
+    // prepared graph (reference mace_kokkos_runtime.cpp:2771-2781, 3992-4000).
+    void set_allow_fixed_workspace(bool allow);
+    bool allow_fixed_workspace() const { return allow_fixed_workspace_; }
+    void set_workspace_receiver_limit(int receivers);
+    int workspace_receiver_limit() const { return receiver_limit_; }
+
     // Per-stage device time (ms) accumulated over profiled evaluations.
     void set_profiling(bool enable);
     void stage_times(double* ms, int* counts) const;
@@ -145,7 +164,10 @@ private:
     void upload_static_tables();
     void finish_graph(const int* host_neigh_types);
     void allocate_workspace();
+    void plan_tiles();
+    void invalidate_graph();
     void evaluate();
+    void evaluate_tiled();
     void reduce(double volume);
 
     HostModel model_;
@@ -183,6 +205,15 @@ private:
         atom_forces_, partials_, totals_, scratch_;
     bool reduced_ = false;
     double reduced_volume_ = 0.0;
+
+    // tiled plan
+    bool allow_fixed_workspace_ = false;
+    int receiver_limit_ = 0;
+    int tile_receivers_ = 0;
+    int num_tiles_ = 0;
+    std::vector<long long> tile_first_edge_;  // [num_tiles + 1]
+    std::vector<int> tile_run_offsets_;       // [num_tiles + 1]
+    DeviceBuffer M0s_, run_source_, run_start_, run_length_;
 
     bool profiling_ = false;
     std::vector<hipEvent_t> events_;  // [stage][begin, end]

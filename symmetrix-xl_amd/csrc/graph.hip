@@ -305,6 +305,48 @@ __global__ void edge_pairs_kernel(int E, const int* __restrict__ receiver, const
     edge_pair[e] = ordered | (unordered << 16);
 }
 
+// Runs of the source-major edge lists by receiver tile (tiles of T
+// consecutive receivers).  The list of each source is ascending in edge id,
+// so its receivers, and their tiles, are non-decreasing: one run per change.
+__global__ void tile_runs_count_kernel(int n, const int* __restrict__ tfirst, const int* __restrict__ tedge,
+                                       const int* __restrict__ receiver, int T, int* __restrict__ per_source,
+                                       int* __restrict__ per_tile)
+{
+    const int src = blockIdx.x * blockDim.x + threadIdx.x;
+    if (src >= n) return;
+    int prev = -1, runs = 0;
+    for (int t = tfirst[src]; t < tfirst[src + 1]; ++t) {
+        const int tile = receiver[tedge[t]] / T;
+        if (tile != prev) {
+            ++runs;
+            atomicAdd(per_tile + tile, 1);
+            prev = tile;
+        }
+    }
+    per_source[src] = runs;
+}
+
+__global__ void tile_runs_fill_kernel(int n, const int* __restrict__ tfirst, const int* __restrict__ tedge,
+                                      const int* __restrict__ receiver, int T, const int* __restrict__ tile_offsets,
+                                      int* __restrict__ cursors, int* __restrict__ run_source,
+                                      int* __restrict__ run_start, int* __restrict__ run_length)
+{
+    const int src = blockIdx.x * blockDim.x + threadIdx.x;
+    if (src >= n) return;
+    const int t1 = tfirst[src + 1];
+    int t = tfirst[src];
+    while (t < t1) {
+        const int tile = receiver[tedge[t]] / T;
+        int u = t + 1;
+        while (u < t1 && receiver[tedge[u]] / T == tile) ++u;
+        const int pos = tile_offsets[tile] + atomicAdd(cursors + tile, 1);
+        run_source[pos] = src;
+        run_start[pos] = t;
+        run_length[pos] = u - t;
+        t = u;
+    }
+}
+
 }  // namespace
 
 hipError_t launch_edge_pairs(int num_edges, const int* receiver, const int* source, const int* node_types,
@@ -407,6 +449,26 @@ hipError_t launch_max_displacement(int n, const double* a, const double* b, doub
     if (err != hipSuccess || n <= 0) return err;
     const int blocks = std::min((n + 255) / 256, 1024);
     max_displacement_kernel<<<blocks, 256, 0, s>>>(n, a, b, reinterpret_cast<unsigned long long*>(out));
+    return hipGetLastError();
+}
+
+hipError_t launch_tile_runs_count(int num_nodes, const int* tfirst, const int* tedge, const int* receiver,
+                                  int tile_receivers, int* runs_per_source, int* runs_per_tile, hipStream_t s)
+{
+    if (num_nodes <= 0) return hipSuccess;
+    tile_runs_count_kernel<<<(num_nodes + 255) / 256, 256, 0, s>>>(num_nodes, tfirst, tedge, receiver,
+                                                                   tile_receivers, runs_per_source, runs_per_tile);
+    return hipGetLastError();
+}
+
+hipError_t launch_tile_runs_fill(int num_nodes, const int* tfirst, const int* tedge, const int* receiver,
+                                 int tile_receivers, const int* tile_offsets, int* tile_cursors, int* run_source,
+                                 int* run_start, int* run_length, hipStream_t s)
+{
+    if (num_nodes <= 0) return hipSuccess;
+    tile_runs_fill_kernel<<<(num_nodes + 255) / 256, 256, 0, s>>>(num_nodes, tfirst, tedge, receiver,
+                                                                  tile_receivers, tile_offsets, tile_cursors,
+                                                                  run_source, run_start, run_length);
     return hipGetLastError();
 }
 

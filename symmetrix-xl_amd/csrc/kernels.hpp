@@ -84,6 +84,12 @@ struct LayerArgs {
     int l_max = 0, L_max = 0;
     int node_offset = 0;  // first receiver handled by this launch
     int node_count = 0;   // receivers handled by this launch
+    // Receiver-indexed work arrays (A0, M0, Phi1, their adjoints) hold rows
+    // i - local_base; per-edge messages hold rows e - edge_base.  Both are 0
+    // when the arrays span the whole graph, and the tile's first receiver /
+    // first edge in tiled execution.
+    int local_base = 0;
+    long long edge_base = 0;
 };
 
 // Layer 0: A0[i] = sum_j R0f_{pair(i,j)}(r) Y(r_hat)   (H0 and A0_W folded in)
@@ -96,7 +102,10 @@ hipError_t launch_r1_forward(const LayerArgs& a, const float* r1, const float* c
                              float* Phi1, hipStream_t s);
 
 struct ReadoutArgs {
-    int num_nodes = 0;
+    int node_offset = 0;            // first node of this launch
+    int num_nodes = 0;              // nodes of this launch
+    int local_base = 0;             // A1 / A1_adj hold rows i - local_base
+    long long m0_stride = 0;        // floats between the M0 scalar rows of consecutive nodes
     int C = 0;
     int num_lm = 0;
     int num_LM = 0;
@@ -104,7 +113,7 @@ struct ReadoutArgs {
     const int* node_types = nullptr;
     const int* type_active = nullptr;
     const float* A1 = nullptr;      // [N][num_lm][C]
-    const float* M0 = nullptr;      // [N][num_LM][C] (scalar block = LM 0)
+    const float* M0 = nullptr;      // scalar block (LM 0) of node i at M0 + i * m0_stride
     PolyTable p1;
     const float* H2M0 = nullptr;    // [active][C][C]
     const float* H2M1 = nullptr;    // [C][C]
@@ -125,6 +134,25 @@ hipError_t launch_r1_reverse(const LayerArgs& a, const float* r1, const float* c
 // H1_adj[s] = sum over edges with source s of msg[e]
 hipError_t launch_gather_messages(const LayerArgs& a, const float* msg, float* H1_adj,
                                   hipStream_t s);
+
+// Tiled execution: the edges of one receiver tile grouped by source.  A run
+// is (source, first index into the source-major edge list, length): the
+// source's edges whose receivers lie in the tile.  H1_adj[source] += the
+// run's messages (tile-local rows e - edge_base), run by run.
+struct TileRuns {
+    int count = 0;
+    const int* source = nullptr;
+    const int* start = nullptr;
+    const int* length = nullptr;
+};
+hipError_t launch_tile_runs_count(int num_nodes, const int* tfirst, const int* tedge, const int* receiver,
+                                  int tile_receivers, int* runs_per_source, int* runs_per_tile,
+                                  hipStream_t s);
+hipError_t launch_tile_runs_fill(int num_nodes, const int* tfirst, const int* tedge, const int* receiver,
+                                 int tile_receivers, const int* tile_offsets, int* tile_cursors,
+                                 int* run_source, int* run_start, int* run_length, hipStream_t s);
+hipError_t launch_gather_tile_runs(const LayerArgs& a, const TileRuns& runs, const float* msg,
+                                   float* H1_adj, hipStream_t s);
 // M0_adj[:, LM 0, :] += direct
 hipError_t launch_add_direct(int nodes, int C, int num_LM, const float* direct, float* M0_adj,
                              hipStream_t s);

@@ -111,19 +111,35 @@ __global__ void __launch_bounds__(256) a0_forward_kernel(LayerArgs a, const floa
         }
         __syncthreads();
         const int count = uniform(s_count);
-        for (int j = 0; j < count; ++j) {
-            const float x = uniform(s_x[j]);
+        // spline rows double-buffered: the row of edge j + 1 is in flight
+        // while edge j is accumulated
+        auto fetch = [&](int j, float4v* c) {
             const auto rs = buffer_rsrc(r0f + static_cast<size_t>(uniform(s_row[j])) * NL * C * 4, row_bytes);
 #pragma unroll
+            for (int l = 0; l < NL; ++l) c[l] = load4(rs, voff, l * C * 16);
+        };
+        auto accumulate = [&](int j, const float4v* c) {
+            const float x = uniform(s_x[j]);
+#pragma unroll
             for (int l = 0; l <= LMAX; ++l) {
-                const float R = cubic(load4(rs, voff, l * C * 16), x);
+                const float R = cubic(c[l], x);
 #pragma unroll
                 for (int lm = l * l; lm < (l + 1) * (l + 1); ++lm) acc[lm] = fmaf(R, s_Y[j][lm], acc[lm]);
+            }
+        };
+        float4v ca[NL], cb[NL];
+        if (count > 0) fetch(0, ca);
+        for (int j = 0; j < count; j += 2) {
+            fetch(min(j + 1, count - 1), cb);
+            accumulate(j, ca);
+            if (j + 1 < count) {
+                fetch(min(j + 2, count - 1), ca);
+                accumulate(j + 1, cb);
             }
         }
     }
     if (k < C) {
-        float* out = A0 + static_cast<size_t>(i) * NLM * C + k;
+        float* out = A0 + static_cast<size_t>(i - a.local_base) * NLM * C + k;
 #pragma unroll
         for (int lm = 0; lm < NLM; ++lm) out[lm * C] = acc[lm];
     }
@@ -191,11 +207,11 @@ __global__ void __launch_bounds__(256) m0_forward_kernel(LayerArgs a, PolyTable 
     const int nLM = (a.L_max + 1) * (a.L_max + 1);
     const int stride = blockDim.x;
     float* x = s_mem + k;
-    const float* in = A0 + static_cast<size_t>(i) * nlm * C + k;
+    const float* in = A0 + static_cast<size_t>(i - a.local_base) * nlm * C + k;
     for (int lm = 0; lm < nlm; ++lm) x[lm * stride] = in[lm * C];
     const int at = a.graph.type_active[a.graph.node_types[i]];
     const float* coef = p.coef + static_cast<size_t>(at) * p.num_terms * C + k;
-    float* out = M0 + static_cast<size_t>(i) * nLM * C + k;
+    float* out = M0 + static_cast<size_t>(i - a.local_base) * nLM * C + k;
     for (int LM = 0; LM < nLM; ++LM)
         out[LM * C] = poly_value(p, coef, C, p.offsets[LM], p.offsets[LM + 1], x, stride);
 }
@@ -215,17 +231,17 @@ __global__ void __launch_bounds__(256) m0_reverse_kernel(LayerArgs a, PolyTable 
     const int stride = blockDim.x;
     float* x = s_mem + k;
     float* gsum = s_mem + static_cast<size_t>(nlm) * stride + k;
-    const float* in = A0 + static_cast<size_t>(i) * nlm * C + k;
+    const float* in = A0 + static_cast<size_t>(i - a.local_base) * nlm * C + k;
     for (int lm = 0; lm < nlm; ++lm) {
         x[lm * stride] = in[lm * C];
         gsum[lm * stride] = 0.0f;
     }
     const int at = a.graph.type_active[a.graph.node_types[i]];
     const float* coef = p.coef + static_cast<size_t>(at) * p.num_terms * C + k;
-    const float* lam = M0_adj + static_cast<size_t>(i) * nLM * C + k;
+    const float* lam = M0_adj + static_cast<size_t>(i - a.local_base) * nLM * C + k;
     for (int LM = 0; LM < nLM; ++LM)
         poly_gradient(p, coef, C, p.offsets[LM], p.offsets[LM + 1], x, gsum, lam[LM * C], stride);
-    float* out = A0_adj + static_cast<size_t>(i) * nlm * C + k;
+    float* out = A0_adj + static_cast<size_t>(i - a.local_base) * nlm * C + k;
     for (int lm = 0; lm < nlm; ++lm) out[lm * C] = gsum[lm * stride];
 }
 
@@ -282,24 +298,34 @@ __global__ void __launch_bounds__(256) r1_forward_kernel(LayerArgs a, const floa
         }
         __syncthreads();
         const int count = uniform(s_count);
-        for (int j = 0; j < count; ++j) {
-            const float x = uniform(s_x[j]);
+        // the spline row and source features of edge j + 1 are in flight while
+        // edge j is contracted
+        auto fetch = [&](int j, float4v* c, float* H) {
             const auto rs = buffer_rsrc(r1 + static_cast<size_t>(uniform(s_row[j])) * NP * C * 4, row_bytes);
             const auto hs = buffer_rsrc(H1 + static_cast<size_t>(uniform(s_src[j])) * NLMS * C, h_bytes);
-            float R[NP], H[NLMS], RH[NPQ];
 #pragma unroll
-            for (int p = 0; p < NP; ++p) R[p] = cubic(load4(rs, kk * 16, p * C * 16), x);
+            for (int p = 0; p < NP; ++p) c[p] = load4(rs, kk * 16, p * C * 16);
 #pragma unroll
             for (int q = 0; q < NLMS; ++q) H[q] = load1(hs, kk * 4, q * C * 4);
+        };
+        // One row buffer: once the radial values of edge j are formed, its
+        // coefficient registers are refilled with the row of edge j + 1.
+        float4v c[NP];
+        float H[NLMS];
+        if (count > 0) fetch(0, c, H);
+        for (int j = 0; j < count; ++j) {
+            const float x = uniform(s_x[j]);
+            float RH[NPQ];
 #pragma unroll
-            for (int pq = 0; pq < NPQ; ++pq) RH[pq] = R[S::pq_p[pq]] * H[S::pq_lm2[pq]];
+            for (int pq = 0; pq < NPQ; ++pq) RH[pq] = cubic(c[S::pq_p[pq]], x) * H[S::pq_lm2[pq]];
+            fetch(min(j + 1, count - 1), c, H);
 #pragma unroll
             for (int t = 0; t < NT; ++t)
                 acc[S::term_lme[t]] = fmaf(s_cgY[j][t], RH[S::tr_pq[S::term_tr[t]]], acc[S::term_lme[t]]);
         }
     }
     if (k < C) {
-        float* out = Phi1 + static_cast<size_t>(i) * S::NLME * C + k;
+        float* out = Phi1 + static_cast<size_t>(i - a.local_base) * S::NLME * C + k;
 #pragma unroll
         for (int q = 0; q < S::NLME; ++q) out[q * C] = acc[q];
     }
@@ -318,7 +344,7 @@ __global__ void __launch_bounds__(256) r1_forward_kernel(LayerArgs a, const floa
 // contracted per edge instead, with dPhi1 in registers.
 // ---------------------------------------------------------------------------
 template <class S>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S::NTR <= 96 ? 3 : 1)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S::NTR <= 40 ? 3 : 1)))
 r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
                                                          const float* __restrict__ cg,
                                                          const float* __restrict__ H1,
@@ -359,7 +385,7 @@ r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
 #pragma unroll
     for (int q = 0; q < NG; ++q) G[q] = 0.0f;
     if (k < C) {
-        const float* in = dPhi1 + static_cast<size_t>(i) * S::NLME * C + k;
+        const float* in = dPhi1 + static_cast<size_t>(i - a.local_base) * S::NLME * C + k;
         if constexpr (kFactored) {
             float d[S::NLME];
 #pragma unroll
@@ -404,19 +430,30 @@ r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
         }
         __syncthreads();
         const int count = uniform(s_count);
-        for (int j = 0; j < count; ++j) {
-            const float x = uniform(s_geo[j][3]);
+        auto fetch = [&](int j, float4v* c, float* H) {
             const auto rs = buffer_rsrc(r1 + static_cast<size_t>(uniform(s_row[j])) * NP * C * 4, row_bytes);
             const auto hs = buffer_rsrc(H1 + static_cast<size_t>(uniform(s_src[j])) * NLMS * C, h_bytes);
+#pragma unroll
+            for (int p = 0; p < NP; ++p) c[p] = load4(rs, kk * 16, p * C * 16);
+#pragma unroll
+            for (int q = 0; q < NLMS; ++q) H[q] = load1(hs, kk * 4, q * C * 4);
+        };
+        // One row buffer: once the radial values of edge j are formed, its
+        // coefficient registers are refilled with the row of edge j + 1.
+        float4v cn[NP];
+        float Hn[NLMS];
+        if (count > 0) fetch(0, cn, Hn);
+        for (int j = 0; j < count; ++j) {
+            const float x = uniform(s_geo[j][3]);
             float R[NP], dR[NP], H[NLMS];
 #pragma unroll
             for (int p = 0; p < NP; ++p) {
-                const float4v c = load4(rs, kk * 16, p * C * 16);
-                R[p] = cubic(c, x);
-                dR[p] = cubic_slope(c, x, 3.0f * x);
+                R[p] = cubic(cn[p], x);
+                dR[p] = cubic_slope(cn[p], x, 3.0f * x);
             }
 #pragma unroll
-            for (int q = 0; q < NLMS; ++q) H[q] = load1(hs, kk * 4, q * C * 4);
+            for (int q = 0; q < NLMS; ++q) H[q] = Hn[q];
+            fetch(min(j + 1, count - 1), cn, Hn);
             float sp[NPQ], U[NLM], RH[NPQ];
 #pragma unroll
             for (int pq = 0; pq < NPQ; ++pq) {
@@ -455,7 +492,7 @@ r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
             for (int p = 0; p < NP; ++p) A = fmaf(dR[p], ap[p], A);
             const int e = uniform(s_eid[j]);
             if (k < C) {
-                const auto ms = buffer_rsrc(msg + static_cast<size_t>(e) * NLMS * C, h_bytes);
+                const auto ms = buffer_rsrc(msg + static_cast<size_t>(e - a.edge_base) * NLMS * C, h_bytes);
 #pragma unroll
                 for (int q = 0; q < NLMS; ++q) store1(m[q], ms, k * 4, q * C * 4);
             }
@@ -517,7 +554,7 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
     const int row_bytes = NL * C * 16;
     float adj[NLM];
     if (k < C) {
-        const float* in = A0_adj + static_cast<size_t>(i) * NLM * C + k;
+        const float* in = A0_adj + static_cast<size_t>(i - a.local_base) * NLM * C + k;
 #pragma unroll
         for (int lm = 0; lm < NLM; ++lm) adj[lm] = in[lm * C];
     } else {
@@ -546,14 +583,18 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
         }
         __syncthreads();
         const int count = uniform(s_count);
-        for (int j = 0; j < count; ++j) {
+        auto fetch = [&](int j, float4v* c) {
+            const auto rs = buffer_rsrc(r0f + static_cast<size_t>(uniform(s_row[j])) * NL * C * 4, row_bytes);
+#pragma unroll
+            for (int l = 0; l < NL; ++l) c[l] = load4(rs, voff, l * C * 16);
+        };
+        auto edge_force = [&](int j, const float4v* cl) {
             const float x = uniform(s_geo[j][3]);
             const float x3 = 3.0f * x;
-            const auto rs = buffer_rsrc(r0f + static_cast<size_t>(uniform(s_row[j])) * NL * C * 4, row_bytes);
             float A = 0.0f, gx = 0.0f, gy = 0.0f, gz = 0.0f;
 #pragma unroll
             for (int l = 0; l <= LMAX; ++l) {
-                const float4v c = load4(rs, voff, l * C * 16);
+                const float4v c = cl[l];
                 float yl = 0.0f, ax = 0.0f, ay = 0.0f, az = 0.0f;
 #pragma unroll
                 for (int lm = l * l; lm < (l + 1) * (l + 1); ++lm) {
@@ -575,6 +616,16 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
                 s_f[j][wave][0] = fx;
                 s_f[j][wave][1] = fy;
                 s_f[j][wave][2] = fz;
+            }
+        };
+        float4v ca[NL], cb[NL];
+        if (count > 0) fetch(0, ca);
+        for (int j = 0; j < count; j += 2) {
+            fetch(min(j + 1, count - 1), cb);
+            edge_force(j, ca);
+            if (j + 1 < count) {
+                fetch(min(j + 2, count - 1), ca);
+                edge_force(j + 1, cb);
             }
         }
         __syncthreads();
@@ -636,6 +687,37 @@ __global__ void __launch_bounds__(256) gather_messages_kernel(LayerArgs a,
     for (int q = 0; q < NLMS; ++q) out[q * C] = acc[q];
 }
 
+// Tiled execution: H1_adj[s] += sum over the run's edges (ascending) of
+// msg[e - edge_base]; one workgroup per run of the tile, runs of one tile have
+// distinct sources.
+template <int NLMS>
+__global__ void __launch_bounds__(256) gather_tile_runs_kernel(LayerArgs a, TileRuns runs,
+                                                               const float* __restrict__ msg,
+                                                               float* __restrict__ H1_adj)
+{
+    const int run = blockIdx.x;
+    const int k = threadIdx.x;
+    const int C = a.C;
+    if (k >= C) return;
+    const EdgeGraph& g = a.graph;
+    const int src = runs.source[run];
+    const int t0 = runs.start[run], t1 = t0 + runs.length[run];
+    const size_t row = static_cast<size_t>(NLMS) * C;
+    float acc[NLMS];
+#pragma unroll
+    for (int q = 0; q < NLMS; ++q) acc[q] = 0.0f;
+    for (int t = t0; t < t1; ++t) {
+        const int e = g.tedge[t];
+        if (!(g.r[e] < a.grid.r_cut)) continue;
+        const float* m = msg + static_cast<size_t>(e - a.edge_base) * row + k;
+#pragma unroll
+        for (int q = 0; q < NLMS; ++q) acc[q] += m[q * C];
+    }
+    float* out = H1_adj + static_cast<size_t>(src) * row + k;
+#pragma unroll
+    for (int q = 0; q < NLMS; ++q) out[q * C] += acc[q];
+}
+
 __global__ void add_direct_kernel(int nodes, int C, int nLM, const float* __restrict__ direct,
                                   float* __restrict__ M0_adj)
 {
@@ -653,7 +735,8 @@ __global__ void add_direct_kernel(int nodes, int C, int nLM, const float* __rest
 __global__ void __launch_bounds__(256) readout_kernel(ReadoutArgs a)
 {
     extern __shared__ float s_mem[];
-    const int i = xcd_contiguous(blockIdx.x, a.num_nodes);
+    const int i = a.node_offset + xcd_contiguous(blockIdx.x, a.num_nodes);
+    const int il = i - a.local_base;
     const int k = threadIdx.x;
     const int C = a.C;
     const int stride = blockDim.x;
@@ -670,7 +753,7 @@ __global__ void __launch_bounds__(256) readout_kernel(ReadoutArgs a)
     const int at = a.type_active[a.node_types[i]];
     float m1 = 0.0f;
     if (ok) {
-        const float* in = a.A1 + static_cast<size_t>(i) * nlm * C + k;
+        const float* in = a.A1 + static_cast<size_t>(il) * nlm * C + k;
         for (int lm = 0; lm < nlm; ++lm) {
             x[lm * stride] = in[lm * C];
             grad[lm * stride] = 0.0f;
@@ -678,7 +761,7 @@ __global__ void __launch_bounds__(256) readout_kernel(ReadoutArgs a)
         const float* coef = a.p1.coef + static_cast<size_t>(at) * a.p1.num_terms * C + k;
         m1 = poly_value(a.p1, coef, C, 0, a.p1.num_terms, x, stride);
         poly_gradient(a.p1, coef, C, 0, a.p1.num_terms, x, grad, 1.0f, stride);
-        s_xs[k] = a.M0[static_cast<size_t>(i) * a.num_LM * C + k];
+        s_xs[k] = a.M0[static_cast<size_t>(i) * a.m0_stride + k];
         s_m1[k] = m1;
     }
     __syncthreads();
@@ -736,7 +819,7 @@ __global__ void __launch_bounds__(256) readout_kernel(ReadoutArgs a)
             m1adj += W[o] * g2;
         }
         a.direct[static_cast<size_t>(i) * C + k] = d;
-        float* out = a.A1_adj + static_cast<size_t>(i) * nlm * C + k;
+        float* out = a.A1_adj + static_cast<size_t>(il) * nlm * C + k;
         for (int lm = 0; lm < nlm; ++lm) out[lm * C] = grad[lm * stride] * m1adj;
     }
 }
@@ -1024,6 +1107,19 @@ hipError_t launch_gather_messages(const LayerArgs& a, const float* msg, float* H
     case 1: gather_messages_kernel<4><<<grid, block, 0, s>>>(a, msg, H1_adj); break;
     case 2: gather_messages_kernel<9><<<grid, block, 0, s>>>(a, msg, H1_adj); break;
     default: gather_messages_kernel<1><<<grid, block, 0, s>>>(a, msg, H1_adj); break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gather_tile_runs(const LayerArgs& a, const TileRuns& runs, const float* msg,
+                                   float* H1_adj, hipStream_t s)
+{
+    if (runs.count <= 0) return hipSuccess;
+    const dim3 grid(runs.count), block(node_threads(a.C));
+    switch (a.L_max) {
+    case 1: gather_tile_runs_kernel<4><<<grid, block, 0, s>>>(a, runs, msg, H1_adj); break;
+    case 2: gather_tile_runs_kernel<9><<<grid, block, 0, s>>>(a, runs, msg, H1_adj); break;
+    default: gather_tile_runs_kernel<1><<<grid, block, 0, s>>>(a, runs, msg, H1_adj); break;
     }
     return hipGetLastError();
 }

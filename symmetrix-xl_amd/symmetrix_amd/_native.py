@@ -41,7 +41,8 @@ class Stats(ctypes.Structure):
     _fields_ = [
         ("device_bytes", ctypes.c_int64), ("num_nodes", ctypes.c_int), ("num_edges", ctypes.c_int64),
         ("graph_builds", ctypes.c_int), ("evaluations", ctypes.c_int),
-        ("last_evaluation_ms", ctypes.c_double),
+        ("last_evaluation_ms", ctypes.c_double), ("tiled_evaluations", ctypes.c_int),
+        ("tile_receivers", ctypes.c_int), ("num_tiles", ctypes.c_int),
     ]
 
 
@@ -92,6 +93,9 @@ SIGNATURES = {
     "sxl_num_stages": (ctypes.c_int, []),
     "sxl_stage_name": (ctypes.c_char_p, [ctypes.c_int]),
     "sxl_stage_times": (ctypes.c_int, [ctypes.c_void_p, c_double_p, c_int_p]),
+    "sxl_set_allow_fixed_workspace": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
+    "sxl_allow_fixed_workspace": (ctypes.c_int, [ctypes.c_void_p, c_int_p]),
+    "sxl_set_workspace_receiver_limit": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
 }
 
 _lib = None

@@ -46,7 +46,7 @@ class Symmetrix:
     implemented_properties = ["energy", "free_energy", "energies", "forces", "stress"]
 
     def __init__(self, model_file, dtype="float32", use_kokkos=True, streamed_edges="direct",
-                 neighbor_skin=0.5, head=None, **unused):
+                 neighbor_skin=0.5, head=None, allow_fixed_workspace=False, **unused):
         if dtype not in ("float32", np.float32):
             raise ValueError("the MI355X evaluator computes in float32 (dtype='float32')")
         if streamed_edges not in ("direct", "generic", True):
@@ -54,6 +54,10 @@ class Symmetrix:
         if not (neighbor_skin >= 0.0):
             raise ValueError("neighbor_skin must be non-negative")
         self.evaluator = MACEKokkosFloat(model_file, head or "")
+        if allow_fixed_workspace:
+            # tiled plan when the untiled workspace would not fit
+            # (reference calculator.py:578-582)
+            self.evaluator._set_allow_fixed_workspace(True)
         self.cutoff = float(self.evaluator.r_cut)
         self.neighbor_skin = float(neighbor_skin)
         self._type_of_z = {z: i for i, z in enumerate(self.evaluator.atomic_numbers)}

@@ -288,6 +288,27 @@ class MACEKokkosFloat:
         check(lib.sxl_stage_times(self._h, _p(ms, ctypes.c_double), _p(counts, ctypes.c_int)))
         return {lib.sxl_stage_name(i).decode(): (float(ms[i]), int(counts[i])) for i in range(n)}
 
+    # --- execution plan (reference mace_kokkos.cpp:436-447, 619-620) ---------
+    def _set_allow_fixed_workspace(self, enabled):
+        """Permit the tiled (fixed-workspace) plan; invalidates the prepared
+        graph (reference ``_set_allow_fixed_workspace``)."""
+        check(library().sxl_set_allow_fixed_workspace(self._h, 1 if enabled else 0))
+
+    @property
+    def allow_fixed_workspace(self):
+        v = ctypes.c_int(0)
+        check(library().sxl_allow_fixed_workspace(self._h, ctypes.byref(v)))
+        return bool(v.value)
+
+    def _set_dual_layer_workspace_receiver_limit_for_testing(self, receivers):
+        """Receivers per tile of the tiled plan; invalidates the prepared
+        graph.  Non-positive limits raise ValueError like the reference."""
+        check(library().sxl_set_workspace_receiver_limit(self._h, int(receivers)))
+
+    @property
+    def dual_layer_tiled_evaluation_count(self):
+        return self.stats["tiled_evaluations"]
+
     @property
     def stats(self):
         s = _native.Stats()
