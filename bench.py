@@ -65,6 +65,11 @@ class HipMemory:
         if self.lib.hipMemcpy(ctypes.c_void_p(dst), ctypes.c_void_p(src), nbytes, 3) != 0:  # DeviceToDevice
             raise RuntimeError("hipMemcpy failed")
 
+    def copy_to_device(self, ptr, array):
+        a = np.ascontiguousarray(array)
+        if self.lib.hipMemcpy(ctypes.c_void_p(ptr), a.ctypes.data_as(ctypes.c_void_p), a.nbytes, 1) != 0:
+            raise RuntimeError("hipMemcpy failed")
+
     def synchronize(self):
         if self.lib.hipDeviceSynchronize() != 0:
             raise RuntimeError("hipDeviceSynchronize failed")
@@ -160,6 +165,100 @@ def cpu_baseline(model_path, structure, cutoff, threads, calls):
     return statistics.median(times) / len(structure) * 1e6, times
 
 
+# atomic masses (amu) of the SrTiO3 elements for the NVE run
+MASSES = {38: 87.62, 22: 47.867, 8: 15.999}
+EV_PER_A_AMU_TO_A_PER_FS2 = 9.648533212e-3  # 1 eV/(A amu) in A/fs^2
+KB_EV = 8.617333262e-5
+
+
+def capacity_run(args):
+    """Tiled-mode capacity: medium model on SrTiO3 n^3 (5 n^3 atoms), a
+    velocity-Verlet NVE run of --md-steps steps at --md-dt fs from 300 K
+    Maxwell-Boltzmann velocities.  Positions live on the host and are copied
+    to the device each step; the graph is rebuilt on the device when an atom
+    has moved more than half the skin.  Prints one JSON line."""
+    from symmetrix_amd import MACEKokkosFloat, synthetic
+
+    t_setup = time.perf_counter()
+    model_path = workload_model(args.preset, args.seed)
+    s = synthetic.srtio3_supercell(args.capacity_cells, sigma=args.sigma, seed=args.seed)
+    N = len(s)
+    print(f"[capacity] SrTiO3 {args.capacity_cells}^3: {N} atoms", file=sys.stderr, flush=True)
+    ev = MACEKokkosFloat(model_path)
+    ev._set_allow_fixed_workspace(True)
+    if args.tile_receivers > 0:
+        ev._set_dual_layer_workspace_receiver_limit_for_testing(args.tile_receivers)
+    types = synthetic.node_types(s, ev.atomic_numbers)
+    cutoff = ev.r_cut + args.skin
+    cell = s.cell
+    inv = np.linalg.inv(cell)
+    hip = HipMemory()
+    x = np.ascontiguousarray(s.positions, dtype=np.float64)
+    d_pos = hip.upload(x)
+    info = ev._prepare_periodic_factorized_graph_device(types, d_pos, cell, inv, cutoff)
+    gen = info["generation"]
+    st = ev.stats
+    print(f"[capacity] {info['num_edges']} edges, {st['num_tiles']} tiles of {st['tile_receivers']} receivers, "
+          f"{st['device_bytes'] / 2**30:.1f} GiB on the device, setup {time.perf_counter() - t_setup:.1f} s",
+          file=sys.stderr, flush=True)
+    masses = np.array([MASSES[int(z)] for z in (38, 22, 8)])
+    m = np.empty(N)
+    for z, mass in zip((38, 22, 8), masses):
+        m[s.numbers == z] = mass
+    rng = np.random.default_rng(args.seed + 1)
+    # v in A/fs: sqrt(kT/m), kT/m in eV/amu times the unit factor gives (A/fs)^2
+    v = rng.normal(size=(N, 3)) * np.sqrt(KB_EV * 300.0 * EV_PER_A_AMU_TO_A_PER_FS2 / m)[:, None]
+    v -= (m[:, None] * v).sum(0) / m.sum()
+    inv_m = EV_PER_A_AMU_TO_A_PER_FS2 / m[:, None]
+    rebuilds = 0
+
+    def forces(positions):
+        nonlocal gen, rebuilds
+        hip.copy_to_device(d_pos, positions)
+        if not ev._max_displacement_device(gen, d_pos) <= 0.5 * args.skin:
+            gen = ev._prepare_periodic_factorized_graph_device(types, d_pos, cell, inv, cutoff)["generation"]
+            rebuilds += 1
+        ev._compute_prepared_factorized_positions_device(gen, d_pos)
+        return ev._reduce_atom_forces(N, None, None, gen), ev._total_energy(gen)
+
+    dt = args.md_dt
+    f, epot = forces(x)
+    e0 = epot + 0.5 * float((m[:, None] * v * v).sum()) / EV_PER_A_AMU_TO_A_PER_FS2
+    times = []
+    etot = [e0]
+    for step in range(args.md_steps):
+        t0 = time.perf_counter()
+        a = f * inv_m
+        x = x + v * dt + 0.5 * a * dt * dt
+        f, epot = forces(x)
+        v = v + 0.5 * (a + f * inv_m) * dt
+        times.append(time.perf_counter() - t0)
+        ekin = 0.5 * float((m[:, None] * v * v).sum()) / EV_PER_A_AMU_TO_A_PER_FS2
+        etot.append(epot + ekin)
+        print(f"[capacity] step {step + 1}: {times[-1]:.2f} s, E_tot {etot[-1]:.6f} eV", file=sys.stderr, flush=True)
+    st = ev.stats
+    line = {
+        "metric": "tiled capacity: atoms per MI355X and us/atom/step of a 20-step NVE run (FP32)",
+        "capacity_atoms": N,
+        "edges": int(info["num_edges"]),
+        "us_per_atom_per_step": round(statistics.mean(times) / N * 1e6, 5),
+        "md_steps": args.md_steps,
+        "md_dt_fs": dt,
+        "max_energy_drift_per_atom_eV": round(max(abs(e - e0) for e in etot) / N, 9),
+        "neighbor_rebuilds": rebuilds,
+        "tile_receivers": st["tile_receivers"],
+        "num_tiles": st["num_tiles"],
+        "tiled_evaluations": st["tiled_evaluations"],
+        "device_bytes": st["device_bytes"],
+        "config": {"workload": f"medium-shape random-init MACE ({args.preset}) on SrTiO3 {args.capacity_cells}^3 "
+                               f"({N} atoms, sigma {args.sigma} A, seed {args.seed}), cutoff {ev.r_cut} + "
+                               f"{args.skin} A skin, 300 K Maxwell-Boltzmann start",
+                   "positions": "host, copied to the device each step"},
+    }
+    print(json.dumps(line), flush=True)
+    hip.free(d_pos)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -173,6 +272,11 @@ def main():
     ap.add_argument("--cpu-calls", type=int, default=2, help="timed oracle calls for cpu_baseline (0: skip)")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--host-steps", type=int, default=5, help="host-boundary calculator steps (0: skip)")
+    ap.add_argument("--capacity-cells", type=int, default=0, metavar="N",
+                    help="tiled capacity run on SrTiO3 N^3 (5 N^3 atoms) instead of the 5k-atom benchmark")
+    ap.add_argument("--md-steps", type=int, default=20)
+    ap.add_argument("--md-dt", type=float, default=1.0, help="fs")
+    ap.add_argument("--tile-receivers", type=int, default=0, help="receivers per tile (0: planner)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 3 device-to-device copies of MIB MiB (the known-size kernel that "
                          "scales FETCH_SIZE / WRITE_SIZE counters to bytes), then exit")
@@ -194,6 +298,10 @@ def main():
         print("bench.py runs on one GPU only: this build has no multi-GPU path "
               "(sharding is described in DESIGN.md); use --gpus 1", file=sys.stderr)
         sys.exit(2)
+
+    if args.capacity_cells > 0:
+        capacity_run(args)
+        return
 
     from symmetrix_amd import MACEKokkosFloat, Symmetrix, synthetic
 

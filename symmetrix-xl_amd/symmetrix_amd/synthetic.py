@@ -395,7 +395,11 @@ def water_box(num_molecules: int = 10000, density_g_cm3: float = 1.0, seed: int 
 def node_types(structure: Structure, atomic_numbers) -> np.ndarray:
     """Model element indices of the structure's atoms (not atomic numbers)."""
     lookup = {int(zz): i for i, zz in enumerate(atomic_numbers)}
-    missing = sorted(set(int(zz) for zz in structure.numbers) - set(lookup))
+    present = np.unique(structure.numbers)
+    missing = sorted(set(int(zz) for zz in present) - set(lookup))
     if missing:
         raise ValueError(f"atomic numbers {missing} are not supported by the model")
-    return np.array([lookup[int(zz)] for zz in structure.numbers], dtype=np.int32)
+    table = np.full(int(present.max()) + 1, -1, dtype=np.int32)
+    for zz in present:
+        table[int(zz)] = lookup[int(zz)]
+    return table[np.asarray(structure.numbers, dtype=np.int64)]
