@@ -12,6 +12,7 @@
 #include <stdexcept>
 #include <thread>
 
+#include "poly_shapes.inc"
 #include "r1_shapes.inc"
 
 namespace sxl {
@@ -54,14 +55,93 @@ std::vector<float> transpose(const double* p, int rows, int cols)
     return out;
 }
 
-// Monomial tables -> packed (deg | i0 << 4 | i1 << 10 | i2 << 16)
-std::vector<int> pack_terms(const std::vector<int>& degree, const std::vector<int>& index)
+// Monomial -> packed (deg | i0 << 4 | i1 << 10 | i2 << 16)
+int pack_term(int degree, const int* index)
 {
-    std::vector<int> out(degree.size());
-    for (std::size_t t = 0; t < degree.size(); ++t)
-        out[t] = degree[t] | (index[3 * t] << 4) | (index[3 * t + 1] << 10) | (index[3 * t + 2] << 16);
-    return out;
+    return degree | (index[0] << 4) | (index[1] << 10) | (index[2] << 16);
 }
+
+struct CompiledPoly {
+    int nt = 0;
+    const unsigned char *out = nullptr, *deg = nullptr, *i0 = nullptr, *i1 = nullptr, *i2 = nullptr;
+};
+
+template <class P>
+CompiledPoly compiled_from()
+{
+    return {P::NT, P::out, P::deg, P::i0, P::i1, P::i2};
+}
+
+// Compiled monomial table of (input l_max, output L_max, correlation), if any.
+CompiledPoly compiled_poly(int lin, int lout, int corr)
+{
+    switch (lin * 100 + lout * 10 + corr) {
+    case 212: return compiled_from<PolyShape<2, 1, 2>>();
+    case 313: return compiled_from<PolyShape<3, 1, 3>>();
+    case 323: return compiled_from<PolyShape<3, 2, 3>>();
+    case 202: return compiled_from<PolyShape<2, 0, 2>>();
+    case 303: return compiled_from<PolyShape<3, 0, 3>>();
+    default: return {};
+    }
+}
+
+long long term_key(int out, int deg, int i0, int i1, int i2)
+{
+    return static_cast<long long>(out) | (static_cast<long long>(deg) << 8) | (static_cast<long long>(i0) << 16) |
+           (static_cast<long long>(i1) << 24) | (static_cast<long long>(i2) << 32);
+}
+
+}  // namespace
+
+// Places the terms of a JSON monomial table (grouped by output, offsets
+// [outputs + 1]) onto the slots of the compiled table of its shape; the
+// terms without a compiled slot (other monomials, repeats) follow as the
+// runtime remainder, grouped by output in JSON order.  Compiled slots that
+// the JSON does not use keep a zero coefficient.
+PolyLayout poly_layout(int lin, int lout, const std::vector<int>& offsets, const std::vector<int>& degree,
+                       const std::vector<int>& index)
+{
+    PolyLayout L;
+    const int nout = static_cast<int>(offsets.size()) - 1;
+    const int T = offsets.back();
+    int corr = 0;
+    for (int d : degree) corr = std::max(corr, d);
+    CompiledPoly cp = compiled_poly(lin, lout, corr);
+    std::map<long long, int> slot_of;
+    for (int t = 0; t < cp.nt; ++t) slot_of[term_key(cp.out[t], cp.deg[t], cp.i0[t], cp.i1[t], cp.i2[t])] = t;
+    L.slot.assign(T, -1);
+    std::vector<char> used(cp.nt, 0);
+    int matched = 0;
+    for (int o = 0; o < nout; ++o)
+        for (int j = offsets[o]; j < offsets[o + 1]; ++j) {
+            const int* ix = index.data() + 3 * static_cast<std::size_t>(j);
+            auto it = slot_of.find(term_key(o, degree[j], ix[0], ix[1], ix[2]));
+            if (it != slot_of.end() && !used[it->second]) {
+                L.slot[j] = it->second;
+                used[it->second] = 1;
+                ++matched;
+            }
+        }
+    if (cp.nt > 0 && 2 * matched < T) {  // the compiled table does not describe this model
+        cp = CompiledPoly{};
+        std::fill(L.slot.begin(), L.slot.end(), -1);
+    }
+    L.core = cp.nt > 0 ? corr : 0;
+    L.core_terms = cp.nt;
+    L.rem_offsets.push_back(0);
+    for (int o = 0; o < nout; ++o) {
+        for (int j = offsets[o]; j < offsets[o + 1]; ++j) {
+            if (L.slot[j] >= 0) continue;
+            L.slot[j] = cp.nt + static_cast<int>(L.rem_packed.size());
+            L.rem_packed.push_back(pack_term(degree[j], index.data() + 3 * static_cast<std::size_t>(j)));
+        }
+        L.rem_offsets.push_back(static_cast<int>(L.rem_packed.size()));
+    }
+    L.stride = cp.nt + static_cast<int>(L.rem_packed.size());
+    return L;
+}
+
+namespace {
 
 // Compiled R1 shape: validates the JSON path list against the compiled one and
 // scatters the JSON CG coefficients onto the compiled term slots.
@@ -245,6 +325,7 @@ void Evaluator::upload_static_tables()
         upload(*a1wt_[l], transpose(m.A1W[l].data(), num_e_[l] * C_, C_), stream_);
     }
     upload(h2m1_, to_float(m.H2M1.data(), m.H2M1.size()), stream_);
+    upload(h2m1t_, transpose(m.H2M1.data(), C_, C_), stream_);
     upload(q_, to_float(m.readout_q.data(), m.readout_q.size()), stream_);
     upload(w1_, to_float(m.readout_w1.data(), m.readout_w1.size()), stream_);
     upload(w2_, to_float(m.readout_w2.data(), m.readout_w2.size()), stream_);
@@ -256,13 +337,26 @@ void Evaluator::upload_static_tables()
     else
         cg = shape_cg<R1Shape<3, 2>>(m);
     upload(cg_, cg, stream_);
-    upload(p0_offsets_, m.m0_offsets, stream_);
-    upload(p0_packed_, pack_terms(m.m0_degree, m.m0_index), stream_);
-    p0_terms_ = m.m0_offsets.back();
-    std::vector<int> off1 = {0, static_cast<int>(m.m1_degree.size())};
-    upload(p1_offsets_, off1, stream_);
-    upload(p1_packed_, pack_terms(m.m1_degree, m.m1_index), stream_);
-    p1_terms_ = static_cast<int>(m.m1_degree.size());
+    p0_layout_ = poly_layout(m.l_max, m.L_max, m.m0_offsets, m.m0_degree, m.m0_index);
+    upload(p0_offsets_, p0_layout_.rem_offsets, stream_);
+    upload(p0_packed_, p0_layout_.rem_packed, stream_);
+    const std::vector<int> off1 = {0, static_cast<int>(m.m1_degree.size())};
+    p1_layout_ = poly_layout(m.l_max, 0, off1, m.m1_degree, m.m1_index);
+    upload(p1_offsets_, p1_layout_.rem_offsets, stream_);
+    upload(p1_packed_, p1_layout_.rem_packed, stream_);
+}
+
+PolyArgs Evaluator::poly_args(const PolyLayout& layout, const DeviceBuffer& coef, const DeviceBuffer& offsets,
+                              const DeviceBuffer& packed) const
+{
+    PolyArgs p;
+    p.core = layout.core;
+    p.stride = layout.stride;
+    p.num_rem = static_cast<int>(layout.rem_packed.size());
+    p.rem_offsets = offsets.as<int>();
+    p.rem_packed = packed.as<int>();
+    p.coef = coef.as<float>();
+    return p;
 }
 
 // Radial spline tables and per-type weights of the active element types
@@ -364,23 +458,33 @@ void Evaluator::prepare_active_types(const std::vector<int>& node_types)
     std::vector<int> type_active(m.num_elements, -1);
     for (int a = 0; a < na; ++a) type_active[types[a]] = a;
     upload(type_active_, type_active, stream_);
-    std::vector<float> p0c, p1c, h2m0;
+    std::vector<float> p0c, p1c, h2m0, h2m0t;
     std::vector<double> e0;
-    const std::size_t T0 = p0_terms_, T1 = p1_terms_;
+    // coefficients [active][slot][C] on the slots of the polynomial layouts
+    auto place = [&](const PolyLayout& L, const std::vector<double>& coef, int t, std::vector<float>& out) {
+        const std::size_t T = L.slot.size();
+        const std::size_t base = out.size();
+        out.resize(base + static_cast<std::size_t>(L.stride) * C_, 0.0f);
+        for (std::size_t j = 0; j < T; ++j)
+            for (int k = 0; k < C_; ++k)
+                out[base + static_cast<std::size_t>(L.slot[j]) * C_ + k] =
+                    static_cast<float>(coef[(static_cast<std::size_t>(t) * T + j) * C_ + k]);
+    };
     for (int a = 0; a < na; ++a) {
         const int t = types[a];
-        auto c0 = to_float(m.m0_coef.data() + static_cast<std::size_t>(t) * T0 * C_, T0 * C_);
-        p0c.insert(p0c.end(), c0.begin(), c0.end());
-        auto c1 = to_float(m.m1_coef.data() + static_cast<std::size_t>(t) * T1 * C_, T1 * C_);
-        p1c.insert(p1c.end(), c1.begin(), c1.end());
+        place(p0_layout_, m.m0_coef, t, p0c);
+        place(p1_layout_, m.m1_coef, t, p1c);
         auto hm = to_float(m.H2M0.data() + static_cast<std::size_t>(t) * C_ * C_,
                            static_cast<std::size_t>(C_) * C_);
         h2m0.insert(h2m0.end(), hm.begin(), hm.end());
+        auto hmt = transpose(m.H2M0.data() + static_cast<std::size_t>(t) * C_ * C_, C_, C_);
+        h2m0t.insert(h2m0t.end(), hmt.begin(), hmt.end());
         e0.push_back(m.atomic_energies[t]);
     }
     upload(p0_coef_, p0c, stream_);
     upload(p1_coef_, p1c, stream_);
     upload(h2m0_, h2m0, stream_);
+    upload(h2m0t_, h2m0t, stream_);
     upload(e0_, e0, stream_);
     hip_check(hipStreamSynchronize(stream_), "active type upload");
     active_types_ = types;
@@ -487,6 +591,52 @@ void Evaluator::plan_tiles()
     hip_check(hipStreamSynchronize(stream_), "tile plan");
 }
 
+// Nodes of each tile (the whole graph untiled) grouped by active type, in
+// ascending node order within a type, cut into blocks for the node kernels.
+void Evaluator::plan_node_blocks()
+{
+    const int N = num_nodes_;
+    const int tiles = tile_receivers_ > 0 ? num_tiles_ : 1;
+    const int T = tile_receivers_ > 0 ? tile_receivers_ : std::max(N, 1);
+    const int na = static_cast<int>(active_types_.size());
+    std::vector<int> ta(model_.num_elements, -1);
+    for (int a = 0; a < na; ++a) ta[active_types_[a]] = a;
+    std::vector<int> order;
+    order.reserve(N);
+    std::vector<NodeBlock> m0b, rob;
+    m0_block_offsets_.assign(tiles + 1, 0);
+    readout_block_offsets_.assign(tiles + 1, 0);
+    std::vector<std::vector<int>> by_type(na);
+    for (int t = 0; t < tiles; ++t) {
+        const int lo = t * T, hi = std::min(N, lo + T);
+        for (auto& v : by_type) v.clear();
+        for (int i = lo; i < hi; ++i) by_type[ta[host_types_[i]]].push_back(i);
+        for (int a = 0; a < na; ++a) {
+            const int start = static_cast<int>(order.size());
+            const int n = static_cast<int>(by_type[a].size());
+            order.insert(order.end(), by_type[a].begin(), by_type[a].end());
+            for (int b = 0; b < n; b += kM0BlockNodes) m0b.push_back({start + b, std::min(kM0BlockNodes, n - b), a, 0});
+            for (int b = 0; b < n; b += kReadoutBlockNodes)
+                rob.push_back({start + b, std::min(kReadoutBlockNodes, n - b), a, 0});
+        }
+        m0_block_offsets_[t + 1] = static_cast<int>(m0b.size());
+        readout_block_offsets_[t + 1] = static_cast<int>(rob.size());
+    }
+    upload(node_order_, order, stream_);
+    upload(m0_blocks_, m0b, stream_);
+    upload(readout_blocks_, rob, stream_);
+}
+
+NodeBlocks Evaluator::node_blocks(const DeviceBuffer& blocks, const std::vector<int>& offsets, int tile) const
+{
+    NodeBlocks nb;
+    nb.order = node_order_.as<int>();
+    nb.blocks = blocks.as<NodeBlock>();
+    nb.first = offsets[tile];
+    nb.count = offsets[tile + 1] - offsets[tile];
+    return nb;
+}
+
 void Evaluator::invalidate_graph()
 {
     hip_check(hipStreamSynchronize(stream_), "synchronize");
@@ -570,6 +720,7 @@ void Evaluator::finish_graph(const int* host_neigh_types)
                   "edge pairs");
     }
     plan_tiles();
+    plan_node_blocks();
     allocate_workspace();
     hip_check(hipStreamSynchronize(stream_), "graph preparation");
     ++generation_;
@@ -881,8 +1032,8 @@ void Evaluator::evaluate()
     la.node_offset = 0;
     la.node_count = N;
     hipStream_t s = stream_;
-    PolyTable p0{p0_terms_, p0_offsets_.as<int>(), p0_packed_.as<int>(), p0_coef_.as<float>()};
-    PolyTable p1{p1_terms_, p1_offsets_.as<int>(), p1_packed_.as<int>(), p1_coef_.as<float>()};
+    const PolyArgs p0 = poly_args(p0_layout_, p0_coef_, p0_offsets_, p0_packed_);
+    const PolyArgs p1 = poly_args(p1_layout_, p1_coef_, p1_offsets_, p1_packed_);
     const long long nodeLM = static_cast<long long>(nLM_) * C_;
     const long long nodelm = static_cast<long long>(nlm_) * C_;
     const long long nodelme = static_cast<long long>(nlme_) * C_;
@@ -893,7 +1044,9 @@ void Evaluator::evaluate()
         hip_check(launch_a0_forward(la, r0f_.as<float>(), A0_.as<float>(), s), "A0 forward");
         mark(kStageA0Forward, true);
         mark(kStageM0Forward, false);
-        hip_check(launch_m0_forward(la, p0, A0_.as<float>(), M0_.as<float>(), s), "M0 forward");
+        hip_check(launch_m0_forward(la, p0, node_blocks(m0_blocks_, m0_block_offsets_, 0), A0_.as<float>(),
+                                    M0_.as<float>(), s),
+                  "M0 forward");
         mark(kStageM0Forward, true);
         mark(kStageH1Gemm, false);
         for (int l = 0; l <= model_.L_max; ++l) {
@@ -929,8 +1082,7 @@ void Evaluator::evaluate()
         mark(kStageA1Gemm, true);
         // readout and its reverse down to A1_adj
         ReadoutArgs ra;
-        ra.node_offset = 0;
-        ra.num_nodes = N;
+        ra.nodes = node_blocks(readout_blocks_, readout_block_offsets_, 0);
         ra.local_base = 0;
         ra.m0_stride = nodeLM;
         ra.C = C_;
@@ -943,7 +1095,9 @@ void Evaluator::evaluate()
         ra.M0 = M0_.as<float>();
         ra.p1 = p1;
         ra.H2M0 = h2m0_.as<float>();
+        ra.H2M0T = h2m0t_.as<float>();
         ra.H2M1 = h2m1_.as<float>();
+        ra.H2M1T = h2m1t_.as<float>();
         ra.q = q_.as<float>();
         ra.W1 = w1_.as<float>();
         ra.W2 = w2_.as<float>();
@@ -998,7 +1152,9 @@ void Evaluator::evaluate()
         // A0_adj into the A1 buffer (no longer needed)
         float* A0adj = A1_.as<float>();
         mark(kStageM0Reverse, false);
-        hip_check(launch_m0_reverse(la, p0, A0_.as<float>(), M0adj, A0adj, s), "M0 reverse");
+        hip_check(launch_m0_reverse(la, p0, node_blocks(m0_blocks_, m0_block_offsets_, 0), A0_.as<float>(), M0adj,
+                                    A0adj, s),
+                  "M0 reverse");
         mark(kStageM0Reverse, true);
         mark(kStageA0Reverse, false);
         hip_check(launch_a0_reverse(la, r0f_.as<float>(), A0adj, forces_.as<double>(), s), "A0 reverse");
@@ -1062,8 +1218,8 @@ void Evaluator::evaluate_tiled()
     la.l_max = model_.l_max;
     la.L_max = model_.L_max;
     hipStream_t s = stream_;
-    PolyTable p0{p0_terms_, p0_offsets_.as<int>(), p0_packed_.as<int>(), p0_coef_.as<float>()};
-    PolyTable p1{p1_terms_, p1_offsets_.as<int>(), p1_packed_.as<int>(), p1_coef_.as<float>()};
+    const PolyArgs p0 = poly_args(p0_layout_, p0_coef_, p0_offsets_, p0_packed_);
+    const PolyArgs p1 = poly_args(p1_layout_, p1_coef_, p1_offsets_, p1_packed_);
     const long long nodeLM = static_cast<long long>(nLM_) * C_;
     const long long nodelm = static_cast<long long>(nlm_) * C_;
     const long long nodelme = static_cast<long long>(nlme_) * C_;
@@ -1095,7 +1251,9 @@ void Evaluator::evaluate_tiled()
     for (int t = 0; t < num_tiles_; ++t) {
         tile(t);
         hip_check(launch_a0_forward(la, r0f_.as<float>(), A0_.as<float>(), s), "A0 forward");
-        hip_check(launch_m0_forward(la, p0, A0_.as<float>(), M0_.as<float>(), s), "M0 forward");
+        hip_check(launch_m0_forward(la, p0, node_blocks(m0_blocks_, m0_block_offsets_, t), A0_.as<float>(),
+                                    M0_.as<float>(), s),
+                  "M0 forward");
         h1_gemms(M0_.as<float>(), nodeLM, h1w_.as<float>(), H1 + la.node_offset * nodeLM, nodeLM, "H1 gemm");
         hip_check(hipMemcpy2DAsync(M0s + static_cast<std::size_t>(la.node_offset) * C_, C_ * sizeof(float),
                                    M0_.as<float>(), nodeLM * sizeof(float), C_ * sizeof(float), la.node_count,
@@ -1115,7 +1273,9 @@ void Evaluator::evaluate_tiled()
     ra.m0_stride = C_;
     ra.p1 = p1;
     ra.H2M0 = h2m0_.as<float>();
+    ra.H2M0T = h2m0t_.as<float>();
     ra.H2M1 = h2m1_.as<float>();
+    ra.H2M1T = h2m1t_.as<float>();
     ra.q = q_.as<float>();
     ra.W1 = w1_.as<float>();
     ra.W2 = w2_.as<float>();
@@ -1141,8 +1301,7 @@ void Evaluator::evaluate_tiled()
             g.c = {A1_.as<float>() + l * l * C_, nodelm, C_};
             hip_check(launch_gemm(g, s), "A1 gemm");
         }
-        ra.node_offset = la.node_offset;
-        ra.num_nodes = la.node_count;
+        ra.nodes = node_blocks(readout_blocks_, readout_block_offsets_, t);
         ra.local_base = la.local_base;
         hip_check(launch_readout(ra, s), "readout");
         for (int l = 0; l <= model_.l_max; ++l) {
@@ -1177,7 +1336,9 @@ void Evaluator::evaluate_tiled()
                                     M0adj, s),
                   "direct adjoint");
         hip_check(launch_a0_forward(la, r0f_.as<float>(), A0_.as<float>(), s), "A0 forward");
-        hip_check(launch_m0_reverse(la, p0, A0_.as<float>(), M0adj, A0adj, s), "M0 reverse");
+        hip_check(launch_m0_reverse(la, p0, node_blocks(m0_blocks_, m0_block_offsets_, t), A0_.as<float>(), M0adj,
+                                    A0adj, s),
+                  "M0 reverse");
         hip_check(launch_a0_reverse(la, r0f_.as<float>(), A0adj, forces_.as<double>(), s), "A0 reverse");
     }
     mark(kStageAtomForces, false);

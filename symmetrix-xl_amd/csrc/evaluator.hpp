@@ -58,6 +58,19 @@ void build_periodic_graph(const double* d_positions, int num_nodes, const double
 void validate_periodic_inputs(int num_nodes, const double* cell, const double* inverse_cell,
                               double cutoff);
 
+// Placement of a symmetric-contraction polynomial's terms on the kernels'
+// coefficient slots (see PolyArgs): JSON term j -> slot[j].
+struct PolyLayout {
+    int core = 0;        // correlation order of the compiled table used, 0 = none
+    int core_terms = 0;  // compiled slots
+    int stride = 0;      // slots per active type
+    std::vector<int> slot;
+    std::vector<int> rem_offsets;  // [outputs + 1]
+    std::vector<int> rem_packed;
+};
+PolyLayout poly_layout(int input_lmax, int output_lmax, const std::vector<int>& offsets,
+                       const std::vector<int>& degree, const std::vector<int>& index);
+
 // Bytes of device memory held by this library's buffers (all evaluators).
 std::size_t device_bytes_in_use();
 
@@ -165,6 +178,8 @@ private:
     void finish_graph(const int* host_neigh_types);
     void allocate_workspace();
     void plan_tiles();
+    void plan_node_blocks();
+    NodeBlocks node_blocks(const DeviceBuffer& blocks, const std::vector<int>& offsets, int tile) const;
     void invalidate_graph();
     void evaluate();
     void evaluate_tiled();
@@ -181,10 +196,12 @@ private:
     // model tables on the device
     std::vector<int> active_types_;
     DeviceBuffer type_active_, r0f_, r1_, p0_coef_, p0_packed_, p0_offsets_, p1_coef_, p1_packed_,
-        p1_offsets_, h2m0_, e0_;
-    DeviceBuffer h1w_, h1wt_, h2m1_, q_, w1_, w2_, cg_;
+        p1_offsets_, h2m0_, h2m0t_, e0_;
+    DeviceBuffer h1w_, h1wt_, h2m1_, h2m1t_, q_, w1_, w2_, cg_;
     std::vector<std::unique_ptr<DeviceBuffer>> a1w_, a1wt_;
-    int p0_terms_ = 0, p1_terms_ = 0;
+    PolyLayout p0_layout_, p1_layout_;
+    PolyArgs poly_args(const PolyLayout& layout, const DeviceBuffer& coef, const DeviceBuffer& offsets,
+                       const DeviceBuffer& packed) const;
     SplineGrid grid_;
 
     // graph
@@ -214,6 +231,9 @@ private:
     std::vector<long long> tile_first_edge_;  // [num_tiles + 1]
     std::vector<int> tile_run_offsets_;       // [num_tiles + 1]
     DeviceBuffer M0s_, run_source_, run_start_, run_length_;
+    // nodes grouped by (tile, active type) and their blocks for the node kernels
+    DeviceBuffer node_order_, m0_blocks_, readout_blocks_;
+    std::vector<int> m0_block_offsets_, readout_block_offsets_;  // [tiles + 1]
 
     bool profiling_ = false;
     std::vector<hipEvent_t> events_;  // [stage][begin, end]

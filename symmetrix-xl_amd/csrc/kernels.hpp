@@ -45,12 +45,37 @@ struct SplineGrid {
     double r_cut = 0.0;
 };
 
-struct PolyTable {
-    int num_terms = 0;
-    const int* offsets = nullptr;  // [outputs+1]
-    const int* packed = nullptr;   // [terms] deg | i0<<4 | i1<<10 | i2<<16
-    const float* coef = nullptr;   // [active_type][terms][C]
+// Symmetric-contraction polynomial of one model (M0 or the M1 readout
+// polynomial): the terms matched to a compiled monomial table (poly_shapes.inc,
+// selected by `core` = its correlation order, 0 = none) occupy the first
+// slots of each type's coefficient block, the remaining terms follow and run
+// in a runtime loop.
+struct PolyArgs {
+    int core = 0;                      // correlation order of the compiled table, 0 = none
+    int stride = 0;                    // coefficient slots per active type
+    int num_rem = 0;                   // remainder terms
+    const int* rem_offsets = nullptr;  // [outputs+1] remainder terms grouped by output
+    const int* rem_packed = nullptr;   // [num_rem] deg | i0<<4 | i1<<10 | i2<<16
+    const float* coef = nullptr;       // [active_type][stride][C], compiled slots first
 };
+
+// Nodes grouped by active type: each block holds up to a fixed number of
+// nodes of one type, so that a thread applies each coefficient it loads to
+// several nodes.  A launch covers blocks [first, first + count).
+struct NodeBlock {
+    int start;  // first index into order
+    int count;  // nodes in the block
+    int type;   // active type index
+    int pad;
+};
+struct NodeBlocks {
+    const int* order = nullptr;         // node ids grouped by (tile, active type), ascending within
+    const NodeBlock* blocks = nullptr;
+    int first = 0;
+    int count = 0;
+};
+constexpr int kM0BlockNodes = 4;       // nodes per block of the M0 kernels
+constexpr int kReadoutBlockNodes = 8;  // nodes per block of the readout kernel
 
 struct GemmRows {
     const float* ptr = nullptr;
@@ -94,16 +119,15 @@ struct LayerArgs {
 
 // Layer 0: A0[i] = sum_j R0f_{pair(i,j)}(r) Y(r_hat)   (H0 and A0_W folded in)
 hipError_t launch_a0_forward(const LayerArgs& a, const float* r0f, float* A0, hipStream_t s);
-// M0 = P0(A0) per (node, LM, channel)
-hipError_t launch_m0_forward(const LayerArgs& a, const PolyTable& p0, const float* A0, float* M0,
-                             hipStream_t s);
+// M0 = P0(A0) per (node, LM, channel), over the nodes of the given blocks
+hipError_t launch_m0_forward(const LayerArgs& a, const PolyArgs& p0, const NodeBlocks& nb, const float* A0,
+                             float* M0, hipStream_t s);
 // Layer 1 forward: Phi1[i] = sum_j sum_terms cg R1 Y H1[src]
 hipError_t launch_r1_forward(const LayerArgs& a, const float* r1, const float* cg, const float* H1,
                              float* Phi1, hipStream_t s);
 
 struct ReadoutArgs {
-    int node_offset = 0;            // first node of this launch
-    int num_nodes = 0;              // nodes of this launch
+    NodeBlocks nodes;               // nodes of this launch (readout block size)
     int local_base = 0;             // A1 / A1_adj hold rows i - local_base
     long long m0_stride = 0;        // floats between the M0 scalar rows of consecutive nodes
     int C = 0;
@@ -114,9 +138,11 @@ struct ReadoutArgs {
     const int* type_active = nullptr;
     const float* A1 = nullptr;      // [N][num_lm][C]
     const float* M0 = nullptr;      // scalar block (LM 0) of node i at M0 + i * m0_stride
-    PolyTable p1;
-    const float* H2M0 = nullptr;    // [active][C][C]
-    const float* H2M1 = nullptr;    // [C][C]
+    PolyArgs p1;
+    const float* H2M0 = nullptr;    // [active][C][C]  ([in][out])
+    const float* H2M0T = nullptr;   // [active][C][C]  ([out][in])
+    const float* H2M1 = nullptr;    // [C][C]  ([in][out])
+    const float* H2M1T = nullptr;   // [C][C]  ([out][in])
     const float* q = nullptr;       // [C]
     const float* W1 = nullptr;      // [hidden][C]
     const float* W2 = nullptr;      // [hidden]
@@ -156,8 +182,8 @@ hipError_t launch_gather_tile_runs(const LayerArgs& a, const TileRuns& runs, con
 // M0_adj[:, LM 0, :] += direct
 hipError_t launch_add_direct(int nodes, int C, int num_LM, const float* direct, float* M0_adj,
                              hipStream_t s);
-// A0_adj = sum_LM M0_adj[LM] dP0_LM/dA0
-hipError_t launch_m0_reverse(const LayerArgs& a, const PolyTable& p0, const float* A0,
+// A0_adj = sum_LM M0_adj[LM] dP0_LM/dA0, over the nodes of the given blocks
+hipError_t launch_m0_reverse(const LayerArgs& a, const PolyArgs& p0, const NodeBlocks& nb, const float* A0,
                              const float* M0_adj, float* A0_adj, hipStream_t s);
 // Layer 0 reverse: forces += -(dE/dxyz) through R0f and Y
 hipError_t launch_a0_reverse(const LayerArgs& a, const float* r0f, const float* A0_adj,

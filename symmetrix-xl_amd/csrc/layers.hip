@@ -12,10 +12,10 @@
 // afterwards in a fixed order, so results are run-to-run deterministic).
 //
 // Reference semantics (libsymmetrix/source/mace.cpp): compute_A0_streamed
-// :1355-1403, compute_M0 :1638-1662, compute_Phi1_streamed :2022-2083,
-// compute_M1/H2/readouts and reverse_H2/M1 :2460-2657,
-// reverse_Phi1_streamed :2198-2302, reverse_M0 :1664-1688,
-// reverse_A0_streamed :1485-1559; reductions mace_kokkos_evaluate.cpp:48-291.
+// :1355-1403, compute_Phi1_streamed :2022-2083, reverse_Phi1_streamed
+// :2198-2302, reverse_A0_streamed :1485-1559; reductions
+// mace_kokkos_evaluate.cpp:48-291.  The node kernels (M0, readout) are in
+// nodes.hip.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -143,106 +143,6 @@ __global__ void __launch_bounds__(256) a0_forward_kernel(LayerArgs a, const floa
 #pragma unroll
         for (int lm = 0; lm < NLM; ++lm) out[lm * C] = acc[lm];
     }
-}
-
-// ---------------------------------------------------------------------------
-// Symmetric contraction polynomials.  Each thread owns one channel; its
-// inputs live in an LDS column so that runtime monomial indices address LDS,
-// not registers.
-// ---------------------------------------------------------------------------
-// coef: this channel's coefficients, term stride C; x: LDS column, stride xs
-__device__ __forceinline__ float poly_value(const PolyTable& p, const float* __restrict__ coef,
-                                            int C, int begin, int end, const float* x, int xs)
-{
-    float f = 0.0f;
-    for (int t = begin; t < end; ++t) {
-        const int pk = p.packed[t];
-        const int deg = pk & 15;
-        float v = coef[static_cast<size_t>(t) * C] * x[((pk >> 4) & 63) * xs];
-        if (deg > 1) v *= x[((pk >> 10) & 63) * xs];
-        if (deg > 2) v *= x[((pk >> 16) & 63) * xs];
-        f += v;
-    }
-    return f;
-}
-
-// g[v] += lambda * dP/dx_v  (LDS column, owner thread only)
-__device__ __forceinline__ void poly_gradient(const PolyTable& p, const float* __restrict__ coef,
-                                              int C, int begin, int end, const float* x, float* g,
-                                              float lambda, int xs)
-{
-    for (int t = begin; t < end; ++t) {
-        const int pk = p.packed[t];
-        const int deg = pk & 15;
-        const int i0 = ((pk >> 4) & 63) * xs;
-        const float c = coef[static_cast<size_t>(t) * C] * lambda;
-        if (deg == 1) {
-            g[i0] += c;
-        } else if (deg == 2) {
-            const int i1 = ((pk >> 10) & 63) * xs;
-            const float x0 = x[i0], x1 = x[i1];
-            g[i0] += c * x1;
-            g[i1] += c * x0;
-        } else {
-            const int i1 = ((pk >> 10) & 63) * xs;
-            const int i2 = ((pk >> 16) & 63) * xs;
-            const float x0 = x[i0], x1 = x[i1], x2 = x[i2];
-            g[i0] += c * x1 * x2;
-            g[i1] += c * x0 * x2;
-            g[i2] += c * x0 * x1;
-        }
-    }
-}
-
-__global__ void __launch_bounds__(256) m0_forward_kernel(LayerArgs a, PolyTable p,
-                                                          const float* __restrict__ A0,
-                                                          float* __restrict__ M0)
-{
-    extern __shared__ float s_mem[];
-    const int i = a.node_offset + xcd_contiguous(blockIdx.x, a.node_count);
-    const int k = threadIdx.x;
-    const int C = a.C;
-    if (k >= C) return;
-    const int nlm = (a.l_max + 1) * (a.l_max + 1);
-    const int nLM = (a.L_max + 1) * (a.L_max + 1);
-    const int stride = blockDim.x;
-    float* x = s_mem + k;
-    const float* in = A0 + static_cast<size_t>(i - a.local_base) * nlm * C + k;
-    for (int lm = 0; lm < nlm; ++lm) x[lm * stride] = in[lm * C];
-    const int at = a.graph.type_active[a.graph.node_types[i]];
-    const float* coef = p.coef + static_cast<size_t>(at) * p.num_terms * C + k;
-    float* out = M0 + static_cast<size_t>(i - a.local_base) * nLM * C + k;
-    for (int LM = 0; LM < nLM; ++LM)
-        out[LM * C] = poly_value(p, coef, C, p.offsets[LM], p.offsets[LM + 1], x, stride);
-}
-
-__global__ void __launch_bounds__(256) m0_reverse_kernel(LayerArgs a, PolyTable p,
-                                                          const float* __restrict__ A0,
-                                                          const float* __restrict__ M0_adj,
-                                                          float* __restrict__ A0_adj)
-{
-    extern __shared__ float s_mem[];
-    const int i = a.node_offset + xcd_contiguous(blockIdx.x, a.node_count);
-    const int k = threadIdx.x;
-    const int C = a.C;
-    if (k >= C) return;
-    const int nlm = (a.l_max + 1) * (a.l_max + 1);
-    const int nLM = (a.L_max + 1) * (a.L_max + 1);
-    const int stride = blockDim.x;
-    float* x = s_mem + k;
-    float* gsum = s_mem + static_cast<size_t>(nlm) * stride + k;
-    const float* in = A0 + static_cast<size_t>(i - a.local_base) * nlm * C + k;
-    for (int lm = 0; lm < nlm; ++lm) {
-        x[lm * stride] = in[lm * C];
-        gsum[lm * stride] = 0.0f;
-    }
-    const int at = a.graph.type_active[a.graph.node_types[i]];
-    const float* coef = p.coef + static_cast<size_t>(at) * p.num_terms * C + k;
-    const float* lam = M0_adj + static_cast<size_t>(i - a.local_base) * nLM * C + k;
-    for (int LM = 0; LM < nLM; ++LM)
-        poly_gradient(p, coef, C, p.offsets[LM], p.offsets[LM + 1], x, gsum, lam[LM * C], stride);
-    float* out = A0_adj + static_cast<size_t>(i - a.local_base) * nlm * C + k;
-    for (int lm = 0; lm < nlm; ++lm) out[lm * C] = gsum[lm * stride];
 }
 
 // ---------------------------------------------------------------------------
@@ -728,103 +628,6 @@ __global__ void add_direct_kernel(int nodes, int C, int nLM, const float* __rest
 }
 
 // ---------------------------------------------------------------------------
-// Node readout: M1 = P1(A1), H2 = T_z^T x + W^T M1, E = E0 + q.x + MLP(H2),
-// then the reverse down to A1_adj and the direct scalar adjoint
-// (m0_composite basis, reference mace.cpp:2460-2657).
-// ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) readout_kernel(ReadoutArgs a)
-{
-    extern __shared__ float s_mem[];
-    const int i = a.node_offset + xcd_contiguous(blockIdx.x, a.num_nodes);
-    const int il = i - a.local_base;
-    const int k = threadIdx.x;
-    const int C = a.C;
-    const int stride = blockDim.x;
-    const int nlm = a.num_lm;
-    float* x = s_mem + k;                                     // [nlm][stride]
-    float* grad = s_mem + static_cast<size_t>(nlm) * stride + k;  // [nlm][stride]
-    float* vec = s_mem + static_cast<size_t>(2 * nlm) * stride;   // 4 vectors of stride
-    float* s_xs = vec;
-    float* s_m1 = vec + stride;
-    float* s_h2 = vec + 2 * stride;
-    float* s_tmp = vec + 3 * stride;
-    float* s_hid = vec + 4 * stride;  // 2 * 64
-    const bool ok = k < C;
-    const int at = a.type_active[a.node_types[i]];
-    float m1 = 0.0f;
-    if (ok) {
-        const float* in = a.A1 + static_cast<size_t>(il) * nlm * C + k;
-        for (int lm = 0; lm < nlm; ++lm) {
-            x[lm * stride] = in[lm * C];
-            grad[lm * stride] = 0.0f;
-        }
-        const float* coef = a.p1.coef + static_cast<size_t>(at) * a.p1.num_terms * C + k;
-        m1 = poly_value(a.p1, coef, C, 0, a.p1.num_terms, x, stride);
-        poly_gradient(a.p1, coef, C, 0, a.p1.num_terms, x, grad, 1.0f, stride);
-        s_xs[k] = a.M0[static_cast<size_t>(i) * a.m0_stride + k];
-        s_m1[k] = m1;
-    }
-    __syncthreads();
-    // H2[k] = sum_in T[in][k] xs[in] + W[in][k] m1[in]
-    float h2 = 0.0f;
-    if (ok) {
-        const float* T = a.H2M0 + static_cast<size_t>(at) * C * C + k;
-        const float* W = a.H2M1 + k;
-        for (int in = 0; in < C; ++in) h2 += T[static_cast<size_t>(in) * C] * s_xs[in];
-        for (int in = 0; in < C; ++in) h2 += W[static_cast<size_t>(in) * C] * s_m1[in];
-        s_h2[k] = h2;
-        s_tmp[k] = a.q[k] * s_xs[k];
-    }
-    __syncthreads();
-    // hidden layer of readout_2 (SiLU x scale), one thread per hidden unit
-    float* s_act = s_hid;
-    float* s_gh = s_hid + 64;
-    if (threadIdx.x < a.hidden) {
-        const int h = threadIdx.x;
-        float z = 0.0f;
-        const float* w1 = a.W1 + static_cast<size_t>(h) * C;
-        for (int c = 0; c < C; ++c) z += w1[c] * s_h2[c];
-        const float sig = 1.0f / (1.0f + expf(-z));
-        const float act = a.scale * z * sig;
-        const float dact = a.scale * sig + a.scale * z * sig * (1.0f - sig);
-        s_act[h] = a.W2[h] * act;
-        s_gh[h] = a.W2[h] * dact;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        double e = a.E0[at];
-        float e1 = 0.0f;
-        for (int c = 0; c < C; ++c) e1 += s_tmp[c];
-        float e2 = 0.0f;
-        for (int h = 0; h < a.hidden; ++h) e2 += s_act[h];
-        a.energies[i] = e + static_cast<double>(e1) + static_cast<double>(e2);
-    }
-    // H2_adj[k] = sum_h W2[h] dact[h] W1[h][k], into s_h2: H2 is dead after the
-    // hidden layer (synchronised above), while thread 0 may still be reading
-    // s_tmp for the energy
-    if (ok) {
-        float g2 = 0.0f;
-        for (int h = 0; h < a.hidden; ++h) g2 += s_gh[h] * a.W1[static_cast<size_t>(h) * C + k];
-        s_h2[k] = g2;
-    }
-    __syncthreads();
-    if (ok) {
-        // direct[k] = q[k] + sum_o T[k][o] H2_adj[o];  M1_adj[k] = sum_o W[k][o] H2_adj[o]
-        const float* T = a.H2M0 + static_cast<size_t>(at) * C * C + static_cast<size_t>(k) * C;
-        const float* W = a.H2M1 + static_cast<size_t>(k) * C;
-        float d = a.q[k], m1adj = 0.0f;
-        for (int o = 0; o < C; ++o) {
-            const float g2 = s_h2[o];
-            d += T[o] * g2;
-            m1adj += W[o] * g2;
-        }
-        a.direct[static_cast<size_t>(i) * C + k] = d;
-        float* out = a.A1_adj + static_cast<size_t>(il) * nlm * C + k;
-        for (int lm = 0; lm < nlm; ++lm) out[lm * C] = grad[lm * stride] * m1adj;
-    }
-}
-
-// ---------------------------------------------------------------------------
 // fp32 MFMA GEMM over per-node row blocks.  64x64 output tile per 256-thread
 // workgroup, 2x2 waves of v_mfma_f32_32x32x2f32, K staged through LDS in
 // chunks of 32.  Requires K % 32 == 0.
@@ -1041,28 +844,6 @@ hipError_t launch_a0_reverse(const LayerArgs& a, const float* r0f, const float* 
     return hipGetLastError();
 }
 
-hipError_t launch_m0_forward(const LayerArgs& a, const PolyTable& p0, const float* A0, float* M0,
-                             hipStream_t s)
-{
-    if (a.node_count <= 0) return hipSuccess;
-    const int threads = node_threads(a.C);
-    const int nlm = (a.l_max + 1) * (a.l_max + 1);
-    const size_t shmem = sizeof(float) * nlm * threads;
-    m0_forward_kernel<<<a.node_count, threads, shmem, s>>>(a, p0, A0, M0);
-    return hipGetLastError();
-}
-
-hipError_t launch_m0_reverse(const LayerArgs& a, const PolyTable& p0, const float* A0,
-                             const float* M0_adj, float* A0_adj, hipStream_t s)
-{
-    if (a.node_count <= 0) return hipSuccess;
-    const int threads = node_threads(a.C);
-    const int nlm = (a.l_max + 1) * (a.l_max + 1);
-    const size_t shmem = sizeof(float) * 2 * nlm * threads;
-    m0_reverse_kernel<<<a.node_count, threads, shmem, s>>>(a, p0, A0, M0_adj, A0_adj);
-    return hipGetLastError();
-}
-
 hipError_t launch_r1_forward(const LayerArgs& a, const float* r1, const float* cg, const float* H1,
                              float* Phi1, hipStream_t s)
 {
@@ -1131,15 +912,6 @@ hipError_t launch_add_direct(int nodes, int C, int num_LM, const float* direct, 
     if (n == 0) return hipSuccess;
     add_direct_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(nodes, C, num_LM, direct,
                                                                             M0_adj);
-    return hipGetLastError();
-}
-
-hipError_t launch_readout(const ReadoutArgs& a, hipStream_t s)
-{
-    if (a.num_nodes <= 0) return hipSuccess;
-    const int threads = std::max(node_threads(a.C), 64);
-    const size_t shmem = sizeof(float) * (static_cast<size_t>(2 * a.num_lm + 4) * threads + 128);
-    readout_kernel<<<a.num_nodes, threads, shmem, s>>>(a);
     return hipGetLastError();
 }
 

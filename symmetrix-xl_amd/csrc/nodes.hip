@@ -1,0 +1,621 @@
+// gfx950 node kernels: the symmetric contraction M0 (forward and reverse) and
+// the readout with its reverse (M1, H2, node energies, the direct scalar
+// adjoint and the A1 adjoint).
+//
+// A workgroup owns one block of nodes of a single element type (nodes grouped
+// by type on the host); each thread owns one channel of every node of the
+// block.  The polynomial terms of the compiled monomial table are unrolled,
+// so a channel's inputs, outputs and gradients stay in registers and each
+// coefficient a thread loads is applied to all nodes of the block.  Terms of
+// the model JSON without a compiled slot run in a short runtime loop over an
+// LDS copy of the inputs, so every monomial table is evaluated exactly.
+//
+// Reference semantics (libsymmetrix/source/mace.cpp): compute_M0
+// :1638-1662, reverse_M0 :1664-1688 (MultivariatePolynomial evaluation and
+// gradient, multivariate_polynomial.cpp:10-130), compute_M1 / compute_H2 /
+// compute_readouts and reverse_H2 / reverse_M1 :2460-2657 (m0_composite
+// basis: H2 = T_z^T M0_scalar + W^T M1, E = E0 + q . M0_scalar + MLP(H2)).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <utility>
+
+#include "device_math.hpp"
+#include "kernels.hpp"
+#include "poly_shapes.inc"
+
+namespace sxl {
+namespace {
+
+inline int node_threads(int C) { return ((C + 63) / 64) * 64; }
+
+// ---------------------------------------------------------------------------
+// compiled terms (registers)
+//
+// The term code is expanded at compile time (one instantiation per term), in
+// chunks of kChunk terms: the coefficients of chunk i + 1 are loaded while
+// chunk i is evaluated.  Between chunks a scheduling barrier keeps the
+// compiler from hoisting every load to the top, and the inputs pass through
+// an empty asm statement so that products of inputs are shared only within a
+// chunk (shared across the whole polynomial they would exhaust the register
+// file).
+// ---------------------------------------------------------------------------
+constexpr int kChunk = 16;
+
+template <int NB, int NIN>
+__device__ __forceinline__ void chunk_boundary(float (&x)[NB][NIN])
+{
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int n = 0; n < NB; ++n)
+#pragma unroll
+        for (int v = 0; v < NIN; ++v) asm volatile("" : "+v"(x[n][v]));
+}
+
+template <class P, int BASE>
+__device__ __forceinline__ void load_chunk(__amdgpu_buffer_rsrc_t cs, int voff, int C, float (&c)[kChunk])
+{
+#pragma unroll
+    for (int j = 0; j < kChunk; ++j) c[j] = BASE + j < P::NT ? load1(cs, voff, (BASE + j) * C * 4) : 0.0f;
+}
+
+template <class P, int NB, int T>
+__device__ __forceinline__ void term_value(float c, const float (&x)[NB][P::NIN], float (&out)[NB][P::NOUT])
+{
+    if constexpr (T < P::NT) {
+        constexpr int d = P::deg[T], a0 = P::i0[T], a1 = P::i1[T], a2 = P::i2[T], o = P::out[T];
+#pragma unroll
+        for (int n = 0; n < NB; ++n) {
+            float v = x[n][a0];
+            if constexpr (d > 1) v *= x[n][a1];
+            if constexpr (d > 2) v *= x[n][a2];
+            out[n][o] = fmaf(c, v, out[n][o]);
+        }
+    }
+}
+
+template <class P, int NB, int T>
+__device__ __forceinline__ void term_gradient(float c, const float (&x)[NB][P::NIN], const float (&lam)[NB][P::NOUT],
+                                              float (&g)[NB][P::NIN])
+{
+    if constexpr (T < P::NT) {
+        constexpr int d = P::deg[T], a0 = P::i0[T], a1 = P::i1[T], a2 = P::i2[T], o = P::out[T];
+#pragma unroll
+        for (int n = 0; n < NB; ++n) {
+            const float u = c * lam[n][o];
+            if constexpr (d == 1) {
+                g[n][a0] += u;
+            } else if constexpr (d == 2) {
+                const float x0 = x[n][a0], x1 = x[n][a1];
+                g[n][a0] = fmaf(u, x1, g[n][a0]);
+                g[n][a1] = fmaf(u, x0, g[n][a1]);
+            } else {
+                const float x0 = x[n][a0], x1 = x[n][a1], x2 = x[n][a2];
+                g[n][a0] = fmaf(u, x1 * x2, g[n][a0]);
+                g[n][a1] = fmaf(u, x0 * x2, g[n][a1]);
+                g[n][a2] = fmaf(u, x0 * x1, g[n][a2]);
+            }
+        }
+    }
+}
+
+template <class P, int NB, int BASE, int... J>
+__device__ __forceinline__ void value_chunk(const float (&c)[kChunk], const float (&x)[NB][P::NIN],
+                                            float (&out)[NB][P::NOUT], std::integer_sequence<int, J...>)
+{
+    (term_value<P, NB, BASE + J>(c[J], x, out), ...);
+}
+
+template <class P, int NB, int BASE, int... J>
+__device__ __forceinline__ void gradient_chunk(const float (&c)[kChunk], const float (&x)[NB][P::NIN],
+                                               const float (&lam)[NB][P::NOUT], float (&g)[NB][P::NIN],
+                                               std::integer_sequence<int, J...>)
+{
+    (term_gradient<P, NB, BASE + J>(c[J], x, lam, g), ...);
+}
+
+template <class P, int NB, int BASE>
+__device__ __forceinline__ void core_value_from(__amdgpu_buffer_rsrc_t cs, int voff, int C, const float (&cur)[kChunk],
+                                                float (&x)[NB][P::NIN], float (&out)[NB][P::NOUT])
+{
+    if constexpr (BASE < P::NT) {
+        float nxt[kChunk];
+        if constexpr (BASE + kChunk < P::NT) load_chunk<P, BASE + kChunk>(cs, voff, C, nxt);
+        value_chunk<P, NB, BASE>(cur, x, out, std::make_integer_sequence<int, kChunk>{});
+        chunk_boundary<NB, P::NIN>(x);
+        core_value_from<P, NB, BASE + kChunk>(cs, voff, C, nxt, x, out);
+    }
+}
+
+template <class P, int NB, int BASE>
+__device__ __forceinline__ void core_gradient_from(__amdgpu_buffer_rsrc_t cs, int voff, int C,
+                                                   const float (&cur)[kChunk], float (&x)[NB][P::NIN],
+                                                   const float (&lam)[NB][P::NOUT], float (&g)[NB][P::NIN])
+{
+    if constexpr (BASE < P::NT) {
+        float nxt[kChunk];
+        if constexpr (BASE + kChunk < P::NT) load_chunk<P, BASE + kChunk>(cs, voff, C, nxt);
+        gradient_chunk<P, NB, BASE>(cur, x, lam, g, std::make_integer_sequence<int, kChunk>{});
+        chunk_boundary<NB, P::NIN>(x);
+        core_gradient_from<P, NB, BASE + kChunk>(cs, voff, C, nxt, x, lam, g);
+    }
+}
+
+// out[n][o] += sum over compiled terms t of output o: c_t prod x[n][i]
+template <class P, int NB>
+__device__ __forceinline__ void core_value(__amdgpu_buffer_rsrc_t cs, int voff, int C,
+                                           float (&x)[NB][P::NIN], float (&out)[NB][P::NOUT])
+{
+    if constexpr (P::NT > 0) {
+        float c[kChunk];
+        load_chunk<P, 0>(cs, voff, C, c);
+        core_value_from<P, NB, 0>(cs, voff, C, c, x, out);
+    }
+}
+
+// g[n][i] += sum over compiled terms t: c_t lam[n][out_t] d(prod x[n])/dx_i
+template <class P, int NB>
+__device__ __forceinline__ void core_gradient(__amdgpu_buffer_rsrc_t cs, int voff, int C,
+                                              float (&x)[NB][P::NIN], const float (&lam)[NB][P::NOUT],
+                                              float (&g)[NB][P::NIN])
+{
+    if constexpr (P::NT > 0) {
+        float c[kChunk];
+        load_chunk<P, 0>(cs, voff, C, c);
+        core_gradient_from<P, NB, 0>(cs, voff, C, c, x, lam, g);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// remainder terms (runtime table; one node, inputs in this thread's LDS column)
+// ---------------------------------------------------------------------------
+template <int NOUT>
+__device__ __forceinline__ void rem_value(const PolyArgs& p, __amdgpu_buffer_rsrc_t cs, int voff, int C,
+                                          int core_terms, const float* xc, int xs, float (&f)[NOUT])
+{
+#pragma unroll
+    for (int o = 0; o < NOUT; ++o)
+        for (int t = p.rem_offsets[o]; t < p.rem_offsets[o + 1]; ++t) {
+            const int pk = p.rem_packed[t];
+            const int d = pk & 15;
+            float v = xc[((pk >> 4) & 63) * xs];
+            if (d > 1) v *= xc[((pk >> 10) & 63) * xs];
+            if (d > 2) v *= xc[((pk >> 16) & 63) * xs];
+            f[o] = fmaf(load1(cs, voff, (core_terms + t) * C * 4), v, f[o]);
+        }
+}
+
+template <int NOUT>
+__device__ __forceinline__ void rem_gradient(const PolyArgs& p, __amdgpu_buffer_rsrc_t cs, int voff, int C,
+                                             int core_terms, const float* xc, float* gc, int xs,
+                                             const float (&lam)[NOUT])
+{
+#pragma unroll
+    for (int o = 0; o < NOUT; ++o)
+        for (int t = p.rem_offsets[o]; t < p.rem_offsets[o + 1]; ++t) {
+            const int pk = p.rem_packed[t];
+            const int d = pk & 15;
+            const int a0 = ((pk >> 4) & 63) * xs, a1 = ((pk >> 10) & 63) * xs, a2 = ((pk >> 16) & 63) * xs;
+            const float u = load1(cs, voff, (core_terms + t) * C * 4) * lam[o];
+            if (d == 1) {
+                gc[a0] += u;
+            } else if (d == 2) {
+                const float x0 = xc[a0], x1 = xc[a1];
+                gc[a0] += u * x1;
+                gc[a1] += u * x0;
+            } else {
+                const float x0 = xc[a0], x1 = xc[a1], x2 = xc[a2];
+                gc[a0] += u * (x1 * x2);
+                gc[a1] += u * (x0 * x2);
+                gc[a2] += u * (x0 * x1);
+            }
+        }
+}
+
+// Forward remainder of the NB nodes held in registers (LDS column of NIN floats).
+template <class P, int NB>
+__device__ __forceinline__ void rem_value_nodes(const PolyArgs& p, __amdgpu_buffer_rsrc_t cs, int voff, int C,
+                                                float* xc, int xs, const float (&x)[NB][P::NIN],
+                                                float (&out)[NB][P::NOUT])
+{
+#pragma unroll
+    for (int n = 0; n < NB; ++n) {
+#pragma unroll
+        for (int v = 0; v < P::NIN; ++v) xc[v * xs] = x[n][v];
+        rem_value<P::NOUT>(p, cs, voff, C, P::NT, xc, xs, out[n]);
+    }
+}
+
+template <class P, int NB>
+__device__ __forceinline__ void rem_gradient_nodes(const PolyArgs& p, __amdgpu_buffer_rsrc_t cs, int voff, int C,
+                                                   float* xc, float* gc, int xs, const float (&x)[NB][P::NIN],
+                                                   const float (&lam)[NB][P::NOUT], float (&g)[NB][P::NIN])
+{
+#pragma unroll
+    for (int n = 0; n < NB; ++n) {
+#pragma unroll
+        for (int v = 0; v < P::NIN; ++v) {
+            xc[v * xs] = x[n][v];
+            gc[v * xs] = 0.0f;
+        }
+        rem_gradient<P::NOUT>(p, cs, voff, C, P::NT, xc, gc, xs, lam[n]);
+#pragma unroll
+        for (int v = 0; v < P::NIN; ++v) g[n][v] += gc[v * xs];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// M0 forward / reverse
+// ---------------------------------------------------------------------------
+template <class P, int NB>
+__global__ void __launch_bounds__(256) m0_forward_kernel(LayerArgs a, PolyArgs p, NodeBlocks nb,
+                                                          const float* __restrict__ A0, float* __restrict__ M0)
+{
+    constexpr int NIN = P::NIN, NOUT = P::NOUT;
+    extern __shared__ float s_mem[];  // remainder terms only: [NIN][blockDim.x]
+    const NodeBlock blk = nb.blocks[nb.first + blockIdx.x];
+    const int k = threadIdx.x;
+    const int C = a.C;
+    const int kk = min(k, C - 1);
+    int node[NB];
+    float x[NB][NIN];
+#pragma unroll
+    for (int n = 0; n < NB; ++n) {
+        node[n] = n < blk.count ? nb.order[blk.start + n] - a.local_base : -1;
+        const float* in = A0 + static_cast<size_t>(max(node[n], 0)) * NIN * C + kk;
+#pragma unroll
+        for (int v = 0; v < NIN; ++v) x[n][v] = node[n] >= 0 ? in[v * C] : 0.0f;
+    }
+    float out[NB][NOUT];
+#pragma unroll
+    for (int n = 0; n < NB; ++n)
+#pragma unroll
+        for (int o = 0; o < NOUT; ++o) out[n][o] = 0.0f;
+    const auto cs = buffer_rsrc(p.coef + static_cast<size_t>(blk.type) * p.stride * C, p.stride * C * 4);
+    core_value<P, NB>(cs, kk * 4, C, x, out);
+    if (p.num_rem > 0) rem_value_nodes<P, NB>(p, cs, kk * 4, C, s_mem + k, blockDim.x, x, out);
+    if (k < C) {
+#pragma unroll
+        for (int n = 0; n < NB; ++n) {
+            if (node[n] < 0) continue;
+            float* o = M0 + static_cast<size_t>(node[n]) * NOUT * C + k;
+#pragma unroll
+            for (int q = 0; q < NOUT; ++q) o[q * C] = out[n][q];
+        }
+    }
+}
+
+template <class P, int NB>
+__global__ void __launch_bounds__(256) m0_reverse_kernel(LayerArgs a, PolyArgs p, NodeBlocks nb,
+                                                          const float* __restrict__ A0,
+                                                          const float* __restrict__ M0_adj,
+                                                          float* __restrict__ A0_adj)
+{
+    constexpr int NIN = P::NIN, NOUT = P::NOUT;
+    extern __shared__ float s_mem[];  // remainder terms only: [2][NIN][blockDim.x]
+    const NodeBlock blk = nb.blocks[nb.first + blockIdx.x];
+    const int k = threadIdx.x;
+    const int C = a.C;
+    const int kk = min(k, C - 1);
+    int node[NB];
+    float x[NB][NIN], lam[NB][NOUT], g[NB][NIN];
+#pragma unroll
+    for (int n = 0; n < NB; ++n) {
+        node[n] = n < blk.count ? nb.order[blk.start + n] - a.local_base : -1;
+        const size_t row = static_cast<size_t>(max(node[n], 0));
+        const float* in = A0 + row * NIN * C + kk;
+        const float* la = M0_adj + row * NOUT * C + kk;
+#pragma unroll
+        for (int v = 0; v < NIN; ++v) {
+            x[n][v] = node[n] >= 0 ? in[v * C] : 0.0f;
+            g[n][v] = 0.0f;
+        }
+#pragma unroll
+        for (int o = 0; o < NOUT; ++o) lam[n][o] = node[n] >= 0 ? la[o * C] : 0.0f;
+    }
+    const auto cs = buffer_rsrc(p.coef + static_cast<size_t>(blk.type) * p.stride * C, p.stride * C * 4);
+    core_gradient<P, NB>(cs, kk * 4, C, x, lam, g);
+    if (p.num_rem > 0)
+        rem_gradient_nodes<P, NB>(p, cs, kk * 4, C, s_mem + k, s_mem + NIN * blockDim.x + k, blockDim.x, x,
+                                  lam, g);
+    if (k < C) {
+#pragma unroll
+        for (int n = 0; n < NB; ++n) {
+            if (node[n] < 0) continue;
+            float* o = A0_adj + static_cast<size_t>(node[n]) * NIN * C + k;
+#pragma unroll
+            for (int v = 0; v < NIN; ++v) o[v * C] = g[n][v];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Readout and its reverse, NB nodes of one type per workgroup:
+//   1. M1[n][k] = P1(A1[n][:, k]), xs[n][k] = M0[n][0][k]          (LDS)
+//   2. H2[n][k] = sum_in T[in][k] xs[n][in] + W[in][k] M1[n][in]  (LDS)
+//   3. hidden units, one thread per (node, unit): z = W1[h] . H2[n],
+//      act = W2[h] s silu(z), dact = W2[h] s silu'(z)
+//   4. E[n] = E0 + q . xs[n] + sum_h act; H2_adj[n][k] = sum_h dact W1[h][k]
+//   5. direct[n][k] = q[k] + sum_o T[k][o] H2_adj[n][o];
+//      M1_adj[n][k] = sum_o W[k][o] H2_adj[n][o]
+//   6. A1_adj[n][lm][k] = M1_adj[n][k] dP1/dA1[lm]
+// ---------------------------------------------------------------------------
+constexpr int kReadoutGroup = 4;  // nodes held in registers by the polynomial phases
+constexpr int kMaxHidden = 64;
+
+template <class P1, int NB>
+__global__ void __launch_bounds__(256) readout_kernel(ReadoutArgs a)
+{
+    constexpr int NIN = P1::NIN;
+    constexpr int G = kReadoutGroup;
+    static_assert(NB % G == 0, "readout block must hold whole register groups");
+    extern __shared__ float s_mem[];
+    const int T = blockDim.x;  // >= C, a multiple of 64
+    float* s_xs = s_mem;                // [NB][T]
+    float* s_m1 = s_xs + NB * T;        // [NB][T]
+    float* s_h2 = s_m1 + NB * T;        // [NB][T]: H2, then its adjoint
+    float* s_act = s_h2 + NB * T;       // [NB][kMaxHidden]
+    float* s_gh = s_act + NB * kMaxHidden;  // [NB][kMaxHidden]
+    float* s_rem = s_gh + NB * kMaxHidden;  // [2][NIN][T], remainder terms only
+    const NodeBlock blk = a.nodes.blocks[a.nodes.first + blockIdx.x];
+    const int k = threadIdx.x;
+    const int C = a.C;
+    const int kk = min(k, C - 1);
+    const bool ok = k < C;
+    const int H = a.hidden;
+    int node[NB];
+#pragma unroll
+    for (int n = 0; n < NB; ++n) node[n] = n < blk.count ? a.nodes.order[blk.start + n] : -1;
+    const auto cs = buffer_rsrc(a.p1.coef + static_cast<size_t>(blk.type) * a.p1.stride * C,
+                                a.p1.stride * C * 4);
+    const int voff = kk * 4;
+
+    // 1. M1 and the scalar M0 block
+#pragma unroll
+    for (int g0 = 0; g0 < NB; g0 += G) {
+        float x[G][NIN], m1[G][1];
+#pragma unroll
+        for (int n = 0; n < G; ++n) {
+            const int i = node[g0 + n];
+            const float* in = a.A1 + static_cast<size_t>(max(i - a.local_base, 0)) * NIN * C + kk;
+#pragma unroll
+            for (int v = 0; v < NIN; ++v) x[n][v] = i >= 0 ? in[v * C] : 0.0f;
+            m1[n][0] = 0.0f;
+        }
+        core_value<P1, G>(cs, voff, C, x, m1);
+        if (a.p1.num_rem > 0) rem_value_nodes<P1, G>(a.p1, cs, voff, C, s_rem + k, T, x, m1);
+#pragma unroll
+        for (int n = 0; n < G; ++n) {
+            const int i = node[g0 + n];
+            const bool on = ok && i >= 0;
+            s_m1[(g0 + n) * T + k] = on ? m1[n][0] : 0.0f;
+            s_xs[(g0 + n) * T + k] = on ? a.M0[static_cast<size_t>(i) * a.m0_stride + k] : 0.0f;
+        }
+    }
+    __syncthreads();
+
+    // 2. H2
+    if (ok) {
+        float h2[NB];
+#pragma unroll
+        for (int n = 0; n < NB; ++n) h2[n] = 0.0f;
+        const float* Tm = a.H2M0 + static_cast<size_t>(blk.type) * C * C + k;
+        const float* Wm = a.H2M1 + k;
+        for (int in = 0; in < C; in += 4) {
+            float t4[4], w4[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                t4[u] = Tm[static_cast<size_t>(in + u) * C];
+                w4[u] = Wm[static_cast<size_t>(in + u) * C];
+            }
+#pragma unroll
+            for (int n = 0; n < NB; ++n) {
+                const float4 xv = *reinterpret_cast<const float4*>(s_xs + n * T + in);
+                const float4 mv = *reinterpret_cast<const float4*>(s_m1 + n * T + in);
+                float h = h2[n];
+                h = fmaf(t4[0], xv.x, h);
+                h = fmaf(t4[1], xv.y, h);
+                h = fmaf(t4[2], xv.z, h);
+                h = fmaf(t4[3], xv.w, h);
+                h = fmaf(w4[0], mv.x, h);
+                h = fmaf(w4[1], mv.y, h);
+                h = fmaf(w4[2], mv.z, h);
+                h = fmaf(w4[3], mv.w, h);
+                h2[n] = h;
+            }
+        }
+#pragma unroll
+        for (int n = 0; n < NB; ++n) s_h2[n * T + k] = h2[n];
+    }
+    __syncthreads();
+
+    // 3. hidden layer of readout_2
+    for (int job = threadIdx.x; job < NB * H; job += T) {
+        const int n = job / H, h = job - (job / H) * H;
+        const float* w1 = a.W1 + static_cast<size_t>(h) * C;
+        const float* hn = s_h2 + n * T;
+        float z = 0.0f;
+        for (int c = 0; c < C; ++c) z = fmaf(w1[c], hn[c], z);
+        const float sig = 1.0f / (1.0f + expf(-z));
+        const float act = a.scale * z * sig;
+        const float dact = a.scale * sig + a.scale * z * sig * (1.0f - sig);
+        s_act[n * kMaxHidden + h] = a.W2[h] * act;
+        s_gh[n * kMaxHidden + h] = a.W2[h] * dact;
+    }
+    __syncthreads();
+
+    // 4. energies (one thread per node) and the H2 adjoint
+    if (threadIdx.x < blk.count) {
+        const int n = threadIdx.x;
+        const int i = a.nodes.order[blk.start + n];
+        float e1 = 0.0f;
+        for (int c = 0; c < C; ++c) e1 = fmaf(a.q[c], s_xs[n * T + c], e1);
+        float e2 = 0.0f;
+        for (int h = 0; h < H; ++h) e2 += s_act[n * kMaxHidden + h];
+        a.energies[i] = a.E0[blk.type] + static_cast<double>(e1) + static_cast<double>(e2);
+    }
+    if (ok) {
+        float gh2[NB];
+#pragma unroll
+        for (int n = 0; n < NB; ++n) gh2[n] = 0.0f;
+        for (int h = 0; h < H; ++h) {
+            const float w = a.W1[static_cast<size_t>(h) * C + k];
+#pragma unroll
+            for (int n = 0; n < NB; ++n) gh2[n] = fmaf(s_gh[n * kMaxHidden + h], w, gh2[n]);
+        }
+        // H2 is dead (its last reader, step 3, finished at the barrier above)
+#pragma unroll
+        for (int n = 0; n < NB; ++n) s_h2[n * T + k] = gh2[n];
+    }
+    __syncthreads();
+
+    // 5. direct scalar adjoint and the M1 adjoint
+    float m1adj[NB];
+#pragma unroll
+    for (int n = 0; n < NB; ++n) m1adj[n] = 0.0f;
+    if (ok) {
+        float d[NB];
+        const float qk = a.q[k];
+#pragma unroll
+        for (int n = 0; n < NB; ++n) d[n] = qk;
+        const float* Tt = a.H2M0T + static_cast<size_t>(blk.type) * C * C + k;
+        const float* Wt = a.H2M1T + k;
+        for (int o = 0; o < C; o += 4) {
+            float t4[4], w4[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                t4[u] = Tt[static_cast<size_t>(o + u) * C];
+                w4[u] = Wt[static_cast<size_t>(o + u) * C];
+            }
+#pragma unroll
+            for (int n = 0; n < NB; ++n) {
+                const float4 gv = *reinterpret_cast<const float4*>(s_h2 + n * T + o);
+                d[n] = fmaf(t4[0], gv.x, d[n]);
+                d[n] = fmaf(t4[1], gv.y, d[n]);
+                d[n] = fmaf(t4[2], gv.z, d[n]);
+                d[n] = fmaf(t4[3], gv.w, d[n]);
+                m1adj[n] = fmaf(w4[0], gv.x, m1adj[n]);
+                m1adj[n] = fmaf(w4[1], gv.y, m1adj[n]);
+                m1adj[n] = fmaf(w4[2], gv.z, m1adj[n]);
+                m1adj[n] = fmaf(w4[3], gv.w, m1adj[n]);
+            }
+        }
+#pragma unroll
+        for (int n = 0; n < NB; ++n)
+            if (node[n] >= 0) a.direct[static_cast<size_t>(node[n]) * C + k] = d[n];
+    }
+
+    // 6. A1 adjoint
+#pragma unroll
+    for (int g0 = 0; g0 < NB; g0 += G) {
+        float x[G][NIN], lam[G][1], g[G][NIN];
+#pragma unroll
+        for (int n = 0; n < G; ++n) {
+            const int i = node[g0 + n];
+            const float* in = a.A1 + static_cast<size_t>(max(i - a.local_base, 0)) * NIN * C + kk;
+#pragma unroll
+            for (int v = 0; v < NIN; ++v) {
+                x[n][v] = i >= 0 ? in[v * C] : 0.0f;
+                g[n][v] = 0.0f;
+            }
+            lam[n][0] = m1adj[g0 + n];
+        }
+        core_gradient<P1, G>(cs, voff, C, x, lam, g);
+        if (a.p1.num_rem > 0)
+            rem_gradient_nodes<P1, G>(a.p1, cs, voff, C, s_rem + k, s_rem + NIN * T + k, T, x, lam, g);
+        if (ok) {
+#pragma unroll
+            for (int n = 0; n < G; ++n) {
+                const int i = node[g0 + n];
+                if (i < 0) continue;
+                float* out = a.A1_adj + static_cast<size_t>(i - a.local_base) * NIN * C + k;
+#pragma unroll
+                for (int v = 0; v < NIN; ++v) out[v * C] = g[n][v];
+            }
+        }
+    }
+}
+
+template <int LIN, int LOUT, int CORR>
+hipError_t m0_forward_launch(const LayerArgs& a, const PolyArgs& p, const NodeBlocks& nb, const float* A0,
+                             float* M0, hipStream_t s)
+{
+    using P = PolyShape<LIN, LOUT, CORR>;
+    const int threads = node_threads(a.C);
+    const size_t shmem = p.num_rem > 0 ? sizeof(float) * P::NIN * threads : 0;
+    m0_forward_kernel<P, kM0BlockNodes><<<nb.count, threads, shmem, s>>>(a, p, nb, A0, M0);
+    return hipGetLastError();
+}
+
+template <int LIN, int LOUT, int CORR>
+hipError_t m0_reverse_launch(const LayerArgs& a, const PolyArgs& p, const NodeBlocks& nb, const float* A0,
+                             const float* M0_adj, float* A0_adj, hipStream_t s)
+{
+    using P = PolyShape<LIN, LOUT, CORR>;
+    const int threads = node_threads(a.C);
+    const size_t shmem = p.num_rem > 0 ? sizeof(float) * 2 * P::NIN * threads : 0;
+    m0_reverse_kernel<P, kM0BlockNodes><<<nb.count, threads, shmem, s>>>(a, p, nb, A0, M0_adj, A0_adj);
+    return hipGetLastError();
+}
+
+template <int LIN, int CORR>
+hipError_t readout_launch(const ReadoutArgs& a, hipStream_t s)
+{
+    using P = PolyShape<LIN, 0, CORR>;
+    const int threads = std::max(node_threads(a.C), 64);
+    const size_t NB = kReadoutBlockNodes;
+    size_t floats = 3 * NB * threads + 2 * NB * kMaxHidden;
+    if (a.p1.num_rem > 0) floats += 2 * static_cast<size_t>(P::NIN) * threads;
+    readout_kernel<P, kReadoutBlockNodes><<<a.nodes.count, threads, sizeof(float) * floats, s>>>(a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_m0_forward(const LayerArgs& a, const PolyArgs& p0, const NodeBlocks& nb, const float* A0,
+                             float* M0, hipStream_t s)
+{
+    if (nb.count <= 0) return hipSuccess;
+    if (node_threads(a.C) > 256) return hipErrorInvalidValue;
+    switch (a.l_max * 100 + a.L_max * 10 + p0.core) {
+    case 212: return m0_forward_launch<2, 1, 2>(a, p0, nb, A0, M0, s);
+    case 313: return m0_forward_launch<3, 1, 3>(a, p0, nb, A0, M0, s);
+    case 323: return m0_forward_launch<3, 2, 3>(a, p0, nb, A0, M0, s);
+    case 210: return m0_forward_launch<2, 1, 0>(a, p0, nb, A0, M0, s);
+    case 310: return m0_forward_launch<3, 1, 0>(a, p0, nb, A0, M0, s);
+    case 320: return m0_forward_launch<3, 2, 0>(a, p0, nb, A0, M0, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_m0_reverse(const LayerArgs& a, const PolyArgs& p0, const NodeBlocks& nb, const float* A0,
+                             const float* M0_adj, float* A0_adj, hipStream_t s)
+{
+    if (nb.count <= 0) return hipSuccess;
+    if (node_threads(a.C) > 256) return hipErrorInvalidValue;
+    switch (a.l_max * 100 + a.L_max * 10 + p0.core) {
+    case 212: return m0_reverse_launch<2, 1, 2>(a, p0, nb, A0, M0_adj, A0_adj, s);
+    case 313: return m0_reverse_launch<3, 1, 3>(a, p0, nb, A0, M0_adj, A0_adj, s);
+    case 323: return m0_reverse_launch<3, 2, 3>(a, p0, nb, A0, M0_adj, A0_adj, s);
+    case 210: return m0_reverse_launch<2, 1, 0>(a, p0, nb, A0, M0_adj, A0_adj, s);
+    case 310: return m0_reverse_launch<3, 1, 0>(a, p0, nb, A0, M0_adj, A0_adj, s);
+    case 320: return m0_reverse_launch<3, 2, 0>(a, p0, nb, A0, M0_adj, A0_adj, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_readout(const ReadoutArgs& a, hipStream_t s)
+{
+    if (a.nodes.count <= 0) return hipSuccess;
+    if (node_threads(a.C) > 256 || a.hidden > kMaxHidden || a.C % 4 != 0) return hipErrorInvalidValue;
+    const int lin = a.num_lm == 9 ? 2 : a.num_lm == 16 ? 3 : -1;
+    switch (lin * 10 + a.p1.core) {
+    case 22: return readout_launch<2, 2>(a, s);
+    case 33: return readout_launch<3, 3>(a, s);
+    case 20: return readout_launch<2, 0>(a, s);
+    case 30: return readout_launch<3, 0>(a, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace sxl

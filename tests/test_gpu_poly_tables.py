@@ -1,0 +1,149 @@
+"""GPU parity for symmetric-contraction tables the compiled monomial tables do
+not describe exactly.
+
+The node kernels evaluate the terms of a model's M0 / M1 monomial lists that
+match a compiled table in registers and every other term in a runtime loop.
+These tests rewrite the generated model JSON so that both paths carry
+weight, and compare the HIP result with the CPU oracle (which evaluates the
+JSON lists as given):
+
+- monomial order shuffled within each output, and the variable order inside
+  each monomial permuted (same polynomial, compiled slots found by value);
+- extra monomials that no compiled slot holds, plus a repeated monomial;
+- a correlation order with no compiled table (every term runs in the loop).
+
+Tolerances as in test_gpu_parity.py (FP32).
+"""
+
+import json
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+E_TOL = 1e-5   # eV/atom
+F_TOL = 1e-4   # eV/A
+S_TOL = 1e-6   # eV/A^3
+
+
+def _write(tmp_path, name, model):
+    path = tmp_path / f"{name}.json"
+    path.write_text(json.dumps(model))
+    return str(path)
+
+
+def _generated(preset_or_shape, seed=0):
+    from symmetrix_amd import synthetic
+
+    return json.loads(synthetic.model_json(synthetic.random_mace_model(preset_or_shape, seed=seed)))
+
+
+def _check(oracle_lib, path, model, structure):
+    from symmetrix_amd import Symmetrix, synthetic
+
+    got = Symmetrix(path).calculate(structure)
+    types = synthetic.node_types(structure, model["atomic_numbers"])
+    orc = oracle_lib.MaceOracle(model, np.unique(types), "float32")
+    want = oracle_lib.evaluate(orc, structure, model["r_cut"] + 0.5)
+    n = len(structure)
+    de = abs(got["energy"] - want["energy"]) / n
+    df = float(np.max(np.abs(got["forces"] - want["forces"])))
+    ds = float(np.max(np.abs(got["stress"] - want["stress"])))
+    print(f"  |dE|/atom={de:.3e}  max|dF|={df:.3e}  max|dS|={ds:.3e}", flush=True)
+    assert de < E_TOL and df < F_TOL and ds < S_TOL
+    return got
+
+
+def _shuffle(model, rng):
+    """Same polynomials, terms and variables in another order."""
+    C = model["num_channels"]
+    ne = model["num_elements"]
+    for LM, monos in model["M0_monomials"].items():
+        perm = rng.permutation(len(monos))
+        model["M0_monomials"][LM] = [[int(v) for v in rng.permutation(monos[p])] for p in perm]
+        for a in range(ne):
+            w = model["M0_weights"][str(a)][LM]
+            for k in range(C):
+                w[str(k)] = [w[str(k)][p] for p in perm]
+    monos = model["M1_monomials"]
+    perm = rng.permutation(len(monos))
+    model["M1_monomials"] = [[int(v) for v in rng.permutation(monos[p])] for p in perm]
+    for a in range(ne):
+        w = model["M1_weights"][str(a)]
+        for k in range(C):
+            w[str(k)] = [w[str(k)][p] for p in perm]
+
+
+def _add_terms(model, rng, extra):
+    """Appends `extra` monomials (and one repeat of an existing one) to the M0
+    outputs with LM >= 1 and to M1, with small random coefficients."""
+    C = model["num_channels"]
+    ne = model["num_elements"]
+    nlm = (model["l_max"] + 1) ** 2
+
+    def new_terms(existing):
+        have = {tuple(sorted(m)) for m in existing}
+        out = []
+        while len(out) < extra:
+            deg = int(rng.integers(2, 4))
+            m = sorted(int(v) for v in rng.integers(0, nlm, size=deg))
+            if tuple(m) not in have:
+                have.add(tuple(m))
+                out.append(m)
+        return out + [list(existing[len(existing) // 2])]
+
+    for LM, monos in model["M0_monomials"].items():
+        if LM == "0":
+            continue
+        add = new_terms(monos)
+        model["M0_monomials"][LM] = monos + add
+        for a in range(ne):
+            w = model["M0_weights"][str(a)][LM]
+            for k in range(C):
+                w[str(k)] = w[str(k)] + list(0.05 * rng.normal(size=len(add)))
+    add = new_terms(model["M1_monomials"])
+    model["M1_monomials"] = model["M1_monomials"] + add
+    for a in range(ne):
+        w = model["M1_weights"][str(a)]
+        for k in range(C):
+            w[str(k)] = w[str(k)] + list(0.05 * rng.normal(size=len(add)))
+
+
+@pytest.mark.parametrize("preset,cells", [("tiny", 2), ("medium3", 2)])
+def test_shuffled_monomial_tables_match_oracle_and_generated_order(oracle_lib, tmp_path, preset, cells):
+    from symmetrix_amd import Symmetrix, synthetic
+
+    s = synthetic.srtio3_supercell(cells, sigma=0.05, seed=3)
+    model = _generated(preset)
+    base = Symmetrix(_write(tmp_path, "base", model)).calculate(s)
+    _shuffle(model, np.random.default_rng(7))
+    print(f"{preset}: shuffled M0/M1 tables, SrTiO3 {cells}^3", flush=True)
+    got = _check(oracle_lib, _write(tmp_path, "shuffled", model), model, s)
+    # the same polynomial in another term order: FP32 summation-order noise only
+    assert abs(got["energy"] - base["energy"]) / len(s) < E_TOL
+    np.testing.assert_allclose(got["forces"], base["forces"], atol=F_TOL)
+
+
+@pytest.mark.parametrize("preset,cells", [("tiny", 2), ("medium3", 2)])
+def test_extra_monomials_run_in_the_remainder_loop(oracle_lib, tmp_path, preset, cells):
+    from symmetrix_amd import synthetic
+
+    s = synthetic.srtio3_supercell(cells, sigma=0.05, seed=4)
+    model = _generated(preset, seed=1)
+    _add_terms(model, np.random.default_rng(11), extra=6)
+    print(f"{preset}: M0/M1 tables with extra and repeated monomials, SrTiO3 {cells}^3", flush=True)
+    _check(oracle_lib, _write(tmp_path, "extra", model), model, s)
+
+
+def test_uncompiled_correlation_order_matches_oracle(oracle_lib, tmp_path):
+    from symmetrix_amd import synthetic
+
+    shape = synthetic.ModelShape(
+        atomic_numbers=(38, 22, 8), channels=64, l_max=3, L_max=1, correlation=2,
+        radial_hidden=(32, 32), r_cut=5.0, avg_num_neighbors=40.0,
+    )
+    model = _generated(shape, seed=2)
+    s = synthetic.srtio3_supercell(2, sigma=0.05, seed=5)
+    print("l_max 3, correlation 2 (no compiled table), SrTiO3 2^3", flush=True)
+    _check(oracle_lib, _write(tmp_path, "corr2", model), model, s)
