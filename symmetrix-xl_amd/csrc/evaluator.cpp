@@ -1002,6 +1002,56 @@ double Evaluator::max_displacement(std::uint64_t generation, const double* posit
     return std::sqrt(d2);
 }
 
+// H1 = M0 H1_W per l block (or, reverse, M0_adj = H1_adj H1_W^T) for
+// `nodes` consecutive nodes, one grouped launch.
+void Evaluator::gemm_h1(int nodes, const float* in, long long in_stride, float* out, long long out_stride,
+                        bool reverse, const char* what)
+{
+    GemmGroup grp;
+    for (int l = 0; l <= model_.L_max; ++l) {
+        GemmArgs& g = grp.g[grp.count++];
+        g.nodes = nodes;
+        g.rows_per_node = 2 * l + 1;
+        g.K = C_;
+        g.Ncols = C_;
+        g.a = {in + l * l * C_, in_stride, C_};
+        // Bt = W^T for H1 = M0 W, and W for M0_adj = H1_adj W^T
+        g.Bt = (reverse ? h1w_ : h1wt_).as<float>() + static_cast<std::size_t>(l) * C_ * C_;
+        g.c = {out + l * l * C_, out_stride, C_};
+    }
+    hip_check(launch_gemm_group(grp, stream_), what);
+}
+
+// A1[l] = Phi1[l group] A1_W[l] (or, reverse, dPhi1[l group] = A1_adj[l]
+// A1_W[l]^T) for `nodes` consecutive tile-local nodes, one grouped launch.
+void Evaluator::gemm_a1(int nodes, const float* in, float* out, bool reverse, const char* what)
+{
+    const long long nodelm = static_cast<long long>(nlm_) * C_;
+    const long long nodelme = static_cast<long long>(nlme_) * C_;
+    GemmGroup grp;
+    for (int l = 0; l <= model_.l_max; ++l) {
+        if (num_e_[l] == 0) continue;
+        GemmArgs& g = grp.g[grp.count++];
+        const long long phi_row = static_cast<long long>(num_e_[l]) * C_;
+        g.nodes = nodes;
+        g.rows_per_node = 2 * l + 1;
+        if (!reverse) {
+            g.K = num_e_[l] * C_;
+            g.Ncols = C_;
+            g.a = {in + static_cast<long long>(lme_off_[l]) * C_, nodelme, phi_row};
+            g.Bt = a1wt_[l]->as<float>();
+            g.c = {out + l * l * C_, nodelm, C_};
+        } else {
+            g.K = C_;
+            g.Ncols = num_e_[l] * C_;
+            g.a = {in + l * l * C_, nodelm, C_};
+            g.Bt = a1w_[l]->as<float>();
+            g.c = {out + static_cast<long long>(lme_off_[l]) * C_, nodelme, phi_row};
+        }
+    }
+    hip_check(launch_gemm_group(grp, stream_), what);
+}
+
 void Evaluator::evaluate()
 {
     if (tile_receivers_ > 0) {
@@ -1035,8 +1085,6 @@ void Evaluator::evaluate()
     const PolyArgs p0 = poly_args(p0_layout_, p0_coef_, p0_offsets_, p0_packed_);
     const PolyArgs p1 = poly_args(p1_layout_, p1_coef_, p1_offsets_, p1_packed_);
     const long long nodeLM = static_cast<long long>(nLM_) * C_;
-    const long long nodelm = static_cast<long long>(nlm_) * C_;
-    const long long nodelme = static_cast<long long>(nlme_) * C_;
 
     if (E > 0 || N > 0) {
         // layer 0: A0 (folded H0, A0_W), M0, H1
@@ -1049,17 +1097,7 @@ void Evaluator::evaluate()
                   "M0 forward");
         mark(kStageM0Forward, true);
         mark(kStageH1Gemm, false);
-        for (int l = 0; l <= model_.L_max; ++l) {
-            GemmArgs g;
-            g.nodes = N;
-            g.rows_per_node = 2 * l + 1;
-            g.K = C_;
-            g.Ncols = C_;
-            g.a = {M0_.as<float>() + l * l * C_, nodeLM, C_};
-            g.B = h1w_.as<float>() + static_cast<std::size_t>(l) * C_ * C_;
-            g.c = {H1_.as<float>() + l * l * C_, nodeLM, C_};
-            hip_check(launch_gemm(g, s), "H1 gemm");
-        }
+        gemm_h1(N, M0_.as<float>(), nodeLM, H1_.as<float>(), nodeLM, false, "H1 gemm");
         mark(kStageH1Gemm, true);
         // layer 1: Phi1 -> A1
         mark(kStageR1Forward, false);
@@ -1067,18 +1105,7 @@ void Evaluator::evaluate()
                   "R1 forward");
         mark(kStageR1Forward, true);
         mark(kStageA1Gemm, false);
-        for (int l = 0; l <= model_.l_max; ++l) {
-            GemmArgs g;
-            g.nodes = N;
-            g.rows_per_node = 2 * l + 1;
-            g.K = num_e_[l] * C_;
-            g.Ncols = C_;
-            g.a = {Phi1_.as<float>() + static_cast<long long>(lme_off_[l]) * C_, nodelme,
-                   static_cast<long long>(num_e_[l]) * C_};
-            g.B = a1w_[l]->as<float>();
-            g.c = {A1_.as<float>() + l * l * C_, nodelm, C_};
-            if (num_e_[l] > 0) hip_check(launch_gemm(g, s), "A1 gemm");
-        }
+        gemm_a1(N, Phi1_.as<float>(), A1_.as<float>(), false, "A1 gemm");
         mark(kStageA1Gemm, true);
         // readout and its reverse down to A1_adj
         ReadoutArgs ra;
@@ -1112,18 +1139,7 @@ void Evaluator::evaluate()
         mark(kStageA1ReverseGemm, false);
         // dPhi1 = A1_adj A1_W^T  (into the Phi1 buffer, no longer needed)
         float* dPhi1 = Phi1_.as<float>();
-        for (int l = 0; l <= model_.l_max; ++l) {
-            if (num_e_[l] == 0) continue;
-            GemmArgs g;
-            g.nodes = N;
-            g.rows_per_node = 2 * l + 1;
-            g.K = C_;
-            g.Ncols = num_e_[l] * C_;
-            g.a = {A1adj_.as<float>() + l * l * C_, nodelm, C_};
-            g.B = a1wt_[l]->as<float>();
-            g.c = {dPhi1 + static_cast<long long>(lme_off_[l]) * C_, nodelme, static_cast<long long>(num_e_[l]) * C_};
-            hip_check(launch_gemm(g, s), "A1 reverse gemm");
-        }
+        gemm_a1(N, A1adj_.as<float>(), dPhi1, true, "A1 reverse gemm");
         mark(kStageA1ReverseGemm, true);
         mark(kStageR1Reverse, false);
         hip_check(launch_r1_reverse(la, r1_.as<float>(), cg_.as<float>(), H1_.as<float>(), dPhi1,
@@ -1136,17 +1152,7 @@ void Evaluator::evaluate()
         mark(kStageH1ReverseGemm, false);
         // M0_adj = H1_adj H1_W^T (+ direct scalar adjoint), into the M0 buffer
         float* M0adj = M0_.as<float>();
-        for (int l = 0; l <= model_.L_max; ++l) {
-            GemmArgs g;
-            g.nodes = N;
-            g.rows_per_node = 2 * l + 1;
-            g.K = C_;
-            g.Ncols = C_;
-            g.a = {H1adj_.as<float>() + l * l * C_, nodeLM, C_};
-            g.B = h1wt_.as<float>() + static_cast<std::size_t>(l) * C_ * C_;
-            g.c = {M0adj + l * l * C_, nodeLM, C_};
-            hip_check(launch_gemm(g, s), "H1 reverse gemm");
-        }
+        gemm_h1(N, H1adj_.as<float>(), nodeLM, M0adj, nodeLM, true, "H1 reverse gemm");
         hip_check(launch_add_direct(N, C_, nLM_, direct_.as<float>(), M0adj, s), "direct adjoint");
         mark(kStageH1ReverseGemm, true);
         // A0_adj into the A1 buffer (no longer needed)
@@ -1221,27 +1227,11 @@ void Evaluator::evaluate_tiled()
     const PolyArgs p0 = poly_args(p0_layout_, p0_coef_, p0_offsets_, p0_packed_);
     const PolyArgs p1 = poly_args(p1_layout_, p1_coef_, p1_offsets_, p1_packed_);
     const long long nodeLM = static_cast<long long>(nLM_) * C_;
-    const long long nodelm = static_cast<long long>(nlm_) * C_;
-    const long long nodelme = static_cast<long long>(nlme_) * C_;
     auto tile = [&](int t) {
         la.node_offset = t * T;
         la.node_count = std::min(T, N - t * T);
         la.local_base = la.node_offset;
         la.edge_base = tile_first_edge_[t];
-    };
-    auto h1_gemms = [&](const float* in, long long in_stride, const float* W, float* out, long long out_stride,
-                        const char* what) {
-        for (int l = 0; l <= model_.L_max; ++l) {
-            GemmArgs g;
-            g.nodes = la.node_count;
-            g.rows_per_node = 2 * l + 1;
-            g.K = C_;
-            g.Ncols = C_;
-            g.a = {in + l * l * C_, in_stride, C_};
-            g.B = W + static_cast<std::size_t>(l) * C_ * C_;
-            g.c = {out + l * l * C_, out_stride, C_};
-            hip_check(launch_gemm(g, s), what);
-        }
     };
     float* H1 = H1_.as<float>();
     float* H1adj = H1adj_.as<float>();
@@ -1254,7 +1244,7 @@ void Evaluator::evaluate_tiled()
         hip_check(launch_m0_forward(la, p0, node_blocks(m0_blocks_, m0_block_offsets_, t), A0_.as<float>(),
                                     M0_.as<float>(), s),
                   "M0 forward");
-        h1_gemms(M0_.as<float>(), nodeLM, h1w_.as<float>(), H1 + la.node_offset * nodeLM, nodeLM, "H1 gemm");
+        gemm_h1(la.node_count, M0_.as<float>(), nodeLM, H1 + la.node_offset * nodeLM, nodeLM, false, "H1 gemm");
         hip_check(hipMemcpy2DAsync(M0s + static_cast<std::size_t>(la.node_offset) * C_, C_ * sizeof(float),
                                    M0_.as<float>(), nodeLM * sizeof(float), C_ * sizeof(float), la.node_count,
                                    hipMemcpyDeviceToDevice, s),
@@ -1288,34 +1278,11 @@ void Evaluator::evaluate_tiled()
     for (int t = 0; t < num_tiles_; ++t) {
         tile(t);
         hip_check(launch_r1_forward(la, r1_.as<float>(), cg_.as<float>(), H1, Phi1_.as<float>(), s), "R1 forward");
-        for (int l = 0; l <= model_.l_max; ++l) {
-            if (num_e_[l] == 0) continue;
-            GemmArgs g;
-            g.nodes = la.node_count;
-            g.rows_per_node = 2 * l + 1;
-            g.K = num_e_[l] * C_;
-            g.Ncols = C_;
-            g.a = {Phi1_.as<float>() + static_cast<long long>(lme_off_[l]) * C_, nodelme,
-                   static_cast<long long>(num_e_[l]) * C_};
-            g.B = a1w_[l]->as<float>();
-            g.c = {A1_.as<float>() + l * l * C_, nodelm, C_};
-            hip_check(launch_gemm(g, s), "A1 gemm");
-        }
+        gemm_a1(la.node_count, Phi1_.as<float>(), A1_.as<float>(), false, "A1 gemm");
         ra.nodes = node_blocks(readout_blocks_, readout_block_offsets_, t);
         ra.local_base = la.local_base;
         hip_check(launch_readout(ra, s), "readout");
-        for (int l = 0; l <= model_.l_max; ++l) {
-            if (num_e_[l] == 0) continue;
-            GemmArgs g;
-            g.nodes = la.node_count;
-            g.rows_per_node = 2 * l + 1;
-            g.K = C_;
-            g.Ncols = num_e_[l] * C_;
-            g.a = {A1adj_.as<float>() + l * l * C_, nodelm, C_};
-            g.B = a1wt_[l]->as<float>();
-            g.c = {dPhi1 + static_cast<long long>(lme_off_[l]) * C_, nodelme, static_cast<long long>(num_e_[l]) * C_};
-            hip_check(launch_gemm(g, s), "A1 reverse gemm");
-        }
+        gemm_a1(la.node_count, A1adj_.as<float>(), dPhi1, true, "A1 reverse gemm");
         hip_check(launch_r1_reverse(la, r1_.as<float>(), cg_.as<float>(), H1, dPhi1, forces_.as<double>(),
                                     msg_.as<float>(), s),
                   "R1 reverse");
@@ -1331,7 +1298,7 @@ void Evaluator::evaluate_tiled()
     float* A0adj = A1_.as<float>();
     for (int t = 0; t < num_tiles_; ++t) {
         tile(t);
-        h1_gemms(H1adj + la.node_offset * nodeLM, nodeLM, h1wt_.as<float>(), M0adj, nodeLM, "H1 reverse gemm");
+        gemm_h1(la.node_count, H1adj + la.node_offset * nodeLM, nodeLM, M0adj, nodeLM, true, "H1 reverse gemm");
         hip_check(launch_add_direct(la.node_count, C_, nLM_, direct_.as<float>() + static_cast<std::size_t>(la.node_offset) * C_,
                                     M0adj, s),
                   "direct adjoint");

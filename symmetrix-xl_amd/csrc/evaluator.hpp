@@ -183,6 +183,9 @@ private:
     void invalidate_graph();
     void evaluate();
     void evaluate_tiled();
+    void gemm_h1(int nodes, const float* in, long long in_stride, float* out, long long out_stride, bool reverse,
+                 const char* what);
+    void gemm_a1(int nodes, const float* in, float* out, bool reverse, const char* what);
     void reduce(double volume);
 
     HostModel model_;

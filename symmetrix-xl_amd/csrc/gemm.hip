@@ -1,0 +1,146 @@
+// gfx950 FP32 MFMA GEMMs of the node linears: H1 = M0 H1_W, A1 = Phi1 A1_W
+// and their adjoints (reference mace.cpp:1690-1724, 2304-2340, 1664-1688,
+// 2380-2458; the reference calls CBLAS / Kokkos batched GEMM for these).
+//
+// All irrep blocks of one stage run in one launch (a group of up to
+// kMaxGemmGroup GEMMs, tiles numbered consecutively across the group).  A
+// 256-thread workgroup computes a 64 x 128 output tile with four waves of
+// v_mfma_f32_32x32x2f32 (each wave 32 x 64: two 32 x 32 blocks).  K is staged
+// through LDS in slices of 32, the next slice's global loads in flight while
+// the current one is multiplied.  Both operands are stored K-contiguous (the
+// weight matrix is passed transposed, Bt[n][k]) so one ds_read_b128 feeds four
+// MFMAs: lane half h supplies k = 8c + 4h + q to MFMA q of chunk c, the same
+// k for both operands, which sums every k of the chunk exactly once.
+#include <hip/hip_runtime.h>
+
+#include "kernels.hpp"
+
+namespace sxl {
+namespace {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int kBM = 64, kBN = 128, kBK = 32, kPad = 4;
+
+__global__ void __launch_bounds__(256) gemm_group_kernel(GemmGroup grp)
+{
+    __shared__ float As[kBM][kBK + kPad];
+    __shared__ float Bs[kBN][kBK + kPad];
+    const int b = blockIdx.x;
+    int item = 0;
+    while (item + 1 < grp.count && b >= grp.tile_start[item + 1]) ++item;
+    const GemmArgs& g = grp.g[item];
+    const int M = g.nodes * g.rows_per_node;
+    const int K = g.K, N = g.Ncols;
+    const int local = b - grp.tile_start[item];
+    const int tiles_m = (M + kBM - 1) / kBM;
+    const int row0 = (local % tiles_m) * kBM;
+    const int col0 = (local / tiles_m) * kBN;
+    const int t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+
+    // global -> register staging: A 64 x 32 (2 float4 per thread), Bt 128 x 32 (4 float4)
+    const int lr = t >> 3, lk = (t & 7) * 4;
+    const float* arow[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int r = row0 + lr + 32 * j;
+        arow[j] = nullptr;
+        if (r < M) {
+            const int node = r / g.rows_per_node;
+            const int m = r - node * g.rows_per_node;
+            arow[j] = g.a.ptr + node * g.a.node_stride + m * g.a.row_stride + lk;
+        }
+    }
+    const float* brow[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int n = col0 + lr + 32 * j;
+        brow[j] = n < N ? g.Bt + static_cast<size_t>(n) * K + lk : nullptr;
+    }
+    float4 ra[2], rb[4];
+    auto fetch = [&](int k0) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            ra[j] = arow[j] ? *reinterpret_cast<const float4*>(arow[j] + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            rb[j] = brow[j] ? *reinterpret_cast<const float4*>(brow[j] + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+    };
+
+    floatx16 acc[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[j][v] = 0.0f;
+
+    fetch(0);
+    const int arow_l = wm * 32 + (lane & 31);
+    const int kh = 4 * (lane >> 5);
+    for (int k0 = 0; k0 < K; k0 += kBK) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) *reinterpret_cast<float4*>(&As[lr + 32 * j][lk]) = ra[j];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) *reinterpret_cast<float4*>(&Bs[lr + 32 * j][lk]) = rb[j];
+        __syncthreads();
+        if (k0 + kBK < K) fetch(k0 + kBK);
+#pragma unroll
+        for (int c = 0; c < kBK; c += 8) {
+            const float4 a4 = *reinterpret_cast<const float4*>(&As[arow_l][c + kh]);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const float4 b4 = *reinterpret_cast<const float4*>(&Bs[wn * 64 + j * 32 + (lane & 31)][c + kh]);
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.x, b4.x, acc[j], 0, 0, 0);
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.y, b4.y, acc[j], 0, 0, 0);
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.z, b4.z, acc[j], 0, 0, 0);
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.w, b4.w, acc[j], 0, 0, 0);
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int col = col0 + wn * 64 + j * 32 + (lane & 31);
+        if (col >= N) continue;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int row = row0 + wm * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+            if (row < M) {
+                const int node = row / g.rows_per_node;
+                const int m = row - node * g.rows_per_node;
+                g.c.ptr[node * g.c.node_stride + m * g.c.row_stride + col] = acc[j][v];
+            }
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_gemm_group(GemmGroup grp, hipStream_t stream)
+{
+    if (grp.count < 0 || grp.count > kMaxGemmGroup) return hipErrorInvalidValue;
+    int tiles = 0;
+    int kept = 0;
+    for (int i = 0; i < grp.count; ++i) {
+        const GemmArgs& g = grp.g[i];
+        const long long M = static_cast<long long>(g.nodes) * g.rows_per_node;
+        if (M <= 0 || g.Ncols <= 0 || g.K <= 0) continue;
+        if (g.K % kBK != 0 || M > 0x7fffffff) return hipErrorInvalidValue;
+        // float4 loads: row strides and bases must keep 16-byte alignment
+        if (g.a.node_stride % 4 != 0 || g.a.row_stride % 4 != 0 ||
+            reinterpret_cast<std::uintptr_t>(g.a.ptr) % 16 != 0 || reinterpret_cast<std::uintptr_t>(g.Bt) % 16 != 0)
+            return hipErrorInvalidValue;
+        grp.g[kept] = g;
+        grp.tile_start[kept] = tiles;
+        tiles += static_cast<int>(((M + kBM - 1) / kBM) * ((g.Ncols + kBN - 1) / kBN));
+        ++kept;
+    }
+    grp.count = kept;
+    grp.tile_start[kept] = tiles;
+    if (tiles == 0) return hipSuccess;
+    gemm_group_kernel<<<tiles, 256, 0, stream>>>(grp);
+    return hipGetLastError();
+}
+
+}  // namespace sxl

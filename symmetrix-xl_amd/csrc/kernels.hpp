@@ -89,18 +89,27 @@ struct GemmOut {
     long long row_stride = 0;
 };
 
-// out(node, m) = in(node, m) @ B (K x Ncols row-major)
+// out(node, m)[n] = sum_k in(node, m)[k] Bt[n][k]   (Bt: Ncols x K row-major,
+// i.e. the right-hand matrix transposed, so both operands are K-contiguous)
 struct GemmArgs {
     int nodes = 0;
     int rows_per_node = 0;
-    int K = 0;
+    int K = 0;      // multiple of 32
     int Ncols = 0;
     GemmRows a;
-    const float* B = nullptr;
+    const float* Bt = nullptr;
     GemmOut c;
 };
 
-hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream);
+// Up to kMaxGemmGroup independent GEMMs (the irrep blocks of one stage) in
+// one launch; tile_start is filled by the launcher.
+constexpr int kMaxGemmGroup = 9;
+struct GemmGroup {
+    int count = 0;
+    GemmArgs g[kMaxGemmGroup];
+    int tile_start[kMaxGemmGroup + 1] = {};
+};
+hipError_t launch_gemm_group(GemmGroup group, hipStream_t stream);
 
 struct LayerArgs {
     EdgeGraph graph;

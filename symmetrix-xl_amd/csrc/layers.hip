@@ -628,76 +628,6 @@ __global__ void add_direct_kernel(int nodes, int C, int nLM, const float* __rest
 }
 
 // ---------------------------------------------------------------------------
-// fp32 MFMA GEMM over per-node row blocks.  64x64 output tile per 256-thread
-// workgroup, 2x2 waves of v_mfma_f32_32x32x2f32, K staged through LDS in
-// chunks of 32.  Requires K % 32 == 0.
-// ---------------------------------------------------------------------------
-typedef float floatx16 __attribute__((ext_vector_type(16)));
-
-__global__ void __launch_bounds__(256) gemm_kernel(GemmArgs g)
-{
-    constexpr int BM = 64, BN = 64, BK = 32;
-    __shared__ float As[BM][BK + 1];
-    __shared__ float Bs[BK][BN + 1];
-    const int M = g.nodes * g.rows_per_node;
-    const int row0 = blockIdx.x * BM;
-    const int col0 = blockIdx.y * BN;
-    const int t = threadIdx.x;
-    const int lane = t & 63;
-    const int wave = t >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int lr = t >> 2, lc = (t & 3) * 8;
-    const int arow_index = row0 + lr;
-    const float* arow = nullptr;
-    if (arow_index < M) {
-        const int node = arow_index / g.rows_per_node;
-        const int m = arow_index - node * g.rows_per_node;
-        arow = g.a.ptr + node * g.a.node_stride + m * g.a.row_stride;
-    }
-    const int br = t >> 3, bc = (t & 7) * 8;
-    floatx16 acc;
-#pragma unroll
-    for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
-    for (int k0 = 0; k0 < g.K; k0 += BK) {
-        if (arow) {
-            const float4 v0 = *reinterpret_cast<const float4*>(arow + k0 + lc);
-            const float4 v1 = *reinterpret_cast<const float4*>(arow + k0 + lc + 4);
-            As[lr][lc + 0] = v0.x, As[lr][lc + 1] = v0.y, As[lr][lc + 2] = v0.z, As[lr][lc + 3] = v0.w;
-            As[lr][lc + 4] = v1.x, As[lr][lc + 5] = v1.y, As[lr][lc + 6] = v1.z, As[lr][lc + 7] = v1.w;
-        } else {
-#pragma unroll
-            for (int q = 0; q < 8; ++q) As[lr][lc + q] = 0.0f;
-        }
-        const float* brow = g.B + static_cast<size_t>(k0 + br) * g.Ncols;
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const int col = col0 + bc + q;
-            Bs[br][bc + q] = col < g.Ncols ? brow[col] : 0.0f;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int kk = 0; kk < BK; kk += 2) {
-            const float av = As[wm * 32 + (lane & 31)][kk + (lane >> 5)];
-            const float bv = Bs[kk + (lane >> 5)][wn * 32 + (lane & 31)];
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc, 0, 0, 0);
-        }
-        __syncthreads();
-    }
-    const int col = col0 + wn * 32 + (lane & 31);
-    if (col >= g.Ncols) return;
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-        const int row = row0 + wm * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-        if (row < M) {
-            const int node = row / g.rows_per_node;
-            const int m = row - node * g.rows_per_node;
-            float* out = g.c.ptr + node * g.c.node_stride + m * g.c.row_stride;
-            out[col] = acc[v];
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
 // geometry and reductions
 // ---------------------------------------------------------------------------
 __global__ void edge_geometry_kernel(int E, const int* __restrict__ receiver,
@@ -809,16 +739,6 @@ inline int node_threads(int C) { return ((C + 63) / 64) * 64; }
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
-hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream)
-{
-    const int M = g.nodes * g.rows_per_node;
-    if (M <= 0 || g.Ncols <= 0) return hipSuccess;
-    if (g.K % 32 != 0) return hipErrorInvalidValue;
-    dim3 grid((M + 63) / 64, (g.Ncols + 63) / 64);
-    gemm_kernel<<<grid, 256, 0, stream>>>(g);
-    return hipGetLastError();
-}
-
 hipError_t launch_a0_forward(const LayerArgs& a, const float* r0f, float* A0, hipStream_t s)
 {
     if (a.node_count <= 0) return hipSuccess;
