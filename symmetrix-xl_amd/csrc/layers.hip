@@ -29,6 +29,9 @@ namespace {
 
 constexpr int kMaxWaves = 4;  // 256 threads
 
+// l of each harmonic index lm (lm = l^2 .. l^2 + 2l), l <= 3
+constexpr int kLmL[16] = {0, 1, 1, 1, 2, 2, 2, 2, 2, 3, 3, 3, 3, 3, 3, 3};
+
 __device__ __forceinline__ int receiver_of_block(const LayerArgs& a)
 {
     return a.node_offset + xcd_contiguous(blockIdx.x, a.node_count);
@@ -43,6 +46,30 @@ __device__ __forceinline__ int receiver_of_block(const LayerArgs& a)
 // coefficient load costs no vector address arithmetic.
 // ---------------------------------------------------------------------------
 constexpr int kTile = 64;
+
+// Streams the active slots 0..count-1 of a tile through a ring of D row
+// buffers: the coefficient rows of the next D - 1 edges are in flight while
+// one edge is processed.  fetch(j, buf) issues the loads of slot j into buf,
+// use(j, buf) consumes them; all slot indices into the ring are compile-time.
+template <int D, class Buf, class Fetch, class Use>
+__device__ __forceinline__ void stream_ring(int count, Buf (&ring)[D], Fetch& fetch, Use& use)
+{
+#pragma unroll
+    for (int d = 0; d < D - 1; ++d)
+        if (d < count) fetch(d, ring[d]);
+    for (int j = 0; j < count; j += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            const int jj = j + d;
+            if (jj < count) {
+                if (jj + D - 1 < count) fetch(jj + D - 1, ring[(d + D - 1) % D]);
+                use(jj, ring[d]);
+            }
+        }
+    }
+}
+
+constexpr int kDepth = 4;  // edges in flight per wave in the layer-0 kernels
 
 struct TileSlot {
     bool active;
@@ -120,23 +147,14 @@ __global__ void __launch_bounds__(256) a0_forward_kernel(LayerArgs a, const floa
         };
         auto accumulate = [&](int j, const float4v* c) {
             const float x = uniform(s_x[j]);
+            float R[NL];
 #pragma unroll
-            for (int l = 0; l <= LMAX; ++l) {
-                const float R = cubic(c[l], x);
+            for (int l = 0; l < NL; ++l) R[l] = cubic(c[l], x);
 #pragma unroll
-                for (int lm = l * l; lm < (l + 1) * (l + 1); ++lm) acc[lm] = fmaf(R, s_Y[j][lm], acc[lm]);
-            }
+            for (int lm = 0; lm < NLM; ++lm) acc[lm] = fmaf(R[kLmL[lm]], s_Y[j][lm], acc[lm]);
         };
-        float4v ca[NL], cb[NL];
-        if (count > 0) fetch(0, ca);
-        for (int j = 0; j < count; j += 2) {
-            fetch(min(j + 1, count - 1), cb);
-            accumulate(j, ca);
-            if (j + 1 < count) {
-                fetch(min(j + 2, count - 1), ca);
-                accumulate(j + 1, cb);
-            }
-        }
+        float4v ring[kDepth][NL];
+        stream_ring<kDepth>(count, ring, fetch, accumulate);
     }
     if (k < C) {
         float* out = A0 + static_cast<size_t>(i - a.local_base) * NLM * C + k;
@@ -491,23 +509,25 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
         auto edge_force = [&](int j, const float4v* cl) {
             const float x = uniform(s_geo[j][3]);
             const float x3 = 3.0f * x;
+            float yl[NL], ax[NL], ay[NL], az[NL];
+#pragma unroll
+            for (int l = 0; l < NL; ++l) yl[l] = ax[l] = ay[l] = az[l] = 0.0f;
+#pragma unroll
+            for (int lm = 0; lm < NLM; ++lm) {
+                const int l = kLmL[lm];
+                yl[l] = fmaf(s_Y[j][lm], adj[lm], yl[l]);
+                ax[l] = fmaf(s_dY[j][0][lm], adj[lm], ax[l]);
+                ay[l] = fmaf(s_dY[j][1][lm], adj[lm], ay[l]);
+                az[l] = fmaf(s_dY[j][2][lm], adj[lm], az[l]);
+            }
             float A = 0.0f, gx = 0.0f, gy = 0.0f, gz = 0.0f;
 #pragma unroll
-            for (int l = 0; l <= LMAX; ++l) {
-                const float4v c = cl[l];
-                float yl = 0.0f, ax = 0.0f, ay = 0.0f, az = 0.0f;
-#pragma unroll
-                for (int lm = l * l; lm < (l + 1) * (l + 1); ++lm) {
-                    yl = fmaf(s_Y[j][lm], adj[lm], yl);
-                    ax = fmaf(s_dY[j][0][lm], adj[lm], ax);
-                    ay = fmaf(s_dY[j][1][lm], adj[lm], ay);
-                    az = fmaf(s_dY[j][2][lm], adj[lm], az);
-                }
-                const float R = cubic(c, x);
-                A = fmaf(cubic_slope(c, x, x3), yl, A);
-                gx = fmaf(R, ax, gx);
-                gy = fmaf(R, ay, gy);
-                gz = fmaf(R, az, gz);
+            for (int l = 0; l < NL; ++l) {
+                const float R = cubic(cl[l], x);
+                A = fmaf(cubic_slope(cl[l], x, x3), yl[l], A);
+                gx = fmaf(R, ax[l], gx);
+                gy = fmaf(R, ay[l], gy);
+                gz = fmaf(R, az[l], gz);
             }
             const float fx = wave_sum_dpp(-fmaf(s_geo[j][0], A, gx));
             const float fy = wave_sum_dpp(-fmaf(s_geo[j][1], A, gy));
@@ -518,16 +538,8 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
                 s_f[j][wave][2] = fz;
             }
         };
-        float4v ca[NL], cb[NL];
-        if (count > 0) fetch(0, ca);
-        for (int j = 0; j < count; j += 2) {
-            fetch(min(j + 1, count - 1), cb);
-            edge_force(j, ca);
-            if (j + 1 < count) {
-                fetch(min(j + 2, count - 1), ca);
-                edge_force(j + 1, cb);
-            }
-        }
+        float4v ring[kDepth][NL];
+        stream_ring<kDepth>(count, ring, fetch, edge_force);
         __syncthreads();
         if (threadIdx.x < count) {
             const int t = threadIdx.x;
