@@ -554,80 +554,96 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
     }
 }
 
-// H1_adj[s, lm2, k] = sum over edges e with source s (ascending e) of msg[e, lm2, k]
-template <int NLMS>
-__global__ void __launch_bounds__(256) gather_messages_kernel(LayerArgs a,
-                                                              const float* __restrict__ msg,
+// H1 adjoint gather.  A message row (num_LM x C floats) is read as float4s,
+// the block's threads covering the whole row, with the rows of kGatherGroup
+// edges in flight.  Edges at or beyond r_cut carry no message (their rows are
+// not read); the sum runs over the edges in ascending edge order.
+constexpr int kGatherGroup = 8;
+
+// The message of edge e is row e - edge_base.
+template <int V>
+__device__ __forceinline__ void gather_range(const EdgeGraph& g, double r_cut, const float4* __restrict__ m4,
+                                             long long edge_base, int row4, int t0, int t1, float4 (&acc)[V])
+{
+    const int tid = threadIdx.x, T = blockDim.x;
+    for (int t = t0; t < t1; t += kGatherGroup) {
+        long long row[kGatherGroup];
+        bool on[kGatherGroup];
+#pragma unroll
+        for (int u = 0; u < kGatherGroup; ++u) {
+            const int tt = min(t + u, t1 - 1);
+            const int e = g.tedge[tt];
+            row[u] = e - edge_base;
+            on[u] = t + u < t1 && g.r[e] < r_cut;
+        }
+        float4 v[kGatherGroup][V];
+#pragma unroll
+        for (int u = 0; u < kGatherGroup; ++u)
+#pragma unroll
+            for (int q = 0; q < V; ++q) {
+                const int c = tid + q * T;
+                v[u][q] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (on[u] && c < row4) v[u][q] = m4[row[u] * row4 + c];
+            }
+#pragma unroll
+        for (int u = 0; u < kGatherGroup; ++u)
+#pragma unroll
+            for (int q = 0; q < V; ++q) {
+                acc[q].x += v[u][q].x;
+                acc[q].y += v[u][q].y;
+                acc[q].z += v[u][q].z;
+                acc[q].w += v[u][q].w;
+            }
+    }
+}
+
+// H1_adj[s] = sum over the edges e with source s (ascending e) of msg[e]
+template <int V>
+__global__ void __launch_bounds__(256) gather_messages_kernel(LayerArgs a, int row4, const float* __restrict__ msg,
                                                               float* __restrict__ H1_adj)
 {
     const int s = a.node_offset + xcd_contiguous(blockIdx.x, a.node_count);
-    const int k = threadIdx.x;
-    const int C = a.C;
-    if (k >= C) return;
-    const EdgeGraph& g = a.graph;
-    float acc[NLMS];
+    float4 acc[V];
 #pragma unroll
-    for (int q = 0; q < NLMS; ++q) acc[q] = 0.0f;
-    const int t0 = g.tfirst[s], t1 = g.tfirst[s + 1];
-    const size_t row = static_cast<size_t>(NLMS) * C;
-    int t = t0;
-    // edges in groups of four: all loads of a group are issued before the adds
-    for (; t + 4 <= t1; t += 4) {
-        float v[4][NLMS];
+    for (int q = 0; q < V; ++q) acc[q] = make_float4(0.f, 0.f, 0.f, 0.f);
+    gather_range<V>(a.graph, a.grid.r_cut, reinterpret_cast<const float4*>(msg), 0, row4, a.graph.tfirst[s],
+                          a.graph.tfirst[s + 1], acc);
+    float4* out = reinterpret_cast<float4*>(H1_adj) + static_cast<size_t>(s) * row4;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int e = g.tedge[t + u];
-            const bool on = g.r[e] < a.grid.r_cut;
-            const float* m = msg + e * row + k;
-#pragma unroll
-            for (int q = 0; q < NLMS; ++q) v[u][q] = on ? m[q * C] : 0.0f;
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-#pragma unroll
-            for (int q = 0; q < NLMS; ++q) acc[q] += v[u][q];
+    for (int q = 0; q < V; ++q) {
+        const int c = threadIdx.x + q * blockDim.x;
+        if (c < row4) out[c] = acc[q];
     }
-    for (; t < t1; ++t) {
-        const int e = g.tedge[t];
-        if (!(g.r[e] < a.grid.r_cut)) continue;
-        const float* m = msg + e * row + k;
-#pragma unroll
-        for (int q = 0; q < NLMS; ++q) acc[q] += m[q * C];
-    }
-    float* out = H1_adj + static_cast<size_t>(s) * NLMS * C + k;
-#pragma unroll
-    for (int q = 0; q < NLMS; ++q) out[q * C] = acc[q];
 }
 
 // Tiled execution: H1_adj[s] += sum over the run's edges (ascending) of
 // msg[e - edge_base]; one workgroup per run of the tile, runs of one tile have
 // distinct sources.
-template <int NLMS>
-__global__ void __launch_bounds__(256) gather_tile_runs_kernel(LayerArgs a, TileRuns runs,
+template <int V>
+__global__ void __launch_bounds__(256) gather_tile_runs_kernel(LayerArgs a, TileRuns runs, int row4,
                                                                const float* __restrict__ msg,
                                                                float* __restrict__ H1_adj)
 {
     const int run = blockIdx.x;
-    const int k = threadIdx.x;
-    const int C = a.C;
-    if (k >= C) return;
-    const EdgeGraph& g = a.graph;
-    const int src = runs.source[run];
-    const int t0 = runs.start[run], t1 = t0 + runs.length[run];
-    const size_t row = static_cast<size_t>(NLMS) * C;
-    float acc[NLMS];
+    const int t0 = runs.start[run];
+    float4 acc[V];
 #pragma unroll
-    for (int q = 0; q < NLMS; ++q) acc[q] = 0.0f;
-    for (int t = t0; t < t1; ++t) {
-        const int e = g.tedge[t];
-        if (!(g.r[e] < a.grid.r_cut)) continue;
-        const float* m = msg + static_cast<size_t>(e - a.edge_base) * row + k;
+    for (int q = 0; q < V; ++q) acc[q] = make_float4(0.f, 0.f, 0.f, 0.f);
+    gather_range<V>(a.graph, a.grid.r_cut, reinterpret_cast<const float4*>(msg), a.edge_base, row4, t0,
+                           t0 + runs.length[run], acc);
+    float4* out = reinterpret_cast<float4*>(H1_adj) + static_cast<size_t>(runs.source[run]) * row4;
 #pragma unroll
-        for (int q = 0; q < NLMS; ++q) acc[q] += m[q * C];
+    for (int q = 0; q < V; ++q) {
+        const int c = threadIdx.x + q * blockDim.x;
+        if (c < row4) {
+            float4 o = out[c];
+            o.x += acc[q].x;
+            o.y += acc[q].y;
+            o.z += acc[q].z;
+            o.w += acc[q].w;
+            out[c] = o;
+        }
     }
-    float* out = H1_adj + static_cast<size_t>(src) * row + k;
-#pragma unroll
-    for (int q = 0; q < NLMS; ++q) out[q * C] += acc[q];
 }
 
 __global__ void add_direct_kernel(int nodes, int C, int nLM, const float* __restrict__ direct,
@@ -812,14 +828,26 @@ hipError_t launch_r1_reverse(const LayerArgs& a, const float* r1, const float* c
     return hipGetLastError();
 }
 
+// threads and float4s per thread covering one message row of num_LM x C floats
+static void gather_shape(const LayerArgs& a, int& row4, int& threads, int& per_thread)
+{
+    const int nLM = (a.L_max + 1) * (a.L_max + 1);
+    row4 = nLM * a.C / 4;
+    threads = std::min(256, ((row4 + 63) / 64) * 64);
+    per_thread = (row4 + threads - 1) / threads;
+}
+
 hipError_t launch_gather_messages(const LayerArgs& a, const float* msg, float* H1_adj, hipStream_t s)
 {
     if (a.node_count <= 0) return hipSuccess;
-    const dim3 grid(a.node_count), block(node_threads(a.C));
-    switch (a.L_max) {
-    case 1: gather_messages_kernel<4><<<grid, block, 0, s>>>(a, msg, H1_adj); break;
-    case 2: gather_messages_kernel<9><<<grid, block, 0, s>>>(a, msg, H1_adj); break;
-    default: gather_messages_kernel<1><<<grid, block, 0, s>>>(a, msg, H1_adj); break;
+    if (a.C % 4 != 0) return hipErrorInvalidValue;
+    int row4, threads, v;
+    gather_shape(a, row4, threads, v);
+    switch (v) {
+    case 1: gather_messages_kernel<1><<<a.node_count, threads, 0, s>>>(a, row4, msg, H1_adj); break;
+    case 2: gather_messages_kernel<2><<<a.node_count, threads, 0, s>>>(a, row4, msg, H1_adj); break;
+    case 3: gather_messages_kernel<3><<<a.node_count, threads, 0, s>>>(a, row4, msg, H1_adj); break;
+    default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
@@ -828,11 +856,14 @@ hipError_t launch_gather_tile_runs(const LayerArgs& a, const TileRuns& runs, con
                                    float* H1_adj, hipStream_t s)
 {
     if (runs.count <= 0) return hipSuccess;
-    const dim3 grid(runs.count), block(node_threads(a.C));
-    switch (a.L_max) {
-    case 1: gather_tile_runs_kernel<4><<<grid, block, 0, s>>>(a, runs, msg, H1_adj); break;
-    case 2: gather_tile_runs_kernel<9><<<grid, block, 0, s>>>(a, runs, msg, H1_adj); break;
-    default: gather_tile_runs_kernel<1><<<grid, block, 0, s>>>(a, runs, msg, H1_adj); break;
+    if (a.C % 4 != 0) return hipErrorInvalidValue;
+    int row4, threads, v;
+    gather_shape(a, row4, threads, v);
+    switch (v) {
+    case 1: gather_tile_runs_kernel<1><<<runs.count, threads, 0, s>>>(a, runs, row4, msg, H1_adj); break;
+    case 2: gather_tile_runs_kernel<2><<<runs.count, threads, 0, s>>>(a, runs, row4, msg, H1_adj); break;
+    case 3: gather_tile_runs_kernel<3><<<runs.count, threads, 0, s>>>(a, runs, row4, msg, H1_adj); break;
+    default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
