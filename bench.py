@@ -32,8 +32,10 @@ for p in (os.path.join(ROOT, "symmetrix-xl_amd"), ROOT):
 
 METRIC = "µs/atom per E+F+stress call (FP32, 1 MI355X) at 5k atoms; max atoms tiled"
 PUBLISHED_US_PER_ATOM = 1.922  # reference, RTX 5090, 5,000-atom SrTiO3
-FP32_PEAK_TFLOPS = 157.3
+FP32_PEAK_TFLOPS = 157.3       # MI355X published FP32 (vector with packed FP32, and matrix)
+FP32_NONPACKED_TFLOPS = 78.6   # one FMA per lane per cycle: the ceiling of non-packed FP32 VALU code
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "medium_5k_hbm_traffic.md")
 
 
 class HipMemory:
@@ -139,6 +141,22 @@ def polynomial_degree_sum(lmax, out_lmax, correlation=3):
     return total
 
 
+def committed_traffic(kernel):
+    """HBM bytes per launch of `kernel` on the default workload, from the
+    committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (copy-calibrated), or
+    None when the summary is absent."""
+    try:
+        text = open(TRAFFIC_PROFILE).read()
+    except OSError:
+        return None
+    block = text.split("```json", 1)[-1].split("```", 1)[0]
+    try:
+        table = json.loads(block)["bytes_per_launch"]
+    except (ValueError, KeyError):
+        return None
+    return table.get(f"{kernel}_kernel")
+
+
 def cpu_baseline(model_path, structure, cutoff, threads, calls):
     from oracle import oracle
     from symmetrix_amd import synthetic
@@ -162,7 +180,12 @@ def cpu_baseline(model_path, structure, cutoff, threads, calls):
         t0 = time.perf_counter()
         call()
         times.append(time.perf_counter() - t0)
-    return statistics.median(times) / len(structure) * 1e6, times
+    t0 = time.perf_counter()
+    e, f = orc.compute(gi["node_types"], gi["num_neigh"], gi["neigh_indices"], gi["neigh_types"],
+                       gi["xyz"], gi["r"], 1)
+    oracle.reduce(gi["num_neigh"], gi["neigh_indices"], f, gi["xyz"], volume)
+    single = time.perf_counter() - t0
+    return statistics.median(times) / len(structure) * 1e6, times, single / len(structure) * 1e6
 
 
 # atomic masses (amu) of the SrTiO3 elements for the NVE run
@@ -269,7 +292,7 @@ def main():
     ap.add_argument("--sigma", type=float, default=0.05)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--skin", type=float, default=0.5)
-    ap.add_argument("--cpu-calls", type=int, default=2, help="timed oracle calls for cpu_baseline (0: skip)")
+    ap.add_argument("--cpu-calls", type=int, default=20, help="timed oracle calls for cpu_baseline (0: skip)")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--host-steps", type=int, default=5, help="host-boundary calculator steps (0: skip)")
     ap.add_argument("--capacity-cells", type=int, default=0, metavar="N",
@@ -370,13 +393,18 @@ def main():
     dominant = max(stage_avg, key=stage_avg.get)
     avg_ms = stage_avg[dominant]
     achieved = flops.get(dominant, 0.0) / (avg_ms * 1e-3) / 1e12 if avg_ms > 0 else 0.0
+    default_workload = (args.preset, args.cells, args.sigma, args.seed, args.skin) == ("medium", 10, 0.05, 0, 0.5)
+    traffic = committed_traffic(dominant) if default_workload else None
     roofline = {
         "bound": "mfma",
         "achieved": round(achieved, 3),
         "peak": FP32_PEAK_TFLOPS,
         "unit": "TFLOP/s",
         "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
-        "traffic": None,
+        "traffic": traffic,
+        "traffic_source": ("profiles/medium_5k_hbm_traffic.md: rocprofv3 FETCH_SIZE + WRITE_SIZE per launch, "
+                           "scaled by a 256 MiB copy" if traffic is not None else None),
+        "frac_of_nonpacked_fp32": round(achieved / FP32_NONPACKED_TFLOPS, 4),
         "kernel": dominant,
         "kernel_avg_ms": round(avg_ms, 4),
         "algorithmic_flops_per_launch": flops.get(dominant, 0.0),
@@ -399,7 +427,7 @@ def main():
     cpu = None
     if args.cpu_calls > 0:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
-        us, times = cpu_baseline(model_path, structure, cutoff, threads, args.cpu_calls)
+        us, times, us1 = cpu_baseline(model_path, structure, cutoff, threads, args.cpu_calls)
         cpu = {
             "value": round(us, 3),
             "unit": "us/atom",
@@ -407,7 +435,8 @@ def main():
             "kind": "port",
             "sample": f"full {N}-atom workload, 1 warmup + median of {args.cpu_calls} oracle calls "
                       f"(OpenMP restatement of the reference CPU path, compute + reductions, "
-                      f"neighbour list reused), {sum(times):.1f} s timed",
+                      f"neighbour list reused), {sum(times):.1f} s timed; one more call on 1 thread",
+            "single_thread_value": round(us1, 3),
         }
 
     line = {
