@@ -157,7 +157,7 @@ def committed_traffic(kernel):
     return table.get(f"{kernel}_kernel")
 
 
-def cpu_baseline(model_path, structure, cutoff, threads, calls):
+def cpu_baseline(model_path, structure, cutoff, threads, calls, single_thread=True):
     from oracle import oracle
     from symmetrix_amd import synthetic
 
@@ -180,12 +180,14 @@ def cpu_baseline(model_path, structure, cutoff, threads, calls):
         t0 = time.perf_counter()
         call()
         times.append(time.perf_counter() - t0)
-    t0 = time.perf_counter()
-    e, f = orc.compute(gi["node_types"], gi["num_neigh"], gi["neigh_indices"], gi["neigh_types"],
-                       gi["xyz"], gi["r"], 1)
-    oracle.reduce(gi["num_neigh"], gi["neigh_indices"], f, gi["xyz"], volume)
-    single = time.perf_counter() - t0
-    return statistics.median(times) / len(structure) * 1e6, times, single / len(structure) * 1e6
+    single = None
+    if single_thread:
+        t0 = time.perf_counter()
+        e, f = orc.compute(gi["node_types"], gi["num_neigh"], gi["neigh_indices"], gi["neigh_types"],
+                           gi["xyz"], gi["r"], 1)
+        oracle.reduce(gi["num_neigh"], gi["neigh_indices"], f, gi["xyz"], volume)
+        single = (time.perf_counter() - t0) / len(structure) * 1e6
+    return statistics.median(times) / len(structure) * 1e6, times, single
 
 
 # atomic masses (amu) of the SrTiO3 elements for the NVE run
@@ -287,12 +289,16 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--preset", default="medium")
+    ap.add_argument("--workload", default="srtio3", choices=["srtio3", "irregular", "water"],
+                    help="srtio3: the metric's 5k-atom case (default); irregular: 20k random atoms of 10 "
+                         "elements, medium model; water: 30k-atom rigid-water box, wide model")
+    ap.add_argument("--preset", default=None, help="model preset (default: medium, wide for water)")
     ap.add_argument("--cells", type=int, default=10, help="SrTiO3 supercell edge (5 n^3 atoms)")
     ap.add_argument("--sigma", type=float, default=0.05)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--skin", type=float, default=0.5)
-    ap.add_argument("--cpu-calls", type=int, default=20, help="timed oracle calls for cpu_baseline (0: skip)")
+    ap.add_argument("--cpu-calls", type=int, default=None,
+                    help="timed oracle calls for cpu_baseline (0: skip; default 20 for srtio3, 3 otherwise)")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--host-steps", type=int, default=5, help="host-boundary calculator steps (0: skip)")
     ap.add_argument("--capacity-cells", type=int, default=0, metavar="N",
@@ -304,6 +310,10 @@ def main():
                     help="only run 3 device-to-device copies of MIB MiB (the known-size kernel that "
                          "scales FETCH_SIZE / WRITE_SIZE counters to bytes), then exit")
     args = ap.parse_args()
+    if args.preset is None:
+        args.preset = "wide" if args.workload == "water" else "medium"
+    if args.cpu_calls is None:
+        args.cpu_calls = 20 if args.workload == "srtio3" else 3
 
     if args.copy_calibration > 0:
         hip = HipMemory()
@@ -330,7 +340,16 @@ def main():
 
     t_setup = time.perf_counter()
     model_path = workload_model(args.preset, args.seed)
-    structure = synthetic.srtio3_supercell(args.cells, sigma=args.sigma, seed=args.seed)
+    if args.workload == "irregular":
+        structure = synthetic.irregular_box(seed=args.seed)
+        system = (f"irregular box ({len(structure)} atoms uniform at 0.08 /A^3, 1.8 A minimum separation, "
+                  f"10 elements, seed {args.seed})")
+    elif args.workload == "water":
+        structure = synthetic.water_box(seed=args.seed)
+        system = f"rigid-water box ({len(structure)} atoms, 1.0 g/cm^3, random orientations, seed {args.seed})"
+    else:
+        structure = synthetic.srtio3_supercell(args.cells, sigma=args.sigma, seed=args.seed)
+        system = f"SrTiO3 {args.cells}^3 ({len(structure)} atoms, sigma {args.sigma} A, seed {args.seed})"
     N = len(structure)
     ev = MACEKokkosFloat(model_path)
     cutoff = ev.r_cut + args.skin
@@ -393,7 +412,8 @@ def main():
     dominant = max(stage_avg, key=stage_avg.get)
     avg_ms = stage_avg[dominant]
     achieved = flops.get(dominant, 0.0) / (avg_ms * 1e-3) / 1e12 if avg_ms > 0 else 0.0
-    default_workload = (args.preset, args.cells, args.sigma, args.seed, args.skin) == ("medium", 10, 0.05, 0, 0.5)
+    default_workload = (args.workload, args.preset, args.cells, args.sigma, args.seed, args.skin) == (
+        "srtio3", "medium", 10, 0.05, 0, 0.5)
     traffic = committed_traffic(dominant) if default_workload else None
     roofline = {
         "bound": "mfma",
@@ -427,7 +447,8 @@ def main():
     cpu = None
     if args.cpu_calls > 0:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
-        us, times, us1 = cpu_baseline(model_path, structure, cutoff, threads, args.cpu_calls)
+        us, times, us1 = cpu_baseline(model_path, structure, cutoff, threads, args.cpu_calls,
+                                      single_thread=args.workload == "srtio3")
         cpu = {
             "value": round(us, 3),
             "unit": "us/atom",
@@ -435,8 +456,9 @@ def main():
             "kind": "port",
             "sample": f"full {N}-atom workload, 1 warmup + median of {args.cpu_calls} oracle calls "
                       f"(OpenMP restatement of the reference CPU path, compute + reductions, "
-                      f"neighbour list reused), {sum(times):.1f} s timed; one more call on 1 thread",
-            "single_thread_value": round(us1, 3),
+                      f"neighbour list reused), {sum(times):.1f} s timed"
+                      + ("; one more call on 1 thread" if us1 is not None else ""),
+            "single_thread_value": None if us1 is None else round(us1, 3),
         }
 
     line = {
@@ -453,9 +475,9 @@ def main():
         "dtype": "fp32",
         "data": "synthetic",
         "config": {
-            "workload": f"medium-shape random-init MACE ({args.preset}: 128x0e+128x1o, lmax 3, correlation 3, "
-                        f"89-element embedding) on SrTiO3 {args.cells}^3 ({N} atoms, sigma {args.sigma} A, "
-                        f"seed {args.seed}), cutoff {ev.r_cut} + {args.skin} A skin, E+F+stress",
+            "workload": f"random-init MACE ({args.preset}: C={ev.num_channels}, l_max {ev.l_max}, L_max {ev.L_max}, "
+                        f"correlation 3, {len(ev.atomic_numbers)}-element embedding) on {system}, "
+                        f"cutoff {ev.r_cut} + {args.skin} A skin, E+F+stress",
             "atoms": N,
             "edges": int(info["num_edges"]),
             "active_edges": active_edges,
