@@ -17,8 +17,11 @@
 //   compute_readouts                              mace.cpp:2621-2657
 //   reverse_Phi1_streamed                         mace.cpp:2198-2302
 //   reverse_A0_streamed                           mace.cpp:1485-1559
-// Splines: cubic Hermite coefficients and evaluation point
-//   (cubic_spline_set.cpp:7-78, computed in Precision as the reference does).
+//   compute/reverse_A0_scaled, A1_scaled          mace.cpp:1561-1636, 2380-2458
+//   ZBL pair term, in double as the device path   zbl_kokkos.cpp:76-126, 154-201
+// Splines: cubic Hermite coefficients (formed in double, stored in Precision,
+//   as the device path's tables, mace_kokkos_factorized_lifecycle.cpp:4002-4013)
+//   and evaluation point (cubic_spline_set.cpp:32-78).
 // Polynomials: evaluate_gradient_simple (multivariate_polynomial.cpp:326-355).
 // Readout MLP: evaluate_gradient (multilayer_perceptron.cpp:85-160).
 // Harmonics: closed-form real harmonics of the permuted unit direction; the
@@ -88,6 +91,21 @@ struct Spec {
     const double* readout_w2;  // [hidden]
     double readout_scale;
     const double* atomic_energies;  // [ne]
+    const int* atomic_numbers;      // [ne]
+    // ZBL
+    int has_zbl;
+    double zbl_a_exp, zbl_a_prefactor;
+    double zbl_c[4];
+    int zbl_num_radii;
+    const double* zbl_radii;        // indexed by atomic number
+    int zbl_p;
+    // density normalisation splines: [pairs][1][nodes]
+    int A0_scaled;
+    const double* a0s_values;
+    const double* a0s_derivs;
+    int A1_scaled;
+    const double* a1s_values;
+    const double* a1s_derivs;
 };
 
 template <typename P>
@@ -104,7 +122,12 @@ struct SplineSet {
     int nodes, nfn;
     std::vector<P> c;  // [(4*i+q)*nfn + f]
 
-    void build(P h_, P x0_, int nodes_, int nfn_, const double* values, const double* derivs)
+    // Hermite coefficients formed in double from the double nodal data and
+    // stored in P, as the device path builds its tables
+    // (mace_kokkos_factorized_lifecycle.cpp:4002-4013); the serial CPU class
+    // forms them in P (cubic_spline_set.cpp:7-29), which in FP32 loses up to
+    // ~1e-4 of the value scale to cancellation at the compact grid spacing.
+    void build(P h_, P x0_, int nodes_, int nfn_, const double* values, const double* derivs, double hd)
     {
         h = h_;
         x0 = x0_;
@@ -113,16 +136,16 @@ struct SplineSet {
         c.assign(static_cast<size_t>(4) * nfn * (nodes - 1), P(0));
         for (int i = 0; i < nodes - 1; ++i)
             for (int j = 0; j < nfn; ++j) {
-                const P v0 = checked<P>(values[static_cast<size_t>(j) * nodes + i]);
-                const P d0 = checked<P>(derivs[static_cast<size_t>(j) * nodes + i]);
-                const P v1 = checked<P>(values[static_cast<size_t>(j) * nodes + i + 1]);
-                const P d1 = checked<P>(derivs[static_cast<size_t>(j) * nodes + i + 1]);
-                c[(4 * i) * static_cast<size_t>(nfn) + j] = v0;
-                c[(4 * i + 1) * static_cast<size_t>(nfn) + j] = d0;
+                const double v0 = values[static_cast<size_t>(j) * nodes + i];
+                const double d0 = derivs[static_cast<size_t>(j) * nodes + i];
+                const double v1 = values[static_cast<size_t>(j) * nodes + i + 1];
+                const double d1 = derivs[static_cast<size_t>(j) * nodes + i + 1];
+                c[(4 * i) * static_cast<size_t>(nfn) + j] = checked<P>(v0);
+                c[(4 * i + 1) * static_cast<size_t>(nfn) + j] = checked<P>(d0);
                 c[(4 * i + 2) * static_cast<size_t>(nfn) + j] =
-                    (-3 * v0 - 2 * h * d0 + 3 * v1 - h * d1) / (h * h);
+                    checked<P>((-3 * v0 - 2 * hd * d0 + 3 * v1 - hd * d1) / (hd * hd));
                 c[(4 * i + 3) * static_cast<size_t>(nfn) + j] =
-                    (2 * v0 + h * d0 - 2 * v1 + h * d1) / (h * h * h);
+                    checked<P>((2 * v0 + hd * d0 - 2 * v1 + hd * d1) / (hd * hd * hd));
             }
     }
     void point(P r, int& interval, P& x) const
@@ -191,6 +214,40 @@ void real_harmonics(int lmax, P x, P y, P z, P* v, P* gx, P* gy, P* gz)
     }
 }
 
+// ZBL pair term of atomic numbers (Zu, Zv) at distance r: value and d/dr of
+// 0.5 V(r) envelope(r), in double (zbl_kokkos.cpp:37-52, 76-126).
+void zbl_pair_term(double a_exp, double a_prefactor, const double* c, const double* radii, int num_radii, int p,
+                   int Zu, int Zv, double r, double& value, double& gradient)
+{
+    if (Zu < 0 || Zv < 0 || Zu >= num_radii || Zv >= num_radii)
+        throw std::out_of_range("ZBL covalent radius index out of range");
+    const double denominator = std::pow(static_cast<double>(Zu), a_exp) + std::pow(static_cast<double>(Zv), a_exp);
+    const double inverse_a = denominator / (a_prefactor * 0.529);
+    const double prefactor = 14.3996 * static_cast<double>(Zu * Zv);
+    const double r_max = radii[Zu] + radii[Zv];
+    if (r >= r_max) {
+        value = gradient = 0.0;
+        return;
+    }
+    const double r_over_a = r * inverse_a;
+    const double e0 = c[0] * std::exp(-3.2 * r_over_a);
+    const double e1 = c[1] * std::exp(-0.9423 * r_over_a);
+    const double e2 = c[2] * std::exp(-0.4028 * r_over_a);
+    const double e3 = c[3] * std::exp(-0.2016 * r_over_a);
+    const double phi = e0 + e1 + e2 + e3;
+    const double dphi = inverse_a * (-3.2 * e0 - 0.9423 * e1 - 0.4028 * e2 - 0.2016 * e3);
+    const double inverse_r = 1.0 / r;
+    const double bare = prefactor * inverse_r * phi;
+    const double bare_gradient = prefactor * inverse_r * inverse_r * (r * dphi - phi);
+    const double k0 = (p + 1.0) * (p + 2.0) / 2.0, k1 = p * (p + 2.0), k2 = p * (p + 1.0) / 2.0;
+    const double x = r / r_max;
+    const double xpm1 = std::pow(x, p - 1), xp = xpm1 * x, xp1 = xp * x, xp2 = xp1 * x;
+    const double envelope = 1.0 - k0 * xp + k1 * xp1 - k2 * xp2;
+    const double envelope_gradient = (-k0 * p * xpm1 + k1 * (p + 1.0) * xp - k2 * (p + 2.0) * xp1) / r_max;
+    value = 0.5 * bare * envelope;
+    gradient = 0.5 * (bare * envelope_gradient + bare_gradient * envelope);
+}
+
 template <typename P>
 struct Oracle {
     int ne, C, lmax, Lmax, nlm, nLM, num_active;
@@ -211,6 +268,13 @@ struct Oracle {
     std::vector<int> path_l, path_l1, path_l2, path_row0, term_lme, term_row, num_e;
     std::vector<P> term_cg;
     std::vector<std::vector<P>> A1W;
+    std::vector<int> Z;
+    bool has_zbl = false;
+    double zbl_a_exp = 0, zbl_a_prefactor = 0, zbl_c[4] = {};
+    std::vector<double> zbl_radii;
+    int zbl_p = 0;
+    bool A0_scaled = false, A1_scaled = false;
+    std::vector<SplineSet<P>> splA0, splA1;
 
     explicit Oracle(const Spec& s)
     {
@@ -234,9 +298,9 @@ struct Oracle {
         const P h = checked<P>(s.spline_h), x0 = checked<P>(s.spline_x0);
         for (int p = 0; p < pairs; ++p) {
             spl0[p].build(h, x0, s.spline_nodes, static_cast<int>(n0),
-                          s.r0_values + p * n0 * s.spline_nodes, s.r0_derivs + p * n0 * s.spline_nodes);
+                          s.r0_values + p * n0 * s.spline_nodes, s.r0_derivs + p * n0 * s.spline_nodes, s.spline_h);
             spl1[p].build(h, x0, s.spline_nodes, static_cast<int>(n1),
-                          s.r1_values + p * n1 * s.spline_nodes, s.r1_derivs + p * n1 * s.spline_nodes);
+                          s.r1_values + p * n1 * s.spline_nodes, s.r1_derivs + p * n1 * s.spline_nodes, s.spline_h);
         }
         auto conv = [](const double* src, size_t n) {
             std::vector<P> out(n);
@@ -282,6 +346,81 @@ struct Oracle {
         W2 = conv(s.readout_w2, hidden);
         scale = checked<P>(s.readout_scale);
         E0.assign(s.atomic_energies, s.atomic_energies + ne);
+        Z.assign(s.atomic_numbers, s.atomic_numbers + ne);
+        has_zbl = s.has_zbl != 0;
+        if (has_zbl) {
+            zbl_a_exp = s.zbl_a_exp;
+            zbl_a_prefactor = s.zbl_a_prefactor;
+            for (int q = 0; q < 4; ++q) zbl_c[q] = s.zbl_c[q];
+            zbl_radii.assign(s.zbl_radii, s.zbl_radii + s.zbl_num_radii);
+            zbl_p = s.zbl_p;
+        }
+        A0_scaled = s.A0_scaled != 0;
+        A1_scaled = s.A1_scaled != 0;
+        if (A0_scaled) {
+            splA0.resize(pairs);
+            for (int p = 0; p < pairs; ++p)
+                splA0[p].build(h, x0, s.spline_nodes, 1, s.a0s_values + static_cast<size_t>(p) * s.spline_nodes,
+                               s.a0s_derivs + static_cast<size_t>(p) * s.spline_nodes, s.spline_h);
+        }
+        if (A1_scaled) {
+            splA1.resize(pairs);
+            for (int p = 0; p < pairs; ++p)
+                splA1[p].build(h, x0, s.spline_nodes, 1, s.a1s_values + static_cast<size_t>(p) * s.spline_nodes,
+                               s.a1s_derivs + static_cast<size_t>(p) * s.spline_nodes, s.spline_h);
+        }
+    }
+
+    void zbl_pair(int Zu, int Zv, double r, double& value, double& gradient) const
+    {
+        zbl_pair_term(zbl_a_exp, zbl_a_prefactor, zbl_c, zbl_radii.data(), static_cast<int>(zbl_radii.size()),
+                      zbl_p, Zu, Zv, r, value, gradient);
+    }
+
+    // 1 + sum over the receiver's neighbours of a density spline
+    // (compute_A0_scaled / compute_A1_scaled, mace.cpp:1573-1580)
+    P scale_factor(const std::vector<SplineSet<P>>& spl, int i, const long long* first, const int* types,
+                   const int* neigh_types, const double* r) const
+    {
+        P s = 1.0;
+        for (long long e = first[i]; e < first[i + 1]; ++e) {
+            const auto& sp = spl[pair_index(types[i], neigh_types[e])];
+            int iv;
+            P x;
+            sp.point(static_cast<P>(r[e]), iv, x);
+            const P* c = sp.coef(iv);
+            s += c[0] + c[1] * x + c[2] * (x * x) + c[3] * (x * x * x);
+        }
+        return s;
+    }
+
+    // reverse_A0_scaled / reverse_A1_scaled (mace.cpp:1584-1636, 2404-2458):
+    // forces += (adj . feat) / s * f'(r) r_hat for every neighbour, adj /= s.
+    void reverse_scale(const std::vector<SplineSet<P>>& spl, int N, const long long* first, const int* types,
+                       const int* neigh_types, const double* xyz, const double* r, const P* feat, P* adj,
+                       double* forces) const
+    {
+        const size_t width = static_cast<size_t>(nlm) * C;
+#pragma omp parallel for schedule(static)
+        for (int i = 0; i < N; ++i) {
+            const P s = scale_factor(spl, i, first, types, neigh_types, r);
+            P dot = 0;
+            const P* f = feat + i * width;
+            P* a = adj + i * width;
+            for (size_t lmk = 0; lmk < width; ++lmk) dot += a[lmk] * f[lmk];
+            for (long long e = first[i]; e < first[i + 1]; ++e) {
+                const auto& sp = spl[pair_index(types[i], neigh_types[e])];
+                int iv;
+                P x;
+                sp.point(static_cast<P>(r[e]), iv, x);
+                const P* c = sp.coef(iv);
+                const P d = static_cast<P>(c[1] + 2.0 * c[2] * x + 3.0 * c[3] * x * x);
+                const P force_scale = dot / s * d;
+                for (int q = 0; q < 3; ++q)
+                    forces[3 * e + q] += static_cast<double>(force_scale * static_cast<P>(xyz[3 * e + q] / r[e]));
+            }
+            for (size_t lmk = 0; lmk < width; ++lmk) a[lmk] /= s;
+        }
     }
 
     int pair_index(int ti, int tj) const
@@ -330,6 +469,22 @@ struct Oracle {
         const long long E = first[N];
         const P rc = static_cast<P>(r_cut);
         for (long long e = 0; e < 3 * E; ++e) forces[e] = 0.0;
+        for (int i = 0; i < N; ++i) energies[i] = 0.0;
+
+        // ---- ZBL (every neighbour, double) ----
+        if (has_zbl) {
+#pragma omp parallel for schedule(static)
+            for (int i = 0; i < N; ++i) {
+                double e_i = 0.0;
+                for (long long e = first[i]; e < first[i + 1]; ++e) {
+                    double v, g;
+                    zbl_pair(Z.at(types[i]), Z.at(neigh_types[e]), r[e], v, g);
+                    e_i += v;
+                    for (int q = 0; q < 3; ++q) forces[3 * e + q] -= xyz[3 * e + q] / r[e] * g;
+                }
+                energies[i] += e_i;
+            }
+        }
 
         // ---- compute_Y: values and gradients w.r.t. xyz (unshuffled) ----
         std::vector<P> Y(static_cast<size_t>(E) * nlm), Yg(static_cast<size_t>(E) * 3 * nlm);
@@ -410,6 +565,16 @@ struct Oracle {
                         }
                     }
                 }
+            }
+        }
+
+        // ---- compute_A0_scaled ----
+        if (A0_scaled) {
+#pragma omp parallel for schedule(static)
+            for (int i = 0; i < N; ++i) {
+                const P sf = scale_factor(splA0, i, first.data(), types, neigh_types, r);
+                P* a = A0.data() + static_cast<size_t>(i) * nlm * C;
+                for (size_t lmk = 0; lmk < static_cast<size_t>(nlm) * C; ++lmk) a[lmk] /= sf;
             }
         }
 
@@ -506,6 +671,16 @@ struct Oracle {
             }
         }
 
+        // ---- compute_A1_scaled ----
+        if (A1_scaled) {
+#pragma omp parallel for schedule(static)
+            for (int i = 0; i < N; ++i) {
+                const P sf = scale_factor(splA1, i, first.data(), types, neigh_types, r);
+                P* a = A1.data() + static_cast<size_t>(i) * nlm * C;
+                for (size_t lmk = 0; lmk < static_cast<size_t>(nlm) * C; ++lmk) a[lmk] /= sf;
+            }
+        }
+
         // ---- compute_M1, compute_H2, compute_readouts, reverse_H2, reverse_M1 ----
         std::vector<P> direct(static_cast<size_t>(N) * C), A1adj(static_cast<size_t>(N) * nlm * C);
 #pragma omp parallel
@@ -545,7 +720,7 @@ struct Oracle {
                     out += W2[h] * hid[h];
                 }
                 energy += out;
-                energies[i] = energy;
+                energies[i] += energy;
                 for (int k = 0; k < C; ++k) {
                     P g2 = 0;
                     for (int h = 0; h < hidden; ++h) g2 += W2[h] * dact[h] * W1[static_cast<size_t>(h) * C + k];
@@ -569,6 +744,10 @@ struct Oracle {
                             M1g[static_cast<size_t>(lm) * C + k] * M1adj[k];
             }
         }
+
+        // ---- reverse_A1_scaled ----
+        if (A1_scaled)
+            reverse_scale(splA1, N, first.data(), types, neigh_types, xyz, r, A1.data(), A1adj.data(), forces);
 
         // ---- reverse_A1: dPhi1 = A1_adj W^T ----
         std::vector<P> dPhi1(static_cast<size_t>(N) * num_lme * C);
@@ -700,6 +879,10 @@ struct Oracle {
                     for (int k = 0; k < C; ++k) out[k] += g[k] * a[k];
                 }
             }
+
+        // ---- reverse_A0_scaled ----
+        if (A0_scaled)
+            reverse_scale(splA0, N, first.data(), types, neigh_types, xyz, r, A0.data(), A0adj.data(), forces);
 
         // ---- reverse_A0_streamed ----
 #pragma omp parallel
@@ -851,6 +1034,20 @@ int oracle_mace_compute_f64(void* h, int N, const int* types, const int* num_nei
                            num_threads);
 }
 
+// The oracle's ZBL pair term (value, d/dr) at n distances; 0 on success.
+int oracle_zbl_pair(double a_exp, double a_prefactor, const double* c, int num_radii, const double* radii, int p,
+                    int Zu, int Zv, long long n, const double* r, double* value, double* gradient)
+{
+    try {
+        for (long long i = 0; i < n; ++i) zbl_pair_term(a_exp, a_prefactor, c, radii, num_radii, p, Zu, Zv, r[i],
+                                                         value[i], gradient[i]);
+        return 0;
+    } catch (const std::exception& e) {
+        g_last_error = e.what();
+        return 1;
+    }
+}
+
 // Harmonics of edge vectors as the oracle forms them in compute():
 // Y [n][num_lm] and dY/d(x,y,z) [n][3][num_lm], double precision.
 void oracle_harmonics(int lmax, long long n, const double* xyz, double* Y, double* dY)
@@ -888,7 +1085,7 @@ void oracle_spline_eval(double h, double x0, int nodes, int nfn, const double* v
                         long long n, const double* r, double* out_value, double* out_deriv)
 {
     SplineSet<double> sp;
-    sp.build(h, x0, nodes, nfn, values, derivs);
+    sp.build(h, x0, nodes, nfn, values, derivs, h);
     for (long long e = 0; e < n; ++e) {
         int iv;
         double x;

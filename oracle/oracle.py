@@ -201,18 +201,33 @@ def compact_radial_grid(model):
     return grid_min, h, points
 
 
+def agnesi_transform(r, r0, a, q, p):
+    """Agnesi distance transform t = 1 / (1 + a s^q / (1 + s^(q - p))),
+    s = r / r0 (compact_radial.cpp:238-247)."""
+    s = r / r0
+    return 1.0 / (1.0 + a * s**q / (1.0 + s ** (q - p)))
+
+
 def radial_features(model, type_i, type_j):
     """Bessel x polynomial-cutoff features on the spline knots
-    (compact_radial.cpp:227-267), shape (knots, num_bessel)."""
+    (compact_radial.cpp:227-267), shape (knots, num_bessel); with the Agnesi
+    transform the Bessel functions take the transformed distance and the
+    cutoff the plain one."""
     cr = model["compact_radial"]
     grid_min, h, points = compact_radial_grid(model)
     w = np.asarray(cr["basis"]["weights"], dtype=np.float64)
     pref = float(cr["basis"]["prefactor"])
     rmax = float(cr["cutoff"]["r_max"])
     p = int(cr["cutoff"]["p"])
-    if cr["distance_transform"]["type"] != "none":
-        raise NotImplementedError("only distance_transform 'none' is restated")
+    tr = cr["distance_transform"]
     r = grid_min + np.arange(points) * h
+    t = r
+    if tr["type"] == "agnesi":
+        radii = np.asarray(tr["covalent_radii"], dtype=np.float64)
+        r0 = 0.5 * (radii[type_i] + radii[type_j])
+        t = agnesi_transform(r, r0, float(tr["a"]), float(tr["q"]), float(tr["p"]))
+    elif tr["type"] != "none":
+        raise NotImplementedError(f"distance_transform {tr['type']!r} is not restated")
     scaled = r / rmax
     cut = np.where(
         r < rmax,
@@ -222,7 +237,7 @@ def radial_features(model, type_i, type_j):
         - (p * (p + 1.0) / 2.0) * scaled ** (p + 2),
         0.0,
     )
-    return pref * np.sin(w[None, :] * r[:, None]) / r[:, None] * cut[:, None]
+    return pref * np.sin(w[None, :] * t[:, None]) / t[:, None] * cut[:, None]
 
 
 def _network(model, name):
@@ -232,16 +247,20 @@ def _network(model, name):
         np.asarray(w, dtype=np.float64).reshape(shape[i + 1], shape[i])
         for i, w in enumerate(net["weights"])
     ]
-    return weights, float(net["activation_scale"])
+    return weights, float(net["activation_scale"]), net.get("postprocess", "") == "tanh-square"
 
 
 def compact_radial_tables(model, type_i, type_j, name):
     """Nodal values and derivatives (functions, knots) of network ``name`` for
-    the unordered pair (type_i, type_j)."""
+    the unordered pair (type_i, type_j); a density network's output is
+    postprocessed by tanh(y^2) before the derivative rule
+    (compact_radial.cpp:271-289)."""
     _, h, _ = compact_radial_grid(model)
     feats = radial_features(model, type_i, type_j)
-    weights, scale = _network(model, name)
+    weights, scale, tanh_square = _network(model, name)
     values = _silu_mlp(feats, weights, scale).T.copy()  # (functions, knots)
+    if tanh_square:
+        values = np.tanh(values * values)
     return values, spline_derivatives_fast(values, h)
 
 
@@ -270,6 +289,12 @@ class _Spec(ctypes.Structure):
         ("readout_hidden", ctypes.c_int), ("readout_w1", ctypes.c_void_p),
         ("readout_w2", ctypes.c_void_p), ("readout_scale", ctypes.c_double),
         ("atomic_energies", ctypes.c_void_p),
+        ("atomic_numbers", ctypes.c_void_p),
+        ("has_zbl", ctypes.c_int), ("zbl_a_exp", ctypes.c_double), ("zbl_a_prefactor", ctypes.c_double),
+        ("zbl_c", ctypes.c_double * 4), ("zbl_num_radii", ctypes.c_int), ("zbl_radii", ctypes.c_void_p),
+        ("zbl_p", ctypes.c_int),
+        ("A0_scaled", ctypes.c_int), ("a0s_values", ctypes.c_void_p), ("a0s_derivs", ctypes.c_void_p),
+        ("A1_scaled", ctypes.c_int), ("a1s_values", ctypes.c_void_p), ("a1s_derivs", ctypes.c_void_p),
     ]
 
 
@@ -289,8 +314,6 @@ class MaceOracle:
     def __init__(self, model: dict, active_types, precision="float32"):
         if model.get("symmetrix_format_version") != 4 or model.get("h1_affine_mode") != "m0_composite":
             raise NotImplementedError("the oracle restates format 4 / m0_composite models")
-        if model.get("has_zbl") or model.get("A0_scaled") or model.get("A1_scaled"):
-            raise NotImplementedError("ZBL and A0/A1 scaling are not restated")
         self.precision = precision
         self.model = model
         ne = int(model["num_elements"])
@@ -305,6 +328,8 @@ class MaceOracle:
             t2a[t] = a
         grid_min, h, points = compact_radial_grid(model)
         r0v, r0d, r1v, r1d = [], [], [], []
+        a0sv, a0sd, a1sv, a1sd = [], [], [], []
+        a0s, a1s = bool(model.get("A0_scaled")), bool(model.get("A1_scaled"))
         for ai in range(len(active)):
             for aj in range(ai, len(active)):
                 v, d = compact_radial_tables(model, active[ai], active[aj], "R0")
@@ -313,6 +338,14 @@ class MaceOracle:
                 v, d = compact_radial_tables(model, active[ai], active[aj], "R1")
                 r1v.append(v)
                 r1d.append(d)
+                if a0s:
+                    v, d = compact_radial_tables(model, active[ai], active[aj], "A0")
+                    a0sv.append(v)
+                    a0sd.append(d)
+                if a1s:
+                    v, d = compact_radial_tables(model, active[ai], active[aj], "A1")
+                    a1sv.append(v)
+                    a1sd.append(d)
         keep = {}
 
         def arr(a, dtype=np.float64):
@@ -364,7 +397,25 @@ class MaceOracle:
             readout_w2=arr(model["readout_2_weights_2"]),
             readout_scale=float(model["readout_2_scale_factor"]),
             atomic_energies=arr(model["atomic_energies"]),
+            atomic_numbers=arr(model["atomic_numbers"], np.int32),
+            has_zbl=int(bool(model.get("has_zbl"))),
+            A0_scaled=int(a0s), A1_scaled=int(a1s),
         )
+        if model.get("has_zbl"):
+            radii = np.asarray(model["zbl_covalent_radii"], dtype=np.float64)
+            spec.zbl_a_exp = float(model["zbl_a_exp"])
+            spec.zbl_a_prefactor = float(model["zbl_a_prefactor"])
+            for q, c in enumerate(model["zbl_c"]):
+                spec.zbl_c[q] = float(c)
+            spec.zbl_num_radii = len(radii)
+            spec.zbl_radii = arr(radii)
+            spec.zbl_p = int(model["zbl_p"])
+        if a0s:
+            spec.a0s_values = arr(np.stack(a0sv))
+            spec.a0s_derivs = arr(np.stack(a0sd))
+        if a1s:
+            spec.a1s_values = arr(np.stack(a1sv))
+            spec.a1s_derivs = arr(np.stack(a1sd))
         lib = _lib()
         suffix = "f32" if precision == "float32" else "f64"
         self._destroy = getattr(lib, f"oracle_mace_destroy_{suffix}")
@@ -425,6 +476,22 @@ def spline_eval(h, x0, values, derivs, r):
                               _ptr(rr, ctypes.c_double), _ptr(out_v, ctypes.c_double),
                               _ptr(out_d, ctypes.c_double))
     return out_v, out_d
+
+
+def zbl_pair(a_exp, a_prefactor, c, covalent_radii, p, Zu, Zv, r):
+    """The oracle's ZBL pair term 0.5 V envelope and its r-derivative at r."""
+    rr = np.ascontiguousarray(np.atleast_1d(r), dtype=np.float64)
+    cc = np.ascontiguousarray(c, dtype=np.float64)
+    radii = np.ascontiguousarray(covalent_radii, dtype=np.float64)
+    value, grad = np.zeros(len(rr)), np.zeros(len(rr))
+    lib = _lib()
+    status = lib.oracle_zbl_pair(ctypes.c_double(a_exp), ctypes.c_double(a_prefactor), _ptr(cc, ctypes.c_double),
+                                 ctypes.c_int(len(radii)), _ptr(radii, ctypes.c_double), ctypes.c_int(p),
+                                 ctypes.c_int(Zu), ctypes.c_int(Zv), ctypes.c_longlong(len(rr)),
+                                 _ptr(rr, ctypes.c_double), _ptr(value, ctypes.c_double), _ptr(grad, ctypes.c_double))
+    if status != 0:
+        raise ValueError(lib.oracle_mace_last_error().decode())
+    return value, grad
 
 
 def poly_eval(monomials, coefficients, x):

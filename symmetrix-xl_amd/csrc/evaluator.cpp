@@ -454,6 +454,39 @@ void Evaluator::prepare_active_types(const std::vector<int>& node_types)
     }
     upload(r1_, r1, stream_);
     upload(r0f_, r0f, stream_);
+    // density-normalisation splines per unordered pair: [pair_u][iv][4]
+    auto density_table = [&](const RadialNetwork& net, DeviceBuffer& out) {
+        std::vector<float> table(static_cast<std::size_t>(npairs) * NI * 4);
+        for (int pu = 0; pu < npairs; ++pu) {
+            std::vector<double> v, d;
+            m.radial_tables(net, types[pair_types[pu].first], types[pair_types[pu].second], v, d);
+            for (int iv = 0; iv < NI; ++iv) {
+                double c4[4];
+                hermite(v, d, 0, iv, c4);
+                for (int q = 0; q < 4; ++q)
+                    table[(static_cast<std::size_t>(pu) * NI + iv) * 4 + q] = static_cast<float>(c4[q]);
+            }
+        }
+        upload(out, table, stream_);
+    };
+    if (m.A0_scaled) density_table(m.A0net, dens0_);
+    if (m.A1_scaled) density_table(m.A1net, dens1_);
+    // ZBL per ordered active pair (receiver, source), zbl_kokkos.cpp:37-52
+    if (m.has_zbl) {
+        std::vector<double> inv_a(na * na), pref(na * na), rmax(na * na);
+        for (int ai = 0; ai < na; ++ai)
+            for (int aj = 0; aj < na; ++aj) {
+                const int zu = m.atomic_numbers[types[ai]], zv = m.atomic_numbers[types[aj]];
+                const double denominator = std::pow(static_cast<double>(zu), m.zbl_a_exp) +
+                                           std::pow(static_cast<double>(zv), m.zbl_a_exp);
+                inv_a[ai * na + aj] = denominator / (m.zbl_a_prefactor * 0.529);
+                pref[ai * na + aj] = 14.3996 * static_cast<double>(zu * zv);
+                rmax[ai * na + aj] = m.zbl_radii[zu] + m.zbl_radii[zv];
+            }
+        upload(zbl_inverse_a_, inv_a, stream_);
+        upload(zbl_prefactor_, pref, stream_);
+        upload(zbl_rmax_, rmax, stream_);
+    }
     // per active type tables
     std::vector<int> type_active(m.num_elements, -1);
     for (int a = 0; a < na; ++a) type_active[types[a]] = a;
@@ -520,6 +553,10 @@ void Evaluator::allocate_workspace()
     H1_.reserve(N * nLM_ * C_ * f);
     H1adj_.reserve(N * nLM_ * C_ * f);
     direct_.reserve(N * C_ * f);
+    if (model_.A1_scaled) {
+        scale1_.reserve(N * f);
+        dot1_.reserve(N * f);
+    }
     energies_.reserve(N * sizeof(double));
     forces_.reserve(E * 3 * sizeof(double));
     atom_forces_.reserve(N * 3 * sizeof(double));
@@ -1002,6 +1039,38 @@ double Evaluator::max_displacement(std::uint64_t generation, const double* posit
     return std::sqrt(d2);
 }
 
+// Density-normalisation arguments of the layer and readout kernels.
+void Evaluator::density_args(LayerArgs& la, ReadoutArgs* ra)
+{
+    la.d0 = DensityScale{};
+    la.d1 = DensityScale{};
+    if (model_.A0_scaled) la.d0.table = dens0_.as<float>();
+    if (model_.A1_scaled) {
+        la.d1.table = dens1_.as<float>();
+        la.d1.scale = scale1_.as<float>();
+        la.d1.dot = dot1_.as<float>();
+    }
+    if (ra) {
+        ra->a1_scale = la.d1.scale;
+        ra->a1_dot = la.d1.dot;
+    }
+}
+
+// ZBL pair term over every receiver (after the forces of the MACE part).
+void Evaluator::launch_zbl_term(hipStream_t s)
+{
+    if (!model_.has_zbl) return;
+    ZblArgs z;
+    z.inverse_a = zbl_inverse_a_.as<double>();
+    z.prefactor = zbl_prefactor_.as<double>();
+    z.r_max = zbl_rmax_.as<double>();
+    for (int q = 0; q < 4; ++q) z.c[q] = model_.zbl_c[q];
+    z.p = model_.zbl_p;
+    hip_check(launch_zbl(num_nodes_, first_.as<int>(), edge_pair_.as<int>(), xyz_.as<double>(), r_.as<double>(), z,
+                         energies_.as<double>(), forces_.as<double>(), s),
+              "ZBL");
+}
+
 // H1 = M0 H1_W per l block (or, reverse, M0_adj = H1_adj H1_W^T) for
 // `nodes` consecutive nodes, one grouped launch.
 void Evaluator::gemm_h1(int nodes, const float* in, long long in_stride, float* out, long long out_stride,
@@ -1081,6 +1150,7 @@ void Evaluator::evaluate()
     la.L_max = model_.L_max;
     la.node_offset = 0;
     la.node_count = N;
+    density_args(la, nullptr);
     hipStream_t s = stream_;
     const PolyArgs p0 = poly_args(p0_layout_, p0_coef_, p0_offsets_, p0_packed_);
     const PolyArgs p1 = poly_args(p1_layout_, p1_coef_, p1_offsets_, p1_packed_);
@@ -1133,6 +1203,7 @@ void Evaluator::evaluate()
         ra.energies = energies_.as<double>();
         ra.direct = direct_.as<float>();
         ra.A1_adj = A1adj_.as<float>();
+        density_args(la, &ra);
         mark(kStageReadout, false);
         hip_check(launch_readout(ra, s), "readout");
         mark(kStageReadout, true);
@@ -1163,8 +1234,10 @@ void Evaluator::evaluate()
                   "M0 reverse");
         mark(kStageM0Reverse, true);
         mark(kStageA0Reverse, false);
-        hip_check(launch_a0_reverse(la, r0f_.as<float>(), A0adj, forces_.as<double>(), s), "A0 reverse");
+        hip_check(launch_a0_reverse(la, r0f_.as<float>(), A0_.as<float>(), A0adj, forces_.as<double>(), s),
+                  "A0 reverse");
         mark(kStageA0Reverse, true);
+        launch_zbl_term(s);
     }
     mark(kStageAtomForces, false);
     hip_check(launch_atom_forces(N, first_.as<int>(), tfirst_.as<int>(), tedge_.as<int>(), forces_.as<double>(),
@@ -1223,6 +1296,7 @@ void Evaluator::evaluate_tiled()
     la.C = C_;
     la.l_max = model_.l_max;
     la.L_max = model_.L_max;
+    density_args(la, nullptr);
     hipStream_t s = stream_;
     const PolyArgs p0 = poly_args(p0_layout_, p0_coef_, p0_offsets_, p0_packed_);
     const PolyArgs p1 = poly_args(p1_layout_, p1_coef_, p1_offsets_, p1_packed_);
@@ -1274,6 +1348,7 @@ void Evaluator::evaluate_tiled()
     ra.energies = energies_.as<double>();
     ra.direct = direct_.as<float>();
     ra.A1_adj = A1adj_.as<float>();
+    density_args(la, &ra);
     float* dPhi1 = Phi1_.as<float>();
     for (int t = 0; t < num_tiles_; ++t) {
         tile(t);
@@ -1306,8 +1381,10 @@ void Evaluator::evaluate_tiled()
         hip_check(launch_m0_reverse(la, p0, node_blocks(m0_blocks_, m0_block_offsets_, t), A0_.as<float>(), M0adj,
                                     A0adj, s),
                   "M0 reverse");
-        hip_check(launch_a0_reverse(la, r0f_.as<float>(), A0adj, forces_.as<double>(), s), "A0 reverse");
+        hip_check(launch_a0_reverse(la, r0f_.as<float>(), A0_.as<float>(), A0adj, forces_.as<double>(), s),
+                  "A0 reverse");
     }
+    launch_zbl_term(s);
     mark(kStageAtomForces, false);
     hip_check(launch_atom_forces(N, first_.as<int>(), tfirst_.as<int>(), tedge_.as<int>(), forces_.as<double>(),
                                  atom_forces_.as<double>(), s),

@@ -203,6 +203,8 @@ private:
     DeviceBuffer h1w_, h1wt_, h2m1_, h2m1t_, q_, w1_, w2_, cg_;
     std::vector<std::unique_ptr<DeviceBuffer>> a1w_, a1wt_;
     PolyLayout p0_layout_, p1_layout_;
+    // density-normalisation splines [pair_u][interval][4] and ZBL pair tables [ordered active pair]
+    DeviceBuffer dens0_, dens1_, zbl_inverse_a_, zbl_prefactor_, zbl_rmax_;
     PolyArgs poly_args(const PolyLayout& layout, const DeviceBuffer& coef, const DeviceBuffer& offsets,
                        const DeviceBuffer& packed) const;
     SplineGrid grid_;
@@ -223,6 +225,9 @@ private:
     // workspace
     DeviceBuffer A0_, M0_, H1_, Phi1_, A1_, A1adj_, direct_, H1adj_, msg_, energies_, forces_,
         atom_forces_, partials_, totals_, scratch_;
+    DeviceBuffer scale1_, dot1_;  // [N] A1 density scale and A1_adj . A1 (scaled models)
+    void density_args(LayerArgs& la, ReadoutArgs* ra);
+    void launch_zbl_term(hipStream_t s);
     bool reduced_ = false;
     double reduced_volume_ = 0.0;
 

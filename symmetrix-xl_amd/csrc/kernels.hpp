@@ -111,9 +111,20 @@ struct GemmGroup {
 };
 hipError_t launch_gemm_group(GemmGroup group, hipStream_t stream);
 
+// Density normalisation of A0 or A1 (reference compute/reverse_A0_scaled,
+// mace.cpp:1561-1636, 2380-2458): per receiver s = 1 + sum over all its
+// neighbours of a scalar spline f_pair(r); the features are divided by s and
+// the reverse adds (adj . feature) / s * f'(r) r_hat to every directed force.
+struct DensityScale {
+    const float* table = nullptr;  // [pair_u][interval][4] cubic coefficients; null: no scaling
+    float* scale = nullptr;        // [N] s per node (A1: written by the R1 forward)
+    float* dot = nullptr;          // [N] adjoint . feature per node (A1: written by the readout)
+};
+
 struct LayerArgs {
     EdgeGraph graph;
     SplineGrid grid;
+    DensityScale d0, d1;  // A0 and A1 density normalisation
     int C = 0;
     int l_max = 0, L_max = 0;
     int node_offset = 0;  // first receiver handled by this launch
@@ -126,7 +137,8 @@ struct LayerArgs {
     long long edge_base = 0;
 };
 
-// Layer 0: A0[i] = sum_j R0f_{pair(i,j)}(r) Y(r_hat)   (H0 and A0_W folded in)
+// Layer 0: A0[i] = sum_j R0f_{pair(i,j)}(r) Y(r_hat)   (H0 and A0_W folded in),
+// divided by the A0 density scale when the model has one
 hipError_t launch_a0_forward(const LayerArgs& a, const float* r0f, float* A0, hipStream_t s);
 // M0 = P0(A0) per (node, LM, channel), over the nodes of the given blocks
 hipError_t launch_m0_forward(const LayerArgs& a, const PolyArgs& p0, const NodeBlocks& nb, const float* A0,
@@ -146,6 +158,8 @@ struct ReadoutArgs {
     const int* node_types = nullptr;
     const int* type_active = nullptr;
     const float* A1 = nullptr;      // [N][num_lm][C]
+    const float* a1_scale = nullptr;  // [N] A1 density scale per node, null: unscaled model
+    float* a1_dot = nullptr;          // [N] A1_adj . A1 per node (scaled model)
     const float* M0 = nullptr;      // scalar block (LM 0) of node i at M0 + i * m0_stride
     PolyArgs p1;
     const float* H2M0 = nullptr;    // [active][C][C]  ([in][out])
@@ -194,9 +208,23 @@ hipError_t launch_add_direct(int nodes, int C, int num_LM, const float* direct, 
 // A0_adj = sum_LM M0_adj[LM] dP0_LM/dA0, over the nodes of the given blocks
 hipError_t launch_m0_reverse(const LayerArgs& a, const PolyArgs& p0, const NodeBlocks& nb, const float* A0,
                              const float* M0_adj, float* A0_adj, hipStream_t s);
-// Layer 0 reverse: forces += -(dE/dxyz) through R0f and Y
-hipError_t launch_a0_reverse(const LayerArgs& a, const float* r0f, const float* A0_adj,
+// Layer 0 reverse: forces += -(dE/dxyz) through R0f and Y (A0: the scaled
+// features, used by the density-scale reverse)
+hipError_t launch_a0_reverse(const LayerArgs& a, const float* r0f, const float* A0, const float* A0_adj,
                              double* forces, hipStream_t s);
+
+// ZBL pair repulsion (zbl_kokkos.cpp:76-201), in double: energies[i] +=
+// sum over all neighbours of V, forces[e] -= r_hat dV/dr.  Per ordered active
+// pair: 1/a, 14.3996 Zu Zv, r_max = cov(Zu) + cov(Zv).
+struct ZblArgs {
+    const double* inverse_a = nullptr;
+    const double* prefactor = nullptr;
+    const double* r_max = nullptr;
+    double c[4] = {};
+    int p = 0;
+};
+hipError_t launch_zbl(int num_nodes, const int* first, const int* edge_pair, const double* xyz, const double* r,
+                      const ZblArgs& z, double* energies, double* forces, hipStream_t s);
 
 // Geometry from positions: xyz = pos[src] - pos[recv] + shift . cell
 hipError_t launch_edge_geometry(int num_edges, const int* receiver, const int* source,

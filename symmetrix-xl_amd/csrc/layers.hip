@@ -93,6 +93,45 @@ __device__ __forceinline__ TileSlot compact_edge(const EdgeGraph& g, const Splin
     return {on, slot};
 }
 
+// Scalar density spline (one cubic per interval and unordered pair) at r:
+// value and slope (reference CubicSpline evaluate / evaluate_deriv).
+__device__ __forceinline__ float4v density_coef(const float* table, const SplineGrid& grid, int pair_u, double r,
+                                                float& x)
+{
+    int iv;
+    spline_point(r, grid, iv, x);
+    return *reinterpret_cast<const float4v*>(table + 4 * (static_cast<size_t>(pair_u) * grid.intervals + iv));
+}
+
+__device__ __forceinline__ float density_value(const float* table, const SplineGrid& grid, int pair_u, double r)
+{
+    float x;
+    const float4v c = density_coef(table, grid, pair_u, r, x);
+    return cubic(c, x);
+}
+
+__device__ __forceinline__ float density_slope(const float* table, const SplineGrid& grid, int pair_u, double r)
+{
+    float x;
+    const float4v c = density_coef(table, grid, pair_u, r, x);
+    return cubic_slope(c, x, 3.0f * x);
+}
+
+// Sum over all edges [e0, e1) of the receiver of its density spline, by
+// wave 0 (all 64 lanes), in a fixed order: returns 1 + sum on every lane.
+__device__ __forceinline__ float density_scale(const DensityScale& d, const EdgeGraph& g, const SplineGrid& grid,
+                                               int e0, int e1)
+{
+    float sum = 0.0f;
+    for (int b = e0; b < e1; b += 64) {
+        const int e = b + static_cast<int>(threadIdx.x);
+        float v = 0.0f;
+        if (e < e1) v = density_value(d.table, grid, g.edge_pair[e] >> 16, g.r[e]);
+        sum += wave_sum_dpp(v);
+    }
+    return 1.0f + sum;
+}
+
 // ---------------------------------------------------------------------------
 // Layer 0 forward: A0[i, lm, k] = sum_j R0f_{pair}(r_ij)[l, k] Y_lm(r_ij)
 // ---------------------------------------------------------------------------
@@ -107,12 +146,18 @@ __global__ void __launch_bounds__(256) a0_forward_kernel(LayerArgs a, const floa
     __shared__ int s_row[kTile];
     __shared__ int s_count;
 
+    __shared__ float s_scale;
+
     const int i = receiver_of_block(a);
     const int k = threadIdx.x;
     const int C = a.C;
     const EdgeGraph& g = a.graph;
     const int voff = min(k, C - 1) * 16;
     const int row_bytes = NL * C * 16;
+    if (a.d0.table && threadIdx.x < 64) {
+        const float sc = density_scale(a.d0, g, a.grid, g.first[i], g.first[i + 1]);
+        if (threadIdx.x == 0) s_scale = sc;
+    }
     float acc[NLM];
 #pragma unroll
     for (int lm = 0; lm < NLM; ++lm) acc[lm] = 0.0f;
@@ -156,6 +201,12 @@ __global__ void __launch_bounds__(256) a0_forward_kernel(LayerArgs a, const floa
         float4v ring[kDepth][NL];
         stream_ring<kDepth>(count, ring, fetch, accumulate);
     }
+    if (a.d0.table) {
+        __syncthreads();
+        const float sc = s_scale;
+#pragma unroll
+        for (int lm = 0; lm < NLM; ++lm) acc[lm] /= sc;
+    }
     if (k < C) {
         float* out = A0 + static_cast<size_t>(i - a.local_base) * NLM * C + k;
 #pragma unroll
@@ -190,6 +241,10 @@ __global__ void __launch_bounds__(256) r1_forward_kernel(LayerArgs a, const floa
     const int kk = min(k, C - 1);
     const int row_bytes = NP * C * 16;
     const int h_bytes = NLMS * C * 4;
+    if (a.d1.table && threadIdx.x < 64) {
+        const float sc = density_scale(a.d1, g, a.grid, g.first[i], g.first[i + 1]);
+        if (threadIdx.x == 0) a.d1.scale[i] = sc;
+    }
     float acc[S::NLME];
 #pragma unroll
     for (int q = 0; q < S::NLME; ++q) acc[q] = 0.0f;
@@ -286,6 +341,7 @@ r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
     __shared__ int s_src[kTile];
     __shared__ int s_eid[kTile];
     __shared__ float s_f[kTile][kMaxWaves][3];
+    __shared__ float s_dsc[kTile];  // A1 density-scale force coefficient per active slot
     __shared__ int s_count;
 
     const int i = receiver_of_block(a);
@@ -298,6 +354,8 @@ r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
     const int kk = min(k, C - 1);
     const int row_bytes = NP * C * 16;
     const int h_bytes = NLMS * C * 4;
+    // (A1_adj . A1) / s of this receiver (reverse_A1_scaled)
+    const float dcoef = a.d1.table ? a.d1.dot[i] / a.d1.scale[i] : 0.0f;
     // G (factored) or dPhi1 (per-term); zero on lanes beyond C
     float G[NG];
 #pragma unroll
@@ -335,15 +393,20 @@ r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
                 s_row[sl] = (g.edge_pair[e] >> 16) * a.grid.intervals + iv;
                 s_src[sl] = g.source[e];
                 s_eid[sl] = e;
+                s_dsc[sl] = a.d1.table ? dcoef * density_slope(a.d1.table, a.grid, g.edge_pair[e] >> 16, rr) : 0.0f;
                 if constexpr (!kFactored) {
 #pragma unroll
                     for (int q = 0; q < NT; ++q) s_cgY[sl][q] = cg[q] * s_Y[sl][S::term_lm1[q]];
                 }
             } else if (t < n) {
+                // beyond r_cut: only the A1 density-scale term (reverse_A1_scaled visits every neighbour)
                 double* out = forces + 3 * static_cast<size_t>(e);
-                out[0] = 0.0;
-                out[1] = 0.0;
-                out[2] = 0.0;
+                float d = 0.0f;
+                if (a.d1.table) d = dcoef * density_slope(a.d1.table, a.grid, g.edge_pair[e] >> 16, rr);
+                const double* x = g.xyz + 3 * static_cast<size_t>(e);
+                out[0] = static_cast<double>(d * static_cast<float>(x[0] / rr));
+                out[1] = static_cast<double>(d * static_cast<float>(x[1] / rr));
+                out[2] = static_cast<double>(d * static_cast<float>(x[2] / rr));
             }
         }
         __syncthreads();
@@ -437,9 +500,8 @@ r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
             for (int w = 0; w < nwaves; ++w)
                 for (int c = 0; c < 3; ++c) f[c] += static_cast<double>(s_f[t][w][c]);
             double* out = forces + 3 * static_cast<size_t>(s_eid[t]);
-            out[0] = f[0];
-            out[1] = f[1];
-            out[2] = f[2];
+#pragma unroll
+            for (int c = 0; c < 3; ++c) out[c] = f[c] + static_cast<double>(s_dsc[t] * s_geo[t][c]);
         }
     }
 }
@@ -448,6 +510,7 @@ r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
 // ---------------------------------------------------------------------------
 template <int LMAX>
 __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const float* __restrict__ r0f,
+                                                          const float* __restrict__ A0,
                                                           const float* __restrict__ A0_adj,
                                                           double* __restrict__ forces)
 {
@@ -459,6 +522,7 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
     __shared__ int s_row[kTile];
     __shared__ int s_eid[kTile];
     __shared__ float s_f[kTile][kMaxWaves][3];
+    __shared__ float s_dsc[kTile];  // A0 density-scale force coefficient per active slot
     __shared__ int s_count;
 
     const int i = receiver_of_block(a);
@@ -480,14 +544,39 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
         for (int lm = 0; lm < NLM; ++lm) adj[lm] = 0.0f;
     }
     const int e0 = g.first[i], e1 = g.first[i + 1];
+    // reverse_A0_scaled: dcoef = (A0_adj . A0) / s for the edge terms, adj /= s
+    float dcoef = 0.0f;
+    if (a.d0.table) {
+        __shared__ float s_red[1 + kMaxWaves];
+        if (threadIdx.x < 64) {
+            const float sc = density_scale(a.d0, g, a.grid, e0, e1);
+            if (threadIdx.x == 0) s_red[0] = sc;
+        }
+        float p = 0.0f;
+        if (k < C) {
+            const float* f = A0 + static_cast<size_t>(i - a.local_base) * NLM * C + k;
+#pragma unroll
+            for (int lm = 0; lm < NLM; ++lm) p = fmaf(adj[lm], f[lm * C], p);
+        }
+        p = wave_sum_dpp(p);
+        if (lane == 0) s_red[1 + wave] = p;
+        __syncthreads();
+        const float sc = s_red[0];
+        float dot = 0.0f;
+        for (int w = 0; w < nwaves; ++w) dot += s_red[1 + w];
+        dcoef = dot / sc;
+#pragma unroll
+        for (int lm = 0; lm < NLM; ++lm) adj[lm] /= sc;
+    }
     for (int base = e0; base < e1; base += kTile) {
         __syncthreads();
         if (threadIdx.x < 64) {
             const int t = threadIdx.x;
             double rr;
-            const TileSlot ts = compact_edge(g, a.grid, base, min(kTile, e1 - base), t, rr, &s_count);
+            const int n = min(kTile, e1 - base);
+            const TileSlot ts = compact_edge(g, a.grid, base, n, t, rr, &s_count);
+            const int e = base + t;
             if (ts.active) {
-                const int e = base + t;
                 int iv;
                 float x;
                 const int sl = ts.slot;
@@ -497,6 +586,15 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
                 s_geo[sl][3] = x;
                 s_row[sl] = (g.edge_pair[e] & 0xffff) * a.grid.intervals + iv;
                 s_eid[sl] = e;
+                s_dsc[sl] = a.d0.table ? dcoef * density_slope(a.d0.table, a.grid, g.edge_pair[e] >> 16, rr) : 0.0f;
+            } else if (t < n && a.d0.table) {
+                // beyond r_cut: only the density-scale term (reverse_A0_scaled visits every neighbour)
+                const float d = dcoef * density_slope(a.d0.table, a.grid, g.edge_pair[e] >> 16, rr);
+                const double* x = g.xyz + 3 * static_cast<size_t>(e);
+                double* out = forces + 3 * static_cast<size_t>(e);
+                out[0] += static_cast<double>(d * static_cast<float>(x[0] / rr));
+                out[1] += static_cast<double>(d * static_cast<float>(x[1] / rr));
+                out[2] += static_cast<double>(d * static_cast<float>(x[2] / rr));
             }
         }
         __syncthreads();
@@ -547,9 +645,8 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
             for (int w = 0; w < nwaves; ++w)
                 for (int c = 0; c < 3; ++c) f[c] += static_cast<double>(s_f[t][w][c]);
             double* out = forces + 3 * static_cast<size_t>(s_eid[t]);
-            out[0] += f[0];
-            out[1] += f[1];
-            out[2] += f[2];
+#pragma unroll
+            for (int c = 0; c < 3; ++c) out[c] += f[c] + static_cast<double>(s_dsc[t] * s_geo[t][c]);
         }
     }
 }
@@ -760,6 +857,54 @@ __global__ void __launch_bounds__(256) totals_final_kernel(int num_partials,
     if (t < 10) out[t] = s[0][t];
 }
 
+// ZBL pair term of every neighbour (zbl_kokkos.cpp:76-126, 154-201): one wave
+// per receiver, lanes over its edges; the energy partial sums are combined
+// by a fixed butterfly, so the result does not depend on scheduling.
+__global__ void __launch_bounds__(256) zbl_kernel(int N, const int* __restrict__ first,
+                                                  const int* __restrict__ edge_pair, const double* __restrict__ xyz,
+                                                  const double* __restrict__ r, ZblArgs z,
+                                                  double* __restrict__ energies, double* __restrict__ forces)
+{
+    const int lane = threadIdx.x & 63;
+    const int i = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (i >= N) return;
+    const int p = z.p;
+    const double k0 = (p + 1.0) * (p + 2.0) / 2.0, k1 = p * (p + 2.0), k2 = p * (p + 1.0) / 2.0;
+    double energy = 0.0;
+    for (int e = first[i] + lane; e < first[i + 1]; e += 64) {
+        const int po = edge_pair[e] & 0xffff;
+        const double rr = r[e];
+        const double r_max = z.r_max[po];
+        if (rr >= r_max) continue;
+        const double inverse_a = z.inverse_a[po];
+        const double r_over_a = rr * inverse_a;
+        const double e0 = z.c[0] * exp(-3.2 * r_over_a);
+        const double e1 = z.c[1] * exp(-0.9423 * r_over_a);
+        const double e2 = z.c[2] * exp(-0.4028 * r_over_a);
+        const double e3 = z.c[3] * exp(-0.2016 * r_over_a);
+        const double phi = e0 + e1 + e2 + e3;
+        const double dphi = inverse_a * (-3.2 * e0 - 0.9423 * e1 - 0.4028 * e2 - 0.2016 * e3);
+        const double inverse_r = 1.0 / rr;
+        const double bare = z.prefactor[po] * inverse_r * phi;
+        const double bare_gradient = z.prefactor[po] * inverse_r * inverse_r * (rr * dphi - phi);
+        const double x = rr / r_max;
+        double xpm1 = 1.0;
+        for (int q = 0; q < p - 1; ++q) xpm1 *= x;
+        const double xp = xpm1 * x, xp1 = xp * x, xp2 = xp1 * x;
+        const double envelope = 1.0 - k0 * xp + k1 * xp1 - k2 * xp2;
+        const double envelope_gradient = (-k0 * p * xpm1 + k1 * (p + 1.0) * xp - k2 * (p + 2.0) * xp1) / r_max;
+        energy += 0.5 * bare * envelope;
+        const double gradient = 0.5 * (bare * envelope_gradient + bare_gradient * envelope);
+        double* f = forces + 3 * static_cast<size_t>(e);
+        const double* v = xyz + 3 * static_cast<size_t>(e);
+        f[0] -= v[0] / rr * gradient;
+        f[1] -= v[1] / rr * gradient;
+        f[2] -= v[2] / rr * gradient;
+    }
+    for (int off = 32; off > 0; off >>= 1) energy += __shfl_xor(energy, off, 64);
+    if (lane == 0) energies[i] += energy;
+}
+
 inline int node_threads(int C) { return ((C + 63) / 64) * 64; }
 
 }  // namespace
@@ -779,14 +924,14 @@ hipError_t launch_a0_forward(const LayerArgs& a, const float* r0f, float* A0, hi
     return hipGetLastError();
 }
 
-hipError_t launch_a0_reverse(const LayerArgs& a, const float* r0f, const float* A0_adj,
+hipError_t launch_a0_reverse(const LayerArgs& a, const float* r0f, const float* A0, const float* A0_adj,
                              double* forces, hipStream_t s)
 {
     if (a.node_count <= 0) return hipSuccess;
     const int threads = node_threads(a.C);
     switch (a.l_max) {
-    case 2: a0_reverse_kernel<2><<<a.node_count, threads, 0, s>>>(a, r0f, A0_adj, forces); break;
-    case 3: a0_reverse_kernel<3><<<a.node_count, threads, 0, s>>>(a, r0f, A0_adj, forces); break;
+    case 2: a0_reverse_kernel<2><<<a.node_count, threads, 0, s>>>(a, r0f, A0, A0_adj, forces); break;
+    case 3: a0_reverse_kernel<3><<<a.node_count, threads, 0, s>>>(a, r0f, A0, A0_adj, forces); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -875,6 +1020,14 @@ hipError_t launch_add_direct(int nodes, int C, int num_LM, const float* direct, 
     if (n == 0) return hipSuccess;
     add_direct_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(nodes, C, num_LM, direct,
                                                                             M0_adj);
+    return hipGetLastError();
+}
+
+hipError_t launch_zbl(int num_nodes, const int* first, const int* edge_pair, const double* xyz, const double* r,
+                      const ZblArgs& z, double* energies, double* forces, hipStream_t s)
+{
+    if (num_nodes <= 0) return hipSuccess;
+    zbl_kernel<<<(num_nodes + 3) / 4, 256, 0, s>>>(num_nodes, first, edge_pair, xyz, r, z, energies, forces);
     return hipGetLastError();
 }
 

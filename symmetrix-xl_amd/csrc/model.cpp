@@ -115,15 +115,22 @@ Value select_head(Value data, const std::string& requested, std::string& selecte
     return data;
 }
 
+// Compact radial network (compact_radial.cpp:12-52, 172-194): SiLU MLP
+// without biases; only the A0/A1 density networks carry the tanh-square
+// postprocess.
 RadialNetwork parse_network(const Value& def, const std::string& name, int inputs)
 {
     RadialNetwork net;
     net.shape = def.at("shape").ints(name + " shape");
+    const Value* post = def.find("postprocess");
+    const std::string postprocess = post && post->kind == Value::Kind::string ? post->str : std::string();
+    require(!post || post->kind == Value::Kind::string,
+            "Compact radial network " + name + " has unsupported postprocessing.");
+    require(postprocess.empty() || postprocess == "tanh-square",
+            "Compact radial network " + name + " has unsupported postprocessing.");
+    net.tanh_square = postprocess == "tanh-square";
     require(def.at("activation").as_string() == "silu",
             "Compact radial network " + name + " must use SiLU.");
-    const Value* post = def.find("postprocess");
-    require(!post || (post->kind == Value::Kind::string && post->str.empty()),
-            "Compact radial R0/R1 networks cannot use postprocessing.");
     net.activation_scale = def.at("activation_scale").as_number();
     require(std::isfinite(net.activation_scale) && net.activation_scale > 0.0,
             "Compact radial network " + name + " has an invalid activation scale.");
@@ -197,7 +204,24 @@ HostModel HostModel::load(const std::string& path, const std::string& head)
     require(static_cast<int>(m.atomic_numbers.size()) == ne,
             "atomic_numbers does not match num_elements.");
 
-    require(!file.at("has_zbl").as_bool("has_zbl"), "ZBL pair repulsion is not supported yet.");
+    // ZBL (mace_kokkos_model.cpp:190-198, zbl_kokkos.cpp:12-56)
+    m.has_zbl = file.at("has_zbl").as_bool("has_zbl");
+    if (m.has_zbl) {
+        m.zbl_a_exp = file.at("zbl_a_exp").as_number("zbl_a_exp");
+        m.zbl_a_prefactor = file.at("zbl_a_prefactor").as_number("zbl_a_prefactor");
+        const std::vector<double> c = numbers(file.at("zbl_c"), "zbl_c", static_cast<std::size_t>(-1));
+        require(c.size() == 4, "ZBL requires four screening coefficients");
+        for (int q = 0; q < 4; ++q) m.zbl_c[q] = c[q];
+        m.zbl_radii = numbers(file.at("zbl_covalent_radii"), "zbl_covalent_radii", static_cast<std::size_t>(-1));
+        require(!m.zbl_radii.empty(), "ZBL requires at least one covalent radius");
+        require(m.zbl_a_prefactor > 0.0, "ZBL screening prefactor must be positive");
+        m.zbl_p = file.at("zbl_p").as_int("zbl_p");
+        require(m.zbl_p >= 1, "ZBL envelope power must be positive");
+        require(std::isfinite(m.zbl_a_exp), "ZBL has an invalid screening exponent");
+        for (int z : m.atomic_numbers)
+            require(z >= 0 && z < static_cast<int>(m.zbl_radii.size()),
+                    "ZBL covalent radii do not cover the model's atomic numbers");
+    }
     const Value* hf = file.find("has_field_coupling");
     require(!(hf && hf->as_bool()), "MACEField coupling is not supported.");
     const Value* fr = file.find("first_interaction_residual");
@@ -252,19 +276,43 @@ HostModel HostModel::load(const std::string& path, const std::string& head)
             "Compact radial model has invalid cutoff data.");
     require(std::abs(m.cutoff_rmax - m.r_cut) <= 1e-12,
             "Compact radial cutoff does not match model r_cut.");
-    require(cr.at("distance_transform").at("type").as_string() == "none",
-            "Only distance_transform 'none' is supported yet.");
+    const Value& transform = cr.at("distance_transform");
+    const std::string transform_type = transform.at("type").as_string();
+    m.agnesi = transform_type == "agnesi";
+    if (m.agnesi) {
+        m.agnesi_a = transform.at("a").as_number();
+        m.agnesi_q = transform.at("q").as_number();
+        m.agnesi_p = transform.at("p").as_number();
+        m.agnesi_radii = numbers(transform.at("covalent_radii"), "covalent_radii", static_cast<std::size_t>(-1));
+        require(static_cast<int>(m.agnesi_radii.size()) == ne,
+                "Compact radial covalent radii do not match atomic numbers.");
+        bool ok = std::isfinite(m.agnesi_a) && std::isfinite(m.agnesi_q) && std::isfinite(m.agnesi_p);
+        for (double v : m.agnesi_radii) ok = ok && std::isfinite(v) && v > 0.0;
+        require(ok, "Compact radial model has invalid Agnesi data.");
+    } else {
+        require(transform_type == "none", "Compact radial model has an unsupported distance transform.");
+    }
     const Value& nets = cr.at("networks");
     const int nb = static_cast<int>(m.bessel_weights.size());
     m.R0 = parse_network(nets.at("R0"), "R0", nb);
     require(nets.contains("R1"), "Compact radial R1 network does not match the MACE interaction count.");
     m.R1 = parse_network(nets.at("R1"), "R1", nb);
-    require(!nets.contains("A0") && !nets.contains("A1"),
-            "Density-normalised (A0/A1 scaled) models are not supported yet.");
+    require(!m.R0.tanh_square && !m.R1.tanh_square, "Compact radial R0/R1 networks cannot use postprocessing.");
+    auto density_network = [&](const char* name, RadialNetwork& net) {
+        net = parse_network(nets.at(name), name, nb);
+        require(net.shape.back() == 1 && net.tanh_square,
+                std::string("Compact radial ") + name + " network has an invalid shape or postprocessing.");
+    };
     const Value* a0s = file.find("A0_scaled");
     const Value* a1s = file.find("A1_scaled");
-    require(!(a0s && a0s->as_bool()) && !(a1s && a1s->as_bool()),
-            "Density-normalised (A0/A1 scaled) models are not supported yet.");
+    require(a0s != nullptr, "MACE model is missing A0_scaled.");
+    m.A0_scaled = a0s->as_bool();
+    m.A1_scaled = a1s && a1s->as_bool();
+    require(m.A0_scaled == nets.contains("A0"), "Compact radial A0 network does not match A0_scaled.");
+    require(m.A1_scaled == nets.contains("A1"), "Compact radial A1 network does not match A1_scaled.");
+    if (m.A0_scaled) density_network("A0", m.A0net);
+    if (m.A1_scaled) density_network("A1", m.A1net);
+
     require(m.R0.shape.back() == (m.l_max + 1) * C, "Compact radial R0 output has an invalid size.");
 
     m.H0 = numbers(file.at("H0_weights"), "H0_weights", static_cast<std::size_t>(ne) * C);
@@ -360,9 +408,10 @@ HostModel HostModel::load(const std::string& path, const std::string& head)
 }
 
 // Compact radial tabulation (compact_radial.cpp:227-370): Bessel features with
-// the polynomial cutoff on the knots, the SiLU MLP, and knot derivatives from
-// the tridiagonal rule with a not-a-knot-like left end and a zero derivative
-// at r_cut.
+// the polynomial cutoff on the knots (of the Agnesi-transformed distance when
+// the model has that transform), the SiLU MLP (tanh(y^2) on the output of a
+// density network), and knot derivatives from the tridiagonal rule with a
+// not-a-knot-like left end and a zero derivative at r_cut.
 void HostModel::radial_tables(const RadialNetwork& net, int type_i, int type_j,
                               std::vector<double>& values, std::vector<double>& derivs) const
 {
@@ -371,8 +420,14 @@ void HostModel::radial_tables(const RadialNetwork& net, int type_i, int type_j,
     const int P = spline_points;
     const int nb = static_cast<int>(bessel_weights.size());
     std::vector<double> layer(static_cast<std::size_t>(P) * nb);
+    const double r0 = agnesi ? 0.5 * (agnesi_radii[type_i] + agnesi_radii[type_j]) : 1.0;
     for (int node = 0; node < P; ++node) {
         const double r = grid_min + node * spline_h;
+        double t = r;
+        if (agnesi) {
+            const double s = r / r0;
+            t = 1.0 / (1.0 + agnesi_a * std::pow(s, agnesi_q) / (1.0 + std::pow(s, agnesi_q - agnesi_p)));
+        }
         double cutoff_value = 0.0;
         if (r < cutoff_rmax) {
             const double s = r / cutoff_rmax;
@@ -383,7 +438,7 @@ void HostModel::radial_tables(const RadialNetwork& net, int type_i, int type_j,
         }
         for (int b = 0; b < nb; ++b)
             layer[static_cast<std::size_t>(node) * nb + b] =
-                bessel_prefactor * std::sin(bessel_weights[b] * r) / r * cutoff_value;
+                bessel_prefactor * std::sin(bessel_weights[b] * t) / t * cutoff_value;
     }
     int width = nb;
     for (std::size_t l = 0; l < net.weights.size(); ++l) {
@@ -407,6 +462,8 @@ void HostModel::radial_tables(const RadialNetwork& net, int type_i, int type_j,
         width = out;
     }
     const int F = width;
+    if (net.tanh_square)
+        for (double& v : layer) v = std::tanh(v * v);
     values.assign(static_cast<std::size_t>(F) * P, 0.0);
     derivs.assign(static_cast<std::size_t>(F) * P, 0.0);
     const int U = P - 2;

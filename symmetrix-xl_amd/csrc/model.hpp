@@ -19,6 +19,7 @@ struct RadialNetwork {
     std::vector<int> shape;
     std::vector<std::vector<double>> weights;  // [layer] row-major [out][in]
     double activation_scale = 1.0;
+    bool tanh_square = false;  // output postprocess tanh(y^2) (A0/A1 density networks)
 };
 
 struct HostModel {
@@ -39,7 +40,22 @@ struct HostModel {
     double bessel_prefactor = 0.0;
     double cutoff_rmax = 0.0;
     int cutoff_p = 0;
+    // Agnesi distance transform of the radial features (compact_radial.cpp:150-170, 238-247)
+    bool agnesi = false;
+    double agnesi_a = 0.0, agnesi_q = 0.0, agnesi_p = 0.0;
+    std::vector<double> agnesi_radii;  // [ne] covalent radius per element type
     RadialNetwork R0, R1;
+    // density normalisation: A0 /= 1 + sum_j A0net(r_ij), same for A1
+    // (mace.cpp:1561-1636, 2380-2458); one-output tanh-square networks
+    bool A0_scaled = false, A1_scaled = false;
+    RadialNetwork A0net, A1net;
+
+    // ZBL pair repulsion (zbl_kokkos.cpp:12-126)
+    bool has_zbl = false;
+    double zbl_a_exp = 0.0, zbl_a_prefactor = 0.0;
+    double zbl_c[4] = {};
+    std::vector<double> zbl_radii;  // indexed by atomic number
+    int zbl_p = 0;
 
     std::vector<double> H0;   // [ne][C]
     std::vector<double> A0W;  // [ne][l_max+1][C][C]  ([in][out])

@@ -342,6 +342,7 @@ __global__ void __launch_bounds__(256) m0_reverse_kernel(LayerArgs a, PolyArgs p
 // ---------------------------------------------------------------------------
 constexpr int kReadoutGroup = 4;  // nodes held in registers by the polynomial phases
 constexpr int kMaxHidden = 64;
+constexpr int kMaxWavesReadout = 4;  // 256 threads
 
 template <class P1, int NB>
 __global__ void __launch_bounds__(256) readout_kernel(ReadoutArgs a)
@@ -370,6 +371,11 @@ __global__ void __launch_bounds__(256) readout_kernel(ReadoutArgs a)
                                 a.p1.stride * C * 4);
     const int voff = kk * 4;
 
+    // A1 density scale of each node (compute_A1_scaled, mace.cpp:2381-2402)
+    float dscale[NB];
+#pragma unroll
+    for (int n = 0; n < NB; ++n) dscale[n] = (a.a1_scale && node[n] >= 0) ? a.a1_scale[node[n]] : 1.0f;
+
     // 1. M1 and the scalar M0 block
 #pragma unroll
     for (int g0 = 0; g0 < NB; g0 += G) {
@@ -380,6 +386,10 @@ __global__ void __launch_bounds__(256) readout_kernel(ReadoutArgs a)
             const float* in = a.A1 + static_cast<size_t>(max(i - a.local_base, 0)) * NIN * C + kk;
 #pragma unroll
             for (int v = 0; v < NIN; ++v) x[n][v] = i >= 0 ? in[v * C] : 0.0f;
+            if (a.a1_scale) {
+#pragma unroll
+                for (int v = 0; v < NIN; ++v) x[n][v] /= dscale[g0 + n];
+            }
             m1[n][0] = 0.0f;
         }
         core_value<P1, G>(cs, voff, C, x, m1);
@@ -505,7 +515,10 @@ __global__ void __launch_bounds__(256) readout_kernel(ReadoutArgs a)
             if (node[n] >= 0) a.direct[static_cast<size_t>(node[n]) * C + k] = d[n];
     }
 
-    // 6. A1 adjoint
+    // 6. A1 adjoint; for a scaled model also A1_adj . A1 per node and the
+    //    adjoint of the unscaled A1 (reverse_A1_scaled, mace.cpp:2404-2458)
+    __shared__ float s_dot[kMaxWavesReadout][NB];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 #pragma unroll
     for (int g0 = 0; g0 < NB; g0 += G) {
         float x[G][NIN], lam[G][1], g[G][NIN];
@@ -518,11 +531,27 @@ __global__ void __launch_bounds__(256) readout_kernel(ReadoutArgs a)
                 x[n][v] = i >= 0 ? in[v * C] : 0.0f;
                 g[n][v] = 0.0f;
             }
+            if (a.a1_scale) {
+#pragma unroll
+                for (int v = 0; v < NIN; ++v) x[n][v] /= dscale[g0 + n];
+            }
             lam[n][0] = m1adj[g0 + n];
         }
         core_gradient<P1, G>(cs, voff, C, x, lam, g);
         if (a.p1.num_rem > 0)
             rem_gradient_nodes<P1, G>(a.p1, cs, voff, C, s_rem + k, s_rem + NIN * T + k, T, x, lam, g);
+        if (a.a1_scale) {
+#pragma unroll
+            for (int n = 0; n < G; ++n) {
+                float p = 0.0f;
+                if (ok) {
+#pragma unroll
+                    for (int v = 0; v < NIN; ++v) p = fmaf(g[n][v], x[n][v], p);
+                }
+                p = wave_sum_dpp(p);
+                if (lane == 0) s_dot[wave][g0 + n] = p;
+            }
+        }
         if (ok) {
 #pragma unroll
             for (int n = 0; n < G; ++n) {
@@ -530,8 +559,17 @@ __global__ void __launch_bounds__(256) readout_kernel(ReadoutArgs a)
                 if (i < 0) continue;
                 float* out = a.A1_adj + static_cast<size_t>(i - a.local_base) * NIN * C + k;
 #pragma unroll
-                for (int v = 0; v < NIN; ++v) out[v * C] = g[n][v];
+                for (int v = 0; v < NIN; ++v) out[v * C] = a.a1_scale ? g[n][v] / dscale[g0 + n] : g[n][v];
             }
+        }
+    }
+    if (a.a1_scale) {
+        __syncthreads();
+        if (threadIdx.x < blk.count) {
+            const int n = threadIdx.x;
+            float dot = 0.0f;
+            for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) dot += s_dot[w][n];
+            a.a1_dot[a.nodes.order[blk.start + n]] = dot;
         }
     }
 }

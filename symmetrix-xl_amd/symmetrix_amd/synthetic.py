@@ -45,8 +45,29 @@ class ModelShape:
     readout_hidden: int = 16
     energy_scale: float = 10.0
     m1_correlation: int | None = None
+    zbl: bool = False            # ZBL pair repulsion (has_zbl)
+    density: tuple = ()          # density-normalised layers: subset of ("A0", "A1")
+    agnesi: bool = False         # Agnesi distance transform of the radial features
     extra: dict = field(default_factory=dict)
 
+
+# Single-bond covalent radii (A) by atomic number, Z = 0..89, of Cordero et al.,
+# Dalton Trans. (2008) 2832 (index 0 is a placeholder); the ZBL envelope and
+# the Agnesi transform of a synthetic model take their radii from here.
+COVALENT_RADII = (
+    0.20, 0.31, 0.28, 1.28, 0.96, 0.84, 0.76, 0.71, 0.66, 0.57, 0.58, 1.66, 1.41, 1.21, 1.11, 1.07,
+    1.05, 1.02, 1.06, 2.03, 1.76, 1.70, 1.60, 1.53, 1.39, 1.39, 1.32, 1.26, 1.24, 1.32, 1.22, 1.22,
+    1.20, 1.19, 1.20, 1.20, 1.16, 2.20, 1.95, 1.90, 1.75, 1.64, 1.54, 1.47, 1.46, 1.42, 1.39, 1.45,
+    1.44, 1.42, 1.39, 1.39, 1.38, 1.39, 1.40, 2.44, 2.15, 2.07, 2.04, 2.03, 2.01, 1.99, 1.98, 1.98,
+    1.96, 1.94, 1.92, 1.92, 1.89, 1.90, 1.87, 1.87, 1.75, 1.70, 1.62, 1.51, 1.44, 1.41, 1.36, 1.36,
+    1.32, 1.45, 1.46, 1.48, 1.40, 1.50, 1.50, 2.60, 2.21, 2.15,
+)
+# ZBL screening constants of the MACE ZBL basis (universal screening function
+# coefficients, a = 0.4543 * 0.529 / (Zu^0.3 + Zv^0.3)) and envelope power
+ZBL_C = (0.1818, 0.5099, 0.2802, 0.02817)
+ZBL_A_EXP, ZBL_A_PREFACTOR, ZBL_P = 0.3, 0.4543, 6
+# Agnesi transform parameters of the MACE Agnesi distance transform
+AGNESI_A, AGNESI_Q, AGNESI_P = 1.0805, 0.9183, 4.5791
 
 PRESETS = {
     # 3 elements, 32x0e+32x1o, lmax 2, correlation 2.
@@ -179,6 +200,15 @@ def random_mace_model(shape: ModelShape | str = "tiny", seed: int = 0) -> dict:
             "activation_scale": SILU_NORMALIZATION,
         },
     }
+    for name in shape.density:
+        if name not in ("A0", "A1"):
+            raise ValueError(f"unknown density-normalised layer {name!r}")
+        networks[name] = {
+            "shape": [radial_in, hidden[0], 1],
+            "activation": "silu",
+            "activation_scale": SILU_NORMALIZATION,
+            "postprocess": "tanh-square",
+        }
     for net in networks.values():
         net["weights"] = mlp(net["shape"])
 
@@ -212,7 +242,11 @@ def random_mace_model(shape: ModelShape | str = "tiny", seed: int = 0) -> dict:
                 "prefactor": float(math.sqrt(2.0 / shape.r_cut)),
             },
             "cutoff": {"type": "polynomial", "r_max": float(shape.r_cut), "p": shape.cutoff_p},
-            "distance_transform": {"type": "none"},
+            "distance_transform": (
+                {"type": "agnesi", "a": AGNESI_A, "q": AGNESI_Q, "p": AGNESI_P,
+                 "covalent_radii": [COVALENT_RADII[zz] for zz in z]}
+                if shape.agnesi else {"type": "none"}
+            ),
             "networks": networks,
         },
         "H0_weights": _Array(rng.normal(size=(ne, C))),
@@ -220,7 +254,7 @@ def random_mace_model(shape: ModelShape | str = "tiny", seed: int = 0) -> dict:
             [_Array(rng.normal(size=(C, C)) / (math.sqrt(C) * avg)) for _ in range(lmax + 1)]
             for _ in range(ne)
         ],
-        "A0_scaled": False,
+        "A0_scaled": "A0" in shape.density,
         "M0_monomials": m0_monomials,
         "M0_weights": {
             str(a): {lm: {str(k): _Array(m0_w[a][lm][k]) for k in range(C)} for lm in m0_monomials}
@@ -237,7 +271,7 @@ def random_mace_model(shape: ModelShape | str = "tiny", seed: int = 0) -> dict:
             _Array(rng.normal(size=(num_e[l] * C, C)) / (math.sqrt(num_e[l] * C) * avg))
             for l in range(lmax + 1)
         ],
-        "A1_scaled": False,
+        "A1_scaled": "A1" in shape.density,
         "M1_monomials": m1_monomials["0"],
         "M1_weights": {
             str(a): {str(k): _Array(m1_w[a]["0"][k]) for k in range(C)} for a in range(ne)
@@ -257,6 +291,11 @@ def random_mace_model(shape: ModelShape | str = "tiny", seed: int = 0) -> dict:
         ),
         "readout_2_scale_factor": SILU_NORMALIZATION,
     }
+    if shape.zbl:
+        model.update({
+            "has_zbl": True, "zbl_a_exp": ZBL_A_EXP, "zbl_a_prefactor": ZBL_A_PREFACTOR,
+            "zbl_c": list(ZBL_C), "zbl_covalent_radii": list(COVALENT_RADII), "zbl_p": ZBL_P,
+        })
     model.update(shape.extra)
     return model
 

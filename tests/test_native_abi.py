@@ -57,7 +57,13 @@ def test_missing_model_file_is_invalid_argument():
     [
         ({"symmetrix_format_version": 2}, "format version 4"),
         ({"h1_affine_mode": "other"}, "h1_affine_mode"),
-        ({"has_zbl": True}, "ZBL"),
+        ({"has_zbl": True}, "zbl_a_exp"),
+        ({"has_zbl": True, "zbl_a_exp": 0.3, "zbl_a_prefactor": 0.4543, "zbl_c": [0.2, 0.5, 0.3],
+          "zbl_covalent_radii": [0.5] * 100, "zbl_p": 6}, "four screening coefficients"),
+        ({"has_zbl": True, "zbl_a_exp": 0.3, "zbl_a_prefactor": 0.4543, "zbl_c": [0.2, 0.5, 0.3, 0.0],
+          "zbl_covalent_radii": [0.5] * 10, "zbl_p": 6}, "do not cover"),
+        ({"A0_scaled": True}, "A0 network does not match A0_scaled"),
+        ({"A1_scaled": True}, "A1 network does not match A1_scaled"),
         ({"radial_representation": "pair-splines"}, "compact radial"),
         ({"l_max": 5}, "L_max <= l_max <= 3"),
         ({"readout_1_weights": [0.0]}, "old-basis"),
@@ -68,6 +74,28 @@ def test_model_validation_errors(tmp_path, change, message):
 
     model = json.loads(synthetic.model_json(synthetic.random_mace_model("tiny", seed=0)))
     model.update(change)
+    path = tmp_path / "m.json"
+    path.write_text(json.dumps(model))
+    status, msg = _create(str(path))
+    assert status == 1, msg
+    assert message in msg
+
+
+@pytest.mark.parametrize(
+    "edit, message",
+    [
+        (lambda cr: cr["distance_transform"].update({"type": "exponential"}), "unsupported distance transform"),
+        (lambda cr: cr["distance_transform"].update({"type": "agnesi", "a": 1.0, "q": 0.9, "p": 4.5,
+                                                     "covalent_radii": [1.0]}), "covalent radii do not match"),
+        (lambda cr: cr["networks"]["R0"].update({"postprocess": "tanh-square"}), "cannot use postprocessing"),
+        (lambda cr: cr["networks"]["R1"].update({"postprocess": "cube"}), "unsupported postprocessing"),
+    ],
+)
+def test_compact_radial_validation_errors(tmp_path, edit, message):
+    from symmetrix_amd import synthetic
+
+    model = json.loads(synthetic.model_json(synthetic.random_mace_model("tiny", seed=0)))
+    edit(model["compact_radial"])
     path = tmp_path / "m.json"
     path.write_text(json.dumps(model))
     status, msg = _create(str(path))

@@ -3,6 +3,11 @@ differences of its own energy (the reference method,
 symmetrix/test/test_mace.py:687-750, rtol 1e-4 / atol 1e-6 in FP64), global
 invariances, FP32 vs FP64 (reference test_mace_streamed_edges.py:556, atol
 3e-5), and skin-masked vs exact graphs (reference :4592-4675).
+
+Every test runs on the plain tiny model and on one with the optional terms of
+the format (ZBL pair repulsion, A0 and A1 density normalisation, Agnesi
+distance transform), so their reverse passes are pinned by the same finite
+differences and invariances.
 """
 
 import json
@@ -11,11 +16,16 @@ import numpy as np
 import pytest
 
 
-@pytest.fixture(scope="module")
-def tiny():
+@pytest.fixture(scope="module", params=["plain", "zbl+density+agnesi"])
+def tiny(request):
+    import dataclasses
+
     from symmetrix_amd import synthetic
 
-    return json.loads(synthetic.model_json(synthetic.random_mace_model("tiny", seed=0)))
+    shape = synthetic.PRESETS["tiny"]
+    if request.param != "plain":
+        shape = dataclasses.replace(shape, zbl=True, density=("A0", "A1"), agnesi=True)
+    return json.loads(synthetic.model_json(synthetic.random_mace_model(shape, seed=0)))
 
 
 @pytest.fixture(scope="module")
@@ -128,6 +138,6 @@ def test_skin_masked_graph_equals_exact_graph(oracle_lib, tiny, structure):
 
 def test_rejects_unsupported_models(oracle_lib, tiny, structure):
     bad = dict(tiny)
-    bad["has_zbl"] = True
+    bad["h1_affine_mode"] = "pre_linear_up"
     with pytest.raises(NotImplementedError):
         make(oracle_lib, bad, structure)
