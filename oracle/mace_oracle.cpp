@@ -13,7 +13,9 @@
 //   compute_Phi1_streamed                         mace.cpp:2022-2083
 //   compute_A1 / reverse_A1                       mace.cpp:2304-2378
 //   compute_M1 / reverse_M1                       mace.cpp:2460-2513
-//   compute_H2 / reverse_H2 (m0_composite)        mace.cpp:2515-2619
+//   compute_H2 / reverse_H2 (format 4)            mace.cpp:2515-2619
+//   pre_linear_up scalar, first-interaction residual
+//                                                 mace.cpp:1759-1813, 1845-1875
 //   compute_readouts                              mace.cpp:2621-2657
 //   reverse_Phi1_streamed                         mace.cpp:2198-2302
 //   reverse_A0_streamed                           mace.cpp:1485-1559
@@ -106,6 +108,13 @@ struct Spec {
     int A1_scaled;
     const double* a1s_values;
     const double* a1s_derivs;
+    // pre_linear_up basis: readout_1 / skip act on x = M0_scalar P0 (+ residual)
+    int pre_linear_up;
+    const double* H1P0;            // [C][C] ([in][out]) H1_product_weights, l = 0 block
+    // first-interaction residual: H1 += fused (residual U), x += residual scalar block
+    int first_residual;
+    const double* residual;        // [ne][nLM][C]
+    const double* residual_fused;  // [ne][nLM][C]
 };
 
 template <typename P>
@@ -255,6 +264,8 @@ struct Oracle {
     std::vector<int> type_to_active;
     std::vector<SplineSet<P>> spl0, spl1;
     std::vector<P> H0, A0W, H1W, H2M0, H2M1, q, W1, W2;
+    bool pre_linear_up = false, first_residual = false;
+    std::vector<P> P0, residual, residual_fused;
     int hidden;
     P scale;
     std::vector<double> E0;
@@ -341,6 +352,13 @@ struct Oracle {
         H2M0 = conv(s.H2M0, static_cast<size_t>(ne) * C * C);
         H2M1 = conv(s.H2M1, static_cast<size_t>(C) * C);
         q = conv(s.readout_q, C);
+        pre_linear_up = s.pre_linear_up != 0;
+        if (pre_linear_up) P0 = conv(s.H1P0, static_cast<size_t>(C) * C);
+        first_residual = s.first_residual != 0;
+        if (first_residual) {
+            residual = conv(s.residual, static_cast<size_t>(ne) * nLM * C);
+            residual_fused = conv(s.residual_fused, static_cast<size_t>(ne) * nLM * C);
+        }
         hidden = s.readout_hidden;
         W1 = conv(s.readout_w1, static_cast<size_t>(hidden) * C);
         W2 = conv(s.readout_w2, hidden);
@@ -597,9 +615,35 @@ struct Oracle {
             }
         }
 
-        // ---- compute_H1 (m0_composite scalar = M0 block l=0) ----
+        // ---- compute_H1, capture_h1_affine_scalar, add_H1_first_residual
+        // (mace.cpp:1690-1783, 1845-1875): H1 = M0 H1_W (+ fused residual of
+        // the node's element); readout input x = M0 scalar block
+        // (m0_composite) or M0_scalar P0 (+ residual scalar block) ----
         std::vector<P> H1(static_cast<size_t>(N) * nLM * C);
         gemm_blocks(N, nLM, Lmax, M0.data(), H1W.data(), H1.data(), false);
+        if (first_residual)
+            for (int i = 0; i < N; ++i) {
+                const P* res = residual_fused.data() + static_cast<size_t>(types[i]) * nLM * C;
+                P* h = H1.data() + static_cast<size_t>(i) * nLM * C;
+                for (int j = 0; j < nLM * C; ++j) h[j] += res[j];
+            }
+        std::vector<P> xs_pre;
+        if (pre_linear_up) {
+            xs_pre.assign(static_cast<size_t>(N) * C, P(0));
+            for (int i = 0; i < N; ++i) {
+                const P* m0 = M0.data() + static_cast<size_t>(i) * nLM * C;
+                P* x = xs_pre.data() + static_cast<size_t>(i) * C;
+                for (int k = 0; k < C; ++k) {
+                    P acc = 0;
+                    for (int kp = 0; kp < C; ++kp) acc += m0[kp] * P0[static_cast<size_t>(kp) * C + k];
+                    x[k] = acc;
+                }
+                if (first_residual) {
+                    const P* res = residual.data() + static_cast<size_t>(types[i]) * nLM * C;
+                    for (int k = 0; k < C; ++k) x[k] += res[k];
+                }
+            }
+        }
 
         // ---- compute_Phi1_streamed ----
         std::vector<P> Phi1(static_cast<size_t>(N) * num_lme * C);
@@ -697,7 +741,8 @@ struct Oracle {
                     M1[k] = poly(coef, m1_deg.data(), m1_idx.data(), 0, m1_terms, x, g, nlm);
                     for (int lm = 0; lm < nlm; ++lm) M1g[static_cast<size_t>(lm) * C + k] = g[lm];
                 }
-                const P* xs = M0.data() + static_cast<size_t>(i) * nLM * C;  // scalar block
+                const P* xs = pre_linear_up ? xs_pre.data() + static_cast<size_t>(i) * C
+                                            : M0.data() + static_cast<size_t>(i) * nLM * C;  // scalar block
                 const P* T = H2M0.data() + static_cast<size_t>(ti) * C * C;
                 for (int o = 0; o < C; ++o) {
                     P acc = 0;
@@ -863,9 +908,21 @@ struct Oracle {
         // ---- reverse_H1 + direct adjoint ----
         std::vector<P> M0adj(static_cast<size_t>(N) * nLM * C);
         gemm_blocks(N, nLM, Lmax, H1adj.data(), H1W.data(), M0adj.data(), true);
-        for (int i = 0; i < N; ++i)
-            for (int k = 0; k < C; ++k)
-                M0adj[static_cast<size_t>(i) * nLM * C + k] += direct[static_cast<size_t>(i) * C + k];
+        // add_h1_affine_direct_adjoint (mace.cpp:1784-1813): M0_adj scalar
+        // block += direct (m0_composite) or P0 direct (pre_linear_up)
+        for (int i = 0; i < N; ++i) {
+            const P* dir = direct.data() + static_cast<size_t>(i) * C;
+            P* adj = M0adj.data() + static_cast<size_t>(i) * nLM * C;
+            if (pre_linear_up) {
+                for (int kp = 0; kp < C; ++kp) {
+                    P acc = 0;
+                    for (int k = 0; k < C; ++k) acc += P0[static_cast<size_t>(kp) * C + k] * dir[k];
+                    adj[kp] += acc;
+                }
+            } else {
+                for (int k = 0; k < C; ++k) adj[k] += dir[k];
+            }
+        }
 
         // ---- reverse_M0 ----
         std::vector<P> A0adj(static_cast<size_t>(N) * nlm * C, P(0));

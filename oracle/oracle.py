@@ -295,6 +295,8 @@ class _Spec(ctypes.Structure):
         ("zbl_p", ctypes.c_int),
         ("A0_scaled", ctypes.c_int), ("a0s_values", ctypes.c_void_p), ("a0s_derivs", ctypes.c_void_p),
         ("A1_scaled", ctypes.c_int), ("a1s_values", ctypes.c_void_p), ("a1s_derivs", ctypes.c_void_p),
+        ("pre_linear_up", ctypes.c_int), ("H1P0", ctypes.c_void_p),
+        ("first_residual", ctypes.c_int), ("residual", ctypes.c_void_p), ("residual_fused", ctypes.c_void_p),
     ]
 
 
@@ -312,8 +314,15 @@ class MaceOracle:
     """CPU restatement of MACECPU for one model and a set of active types."""
 
     def __init__(self, model: dict, active_types, precision="float32"):
-        if model.get("symmetrix_format_version") != 4 or model.get("h1_affine_mode") != "m0_composite":
-            raise NotImplementedError("the oracle restates format 4 / m0_composite models")
+        mode = model.get("h1_affine_mode")
+        if model.get("symmetrix_format_version") != 4 or mode not in ("m0_composite", "pre_linear_up"):
+            raise NotImplementedError("the oracle restates format-4 models (m0_composite or pre_linear_up basis)")
+        if model.get("has_field_coupling"):
+            raise NotImplementedError("the oracle does not restate field coupling")
+        pre = mode == "pre_linear_up"
+        residual = bool(model.get("first_interaction_residual"))
+        if residual and not pre:
+            raise ValueError("first-interaction residual models use the pre_linear_up basis")
         self.precision = precision
         self.model = model
         ne = int(model["num_elements"])
@@ -390,8 +399,10 @@ class MaceOracle:
             term_cg=arr(model["Phi1_clebsch_gordan"]),
             A1W=ctypes.cast(a1_ptrs, ctypes.c_void_p).value, m1_terms=len(m1_deg),
             m1_degree=arr(m1_deg, np.int32), m1_index=arr(m1_idx, np.int32),
-            m1_coef=arr(m1_coef), H2M0=arr(np.asarray(model["H2_weights_for_M0"])),
-            H2M1=arr(model["H2_weights_for_M1"]), readout_q=arr(model["readout_1_weights_for_M0"]),
+            m1_coef=arr(m1_coef),
+            H2M0=arr(np.asarray(model["H2_weights_for_H1_pre_linear_up" if pre else "H2_weights_for_M0"])),
+            H2M1=arr(model["H2_weights_for_M1"]),
+            readout_q=arr(model["readout_1_weights_for_H1_pre_linear_up" if pre else "readout_1_weights_for_M0"]),
             readout_hidden=int(model.get("readout_2_hidden_size", 16)),
             readout_w1=arr(model["readout_2_weights_1"]),
             readout_w2=arr(model["readout_2_weights_2"]),
@@ -410,6 +421,20 @@ class MaceOracle:
             spec.zbl_num_radii = len(radii)
             spec.zbl_radii = arr(radii)
             spec.zbl_p = int(model["zbl_p"])
+        if pre:
+            P = np.asarray(model["H1_product_weights"], dtype=np.float64).reshape(Lmax + 1, C, C)
+            spec.pre_linear_up = 1
+            spec.H1P0 = arr(P[0])
+        if residual:
+            # fused residual (mace.cpp:2808-2822): residual of element a, row lm,
+            # times H1_linear_up_weights of l(lm)
+            res = np.asarray(model["H1_first_residual_weights"], dtype=np.float64).reshape(ne, nLM, C)
+            U = np.asarray(model["H1_linear_up_weights"], dtype=np.float64).reshape(Lmax + 1, C, C)
+            l_of = np.repeat(np.arange(Lmax + 1), 2 * np.arange(Lmax + 1) + 1)
+            fused = np.einsum("alk,lko->alo", res, U[l_of])
+            spec.first_residual = 1
+            spec.residual = arr(res)
+            spec.residual_fused = arr(fused)
         if a0s:
             spec.a0s_values = arr(np.stack(a0sv))
             spec.a0s_derivs = arr(np.stack(a0sd))

@@ -324,6 +324,14 @@ void Evaluator::upload_static_tables()
         upload(*a1w_[l], to_float(m.A1W[l].data(), m.A1W[l].size()), stream_);
         upload(*a1wt_[l], transpose(m.A1W[l].data(), num_e_[l] * C_, C_), stream_);
     }
+    if (m.pre_linear_up) {
+        upload(p0w_, to_float(m.H1P.data(), static_cast<std::size_t>(C_) * C_), stream_);
+        upload(p0wt_, transpose(m.H1P.data(), C_, C_), stream_);
+    }
+    if (m.first_residual) {
+        upload(residual_, to_float(m.residual.data(), m.residual.size()), stream_);
+        upload(residual_fused_, to_float(m.residual_fused.data(), m.residual_fused.size()), stream_);
+    }
     upload(h2m1_, to_float(m.H2M1.data(), m.H2M1.size()), stream_);
     upload(h2m1t_, transpose(m.H2M1.data(), C_, C_), stream_);
     upload(q_, to_float(m.readout_q.data(), m.readout_q.size()), stream_);
@@ -541,8 +549,8 @@ void Evaluator::allocate_workspace()
         ET = 1;
         for (int t = 0; t < num_tiles_; ++t)
             ET = std::max<std::size_t>(ET, tile_first_edge_[t + 1] - tile_first_edge_[t]);
-        M0s_.reserve(N * C_ * f);
     }
+    if (tile_receivers_ > 0 || model_.pre_linear_up) M0s_.reserve(N * C_ * f);
     A0_.reserve(NT * nlm_ * C_ * f);
     M0_.reserve(NT * nLM_ * C_ * f);
     Phi1_.reserve(NT * nlme_ * C_ * f);
@@ -1071,11 +1079,16 @@ void Evaluator::launch_zbl_term(hipStream_t s)
               "ZBL");
 }
 
-// H1 = M0 H1_W per l block (or, reverse, M0_adj = H1_adj H1_W^T) for
-// `nodes` consecutive nodes, one grouped launch.
-void Evaluator::gemm_h1(int nodes, const float* in, long long in_stride, float* out, long long out_stride,
-                        bool reverse, const char* what)
+// H1 = M0 H1_W per l block (+ the fused first-interaction residual of the
+// node's element, mace_kokkos_h1_phi1.cpp:511-537) or, reverse, M0_adj =
+// H1_adj H1_W^T, for `nodes` consecutive nodes from graph node `node_base`,
+// one grouped launch.  With x_out (pre_linear_up basis, forward) the same
+// launch forms the readout input x = M0_scalar P0 + residual_scalar
+// (mace_kokkos_h1_phi1.cpp:253-280, 538-552).
+void Evaluator::gemm_h1(int nodes, int node_base, const float* in, long long in_stride, float* out,
+                        long long out_stride, bool reverse, float* x_out, const char* what)
 {
+    const long long type_stride = static_cast<long long>(nLM_) * C_;
     GemmGroup grp;
     for (int l = 0; l <= model_.L_max; ++l) {
         GemmArgs& g = grp.g[grp.count++];
@@ -1087,8 +1100,45 @@ void Evaluator::gemm_h1(int nodes, const float* in, long long in_stride, float* 
         // Bt = W^T for H1 = M0 W, and W for M0_adj = H1_adj W^T
         g.Bt = (reverse ? h1w_ : h1wt_).as<float>() + static_cast<std::size_t>(l) * C_ * C_;
         g.c = {out + l * l * C_, out_stride, C_};
+        if (!reverse && model_.first_residual)
+            g.bias = {residual_fused_.as<float>() + l * l * C_, node_types_.as<int>(), node_base, type_stride, C_};
+    }
+    if (x_out) {
+        GemmArgs& g = grp.g[grp.count++];
+        g.nodes = nodes;
+        g.rows_per_node = 1;
+        g.K = C_;
+        g.Ncols = C_;
+        g.a = {in, in_stride, C_};
+        g.Bt = p0wt_.as<float>();
+        g.c = {x_out, C_, C_};
+        if (model_.first_residual)
+            g.bias = {residual_.as<float>(), node_types_.as<int>(), node_base, type_stride, C_};
     }
     hip_check(launch_gemm_group(grp, stream_), what);
+}
+
+// M0_adj scalar block += the readout's direct adjoint of x: direct itself
+// (m0_composite, x = M0_scalar) or direct P0^T (pre_linear_up, reference
+// add_h1_affine_direct_adjoint, mace_kokkos_h1_phi1.cpp:296-345).
+void Evaluator::add_direct(int nodes, int node_base, float* M0adj, hipStream_t s)
+{
+    const float* direct = direct_.as<float>() + static_cast<std::size_t>(node_base) * C_;
+    if (!model_.pre_linear_up) {
+        hip_check(launch_add_direct(nodes, C_, nLM_, direct, M0adj, s), "direct adjoint");
+        return;
+    }
+    GemmGroup grp;
+    GemmArgs& g = grp.g[grp.count++];
+    g.nodes = nodes;
+    g.rows_per_node = 1;
+    g.K = C_;
+    g.Ncols = C_;
+    g.a = {direct, C_, C_};
+    g.Bt = p0w_.as<float>();  // M0_adj[kp] += sum_k P0[kp][k] direct[k]
+    g.c = {M0adj, static_cast<long long>(nLM_) * C_, C_};
+    g.accumulate = 1;
+    hip_check(launch_gemm_group(grp, s), "direct adjoint");
 }
 
 // A1[l] = Phi1[l group] A1_W[l] (or, reverse, dPhi1[l group] = A1_adj[l]
@@ -1167,7 +1217,8 @@ void Evaluator::evaluate()
                   "M0 forward");
         mark(kStageM0Forward, true);
         mark(kStageH1Gemm, false);
-        gemm_h1(N, M0_.as<float>(), nodeLM, H1_.as<float>(), nodeLM, false, "H1 gemm");
+        gemm_h1(N, 0, M0_.as<float>(), nodeLM, H1_.as<float>(), nodeLM, false,
+                model_.pre_linear_up ? M0s_.as<float>() : nullptr, "H1 gemm");
         mark(kStageH1Gemm, true);
         // layer 1: Phi1 -> A1
         mark(kStageR1Forward, false);
@@ -1189,7 +1240,12 @@ void Evaluator::evaluate()
         ra.node_types = node_types_.as<int>();
         ra.type_active = type_active_.as<int>();
         ra.A1 = A1_.as<float>();
-        ra.M0 = M0_.as<float>();
+        if (model_.pre_linear_up) {
+            ra.M0 = M0s_.as<float>();
+            ra.m0_stride = C_;
+        } else {
+            ra.M0 = M0_.as<float>();
+        }
         ra.p1 = p1;
         ra.H2M0 = h2m0_.as<float>();
         ra.H2M0T = h2m0t_.as<float>();
@@ -1223,8 +1279,8 @@ void Evaluator::evaluate()
         mark(kStageH1ReverseGemm, false);
         // M0_adj = H1_adj H1_W^T (+ direct scalar adjoint), into the M0 buffer
         float* M0adj = M0_.as<float>();
-        gemm_h1(N, H1adj_.as<float>(), nodeLM, M0adj, nodeLM, true, "H1 reverse gemm");
-        hip_check(launch_add_direct(N, C_, nLM_, direct_.as<float>(), M0adj, s), "direct adjoint");
+        gemm_h1(N, 0, H1adj_.as<float>(), nodeLM, M0adj, nodeLM, true, nullptr, "H1 reverse gemm");
+        add_direct(N, 0, M0adj, s);
         mark(kStageH1ReverseGemm, true);
         // A0_adj into the A1 buffer (no longer needed)
         float* A0adj = A1_.as<float>();
@@ -1318,11 +1374,13 @@ void Evaluator::evaluate_tiled()
         hip_check(launch_m0_forward(la, p0, node_blocks(m0_blocks_, m0_block_offsets_, t), A0_.as<float>(),
                                     M0_.as<float>(), s),
                   "M0 forward");
-        gemm_h1(la.node_count, M0_.as<float>(), nodeLM, H1 + la.node_offset * nodeLM, nodeLM, false, "H1 gemm");
-        hip_check(hipMemcpy2DAsync(M0s + static_cast<std::size_t>(la.node_offset) * C_, C_ * sizeof(float),
-                                   M0_.as<float>(), nodeLM * sizeof(float), C_ * sizeof(float), la.node_count,
-                                   hipMemcpyDeviceToDevice, s),
-                  "M0 scalar block");
+        float* x = M0s + static_cast<std::size_t>(la.node_offset) * C_;
+        gemm_h1(la.node_count, la.node_offset, M0_.as<float>(), nodeLM, H1 + la.node_offset * nodeLM, nodeLM, false,
+                model_.pre_linear_up ? x : nullptr, "H1 gemm");
+        if (!model_.pre_linear_up)
+            hip_check(hipMemcpy2DAsync(x, C_ * sizeof(float), M0_.as<float>(), nodeLM * sizeof(float),
+                                       C_ * sizeof(float), la.node_count, hipMemcpyDeviceToDevice, s),
+                      "M0 scalar block");
     }
     // sweep 2
     ReadoutArgs ra;
@@ -1373,10 +1431,9 @@ void Evaluator::evaluate_tiled()
     float* A0adj = A1_.as<float>();
     for (int t = 0; t < num_tiles_; ++t) {
         tile(t);
-        gemm_h1(la.node_count, H1adj + la.node_offset * nodeLM, nodeLM, M0adj, nodeLM, true, "H1 reverse gemm");
-        hip_check(launch_add_direct(la.node_count, C_, nLM_, direct_.as<float>() + static_cast<std::size_t>(la.node_offset) * C_,
-                                    M0adj, s),
-                  "direct adjoint");
+        gemm_h1(la.node_count, la.node_offset, H1adj + la.node_offset * nodeLM, nodeLM, M0adj, nodeLM, true, nullptr,
+                "H1 reverse gemm");
+        add_direct(la.node_count, la.node_offset, M0adj, s);
         hip_check(launch_a0_forward(la, r0f_.as<float>(), A0_.as<float>(), s), "A0 forward");
         hip_check(launch_m0_reverse(la, p0, node_blocks(m0_blocks_, m0_block_offsets_, t), A0_.as<float>(), M0adj,
                                     A0adj, s),

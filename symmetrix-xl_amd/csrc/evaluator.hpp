@@ -183,8 +183,9 @@ private:
     void invalidate_graph();
     void evaluate();
     void evaluate_tiled();
-    void gemm_h1(int nodes, const float* in, long long in_stride, float* out, long long out_stride, bool reverse,
-                 const char* what);
+    void gemm_h1(int nodes, int node_base, const float* in, long long in_stride, float* out, long long out_stride,
+                 bool reverse, float* x_out, const char* what);
+    void add_direct(int nodes, int node_base, float* M0adj, hipStream_t s);
     void gemm_a1(int nodes, const float* in, float* out, bool reverse, const char* what);
     void reduce(double volume);
 
@@ -201,6 +202,8 @@ private:
     DeviceBuffer type_active_, r0f_, r1_, p0_coef_, p0_packed_, p0_offsets_, p1_coef_, p1_packed_,
         p1_offsets_, h2m0_, h2m0t_, e0_;
     DeviceBuffer h1w_, h1wt_, h2m1_, h2m1t_, q_, w1_, w2_, cg_;
+    // pre_linear_up basis: P0 ([in][out]) and P0^T; residual tables [ne][num_LM][C]
+    DeviceBuffer p0w_, p0wt_, residual_, residual_fused_;
     std::vector<std::unique_ptr<DeviceBuffer>> a1w_, a1wt_;
     PolyLayout p0_layout_, p1_layout_;
     // density-normalisation splines [pair_u][interval][4] and ZBL pair tables [ordered active pair]
@@ -238,6 +241,8 @@ private:
     int num_tiles_ = 0;
     std::vector<long long> tile_first_edge_;  // [num_tiles + 1]
     std::vector<int> tile_run_offsets_;       // [num_tiles + 1]
+    // M0s_: [N][C] scalar readout input x (M0 scalar block, or M0_scalar P0
+    // (+ residual) in the pre_linear_up basis), graph-wide
     DeviceBuffer M0s_, run_source_, run_start_, run_length_;
     // nodes grouped by (tile, active type) and their blocks for the node kernels
     DeviceBuffer node_order_, m0_blocks_, readout_blocks_;

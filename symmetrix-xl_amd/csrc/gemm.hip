@@ -1,6 +1,9 @@
 // gfx950 FP32 MFMA GEMMs of the node linears: H1 = M0 H1_W, A1 = Phi1 A1_W
 // and their adjoints (reference mace.cpp:1690-1724, 2304-2340, 1664-1688,
-// 2380-2458; the reference calls CBLAS / Kokkos batched GEMM for these).
+// 2380-2458; the reference calls CBLAS / Kokkos batched GEMM for these), plus
+// the pre_linear_up scalar x = M0_scalar P0 (+ residual) and its adjoint
+// M0_adj += direct P0^T (mace_kokkos_h1_phi1.cpp:253-345, 511-553), which use
+// the optional per-type bias and the accumulating store.
 //
 // All irrep blocks of one stage run in one launch (a group of up to
 // kMaxGemmGroup GEMMs, tiles numbered consecutively across the group).  A
@@ -109,7 +112,13 @@ __global__ void __launch_bounds__(256) gemm_group_kernel(GemmGroup grp)
             if (row < M) {
                 const int node = row / g.rows_per_node;
                 const int m = row - node * g.rows_per_node;
-                g.c.ptr[node * g.c.node_stride + m * g.c.row_stride + col] = acc[j][v];
+                float value = acc[j][v];
+                if (g.bias.ptr)
+                    value += g.bias.ptr[g.bias.node_types[g.bias.node_base + node] * g.bias.type_stride +
+                                        m * g.bias.row_stride + col];
+                float* dst = g.c.ptr + node * g.c.node_stride + m * g.c.row_stride + col;
+                if (g.accumulate) value += *dst;
+                *dst = value;
             }
         }
     }

@@ -89,8 +89,19 @@ struct GemmOut {
     long long row_stride = 0;
 };
 
-// out(node, m)[n] = sum_k in(node, m)[k] Bt[n][k]   (Bt: Ncols x K row-major,
-// i.e. the right-hand matrix transposed, so both operands are K-contiguous)
+// Optional per-element-type bias of a GEMM's output rows:
+// bias(node, m)[n] = ptr[node_types[node_base + node] * type_stride + m * row_stride + n]
+struct GemmBias {
+    const float* ptr = nullptr;
+    const int* node_types = nullptr;  // element type of each graph node
+    int node_base = 0;                // graph index of the GEMM's node 0
+    long long type_stride = 0;
+    long long row_stride = 0;
+};
+
+// out(node, m)[n] (+)= sum_k in(node, m)[k] Bt[n][k] + bias(node, m)[n]
+// (Bt: Ncols x K row-major, i.e. the right-hand matrix transposed, so both
+// operands are K-contiguous; accumulate adds to what out holds)
 struct GemmArgs {
     int nodes = 0;
     int rows_per_node = 0;
@@ -99,6 +110,8 @@ struct GemmArgs {
     GemmRows a;
     const float* Bt = nullptr;
     GemmOut c;
+    GemmBias bias;
+    int accumulate = 0;
 };
 
 // Up to kMaxGemmGroup independent GEMMs (the irrep blocks of one stage) in

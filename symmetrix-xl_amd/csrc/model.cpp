@@ -225,9 +225,9 @@ HostModel HostModel::load(const std::string& path, const std::string& head)
     const Value* hf = file.find("has_field_coupling");
     require(!(hf && hf->as_bool()), "MACEField coupling is not supported.");
     const Value* fr = file.find("first_interaction_residual");
-    require(!(fr && fr->as_bool()), "First-interaction residual models are not supported yet.");
+    m.first_residual = fr && fr->as_bool();
 
-    // format 4, m0_composite basis (h1_affine_schema.hpp:168-258)
+    // format 4, m0_composite or pre_linear_up basis (h1_affine_schema.hpp:168-258)
     const Value* fv = file.find("symmetrix_format_version");
     const int version = fv ? fv->as_int() : 1;
     require(version == 4,
@@ -237,16 +237,31 @@ HostModel HostModel::load(const std::string& path, const std::string& head)
                 (mode->str == "m0_composite" || mode->str == "pre_linear_up"),
             "Symmetrix MACE format version 4 requires h1_affine_mode 'm0_composite' or "
             "'pre_linear_up'.");
-    require(mode->str == "m0_composite", "The pre_linear_up basis is not supported yet.");
+    m.pre_linear_up = mode->str == "pre_linear_up";
     const Value* av = file.find("h1_affine_version");
     require(av && av->as_number() == 1, "Unsupported h1_affine_version (supported: 1).");
     require(!file.contains("readout_1_weights") && !file.contains("H2_weights_for_H1"),
             "A format-version-4 MACE JSON must not contain the old-basis readout_1_weights or "
             "H2_weights_for_H1 fields.");
-    require(!file.contains("readout_1_weights_for_H1_pre_linear_up") &&
-                !file.contains("H2_weights_for_H1_pre_linear_up"),
-            "A 'm0_composite' MACE JSON must not contain readout_1_weights_for_H1_pre_linear_up "
-            "or H2_weights_for_H1_pre_linear_up.");
+    const char* readout_key =
+        m.pre_linear_up ? "readout_1_weights_for_H1_pre_linear_up" : "readout_1_weights_for_M0";
+    const char* skip_key = m.pre_linear_up ? "H2_weights_for_H1_pre_linear_up" : "H2_weights_for_M0";
+    if (m.pre_linear_up)
+        require(!file.contains("readout_1_weights_for_M0") && !file.contains("H2_weights_for_M0"),
+                "A 'pre_linear_up' MACE JSON must not contain readout_1_weights_for_M0 or "
+                "H2_weights_for_M0.");
+    else
+        require(!file.contains("readout_1_weights_for_H1_pre_linear_up") &&
+                    !file.contains("H2_weights_for_H1_pre_linear_up"),
+                "A 'm0_composite' MACE JSON must not contain readout_1_weights_for_H1_pre_linear_up "
+                "or H2_weights_for_H1_pre_linear_up.");
+    require(m.pre_linear_up || !m.first_residual,
+            "The m0_composite basis cannot represent first-interaction residual or field-coupled "
+            "features; such models use h1_affine_mode 'pre_linear_up'.");
+    require(!m.pre_linear_up || file.contains("H1_product_weights"),
+            "The pre_linear_up basis requires H1_product_weights.");
+    require(file.contains(readout_key) && file.contains(skip_key),
+            std::string("A '") + mode->str + "' MACE JSON requires " + readout_key + " and " + skip_key + ".");
 
     // compact radial model (compact_radial.cpp:110-205)
     const Value* rr = file.find("radial_representation");
@@ -347,8 +362,43 @@ HostModel HostModel::load(const std::string& path, const std::string& head)
         }
     }
 
-    m.H1W = numbers(file.at("H1_weights"), "H1_weights",
-                    static_cast<std::size_t>(m.L_max + 1) * C * C);
+    const std::size_t h1_size = static_cast<std::size_t>(m.L_max + 1) * C * C;
+    m.H1W = numbers(file.at("H1_weights"), "H1_weights", h1_size);
+
+    // split H1 weights and the first-interaction residual (mace.cpp:2790-2829)
+    auto optional_numbers = [&](const char* key) {
+        const Value* v = file.find(key);
+        return v ? numbers(*v, key, static_cast<std::size_t>(-1)) : std::vector<double>{};
+    };
+    const std::vector<double> product = optional_numbers("H1_product_weights");
+    const std::vector<double> linear_up = optional_numbers("H1_linear_up_weights");
+    const std::vector<double> residual = optional_numbers("H1_first_residual_weights");
+    const std::size_t residual_size = static_cast<std::size_t>(ne) * m.num_LM * C;
+    if (m.first_residual) {
+        require(residual.size() == residual_size, "Residual-first MACE JSON has an invalid H1 residual extent.");
+        require(product.size() == h1_size && linear_up.size() == h1_size,
+                "Residual-first MACE JSON requires split H1 weights.");
+        m.residual = residual;
+        // fused residual: residual U, per element, per l block
+        m.residual_fused.assign(residual_size, 0.0);
+        for (int a = 0; a < ne; ++a)
+            for (int l = 0; l <= m.L_max; ++l)
+                for (int lm = l * l; lm < (l + 1) * (l + 1); ++lm) {
+                    const double* res = residual.data() + (static_cast<std::size_t>(a) * m.num_LM + lm) * C;
+                    double* out = m.residual_fused.data() + (static_cast<std::size_t>(a) * m.num_LM + lm) * C;
+                    for (int in = 0; in < C; ++in) {
+                        const double* u = linear_up.data() + (static_cast<std::size_t>(l) * C + in) * C;
+                        for (int k = 0; k < C; ++k) out[k] += res[in] * u[k];
+                    }
+                }
+    } else {
+        require(residual.empty(), "Non-residual MACE JSON must not contain H1 residual weights.");
+    }
+    if (m.pre_linear_up) {
+        require(product.size() == h1_size,
+                "The pre_linear_up basis requires H1_product_weights of the H1_weights extent.");
+        m.H1P = product;
+    }
 
     // second interaction tables
     m.Phi1_l = file.at("Phi1_l").ints("Phi1_l");
@@ -388,13 +438,20 @@ HostModel HostModel::load(const std::string& path, const std::string& head)
         }
     }
 
-    // H2 and readouts (m0_composite)
-    const Value& skip = file.at("H2_weights_for_M0");
-    require(static_cast<int>(skip.size()) == ne, "H2_weights_for_M0 must hold one row per element.");
-    m.H2M0 = numbers(skip, "H2_weights_for_M0", static_cast<std::size_t>(ne) * C * C);
+    // H2 and readouts: skip map and readout_1 on the scalar x of the basis
+    const Value& skip = file.at(skip_key);
+    require(skip.kind == Value::Kind::array && static_cast<int>(skip.size()) == ne,
+            std::string(skip_key) + " must hold one row per element.");
+    for (std::size_t a = 0; a < skip.size(); ++a)
+        require(skip[a].is_array() && skip[a].size() == static_cast<std::size_t>(C) * C,
+                std::string("Every ") + skip_key + " row must hold num_channels^2 values.");
+    m.H2M0 = numbers(skip, skip_key, static_cast<std::size_t>(ne) * C * C);
     m.H2M1 = numbers(file.at("H2_weights_for_M1"), "H2_weights_for_M1",
                      static_cast<std::size_t>(C) * C);
-    m.readout_q = numbers(file.at("readout_1_weights_for_M0"), "readout_1_weights_for_M0", C);
+    const Value& readout = file.at(readout_key);
+    require(readout.is_array() && readout.size() == static_cast<std::size_t>(C),
+            std::string(readout_key) + " must hold num_channels values.");
+    m.readout_q = numbers(readout, readout_key, C);
     const Value* hs = file.find("readout_2_hidden_size");
     m.readout_hidden = hs ? hs->as_int() : 16;
     require(m.readout_hidden > 0 && m.readout_hidden <= 64,

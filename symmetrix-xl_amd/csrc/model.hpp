@@ -3,11 +3,11 @@
 //
 // Loader semantics follow the reference's MACECPU::load_from_json
 // (libsymmetrix/source/mace.cpp:2659-2959) and the format-4 H1 affine
-// validation (h1_affine_schema.hpp:168-258) for the "m0_composite" basis;
-// the radial tabulation follows CompactRadialModel
-// (compact_radial.cpp:110-420).  Unsupported options (ZBL, A0/A1 density
-// scaling, field coupling, first-interaction residual, Agnesi transform,
-// pair-spline radial form) are rejected with an error, never ignored.
+// validation (h1_affine_schema.hpp:168-258) for the "m0_composite" and
+// "pre_linear_up" bases; the radial tabulation follows CompactRadialModel
+// (compact_radial.cpp:110-420).  Unsupported options (field coupling,
+// pair-spline radial form, single-layer models) are rejected with an error,
+// never ignored.
 #pragma once
 
 #include <string>
@@ -68,6 +68,18 @@ struct HostModel {
 
     std::vector<double> H1W;  // [L_max+1][C][C]
 
+    // pre_linear_up basis (h1_affine_schema.hpp:14-24): the readout_1 and
+    // H1->H2 skip maps act on x = P0^T M0_scalar (+ the residual's scalar
+    // block), P = H1_product_weights; m0_composite: x = M0_scalar.
+    bool pre_linear_up = false;
+    std::vector<double> H1P;  // [L_max+1][C][C] ([in][out]); only l = 0 is used
+    // first-interaction residual (mace.cpp:1845-1880, 2796-2825): per element
+    // constants added to the pre-linear_up features; H1 gains the fused
+    // residual (residual U per l), x the unfused scalar block
+    bool first_residual = false;
+    std::vector<double> residual;        // [ne][num_LM][C]
+    std::vector<double> residual_fused;  // [ne][num_LM][C]
+
     std::vector<int> Phi1_l, Phi1_l1, Phi1_l2, Phi1_lme, Phi1_row;
     std::vector<double> Phi1_cg;
     std::vector<std::vector<double>> A1W;  // [l] -> [num_e[l]*C][C]
@@ -75,9 +87,9 @@ struct HostModel {
     std::vector<int> m1_degree, m1_index;  // [T1], [T1][3]
     std::vector<double> m1_coef;           // [ne][T1][C]
 
-    std::vector<double> H2M0;  // [ne][C][C]  ([in][out])
+    std::vector<double> H2M0;  // [ne][C][C]  ([in][out]) skip map on x
     std::vector<double> H2M1;  // [C][C]
-    std::vector<double> readout_q;  // [C]
+    std::vector<double> readout_q;  // [C] readout_1 on x
     int readout_hidden = 16;
     std::vector<double> readout_w1;  // [hidden][C]
     std::vector<double> readout_w2;  // [hidden]

@@ -2,7 +2,7 @@
 
 No checkpoint converter is available offline, so models are written directly
 in the compact JSON format version 4 with ``h1_affine_mode`` "m0_composite"
-that the evaluator loads (keys and layouts: reference
+(or "pre_linear_up", optionally residual-first) that the evaluator loads (keys and layouts: reference
 ``libsymmetrix/source/mace.cpp:2659-2959``, ``h1_affine_schema.hpp:1-62``,
 ``symmetrix/test/compact_r1_model.py:97-170``).  Weights are random with the
 fan-in scaling of a freshly initialised MACE; the message-passing sums are
@@ -48,6 +48,10 @@ class ModelShape:
     zbl: bool = False            # ZBL pair repulsion (has_zbl)
     density: tuple = ()          # density-normalised layers: subset of ("A0", "A1")
     agnesi: bool = False         # Agnesi distance transform of the radial features
+    # H1 affine basis of format 4: "m0_composite", or "pre_linear_up" with split
+    # H1 weights (H1_weights = P U) and readout_1 / skip on M0_scalar P0 (+ residual)
+    h1_basis: str = "m0_composite"
+    residual: bool = False       # first-interaction residual (pre_linear_up basis only)
     extra: dict = field(default_factory=dict)
 
 
@@ -166,7 +170,8 @@ def _polynomial_block(rng, num_elements, channels, input_lmax, out_l_max, correl
 
 
 def random_mace_model(shape: ModelShape | str = "tiny", seed: int = 0) -> dict:
-    """Random-init compact MACE model dict (format version 4, m0_composite)."""
+    """Random-init compact MACE model dict (format version 4, m0_composite or
+    pre_linear_up basis per ``shape.h1_basis``)."""
     if isinstance(shape, str):
         shape = PRESETS[shape]
     rng = np.random.default_rng(seed)
@@ -291,6 +296,10 @@ def random_mace_model(shape: ModelShape | str = "tiny", seed: int = 0) -> dict:
         ),
         "readout_2_scale_factor": SILU_NORMALIZATION,
     }
+    if shape.h1_basis == "pre_linear_up":
+        _split_h1(model, shape, np.random.default_rng([seed, 1]))
+    elif shape.h1_basis != "m0_composite" or shape.residual:
+        raise ValueError("the first-interaction residual requires the pre_linear_up basis")
     if shape.zbl:
         model.update({
             "has_zbl": True, "zbl_a_exp": ZBL_A_EXP, "zbl_a_prefactor": ZBL_A_PREFACTOR,
@@ -298,6 +307,33 @@ def random_mace_model(shape: ModelShape | str = "tiny", seed: int = 0) -> dict:
         })
     model.update(shape.extra)
     return model
+
+
+def _split_h1(model: dict, shape: ModelShape, rng) -> None:
+    """Rewrite a model in the pre_linear_up basis (h1_affine_schema.hpp:14-24):
+    H1_weights = P U per l with the product (P) and linear_up (U) weights kept,
+    readout_1 r0 and skip S0_z on the pre-linear_up scalar features, and, for a
+    residual-first model, per-element residual constants on the scalar block
+    (the first interaction's skip of the scalar node embedding; the blocks of
+    l > 0 are zero as in a MACE whose first-layer features are scalars)."""
+    C, Lmax = shape.channels, shape.L_max
+    ne = len(shape.atomic_numbers)
+    P = _f32(rng.normal(size=(Lmax + 1, C, C)) / math.sqrt(C))
+    U = _f32(rng.normal(size=(Lmax + 1, C, C)) / math.sqrt(C))
+    model["H1_weights"] = _Array(np.einsum("lij,ljk->lik", P.astype(np.float64), U.astype(np.float64)))
+    model["H1_product_weights"] = _Array(P)
+    model["H1_linear_up_weights"] = _Array(U)
+    del model["readout_1_weights_for_M0"], model["H2_weights_for_M0"]
+    model["h1_affine_mode"] = "pre_linear_up"
+    model["readout_1_weights_for_H1_pre_linear_up"] = _Array(
+        rng.normal(size=C) * shape.energy_scale / math.sqrt(C))
+    model["H2_weights_for_H1_pre_linear_up"] = [
+        _Array(rng.normal(size=(C, C)) / math.sqrt(C)) for _ in range(ne)]
+    model["first_interaction_residual"] = bool(shape.residual)
+    if shape.residual:
+        b = np.zeros((ne, (Lmax + 1) ** 2, C))
+        b[:, 0, :] = rng.normal(size=(ne, C)) * 0.5
+        model["H1_first_residual_weights"] = _Array(b)
 
 
 def model_json(model: dict) -> str:

@@ -6,9 +6,12 @@ oracle on the same seeded inputs (BASELINE north-star tolerances, FP32):
   density networks; mace.cpp:1561-1636, 2380-2458),
 - the Agnesi distance transform of the radial features
   (compact_radial.cpp:150-170, 238-247),
+- the pre_linear_up H1 basis and the first-interaction residual
+  (h1_affine_schema.hpp:9-24, mace.cpp:1759-1813, 1845-1875),
 
 each alone and all together, on the tiny, medium and wide shapes, in the
-untiled and the tiled plan, plus the directed forces edge by edge.
+untiled and the tiled plan, plus the directed forces edge by edge and the
+closed-form energy of isolated atoms of a residual-first model.
 """
 
 import dataclasses
@@ -28,7 +31,9 @@ OPTIONS = {
     "A0": dict(density=("A0",)),
     "A1": dict(density=("A1",)),
     "agnesi": dict(agnesi=True),
-    "all": dict(zbl=True, density=("A0", "A1"), agnesi=True),
+    "pre_linear_up": dict(h1_basis="pre_linear_up"),
+    "residual": dict(h1_basis="pre_linear_up", residual=True),
+    "all": dict(zbl=True, density=("A0", "A1"), agnesi=True, h1_basis="pre_linear_up", residual=True),
 }
 
 
@@ -68,7 +73,8 @@ def test_tiny_options_match_oracle(oracle_lib, tmp_path, option):
     _compare(Symmetrix(path).calculate(s), _oracle(oracle_lib, model, s), len(s))
 
 
-@pytest.mark.parametrize("preset,option", [("medium3", "all"), ("medium3", "A1"), ("wide", "all")])
+@pytest.mark.parametrize("preset,option", [("medium3", "all"), ("medium3", "A1"), ("medium3", "residual"),
+                                           ("wide", "all")])
 def test_larger_shapes_with_options_match_oracle(oracle_lib, tmp_path, preset, option):
     from symmetrix_amd import Symmetrix, synthetic
 
@@ -113,3 +119,30 @@ def test_all_options_tiled_plan_matches_oracle(oracle_lib, tmp_path, limit):
     n = len(s)
     assert abs(ev._total_energy(gen) - want["energy"]) / n < E_TOL
     np.testing.assert_allclose(ev._reduce_atom_forces(n, None, None, gen), want["forces"], atol=F_TOL)
+
+
+def test_isolated_atoms_of_residual_model_closed_form(tmp_path):
+    """No neighbours: A0 = M0 = M1 = 0, so the energy is E0 + r0 . b0 +
+    readout_2(S0_z^T b0) with b0 the element's scalar residual."""
+    from symmetrix_amd import Symmetrix, synthetic
+
+    path, model = _model(tmp_path, "tiny", "residual", seed=3)
+    pos = np.array([[1.0, 1.0, 1.0], [13.0, 1.0, 1.0], [1.0, 13.0, 1.0]])
+    s = synthetic.Structure(pos, np.array([38, 22, 8]), np.eye(3) * 36.0)
+    C, ne = model["num_channels"], model["num_elements"]
+    nLM = (model["L_max"] + 1) ** 2
+    b = np.asarray(model["H1_first_residual_weights"]).reshape(ne, nLM, C)
+    r0 = np.asarray(model["readout_1_weights_for_H1_pre_linear_up"])
+    S0 = np.asarray(model["H2_weights_for_H1_pre_linear_up"]).reshape(ne, C, C)
+    W1 = np.asarray(model["readout_2_weights_1"]).reshape(-1, C)
+    W2 = np.asarray(model["readout_2_weights_2"])
+    want = 0.0
+    for z in (38, 22, 8):
+        t = model["atomic_numbers"].index(z)
+        zh = W1 @ (S0[t].T @ b[t, 0])
+        want += model["atomic_energies"][t] + r0 @ b[t, 0] + model["readout_2_scale_factor"] * (
+            W2 @ (zh / (1.0 + np.exp(-zh))))
+    got = Symmetrix(path).calculate(s)
+    print(f"  |dE|={abs(got['energy'] - want):.3e}", flush=True)
+    assert abs(got["energy"] - want) / 3 < E_TOL
+    np.testing.assert_array_equal(got["forces"], np.zeros((3, 3)))

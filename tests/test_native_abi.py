@@ -44,7 +44,10 @@ def _create(path):
 
     h = ctypes.c_void_p()
     status = _native.library().sxl_create(path.encode(), b"", ctypes.byref(h))
-    return status, _native.library().sxl_last_error().decode()
+    msg = _native.library().sxl_last_error().decode()
+    if status == 0:
+        _native.library().sxl_destroy(h)
+    return status, msg
 
 
 def test_missing_model_file_is_invalid_argument():
@@ -67,6 +70,9 @@ def test_missing_model_file_is_invalid_argument():
         ({"radial_representation": "pair-splines"}, "compact radial"),
         ({"l_max": 5}, "L_max <= l_max <= 3"),
         ({"readout_1_weights": [0.0]}, "old-basis"),
+        ({"first_interaction_residual": True}, "m0_composite basis cannot represent"),
+        ({"h1_affine_mode": "pre_linear_up"}, "must not contain readout_1_weights_for_M0"),
+        ({"has_field_coupling": True}, "MACEField coupling is not supported"),
     ],
 )
 def test_model_validation_errors(tmp_path, change, message):
@@ -96,6 +102,50 @@ def test_compact_radial_validation_errors(tmp_path, edit, message):
 
     model = json.loads(synthetic.model_json(synthetic.random_mace_model("tiny", seed=0)))
     edit(model["compact_radial"])
+    path = tmp_path / "m.json"
+    path.write_text(json.dumps(model))
+    status, msg = _create(str(path))
+    assert status == 1, msg
+    assert message in msg
+
+
+def _split_edit(key, value):
+    def edit(model):
+        if value is None:
+            del model[key]
+        else:
+            model[key] = value
+    return edit
+
+
+@pytest.mark.parametrize(
+    "edit, message",
+    [
+        (_split_edit("H1_product_weights", None), "requires H1_product_weights"),
+        (_split_edit("H1_linear_up_weights", None), "requires split H1 weights"),
+        (_split_edit("H1_first_residual_weights", [0.0] * 7), "invalid H1 residual extent"),
+        (_split_edit("first_interaction_residual", False), "must not contain H1 residual weights"),
+        (_split_edit("readout_1_weights_for_H1_pre_linear_up", [0.0] * 3), "must hold num_channels values"),
+        (_split_edit("H2_weights_for_H1_pre_linear_up", [[0.0] * 4] * 3), "num_channels^2 values"),
+        (_split_edit("H2_weights_for_H1_pre_linear_up", None), "requires readout_1_weights_for_H1_pre_linear_up"),
+        (_split_edit("readout_1_weights_for_M0", [0.0]), "must not contain readout_1_weights_for_M0"),
+    ],
+)
+def test_pre_linear_up_validation_errors(tmp_path, edit, message):
+    """The reference's format-4 / residual validation (h1_affine_schema.hpp:
+    191-258, mace.cpp:2796-2829) on a residual-first pre_linear_up model."""
+    import dataclasses
+
+    from symmetrix_amd import synthetic
+
+    shape = dataclasses.replace(synthetic.PRESETS["tiny"], h1_basis="pre_linear_up", residual=True)
+    model = json.loads(synthetic.model_json(synthetic.random_mace_model(shape, seed=0)))
+    path = tmp_path / "ok.json"
+    path.write_text(json.dumps(model))
+    status, msg = _create(str(path))
+    # a valid model fails only at device creation (no GPU here) or succeeds
+    assert "pre_linear_up" not in msg and "residual" not in msg, msg
+    edit(model)
     path = tmp_path / "m.json"
     path.write_text(json.dumps(model))
     status, msg = _create(str(path))

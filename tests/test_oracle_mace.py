@@ -4,10 +4,11 @@ symmetrix/test/test_mace.py:687-750, rtol 1e-4 / atol 1e-6 in FP64), global
 invariances, FP32 vs FP64 (reference test_mace_streamed_edges.py:556, atol
 3e-5), and skin-masked vs exact graphs (reference :4592-4675).
 
-Every test runs on the plain tiny model and on one with the optional terms of
+Every test runs on the plain tiny model, on one with the optional terms of
 the format (ZBL pair repulsion, A0 and A1 density normalisation, Agnesi
-distance transform), so their reverse passes are pinned by the same finite
-differences and invariances.
+distance transform) and on a residual-first model in the pre_linear_up basis,
+so their reverse passes are pinned by the same finite differences and
+invariances.
 """
 
 import json
@@ -16,15 +17,17 @@ import numpy as np
 import pytest
 
 
-@pytest.fixture(scope="module", params=["plain", "zbl+density+agnesi"])
+@pytest.fixture(scope="module", params=["plain", "zbl+density+agnesi", "pre_linear_up+residual"])
 def tiny(request):
     import dataclasses
 
     from symmetrix_amd import synthetic
 
     shape = synthetic.PRESETS["tiny"]
-    if request.param != "plain":
+    if request.param == "zbl+density+agnesi":
         shape = dataclasses.replace(shape, zbl=True, density=("A0", "A1"), agnesi=True)
+    elif request.param == "pre_linear_up+residual":
+        shape = dataclasses.replace(shape, h1_basis="pre_linear_up", residual=True)
     return json.loads(synthetic.model_json(synthetic.random_mace_model(shape, seed=0)))
 
 
@@ -138,6 +141,10 @@ def test_skin_masked_graph_equals_exact_graph(oracle_lib, tiny, structure):
 
 def test_rejects_unsupported_models(oracle_lib, tiny, structure):
     bad = dict(tiny)
-    bad["h1_affine_mode"] = "pre_linear_up"
+    bad["has_field_coupling"] = True
+    with pytest.raises(NotImplementedError):
+        make(oracle_lib, bad, structure)
+    bad = dict(tiny)
+    bad["symmetrix_format_version"] = 2
     with pytest.raises(NotImplementedError):
         make(oracle_lib, bad, structure)
