@@ -108,13 +108,18 @@ int sxl_prepare_periodic_graph_device(sxl_evaluator* evaluator, int num_nodes, c
 int sxl_graph_arrays(sxl_evaluator* evaluator, uint64_t generation, int* num_neigh, int* receiver_offsets,
                      int* sources, int* shifts, double* fractional_xyz);
 
-/* New cell for the prepared periodic graph (_update_factorized_cell). */
+/* New cell for the prepared periodic graph (_update_factorized_cell,
+ * mace_kokkos.cpp:1673-1685): later evaluations form each edge vector as the
+ * build's fractional edge vector in this cell plus the atoms' minimum-image
+ * displacements.  Invalid argument when the cell is non-finite or does not
+ * match its inverse. */
 int sxl_update_cell(sxl_evaluator* evaluator, uint64_t generation, const double* cell,
                     const double* inverse_cell);
 
 /* Evaluate energies and forces at new positions of a prepared periodic graph.
  * Replaces _compute_prepared_factorized_positions(generation, positions)
- * (mace_kokkos.cpp:1828-1836). */
+ * (mace_kokkos.cpp:1828-1836).  Invalid argument when an edge of the graph has
+ * zero or non-finite length at these positions (coincident atoms). */
 int sxl_compute_prepared_positions(sxl_evaluator* evaluator, uint64_t generation, const double* positions);
 int sxl_compute_prepared_positions_device(sxl_evaluator* evaluator, uint64_t generation,
                                           const double* d_positions);
@@ -131,8 +136,9 @@ int sxl_compute_node_energies_forces(sxl_evaluator* evaluator, int num_nodes, co
                                      const int* num_neigh, const int* neigh_indices, const int* neigh_types,
                                      const double* xyz, const double* r);
 
-/* Largest displacement of positions since the periodic graph was built (for
- * skin-based neighbour reuse, calculator.py:2851-2898). */
+/* Largest minimum-image displacement of positions from the build's
+ * fractional positions expressed in the current cell (the non-affine motion
+ * of the skin-reuse rule, calculator.py:2851-2898). */
 int sxl_max_displacement(sxl_evaluator* evaluator, uint64_t generation, const double* positions,
                          int positions_on_device, double* out);
 

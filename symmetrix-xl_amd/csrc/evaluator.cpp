@@ -860,6 +860,7 @@ void build_periodic_graph(const double* d_positions, int num_nodes, const double
         throw std::length_error("neighbor graph bin count exceeds 32-bit indexing");
     const int num_bins = static_cast<int>(num_bins_size);
     DeviceBuffer wp, wf, wrap, atom_bins, bin_sizes, bin_off64, bin_offsets, bin_atoms, counts, offsets, scratch;
+    out.fractional_positions.reserve(std::max(N, 1) * 3 * sizeof(double));
     wp.reserve(std::max(N, 1) * 3 * sizeof(double));
     wf.reserve(std::max(N, 1) * 3 * sizeof(double));
     wrap.reserve(std::max(N, 1) * 3 * sizeof(int));
@@ -872,8 +873,8 @@ void build_periodic_graph(const double* d_positions, int num_nodes, const double
     offsets.reserve((N + 1) * sizeof(long long));
     scratch.reserve(scan_scratch_size(std::max(num_bins, N) + 1) * sizeof(long long));
     hip_check(hipMemsetAsync(bin_sizes.as<void>(), 0, (num_bins + 1) * sizeof(int), stream), "memset");
-    hip_check(launch_neighbor_bins(plan, d_positions, wp.as<double>(), wf.as<double>(), wrap.as<int>(),
-                                   atom_bins.as<int>(), bin_sizes.as<int>(), stream),
+    hip_check(launch_neighbor_bins(plan, d_positions, out.fractional_positions.as<double>(), wp.as<double>(),
+                                   wf.as<double>(), wrap.as<int>(), atom_bins.as<int>(), bin_sizes.as<int>(), stream),
               "bins");
     hip_check(launch_exclusive_scan_i32(bin_sizes.as<int>(), num_bins, bin_off64.as<long long>(),
                                         scratch.as<long long>(), stream),
@@ -930,11 +931,7 @@ std::uint64_t Evaluator::prepare_periodic_graph(int num_nodes, const int* node_t
         hip_check(hipMemcpyAsync(positions_.as<double>(), positions, N * 3 * sizeof(double),
                                  device_positions ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, stream_),
                   "positions");
-    ref_positions_.reserve(std::max(N, 1) * 3 * sizeof(double));
-    if (N > 0)
-        hip_check(hipMemcpyAsync(ref_positions_.as<double>(), positions_.as<double>(), N * 3 * sizeof(double),
-                                 hipMemcpyDeviceToDevice, stream_),
-                  "positions");
+    disp_.reserve(std::max(N, 1) * 3 * sizeof(double));
     build_periodic_graph(positions_.as<double>(), N, cell, inverse_cell, cutoff, stream_, pgraph_);
     const int E = static_cast<int>(pgraph_.num_edges);
     first_.reserve((N + 1) * sizeof(int));
@@ -953,20 +950,30 @@ std::uint64_t Evaluator::prepare_periodic_graph(int num_nodes, const int* node_t
     std::memcpy(cell_, cell, sizeof(cell_));
     std::memcpy(inverse_cell_, inverse_cell, sizeof(inverse_cell_));
     upload(node_types_, types, stream_);
-    std::vector<double> cellv(cell, cell + 9);
-    upload(cell_dev_, cellv, stream_);
+    upload_cell();
     finish_graph(nullptr);
     return generation_;
 }
 
+void Evaluator::upload_cell()
+{
+    std::vector<double> cellv(cell_, cell_ + 9);
+    cellv.insert(cellv.end(), inverse_cell_, inverse_cell_ + 9);
+    upload(cell_dev_, cellv, stream_);
+}
+
+// New cell for the prepared graph (reference update_factorized_cell): edge
+// vectors are formed from the build's fractional edge vectors in this cell
+// plus the atoms' minimum-image displacements, so a strained or sheared cell
+// reuses the graph while it still covers the cutoff.
 void Evaluator::update_cell(std::uint64_t generation, const double* cell, const double* inverse_cell)
 {
     check_generation(generation);
     if (!periodic_) throw std::invalid_argument("update_cell requires a periodic graph");
+    validate_periodic_inputs(num_nodes_, cell, inverse_cell, 1.0);
     std::memcpy(cell_, cell, sizeof(cell_));
     std::memcpy(inverse_cell_, inverse_cell, sizeof(inverse_cell_));
-    std::vector<double> cellv(cell, cell + 9);
-    upload(cell_dev_, cellv, stream_);
+    upload_cell();
 }
 
 void Evaluator::graph_arrays(std::uint64_t generation, int* num_neigh, int* receiver_offsets, int* sources,
@@ -1007,11 +1014,17 @@ void Evaluator::compute_positions(std::uint64_t generation, const double* positi
                   "positions");
     for (int i = 0; i < kNumStages; ++i) stage_used_[i] = false;
     mark(kStageGeometry, false);
+    const double* cell = cell_dev_.as<double>();
+    hip_check(launch_atom_displacements(N, positions_.as<double>(), pgraph_.fractional_positions.as<double>(), cell,
+                                        cell + 9, disp_.as<double>(), totals_.as<double>() + 12, stream_),
+              "displacements");
     hip_check(launch_edge_geometry(static_cast<int>(num_edges_), receiver_.as<int>(), source_.as<int>(),
-                                   pgraph_.shifts.as<int>(), positions_.as<double>(), cell_dev_.as<double>(),
-                                   xyz_.as<double>(), r_.as<double>(), stream_),
+                                   pgraph_.fractional_xyz.as<double>(), disp_.as<double>(), cell, model_.r_cut,
+                                   xyz_.as<double>(), r_.as<double>(),
+                                   reinterpret_cast<unsigned long long*>(totals_.as<double>() + 13), stream_),
               "edge geometry");
     mark(kStageGeometry, true);
+    check_geometry_ = true;
     evaluate();
 }
 
@@ -1025,6 +1038,7 @@ void Evaluator::compute_xyz(std::uint64_t generation, const double* xyz, const d
         hip_check(hipMemcpyAsync(r_.as<double>(), r, E * sizeof(double), kind, stream_), "r");
     }
     for (int i = 0; i < kNumStages; ++i) stage_used_[i] = false;
+    check_geometry_ = false;
     evaluate();
 }
 
@@ -1037,8 +1051,9 @@ double Evaluator::max_displacement(std::uint64_t generation, const double* posit
         hip_check(hipMemcpyAsync(positions_.as<double>(), positions, N * 3 * sizeof(double),
                                  device_positions ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, stream_),
                   "positions");
-    hip_check(launch_max_displacement(N, positions_.as<double>(), ref_positions_.as<double>(),
-                                      totals_.as<double>() + 12, stream_),
+    const double* cell = cell_dev_.as<double>();
+    hip_check(launch_atom_displacements(N, positions_.as<double>(), pgraph_.fractional_positions.as<double>(), cell,
+                                        cell + 9, disp_.as<double>(), totals_.as<double>() + 12, stream_),
               "displacement");
     double d2 = 0.0;
     hip_check(hipMemcpyAsync(&d2, totals_.as<double>() + 12, sizeof(double), hipMemcpyDeviceToHost, stream_),
@@ -1302,7 +1317,7 @@ void Evaluator::evaluate()
     mark(kStageAtomForces, true);
     // the evaluation (and any copy from caller-owned host arrays) has completed
     // when this returns
-    hip_check(hipStreamSynchronize(s), "evaluation");
+    finish_evaluation();
     if (profiling_)
         for (int i = 0; i < kNumStages; ++i) {
             if (!stage_used_[i]) continue;
@@ -1447,7 +1462,7 @@ void Evaluator::evaluate_tiled()
                                  atom_forces_.as<double>(), s),
               "atom forces");
     mark(kStageAtomForces, true);
-    hip_check(hipStreamSynchronize(s), "evaluation");
+    finish_evaluation();
     if (profiling_ && stage_used_[kStageAtomForces]) {
         float ms = 0.0f;
         hip_check(hipEventElapsedTime(&ms, events_[2 * kStageAtomForces], events_[2 * kStageAtomForces + 1]),
@@ -1461,6 +1476,25 @@ void Evaluator::evaluate_tiled()
     stats_.tiled_evaluations += 1;
     stats_.last_evaluation_ms =
         std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+}
+
+// Waits for the evaluation; an evaluation from positions raises when the
+// edge geometry held an edge of zero or non-finite length (reference
+// validate_prepared_factorized_positions_geometry,
+// mace_kokkos_factorized_lifecycle.cpp:3078-3085).
+void Evaluator::finish_evaluation()
+{
+    invalid_edges_ = 0;
+    if (check_geometry_)
+        hip_check(hipMemcpyAsync(&invalid_edges_, totals_.as<double>() + 13, sizeof(invalid_edges_),
+                                 hipMemcpyDeviceToHost, stream_),
+                  "geometry check");
+    hip_check(hipStreamSynchronize(stream_), "evaluation");
+    if (check_geometry_ && invalid_edges_ != 0) {
+        check_geometry_ = false;
+        evaluated_generation_ = 0;
+        throw std::invalid_argument("Execution R1 prepared positions produced an invalid edge geometry.");
+    }
 }
 
 void Evaluator::reduce(double volume)

@@ -48,6 +48,7 @@ struct PeriodicGraph {
     DeviceBuffer sources;         // [E] int
     DeviceBuffer shifts;          // [E][3] int
     DeviceBuffer fractional_xyz;  // [E][3] double
+    DeviceBuffer fractional_positions;  // [N][3] double: positions . inverse_cell at the build
 };
 
 // Builds the graph of N positions (device pointer) with the given cell.
@@ -221,8 +222,14 @@ private:
     std::vector<int> host_types_;
     double cell_[9] = {}, inverse_cell_[9] = {};
     PeriodicGraph pgraph_;
-    DeviceBuffer node_types_, first_, receiver_, source_, tfirst_, tedge_, edge_pair_, ref_positions_,
-        positions_, cell_dev_;
+    // cell_dev_: cell (9) then inverse cell (9); disp_: [N][3] minimum-image
+    // displacements from the build's fractional positions in the current cell
+    DeviceBuffer node_types_, first_, receiver_, source_, tfirst_, tedge_, edge_pair_, disp_, positions_,
+        cell_dev_;
+    bool check_geometry_ = false;          // evaluation from positions: invalid edges raise
+    unsigned long long invalid_edges_ = 0;
+    void upload_cell();
+    void finish_evaluation();
     DeviceBuffer xyz_, r_;
 
     // workspace

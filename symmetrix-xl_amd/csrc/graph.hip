@@ -27,9 +27,9 @@ __device__ __forceinline__ int floor_div(int numerator, int denominator)
     return quotient - ((remainder != 0 && remainder < 0) ? 1 : 0);
 }
 
-__global__ void bins_kernel(NeighborPlan p, const double* __restrict__ pos, double* __restrict__ wp,
-                            double* __restrict__ wf, int* __restrict__ wrap, int* __restrict__ atom_bins,
-                            int* __restrict__ bin_sizes)
+__global__ void bins_kernel(NeighborPlan p, const double* __restrict__ pos, double* __restrict__ rf,
+                            double* __restrict__ wp, double* __restrict__ wf, int* __restrict__ wrap,
+                            int* __restrict__ atom_bins, int* __restrict__ bin_sizes)
 {
     const int atom = blockIdx.x * blockDim.x + threadIdx.x;
     if (atom >= p.num_nodes) return;
@@ -38,6 +38,7 @@ __global__ void bins_kernel(NeighborPlan p, const double* __restrict__ pos, doub
         double value = 0.0;
         for (int component = 0; component < 3; ++component)
             value += pos[3 * static_cast<size_t>(atom) + component] * p.inverse_cell[3 * component + axis];
+        rf[3 * static_cast<size_t>(atom) + axis] = value;
         const int w = static_cast<int>(floor(value));
         value -= w;
         fractional[axis] = value;
@@ -269,19 +270,42 @@ __global__ void sort_segments_kernel(int nseg, const int* __restrict__ offsets, 
     }
 }
 
-__global__ void max_displacement_kernel(int n, const double* __restrict__ a, const double* __restrict__ b,
-                                        unsigned long long* __restrict__ out)
+// Minimum-image displacement of every atom from its reference position,
+// the build's fractional position in the current cell (reference
+// prepared_atom_displacements, mace_kokkos_factorized_lifecycle.cpp:2986-3023):
+// delta = pos - frac_ref cell, f = delta cell^-1, f -= floor(f + 1/2),
+// disp = f cell.  out[0] collects max |disp|^2 (as ordered bits; non-finite:
+// infinite).
+__global__ void atom_displacements_kernel(int n, const double* __restrict__ pos,
+                                          const double* __restrict__ frac_ref, const double* __restrict__ cell,
+                                          const double* __restrict__ inverse_cell, double* __restrict__ disp,
+                                          unsigned long long* __restrict__ out)
 {
     __shared__ double s[256];
     const int t = threadIdx.x;
     double m = 0.0;
     for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + t; i < static_cast<size_t>(n);
          i += static_cast<size_t>(gridDim.x) * blockDim.x) {
-        const double dx = a[3 * i] - b[3 * i], dy = a[3 * i + 1] - b[3 * i + 1],
-                     dz = a[3 * i + 2] - b[3 * i + 2];
-        const double d2 = dx * dx + dy * dy + dz * dz;
+        double delta[3], f[3], d[3];
+        for (int c = 0; c < 3; ++c) {
+            double reference = 0.0;
+            for (int axis = 0; axis < 3; ++axis) reference += frac_ref[3 * i + axis] * cell[3 * axis + c];
+            delta[c] = pos[3 * i + c] - reference;
+        }
+        for (int axis = 0; axis < 3; ++axis) {
+            double v = 0.0;
+            for (int c = 0; c < 3; ++c) v += delta[c] * inverse_cell[3 * c + axis];
+            f[axis] = v - floor(v + 0.5);
+        }
+        for (int c = 0; c < 3; ++c) {
+            double v = 0.0;
+            for (int axis = 0; axis < 3; ++axis) v += f[axis] * cell[3 * axis + c];
+            d[c] = v;
+            disp[3 * i + c] = v;
+        }
+        const double d2 = d[0] * d[0] + d[1] * d[1] + d[2] * d[2];
         m = d2 > m ? d2 : m;
-        if (d2 != d2) m = __longlong_as_double(0x7ff0000000000000LL);  // non-finite input: infinite
+        if (!(d2 == d2) || d2 > 1.0e300) m = __longlong_as_double(0x7ff0000000000000LL);
     }
     s[t] = m;
     __syncthreads();
@@ -358,12 +382,12 @@ hipError_t launch_edge_pairs(int num_edges, const int* receiver, const int* sour
     return hipGetLastError();
 }
 
-hipError_t launch_neighbor_bins(const NeighborPlan& p, const double* positions, double* wrapped_positions,
-                                double* wrapped_fractional, int* wrap_shifts, int* atom_bins,
-                                int* bin_sizes, hipStream_t s)
+hipError_t launch_neighbor_bins(const NeighborPlan& p, const double* positions, double* reference_fractional,
+                                double* wrapped_positions, double* wrapped_fractional, int* wrap_shifts,
+                                int* atom_bins, int* bin_sizes, hipStream_t s)
 {
     if (p.num_nodes <= 0) return hipSuccess;
-    bins_kernel<<<(p.num_nodes + 255) / 256, 256, 0, s>>>(p, positions, wrapped_positions,
+    bins_kernel<<<(p.num_nodes + 255) / 256, 256, 0, s>>>(p, positions, reference_fractional, wrapped_positions,
                                                           wrapped_fractional, wrap_shifts, atom_bins,
                                                           bin_sizes);
     return hipGetLastError();
@@ -443,12 +467,16 @@ hipError_t launch_sort_segments(int num_segments, const int* offsets, int* value
     return hipGetLastError();
 }
 
-hipError_t launch_max_displacement(int n, const double* a, const double* b, double* out, hipStream_t s)
+hipError_t launch_atom_displacements(int n, const double* positions, const double* reference_fractional,
+                                     const double* cell, const double* inverse_cell, double* displacements,
+                                     double* out, hipStream_t s)
 {
-    hipError_t err = hipMemsetAsync(out, 0, sizeof(double), s);
+    // out[0]: max |disp|^2, out[1]: invalid-edge count of the edge geometry that follows
+    hipError_t err = hipMemsetAsync(out, 0, 2 * sizeof(double), s);
     if (err != hipSuccess || n <= 0) return err;
     const int blocks = std::min((n + 255) / 256, 1024);
-    max_displacement_kernel<<<blocks, 256, 0, s>>>(n, a, b, reinterpret_cast<unsigned long long*>(out));
+    atom_displacements_kernel<<<blocks, 256, 0, s>>>(n, positions, reference_fractional, cell, inverse_cell,
+                                                     displacements, reinterpret_cast<unsigned long long*>(out));
     return hipGetLastError();
 }
 

@@ -239,10 +239,13 @@ struct ZblArgs {
 hipError_t launch_zbl(int num_nodes, const int* first, const int* edge_pair, const double* xyz, const double* r,
                       const ZblArgs& z, double* energies, double* forces, hipStream_t s);
 
-// Geometry from positions: xyz = pos[src] - pos[recv] + shift . cell
+// Geometry from positions (reference prepared_edge_geometry,
+// mace_kokkos_factorized_lifecycle.cpp:3024-3074): xyz = fractional_xyz . cell
+// + disp[src] - disp[recv]; an edge of zero or non-finite length is set to
+// (r_cut, 0, 0) (inactive) and counted in *invalid.
 hipError_t launch_edge_geometry(int num_edges, const int* receiver, const int* source,
-                                const int* shifts, const double* positions, const double* cell,
-                                double* xyz, double* r, hipStream_t s);
+                                const double* fractional_xyz, const double* displacements, const double* cell,
+                                double r_cut, double* xyz, double* r, unsigned long long* invalid, hipStream_t s);
 
 // Reductions (deterministic, f64)
 hipError_t launch_atom_forces(int num_nodes, const int* first, const int* tfirst, const int* tedge,
@@ -263,9 +266,9 @@ struct NeighborPlan {
     double inverse_cell[9] = {};
     double cutoff_squared = 0.0;
 };
-hipError_t launch_neighbor_bins(const NeighborPlan& p, const double* positions,
-                                double* wrapped_positions, double* wrapped_fractional,
-                                int* wrap_shifts, int* atom_bins, int* bin_sizes, hipStream_t s);
+hipError_t launch_neighbor_bins(const NeighborPlan& p, const double* positions, double* reference_fractional,
+                                double* wrapped_positions, double* wrapped_fractional, int* wrap_shifts,
+                                int* atom_bins, int* bin_sizes, hipStream_t s);
 hipError_t launch_neighbor_fill_bins(const NeighborPlan& p, const int* atom_bins,
                                      const int* bin_offsets, int* bin_cursors, int* bin_atoms,
                                      hipStream_t s);
@@ -290,8 +293,12 @@ hipError_t launch_transpose_count(int num_edges, const int* source, int* counts,
 hipError_t launch_transpose_fill(int num_edges, const int* source, const int* tfirst, int* cursors,
                                  int* tedge, hipStream_t s);
 hipError_t launch_sort_segments(int num_segments, const int* offsets, int* values, hipStream_t s);
-hipError_t launch_max_displacement(int n, const double* a, const double* b, double* out,
-                                   hipStream_t s);
+// Minimum-image displacements of the atoms from their reference fractional
+// positions in the current cell; out[0] = max |disp|^2, out[1] zeroed (the
+// invalid-edge count of launch_edge_geometry).
+hipError_t launch_atom_displacements(int n, const double* positions, const double* reference_fractional,
+                                     const double* cell, const double* inverse_cell, double* displacements,
+                                     double* out, hipStream_t s);
 // edge_pair[e] = ordered | unordered << 16 from the active indices of the
 // receiver and source element types
 hipError_t launch_edge_pairs(int num_edges, const int* receiver, const int* source,

@@ -756,19 +756,26 @@ __global__ void add_direct_kernel(int nodes, int C, int nLM, const float* __rest
 // geometry and reductions
 // ---------------------------------------------------------------------------
 __global__ void edge_geometry_kernel(int E, const int* __restrict__ receiver,
-                                     const int* __restrict__ source, const int* __restrict__ shifts,
-                                     const double* __restrict__ pos, const double* __restrict__ cell,
-                                     double* __restrict__ xyz, double* __restrict__ r)
+                                     const int* __restrict__ source, const double* __restrict__ frac,
+                                     const double* __restrict__ disp, const double* __restrict__ cell,
+                                     double r_cut, double* __restrict__ xyz, double* __restrict__ r,
+                                     unsigned long long* __restrict__ invalid)
 {
     const int e = blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= E) return;
-    const int i = receiver[e], j = source[e];
-    const double s0 = shifts[3 * static_cast<size_t>(e)], s1 = shifts[3 * static_cast<size_t>(e) + 1],
-                 s2 = shifts[3 * static_cast<size_t>(e) + 2];
+    const size_t i = receiver[e], j = source[e];
+    const double f0 = frac[3 * static_cast<size_t>(e)], f1 = frac[3 * static_cast<size_t>(e) + 1],
+                 f2 = frac[3 * static_cast<size_t>(e) + 2];
     double v[3];
     for (int c = 0; c < 3; ++c)
-        v[c] = pos[3 * static_cast<size_t>(j) + c] - pos[3 * static_cast<size_t>(i) + c] +
-               s0 * cell[c] + s1 * cell[3 + c] + s2 * cell[6 + c];
+        v[c] = (f0 * cell[c] + f1 * cell[3 + c] + f2 * cell[6 + c]) + disp[3 * j + c] - disp[3 * i + c];
+    const double d2 = v[0] * v[0] + v[1] * v[1] + v[2] * v[2];
+    if (!(d2 > 0.0) || !(d2 < 1.0e300)) {
+        atomicAdd(invalid, 1ull);
+        v[0] = r_cut;
+        v[1] = 0.0;
+        v[2] = 0.0;
+    }
     xyz[3 * static_cast<size_t>(e)] = v[0];
     xyz[3 * static_cast<size_t>(e) + 1] = v[1];
     xyz[3 * static_cast<size_t>(e) + 2] = v[2];
@@ -1032,12 +1039,12 @@ hipError_t launch_zbl(int num_nodes, const int* first, const int* edge_pair, con
 }
 
 hipError_t launch_edge_geometry(int num_edges, const int* receiver, const int* source,
-                                const int* shifts, const double* positions, const double* cell,
-                                double* xyz, double* r, hipStream_t s)
+                                const double* fractional_xyz, const double* displacements, const double* cell,
+                                double r_cut, double* xyz, double* r, unsigned long long* invalid, hipStream_t s)
 {
     if (num_edges <= 0) return hipSuccess;
-    edge_geometry_kernel<<<(num_edges + 255) / 256, 256, 0, s>>>(num_edges, receiver, source, shifts,
-                                                                 positions, cell, xyz, r);
+    edge_geometry_kernel<<<(num_edges + 255) / 256, 256, 0, s>>>(num_edges, receiver, source, fractional_xyz,
+                                                                 displacements, cell, r_cut, xyz, r, invalid);
     return hipGetLastError();
 }
 

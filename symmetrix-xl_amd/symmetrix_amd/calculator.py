@@ -3,8 +3,13 @@
 Counterpart of the reference's ASE calculator ``Symmetrix``
 (``symmetrix/source/symmetrix/calculator.py:539-757, 2838-3093, 3821-4021``)
 for the model-evaluation path: the neighbour graph is built on the device at
-cutoff + skin and reused while no atom has moved more than skin/2 since the
-build (``calculator.py:2851-2898``); every call evaluates at the current
+cutoff + skin and reused across calls, also across cell changes
+(``calculator.py:2851-2898``): edge vectors are the build's fractional edge
+vectors in the current cell plus the atoms' minimum-image non-affine
+displacements, and the graph stays valid while
+``||cell^-1 cell_build||_2 (cutoff + 2 max|non-affine|) <= cutoff + skin``
+(with an unchanged cell: no atom moved more than skin/2; atoms wrapped back
+into the cell count as not moved).  Every call evaluates at the current
 positions; energy is the FP64 sum of node energies, forces are reduced from
 the directed edge forces, stress is -(1/V) sum f (x) xyz in Voigt order
 (``calculator.py:3821-3894``).
@@ -32,6 +37,22 @@ def _arrays(atoms):
         cell = np.asarray(atoms.cell, dtype=np.float64)
         pbc = np.asarray(getattr(atoms, "pbc", (True, True, True)), dtype=bool)
     return positions, numbers, cell, pbc
+
+
+def topology_valid(cell, topology_cell, max_non_affine, cutoff, skin):
+    """Whether a graph built at cutoff + skin in ``topology_cell`` still holds
+    every pair within ``cutoff`` in ``cell`` after non-affine displacements of
+    at most ``max_non_affine`` (reference calculator.py:2872-2877): a pair
+    within cutoff now was within contraction * (cutoff + 2 max_non_affine) in
+    the build's cell, contraction = ||cell^-1 topology_cell||_2."""
+    try:
+        deformation = np.linalg.solve(np.asarray(cell, dtype=float), np.asarray(topology_cell, dtype=float))
+    except np.linalg.LinAlgError:
+        return False
+    contraction = float(np.linalg.norm(deformation, ord=2))
+    if not np.isfinite(contraction) or not np.isfinite(max_non_affine):
+        return False
+    return contraction * (cutoff + 2.0 * max_non_affine) <= cutoff + skin
 
 
 def full_3x3_to_voigt_6_stress(stress):
@@ -63,8 +84,15 @@ class Symmetrix:
         self._type_of_z = {z: i for i, z in enumerate(self.evaluator.atomic_numbers)}
         self._cache = None
         self.results = {}
-        self.neighbor_rebuild_count = 0
+        # counters of the reference calculator (calculator.py:2900-3040)
+        self.neighbor_cache_build_count = 0
+        self.neighbor_cache_reuse_count = 0
+        self.neighbor_cache_geometry_update_count = 0
         self.calculation_count = 0
+
+    @property
+    def neighbor_rebuild_count(self):
+        return self.neighbor_cache_build_count
 
     # ---- neighbour cache -----------------------------------------------------
     def _node_types(self, numbers):
@@ -73,39 +101,64 @@ class Symmetrix:
         except KeyError as err:
             raise ValueError(f"atomic number {err.args[0]} is not supported by the model") from None
 
-    def _geometry(self, atoms):
-        positions, numbers, cell, pbc = _arrays(atoms)
-        if np.all(pbc):
-            return positions, numbers, cell, True
-        if np.any(pbc):
-            raise NotImplementedError("mixed periodic boundary conditions are not supported")
-        # isolated system: a cubic box larger than the extent plus twice the
-        # neighbour cutoff has no periodic image within the cutoff
+    def _isolated_box(self, positions):
+        """Cubic box of an isolated system: side = extent + 2 (cutoff + skin) + 1,
+        so no periodic image lies within cutoff + skin while the graph is
+        valid (atoms move at most skin/2 each before a rebuild)."""
         reach = self.cutoff + self.neighbor_skin
         lo = positions.min(axis=0) if len(positions) else np.zeros(3)
         hi = positions.max(axis=0) if len(positions) else np.zeros(3)
         side = float(np.max(hi - lo)) + 2.0 * reach + 1.0
-        return positions - lo + reach, numbers, np.eye(3) * side, False
+        return lo - reach, np.eye(3) * side
 
-    def _needs_rebuild(self, positions, numbers, cell):
+    def _geometry(self, atoms):
+        positions, numbers, cell, pbc = _arrays(atoms)
+        if np.any(pbc) and not np.all(pbc):
+            raise NotImplementedError("mixed periodic boundary conditions are not supported")
+        return positions, numbers, cell, bool(np.all(pbc))
+
+    def _reusable(self, positions, numbers, cell, periodic):
         c = self._cache
-        if c is None or len(numbers) != len(c["numbers"]) or np.any(numbers != c["numbers"]):
-            return True
+        if c is None or c["periodic"] != periodic or len(numbers) != len(c["numbers"]) or \
+                np.any(numbers != c["numbers"]):
+            return False
+        ev, gen = self.evaluator, c["generation"]
+        if not periodic:
+            moved = ev._max_displacement(gen, positions - c["offset"])
+            return moved <= 0.5 * self.neighbor_skin
         if not np.array_equal(cell, c["cell"]):
-            return True
-        moved = self.evaluator._max_displacement(c["generation"], positions)
-        return not (moved <= 0.5 * self.neighbor_skin)
+            try:
+                inverse = np.linalg.inv(cell)
+            except np.linalg.LinAlgError:
+                return False
+            ev._update_factorized_cell(gen, cell, inverse)
+            c["cell"] = cell.copy()
+            self.neighbor_cache_geometry_update_count += 1
+        moved = ev._max_displacement(gen, positions)
+        return topology_valid(cell, c["topology_cell"], moved, self.cutoff, self.neighbor_skin)
 
     def _prepare(self, atoms):
+        """Positions and cell the evaluator sees (isolated systems are shifted
+        into their cached box), rebuilding the graph when it is not reusable."""
         positions, numbers, cell, periodic = self._geometry(atoms)
-        if self._needs_rebuild(positions, numbers, cell):
+        if self._reusable(positions, numbers, cell, periodic):
+            self.neighbor_cache_reuse_count += 1
+        else:
+            offset = np.zeros(3)
+            if not periodic:
+                offset, cell = self._isolated_box(positions)
             types = self._node_types(numbers)
             info = self.evaluator._prepare_periodic_factorized_graph(
-                types, positions, cell, np.linalg.inv(cell), self.cutoff + self.neighbor_skin)
-            self._cache = {"generation": info["generation"], "numbers": numbers.copy(), "cell": cell.copy(),
+                types, positions - offset, cell, np.linalg.inv(cell), self.cutoff + self.neighbor_skin)
+            self._cache = {"generation": info["generation"], "numbers": numbers.copy(), "periodic": periodic,
+                           "cell": cell.copy(), "topology_cell": cell.copy(), "offset": offset,
                            "num_edges": info["num_edges"]}
-            self.neighbor_rebuild_count += 1
-        return positions, cell, periodic
+            self.neighbor_cache_build_count += 1
+            self.neighbor_cache_geometry_update_count += 1
+        c = self._cache
+        if not periodic:
+            return positions - c["offset"], c["cell"], False
+        return positions, cell, True
 
     # ---- evaluation -----------------------------------------------------------------
     def calculate(self, atoms=None, properties=("energy", "forces", "stress"), system_changes=None):

@@ -1,0 +1,143 @@
+"""GPU: the calculator's neighbour-graph reuse across wrapped atoms, cell
+changes and isolated-system motion (reference calculator.py:2838-3093), each
+against a freshly built graph and the CPU oracle on the same inputs, plus the
+invalid-geometry error of the prepared-positions path
+(mace_kokkos_factorized_lifecycle.cpp:3078-3085)."""
+
+import json
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+E_TOL = 1e-5   # eV/atom
+F_TOL = 1e-4   # eV/A
+S_TOL = 1e-6   # eV/A^3
+
+
+@pytest.fixture(scope="module")
+def tiny(tmp_path_factory):
+    from symmetrix_amd import synthetic
+
+    text = synthetic.model_json(synthetic.random_mace_model("tiny", seed=0))
+    path = tmp_path_factory.mktemp("calc") / "tiny.json"
+    path.write_text(text)
+    return str(path), json.loads(text)
+
+
+def _close(a, b, n, stress=True):
+    de = abs(a["energy"] - b["energy"]) / n
+    df = float(np.max(np.abs(a["forces"] - b["forces"])))
+    ds = float(np.max(np.abs(a["stress"] - b["stress"]))) if stress else 0.0
+    print(f"  |dE|/atom={de:.3e}  max|dF|={df:.3e}  max|dS|={ds:.3e}", flush=True)
+    assert de < E_TOL and df < F_TOL and ds < S_TOL
+
+
+def _oracle(oracle_lib, model, s):
+    from symmetrix_amd import synthetic
+
+    types = synthetic.node_types(s, model["atomic_numbers"])
+    orc = oracle_lib.MaceOracle(model, np.unique(types), "float32")
+    return oracle_lib.evaluate(orc, s, model["r_cut"] + 0.5)
+
+
+def test_wrapped_atoms_reuse_the_graph(tiny):
+    from symmetrix_amd import Symmetrix, synthetic
+
+    path, _ = tiny
+    s = synthetic.srtio3_supercell(3, sigma=0.05, seed=11)
+    calc = Symmetrix(path, neighbor_skin=0.5)
+    base = calc.calculate(s)
+    wrapped = s.copy()
+    # whole lattice vectors on a few atoms, then every atom wrapped into the cell
+    wrapped.positions[[0, 7, 40]] += s.cell[0] - 2 * s.cell[2]
+    frac = wrapped.positions @ np.linalg.inv(s.cell)
+    wrapped.positions = (frac - np.floor(frac)) @ s.cell
+    print("wrapped atoms, unchanged cell", flush=True)
+    assert calc.evaluator._max_displacement(calc._cache["generation"], wrapped.positions) < 1e-9
+    got = calc.calculate(wrapped)
+    assert calc.neighbor_cache_build_count == 1 and calc.neighbor_cache_reuse_count == 1
+    _close(got, base, len(s))
+
+
+@pytest.mark.parametrize("strain", [0.01, -0.01, "shear"])
+def test_cell_change_reuses_the_graph(oracle_lib, tiny, strain):
+    from symmetrix_amd import Symmetrix, synthetic
+
+    path, model = tiny
+    s = synthetic.srtio3_supercell(3, sigma=0.05, seed=12)
+    calc = Symmetrix(path, neighbor_skin=0.5)
+    calc.calculate(s)
+    F = np.eye(3)
+    if strain == "shear":
+        F[0, 1] = 0.02
+    else:
+        F *= 1.0 + strain
+    t = s.copy()
+    t.cell = s.cell @ F.T
+    t.positions = s.positions @ F.T + np.random.default_rng(3).normal(scale=0.03, size=s.positions.shape)
+    print(f"cell change {strain}", flush=True)
+    got = calc.calculate(t)
+    assert calc.neighbor_cache_build_count == 1 and calc.neighbor_cache_reuse_count == 1
+    assert calc.neighbor_cache_geometry_update_count == 2
+    _close(got, Symmetrix(path, neighbor_skin=0.5).calculate(t), len(s))
+    _close(got, _oracle(oracle_lib, model, t), len(s))
+
+
+def test_large_compression_rebuilds(tiny):
+    from symmetrix_amd import Symmetrix, synthetic
+
+    path, _ = tiny
+    s = synthetic.srtio3_supercell(3, sigma=0.05, seed=13)
+    calc = Symmetrix(path, neighbor_skin=0.5)
+    calc.calculate(s)
+    t = s.copy()
+    t.cell = s.cell * 0.9
+    t.positions = s.positions * 0.9
+    got = calc.calculate(t)
+    assert calc.neighbor_cache_build_count == 2
+    _close(got, Symmetrix(path, neighbor_skin=0.5).calculate(t), len(s))
+
+
+def test_isolated_cluster_reuses_its_box(oracle_lib, tiny):
+    from symmetrix_amd import Symmetrix, synthetic
+
+    path, model = tiny
+    rng = np.random.default_rng(5)
+    pos = synthetic.srtio3_supercell(2, sigma=0.05, seed=14).positions[:20]
+    nums = np.array([38, 22, 8, 8, 8] * 4)
+    cluster = synthetic.Structure(pos, nums, np.zeros((3, 3)), pbc=(False, False, False))
+    calc = Symmetrix(path, neighbor_skin=0.5)
+    calc.calculate(cluster)
+    moved = cluster.copy()
+    # within skin/2 = 0.25 A of the build positions (a rigid shift counts as motion)
+    moved.positions = moved.positions + rng.normal(scale=0.03, size=pos.shape) + np.array([0.05, -0.03, 0.02])
+    assert np.max(np.linalg.norm(moved.positions - cluster.positions, axis=1)) < 0.25
+    print("isolated cluster, small motion", flush=True)
+    got = calc.calculate(moved)
+    assert calc.neighbor_cache_build_count == 1
+    fresh = Symmetrix(path, neighbor_skin=0.5).calculate(moved)
+    _close(got, fresh, len(nums), stress=False)
+    # the oracle in a box large enough to hold no images within the cutoff
+    boxed = synthetic.Structure(moved.positions - moved.positions.min(axis=0) + 7.0, nums, np.eye(3) * 40.0)
+    want = _oracle(oracle_lib, model, boxed)
+    _close(got, want, len(nums), stress=False)
+
+
+def test_coincident_atoms_raise_invalid_geometry(tiny):
+    from symmetrix_amd import MACEKokkosFloat, synthetic
+
+    path, model = tiny
+    s = synthetic.srtio3_supercell(2, sigma=0.0, seed=0)
+    s.positions[1] = s.positions[0]
+    ev = MACEKokkosFloat(path)
+    types = synthetic.node_types(s, model["atomic_numbers"])
+    gen = ev._prepare_periodic_factorized_graph(types, s.positions, s.cell, np.linalg.inv(s.cell), 5.5)["generation"]
+    with pytest.raises(ValueError, match="invalid edge geometry"):
+        ev._compute_prepared_factorized_positions(gen, s.positions)
+    # the next valid evaluation of a separated configuration succeeds
+    s.positions[1] += np.array([0.9, 0.0, 0.0])
+    gen = ev._prepare_periodic_factorized_graph(types, s.positions, s.cell, np.linalg.inv(s.cell), 5.5)["generation"]
+    ev._compute_prepared_factorized_positions(gen, s.positions)
+    assert np.isfinite(ev._total_energy(gen))
