@@ -199,9 +199,9 @@ KB_EV = 8.617333262e-5
 def capacity_run(args):
     """Tiled-mode capacity: medium model on SrTiO3 n^3 (5 n^3 atoms), a
     velocity-Verlet NVE run of --md-steps steps at --md-dt fs from 300 K
-    Maxwell-Boltzmann velocities.  Positions live on the host and are copied
-    to the device each step; the graph is rebuilt on the device when an atom
-    has moved more than half the skin.  Prints one JSON line."""
+    Maxwell-Boltzmann velocities with the device NVE driver (positions,
+    velocities and forces stay in HBM; the graph is rebuilt on the device when
+    an atom has moved more than half the skin).  Prints one JSON line."""
     from symmetrix_amd import MACEKokkosFloat, synthetic
 
     t_setup = time.perf_counter()
@@ -214,63 +214,32 @@ def capacity_run(args):
     if args.tile_receivers > 0:
         ev._set_dual_layer_workspace_receiver_limit_for_testing(args.tile_receivers)
     types = synthetic.node_types(s, ev.atomic_numbers)
-    cutoff = ev.r_cut + args.skin
-    cell = s.cell
-    inv = np.linalg.inv(cell)
-    hip = HipMemory()
-    x = np.ascontiguousarray(s.positions, dtype=np.float64)
-    d_pos = hip.upload(x)
-    info = ev._prepare_periodic_factorized_graph_device(types, d_pos, cell, inv, cutoff)
-    gen = info["generation"]
-    st = ev.stats
-    print(f"[capacity] {info['num_edges']} edges, {st['num_tiles']} tiles of {st['tile_receivers']} receivers, "
-          f"{st['device_bytes'] / 2**30:.1f} GiB on the device, setup {time.perf_counter() - t_setup:.1f} s",
-          file=sys.stderr, flush=True)
-    masses = np.array([MASSES[int(z)] for z in (38, 22, 8)])
-    m = np.empty(N)
-    for z, mass in zip((38, 22, 8), masses):
-        m[s.numbers == z] = mass
+    m = np.array([MASSES[int(z)] for z in s.numbers])
     rng = np.random.default_rng(args.seed + 1)
     # v in A/fs: sqrt(kT/m), kT/m in eV/amu times the unit factor gives (A/fs)^2
     v = rng.normal(size=(N, 3)) * np.sqrt(KB_EV * 300.0 * EV_PER_A_AMU_TO_A_PER_FS2 / m)[:, None]
     v -= (m[:, None] * v).sum(0) / m.sum()
-    inv_m = EV_PER_A_AMU_TO_A_PER_FS2 / m[:, None]
-    rebuilds = 0
-
-    def forces(positions):
-        nonlocal gen, rebuilds
-        hip.copy_to_device(d_pos, positions)
-        if not ev._max_displacement_device(gen, d_pos) <= 0.5 * args.skin:
-            gen = ev._prepare_periodic_factorized_graph_device(types, d_pos, cell, inv, cutoff)["generation"]
-            rebuilds += 1
-        ev._compute_prepared_factorized_positions_device(gen, d_pos)
-        return ev._reduce_atom_forces(N, None, None, gen), ev._total_energy(gen)
-
-    dt = args.md_dt
-    f, epot = forces(x)
-    e0 = epot + 0.5 * float((m[:, None] * v * v).sum()) / EV_PER_A_AMU_TO_A_PER_FS2
-    times = []
-    etot = [e0]
-    for step in range(args.md_steps):
-        t0 = time.perf_counter()
-        a = f * inv_m
-        x = x + v * dt + 0.5 * a * dt * dt
-        f, epot = forces(x)
-        v = v + 0.5 * (a + f * inv_m) * dt
-        times.append(time.perf_counter() - t0)
-        ekin = 0.5 * float((m[:, None] * v * v).sum()) / EV_PER_A_AMU_TO_A_PER_FS2
-        etot.append(epot + ekin)
-        print(f"[capacity] step {step + 1}: {times[-1]:.2f} s, E_tot {etot[-1]:.6f} eV", file=sys.stderr, flush=True)
+    print(f"[capacity] setup {time.perf_counter() - t_setup:.1f} s; running {args.md_steps} steps on the device",
+          file=sys.stderr, flush=True)
+    t_run = time.perf_counter()
+    res = ev._md_nve(types, m, s.positions, v, s.cell, args.skin, args.md_dt, args.md_steps)
+    t_run = time.perf_counter() - t_run
+    times = list(res["step_seconds"])
+    etot = res["potential_energy"] + res["kinetic_energy"]
+    for step, t in enumerate(times):
+        print(f"[capacity] step {step + 1}: {t:.3f} s, E_tot {etot[step + 1]:.6f} eV", file=sys.stderr, flush=True)
     st = ev.stats
     line = {
         "metric": "tiled capacity: atoms per MI355X and us/atom/step of a 20-step NVE run (FP32)",
         "capacity_atoms": N,
-        "edges": int(info["num_edges"]),
-        "us_per_atom_per_step": round(statistics.mean(times) / N * 1e6, 5),
+        "edges": int(ev._graph_size()[1]),
+        "us_per_atom_per_step": round(statistics.mean(times) / N * 1e6, 5) if times else None,
+        "us_per_atom_per_step_median": round(statistics.median(times) / N * 1e6, 5) if times else None,
         "md_steps": args.md_steps,
-        "md_dt_fs": dt,
-        "max_energy_drift_per_atom_eV": round(max(abs(e - e0) for e in etot) / N, 9),
-        "neighbor_rebuilds": rebuilds,
+        "md_dt_fs": args.md_dt,
+        "max_energy_drift_per_atom_eV": round(float(np.max(np.abs(etot - etot[0]))) / N, 9),
+        "neighbor_rebuilds": res["rebuilds"],
+        "run_seconds_including_first_build": round(t_run, 2),
         "tile_receivers": st["tile_receivers"],
         "num_tiles": st["num_tiles"],
         "tiled_evaluations": st["tiled_evaluations"],
@@ -278,10 +247,9 @@ def capacity_run(args):
         "config": {"workload": f"medium-shape random-init MACE ({args.preset}) on SrTiO3 {args.capacity_cells}^3 "
                                f"({N} atoms, sigma {args.sigma} A, seed {args.seed}), cutoff {ev.r_cut} + "
                                f"{args.skin} A skin, 300 K Maxwell-Boltzmann start",
-                   "positions": "host, copied to the device each step"},
+                   "integrator": "device velocity-Verlet NVE (sxl_md_nve)"},
     }
     print(json.dumps(line), flush=True)
-    hip.free(d_pos)
 
 
 def main():

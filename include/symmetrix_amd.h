@@ -142,6 +142,25 @@ int sxl_compute_node_energies_forces(sxl_evaluator* evaluator, int num_nodes, co
 int sxl_max_displacement(sxl_evaluator* evaluator, uint64_t generation, const double* positions,
                          int positions_on_device, double* out);
 
+/* Velocity-Verlet NVE molecular dynamics with positions, velocities and
+ * forces resident on the device: the update of LAMMPS `fix nve` that the
+ * reference's capacity runs apply with pair_style symmetrix/mace
+ * (pair_symmetrix/pair_symmetrix_mace.cpp:309-441 supplies the forces).  Per
+ * step: v += dt/2 F/m, x += dt v, forces at x, v += dt/2 F/m, with F/m in
+ * A/fs^2 from eV/A and amu.  positions [N][3] (A) and velocities [N][3]
+ * (A/fs) are read and overwritten with the final state; masses [N] in amu;
+ * node_types are model element indices; dt in fs.  The periodic graph is
+ * built on the device at r_cut + skin and rebuilt whenever an atom has moved
+ * more than skin/2.  potential_energy and kinetic_energy (eV, steps + 1
+ * values each, may be null) receive the energies after every step (index 0:
+ * the start); step_seconds (steps values, may be null) the wall time of each
+ * step with its work completed; rebuilds (may be null) the number of rebuilds
+ * after the first build.  Leaves the last step's graph prepared. */
+int sxl_md_nve(sxl_evaluator* evaluator, int num_atoms, const int* node_types, const double* masses,
+               double* positions, double* velocities, const double* cell, const double* inverse_cell, double skin,
+               double dt, int steps, double* potential_energy, double* kinetic_energy, double* step_seconds,
+               int* rebuilds);
+
 /* node_energies property, N doubles (mace_kokkos.cpp:2086-2093). */
 int sxl_node_energies(const sxl_evaluator* evaluator, double* out, int num_nodes);
 /* node_forces property, directed edge forces [E][3] (mace_kokkos.cpp:2094-2101). */

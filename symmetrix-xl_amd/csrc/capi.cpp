@@ -197,6 +197,18 @@ int sxl_max_displacement(sxl_evaluator* ev, uint64_t generation, const double* p
     return guarded([&] { *out = ev->impl.max_displacement(generation, positions, on_device != 0); });
 }
 
+int sxl_md_nve(sxl_evaluator* ev, int num_atoms, const int* node_types, const double* masses, double* positions,
+               double* velocities, const double* cell, const double* inverse_cell, double skin, double dt, int steps,
+               double* potential_energy, double* kinetic_energy, double* step_seconds, int* rebuilds)
+{
+    if (!ev || !node_types || !masses || !positions || !velocities || !cell || !inverse_cell) return null_handle();
+    return guarded([&] {
+        const int n = ev->impl.md_nve(num_atoms, node_types, masses, positions, velocities, cell, inverse_cell, skin,
+                                      dt, steps, potential_energy, kinetic_energy, step_seconds);
+        if (rebuilds) *rebuilds = n;
+    });
+}
+
 int sxl_node_energies(const sxl_evaluator* ev, double* out, int num_nodes)
 {
     if (!ev || (!out && num_nodes > 0)) return null_handle();

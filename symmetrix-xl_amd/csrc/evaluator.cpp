@@ -710,7 +710,7 @@ void Evaluator::finish_graph(const int* host_neigh_types)
 {
     const int N = num_nodes_;
     const int E = static_cast<int>(num_edges_);
-    receiver_.reserve(std::max(E, 1) * sizeof(int));
+    receiver_.reserve(static_cast<std::size_t>(std::max(E, 1)) * sizeof(int));
     hip_check(launch_receivers(N, first_.as<int>(), receiver_.as<int>(), stream_), "receivers");
     // transpose: count -> scan -> fill -> sort each source segment ascending
     DeviceBuffer counts, offsets64;
@@ -725,14 +725,14 @@ void Evaluator::finish_graph(const int* host_neigh_types)
     tfirst_.reserve((N + 1) * sizeof(int));
     hip_check(launch_narrow_offsets(offsets64.as<long long>(), N, tfirst_.as<int>(), nullptr, stream_),
               "narrow");
-    tedge_.reserve(std::max(E, 1) * sizeof(int));
+    tedge_.reserve(static_cast<std::size_t>(std::max(E, 1)) * sizeof(int));
     hip_check(hipMemsetAsync(counts.as<void>(), 0, (N + 1) * sizeof(int), stream_), "memset");
     hip_check(launch_transpose_fill(E, source_.as<int>(), tfirst_.as<int>(), counts.as<int>(),
                                     tedge_.as<int>(), stream_),
               "transpose fill");
     hip_check(launch_sort_segments(N, tfirst_.as<int>(), tedge_.as<int>(), stream_), "sort");
     // edge pair indices
-    edge_pair_.reserve(std::max(E, 1) * sizeof(int));
+    edge_pair_.reserve(static_cast<std::size_t>(std::max(E, 1)) * sizeof(int));
     if (host_neigh_types) {
         // caller-provided source types (prepare_graph): computed on the host
         std::vector<int> ta(model_.num_elements, -1);
@@ -860,10 +860,11 @@ void build_periodic_graph(const double* d_positions, int num_nodes, const double
         throw std::length_error("neighbor graph bin count exceeds 32-bit indexing");
     const int num_bins = static_cast<int>(num_bins_size);
     DeviceBuffer wp, wf, wrap, atom_bins, bin_sizes, bin_off64, bin_offsets, bin_atoms, counts, offsets, scratch;
-    out.fractional_positions.reserve(std::max(N, 1) * 3 * sizeof(double));
-    wp.reserve(std::max(N, 1) * 3 * sizeof(double));
-    wf.reserve(std::max(N, 1) * 3 * sizeof(double));
-    wrap.reserve(std::max(N, 1) * 3 * sizeof(int));
+    const std::size_t N3 = static_cast<std::size_t>(std::max(N, 1)) * 3;
+    out.fractional_positions.reserve(N3 * sizeof(double));
+    wp.reserve(N3 * sizeof(double));
+    wf.reserve(N3 * sizeof(double));
+    wrap.reserve(N3 * sizeof(int));
     atom_bins.reserve(std::max(N, 1) * sizeof(int));
     bin_sizes.reserve((num_bins + 1) * sizeof(int));
     bin_off64.reserve((num_bins + 1) * sizeof(long long));
@@ -905,9 +906,10 @@ void build_periodic_graph(const double* d_positions, int num_nodes, const double
     const int E = static_cast<int>(total);
     out.first.reserve((N + 1) * sizeof(int));
     hip_check(launch_narrow_offsets(offsets.as<long long>(), N, out.first.as<int>(), nullptr, stream), "narrow");
-    out.sources.reserve(std::max(E, 1) * sizeof(int));
-    out.shifts.reserve(std::max(E, 1) * 3 * sizeof(int));
-    out.fractional_xyz.reserve(std::max(E, 1) * 3 * sizeof(double));
+    out.sources.reserve(static_cast<std::size_t>(std::max(E, 1)) * sizeof(int));
+    // sizes in size_t: 3 E overflows 32 bits beyond ~1.43 G edges
+    out.shifts.reserve(static_cast<std::size_t>(std::max(E, 1)) * 3 * sizeof(int));
+    out.fractional_xyz.reserve(static_cast<std::size_t>(std::max(E, 1)) * 3 * sizeof(double));
     hip_check(launch_neighbor_edges(plan, wp.as<double>(), wf.as<double>(), wrap.as<int>(), atom_bins.as<int>(),
                                     bin_offsets.as<int>(), bin_atoms.as<int>(), offsets.as<long long>(), nullptr,
                                     out.sources.as<int>(), out.shifts.as<int>(), out.fractional_xyz.as<double>(),
@@ -926,19 +928,19 @@ std::uint64_t Evaluator::prepare_periodic_graph(int num_nodes, const int* node_t
     std::vector<int> types(node_types, node_types + num_nodes);
     prepare_active_types(types);
     const int N = num_nodes;
-    positions_.reserve(std::max(N, 1) * 3 * sizeof(double));
+    positions_.reserve(static_cast<std::size_t>(std::max(N, 1)) * 3 * sizeof(double));
     if (N > 0)
         hip_check(hipMemcpyAsync(positions_.as<double>(), positions, N * 3 * sizeof(double),
                                  device_positions ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, stream_),
                   "positions");
-    disp_.reserve(std::max(N, 1) * 3 * sizeof(double));
+    disp_.reserve(static_cast<std::size_t>(std::max(N, 1)) * 3 * sizeof(double));
     build_periodic_graph(positions_.as<double>(), N, cell, inverse_cell, cutoff, stream_, pgraph_);
     const int E = static_cast<int>(pgraph_.num_edges);
     first_.reserve((N + 1) * sizeof(int));
     hip_check(hipMemcpyAsync(first_.as<int>(), pgraph_.first.as<int>(), (N + 1) * sizeof(int),
                              hipMemcpyDeviceToDevice, stream_),
               "copy");
-    source_.reserve(std::max(E, 1) * sizeof(int));
+    source_.reserve(static_cast<std::size_t>(std::max(E, 1)) * sizeof(int));
     if (E > 0)
         hip_check(hipMemcpyAsync(source_.as<int>(), pgraph_.sources.as<int>(), E * sizeof(int),
                                  hipMemcpyDeviceToDevice, stream_),
@@ -1476,6 +1478,81 @@ void Evaluator::evaluate_tiled()
     stats_.tiled_evaluations += 1;
     stats_.last_evaluation_ms =
         std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+}
+
+// 1 eV / (A amu) in A / fs^2
+constexpr double kForceToAcceleration = 9.648533212e-3;
+
+// Velocity-Verlet NVE (the LAMMPS `fix nve` update the reference's capacity
+// runs use with pair_style symmetrix/mace): per step v += dt/2 a, x += dt v,
+// forces at the new positions, v += dt/2 a.  Every array stays on the
+// device; the host reads three scalars per step (max displacement, potential
+// and kinetic energy).
+int Evaluator::md_nve(int num_atoms, const int* node_types, const double* masses, double* x, double* v,
+                      const double* cell, const double* inverse_cell, double skin, double dt, int steps,
+                      double* epot, double* ekin, double* step_seconds)
+{
+    if (num_atoms <= 0) throw std::invalid_argument("MD requires at least one atom");
+    if (steps < 0) throw std::invalid_argument("MD step count must be non-negative");
+    if (!std::isfinite(dt) || !(dt > 0.0)) throw std::invalid_argument("MD time step must be finite and positive");
+    if (!std::isfinite(skin) || skin < 0.0) throw std::invalid_argument("neighbor skin must be finite and non-negative");
+    const int N = num_atoms;
+    std::vector<double> m(masses, masses + N), inv_m(N);
+    for (int a = 0; a < N; ++a) {
+        if (!std::isfinite(m[a]) || !(m[a] > 0.0)) throw std::invalid_argument("MD masses must be finite and positive");
+        inv_m[a] = kForceToAcceleration / m[a];
+    }
+    const std::size_t bytes3 = static_cast<std::size_t>(N) * 3 * sizeof(double);
+    md_x_.reserve(bytes3);
+    md_v_.reserve(bytes3);
+    hip_check(hipMemcpyAsync(md_x_.as<double>(), x, bytes3, hipMemcpyHostToDevice, stream_), "MD positions");
+    hip_check(hipMemcpyAsync(md_v_.as<double>(), v, bytes3, hipMemcpyHostToDevice, stream_), "MD velocities");
+    upload(md_m_, m, stream_);
+    upload(md_inv_m_, inv_m, stream_);
+    const int np = md_kinetic_partials(N);
+    md_partials_.reserve(static_cast<std::size_t>(np) * sizeof(double));
+    double* xd = md_x_.as<double>();
+    double* vd = md_v_.as<double>();
+    const double cutoff = model_.r_cut + skin;
+
+    std::uint64_t gen = prepare_periodic_graph(N, node_types, xd, true, cell, inverse_cell, cutoff);
+    int rebuilds = 0;
+    auto energies = [&](int step) {
+        if (epot) epot[step] = total_energy(gen);
+        if (ekin) {
+            hip_check(launch_md_kinetic(N, vd, md_m_.as<double>(), md_partials_.as<double>(), np,
+                                        totals_.as<double>() + 14, stream_),
+                      "kinetic energy");
+            double mv2 = 0.0;
+            hip_check(hipMemcpyAsync(&mv2, totals_.as<double>() + 14, sizeof(double), hipMemcpyDeviceToHost, stream_),
+                      "copy");
+            hip_check(hipStreamSynchronize(stream_), "kinetic energy");
+            ekin[step] = 0.5 * mv2 / kForceToAcceleration;
+        }
+    };
+    compute_positions(gen, xd, true);
+    energies(0);
+    const double dtf = 0.5 * dt;
+    for (int step = 1; step <= steps; ++step) {
+        const auto t0 = std::chrono::steady_clock::now();
+        hip_check(launch_md_kick_drift(N, xd, vd, atom_forces_.as<double>(), md_inv_m_.as<double>(), dtf, dt, stream_),
+                  "MD drift");
+        if (!(max_displacement(gen, xd, true) <= 0.5 * skin)) {
+            gen = prepare_periodic_graph(N, node_types, xd, true, cell, inverse_cell, cutoff);
+            ++rebuilds;
+        }
+        compute_positions(gen, xd, true);
+        hip_check(launch_md_kick(N, vd, atom_forces_.as<double>(), md_inv_m_.as<double>(), dtf, stream_), "MD kick");
+        if (step_seconds) {
+            hip_check(hipStreamSynchronize(stream_), "MD step");
+            step_seconds[step - 1] = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+        }
+        energies(step);
+    }
+    hip_check(hipMemcpyAsync(x, xd, bytes3, hipMemcpyDeviceToHost, stream_), "MD positions");
+    hip_check(hipMemcpyAsync(v, vd, bytes3, hipMemcpyDeviceToHost, stream_), "MD velocities");
+    hip_check(hipStreamSynchronize(stream_), "MD");
+    return rebuilds;
 }
 
 // Waits for the evaluation; an evaluation from positions raises when the

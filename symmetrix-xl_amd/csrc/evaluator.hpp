@@ -145,6 +145,18 @@ public:
     // periodic graph build, on the device (for neighbour-list skin reuse).
     double max_displacement(std::uint64_t generation, const double* positions, bool device_positions);
 
+    // --- device NVE molecular dynamics -----------------------------------------
+    // Velocity-Verlet NVE run of `steps` steps of dt (fs) with positions,
+    // velocities and forces resident on the device: x [N][3] (A) and v [N][3]
+    // (A/fs) host arrays in/out, masses [N] (amu), epot / ekin [steps + 1]
+    // (eV) and step_seconds [steps] (wall time of each step, the step's work
+    // completed) host outputs (may be null).  The graph is built at r_cut +
+    // skin and rebuilt on the device when an atom has moved more than skin/2.
+    // Returns the number of rebuilds after the first build.
+    int md_nve(int num_atoms, const int* node_types, const double* masses, double* x, double* v,
+               const double* cell, const double* inverse_cell, double skin, double dt, int steps, double* epot,
+               double* ekin, double* step_seconds);
+
     // --- results -------------------------------------------------------------
     void node_energies(double* out) const;            // [N]
     void node_forces(double* out) const;              // [E][3] directed, -dE/dxyz
@@ -251,6 +263,8 @@ private:
     // M0s_: [N][C] scalar readout input x (M0 scalar block, or M0_scalar P0
     // (+ residual) in the pre_linear_up basis), graph-wide
     DeviceBuffer M0s_, run_source_, run_start_, run_length_;
+    // device NVE driver state: positions, velocities, masses, unit factor / mass, kinetic partials
+    DeviceBuffer md_x_, md_v_, md_m_, md_inv_m_, md_partials_;
     // nodes grouped by (tile, active type) and their blocks for the node kernels
     DeviceBuffer node_order_, m0_blocks_, readout_blocks_;
     std::vector<int> m0_block_offsets_, readout_block_offsets_;  // [tiles + 1]

@@ -293,6 +293,16 @@ hipError_t launch_transpose_count(int num_edges, const int* source, int* counts,
 hipError_t launch_transpose_fill(int num_edges, const int* source, const int* tfirst, int* cursors,
                                  int* tedge, hipStream_t s);
 hipError_t launch_sort_segments(int num_segments, const int* offsets, int* values, hipStream_t s);
+// Velocity-Verlet updates of the device NVE driver (md.hip): x, v, f are
+// [N][3] doubles, inv_m [N] (unit factor / mass), m [N] masses.
+hipError_t launch_md_kick_drift(int num_atoms, double* x, double* v, const double* f, const double* inv_m,
+                                double dtf, double dt, hipStream_t s);
+hipError_t launch_md_kick(int num_atoms, double* v, const double* f, const double* inv_m, double dtf,
+                          hipStream_t s);
+// out[0] = sum m |v|^2 over the atoms (deterministic two-stage sum)
+int md_kinetic_partials(int num_atoms);
+hipError_t launch_md_kinetic(int num_atoms, const double* v, const double* m, double* partials, int num_partials,
+                             double* out, hipStream_t s);
 // Minimum-image displacements of the atoms from their reference fractional
 // positions in the current cell; out[0] = max |disp|^2, out[1] zeroed (the
 // invalid-edge count of launch_edge_geometry).

@@ -73,6 +73,9 @@ SIGNATURES = {
                                                         c_int_p, c_int_p, c_double_p, c_double_p]),
     "sxl_max_displacement": (ctypes.c_int, [ctypes.c_void_p, c_u64, ctypes.c_void_p, ctypes.c_int,
                                             c_double_p]),
+    "sxl_md_nve": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, c_int_p, c_double_p, c_double_p, c_double_p,
+                                  c_double_p, c_double_p, ctypes.c_double, ctypes.c_double, ctypes.c_int,
+                                  c_double_p, c_double_p, c_double_p, c_int_p]),
     "sxl_node_energies": (ctypes.c_int, [ctypes.c_void_p, c_double_p, ctypes.c_int]),
     "sxl_node_forces": (ctypes.c_int, [ctypes.c_void_p, c_double_p, c_i64]),
     "sxl_reduce_atom_forces": (ctypes.c_int, [ctypes.c_void_p, c_u64, c_double_p]),

@@ -214,6 +214,34 @@ class MACEKokkosFloat:
         _, _, self._generation = self._graph_size()
         self._evaluated = True
 
+    def _md_nve(self, node_types, masses, positions, velocities, cell, skin, dt, steps):
+        """Velocity-Verlet NVE run on the device (the `fix nve` update of the
+        reference's LAMMPS capacity runs).  positions (A), velocities (A/fs),
+        masses (amu), dt (fs).  Returns the final positions and velocities,
+        the potential and kinetic energies (eV) at the start and after every
+        step, each step's wall time and the number of neighbour-graph
+        rebuilds."""
+        types = _i32(node_types, name="node_types")
+        n = types.size
+        m = _f64(masses, n, "masses")
+        x = _f64(positions, 3 * n, "positions").copy()
+        v = _f64(velocities, 3 * n, "velocities").copy()
+        c = _f64(cell, 9, "cell")
+        inv = _f64(np.linalg.inv(c.reshape(3, 3)), 9, "inverse_cell")
+        steps = int(steps)
+        epot = np.zeros(max(steps, 0) + 1)
+        ekin = np.zeros(max(steps, 0) + 1)
+        seconds = np.zeros(max(steps, 1))
+        rebuilds = ctypes.c_int(0)
+        check(library().sxl_md_nve(self._h, n, _p(types, ctypes.c_int), _p(m, ctypes.c_double),
+                                   _p(x, ctypes.c_double), _p(v, ctypes.c_double), _p(c, ctypes.c_double),
+                                   _p(inv, ctypes.c_double), float(skin), float(dt), steps,
+                                   _p(epot, ctypes.c_double), _p(ekin, ctypes.c_double),
+                                   _p(seconds, ctypes.c_double), ctypes.byref(rebuilds)))
+        self._evaluated = True
+        return {"positions": x.reshape(n, 3), "velocities": v.reshape(n, 3), "potential_energy": epot,
+                "kinetic_energy": ekin, "step_seconds": seconds[:max(steps, 0)], "rebuilds": int(rebuilds.value)}
+
     def _max_displacement(self, generation, positions):
         n, _, _ = self._graph_size()
         pos = _f64(positions, 3 * n, "positions")
