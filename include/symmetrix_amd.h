@@ -142,6 +142,23 @@ int sxl_compute_node_energies_forces(sxl_evaluator* evaluator, int num_nodes, co
 int sxl_max_displacement(sxl_evaluator* evaluator, uint64_t generation, const double* positions,
                          int positions_on_device, double* out);
 
+/* LAMMPS pair_style symmetrix/mace on one rank: replaces
+ * PairSymmetrixMACE::compute_no_domain_decomposition
+ * (pair_symmetrix/pair_symmetrix_mace.cpp:309-441).  The arguments are the
+ * pair style's own data: a full neighbour list (inum, ilist, numneigh and
+ * firstneigh indexed by atom, entries masked with NEIGHMASK 0x1FFFFFFF) over
+ * nall local + ghost atoms with coordinates x [nall][3] and 1-based types;
+ * local_of[j] = atom->map(atom->tag[j]) maps every atom to its local atom;
+ * mace_types [ntypes] is the pair_coeff map from LAMMPS type to model element.
+ * Pairs with r < r_cut become edges i <- local_of[j]; f [nall][3] receives
+ * f_i -= f_ij, f_local(j) += f_ij; energy (eng_vdwl) and virial [6] (xx yy zz
+ * xy xz yz of sum xyz (x) f) are accumulated; eatom [nall] is set for local
+ * atoms.  energy, eatom and virial may be null.  Invalid argument when a
+ * neighbour maps to an atom outside ilist or a type is not mapped. */
+int sxl_pair_compute(sxl_evaluator* evaluator, int inum, const int* ilist, const int* numneigh,
+                     const int* const* firstneigh, int nall, const double* x, const int* type, const int* local_of,
+                     int ntypes, const int* mace_types, double* f, double* energy, double* eatom, double* virial);
+
 /* Velocity-Verlet NVE molecular dynamics with positions, velocities and
  * forces resident on the device: the update of LAMMPS `fix nve` that the
  * reference's capacity runs apply with pair_style symmetrix/mace

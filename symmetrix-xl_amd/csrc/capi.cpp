@@ -10,9 +10,11 @@
 #include <vector>
 
 #include "evaluator.hpp"
+#include "pair.hpp"
 
 struct sxl_evaluator {
     sxl::Evaluator impl;
+    sxl::PairDriver pair;
     sxl_evaluator(const char* path, const char* head) : impl(path, head ? head : "") {}
 };
 
@@ -195,6 +197,32 @@ int sxl_max_displacement(sxl_evaluator* ev, uint64_t generation, const double* p
 {
     if (!ev || !out) return null_handle();
     return guarded([&] { *out = ev->impl.max_displacement(generation, positions, on_device != 0); });
+}
+
+int sxl_pair_compute(sxl_evaluator* ev, int inum, const int* ilist, const int* numneigh,
+                     const int* const* firstneigh, int nall, const double* x, const int* type, const int* local_of,
+                     int ntypes, const int* mace_types, double* f, double* energy, double* eatom, double* virial)
+{
+    if (!ev || !f) return null_handle();
+    return guarded([&] {
+        sxl::PairInput in;
+        in.inum = inum;
+        in.ilist = ilist;
+        in.numneigh = numneigh;
+        in.firstneigh = firstneigh;
+        in.nall = nall;
+        in.x = x;
+        in.type = type;
+        in.local_of = local_of;
+        in.ntypes = ntypes;
+        in.mace_types = mace_types;
+        sxl::PairOutput out;
+        out.f = f;
+        out.energy = energy;
+        out.eatom = eatom;
+        out.virial = virial;
+        ev->pair.compute(ev->impl, in, out);
+    });
 }
 
 int sxl_md_nve(sxl_evaluator* ev, int num_atoms, const int* node_types, const double* masses, double* positions,

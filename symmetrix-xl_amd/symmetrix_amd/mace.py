@@ -214,6 +214,34 @@ class MACEKokkosFloat:
         _, _, self._generation = self._graph_size()
         self._evaluated = True
 
+    def _pair_compute(self, ilist, numneigh, firstneigh, x, atom_type, local_of, mace_types, f=None):
+        """One pair_style symmetrix/mace force call on a LAMMPS-style full
+        neighbour list (sxl_pair_compute): ilist [inum], numneigh [nall] and
+        firstneigh (nall integer arrays) indexed by atom, x [nall][3], 1-based
+        types, local_of [nall], mace_types [ntypes].  Returns the forces
+        [nall][3] (accumulated into f when given), eng_vdwl, eatom [nall] and
+        the virial [6]."""
+        il = _i32(ilist, name="ilist")
+        nall = int(np.asarray(atom_type).size)
+        nn = _i32(numneigh, nall, "numneigh")
+        lists = [_i32(firstneigh[i], int(nn[i]), "firstneigh") for i in range(nall)]
+        ptrs = (c_int_p * nall)(*[_p(a, ctypes.c_int) if a.size else c_int_p() for a in lists])
+        xx = _f64(x, 3 * nall, "x")
+        tt = _i32(atom_type, nall, "type")
+        lo = _i32(local_of, nall, "local_of")
+        mt = _i32(mace_types, name="mace_types")
+        out = np.zeros(3 * nall) if f is None else _f64(f, 3 * nall, "f").copy()
+        energy = ctypes.c_double(0.0)
+        eatom = np.zeros(nall)
+        virial = np.zeros(6)
+        check(library().sxl_pair_compute(self._h, il.size, _p(il, ctypes.c_int), _p(nn, ctypes.c_int), ptrs, nall,
+                                         _p(xx, ctypes.c_double), _p(tt, ctypes.c_int), _p(lo, ctypes.c_int),
+                                         mt.size, _p(mt, ctypes.c_int), _p(out, ctypes.c_double),
+                                         ctypes.byref(energy), _p(eatom, ctypes.c_double),
+                                         _p(virial, ctypes.c_double)))
+        self._evaluated = True
+        return {"f": out.reshape(nall, 3), "energy": float(energy.value), "eatom": eatom, "virial": virial}
+
     def _md_nve(self, node_types, masses, positions, velocities, cell, skin, dt, steps):
         """Velocity-Verlet NVE run on the device (the `fix nve` update of the
         reference's LAMMPS capacity runs).  positions (A), velocities (A/fs),

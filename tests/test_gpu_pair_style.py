@@ -1,0 +1,107 @@
+"""GPU: the single-rank LAMMPS pair-style driver (sxl_pair_compute,
+counterpart of PairSymmetrixMACE::compute_no_domain_decomposition,
+pair_symmetrix_mace.cpp:309-441) on a LAMMPS-style full neighbour list with
+ghost atoms, special-bond bits and a shuffled ilist, against the calculator
+and the CPU oracle on the same structure: energy, forces (ghost forces folded
+into local atoms) and the global virial (= -V stress)."""
+
+import json
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+E_TOL = 1e-5   # eV/atom
+F_TOL = 1e-4   # eV/A
+S_TOL = 1e-6   # eV/A^3
+
+
+@pytest.fixture(scope="module")
+def tiny(tmp_path_factory):
+    from symmetrix_amd import synthetic
+
+    text = synthetic.model_json(synthetic.random_mace_model("tiny", seed=0))
+    path = tmp_path_factory.mktemp("pair") / "tiny.json"
+    path.write_text(text)
+    return str(path), json.loads(text)
+
+
+def lammps_lists(s, cutoff, seed=0):
+    """Local atoms, one shell of periodic ghost images and a full neighbour
+    list of the local atoms over all atoms within cutoff (as LAMMPS builds
+    with cutoff = force cutoff + skin)."""
+    rng = np.random.default_rng(seed)
+    n = len(s)
+    shifts = [np.array([a, b, c]) for a in (-1, 0, 1) for b in (-1, 0, 1) for c in (-1, 0, 1)
+              if (a, b, c) != (0, 0, 0)]
+    x = np.concatenate([s.positions] + [s.positions + sh @ s.cell for sh in shifts])
+    nall = len(x)
+    local_of = np.arange(nall) % n
+    species = [38, 22, 8]
+    atom_type = np.array([species.index(int(z)) + 1 for z in s.numbers])[local_of]
+    firstneigh = [np.zeros(0, np.int32) for _ in range(nall)]
+    numneigh = np.zeros(nall, np.int32)
+    for i in range(n):
+        d = np.linalg.norm(x - x[i], axis=1)
+        js = np.nonzero((d < cutoff) & (np.arange(nall) != i))[0]
+        rng.shuffle(js)
+        js = js.astype(np.int64)
+        js[::7] |= 1 << 30  # special-bond bits above NEIGHMASK
+        firstneigh[i] = js.astype(np.int32)
+        numneigh[i] = len(js)
+    ilist = rng.permutation(n).astype(np.int32)
+    return ilist, numneigh, firstneigh, x, atom_type, local_of
+
+
+def test_pair_style_matches_calculator_and_oracle(oracle_lib, tiny):
+    from symmetrix_amd import MACEKokkosFloat, Symmetrix, synthetic
+
+    path, model = tiny
+    s = synthetic.srtio3_supercell(3, sigma=0.08, seed=31)
+    n = len(s)
+    ilist, numneigh, firstneigh, x, atom_type, local_of = lammps_lists(s, model["r_cut"] + 1.0)
+    mace_types = [model["atomic_numbers"].index(z) for z in (38, 22, 8)]
+    print(f"pair style: {n} local + {len(x) - n} ghost atoms, {int(numneigh.sum())} list entries", flush=True)
+    ev = MACEKokkosFloat(path)
+    res = ev._pair_compute(ilist, numneigh, firstneigh, x, atom_type, local_of, mace_types)
+    assert np.all(res["f"][n:] == 0.0)  # forces land on local atoms only
+    assert np.all(res["eatom"][n:] == 0.0)
+    assert res["energy"] == pytest.approx(res["eatom"][:n].sum(), abs=1e-9)
+
+    calc = Symmetrix(path).calculate(s)
+    V = s.volume
+    sigma = calc["stress"]  # Voigt xx yy zz yz xz xy
+    want_virial = -V * np.array([sigma[0], sigma[1], sigma[2], sigma[5], sigma[4], sigma[3]])
+    de = abs(res["energy"] - calc["energy"]) / n
+    df = float(np.max(np.abs(res["f"][:n] - calc["forces"])))
+    dv = float(np.max(np.abs(res["virial"] - want_virial))) / V
+    print(f"  vs calculator: |dE|/atom={de:.3e} max|dF|={df:.3e} max|dvirial|/V={dv:.3e}", flush=True)
+    assert de < E_TOL and df < F_TOL and dv < S_TOL
+    np.testing.assert_allclose(res["eatom"][:n], calc["energies"], atol=E_TOL)
+
+    types = synthetic.node_types(s, model["atomic_numbers"])
+    orc = oracle_lib.MaceOracle(model, np.unique(types), "float32")
+    want = oracle_lib.evaluate(orc, s, model["r_cut"] + 0.5)
+    assert abs(res["energy"] - want["energy"]) / n < E_TOL
+    np.testing.assert_allclose(res["f"][:n], want["forces"], atol=F_TOL)
+
+
+def test_pair_style_accumulates_and_validates(tiny):
+    from symmetrix_amd import MACEKokkosFloat, synthetic
+
+    path, model = tiny
+    s = synthetic.srtio3_supercell(2, sigma=0.05, seed=32)
+    ilist, numneigh, firstneigh, x, atom_type, local_of = lammps_lists(s, model["r_cut"])
+    mace_types = [model["atomic_numbers"].index(z) for z in (38, 22, 8)]
+    ev = MACEKokkosFloat(path)
+    base = ev._pair_compute(ilist, numneigh, firstneigh, x, atom_type, local_of, mace_types)
+    prior = np.random.default_rng(0).normal(size=base["f"].shape)
+    again = ev._pair_compute(ilist, numneigh, firstneigh, x, atom_type, local_of, mace_types, f=prior)
+    np.testing.assert_allclose(again["f"], prior + base["f"], atol=1e-12)
+    bad = local_of.copy()
+    bad[len(s):] = len(s)  # ghosts mapped to a ghost, not to their local atoms
+    with pytest.raises(ValueError, match="not in the local list"):
+        ev._pair_compute(ilist, numneigh, firstneigh, x, atom_type, bad, mace_types)
+    with pytest.raises(ValueError, match="outside the model"):
+        ev._pair_compute(ilist, numneigh, firstneigh, x, atom_type, local_of, [0, 1, 99])
