@@ -219,6 +219,24 @@ int sxl_num_stages(void);
 const char* sxl_stage_name(int stage);
 int sxl_stage_times(const sxl_evaluator* evaluator, double* ms, int* counts);
 
+/* Execution-plan request (_set_execution_plan_request,
+ * mace_kokkos.cpp:266-269): algorithm "direct"; profile "capacity" (receiver
+ * tiles when the untiled estimate exceeds the memory budget and fixed
+ * workspace is allowed) or "speed" (untiled); debug_plan NULL/"" or
+ * "mh0-direct-speed" / "mh0-dual-layer-tiled-v1" to pin a plan.  Invalidates
+ * the prepared graph. */
+int sxl_set_execution_plan_request(sxl_evaluator* evaluator, const char* algorithm, const char* profile,
+                                   const char* debug_plan);
+
+/* execution_plan_report property (mace_kokkos.cpp:271-297) as a JSON object
+ * with the reference's fields: requested_algorithm, requested_profile,
+ * selection_source, state, selected_id, selection_reason, available_bytes,
+ * reserve_bytes, boundary_attempt, candidates [{id, qualified,
+ * estimated_bytes, reason}].  *length receives the text length; with a
+ * non-null buffer the text and a NUL are written (length error when capacity
+ * is not larger than the length). */
+int sxl_execution_plan_json(const sxl_evaluator* evaluator, char* buffer, int64_t capacity, int64_t* length);
+
 /* Tiled ("fixed workspace") execution for capacity runs: receivers are
  * processed in tiles with one reused work arena; graph-wide state is H1, its
  * adjoint and two per-node scalar blocks.  With allow != 0 the plan of the

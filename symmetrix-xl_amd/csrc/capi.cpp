@@ -321,6 +321,27 @@ int sxl_allow_fixed_workspace(const sxl_evaluator* ev, int* allow)
     return guarded([&] { *allow = ev->impl.allow_fixed_workspace() ? 1 : 0; });
 }
 
+int sxl_set_execution_plan_request(sxl_evaluator* ev, const char* algorithm, const char* profile,
+                                   const char* debug_plan)
+{
+    if (!ev || !algorithm || !profile) return null_handle();
+    return guarded([&] { ev->impl.set_execution_plan_request(algorithm, profile, debug_plan ? debug_plan : ""); });
+}
+
+int sxl_execution_plan_json(const sxl_evaluator* ev, char* buffer, int64_t capacity, int64_t* length)
+{
+    if (!ev || !length) return null_handle();
+    return guarded([&] {
+        const std::string text = ev->impl.execution_plan_report().json();
+        *length = static_cast<int64_t>(text.size());
+        if (!buffer) return;
+        if (capacity <= static_cast<int64_t>(text.size()))
+            throw std::length_error("execution-plan buffer is smaller than the report");
+        std::copy(text.begin(), text.end(), buffer);
+        buffer[text.size()] = '\0';
+    });
+}
+
 int sxl_set_workspace_receiver_limit(sxl_evaluator* ev, int receivers)
 {
     if (!ev) return null_handle();

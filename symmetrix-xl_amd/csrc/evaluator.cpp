@@ -587,27 +587,78 @@ void Evaluator::plan_tiles()
     tile_first_edge_.clear();
     tile_run_offsets_.clear();
     const int N = num_nodes_;
-    if (!allow_fixed_workspace_ || N == 0) return;
-    int T = receiver_limit_;
-    if (T <= 0) {
-        const std::size_t per_node = static_cast<std::size_t>(C_) * sizeof(float) * (3 * nlm_ + nLM_ + nlme_);
-        const std::size_t per_edge = static_cast<std::size_t>(nLM_) * C_ * sizeof(float);
-        const std::size_t untiled = per_node * N + per_edge * static_cast<std::size_t>(num_edges_);
-        std::size_t free_bytes = 0, total_bytes = 0;
-        hip_check(hipMemGetInfo(&free_bytes, &total_bytes), "memory info");
-        const std::size_t held = A0_.bytes() + M0_.bytes() + Phi1_.bytes() + A1_.bytes() + A1adj_.bytes() +
-                                 msg_.bytes();
-        if (untiled > (free_bytes + held) / 10 * 9) T = kDefaultTileReceivers;
+    const long long E = num_edges_;
+    static const char* kSpeed = "mh0-direct-speed";
+    static const char* kTiled = "mh0-dual-layer-tiled-v1";
+
+    ExecutionPlanReport rep;
+    rep.requested_profile = plan_profile_;
+    rep.selection_source = plan_debug_.empty() ? "native_request" : "debug_override";
+    std::vector<int> first(N + 1, 0);
+    if (N > 0) {
+        hip_check(hipMemcpyAsync(first.data(), first_.as<int>(), (N + 1) * sizeof(int), hipMemcpyDeviceToHost,
+                                 stream_),
+                  "copy");
+        hip_check(hipStreamSynchronize(stream_), "sync");
     }
-    if (T <= 0 || T >= N) return;
+    // candidate estimates: graph state + work arrays
+    const std::size_t graph = graph_bytes_estimate();
+    const std::size_t untiled = graph + work_bytes_estimate(N, E);
+    const int T = receiver_limit_ > 0 ? receiver_limit_ : kDefaultTileReceivers;
+    long long tile_edges = 0;
+    for (long long t0 = 0; t0 < N; t0 += T)
+        tile_edges = std::max<long long>(tile_edges, first[std::min<long long>(N, t0 + T)] - first[t0]);
+    const std::size_t tiled = graph + work_bytes_estimate(std::min(T, std::max(N, 1)), tile_edges) +
+                              static_cast<std::size_t>(N) * C_ * sizeof(float) +
+                              3 * sizeof(int) * static_cast<std::size_t>(E);
+    // memory budget: free device memory plus what this evaluator already holds
+    std::size_t free_bytes = 0, total_bytes = 0;
+    hip_check(hipMemGetInfo(&free_bytes, &total_bytes), "memory info");
+    const std::size_t held = A0_.bytes() + M0_.bytes() + Phi1_.bytes() + A1_.bytes() + A1adj_.bytes() +
+                             msg_.bytes() + M0s_.bytes() + run_source_.bytes() + run_start_.bytes() +
+                             run_length_.bytes();
+    rep.available_bytes = free_bytes + held + graph;
+    rep.reserve_bytes = rep.available_bytes / 10;
+    const std::size_t budget = rep.available_bytes - rep.reserve_bytes;
+    const bool tiled_permitted = allow_fixed_workspace_ || plan_debug_ == kTiled;
+    rep.candidates.push_back({kSpeed, true, untiled, untiled <= budget ? "estimated fit" : "exceeds advisory memory budget"});
+    rep.candidates.push_back(
+        {kTiled, tiled_permitted && N > T, tiled,
+         !tiled_permitted ? "fixed-workspace execution requires explicit opt-in via allow_fixed_workspace"
+         : N > T          ? "qualified"
+                          : "the graph fits in one tile of " + std::to_string(T) + " receivers"});
+
+    bool tile = false;
+    if (plan_debug_ == kSpeed) {
+        rep.selection_reason = "debug override selected the untiled plan";
+    } else if (plan_debug_ == kTiled) {
+        tile = N > T;
+        rep.selection_reason = tile ? "debug override selected receiver tiles"
+                                    : "debug override: the graph fits in one tile, untiled";
+    } else if (plan_profile_ == "speed") {
+        rep.selection_reason = "speed request selected the untiled plan";
+    } else if (allow_fixed_workspace_ && receiver_limit_ > 0 && N > T) {
+        tile = true;
+        rep.selection_reason = "receiver limit " + std::to_string(T) + " set for the tiled plan";
+    } else if (untiled <= budget) {
+        rep.selection_reason = "untiled estimate fits within the post-reserve budget";
+    } else if (allow_fixed_workspace_ && N > T) {
+        tile = true;
+        rep.selection_reason = "untiled estimate exceeds the post-reserve budget; tiles of " + std::to_string(T) +
+                               " receivers";
+    } else {
+        rep.selection_reason = "no permitted plan fits the post-reserve budget; attempting the untiled plan";
+    }
+    rep.selected_id = tile ? kTiled : kSpeed;
+    rep.boundary_attempt = (tile ? tiled : untiled) > budget;
+    rep.state = "active";
+    plan_report_ = rep;
+    if (!tile) return;
+
     tile_receivers_ = T;
     num_tiles_ = (N + T - 1) / T;
-    std::vector<int> first(N + 1);
-    hip_check(hipMemcpyAsync(first.data(), first_.as<int>(), (N + 1) * sizeof(int), hipMemcpyDeviceToHost, stream_),
-              "copy");
-    hip_check(hipStreamSynchronize(stream_), "sync");
     tile_first_edge_.resize(num_tiles_ + 1);
-    for (int t = 0; t <= num_tiles_; ++t) tile_first_edge_[t] = first[std::min(N, t * T)];
+    for (int t = 0; t <= num_tiles_; ++t) tile_first_edge_[t] = first[std::min<long long>(N, static_cast<long long>(t) * T)];
     // runs: count per tile, scan on the host, fill
     DeviceBuffer per_source, per_tile, offsets;
     per_source.reserve(static_cast<std::size_t>(N) * sizeof(int));
@@ -624,9 +675,9 @@ void Evaluator::plan_tiles()
     tile_run_offsets_.assign(num_tiles_ + 1, 0);
     for (int t = 0; t < num_tiles_; ++t) tile_run_offsets_[t + 1] = tile_run_offsets_[t] + counts[t];
     const int runs = tile_run_offsets_[num_tiles_];
-    run_source_.reserve(std::max(runs, 1) * sizeof(int));
-    run_start_.reserve(std::max(runs, 1) * sizeof(int));
-    run_length_.reserve(std::max(runs, 1) * sizeof(int));
+    run_source_.reserve(static_cast<std::size_t>(std::max(runs, 1)) * sizeof(int));
+    run_start_.reserve(static_cast<std::size_t>(std::max(runs, 1)) * sizeof(int));
+    run_length_.reserve(static_cast<std::size_t>(std::max(runs, 1)) * sizeof(int));
     upload(offsets, tile_run_offsets_, stream_);
     hip_check(hipMemsetAsync(per_tile.as<void>(), 0, num_tiles_ * sizeof(int), stream_), "memset");
     hip_check(launch_tile_runs_fill(N, tfirst_.as<int>(), tedge_.as<int>(), receiver_.as<int>(), T,
@@ -634,6 +685,103 @@ void Evaluator::plan_tiles()
                                     run_start_.as<int>(), run_length_.as<int>(), stream_),
               "tile runs");
     hip_check(hipStreamSynchronize(stream_), "tile plan");
+}
+
+// Device bytes of the graph-wide state of the prepared graph: per-edge
+// arrays (receiver, source, transpose, pair index, geometry, directed forces
+// and, for a periodic graph, shifts and fractional edge vectors) and per-node
+// arrays (offsets, types, energies, forces, H1 and its adjoint, the direct
+// adjoint and, periodic, positions and displacements).
+std::size_t Evaluator::graph_bytes_estimate() const
+{
+    const std::size_t N = num_nodes_, E = static_cast<std::size_t>(num_edges_);
+    std::size_t per_edge = 4 * sizeof(int) + 4 * sizeof(double) + 3 * sizeof(double);
+    std::size_t per_node = 4 * sizeof(int) + 4 * sizeof(double) + 2 * static_cast<std::size_t>(nLM_) * C_ * sizeof(float) +
+                           static_cast<std::size_t>(C_) * sizeof(float);
+    if (periodic_) {
+        per_edge += sizeof(int) + 3 * sizeof(int) + 3 * sizeof(double);
+        per_node += sizeof(int) + 9 * sizeof(double);
+    }
+    if (model_.A1_scaled) per_node += 2 * sizeof(float);
+    if (model_.pre_linear_up) per_node += static_cast<std::size_t>(C_) * sizeof(float);
+    return per_edge * E + per_node * N;
+}
+
+// Device bytes of the work arrays for `receivers` receivers and `edges`
+// edges: A0, A1 and A1_adj [lm], M0 [LM], Phi1 [lme] per receiver and the
+// H1-adjoint messages [LM] per edge.
+std::size_t Evaluator::work_bytes_estimate(long long receivers, long long edges) const
+{
+    const std::size_t per_node = static_cast<std::size_t>(C_) * sizeof(float) * (3 * nlm_ + nLM_ + nlme_);
+    const std::size_t per_edge = static_cast<std::size_t>(nLM_) * C_ * sizeof(float);
+    return per_node * static_cast<std::size_t>(std::max(receivers, 1LL)) +
+           per_edge * static_cast<std::size_t>(std::max(edges, 1LL));
+}
+
+void Evaluator::set_execution_plan_request(const std::string& algorithm, const std::string& profile,
+                                           const std::string& debug_plan)
+{
+    if (algorithm != "direct")
+        throw std::invalid_argument("streamed_edges must be 'direct' on this backend (got '" + algorithm + "').");
+    if (profile != "capacity" && profile != "speed")
+        throw std::invalid_argument("execution_profile must be 'capacity' or 'speed'.");
+    if (!debug_plan.empty() && debug_plan != "mh0-direct-speed" && debug_plan != "mh0-dual-layer-tiled-v1")
+        throw std::invalid_argument("_debug_execution_plan must be 'mh0-direct-speed' or 'mh0-dual-layer-tiled-v1' "
+                                    "on this backend.");
+    if (debug_plan == "mh0-dual-layer-tiled-v1" && profile != "capacity")
+        throw std::invalid_argument("MH-0 capacity debug plans require execution_profile='capacity'.");
+    invalidate_graph();
+    plan_profile_ = profile;
+    plan_debug_ = debug_plan;
+    plan_report_ = ExecutionPlanReport{};
+    plan_report_.requested_profile = profile;
+    plan_report_.selection_source = debug_plan.empty() ? "native_request" : "debug_override";
+}
+
+namespace {
+void json_string(std::string& out, const std::string& v)
+{
+    out += '"';
+    for (char c : v) {
+        if (c == '"' || c == '\\') out += '\\';
+        out += c;
+    }
+    out += '"';
+}
+}  // namespace
+
+std::string ExecutionPlanReport::json() const
+{
+    std::string out = "{";
+    auto key = [&](const char* k) {
+        if (out.size() > 1) out += ", ";
+        json_string(out, k);
+        out += ": ";
+    };
+    key("requested_algorithm"), json_string(out, requested_algorithm);
+    key("requested_profile"), json_string(out, requested_profile);
+    key("selection_source"), json_string(out, selection_source);
+    key("state"), json_string(out, state);
+    key("selected_id"), json_string(out, selected_id);
+    key("selection_reason"), json_string(out, selection_reason);
+    key("available_bytes"), out += std::to_string(available_bytes);
+    key("reserve_bytes"), out += std::to_string(reserve_bytes);
+    key("boundary_attempt"), out += boundary_attempt ? "true" : "false";
+    key("candidates");
+    out += "[";
+    for (std::size_t i = 0; i < candidates.size(); ++i) {
+        const PlanCandidate& c = candidates[i];
+        if (i) out += ", ";
+        out += "{\"id\": ";
+        json_string(out, c.id);
+        out += ", \"qualified\": ";
+        out += c.qualified ? "true" : "false";
+        out += ", \"estimated_bytes\": " + std::to_string(c.estimated_bytes) + ", \"reason\": ";
+        json_string(out, c.reason);
+        out += "}";
+    }
+    out += "]}";
+    return out;
 }
 
 // Nodes of each tile (the whole graph untiled) grouped by active type, in

@@ -91,6 +91,32 @@ struct EvaluatorStats {
 // and the untiled workspace does not fit (reference mace_kokkos.hpp:542).
 constexpr int kDefaultTileReceivers = 32768;
 
+// Execution-plan report (reference execution_plan.hpp:32-50 and
+// mace_kokkos_runtime.cpp:3843-3915): the candidate plans with their memory
+// estimates for the prepared graph and the one selected.  Plan identifiers
+// are the reference's: "mh0-direct-speed" (untiled: graph-wide work arrays
+// and per-edge messages) and "mh0-dual-layer-tiled-v1" (receiver tiles with
+// one reused arena).
+struct PlanCandidate {
+    std::string id;
+    bool qualified = false;
+    std::size_t estimated_bytes = 0;
+    std::string reason;
+};
+struct ExecutionPlanReport {
+    std::string requested_algorithm = "direct";
+    std::string requested_profile = "capacity";
+    std::string selection_source = "native_request";
+    std::string state = "pending";
+    std::string selected_id;
+    std::string selection_reason = "awaiting a prepared graph";
+    std::size_t available_bytes = 0;
+    std::size_t reserve_bytes = 0;
+    bool boundary_attempt = false;
+    std::vector<PlanCandidate> candidates;
+    std::string json() const;
+};
+
 // Stages of one evaluation, timed with HIP events on the evaluator's stream
 // when profiling is enabled.
 enum Stage {
@@ -179,6 +205,13 @@ public:
     bool allow_fixed_workspace() const { return allow_fixed_workspace_; }
     void set_workspace_receiver_limit(int receivers);
     int workspace_receiver_limit() const { return receiver_limit_; }
+    // Plan request (reference _set_execution_plan_request): algorithm
+    // "direct"; profile "capacity" (tiles when the untiled estimate exceeds
+    // the memory budget and fixed workspace is allowed) or "speed" (untiled);
+    // debug_plan "" or a plan identifier to pin.  Invalidates the graph.
+    void set_execution_plan_request(const std::string& algorithm, const std::string& profile,
+                                    const std::string& debug_plan);
+    const ExecutionPlanReport& execution_plan_report() const { return plan_report_; }
 
     // Per-stage device time (ms) accumulated over profiled evaluations.
     void set_profiling(bool enable);
@@ -256,6 +289,10 @@ private:
     // tiled plan
     bool allow_fixed_workspace_ = false;
     int receiver_limit_ = 0;
+    std::string plan_profile_ = "capacity", plan_debug_;
+    ExecutionPlanReport plan_report_;
+    std::size_t graph_bytes_estimate() const;
+    std::size_t work_bytes_estimate(long long receivers, long long edges) const;
     int tile_receivers_ = 0;
     int num_tiles_ = 0;
     std::vector<long long> tile_first_edge_;  // [num_tiles + 1]

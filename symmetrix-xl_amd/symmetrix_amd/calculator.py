@@ -67,7 +67,8 @@ class Symmetrix:
     implemented_properties = ["energy", "free_energy", "energies", "forces", "stress"]
 
     def __init__(self, model_file, dtype="float32", use_kokkos=True, streamed_edges="direct",
-                 neighbor_skin=0.5, head=None, allow_fixed_workspace=False, **unused):
+                 neighbor_skin=0.5, head=None, allow_fixed_workspace=False, execution_profile="capacity",
+                 _debug_execution_plan=None, **unused):
         if dtype not in ("float32", np.float32):
             raise ValueError("the MI355X evaluator computes in float32 (dtype='float32')")
         if streamed_edges not in ("direct", "generic", True):
@@ -75,6 +76,10 @@ class Symmetrix:
         if not (neighbor_skin >= 0.0):
             raise ValueError("neighbor_skin must be non-negative")
         self.evaluator = MACEKokkosFloat(model_file, head or "")
+        # plan request (reference calculator.py:740-889): the planner picks
+        # untiled or receiver-tiled execution per prepared graph
+        self.execution_profile = execution_profile
+        self.evaluator._set_execution_plan_request("direct", execution_profile, _debug_execution_plan or "")
         if allow_fixed_workspace:
             # tiled plan when the untiled workspace would not fit
             # (reference calculator.py:578-582)
@@ -89,6 +94,12 @@ class Symmetrix:
         self.neighbor_cache_reuse_count = 0
         self.neighbor_cache_geometry_update_count = 0
         self.calculation_count = 0
+
+    @property
+    def execution_plan(self):
+        """Current execution selection and its memory diagnostics (reference
+        calculator.py:1691-1725): pending until the first graph is prepared."""
+        return dict(self.evaluator.execution_plan_report)
 
     @property
     def neighbor_rebuild_count(self):

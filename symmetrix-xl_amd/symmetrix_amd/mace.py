@@ -11,6 +11,7 @@ computes model quantities.
 from __future__ import annotations
 
 import ctypes
+import json
 
 import numpy as np
 
@@ -213,6 +214,21 @@ class MACEKokkosFloat:
             _p(nt, ctypes.c_int), _p(x, ctypes.c_double), _p(rr, ctypes.c_double)))
         _, _, self._generation = self._graph_size()
         self._evaluated = True
+
+    def _set_execution_plan_request(self, algorithm, profile, debug_plan=""):
+        check(library().sxl_set_execution_plan_request(self._h, str(algorithm).encode(), str(profile).encode(),
+                                                       str(debug_plan or "").encode()))
+        self._evaluated = False
+
+    @property
+    def execution_plan_report(self):
+        """The planner's candidates, memory estimates and selection for the
+        prepared graph (reference execution_plan_report)."""
+        length = c_i64(0)
+        check(library().sxl_execution_plan_json(self._h, None, 0, ctypes.byref(length)))
+        buf = ctypes.create_string_buffer(int(length.value) + 1)
+        check(library().sxl_execution_plan_json(self._h, buf, len(buf), ctypes.byref(length)))
+        return json.loads(buf.value.decode())
 
     def _pair_compute(self, ilist, numneigh, firstneigh, x, atom_type, local_of, mace_types, f=None):
         """One pair_style symmetrix/mace force call on a LAMMPS-style full
