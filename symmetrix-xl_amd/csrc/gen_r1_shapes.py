@@ -18,6 +18,13 @@ sys.path.insert(0, os.path.dirname(HERE))
 from symmetrix_amd import irreps  # noqa: E402
 
 SHAPES = [(2, 1), (3, 1), (3, 2)]
+# Shapes whose per-channel reverse state does not fit the register file in
+# one pass run the second-interaction reverse in passes over disjoint path
+# groups by source l2: each pass owns its message rows and edge forces add up
+# over passes.  (Forward passes by output l were measured slower on the wide
+# shape than one pass: every extra sweep re-reads the source features.)
+REV_GROUPS = {(3, 2): [[0], [1], [2]]}
+FACTORED_MAX_TRIPLES = 64
 
 
 def emit_shape(lmax, Lmax):
@@ -59,6 +66,8 @@ def emit_shape(lmax, Lmax):
     def arr(vals):
         return "{" + ", ".join(str(v) for v in vals) + "}"
 
+    groups = emit_groups(lmax, Lmax, paths, terms)
+
     lines = [
         "template <>",
         f"struct {name} {{",
@@ -92,7 +101,65 @@ def emit_shape(lmax, Lmax):
         "};",
         "",
     ]
-    return "\n".join(lines)
+    return "\n".join(lines) + groups
+
+
+def _arr(vals):
+    return "{" + ", ".join(str(v) for v in vals) + "}"
+
+
+def emit_groups(lmax, Lmax, paths, terms):
+    """Pass structures of a grouped shape.  `terms` is the shape's sorted
+    term list (path, lm2, lm1, lme, row); group arrays index it."""
+    rev = REV_GROUPS.get((lmax, Lmax), [])
+    if not rev:
+        return ""
+    out = [
+        "template <>",
+        f"struct R1Groups<{lmax}, {Lmax}> {{",
+        f"    static constexpr int NREV = {len(rev)};",
+        "};",
+        "",
+    ]
+    for g, l2s in enumerate(rev):
+        gp = [p for p, (_, l2, _) in enumerate(paths) if l2 in l2s]
+        ts = [t for t, x in enumerate(terms) if x[0] in gp]
+        rows = sorted({terms[t][3] for t in ts})
+        pqs, trs = [], []
+        for t in ts:
+            p, lm2, lm1 = terms[t][:3]
+            if (p, lm2) not in pqs:
+                pqs.append((p, lm2))
+            if (p, lm2, lm1) not in trs:
+                trs.append((p, lm2, lm1))
+        hl = sorted({lm2 for _, lm2 in pqs})
+        factored = len(trs) <= FACTORED_MAX_TRIPLES
+        out += [
+            "template <>",
+            f"struct R1RevGroup<{lmax}, {Lmax}, {g}> {{",
+            f"    // source l2 in {l2s}",
+            f"    static constexpr bool FACTORED = {'true' if factored else 'false'};",
+            f"    static constexpr int NP = {len(gp)};",
+            f"    static constexpr int path[NP] = {_arr(gp)};",
+            f"    static constexpr int NH = {len(hl)};",
+            f"    static constexpr int h_lm2[NH] = {_arr(hl)};",
+            f"    static constexpr int NROW = {len(rows)};",
+            f"    static constexpr int row_lme[NROW] = {_arr(rows)};",
+            f"    static constexpr int NPQ = {len(pqs)};",
+            f"    static constexpr int pq_p[NPQ] = {_arr([gp.index(p) for p, _ in pqs])};",
+            f"    static constexpr int pq_h[NPQ] = {_arr([hl.index(lm2) for _, lm2 in pqs])};",
+            f"    static constexpr int NTR = {len(trs)};",
+            f"    static constexpr int tr_pq[NTR] = {_arr([pqs.index(x[:2]) for x in trs])};",
+            f"    static constexpr int tr_lm1[NTR] = {_arr([x[2] for x in trs])};",
+            f"    static constexpr int NT = {len(ts)};",
+            f"    static constexpr int term[NT] = {_arr(ts)};",
+            f"    static constexpr int term_lm1[NT] = {_arr([terms[t][2] for t in ts])};",
+            f"    static constexpr int term_row[NT] = {_arr([rows.index(terms[t][3]) for t in ts])};",
+            f"    static constexpr int term_tr[NT] = {_arr([trs.index(terms[t][:3]) for t in ts])};",
+            "};",
+            "",
+        ]
+    return "\n".join(out)
 
 
 def main():
@@ -104,6 +171,14 @@ def main():
         "",
         "template <int LMAX, int LLMAX>",
         "struct R1Shape;",
+        "",
+        "// reverse pass structure of the shapes run in path-group passes (none: one pass)",
+        "template <int LMAX, int LLMAX>",
+        "struct R1Groups {",
+        "    static constexpr int NREV = 0;",
+        "};",
+        "template <int LMAX, int LLMAX, int G>",
+        "struct R1RevGroup;",
         "",
     ]
     for lmax, Lmax in SHAPES:

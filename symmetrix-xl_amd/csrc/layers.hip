@@ -506,6 +506,232 @@ r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
     }
 }
 // ---------------------------------------------------------------------------
+// Layer 1 reverse in path-group passes, for shapes whose per-channel state
+// does not fit one thread's registers in a single pass (R1Groups): per edge
+// tile, pass G handles the paths of its source-l2 group, writes those message
+// rows complete and adds its part of each edge force (the force is linear in
+// the per-path terms).  The tile's edge geometry is staged once for all
+// passes.
+// ---------------------------------------------------------------------------
+template <class S, int G>
+using RevGroup = R1RevGroup<S::LMAX, S::LLMAX, G>;
+
+template <int MAXT>
+struct RevTileLds {
+    float Y[kTile][16];
+    float dY[kTile][3][16];
+    float geo[kTile][4];  // r_hat, local spline coordinate
+    float cgY[kTile][MAXT];
+    int row[kTile];
+    int src[kTile];
+    int eid[kTile];
+    float f[kTile][kMaxWaves][3];
+    float dsc[kTile];
+    int count;
+};
+
+template <class S, class RG, int MAXT>
+__device__ __forceinline__ void r1_reverse_pass(const LayerArgs& a, int i, bool first, int count,
+                                                const float* __restrict__ r1, const float* __restrict__ cg,
+                                                const float* __restrict__ H1, const float* __restrict__ dPhi1,
+                                                float* __restrict__ msg, RevTileLds<MAXT>& L)
+{
+    constexpr int NLM = (S::LMAX + 1) * (S::LMAX + 1);
+    constexpr int NLMS = (S::LLMAX + 1) * (S::LLMAX + 1);
+    constexpr int NG = RG::FACTORED ? RG::NTR : RG::NROW;
+    const int k = threadIdx.x;
+    const int C = a.C;
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int kk = min(k, C - 1);
+    const int row_bytes = S::NP * C * 16;
+    const int h_bytes = NLMS * C * 4;
+    // this group's dPhi1 rows, contracted with the CG coefficients per
+    // (path, lm2, lm1) triple when the triples fit the register budget.  They
+    // are reloaded per tile (an opaque zero offset keeps the compiler from
+    // hoisting every pass's rows out of the tile loop at once).
+    float G[NG];
+#pragma unroll
+    for (int q = 0; q < NG; ++q) G[q] = 0.0f;
+    if (k < C) {
+        int zero;
+        asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+        const float* in = dPhi1 + static_cast<size_t>(i - a.local_base) * S::NLME * C + k + zero;
+        if constexpr (RG::FACTORED) {
+            float d[RG::NROW];
+#pragma unroll
+            for (int q = 0; q < RG::NROW; ++q) d[q] = in[RG::row_lme[q] * C];
+#pragma unroll
+            for (int t = 0; t < RG::NT; ++t)
+                G[RG::term_tr[t]] = fmaf(cg[RG::term[t]], d[RG::term_row[t]], G[RG::term_tr[t]]);
+        } else {
+#pragma unroll
+            for (int q = 0; q < RG::NROW; ++q) G[q] = in[RG::row_lme[q] * C];
+        }
+    }
+    if constexpr (!RG::FACTORED) {
+        __syncthreads();  // the previous pass has finished reading cgY
+        if (threadIdx.x < count) {
+            const int j = threadIdx.x;
+#pragma unroll
+            for (int t = 0; t < RG::NT; ++t) L.cgY[j][t] = cg[RG::term[t]] * L.Y[j][RG::term_lm1[t]];
+        }
+        __syncthreads();
+    }
+    auto fetch = [&](int j, float4v* c, float* H) {
+        const auto rs = buffer_rsrc(r1 + static_cast<size_t>(uniform(L.row[j])) * S::NP * C * 4, row_bytes);
+        const auto hs = buffer_rsrc(H1 + static_cast<size_t>(uniform(L.src[j])) * NLMS * C, h_bytes);
+#pragma unroll
+        for (int p = 0; p < RG::NP; ++p) c[p] = load4(rs, kk * 16, RG::path[p] * C * 16);
+#pragma unroll
+        for (int q = 0; q < RG::NH; ++q) H[q] = load1(hs, kk * 4, RG::h_lm2[q] * C * 4);
+    };
+    float4v cn[RG::NP];
+    float Hn[RG::NH];
+    if (count > 0) fetch(0, cn, Hn);
+    for (int j = 0; j < count; ++j) {
+        const float x = uniform(L.geo[j][3]);
+        float R[RG::NP], dR[RG::NP], H[RG::NH];
+#pragma unroll
+        for (int p = 0; p < RG::NP; ++p) {
+            R[p] = cubic(cn[p], x);
+            dR[p] = cubic_slope(cn[p], x, 3.0f * x);
+        }
+#pragma unroll
+        for (int q = 0; q < RG::NH; ++q) H[q] = Hn[q];
+        fetch(min(j + 1, count - 1), cn, Hn);
+        float sp[RG::NPQ], RH[RG::NPQ], U[NLM];
+#pragma unroll
+        for (int pq = 0; pq < RG::NPQ; ++pq) {
+            sp[pq] = 0.0f;
+            RH[pq] = R[RG::pq_p[pq]] * H[RG::pq_h[pq]];
+        }
+#pragma unroll
+        for (int lm = 0; lm < NLM; ++lm) U[lm] = 0.0f;
+        if constexpr (RG::FACTORED) {
+#pragma unroll
+            for (int tr = 0; tr < RG::NTR; ++tr) {
+                sp[RG::tr_pq[tr]] = fmaf(L.Y[j][RG::tr_lm1[tr]], G[tr], sp[RG::tr_pq[tr]]);
+                U[RG::tr_lm1[tr]] = fmaf(RH[RG::tr_pq[tr]], G[tr], U[RG::tr_lm1[tr]]);
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < RG::NT; ++t) {
+                const int pq = RG::tr_pq[RG::term_tr[t]];
+                const float d = G[RG::term_row[t]];
+                sp[pq] = fmaf(L.cgY[j][t], d, sp[pq]);
+                U[RG::term_lm1[t]] = fmaf(cg[RG::term[t]], RH[pq] * d, U[RG::term_lm1[t]]);
+            }
+        }
+        float m[RG::NH], ap[RG::NP];
+#pragma unroll
+        for (int q = 0; q < RG::NH; ++q) m[q] = 0.0f;
+#pragma unroll
+        for (int p = 0; p < RG::NP; ++p) ap[p] = 0.0f;
+#pragma unroll
+        for (int pq = 0; pq < RG::NPQ; ++pq) {
+            m[RG::pq_h[pq]] = fmaf(R[RG::pq_p[pq]], sp[pq], m[RG::pq_h[pq]]);
+            ap[RG::pq_p[pq]] = fmaf(H[RG::pq_h[pq]], sp[pq], ap[RG::pq_p[pq]]);
+        }
+        float A = 0.0f;
+#pragma unroll
+        for (int p = 0; p < RG::NP; ++p) A = fmaf(dR[p], ap[p], A);
+        const int e = uniform(L.eid[j]);
+        if (k < C) {
+            const auto ms = buffer_rsrc(msg + static_cast<size_t>(e - a.edge_base) * NLMS * C, h_bytes);
+#pragma unroll
+            for (int q = 0; q < RG::NH; ++q) store1(m[q], ms, k * 4, RG::h_lm2[q] * C * 4);
+        }
+        float gx = 0.0f, gy = 0.0f, gz = 0.0f;
+#pragma unroll
+        for (int lm = 0; lm < NLM; ++lm) {
+            gx = fmaf(L.dY[j][0][lm], U[lm], gx);
+            gy = fmaf(L.dY[j][1][lm], U[lm], gy);
+            gz = fmaf(L.dY[j][2][lm], U[lm], gz);
+        }
+        const float fx = wave_sum_dpp(-fmaf(L.geo[j][0], A, gx));
+        const float fy = wave_sum_dpp(-fmaf(L.geo[j][1], A, gy));
+        const float fz = wave_sum_dpp(-fmaf(L.geo[j][2], A, gz));
+        if (lane == 0) {
+            L.f[j][wave][0] = first ? fx : L.f[j][wave][0] + fx;
+            L.f[j][wave][1] = first ? fy : L.f[j][wave][1] + fy;
+            L.f[j][wave][2] = first ? fz : L.f[j][wave][2] + fz;
+        }
+    }
+}
+
+template <class S, int... G>
+constexpr int rev_group_terms()
+{
+    int m = 1;
+    ((m = !RevGroup<S, G>::FACTORED && RevGroup<S, G>::NT > m ? RevGroup<S, G>::NT : m), ...);
+    return (m + 3) / 4 * 4;
+}
+
+template <class S, int... G>
+__global__ void __launch_bounds__(256) r1_reverse_grouped_kernel(LayerArgs a, const float* __restrict__ r1,
+                                                                  const float* __restrict__ cg,
+                                                                  const float* __restrict__ H1,
+                                                                  const float* __restrict__ dPhi1,
+                                                                  double* __restrict__ forces,
+                                                                  float* __restrict__ msg)
+{
+    constexpr int MAXT = rev_group_terms<S, G...>();
+    static_assert((S::LMAX + 1) * (S::LMAX + 1) <= 16, "harmonics beyond l = 3");
+    __shared__ RevTileLds<MAXT> L;
+    const int i = receiver_of_block(a);
+    const int nwaves = blockDim.x >> 6;
+    const EdgeGraph& g = a.graph;
+    const float dcoef = a.d1.table ? a.d1.dot[i] / a.d1.scale[i] : 0.0f;
+    const int e0 = g.first[i], e1 = g.first[i + 1];
+    for (int base = e0; base < e1; base += kTile) {
+        __syncthreads();
+        if (threadIdx.x < 64) {
+            const int t = threadIdx.x;
+            double rr;
+            const int n = min(kTile, e1 - base);
+            const TileSlot ts = compact_edge(g, a.grid, base, n, t, rr, &L.count);
+            const int e = base + t;
+            if (ts.active) {
+                int iv;
+                float x;
+                const int sl = ts.slot;
+                spline_point(rr, a.grid, iv, x);
+                edge_harmonics<S::LMAX, true>(g.xyz + 3 * static_cast<size_t>(e), rr, L.Y[sl], L.dY[sl][0],
+                                              L.dY[sl][1], L.dY[sl][2], L.geo[sl]);
+                L.geo[sl][3] = x;
+                L.row[sl] = (g.edge_pair[e] >> 16) * a.grid.intervals + iv;
+                L.src[sl] = g.source[e];
+                L.eid[sl] = e;
+                L.dsc[sl] = a.d1.table ? dcoef * density_slope(a.d1.table, a.grid, g.edge_pair[e] >> 16, rr) : 0.0f;
+            } else if (t < n) {
+                // beyond r_cut: only the A1 density-scale term (reverse_A1_scaled visits every neighbour)
+                double* out = forces + 3 * static_cast<size_t>(e);
+                float d = 0.0f;
+                if (a.d1.table) d = dcoef * density_slope(a.d1.table, a.grid, g.edge_pair[e] >> 16, rr);
+                const double* x = g.xyz + 3 * static_cast<size_t>(e);
+                out[0] = static_cast<double>(d * static_cast<float>(x[0] / rr));
+                out[1] = static_cast<double>(d * static_cast<float>(x[1] / rr));
+                out[2] = static_cast<double>(d * static_cast<float>(x[2] / rr));
+            }
+        }
+        __syncthreads();
+        const int count = uniform(L.count);
+        (r1_reverse_pass<S, RevGroup<S, G>, MAXT>(a, i, G == 0, count, r1, cg, H1, dPhi1, msg, L), ...);
+        __syncthreads();
+        if (threadIdx.x < count) {
+            const int t = threadIdx.x;
+            double f[3] = {0.0, 0.0, 0.0};
+            for (int w = 0; w < nwaves; ++w)
+                for (int c = 0; c < 3; ++c) f[c] += static_cast<double>(L.f[t][w][c]);
+            double* out = forces + 3 * static_cast<size_t>(L.eid[t]);
+#pragma unroll
+            for (int c = 0; c < 3; ++c) out[c] = f[c] + static_cast<double>(L.dsc[t] * L.geo[t][c]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Layer 0 reverse: f_ij += -sum_{lm,k} A0_adj[i,lm,k] (r_hat R0f' Y_lm + R0f dY_lm)
 // ---------------------------------------------------------------------------
 template <int LMAX>
@@ -960,6 +1186,9 @@ hipError_t launch_r1_forward(const LayerArgs& a, const float* r1, const float* c
     return hipGetLastError();
 }
 
+// the (3, 2) reverse runs passes 0, 1, 2: the generated source-l2 groups
+static_assert(R1Groups<3, 2>::NREV == 3, "reverse pass list out of date");
+
 hipError_t launch_r1_reverse(const LayerArgs& a, const float* r1, const float* cg, const float* H1,
                              const float* dPhi1, double* forces, float* msg, hipStream_t s)
 {
@@ -973,8 +1202,8 @@ hipError_t launch_r1_reverse(const LayerArgs& a, const float* r1, const float* c
         r1_reverse_kernel<R1Shape<3, 1>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, dPhi1,
                                                                           forces, msg);
     else if (a.l_max == 3 && a.L_max == 2)
-        r1_reverse_kernel<R1Shape<3, 2>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, dPhi1,
-                                                                          forces, msg);
+        r1_reverse_grouped_kernel<R1Shape<3, 2>, 0, 1, 2><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, dPhi1,
+                                                                                          forces, msg);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
