@@ -385,12 +385,15 @@ void Evaluator::prepare_active_types(const std::vector<int>& node_types)
     if (na * na > 0xffff) throw std::invalid_argument("too many active element types");
     const int P = m.spline_points, NI = P - 1, NL = m.l_max + 1, NP = m.num_paths();
     const double h = m.spline_h;
-    // nodal tables per unordered pair
-    const int npairs = na * (na + 1) / 2;
+    // nodal tables per unordered pair; one table for all pairs when the
+    // radial functions do not depend on the element types (no distance
+    // transform with per-element radii): the kernels then index table 0
+    const int npairs = shared_pair_tables() ? 1 : na * (na + 1) / 2;
     std::vector<std::vector<double>> r0v(npairs), r0d(npairs), r1v(npairs), r1d(npairs);
     std::vector<std::pair<int, int>> pair_types;
     for (int a = 0; a < na; ++a)
         for (int b = a; b < na; ++b) pair_types.push_back({a, b});
+    pair_types.resize(npairs);
     auto tabulate = [&](int p) {
         const int ti = types[pair_types[p].first], tj = types[pair_types[p].second];
         m.radial_tables(m.R0, ti, tj, r0v[p], r0d[p]);
@@ -431,7 +434,9 @@ void Evaluator::prepare_active_types(const std::vector<int>& node_types)
     auto fold = [&](int po) {
         const int ai = po / na, aj = po % na;
         const int ti = types[ai], tj = types[aj];
-        const int pu = ai <= aj ? ai * (2 * na - ai - 1) / 2 + aj : aj * (2 * na - aj - 1) / 2 + ai;
+        const int pu = npairs == 1 ? 0
+                       : ai <= aj ? ai * (2 * na - ai - 1) / 2 + aj
+                                  : aj * (2 * na - aj - 1) / 2 + ai;
         std::vector<double> u(C_), out(C_);
         for (int iv = 0; iv < NI; ++iv)
             for (int q = 0; q < 4; ++q)
@@ -901,7 +906,7 @@ void Evaluator::finish_graph(const int* host_neigh_types)
                 const int b = ta[t];
                 if (b < 0) throw std::runtime_error("MACE radial cache is not prepared for an active type.");
                 const int po = a * na + b;
-                const int pu = a <= b ? a * (2 * na - a - 1) / 2 + b : b * (2 * na - b - 1) / 2 + a;
+                const int pu = shared_pair_tables() ? 0 : a <= b ? a * (2 * na - a - 1) / 2 + b : b * (2 * na - b - 1) / 2 + a;
                 pairs[e] = po | (pu << 16);
             }
         }
@@ -909,7 +914,7 @@ void Evaluator::finish_graph(const int* host_neigh_types)
     } else {
         hip_check(launch_edge_pairs(E, receiver_.as<int>(), source_.as<int>(), node_types_.as<int>(),
                                     type_active_.as<int>(), static_cast<int>(active_types_.size()),
-                                    edge_pair_.as<int>(), stream_),
+                                    shared_pair_tables(), edge_pair_.as<int>(), stream_),
                   "edge pairs");
     }
     plan_tiles();

@@ -256,6 +256,10 @@ private:
     DeviceBuffer dens0_, dens1_, zbl_inverse_a_, zbl_prefactor_, zbl_rmax_;
     PolyArgs poly_args(const PolyLayout& layout, const DeviceBuffer& coef, const DeviceBuffer& offsets,
                        const DeviceBuffer& packed) const;
+    // The radial functions depend on the element pair only through a
+    // distance transform with per-element radii; without one, every pair
+    // shares one R1 and density table (table index 0 in edge_pair).
+    bool shared_pair_tables() const { return !model_.agnesi; }
     SplineGrid grid_;
 
     // graph

@@ -318,14 +318,14 @@ __global__ void atom_displacements_kernel(int n, const double* __restrict__ pos,
 
 __global__ void edge_pairs_kernel(int E, const int* __restrict__ receiver, const int* __restrict__ source,
                                   const int* __restrict__ node_types, const int* __restrict__ type_active,
-                                  int n, int* __restrict__ edge_pair)
+                                  int n, bool shared, int* __restrict__ edge_pair)
 {
     const int e = blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= E) return;
     const int a = type_active[node_types[receiver[e]]];
     const int b = type_active[node_types[source[e]]];
     const int ordered = a * n + b;
-    const int unordered = a <= b ? a * (2 * n - a - 1) / 2 + b : b * (2 * n - b - 1) / 2 + a;
+    const int unordered = shared ? 0 : a <= b ? a * (2 * n - a - 1) / 2 + b : b * (2 * n - b - 1) / 2 + a;
     edge_pair[e] = ordered | (unordered << 16);
 }
 
@@ -374,11 +374,12 @@ __global__ void tile_runs_fill_kernel(int n, const int* __restrict__ tfirst, con
 }  // namespace
 
 hipError_t launch_edge_pairs(int num_edges, const int* receiver, const int* source, const int* node_types,
-                             const int* type_active, int num_active, int* edge_pair, hipStream_t s)
+                             const int* type_active, int num_active, bool shared_tables, int* edge_pair,
+                             hipStream_t s)
 {
     if (num_edges <= 0) return hipSuccess;
     edge_pairs_kernel<<<(num_edges + 255) / 256, 256, 0, s>>>(num_edges, receiver, source, node_types,
-                                                              type_active, num_active, edge_pair);
+                                                              type_active, num_active, shared_tables, edge_pair);
     return hipGetLastError();
 }
 

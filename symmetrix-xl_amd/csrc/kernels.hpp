@@ -33,7 +33,7 @@ struct EdgeGraph {
     const int* source = nullptr;       // [E]
     const int* tfirst = nullptr;       // [N+1] source-major offsets
     const int* tedge = nullptr;        // [E] edge ids grouped by source, ascending
-    const int* edge_pair = nullptr;    // [E] ordered pair | unordered pair << 16 (active types)
+    const int* edge_pair = nullptr;    // [E] ordered pair | unordered-pair table << 16 (active types; table 0 when shared)
     const double* xyz = nullptr;       // [E][3]
     const double* r = nullptr;         // [E]
 };
@@ -310,9 +310,9 @@ hipError_t launch_atom_displacements(int n, const double* positions, const doubl
                                      const double* cell, const double* inverse_cell, double* displacements,
                                      double* out, hipStream_t s);
 // edge_pair[e] = ordered | unordered << 16 from the active indices of the
-// receiver and source element types
+// receiver and source element types (unordered = 0 with shared tables)
 hipError_t launch_edge_pairs(int num_edges, const int* receiver, const int* source,
                              const int* node_types, const int* type_active, int num_active,
-                             int* edge_pair, hipStream_t s);
+                             bool shared_tables, int* edge_pair, hipStream_t s);
 
 }  // namespace sxl
