@@ -1371,6 +1371,7 @@ void Evaluator::evaluate()
     la.node_offset = 0;
     la.node_count = N;
     density_args(la, nullptr);
+    la.type_order = node_order_.as<int>();
     hipStream_t s = stream_;
     const PolyArgs p0 = poly_args(p0_layout_, p0_coef_, p0_offsets_, p0_packed_);
     const PolyArgs p1 = poly_args(p1_layout_, p1_coef_, p1_offsets_, p1_packed_);
@@ -1523,6 +1524,7 @@ void Evaluator::evaluate_tiled()
     la.l_max = model_.l_max;
     la.L_max = model_.L_max;
     density_args(la, nullptr);
+    la.type_order = node_order_.as<int>();
     hipStream_t s = stream_;
     const PolyArgs p0 = poly_args(p0_layout_, p0_coef_, p0_offsets_, p0_packed_);
     const PolyArgs p1 = poly_args(p1_layout_, p1_coef_, p1_offsets_, p1_packed_);

@@ -148,6 +148,8 @@ struct LayerArgs {
     // first edge in tiled execution.
     int local_base = 0;
     long long edge_base = 0;
+    // receivers of this launch in element-type order (layer-0 kernels), or null
+    const int* type_order = nullptr;
 };
 
 // Layer 0: A0[i] = sum_j R0f_{pair(i,j)}(r) Y(r_hat)   (H0 and A0_W folded in),

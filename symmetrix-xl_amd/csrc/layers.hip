@@ -37,6 +37,14 @@ __device__ __forceinline__ int receiver_of_block(const LayerArgs& a)
     return a.node_offset + xcd_contiguous(blockIdx.x, a.node_count);
 }
 
+// Layer-0 receivers in element-type order when the type order is given: the
+// workgroups running at any moment (on every XCD) then share the folded
+// spline tables of one receiver type, whose rows are per ordered pair.
+__device__ __forceinline__ int layer0_receiver(const LayerArgs& a)
+{
+    return a.type_order ? a.type_order[a.node_offset + blockIdx.x] : receiver_of_block(a);
+}
+
 // ---------------------------------------------------------------------------
 // Edge tiles.  Wave 0 of the workgroup stages up to 64 edges of the receiver:
 // the edges within r_cut are compacted (ballot + lane prefix count) into LDS
@@ -148,7 +156,7 @@ __global__ void __launch_bounds__(256) a0_forward_kernel(LayerArgs a, const floa
 
     __shared__ float s_scale;
 
-    const int i = receiver_of_block(a);
+    const int i = layer0_receiver(a);
     const int k = threadIdx.x;
     const int C = a.C;
     const EdgeGraph& g = a.graph;
@@ -751,7 +759,7 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
     __shared__ float s_dsc[kTile];  // A0 density-scale force coefficient per active slot
     __shared__ int s_count;
 
-    const int i = receiver_of_block(a);
+    const int i = layer0_receiver(a);
     const int k = threadIdx.x;
     const int C = a.C;
     const int wave = threadIdx.x >> 6;
