@@ -136,6 +136,14 @@ int sxl_compute_node_energies_forces(sxl_evaluator* evaluator, int num_nodes, co
                                      const int* num_neigh, const int* neigh_indices, const int* neigh_types,
                                      const double* xyz, const double* r);
 
+/* Largest displacement (A) measured by the last evaluation from positions
+ * (sxl_compute_prepared_positions*): the same minimum-image displacement as
+ * sxl_max_displacement, formed in that pass.  A caller may evaluate first
+ * and rebuild and evaluate again when it breaks its skin rule, which saves
+ * the separate check.  Invalid argument when the last evaluation was not
+ * from positions or the graph changed since. */
+int sxl_last_max_displacement(const sxl_evaluator* evaluator, double* out);
+
 /* Largest minimum-image displacement of positions from the build's
  * fractional positions expressed in the current cell (the non-affine motion
  * of the skin-reuse rule, calculator.py:2851-2898). */
@@ -215,6 +223,9 @@ int sxl_stats(const sxl_evaluator* evaluator, sxl_stats_t* out);
  * the stage names (kernel families).  Counterpart of the reference's
  * factorized_last_evaluation_ms timing fields (mace_kokkos.hpp:1425-1455). */
 int sxl_set_profiling(sxl_evaluator* evaluator, int enable);
+/* Profile only the stages whose bit is set in mask (bit i = stage i; 0 turns
+ * profiling off): two events per profiled stage and evaluation. */
+int sxl_set_profiling_stages(sxl_evaluator* evaluator, uint32_t mask);
 int sxl_num_stages(void);
 const char* sxl_stage_name(int stage);
 int sxl_stage_times(const sxl_evaluator* evaluator, double* ms, int* counts);

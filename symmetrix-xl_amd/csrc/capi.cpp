@@ -403,6 +403,18 @@ int sxl_neighbor_graph_copy(const sxl_graph* g, int* num_neigh, int* receiver_of
 
 void sxl_neighbor_graph_free(sxl_graph* graph) { delete graph; }
 
+int sxl_set_profiling_stages(sxl_evaluator* ev, uint32_t mask)
+{
+    if (!ev) return null_handle();
+    return guarded([&] { ev->impl.set_profiling_stages(mask); });
+}
+
+int sxl_last_max_displacement(const sxl_evaluator* ev, double* out)
+{
+    if (!ev || !out) return null_handle();
+    return guarded([&] { *out = ev->impl.last_max_displacement(); });
+}
+
 int sxl_set_profiling(sxl_evaluator* ev, int enable)
 {
     if (!ev) return null_handle();

@@ -268,8 +268,12 @@ Evaluator::Evaluator(const std::string& model_path, const std::string& head)
     hip_check(hipStreamSynchronize(stream_), "model upload");
 }
 
-void Evaluator::set_profiling(bool enable)
+void Evaluator::set_profiling(bool enable) { set_profiling_stages(enable ? ~0u : 0u); }
+
+void Evaluator::set_profiling_stages(unsigned mask)
 {
+    const bool enable = mask != 0;
+    profile_mask_ = mask;
     if (enable && events_.empty()) {
         events_.resize(2 * kNumStages);
         for (auto& e : events_) hip_check(hipEventCreate(&e), "event create");
@@ -291,7 +295,7 @@ void Evaluator::stage_times(double* ms, int* counts) const
 
 void Evaluator::mark(int stage, bool end)
 {
-    if (!profiling_) return;
+    if (!profiling_ || !((profile_mask_ >> stage) & 1u)) return;
     hip_check(hipEventRecord(events_[2 * stage + (end ? 1 : 0)], stream_), "event record");
     if (end) stage_used_[stage] = true;
 }
@@ -1483,7 +1487,8 @@ void Evaluator::evaluate()
             stage_count_[i] += 1;
         }
     evaluated_generation_ = generation_;
-    reduced_ = false;
+    reduced_ = fused_volume_ > 0.0;
+    reduced_volume_ = fused_volume_;
     stats_.evaluations += 1;
     stats_.last_evaluation_ms =
         std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
@@ -1628,7 +1633,8 @@ void Evaluator::evaluate_tiled()
         stage_count_[kStageAtomForces] += 1;
     }
     evaluated_generation_ = generation_;
-    reduced_ = false;
+    reduced_ = fused_volume_ > 0.0;
+    reduced_volume_ = fused_volume_;
     stats_.evaluations += 1;
     stats_.tiled_evaluations += 1;
     stats_.last_evaluation_ms =
@@ -1717,11 +1723,28 @@ int Evaluator::md_nve(int num_atoms, const int* node_types, const double* masses
 void Evaluator::finish_evaluation()
 {
     invalid_edges_ = 0;
-    if (check_geometry_)
-        hip_check(hipMemcpyAsync(&invalid_edges_, totals_.as<double>() + 13, sizeof(invalid_edges_),
-                                 hipMemcpyDeviceToHost, stream_),
-                  "geometry check");
+    fused_volume_ = 0.0;
+    last_from_positions_ = check_geometry_;
+    if (check_geometry_) {
+        // energy and stress for the current cell in the same pass, copied
+        // back with the displacement maximum and the invalid-edge count
+        const double* c = cell_;
+        const double volume = std::abs(c[0] * (c[4] * c[8] - c[5] * c[7]) - c[1] * (c[3] * c[8] - c[5] * c[6]) +
+                                       c[2] * (c[3] * c[7] - c[4] * c[6]));
+        if (std::isfinite(volume) && volume > 0.0) {
+            const int np = reduce_totals_partials(num_nodes_, static_cast<int>(num_edges_));
+            hip_check(launch_reduce_totals(num_nodes_, static_cast<int>(num_edges_), energies_.as<double>(),
+                                           forces_.as<double>(), xyz_.as<double>(), 1.0 / volume,
+                                           partials_.as<double>(), np, totals_.as<double>(), stream_),
+                      "totals");
+            fused_volume_ = volume;
+        }
+        hip_check(hipMemcpyAsync(host_totals_, totals_.as<double>(), 14 * sizeof(double), hipMemcpyDeviceToHost,
+                                 stream_),
+                  "totals copy");
+    }
     hip_check(hipStreamSynchronize(stream_), "evaluation");
+    if (check_geometry_) std::memcpy(&invalid_edges_, host_totals_ + 13, sizeof(invalid_edges_));
     if (check_geometry_ && invalid_edges_ != 0) {
         check_geometry_ = false;
         evaluated_generation_ = 0;
@@ -1729,6 +1752,8 @@ void Evaluator::finish_evaluation()
     }
 }
 
+// Energy and stress totals of the completed evaluation for `volume`, in
+// host_totals_ (reused when already reduced for this volume).
 void Evaluator::reduce(double volume)
 {
     if (evaluated_generation_ != generation_)
@@ -1741,8 +1766,18 @@ void Evaluator::reduce(double volume)
                                    forces_.as<double>(), xyz_.as<double>(), 1.0 / volume, partials_.as<double>(), np,
                                    totals_.as<double>(), stream_),
               "totals");
+    hip_check(hipMemcpyAsync(host_totals_, totals_.as<double>(), 10 * sizeof(double), hipMemcpyDeviceToHost, stream_),
+              "totals copy");
+    synchronize();
     reduced_ = true;
     reduced_volume_ = volume;
+}
+
+double Evaluator::last_max_displacement() const
+{
+    if (!last_from_positions_ || evaluated_generation_ != generation_ || generation_ == 0)
+        throw std::invalid_argument("no completed evaluation from positions of the current graph");
+    return std::sqrt(host_totals_[12]);
 }
 
 void Evaluator::synchronize() const { hip_check(hipStreamSynchronize(stream_), "synchronize"); }
@@ -1782,20 +1817,23 @@ void Evaluator::atom_forces(std::uint64_t generation, double* out)
 void Evaluator::stress(std::uint64_t generation, double volume, double* out9)
 {
     check_generation(generation);
+    // the totals of this evaluation were formed for the cell volume: a volume
+    // equal to it up to rounding rescales them instead of a second reduction
+    if (reduced_ && std::isfinite(volume) && volume > 0.0 &&
+        std::abs(volume - reduced_volume_) <= 1e-12 * reduced_volume_) {
+        const double f = reduced_volume_ / volume;
+        for (int q = 0; q < 9; ++q) out9[q] = volume == reduced_volume_ ? host_totals_[1 + q] : host_totals_[1 + q] * f;
+        return;
+    }
     reduce(volume);
-    hip_check(hipMemcpyAsync(out9, totals_.as<double>() + 1, 9 * sizeof(double), hipMemcpyDeviceToHost, stream_),
-              "copy");
-    synchronize();
+    std::memcpy(out9, host_totals_ + 1, 9 * sizeof(double));
 }
 
 double Evaluator::total_energy(std::uint64_t generation)
 {
     check_generation(generation);
     reduce(reduced_ ? reduced_volume_ : 1.0);
-    double e = 0.0;
-    hip_check(hipMemcpyAsync(&e, totals_.as<double>(), sizeof(double), hipMemcpyDeviceToHost, stream_), "copy");
-    synchronize();
-    return e;
+    return host_totals_[0];
 }
 
 }  // namespace sxl

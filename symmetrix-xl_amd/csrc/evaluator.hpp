@@ -215,6 +215,12 @@ public:
 
     // Per-stage device time (ms) accumulated over profiled evaluations.
     void set_profiling(bool enable);
+    // profile only the stages whose bit is set in mask (bit i = stage i)
+    void set_profiling_stages(unsigned mask);
+    // Largest displacement (A) of the last evaluation from positions, from
+    // the same pass (no extra device work): callers may evaluate first and
+    // rebuild and evaluate again when it exceeds their skin rule.
+    double last_max_displacement() const;
     void stage_times(double* ms, int* counts) const;
 
 private:
@@ -289,6 +295,12 @@ private:
     void launch_zbl_term(hipStream_t s);
     bool reduced_ = false;
     double reduced_volume_ = 0.0;
+    // host copy of totals_: [0] energy, [1..9] stress 3x3, [12] max |disp|^2,
+    // [13] invalid-edge count; an evaluation from positions reduces energy and
+    // stress (cell volume) in the same pass and fills it with one copy
+    double host_totals_[16] = {};
+    double fused_volume_ = 0.0;
+    bool last_from_positions_ = false;
 
     // tiled plan
     bool allow_fixed_workspace_ = false;
@@ -311,6 +323,7 @@ private:
     std::vector<int> m0_block_offsets_, readout_block_offsets_;  // [tiles + 1]
 
     bool profiling_ = false;
+    unsigned profile_mask_ = 0;
     std::vector<hipEvent_t> events_;  // [stage][begin, end]
     double stage_ms_[kNumStages] = {};
     int stage_count_[kNumStages] = {};

@@ -73,6 +73,8 @@ SIGNATURES = {
                                                         c_int_p, c_int_p, c_double_p, c_double_p]),
     "sxl_max_displacement": (ctypes.c_int, [ctypes.c_void_p, c_u64, ctypes.c_void_p, ctypes.c_int,
                                             c_double_p]),
+    "sxl_set_profiling_stages": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_uint32]),
+    "sxl_last_max_displacement": (ctypes.c_int, [ctypes.c_void_p, c_double_p]),
     "sxl_set_execution_plan_request": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_char_p,
                                                       ctypes.c_char_p]),
     "sxl_execution_plan_json": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_char_p, c_i64, ctypes.POINTER(c_i64)]),

@@ -128,55 +128,68 @@ class Symmetrix:
             raise NotImplementedError("mixed periodic boundary conditions are not supported")
         return positions, numbers, cell, bool(np.all(pbc))
 
-    def _reusable(self, positions, numbers, cell, periodic):
+    def _compatible(self, numbers, cell, periodic):
+        """Whether the cached graph may serve these atoms (same species in the
+        same order, same periodicity); a changed cell is moved to the device."""
         c = self._cache
         if c is None or c["periodic"] != periodic or len(numbers) != len(c["numbers"]) or \
                 np.any(numbers != c["numbers"]):
             return False
-        ev, gen = self.evaluator, c["generation"]
-        if not periodic:
-            moved = ev._max_displacement(gen, positions - c["offset"])
-            return moved <= 0.5 * self.neighbor_skin
-        if not np.array_equal(cell, c["cell"]):
+        if periodic and not np.array_equal(cell, c["cell"]):
             try:
                 inverse = np.linalg.inv(cell)
             except np.linalg.LinAlgError:
                 return False
-            ev._update_factorized_cell(gen, cell, inverse)
+            self.evaluator._update_factorized_cell(c["generation"], cell, inverse)
             c["cell"] = cell.copy()
             self.neighbor_cache_geometry_update_count += 1
-        moved = ev._max_displacement(gen, positions)
-        return topology_valid(cell, c["topology_cell"], moved, self.cutoff, self.neighbor_skin)
+        return True
 
-    def _prepare(self, atoms):
-        """Positions and cell the evaluator sees (isolated systems are shifted
-        into their cached box), rebuilding the graph when it is not reusable."""
-        positions, numbers, cell, periodic = self._geometry(atoms)
-        if self._reusable(positions, numbers, cell, periodic):
-            self.neighbor_cache_reuse_count += 1
-        else:
-            offset = np.zeros(3)
-            if not periodic:
-                offset, cell = self._isolated_box(positions)
-            types = self._node_types(numbers)
-            info = self.evaluator._prepare_periodic_factorized_graph(
-                types, positions - offset, cell, np.linalg.inv(cell), self.cutoff + self.neighbor_skin)
-            self._cache = {"generation": info["generation"], "numbers": numbers.copy(), "periodic": periodic,
-                           "cell": cell.copy(), "topology_cell": cell.copy(), "offset": offset,
-                           "num_edges": info["num_edges"]}
-            self.neighbor_cache_build_count += 1
-            self.neighbor_cache_geometry_update_count += 1
-        c = self._cache
+    def _still_valid(self, cell, periodic, moved):
         if not periodic:
-            return positions - c["offset"], c["cell"], False
-        return positions, cell, True
+            return moved <= 0.5 * self.neighbor_skin
+        return topology_valid(cell, self._cache["topology_cell"], moved, self.cutoff, self.neighbor_skin)
+
+    def _build(self, positions, numbers, cell, periodic):
+        offset = np.zeros(3)
+        if not periodic:
+            offset, cell = self._isolated_box(positions)
+        types = self._node_types(numbers)
+        info = self.evaluator._prepare_periodic_factorized_graph(
+            types, positions - offset, cell, np.linalg.inv(cell), self.cutoff + self.neighbor_skin)
+        self._cache = {"generation": info["generation"], "numbers": numbers.copy(), "periodic": periodic,
+                       "cell": cell.copy(), "topology_cell": cell.copy(), "offset": offset,
+                       "num_edges": info["num_edges"]}
+        self.neighbor_cache_build_count += 1
+        self.neighbor_cache_geometry_update_count += 1
+
+    def _evaluate(self, atoms):
+        """Evaluates at the atoms' positions: on the cached graph when it is
+        still valid, else on a rebuilt one.  The validity check uses the
+        displacement the evaluation itself measured, so a reused graph costs
+        one device pass; the rare failed check rebuilds and evaluates again.
+        Returns the positions and cell the evaluator saw (isolated systems are
+        shifted into their cached box) and the periodicity."""
+        positions, numbers, cell, periodic = self._geometry(atoms)
+        ev = self.evaluator
+        if self._compatible(numbers, cell, periodic):
+            c = self._cache
+            x = positions if periodic else positions - c["offset"]
+            ev._compute_prepared_factorized_positions(c["generation"], x)
+            if self._still_valid(cell, periodic, ev._last_max_displacement()):
+                self.neighbor_cache_reuse_count += 1
+                return x, c["cell"], periodic
+        self._build(positions, numbers, cell, periodic)
+        c = self._cache
+        x = positions if periodic else positions - c["offset"]
+        ev._compute_prepared_factorized_positions(c["generation"], x)
+        return x, c["cell"], periodic
 
     # ---- evaluation -----------------------------------------------------------------
     def calculate(self, atoms=None, properties=("energy", "forces", "stress"), system_changes=None):
-        positions, cell, periodic = self._prepare(atoms)
+        positions, cell, periodic = self._evaluate(atoms)
         gen = self._cache["generation"]
         ev = self.evaluator
-        ev._compute_prepared_factorized_positions(gen, positions)
         energy = ev._total_energy(gen)
         results = {
             "energy": energy,

@@ -348,8 +348,23 @@ class MACEKokkosFloat:
     def _synchronize(self):
         check(library().sxl_synchronize(self._h))
 
-    def _set_profiling(self, enable=True):
-        check(library().sxl_set_profiling(self._h, 1 if enable else 0))
+    def _set_profiling(self, enable=True, stages=None):
+        """Per-stage HIP-event timing (counters reset); `stages` limits it
+        to the named stages (two events per stage and evaluation)."""
+        if stages is None:
+            check(library().sxl_set_profiling(self._h, 1 if enable else 0))
+            return
+        names = [library().sxl_stage_name(i).decode() for i in range(library().sxl_num_stages())]
+        mask = 0
+        for name in stages:
+            mask |= 1 << names.index(name)
+        check(library().sxl_set_profiling_stages(self._h, mask if enable else 0))
+
+    def _last_max_displacement(self):
+        """Largest displacement measured by the last evaluation from positions."""
+        out = ctypes.c_double(0.0)
+        check(library().sxl_last_max_displacement(self._h, ctypes.byref(out)))
+        return float(out.value)
 
     def _stage_times(self):
         """{stage: (accumulated device ms, count)} of profiled evaluations."""

@@ -141,3 +141,32 @@ def test_coincident_atoms_raise_invalid_geometry(tiny):
     gen = ev._prepare_periodic_factorized_graph(types, s.positions, s.cell, np.linalg.inv(s.cell), 5.5)["generation"]
     ev._compute_prepared_factorized_positions(gen, s.positions)
     assert np.isfinite(ev._total_energy(gen))
+
+
+def test_fused_totals_and_displacement_match_separate_calls(tiny):
+    """An evaluation from positions reduces energy and stress for the cell
+    volume and measures the displacement in the same pass: both equal the
+    separate reductions and the separate displacement check."""
+    from symmetrix_amd import MACEKokkosFloat, synthetic
+
+    path, model = tiny
+    s = synthetic.srtio3_supercell(3, sigma=0.05, seed=15)
+    ev = MACEKokkosFloat(path)
+    types = synthetic.node_types(s, model["atomic_numbers"])
+    gen = ev._prepare_periodic_factorized_graph(types, s.positions, s.cell, np.linalg.inv(s.cell), 5.5)["generation"]
+    moved = s.positions + np.random.default_rng(2).normal(scale=0.04, size=s.positions.shape)
+    ev._compute_prepared_factorized_positions(gen, moved)
+    fused_d = ev._last_max_displacement()
+    fused_e = ev._total_energy(gen)
+    fused_s = ev._reduce_stress(s.volume, None, gen)
+    assert fused_d == pytest.approx(ev._max_displacement(gen, moved), rel=0, abs=1e-14)
+    assert fused_d == pytest.approx(float(np.max(np.linalg.norm(moved - s.positions, axis=1))), abs=1e-12)
+    # a different volume reduces again; stress scales as 1/V
+    other = ev._reduce_stress(2.0 * s.volume, None, gen)
+    np.testing.assert_allclose(other, 0.5 * fused_s, rtol=1e-12, atol=1e-15)
+    again = ev._reduce_stress(s.volume, None, gen)
+    np.testing.assert_allclose(again, fused_s, rtol=1e-12, atol=1e-15)
+    assert ev._total_energy(gen) == fused_e
+    # an evaluation from edge vectors has no displacement of its own
+    gi = ev._periodic_graph_arrays(gen)
+    assert gi["num_neigh"].sum() == ev._graph_size()[1]
