@@ -239,6 +239,12 @@ int sxl_stage_times(const sxl_evaluator* evaluator, double* ms, int* counts);
 int sxl_set_execution_plan_request(sxl_evaluator* evaluator, const char* algorithm, const char* profile,
                                    const char* debug_plan);
 
+/* selected_head and available_heads of the loaded model
+ * (mace_kokkos.cpp:1904-1905; head selection prediction_heads.hpp:10-89) as
+ * a JSON object {"selected_head": ..., "available_heads": [...]}; buffer,
+ * capacity and length as for sxl_execution_plan_json. */
+int sxl_model_heads_json(const sxl_evaluator* evaluator, char* buffer, int64_t capacity, int64_t* length);
+
 /* execution_plan_report property (mace_kokkos.cpp:271-297) as a JSON object
  * with the reference's fields: requested_algorithm, requested_profile,
  * selection_source, state, selected_id, selection_reason, available_bytes,

@@ -328,6 +328,32 @@ int sxl_set_execution_plan_request(sxl_evaluator* ev, const char* algorithm, con
     return guarded([&] { ev->impl.set_execution_plan_request(algorithm, profile, debug_plan ? debug_plan : ""); });
 }
 
+int sxl_model_heads_json(const sxl_evaluator* ev, char* buffer, int64_t capacity, int64_t* length)
+{
+    if (!ev || !length) return null_handle();
+    return guarded([&] {
+        const sxl::HostModel& m = ev->impl.model();
+        auto quote = [](const std::string& v) {
+            std::string out = "\"";
+            for (char c : v) {
+                if (c == '"' || c == '\\') out += '\\';
+                out += c;
+            }
+            return out + "\"";
+        };
+        std::string text = "{\"selected_head\": " + quote(m.selected_head) + ", \"available_heads\": [";
+        for (std::size_t i = 0; i < m.available_heads.size(); ++i)
+            text += (i ? ", " : "") + quote(m.available_heads[i]);
+        text += "]}";
+        *length = static_cast<int64_t>(text.size());
+        if (!buffer) return;
+        if (capacity <= static_cast<int64_t>(text.size()))
+            throw std::length_error("head buffer is smaller than the report");
+        std::copy(text.begin(), text.end(), buffer);
+        buffer[text.size()] = '\0';
+    });
+}
+
 int sxl_execution_plan_json(const sxl_evaluator* ev, char* buffer, int64_t capacity, int64_t* length)
 {
     if (!ev || !length) return null_handle();

@@ -96,6 +96,25 @@ Value select_head(Value data, const std::string& requested, std::string& selecte
     const Value& params = section->at("parameters");
     require(params.is_object() && params.size() == names.size(),
             "prediction_heads.parameters must define every named head.");
+    // every head carries exactly the per-head fields of the format: atomic
+    // energies, readout_1 (named after the H1 basis in format 4) and readout_2,
+    // plus the ZBL coefficients when the model has ZBL
+    std::set<std::string> expected = {"atomic_energies", "readout_2_weights_1", "readout_2_weights_2"};
+    const Value* fv = data.find("symmetrix_format_version");
+    const Value* mode = data.find("h1_affine_mode");
+    const bool v4 = fv && fv->is_number() && fv->as_number() == 4;
+    const bool pre = mode && mode->kind == Value::Kind::string && mode->str == "pre_linear_up";
+    expected.insert(!v4 ? "readout_1_weights" : pre ? "readout_1_weights_for_H1_pre_linear_up"
+                                                    : "readout_1_weights_for_M0");
+    const Value* zbl = data.find("has_zbl");
+    if (zbl && zbl->kind == Value::Kind::boolean && zbl->b) expected.insert("zbl_c");
+    for (const auto& name : names) {
+        const Value* head = params.find(name);
+        require(head && head->is_object(), "prediction_heads.parameters must define every named head.");
+        std::set<std::string> fields;
+        for (const auto& kv : head->obj) fields.insert(kv.first);
+        require(fields == expected, "Every prediction-head payload must contain exactly the supported fields.");
+    }
     const Value* def = section->find("default");
     const std::string default_head = def && def->kind == Value::Kind::string ? def->str : "";
     require(unique.count(default_head) == 1, "prediction_heads.default must name a stored head.");

@@ -220,6 +220,23 @@ class MACEKokkosFloat:
                                                        str(debug_plan or "").encode()))
         self._evaluated = False
 
+    def _heads(self):
+        length = c_i64(0)
+        check(library().sxl_model_heads_json(self._h, None, 0, ctypes.byref(length)))
+        buf = ctypes.create_string_buffer(int(length.value) + 1)
+        check(library().sxl_model_heads_json(self._h, buf, len(buf), ctypes.byref(length)))
+        return json.loads(buf.value.decode())
+
+    @property
+    def selected_head(self):
+        """Prediction head whose parameters were loaded (reference selected_head)."""
+        return self._heads()["selected_head"]
+
+    @property
+    def available_heads(self):
+        """Prediction heads stored in the model file (reference available_heads)."""
+        return self._heads()["available_heads"]
+
     @property
     def execution_plan_report(self):
         """The planner's candidates, memory estimates and selection for the

@@ -336,6 +336,34 @@ def _split_h1(model: dict, shape: ModelShape, rng) -> None:
         model["H1_first_residual_weights"] = _Array(b)
 
 
+def multihead_model(model: dict, names=("default", "other"), default=None, seed: int = 1) -> dict:
+    """A multi-head file (prediction_heads schema 1, reference
+    prediction_heads.hpp:10-89) from a single-head model: the first head keeps
+    the model's own per-head fields, the others get fresh random readouts and
+    atomic energies of the same shapes."""
+    rng = np.random.default_rng([seed, 7])
+    pre = model.get("h1_affine_mode") == "pre_linear_up"
+    readout_1 = "readout_1_weights_for_H1_pre_linear_up" if pre else "readout_1_weights_for_M0"
+    fields = ["atomic_energies", readout_1, "readout_2_weights_1", "readout_2_weights_2"]
+    if model.get("has_zbl"):
+        fields.append("zbl_c")
+    out = dict(model)
+    params = {}
+    for i, name in enumerate(names):
+        head = {}
+        for f in fields:
+            v = model[f]
+            if i == 0 or f == "zbl_c":
+                head[f] = v
+            else:
+                arr = np.asarray(v if not isinstance(v, _Array) else v.values, dtype=np.float64)
+                head[f] = _Array(arr + rng.normal(size=arr.shape) * (0.5 * np.std(arr) + 1e-3))
+        params[name] = head
+    out["prediction_heads"] = {"schema_version": 1, "names": list(names),
+                               "default": default or names[0], "parameters": params}
+    return out
+
+
 def model_json(model: dict) -> str:
     return _dump(model)
 

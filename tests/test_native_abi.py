@@ -39,11 +39,11 @@ def test_stage_names():
     assert "r1_reverse" in names and "a0_forward" in names and len(set(names)) == n
 
 
-def _create(path):
+def _create(path, head=""):
     from symmetrix_amd import _native
 
     h = ctypes.c_void_p()
-    status = _native.library().sxl_create(path.encode(), b"", ctypes.byref(h))
+    status = _native.library().sxl_create(path.encode(), head.encode(), ctypes.byref(h))
     msg = _native.library().sxl_last_error().decode()
     if status == 0:
         _native.library().sxl_destroy(h)
@@ -151,6 +151,53 @@ def test_pre_linear_up_validation_errors(tmp_path, edit, message):
     status, msg = _create(str(path))
     assert status == 1, msg
     assert message in msg
+
+
+def _multihead(**edits):
+    from symmetrix_amd import synthetic
+
+    model = synthetic.multihead_model(synthetic.random_mace_model("tiny", seed=0), names=("a", "b"))
+    model = json.loads(synthetic.model_json(model))
+    section = model["prediction_heads"]
+    for key, value in edits.items():
+        if key == "drop_field":
+            del section["parameters"]["b"][value]
+        else:
+            section[key] = value
+    return model
+
+
+@pytest.mark.parametrize(
+    "edits, head, message",
+    [
+        ({}, "c", "Requested prediction head 'c' is unavailable"),
+        ({"schema_version": 2}, "", "unsupported schema version"),
+        ({"names": ["a", "a"]}, "", "unique non-empty strings"),
+        ({"default": "z"}, "", "default must name a stored head"),
+        ({"drop_field": "readout_2_weights_2"}, "", "exactly the supported fields"),
+    ],
+)
+def test_prediction_head_validation(tmp_path, edits, head, message):
+    """Head selection errors of the reference (prediction_heads.hpp:30-82)."""
+    path = tmp_path / "m.json"
+    path.write_text(json.dumps(_multihead(**edits)))
+    status, msg = _create(str(path), head)
+    assert status == 1, msg
+    assert message in msg
+
+
+def test_single_head_file_rejects_a_named_head(tmp_path):
+    from symmetrix_amd import synthetic
+
+    model = json.loads(synthetic.model_json(synthetic.random_mace_model("tiny", seed=0)))
+    path = tmp_path / "m.json"
+    path.write_text(json.dumps(model))
+    status, msg = _create(str(path), "x")
+    assert status == 1 and "does not identify a prediction head" in msg
+    model["head"] = "pbe"
+    path.write_text(json.dumps(model))
+    status, msg = _create(str(path), "x")
+    assert status == 1 and "the JSON contains 'pbe'" in msg
 
 
 def test_malformed_json(tmp_path):
