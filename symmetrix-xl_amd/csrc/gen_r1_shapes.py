@@ -61,6 +61,13 @@ def emit_shape(lmax, Lmax):
         if (p, lm2, lm1) not in triples:
             triples.append((p, lm2, lm1))
         term_tr.append(triples.index((p, lm2, lm1)))
+    # distinct (path, lm2, lme) groups in term order: the forward pass folds
+    # the terms of a group into one per-edge weight sum_t cg_t Y[lm1_t]
+    pls, term_pl = [], []
+    for p, lm2, _, lme, _ in terms:
+        if (p, lm2, lme) not in pls:
+            pls.append((p, lm2, lme))
+        term_pl.append(pls.index((p, lm2, lme)))
     name = f"R1Shape<{lmax}, {Lmax}>"
 
     def arr(vals):
@@ -98,6 +105,11 @@ def emit_shape(lmax, Lmax):
         f"    static constexpr int tr_pq[NTR] = {arr([pqs.index(x[:2]) for x in triples])};",
         f"    static constexpr int tr_lm1[NTR] = {arr([x[2] for x in triples])};",
         f"    static constexpr int term_tr[NT] = {arr(term_tr)};",
+        "    // distinct (path, lm2, lme) groups, term order",
+        f"    static constexpr int NPL = {len(pls)};",
+        f"    static constexpr int pl_pq[NPL] = {arr([pqs.index(x[:2]) for x in pls])};",
+        f"    static constexpr int pl_lme[NPL] = {arr([x[2] for x in pls])};",
+        f"    static constexpr int term_pl[NT] = {arr(term_pl)};",
         "};",
         "",
     ]

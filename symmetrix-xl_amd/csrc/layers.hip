@@ -82,23 +82,54 @@ constexpr int kDepth = 4;  // edges in flight per wave in the layer-0 kernels
 struct TileSlot {
     bool active;
     int slot;
+    int row;  // spline coefficient row: pair * intervals + interval
+    float x;  // local coordinate in the interval
 };
 
-// Ballot-compacts the edges [base, base + n) of the tile; lanes 0..63 of wave 0.
-__device__ __forceinline__ TileSlot compact_edge(const EdgeGraph& g, const SplineGrid& grid, int base,
-                                                 int n, int t, double& rr, int* count)
+// Compacts the edges [base, base + n) of the tile within r_cut into slots;
+// lanes 0..63 of wave 0.  kOrdered selects the ordered-pair rows of the
+// layer-0 tables, else the unordered (or shared) rows of the second
+// interaction.  With kSorted the slots are ordered by spline row (ties in
+// edge order): edges that share a coefficient row become neighbours in the
+// channel loop and find the row in L1 (in a crystal most of a receiver's
+// edges fall into a few shells); the slot is then the number of active lanes
+// with a smaller (row, lane) key.  The forward kernels, bound by their row
+// loads, sort; the reverse kernels, bound by arithmetic, keep edge order
+// (slot = lane prefix count) and skip the ranking.
+template <bool kOrdered, bool kSorted>
+__device__ __forceinline__ TileSlot compact_edge(const EdgeGraph& g, const SplineGrid& grid, int base, int n,
+                                                 int t, double& rr, int* count)
 {
     bool on = false;
     rr = 0.0;
+    int row = 0;
+    float x = 0.0f;
     if (t < n) {
         rr = g.r[base + t];
         on = rr < grid.r_cut;
     }
+    if (on) {
+        int iv;
+        spline_point(rr, grid, iv, x);
+        const int pair = kOrdered ? g.edge_pair[base + t] & 0xffff : g.edge_pair[base + t] >> 16;
+        row = pair * grid.intervals + iv;
+    }
     const unsigned long long mask = __ballot(on);
-    const int slot = __builtin_amdgcn_mbcnt_hi(static_cast<unsigned>(mask >> 32),
-                                               __builtin_amdgcn_mbcnt_lo(static_cast<unsigned>(mask), 0));
+    int slot;
+    if constexpr (kSorted) {
+        constexpr unsigned kRowCap = (1u << 26) - 2;  // keys stay below the inactive sentinel
+        const unsigned key = on ? (min(static_cast<unsigned>(row), kRowCap) << 6) | static_cast<unsigned>(t)
+                                : 0xffffffffu;
+        slot = 0;
+#pragma unroll
+        for (int u = 0; u < 64; ++u)
+            slot += static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(key), u)) < key ? 1 : 0;
+    } else {
+        slot = __builtin_amdgcn_mbcnt_hi(static_cast<unsigned>(mask >> 32),
+                                         __builtin_amdgcn_mbcnt_lo(static_cast<unsigned>(mask), 0));
+    }
     if (t == 0) *count = __popcll(mask);
-    return {on, slot};
+    return {on, slot, row, x};
 }
 
 // Scalar density spline (one cubic per interval and unordered pair) at r:
@@ -175,16 +206,14 @@ __global__ void __launch_bounds__(256) a0_forward_kernel(LayerArgs a, const floa
         if (threadIdx.x < 64) {
             const int t = threadIdx.x;
             double rr;
-            const TileSlot ts = compact_edge(g, a.grid, base, min(kTile, e1 - base), t, rr, &s_count);
+            const TileSlot ts = compact_edge<true, true>(g, a.grid, base, min(kTile, e1 - base), t, rr, &s_count);
             if (ts.active) {
                 const int e = base + t;
-                int iv;
-                float x, Y[NLM], dir[3];
-                spline_point(rr, a.grid, iv, x);
+                float Y[NLM], dir[3];
                 edge_harmonics<LMAX, false>(g.xyz + 3 * static_cast<size_t>(e), rr, Y, nullptr,
                                             nullptr, nullptr, dir);
-                s_x[ts.slot] = x;
-                s_row[ts.slot] = (g.edge_pair[e] & 0xffff) * a.grid.intervals + iv;
+                s_x[ts.slot] = ts.x;
+                s_row[ts.slot] = ts.row;
 #pragma unroll
                 for (int lm = 0; lm < NLM; ++lm) s_Y[ts.slot][lm] = Y[lm];
             }
@@ -224,9 +253,19 @@ __global__ void __launch_bounds__(256) a0_forward_kernel(LayerArgs a, const floa
 
 // ---------------------------------------------------------------------------
 // Layer 1 forward: Phi1[i, lme, k] = sum_j sum_t cg_t Y_{lm1_t} R1_{p_t}(r)[k] H1[src, lm2_t, k]
+//
+// The terms are grouped by (path, lm2, lme): the tile prologue folds each
+// group's CG-weighted harmonics into one edge weight W_g = sum_t cg_t Y_lm1(t),
+// and the channel loop does one FMA per group, acc[lme_g] += W_g R_p H_lm2.
+// W is read from LDS in batches of kWBatch float4s, double-buffered, with
+// scheduling barriers so each batch is in flight while the previous one is
+// consumed (the compiler otherwise issues each read just before its use).
 // ---------------------------------------------------------------------------
+constexpr int kWBatch = 4;
+
 template <class S>
-__global__ void __launch_bounds__(256) r1_forward_kernel(LayerArgs a, const float* __restrict__ r1,
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S::NPL <= 96 ? 3 : 1)))
+r1_forward_kernel(LayerArgs a, const float* __restrict__ r1,
                                                           const float* __restrict__ cg,
                                                           const float* __restrict__ H1,
                                                           float* __restrict__ Phi1)
@@ -236,7 +275,10 @@ __global__ void __launch_bounds__(256) r1_forward_kernel(LayerArgs a, const floa
     constexpr int NP = S::NP;
     constexpr int NT = S::NT;
     constexpr int NPQ = S::NPQ;
-    __shared__ float s_cgY[kTile][(NT + 3) / 4 * 4];
+    constexpr int NPL = S::NPL;
+    constexpr int NQ = (NPL + 3) / 4;                 // float4s of W per edge
+    constexpr int NB = (NQ + kWBatch - 1) / kWBatch;  // batches per edge
+    __shared__ float4v s_W[kTile][NQ];
     __shared__ float s_x[kTile];
     __shared__ int s_row[kTile];
     __shared__ int s_src[kTile];
@@ -262,25 +304,29 @@ __global__ void __launch_bounds__(256) r1_forward_kernel(LayerArgs a, const floa
         if (threadIdx.x < 64) {
             const int t = threadIdx.x;
             double rr;
-            const TileSlot ts = compact_edge(g, a.grid, base, min(kTile, e1 - base), t, rr, &s_count);
+            const TileSlot ts = compact_edge<false, true>(g, a.grid, base, min(kTile, e1 - base), t, rr, &s_count);
             if (ts.active) {
                 const int e = base + t;
-                int iv;
-                float x, Y[NLM], dir[3];
-                spline_point(rr, a.grid, iv, x);
+                float Y[NLM], dir[3];
                 edge_harmonics<S::LMAX, false>(g.xyz + 3 * static_cast<size_t>(e), rr, Y, nullptr,
                                                nullptr, nullptr, dir);
-                s_x[ts.slot] = x;
-                s_row[ts.slot] = (g.edge_pair[e] >> 16) * a.grid.intervals + iv;
+                s_x[ts.slot] = ts.x;
+                s_row[ts.slot] = ts.row;
                 s_src[ts.slot] = g.source[e];
+                // one float4 of W at a time (terms filtered at compile time)
 #pragma unroll
-                for (int q = 0; q < NT; ++q) s_cgY[ts.slot][q] = cg[q] * Y[S::term_lm1[q]];
+                for (int q = 0; q < NQ; ++q) {
+                    float4v w = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int u = 0; u < NT; ++u)
+                        if (S::term_pl[u] / 4 == q)
+                            w[S::term_pl[u] % 4] = fmaf(cg[u], Y[S::term_lm1[u]], w[S::term_pl[u] % 4]);
+                    s_W[ts.slot][q] = w;
+                }
             }
         }
         __syncthreads();
         const int count = uniform(s_count);
-        // the spline row and source features of edge j + 1 are in flight while
-        // edge j is contracted
         auto fetch = [&](int j, float4v* c, float* H) {
             const auto rs = buffer_rsrc(r1 + static_cast<size_t>(uniform(s_row[j])) * NP * C * 4, row_bytes);
             const auto hs = buffer_rsrc(H1 + static_cast<size_t>(uniform(s_src[j])) * NLMS * C, h_bytes);
@@ -290,19 +336,41 @@ __global__ void __launch_bounds__(256) r1_forward_kernel(LayerArgs a, const floa
             for (int q = 0; q < NLMS; ++q) H[q] = load1(hs, kk * 4, q * C * 4);
         };
         // One row buffer: once the radial values of edge j are formed, its
-        // coefficient registers are refilled with the row of edge j + 1.
+        // coefficient registers are refilled with the row of edge j + 1 (an
+        // L1 hit when both share the row).
         float4v c[NP];
         float H[NLMS];
         if (count > 0) fetch(0, c, H);
         for (int j = 0; j < count; ++j) {
+            const float4v* Wj = s_W[j];
+            float4v wb[2][kWBatch];
+#pragma unroll
+            for (int q = 0; q < kWBatch; ++q)
+                if (q < NQ) wb[0][q] = Wj[q];
             const float x = uniform(s_x[j]);
             float RH[NPQ];
 #pragma unroll
             for (int pq = 0; pq < NPQ; ++pq) RH[pq] = cubic(c[S::pq_p[pq]], x) * H[S::pq_lm2[pq]];
             fetch(min(j + 1, count - 1), c, H);
 #pragma unroll
-            for (int t = 0; t < NT; ++t)
-                acc[S::term_lme[t]] = fmaf(s_cgY[j][t], RH[S::tr_pq[S::term_tr[t]]], acc[S::term_lme[t]]);
+            for (int b = 0; b < NB; ++b) {
+                if (b + 1 < NB) {
+#pragma unroll
+                    for (int q = 0; q < kWBatch; ++q)
+                        if ((b + 1) * kWBatch + q < NQ) wb[(b + 1) & 1][q] = Wj[(b + 1) * kWBatch + q];
+                }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int q = 0; q < kWBatch; ++q) {
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const int gidx = 4 * (b * kWBatch + q) + u;
+                        if (gidx < NPL)
+                            acc[S::pl_lme[gidx]] = fmaf(wb[b & 1][q][u], RH[S::pl_pq[gidx]], acc[S::pl_lme[gidx]]);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
     }
     if (k < C) {
@@ -388,17 +456,14 @@ r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
             const int t = threadIdx.x;
             double rr;
             const int n = min(kTile, e1 - base);
-            const TileSlot ts = compact_edge(g, a.grid, base, n, t, rr, &s_count);
+            const TileSlot ts = compact_edge<false, false>(g, a.grid, base, n, t, rr, &s_count);
             const int e = base + t;
             if (ts.active) {
-                int iv;
-                float x;
                 const int sl = ts.slot;
-                spline_point(rr, a.grid, iv, x);
                 edge_harmonics<S::LMAX, true>(g.xyz + 3 * static_cast<size_t>(e), rr, s_Y[sl], s_dY[sl][0],
                                               s_dY[sl][1], s_dY[sl][2], s_geo[sl]);
-                s_geo[sl][3] = x;
-                s_row[sl] = (g.edge_pair[e] >> 16) * a.grid.intervals + iv;
+                s_geo[sl][3] = ts.x;
+                s_row[sl] = ts.row;
                 s_src[sl] = g.source[e];
                 s_eid[sl] = e;
                 s_dsc[sl] = a.d1.table ? dcoef * density_slope(a.d1.table, a.grid, g.edge_pair[e] >> 16, rr) : 0.0f;
@@ -429,20 +494,18 @@ r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
         };
         // One row buffer: once the radial values of edge j are formed, its
         // coefficient registers are refilled with the row of edge j + 1.
-        float4v cn[NP];
-        float Hn[NLMS];
-        if (count > 0) fetch(0, cn, Hn);
-        for (int j = 0; j < count; ++j) {
+        // edge j from its row buffer (cj, Hj); the row of edge j + 1 is
+        // already in flight in the other buffer
+        auto edge = [&](int j, const float4v* cj, const float* Hj) {
             const float x = uniform(s_geo[j][3]);
             float R[NP], dR[NP], H[NLMS];
 #pragma unroll
             for (int p = 0; p < NP; ++p) {
-                R[p] = cubic(cn[p], x);
-                dR[p] = cubic_slope(cn[p], x, 3.0f * x);
+                R[p] = cubic(cj[p], x);
+                dR[p] = cubic_slope(cj[p], x, 3.0f * x);
             }
 #pragma unroll
-            for (int q = 0; q < NLMS; ++q) H[q] = Hn[q];
-            fetch(min(j + 1, count - 1), cn, Hn);
+            for (int q = 0; q < NLMS; ++q) H[q] = Hj[q];
             float sp[NPQ], U[NLM], RH[NPQ];
 #pragma unroll
             for (int pq = 0; pq < NPQ; ++pq) {
@@ -500,7 +563,22 @@ r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
                 s_f[j][wave][1] = fy;
                 s_f[j][wave][2] = fz;
             }
+        };
+        // Two row buffers used in turn (unrolled by two, so no register
+        // copies).
+        // A pair loop plus a one-edge tail keeps every path into the loop
+        // head alike (a conditional second half would make the compiler wait
+        // for the prefetch there).
+        float4v ca[NP], cb[NP];
+        float Ha[NLMS], Hb[NLMS];
+        if (count > 0) fetch(0, ca, Ha);
+        for (int j = 0; j + 1 < count; j += 2) {
+            fetch(j + 1, cb, Hb);
+            edge(j, ca, Ha);
+            fetch(min(j + 2, count - 1), ca, Ha);
+            edge(j + 1, cb, Hb);
         }
+        if (count & 1) edge(count - 1, ca, Ha);
         __syncthreads();
         if (threadIdx.x < count) {
             const int t = threadIdx.x;
@@ -698,17 +776,14 @@ __global__ void __launch_bounds__(256) r1_reverse_grouped_kernel(LayerArgs a, co
             const int t = threadIdx.x;
             double rr;
             const int n = min(kTile, e1 - base);
-            const TileSlot ts = compact_edge(g, a.grid, base, n, t, rr, &L.count);
+            const TileSlot ts = compact_edge<false, false>(g, a.grid, base, n, t, rr, &L.count);
             const int e = base + t;
             if (ts.active) {
-                int iv;
-                float x;
                 const int sl = ts.slot;
-                spline_point(rr, a.grid, iv, x);
                 edge_harmonics<S::LMAX, true>(g.xyz + 3 * static_cast<size_t>(e), rr, L.Y[sl], L.dY[sl][0],
                                               L.dY[sl][1], L.dY[sl][2], L.geo[sl]);
-                L.geo[sl][3] = x;
-                L.row[sl] = (g.edge_pair[e] >> 16) * a.grid.intervals + iv;
+                L.geo[sl][3] = ts.x;
+                L.row[sl] = ts.row;
                 L.src[sl] = g.source[e];
                 L.eid[sl] = e;
                 L.dsc[sl] = a.d1.table ? dcoef * density_slope(a.d1.table, a.grid, g.edge_pair[e] >> 16, rr) : 0.0f;
@@ -808,17 +883,14 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
             const int t = threadIdx.x;
             double rr;
             const int n = min(kTile, e1 - base);
-            const TileSlot ts = compact_edge(g, a.grid, base, n, t, rr, &s_count);
+            const TileSlot ts = compact_edge<true, false>(g, a.grid, base, n, t, rr, &s_count);
             const int e = base + t;
             if (ts.active) {
-                int iv;
-                float x;
                 const int sl = ts.slot;
-                spline_point(rr, a.grid, iv, x);
                 edge_harmonics<LMAX, true>(g.xyz + 3 * static_cast<size_t>(e), rr, s_Y[sl], s_dY[sl][0],
                                            s_dY[sl][1], s_dY[sl][2], s_geo[sl]);
-                s_geo[sl][3] = x;
-                s_row[sl] = (g.edge_pair[e] & 0xffff) * a.grid.intervals + iv;
+                s_geo[sl][3] = ts.x;
+                s_row[sl] = ts.row;
                 s_eid[sl] = e;
                 s_dsc[sl] = a.d0.table ? dcoef * density_slope(a.d0.table, a.grid, g.edge_pair[e] >> 16, rr) : 0.0f;
             } else if (t < n && a.d0.table) {
