@@ -182,6 +182,20 @@ __device__ __forceinline__ float wave_sum_dpp(float v)
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+// The same reduction left in the lanes: lanes 48..63 (in particular lane 63)
+// hold the wave sum, the other lanes partial sums.  For a sum that only one
+// lane stores, this saves the broadcast.
+__device__ __forceinline__ float wave_sum_lane63(float v)
+{
+    v += dpp_moved<0xb1>(v);
+    v += dpp_moved<0x4e>(v);
+    v += dpp_moved<0x141>(v);
+    v += dpp_moved<0x140>(v);
+    v += dpp_moved<0x142, 0xa>(v);
+    v += dpp_moved<0x143, 0xc>(v);
+    return v;
+}
+
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 __device__ __forceinline__ float uniform(float v)
 {
@@ -223,6 +237,17 @@ __device__ __forceinline__ float cubic(const float4v& c, float x)
 __device__ __forceinline__ float cubic_slope(const float4v& c, float x, float x3)
 {
     return fmaf(x, fmaf(x3, c.w, c.z + c.z), c.y);
+}
+
+// Value and slope of the cubic sharing its Horner terms: with
+// t1 = c2 + x c3 and t2 = c1 + x t1, value = c0 + x t2 and
+// slope = t2 + x (t1 + x c3) = c1 + 2 c2 x + 3 c3 x^2 (five FMAs).
+__device__ __forceinline__ void cubic_value_slope(const float4v& c, float x, float& value, float& slope)
+{
+    const float t1 = fmaf(x, c.w, c.z);
+    const float t2 = fmaf(x, t1, c.y);
+    value = fmaf(x, t2, c.x);
+    slope = fmaf(x, fmaf(x, c.w, t1), t2);
 }
 
 __device__ __forceinline__ int unordered_pair(int a, int b, int n)

@@ -500,10 +500,7 @@ r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
             const float x = uniform(s_geo[j][3]);
             float R[NP], dR[NP], H[NLMS];
 #pragma unroll
-            for (int p = 0; p < NP; ++p) {
-                R[p] = cubic(cj[p], x);
-                dR[p] = cubic_slope(cj[p], x, 3.0f * x);
-            }
+            for (int p = 0; p < NP; ++p) cubic_value_slope(cj[p], x, R[p], dR[p]);
 #pragma unroll
             for (int q = 0; q < NLMS; ++q) H[q] = Hj[q];
             float sp[NPQ], U[NLM], RH[NPQ];
@@ -555,10 +552,10 @@ r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
                 gy = fmaf(s_dY[j][1][lm], U[lm], gy);
                 gz = fmaf(s_dY[j][2][lm], U[lm], gz);
             }
-            const float fx = wave_sum_dpp(-fmaf(s_geo[j][0], A, gx));
-            const float fy = wave_sum_dpp(-fmaf(s_geo[j][1], A, gy));
-            const float fz = wave_sum_dpp(-fmaf(s_geo[j][2], A, gz));
-            if (lane == 0) {
+            const float fx = wave_sum_lane63(-fmaf(s_geo[j][0], A, gx));
+            const float fy = wave_sum_lane63(-fmaf(s_geo[j][1], A, gy));
+            const float fz = wave_sum_lane63(-fmaf(s_geo[j][2], A, gz));
+            if (lane == 63) {
                 s_f[j][wave][0] = fx;
                 s_f[j][wave][1] = fy;
                 s_f[j][wave][2] = fz;
@@ -679,10 +676,7 @@ __device__ __forceinline__ void r1_reverse_pass(const LayerArgs& a, int i, bool 
         const float x = uniform(L.geo[j][3]);
         float R[RG::NP], dR[RG::NP], H[RG::NH];
 #pragma unroll
-        for (int p = 0; p < RG::NP; ++p) {
-            R[p] = cubic(cn[p], x);
-            dR[p] = cubic_slope(cn[p], x, 3.0f * x);
-        }
+        for (int p = 0; p < RG::NP; ++p) cubic_value_slope(cn[p], x, R[p], dR[p]);
 #pragma unroll
         for (int q = 0; q < RG::NH; ++q) H[q] = Hn[q];
         fetch(min(j + 1, count - 1), cn, Hn);
@@ -735,10 +729,10 @@ __device__ __forceinline__ void r1_reverse_pass(const LayerArgs& a, int i, bool 
             gy = fmaf(L.dY[j][1][lm], U[lm], gy);
             gz = fmaf(L.dY[j][2][lm], U[lm], gz);
         }
-        const float fx = wave_sum_dpp(-fmaf(L.geo[j][0], A, gx));
-        const float fy = wave_sum_dpp(-fmaf(L.geo[j][1], A, gy));
-        const float fz = wave_sum_dpp(-fmaf(L.geo[j][2], A, gz));
-        if (lane == 0) {
+        const float fx = wave_sum_lane63(-fmaf(L.geo[j][0], A, gx));
+        const float fy = wave_sum_lane63(-fmaf(L.geo[j][1], A, gy));
+        const float fz = wave_sum_lane63(-fmaf(L.geo[j][2], A, gz));
+        if (lane == 63) {
             L.f[j][wave][0] = first ? fx : L.f[j][wave][0] + fx;
             L.f[j][wave][1] = first ? fy : L.f[j][wave][1] + fy;
             L.f[j][wave][2] = first ? fz : L.f[j][wave][2] + fz;
@@ -912,7 +906,6 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
         };
         auto edge_force = [&](int j, const float4v* cl) {
             const float x = uniform(s_geo[j][3]);
-            const float x3 = 3.0f * x;
             float yl[NL], ax[NL], ay[NL], az[NL];
 #pragma unroll
             for (int l = 0; l < NL; ++l) yl[l] = ax[l] = ay[l] = az[l] = 0.0f;
@@ -927,16 +920,17 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
             float A = 0.0f, gx = 0.0f, gy = 0.0f, gz = 0.0f;
 #pragma unroll
             for (int l = 0; l < NL; ++l) {
-                const float R = cubic(cl[l], x);
-                A = fmaf(cubic_slope(cl[l], x, x3), yl[l], A);
+                float R, dR;
+                cubic_value_slope(cl[l], x, R, dR);
+                A = fmaf(dR, yl[l], A);
                 gx = fmaf(R, ax[l], gx);
                 gy = fmaf(R, ay[l], gy);
                 gz = fmaf(R, az[l], gz);
             }
-            const float fx = wave_sum_dpp(-fmaf(s_geo[j][0], A, gx));
-            const float fy = wave_sum_dpp(-fmaf(s_geo[j][1], A, gy));
-            const float fz = wave_sum_dpp(-fmaf(s_geo[j][2], A, gz));
-            if (lane == 0) {
+            const float fx = wave_sum_lane63(-fmaf(s_geo[j][0], A, gx));
+            const float fy = wave_sum_lane63(-fmaf(s_geo[j][1], A, gy));
+            const float fz = wave_sum_lane63(-fmaf(s_geo[j][2], A, gz));
+            if (lane == 63) {
                 s_f[j][wave][0] = fx;
                 s_f[j][wave][1] = fy;
                 s_f[j][wave][2] = fz;
