@@ -25,7 +25,7 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kBM = 64, kBN = 128, kBK = 32, kPad = 4;
 
-__global__ void __launch_bounds__(256) gemm_group_kernel(GemmGroup grp)
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 5))) gemm_group_kernel(GemmGroup grp)
 {
     __shared__ float As[kBM][kBK + kPad];
     __shared__ float Bs[kBN][kBK + kPad];
@@ -43,12 +43,15 @@ __global__ void __launch_bounds__(256) gemm_group_kernel(GemmGroup grp)
     const int lane = t & 63, wave = t >> 6;
     const int wm = wave >> 1, wn = wave & 1;
 
-    // global -> register staging: A 64 x 32 (2 float4 per thread), Bt 128 x 32 (4 float4)
-    const int lr = t >> 3, lk = (t & 7) * 4;
-    const float* arow[2];
+    // global -> register staging: kBK / 4 threads per row (one float4 each),
+    // kRowsPerPass rows per pass; A takes kAPasses passes, Bt kBPasses
+    constexpr int kThreadsPerRow = kBK / 4, kRowsPerPass = 256 / kThreadsPerRow;
+    constexpr int kAPasses = kBM / kRowsPerPass, kBPasses = kBN / kRowsPerPass;
+    const int lr = t / kThreadsPerRow, lk = (t % kThreadsPerRow) * 4;
+    const float* arow[kAPasses];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int r = row0 + lr + 32 * j;
+    for (int j = 0; j < kAPasses; ++j) {
+        const int r = row0 + lr + kRowsPerPass * j;
         arow[j] = nullptr;
         if (r < M) {
             const int node = r / g.rows_per_node;
@@ -56,19 +59,19 @@ __global__ void __launch_bounds__(256) gemm_group_kernel(GemmGroup grp)
             arow[j] = g.a.ptr + node * g.a.node_stride + m * g.a.row_stride + lk;
         }
     }
-    const float* brow[4];
+    const float* brow[kBPasses];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int n = col0 + lr + 32 * j;
+    for (int j = 0; j < kBPasses; ++j) {
+        const int n = col0 + lr + kRowsPerPass * j;
         brow[j] = n < N ? g.Bt + static_cast<size_t>(n) * K + lk : nullptr;
     }
-    float4 ra[2], rb[4];
+    float4 ra[kAPasses], rb[kBPasses];
     auto fetch = [&](int k0) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < kAPasses; ++j)
             ra[j] = arow[j] ? *reinterpret_cast<const float4*>(arow[j] + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < kBPasses; ++j)
             rb[j] = brow[j] ? *reinterpret_cast<const float4*>(brow[j] + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
     };
 
@@ -83,9 +86,9 @@ __global__ void __launch_bounds__(256) gemm_group_kernel(GemmGroup grp)
     const int kh = 4 * (lane >> 5);
     for (int k0 = 0; k0 < K; k0 += kBK) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) *reinterpret_cast<float4*>(&As[lr + 32 * j][lk]) = ra[j];
+        for (int j = 0; j < kAPasses; ++j) *reinterpret_cast<float4*>(&As[lr + kRowsPerPass * j][lk]) = ra[j];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) *reinterpret_cast<float4*>(&Bs[lr + 32 * j][lk]) = rb[j];
+        for (int j = 0; j < kBPasses; ++j) *reinterpret_cast<float4*>(&Bs[lr + kRowsPerPass * j][lk]) = rb[j];
         __syncthreads();
         if (k0 + kBK < K) fetch(k0 + kBK);
 #pragma unroll
