@@ -340,6 +340,37 @@ __global__ void __launch_bounds__(256) m0_reverse_kernel(LayerArgs a, PolyArgs p
 //      M1_adj[n][k] = sum_o W[k][o] H2_adj[n][o]
 //   6. A1_adj[n][lm][k] = M1_adj[n][k] dP1/dA1[lm]
 // ---------------------------------------------------------------------------
+// Weight streaming of the readout's matrix-vector phases.  A phase reads
+// W[in][k] (in = 0..n_in-1, column k of the thread) for blocks of kStreamW
+// inputs; the blocks pass through a ring of kStreamRing register buffers so
+// the loads of the next kStreamRing - 1 blocks are in flight while one block
+// is consumed (waiting on each block's loads in turn would put one memory
+// round trip per block on the critical path).  `load(b, buf)` fills buf with
+// block b (clamped to the last block: every step issues the same loads, so
+// the waits stay exact), `use(b, buf)` consumes it.  Blocks beyond the last
+// whole ring round are handled by `tail(b)` without the ring.
+constexpr int kStreamRing = 4;
+
+template <int W, class Load, class Use, class Tail>
+__device__ __forceinline__ void stream_blocks(int nblocks, Load& load, Use& use, Tail& tail)
+{
+    constexpr int R = kStreamRing;
+    float ring[R][W];
+    const int full = nblocks / R * R;
+    if (full > 0) {
+#pragma unroll
+        for (int d = 0; d < R - 1; ++d) load(d, ring[d]);
+        for (int b0 = 0; b0 < full; b0 += R) {
+#pragma unroll
+            for (int d = 0; d < R; ++d) {
+                load(min(b0 + d + R - 1, full - 1), ring[(d + R - 1) % R]);
+                use(b0 + d, ring[d]);
+            }
+        }
+    }
+    for (int b = full; b < nblocks; ++b) tail(b);
+}
+
 constexpr int kReadoutGroup = 4;  // nodes held in registers by the polynomial phases
 constexpr int kMaxHidden = 64;
 constexpr int kMaxWavesReadout = 4;  // 256 threads
@@ -404,38 +435,57 @@ __global__ void __launch_bounds__(256) readout_kernel(ReadoutArgs a)
     }
     __syncthreads();
 
-    // 2. H2
+    // 2. H2 (weight columns streamed, 4 inputs per block); per-wave partial
+    //    sums of q . xs for the energies
     if (ok) {
         float h2[NB];
 #pragma unroll
         for (int n = 0; n < NB; ++n) h2[n] = 0.0f;
         const float* Tm = a.H2M0 + static_cast<size_t>(blk.type) * C * C + k;
         const float* Wm = a.H2M1 + k;
-        for (int in = 0; in < C; in += 4) {
-            float t4[4], w4[4];
+        auto load = [&](int b, float (&w)[8]) {
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                t4[u] = Tm[static_cast<size_t>(in + u) * C];
-                w4[u] = Wm[static_cast<size_t>(in + u) * C];
+                w[u] = Tm[static_cast<size_t>(4 * b + u) * C];
+                w[4 + u] = Wm[static_cast<size_t>(4 * b + u) * C];
             }
+        };
+        auto use = [&](int b, const float (&w)[8]) {
+            const int in = 4 * b;
 #pragma unroll
             for (int n = 0; n < NB; ++n) {
                 const float4 xv = *reinterpret_cast<const float4*>(s_xs + n * T + in);
                 const float4 mv = *reinterpret_cast<const float4*>(s_m1 + n * T + in);
                 float h = h2[n];
-                h = fmaf(t4[0], xv.x, h);
-                h = fmaf(t4[1], xv.y, h);
-                h = fmaf(t4[2], xv.z, h);
-                h = fmaf(t4[3], xv.w, h);
-                h = fmaf(w4[0], mv.x, h);
-                h = fmaf(w4[1], mv.y, h);
-                h = fmaf(w4[2], mv.z, h);
-                h = fmaf(w4[3], mv.w, h);
+                h = fmaf(w[0], xv.x, h);
+                h = fmaf(w[1], xv.y, h);
+                h = fmaf(w[2], xv.z, h);
+                h = fmaf(w[3], xv.w, h);
+                h = fmaf(w[4], mv.x, h);
+                h = fmaf(w[5], mv.y, h);
+                h = fmaf(w[6], mv.z, h);
+                h = fmaf(w[7], mv.w, h);
                 h2[n] = h;
             }
-        }
+        };
+        auto tail = [&](int b) {
+            float w[8];
+            load(b, w);
+            use(b, w);
+        };
+        stream_blocks<8>(C / 4, load, use, tail);
 #pragma unroll
         for (int n = 0; n < NB; ++n) s_h2[n * T + k] = h2[n];
+    }
+    __shared__ float s_e1[kMaxWavesReadout][NB];
+    {
+        const float qk = ok ? a.q[k] : 0.0f;
+        const int wv = threadIdx.x >> 6;
+#pragma unroll
+        for (int n = 0; n < NB; ++n) {
+            const float e = wave_sum_lane63(ok ? qk * s_xs[n * T + k] : 0.0f);
+            if ((threadIdx.x & 63) == 63) s_e1[wv][n] = e;
+        }
     }
     __syncthreads();
 
@@ -445,7 +495,27 @@ __global__ void __launch_bounds__(256) readout_kernel(ReadoutArgs a)
         const float* w1 = a.W1 + static_cast<size_t>(h) * C;
         const float* hn = s_h2 + n * T;
         float z = 0.0f;
-        for (int c = 0; c < C; ++c) z = fmaf(w1[c], hn[c], z);
+        // the weight row streamed in blocks of 4 (C is a multiple of 4)
+        auto load = [&](int b, float (&w)[4]) {
+            const float4 v = *reinterpret_cast<const float4*>(w1 + 4 * b);
+            w[0] = v.x;
+            w[1] = v.y;
+            w[2] = v.z;
+            w[3] = v.w;
+        };
+        auto use = [&](int b, const float (&w)[4]) {
+            const float4 hv = *reinterpret_cast<const float4*>(hn + 4 * b);
+            z = fmaf(w[0], hv.x, z);
+            z = fmaf(w[1], hv.y, z);
+            z = fmaf(w[2], hv.z, z);
+            z = fmaf(w[3], hv.w, z);
+        };
+        auto tail = [&](int b) {
+            float w[4];
+            load(b, w);
+            use(b, w);
+        };
+        stream_blocks<4>(C / 4, load, use, tail);
         const float sig = 1.0f / (1.0f + expf(-z));
         const float act = a.scale * z * sig;
         const float dact = a.scale * sig + a.scale * z * sig * (1.0f - sig);
@@ -459,7 +529,7 @@ __global__ void __launch_bounds__(256) readout_kernel(ReadoutArgs a)
         const int n = threadIdx.x;
         const int i = a.nodes.order[blk.start + n];
         float e1 = 0.0f;
-        for (int c = 0; c < C; ++c) e1 = fmaf(a.q[c], s_xs[n * T + c], e1);
+        for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) e1 += s_e1[w][n];
         float e2 = 0.0f;
         for (int h = 0; h < H; ++h) e2 += s_act[n * kMaxHidden + h];
         a.energies[i] = a.E0[blk.type] + static_cast<double>(e1) + static_cast<double>(e2);
@@ -490,26 +560,34 @@ __global__ void __launch_bounds__(256) readout_kernel(ReadoutArgs a)
         for (int n = 0; n < NB; ++n) d[n] = qk;
         const float* Tt = a.H2M0T + static_cast<size_t>(blk.type) * C * C + k;
         const float* Wt = a.H2M1T + k;
-        for (int o = 0; o < C; o += 4) {
-            float t4[4], w4[4];
+        auto load = [&](int b, float (&w)[8]) {
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                t4[u] = Tt[static_cast<size_t>(o + u) * C];
-                w4[u] = Wt[static_cast<size_t>(o + u) * C];
+                w[u] = Tt[static_cast<size_t>(4 * b + u) * C];
+                w[4 + u] = Wt[static_cast<size_t>(4 * b + u) * C];
             }
+        };
+        auto use = [&](int b, const float (&w)[8]) {
+            const int o = 4 * b;
 #pragma unroll
             for (int n = 0; n < NB; ++n) {
                 const float4 gv = *reinterpret_cast<const float4*>(s_h2 + n * T + o);
-                d[n] = fmaf(t4[0], gv.x, d[n]);
-                d[n] = fmaf(t4[1], gv.y, d[n]);
-                d[n] = fmaf(t4[2], gv.z, d[n]);
-                d[n] = fmaf(t4[3], gv.w, d[n]);
-                m1adj[n] = fmaf(w4[0], gv.x, m1adj[n]);
-                m1adj[n] = fmaf(w4[1], gv.y, m1adj[n]);
-                m1adj[n] = fmaf(w4[2], gv.z, m1adj[n]);
-                m1adj[n] = fmaf(w4[3], gv.w, m1adj[n]);
+                d[n] = fmaf(w[0], gv.x, d[n]);
+                d[n] = fmaf(w[1], gv.y, d[n]);
+                d[n] = fmaf(w[2], gv.z, d[n]);
+                d[n] = fmaf(w[3], gv.w, d[n]);
+                m1adj[n] = fmaf(w[4], gv.x, m1adj[n]);
+                m1adj[n] = fmaf(w[5], gv.y, m1adj[n]);
+                m1adj[n] = fmaf(w[6], gv.z, m1adj[n]);
+                m1adj[n] = fmaf(w[7], gv.w, m1adj[n]);
             }
-        }
+        };
+        auto tail = [&](int b) {
+            float w[8];
+            load(b, w);
+            use(b, w);
+        };
+        stream_blocks<8>(C / 4, load, use, tail);
 #pragma unroll
         for (int n = 0; n < NB; ++n)
             if (node[n] >= 0) a.direct[static_cast<size_t>(node[n]) * C + k] = d[n];
