@@ -340,9 +340,9 @@ __global__ void __launch_bounds__(256) m0_reverse_kernel(LayerArgs a, PolyArgs p
 //      M1_adj[n][k] = sum_o W[k][o] H2_adj[n][o]
 //   6. A1_adj[n][lm][k] = M1_adj[n][k] dP1/dA1[lm]
 // ---------------------------------------------------------------------------
-// Weight streaming of the readout's matrix-vector phases.  A phase reads
-// W[in][k] (in = 0..n_in-1, column k of the thread) for blocks of kStreamW
-// inputs; the blocks pass through a ring of kStreamRing register buffers so
+// Weight streaming of the readout's matrix-vector phases.  A phase reads its
+// weights (column k of the thread, or one row) in blocks of W floats; the
+// blocks pass through a ring of kStreamRing register buffers so
 // the loads of the next kStreamRing - 1 blocks are in flight while one block
 // is consumed (waiting on each block's loads in turn would put one memory
 // round trip per block on the critical path).  `load(b, buf)` fills buf with
