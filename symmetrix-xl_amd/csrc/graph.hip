@@ -67,15 +67,23 @@ __global__ void fill_bins_kernel(int n, const int* __restrict__ atom_bins, int* 
     bin_atoms[index] = atom;
 }
 
-__global__ void edges_kernel(NeighborPlan p, const double* __restrict__ wp,
-                             const double* __restrict__ wf, const int* __restrict__ wrap,
-                             const int* __restrict__ atom_bins, const int* __restrict__ bin_offsets,
-                             const int* __restrict__ bin_atoms, const long long* __restrict__ offsets,
-                             long long* __restrict__ counts, int* __restrict__ sources,
-                             int* __restrict__ shifts, double* __restrict__ frac)
+// One wave per receiver: the stencil cells are visited in order
+// (dz -> dy -> dx), the atoms of a cell are tested 64 at a time, and the
+// accepted ones are placed by ballot and lane prefix count, so every
+// receiver's edges come out in the same order as one thread walking the
+// cells and their (sorted) atoms one by one.  The count pass (offsets null)
+// stores the number of edges; the fill pass writes them.
+constexpr int kEdgeThreads = 256;
+
+__global__ void __launch_bounds__(kEdgeThreads) edges_kernel(
+    NeighborPlan p, const double* __restrict__ wp, const double* __restrict__ wf, const int* __restrict__ wrap,
+    const int* __restrict__ atom_bins, const int* __restrict__ bin_offsets, const int* __restrict__ bin_atoms,
+    const long long* __restrict__ offsets, long long* __restrict__ counts, int* __restrict__ sources,
+    int* __restrict__ shifts, double* __restrict__ frac)
 {
-    const int receiver = blockIdx.x * blockDim.x + threadIdx.x;
-    if (receiver >= p.num_nodes) return;
+    const int lane = threadIdx.x & 63;
+    const int receiver = blockIdx.x * (kEdgeThreads / 64) + (threadIdx.x >> 6);
+    if (receiver >= p.num_nodes) return;  // whole wave
     const bool fill = offsets != nullptr;
     const int bx = p.bins[0], by = p.bins[1], bz = p.bins[2];
     const int receiver_bin = atom_bins[receiver];
@@ -102,19 +110,29 @@ __global__ void edges_kernel(NeighborPlan p, const double* __restrict__ wp,
                 const int source_bin = static_cast<int>(
                     (static_cast<size_t>(source_z) * by + source_y) * bx + source_x);
                 const int image[3] = {shift_x, shift_y, shift_z};
-                for (int index = bin_offsets[source_bin]; index < bin_offsets[source_bin + 1]; ++index) {
-                    const int source = bin_atoms[index];
-                    if (source == receiver && shift_x == 0 && shift_y == 0 && shift_z == 0) continue;
-                    double distance_squared = 0.0;
-                    for (int component = 0; component < 3; ++component) {
-                        double displacement = wp[3 * static_cast<size_t>(source) + component] - rp[component];
-                        for (int axis = 0; axis < 3; ++axis)
-                            displacement += image[axis] * p.cell[3 * axis + component];
-                        distance_squared += displacement * displacement;
+                const int b0 = bin_offsets[source_bin], b1 = bin_offsets[source_bin + 1];
+                for (int base = b0; base < b1; base += 64) {
+                    const int index = base + lane;
+                    bool accept = false;
+                    int source = 0;
+                    if (index < b1) {
+                        source = bin_atoms[index];
+                        if (!(source == receiver && shift_x == 0 && shift_y == 0 && shift_z == 0)) {
+                            double distance_squared = 0.0;
+                            for (int component = 0; component < 3; ++component) {
+                                double displacement = wp[3 * static_cast<size_t>(source) + component] - rp[component];
+                                for (int axis = 0; axis < 3; ++axis)
+                                    displacement += image[axis] * p.cell[3 * axis + component];
+                                distance_squared += displacement * displacement;
+                            }
+                            accept = !(distance_squared > p.cutoff_squared);
+                        }
                     }
-                    if (distance_squared > p.cutoff_squared) continue;
-                    if (fill) {
-                        const size_t edge = static_cast<size_t>(out0 + local);
+                    const unsigned long long mask = __ballot(accept);
+                    if (fill && accept) {
+                        const int rank = __builtin_amdgcn_mbcnt_hi(
+                            static_cast<unsigned>(mask >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<unsigned>(mask), 0));
+                        const size_t edge = static_cast<size_t>(out0 + local + rank);
                         sources[edge] = source;
                         for (int axis = 0; axis < 3; ++axis) {
                             shifts[3 * edge + axis] = image[axis] - wrap[3 * static_cast<size_t>(source) + axis] +
@@ -123,12 +141,12 @@ __global__ void edges_kernel(NeighborPlan p, const double* __restrict__ wp,
                                                     wf[3 * static_cast<size_t>(receiver) + axis] + image[axis];
                         }
                     }
-                    ++local;
+                    local += __popcll(mask);
                 }
             }
         }
     }
-    if (!fill) counts[receiver] = local;
+    if (!fill && lane == 0) counts[receiver] = local;
 }
 
 // ---- scans ---------------------------------------------------------------
@@ -253,20 +271,50 @@ __global__ void transpose_fill_kernel(int E, const int* __restrict__ source, con
     tedge[tfirst[s] + slot] = e;
 }
 
-// insertion sort of each segment (ascending): makes atomic fill orders canonical
-__global__ void sort_segments_kernel(int nseg, const int* __restrict__ offsets, int* __restrict__ values)
+// Ascending sort of each segment: makes atomic fill orders canonical.  One
+// wave per segment: the segment is staged in LDS and every element is
+// written at its rank (the number of smaller elements, ties by position), so
+// the result is the stable ascending order.  A segment longer than the LDS
+// stage is sorted in place by lane 0 (insertion sort).
+constexpr int kSortThreads = 256;
+constexpr int kSortStage = 1024;  // elements staged per wave
+
+__global__ void __launch_bounds__(kSortThreads) sort_segments_kernel(int nseg, const int* __restrict__ offsets,
+                                                                     int* __restrict__ values)
 {
-    const int sgm = blockIdx.x * blockDim.x + threadIdx.x;
-    if (sgm >= nseg) return;
+    __shared__ int stage[kSortThreads / 64][kSortStage];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int sgm = blockIdx.x * (kSortThreads / 64) + wave;
+    if (sgm >= nseg) return;  // whole wave: no block barrier follows
     const int begin = offsets[sgm], end = offsets[sgm + 1];
-    for (int index = begin + 1; index < end; ++index) {
-        const int v = values[index];
-        int ins = index;
-        while (ins > begin && values[ins - 1] > v) {
-            values[ins] = values[ins - 1];
-            --ins;
+    const int n = end - begin;
+    if (n <= 1) return;
+    if (n > kSortStage) {
+        if (lane == 0) {
+            for (int index = begin + 1; index < end; ++index) {
+                const int v = values[index];
+                int ins = index;
+                while (ins > begin && values[ins - 1] > v) {
+                    values[ins] = values[ins - 1];
+                    --ins;
+                }
+                values[ins] = v;
+            }
         }
-        values[ins] = v;
+        return;
+    }
+    int* st = stage[wave];
+    for (int i = lane; i < n; i += 64) st[i] = values[begin + i];
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    for (int i = lane; i < n; i += 64) {
+        const int v = st[i];
+        int rank = 0;
+        for (int j = 0; j < n; ++j) {
+            const int u = st[j];
+            rank += (u < v || (u == v && j < i)) ? 1 : 0;
+        }
+        values[begin + rank] = v;
     }
 }
 
@@ -411,7 +459,8 @@ hipError_t launch_neighbor_edges(const NeighborPlan& p, const double* wrapped_po
                                  int* shifts, double* fractional_xyz, hipStream_t s)
 {
     if (p.num_nodes <= 0) return hipSuccess;
-    edges_kernel<<<(p.num_nodes + 127) / 128, 128, 0, s>>>(
+    constexpr int per_block = kEdgeThreads / 64;
+    edges_kernel<<<(p.num_nodes + per_block - 1) / per_block, kEdgeThreads, 0, s>>>(
         p, wrapped_positions, wrapped_fractional, wrap_shifts, atom_bins, bin_offsets, bin_atoms,
         edge_offsets, edge_counts, sources, shifts, fractional_xyz);
     return hipGetLastError();
@@ -464,7 +513,9 @@ hipError_t launch_transpose_fill(int num_edges, const int* source, const int* tf
 hipError_t launch_sort_segments(int num_segments, const int* offsets, int* values, hipStream_t s)
 {
     if (num_segments <= 0) return hipSuccess;
-    sort_segments_kernel<<<(num_segments + 127) / 128, 128, 0, s>>>(num_segments, offsets, values);
+    constexpr int per_block = kSortThreads / 64;
+    sort_segments_kernel<<<(num_segments + per_block - 1) / per_block, kSortThreads, 0, s>>>(num_segments,
+                                                                                           offsets, values);
     return hipGetLastError();
 }
 
