@@ -170,3 +170,30 @@ def test_fused_totals_and_displacement_match_separate_calls(tiny):
     # an evaluation from edge vectors has no displacement of its own
     gi = ev._periodic_graph_arrays(gen)
     assert gi["num_neigh"].sum() == ev._graph_size()[1]
+
+
+def test_long_neighbour_cutoff_gives_the_same_results(tiny):
+    """A neighbour cutoff far beyond r_cut (sources with more than 1,024
+    edges, beyond what the device sort stages per segment) changes the graph
+    but not the physics: energies, forces and stress agree with the graph at
+    r_cut + skin."""
+    from symmetrix_amd import MACEKokkosFloat, synthetic
+
+    path, model = tiny
+    s = synthetic.srtio3_supercell(5, sigma=0.05, seed=16)
+    types = synthetic.node_types(s, model["atomic_numbers"])
+    inv = np.linalg.inv(s.cell)
+    out = []
+    for cutoff in (model["r_cut"] + 0.5, 15.0):
+        ev = MACEKokkosFloat(path)
+        info = ev._prepare_periodic_factorized_graph(types, s.positions, s.cell, inv, cutoff)
+        gen = info["generation"]
+        ev._compute_prepared_factorized_positions(gen, s.positions)
+        out.append((info["num_edges"], ev._total_energy(gen), ev._reduce_atom_forces(len(s), None, None, gen),
+                    ev._reduce_stress(s.volume, None, gen)))
+    (e0, E0, F0, S0), (e1, E1, F1, S1) = out
+    print(f"  edges {e0} -> {e1} ({e1 / len(s):.0f} per atom)", flush=True)
+    assert e1 / len(s) > 1024
+    assert abs(E1 - E0) / len(s) < E_TOL
+    np.testing.assert_allclose(F1, F0, atol=F_TOL)
+    np.testing.assert_allclose(S1, S0, atol=S_TOL)

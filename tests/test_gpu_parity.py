@@ -107,7 +107,7 @@ def test_neighbor_graph_rejects_invalid_inputs(native):
         periodic_neighbor_graph(np.zeros((1, 3)), cell, np.zeros((3, 3)), 1.0)
 
 
-@pytest.mark.parametrize("case", ["srtio3", "triclinic", "small_cell"])
+@pytest.mark.parametrize("case", ["srtio3", "triclinic", "small_cell", "one_bin"])
 def test_neighbor_graph_bit_exact_vs_oracle(native, oracle_lib, case):
     from symmetrix_amd import periodic_neighbor_graph, synthetic
 
@@ -115,6 +115,11 @@ def test_neighbor_graph_bit_exact_vs_oracle(native, oracle_lib, case):
     if case == "srtio3":
         s = synthetic.srtio3_supercell(4, sigma=0.05, seed=3)
         pos, cell, cutoff = s.positions, s.cell, 6.5
+    elif case == "one_bin":
+        # a cutoff above half the cell: one bin holding all 1,080 atoms, more
+        # than the device sort stages per segment
+        s = synthetic.srtio3_supercell(6, sigma=0.05, seed=4)
+        pos, cell, cutoff = s.positions, s.cell, 12.0
     elif case == "triclinic":
         cell = np.array([[9.2, 0.0, 0.0], [1.7, 8.1, 0.0], [-0.9, 1.3, 10.3]])
         pos = rng.uniform(-2.0, 12.0, size=(200, 3))  # includes atoms outside the cell
