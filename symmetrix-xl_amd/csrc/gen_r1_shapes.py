@@ -22,8 +22,12 @@ SHAPES = [(2, 1), (3, 1), (3, 2)]
 # one pass run the second-interaction reverse in passes over disjoint path
 # groups by source l2: each pass owns its message rows and edge forces add up
 # over passes.  (Forward passes by output l were measured slower on the wide
-# shape than one pass: every extra sweep re-reads the source features.)
-REV_GROUPS = {(3, 2): [[0], [1], [2]]}
+# shape than one pass: every extra sweep re-reads the source features.)  The
+# wide shape runs two passes, source l2 in {0, 1} and {2}: 219 VGPRs without
+# spills at two waves per SIMD; one pass spills, three repeat more per-edge
+# work.  Passes only pay where one pass does not fit: the medium shape split
+# in two (164 VGPRs, three waves per SIMD) was measured 33 % slower.
+REV_GROUPS = {(3, 2): [[0, 1], [2]]}
 FACTORED_MAX_TRIPLES = 64
 
 

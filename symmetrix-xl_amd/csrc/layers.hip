@@ -1260,8 +1260,8 @@ hipError_t launch_r1_forward(const LayerArgs& a, const float* r1, const float* c
     return hipGetLastError();
 }
 
-// the (3, 2) reverse runs passes 0, 1, 2: the generated source-l2 groups
-static_assert(R1Groups<3, 2>::NREV == 3, "reverse pass list out of date");
+// the (3, 2) reverse runs passes 0 and 1: the generated source-l2 groups
+static_assert(R1Groups<3, 2>::NREV == 2, "reverse pass list out of date");
 
 hipError_t launch_r1_reverse(const LayerArgs& a, const float* r1, const float* cg, const float* H1,
                              const float* dPhi1, double* forces, float* msg, hipStream_t s)
@@ -1276,8 +1276,8 @@ hipError_t launch_r1_reverse(const LayerArgs& a, const float* r1, const float* c
         r1_reverse_kernel<R1Shape<3, 1>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, dPhi1,
                                                                           forces, msg);
     else if (a.l_max == 3 && a.L_max == 2)
-        r1_reverse_grouped_kernel<R1Shape<3, 2>, 0, 1, 2><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, dPhi1,
-                                                                                          forces, msg);
+        r1_reverse_grouped_kernel<R1Shape<3, 2>, 0, 1><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, dPhi1,
+                                                                                       forces, msg);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
