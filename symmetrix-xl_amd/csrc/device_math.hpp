@@ -182,18 +182,30 @@ __device__ __forceinline__ float wave_sum_dpp(float v)
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
-// The same reduction left in the lanes: lanes 48..63 (in particular lane 63)
-// hold the wave sum, the other lanes partial sums.  For a sum that only one
-// lane stores, this saves the broadcast.
-__device__ __forceinline__ float wave_sum_lane63(float v)
+// Partial wave sums for values the caller stores and adds up itself.  With
+// PARTS = 4 the reduction stops within rows of 16 lanes (lanes 15, 31, 47 and
+// 63 hold the four row sums); with PARTS = 2 one row broadcast follows (lanes
+// 31 and 63 hold the sums of lanes 0..31 and 32..63); with PARTS = 1 lane 63
+// holds the wave sum.  The row broadcasts carry a row mask, so each costs a
+// zeroed register, a move and an add: stopping early saves them.
+template <int PARTS>
+__device__ __forceinline__ float partial_sum_dpp(float v)
 {
+    static_assert(PARTS == 1 || PARTS == 2 || PARTS == 4, "1, 2 or 4 partial sums per wave");
     v += dpp_moved<0xb1>(v);
     v += dpp_moved<0x4e>(v);
     v += dpp_moved<0x141>(v);
     v += dpp_moved<0x140>(v);
-    v += dpp_moved<0x142, 0xa>(v);
-    v += dpp_moved<0x143, 0xc>(v);
+    if constexpr (PARTS <= 2) v += dpp_moved<0x142, 0xa>(v);
+    if constexpr (PARTS == 1) v += dpp_moved<0x143, 0xc>(v);
     return v;
+}
+
+// The lane that holds partial `lane / (64 / PARTS)` of partial_sum_dpp.
+template <int PARTS>
+__device__ __forceinline__ bool holds_partial(int lane)
+{
+    return (lane & (64 / PARTS - 1)) == 64 / PARTS - 1;
 }
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }

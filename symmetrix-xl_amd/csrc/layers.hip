@@ -28,6 +28,14 @@ namespace sxl {
 namespace {
 
 constexpr int kMaxWaves = 4;  // 256 threads
+// partial sums per wave of an edge force component, stored in LDS and added
+// in double by the edge's thread (fewer DPP steps than a full reduction; the
+// layer-0 reverse keeps two to fit three workgroups' LDS per CU at 3 waves)
+constexpr int kForceParts = 4;
+constexpr int kForcePartsA0 = 2;
+// the path-group passes add into their partials once per pass: one per wave
+// (measured: four per wave made the wide shape's reverse 1 % slower)
+constexpr int kForcePartsGrouped = 1;
 
 // l of each harmonic index lm (lm = l^2 .. l^2 + 2l), l <= 3
 constexpr int kLmL[16] = {0, 1, 1, 1, 2, 2, 2, 2, 2, 3, 3, 3, 3, 3, 3, 3};
@@ -416,7 +424,7 @@ r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
     __shared__ int s_row[kTile];
     __shared__ int s_src[kTile];
     __shared__ int s_eid[kTile];
-    __shared__ float s_f[kTile][kMaxWaves][3];
+    __shared__ float s_f[kTile][kMaxWaves * kForceParts][3];
     __shared__ float s_dsc[kTile];  // A1 density-scale force coefficient per active slot
     __shared__ int s_count;
 
@@ -552,13 +560,15 @@ r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
                 gy = fmaf(s_dY[j][1][lm], U[lm], gy);
                 gz = fmaf(s_dY[j][2][lm], U[lm], gz);
             }
-            const float fx = wave_sum_lane63(-fmaf(s_geo[j][0], A, gx));
-            const float fy = wave_sum_lane63(-fmaf(s_geo[j][1], A, gy));
-            const float fz = wave_sum_lane63(-fmaf(s_geo[j][2], A, gz));
-            if (lane == 63) {
-                s_f[j][wave][0] = fx;
-                s_f[j][wave][1] = fy;
-                s_f[j][wave][2] = fz;
+            // partial sums of +dE/dxyz; the edge's thread negates their total
+            const float fx = partial_sum_dpp<kForceParts>(fmaf(s_geo[j][0], A, gx));
+            const float fy = partial_sum_dpp<kForceParts>(fmaf(s_geo[j][1], A, gy));
+            const float fz = partial_sum_dpp<kForceParts>(fmaf(s_geo[j][2], A, gz));
+            if (holds_partial<kForceParts>(lane)) {
+                const int part = wave * kForceParts + lane / (64 / kForceParts);
+                s_f[j][part][0] = fx;
+                s_f[j][part][1] = fy;
+                s_f[j][part][2] = fz;
             }
         };
         // Two row buffers used in turn (unrolled by two, so no register
@@ -580,11 +590,11 @@ r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
         if (threadIdx.x < count) {
             const int t = threadIdx.x;
             double f[3] = {0.0, 0.0, 0.0};
-            for (int w = 0; w < nwaves; ++w)
+            for (int w = 0; w < nwaves * kForceParts; ++w)
                 for (int c = 0; c < 3; ++c) f[c] += static_cast<double>(s_f[t][w][c]);
             double* out = forces + 3 * static_cast<size_t>(s_eid[t]);
 #pragma unroll
-            for (int c = 0; c < 3; ++c) out[c] = f[c] + static_cast<double>(s_dsc[t] * s_geo[t][c]);
+            for (int c = 0; c < 3; ++c) out[c] = -f[c] + static_cast<double>(s_dsc[t] * s_geo[t][c]);
         }
     }
 }
@@ -608,7 +618,7 @@ struct RevTileLds {
     int row[kTile];
     int src[kTile];
     int eid[kTile];
-    float f[kTile][kMaxWaves][3];
+    float f[kTile][kMaxWaves * kForcePartsGrouped][3];
     float dsc[kTile];
     int count;
 };
@@ -729,13 +739,14 @@ __device__ __forceinline__ void r1_reverse_pass(const LayerArgs& a, int i, bool 
             gy = fmaf(L.dY[j][1][lm], U[lm], gy);
             gz = fmaf(L.dY[j][2][lm], U[lm], gz);
         }
-        const float fx = wave_sum_lane63(-fmaf(L.geo[j][0], A, gx));
-        const float fy = wave_sum_lane63(-fmaf(L.geo[j][1], A, gy));
-        const float fz = wave_sum_lane63(-fmaf(L.geo[j][2], A, gz));
-        if (lane == 63) {
-            L.f[j][wave][0] = first ? fx : L.f[j][wave][0] + fx;
-            L.f[j][wave][1] = first ? fy : L.f[j][wave][1] + fy;
-            L.f[j][wave][2] = first ? fz : L.f[j][wave][2] + fz;
+        const float fx = partial_sum_dpp<kForcePartsGrouped>(fmaf(L.geo[j][0], A, gx));
+        const float fy = partial_sum_dpp<kForcePartsGrouped>(fmaf(L.geo[j][1], A, gy));
+        const float fz = partial_sum_dpp<kForcePartsGrouped>(fmaf(L.geo[j][2], A, gz));
+        if (holds_partial<kForcePartsGrouped>(lane)) {
+            const int part = wave * kForcePartsGrouped + lane / (64 / kForcePartsGrouped);
+            L.f[j][part][0] = first ? fx : L.f[j][part][0] + fx;
+            L.f[j][part][1] = first ? fy : L.f[j][part][1] + fy;
+            L.f[j][part][2] = first ? fz : L.f[j][part][2] + fz;
         }
     }
 }
@@ -799,11 +810,11 @@ __global__ void __launch_bounds__(256) r1_reverse_grouped_kernel(LayerArgs a, co
         if (threadIdx.x < count) {
             const int t = threadIdx.x;
             double f[3] = {0.0, 0.0, 0.0};
-            for (int w = 0; w < nwaves; ++w)
+            for (int w = 0; w < nwaves * kForcePartsGrouped; ++w)
                 for (int c = 0; c < 3; ++c) f[c] += static_cast<double>(L.f[t][w][c]);
             double* out = forces + 3 * static_cast<size_t>(L.eid[t]);
 #pragma unroll
-            for (int c = 0; c < 3; ++c) out[c] = f[c] + static_cast<double>(L.dsc[t] * L.geo[t][c]);
+            for (int c = 0; c < 3; ++c) out[c] = -f[c] + static_cast<double>(L.dsc[t] * L.geo[t][c]);
         }
     }
 }
@@ -824,7 +835,7 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
     __shared__ float s_geo[kTile][4];
     __shared__ int s_row[kTile];
     __shared__ int s_eid[kTile];
-    __shared__ float s_f[kTile][kMaxWaves][3];
+    __shared__ float s_f[kTile][kMaxWaves * kForcePartsA0][3];
     __shared__ float s_dsc[kTile];  // A0 density-scale force coefficient per active slot
     __shared__ int s_count;
 
@@ -927,13 +938,14 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
                 gy = fmaf(R, ay[l], gy);
                 gz = fmaf(R, az[l], gz);
             }
-            const float fx = wave_sum_lane63(-fmaf(s_geo[j][0], A, gx));
-            const float fy = wave_sum_lane63(-fmaf(s_geo[j][1], A, gy));
-            const float fz = wave_sum_lane63(-fmaf(s_geo[j][2], A, gz));
-            if (lane == 63) {
-                s_f[j][wave][0] = fx;
-                s_f[j][wave][1] = fy;
-                s_f[j][wave][2] = fz;
+            const float fx = partial_sum_dpp<kForcePartsA0>(fmaf(s_geo[j][0], A, gx));
+            const float fy = partial_sum_dpp<kForcePartsA0>(fmaf(s_geo[j][1], A, gy));
+            const float fz = partial_sum_dpp<kForcePartsA0>(fmaf(s_geo[j][2], A, gz));
+            if (holds_partial<kForcePartsA0>(lane)) {
+                const int part = wave * kForcePartsA0 + lane / (64 / kForcePartsA0);
+                s_f[j][part][0] = fx;
+                s_f[j][part][1] = fy;
+                s_f[j][part][2] = fz;
             }
         };
         float4v ring[kDepth][NL];
@@ -942,11 +954,11 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
         if (threadIdx.x < count) {
             const int t = threadIdx.x;
             double f[3] = {0.0, 0.0, 0.0};
-            for (int w = 0; w < nwaves; ++w)
+            for (int w = 0; w < nwaves * kForcePartsA0; ++w)
                 for (int c = 0; c < 3; ++c) f[c] += static_cast<double>(s_f[t][w][c]);
             double* out = forces + 3 * static_cast<size_t>(s_eid[t]);
 #pragma unroll
-            for (int c = 0; c < 3; ++c) out[c] += f[c] + static_cast<double>(s_dsc[t] * s_geo[t][c]);
+            for (int c = 0; c < 3; ++c) out[c] += -f[c] + static_cast<double>(s_dsc[t] * s_geo[t][c]);
         }
     }
 }

@@ -483,7 +483,7 @@ __global__ void __launch_bounds__(256) readout_kernel(ReadoutArgs a)
         const int wv = threadIdx.x >> 6;
 #pragma unroll
         for (int n = 0; n < NB; ++n) {
-            const float e = wave_sum_lane63(ok ? qk * s_xs[n * T + k] : 0.0f);
+            const float e = partial_sum_dpp<1>(ok ? qk * s_xs[n * T + k] : 0.0f);
             if ((threadIdx.x & 63) == 63) s_e1[wv][n] = e;
         }
     }
