@@ -23,10 +23,18 @@ namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int kBM = 64, kBN = 128, kBK = 32, kPad = 4;
+constexpr int kBN = 128, kBK = 32, kPad = 4;
 
+// kBM output rows per tile: 64 (four waves as 2 x 2, each 32 x 64: two MFMA
+// blocks) or, for launches too small to fill the chip, 32 (four waves side by
+// side, each 32 x 32: one block), which doubles the workgroups and halves
+// each one's chain of K slices.
+template <int kBM>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 5))) gemm_group_kernel(GemmGroup grp)
 {
+    constexpr int kWN = kBM == 64 ? 2 : 4;       // waves along N
+    constexpr int kNB = kBN / kWN / 32;          // 32 x 32 MFMA blocks per wave along N
+    static_assert(kBM == 64 || kBM == 32, "64- or 32-row tiles");
     __shared__ float As[kBM][kBK + kPad];
     __shared__ float Bs[kBN][kBK + kPad];
     const int b = blockIdx.x;
@@ -41,7 +49,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 5))
     const int col0 = (local / tiles_m) * kBN;
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / kWN, wn = wave % kWN;
 
     // global -> register staging: kBK / 4 threads per row (one float4 each),
     // kRowsPerPass rows per pass; A takes kAPasses passes, Bt kBPasses
@@ -75,9 +83,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 5))
             rb[j] = brow[j] ? *reinterpret_cast<const float4*>(brow[j] + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
     };
 
-    floatx16 acc[2];
+    floatx16 acc[kNB];
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < kNB; ++j)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[j][v] = 0.0f;
 
@@ -95,8 +103,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 5))
         for (int c = 0; c < kBK; c += 8) {
             const float4 a4 = *reinterpret_cast<const float4*>(&As[arow_l][c + kh]);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const float4 b4 = *reinterpret_cast<const float4*>(&Bs[wn * 64 + j * 32 + (lane & 31)][c + kh]);
+            for (int j = 0; j < kNB; ++j) {
+                const float4 b4 = *reinterpret_cast<const float4*>(&Bs[wn * (kBN / kWN) + j * 32 + (lane & 31)][c + kh]);
                 acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.x, b4.x, acc[j], 0, 0, 0);
                 acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.y, b4.y, acc[j], 0, 0, 0);
                 acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.z, b4.z, acc[j], 0, 0, 0);
@@ -106,8 +114,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 5))
         __syncthreads();
     }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int col = col0 + wn * 64 + j * 32 + (lane & 31);
+    for (int j = 0; j < kNB; ++j) {
+        const int col = col0 + wn * (kBN / kWN) + j * 32 + (lane & 31);
         if (col >= N) continue;
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
@@ -132,7 +140,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 5))
 hipError_t launch_gemm_group(GemmGroup grp, hipStream_t stream)
 {
     if (grp.count < 0 || grp.count > kMaxGemmGroup) return hipErrorInvalidValue;
-    int tiles = 0;
     int kept = 0;
     for (int i = 0; i < grp.count; ++i) {
         const GemmArgs& g = grp.g[i];
@@ -143,15 +150,29 @@ hipError_t launch_gemm_group(GemmGroup grp, hipStream_t stream)
         if (g.a.node_stride % 4 != 0 || g.a.row_stride % 4 != 0 ||
             reinterpret_cast<std::uintptr_t>(g.a.ptr) % 16 != 0 || reinterpret_cast<std::uintptr_t>(g.Bt) % 16 != 0)
             return hipErrorInvalidValue;
-        grp.g[kept] = g;
-        grp.tile_start[kept] = tiles;
-        tiles += static_cast<int>(((M + kBM - 1) / kBM) * ((g.Ncols + kBN - 1) / kBN));
-        ++kept;
+        grp.g[kept++] = g;
     }
     grp.count = kept;
-    grp.tile_start[kept] = tiles;
+    auto number_tiles = [&](int bm) {
+        int tiles = 0;
+        for (int i = 0; i < kept; ++i) {
+            const long long M = static_cast<long long>(grp.g[i].nodes) * grp.g[i].rows_per_node;
+            grp.tile_start[i] = tiles;
+            tiles += static_cast<int>(((M + bm - 1) / bm) * ((grp.g[i].Ncols + kBN - 1) / kBN));
+        }
+        grp.tile_start[kept] = tiles;
+        return tiles;
+    };
+    // 64-row tiles unless they leave most compute units with at most one
+    // workgroup (256 CUs, five resident per CU)
+    int tiles = number_tiles(64);
     if (tiles == 0) return hipSuccess;
-    gemm_group_kernel<<<tiles, 256, 0, stream>>>(grp);
+    if (tiles < 2 * 256) {
+        tiles = number_tiles(32);
+        gemm_group_kernel<32><<<tiles, 256, 0, stream>>>(grp);
+    } else {
+        gemm_group_kernel<64><<<tiles, 256, 0, stream>>>(grp);
+    }
     return hipGetLastError();
 }
 
