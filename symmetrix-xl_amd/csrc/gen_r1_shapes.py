@@ -178,7 +178,8 @@ def emit_groups(lmax, Lmax, paths, terms):
     return "\n".join(out)
 
 
-def main():
+def render():
+    """The text of r1_shapes.inc."""
     out = [
         "// Generated by gen_r1_shapes.py -- do not edit.",
         "// Path lists and CG sparsity of the second interaction for the",
@@ -199,9 +200,13 @@ def main():
     ]
     for lmax, Lmax in SHAPES:
         out.append(emit_shape(lmax, Lmax))
+    return "\n".join(out)
+
+
+def main():
     path = os.path.join(HERE, "r1_shapes.inc")
     with open(path, "w") as f:
-        f.write("\n".join(out))
+        f.write(render())
     print(path)
 
 
