@@ -24,7 +24,9 @@
 // Splines: cubic Hermite coefficients (formed in double, stored in Precision,
 //   as the device path's tables, mace_kokkos_factorized_lifecycle.cpp:4002-4013)
 //   and evaluation point (cubic_spline_set.cpp:32-78).
-// Polynomials: evaluate_gradient_simple (multivariate_polynomial.cpp:326-355).
+// Polynomials: evaluate_gradient_simple (multivariate_polynomial.cpp:326-355)
+//   over each output's terms as the constructor stores them: a repeated
+//   monomial keeps its first coefficient (multivariate_polynomial.cpp:36-46).
 // Readout MLP: evaluate_gradient (multilayer_perceptron.cpp:85-160).
 // Harmonics: closed-form real harmonics of the permuted unit direction; the
 //   gradient is (grad P(u) - l P(u) u)/r for the degree-l homogeneous form P.
@@ -270,6 +272,7 @@ struct Oracle {
     P scale;
     std::vector<double> E0;
     std::vector<int> m0_off, m0_deg, m0_idx;
+    std::vector<char> m0_used, m1_used;  // first occurrence of each monomial per output
     std::vector<P> m0_coef;
     int m0_terms;
     std::vector<int> m1_deg, m1_idx;
@@ -325,6 +328,9 @@ struct Oracle {
         m0_terms = m0_off[nLM];
         m0_deg.assign(s.m0_degree, s.m0_degree + m0_terms);
         m0_idx.assign(s.m0_index, s.m0_index + 3 * m0_terms);
+        m0_used.assign(m0_terms, 1);
+        for (int LM = 0; LM < nLM; ++LM)
+            first_terms(m0_deg.data(), m0_idx.data(), m0_off[LM], m0_off[LM + 1], m0_used.data());
         m0_coef = conv(s.m0_coef, static_cast<size_t>(ne) * C * m0_terms);
         num_terms = s.num_terms;
         path_l.assign(s.path_l, s.path_l + num_paths);
@@ -348,6 +354,8 @@ struct Oracle {
         m1_terms = s.m1_terms;
         m1_deg.assign(s.m1_degree, s.m1_degree + m1_terms);
         m1_idx.assign(s.m1_index, s.m1_index + 3 * m1_terms);
+        m1_used.assign(m1_terms, 1);
+        first_terms(m1_deg.data(), m1_idx.data(), 0, m1_terms, m1_used.data());
         m1_coef = conv(s.m1_coef, static_cast<size_t>(ne) * C * m1_terms);
         H2M0 = conv(s.H2M0, static_cast<size_t>(ne) * C * C);
         H2M1 = conv(s.H2M1, static_cast<size_t>(C) * C);
@@ -449,13 +457,30 @@ struct Oracle {
         return ai <= aj ? ai * (2 * n - ai - 1) / 2 + aj : aj * (2 * n - aj - 1) / 2 + ai;
     }
 
-    // polynomial value and gradient (evaluate_gradient_simple)
-    static P poly(const P* coef, const int* deg, const int* idx, int begin, int end, const P* x, P* g,
-                  int nvar)
+    // Terms of one polynomial output that the reference keeps: it stores the
+    // (monomial, coefficient) pairs in a std::map keyed by the exact index
+    // vector, and map::insert ignores a key already present, so a monomial
+    // listed again keeps its first coefficient; [0,1] and [1,0] are distinct
+    // keys (multivariate_polynomial.cpp:36-46).  used[t] = 0 marks a repeat.
+    static void first_terms(const int* deg, const int* idx, int begin, int end, char* used)
+    {
+        for (int t = begin; t < end; ++t) {
+            used[t] = 1;
+            for (int u = begin; u < t && used[t]; ++u)
+                if (used[u] && deg[u] == deg[t] && std::equal(idx + 3 * u, idx + 3 * u + deg[t], idx + 3 * t))
+                    used[t] = 0;
+        }
+    }
+
+    // polynomial value and gradient (evaluate_gradient_simple) over the terms
+    // with used[t] != 0
+    static P poly(const P* coef, const int* deg, const int* idx, const char* used, int begin, int end, const P* x,
+                  P* g, int nvar)
     {
         P f = 0;
         for (int v = 0; v < nvar; ++v) g[v] = 0;
         for (int t = begin; t < end; ++t) {
+            if (!used[t]) continue;
             const int* i = idx + 3 * t;
             const P c = coef[t];
             if (deg[t] == 1) {
@@ -606,7 +631,7 @@ struct Oracle {
                 for (int lm = 0; lm < nlm; ++lm) x[lm] = A0[(static_cast<size_t>(i) * nlm + lm) * C + k];
                 const P* coef = m0_coef.data() + (static_cast<size_t>(types[i]) * C + k) * m0_terms;
                 for (int LM = 0; LM < nLM; ++LM) {
-                    const P f = poly(coef, m0_deg.data(), m0_idx.data(), m0_off[LM], m0_off[LM + 1],
+                    const P f = poly(coef, m0_deg.data(), m0_idx.data(), m0_used.data(), m0_off[LM], m0_off[LM + 1],
                                      x, g, nlm);
                     M0[(static_cast<size_t>(i) * nLM + LM) * C + k] = f;
                     for (int lm = 0; lm < nlm; ++lm)
@@ -738,7 +763,7 @@ struct Oracle {
                 for (int k = 0; k < C; ++k) {
                     for (int lm = 0; lm < nlm; ++lm) x[lm] = A1[(static_cast<size_t>(i) * nlm + lm) * C + k];
                     const P* coef = m1_coef.data() + (static_cast<size_t>(ti) * C + k) * m1_terms;
-                    M1[k] = poly(coef, m1_deg.data(), m1_idx.data(), 0, m1_terms, x, g, nlm);
+                    M1[k] = poly(coef, m1_deg.data(), m1_idx.data(), m1_used.data(), 0, m1_terms, x, g, nlm);
                     for (int lm = 0; lm < nlm; ++lm) M1g[static_cast<size_t>(lm) * C + k] = g[lm];
                 }
                 const P* xs = pre_linear_up ? xs_pre.data() + static_cast<size_t>(i) * C
@@ -1159,7 +1184,9 @@ void oracle_spline_eval(double h, double x0, int nodes, int nfn, const double* v
 double oracle_poly_eval(int num_terms, const int* degree, const int* index, const double* coef, int nvar,
                         const double* x, double* grad)
 {
-    return Oracle<double>::poly(coef, degree, index, 0, num_terms, x, grad, nvar);
+    std::vector<char> used(std::max(num_terms, 1));
+    Oracle<double>::first_terms(degree, index, 0, num_terms, used.data());
+    return Oracle<double>::poly(coef, degree, index, used.data(), 0, num_terms, x, grad, nvar);
 }
 
 // Atom forces F_a = sum_{e: src=a} f_e - sum_{e: recv=a} f_e and stress

@@ -93,9 +93,11 @@ long long term_key(int out, int deg, int i0, int i1, int i2)
 
 }  // namespace
 
-// Places the terms of a JSON monomial table (grouped by output, offsets
-// [outputs + 1]) onto the slots of the compiled table of its shape; the
-// terms without a compiled slot (other monomials, repeats) follow as the
+// Places the terms of a monomial table (grouped by output, offsets
+// [outputs + 1]; the loader has already dropped exact repeats, keeping each
+// monomial's first coefficient) onto the slots of the compiled table of its
+// shape; the terms without a compiled slot (other monomials, a second
+// permutation of one index set such as [1,0] beside [0,1]) follow as the
 // runtime remainder, grouped by output in JSON order.  Compiled slots that
 // the JSON does not use keep a zero coefficient.
 PolyLayout poly_layout(int lin, int lout, const std::vector<int>& offsets, const std::vector<int>& degree,
@@ -953,6 +955,9 @@ std::uint64_t Evaluator::prepare_graph(int num_nodes, const int* node_types, con
     for (long long e = 0; e < E; ++e)
         if (neigh_indices[e] < 0 || neigh_indices[e] >= num_nodes)
             throw std::out_of_range("neighbour index out of range.");
+    // from here on the graph state changes: a preparation that fails part way
+    // must leave no earlier token valid
+    invalidate_graph();
     prepare_active_types(types);
     host_types_ = types;
     num_nodes_ = num_nodes;
@@ -1083,6 +1088,9 @@ std::uint64_t Evaluator::prepare_periodic_graph(int num_nodes, const int* node_t
 {
     validate_periodic_inputs(num_nodes, cell, inverse_cell, cutoff);
     std::vector<int> types(node_types, node_types + num_nodes);
+    // from here on the graph state changes: a preparation that fails part way
+    // must leave no earlier token valid
+    invalidate_graph();
     prepare_active_types(types);
     const int N = num_nodes;
     positions_.reserve(static_cast<std::size_t>(std::max(N, 1)) * 3 * sizeof(double));

@@ -168,15 +168,30 @@ RadialNetwork parse_network(const Value& def, const std::string& name, int input
     return net;
 }
 
+// Monomials of one polynomial output.  A monomial listed again (the same
+// index vector, in the same order) keeps the coefficient of its first entry:
+// the reference stores an output's terms in a std::map keyed by the index
+// vector, whose insert ignores later duplicates
+// (libsymmetrix/source/multivariate_polynomial.cpp:36-46; the Kokkos loader
+// does the same, mace_kokkos_model.cpp:55-76).  Permutations of one vector
+// ([0,1] and [1,0]) are distinct keys there and stay distinct terms here.
+// keep[j] tells whether JSON entry j is a term; degree and index receive the
+// kept terms, indices sorted ascending (the product does not depend on their
+// order).
 void parse_monomials(const Value& list, const std::string& what, std::vector<int>& degree,
-                     std::vector<int>& index, int num_variables)
+                     std::vector<int>& index, int num_variables, std::vector<char>& keep)
 {
     require(list.kind == Value::Kind::array || (list.kind == Value::Kind::numbers && list.nums.empty()),
             what + " must be a list of monomials");
+    std::set<std::vector<int>> seen;
+    keep.clear();
     for (const auto& mono : list.items) {
         std::vector<int> m = mono.ints(what);
         require(!m.empty() && m.size() <= 3,
                 what + ": only monomials of degree 1 to 3 (correlation <= 3) are supported");
+        const bool first = seen.insert(m).second;
+        keep.push_back(first ? 1 : 0);
+        if (!first) continue;
         std::sort(m.begin(), m.end());
         for (int v : m) require(v >= 0 && v < num_variables, what + " references an invalid input");
         degree.push_back(static_cast<int>(m.size()));
@@ -357,11 +372,11 @@ HostModel HostModel::load(const std::string& path, const std::string& head)
     const Value& m0_mono = file.at("M0_monomials");
     const Value& m0_w = file.at("M0_weights");
     m.m0_offsets.push_back(0);
-    std::vector<std::vector<int>> m0_lm_degree(m.num_LM);
+    std::vector<std::vector<char>> m0_keep(m.num_LM);
     for (int LM = 0; LM < m.num_LM; ++LM) {
         const std::string key = std::to_string(LM);
         std::vector<int> deg, idx;
-        parse_monomials(m0_mono.at(key), "M0_monomials", deg, idx, m.num_lm);
+        parse_monomials(m0_mono.at(key), "M0_monomials", deg, idx, m.num_lm, m0_keep[LM]);
         m.m0_degree.insert(m.m0_degree.end(), deg.begin(), deg.end());
         m.m0_index.insert(m.m0_index.end(), idx.begin(), idx.end());
         m.m0_offsets.push_back(m.m0_offsets.back() + static_cast<int>(deg.size()));
@@ -372,11 +387,11 @@ HostModel HostModel::load(const std::string& path, const std::string& head)
         const Value& wa = m0_w.at(std::to_string(a));
         for (int LM = 0; LM < m.num_LM; ++LM) {
             const Value& wl = wa.at(std::to_string(LM));
-            const int n = m.m0_offsets[LM + 1] - m.m0_offsets[LM];
+            const std::vector<char>& keep = m0_keep[LM];
             for (int k = 0; k < C; ++k) {
-                std::vector<double> c = numbers(wl.at(std::to_string(k)), "M0_weights", n);
-                for (int t = 0; t < n; ++t)
-                    m.m0_coef[(static_cast<std::size_t>(a) * T0 + m.m0_offsets[LM] + t) * C + k] = c[t];
+                std::vector<double> c = numbers(wl.at(std::to_string(k)), "M0_weights", keep.size());
+                for (std::size_t j = 0, t = 0; j < keep.size(); ++j)
+                    if (keep[j]) m.m0_coef[(static_cast<std::size_t>(a) * T0 + m.m0_offsets[LM] + t++) * C + k] = c[j];
             }
         }
     }
@@ -442,7 +457,8 @@ HostModel HostModel::load(const std::string& path, const std::string& head)
 
     // M1
     std::vector<int> deg1, idx1;
-    parse_monomials(file.at("M1_monomials"), "M1_monomials", deg1, idx1, m.num_lm);
+    std::vector<char> m1_keep;
+    parse_monomials(file.at("M1_monomials"), "M1_monomials", deg1, idx1, m.num_lm, m1_keep);
     m.m1_degree = deg1;
     m.m1_index = idx1;
     const int T1 = static_cast<int>(deg1.size());
@@ -451,9 +467,9 @@ HostModel HostModel::load(const std::string& path, const std::string& head)
     for (int a = 0; a < ne; ++a) {
         const Value& wa = m1_w.at(std::to_string(a));
         for (int k = 0; k < C; ++k) {
-            std::vector<double> c = numbers(wa.at(std::to_string(k)), "M1_weights", T1);
-            for (int t = 0; t < T1; ++t)
-                m.m1_coef[(static_cast<std::size_t>(a) * T1 + t) * C + k] = c[t];
+            std::vector<double> c = numbers(wa.at(std::to_string(k)), "M1_weights", m1_keep.size());
+            for (std::size_t j = 0, t = 0; j < m1_keep.size(); ++j)
+                if (m1_keep[j]) m.m1_coef[(static_cast<std::size_t>(a) * T1 + t++) * C + k] = c[j];
         }
     }
 

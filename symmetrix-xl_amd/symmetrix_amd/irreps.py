@@ -162,9 +162,16 @@ def coupling_tensor(l1: int, l2: int, lout: int) -> np.ndarray:
     """Real coupling tensor C[m1, m2, M] of l1 x l2 -> lout.
 
     Solved as the one-dimensional null space of the equivariance constraint
-    over a few random rotations, normalised per output component, with the
-    sign fixed so that the entry of largest magnitude (first in C order on
-    ties) is positive.
+    over a few random rotations, normalised per output component.  Sign: for
+    a natural-parity triple (l1 + l2 + lout even) the m = 0 x m = 0 -> m = 0
+    entry, C[l1, l2, lout], is nonzero (the 3j symbol (l1 l2 lout; 0 0 0)
+    vanishes only for odd sums) and is made positive.  This is the convention
+    of the reference's coupling values: it reproduces every term of its
+    contracts for the (3,1), (3,2) and (3,0) shapes
+    (symmetrix/test/data/execution_contracts/jit_r1_*_contract.json), where
+    the previous "largest entry positive" rule flipped the (2,2,2) and (3,2,3)
+    paths.  Other triples keep the entry of largest magnitude (first in C
+    order on ties) positive.
     """
     if not triangle(l1, l2, lout):
         raise ValueError(f"({l1}, {l2}) cannot couple to {lout}")
@@ -181,11 +188,15 @@ def coupling_tensor(l1: int, l2: int, lout: int) -> np.ndarray:
     if sing[-1] > 1e-8 or (len(sing) > 1 and sing[-2] < 1e-6):
         raise RuntimeError("coupling null space is not one-dimensional")
     tensor = vt[-1].reshape(d1, d2, d3) * math.sqrt(d3)
-    flat = tensor.reshape(-1)
-    peak = np.max(np.abs(flat))
-    first = int(np.flatnonzero(np.abs(flat) > peak - 1e-9)[0])
-    if flat[first] < 0:
-        tensor = -tensor
+    if (l1 + l2 + lout) % 2 == 0:
+        if tensor[l1, l2, lout] < 0:
+            tensor = -tensor
+    else:
+        flat = tensor.reshape(-1)
+        peak = np.max(np.abs(flat))
+        first = int(np.flatnonzero(np.abs(flat) > peak - 1e-9)[0])
+        if flat[first] < 0:
+            tensor = -tensor
     tensor[np.abs(tensor) < 1e-12] = 0.0
     return tensor
 

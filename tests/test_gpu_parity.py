@@ -226,6 +226,28 @@ def test_stale_generation_is_rejected(native, tiny):
         ev._compute_prepared_factorized_positions(g1, s.positions)
 
 
+def test_failed_preparation_makes_earlier_tokens_stale(native, tiny):
+    """A preparation that raises after it has started to change the graph
+    state (here: a neighbour type outside the model, found while the edge
+    pair table is formed) leaves no earlier generation usable."""
+    from symmetrix_amd import MACEKokkosFloat, synthetic
+
+    path, model = tiny
+    s = synthetic.srtio3_supercell(2, sigma=0.05, seed=4)
+    ev = MACEKokkosFloat(path)
+    types = synthetic.node_types(s, model["atomic_numbers"])
+    g1 = ev._prepare_periodic_factorized_graph(types, s.positions, s.cell, np.linalg.inv(s.cell), 5.5)["generation"]
+    ev._compute_prepared_factorized_positions(g1, s.positions)
+    n = len(s)
+    num_neigh = np.ones(n, dtype=np.int32)
+    neigh = ((np.arange(n) + 1) % n).astype(np.int32)
+    bad_types = np.full(n, model["num_elements"], dtype=np.int32)  # out of range
+    with pytest.raises(IndexError):
+        ev._prepare_factorized_graph(n, types, num_neigh, neigh, bad_types)
+    with pytest.raises(ValueError, match="stale"):
+        ev._compute_prepared_factorized_positions(g1, s.positions)
+
+
 def test_skin_reuse_matches_fresh_graph(native, tiny):
     from symmetrix_amd import Symmetrix, synthetic
 

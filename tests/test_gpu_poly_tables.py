@@ -9,7 +9,9 @@ JSON lists as given):
 
 - monomial order shuffled within each output, and the variable order inside
   each monomial permuted (same polynomial, compiled slots found by value);
-- extra monomials that no compiled slot holds, plus a repeated monomial;
+- extra monomials that no compiled slot holds, plus a repeated monomial
+  (first coefficient kept, as the reference's polynomial does) and a
+  permutation of an existing one (a distinct term);
 - a correlation order with no compiled table (every term runs in the loop).
 
 Tolerances as in test_gpu_parity.py (FP32).
@@ -76,8 +78,11 @@ def _shuffle(model, rng):
 
 
 def _add_terms(model, rng, extra):
-    """Appends `extra` monomials (and one repeat of an existing one) to the M0
-    outputs with LM >= 1 and to M1, with small random coefficients."""
+    """Appends `extra` monomials, then a repeat of an existing one and a
+    permutation of another, to the M0 outputs with LM >= 1 and to M1, with
+    small random coefficients (the repeat's is large: the reference keeps the
+    first coefficient of a repeated monomial, multivariate_polynomial.cpp:36-46,
+    so summing it would move the result far outside the tolerances)."""
     C = model["num_channels"]
     ne = model["num_elements"]
     nlm = (model["l_max"] + 1) ** 2
@@ -91,7 +96,14 @@ def _add_terms(model, rng, extra):
             if tuple(m) not in have:
                 have.add(tuple(m))
                 out.append(m)
-        return out + [list(existing[len(existing) // 2])]
+        repeat = list(existing[len(existing) // 2])
+        permuted = next(list(reversed(m)) for m in existing if len(m) > 1 and m[0] != m[-1])
+        return out + [repeat, permuted]
+
+    def coefficients(n):
+        c = list(0.05 * rng.normal(size=n))
+        c[-2] = 2.0  # the repeat
+        return c
 
     for LM, monos in model["M0_monomials"].items():
         if LM == "0":
@@ -101,13 +113,42 @@ def _add_terms(model, rng, extra):
         for a in range(ne):
             w = model["M0_weights"][str(a)][LM]
             for k in range(C):
-                w[str(k)] = w[str(k)] + list(0.05 * rng.normal(size=len(add)))
+                w[str(k)] = w[str(k)] + coefficients(len(add))
     add = new_terms(model["M1_monomials"])
     model["M1_monomials"] = model["M1_monomials"] + add
     for a in range(ne):
         w = model["M1_weights"][str(a)]
         for k in range(C):
-            w[str(k)] = w[str(k)] + list(0.05 * rng.normal(size=len(add)))
+            w[str(k)] = w[str(k)] + coefficients(len(add))
+
+
+def _summed_repeats(model):
+    """The same tables with each repeated monomial's coefficients added to its
+    first entry (the semantics the reference does not have)."""
+    model = json.loads(json.dumps(model))
+    ne, C = model["num_elements"], model["num_channels"]
+
+    def fold(monos, weight_lists):
+        first, keep = {}, []
+        for j, m in enumerate(monos):
+            key = tuple(m)
+            if key in first:
+                for w in weight_lists:
+                    for k in range(C):
+                        w[str(k)][first[key]] += w[str(k)][j]
+            else:
+                first[key] = j
+                keep.append(j)
+        for w in weight_lists:
+            for k in range(C):
+                w[str(k)] = [w[str(k)][j] for j in keep]
+        return [monos[j] for j in keep]
+
+    for LM in model["M0_monomials"]:
+        model["M0_monomials"][LM] = fold(
+            model["M0_monomials"][LM], [model["M0_weights"][str(a)][LM] for a in range(ne)])
+    model["M1_monomials"] = fold(model["M1_monomials"], [model["M1_weights"][str(a)] for a in range(ne)])
+    return model
 
 
 @pytest.mark.parametrize("preset,cells", [("tiny", 2), ("medium3", 2)])
@@ -132,8 +173,14 @@ def test_extra_monomials_run_in_the_remainder_loop(oracle_lib, tmp_path, preset,
     s = synthetic.srtio3_supercell(cells, sigma=0.05, seed=4)
     model = _generated(preset, seed=1)
     _add_terms(model, np.random.default_rng(11), extra=6)
-    print(f"{preset}: M0/M1 tables with extra and repeated monomials, SrTiO3 {cells}^3", flush=True)
-    _check(oracle_lib, _write(tmp_path, "extra", model), model, s)
+    print(f"{preset}: M0/M1 tables with extra, repeated and permuted monomials, SrTiO3 {cells}^3", flush=True)
+    got = _check(oracle_lib, _write(tmp_path, "extra", model), model, s)
+    # summing the repeats instead would give a clearly different result
+    summed = _summed_repeats(model)
+    types = synthetic.node_types(s, summed["atomic_numbers"])
+    orc = oracle_lib.MaceOracle(summed, np.unique(types), "float32")
+    other = oracle_lib.evaluate(orc, s, summed["r_cut"] + 0.5)
+    assert abs(got["energy"] - other["energy"]) / len(s) > 100 * E_TOL
 
 
 def test_uncompiled_correlation_order_matches_oracle(oracle_lib, tmp_path):

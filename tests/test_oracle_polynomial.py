@@ -1,10 +1,14 @@
 """Symmetric-contraction polynomials and coupling tables.
 
 * The oracle's polynomial value/gradient against a direct numpy evaluation
-  and finite differences (reference multivariate_polynomial.cpp:313-355).
-* The generated real coupling (CG) tables against the reference's medium R1
-  contract fixture, all 86 terms (tests/golden, copied from
-  symmetrix/test/data/execution_contracts/jit_r1_mace_mpa0_medium_contract.json).
+  and finite differences (reference multivariate_polynomial.cpp:313-355), and
+  the reference's repeated-monomial rule (first coefficient kept, exact index
+  vectors as keys; multivariate_polynomial.cpp:36-46) on its own fixture.
+* The generated real coupling (CG) tables against the reference's R1
+  contract fixtures, every term and sign (tests/golden, copied from
+  symmetrix/test/data/execution_contracts/jit_r1_*_contract.json): the
+  medium (3,1) shape, 86 terms; the wide (3,2) shape, 215 terms; the
+  L_max = 0 (3,0) shape, 16 terms; the 1-term l = 0 fixture.
 * The generated M0 monomial tables against standard_m0_contract.json
   (tests/golden): identical for the scalar and m=0 outputs; the fixture's
   m=+-1 tables carry 6 extra cubic monomials each that no O(3)-equivariant
@@ -43,17 +47,71 @@ def test_oracle_polynomial_value_and_gradient(oracle_lib):
         assert g[v] == pytest.approx(fd, abs=1e-8)
 
 
-def test_cg_tables_match_reference_contract():
+def test_repeated_monomial_retains_first_coefficient(oracle_lib):
+    # the reference's own known answer (symmetrix/test/test_multivariate_polynomial.py:65-68):
+    # [0] listed twice keeps 2.0, so f = 2*4 + 3*4*5 = 68 (summing both would give 104)
+    f, g = oracle_lib.poly_eval([[0], [0], [0, 1]], [2.0, 9.0, 3.0], [4.0, 5.0])
+    assert f == pytest.approx(68.0, abs=1e-12)
+    np.testing.assert_allclose(g, [2.0 + 3.0 * 5.0, 3.0 * 4.0], atol=1e-12)
+
+
+def test_permuted_monomials_are_distinct_terms(oracle_lib):
+    # map keys are exact index vectors: [0,1] and [1,0] are two terms, [1,0] again is a repeat
+    monos = [[0, 1], [1, 0], [1, 0], [2, 2, 1], [1, 2, 2], [2, 1, 2], [2, 2, 1]]
+    coef = [2.0, 3.0, 100.0, 0.5, 0.25, 0.125, 100.0]
+    x = np.array([4.0, 5.0, -1.5])
+    f, g = oracle_lib.poly_eval(monos, coef, x)
+    want = (2.0 + 3.0) * x[0] * x[1] + (0.5 + 0.25 + 0.125) * x[1] * x[2] ** 2
+    assert f == pytest.approx(want, abs=1e-12)
+    eps = 1e-6
+    for v in range(3):
+        dx = np.zeros(3)
+        dx[v] = eps
+        fd = (oracle_lib.poly_eval(monos, coef, x + dx)[0] - oracle_lib.poly_eval(monos, coef, x - dx)[0]) / (2 * eps)
+        assert g[v] == pytest.approx(fd, abs=1e-7)
+
+
+# The reference's R1 coupling contracts (symmetrix/test/data/execution_contracts/,
+# copied into tests/golden): (file, edge l_max, source l_max, terms, tolerance).
+# jit_r1_contract.json stores its values to 8 significant digits.
+R1_CONTRACTS = [
+    ("jit_r1_mace_mpa0_medium_contract.json", 3, 1, 86, 1e-12),
+    ("jit_r1_contract.json", 3, 1, 86, 5e-8),
+    ("jit_r1_mace_mp0b2_large_contract.json", 3, 2, 215, 1e-12),
+    ("jit_r1_mace_omat0_small_contract.json", 3, 0, 16, 1e-12),
+    ("jit_r1_mace_off23_small_contract.json", 3, 0, 16, 1e-12),
+    ("jit_r1_fixture_c4_e3_l0_contract.json", 0, 0, 1, 1e-12),
+]
+
+
+@pytest.mark.parametrize("name,edge_lmax,source_lmax,count,tol", R1_CONTRACTS)
+def test_cg_tables_match_reference_contract(name, edge_lmax, source_lmax, count, tol):
+    # every path, row, output row and coefficient (sign included) of the
+    # generated table equals the reference's contract
     from symmetrix_amd import irreps
 
-    ref = load("jit_r1_mace_mpa0_medium_contract.json")
-    t = irreps.phi1_tables(3, 1)
+    ref = load(name)
+    t = irreps.phi1_tables(edge_lmax, source_lmax)
     assert [tuple(p) for p in t["paths"]] == [(p["edge_l"], p["source_l"], p["output_l"]) for p in ref["paths"]]
     mine = {(x["lm1"], x["lm2"], x["row"], x["lme"]): x["coefficient"] for x in t["terms"]}
     theirs = {(x["lm1"], x["lm2"], x["row"], x["lme"]): x["coefficient"] for x in ref["sparse_coupling"]["terms"]}
-    assert set(mine) == set(theirs) and len(theirs) == ref["sparse_coupling"]["term_count"] == 86
+    assert set(mine) == set(theirs) and len(theirs) == ref["sparse_coupling"]["term_count"] == count
     for k in theirs:
-        assert mine[k] == pytest.approx(theirs[k], abs=1e-12)
+        assert mine[k] == pytest.approx(theirs[k], abs=tol)
+
+
+def test_cg_sign_rule_is_not_the_largest_entry_rule():
+    # the two paths of the wide shape on which "largest entry positive" and
+    # the reference's convention (m=0 x m=0 -> m=0 entry positive) disagree
+    from symmetrix_amd import irreps
+
+    for triple in [(2, 2, 2), (3, 2, 3)]:
+        c = irreps.coupling_tensor(*triple)
+        flat = c.reshape(-1)
+        assert c[triple[0], triple[1], triple[2]] > 0
+        peak = np.max(np.abs(flat))
+        first_peak = flat[np.flatnonzero(np.abs(flat) > peak - 1e-9)[0]]
+        assert first_peak < 0
 
 
 def test_r0_contract_rows_are_the_edge_harmonics():
