@@ -108,18 +108,65 @@ int sxl_prepare_periodic_graph_device(sxl_evaluator* evaluator, int num_nodes, c
 int sxl_graph_arrays(sxl_evaluator* evaluator, uint64_t generation, int* num_neigh, int* receiver_offsets,
                      int* sources, int* shifts, double* fractional_xyz);
 
-/* New cell for the prepared periodic graph (_update_factorized_cell,
+/* New cell for the prepared graph (_update_factorized_cell,
  * mace_kokkos.cpp:1673-1685): later evaluations form each edge vector as the
- * build's fractional edge vector in this cell plus the atoms' minimum-image
- * displacements.  Invalid argument when the cell is non-finite or does not
- * match its inverse. */
+ * fractional reference edge vector (the device build's, or the caller's
+ * fractional or shift geometry) in this cell plus the atoms' minimum-image
+ * displacements.  Invalid argument without such a geometry, or when the cell
+ * is non-finite, singular or (device-built graph) does not match its
+ * inverse. */
 int sxl_update_cell(sxl_evaluator* evaluator, uint64_t generation, const double* cell,
                     const double* inverse_cell);
 
-/* Evaluate energies and forces at new positions of a prepared periodic graph.
- * Replaces _compute_prepared_factorized_positions(generation, positions)
- * (mace_kokkos.cpp:1828-1836).  Invalid argument when an edge of the graph has
- * zero or non-finite length at these positions (coincident atoms). */
+/* 32-bit cardinality checks of a graph the caller is about to prepare:
+ * length error when the receiver or feature-node count reaches INT32_MAX or
+ * the edge count exceeds it, invalid argument when there are fewer feature
+ * nodes than receivers.  Replaces _validate_graph_cardinality(num_receivers,
+ * num_feature_nodes, num_edges) (symmetrix/source/cpp/mace_kokkos.cpp:1604-1607;
+ * MACEKokkos::validate_graph_cardinality, mace_kokkos_runtime.cpp:199-260). */
+int sxl_validate_graph_cardinality(const sxl_evaluator* evaluator, int64_t num_receivers, int64_t num_feature_nodes,
+                                   int64_t num_edges);
+
+/* Geometry of a graph prepared with sxl_prepare_graph, for evaluations from
+ * positions (sxl_compute_prepared_positions*): the reference positions
+ * [N][3] and the edge vectors [E][3] at which the caller built its graph, the
+ * cell and its inverse (row-major 3x3) and pbc [3] (non-zero = periodic lattice
+ * axis).  An evaluation at positions x forms each edge vector as the
+ * reference edge vector + d[src] - d[recv], with d = x - reference position
+ * wrapped to the minimum image along the periodic axes (no wrap without
+ * one).  num_positions and num_xyz are element counts (3N, 3E); invalid
+ * argument on a stale token, other extents or a non-finite value.  Replaces
+ * _prepare_factorized_geometry(generation, reference_positions,
+ * reference_xyz, cell, inverse_cell, pbc) (mace_kokkos.cpp:1608-1629). */
+int sxl_prepare_geometry(sxl_evaluator* evaluator, uint64_t generation, const double* reference_positions,
+                         int64_t num_positions, const double* reference_xyz, int64_t num_xyz, const double* cell,
+                         const double* inverse_cell, const int* pbc);
+/* As sxl_prepare_geometry with fractional reference positions and edge
+ * vectors (in units of the lattice vectors), which follow later cells set by
+ * sxl_update_cell; requires a fully periodic, invertible cell.  Replaces
+ * _prepare_factorized_fractional_geometry(generation, fractional_positions,
+ * fractional_xyz, cell, inverse_cell, pbc) (mace_kokkos.cpp:1650-1669). */
+int sxl_prepare_fractional_geometry(sxl_evaluator* evaluator, uint64_t generation, const double* fractional_positions,
+                                    int64_t num_positions, const double* fractional_xyz, int64_t num_xyz,
+                                    const double* cell, const double* inverse_cell, const int* pbc);
+/* As sxl_prepare_geometry with each reference edge vector given as
+ * reference_position[src] - reference_position[recv] + shift . cell from
+ * integer cell shifts [E][3] (12 bytes per edge); later cells set by
+ * sxl_update_cell apply.  Replaces _prepare_factorized_shift_geometry(
+ * generation, reference_positions, shifts, cell, inverse_cell, pbc)
+ * (mace_kokkos.cpp:1630-1649), which the reference accepts only for its tiled
+ * plans; here either plan. */
+int sxl_prepare_shift_geometry(sxl_evaluator* evaluator, uint64_t generation, const double* reference_positions,
+                               int64_t num_positions, const int* shifts, int64_t num_shifts, const double* cell,
+                               const double* inverse_cell, const int* pbc);
+
+/* Evaluate energies and forces at new positions of a prepared graph: a
+ * periodic graph built on the device, or a caller's graph with a geometry set
+ * by one of the functions above.  Replaces
+ * _compute_prepared_factorized_positions(generation, positions)
+ * (mace_kokkos.cpp:1828-1836).  Invalid argument when the graph has no
+ * geometry, or when an edge of the graph has zero or non-finite length at
+ * these positions (coincident atoms). */
 int sxl_compute_prepared_positions(sxl_evaluator* evaluator, uint64_t generation, const double* positions);
 int sxl_compute_prepared_positions_device(sxl_evaluator* evaluator, uint64_t generation,
                                           const double* d_positions);

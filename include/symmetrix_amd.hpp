@@ -177,6 +177,59 @@ public:
         detail::check(sxl_update_cell(handle_, graph_generation, cell.data(), inverse_cell.data()));
     }
 
+    // validate_graph_cardinality(num_receivers, num_feature_nodes, num_edges)
+    void validate_graph_cardinality(std::size_t num_receivers, std::size_t num_feature_nodes,
+                                    std::size_t num_edges) const
+    {
+        detail::check(sxl_validate_graph_cardinality(handle_, static_cast<std::int64_t>(num_receivers),
+                                                     static_cast<std::int64_t>(num_feature_nodes),
+                                                     static_cast<std::int64_t>(num_edges)));
+    }
+
+    // prepare_factorized_geometry(graph_generation, reference_positions,
+    // reference_xyz, cell, inverse_cell, pbc)
+    void prepare_factorized_geometry(std::uint64_t graph_generation, std::span<const double> reference_positions,
+                                     std::span<const double> reference_xyz, std::span<const double> cell,
+                                     std::span<const double> inverse_cell, std::span<const int> pbc)
+    {
+        detail::require(cell.size() == 9 && inverse_cell.size() == 9 && pbc.size() == 3,
+                        "Execution R1 prepared geometry extents are inconsistent.");
+        detail::check(sxl_prepare_geometry(handle_, graph_generation, reference_positions.data(),
+                                           static_cast<std::int64_t>(reference_positions.size()),
+                                           reference_xyz.data(), static_cast<std::int64_t>(reference_xyz.size()),
+                                           cell.data(), inverse_cell.data(), pbc.data()));
+    }
+
+    // prepare_factorized_fractional_geometry(graph_generation,
+    // fractional_positions, fractional_xyz, cell, inverse_cell, pbc)
+    void prepare_factorized_fractional_geometry(std::uint64_t graph_generation,
+                                                std::span<const double> fractional_positions,
+                                                std::span<const double> fractional_xyz, std::span<const double> cell,
+                                                std::span<const double> inverse_cell, std::span<const int> pbc)
+    {
+        detail::require(cell.size() == 9 && inverse_cell.size() == 9 && pbc.size() == 3,
+                        "Fractional Execution R1 geometry requires 3x3 cell matrices and three PBC flags.");
+        detail::check(sxl_prepare_fractional_geometry(
+            handle_, graph_generation, fractional_positions.data(),
+            static_cast<std::int64_t>(fractional_positions.size()), fractional_xyz.data(),
+            static_cast<std::int64_t>(fractional_xyz.size()), cell.data(), inverse_cell.data(), pbc.data()));
+    }
+
+    // prepare_factorized_shift_geometry(graph_generation, reference_positions,
+    // shifts, cell, inverse_cell, pbc)
+    void prepare_factorized_shift_geometry(std::uint64_t graph_generation,
+                                           std::span<const double> reference_positions, std::span<const int> shifts,
+                                           std::span<const double> cell, std::span<const double> inverse_cell,
+                                           std::span<const int> pbc)
+    {
+        detail::require(cell.size() == 9 && inverse_cell.size() == 9 && pbc.size() == 3,
+                        "Shift geometry extents are inconsistent.");
+        detail::check(sxl_prepare_shift_geometry(handle_, graph_generation, reference_positions.data(),
+                                                 static_cast<std::int64_t>(reference_positions.size()),
+                                                 shifts.data(), static_cast<std::int64_t>(shifts.size()),
+                                                 cell.data(), inverse_cell.data(), pbc.data()));
+    }
+
     // compute_prepared_factorized(graph_generation, xyz, r)
     void compute_prepared_factorized(std::uint64_t graph_generation, std::span<const double> xyz,
                                      std::span<const double> r)

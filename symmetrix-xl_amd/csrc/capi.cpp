@@ -163,6 +163,58 @@ int sxl_update_cell(sxl_evaluator* ev, uint64_t generation, const double* cell, 
     return guarded([&] { ev->impl.update_cell(generation, cell, inverse_cell); });
 }
 
+int sxl_validate_graph_cardinality(const sxl_evaluator* ev, int64_t num_receivers, int64_t num_feature_nodes,
+                                   int64_t num_edges)
+{
+    if (!ev) return null_handle();
+    return guarded([&] {
+        if (num_receivers < 0 || num_feature_nodes < 0 || num_edges < 0)
+            throw std::invalid_argument("MACE graph cardinalities must be non-negative.");
+        ev->impl.validate_graph_cardinality(static_cast<uint64_t>(num_receivers),
+                                            static_cast<uint64_t>(num_feature_nodes),
+                                            static_cast<uint64_t>(num_edges));
+    });
+}
+
+int sxl_prepare_geometry(sxl_evaluator* ev, uint64_t generation, const double* reference_positions,
+                         int64_t num_positions, const double* reference_xyz, int64_t num_xyz, const double* cell,
+                         const double* inverse_cell, const int* pbc)
+{
+    if (!ev || !cell || !inverse_cell || !pbc || num_positions < 0 || num_xyz < 0 ||
+        (num_positions > 0 && !reference_positions) || (num_xyz > 0 && !reference_xyz))
+        return null_handle();
+    return guarded([&] {
+        ev->impl.prepare_geometry(generation, reference_positions, static_cast<std::size_t>(num_positions),
+                                  reference_xyz, static_cast<std::size_t>(num_xyz), cell, inverse_cell, pbc, false);
+    });
+}
+
+int sxl_prepare_fractional_geometry(sxl_evaluator* ev, uint64_t generation, const double* fractional_positions,
+                                    int64_t num_positions, const double* fractional_xyz, int64_t num_xyz,
+                                    const double* cell, const double* inverse_cell, const int* pbc)
+{
+    if (!ev || !cell || !inverse_cell || !pbc || num_positions < 0 || num_xyz < 0 ||
+        (num_positions > 0 && !fractional_positions) || (num_xyz > 0 && !fractional_xyz))
+        return null_handle();
+    return guarded([&] {
+        ev->impl.prepare_geometry(generation, fractional_positions, static_cast<std::size_t>(num_positions),
+                                  fractional_xyz, static_cast<std::size_t>(num_xyz), cell, inverse_cell, pbc, true);
+    });
+}
+
+int sxl_prepare_shift_geometry(sxl_evaluator* ev, uint64_t generation, const double* reference_positions,
+                               int64_t num_positions, const int* shifts, int64_t num_shifts, const double* cell,
+                               const double* inverse_cell, const int* pbc)
+{
+    if (!ev || !cell || !inverse_cell || !pbc || num_positions < 0 || num_shifts < 0 ||
+        (num_positions > 0 && !reference_positions) || (num_shifts > 0 && !shifts))
+        return null_handle();
+    return guarded([&] {
+        ev->impl.prepare_shift_geometry(generation, reference_positions, static_cast<std::size_t>(num_positions),
+                                        shifts, static_cast<std::size_t>(num_shifts), cell, inverse_cell, pbc);
+    });
+}
+
 int sxl_compute_prepared_positions(sxl_evaluator* ev, uint64_t generation, const double* positions)
 {
     if (!ev || (!positions && ev->impl.num_nodes() > 0)) return null_handle();

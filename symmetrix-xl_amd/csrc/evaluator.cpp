@@ -967,6 +967,9 @@ std::uint64_t Evaluator::prepare_graph(int num_nodes, const int* node_types, con
     upload(first_, first, stream_);
     std::vector<int> src(neigh_indices, neigh_indices + E);
     upload(source_, src, stream_);
+    positions_.reserve(static_cast<std::size_t>(std::max(num_nodes, 1)) * 3 * sizeof(double));
+    disp_.reserve(static_cast<std::size_t>(std::max(num_nodes, 1)) * 3 * sizeof(double));
+    geometry_mode_ = kGeometryNone;
     finish_graph(neigh_types);
     return generation_;
 }
@@ -1119,6 +1122,10 @@ std::uint64_t Evaluator::prepare_periodic_graph(int num_nodes, const int* node_t
     upload(node_types_, types, stream_);
     upload_cell();
     finish_graph(nullptr);
+    // the build's fractional positions and edge vectors are the graph's geometry
+    geometry_mode_ = kGeometryBuilt;
+    geometry_generation_ = generation_;
+    geometry_pbc_ = 7;
     return generation_;
 }
 
@@ -1133,14 +1140,149 @@ void Evaluator::upload_cell()
 // vectors are formed from the build's fractional edge vectors in this cell
 // plus the atoms' minimum-image displacements, so a strained or sheared cell
 // reuses the graph while it still covers the cutoff.
-void Evaluator::update_cell(std::uint64_t generation, const double* cell, const double* inverse_cell)
+void Evaluator::set_cell(const double* cell, const double* inverse_cell)
 {
-    check_generation(generation);
-    if (!periodic_) throw std::invalid_argument("update_cell requires a periodic graph");
-    validate_periodic_inputs(num_nodes_, cell, inverse_cell, 1.0);
     std::memcpy(cell_, cell, sizeof(cell_));
     std::memcpy(inverse_cell_, inverse_cell, sizeof(inverse_cell_));
     upload_cell();
+}
+
+namespace {
+double determinant3(const double* c)
+{
+    return c[0] * (c[4] * c[8] - c[5] * c[7]) - c[1] * (c[3] * c[8] - c[5] * c[6]) +
+           c[2] * (c[3] * c[7] - c[4] * c[6]);
+}
+
+bool all_finite(const double* p, std::size_t n)
+{
+    for (std::size_t i = 0; i < n; ++i)
+        if (!std::isfinite(p[i])) return false;
+    return true;
+}
+}  // namespace
+
+// Requires fractional geometry (the device-built graph's, or the caller's) or
+// shift geometry (reference update_factorized_cell,
+// mace_kokkos_factorized_lifecycle.cpp:2735-2780).
+void Evaluator::update_cell(std::uint64_t generation, const double* cell, const double* inverse_cell)
+{
+    check_generation(generation);
+    if (geometry_generation_ != generation_ ||
+        (geometry_mode_ != kGeometryBuilt && geometry_mode_ != kGeometryFractional &&
+         geometry_mode_ != kGeometryShifts))
+        throw std::invalid_argument(
+            "Prepared Execution R1 cell update requires current graph and fractional or shift geometry tokens.");
+    if (geometry_mode_ == kGeometryBuilt) {
+        validate_periodic_inputs(num_nodes_, cell, inverse_cell, 1.0);
+    } else {
+        if (!all_finite(cell, 9) || !all_finite(inverse_cell, 9))
+            throw std::invalid_argument("Prepared Execution R1 cell matrices contain a non-finite value.");
+        const double det = determinant3(cell);
+        if (!std::isfinite(det) || det == 0.0)
+            throw std::invalid_argument("Prepared Execution R1 cell matrix must be invertible.");
+    }
+    set_cell(cell, inverse_cell);
+}
+
+// Caller geometry of a prepared graph (reference prepare_factorized_geometry
+// and prepare_factorized_fractional_geometry,
+// mace_kokkos_factorized_lifecycle.cpp:2455-2568, 2699-2733): same checks and
+// messages; the arrays are copied to the device.
+void Evaluator::prepare_geometry(std::uint64_t generation, const double* reference_positions,
+                                 std::size_t num_positions, const double* reference_xyz, std::size_t num_xyz,
+                                 const double* cell, const double* inverse_cell, const int* pbc, bool fractional)
+{
+    if (fractional) {
+        if (!(pbc[0] && pbc[1] && pbc[2]))
+            throw std::invalid_argument("Fractional Execution R1 geometry requires a fully periodic cell.");
+        const double det = determinant3(cell);
+        if (!std::isfinite(det) || det == 0.0)
+            throw std::invalid_argument("Fractional Execution R1 cell matrix must be invertible.");
+    }
+    if (generation == 0 || generation != generation_)
+        throw std::invalid_argument("Execution R1 geometry requires the current prepared graph token.");
+    const std::size_t N = num_nodes_, E = static_cast<std::size_t>(num_edges_);
+    if (num_positions != 3 * N || num_xyz != 3 * E)
+        throw std::invalid_argument("Execution R1 prepared geometry extents are inconsistent.");
+    if (!all_finite(reference_positions, num_positions) || !all_finite(reference_xyz, num_xyz) ||
+        !all_finite(cell, 9) || !all_finite(inverse_cell, 9))
+        throw std::invalid_argument("Execution R1 prepared geometry contains a non-finite value.");
+    geometry_mode_ = kGeometryNone;
+    upload(geo_positions_, std::vector<double>(reference_positions, reference_positions + num_positions), stream_);
+    upload(geo_edges_, std::vector<double>(reference_xyz, reference_xyz + num_xyz), stream_);
+    set_cell(cell, inverse_cell);
+    geometry_pbc_ = (pbc[0] ? 1 : 0) | (pbc[1] ? 2 : 0) | (pbc[2] ? 4 : 0);
+    geometry_mode_ = fractional ? kGeometryFractional : kGeometryCartesian;
+    geometry_generation_ = generation_;
+}
+
+// Positions plus integer cell shifts per edge (reference
+// prepare_factorized_shift_geometry, mace_kokkos_factorized_lifecycle.cpp:2570-2697):
+// 12 bytes per edge instead of 24.  The reference accepts it only for its
+// tiled plans; here both plans form edge vectors from it.
+void Evaluator::prepare_shift_geometry(std::uint64_t generation, const double* reference_positions,
+                                       std::size_t num_positions, const int* shifts, std::size_t num_shifts,
+                                       const double* cell, const double* inverse_cell, const int* pbc)
+{
+    if (generation == 0 || generation != generation_)
+        throw std::invalid_argument("Shift geometry requires the current prepared graph token.");
+    const std::size_t N = num_nodes_, E = static_cast<std::size_t>(num_edges_);
+    if (num_positions != 3 * N || num_shifts != 3 * E)
+        throw std::invalid_argument("Shift geometry extents are inconsistent.");
+    if (!all_finite(reference_positions, num_positions) || !all_finite(cell, 9) || !all_finite(inverse_cell, 9))
+        throw std::invalid_argument("Shift geometry contains a non-finite value.");
+    geometry_mode_ = kGeometryNone;
+    upload(geo_positions_, std::vector<double>(reference_positions, reference_positions + num_positions), stream_);
+    upload(geo_shifts_, std::vector<int>(shifts, shifts + num_shifts), stream_);
+    set_cell(cell, inverse_cell);
+    geometry_pbc_ = (pbc[0] ? 1 : 0) | (pbc[1] ? 2 : 0) | (pbc[2] ? 4 : 0);
+    geometry_mode_ = kGeometryShifts;
+    geometry_generation_ = generation_;
+}
+
+void Evaluator::validate_graph_cardinality(std::uint64_t num_receivers, std::uint64_t num_feature_nodes,
+                                           std::uint64_t num_edges) const
+{
+    constexpr std::uint64_t int_max = static_cast<std::uint64_t>(std::numeric_limits<int>::max());
+    if (num_receivers >= int_max)
+        throw std::length_error("MACE graph atom count " + std::to_string(num_receivers) +
+                                " exceeds the 32-bit CSR limit " + std::to_string(int_max - 1) + ".");
+    if (num_feature_nodes >= int_max)
+        throw std::length_error("MACE graph feature-node count " + std::to_string(num_feature_nodes) +
+                                " exceeds the 32-bit CSR limit " + std::to_string(int_max - 1) + ".");
+    if (num_feature_nodes < num_receivers)
+        throw std::invalid_argument("MACE graph feature-node count is smaller than its receiver count.");
+    if (num_edges > int_max)
+        throw std::length_error("MACE graph directed-edge count " + std::to_string(num_edges) +
+                                " exceeds the 32-bit topology limit " + std::to_string(int_max) + ".");
+}
+
+GeometryRef Evaluator::geometry_ref() const
+{
+    GeometryRef g;
+    if (geometry_mode_ == kGeometryBuilt) {
+        g.positions = pgraph_.fractional_positions.as<double>();
+        g.edges = pgraph_.fractional_xyz.as<double>();
+        g.fractional = 1;
+        g.pbc = 7;
+        return g;
+    }
+    g.positions = geo_positions_.as<double>();
+    if (geometry_mode_ == kGeometryShifts)
+        g.shifts = geo_shifts_.as<int>();
+    else
+        g.edges = geo_edges_.as<double>();
+    g.fractional = geometry_mode_ == kGeometryFractional ? 1 : 0;
+    g.pbc = geometry_pbc_;
+    return g;
+}
+
+void Evaluator::require_geometry(std::uint64_t generation) const
+{
+    check_generation(generation);
+    if (geometry_mode_ == kGeometryNone || geometry_generation_ != generation_)
+        throw std::invalid_argument("Execution R1 positions require current graph and geometry tokens.");
 }
 
 void Evaluator::graph_arrays(std::uint64_t generation, int* num_neigh, int* receiver_offsets, int* sources,
@@ -1172,8 +1314,7 @@ void Evaluator::graph_arrays(std::uint64_t generation, int* num_neigh, int* rece
 
 void Evaluator::compute_positions(std::uint64_t generation, const double* positions, bool device_positions)
 {
-    check_generation(generation);
-    if (!periodic_) throw std::invalid_argument("positions require a periodic graph; use edge vectors instead");
+    require_geometry(generation);
     const int N = num_nodes_;
     if (N > 0 && positions != positions_.as<double>())
         hip_check(hipMemcpyAsync(positions_.as<double>(), positions, N * 3 * sizeof(double),
@@ -1182,12 +1323,12 @@ void Evaluator::compute_positions(std::uint64_t generation, const double* positi
     for (int i = 0; i < kNumStages; ++i) stage_used_[i] = false;
     mark(kStageGeometry, false);
     const double* cell = cell_dev_.as<double>();
-    hip_check(launch_atom_displacements(N, positions_.as<double>(), pgraph_.fractional_positions.as<double>(), cell,
-                                        cell + 9, disp_.as<double>(), totals_.as<double>() + 12, stream_),
+    const GeometryRef ref = geometry_ref();
+    hip_check(launch_atom_displacements(N, positions_.as<double>(), ref, cell, cell + 9, disp_.as<double>(),
+                                        totals_.as<double>() + 12, stream_),
               "displacements");
-    hip_check(launch_edge_geometry(static_cast<int>(num_edges_), receiver_.as<int>(), source_.as<int>(),
-                                   pgraph_.fractional_xyz.as<double>(), disp_.as<double>(), cell, model_.r_cut,
-                                   xyz_.as<double>(), r_.as<double>(),
+    hip_check(launch_edge_geometry(static_cast<int>(num_edges_), receiver_.as<int>(), source_.as<int>(), ref,
+                                   disp_.as<double>(), cell, model_.r_cut, xyz_.as<double>(), r_.as<double>(),
                                    reinterpret_cast<unsigned long long*>(totals_.as<double>() + 13), stream_),
               "edge geometry");
     mark(kStageGeometry, true);
@@ -1211,16 +1352,15 @@ void Evaluator::compute_xyz(std::uint64_t generation, const double* xyz, const d
 
 double Evaluator::max_displacement(std::uint64_t generation, const double* positions, bool device_positions)
 {
-    check_generation(generation);
-    if (!periodic_) throw std::invalid_argument("displacements require a periodic graph");
+    require_geometry(generation);
     const int N = num_nodes_;
     if (N > 0 && positions != positions_.as<double>())
         hip_check(hipMemcpyAsync(positions_.as<double>(), positions, N * 3 * sizeof(double),
                                  device_positions ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, stream_),
                   "positions");
     const double* cell = cell_dev_.as<double>();
-    hip_check(launch_atom_displacements(N, positions_.as<double>(), pgraph_.fractional_positions.as<double>(), cell,
-                                        cell + 9, disp_.as<double>(), totals_.as<double>() + 12, stream_),
+    hip_check(launch_atom_displacements(N, positions_.as<double>(), geometry_ref(), cell, cell + 9,
+                                        disp_.as<double>(), totals_.as<double>() + 12, stream_),
               "displacement");
     double d2 = 0.0;
     hip_check(hipMemcpyAsync(&d2, totals_.as<double>() + 12, sizeof(double), hipMemcpyDeviceToHost, stream_),

@@ -157,6 +157,24 @@ public:
                                          bool device_positions, const double* cell,
                                          const double* inverse_cell, double cutoff);
     void update_cell(std::uint64_t generation, const double* cell, const double* inverse_cell);
+    // Reference geometry of the prepared graph for evaluations from positions
+    // (reference prepare_factorized_geometry / _fractional_geometry /
+    // _shift_geometry, mace_kokkos_factorized_lifecycle.cpp:2455-2733): the
+    // positions [N][3] and edge vectors [E][3] at which the caller built its
+    // graph (Cartesian, or fractional in a fully periodic cell), or the
+    // positions and integer cell shifts [E][3] of its edges; pbc [3] marks the
+    // periodic lattice axes.  Sizes are the arrays' element counts.  A graph
+    // built on the device carries its own (fractional) geometry.
+    void prepare_geometry(std::uint64_t generation, const double* reference_positions, std::size_t num_positions,
+                          const double* reference_xyz, std::size_t num_xyz, const double* cell,
+                          const double* inverse_cell, const int* pbc, bool fractional);
+    void prepare_shift_geometry(std::uint64_t generation, const double* reference_positions,
+                                std::size_t num_positions, const int* shifts, std::size_t num_shifts,
+                                const double* cell, const double* inverse_cell, const int* pbc);
+    // 32-bit cardinality and extent checks of a graph before it is prepared
+    // (reference validate_graph_cardinality, mace_kokkos_runtime.cpp:199-260).
+    void validate_graph_cardinality(std::uint64_t num_receivers, std::uint64_t num_feature_nodes,
+                                    std::uint64_t num_edges) const;
     long long num_edges() const { return num_edges_; }
     int num_nodes() const { return num_nodes_; }
     std::uint64_t generation() const { return generation_; }
@@ -286,6 +304,15 @@ private:
     void upload_cell();
     void finish_evaluation();
     DeviceBuffer xyz_, r_;
+    // reference geometry for evaluations from positions (see prepare_geometry)
+    enum GeometryMode { kGeometryNone = 0, kGeometryBuilt, kGeometryCartesian, kGeometryFractional, kGeometryShifts };
+    GeometryMode geometry_mode_ = kGeometryNone;
+    std::uint64_t geometry_generation_ = 0;
+    int geometry_pbc_ = 7;
+    DeviceBuffer geo_positions_, geo_edges_, geo_shifts_;
+    GeometryRef geometry_ref() const;
+    void require_geometry(std::uint64_t generation) const;
+    void set_cell(const double* cell, const double* inverse_cell);
 
     // workspace
     DeviceBuffer A0_, M0_, H1_, Phi1_, A1_, A1adj_, direct_, H1adj_, msg_, energies_, forces_,

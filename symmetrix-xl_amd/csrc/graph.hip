@@ -318,39 +318,47 @@ __global__ void __launch_bounds__(kSortThreads) sort_segments_kernel(int nseg, c
     }
 }
 
-// Minimum-image displacement of every atom from its reference position,
-// the build's fractional position in the current cell (reference
+// Displacement of every atom from its reference position (reference
 // prepared_atom_displacements, mace_kokkos_factorized_lifecycle.cpp:2986-3023):
-// delta = pos - frac_ref cell, f = delta cell^-1, f -= floor(f + 1/2),
-// disp = f cell.  out[0] collects max |disp|^2 (as ordered bits; non-finite:
-// infinite).
-__global__ void atom_displacements_kernel(int n, const double* __restrict__ pos,
-                                          const double* __restrict__ frac_ref, const double* __restrict__ cell,
+// delta = pos - ref (ref = frac_ref cell for fractional reference positions);
+// with any periodic axis, f = delta cell^-1, f -= floor(f + 1/2) on the
+// periodic axes, disp = f cell; without, disp = delta.  out[0] collects
+// max |disp|^2 (as ordered bits; non-finite: infinite).
+__global__ void atom_displacements_kernel(int n, const double* __restrict__ pos, GeometryRef g,
+                                          const double* __restrict__ cell,
                                           const double* __restrict__ inverse_cell, double* __restrict__ disp,
                                           unsigned long long* __restrict__ out)
 {
     __shared__ double s[256];
     const int t = threadIdx.x;
+    const double* __restrict__ ref = g.positions;
     double m = 0.0;
     for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + t; i < static_cast<size_t>(n);
          i += static_cast<size_t>(gridDim.x) * blockDim.x) {
         double delta[3], f[3], d[3];
         for (int c = 0; c < 3; ++c) {
-            double reference = 0.0;
-            for (int axis = 0; axis < 3; ++axis) reference += frac_ref[3 * i + axis] * cell[3 * axis + c];
+            double reference = ref[3 * i + c];
+            if (g.fractional) {
+                reference = 0.0;
+                for (int axis = 0; axis < 3; ++axis) reference += ref[3 * i + axis] * cell[3 * axis + c];
+            }
             delta[c] = pos[3 * i + c] - reference;
         }
-        for (int axis = 0; axis < 3; ++axis) {
-            double v = 0.0;
-            for (int c = 0; c < 3; ++c) v += delta[c] * inverse_cell[3 * c + axis];
-            f[axis] = v - floor(v + 0.5);
+        if (g.pbc == 0) {
+            for (int c = 0; c < 3; ++c) d[c] = delta[c];
+        } else {
+            for (int axis = 0; axis < 3; ++axis) {
+                double v = 0.0;
+                for (int c = 0; c < 3; ++c) v += delta[c] * inverse_cell[3 * c + axis];
+                f[axis] = (g.pbc >> axis) & 1 ? v - floor(v + 0.5) : v;
+            }
+            for (int c = 0; c < 3; ++c) {
+                double v = 0.0;
+                for (int axis = 0; axis < 3; ++axis) v += f[axis] * cell[3 * axis + c];
+                d[c] = v;
+            }
         }
-        for (int c = 0; c < 3; ++c) {
-            double v = 0.0;
-            for (int axis = 0; axis < 3; ++axis) v += f[axis] * cell[3 * axis + c];
-            d[c] = v;
-            disp[3 * i + c] = v;
-        }
+        for (int c = 0; c < 3; ++c) disp[3 * i + c] = d[c];
         const double d2 = d[0] * d[0] + d[1] * d[1] + d[2] * d[2];
         m = d2 > m ? d2 : m;
         if (!(d2 == d2) || d2 > 1.0e300) m = __longlong_as_double(0x7ff0000000000000LL);
@@ -519,16 +527,15 @@ hipError_t launch_sort_segments(int num_segments, const int* offsets, int* value
     return hipGetLastError();
 }
 
-hipError_t launch_atom_displacements(int n, const double* positions, const double* reference_fractional,
-                                     const double* cell, const double* inverse_cell, double* displacements,
-                                     double* out, hipStream_t s)
+hipError_t launch_atom_displacements(int n, const double* positions, const GeometryRef& ref, const double* cell,
+                                     const double* inverse_cell, double* displacements, double* out, hipStream_t s)
 {
     // out[0]: max |disp|^2, out[1]: invalid-edge count of the edge geometry that follows
     hipError_t err = hipMemsetAsync(out, 0, 2 * sizeof(double), s);
     if (err != hipSuccess || n <= 0) return err;
     const int blocks = std::min((n + 255) / 256, 1024);
-    atom_displacements_kernel<<<blocks, 256, 0, s>>>(n, positions, reference_fractional, cell, inverse_cell,
-                                                     displacements, reinterpret_cast<unsigned long long*>(out));
+    atom_displacements_kernel<<<blocks, 256, 0, s>>>(n, positions, ref, cell, inverse_cell, displacements,
+                                                     reinterpret_cast<unsigned long long*>(out));
     return hipGetLastError();
 }
 

@@ -241,13 +241,29 @@ struct ZblArgs {
 hipError_t launch_zbl(int num_nodes, const int* first, const int* edge_pair, const double* xyz, const double* r,
                       const ZblArgs& z, double* energies, double* forces, hipStream_t s);
 
+// Reference geometry of a prepared graph (reference
+// prepare_factorized_geometry / _fractional_geometry / _shift_geometry,
+// mace_kokkos_factorized_lifecycle.cpp:2455-2733): an edge's current vector
+// is its reference vector plus disp[src] - disp[recv], disp being each atom's
+// displacement from its reference position, wrapped to the minimum image
+// along the periodic axes.  Reference edge vectors are given directly
+// (`edges`, fractional or Cartesian) or as integer cell shifts:
+// pos_ref[src] - pos_ref[recv] + shift . cell (Cartesian positions).
+struct GeometryRef {
+    const double* positions = nullptr;  // [N][3] reference positions (fractional coordinates when fractional)
+    const double* edges = nullptr;      // [E][3] reference edge vectors (fractional when fractional), or null
+    const int* shifts = nullptr;        // [E][3] integer cell shifts when edges is null
+    int fractional = 0;
+    int pbc = 7;                        // bit a set: lattice axis a is periodic
+};
+
 // Geometry from positions (reference prepared_edge_geometry,
-// mace_kokkos_factorized_lifecycle.cpp:3024-3074): xyz = fractional_xyz . cell
-// + disp[src] - disp[recv]; an edge of zero or non-finite length is set to
-// (r_cut, 0, 0) (inactive) and counted in *invalid.
-hipError_t launch_edge_geometry(int num_edges, const int* receiver, const int* source,
-                                const double* fractional_xyz, const double* displacements, const double* cell,
-                                double r_cut, double* xyz, double* r, unsigned long long* invalid, hipStream_t s);
+// mace_kokkos_factorized_lifecycle.cpp:3024-3074): xyz = reference edge
+// vector + disp[src] - disp[recv]; an edge of zero or non-finite length is
+// set to (r_cut, 0, 0) (inactive) and counted in *invalid.
+hipError_t launch_edge_geometry(int num_edges, const int* receiver, const int* source, const GeometryRef& ref,
+                                const double* displacements, const double* cell, double r_cut, double* xyz, double* r,
+                                unsigned long long* invalid, hipStream_t s);
 
 // Reductions (deterministic, f64)
 hipError_t launch_atom_forces(int num_nodes, const int* first, const int* tfirst, const int* tedge,
@@ -305,12 +321,12 @@ hipError_t launch_md_kick(int num_atoms, double* v, const double* f, const doubl
 int md_kinetic_partials(int num_atoms);
 hipError_t launch_md_kinetic(int num_atoms, const double* v, const double* m, double* partials, int num_partials,
                              double* out, hipStream_t s);
-// Minimum-image displacements of the atoms from their reference fractional
-// positions in the current cell; out[0] = max |disp|^2, out[1] zeroed (the
+// Displacements of the atoms from their reference positions (ref.positions,
+// in the current cell when fractional), wrapped to the minimum image along
+// the periodic axes of ref.pbc; out[0] = max |disp|^2, out[1] zeroed (the
 // invalid-edge count of launch_edge_geometry).
-hipError_t launch_atom_displacements(int n, const double* positions, const double* reference_fractional,
-                                     const double* cell, const double* inverse_cell, double* displacements,
-                                     double* out, hipStream_t s);
+hipError_t launch_atom_displacements(int n, const double* positions, const GeometryRef& ref, const double* cell,
+                                     const double* inverse_cell, double* displacements, double* out, hipStream_t s);
 // edge_pair[e] = ordered | unordered << 16 from the active indices of the
 // receiver and source element types (unordered = 0 with shared tables)
 hipError_t launch_edge_pairs(int num_edges, const int* receiver, const int* source,

@@ -1068,7 +1068,7 @@ __global__ void add_direct_kernel(int nodes, int C, int nLM, const float* __rest
 // geometry and reductions
 // ---------------------------------------------------------------------------
 __global__ void edge_geometry_kernel(int E, const int* __restrict__ receiver,
-                                     const int* __restrict__ source, const double* __restrict__ frac,
+                                     const int* __restrict__ source, GeometryRef g,
                                      const double* __restrict__ disp, const double* __restrict__ cell,
                                      double r_cut, double* __restrict__ xyz, double* __restrict__ r,
                                      unsigned long long* __restrict__ invalid)
@@ -1076,11 +1076,26 @@ __global__ void edge_geometry_kernel(int E, const int* __restrict__ receiver,
     const int e = blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= E) return;
     const size_t i = receiver[e], j = source[e];
-    const double f0 = frac[3 * static_cast<size_t>(e)], f1 = frac[3 * static_cast<size_t>(e) + 1],
-                 f2 = frac[3 * static_cast<size_t>(e) + 2];
+    double ref[3];
+    if (g.edges) {
+        const double f0 = g.edges[3 * static_cast<size_t>(e)], f1 = g.edges[3 * static_cast<size_t>(e) + 1],
+                     f2 = g.edges[3 * static_cast<size_t>(e) + 2];
+        if (g.fractional) {
+            for (int c = 0; c < 3; ++c) ref[c] = f0 * cell[c] + f1 * cell[3 + c] + f2 * cell[6 + c];
+        } else {
+            ref[0] = f0, ref[1] = f1, ref[2] = f2;
+        }
+    } else {
+        // reference edge from the reference positions and the cell shift
+        // (single_layer_tiled_edge_geometry, mace_kokkos_factorized_lifecycle.cpp:1858-1866)
+        const int* sh = g.shifts + 3 * static_cast<size_t>(e);
+        for (int c = 0; c < 3; ++c) {
+            ref[c] = g.positions[3 * j + c] - g.positions[3 * i + c];
+            for (int axis = 0; axis < 3; ++axis) ref[c] += static_cast<double>(sh[axis]) * cell[3 * axis + c];
+        }
+    }
     double v[3];
-    for (int c = 0; c < 3; ++c)
-        v[c] = (f0 * cell[c] + f1 * cell[3 + c] + f2 * cell[6 + c]) + disp[3 * j + c] - disp[3 * i + c];
+    for (int c = 0; c < 3; ++c) v[c] = ref[c] + disp[3 * j + c] - disp[3 * i + c];
     const double d2 = v[0] * v[0] + v[1] * v[1] + v[2] * v[2];
     if (!(d2 > 0.0) || !(d2 < 1.0e300)) {
         atomicAdd(invalid, 1ull);
@@ -1353,13 +1368,14 @@ hipError_t launch_zbl(int num_nodes, const int* first, const int* edge_pair, con
     return hipGetLastError();
 }
 
-hipError_t launch_edge_geometry(int num_edges, const int* receiver, const int* source,
-                                const double* fractional_xyz, const double* displacements, const double* cell,
-                                double r_cut, double* xyz, double* r, unsigned long long* invalid, hipStream_t s)
+hipError_t launch_edge_geometry(int num_edges, const int* receiver, const int* source, const GeometryRef& ref,
+                                const double* displacements, const double* cell, double r_cut, double* xyz, double* r,
+                                unsigned long long* invalid, hipStream_t s)
 {
     if (num_edges <= 0) return hipSuccess;
-    edge_geometry_kernel<<<(num_edges + 255) / 256, 256, 0, s>>>(num_edges, receiver, source, fractional_xyz,
-                                                                 displacements, cell, r_cut, xyz, r, invalid);
+    if (!ref.edges && !(ref.shifts && ref.positions)) return hipErrorInvalidValue;
+    edge_geometry_kernel<<<(num_edges + 255) / 256, 256, 0, s>>>(num_edges, receiver, source, ref, displacements,
+                                                                 cell, r_cut, xyz, r, invalid);
     return hipGetLastError();
 }
 

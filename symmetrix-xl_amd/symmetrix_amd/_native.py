@@ -66,6 +66,13 @@ SIGNATURES = {
     "sxl_graph_arrays": (ctypes.c_int, [ctypes.c_void_p, c_u64, c_int_p, c_int_p, c_int_p, c_int_p,
                                         c_double_p]),
     "sxl_update_cell": (ctypes.c_int, [ctypes.c_void_p, c_u64, c_double_p, c_double_p]),
+    "sxl_validate_graph_cardinality": (ctypes.c_int, [ctypes.c_void_p, c_i64, c_i64, c_i64]),
+    "sxl_prepare_geometry": (ctypes.c_int, [ctypes.c_void_p, c_u64, c_double_p, c_i64, c_double_p, c_i64,
+                                            c_double_p, c_double_p, c_int_p]),
+    "sxl_prepare_fractional_geometry": (ctypes.c_int, [ctypes.c_void_p, c_u64, c_double_p, c_i64, c_double_p,
+                                                       c_i64, c_double_p, c_double_p, c_int_p]),
+    "sxl_prepare_shift_geometry": (ctypes.c_int, [ctypes.c_void_p, c_u64, c_double_p, c_i64, c_int_p, c_i64,
+                                                  c_double_p, c_double_p, c_int_p]),
     "sxl_compute_prepared_positions": (ctypes.c_int, [ctypes.c_void_p, c_u64, c_double_p]),
     "sxl_compute_prepared_positions_device": (ctypes.c_int, [ctypes.c_void_p, c_u64, ctypes.c_void_p]),
     "sxl_compute_prepared": (ctypes.c_int, [ctypes.c_void_p, c_u64, c_double_p, c_double_p]),

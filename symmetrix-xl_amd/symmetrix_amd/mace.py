@@ -152,6 +152,52 @@ class MACEKokkosFloat:
         check(library().sxl_update_cell(self._h, c_u64(int(generation)), _p(c, ctypes.c_double),
                                         _p(ic, ctypes.c_double)))
 
+    def _validate_graph_cardinality(self, num_receivers, num_feature_nodes, num_edges):
+        """32-bit cardinality checks (reference ``_validate_graph_cardinality``,
+        mace_kokkos.cpp:1604-1607): OverflowError (length_error) or ValueError."""
+        check(library().sxl_validate_graph_cardinality(self._h, int(num_receivers), int(num_feature_nodes),
+                                                       int(num_edges)))
+
+    def _geometry_arrays(self, positions, second, cell, inverse_cell, pbc, second_kind):
+        pos = np.ascontiguousarray(np.asarray(positions, dtype=np.float64).reshape(-1))
+        if second_kind == "shifts":
+            other = np.ascontiguousarray(np.asarray(second, dtype=np.int32).reshape(-1))
+            other_p = _p(other, ctypes.c_int)
+        else:
+            other = np.ascontiguousarray(np.asarray(second, dtype=np.float64).reshape(-1))
+            other_p = _p(other, ctypes.c_double)
+        c = _f64(cell, 9, "cell")
+        ic = _f64(inverse_cell, 9, "inverse_cell")
+        pb = _i32(pbc, 3, "pbc")
+        keep = (pos, other, c, ic, pb)
+        return keep, (_p(pos, ctypes.c_double), pos.size, other_p, other.size, _p(c, ctypes.c_double),
+                      _p(ic, ctypes.c_double), _p(pb, ctypes.c_int))
+
+    def _prepare_factorized_geometry(self, execution_graph_generation, reference_positions, reference_xyz, cell,
+                                     inverse_cell, pbc):
+        """Geometry of a caller's graph for evaluations from positions: the
+        positions and edge vectors at which it was built (reference
+        ``_prepare_factorized_geometry``, mace_kokkos.cpp:1608-1629)."""
+        keep, args = self._geometry_arrays(reference_positions, reference_xyz, cell, inverse_cell, pbc, "xyz")
+        check(library().sxl_prepare_geometry(self._h, c_u64(int(execution_graph_generation)), *args))
+        del keep
+
+    def _prepare_factorized_fractional_geometry(self, execution_graph_generation, fractional_positions,
+                                                fractional_xyz, cell, inverse_cell, pbc):
+        """As ``_prepare_factorized_geometry`` in fractional coordinates of a
+        fully periodic cell (reference mace_kokkos.cpp:1650-1669)."""
+        keep, args = self._geometry_arrays(fractional_positions, fractional_xyz, cell, inverse_cell, pbc, "xyz")
+        check(library().sxl_prepare_fractional_geometry(self._h, c_u64(int(execution_graph_generation)), *args))
+        del keep
+
+    def _prepare_factorized_shift_geometry(self, execution_graph_generation, reference_positions, shifts, cell,
+                                           inverse_cell, pbc):
+        """As ``_prepare_factorized_geometry`` with integer cell shifts per
+        edge in place of edge vectors (reference mace_kokkos.cpp:1630-1649)."""
+        keep, args = self._geometry_arrays(reference_positions, shifts, cell, inverse_cell, pbc, "shifts")
+        check(library().sxl_prepare_shift_geometry(self._h, c_u64(int(execution_graph_generation)), *args))
+        del keep
+
     def _graph_size(self):
         n = ctypes.c_int(0)
         e = c_i64(0)

@@ -1,6 +1,10 @@
 """GPU parity on the benchmark configurations at their full sizes, and on the
 degenerate inputs the reference's tests exercise.
 
+- headline: the 89-element medium model on SrTiO3 10^3 (5,000 atoms,
+  BASELINE configs[1]), the workload bench.py times;
+- the wide shape carrying the reference's own 215 coupling terms
+  (jit_r1_mace_mp0b2_large_contract.json) on 300 water molecules;
 - irregular: 20,000 atoms uniform at 0.08 /A^3 with 1.8 A minimum separation,
   10 elements, the 89-element medium-shape model: a
   wide neighbour-count distribution and 100 ordered element pairs;
@@ -59,10 +63,53 @@ def _full_size_check(oracle_lib, path, model, s, label):
         np.testing.assert_allclose(sigma, sigma.T, atol=1e-9)
 
 
-def test_irregular_config_full_size(oracle_lib, tmp_path_factory):
+@pytest.fixture(scope="module")
+def medium(tmp_path_factory):
+    return _model(tmp_path_factory, "medium")
+
+
+def test_headline_config_full_size(oracle_lib, medium):
+    # the workload bench.py times: the 89-element medium model on the perturbed
+    # SrTiO3 10^3 supercell, sigma 0.05 A, seed 0
     from symmetrix_amd import synthetic
 
-    path, model = _model(tmp_path_factory, "medium")
+    path, model = medium
+    s = synthetic.srtio3_supercell(10, sigma=0.05, seed=0)
+    _full_size_check(oracle_lib, path, model, s, "SrTiO3 10^3, medium model (89 elements, 3 active)")
+
+
+def test_wide_model_with_reference_coupling_values(oracle_lib, tmp_path):
+    # the wide (3,2) shape with the coupling terms of the reference's own
+    # contract (tests/golden, from symmetrix/test/data/execution_contracts/
+    # jit_r1_mace_mp0b2_large_contract.json: 17 paths, 215 terms) in place of
+    # the generated ones
+    import dataclasses
+    import os
+
+    from symmetrix_amd import synthetic
+
+    golden = os.path.join(os.path.dirname(__file__), "golden", "jit_r1_mace_mp0b2_large_contract.json")
+    with open(golden) as f:
+        contract = json.load(f)
+    shape = dataclasses.replace(synthetic.PRESETS["wide"], channels=128)
+    model = json.loads(synthetic.model_json(synthetic.random_mace_model(shape, seed=5)))
+    assert [(l1, l2, lo) for l1, l2, lo in zip(model["Phi1_l1"], model["Phi1_l2"], model["Phi1_l"])] == [
+        (p["edge_l"], p["source_l"], p["output_l"]) for p in contract["paths"]]
+    terms = contract["sparse_coupling"]["terms"]
+    assert len(terms) == 215
+    model["Phi1_lme"] = [t["lme"] for t in terms]
+    model["Phi1_lelm1lm2"] = [t["row"] for t in terms]
+    model["Phi1_clebsch_gordan"] = [t["coefficient"] for t in terms]
+    path = tmp_path / "wide_contract.json"
+    path.write_text(json.dumps(model))
+    s = synthetic.water_box(300, seed=2)
+    _full_size_check(oracle_lib, str(path), model, s, "water 300 H2O, wide shape with the reference's 215 coupling terms")
+
+
+def test_irregular_config_full_size(oracle_lib, medium):
+    from symmetrix_amd import synthetic
+
+    path, model = medium
     s = synthetic.irregular_box(seed=0)
     _full_size_check(oracle_lib, path, model, s, "irregular box, medium model (89 elements, 10 active)")
 
