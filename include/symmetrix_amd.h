@@ -262,6 +262,34 @@ int sxl_neighbor_graph_build(const double* positions, int num_nodes, const doubl
 int sxl_neighbor_graph_copy(const sxl_graph* graph, int* num_neigh, int* receiver_offsets, int* sources,
                             int* shifts, double* fractional_xyz);
 void sxl_neighbor_graph_free(sxl_graph* graph);
+
+/* No counterpart in the reference.  An allocation-free variant of
+ * sxl_neighbor_graph_build for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc): the same kernels and the same, bit-identical, edge list, with
+ * the positions [N][3] and every output in the caller's device memory --
+ * receiver_offsets [N+1], sources [edge_capacity], shifts and
+ * fractional_xyz [edge_capacity][3] -- and the build's intermediate arrays
+ * in one fixed device array of the library (SXL_NOALLOC_SCRATCH_BYTES per
+ * GPU, held until the process ends).  No hipMalloc, hipFree or allocating
+ * library call is made.  cell and inverse_cell are host arrays.  At most
+ * SXL_NOALLOC_MAX_ATOMS atoms and SXL_NOALLOC_MAX_BINS cell bins (cell face
+ * height / cutoff per axis, multiplied); more is a length error.  *num_edges
+ * receives the edge count; when it exceeds edge_capacity the call returns a
+ * length error and writes no output array (call again with larger arrays).
+ * The work runs on `stream` (a hipStream_t; NULL: the default stream) and has
+ * completed when the call returns.  All calls on one GPU share the library's
+ * array: calls that overlap on one GPU (other threads, other streams) race. */
+#define SXL_NOALLOC_MAX_ATOMS 131072
+#define SXL_NOALLOC_MAX_BINS 262144
+#define SXL_NOALLOC_SCRATCH_BYTES 18353408 /* about 17.5 MiB */
+int sxl_neighbor_graph_build_noalloc(const double* d_positions, int num_nodes, const double* cell,
+                                     const double* inverse_cell, double cutoff, int64_t edge_capacity,
+                                     int* d_receiver_offsets, int* d_sources, int* d_shifts, double* d_fractional_xyz,
+                                     int64_t* num_edges, void* stream);
+/* Limits of sxl_neighbor_graph_build_noalloc (atoms and bins, may be NULL);
+ * returns the bytes of its device array (SXL_NOALLOC_SCRATCH_BYTES). */
+int64_t sxl_neighbor_graph_noalloc_limits(int* max_atoms, int* max_bins);
 int sxl_stats(const sxl_evaluator* evaluator, sxl_stats_t* out);
 /* Stage profiling: with enable != 0 every evaluation records HIP events
  * around each stage on the evaluator's stream (counters reset).  The

@@ -481,6 +481,36 @@ int sxl_neighbor_graph_copy(const sxl_graph* g, int* num_neigh, int* receiver_of
 
 void sxl_neighbor_graph_free(sxl_graph* graph) { delete graph; }
 
+int sxl_neighbor_graph_build_noalloc(const double* d_positions, int num_nodes, const double* cell,
+                                     const double* inverse_cell, double cutoff, int64_t edge_capacity,
+                                     int* d_receiver_offsets, int* d_sources, int* d_shifts, double* d_fractional_xyz,
+                                     int64_t* num_edges, void* stream)
+{
+    if (!cell || !inverse_cell || !num_edges || !d_receiver_offsets || (num_nodes > 0 && !d_positions) ||
+        (edge_capacity > 0 && (!d_sources || !d_shifts || !d_fractional_xyz)))
+        return null_handle();
+    *num_edges = 0;
+    return guarded([&] {
+        long long edges = 0;
+        try {
+            sxl::build_periodic_graph_noalloc(d_positions, num_nodes, cell, inverse_cell, cutoff, edge_capacity,
+                                              d_receiver_offsets, d_sources, d_shifts, d_fractional_xyz, &edges,
+                                              static_cast<hipStream_t>(stream));
+        } catch (...) {
+            *num_edges = edges;
+            throw;
+        }
+        *num_edges = edges;
+    });
+}
+
+int64_t sxl_neighbor_graph_noalloc_limits(int* max_atoms, int* max_bins)
+{
+    if (max_atoms) *max_atoms = sxl::kNoAllocMaxAtoms;
+    if (max_bins) *max_bins = sxl::kNoAllocMaxBins;
+    return static_cast<int64_t>(sxl::noalloc_scratch_bytes());
+}
+
 int sxl_set_profiling_stages(sxl_evaluator* ev, uint32_t mask)
 {
     if (!ev) return null_handle();

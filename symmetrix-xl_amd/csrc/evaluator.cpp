@@ -992,12 +992,11 @@ void validate_periodic_inputs(int num_nodes, const double* cell, const double* i
         }
 }
 
-void build_periodic_graph(const double* d_positions, int num_nodes, const double* cell, const double* inverse_cell,
-                          double cutoff, hipStream_t stream, PeriodicGraph& out)
+NeighborPlan neighbor_plan(int num_nodes, const double* cell, const double* inverse_cell, double cutoff)
 {
     validate_periodic_inputs(num_nodes, cell, inverse_cell, cutoff);
-    const int N = num_nodes;
     NeighborPlan plan;
+    const int N = num_nodes;
     plan.num_nodes = N;
     std::memcpy(plan.cell, cell, sizeof(plan.cell));
     std::memcpy(plan.inverse_cell, inverse_cell, sizeof(plan.inverse_cell));
@@ -1023,7 +1022,17 @@ void build_periodic_graph(const double* d_positions, int num_nodes, const double
         static_cast<std::size_t>(plan.bins[0]) * plan.bins[1] * static_cast<std::size_t>(plan.bins[2]);
     if (num_bins_size >= static_cast<std::size_t>(std::numeric_limits<int>::max()))
         throw std::length_error("neighbor graph bin count exceeds 32-bit indexing");
-    const int num_bins = static_cast<int>(num_bins_size);
+    return plan;
+}
+
+int neighbor_plan_bins(const NeighborPlan& plan) { return plan.bins[0] * plan.bins[1] * plan.bins[2]; }
+
+void build_periodic_graph(const double* d_positions, int num_nodes, const double* cell, const double* inverse_cell,
+                          double cutoff, hipStream_t stream, PeriodicGraph& out)
+{
+    const NeighborPlan plan = neighbor_plan(num_nodes, cell, inverse_cell, cutoff);
+    const int N = num_nodes;
+    const int num_bins = neighbor_plan_bins(plan);
     DeviceBuffer wp, wf, wrap, atom_bins, bin_sizes, bin_off64, bin_offsets, bin_atoms, counts, offsets, scratch;
     const std::size_t N3 = static_cast<std::size_t>(std::max(N, 1)) * 3;
     out.fractional_positions.reserve(N3 * sizeof(double));

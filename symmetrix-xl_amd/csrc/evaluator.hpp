@@ -58,6 +58,27 @@ void build_periodic_graph(const double* d_positions, int num_nodes, const double
                           PeriodicGraph& out);
 void validate_periodic_inputs(int num_nodes, const double* cell, const double* inverse_cell,
                               double cutoff);
+// Bins and stencil reach of the cell-binned search (validates like the
+// reference, neighbor_graph_kokkos.cpp:38-166).
+NeighborPlan neighbor_plan(int num_nodes, const double* cell, const double* inverse_cell, double cutoff);
+int neighbor_plan_bins(const NeighborPlan& plan);
+
+// Allocation-free variant of build_periodic_graph for callers that cannot
+// allocate device memory: positions and outputs are the caller's device
+// arrays (receiver_offsets [N+1], sources [capacity], shifts and
+// fractional_xyz [capacity][3]); every intermediate array lives in one
+// fixed device array of the library (graph.hip), which bounds the atoms and
+// cell bins below.  *num_edges receives the edge count; when it exceeds
+// edge_capacity a length error is thrown and only *num_edges is written.
+// The work runs on `stream` and has completed on return.  Calls that overlap
+// on one GPU share that array and race.
+constexpr int kNoAllocMaxAtoms = 1 << 17;
+constexpr int kNoAllocMaxBins = 1 << 18;
+void build_periodic_graph_noalloc(const double* d_positions, int num_nodes, const double* cell,
+                                  const double* inverse_cell, double cutoff, long long edge_capacity,
+                                  int* d_receiver_offsets, int* d_sources, int* d_shifts, double* d_fractional_xyz,
+                                  long long* num_edges, hipStream_t stream);
+std::size_t noalloc_scratch_bytes();
 
 // Placement of a symmetric-contraction polynomial's terms on the kernels'
 // coefficient slots (see PolyArgs): JSON term j -> slot[j].

@@ -14,7 +14,13 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <limits>
+#include <mutex>
+#include <stdexcept>
+#include <string>
 
+#include "../../include/symmetrix_amd.h"
+#include "evaluator.hpp"
 #include "kernels.hpp"
 
 namespace sxl {
@@ -557,6 +563,163 @@ hipError_t launch_tile_runs_fill(int num_nodes, const int* tfirst, const int* te
                                                                   tile_receivers, tile_offsets, tile_cursors,
                                                                   run_source, run_start, run_length);
     return hipGetLastError();
+}
+
+
+// ---------------------------------------------------------------------------
+// Allocation-free neighbour graph (build_periodic_graph_noalloc).  The
+// intermediate arrays of the build (wrapped and fractional positions, bins,
+// per-receiver counts and offsets, scan partials) are carved from one
+// file-scope device array sized for kNoAllocMaxAtoms atoms and
+// kNoAllocMaxBins bins.  Host code never uses the array's name as an address:
+// each device's copy is found once with hipGetSymbolAddress and that pointer
+// is what the kernels receive.  Every region is written before it is read
+// (bin sizes are cleared by a fill kernel), so nothing depends on what an
+// earlier call left there.
+// ---------------------------------------------------------------------------
+namespace noalloc {
+
+constexpr std::size_t align256(std::size_t bytes) { return (bytes + 255) / 256 * 256; }
+constexpr std::size_t kAtoms = kNoAllocMaxAtoms;
+constexpr std::size_t kBins = kNoAllocMaxBins;
+constexpr std::size_t kScanParts = (std::max(kAtoms, kBins) + 1) / kScanSpan + 2;
+// byte offsets of the regions
+constexpr std::size_t kRf = 0;                                           // [N][3] f64
+constexpr std::size_t kWp = kRf + align256(kAtoms * 3 * sizeof(double));  // [N][3] f64
+constexpr std::size_t kWf = kWp + align256(kAtoms * 3 * sizeof(double));  // [N][3] f64
+constexpr std::size_t kWrap = kWf + align256(kAtoms * 3 * sizeof(double));    // [N][3] i32
+constexpr std::size_t kAtomBins = kWrap + align256(kAtoms * 3 * sizeof(int));  // [N] i32
+constexpr std::size_t kBinAtoms = kAtomBins + align256(kAtoms * sizeof(int));  // [N] i32
+constexpr std::size_t kCounts = kBinAtoms + align256(kAtoms * sizeof(int));    // [N] i64
+constexpr std::size_t kOffsets = kCounts + align256(kAtoms * sizeof(long long));  // [N+1] i64
+constexpr std::size_t kBinSizes = kOffsets + align256((kAtoms + 1) * sizeof(long long));  // [B+1] i32
+constexpr std::size_t kBinOff64 = kBinSizes + align256((kBins + 1) * sizeof(int));        // [B+1] i64
+constexpr std::size_t kBinOffsets = kBinOff64 + align256((kBins + 1) * sizeof(long long));  // [B+1] i32
+constexpr std::size_t kScan = kBinOffsets + align256((kBins + 1) * sizeof(int));            // scan partials
+constexpr std::size_t kBytes = kScan + align256(kScanParts * sizeof(long long));
+
+static_assert(kBytes == SXL_NOALLOC_SCRATCH_BYTES && kAtoms == SXL_NOALLOC_MAX_ATOMS && kBins == SXL_NOALLOC_MAX_BINS,
+              "the C header states the allocation-free builder's limits and array size");
+
+}  // namespace noalloc
+
+}  // namespace sxl
+
+// the allocation-free builder's working memory, one copy per device
+static __device__ __align__(256) unsigned char scratch[sxl::noalloc::kBytes];
+
+namespace sxl {
+namespace {
+
+__global__ void fill_i32_kernel(int* __restrict__ out, int n, int value)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = value;
+}
+
+__global__ void copy_i32_kernel(int* __restrict__ out, const int* __restrict__ in, int n)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = in[i];
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+unsigned char* g_scratch_address[kMaxDevices] = {};
+
+// Device address of the current device's copy of `scratch`, looked up once
+// per device with that device current.
+unsigned char* scratch_address()
+{
+    int device = 0;
+    hipError_t err = hipGetDevice(&device);
+    if (err != hipSuccess) throw std::runtime_error(std::string("hipGetDevice: ") + hipGetErrorString(err));
+    if (device < 0 || device >= kMaxDevices) throw std::runtime_error("device index beyond the scratch table");
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_address[device]) {
+        void* p = nullptr;
+        err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || !p)
+            throw std::runtime_error(std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(err));
+        g_scratch_address[device] = static_cast<unsigned char*>(p);
+    }
+    return g_scratch_address[device];
+}
+
+void launch_check(hipError_t err, const char* what)
+{
+    if (err != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(err));
+}
+
+}  // namespace
+
+std::size_t noalloc_scratch_bytes() { return noalloc::kBytes; }
+
+void build_periodic_graph_noalloc(const double* d_positions, int num_nodes, const double* cell,
+                                  const double* inverse_cell, double cutoff, long long edge_capacity,
+                                  int* d_receiver_offsets, int* d_sources, int* d_shifts, double* d_fractional_xyz,
+                                  long long* num_edges, hipStream_t s)
+{
+    const NeighborPlan plan = neighbor_plan(num_nodes, cell, inverse_cell, cutoff);
+    const int N = num_nodes;
+    const int B = neighbor_plan_bins(plan);
+    if (N > kNoAllocMaxAtoms)
+        throw std::length_error("allocation-free neighbor graph holds at most " + std::to_string(kNoAllocMaxAtoms) +
+                                " atoms (got " + std::to_string(N) + ")");
+    if (B > kNoAllocMaxBins)
+        throw std::length_error("allocation-free neighbor graph holds at most " + std::to_string(kNoAllocMaxBins) +
+                                " cell bins (the cell needs " + std::to_string(B) + ")");
+    if (edge_capacity < 0) throw std::invalid_argument("edge capacity must be non-negative");
+    if (N == 0) {
+        // no atoms, no edges: receiver_offsets = [0]
+        fill_i32_kernel<<<1, 64, 0, s>>>(d_receiver_offsets, 1, 0);
+        launch_check(hipGetLastError(), "neighbor graph");
+        launch_check(hipStreamSynchronize(s), "neighbor graph");
+        *num_edges = 0;
+        return;
+    }
+    unsigned char* base = scratch_address();
+    double* rf = reinterpret_cast<double*>(base + noalloc::kRf);
+    double* wp = reinterpret_cast<double*>(base + noalloc::kWp);
+    double* wf = reinterpret_cast<double*>(base + noalloc::kWf);
+    int* wrap = reinterpret_cast<int*>(base + noalloc::kWrap);
+    int* atom_bins = reinterpret_cast<int*>(base + noalloc::kAtomBins);
+    int* bin_atoms = reinterpret_cast<int*>(base + noalloc::kBinAtoms);
+    long long* counts = reinterpret_cast<long long*>(base + noalloc::kCounts);
+    long long* offsets = reinterpret_cast<long long*>(base + noalloc::kOffsets);
+    int* bin_sizes = reinterpret_cast<int*>(base + noalloc::kBinSizes);
+    long long* bin_off64 = reinterpret_cast<long long*>(base + noalloc::kBinOff64);
+    int* bin_offsets = reinterpret_cast<int*>(base + noalloc::kBinOffsets);
+    long long* scan = reinterpret_cast<long long*>(base + noalloc::kScan);
+
+    fill_i32_kernel<<<(B + 1 + 255) / 256, 256, 0, s>>>(bin_sizes, B + 1, 0);
+    launch_check(hipGetLastError(), "clear bins");
+    launch_check(launch_neighbor_bins(plan, d_positions, rf, wp, wf, wrap, atom_bins, bin_sizes, s), "bins");
+    launch_check(launch_exclusive_scan_i32(bin_sizes, B, bin_off64, scan, s), "bin scan");
+    launch_check(launch_narrow_offsets(bin_off64, B, bin_offsets, nullptr, s), "narrow");
+    // cursors start at the bin offsets
+    copy_i32_kernel<<<(B + 255) / 256, 256, 0, s>>>(bin_sizes, bin_offsets, B);
+    launch_check(hipGetLastError(), "cursors");
+    launch_check(launch_neighbor_fill_bins(plan, atom_bins, bin_offsets, bin_sizes, bin_atoms, s), "fill bins");
+    launch_check(launch_sort_segments(B, bin_offsets, bin_atoms, s), "sort bins");
+    launch_check(launch_neighbor_edges(plan, wp, wf, wrap, atom_bins, bin_offsets, bin_atoms, nullptr, counts,
+                                       nullptr, nullptr, nullptr, s),
+                 "count edges");
+    launch_check(launch_exclusive_scan_i64(counts, N, offsets, scan, s), "edge scan");
+    long long total = 0;
+    launch_check(hipMemcpyAsync(&total, offsets + N, sizeof(long long), hipMemcpyDeviceToHost, s), "edge count");
+    launch_check(hipStreamSynchronize(s), "edge count");
+    *num_edges = total;
+    if (total > std::numeric_limits<int>::max())
+        throw std::length_error("neighbor graph exceeds 32-bit edge indexing");
+    if (total > edge_capacity)
+        throw std::length_error("neighbor graph has " + std::to_string(total) + " edges, more than the capacity " +
+                                std::to_string(edge_capacity) + " of the output arrays");
+    launch_check(launch_narrow_offsets(offsets, N, d_receiver_offsets, nullptr, s), "narrow");
+    launch_check(launch_neighbor_edges(plan, wp, wf, wrap, atom_bins, bin_offsets, bin_atoms, offsets, nullptr,
+                                       d_sources, d_shifts, d_fractional_xyz, s),
+                 "fill edges");
+    launch_check(hipStreamSynchronize(s), "neighbor graph");
 }
 
 }  // namespace sxl

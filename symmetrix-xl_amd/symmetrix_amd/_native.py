@@ -66,6 +66,11 @@ SIGNATURES = {
     "sxl_graph_arrays": (ctypes.c_int, [ctypes.c_void_p, c_u64, c_int_p, c_int_p, c_int_p, c_int_p,
                                         c_double_p]),
     "sxl_update_cell": (ctypes.c_int, [ctypes.c_void_p, c_u64, c_double_p, c_double_p]),
+    "sxl_neighbor_graph_build_noalloc": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, c_double_p, c_double_p,
+                                                        ctypes.c_double, c_i64, ctypes.c_void_p, ctypes.c_void_p,
+                                                        ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(c_i64),
+                                                        ctypes.c_void_p]),
+    "sxl_neighbor_graph_noalloc_limits": (c_i64, [c_int_p, c_int_p]),
     "sxl_validate_graph_cardinality": (ctypes.c_int, [ctypes.c_void_p, c_i64, c_i64, c_i64]),
     "sxl_prepare_geometry": (ctypes.c_int, [ctypes.c_void_p, c_u64, c_double_p, c_i64, c_double_p, c_i64,
                                             c_double_p, c_double_p, c_int_p]),
