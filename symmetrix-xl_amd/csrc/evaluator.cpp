@@ -553,15 +553,19 @@ void Evaluator::allocate_workspace()
     const std::size_t N = std::max(num_nodes_, 1);
     const std::size_t E = std::max<long long>(num_edges_, 1);
     const std::size_t f = sizeof(float);
+    const bool tiled = tile_receivers_ > 0;
     // receiver-indexed work arrays span one tile (the whole graph untiled)
-    const std::size_t NT = tile_receivers_ > 0 ? static_cast<std::size_t>(tile_receivers_) : N;
+    const std::size_t NT = tiled ? static_cast<std::size_t>(tile_receivers_) : N;
     std::size_t ET = E;
-    if (tile_receivers_ > 0) {
+    if (tiled) {
         ET = 1;
         for (int t = 0; t < num_tiles_; ++t)
             ET = std::max<std::size_t>(ET, tile_first_edge_[t + 1] - tile_first_edge_[t]);
     }
-    if (tile_receivers_ > 0 || model_.pre_linear_up) M0s_.reserve(N * C_ * f);
+    if (tiled || model_.pre_linear_up)
+        M0s_.reserve(N * C_ * f);
+    else
+        M0s_.release();
     A0_.reserve(NT * nlm_ * C_ * f);
     M0_.reserve(NT * nLM_ * C_ * f);
     Phi1_.reserve(NT * nlme_ * C_ * f);
@@ -577,13 +581,30 @@ void Evaluator::allocate_workspace()
         dot1_.reserve(N * f);
     }
     energies_.reserve(N * sizeof(double));
-    forces_.reserve(E * 3 * sizeof(double));
     atom_forces_.reserve(N * 3 * sizeof(double));
     partials_.reserve(static_cast<std::size_t>(reduce_totals_partials(num_nodes_, static_cast<int>(num_edges_))) *
                       10 * sizeof(double));
-    totals_.reserve(16 * sizeof(double));
-    xyz_.reserve(E * 3 * sizeof(double));
-    r_.reserve(E * sizeof(double));
+    // [0] energy, [1..9] stress, [12] max |disp|^2, [13] invalid edges,
+    // [16..25] tiled plan: -sum f (x) xyz accumulated over the tiles
+    totals_.reserve(32 * sizeof(double));
+    if (tiled) {
+        // per-edge state lives in the tile arena
+        forces_.release();
+        xyz_.release();
+        r_.release();
+        tile_xyz_.reserve(ET * 3 * sizeof(double));
+        tile_r_.reserve(ET * sizeof(double));
+        tile_pair_.reserve(ET * sizeof(int));
+        tile_forces_.reserve(ET * 3 * sizeof(double));
+    } else {
+        tile_xyz_.release();
+        tile_r_.release();
+        tile_pair_.release();
+        tile_forces_.release();
+        forces_.reserve(E * 3 * sizeof(double));
+        xyz_.reserve(E * 3 * sizeof(double));
+        r_.reserve(E * sizeof(double));
+    }
 }
 
 // Execution plan of the prepared graph.  With fixed workspace allowed, the
@@ -613,21 +634,25 @@ void Evaluator::plan_tiles()
         hip_check(hipStreamSynchronize(stream_), "sync");
     }
     // candidate estimates: graph state + work arrays
-    const std::size_t graph = graph_bytes_estimate();
-    const std::size_t untiled = graph + work_bytes_estimate(N, E);
+    const std::size_t graph_untiled = graph_bytes_estimate(false);
+    const std::size_t graph_tiled = graph_bytes_estimate(true);
+    const std::size_t untiled = graph_untiled + work_bytes_estimate(N, E, false);
     const int T = receiver_limit_ > 0 ? receiver_limit_ : kDefaultTileReceivers;
     long long tile_edges = 0;
     for (long long t0 = 0; t0 < N; t0 += T)
         tile_edges = std::max<long long>(tile_edges, first[std::min<long long>(N, t0 + T)] - first[t0]);
-    const std::size_t tiled = graph + work_bytes_estimate(std::min(T, std::max(N, 1)), tile_edges) +
-                              static_cast<std::size_t>(N) * C_ * sizeof(float) +
-                              3 * sizeof(int) * static_cast<std::size_t>(E);
+    // runs of the source-major lists per tile: at least one per source with edges
+    const std::size_t tiled = graph_tiled + work_bytes_estimate(std::min(T, std::max(N, 1)), tile_edges, true) +
+                              3 * sizeof(int) * static_cast<std::size_t>(std::max(N, 1));
     // memory budget: free device memory plus what this evaluator already holds
+    // of what the plans allocate
     std::size_t free_bytes = 0, total_bytes = 0;
     hip_check(hipMemGetInfo(&free_bytes, &total_bytes), "memory info");
     const std::size_t held = A0_.bytes() + M0_.bytes() + Phi1_.bytes() + A1_.bytes() + A1adj_.bytes() +
                              msg_.bytes() + M0s_.bytes() + run_source_.bytes() + run_start_.bytes() +
-                             run_length_.bytes();
+                             run_length_.bytes() + tile_xyz_.bytes() + tile_r_.bytes() + tile_pair_.bytes() +
+                             tile_forces_.bytes() + xyz_.bytes() + r_.bytes() + forces_.bytes();
+    const std::size_t graph = graph_tiled;  // held by both plans at this point
     rep.available_bytes = free_bytes + held + graph;
     rep.reserve_bytes = rep.available_bytes / 10;
     const std::size_t budget = rep.available_bytes - rep.reserve_bytes;
@@ -670,13 +695,16 @@ void Evaluator::plan_tiles()
     num_tiles_ = (N + T - 1) / T;
     tile_first_edge_.resize(num_tiles_ + 1);
     for (int t = 0; t <= num_tiles_; ++t) tile_first_edge_[t] = first[std::min<long long>(N, static_cast<long long>(t) * T)];
-    // runs: count per tile, scan on the host, fill
+    // runs: count per tile, scan on the host, fill (an edge's tile from the
+    // tiles' first edges)
+    std::vector<int> tfe(tile_first_edge_.begin(), tile_first_edge_.end());
+    upload(tile_first_edge_dev_, tfe, stream_);
     DeviceBuffer per_source, per_tile, offsets;
     per_source.reserve(static_cast<std::size_t>(N) * sizeof(int));
     per_tile.reserve(static_cast<std::size_t>(num_tiles_) * sizeof(int));
     hip_check(hipMemsetAsync(per_tile.as<void>(), 0, num_tiles_ * sizeof(int), stream_), "memset");
-    hip_check(launch_tile_runs_count(N, tfirst_.as<int>(), tedge_.as<int>(), receiver_.as<int>(), T,
-                                     per_source.as<int>(), per_tile.as<int>(), stream_),
+    hip_check(launch_tile_runs_count(N, tfirst_.as<int>(), tedge_.as<int>(), tile_first_edge_dev_.as<int>(),
+                                     num_tiles_, per_source.as<int>(), per_tile.as<int>(), stream_),
               "tile runs");
     std::vector<int> counts(num_tiles_);
     hip_check(hipMemcpyAsync(counts.data(), per_tile.as<int>(), num_tiles_ * sizeof(int), hipMemcpyDeviceToHost,
@@ -691,40 +719,52 @@ void Evaluator::plan_tiles()
     run_length_.reserve(static_cast<std::size_t>(std::max(runs, 1)) * sizeof(int));
     upload(offsets, tile_run_offsets_, stream_);
     hip_check(hipMemsetAsync(per_tile.as<void>(), 0, num_tiles_ * sizeof(int), stream_), "memset");
-    hip_check(launch_tile_runs_fill(N, tfirst_.as<int>(), tedge_.as<int>(), receiver_.as<int>(), T,
-                                    offsets.as<int>(), per_tile.as<int>(), run_source_.as<int>(),
+    hip_check(launch_tile_runs_fill(N, tfirst_.as<int>(), tedge_.as<int>(), tile_first_edge_dev_.as<int>(),
+                                    num_tiles_, offsets.as<int>(), per_tile.as<int>(), run_source_.as<int>(),
                                     run_start_.as<int>(), run_length_.as<int>(), stream_),
               "tile runs");
     hip_check(hipStreamSynchronize(stream_), "tile plan");
 }
 
-// Device bytes of the graph-wide state of the prepared graph: per-edge
-// arrays (receiver, source, transpose, pair index, geometry, directed forces
-// and, for a periodic graph, shifts and fractional edge vectors) and per-node
-// arrays (offsets, types, energies, forces, H1 and its adjoint, the direct
-// adjoint and, periodic, positions and displacements).
-std::size_t Evaluator::graph_bytes_estimate() const
+// Device bytes of the graph-wide state of the prepared graph.  Both plans:
+// per edge the sources and the source-major list (and for a periodic graph
+// the cell shifts); per node types, offsets, energies, atom forces, H1 and
+// its adjoint, the direct adjoint, positions and displacements (periodic: the
+// build's offsets and fractional positions).  The untiled plan adds per edge
+// receivers, pair codes, geometry and directed forces (periodic: fractional
+// edge vectors); the tiled plan the scalar M0 block per node (and pair codes
+// per edge when a caller's neighbour types differ from its sources').
+std::size_t Evaluator::graph_bytes_estimate(bool tiled) const
 {
     const std::size_t N = num_nodes_, E = static_cast<std::size_t>(num_edges_);
-    std::size_t per_edge = 4 * sizeof(int) + 4 * sizeof(double) + 3 * sizeof(double);
+    std::size_t per_edge = 2 * sizeof(int);
     std::size_t per_node = 4 * sizeof(int) + 4 * sizeof(double) + 2 * static_cast<std::size_t>(nLM_) * C_ * sizeof(float) +
-                           static_cast<std::size_t>(C_) * sizeof(float);
+                           static_cast<std::size_t>(C_) * sizeof(float) + 6 * sizeof(double);
     if (periodic_) {
-        per_edge += sizeof(int) + 3 * sizeof(int) + 3 * sizeof(double);
-        per_node += sizeof(int) + 9 * sizeof(double);
+        per_edge += 3 * sizeof(int);
+        per_node += sizeof(int) + 3 * sizeof(double);
+    }
+    if (!tiled) {
+        per_edge += 2 * sizeof(int) + 7 * sizeof(double);
+        if (periodic_) per_edge += 3 * sizeof(double);
+    } else {
+        per_node += static_cast<std::size_t>(C_) * sizeof(float);
+        if (!pair_from_types_) per_edge += sizeof(int);
     }
     if (model_.A1_scaled) per_node += 2 * sizeof(float);
-    if (model_.pre_linear_up) per_node += static_cast<std::size_t>(C_) * sizeof(float);
+    if (model_.pre_linear_up && !tiled) per_node += static_cast<std::size_t>(C_) * sizeof(float);
     return per_edge * E + per_node * N;
 }
 
 // Device bytes of the work arrays for `receivers` receivers and `edges`
 // edges: A0, A1 and A1_adj [lm], M0 [LM], Phi1 [lme] per receiver and the
-// H1-adjoint messages [LM] per edge.
-std::size_t Evaluator::work_bytes_estimate(long long receivers, long long edges) const
+// H1-adjoint messages [LM] per edge; the tiled plan's arena also holds each
+// tile edge's geometry, pair code and directed force.
+std::size_t Evaluator::work_bytes_estimate(long long receivers, long long edges, bool tiled) const
 {
     const std::size_t per_node = static_cast<std::size_t>(C_) * sizeof(float) * (3 * nlm_ + nLM_ + nlme_);
-    const std::size_t per_edge = static_cast<std::size_t>(nLM_) * C_ * sizeof(float);
+    std::size_t per_edge = static_cast<std::size_t>(nLM_) * C_ * sizeof(float);
+    if (tiled) per_edge += 7 * sizeof(double) + sizeof(int);
     return per_node * static_cast<std::size_t>(std::max(receivers, 1LL)) +
            per_edge * static_cast<std::size_t>(std::max(edges, 1LL));
 }
@@ -863,41 +903,45 @@ void Evaluator::set_workspace_receiver_limit(int receivers)
     receiver_limit_ = receivers;
 }
 
-// Shared tail of both graph preparations: receivers, source-major transpose,
-// edge pair indices, workspace.
-void Evaluator::finish_graph(const int* host_neigh_types)
+// Shared tail of both graph preparations: source-major transpose, the
+// execution plan, and for the untiled plan the graph-wide receiver and pair
+// arrays (the tiled plan forms pair codes per tile), node blocks, workspace.
+void Evaluator::finish_graph(const int* host_neigh_types, const int* host_sources)
 {
     const int N = num_nodes_;
     const int E = static_cast<int>(num_edges_);
-    receiver_.reserve(static_cast<std::size_t>(std::max(E, 1)) * sizeof(int));
-    hip_check(launch_receivers(N, first_.as<int>(), receiver_.as<int>(), stream_), "receivers");
     // transpose: count -> scan -> fill -> sort each source segment ascending
-    DeviceBuffer counts, offsets64;
-    counts.reserve((N + 1) * sizeof(int));
-    offsets64.reserve((N + 1) * sizeof(long long));
-    scratch_.reserve(scan_scratch_size(N + 1) * sizeof(long long));
-    hip_check(hipMemsetAsync(counts.as<void>(), 0, (N + 1) * sizeof(int), stream_), "memset");
-    hip_check(launch_transpose_count(E, source_.as<int>(), counts.as<int>(), stream_), "transpose");
-    hip_check(launch_exclusive_scan_i32(counts.as<int>(), N, offsets64.as<long long>(),
-                                        scratch_.as<long long>(), stream_),
-              "scan");
-    tfirst_.reserve((N + 1) * sizeof(int));
-    hip_check(launch_narrow_offsets(offsets64.as<long long>(), N, tfirst_.as<int>(), nullptr, stream_),
-              "narrow");
-    tedge_.reserve(static_cast<std::size_t>(std::max(E, 1)) * sizeof(int));
-    hip_check(hipMemsetAsync(counts.as<void>(), 0, (N + 1) * sizeof(int), stream_), "memset");
-    hip_check(launch_transpose_fill(E, source_.as<int>(), tfirst_.as<int>(), counts.as<int>(),
-                                    tedge_.as<int>(), stream_),
-              "transpose fill");
-    hip_check(launch_sort_segments(N, tfirst_.as<int>(), tedge_.as<int>(), stream_), "sort");
-    // edge pair indices
-    edge_pair_.reserve(static_cast<std::size_t>(std::max(E, 1)) * sizeof(int));
+    {
+        DeviceBuffer counts, offsets64;
+        counts.reserve((N + 1) * sizeof(int));
+        offsets64.reserve((N + 1) * sizeof(long long));
+        scratch_.reserve(scan_scratch_size(N + 1) * sizeof(long long));
+        hip_check(hipMemsetAsync(counts.as<void>(), 0, (N + 1) * sizeof(int), stream_), "memset");
+        hip_check(launch_transpose_count(E, source_.as<int>(), counts.as<int>(), stream_), "transpose");
+        hip_check(launch_exclusive_scan_i32(counts.as<int>(), N, offsets64.as<long long>(),
+                                            scratch_.as<long long>(), stream_),
+                  "scan");
+        tfirst_.reserve((N + 1) * sizeof(int));
+        hip_check(launch_narrow_offsets(offsets64.as<long long>(), N, tfirst_.as<int>(), nullptr, stream_),
+                  "narrow");
+        tedge_.reserve(static_cast<std::size_t>(std::max(E, 1)) * sizeof(int));
+        hip_check(hipMemsetAsync(counts.as<void>(), 0, (N + 1) * sizeof(int), stream_), "memset");
+        hip_check(launch_transpose_fill(E, source_.as<int>(), tfirst_.as<int>(), counts.as<int>(),
+                                        tedge_.as<int>(), stream_),
+                  "transpose fill");
+        hip_check(launch_sort_segments(N, tfirst_.as<int>(), tedge_.as<int>(), stream_), "sort");
+        hip_check(hipStreamSynchronize(stream_), "transpose");
+    }
+    // caller-provided source types (prepare_graph): checked, and the pair
+    // codes formed on the host; they follow from the node types unless a
+    // neighbour type differs from its source's type
+    std::vector<int> host_pairs;
+    pair_from_types_ = true;
     if (host_neigh_types) {
-        // caller-provided source types (prepare_graph): computed on the host
         std::vector<int> ta(model_.num_elements, -1);
         for (std::size_t a = 0; a < active_types_.size(); ++a) ta[active_types_[a]] = static_cast<int>(a);
         const int na = static_cast<int>(active_types_.size());
-        std::vector<int> pairs(E);
+        host_pairs.resize(E);
         std::size_t e = 0;
         std::vector<int> first(N + 1);
         hip_check(hipMemcpyAsync(first.data(), first_.as<int>(), (N + 1) * sizeof(int), hipMemcpyDeviceToHost,
@@ -911,19 +955,36 @@ void Evaluator::finish_graph(const int* host_neigh_types)
                 if (t < 0 || t >= model_.num_elements) throw std::out_of_range("MACE radial type index is out of range.");
                 const int b = ta[t];
                 if (b < 0) throw std::runtime_error("MACE radial cache is not prepared for an active type.");
+                if (t != host_types_[host_sources[e]]) pair_from_types_ = false;
                 const int po = a * na + b;
                 const int pu = shared_pair_tables() ? 0 : a <= b ? a * (2 * na - a - 1) / 2 + b : b * (2 * na - b - 1) / 2 + a;
-                pairs[e] = po | (pu << 16);
+                host_pairs[e] = po | (pu << 16);
             }
         }
-        upload(edge_pair_, pairs, stream_);
-    } else {
-        hip_check(launch_edge_pairs(E, receiver_.as<int>(), source_.as<int>(), node_types_.as<int>(),
-                                    type_active_.as<int>(), static_cast<int>(active_types_.size()),
-                                    shared_pair_tables(), edge_pair_.as<int>(), stream_),
-                  "edge pairs");
     }
     plan_tiles();
+    if (tile_receivers_ == 0) {
+        receiver_.reserve(static_cast<std::size_t>(std::max(E, 1)) * sizeof(int));
+        hip_check(launch_receivers(N, first_.as<int>(), receiver_.as<int>(), stream_), "receivers");
+        if (host_neigh_types) {
+            upload(edge_pair_, host_pairs, stream_);
+        } else {
+            edge_pair_.reserve(static_cast<std::size_t>(std::max(E, 1)) * sizeof(int));
+            hip_check(launch_edge_pairs(E, receiver_.as<int>(), source_.as<int>(), node_types_.as<int>(),
+                                        type_active_.as<int>(), static_cast<int>(active_types_.size()),
+                                        shared_pair_tables(), edge_pair_.as<int>(), stream_),
+                      "edge pairs");
+        }
+    } else {
+        // graph-wide per-edge state of the untiled plan is not kept
+        hip_check(hipStreamSynchronize(stream_), "synchronize");
+        receiver_.release();
+        if (pair_from_types_)
+            edge_pair_.release();
+        else
+            upload(edge_pair_, host_pairs, stream_);
+        if (periodic_) pgraph_.fractional_xyz.release();  // edges from cell shifts instead
+    }
     plan_node_blocks();
     allocate_workspace();
     hip_check(hipStreamSynchronize(stream_), "graph preparation");
@@ -970,7 +1031,7 @@ std::uint64_t Evaluator::prepare_graph(int num_nodes, const int* node_types, con
     positions_.reserve(static_cast<std::size_t>(std::max(num_nodes, 1)) * 3 * sizeof(double));
     disp_.reserve(static_cast<std::size_t>(std::max(num_nodes, 1)) * 3 * sizeof(double));
     geometry_mode_ = kGeometryNone;
-    finish_graph(neigh_types);
+    finish_graph(neigh_types, neigh_indices);
     return generation_;
 }
 
@@ -1117,11 +1178,9 @@ std::uint64_t Evaluator::prepare_periodic_graph(int num_nodes, const int* node_t
     hip_check(hipMemcpyAsync(first_.as<int>(), pgraph_.first.as<int>(), (N + 1) * sizeof(int),
                              hipMemcpyDeviceToDevice, stream_),
               "copy");
-    source_.reserve(static_cast<std::size_t>(std::max(E, 1)) * sizeof(int));
-    if (E > 0)
-        hip_check(hipMemcpyAsync(source_.as<int>(), pgraph_.sources.as<int>(), E * sizeof(int),
-                                 hipMemcpyDeviceToDevice, stream_),
-                  "copy");
+    // the build's source array becomes the graph's (no copy)
+    source_.swap(pgraph_.sources);
+    pgraph_.sources.release();
     host_types_ = types;
     num_nodes_ = N;
     num_edges_ = E;
@@ -1130,7 +1189,7 @@ std::uint64_t Evaluator::prepare_periodic_graph(int num_nodes, const int* node_t
     std::memcpy(inverse_cell_, inverse_cell, sizeof(inverse_cell_));
     upload(node_types_, types, stream_);
     upload_cell();
-    finish_graph(nullptr);
+    finish_graph(nullptr, nullptr);
     // the build's fractional positions and edge vectors are the graph's geometry
     geometry_mode_ = kGeometryBuilt;
     geometry_generation_ = generation_;
@@ -1271,8 +1330,13 @@ GeometryRef Evaluator::geometry_ref() const
 {
     GeometryRef g;
     if (geometry_mode_ == kGeometryBuilt) {
+        // the build's fractional positions with its fractional edge vectors,
+        // or (tiled plan, which does not keep those) with its cell shifts
         g.positions = pgraph_.fractional_positions.as<double>();
-        g.edges = pgraph_.fractional_xyz.as<double>();
+        if (pgraph_.fractional_xyz.bytes() > 0)
+            g.edges = pgraph_.fractional_xyz.as<double>();
+        else
+            g.shifts = pgraph_.shifts.as<int>();
         g.fractional = 1;
         g.pbc = 7;
         return g;
@@ -1310,7 +1374,7 @@ void Evaluator::graph_arrays(std::uint64_t generation, int* num_neigh, int* rece
             hip_check(hipMemcpyAsync(shifts, pgraph_.shifts.as<int>(), E * 3 * sizeof(int), hipMemcpyDeviceToHost,
                                      stream_),
                       "copy");
-        if (fractional_xyz && E)
+        if (fractional_xyz && E && pgraph_.fractional_xyz.bytes() > 0)
             hip_check(hipMemcpyAsync(fractional_xyz, pgraph_.fractional_xyz.as<double>(), E * 3 * sizeof(double),
                                      hipMemcpyDeviceToHost, stream_),
                       "copy");
@@ -1319,6 +1383,27 @@ void Evaluator::graph_arrays(std::uint64_t generation, int* num_neigh, int* rece
     if (receiver_offsets) std::copy(first.begin(), first.end(), receiver_offsets);
     if (num_neigh)
         for (int i = 0; i < N; ++i) num_neigh[i] = first[i + 1] - first[i];
+    if (periodic_ && fractional_xyz && E && pgraph_.fractional_xyz.bytes() == 0) {
+        // the tiled plan keeps the cell shifts only: the fractional edge
+        // vector is the fractional position difference plus the shift (equal
+        // to the build's value up to rounding)
+        std::vector<int> src(E), sh(3 * E);
+        std::vector<double> frac(3 * static_cast<std::size_t>(N));
+        hip_check(hipMemcpyAsync(src.data(), source_.as<int>(), E * sizeof(int), hipMemcpyDeviceToHost, stream_),
+                  "copy");
+        hip_check(hipMemcpyAsync(sh.data(), pgraph_.shifts.as<int>(), E * 3 * sizeof(int), hipMemcpyDeviceToHost,
+                                 stream_),
+                  "copy");
+        hip_check(hipMemcpyAsync(frac.data(), pgraph_.fractional_positions.as<double>(), N * 3 * sizeof(double),
+                                 hipMemcpyDeviceToHost, stream_),
+                  "copy");
+        hip_check(hipStreamSynchronize(stream_), "graph copy");
+        for (int i = 0; i < N; ++i)
+            for (long long e = first[i]; e < first[i + 1]; ++e)
+                for (int a = 0; a < 3; ++a)
+                    fractional_xyz[3 * e + a] = frac[3 * static_cast<std::size_t>(src[e]) + a] -
+                                                frac[3 * static_cast<std::size_t>(i) + a] + sh[3 * e + a];
+    }
 }
 
 void Evaluator::compute_positions(std::uint64_t generation, const double* positions, bool device_positions)
@@ -1336,12 +1421,15 @@ void Evaluator::compute_positions(std::uint64_t generation, const double* positi
     hip_check(launch_atom_displacements(N, positions_.as<double>(), ref, cell, cell + 9, disp_.as<double>(),
                                         totals_.as<double>() + 12, stream_),
               "displacements");
-    hip_check(launch_edge_geometry(static_cast<int>(num_edges_), receiver_.as<int>(), source_.as<int>(), ref,
-                                   disp_.as<double>(), cell, model_.r_cut, xyz_.as<double>(), r_.as<double>(),
-                                   reinterpret_cast<unsigned long long*>(totals_.as<double>() + 13), stream_),
-              "edge geometry");
+    // the tiled plan forms each tile's edges from the displacements per tile
+    if (tile_receivers_ == 0)
+        hip_check(launch_edge_geometry(static_cast<int>(num_edges_), receiver_.as<int>(), source_.as<int>(), ref,
+                                       disp_.as<double>(), cell, model_.r_cut, xyz_.as<double>(), r_.as<double>(),
+                                       reinterpret_cast<unsigned long long*>(totals_.as<double>() + 13), stream_),
+                  "edge geometry");
     mark(kStageGeometry, true);
     check_geometry_ = true;
+    explicit_geometry_ = false;
     evaluate();
 }
 
@@ -1350,12 +1438,16 @@ void Evaluator::compute_xyz(std::uint64_t generation, const double* xyz, const d
     check_generation(generation);
     const long long E = num_edges_;
     const hipMemcpyKind kind = device_arrays ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+    // the tiled plan copies each tile's edges from these graph-wide arrays
+    xyz_.reserve(static_cast<std::size_t>(std::max<long long>(E, 1)) * 3 * sizeof(double));
+    r_.reserve(static_cast<std::size_t>(std::max<long long>(E, 1)) * sizeof(double));
     if (E > 0) {
         hip_check(hipMemcpyAsync(xyz_.as<double>(), xyz, E * 3 * sizeof(double), kind, stream_), "xyz");
         hip_check(hipMemcpyAsync(r_.as<double>(), r, E * sizeof(double), kind, stream_), "r");
     }
     for (int i = 0; i < kNumStages; ++i) stage_used_[i] = false;
     check_geometry_ = false;
+    explicit_geometry_ = true;
     evaluate();
 }
 
@@ -1396,7 +1488,7 @@ void Evaluator::density_args(LayerArgs& la, ReadoutArgs* ra)
 }
 
 // ZBL pair term over every receiver (after the forces of the MACE part).
-void Evaluator::launch_zbl_term(hipStream_t s)
+void Evaluator::launch_zbl_term(const LayerArgs& la, double* forces, hipStream_t s)
 {
     if (!model_.has_zbl) return;
     ZblArgs z;
@@ -1405,8 +1497,9 @@ void Evaluator::launch_zbl_term(hipStream_t s)
     z.r_max = zbl_rmax_.as<double>();
     for (int q = 0; q < 4; ++q) z.c[q] = model_.zbl_c[q];
     z.p = model_.zbl_p;
-    hip_check(launch_zbl(num_nodes_, first_.as<int>(), edge_pair_.as<int>(), xyz_.as<double>(), r_.as<double>(), z,
-                         energies_.as<double>(), forces_.as<double>(), s),
+    const EdgeGraph& g = la.graph;
+    hip_check(launch_zbl(la.node_offset, la.node_count, g.first, g.edge_base, g.edge_pair, g.xyz, g.r, z,
+                         energies_.as<double>(), forces, s),
               "ZBL");
 }
 
@@ -1625,7 +1718,7 @@ void Evaluator::evaluate()
         hip_check(launch_a0_reverse(la, r0f_.as<float>(), A0_.as<float>(), A0adj, forces_.as<double>(), s),
                   "A0 reverse");
         mark(kStageA0Reverse, true);
-        launch_zbl_term(s);
+        launch_zbl_term(la, forces_.as<double>(), s);
     }
     mark(kStageAtomForces, false);
     hip_check(launch_atom_forces(N, first_.as<int>(), tfirst_.as<int>(), tedge_.as<int>(), forces_.as<double>(),
@@ -1653,14 +1746,24 @@ void Evaluator::evaluate()
 
 // Tiled evaluation (reference compute_dual_layer_tiled,
 // mace_kokkos_evaluate.cpp:754-1238): three sweeps over receiver tiles with
-// one reused arena.
-//   1. A0 -> M0 -> H1 (graph-wide), keeping the scalar M0 block graph-wide;
-//   2. Phi1 -> A1 -> readout (energies, direct adjoint) -> dPhi1 -> R1
-//      reverse (directed forces, per-edge messages) -> H1 adjoint += the
-//      tile's messages, run by run;
-//   3. M0 adjoint = H1 adjoint H1_W^T + direct -> A0 (recomputed) -> A0
-//      adjoint -> A0 reverse (directed forces +=).
-// Each tile's edges are its receivers' contiguous CSR range.
+// one reused arena.  The arena holds the tile's receiver work arrays and, per
+// tile edge, its geometry, pair code, directed force and H1-adjoint message;
+// graph-wide state is per node (H1, its adjoint, the scalar M0 block, the
+// direct adjoint, energies, atom forces) plus the sources, cell shifts and
+// source-major edge list.
+//   1. edge geometry -> A0 -> M0 -> H1 (graph-wide), keeping the scalar M0
+//      block graph-wide;
+//   2. edge geometry -> Phi1 -> A1 -> readout (energies, direct adjoint) ->
+//      dPhi1 -> R1 reverse (directed forces, messages) -> H1 adjoint += the
+//      tile's messages, run by run; the directed forces are folded into the
+//      atom forces and the virial;
+//   3. edge geometry -> M0 adjoint = H1 adjoint H1_W^T + direct -> A0
+//      (recomputed) -> A0 adjoint -> A0 reverse (+ ZBL) directed forces,
+//      folded likewise.
+// Each tile's edges are its receivers' contiguous CSR range.  Atom forces and
+// the virial are linear in the directed forces, so folding the two sweeps'
+// parts separately gives the same totals; the fold order is fixed (receiver
+// part, then the tile's source runs), so results are run-to-run identical.
 void Evaluator::evaluate_tiled()
 {
     const auto t0 = std::chrono::steady_clock::now();
@@ -1674,13 +1777,13 @@ void Evaluator::evaluate_tiled()
     la.graph.type_active = type_active_.as<int>();
     la.graph.num_active = static_cast<int>(active_types_.size());
     la.graph.first = first_.as<int>();
-    la.graph.receiver = receiver_.as<int>();
+    la.graph.receiver = nullptr;  // not kept by the tiled plan
     la.graph.source = source_.as<int>();
     la.graph.tfirst = tfirst_.as<int>();
     la.graph.tedge = tedge_.as<int>();
-    la.graph.edge_pair = edge_pair_.as<int>();
-    la.graph.xyz = xyz_.as<double>();
-    la.graph.r = r_.as<double>();
+    la.graph.edge_pair = tile_pair_.as<int>();
+    la.graph.xyz = tile_xyz_.as<double>();
+    la.graph.r = tile_r_.as<double>();
     la.grid = grid_;
     la.C = C_;
     la.l_max = model_.l_max;
@@ -1691,19 +1794,74 @@ void Evaluator::evaluate_tiled()
     const PolyArgs p0 = poly_args(p0_layout_, p0_coef_, p0_offsets_, p0_packed_);
     const PolyArgs p1 = poly_args(p1_layout_, p1_coef_, p1_offsets_, p1_packed_);
     const long long nodeLM = static_cast<long long>(nLM_) * C_;
-    auto tile = [&](int t) {
+    double* forces = tile_forces_.as<double>();
+    double* atom_forces = atom_forces_.as<double>();
+    double* virial = totals_.as<double>() + 16;  // [16] unused, [17..25] -sum f (x) xyz
+    // the tile's geometry: the caller's edge vectors, or the prepared
+    // geometry with the displacements of this evaluation
+    TileGeometry tg;
+    tg.first = first_.as<int>();
+    tg.source = source_.as<int>();
+    tg.node_types = node_types_.as<int>();
+    tg.type_active = type_active_.as<int>();
+    tg.num_active = static_cast<int>(active_types_.size());
+    tg.shared_tables = shared_pair_tables();
+    tg.pair_source = pair_from_types_ ? nullptr : edge_pair_.as<int>();
+    if (explicit_geometry_) {
+        tg.explicit_xyz = xyz_.as<double>();
+        tg.explicit_r = r_.as<double>();
+    } else {
+        tg.ref = geometry_ref();
+        tg.disp = disp_.as<double>();
+        tg.cell = cell_dev_.as<double>();
+    }
+    tg.r_cut = model_.r_cut;
+    tg.xyz = tile_xyz_.as<double>();
+    tg.r = tile_r_.as<double>();
+    tg.edge_pair = tile_pair_.as<int>();
+    auto tile = [&](int t, bool count_invalid) {
         la.node_offset = t * T;
         la.node_count = std::min(T, N - t * T);
         la.local_base = la.node_offset;
-        la.edge_base = tile_first_edge_[t];
+        la.graph.edge_base = tile_first_edge_[t];
+        tg.node_begin = la.node_offset;
+        tg.node_count = la.node_count;
+        tg.edge_base = la.graph.edge_base;
+        tg.invalid = count_invalid && check_geometry_
+                         ? reinterpret_cast<unsigned long long*>(totals_.as<double>() + 13)
+                         : nullptr;
+        hip_check(launch_tile_geometry(tg, s), "tile geometry");
+    };
+    auto runs_of = [&](int t) {
+        TileRuns runs;
+        runs.count = tile_run_offsets_[t + 1] - tile_run_offsets_[t];
+        runs.source = run_source_.as<int>() + tile_run_offsets_[t];
+        runs.start = run_start_.as<int>() + tile_run_offsets_[t];
+        runs.length = run_length_.as<int>() + tile_run_offsets_[t];
+        return runs;
+    };
+    // the tile's directed forces into the atom forces and the virial
+    auto fold = [&](int t) {
+        const long long tile_edges = tile_first_edge_[t + 1] - tile_first_edge_[t];
+        hip_check(launch_fold_tile_forces(la.node_offset, la.node_count, first_.as<int>(), runs_of(t),
+                                          tedge_.as<int>(), la.graph.edge_base, forces, atom_forces, s),
+                  "fold forces");
+        if (tile_edges > 0) {
+            const int np = reduce_totals_partials(0, static_cast<int>(tile_edges));
+            hip_check(launch_reduce_totals(0, static_cast<int>(tile_edges), nullptr, forces, tile_xyz_.as<double>(),
+                                           1.0, partials_.as<double>(), np, virial, s, true),
+                      "virial");
+        }
     };
     float* H1 = H1_.as<float>();
     float* H1adj = H1adj_.as<float>();
     float* M0s = M0s_.as<float>();
     hip_check(hipMemsetAsync(H1adj, 0, static_cast<std::size_t>(N) * nodeLM * sizeof(float), s), "memset");
+    hip_check(launch_fill_f64(atom_forces, 3LL * N, 0.0, s), "clear forces");
+    hip_check(launch_fill_f64(virial, 10, 0.0, s), "clear virial");
     // sweep 1
     for (int t = 0; t < num_tiles_; ++t) {
-        tile(t);
+        tile(t, true);
         hip_check(launch_a0_forward(la, r0f_.as<float>(), A0_.as<float>(), s), "A0 forward");
         hip_check(launch_m0_forward(la, p0, node_blocks(m0_blocks_, m0_block_offsets_, t), A0_.as<float>(),
                                     M0_.as<float>(), s),
@@ -1743,28 +1901,23 @@ void Evaluator::evaluate_tiled()
     density_args(la, &ra);
     float* dPhi1 = Phi1_.as<float>();
     for (int t = 0; t < num_tiles_; ++t) {
-        tile(t);
+        tile(t, false);
         hip_check(launch_r1_forward(la, r1_.as<float>(), cg_.as<float>(), H1, Phi1_.as<float>(), s), "R1 forward");
         gemm_a1(la.node_count, Phi1_.as<float>(), A1_.as<float>(), false, "A1 gemm");
         ra.nodes = node_blocks(readout_blocks_, readout_block_offsets_, t);
         ra.local_base = la.local_base;
         hip_check(launch_readout(ra, s), "readout");
         gemm_a1(la.node_count, A1adj_.as<float>(), dPhi1, true, "A1 reverse gemm");
-        hip_check(launch_r1_reverse(la, r1_.as<float>(), cg_.as<float>(), H1, dPhi1, forces_.as<double>(),
-                                    msg_.as<float>(), s),
+        hip_check(launch_r1_reverse(la, r1_.as<float>(), cg_.as<float>(), H1, dPhi1, forces, msg_.as<float>(), s),
                   "R1 reverse");
-        TileRuns runs;
-        runs.count = tile_run_offsets_[t + 1] - tile_run_offsets_[t];
-        runs.source = run_source_.as<int>() + tile_run_offsets_[t];
-        runs.start = run_start_.as<int>() + tile_run_offsets_[t];
-        runs.length = run_length_.as<int>() + tile_run_offsets_[t];
-        hip_check(launch_gather_tile_runs(la, runs, msg_.as<float>(), H1adj, s), "H1 adjoint gather");
+        hip_check(launch_gather_tile_runs(la, runs_of(t), msg_.as<float>(), H1adj, s), "H1 adjoint gather");
+        fold(t);
     }
     // sweep 3
     float* M0adj = M0_.as<float>();
     float* A0adj = A1_.as<float>();
     for (int t = 0; t < num_tiles_; ++t) {
-        tile(t);
+        tile(t, false);
         gemm_h1(la.node_count, la.node_offset, H1adj + la.node_offset * nodeLM, nodeLM, M0adj, nodeLM, true, nullptr,
                 "H1 reverse gemm");
         add_direct(la.node_count, la.node_offset, M0adj, s);
@@ -1772,23 +1925,14 @@ void Evaluator::evaluate_tiled()
         hip_check(launch_m0_reverse(la, p0, node_blocks(m0_blocks_, m0_block_offsets_, t), A0_.as<float>(), M0adj,
                                     A0adj, s),
                   "M0 reverse");
-        hip_check(launch_a0_reverse(la, r0f_.as<float>(), A0_.as<float>(), A0adj, forces_.as<double>(), s),
-                  "A0 reverse");
+        // the A0 reverse adds into the directed forces: this sweep's part starts at zero
+        const long long tile_edges = tile_first_edge_[t + 1] - tile_first_edge_[t];
+        hip_check(launch_fill_f64(forces, 3 * tile_edges, 0.0, s), "clear tile forces");
+        hip_check(launch_a0_reverse(la, r0f_.as<float>(), A0_.as<float>(), A0adj, forces, s), "A0 reverse");
+        launch_zbl_term(la, forces, s);
+        fold(t);
     }
-    launch_zbl_term(s);
-    mark(kStageAtomForces, false);
-    hip_check(launch_atom_forces(N, first_.as<int>(), tfirst_.as<int>(), tedge_.as<int>(), forces_.as<double>(),
-                                 atom_forces_.as<double>(), s),
-              "atom forces");
-    mark(kStageAtomForces, true);
     finish_evaluation();
-    if (profiling_ && stage_used_[kStageAtomForces]) {
-        float ms = 0.0f;
-        hip_check(hipEventElapsedTime(&ms, events_[2 * kStageAtomForces], events_[2 * kStageAtomForces + 1]),
-                  "event time");
-        stage_ms_[kStageAtomForces] += ms;
-        stage_count_[kStageAtomForces] += 1;
-    }
     evaluated_generation_ = generation_;
     reduced_ = fused_volume_ > 0.0;
     reduced_volume_ = fused_volume_;
@@ -1882,13 +2026,24 @@ void Evaluator::finish_evaluation()
     invalid_edges_ = 0;
     fused_volume_ = 0.0;
     last_from_positions_ = check_geometry_;
-    if (check_geometry_) {
-        // energy and stress for the current cell in the same pass, copied
-        // back with the displacement maximum and the invalid-edge count
-        const double* c = cell_;
-        const double volume = std::abs(c[0] * (c[4] * c[8] - c[5] * c[7]) - c[1] * (c[3] * c[8] - c[5] * c[6]) +
-                                       c[2] * (c[3] * c[7] - c[4] * c[6]));
-        if (std::isfinite(volume) && volume > 0.0) {
+    const bool tiled = tile_receivers_ > 0;
+    // energy and stress for the current cell in the same pass, copied back
+    // with the displacement maximum and the invalid-edge count
+    const double* c = cell_;
+    const double volume = std::abs(c[0] * (c[4] * c[8] - c[5] * c[7]) - c[1] * (c[3] * c[8] - c[5] * c[6]) +
+                                   c[2] * (c[3] * c[7] - c[4] * c[6]));
+    const bool fuse = check_geometry_ && std::isfinite(volume) && volume > 0.0;
+    if (tiled) {
+        // the energy over the nodes; the virial was accumulated tile by tile
+        const int np = reduce_totals_partials(num_nodes_, 0);
+        hip_check(launch_reduce_totals(num_nodes_, 0, energies_.as<double>(), nullptr, nullptr, 1.0,
+                                       partials_.as<double>(), np, totals_.as<double>(), stream_),
+                  "totals");
+        hip_check(hipMemcpyAsync(host_totals_, totals_.as<double>(), 26 * sizeof(double), hipMemcpyDeviceToHost,
+                                 stream_),
+                  "totals copy");
+    } else if (check_geometry_) {
+        if (fuse) {
             const int np = reduce_totals_partials(num_nodes_, static_cast<int>(num_edges_));
             hip_check(launch_reduce_totals(num_nodes_, static_cast<int>(num_edges_), energies_.as<double>(),
                                            forces_.as<double>(), xyz_.as<double>(), 1.0 / volume,
@@ -1901,12 +2056,30 @@ void Evaluator::finish_evaluation()
                   "totals copy");
     }
     hip_check(hipStreamSynchronize(stream_), "evaluation");
+    if (tiled) {
+        for (int q = 0; q < 9; ++q) host_virial_[q] = host_totals_[17 + q];
+        if (fuse) {
+            set_stress_from_virial(volume);
+            fused_volume_ = volume;
+        }
+    }
     if (check_geometry_) std::memcpy(&invalid_edges_, host_totals_ + 13, sizeof(invalid_edges_));
     if (check_geometry_ && invalid_edges_ != 0) {
         check_geometry_ = false;
         evaluated_generation_ = 0;
         throw std::invalid_argument("Execution R1 prepared positions produced an invalid edge geometry.");
     }
+}
+
+// Tiled plan: stress = (-sum_e f_e (x) xyz_e) / V on the host, also written
+// to the device totals (device results hold the last reduced stress).
+void Evaluator::set_stress_from_virial(double volume)
+{
+    for (int q = 0; q < 9; ++q) host_totals_[1 + q] = host_virial_[q] / volume;
+    hip_check(hipMemcpyAsync(totals_.as<double>() + 1, host_totals_ + 1, 9 * sizeof(double), hipMemcpyHostToDevice,
+                             stream_),
+              "stress copy");
+    hip_check(hipStreamSynchronize(stream_), "stress copy");
 }
 
 // Energy and stress totals of the completed evaluation for `volume`, in
@@ -1918,6 +2091,12 @@ void Evaluator::reduce(double volume)
     if (reduced_ && reduced_volume_ == volume) return;
     if (!std::isfinite(volume) || !(volume > 0.0))
         throw std::invalid_argument("Stress reduction requires a positive finite volume.");
+    if (tile_receivers_ > 0) {  // energy and virial are on the host already
+        set_stress_from_virial(volume);
+        reduced_ = true;
+        reduced_volume_ = volume;
+        return;
+    }
     const int np = reduce_totals_partials(num_nodes_, static_cast<int>(num_edges_));
     hip_check(launch_reduce_totals(num_nodes_, static_cast<int>(num_edges_), energies_.as<double>(),
                                    forces_.as<double>(), xyz_.as<double>(), 1.0 / volume, partials_.as<double>(), np,
@@ -1952,6 +2131,10 @@ void Evaluator::node_energies(double* out) const
 void Evaluator::node_forces(double* out) const
 {
     if (evaluated_generation_ != generation_) throw std::invalid_argument("no completed evaluation");
+    if (tile_receivers_ > 0)
+        throw std::invalid_argument(
+            "The tiled plan folds directed edge forces into atom forces tile by tile and does not keep them; "
+            "use the reduced atom forces.");
     if (num_edges_ > 0)
         hip_check(hipMemcpyAsync(out, forces_.as<double>(), num_edges_ * 3 * sizeof(double), hipMemcpyDeviceToHost,
                                  stream_),

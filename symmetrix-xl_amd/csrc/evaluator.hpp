@@ -15,6 +15,7 @@
 #include <cstdint>
 #include <memory>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "kernels.hpp"
@@ -30,6 +31,11 @@ public:
     ~DeviceBuffer();
     void reserve(std::size_t bytes);  // grow-only
     void release();
+    void swap(DeviceBuffer& other) noexcept
+    {
+        std::swap(ptr_, other.ptr_);
+        std::swap(bytes_, other.bytes_);
+    }
     template <class T>
     T* as() const { return static_cast<T*>(ptr_); }
     std::size_t bytes() const { return bytes_; }
@@ -266,7 +272,7 @@ private:
     void check_generation(std::uint64_t generation) const;
     void prepare_active_types(const std::vector<int>& node_types);
     void upload_static_tables();
-    void finish_graph(const int* host_neigh_types);
+    void finish_graph(const int* host_neigh_types, const int* host_sources);
     void allocate_workspace();
     void plan_tiles();
     void plan_node_blocks();
@@ -340,13 +346,14 @@ private:
         atom_forces_, partials_, totals_, scratch_;
     DeviceBuffer scale1_, dot1_;  // [N] A1 density scale and A1_adj . A1 (scaled models)
     void density_args(LayerArgs& la, ReadoutArgs* ra);
-    void launch_zbl_term(hipStream_t s);
+    void launch_zbl_term(const LayerArgs& la, double* forces, hipStream_t s);
     bool reduced_ = false;
     double reduced_volume_ = 0.0;
     // host copy of totals_: [0] energy, [1..9] stress 3x3, [12] max |disp|^2,
     // [13] invalid-edge count; an evaluation from positions reduces energy and
     // stress (cell volume) in the same pass and fills it with one copy
-    double host_totals_[16] = {};
+    double host_totals_[32] = {};
+    void set_stress_from_virial(double volume);
     double fused_volume_ = 0.0;
     bool last_from_positions_ = false;
 
@@ -355,8 +362,19 @@ private:
     int receiver_limit_ = 0;
     std::string plan_profile_ = "capacity", plan_debug_;
     ExecutionPlanReport plan_report_;
-    std::size_t graph_bytes_estimate() const;
-    std::size_t work_bytes_estimate(long long receivers, long long edges) const;
+    std::size_t graph_bytes_estimate(bool tiled) const;
+    std::size_t work_bytes_estimate(long long receivers, long long edges, bool tiled) const;
+    // tile arena: geometry, pair codes and directed forces of one tile's
+    // edges (edge e at index e - first edge of the tile)
+    DeviceBuffer tile_xyz_, tile_r_, tile_pair_, tile_forces_, tile_first_edge_dev_;
+    // pair codes follow from the node types of receiver and source (false when
+    // a caller's neighbour types differ: the tiled plan then keeps edge_pair_)
+    bool pair_from_types_ = true;
+    // tiled plan: the last evaluation's edge vectors came from the caller
+    // (xyz_ / r_ kept graph-wide) rather than from the prepared geometry
+    bool explicit_geometry_ = false;
+    // tiled plan: -sum_e f_e (x) xyz_e of the last evaluation (stress = this / V)
+    double host_virial_[9] = {};
     int tile_receivers_ = 0;
     int num_tiles_ = 0;
     std::vector<long long> tile_first_edge_;  // [num_tiles + 1]

@@ -394,15 +394,31 @@ __global__ void edge_pairs_kernel(int E, const int* __restrict__ receiver, const
 // Runs of the source-major edge lists by receiver tile (tiles of T
 // consecutive receivers).  The list of each source is ascending in edge id,
 // so its receivers, and their tiles, are non-decreasing: one run per change.
+// Tile of edge e: the last tile whose first edge is <= e (tile_first_edge
+// holds num_tiles + 1 ascending offsets; empty tiles share an offset with the
+// next one, which is the one returned).
+__device__ __forceinline__ int tile_of_edge(int e, const int* __restrict__ tile_first_edge, int num_tiles)
+{
+    int lo = 0, hi = num_tiles;  // answer in [lo, hi)
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) / 2;
+        if (tile_first_edge[mid] <= e)
+            lo = mid;
+        else
+            hi = mid;
+    }
+    return lo;
+}
+
 __global__ void tile_runs_count_kernel(int n, const int* __restrict__ tfirst, const int* __restrict__ tedge,
-                                       const int* __restrict__ receiver, int T, int* __restrict__ per_source,
-                                       int* __restrict__ per_tile)
+                                       const int* __restrict__ tile_first_edge, int num_tiles,
+                                       int* __restrict__ per_source, int* __restrict__ per_tile)
 {
     const int src = blockIdx.x * blockDim.x + threadIdx.x;
     if (src >= n) return;
     int prev = -1, runs = 0;
     for (int t = tfirst[src]; t < tfirst[src + 1]; ++t) {
-        const int tile = receiver[tedge[t]] / T;
+        const int tile = tile_of_edge(tedge[t], tile_first_edge, num_tiles);
         if (tile != prev) {
             ++runs;
             atomicAdd(per_tile + tile, 1);
@@ -413,18 +429,19 @@ __global__ void tile_runs_count_kernel(int n, const int* __restrict__ tfirst, co
 }
 
 __global__ void tile_runs_fill_kernel(int n, const int* __restrict__ tfirst, const int* __restrict__ tedge,
-                                      const int* __restrict__ receiver, int T, const int* __restrict__ tile_offsets,
-                                      int* __restrict__ cursors, int* __restrict__ run_source,
-                                      int* __restrict__ run_start, int* __restrict__ run_length)
+                                      const int* __restrict__ tile_first_edge, int num_tiles,
+                                      const int* __restrict__ tile_offsets, int* __restrict__ cursors,
+                                      int* __restrict__ run_source, int* __restrict__ run_start,
+                                      int* __restrict__ run_length)
 {
     const int src = blockIdx.x * blockDim.x + threadIdx.x;
     if (src >= n) return;
     const int t1 = tfirst[src + 1];
     int t = tfirst[src];
     while (t < t1) {
-        const int tile = receiver[tedge[t]] / T;
+        const int tile = tile_of_edge(tedge[t], tile_first_edge, num_tiles);
         int u = t + 1;
-        while (u < t1 && receiver[tedge[u]] / T == tile) ++u;
+        while (u < t1 && tile_of_edge(tedge[u], tile_first_edge, num_tiles) == tile) ++u;
         const int pos = tile_offsets[tile] + atomicAdd(cursors + tile, 1);
         run_source[pos] = src;
         run_start[pos] = t;
@@ -545,23 +562,23 @@ hipError_t launch_atom_displacements(int n, const double* positions, const Geome
     return hipGetLastError();
 }
 
-hipError_t launch_tile_runs_count(int num_nodes, const int* tfirst, const int* tedge, const int* receiver,
-                                  int tile_receivers, int* runs_per_source, int* runs_per_tile, hipStream_t s)
+hipError_t launch_tile_runs_count(int num_nodes, const int* tfirst, const int* tedge, const int* tile_first_edge,
+                                  int num_tiles, int* runs_per_source, int* runs_per_tile, hipStream_t s)
 {
     if (num_nodes <= 0) return hipSuccess;
-    tile_runs_count_kernel<<<(num_nodes + 255) / 256, 256, 0, s>>>(num_nodes, tfirst, tedge, receiver,
-                                                                   tile_receivers, runs_per_source, runs_per_tile);
+    tile_runs_count_kernel<<<(num_nodes + 255) / 256, 256, 0, s>>>(num_nodes, tfirst, tedge, tile_first_edge,
+                                                                   num_tiles, runs_per_source, runs_per_tile);
     return hipGetLastError();
 }
 
-hipError_t launch_tile_runs_fill(int num_nodes, const int* tfirst, const int* tedge, const int* receiver,
-                                 int tile_receivers, const int* tile_offsets, int* tile_cursors, int* run_source,
+hipError_t launch_tile_runs_fill(int num_nodes, const int* tfirst, const int* tedge, const int* tile_first_edge,
+                                 int num_tiles, const int* tile_offsets, int* tile_cursors, int* run_source,
                                  int* run_start, int* run_length, hipStream_t s)
 {
     if (num_nodes <= 0) return hipSuccess;
-    tile_runs_fill_kernel<<<(num_nodes + 255) / 256, 256, 0, s>>>(num_nodes, tfirst, tedge, receiver,
-                                                                  tile_receivers, tile_offsets, tile_cursors,
-                                                                  run_source, run_start, run_length);
+    tile_runs_fill_kernel<<<(num_nodes + 255) / 256, 256, 0, s>>>(num_nodes, tfirst, tedge, tile_first_edge,
+                                                                  num_tiles, tile_offsets, tile_cursors, run_source,
+                                                                  run_start, run_length);
     return hipGetLastError();
 }
 

@@ -36,6 +36,10 @@ struct EdgeGraph {
     const int* edge_pair = nullptr;    // [E] ordered pair | unordered-pair table << 16 (active types; table 0 when shared)
     const double* xyz = nullptr;       // [E][3]
     const double* r = nullptr;         // [E]
+    // The per-edge arrays (edge_pair, xyz, r, and the directed forces and
+    // messages the kernels write) hold edge e at index e - edge_base: 0 when
+    // they span the whole graph, the tile's first edge in tiled execution.
+    long long edge_base = 0;
 };
 
 struct SplineGrid {
@@ -143,11 +147,9 @@ struct LayerArgs {
     int node_offset = 0;  // first receiver handled by this launch
     int node_count = 0;   // receivers handled by this launch
     // Receiver-indexed work arrays (A0, M0, Phi1, their adjoints) hold rows
-    // i - local_base; per-edge messages hold rows e - edge_base.  Both are 0
-    // when the arrays span the whole graph, and the tile's first receiver /
-    // first edge in tiled execution.
+    // i - local_base: 0 when the arrays span the whole graph, the tile's
+    // first receiver in tiled execution (per-edge arrays: graph.edge_base).
     int local_base = 0;
-    long long edge_base = 0;
     // receivers of this launch in element-type order (layer-0 kernels), or null
     const int* type_order = nullptr;
 };
@@ -202,19 +204,20 @@ hipError_t launch_gather_messages(const LayerArgs& a, const float* msg, float* H
 // Tiled execution: the edges of one receiver tile grouped by source.  A run
 // is (source, first index into the source-major edge list, length): the
 // source's edges whose receivers lie in the tile.  H1_adj[source] += the
-// run's messages (tile-local rows e - edge_base), run by run.
+// run's messages (tile-local rows e - graph.edge_base), run by run.
 struct TileRuns {
     int count = 0;
     const int* source = nullptr;
     const int* start = nullptr;
     const int* length = nullptr;
 };
-hipError_t launch_tile_runs_count(int num_nodes, const int* tfirst, const int* tedge, const int* receiver,
-                                  int tile_receivers, int* runs_per_source, int* runs_per_tile,
-                                  hipStream_t s);
-hipError_t launch_tile_runs_fill(int num_nodes, const int* tfirst, const int* tedge, const int* receiver,
-                                 int tile_receivers, const int* tile_offsets, int* tile_cursors,
-                                 int* run_source, int* run_start, int* run_length, hipStream_t s);
+// (tile_first_edge [num_tiles + 1]: the first edge of each tile; an edge's
+// tile is found by binary search, so no per-edge receiver array is needed)
+hipError_t launch_tile_runs_count(int num_nodes, const int* tfirst, const int* tedge, const int* tile_first_edge,
+                                  int num_tiles, int* runs_per_source, int* runs_per_tile, hipStream_t s);
+hipError_t launch_tile_runs_fill(int num_nodes, const int* tfirst, const int* tedge, const int* tile_first_edge,
+                                 int num_tiles, const int* tile_offsets, int* tile_cursors, int* run_source,
+                                 int* run_start, int* run_length, hipStream_t s);
 hipError_t launch_gather_tile_runs(const LayerArgs& a, const TileRuns& runs, const float* msg,
                                    float* H1_adj, hipStream_t s);
 // M0_adj[:, LM 0, :] += direct
@@ -238,8 +241,11 @@ struct ZblArgs {
     double c[4] = {};
     int p = 0;
 };
-hipError_t launch_zbl(int num_nodes, const int* first, const int* edge_pair, const double* xyz, const double* r,
-                      const ZblArgs& z, double* energies, double* forces, hipStream_t s);
+// ZBL of receivers [node_begin, node_begin + num_nodes); the per-edge arrays
+// hold edge e at index e - edge_base
+hipError_t launch_zbl(int node_begin, int num_nodes, const int* first, long long edge_base, const int* edge_pair,
+                      const double* xyz, const double* r, const ZblArgs& z, double* energies, double* forces,
+                      hipStream_t s);
 
 // Reference geometry of a prepared graph (reference
 // prepare_factorized_geometry / _fractional_geometry / _shift_geometry,
@@ -265,13 +271,52 @@ hipError_t launch_edge_geometry(int num_edges, const int* receiver, const int* s
                                 const double* displacements, const double* cell, double r_cut, double* xyz, double* r,
                                 unsigned long long* invalid, hipStream_t s);
 
+// Tiled execution: the edges of receivers [node_begin, node_begin +
+// node_count) in the tile arena (edge e at index e - edge_base): xyz, r and
+// the pair code, from the caller's explicit edge vectors or from the
+// prepared geometry (ref) and the atoms' displacements; edges of zero or
+// non-finite length are set to (r_cut, 0, 0) and counted in *invalid (when
+// given).  Pair codes come from pair_source (a graph-wide table) or from the
+// active types of receiver and source.
+struct TileGeometry {
+    int node_begin = 0, node_count = 0;
+    long long edge_base = 0;
+    const int* first = nullptr;
+    const int* source = nullptr;
+    const int* node_types = nullptr;
+    const int* type_active = nullptr;
+    int num_active = 0;
+    bool shared_tables = false;
+    const int* pair_source = nullptr;
+    GeometryRef ref;
+    const double* disp = nullptr;
+    const double* cell = nullptr;  // 9 doubles on the device
+    const double* explicit_xyz = nullptr;  // graph-wide [E][3] and [E], or null
+    const double* explicit_r = nullptr;
+    double r_cut = 0.0;
+    double* xyz = nullptr;
+    double* r = nullptr;
+    int* edge_pair = nullptr;
+    unsigned long long* invalid = nullptr;
+};
+hipError_t launch_tile_geometry(const TileGeometry& g, hipStream_t s);
+// atom_forces[i] -= sum of the directed forces of receiver i's edges, for the
+// tile's receivers, then atom_forces[source] += sum over each source run of
+// the tile (deterministic order; forces hold edge e at index e - edge_base)
+hipError_t launch_fold_tile_forces(int node_begin, int node_count, const int* first, const TileRuns& runs,
+                                   const int* tedge, long long edge_base, const double* forces, double* atom_forces,
+                                   hipStream_t s);
+hipError_t launch_fill_f64(double* out, long long n, double value, hipStream_t s);
+
 // Reductions (deterministic, f64)
 hipError_t launch_atom_forces(int num_nodes, const int* first, const int* tfirst, const int* tedge,
                               const double* forces, double* atom_forces, hipStream_t s);
 // partial sums per block then one final pass: out[0] = sum energies, out[1..9] = stress
+// (accumulate: out += the totals instead of out =)
 hipError_t launch_reduce_totals(int num_nodes, int num_edges, const double* energies,
                                 const double* forces, const double* xyz, double inv_volume,
-                                double* partials, int num_partials, double* out, hipStream_t s);
+                                double* partials, int num_partials, double* out, hipStream_t s,
+                                bool accumulate = false);
 int reduce_totals_partials(int num_nodes, int num_edges);
 
 // Neighbour graph construction (bit-identical to the reference's device

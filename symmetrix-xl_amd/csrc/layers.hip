@@ -113,13 +113,14 @@ __device__ __forceinline__ TileSlot compact_edge(const EdgeGraph& g, const Splin
     int row = 0;
     float x = 0.0f;
     if (t < n) {
-        rr = g.r[base + t];
+        rr = g.r[base + t - g.edge_base];
         on = rr < grid.r_cut;
     }
     if (on) {
         int iv;
         spline_point(rr, grid, iv, x);
-        const int pair = kOrdered ? g.edge_pair[base + t] & 0xffff : g.edge_pair[base + t] >> 16;
+        const int code = g.edge_pair[base + t - g.edge_base];
+        const int pair = kOrdered ? code & 0xffff : code >> 16;
         row = pair * grid.intervals + iv;
     }
     const unsigned long long mask = __ballot(on);
@@ -173,7 +174,7 @@ __device__ __forceinline__ float density_scale(const DensityScale& d, const Edge
     for (int b = e0; b < e1; b += 64) {
         const int e = b + static_cast<int>(threadIdx.x);
         float v = 0.0f;
-        if (e < e1) v = density_value(d.table, grid, g.edge_pair[e] >> 16, g.r[e]);
+        if (e < e1) v = density_value(d.table, grid, g.edge_pair[e - g.edge_base] >> 16, g.r[e - g.edge_base]);
         sum += wave_sum_dpp(v);
     }
     return 1.0f + sum;
@@ -218,7 +219,7 @@ __global__ void __launch_bounds__(256) a0_forward_kernel(LayerArgs a, const floa
             if (ts.active) {
                 const int e = base + t;
                 float Y[NLM], dir[3];
-                edge_harmonics<LMAX, false>(g.xyz + 3 * static_cast<size_t>(e), rr, Y, nullptr,
+                edge_harmonics<LMAX, false>(g.xyz + 3 * static_cast<size_t>(e - g.edge_base), rr, Y, nullptr,
                                             nullptr, nullptr, dir);
                 s_x[ts.slot] = ts.x;
                 s_row[ts.slot] = ts.row;
@@ -316,7 +317,7 @@ r1_forward_kernel(LayerArgs a, const float* __restrict__ r1,
             if (ts.active) {
                 const int e = base + t;
                 float Y[NLM], dir[3];
-                edge_harmonics<S::LMAX, false>(g.xyz + 3 * static_cast<size_t>(e), rr, Y, nullptr,
+                edge_harmonics<S::LMAX, false>(g.xyz + 3 * static_cast<size_t>(e - g.edge_base), rr, Y, nullptr,
                                                nullptr, nullptr, dir);
                 s_x[ts.slot] = ts.x;
                 s_row[ts.slot] = ts.row;
@@ -468,23 +469,23 @@ r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
             const int e = base + t;
             if (ts.active) {
                 const int sl = ts.slot;
-                edge_harmonics<S::LMAX, true>(g.xyz + 3 * static_cast<size_t>(e), rr, s_Y[sl], s_dY[sl][0],
+                edge_harmonics<S::LMAX, true>(g.xyz + 3 * static_cast<size_t>(e - g.edge_base), rr, s_Y[sl], s_dY[sl][0],
                                               s_dY[sl][1], s_dY[sl][2], s_geo[sl]);
                 s_geo[sl][3] = ts.x;
                 s_row[sl] = ts.row;
                 s_src[sl] = g.source[e];
                 s_eid[sl] = e;
-                s_dsc[sl] = a.d1.table ? dcoef * density_slope(a.d1.table, a.grid, g.edge_pair[e] >> 16, rr) : 0.0f;
+                s_dsc[sl] = a.d1.table ? dcoef * density_slope(a.d1.table, a.grid, g.edge_pair[e - g.edge_base] >> 16, rr) : 0.0f;
                 if constexpr (!kFactored) {
 #pragma unroll
                     for (int q = 0; q < NT; ++q) s_cgY[sl][q] = cg[q] * s_Y[sl][S::term_lm1[q]];
                 }
             } else if (t < n) {
                 // beyond r_cut: only the A1 density-scale term (reverse_A1_scaled visits every neighbour)
-                double* out = forces + 3 * static_cast<size_t>(e);
+                double* out = forces + 3 * static_cast<size_t>(e - g.edge_base);
                 float d = 0.0f;
-                if (a.d1.table) d = dcoef * density_slope(a.d1.table, a.grid, g.edge_pair[e] >> 16, rr);
-                const double* x = g.xyz + 3 * static_cast<size_t>(e);
+                if (a.d1.table) d = dcoef * density_slope(a.d1.table, a.grid, g.edge_pair[e - g.edge_base] >> 16, rr);
+                const double* x = g.xyz + 3 * static_cast<size_t>(e - g.edge_base);
                 out[0] = static_cast<double>(d * static_cast<float>(x[0] / rr));
                 out[1] = static_cast<double>(d * static_cast<float>(x[1] / rr));
                 out[2] = static_cast<double>(d * static_cast<float>(x[2] / rr));
@@ -549,7 +550,7 @@ r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
             for (int p = 0; p < NP; ++p) A = fmaf(dR[p], ap[p], A);
             const int e = uniform(s_eid[j]);
             if (k < C) {
-                const auto ms = buffer_rsrc(msg + static_cast<size_t>(e - a.edge_base) * NLMS * C, h_bytes);
+                const auto ms = buffer_rsrc(msg + static_cast<size_t>(e - a.graph.edge_base) * NLMS * C, h_bytes);
 #pragma unroll
                 for (int q = 0; q < NLMS; ++q) store1(m[q], ms, k * 4, q * C * 4);
             }
@@ -592,7 +593,7 @@ r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
             double f[3] = {0.0, 0.0, 0.0};
             for (int w = 0; w < nwaves * kForceParts; ++w)
                 for (int c = 0; c < 3; ++c) f[c] += static_cast<double>(s_f[t][w][c]);
-            double* out = forces + 3 * static_cast<size_t>(s_eid[t]);
+            double* out = forces + 3 * static_cast<size_t>(s_eid[t] - g.edge_base);
 #pragma unroll
             for (int c = 0; c < 3; ++c) out[c] = -f[c] + static_cast<double>(s_dsc[t] * s_geo[t][c]);
         }
@@ -728,7 +729,7 @@ __device__ __forceinline__ void r1_reverse_pass(const LayerArgs& a, int i, bool 
         for (int p = 0; p < RG::NP; ++p) A = fmaf(dR[p], ap[p], A);
         const int e = uniform(L.eid[j]);
         if (k < C) {
-            const auto ms = buffer_rsrc(msg + static_cast<size_t>(e - a.edge_base) * NLMS * C, h_bytes);
+            const auto ms = buffer_rsrc(msg + static_cast<size_t>(e - a.graph.edge_base) * NLMS * C, h_bytes);
 #pragma unroll
             for (int q = 0; q < RG::NH; ++q) store1(m[q], ms, k * 4, RG::h_lm2[q] * C * 4);
         }
@@ -785,19 +786,19 @@ __global__ void __launch_bounds__(256) r1_reverse_grouped_kernel(LayerArgs a, co
             const int e = base + t;
             if (ts.active) {
                 const int sl = ts.slot;
-                edge_harmonics<S::LMAX, true>(g.xyz + 3 * static_cast<size_t>(e), rr, L.Y[sl], L.dY[sl][0],
+                edge_harmonics<S::LMAX, true>(g.xyz + 3 * static_cast<size_t>(e - g.edge_base), rr, L.Y[sl], L.dY[sl][0],
                                               L.dY[sl][1], L.dY[sl][2], L.geo[sl]);
                 L.geo[sl][3] = ts.x;
                 L.row[sl] = ts.row;
                 L.src[sl] = g.source[e];
                 L.eid[sl] = e;
-                L.dsc[sl] = a.d1.table ? dcoef * density_slope(a.d1.table, a.grid, g.edge_pair[e] >> 16, rr) : 0.0f;
+                L.dsc[sl] = a.d1.table ? dcoef * density_slope(a.d1.table, a.grid, g.edge_pair[e - g.edge_base] >> 16, rr) : 0.0f;
             } else if (t < n) {
                 // beyond r_cut: only the A1 density-scale term (reverse_A1_scaled visits every neighbour)
-                double* out = forces + 3 * static_cast<size_t>(e);
+                double* out = forces + 3 * static_cast<size_t>(e - g.edge_base);
                 float d = 0.0f;
-                if (a.d1.table) d = dcoef * density_slope(a.d1.table, a.grid, g.edge_pair[e] >> 16, rr);
-                const double* x = g.xyz + 3 * static_cast<size_t>(e);
+                if (a.d1.table) d = dcoef * density_slope(a.d1.table, a.grid, g.edge_pair[e - g.edge_base] >> 16, rr);
+                const double* x = g.xyz + 3 * static_cast<size_t>(e - g.edge_base);
                 out[0] = static_cast<double>(d * static_cast<float>(x[0] / rr));
                 out[1] = static_cast<double>(d * static_cast<float>(x[1] / rr));
                 out[2] = static_cast<double>(d * static_cast<float>(x[2] / rr));
@@ -812,7 +813,7 @@ __global__ void __launch_bounds__(256) r1_reverse_grouped_kernel(LayerArgs a, co
             double f[3] = {0.0, 0.0, 0.0};
             for (int w = 0; w < nwaves * kForcePartsGrouped; ++w)
                 for (int c = 0; c < 3; ++c) f[c] += static_cast<double>(L.f[t][w][c]);
-            double* out = forces + 3 * static_cast<size_t>(L.eid[t]);
+            double* out = forces + 3 * static_cast<size_t>(L.eid[t] - g.edge_base);
 #pragma unroll
             for (int c = 0; c < 3; ++c) out[c] = -f[c] + static_cast<double>(L.dsc[t] * L.geo[t][c]);
         }
@@ -892,17 +893,17 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
             const int e = base + t;
             if (ts.active) {
                 const int sl = ts.slot;
-                edge_harmonics<LMAX, true>(g.xyz + 3 * static_cast<size_t>(e), rr, s_Y[sl], s_dY[sl][0],
+                edge_harmonics<LMAX, true>(g.xyz + 3 * static_cast<size_t>(e - g.edge_base), rr, s_Y[sl], s_dY[sl][0],
                                            s_dY[sl][1], s_dY[sl][2], s_geo[sl]);
                 s_geo[sl][3] = ts.x;
                 s_row[sl] = ts.row;
                 s_eid[sl] = e;
-                s_dsc[sl] = a.d0.table ? dcoef * density_slope(a.d0.table, a.grid, g.edge_pair[e] >> 16, rr) : 0.0f;
+                s_dsc[sl] = a.d0.table ? dcoef * density_slope(a.d0.table, a.grid, g.edge_pair[e - g.edge_base] >> 16, rr) : 0.0f;
             } else if (t < n && a.d0.table) {
                 // beyond r_cut: only the density-scale term (reverse_A0_scaled visits every neighbour)
-                const float d = dcoef * density_slope(a.d0.table, a.grid, g.edge_pair[e] >> 16, rr);
-                const double* x = g.xyz + 3 * static_cast<size_t>(e);
-                double* out = forces + 3 * static_cast<size_t>(e);
+                const float d = dcoef * density_slope(a.d0.table, a.grid, g.edge_pair[e - g.edge_base] >> 16, rr);
+                const double* x = g.xyz + 3 * static_cast<size_t>(e - g.edge_base);
+                double* out = forces + 3 * static_cast<size_t>(e - g.edge_base);
                 out[0] += static_cast<double>(d * static_cast<float>(x[0] / rr));
                 out[1] += static_cast<double>(d * static_cast<float>(x[1] / rr));
                 out[2] += static_cast<double>(d * static_cast<float>(x[2] / rr));
@@ -956,7 +957,7 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
             double f[3] = {0.0, 0.0, 0.0};
             for (int w = 0; w < nwaves * kForcePartsA0; ++w)
                 for (int c = 0; c < 3; ++c) f[c] += static_cast<double>(s_f[t][w][c]);
-            double* out = forces + 3 * static_cast<size_t>(s_eid[t]);
+            double* out = forces + 3 * static_cast<size_t>(s_eid[t] - g.edge_base);
 #pragma unroll
             for (int c = 0; c < 3; ++c) out[c] += -f[c] + static_cast<double>(s_dsc[t] * s_geo[t][c]);
         }
@@ -969,10 +970,10 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
 // not read); the sum runs over the edges in ascending edge order.
 constexpr int kGatherGroup = 8;
 
-// The message of edge e is row e - edge_base.
+// The message (and r) of edge e is row e - g.edge_base.
 template <int V>
 __device__ __forceinline__ void gather_range(const EdgeGraph& g, double r_cut, const float4* __restrict__ m4,
-                                             long long edge_base, int row4, int t0, int t1, float4 (&acc)[V])
+                                             int row4, int t0, int t1, float4 (&acc)[V])
 {
     const int tid = threadIdx.x, T = blockDim.x;
     for (int t = t0; t < t1; t += kGatherGroup) {
@@ -982,8 +983,8 @@ __device__ __forceinline__ void gather_range(const EdgeGraph& g, double r_cut, c
         for (int u = 0; u < kGatherGroup; ++u) {
             const int tt = min(t + u, t1 - 1);
             const int e = g.tedge[tt];
-            row[u] = e - edge_base;
-            on[u] = t + u < t1 && g.r[e] < r_cut;
+            row[u] = e - g.edge_base;
+            on[u] = t + u < t1 && g.r[row[u]] < r_cut;
         }
         float4 v[kGatherGroup][V];
 #pragma unroll
@@ -1015,8 +1016,8 @@ __global__ void __launch_bounds__(256) gather_messages_kernel(LayerArgs a, int r
     float4 acc[V];
 #pragma unroll
     for (int q = 0; q < V; ++q) acc[q] = make_float4(0.f, 0.f, 0.f, 0.f);
-    gather_range<V>(a.graph, a.grid.r_cut, reinterpret_cast<const float4*>(msg), 0, row4, a.graph.tfirst[s],
-                          a.graph.tfirst[s + 1], acc);
+    gather_range<V>(a.graph, a.grid.r_cut, reinterpret_cast<const float4*>(msg), row4, a.graph.tfirst[s],
+                    a.graph.tfirst[s + 1], acc);
     float4* out = reinterpret_cast<float4*>(H1_adj) + static_cast<size_t>(s) * row4;
 #pragma unroll
     for (int q = 0; q < V; ++q) {
@@ -1038,8 +1039,8 @@ __global__ void __launch_bounds__(256) gather_tile_runs_kernel(LayerArgs a, Tile
     float4 acc[V];
 #pragma unroll
     for (int q = 0; q < V; ++q) acc[q] = make_float4(0.f, 0.f, 0.f, 0.f);
-    gather_range<V>(a.graph, a.grid.r_cut, reinterpret_cast<const float4*>(msg), a.edge_base, row4, t0,
-                           t0 + runs.length[run], acc);
+    gather_range<V>(a.graph, a.grid.r_cut, reinterpret_cast<const float4*>(msg), row4, t0, t0 + runs.length[run],
+                    acc);
     float4* out = reinterpret_cast<float4*>(H1_adj) + static_cast<size_t>(runs.source[run]) * row4;
 #pragma unroll
     for (int q = 0; q < V; ++q) {
@@ -1173,7 +1174,7 @@ __global__ void __launch_bounds__(kReduceThreads) totals_partial_kernel(
 
 __global__ void __launch_bounds__(256) totals_final_kernel(int num_partials,
                                                          const double* __restrict__ partials,
-                                                         double* __restrict__ out)
+                                                         double* __restrict__ out, int accumulate)
 {
     __shared__ double s[256][10];
     const int t = threadIdx.x;
@@ -1188,24 +1189,27 @@ __global__ void __launch_bounds__(256) totals_final_kernel(int num_partials,
             for (int c = 0; c < 10; ++c) s[t][c] += s[t + w][c];
         __syncthreads();
     }
-    if (t < 10) out[t] = s[0][t];
+    if (t < 10) out[t] = accumulate ? out[t] + s[0][t] : s[0][t];
 }
 
 // ZBL pair term of every neighbour (zbl_kokkos.cpp:76-126, 154-201): one wave
 // per receiver, lanes over its edges; the energy partial sums are combined
 // by a fixed butterfly, so the result does not depend on scheduling.
-__global__ void __launch_bounds__(256) zbl_kernel(int N, const int* __restrict__ first,
-                                                  const int* __restrict__ edge_pair, const double* __restrict__ xyz,
-                                                  const double* __restrict__ r, ZblArgs z,
-                                                  double* __restrict__ energies, double* __restrict__ forces)
+__global__ void __launch_bounds__(256) zbl_kernel(int node_begin, int N, const int* __restrict__ first,
+                                                  long long edge_base, const int* __restrict__ edge_pair,
+                                                  const double* __restrict__ xyz, const double* __restrict__ r,
+                                                  ZblArgs z, double* __restrict__ energies,
+                                                  double* __restrict__ forces)
 {
     const int lane = threadIdx.x & 63;
-    const int i = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (i >= N) return;
+    const int local = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (local >= N) return;
+    const int i = node_begin + local;
     const int p = z.p;
     const double k0 = (p + 1.0) * (p + 2.0) / 2.0, k1 = p * (p + 2.0), k2 = p * (p + 1.0) / 2.0;
     double energy = 0.0;
-    for (int e = first[i] + lane; e < first[i + 1]; e += 64) {
+    for (int ge = first[i] + lane; ge < first[i + 1]; ge += 64) {
+        const long long e = ge - edge_base;  // index into the per-edge arrays
         const int po = edge_pair[e] & 0xffff;
         const double rr = r[e];
         const double r_max = z.r_max[po];
@@ -1237,6 +1241,127 @@ __global__ void __launch_bounds__(256) zbl_kernel(int N, const int* __restrict__
     }
     for (int off = 32; off > 0; off >>= 1) energy += __shfl_xor(energy, off, 64);
     if (lane == 0) energies[i] += energy;
+}
+
+// Tiled execution: the geometry of one tile's edges in the reused arena --
+// edge vector, length and pair code of edge e at index e - edge_base.  One
+// wave per receiver, lanes over its edges.  The vector is the caller's
+// (explicit) or the reference vector of the prepared geometry plus the
+// displacement difference, as edge_geometry_kernel forms it graph-wide.
+__global__ void __launch_bounds__(256) tile_geometry_kernel(TileGeometry g)
+{
+    const int lane = threadIdx.x & 63;
+    const int local = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (local >= g.node_count) return;
+    const int i = g.node_begin + local;
+    const int a = g.type_active[g.node_types[i]];
+    const double* cell = g.cell;
+    for (int e = g.first[i] + lane; e < g.first[i + 1]; e += 64) {
+        const size_t le = static_cast<size_t>(e - g.edge_base);
+        const size_t j = g.source[e];
+        double v[3];
+        if (g.explicit_xyz) {
+            for (int c = 0; c < 3; ++c) v[c] = g.explicit_xyz[3 * static_cast<size_t>(e) + c];
+            g.xyz[3 * le] = v[0];
+            g.xyz[3 * le + 1] = v[1];
+            g.xyz[3 * le + 2] = v[2];
+            g.r[le] = g.explicit_r[e];
+        } else {
+            double ref[3];
+            if (g.ref.edges) {
+                const double* f = g.ref.edges + 3 * static_cast<size_t>(e);
+                if (g.ref.fractional) {
+                    for (int c = 0; c < 3; ++c) ref[c] = f[0] * cell[c] + f[1] * cell[3 + c] + f[2] * cell[6 + c];
+                } else {
+                    ref[0] = f[0], ref[1] = f[1], ref[2] = f[2];
+                }
+            } else {
+                const int* sh = g.ref.shifts + 3 * static_cast<size_t>(e);
+                const double* pj = g.ref.positions + 3 * j;
+                const double* pi = g.ref.positions + 3 * static_cast<size_t>(i);
+                if (g.ref.fractional) {
+                    double d[3];
+                    for (int axis = 0; axis < 3; ++axis) d[axis] = pj[axis] - pi[axis] + static_cast<double>(sh[axis]);
+                    for (int c = 0; c < 3; ++c) ref[c] = d[0] * cell[c] + d[1] * cell[3 + c] + d[2] * cell[6 + c];
+                } else {
+                    for (int c = 0; c < 3; ++c) {
+                        ref[c] = pj[c] - pi[c];
+                        for (int axis = 0; axis < 3; ++axis) ref[c] += static_cast<double>(sh[axis]) * cell[3 * axis + c];
+                    }
+                }
+            }
+            for (int c = 0; c < 3; ++c) v[c] = ref[c] + g.disp[3 * j + c] - g.disp[3 * static_cast<size_t>(i) + c];
+            const double d2 = v[0] * v[0] + v[1] * v[1] + v[2] * v[2];
+            if (!(d2 > 0.0) || !(d2 < 1.0e300)) {
+                if (g.invalid) atomicAdd(g.invalid, 1ull);
+                v[0] = g.r_cut;
+                v[1] = 0.0;
+                v[2] = 0.0;
+            }
+            g.xyz[3 * le] = v[0];
+            g.xyz[3 * le + 1] = v[1];
+            g.xyz[3 * le + 2] = v[2];
+            g.r[le] = sqrt(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]);
+        }
+        if (g.pair_source) {
+            g.edge_pair[le] = g.pair_source[e];
+        } else {
+            const int b = g.type_active[g.node_types[j]];
+            const int po = a * g.num_active + b;
+            const int pu = g.shared_tables ? 0 : unordered_pair(a, b, g.num_active);
+            g.edge_pair[le] = po | (pu << 16);
+        }
+    }
+}
+
+// Tiled execution: a tile's directed forces into the atom forces, in a fixed
+// order.  Receiver part: F[i] -= sum over the receiver's edges (one wave per
+// receiver, lanes over edges, fixed butterfly).  Source part: F[s] += sum
+// over each source run of the tile (one wave per run; the runs of a tile have
+// distinct sources, and both launches run in stream order).
+__global__ void __launch_bounds__(256) fold_receiver_forces_kernel(int node_begin, int N, const int* __restrict__ first,
+                                                                   long long edge_base, const double* __restrict__ f,
+                                                                   double* __restrict__ out)
+{
+    const int lane = threadIdx.x & 63;
+    const int local = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (local >= N) return;
+    const int i = node_begin + local;
+    double acc[3] = {0.0, 0.0, 0.0};
+    for (int e = first[i] + lane; e < first[i + 1]; e += 64) {
+        const size_t le = static_cast<size_t>(e - edge_base);
+        acc[0] += f[3 * le], acc[1] += f[3 * le + 1], acc[2] += f[3 * le + 2];
+    }
+    for (int off = 32; off > 0; off >>= 1)
+        for (int c = 0; c < 3; ++c) acc[c] += __shfl_xor(acc[c], off, 64);
+    if (lane == 0)
+        for (int c = 0; c < 3; ++c) out[3 * static_cast<size_t>(i) + c] -= acc[c];
+}
+
+__global__ void __launch_bounds__(256) fold_source_runs_kernel(TileRuns runs, const int* __restrict__ tedge,
+                                                               long long edge_base, const double* __restrict__ f,
+                                                               double* __restrict__ out)
+{
+    const int lane = threadIdx.x & 63;
+    const int run = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (run >= runs.count) return;
+    const int t0 = runs.start[run], t1 = t0 + runs.length[run];
+    double acc[3] = {0.0, 0.0, 0.0};
+    for (int t = t0 + lane; t < t1; t += 64) {
+        const size_t le = static_cast<size_t>(tedge[t] - edge_base);
+        acc[0] += f[3 * le], acc[1] += f[3 * le + 1], acc[2] += f[3 * le + 2];
+    }
+    for (int off = 32; off > 0; off >>= 1)
+        for (int c = 0; c < 3; ++c) acc[c] += __shfl_xor(acc[c], off, 64);
+    if (lane == 0)
+        for (int c = 0; c < 3; ++c) out[3 * static_cast<size_t>(runs.source[run]) + c] += acc[c];
+}
+
+__global__ void fill_f64_kernel(double* __restrict__ out, long long n, double value)
+{
+    for (long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += static_cast<long long>(gridDim.x) * blockDim.x)
+        out[i] = value;
 }
 
 inline int node_threads(int C) { return ((C + 63) / 64) * 64; }
@@ -1360,11 +1485,41 @@ hipError_t launch_add_direct(int nodes, int C, int num_LM, const float* direct, 
     return hipGetLastError();
 }
 
-hipError_t launch_zbl(int num_nodes, const int* first, const int* edge_pair, const double* xyz, const double* r,
-                      const ZblArgs& z, double* energies, double* forces, hipStream_t s)
+hipError_t launch_zbl(int node_begin, int num_nodes, const int* first, long long edge_base, const int* edge_pair,
+                      const double* xyz, const double* r, const ZblArgs& z, double* energies, double* forces,
+                      hipStream_t s)
 {
     if (num_nodes <= 0) return hipSuccess;
-    zbl_kernel<<<(num_nodes + 3) / 4, 256, 0, s>>>(num_nodes, first, edge_pair, xyz, r, z, energies, forces);
+    zbl_kernel<<<(num_nodes + 3) / 4, 256, 0, s>>>(node_begin, num_nodes, first, edge_base, edge_pair, xyz, r, z,
+                                                   energies, forces);
+    return hipGetLastError();
+}
+
+hipError_t launch_tile_geometry(const TileGeometry& g, hipStream_t s)
+{
+    if (g.node_count <= 0) return hipSuccess;
+    if (!g.explicit_xyz && !g.ref.edges && !(g.ref.shifts && g.ref.positions)) return hipErrorInvalidValue;
+    tile_geometry_kernel<<<(g.node_count + 3) / 4, 256, 0, s>>>(g);
+    return hipGetLastError();
+}
+
+hipError_t launch_fold_tile_forces(int node_begin, int node_count, const int* first, const TileRuns& runs,
+                                   const int* tedge, long long edge_base, const double* forces, double* atom_forces,
+                                   hipStream_t s)
+{
+    if (node_count > 0)
+        fold_receiver_forces_kernel<<<(node_count + 3) / 4, 256, 0, s>>>(node_begin, node_count, first, edge_base,
+                                                                         forces, atom_forces);
+    if (runs.count > 0)
+        fold_source_runs_kernel<<<(runs.count + 3) / 4, 256, 0, s>>>(runs, tedge, edge_base, forces, atom_forces);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_f64(double* out, long long n, double value, hipStream_t s)
+{
+    if (n <= 0) return hipSuccess;
+    const long long blocks = std::min<long long>((n + 255) / 256, 65536);
+    fill_f64_kernel<<<static_cast<int>(blocks), 256, 0, s>>>(out, n, value);
     return hipGetLastError();
 }
 
@@ -1397,11 +1552,11 @@ int reduce_totals_partials(int num_nodes, int num_edges)
 
 hipError_t launch_reduce_totals(int num_nodes, int num_edges, const double* energies,
                                 const double* forces, const double* xyz, double inv_volume,
-                                double* partials, int num_partials, double* out, hipStream_t s)
+                                double* partials, int num_partials, double* out, hipStream_t s, bool accumulate)
 {
     totals_partial_kernel<<<num_partials, kReduceThreads, 0, s>>>(num_nodes, num_edges, energies, forces,
                                                                   xyz, inv_volume, partials);
-    totals_final_kernel<<<1, 256, 0, s>>>(num_partials, partials, out);
+    totals_final_kernel<<<1, 256, 0, s>>>(num_partials, partials, out, accumulate ? 1 : 0);
     return hipGetLastError();
 }
 
