@@ -276,7 +276,17 @@ def capacity_run(args):
     print(f"[capacity] setup {time.perf_counter() - t_setup:.1f} s; running {args.md_steps} steps on the device",
           file=sys.stderr, flush=True)
     t_run = time.perf_counter()
-    res = ev._md_nve(types, m, s.positions, v, s.cell, args.skin, args.md_dt, args.md_steps)
+    try:
+        res = ev._md_nve(types, m, s.positions, v, s.cell, args.skin, args.md_dt, args.md_steps)
+    except (OverflowError, MemoryError, RuntimeError, ValueError) as err:
+        # refused before any evaluation (int32 edge limit, memory): say why
+        print(json.dumps({
+            "metric": "tiled capacity: atoms per MI355X and us/atom/step of a 20-step NVE run (FP32)",
+            "capacity_atoms": N, "refused": True, "error": f"{type(err).__name__}: {err}",
+            "execution_plan": ev.execution_plan_report,
+            "config": {"workload": f"medium-shape random-init MACE ({args.preset}) on SrTiO3 "
+                                   f"{args.capacity_cells}^3 ({N} atoms)"}}), flush=True)
+        return
     t_run = time.perf_counter() - t_run
     times = list(res["step_seconds"])
     etot = res["potential_energy"] + res["kinetic_energy"]
@@ -298,6 +308,10 @@ def capacity_run(args):
         "num_tiles": st["num_tiles"],
         "tiled_evaluations": st["tiled_evaluations"],
         "device_bytes": st["device_bytes"],
+        "device_bytes_per_atom": round(st["device_bytes"] / N, 1),
+        "execution_plan": {k: v for k, v in ev.execution_plan_report.items() if k != "candidates"}
+        | {"candidates": [{k: c[k] for k in ("id", "qualified", "estimated_bytes")}
+                          for c in ev.execution_plan_report["candidates"]]},
         "config": {"workload": f"medium-shape random-init MACE ({args.preset}) on SrTiO3 {args.capacity_cells}^3 "
                                f"({N} atoms, sigma {args.sigma} A, seed {args.seed}), cutoff {ev.r_cut} + "
                                f"{args.skin} A skin, 300 K Maxwell-Boltzmann start",

@@ -644,16 +644,11 @@ void Evaluator::plan_tiles()
     // runs of the source-major lists per tile: at least one per source with edges
     const std::size_t tiled = graph_tiled + work_bytes_estimate(std::min(T, std::max(N, 1)), tile_edges, true) +
                               3 * sizeof(int) * static_cast<std::size_t>(std::max(N, 1));
-    // memory budget: free device memory plus what this evaluator already holds
-    // of what the plans allocate
+    // memory budget: free device memory plus the graph and work memory this
+    // evaluator holds now (the estimates count all of a plan's memory)
     std::size_t free_bytes = 0, total_bytes = 0;
     hip_check(hipMemGetInfo(&free_bytes, &total_bytes), "memory info");
-    const std::size_t held = A0_.bytes() + M0_.bytes() + Phi1_.bytes() + A1_.bytes() + A1adj_.bytes() +
-                             msg_.bytes() + M0s_.bytes() + run_source_.bytes() + run_start_.bytes() +
-                             run_length_.bytes() + tile_xyz_.bytes() + tile_r_.bytes() + tile_pair_.bytes() +
-                             tile_forces_.bytes() + xyz_.bytes() + r_.bytes() + forces_.bytes();
-    const std::size_t graph = graph_tiled;  // held by both plans at this point
-    rep.available_bytes = free_bytes + held + graph;
+    rep.available_bytes = free_bytes + held_graph_bytes();
     rep.reserve_bytes = rep.available_bytes / 10;
     const std::size_t budget = rep.available_bytes - rep.reserve_bytes;
     const bool tiled_permitted = allow_fixed_workspace_ || plan_debug_ == kTiled;
@@ -724,6 +719,22 @@ void Evaluator::plan_tiles()
                                     run_start_.as<int>(), run_length_.as<int>(), stream_),
               "tile runs");
     hip_check(hipStreamSynchronize(stream_), "tile plan");
+}
+
+// Device bytes this evaluator holds for graphs and their work arrays (not
+// the model and radial tables).
+std::size_t Evaluator::held_graph_bytes() const
+{
+    const DeviceBuffer* buffers[] = {
+        &node_types_, &first_, &receiver_, &source_, &tfirst_, &tedge_, &edge_pair_, &disp_, &positions_,
+        &cell_dev_, &xyz_, &r_, &geo_positions_, &geo_edges_, &geo_shifts_, &A0_, &M0_, &H1_, &Phi1_, &A1_,
+        &A1adj_, &direct_, &H1adj_, &msg_, &energies_, &forces_, &atom_forces_, &partials_, &totals_, &scratch_,
+        &scale1_, &dot1_, &M0s_, &run_source_, &run_start_, &run_length_, &node_order_, &m0_blocks_,
+        &readout_blocks_, &tile_xyz_, &tile_r_, &tile_pair_, &tile_forces_, &tile_first_edge_dev_,
+        &pgraph_.first, &pgraph_.sources, &pgraph_.shifts, &pgraph_.fractional_xyz, &pgraph_.fractional_positions};
+    std::size_t total = 0;
+    for (const DeviceBuffer* b : buffers) total += b->bytes();
+    return total;
 }
 
 // Device bytes of the graph-wide state of the prepared graph.  Both plans:

@@ -363,6 +363,7 @@ private:
     std::string plan_profile_ = "capacity", plan_debug_;
     ExecutionPlanReport plan_report_;
     std::size_t graph_bytes_estimate(bool tiled) const;
+    std::size_t held_graph_bytes() const;
     std::size_t work_bytes_estimate(long long receivers, long long edges, bool tiled) const;
     // tile arena: geometry, pair codes and directed forces of one tile's
     // edges (edge e at index e - first edge of the tile)
