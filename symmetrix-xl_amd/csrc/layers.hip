@@ -271,6 +271,9 @@ __global__ void __launch_bounds__(256) a0_forward_kernel(LayerArgs a, const floa
 // consumed (the compiler otherwise issues each read just before its use).
 // ---------------------------------------------------------------------------
 constexpr int kWBatch = 4;
+// shapes with at most this many paths keep a spline row in registers for the
+// next edge of the same interval
+constexpr int kRowReusePaths = 10;
 
 template <class S>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S::NPL <= 96 ? 3 : 1)))
@@ -336,20 +339,27 @@ r1_forward_kernel(LayerArgs a, const float* __restrict__ r1,
         }
         __syncthreads();
         const int count = uniform(s_count);
-        auto fetch = [&](int j, float4v* c, float* H) {
+        auto fetch_row = [&](int j, float4v* c) {
             const auto rs = buffer_rsrc(r1 + static_cast<size_t>(uniform(s_row[j])) * NP * C * 4, row_bytes);
-            const auto hs = buffer_rsrc(H1 + static_cast<size_t>(uniform(s_src[j])) * NLMS * C, h_bytes);
 #pragma unroll
             for (int p = 0; p < NP; ++p) c[p] = load4(rs, kk * 16, p * C * 16);
+        };
+        auto fetch_h = [&](int j, float* H) {
+            const auto hs = buffer_rsrc(H1 + static_cast<size_t>(uniform(s_src[j])) * NLMS * C, h_bytes);
 #pragma unroll
             for (int q = 0; q < NLMS; ++q) H[q] = load1(hs, kk * 4, q * C * 4);
         };
         // One row buffer: once the radial values of edge j are formed, its
-        // coefficient registers are refilled with the row of edge j + 1 (an
-        // L1 hit when both share the row).
+        // coefficient registers are refilled with the row of edge j + 1 --
+        // only when that row differs: the slots are sorted by row, so edges
+        // of one spline interval reuse the registers (a wave-uniform branch;
+        // shapes with up to kRowReusePaths paths).
         float4v c[NP];
         float H[NLMS];
-        if (count > 0) fetch(0, c, H);
+        if (count > 0) {
+            fetch_row(0, c);
+            fetch_h(0, H);
+        }
         for (int j = 0; j < count; ++j) {
             const float4v* Wj = s_W[j];
             float4v wb[2][kWBatch];
@@ -360,7 +370,11 @@ r1_forward_kernel(LayerArgs a, const float* __restrict__ r1,
             float RH[NPQ];
 #pragma unroll
             for (int pq = 0; pq < NPQ; ++pq) RH[pq] = cubic(c[S::pq_p[pq]], x) * H[S::pq_lm2[pq]];
-            fetch(min(j + 1, count - 1), c, H);
+            const int jn = min(j + 1, count - 1);
+            // (the wide shapes' row registers leave no room for the branch:
+            // they reload, an L1 hit)
+            if (S::NP > kRowReusePaths || uniform(s_row[jn]) != uniform(s_row[j])) fetch_row(jn, c);
+            fetch_h(jn, H);
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
                 if (b + 1 < NB) {
@@ -965,45 +979,63 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
 }
 
 // H1 adjoint gather.  A message row (num_LM x C floats) is read as float4s,
-// the block's threads covering the whole row, with the rows of kGatherGroup
-// edges in flight.  Edges at or beyond r_cut carry no message (their rows are
-// not read); the sum runs over the edges in ascending edge order.
-constexpr int kGatherGroup = 8;
+// the block's threads covering the whole row.  The source's edge list is
+// taken 64 edges at a time: wave 0 reads the edge ids and lengths and
+// compacts the edges within r_cut (the others carry no message) into LDS in
+// ascending edge order, then every thread streams the listed rows with
+// kGatherDepth float4 loads in flight (kGatherDepth / V rows of V float4s)
+// -- no load in the streaming loop waits on another.  Rows are summed in
+// ascending edge order.
+constexpr int kGatherStage = 64;
+constexpr int kGatherDepth = 16;
 
 // The message (and r) of edge e is row e - g.edge_base.
 template <int V>
 __device__ __forceinline__ void gather_range(const EdgeGraph& g, double r_cut, const float4* __restrict__ m4,
                                              int row4, int t0, int t1, float4 (&acc)[V])
 {
+    __shared__ int s_rows[kGatherStage];
+    __shared__ int s_n;
     const int tid = threadIdx.x, T = blockDim.x;
-    for (int t = t0; t < t1; t += kGatherGroup) {
-        long long row[kGatherGroup];
-        bool on[kGatherGroup];
-#pragma unroll
-        for (int u = 0; u < kGatherGroup; ++u) {
-            const int tt = min(t + u, t1 - 1);
-            const int e = g.tedge[tt];
-            row[u] = e - g.edge_base;
-            on[u] = t + u < t1 && g.r[row[u]] < r_cut;
+    for (int base = t0; base < t1; base += kGatherStage) {
+        __syncthreads();  // the previous rows are consumed
+        if (tid < 64) {
+            const int tt = base + tid;
+            bool on = false;
+            int row = 0;
+            if (tt < t1) {
+                row = static_cast<int>(g.tedge[tt] - g.edge_base);
+                on = g.r[row] < r_cut;
+            }
+            const unsigned long long mask = __ballot(on);
+            const int slot = __builtin_amdgcn_mbcnt_hi(static_cast<unsigned>(mask >> 32),
+                                                       __builtin_amdgcn_mbcnt_lo(static_cast<unsigned>(mask), 0));
+            if (on) s_rows[slot] = row;
+            if (tid == 0) s_n = __popcll(mask);
         }
-        float4 v[kGatherGroup][V];
+        __syncthreads();
+        const int n = s_n;
+        constexpr int D = kGatherDepth / V > 4 ? kGatherDepth / V : 4;  // rows per thread in flight
+        for (int j = 0; j < n; j += D) {
+            float4 v[D][V];
 #pragma unroll
-        for (int u = 0; u < kGatherGroup; ++u)
+            for (int u = 0; u < D; ++u)
 #pragma unroll
-            for (int q = 0; q < V; ++q) {
-                const int c = tid + q * T;
-                v[u][q] = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (on[u] && c < row4) v[u][q] = m4[row[u] * row4 + c];
-            }
+                for (int q = 0; q < V; ++q) {
+                    const int c = tid + q * T;
+                    v[u][q] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (j + u < n && c < row4) v[u][q] = m4[static_cast<size_t>(s_rows[j + u]) * row4 + c];
+                }
 #pragma unroll
-        for (int u = 0; u < kGatherGroup; ++u)
+            for (int u = 0; u < D; ++u)
 #pragma unroll
-            for (int q = 0; q < V; ++q) {
-                acc[q].x += v[u][q].x;
-                acc[q].y += v[u][q].y;
-                acc[q].z += v[u][q].z;
-                acc[q].w += v[u][q].w;
-            }
+                for (int q = 0; q < V; ++q) {
+                    acc[q].x += v[u][q].x;
+                    acc[q].y += v[u][q].y;
+                    acc[q].z += v[u][q].z;
+                    acc[q].w += v[u][q].w;
+                }
+        }
     }
 }
 
