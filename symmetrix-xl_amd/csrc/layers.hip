@@ -192,7 +192,8 @@ __global__ void __launch_bounds__(256) a0_forward_kernel(LayerArgs a, const floa
     __shared__ float s_Y[kTile][NLM];
     __shared__ float s_x[kTile];
     __shared__ int s_row[kTile];
-    __shared__ int s_count;
+    __shared__ int s_gstart[kTile + 1];  // first slot of each run of equal rows
+    __shared__ int s_count, s_groups;
 
     __shared__ float s_scale;
 
@@ -226,26 +227,45 @@ __global__ void __launch_bounds__(256) a0_forward_kernel(LayerArgs a, const floa
 #pragma unroll
                 for (int lm = 0; lm < NLM; ++lm) s_Y[ts.slot][lm] = Y[lm];
             }
+            // runs of equal rows among the (row-sorted) slots: lane t checks
+            // slot t against slot t - 1
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const int count = uniform(s_count);
+            const bool start = t < count && (t == 0 || s_row[t] != s_row[t - 1]);
+            const unsigned long long starts = __ballot(start);
+            const int g = __builtin_amdgcn_mbcnt_hi(static_cast<unsigned>(starts >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo(static_cast<unsigned>(starts), 0));
+            if (start) s_gstart[g] = t;
+            if (t == 0) {
+                s_groups = __popcll(starts);
+                s_gstart[__popcll(starts)] = count;
+            }
         }
         __syncthreads();
-        const int count = uniform(s_count);
-        // spline rows double-buffered: the row of edge j + 1 is in flight
-        // while edge j is accumulated
-        auto fetch = [&](int j, float4v* c) {
-            const auto rs = buffer_rsrc(r0f + static_cast<size_t>(uniform(s_row[j])) * NL * C * 4, row_bytes);
+        // one spline row per run of edges in the same interval, a ring of
+        // kDepth rows in flight while earlier runs are accumulated
+        const int groups = uniform(s_groups);
+        auto fetch = [&](int gi, float4v* c) {
+            const int row = uniform(s_row[uniform(s_gstart[gi])]);
+            const auto rs = buffer_rsrc(r0f + static_cast<size_t>(row) * NL * C * 4, row_bytes);
 #pragma unroll
             for (int l = 0; l < NL; ++l) c[l] = load4(rs, voff, l * C * 16);
         };
-        auto accumulate = [&](int j, const float4v* c) {
-            const float x = uniform(s_x[j]);
-            float R[NL];
+        auto accumulate = [&](int gi, const float4v* c) {
+            const int j1 = uniform(s_gstart[gi + 1]);
+            for (int j = uniform(s_gstart[gi]); j < j1; ++j) {
+                const float x = uniform(s_x[j]);
+                float R[NL];
 #pragma unroll
-            for (int l = 0; l < NL; ++l) R[l] = cubic(c[l], x);
+                for (int l = 0; l < NL; ++l) R[l] = cubic(c[l], x);
 #pragma unroll
-            for (int lm = 0; lm < NLM; ++lm) acc[lm] = fmaf(R[kLmL[lm]], s_Y[j][lm], acc[lm]);
+                for (int lm = 0; lm < NLM; ++lm) acc[lm] = fmaf(R[kLmL[lm]], s_Y[j][lm], acc[lm]);
+            }
         };
         float4v ring[kDepth][NL];
-        stream_ring<kDepth>(count, ring, fetch, accumulate);
+        stream_ring<kDepth>(groups, ring, fetch, accumulate);
     }
     if (a.d0.table) {
         __syncthreads();
