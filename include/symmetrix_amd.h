@@ -66,6 +66,18 @@ typedef struct {
     int tiled_evaluations;     /* evaluations that ran the tiled plan */
     int tile_receivers;        /* receivers per tile of the prepared graph, 0 = untiled */
     int num_tiles;
+    /* Observability counters (factorized_prepared_graph_count,
+     * factorized_prepared_evaluation_count, factorized_preparation_fence_count,
+     * factorized_evaluation_fence_count, mace_kokkos.cpp:925-970): host time
+     * of the last graph preparation; host waits on the evaluator's stream
+     * summed over graph preparations and over evaluations; kernel launches,
+     * device allocations and host waits of the last evaluation. */
+    double last_graph_prepare_ms;
+    int64_t preparation_fences;
+    int64_t evaluation_fences;
+    int64_t last_evaluation_launches;
+    int64_t last_evaluation_allocations;
+    int64_t last_evaluation_fences;
 } sxl_stats_t;
 
 /* Message of the last failed call on this thread ("" if none). */

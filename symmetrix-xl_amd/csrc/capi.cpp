@@ -358,6 +358,12 @@ int sxl_stats(const sxl_evaluator* ev, sxl_stats_t* out)
         out->tiled_evaluations = s.tiled_evaluations;
         out->tile_receivers = s.tile_receivers;
         out->num_tiles = s.num_tiles;
+        out->last_graph_prepare_ms = s.last_graph_prepare_ms;
+        out->preparation_fences = s.preparation_fences;
+        out->evaluation_fences = s.evaluation_fences;
+        out->last_evaluation_launches = s.last_evaluation_launches;
+        out->last_evaluation_allocations = s.last_evaluation_allocations;
+        out->last_evaluation_fences = s.last_evaluation_fences;
     });
 }
 

@@ -25,18 +25,25 @@ void hip_check(hipError_t err, const char* what)
         throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(err));
 }
 
-// Copies a host vector into a device buffer and waits, so the (often
-// temporary) host vector may be released as soon as this returns.
+// Copies a host vector into a device buffer.  Without staging it waits, so
+// the (often temporary) host vector may be released as soon as this returns;
+// with staging the copy is made from a byte copy kept in *staging, which the
+// caller holds until its next wait on the stream.
 template <class T>
-void upload(DeviceBuffer& buf, const std::vector<T>& host, hipStream_t s)
+void upload(DeviceBuffer& buf, const std::vector<T>& host, hipStream_t s,
+            std::vector<std::vector<unsigned char>>* staging = nullptr)
 {
     buf.reserve(std::max<std::size_t>(host.size() * sizeof(T), sizeof(T)));
-    if (!host.empty()) {
-        hip_check(hipMemcpyAsync(buf.as<void>(), host.data(), host.size() * sizeof(T),
-                                 hipMemcpyHostToDevice, s),
-                  "upload");
-        hip_check(hipStreamSynchronize(s), "upload");
+    if (host.empty()) return;
+    const std::size_t bytes = host.size() * sizeof(T);
+    const void* src = host.data();
+    if (staging) {
+        const auto* b = reinterpret_cast<const unsigned char*>(host.data());
+        staging->emplace_back(b, b + bytes);
+        src = staging->back().data();
     }
+    hip_check(hipMemcpyAsync(buf.as<void>(), src, bytes, hipMemcpyHostToDevice, s), "upload");
+    if (!staging) hip_check(host_fence(s), "upload");
 }
 
 std::vector<float> to_float(const double* p, std::size_t n)
@@ -204,6 +211,12 @@ std::atomic<std::size_t> g_device_bytes{0};
 
 std::size_t device_bytes_in_use() { return g_device_bytes.load(); }
 
+ThreadCounters& thread_counters()
+{
+    thread_local ThreadCounters counters;
+    return counters;
+}
+
 DeviceBuffer::~DeviceBuffer() { release(); }
 
 void DeviceBuffer::release()
@@ -230,6 +243,29 @@ void DeviceBuffer::reserve(std::size_t bytes)
     ptr_ = p;
     bytes_ = bytes;
     g_device_bytes += bytes;
+    ++thread_counters().allocations;
+}
+
+void Evaluator::account_preparation(const CallStart& start)
+{
+    stats_.preparation_fences += static_cast<long long>(thread_counters().fences - start.counters.fences);
+    stats_.last_graph_prepare_ms =
+        std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - start.time).count();
+}
+
+void Evaluator::wait(const char* what)
+{
+    hip_check(host_fence(stream_), what);
+    staged_.clear();
+}
+
+void Evaluator::account_evaluation(const CallStart& start)
+{
+    const ThreadCounters& now = thread_counters();
+    stats_.last_evaluation_launches = static_cast<long long>(now.launches - start.counters.launches);
+    stats_.last_evaluation_allocations = static_cast<long long>(now.allocations - start.counters.allocations);
+    stats_.last_evaluation_fences = static_cast<long long>(now.fences - start.counters.fences);
+    stats_.evaluation_fences += stats_.last_evaluation_fences;
 }
 
 Evaluator::Evaluator(const std::string& model_path, const std::string& head)
@@ -267,7 +303,7 @@ Evaluator::Evaluator(const std::string& model_path, const std::string& head)
     grid_.intervals = model_.spline_points - 1;
     grid_.r_cut = model_.r_cut;
     upload_static_tables();
-    hip_check(hipStreamSynchronize(stream_), "model upload");
+    hip_check(host_fence(stream_), "model upload");
 }
 
 void Evaluator::set_profiling(bool enable) { set_profiling_stages(enable ? ~0u : 0u); }
@@ -304,7 +340,7 @@ void Evaluator::mark(int stage, bool end)
 
 Evaluator::~Evaluator()
 {
-    if (stream_) (void)hipStreamSynchronize(stream_);
+    if (stream_) (void)host_fence(stream_);
     for (auto& e : events_) (void)hipEventDestroy(e);
     // buffers free themselves; the stream goes last
     A0_.release();
@@ -471,8 +507,8 @@ void Evaluator::prepare_active_types(const std::vector<int>& node_types)
             });
         for (auto& t : pool) t.join();
     }
-    upload(r1_, r1, stream_);
-    upload(r0f_, r0f, stream_);
+    upload(r1_, r1, stream_, &staged_);
+    upload(r0f_, r0f, stream_, &staged_);
     // density-normalisation splines per unordered pair: [pair_u][iv][4]
     auto density_table = [&](const RadialNetwork& net, DeviceBuffer& out) {
         std::vector<float> table(static_cast<std::size_t>(npairs) * NI * 4);
@@ -486,7 +522,7 @@ void Evaluator::prepare_active_types(const std::vector<int>& node_types)
                     table[(static_cast<std::size_t>(pu) * NI + iv) * 4 + q] = static_cast<float>(c4[q]);
             }
         }
-        upload(out, table, stream_);
+        upload(out, table, stream_, &staged_);
     };
     if (m.A0_scaled) density_table(m.A0net, dens0_);
     if (m.A1_scaled) density_table(m.A1net, dens1_);
@@ -502,14 +538,14 @@ void Evaluator::prepare_active_types(const std::vector<int>& node_types)
                 pref[ai * na + aj] = 14.3996 * static_cast<double>(zu * zv);
                 rmax[ai * na + aj] = m.zbl_radii[zu] + m.zbl_radii[zv];
             }
-        upload(zbl_inverse_a_, inv_a, stream_);
-        upload(zbl_prefactor_, pref, stream_);
-        upload(zbl_rmax_, rmax, stream_);
+        upload(zbl_inverse_a_, inv_a, stream_, &staged_);
+        upload(zbl_prefactor_, pref, stream_, &staged_);
+        upload(zbl_rmax_, rmax, stream_, &staged_);
     }
     // per active type tables
     std::vector<int> type_active(m.num_elements, -1);
     for (int a = 0; a < na; ++a) type_active[types[a]] = a;
-    upload(type_active_, type_active, stream_);
+    upload(type_active_, type_active, stream_, &staged_);
     std::vector<float> p0c, p1c, h2m0, h2m0t;
     std::vector<double> e0;
     // coefficients [active][slot][C] on the slots of the polynomial layouts
@@ -533,12 +569,11 @@ void Evaluator::prepare_active_types(const std::vector<int>& node_types)
         h2m0t.insert(h2m0t.end(), hmt.begin(), hmt.end());
         e0.push_back(m.atomic_energies[t]);
     }
-    upload(p0_coef_, p0c, stream_);
-    upload(p1_coef_, p1c, stream_);
-    upload(h2m0_, h2m0, stream_);
-    upload(h2m0t_, h2m0t, stream_);
-    upload(e0_, e0, stream_);
-    hip_check(hipStreamSynchronize(stream_), "active type upload");
+    upload(p0_coef_, p0c, stream_, &staged_);
+    upload(p1_coef_, p1c, stream_, &staged_);
+    upload(h2m0_, h2m0, stream_, &staged_);
+    upload(h2m0t_, h2m0t, stream_, &staged_);
+    upload(e0_, e0, stream_, &staged_);
     active_types_ = types;
 }
 
@@ -626,13 +661,7 @@ void Evaluator::plan_tiles()
     ExecutionPlanReport rep;
     rep.requested_profile = plan_profile_;
     rep.selection_source = plan_debug_.empty() ? "native_request" : "debug_override";
-    std::vector<int> first(N + 1, 0);
-    if (N > 0) {
-        hip_check(hipMemcpyAsync(first.data(), first_.as<int>(), (N + 1) * sizeof(int), hipMemcpyDeviceToHost,
-                                 stream_),
-                  "copy");
-        hip_check(hipStreamSynchronize(stream_), "sync");
-    }
+    const std::vector<int>& first = host_first_;
     // candidate estimates: graph state + work arrays
     const std::size_t graph_untiled = graph_bytes_estimate(false);
     const std::size_t graph_tiled = graph_bytes_estimate(true);
@@ -693,7 +722,7 @@ void Evaluator::plan_tiles()
     // runs: count per tile, scan on the host, fill (an edge's tile from the
     // tiles' first edges)
     std::vector<int> tfe(tile_first_edge_.begin(), tile_first_edge_.end());
-    upload(tile_first_edge_dev_, tfe, stream_);
+    upload(tile_first_edge_dev_, tfe, stream_, &staged_);
     DeviceBuffer per_source, per_tile, offsets;
     per_source.reserve(static_cast<std::size_t>(N) * sizeof(int));
     per_tile.reserve(static_cast<std::size_t>(num_tiles_) * sizeof(int));
@@ -705,20 +734,20 @@ void Evaluator::plan_tiles()
     hip_check(hipMemcpyAsync(counts.data(), per_tile.as<int>(), num_tiles_ * sizeof(int), hipMemcpyDeviceToHost,
                              stream_),
               "copy");
-    hip_check(hipStreamSynchronize(stream_), "sync");
+    wait("sync");
     tile_run_offsets_.assign(num_tiles_ + 1, 0);
     for (int t = 0; t < num_tiles_; ++t) tile_run_offsets_[t + 1] = tile_run_offsets_[t] + counts[t];
     const int runs = tile_run_offsets_[num_tiles_];
     run_source_.reserve(static_cast<std::size_t>(std::max(runs, 1)) * sizeof(int));
     run_start_.reserve(static_cast<std::size_t>(std::max(runs, 1)) * sizeof(int));
     run_length_.reserve(static_cast<std::size_t>(std::max(runs, 1)) * sizeof(int));
-    upload(offsets, tile_run_offsets_, stream_);
+    upload(offsets, tile_run_offsets_, stream_, &staged_);
     hip_check(hipMemsetAsync(per_tile.as<void>(), 0, num_tiles_ * sizeof(int), stream_), "memset");
     hip_check(launch_tile_runs_fill(N, tfirst_.as<int>(), tedge_.as<int>(), tile_first_edge_dev_.as<int>(),
                                     num_tiles_, offsets.as<int>(), per_tile.as<int>(), run_source_.as<int>(),
                                     run_start_.as<int>(), run_length_.as<int>(), stream_),
               "tile runs");
-    hip_check(hipStreamSynchronize(stream_), "tile plan");
+    wait("tile plan");
 }
 
 // Device bytes this evaluator holds for graphs and their work arrays (not
@@ -877,9 +906,9 @@ void Evaluator::plan_node_blocks()
         m0_block_offsets_[t + 1] = static_cast<int>(m0b.size());
         readout_block_offsets_[t + 1] = static_cast<int>(rob.size());
     }
-    upload(node_order_, order, stream_);
-    upload(m0_blocks_, m0b, stream_);
-    upload(readout_blocks_, rob, stream_);
+    upload(node_order_, order, stream_, &staged_);
+    upload(m0_blocks_, m0b, stream_, &staged_);
+    upload(readout_blocks_, rob, stream_, &staged_);
 }
 
 NodeBlocks Evaluator::node_blocks(const DeviceBuffer& blocks, const std::vector<int>& offsets, int tile) const
@@ -894,7 +923,7 @@ NodeBlocks Evaluator::node_blocks(const DeviceBuffer& blocks, const std::vector<
 
 void Evaluator::invalidate_graph()
 {
-    hip_check(hipStreamSynchronize(stream_), "synchronize");
+    wait("synchronize");
     ++generation_;
     evaluated_generation_ = 0;
     reduced_ = false;
@@ -922,8 +951,9 @@ void Evaluator::finish_graph(const int* host_neigh_types, const int* host_source
     const int N = num_nodes_;
     const int E = static_cast<int>(num_edges_);
     // transpose: count -> scan -> fill -> sort each source segment ascending
+    // (its work arrays live until the preparation's final wait)
+    DeviceBuffer counts, offsets64;
     {
-        DeviceBuffer counts, offsets64;
         counts.reserve((N + 1) * sizeof(int));
         offsets64.reserve((N + 1) * sizeof(long long));
         scratch_.reserve(scan_scratch_size(N + 1) * sizeof(long long));
@@ -941,7 +971,6 @@ void Evaluator::finish_graph(const int* host_neigh_types, const int* host_source
                                         tedge_.as<int>(), stream_),
                   "transpose fill");
         hip_check(launch_sort_segments(N, tfirst_.as<int>(), tedge_.as<int>(), stream_), "sort");
-        hip_check(hipStreamSynchronize(stream_), "transpose");
     }
     // caller-provided source types (prepare_graph): checked, and the pair
     // codes formed on the host; they follow from the node types unless a
@@ -954,11 +983,7 @@ void Evaluator::finish_graph(const int* host_neigh_types, const int* host_source
         const int na = static_cast<int>(active_types_.size());
         host_pairs.resize(E);
         std::size_t e = 0;
-        std::vector<int> first(N + 1);
-        hip_check(hipMemcpyAsync(first.data(), first_.as<int>(), (N + 1) * sizeof(int), hipMemcpyDeviceToHost,
-                                 stream_),
-                  "copy");
-        hip_check(hipStreamSynchronize(stream_), "sync");
+        const std::vector<int>& first = host_first_;
         for (int i = 0; i < N; ++i) {
             const int a = ta[host_types_[i]];
             for (int j = first[i]; j < first[i + 1]; ++j, ++e) {
@@ -978,7 +1003,7 @@ void Evaluator::finish_graph(const int* host_neigh_types, const int* host_source
         receiver_.reserve(static_cast<std::size_t>(std::max(E, 1)) * sizeof(int));
         hip_check(launch_receivers(N, first_.as<int>(), receiver_.as<int>(), stream_), "receivers");
         if (host_neigh_types) {
-            upload(edge_pair_, host_pairs, stream_);
+            upload(edge_pair_, host_pairs, stream_, &staged_);
         } else {
             edge_pair_.reserve(static_cast<std::size_t>(std::max(E, 1)) * sizeof(int));
             hip_check(launch_edge_pairs(E, receiver_.as<int>(), source_.as<int>(), node_types_.as<int>(),
@@ -988,17 +1013,17 @@ void Evaluator::finish_graph(const int* host_neigh_types, const int* host_source
         }
     } else {
         // graph-wide per-edge state of the untiled plan is not kept
-        hip_check(hipStreamSynchronize(stream_), "synchronize");
+        wait("synchronize");
         receiver_.release();
         if (pair_from_types_)
             edge_pair_.release();
         else
-            upload(edge_pair_, host_pairs, stream_);
+            upload(edge_pair_, host_pairs, stream_, &staged_);
         if (periodic_) pgraph_.fractional_xyz.release();  // edges from cell shifts instead
     }
     plan_node_blocks();
     allocate_workspace();
-    hip_check(hipStreamSynchronize(stream_), "graph preparation");
+    wait("graph preparation");
     ++generation_;
     evaluated_generation_ = 0;
     reduced_ = false;
@@ -1012,6 +1037,7 @@ void Evaluator::finish_graph(const int* host_neigh_types, const int* host_source
 std::uint64_t Evaluator::prepare_graph(int num_nodes, const int* node_types, const int* num_neigh,
                                        const int* neigh_indices, const int* neigh_types)
 {
+    const CallStart start;
     if (num_nodes < 0 || num_nodes >= std::numeric_limits<int>::max())
         throw std::length_error("MACE graph atom count exceeds the 32-bit CSR limit.");
     std::vector<int> types(node_types, node_types + num_nodes);
@@ -1035,14 +1061,16 @@ std::uint64_t Evaluator::prepare_graph(int num_nodes, const int* node_types, con
     num_nodes_ = num_nodes;
     num_edges_ = E;
     periodic_ = false;
-    upload(node_types_, types, stream_);
-    upload(first_, first, stream_);
+    upload(node_types_, types, stream_, &staged_);
+    upload(first_, first, stream_, &staged_);
+    host_first_ = std::move(first);
     std::vector<int> src(neigh_indices, neigh_indices + E);
-    upload(source_, src, stream_);
+    upload(source_, src, stream_, &staged_);
     positions_.reserve(static_cast<std::size_t>(std::max(num_nodes, 1)) * 3 * sizeof(double));
     disp_.reserve(static_cast<std::size_t>(std::max(num_nodes, 1)) * 3 * sizeof(double));
     geometry_mode_ = kGeometryNone;
     finish_graph(neigh_types, neigh_indices);
+    account_preparation(start);
     return generation_;
 }
 
@@ -1100,7 +1128,7 @@ NeighborPlan neighbor_plan(int num_nodes, const double* cell, const double* inve
 int neighbor_plan_bins(const NeighborPlan& plan) { return plan.bins[0] * plan.bins[1] * plan.bins[2]; }
 
 void build_periodic_graph(const double* d_positions, int num_nodes, const double* cell, const double* inverse_cell,
-                          double cutoff, hipStream_t stream, PeriodicGraph& out)
+                          double cutoff, hipStream_t stream, PeriodicGraph& out, std::vector<int>* host_first)
 {
     const NeighborPlan plan = neighbor_plan(num_nodes, cell, inverse_cell, cutoff);
     const int N = num_nodes;
@@ -1146,7 +1174,7 @@ void build_periodic_graph(const double* d_positions, int num_nodes, const double
     long long total = 0;
     hip_check(hipMemcpyAsync(&total, offsets.as<long long>() + N, sizeof(long long), hipMemcpyDeviceToHost, stream),
               "copy");
-    hip_check(hipStreamSynchronize(stream), "edge count");
+    hip_check(host_fence(stream), "edge count");
     if (total > std::numeric_limits<int>::max())
         throw std::length_error("neighbor graph exceeds 32-bit edge indexing");
     const int E = static_cast<int>(total);
@@ -1161,7 +1189,13 @@ void build_periodic_graph(const double* d_positions, int num_nodes, const double
                                     out.sources.as<int>(), out.shifts.as<int>(), out.fractional_xyz.as<double>(),
                                     stream),
               "fill edges");
-    hip_check(hipStreamSynchronize(stream), "graph build");
+    if (host_first) {
+        host_first->resize(static_cast<std::size_t>(N) + 1);
+        hip_check(hipMemcpyAsync(host_first->data(), out.first.as<int>(), (N + 1) * sizeof(int),
+                                 hipMemcpyDeviceToHost, stream),
+                  "offsets copy");
+    }
+    hip_check(host_fence(stream), "graph build");
     out.num_nodes = N;
     out.num_edges = E;
 }
@@ -1170,6 +1204,7 @@ std::uint64_t Evaluator::prepare_periodic_graph(int num_nodes, const int* node_t
                                                 bool device_positions, const double* cell,
                                                 const double* inverse_cell, double cutoff)
 {
+    const CallStart start;
     validate_periodic_inputs(num_nodes, cell, inverse_cell, cutoff);
     std::vector<int> types(node_types, node_types + num_nodes);
     // from here on the graph state changes: a preparation that fails part way
@@ -1183,7 +1218,7 @@ std::uint64_t Evaluator::prepare_periodic_graph(int num_nodes, const int* node_t
                                  device_positions ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, stream_),
                   "positions");
     disp_.reserve(static_cast<std::size_t>(std::max(N, 1)) * 3 * sizeof(double));
-    build_periodic_graph(positions_.as<double>(), N, cell, inverse_cell, cutoff, stream_, pgraph_);
+    build_periodic_graph(positions_.as<double>(), N, cell, inverse_cell, cutoff, stream_, pgraph_, &host_first_);
     const int E = static_cast<int>(pgraph_.num_edges);
     first_.reserve((N + 1) * sizeof(int));
     hip_check(hipMemcpyAsync(first_.as<int>(), pgraph_.first.as<int>(), (N + 1) * sizeof(int),
@@ -1198,13 +1233,14 @@ std::uint64_t Evaluator::prepare_periodic_graph(int num_nodes, const int* node_t
     periodic_ = true;
     std::memcpy(cell_, cell, sizeof(cell_));
     std::memcpy(inverse_cell_, inverse_cell, sizeof(inverse_cell_));
-    upload(node_types_, types, stream_);
+    upload(node_types_, types, stream_, &staged_);
     upload_cell();
     finish_graph(nullptr, nullptr);
     // the build's fractional positions and edge vectors are the graph's geometry
     geometry_mode_ = kGeometryBuilt;
     geometry_generation_ = generation_;
     geometry_pbc_ = 7;
+    account_preparation(start);
     return generation_;
 }
 
@@ -1212,7 +1248,7 @@ void Evaluator::upload_cell()
 {
     std::vector<double> cellv(cell_, cell_ + 9);
     cellv.insert(cellv.end(), inverse_cell_, inverse_cell_ + 9);
-    upload(cell_dev_, cellv, stream_);
+    upload(cell_dev_, cellv, stream_, &staged_);
 }
 
 // New cell for the prepared graph (reference update_factorized_cell): edge
@@ -1288,8 +1324,8 @@ void Evaluator::prepare_geometry(std::uint64_t generation, const double* referen
         !all_finite(cell, 9) || !all_finite(inverse_cell, 9))
         throw std::invalid_argument("Execution R1 prepared geometry contains a non-finite value.");
     geometry_mode_ = kGeometryNone;
-    upload(geo_positions_, std::vector<double>(reference_positions, reference_positions + num_positions), stream_);
-    upload(geo_edges_, std::vector<double>(reference_xyz, reference_xyz + num_xyz), stream_);
+    upload(geo_positions_, std::vector<double>(reference_positions, reference_positions + num_positions), stream_, &staged_);
+    upload(geo_edges_, std::vector<double>(reference_xyz, reference_xyz + num_xyz), stream_, &staged_);
     set_cell(cell, inverse_cell);
     geometry_pbc_ = (pbc[0] ? 1 : 0) | (pbc[1] ? 2 : 0) | (pbc[2] ? 4 : 0);
     geometry_mode_ = fractional ? kGeometryFractional : kGeometryCartesian;
@@ -1312,8 +1348,8 @@ void Evaluator::prepare_shift_geometry(std::uint64_t generation, const double* r
     if (!all_finite(reference_positions, num_positions) || !all_finite(cell, 9) || !all_finite(inverse_cell, 9))
         throw std::invalid_argument("Shift geometry contains a non-finite value.");
     geometry_mode_ = kGeometryNone;
-    upload(geo_positions_, std::vector<double>(reference_positions, reference_positions + num_positions), stream_);
-    upload(geo_shifts_, std::vector<int>(shifts, shifts + num_shifts), stream_);
+    upload(geo_positions_, std::vector<double>(reference_positions, reference_positions + num_positions), stream_, &staged_);
+    upload(geo_shifts_, std::vector<int>(shifts, shifts + num_shifts), stream_, &staged_);
     set_cell(cell, inverse_cell);
     geometry_pbc_ = (pbc[0] ? 1 : 0) | (pbc[1] ? 2 : 0) | (pbc[2] ? 4 : 0);
     geometry_mode_ = kGeometryShifts;
@@ -1390,7 +1426,7 @@ void Evaluator::graph_arrays(std::uint64_t generation, int* num_neigh, int* rece
                                      hipMemcpyDeviceToHost, stream_),
                       "copy");
     }
-    hip_check(hipStreamSynchronize(stream_), "graph copy");
+    hip_check(host_fence(stream_), "graph copy");
     if (receiver_offsets) std::copy(first.begin(), first.end(), receiver_offsets);
     if (num_neigh)
         for (int i = 0; i < N; ++i) num_neigh[i] = first[i + 1] - first[i];
@@ -1408,7 +1444,7 @@ void Evaluator::graph_arrays(std::uint64_t generation, int* num_neigh, int* rece
         hip_check(hipMemcpyAsync(frac.data(), pgraph_.fractional_positions.as<double>(), N * 3 * sizeof(double),
                                  hipMemcpyDeviceToHost, stream_),
                   "copy");
-        hip_check(hipStreamSynchronize(stream_), "graph copy");
+        hip_check(host_fence(stream_), "graph copy");
         for (int i = 0; i < N; ++i)
             for (long long e = first[i]; e < first[i + 1]; ++e)
                 for (int a = 0; a < 3; ++a)
@@ -1419,6 +1455,7 @@ void Evaluator::graph_arrays(std::uint64_t generation, int* num_neigh, int* rece
 
 void Evaluator::compute_positions(std::uint64_t generation, const double* positions, bool device_positions)
 {
+    const CallStart start;
     require_geometry(generation);
     const int N = num_nodes_;
     if (N > 0 && positions != positions_.as<double>())
@@ -1442,10 +1479,12 @@ void Evaluator::compute_positions(std::uint64_t generation, const double* positi
     check_geometry_ = true;
     explicit_geometry_ = false;
     evaluate();
+    account_evaluation(start);
 }
 
 void Evaluator::compute_xyz(std::uint64_t generation, const double* xyz, const double* r, bool device_arrays)
 {
+    const CallStart start;
     check_generation(generation);
     const long long E = num_edges_;
     const hipMemcpyKind kind = device_arrays ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
@@ -1460,6 +1499,7 @@ void Evaluator::compute_xyz(std::uint64_t generation, const double* xyz, const d
     check_geometry_ = false;
     explicit_geometry_ = true;
     evaluate();
+    account_evaluation(start);
 }
 
 double Evaluator::max_displacement(std::uint64_t generation, const double* positions, bool device_positions)
@@ -1477,7 +1517,7 @@ double Evaluator::max_displacement(std::uint64_t generation, const double* posit
     double d2 = 0.0;
     hip_check(hipMemcpyAsync(&d2, totals_.as<double>() + 12, sizeof(double), hipMemcpyDeviceToHost, stream_),
               "copy");
-    hip_check(hipStreamSynchronize(stream_), "displacement");
+    wait("displacement");
     return std::sqrt(d2);
 }
 
@@ -1980,8 +2020,8 @@ int Evaluator::md_nve(int num_atoms, const int* node_types, const double* masses
     md_v_.reserve(bytes3);
     hip_check(hipMemcpyAsync(md_x_.as<double>(), x, bytes3, hipMemcpyHostToDevice, stream_), "MD positions");
     hip_check(hipMemcpyAsync(md_v_.as<double>(), v, bytes3, hipMemcpyHostToDevice, stream_), "MD velocities");
-    upload(md_m_, m, stream_);
-    upload(md_inv_m_, inv_m, stream_);
+    upload(md_m_, m, stream_, &staged_);
+    upload(md_inv_m_, inv_m, stream_, &staged_);
     const int np = md_kinetic_partials(N);
     md_partials_.reserve(static_cast<std::size_t>(np) * sizeof(double));
     double* xd = md_x_.as<double>();
@@ -1999,7 +2039,7 @@ int Evaluator::md_nve(int num_atoms, const int* node_types, const double* masses
             double mv2 = 0.0;
             hip_check(hipMemcpyAsync(&mv2, totals_.as<double>() + 14, sizeof(double), hipMemcpyDeviceToHost, stream_),
                       "copy");
-            hip_check(hipStreamSynchronize(stream_), "kinetic energy");
+            wait("kinetic energy");
             ekin[step] = 0.5 * mv2 / kForceToAcceleration;
         }
     };
@@ -2017,14 +2057,14 @@ int Evaluator::md_nve(int num_atoms, const int* node_types, const double* masses
         compute_positions(gen, xd, true);
         hip_check(launch_md_kick(N, vd, atom_forces_.as<double>(), md_inv_m_.as<double>(), dtf, stream_), "MD kick");
         if (step_seconds) {
-            hip_check(hipStreamSynchronize(stream_), "MD step");
+            wait("MD step");
             step_seconds[step - 1] = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
         }
         energies(step);
     }
     hip_check(hipMemcpyAsync(x, xd, bytes3, hipMemcpyDeviceToHost, stream_), "MD positions");
     hip_check(hipMemcpyAsync(v, vd, bytes3, hipMemcpyDeviceToHost, stream_), "MD velocities");
-    hip_check(hipStreamSynchronize(stream_), "MD");
+    wait("MD");
     return rebuilds;
 }
 
@@ -2066,7 +2106,7 @@ void Evaluator::finish_evaluation()
                                  stream_),
                   "totals copy");
     }
-    hip_check(hipStreamSynchronize(stream_), "evaluation");
+    wait("evaluation");
     if (tiled) {
         for (int q = 0; q < 9; ++q) host_virial_[q] = host_totals_[17 + q];
         if (fuse) {
@@ -2087,10 +2127,13 @@ void Evaluator::finish_evaluation()
 void Evaluator::set_stress_from_virial(double volume)
 {
     for (int q = 0; q < 9; ++q) host_totals_[1 + q] = host_virial_[q] / volume;
-    hip_check(hipMemcpyAsync(totals_.as<double>() + 1, host_totals_ + 1, 9 * sizeof(double), hipMemcpyHostToDevice,
-                             stream_),
+    // copied from a staged copy: no wait here, the stream orders it before
+    // any later read of the device totals
+    const auto* b = reinterpret_cast<const unsigned char*>(host_totals_ + 1);
+    staged_.emplace_back(b, b + 9 * sizeof(double));
+    hip_check(hipMemcpyAsync(totals_.as<double>() + 1, staged_.back().data(), 9 * sizeof(double),
+                             hipMemcpyHostToDevice, stream_),
               "stress copy");
-    hip_check(hipStreamSynchronize(stream_), "stress copy");
 }
 
 // Energy and stress totals of the completed evaluation for `volume`, in
@@ -2127,7 +2170,7 @@ double Evaluator::last_max_displacement() const
     return std::sqrt(host_totals_[12]);
 }
 
-void Evaluator::synchronize() const { hip_check(hipStreamSynchronize(stream_), "synchronize"); }
+void Evaluator::synchronize() const { hip_check(host_fence(stream_), "synchronize"); }
 
 void Evaluator::node_energies(double* out) const
 {

@@ -12,6 +12,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <chrono>
 #include <cstdint>
 #include <memory>
 #include <string>
@@ -61,7 +62,7 @@ struct PeriodicGraph {
 // Validates inputs like the reference and throws on failure.
 void build_periodic_graph(const double* d_positions, int num_nodes, const double* cell,
                           const double* inverse_cell, double cutoff, hipStream_t stream,
-                          PeriodicGraph& out);
+                          PeriodicGraph& out, std::vector<int>* host_first = nullptr);
 void validate_periodic_inputs(int num_nodes, const double* cell, const double* inverse_cell,
                               double cutoff);
 // Bins and stencil reach of the cell-binned search (validates like the
@@ -112,6 +113,17 @@ struct EvaluatorStats {
     int tiled_evaluations = 0;
     int tile_receivers = 0;  // receivers per tile of the prepared graph, 0 = untiled plan
     int num_tiles = 0;
+    // Observability (reference mace_kokkos.cpp:925-970: prepared graph and
+    // evaluation counts, preparation and evaluation fences): host time of
+    // the last graph preparation; host waits on the stream summed over all
+    // graph preparations and over all evaluations; kernel launches, device
+    // allocations and host waits of the last evaluation.
+    double last_graph_prepare_ms = 0.0;
+    long long preparation_fences = 0;
+    long long evaluation_fences = 0;
+    long long last_evaluation_launches = 0;
+    long long last_evaluation_allocations = 0;
+    long long last_evaluation_fences = 0;
 };
 
 // Receivers per tile chosen by the planner when tiled execution is allowed
@@ -285,6 +297,15 @@ private:
     void add_direct(int nodes, int node_base, float* M0adj, hipStream_t s);
     void gemm_a1(int nodes, const float* in, float* out, bool reverse, const char* what);
     void reduce(double volume);
+    // counts of the calling thread at the start of a preparation/evaluation
+    struct CallStart {
+        ThreadCounters counters = thread_counters();
+        std::chrono::steady_clock::time_point time = std::chrono::steady_clock::now();
+    };
+    void account_preparation(const CallStart& start);
+    // waits for the stream and drops the host copies of staged uploads
+    void wait(const char* what);
+    void account_evaluation(const CallStart& start);
 
     HostModel model_;
     hipStream_t stream_ = nullptr;
@@ -320,6 +341,9 @@ private:
     int num_nodes_ = 0;
     long long num_edges_ = 0;
     std::vector<int> host_types_;
+    std::vector<int> host_first_;  // CSR receiver offsets of the prepared graph, [N + 1]
+    // host copies of uploads in flight, released at the next wait()
+    std::vector<std::vector<unsigned char>> staged_;
     double cell_[9] = {}, inverse_cell_[9] = {};
     PeriodicGraph pgraph_;
     // cell_dev_: cell (9) then inverse cell (9); disp_: [N][3] minimum-image

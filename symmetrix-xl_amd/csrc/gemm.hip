@@ -169,9 +169,9 @@ hipError_t launch_gemm_group(GemmGroup grp, hipStream_t stream)
     if (tiles == 0) return hipSuccess;
     if (tiles < 2 * 256) {
         tiles = number_tiles(32);
-        gemm_group_kernel<32><<<tiles, 256, 0, stream>>>(grp);
+        gemm_group_kernel<32><<<tiles, 256, 0, stream>>>(grp), note_launch();
     } else {
-        gemm_group_kernel<64><<<tiles, 256, 0, stream>>>(grp);
+        gemm_group_kernel<64><<<tiles, 256, 0, stream>>>(grp), note_launch();
     }
     return hipGetLastError();
 }

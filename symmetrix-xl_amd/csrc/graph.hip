@@ -234,9 +234,9 @@ hipError_t exclusive_scan(const In* in, int n, long long* out, long long* scratc
     // out has n+1 entries; out[n] = total
     const int nb = n > 0 ? (n + kScanSpan - 1) / kScanSpan : 0;
     if (nb > 0) {
-        scan_blocks_kernel<In><<<nb, kScanThreads, 0, s>>>(in, n, out, scratch);
-        scan_sums_kernel<<<1, kScanThreads, 0, s>>>(scratch, nb, out + n);
-        scan_add_kernel<<<(n + 255) / 256, 256, 0, s>>>(out, n, scratch);
+        scan_blocks_kernel<In><<<nb, kScanThreads, 0, s>>>(in, n, out, scratch), note_launch();
+        scan_sums_kernel<<<1, kScanThreads, 0, s>>>(scratch, nb, out + n), note_launch();
+        scan_add_kernel<<<(n + 255) / 256, 256, 0, s>>>(out, n, scratch), note_launch();
     } else {
         hipError_t err = hipMemsetAsync(out, 0, sizeof(long long), s);
         if (err != hipSuccess) return err;
@@ -458,7 +458,7 @@ hipError_t launch_edge_pairs(int num_edges, const int* receiver, const int* sour
 {
     if (num_edges <= 0) return hipSuccess;
     edge_pairs_kernel<<<(num_edges + 255) / 256, 256, 0, s>>>(num_edges, receiver, source, node_types,
-                                                              type_active, num_active, shared_tables, edge_pair);
+                                                              type_active, num_active, shared_tables, edge_pair), note_launch();
     return hipGetLastError();
 }
 
@@ -469,7 +469,7 @@ hipError_t launch_neighbor_bins(const NeighborPlan& p, const double* positions, 
     if (p.num_nodes <= 0) return hipSuccess;
     bins_kernel<<<(p.num_nodes + 255) / 256, 256, 0, s>>>(p, positions, reference_fractional, wrapped_positions,
                                                           wrapped_fractional, wrap_shifts, atom_bins,
-                                                          bin_sizes);
+                                                          bin_sizes), note_launch();
     return hipGetLastError();
 }
 
@@ -479,7 +479,7 @@ hipError_t launch_neighbor_fill_bins(const NeighborPlan& p, const int* atom_bins
     (void)bin_offsets;
     if (p.num_nodes <= 0) return hipSuccess;
     fill_bins_kernel<<<(p.num_nodes + 255) / 256, 256, 0, s>>>(p.num_nodes, atom_bins, bin_cursors,
-                                                               bin_atoms);
+                                                               bin_atoms), note_launch();
     return hipGetLastError();
 }
 
@@ -493,7 +493,7 @@ hipError_t launch_neighbor_edges(const NeighborPlan& p, const double* wrapped_po
     constexpr int per_block = kEdgeThreads / 64;
     edges_kernel<<<(p.num_nodes + per_block - 1) / per_block, kEdgeThreads, 0, s>>>(
         p, wrapped_positions, wrapped_fractional, wrap_shifts, atom_bins, bin_offsets, bin_atoms,
-        edge_offsets, edge_counts, sources, shifts, fractional_xyz);
+        edge_offsets, edge_counts, sources, shifts, fractional_xyz), note_launch();
     return hipGetLastError();
 }
 
@@ -514,21 +514,21 @@ hipError_t launch_exclusive_scan_i64(const long long* in, int n, long long* out,
 hipError_t launch_narrow_offsets(const long long* offsets, int n, int* out_offsets, int* out_counts,
                                  hipStream_t s)
 {
-    narrow_kernel<<<(n + 1 + 255) / 256, 256, 0, s>>>(offsets, n, out_offsets, out_counts);
+    narrow_kernel<<<(n + 1 + 255) / 256, 256, 0, s>>>(offsets, n, out_offsets, out_counts), note_launch();
     return hipGetLastError();
 }
 
 hipError_t launch_receivers(int num_nodes, const int* first, int* receiver, hipStream_t s)
 {
     if (num_nodes <= 0) return hipSuccess;
-    receivers_kernel<<<(num_nodes + 255) / 256, 256, 0, s>>>(num_nodes, first, receiver);
+    receivers_kernel<<<(num_nodes + 255) / 256, 256, 0, s>>>(num_nodes, first, receiver), note_launch();
     return hipGetLastError();
 }
 
 hipError_t launch_transpose_count(int num_edges, const int* source, int* counts, hipStream_t s)
 {
     if (num_edges <= 0) return hipSuccess;
-    transpose_count_kernel<<<(num_edges + 255) / 256, 256, 0, s>>>(num_edges, source, counts);
+    transpose_count_kernel<<<(num_edges + 255) / 256, 256, 0, s>>>(num_edges, source, counts), note_launch();
     return hipGetLastError();
 }
 
@@ -537,7 +537,7 @@ hipError_t launch_transpose_fill(int num_edges, const int* source, const int* tf
 {
     if (num_edges <= 0) return hipSuccess;
     transpose_fill_kernel<<<(num_edges + 255) / 256, 256, 0, s>>>(num_edges, source, tfirst, cursors,
-                                                                  tedge);
+                                                                  tedge), note_launch();
     return hipGetLastError();
 }
 
@@ -546,7 +546,7 @@ hipError_t launch_sort_segments(int num_segments, const int* offsets, int* value
     if (num_segments <= 0) return hipSuccess;
     constexpr int per_block = kSortThreads / 64;
     sort_segments_kernel<<<(num_segments + per_block - 1) / per_block, kSortThreads, 0, s>>>(num_segments,
-                                                                                           offsets, values);
+                                                                                           offsets, values), note_launch();
     return hipGetLastError();
 }
 
@@ -558,7 +558,7 @@ hipError_t launch_atom_displacements(int n, const double* positions, const Geome
     if (err != hipSuccess || n <= 0) return err;
     const int blocks = std::min((n + 255) / 256, 1024);
     atom_displacements_kernel<<<blocks, 256, 0, s>>>(n, positions, ref, cell, inverse_cell, displacements,
-                                                     reinterpret_cast<unsigned long long*>(out));
+                                                     reinterpret_cast<unsigned long long*>(out)), note_launch();
     return hipGetLastError();
 }
 
@@ -567,7 +567,7 @@ hipError_t launch_tile_runs_count(int num_nodes, const int* tfirst, const int* t
 {
     if (num_nodes <= 0) return hipSuccess;
     tile_runs_count_kernel<<<(num_nodes + 255) / 256, 256, 0, s>>>(num_nodes, tfirst, tedge, tile_first_edge,
-                                                                   num_tiles, runs_per_source, runs_per_tile);
+                                                                   num_tiles, runs_per_source, runs_per_tile), note_launch();
     return hipGetLastError();
 }
 
@@ -578,7 +578,7 @@ hipError_t launch_tile_runs_fill(int num_nodes, const int* tfirst, const int* te
     if (num_nodes <= 0) return hipSuccess;
     tile_runs_fill_kernel<<<(num_nodes + 255) / 256, 256, 0, s>>>(num_nodes, tfirst, tedge, tile_first_edge,
                                                                   num_tiles, tile_offsets, tile_cursors, run_source,
-                                                                  run_start, run_length);
+                                                                  run_start, run_length), note_launch();
     return hipGetLastError();
 }
 
@@ -689,9 +689,9 @@ void build_periodic_graph_noalloc(const double* d_positions, int num_nodes, cons
     if (edge_capacity < 0) throw std::invalid_argument("edge capacity must be non-negative");
     if (N == 0) {
         // no atoms, no edges: receiver_offsets = [0]
-        fill_i32_kernel<<<1, 64, 0, s>>>(d_receiver_offsets, 1, 0);
+        fill_i32_kernel<<<1, 64, 0, s>>>(d_receiver_offsets, 1, 0), note_launch();
         launch_check(hipGetLastError(), "neighbor graph");
-        launch_check(hipStreamSynchronize(s), "neighbor graph");
+        launch_check(host_fence(s), "neighbor graph");
         *num_edges = 0;
         return;
     }
@@ -709,13 +709,13 @@ void build_periodic_graph_noalloc(const double* d_positions, int num_nodes, cons
     int* bin_offsets = reinterpret_cast<int*>(base + noalloc::kBinOffsets);
     long long* scan = reinterpret_cast<long long*>(base + noalloc::kScan);
 
-    fill_i32_kernel<<<(B + 1 + 255) / 256, 256, 0, s>>>(bin_sizes, B + 1, 0);
+    fill_i32_kernel<<<(B + 1 + 255) / 256, 256, 0, s>>>(bin_sizes, B + 1, 0), note_launch();
     launch_check(hipGetLastError(), "clear bins");
     launch_check(launch_neighbor_bins(plan, d_positions, rf, wp, wf, wrap, atom_bins, bin_sizes, s), "bins");
     launch_check(launch_exclusive_scan_i32(bin_sizes, B, bin_off64, scan, s), "bin scan");
     launch_check(launch_narrow_offsets(bin_off64, B, bin_offsets, nullptr, s), "narrow");
     // cursors start at the bin offsets
-    copy_i32_kernel<<<(B + 255) / 256, 256, 0, s>>>(bin_sizes, bin_offsets, B);
+    copy_i32_kernel<<<(B + 255) / 256, 256, 0, s>>>(bin_sizes, bin_offsets, B), note_launch();
     launch_check(hipGetLastError(), "cursors");
     launch_check(launch_neighbor_fill_bins(plan, atom_bins, bin_offsets, bin_sizes, bin_atoms, s), "fill bins");
     launch_check(launch_sort_segments(B, bin_offsets, bin_atoms, s), "sort bins");
@@ -725,7 +725,7 @@ void build_periodic_graph_noalloc(const double* d_positions, int num_nodes, cons
     launch_check(launch_exclusive_scan_i64(counts, N, offsets, scan, s), "edge scan");
     long long total = 0;
     launch_check(hipMemcpyAsync(&total, offsets + N, sizeof(long long), hipMemcpyDeviceToHost, s), "edge count");
-    launch_check(hipStreamSynchronize(s), "edge count");
+    launch_check(host_fence(s), "edge count");
     *num_edges = total;
     if (total > std::numeric_limits<int>::max())
         throw std::length_error("neighbor graph exceeds 32-bit edge indexing");
@@ -736,7 +736,7 @@ void build_periodic_graph_noalloc(const double* d_positions, int num_nodes, cons
     launch_check(launch_neighbor_edges(plan, wp, wf, wrap, atom_bins, bin_offsets, bin_atoms, offsets, nullptr,
                                        d_sources, d_shifts, d_fractional_xyz, s),
                  "fill edges");
-    launch_check(hipStreamSynchronize(s), "neighbor graph");
+    launch_check(host_fence(s), "neighbor graph");
 }
 
 }  // namespace sxl

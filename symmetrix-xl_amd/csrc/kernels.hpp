@@ -22,6 +22,25 @@
 
 namespace sxl {
 
+// Work this library issues on the calling thread: kernel launches (every
+// launch site calls note_launch() after its <<<...>>>), device allocations
+// and host waits on a stream.  Counted per thread, so that the counts an
+// evaluator reads around one of its calls are its own while other threads
+// drive other evaluators.
+struct ThreadCounters {
+    std::uint64_t launches = 0;
+    std::uint64_t allocations = 0;
+    std::uint64_t fences = 0;
+};
+ThreadCounters& thread_counters();
+inline void note_launch() { ++thread_counters().launches; }
+// hipStreamSynchronize, counted as one host fence.
+inline hipError_t host_fence(hipStream_t s)
+{
+    ++thread_counters().fences;
+    return hipStreamSynchronize(s);
+}
+
 struct EdgeGraph {
     int num_nodes = 0;
     int num_edges = 0;

@@ -1428,8 +1428,8 @@ hipError_t launch_a0_forward(const LayerArgs& a, const float* r0f, float* A0, hi
     if (a.node_count <= 0) return hipSuccess;
     const int threads = node_threads(a.C);
     switch (a.l_max) {
-    case 2: a0_forward_kernel<2><<<a.node_count, threads, 0, s>>>(a, r0f, A0); break;
-    case 3: a0_forward_kernel<3><<<a.node_count, threads, 0, s>>>(a, r0f, A0); break;
+    case 2: a0_forward_kernel<2><<<a.node_count, threads, 0, s>>>(a, r0f, A0), note_launch(); break;
+    case 3: a0_forward_kernel<3><<<a.node_count, threads, 0, s>>>(a, r0f, A0), note_launch(); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -1441,8 +1441,8 @@ hipError_t launch_a0_reverse(const LayerArgs& a, const float* r0f, const float* 
     if (a.node_count <= 0) return hipSuccess;
     const int threads = node_threads(a.C);
     switch (a.l_max) {
-    case 2: a0_reverse_kernel<2><<<a.node_count, threads, 0, s>>>(a, r0f, A0, A0_adj, forces); break;
-    case 3: a0_reverse_kernel<3><<<a.node_count, threads, 0, s>>>(a, r0f, A0, A0_adj, forces); break;
+    case 2: a0_reverse_kernel<2><<<a.node_count, threads, 0, s>>>(a, r0f, A0, A0_adj, forces), note_launch(); break;
+    case 3: a0_reverse_kernel<3><<<a.node_count, threads, 0, s>>>(a, r0f, A0, A0_adj, forces), note_launch(); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -1454,11 +1454,11 @@ hipError_t launch_r1_forward(const LayerArgs& a, const float* r1, const float* c
     if (a.node_count <= 0) return hipSuccess;
     const int threads = node_threads(a.C);
     if (a.l_max == 2 && a.L_max == 1)
-        r1_forward_kernel<R1Shape<2, 1>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, Phi1);
+        r1_forward_kernel<R1Shape<2, 1>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, Phi1), note_launch();
     else if (a.l_max == 3 && a.L_max == 1)
-        r1_forward_kernel<R1Shape<3, 1>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, Phi1);
+        r1_forward_kernel<R1Shape<3, 1>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, Phi1), note_launch();
     else if (a.l_max == 3 && a.L_max == 2)
-        r1_forward_kernel<R1Shape<3, 2>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, Phi1);
+        r1_forward_kernel<R1Shape<3, 2>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, Phi1), note_launch();
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
@@ -1475,13 +1475,13 @@ hipError_t launch_r1_reverse(const LayerArgs& a, const float* r1, const float* c
     if (threads > 256) return hipErrorInvalidValue;
     if (a.l_max == 2 && a.L_max == 1)
         r1_reverse_kernel<R1Shape<2, 1>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, dPhi1,
-                                                                          forces, msg);
+                                                                          forces, msg), note_launch();
     else if (a.l_max == 3 && a.L_max == 1)
         r1_reverse_kernel<R1Shape<3, 1>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, dPhi1,
-                                                                          forces, msg);
+                                                                          forces, msg), note_launch();
     else if (a.l_max == 3 && a.L_max == 2)
         r1_reverse_grouped_kernel<R1Shape<3, 2>, 0, 1><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, dPhi1,
-                                                                                       forces, msg);
+                                                                                       forces, msg), note_launch();
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
@@ -1503,9 +1503,9 @@ hipError_t launch_gather_messages(const LayerArgs& a, const float* msg, float* H
     int row4, threads, v;
     gather_shape(a, row4, threads, v);
     switch (v) {
-    case 1: gather_messages_kernel<1><<<a.node_count, threads, 0, s>>>(a, row4, msg, H1_adj); break;
-    case 2: gather_messages_kernel<2><<<a.node_count, threads, 0, s>>>(a, row4, msg, H1_adj); break;
-    case 3: gather_messages_kernel<3><<<a.node_count, threads, 0, s>>>(a, row4, msg, H1_adj); break;
+    case 1: gather_messages_kernel<1><<<a.node_count, threads, 0, s>>>(a, row4, msg, H1_adj), note_launch(); break;
+    case 2: gather_messages_kernel<2><<<a.node_count, threads, 0, s>>>(a, row4, msg, H1_adj), note_launch(); break;
+    case 3: gather_messages_kernel<3><<<a.node_count, threads, 0, s>>>(a, row4, msg, H1_adj), note_launch(); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -1519,9 +1519,9 @@ hipError_t launch_gather_tile_runs(const LayerArgs& a, const TileRuns& runs, con
     int row4, threads, v;
     gather_shape(a, row4, threads, v);
     switch (v) {
-    case 1: gather_tile_runs_kernel<1><<<runs.count, threads, 0, s>>>(a, runs, row4, msg, H1_adj); break;
-    case 2: gather_tile_runs_kernel<2><<<runs.count, threads, 0, s>>>(a, runs, row4, msg, H1_adj); break;
-    case 3: gather_tile_runs_kernel<3><<<runs.count, threads, 0, s>>>(a, runs, row4, msg, H1_adj); break;
+    case 1: gather_tile_runs_kernel<1><<<runs.count, threads, 0, s>>>(a, runs, row4, msg, H1_adj), note_launch(); break;
+    case 2: gather_tile_runs_kernel<2><<<runs.count, threads, 0, s>>>(a, runs, row4, msg, H1_adj), note_launch(); break;
+    case 3: gather_tile_runs_kernel<3><<<runs.count, threads, 0, s>>>(a, runs, row4, msg, H1_adj), note_launch(); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -1533,7 +1533,7 @@ hipError_t launch_add_direct(int nodes, int C, int num_LM, const float* direct, 
     const size_t n = static_cast<size_t>(nodes) * C;
     if (n == 0) return hipSuccess;
     add_direct_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(nodes, C, num_LM, direct,
-                                                                            M0_adj);
+                                                                            M0_adj), note_launch();
     return hipGetLastError();
 }
 
@@ -1543,7 +1543,7 @@ hipError_t launch_zbl(int node_begin, int num_nodes, const int* first, long long
 {
     if (num_nodes <= 0) return hipSuccess;
     zbl_kernel<<<(num_nodes + 3) / 4, 256, 0, s>>>(node_begin, num_nodes, first, edge_base, edge_pair, xyz, r, z,
-                                                   energies, forces);
+                                                   energies, forces), note_launch();
     return hipGetLastError();
 }
 
@@ -1551,7 +1551,7 @@ hipError_t launch_tile_geometry(const TileGeometry& g, hipStream_t s)
 {
     if (g.node_count <= 0) return hipSuccess;
     if (!g.explicit_xyz && !g.ref.edges && !(g.ref.shifts && g.ref.positions)) return hipErrorInvalidValue;
-    tile_geometry_kernel<<<(g.node_count + 3) / 4, 256, 0, s>>>(g);
+    tile_geometry_kernel<<<(g.node_count + 3) / 4, 256, 0, s>>>(g), note_launch();
     return hipGetLastError();
 }
 
@@ -1561,9 +1561,9 @@ hipError_t launch_fold_tile_forces(int node_begin, int node_count, const int* fi
 {
     if (node_count > 0)
         fold_receiver_forces_kernel<<<(node_count + 3) / 4, 256, 0, s>>>(node_begin, node_count, first, edge_base,
-                                                                         forces, atom_forces);
+                                                                         forces, atom_forces), note_launch();
     if (runs.count > 0)
-        fold_source_runs_kernel<<<(runs.count + 3) / 4, 256, 0, s>>>(runs, tedge, edge_base, forces, atom_forces);
+        fold_source_runs_kernel<<<(runs.count + 3) / 4, 256, 0, s>>>(runs, tedge, edge_base, forces, atom_forces), note_launch();
     return hipGetLastError();
 }
 
@@ -1571,7 +1571,7 @@ hipError_t launch_fill_f64(double* out, long long n, double value, hipStream_t s
 {
     if (n <= 0) return hipSuccess;
     const long long blocks = std::min<long long>((n + 255) / 256, 65536);
-    fill_f64_kernel<<<static_cast<int>(blocks), 256, 0, s>>>(out, n, value);
+    fill_f64_kernel<<<static_cast<int>(blocks), 256, 0, s>>>(out, n, value), note_launch();
     return hipGetLastError();
 }
 
@@ -1582,7 +1582,7 @@ hipError_t launch_edge_geometry(int num_edges, const int* receiver, const int* s
     if (num_edges <= 0) return hipSuccess;
     if (!ref.edges && !(ref.shifts && ref.positions)) return hipErrorInvalidValue;
     edge_geometry_kernel<<<(num_edges + 255) / 256, 256, 0, s>>>(num_edges, receiver, source, ref, displacements,
-                                                                 cell, r_cut, xyz, r, invalid);
+                                                                 cell, r_cut, xyz, r, invalid), note_launch();
     return hipGetLastError();
 }
 
@@ -1591,7 +1591,7 @@ hipError_t launch_atom_forces(int num_nodes, const int* first, const int* tfirst
 {
     if (num_nodes <= 0) return hipSuccess;
     atom_forces_kernel<<<(num_nodes + 3) / 4, 256, 0, s>>>(num_nodes, first, tfirst, tedge, forces,
-                                                           atom_forces);
+                                                           atom_forces), note_launch();
     return hipGetLastError();
 }
 
@@ -1607,8 +1607,8 @@ hipError_t launch_reduce_totals(int num_nodes, int num_edges, const double* ener
                                 double* partials, int num_partials, double* out, hipStream_t s, bool accumulate)
 {
     totals_partial_kernel<<<num_partials, kReduceThreads, 0, s>>>(num_nodes, num_edges, energies, forces,
-                                                                  xyz, inv_volume, partials);
-    totals_final_kernel<<<1, 256, 0, s>>>(num_partials, partials, out, accumulate ? 1 : 0);
+                                                                  xyz, inv_volume, partials), note_launch();
+    totals_final_kernel<<<1, 256, 0, s>>>(num_partials, partials, out, accumulate ? 1 : 0), note_launch();
     return hipGetLastError();
 }
 

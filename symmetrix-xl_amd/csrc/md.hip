@@ -88,7 +88,7 @@ hipError_t launch_md_kick_drift(int num_atoms, double* x, double* v, const doubl
                                 double dtf, double dt, hipStream_t s)
 {
     if (num_atoms <= 0) return hipSuccess;
-    kick_drift_kernel<<<blocks_for(3LL * num_atoms), kMdThreads, 0, s>>>(num_atoms, x, v, f, inv_m, dtf, dt);
+    kick_drift_kernel<<<blocks_for(3LL * num_atoms), kMdThreads, 0, s>>>(num_atoms, x, v, f, inv_m, dtf, dt), note_launch();
     return hipGetLastError();
 }
 
@@ -96,15 +96,15 @@ hipError_t launch_md_kick(int num_atoms, double* v, const double* f, const doubl
                           hipStream_t s)
 {
     if (num_atoms <= 0) return hipSuccess;
-    kick_kernel<<<blocks_for(3LL * num_atoms), kMdThreads, 0, s>>>(num_atoms, v, f, inv_m, dtf);
+    kick_kernel<<<blocks_for(3LL * num_atoms), kMdThreads, 0, s>>>(num_atoms, v, f, inv_m, dtf), note_launch();
     return hipGetLastError();
 }
 
 hipError_t launch_md_kinetic(int num_atoms, const double* v, const double* m, double* partials, int num_partials,
                              double* out, hipStream_t s)
 {
-    kinetic_partial_kernel<<<num_partials, kMdThreads, 0, s>>>(num_atoms, v, m, partials);
-    kinetic_final_kernel<<<1, kMdThreads, 0, s>>>(num_partials, partials, out);
+    kinetic_partial_kernel<<<num_partials, kMdThreads, 0, s>>>(num_atoms, v, m, partials), note_launch();
+    kinetic_final_kernel<<<1, kMdThreads, 0, s>>>(num_partials, partials, out), note_launch();
     return hipGetLastError();
 }
 

@@ -659,7 +659,7 @@ hipError_t m0_forward_launch(const LayerArgs& a, const PolyArgs& p, const NodeBl
     using P = PolyShape<LIN, LOUT, CORR>;
     const int threads = node_threads(a.C);
     const size_t shmem = p.num_rem > 0 ? sizeof(float) * P::NIN * threads : 0;
-    m0_forward_kernel<P, kM0BlockNodes><<<nb.count, threads, shmem, s>>>(a, p, nb, A0, M0);
+    m0_forward_kernel<P, kM0BlockNodes><<<nb.count, threads, shmem, s>>>(a, p, nb, A0, M0), note_launch();
     return hipGetLastError();
 }
 
@@ -670,7 +670,7 @@ hipError_t m0_reverse_launch(const LayerArgs& a, const PolyArgs& p, const NodeBl
     using P = PolyShape<LIN, LOUT, CORR>;
     const int threads = node_threads(a.C);
     const size_t shmem = p.num_rem > 0 ? sizeof(float) * 2 * P::NIN * threads : 0;
-    m0_reverse_kernel<P, kM0BlockNodes><<<nb.count, threads, shmem, s>>>(a, p, nb, A0, M0_adj, A0_adj);
+    m0_reverse_kernel<P, kM0BlockNodes><<<nb.count, threads, shmem, s>>>(a, p, nb, A0, M0_adj, A0_adj), note_launch();
     return hipGetLastError();
 }
 
@@ -682,7 +682,7 @@ hipError_t readout_launch(const ReadoutArgs& a, hipStream_t s)
     const size_t NB = kReadoutBlockNodes;
     size_t floats = 3 * NB * threads + 2 * NB * kMaxHidden;
     if (a.p1.num_rem > 0) floats += 2 * static_cast<size_t>(P::NIN) * threads;
-    readout_kernel<P, kReadoutBlockNodes><<<a.nodes.count, threads, sizeof(float) * floats, s>>>(a);
+    readout_kernel<P, kReadoutBlockNodes><<<a.nodes.count, threads, sizeof(float) * floats, s>>>(a), note_launch();
     return hipGetLastError();
 }
 

@@ -43,6 +43,9 @@ class Stats(ctypes.Structure):
         ("graph_builds", ctypes.c_int), ("evaluations", ctypes.c_int),
         ("last_evaluation_ms", ctypes.c_double), ("tiled_evaluations", ctypes.c_int),
         ("tile_receivers", ctypes.c_int), ("num_tiles", ctypes.c_int),
+        ("last_graph_prepare_ms", ctypes.c_double), ("preparation_fences", ctypes.c_int64),
+        ("evaluation_fences", ctypes.c_int64), ("last_evaluation_launches", ctypes.c_int64),
+        ("last_evaluation_allocations", ctypes.c_int64), ("last_evaluation_fences", ctypes.c_int64),
     ]
 
 

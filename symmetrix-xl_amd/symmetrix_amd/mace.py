@@ -459,6 +459,44 @@ class MACEKokkosFloat:
     def dual_layer_tiled_evaluation_count(self):
         return self.stats["tiled_evaluations"]
 
+    # --- observability (reference mace_kokkos.cpp:925-970) ---------------------
+    @property
+    def factorized_prepared_graph_count(self):
+        return self.stats["graph_builds"]
+
+    @property
+    def factorized_prepared_evaluation_count(self):
+        return self.stats["evaluations"]
+
+    @property
+    def factorized_preparation_fence_count(self):
+        """Host waits on the evaluator's stream over all graph preparations."""
+        return self.stats["preparation_fences"]
+
+    @property
+    def factorized_evaluation_fence_count(self):
+        """Host waits on the evaluator's stream over all evaluations."""
+        return self.stats["evaluation_fences"]
+
+    @property
+    def factorized_last_evaluation_ms(self):
+        return self.stats["last_evaluation_ms"]
+
+    @property
+    def factorized_last_graph_prepare_ms(self):
+        return self.stats["last_graph_prepare_ms"]
+
+    @property
+    def last_evaluation_launch_count(self):
+        """Kernel launches of the last evaluation."""
+        return self.stats["last_evaluation_launches"]
+
+    @property
+    def last_evaluation_allocation_count(self):
+        """Device allocations of the last evaluation (0 once the workspace
+        of the prepared graph exists)."""
+        return self.stats["last_evaluation_allocations"]
+
     @property
     def stats(self):
         s = _native.Stats()
