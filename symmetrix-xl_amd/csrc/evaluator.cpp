@@ -287,10 +287,12 @@ Evaluator::Evaluator(const std::string& model_path, const std::string& head)
         info = shape_info<R1Shape<3, 1>>();
     else if (model_.l_max == 3 && model_.L_max == 2)
         info = shape_info<R1Shape<3, 2>>();
+    else if (model_.l_max == 3 && model_.L_max == 0)
+        info = shape_info<R1Shape<3, 0>>();
     else
         throw std::invalid_argument("no compiled kernels for (l_max, L_max) = (" +
                                     std::to_string(model_.l_max) + ", " + std::to_string(model_.L_max) +
-                                    "); compiled shapes: (2,1), (3,1), (3,2)");
+                                    "); compiled shapes: (2,1), (3,1), (3,2), (3,0)");
     nlme_ = info.nlme;
     num_e_ = info.num_e;
     lme_off_ = info.lme_off;
@@ -384,6 +386,8 @@ void Evaluator::upload_static_tables()
         cg = shape_cg<R1Shape<2, 1>>(m);
     else if (m.l_max == 3 && m.L_max == 1)
         cg = shape_cg<R1Shape<3, 1>>(m);
+    else if (m.l_max == 3 && m.L_max == 0)
+        cg = shape_cg<R1Shape<3, 0>>(m);
     else
         cg = shape_cg<R1Shape<3, 2>>(m);
     upload(cg_, cg, stream_);

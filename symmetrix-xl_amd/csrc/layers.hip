@@ -1459,6 +1459,8 @@ hipError_t launch_r1_forward(const LayerArgs& a, const float* r1, const float* c
         r1_forward_kernel<R1Shape<3, 1>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, Phi1), note_launch();
     else if (a.l_max == 3 && a.L_max == 2)
         r1_forward_kernel<R1Shape<3, 2>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, Phi1), note_launch();
+    else if (a.l_max == 3 && a.L_max == 0)
+        r1_forward_kernel<R1Shape<3, 0>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, Phi1), note_launch();
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
@@ -1482,6 +1484,9 @@ hipError_t launch_r1_reverse(const LayerArgs& a, const float* r1, const float* c
     else if (a.l_max == 3 && a.L_max == 2)
         r1_reverse_grouped_kernel<R1Shape<3, 2>, 0, 1><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, dPhi1,
                                                                                        forces, msg), note_launch();
+    else if (a.l_max == 3 && a.L_max == 0)
+        r1_reverse_kernel<R1Shape<3, 0>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, dPhi1,
+                                                                          forces, msg), note_launch();
     else
         return hipErrorInvalidValue;
     return hipGetLastError();

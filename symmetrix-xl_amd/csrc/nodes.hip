@@ -697,9 +697,11 @@ hipError_t launch_m0_forward(const LayerArgs& a, const PolyArgs& p0, const NodeB
     case 212: return m0_forward_launch<2, 1, 2>(a, p0, nb, A0, M0, s);
     case 313: return m0_forward_launch<3, 1, 3>(a, p0, nb, A0, M0, s);
     case 323: return m0_forward_launch<3, 2, 3>(a, p0, nb, A0, M0, s);
+    case 303: return m0_forward_launch<3, 0, 3>(a, p0, nb, A0, M0, s);
     case 210: return m0_forward_launch<2, 1, 0>(a, p0, nb, A0, M0, s);
     case 310: return m0_forward_launch<3, 1, 0>(a, p0, nb, A0, M0, s);
     case 320: return m0_forward_launch<3, 2, 0>(a, p0, nb, A0, M0, s);
+    case 300: return m0_forward_launch<3, 0, 0>(a, p0, nb, A0, M0, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -713,9 +715,11 @@ hipError_t launch_m0_reverse(const LayerArgs& a, const PolyArgs& p0, const NodeB
     case 212: return m0_reverse_launch<2, 1, 2>(a, p0, nb, A0, M0_adj, A0_adj, s);
     case 313: return m0_reverse_launch<3, 1, 3>(a, p0, nb, A0, M0_adj, A0_adj, s);
     case 323: return m0_reverse_launch<3, 2, 3>(a, p0, nb, A0, M0_adj, A0_adj, s);
+    case 303: return m0_reverse_launch<3, 0, 3>(a, p0, nb, A0, M0_adj, A0_adj, s);
     case 210: return m0_reverse_launch<2, 1, 0>(a, p0, nb, A0, M0_adj, A0_adj, s);
     case 310: return m0_reverse_launch<3, 1, 0>(a, p0, nb, A0, M0_adj, A0_adj, s);
     case 320: return m0_reverse_launch<3, 2, 0>(a, p0, nb, A0, M0_adj, A0_adj, s);
+    case 300: return m0_reverse_launch<3, 0, 0>(a, p0, nb, A0, M0_adj, A0_adj, s);
     default: return hipErrorInvalidValue;
     }
 }

@@ -106,6 +106,33 @@ def test_wide_model_with_reference_coupling_values(oracle_lib, tmp_path):
     _full_size_check(oracle_lib, str(path), model, s, "water 300 H2O, wide shape with the reference's 215 coupling terms")
 
 
+def test_scalar_model_with_reference_coupling_values(oracle_lib, tmp_path):
+    # the scalar (3,0) shape with the coupling terms of the reference's
+    # omat0-small contract (tests/golden, from symmetrix/test/data/
+    # execution_contracts/jit_r1_mace_omat0_small_contract.json: 4 paths,
+    # 16 terms, 128 channels)
+    import os
+
+    from symmetrix_amd import synthetic
+
+    golden = os.path.join(os.path.dirname(__file__), "golden", "jit_r1_mace_omat0_small_contract.json")
+    with open(golden) as f:
+        contract = json.load(f)
+    assert contract["channels"] == synthetic.PRESETS["scalar"].channels
+    model = json.loads(synthetic.model_json(synthetic.random_mace_model("scalar", seed=5)))
+    assert [(l1, l2, lo) for l1, l2, lo in zip(model["Phi1_l1"], model["Phi1_l2"], model["Phi1_l"])] == [
+        (p["edge_l"], p["source_l"], p["output_l"]) for p in contract["paths"]]
+    terms = contract["sparse_coupling"]["terms"]
+    assert len(terms) == 16
+    model["Phi1_lme"] = [t["lme"] for t in terms]
+    model["Phi1_lelm1lm2"] = [t["row"] for t in terms]
+    model["Phi1_clebsch_gordan"] = [t["coefficient"] for t in terms]
+    path = tmp_path / "scalar_contract.json"
+    path.write_text(json.dumps(model))
+    s = synthetic.srtio3_supercell(6, sigma=0.05, seed=2)
+    _full_size_check(oracle_lib, str(path), model, s, "SrTiO3 6^3, scalar shape with the reference's 16 coupling terms")
+
+
 def test_irregular_config_full_size(oracle_lib, medium):
     from symmetrix_amd import synthetic
 

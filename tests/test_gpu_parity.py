@@ -195,6 +195,17 @@ def test_wide_shape_parity(native, oracle_lib, wide):
     _compare(got, _oracle_eval(oracle_lib, model, s), len(s))
 
 
+def test_scalar_shape_parity(native, oracle_lib, tmp_path_factory):
+    # L_max = 0: scalar H1, 4 coupling paths (l, 0 -> l), 16 terms
+    from symmetrix_amd import Symmetrix, synthetic
+
+    path, model = _model_file(tmp_path_factory, "scalar")
+    s = synthetic.srtio3_supercell(3, sigma=0.05, seed=0)
+    print(f"scalar shape SrTiO3 3^3 ({len(s)} atoms)", flush=True)
+    got = Symmetrix(path).calculate(s)
+    _compare(got, _oracle_eval(oracle_lib, model, s), len(s))
+
+
 def test_repeat_evaluation_is_bitwise_deterministic(native, tiny):
     from symmetrix_amd import MACEKokkosFloat, synthetic
 

@@ -144,7 +144,7 @@ def test_receiver_limit_at_or_above_node_count_keeps_untiled_plan(tiny):
     assert out["stats"]["tile_receivers"] == 0 and out["tiled_count"] == 0
 
 
-@pytest.mark.parametrize("preset,limit", [("medium3", 32), ("wide", 50)])
+@pytest.mark.parametrize("preset,limit", [("medium3", 32), ("wide", 50), ("scalar", 40)])
 def test_tiled_matches_oracle(oracle_lib, tmp_path_factory, preset, limit):
     from symmetrix_amd import synthetic
 

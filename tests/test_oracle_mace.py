@@ -14,6 +14,9 @@ Every test runs on
 - the wide shape (l_max 3, L_max 2: H1 with an l = 2 block, A1 with L = 2
   blocks, 17 coupling paths and 215 terms, 256 channels) on 12 rigid water
   molecules;
+- the scalar shape (l_max 3, L_max 0: scalar H1, 4 coupling paths and 16
+  terms, 128 channels; the reference's omat0-small / off23-small models) on
+  SrTiO3 2^3;
 so the reverse passes of every shape the evaluator compiles are pinned by
 finite differences of the forward, and the forward's l = 2 / l = 3 blocks by
 rotation invariance (a wrong row, sign or index in one block breaks the
@@ -25,7 +28,7 @@ import json
 import numpy as np
 import pytest
 
-CASES = ["tiny", "tiny+zbl+density+agnesi", "tiny+pre_linear_up+residual", "medium3", "wide"]
+CASES = ["tiny", "tiny+zbl+density+agnesi", "tiny+pre_linear_up+residual", "medium3", "wide", "scalar"]
 
 
 @pytest.fixture(scope="module", params=CASES)
