@@ -154,6 +154,24 @@ __device__ __forceinline__ int xcd_contiguous(int block, int count)
     return x * base + min(x, rem) + q;
 }
 
+// Channel-sliced receivers: `slices` (1, 2, 4 or 8) workgroups per receiver,
+// one per channel slice.  Block b runs slice b % slices -- so every XCD
+// (b % 8) runs one slice only and its L2 holds that slice's columns of the
+// coefficient tables -- of a receiver from a contiguous range per XCD of the
+// group of 8 / slices XCDs that run the slice.  Blocks 0 .. slices * count - 1
+// cover every (receiver, slice) once.
+__device__ __forceinline__ int xcd_slice_receiver(int block, int count, int slices, int& slice)
+{
+    slice = block % slices;
+    const int groups = 8 / slices;
+    const int b = block / slices;
+    const int x = b % groups;
+    const int q = b / groups;
+    const int base = count / groups;
+    const int rem = count % groups;
+    return x * base + min(x, rem) + q;
+}
+
 __device__ __forceinline__ float wave_sum(float v)
 {
 #pragma unroll

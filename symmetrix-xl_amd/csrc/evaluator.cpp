@@ -513,6 +513,10 @@ void Evaluator::prepare_active_types(const std::vector<int>& node_types)
     }
     upload(r1_, r1, stream_, &staged_);
     upload(r0f_, r0f, stream_, &staged_);
+    // the second-interaction forward runs in 64-channel slices, one slice per
+    // XCD, when its coefficient table is far beyond one XCD's L2 (4 MiB)
+    r1_slices_ = 1;
+    if ((C_ == 128 || C_ == 256) && r1.size() * sizeof(float) > kR1SliceTableBytes) r1_slices_ = C_ / 64;
     // density-normalisation splines per unordered pair: [pair_u][iv][4]
     auto density_table = [&](const RadialNetwork& net, DeviceBuffer& out) {
         std::vector<float> table(static_cast<std::size_t>(npairs) * NI * 4);
@@ -1677,6 +1681,7 @@ void Evaluator::evaluate()
     la.C = C_;
     la.l_max = model_.l_max;
     la.L_max = model_.L_max;
+    la.channel_slices = r1_slices_;
     la.node_offset = 0;
     la.node_count = N;
     density_args(la, nullptr);
@@ -1843,6 +1848,7 @@ void Evaluator::evaluate_tiled()
     la.C = C_;
     la.l_max = model_.l_max;
     la.L_max = model_.L_max;
+    la.channel_slices = r1_slices_;
     density_args(la, nullptr);
     la.type_order = node_order_.as<int>();
     hipStream_t s = stream_;

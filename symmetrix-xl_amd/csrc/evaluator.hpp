@@ -130,6 +130,12 @@ struct EvaluatorStats {
 // and the untiled workspace does not fit (reference mace_kokkos.hpp:542).
 constexpr int kDefaultTileReceivers = 32768;
 
+// Coefficient-table size above which the second-interaction forward runs in
+// channel slices.  Measured: the wide shape's 17.8 MB table (C = 256, 4
+// slices) 9.4 -> 6.9 ms on 30,000 water atoms; the medium shape's 5.2 MB
+// table (C = 128, 2 slices, mostly L2-resident already) 0.31 -> 0.38 ms.
+constexpr std::size_t kR1SliceTableBytes = std::size_t(8) << 20;
+
 // Execution-plan report (reference execution_plan.hpp:32-50 and
 // mace_kokkos_runtime.cpp:3843-3915): the candidate plans with their memory
 // estimates for the prepared graph and the one selected.  Plan identifiers
@@ -342,6 +348,7 @@ private:
     long long num_edges_ = 0;
     std::vector<int> host_types_;
     std::vector<int> host_first_;  // CSR receiver offsets of the prepared graph, [N + 1]
+    int r1_slices_ = 1;            // channel slices of the second-interaction forward
     // host copies of uploads in flight, released at the next wait()
     std::vector<std::vector<unsigned char>> staged_;
     double cell_[9] = {}, inverse_cell_[9] = {};

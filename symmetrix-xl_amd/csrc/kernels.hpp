@@ -171,6 +171,11 @@ struct LayerArgs {
     int local_base = 0;
     // receivers of this launch in element-type order (layer-0 kernels), or null
     const int* type_order = nullptr;
+    // Second-interaction forward: workgroups per receiver, each over a slice
+    // of 64 channels with its 4 waves splitting the edges (1: one workgroup
+    // of all channels).  Set where the coefficient table outgrows one XCD's
+    // L2: each XCD then reads only its slice's columns.
+    int channel_slices = 1;
 };
 
 // Layer 0: A0[i] = sum_j R0f_{pair(i,j)}(r) Y(r_hat)   (H0 and A0_W folded in),

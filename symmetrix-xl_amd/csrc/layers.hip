@@ -295,21 +295,148 @@ constexpr int kWBatch = 4;
 // next edge of the same interval
 constexpr int kRowReusePaths = 10;
 
+// The terms of a shape in the order of their edge-weight float4 (term_pl / 4):
+// the staging loop visits each term once (an unrolled loop over all terms per
+// float4 would be NT x NQ compile-time branches, too many to unroll for the
+// wide shape).
 template <class S>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S::NPL <= 96 ? 3 : 1)))
-r1_forward_kernel(LayerArgs a, const float* __restrict__ r1,
-                                                          const float* __restrict__ cg,
-                                                          const float* __restrict__ H1,
-                                                          float* __restrict__ Phi1)
+struct R1TermsByQuad {
+    static constexpr int NQ = (S::NPL + 3) / 4;
+    int order[S::NT] = {};
+    int start[NQ + 1] = {};
+    constexpr R1TermsByQuad()
+    {
+        int n = 0;
+        for (int q = 0; q < NQ; ++q) {
+            start[q] = n;
+            for (int u = 0; u < S::NT; ++u)
+                if (S::term_pl[u] / 4 == q) order[n++] = u;
+        }
+        start[NQ] = n;
+    }
+};
+template <class S>
+inline constexpr R1TermsByQuad<S> kTermsByQuad{};
+
+// Stages edge t of the tile [base, base + n) of a receiver's edges (lanes
+// 0..63 of one wave): compacted slot, spline row, local coordinate, source
+// and the folded edge weights W_g = sum_{t in g} cg_t Y_lm1(t) of the
+// (path, lm2, lme) groups.
+template <class S, bool kSorted>
+__device__ __forceinline__ void r1_stage_edge(const LayerArgs& a, const float* __restrict__ cg, int base, int n,
+                                              int t, float4v (*s_W)[(S::NPL + 3) / 4], float* s_x, int* s_row,
+                                              int* s_src, int* s_count)
 {
     constexpr int NLM = (S::LMAX + 1) * (S::LMAX + 1);
+    constexpr int NQ = (S::NPL + 3) / 4;
+    const EdgeGraph& g = a.graph;
+    double rr;
+    const TileSlot ts = compact_edge<false, kSorted>(g, a.grid, base, n, t, rr, s_count);
+    if (ts.active) {
+        const int e = base + t;
+        float Y[NLM], dir[3];
+        edge_harmonics<S::LMAX, false>(g.xyz + 3 * static_cast<size_t>(e - g.edge_base), rr, Y, nullptr, nullptr,
+                                       nullptr, dir);
+        s_x[ts.slot] = ts.x;
+        s_row[ts.slot] = ts.row;
+        s_src[ts.slot] = g.source[e];
+        // one float4 of W at a time, over the terms of that float4
+        constexpr const R1TermsByQuad<S>& tq = kTermsByQuad<S>;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            float4v w = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int v = tq.start[q]; v < tq.start[q + 1]; ++v) {
+                const int u = tq.order[v];
+                w[S::term_pl[u] % 4] = fmaf(cg[u], Y[S::term_lm1[u]], w[S::term_pl[u] % 4]);
+            }
+            s_W[ts.slot][q] = w;
+        }
+    }
+}
+
+// Channel loop over the staged slots [lo, hi) of a tile: per slot the radial
+// values R_p(r) of the thread's channel kk (one coefficient row per slot,
+// refilled for the next slot while this one is accumulated), the source
+// features H1[src, lm2, kk], and acc[lme_g] += W_g R_p H_lm2 per group.
+template <class S>
+__device__ __forceinline__ void r1_forward_slots(const float4v (*s_W)[(S::NPL + 3) / 4], const float* s_x,
+                                                 const int* s_row, const int* s_src, int lo, int hi, int C, int kk,
+                                                 const float* __restrict__ r1, const float* __restrict__ H1,
+                                                 float (&acc)[S::NLME])
+{
     constexpr int NLMS = (S::LLMAX + 1) * (S::LLMAX + 1);
     constexpr int NP = S::NP;
-    constexpr int NT = S::NT;
     constexpr int NPQ = S::NPQ;
     constexpr int NPL = S::NPL;
     constexpr int NQ = (NPL + 3) / 4;                 // float4s of W per edge
     constexpr int NB = (NQ + kWBatch - 1) / kWBatch;  // batches per edge
+    const int row_bytes = NP * C * 16;
+    const int h_bytes = NLMS * C * 4;
+    auto fetch_row = [&](int j, float4v* c) {
+        const auto rs = buffer_rsrc(r1 + static_cast<size_t>(uniform(s_row[j])) * NP * C * 4, row_bytes);
+#pragma unroll
+        for (int p = 0; p < NP; ++p) c[p] = load4(rs, kk * 16, p * C * 16);
+    };
+    auto fetch_h = [&](int j, float* H) {
+        const auto hs = buffer_rsrc(H1 + static_cast<size_t>(uniform(s_src[j])) * NLMS * C, h_bytes);
+#pragma unroll
+        for (int q = 0; q < NLMS; ++q) H[q] = load1(hs, kk * 4, q * C * 4);
+    };
+    // One row buffer: once the radial values of slot j are formed, its
+    // coefficient registers are refilled with the row of slot j + 1 -- only
+    // when that row differs: slots sorted by row let edges of one spline
+    // interval reuse the registers (a wave-uniform branch; shapes with up to
+    // kRowReusePaths paths).
+    float4v c[NP];
+    float H[NLMS];
+    if (lo < hi) {
+        fetch_row(lo, c);
+        fetch_h(lo, H);
+    }
+    for (int j = lo; j < hi; ++j) {
+        const float4v* Wj = s_W[j];
+        float4v wb[2][kWBatch];
+#pragma unroll
+        for (int q = 0; q < kWBatch; ++q)
+            if (q < NQ) wb[0][q] = Wj[q];
+        const float x = uniform(s_x[j]);
+        float RH[NPQ];
+#pragma unroll
+        for (int pq = 0; pq < NPQ; ++pq) RH[pq] = cubic(c[S::pq_p[pq]], x) * H[S::pq_lm2[pq]];
+        const int jn = min(j + 1, hi - 1);
+        // (the wide shapes' row registers leave no room for the branch: they
+        // reload, an L1 hit)
+        if (S::NP > kRowReusePaths || uniform(s_row[jn]) != uniform(s_row[j])) fetch_row(jn, c);
+        fetch_h(jn, H);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            if (b + 1 < NB) {
+#pragma unroll
+                for (int q = 0; q < kWBatch; ++q)
+                    if ((b + 1) * kWBatch + q < NQ) wb[(b + 1) & 1][q] = Wj[(b + 1) * kWBatch + q];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int q = 0; q < kWBatch; ++q) {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int gidx = 4 * (b * kWBatch + q) + u;
+                    if (gidx < NPL)
+                        acc[S::pl_lme[gidx]] = fmaf(wb[b & 1][q][u], RH[S::pl_pq[gidx]], acc[S::pl_lme[gidx]]);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+}
+
+template <class S>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S::NPL <= 96 ? 3 : 1)))
+r1_forward_kernel(LayerArgs a, const float* __restrict__ r1, const float* __restrict__ cg,
+                  const float* __restrict__ H1, float* __restrict__ Phi1)
+{
+    constexpr int NQ = (S::NPL + 3) / 4;
     __shared__ float4v s_W[kTile][NQ];
     __shared__ float s_x[kTile];
     __shared__ int s_row[kTile];
@@ -321,8 +448,6 @@ r1_forward_kernel(LayerArgs a, const float* __restrict__ r1,
     const int C = a.C;
     const EdgeGraph& g = a.graph;
     const int kk = min(k, C - 1);
-    const int row_bytes = NP * C * 16;
-    const int h_bytes = NLMS * C * 4;
     if (a.d1.table && threadIdx.x < 64) {
         const float sc = density_scale(a.d1, g, a.grid, g.first[i], g.first[i + 1]);
         if (threadIdx.x == 0) a.d1.scale[i] = sc;
@@ -333,90 +458,100 @@ r1_forward_kernel(LayerArgs a, const float* __restrict__ r1,
     const int e0 = g.first[i], e1 = g.first[i + 1];
     for (int base = e0; base < e1; base += kTile) {
         __syncthreads();
-        if (threadIdx.x < 64) {
-            const int t = threadIdx.x;
-            double rr;
-            const TileSlot ts = compact_edge<false, true>(g, a.grid, base, min(kTile, e1 - base), t, rr, &s_count);
-            if (ts.active) {
-                const int e = base + t;
-                float Y[NLM], dir[3];
-                edge_harmonics<S::LMAX, false>(g.xyz + 3 * static_cast<size_t>(e - g.edge_base), rr, Y, nullptr,
-                                               nullptr, nullptr, dir);
-                s_x[ts.slot] = ts.x;
-                s_row[ts.slot] = ts.row;
-                s_src[ts.slot] = g.source[e];
-                // one float4 of W at a time (terms filtered at compile time)
-#pragma unroll
-                for (int q = 0; q < NQ; ++q) {
-                    float4v w = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                    for (int u = 0; u < NT; ++u)
-                        if (S::term_pl[u] / 4 == q)
-                            w[S::term_pl[u] % 4] = fmaf(cg[u], Y[S::term_lm1[u]], w[S::term_pl[u] % 4]);
-                    s_W[ts.slot][q] = w;
-                }
-            }
-        }
+        if (threadIdx.x < 64)
+            r1_stage_edge<S, true>(a, cg, base, min(kTile, e1 - base), threadIdx.x, s_W, s_x, s_row, s_src,
+                                   &s_count);
         __syncthreads();
-        const int count = uniform(s_count);
-        auto fetch_row = [&](int j, float4v* c) {
-            const auto rs = buffer_rsrc(r1 + static_cast<size_t>(uniform(s_row[j])) * NP * C * 4, row_bytes);
-#pragma unroll
-            for (int p = 0; p < NP; ++p) c[p] = load4(rs, kk * 16, p * C * 16);
-        };
-        auto fetch_h = [&](int j, float* H) {
-            const auto hs = buffer_rsrc(H1 + static_cast<size_t>(uniform(s_src[j])) * NLMS * C, h_bytes);
-#pragma unroll
-            for (int q = 0; q < NLMS; ++q) H[q] = load1(hs, kk * 4, q * C * 4);
-        };
-        // One row buffer: once the radial values of edge j are formed, its
-        // coefficient registers are refilled with the row of edge j + 1 --
-        // only when that row differs: the slots are sorted by row, so edges
-        // of one spline interval reuse the registers (a wave-uniform branch;
-        // shapes with up to kRowReusePaths paths).
-        float4v c[NP];
-        float H[NLMS];
-        if (count > 0) {
-            fetch_row(0, c);
-            fetch_h(0, H);
-        }
-        for (int j = 0; j < count; ++j) {
-            const float4v* Wj = s_W[j];
-            float4v wb[2][kWBatch];
-#pragma unroll
-            for (int q = 0; q < kWBatch; ++q)
-                if (q < NQ) wb[0][q] = Wj[q];
-            const float x = uniform(s_x[j]);
-            float RH[NPQ];
-#pragma unroll
-            for (int pq = 0; pq < NPQ; ++pq) RH[pq] = cubic(c[S::pq_p[pq]], x) * H[S::pq_lm2[pq]];
-            const int jn = min(j + 1, count - 1);
-            // (the wide shapes' row registers leave no room for the branch:
-            // they reload, an L1 hit)
-            if (S::NP > kRowReusePaths || uniform(s_row[jn]) != uniform(s_row[j])) fetch_row(jn, c);
-            fetch_h(jn, H);
-#pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                if (b + 1 < NB) {
-#pragma unroll
-                    for (int q = 0; q < kWBatch; ++q)
-                        if ((b + 1) * kWBatch + q < NQ) wb[(b + 1) & 1][q] = Wj[(b + 1) * kWBatch + q];
-                }
-                __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                for (int q = 0; q < kWBatch; ++q) {
-#pragma unroll
-                    for (int u = 0; u < 4; ++u) {
-                        const int gidx = 4 * (b * kWBatch + q) + u;
-                        if (gidx < NPL)
-                            acc[S::pl_lme[gidx]] = fmaf(wb[b & 1][q][u], RH[S::pl_pq[gidx]], acc[S::pl_lme[gidx]]);
-                    }
-                }
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
+        r1_forward_slots<S>(s_W, s_x, s_row, s_src, 0, uniform(s_count), C, kk, r1, H1, acc);
     }
     if (k < C) {
+        float* out = Phi1 + static_cast<size_t>(i - a.local_base) * S::NLME * C + k;
+#pragma unroll
+        for (int q = 0; q < S::NLME; ++q) out[q * C] = acc[q];
+    }
+}
+
+// Channel-sliced forward (LayerArgs::channel_slices workgroups per receiver,
+// XCD-aligned): a workgroup runs one 64-channel slice of a receiver; each of
+// its 4 waves takes a contiguous quarter of the receiver's edges and stages
+// and consumes its own tiles of kWaveTile edges (no workgroup barrier in the
+// edge loop); the waves' partial sums are added at the end in a fixed order,
+// (w0 + w2) + (w1 + w3), through the tiles' LDS.
+constexpr int kWaveTile = 16;
+
+template <class S>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S::NPL <= 96 ? 3 : 1)))
+r1_forward_sliced_kernel(LayerArgs a, const float* __restrict__ r1, const float* __restrict__ cg,
+                         const float* __restrict__ H1, float* __restrict__ Phi1)
+{
+    constexpr int NQ = (S::NPL + 3) / 4;
+    __shared__ float4v s_W[kMaxWaves][kWaveTile][NQ];
+    __shared__ float s_x[kMaxWaves][kWaveTile];
+    __shared__ int s_row[kMaxWaves][kWaveTile];
+    __shared__ int s_src[kMaxWaves][kWaveTile];
+    __shared__ int s_count[kMaxWaves];
+
+    int slice;
+    const int i = a.node_offset + xcd_slice_receiver(blockIdx.x, a.node_count, a.channel_slices, slice);
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int C = a.C;
+    const int k = slice * 64 + lane;  // < C: C = 64 slices
+    const EdgeGraph& g = a.graph;
+    if (a.d1.table && wave == 0) {
+        const float sc = density_scale(a.d1, g, a.grid, g.first[i], g.first[i + 1]);
+        if (lane == 0 && slice == 0) a.d1.scale[i] = sc;
+    }
+    float acc[S::NLME];
+#pragma unroll
+    for (int q = 0; q < S::NLME; ++q) acc[q] = 0.0f;
+    const int e0 = g.first[i], n = g.first[i + 1] - e0;
+    const int lo = e0 + (n * wave) / kMaxWaves, hi = e0 + (n * (wave + 1)) / kMaxWaves;
+    for (int base = lo; base < hi; base += kWaveTile) {
+        // the wave's previous tile is consumed before its slots are rewritten
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        r1_stage_edge<S, (S::NP <= kRowReusePaths)>(a, cg, base, min(kWaveTile, hi - base), lane, s_W[wave],
+                                                     s_x[wave], s_row[wave], s_src[wave], &s_count[wave]);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        r1_forward_slots<S>(s_W[wave], s_x[wave], s_row[wave], s_src[wave], 0, uniform(s_count[wave]), C, k, r1,
+                            H1, acc);
+    }
+    // partial sums of the 4 waves, kRows rows of the receiver's Phi1 at a time
+    float* red = reinterpret_cast<float*>(&s_W[0][0][0]);
+    constexpr int kCap = kMaxWaves * kWaveTile * NQ * 4 / 128;
+    constexpr int kRows = kCap < S::NLME ? kCap : S::NLME;
+#pragma unroll
+    for (int r0 = 0; r0 < S::NLME; r0 += kRows) {
+        __syncthreads();
+        if (wave >= 2) {
+#pragma unroll
+            for (int q = 0; q < S::NLME; ++q)
+                if (q >= r0 && q < r0 + kRows) red[((wave - 2) * kRows + q - r0) * 64 + lane] = acc[q];
+        }
+        __syncthreads();
+        if (wave < 2) {
+#pragma unroll
+            for (int q = 0; q < S::NLME; ++q)
+                if (q >= r0 && q < r0 + kRows) acc[q] += red[(wave * kRows + q - r0) * 64 + lane];
+        }
+        __syncthreads();
+        if (wave == 1) {
+#pragma unroll
+            for (int q = 0; q < S::NLME; ++q)
+                if (q >= r0 && q < r0 + kRows) red[(q - r0) * 64 + lane] = acc[q];
+        }
+        __syncthreads();
+        if (wave == 0) {
+#pragma unroll
+            for (int q = 0; q < S::NLME; ++q)
+                if (q >= r0 && q < r0 + kRows) acc[q] += red[(q - r0) * 64 + lane];
+        }
+    }
+    if (wave == 0) {
         float* out = Phi1 + static_cast<size_t>(i - a.local_base) * S::NLME * C + k;
 #pragma unroll
         for (int q = 0; q < S::NLME; ++q) out[q * C] = acc[q];
@@ -1452,13 +1587,20 @@ hipError_t launch_r1_forward(const LayerArgs& a, const float* r1, const float* c
                              float* Phi1, hipStream_t s)
 {
     if (a.node_count <= 0) return hipSuccess;
+    const int slices = a.channel_slices;
+    if (slices != 1 && (a.C != 64 * slices || (slices != 2 && slices != 4))) return hipErrorInvalidValue;
     const int threads = node_threads(a.C);
+    const int blocks = a.node_count * slices;
     if (a.l_max == 2 && a.L_max == 1)
         r1_forward_kernel<R1Shape<2, 1>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, Phi1), note_launch();
-    else if (a.l_max == 3 && a.L_max == 1)
+    else if (a.l_max == 3 && a.L_max == 1 && slices == 1)
         r1_forward_kernel<R1Shape<3, 1>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, Phi1), note_launch();
-    else if (a.l_max == 3 && a.L_max == 2)
+    else if (a.l_max == 3 && a.L_max == 1)
+        r1_forward_sliced_kernel<R1Shape<3, 1>><<<blocks, 256, 0, s>>>(a, r1, cg, H1, Phi1), note_launch();
+    else if (a.l_max == 3 && a.L_max == 2 && slices == 1)
         r1_forward_kernel<R1Shape<3, 2>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, Phi1), note_launch();
+    else if (a.l_max == 3 && a.L_max == 2)
+        r1_forward_sliced_kernel<R1Shape<3, 2>><<<blocks, 256, 0, s>>>(a, r1, cg, H1, Phi1), note_launch();
     else if (a.l_max == 3 && a.L_max == 0)
         r1_forward_kernel<R1Shape<3, 0>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, Phi1), note_launch();
     else
