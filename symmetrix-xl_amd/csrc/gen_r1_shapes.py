@@ -52,10 +52,12 @@ def emit_shape(lmax, Lmax):
     row_path = []
     for p, (l1, l2, _) in enumerate(paths):
         row_path += [p] * ((2 * l1 + 1) * (2 * l2 + 1))
-    terms = []
+    terms, coef = [], {}
     for term in t["terms"]:
         p = row_path[term["row"]]
-        terms.append((p, term["lm2"], term["lm1"], term["lme"], term["row"]))
+        key = (p, term["lm2"], term["lm1"], term["lme"], term["row"])
+        terms.append(key)
+        coef[key] = coef.get(key, 0.0) + term["coefficient"]
     terms.sort()
     # (path, lm2) pairs and (path, lm2, lm1) triples in term order
     pqs, triples, term_tr = [], [], []
@@ -101,6 +103,9 @@ def emit_shape(lmax, Lmax):
         f"    static constexpr int term_lm1[NT] = {arr([x[2] for x in terms])};",
         f"    static constexpr int term_lme[NT] = {arr([x[3] for x in terms])};",
         f"    static constexpr int term_row[NT] = {arr([x[4] for x in terms])};",
+        "    // the coefficients of the standard real coupling (float32): kernels use",
+        "    // them as literals when the model's values equal them",
+        f"    static constexpr float cg_value[NT] = {{{', '.join(_f32_literal(coef[x]) for x in terms)}}};",
         "    // distinct (path, lm2) pairs and (path, lm2, lm1) triples, term order",
         f"    static constexpr int NPQ = {len(pqs)};",
         f"    static constexpr int pq_p[NPQ] = {arr([x[0] for x in pqs])};",
@@ -118,6 +123,13 @@ def emit_shape(lmax, Lmax):
         "",
     ]
     return "\n".join(lines) + groups
+
+
+def _f32_literal(v):
+    """The float32 nearest v, as a C++ literal that reads back exactly."""
+    import numpy as np
+
+    return repr(float(np.float32(v))) + "f"
 
 
 def _arr(vals):

@@ -793,7 +793,9 @@ struct RevTileLds {
     int count;
 };
 
-template <class S, class RG, int MAXT>
+// kLit: the model carries the standard coupling, whose coefficients are
+// compile-time literals (S::cg_value); else they are read from cg.
+template <class S, class RG, int MAXT, bool kLit>
 __device__ __forceinline__ void r1_reverse_pass(const LayerArgs& a, int i, bool first, int count,
                                                 const float* __restrict__ r1, const float* __restrict__ cg,
                                                 const float* __restrict__ H1, const float* __restrict__ dPhi1,
@@ -837,7 +839,8 @@ __device__ __forceinline__ void r1_reverse_pass(const LayerArgs& a, int i, bool 
         if (threadIdx.x < count) {
             const int j = threadIdx.x;
 #pragma unroll
-            for (int t = 0; t < RG::NT; ++t) L.cgY[j][t] = cg[RG::term[t]] * L.Y[j][RG::term_lm1[t]];
+            for (int t = 0; t < RG::NT; ++t)
+                L.cgY[j][t] = (kLit ? S::cg_value[RG::term[t]] : cg[RG::term[t]]) * L.Y[j][RG::term_lm1[t]];
         }
         __syncthreads();
     }
@@ -880,7 +883,8 @@ __device__ __forceinline__ void r1_reverse_pass(const LayerArgs& a, int i, bool 
                 const int pq = RG::tr_pq[RG::term_tr[t]];
                 const float d = G[RG::term_row[t]];
                 sp[pq] = fmaf(L.cgY[j][t], d, sp[pq]);
-                U[RG::term_lm1[t]] = fmaf(cg[RG::term[t]], RH[pq] * d, U[RG::term_lm1[t]]);
+                U[RG::term_lm1[t]] =
+                    fmaf(kLit ? S::cg_value[RG::term[t]] : cg[RG::term[t]], RH[pq] * d, U[RG::term_lm1[t]]);
             }
         }
         float m[RG::NH], ap[RG::NP];
@@ -929,7 +933,7 @@ constexpr int rev_group_terms()
     return (m + 3) / 4 * 4;
 }
 
-template <class S, int... G>
+template <class S, bool kLit, int... G>
 __global__ void __launch_bounds__(256) r1_reverse_grouped_kernel(LayerArgs a, const float* __restrict__ r1,
                                                                   const float* __restrict__ cg,
                                                                   const float* __restrict__ H1,
@@ -975,7 +979,7 @@ __global__ void __launch_bounds__(256) r1_reverse_grouped_kernel(LayerArgs a, co
         }
         __syncthreads();
         const int count = uniform(L.count);
-        (r1_reverse_pass<S, RevGroup<S, G>, MAXT>(a, i, G == 0, count, r1, cg, H1, dPhi1, msg, L), ...);
+        (r1_reverse_pass<S, RevGroup<S, G>, MAXT, kLit>(a, i, G == 0, count, r1, cg, H1, dPhi1, msg, L), ...);
         __syncthreads();
         if (threadIdx.x < count) {
             const int t = threadIdx.x;
@@ -1623,9 +1627,14 @@ hipError_t launch_r1_reverse(const LayerArgs& a, const float* r1, const float* c
     else if (a.l_max == 3 && a.L_max == 1)
         r1_reverse_kernel<R1Shape<3, 1>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, dPhi1,
                                                                           forces, msg), note_launch();
+    else if (a.l_max == 3 && a.L_max == 2 && a.cg_compiled)
+        r1_reverse_grouped_kernel<R1Shape<3, 2>, true, 0, 1><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, dPhi1,
+                                                                                             forces, msg),
+            note_launch();
     else if (a.l_max == 3 && a.L_max == 2)
-        r1_reverse_grouped_kernel<R1Shape<3, 2>, 0, 1><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, dPhi1,
-                                                                                       forces, msg), note_launch();
+        r1_reverse_grouped_kernel<R1Shape<3, 2>, false, 0, 1><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, dPhi1,
+                                                                                              forces, msg),
+            note_launch();
     else if (a.l_max == 3 && a.L_max == 0)
         r1_reverse_kernel<R1Shape<3, 0>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, dPhi1,
                                                                           forces, msg), note_launch();
