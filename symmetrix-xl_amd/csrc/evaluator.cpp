@@ -179,18 +179,6 @@ std::vector<float> shape_cg(const HostModel& m)
     return std::vector<float>(cg.begin(), cg.end());
 }
 
-// The model's coupling coefficients are the compiled standard ones (to a few
-// float32 ulps): the kernels may then use the compiled literals.
-template <class S>
-bool cg_is_compiled(const std::vector<float>& cg)
-{
-    for (int t = 0; t < S::NT; ++t) {
-        const double want = S::cg_value[t];
-        if (std::abs(cg[t] - want) > 4e-7 * std::max(1.0, std::abs(want))) return false;
-    }
-    return true;
-}
-
 struct ShapeInfo {
     int nlme;
     std::vector<int> num_e, lme_off;
@@ -402,14 +390,6 @@ void Evaluator::upload_static_tables()
         cg = shape_cg<R1Shape<3, 0>>(m);
     else
         cg = shape_cg<R1Shape<3, 2>>(m);
-    if (m.l_max == 2 && m.L_max == 1)
-        cg_compiled_ = cg_is_compiled<R1Shape<2, 1>>(cg);
-    else if (m.l_max == 3 && m.L_max == 1)
-        cg_compiled_ = cg_is_compiled<R1Shape<3, 1>>(cg);
-    else if (m.l_max == 3 && m.L_max == 0)
-        cg_compiled_ = cg_is_compiled<R1Shape<3, 0>>(cg);
-    else
-        cg_compiled_ = cg_is_compiled<R1Shape<3, 2>>(cg);
     upload(cg_, cg, stream_);
     p0_layout_ = poly_layout(m.l_max, m.L_max, m.m0_offsets, m.m0_degree, m.m0_index);
     upload(p0_offsets_, p0_layout_.rem_offsets, stream_);
@@ -1702,7 +1682,6 @@ void Evaluator::evaluate()
     la.l_max = model_.l_max;
     la.L_max = model_.L_max;
     la.channel_slices = r1_slices_;
-    la.cg_compiled = cg_compiled_;
     la.node_offset = 0;
     la.node_count = N;
     density_args(la, nullptr);
@@ -1870,7 +1849,6 @@ void Evaluator::evaluate_tiled()
     la.l_max = model_.l_max;
     la.L_max = model_.L_max;
     la.channel_slices = r1_slices_;
-    la.cg_compiled = cg_compiled_;
     density_args(la, nullptr);
     la.type_order = node_order_.as<int>();
     hipStream_t s = stream_;

@@ -349,7 +349,6 @@ private:
     std::vector<int> host_types_;
     std::vector<int> host_first_;  // CSR receiver offsets of the prepared graph, [N + 1]
     int r1_slices_ = 1;            // channel slices of the second-interaction forward
-    bool cg_compiled_ = false;     // the model's coupling is the compiled standard one
     // host copies of uploads in flight, released at the next wait()
     std::vector<std::vector<unsigned char>> staged_;
     double cell_[9] = {}, inverse_cell_[9] = {};

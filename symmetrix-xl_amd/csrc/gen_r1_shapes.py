@@ -23,12 +23,16 @@ SHAPES = [(2, 1), (3, 1), (3, 2), (3, 0)]
 # groups by source l2: each pass owns its message rows and edge forces add up
 # over passes.  (Forward passes by output l were measured slower on the wide
 # shape than one pass: every extra sweep re-reads the source features.)  The
-# wide shape runs two passes, source l2 in {0, 1} and {2}: 219 VGPRs without
-# spills at two waves per SIMD; one pass spills, three repeat more per-edge
-# work.  Passes only pay where one pass does not fit: the medium shape split
+# wide shape runs two passes, source l2 in {0, 1} and {2}, at two waves per
+# SIMD; one pass spills, three repeat more per-edge work.  Passes only pay where one pass does not fit: the medium shape split
 # in two (164 VGPRs, three waves per SIMD) was measured 33 % slower.
 REV_GROUPS = {(3, 2): [[0, 1], [2]]}
-FACTORED_MAX_TRIPLES = 64
+# A pass holds its CG-contracted dPhi1 per (path, lm2, lm1) triple in
+# registers ("factored": two FMAs per triple and edge, no coefficient
+# operand) up to this many triples; the wide shape's passes hold 76 and 111
+# (211 VGPRs, no spills).  Beyond it a pass contracts per term with dPhi1 rows
+# in registers.
+FACTORED_MAX_TRIPLES = 128
 
 
 def emit_shape(lmax, Lmax):
@@ -52,12 +56,10 @@ def emit_shape(lmax, Lmax):
     row_path = []
     for p, (l1, l2, _) in enumerate(paths):
         row_path += [p] * ((2 * l1 + 1) * (2 * l2 + 1))
-    terms, coef = [], {}
+    terms = []
     for term in t["terms"]:
         p = row_path[term["row"]]
-        key = (p, term["lm2"], term["lm1"], term["lme"], term["row"])
-        terms.append(key)
-        coef[key] = coef.get(key, 0.0) + term["coefficient"]
+        terms.append((p, term["lm2"], term["lm1"], term["lme"], term["row"]))
     terms.sort()
     # (path, lm2) pairs and (path, lm2, lm1) triples in term order
     pqs, triples, term_tr = [], [], []
@@ -103,9 +105,6 @@ def emit_shape(lmax, Lmax):
         f"    static constexpr int term_lm1[NT] = {arr([x[2] for x in terms])};",
         f"    static constexpr int term_lme[NT] = {arr([x[3] for x in terms])};",
         f"    static constexpr int term_row[NT] = {arr([x[4] for x in terms])};",
-        "    // the coefficients of the standard real coupling (float32): kernels use",
-        "    // them as literals when the model's values equal them",
-        f"    static constexpr float cg_value[NT] = {{{', '.join(_f32_literal(coef[x]) for x in terms)}}};",
         "    // distinct (path, lm2) pairs and (path, lm2, lm1) triples, term order",
         f"    static constexpr int NPQ = {len(pqs)};",
         f"    static constexpr int pq_p[NPQ] = {arr([x[0] for x in pqs])};",
@@ -123,13 +122,6 @@ def emit_shape(lmax, Lmax):
         "",
     ]
     return "\n".join(lines) + groups
-
-
-def _f32_literal(v):
-    """The float32 nearest v, as a C++ literal that reads back exactly."""
-    import numpy as np
-
-    return repr(float(np.float32(v))) + "f"
 
 
 def _arr(vals):

@@ -176,9 +176,6 @@ struct LayerArgs {
     // of all channels).  Set where the coefficient table outgrows one XCD's
     // L2: each XCD then reads only its slice's columns.
     int channel_slices = 1;
-    // the model's coupling coefficients equal the compiled standard ones
-    // (R1Shape::cg_value): kernels may use them as literals
-    bool cg_compiled = false;
 };
 
 // Layer 0: A0[i] = sum_j R0f_{pair(i,j)}(r) Y(r_hat)   (H0 and A0_W folded in),

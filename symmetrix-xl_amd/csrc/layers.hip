@@ -558,6 +558,25 @@ r1_forward_sliced_kernel(LayerArgs a, const float* __restrict__ r1, const float*
     }
 }
 
+// The (path, lm2, lm1) triples of a shape or path group are contiguous per
+// (path, lm2) pair (term order): start[pq] .. start[pq + 1].
+template <class RG>
+struct RevTrRanges {
+    int start[RG::NPQ + 1] = {};
+    bool ordered = true;
+    constexpr RevTrRanges()
+    {
+        int pq = 0;
+        for (int tr = 0; tr < RG::NTR; ++tr) {
+            if (RG::tr_pq[tr] < pq) ordered = false;
+            while (pq < RG::tr_pq[tr]) start[++pq] = tr;
+        }
+        while (pq < RG::NPQ) start[++pq] = RG::NTR;
+    }
+};
+template <class RG>
+inline constexpr RevTrRanges<RG> kRevTrRanges{};
+
 // ---------------------------------------------------------------------------
 // Layer 1 reverse.  Per receiver and channel, the CG contraction of dPhi1 is
 // taken once: G[p, lm2, lm1] = sum_{t in (p, lm2, lm1)} cg_t dPhi1[lme_t].
@@ -793,9 +812,8 @@ struct RevTileLds {
     int count;
 };
 
-// kLit: the model carries the standard coupling, whose coefficients are
-// compile-time literals (S::cg_value); else they are read from cg.
-template <class S, class RG, int MAXT, bool kLit>
+
+template <class S, class RG, int MAXT>
 __device__ __forceinline__ void r1_reverse_pass(const LayerArgs& a, int i, bool first, int count,
                                                 const float* __restrict__ r1, const float* __restrict__ cg,
                                                 const float* __restrict__ H1, const float* __restrict__ dPhi1,
@@ -839,8 +857,7 @@ __device__ __forceinline__ void r1_reverse_pass(const LayerArgs& a, int i, bool 
         if (threadIdx.x < count) {
             const int j = threadIdx.x;
 #pragma unroll
-            for (int t = 0; t < RG::NT; ++t)
-                L.cgY[j][t] = (kLit ? S::cg_value[RG::term[t]] : cg[RG::term[t]]) * L.Y[j][RG::term_lm1[t]];
+            for (int t = 0; t < RG::NT; ++t) L.cgY[j][t] = cg[RG::term[t]] * L.Y[j][RG::term_lm1[t]];
         }
         __syncthreads();
     }
@@ -863,39 +880,53 @@ __device__ __forceinline__ void r1_reverse_pass(const LayerArgs& a, int i, bool 
 #pragma unroll
         for (int q = 0; q < RG::NH; ++q) H[q] = Hn[q];
         fetch(min(j + 1, count - 1), cn, Hn);
-        float sp[RG::NPQ], RH[RG::NPQ], U[NLM];
-#pragma unroll
-        for (int pq = 0; pq < RG::NPQ; ++pq) {
-            sp[pq] = 0.0f;
-            RH[pq] = R[RG::pq_p[pq]] * H[RG::pq_h[pq]];
-        }
+        float U[NLM], m[RG::NH], ap[RG::NP];
 #pragma unroll
         for (int lm = 0; lm < NLM; ++lm) U[lm] = 0.0f;
-        if constexpr (RG::FACTORED) {
 #pragma unroll
-            for (int tr = 0; tr < RG::NTR; ++tr) {
-                sp[RG::tr_pq[tr]] = fmaf(L.Y[j][RG::tr_lm1[tr]], G[tr], sp[RG::tr_pq[tr]]);
-                U[RG::tr_lm1[tr]] = fmaf(RH[RG::tr_pq[tr]], G[tr], U[RG::tr_lm1[tr]]);
+        for (int q = 0; q < RG::NH; ++q) m[q] = 0.0f;
+#pragma unroll
+        for (int p = 0; p < RG::NP; ++p) ap[p] = 0.0f;
+        if constexpr (RG::FACTORED) {
+            static_assert(kRevTrRanges<RG>.ordered, "triples of a (path, lm2) pair are not contiguous");
+            // one (path, lm2) pair at a time: its triples' sum sp is consumed
+            // at once, so no per-pair arrays are held
+            constexpr const RevTrRanges<RG>& tq = kRevTrRanges<RG>;
+            float Y[NLM];
+#pragma unroll
+            for (int lm = 0; lm < NLM; ++lm) Y[lm] = L.Y[j][lm];
+#pragma unroll
+            for (int pq = 0; pq < RG::NPQ; ++pq) {
+                const int p = RG::pq_p[pq], h = RG::pq_h[pq];
+                const float rh = R[p] * H[h];
+                float sp = 0.0f;
+#pragma unroll
+                for (int tr = tq.start[pq]; tr < tq.start[pq + 1]; ++tr) {
+                    sp = fmaf(Y[RG::tr_lm1[tr]], G[tr], sp);
+                    U[RG::tr_lm1[tr]] = fmaf(rh, G[tr], U[RG::tr_lm1[tr]]);
+                }
+                m[h] = fmaf(R[p], sp, m[h]);
+                ap[p] = fmaf(H[h], sp, ap[p]);
             }
         } else {
+            float sp[RG::NPQ], RH[RG::NPQ];
+#pragma unroll
+            for (int pq = 0; pq < RG::NPQ; ++pq) {
+                sp[pq] = 0.0f;
+                RH[pq] = R[RG::pq_p[pq]] * H[RG::pq_h[pq]];
+            }
 #pragma unroll
             for (int t = 0; t < RG::NT; ++t) {
                 const int pq = RG::tr_pq[RG::term_tr[t]];
                 const float d = G[RG::term_row[t]];
                 sp[pq] = fmaf(L.cgY[j][t], d, sp[pq]);
-                U[RG::term_lm1[t]] =
-                    fmaf(kLit ? S::cg_value[RG::term[t]] : cg[RG::term[t]], RH[pq] * d, U[RG::term_lm1[t]]);
+                U[RG::term_lm1[t]] = fmaf(cg[RG::term[t]], RH[pq] * d, U[RG::term_lm1[t]]);
             }
-        }
-        float m[RG::NH], ap[RG::NP];
 #pragma unroll
-        for (int q = 0; q < RG::NH; ++q) m[q] = 0.0f;
-#pragma unroll
-        for (int p = 0; p < RG::NP; ++p) ap[p] = 0.0f;
-#pragma unroll
-        for (int pq = 0; pq < RG::NPQ; ++pq) {
-            m[RG::pq_h[pq]] = fmaf(R[RG::pq_p[pq]], sp[pq], m[RG::pq_h[pq]]);
-            ap[RG::pq_p[pq]] = fmaf(H[RG::pq_h[pq]], sp[pq], ap[RG::pq_p[pq]]);
+            for (int pq = 0; pq < RG::NPQ; ++pq) {
+                m[RG::pq_h[pq]] = fmaf(R[RG::pq_p[pq]], sp[pq], m[RG::pq_h[pq]]);
+                ap[RG::pq_p[pq]] = fmaf(H[RG::pq_h[pq]], sp[pq], ap[RG::pq_p[pq]]);
+            }
         }
         float A = 0.0f;
 #pragma unroll
@@ -933,7 +964,7 @@ constexpr int rev_group_terms()
     return (m + 3) / 4 * 4;
 }
 
-template <class S, bool kLit, int... G>
+template <class S, int... G>
 __global__ void __launch_bounds__(256) r1_reverse_grouped_kernel(LayerArgs a, const float* __restrict__ r1,
                                                                   const float* __restrict__ cg,
                                                                   const float* __restrict__ H1,
@@ -979,7 +1010,7 @@ __global__ void __launch_bounds__(256) r1_reverse_grouped_kernel(LayerArgs a, co
         }
         __syncthreads();
         const int count = uniform(L.count);
-        (r1_reverse_pass<S, RevGroup<S, G>, MAXT, kLit>(a, i, G == 0, count, r1, cg, H1, dPhi1, msg, L), ...);
+        (r1_reverse_pass<S, RevGroup<S, G>, MAXT>(a, i, G == 0, count, r1, cg, H1, dPhi1, msg, L), ...);
         __syncthreads();
         if (threadIdx.x < count) {
             const int t = threadIdx.x;
@@ -1627,14 +1658,9 @@ hipError_t launch_r1_reverse(const LayerArgs& a, const float* r1, const float* c
     else if (a.l_max == 3 && a.L_max == 1)
         r1_reverse_kernel<R1Shape<3, 1>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, dPhi1,
                                                                           forces, msg), note_launch();
-    else if (a.l_max == 3 && a.L_max == 2 && a.cg_compiled)
-        r1_reverse_grouped_kernel<R1Shape<3, 2>, true, 0, 1><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, dPhi1,
-                                                                                             forces, msg),
-            note_launch();
     else if (a.l_max == 3 && a.L_max == 2)
-        r1_reverse_grouped_kernel<R1Shape<3, 2>, false, 0, 1><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, dPhi1,
-                                                                                              forces, msg),
-            note_launch();
+        r1_reverse_grouped_kernel<R1Shape<3, 2>, 0, 1><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, dPhi1,
+                                                                                       forces, msg), note_launch();
     else if (a.l_max == 3 && a.L_max == 0)
         r1_reverse_kernel<R1Shape<3, 0>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, dPhi1,
                                                                           forces, msg), note_launch();
