@@ -106,20 +106,24 @@ def test_wide_model_with_reference_coupling_values(oracle_lib, tmp_path):
     _full_size_check(oracle_lib, str(path), model, s, "water 300 H2O, wide shape with the reference's 215 coupling terms")
 
 
-def test_scalar_model_with_reference_coupling_values(oracle_lib, tmp_path):
-    # the scalar (3,0) shape with the coupling terms of the reference's
-    # omat0-small contract (tests/golden, from symmetrix/test/data/
-    # execution_contracts/jit_r1_mace_omat0_small_contract.json: 4 paths,
-    # 16 terms, 128 channels)
+@pytest.mark.parametrize("contract_name", ["jit_r1_mace_omat0_small_contract.json",
+                                           "jit_r1_mace_off23_small_contract.json"])
+def test_scalar_model_with_reference_coupling_values(oracle_lib, tmp_path, contract_name):
+    # the scalar (3,0) shape with the coupling terms and channel count of the
+    # reference's omat0-small (128 channels) and off23-small (96 channels)
+    # contracts (tests/golden, from symmetrix/test/data/execution_contracts/:
+    # 4 paths, 16 terms)
+    import dataclasses
     import os
 
     from symmetrix_amd import synthetic
 
-    golden = os.path.join(os.path.dirname(__file__), "golden", "jit_r1_mace_omat0_small_contract.json")
+    golden = os.path.join(os.path.dirname(__file__), "golden", contract_name)
     with open(golden) as f:
         contract = json.load(f)
-    assert contract["channels"] == synthetic.PRESETS["scalar"].channels
-    model = json.loads(synthetic.model_json(synthetic.random_mace_model("scalar", seed=5)))
+    shape = dataclasses.replace(synthetic.PRESETS["scalar"], channels=contract["channels"])
+    model = json.loads(synthetic.model_json(synthetic.random_mace_model(shape, seed=5)))
+    assert model["num_channels"] == contract["channels"]
     assert [(l1, l2, lo) for l1, l2, lo in zip(model["Phi1_l1"], model["Phi1_l2"], model["Phi1_l"])] == [
         (p["edge_l"], p["source_l"], p["output_l"]) for p in contract["paths"]]
     terms = contract["sparse_coupling"]["terms"]
@@ -130,7 +134,8 @@ def test_scalar_model_with_reference_coupling_values(oracle_lib, tmp_path):
     path = tmp_path / "scalar_contract.json"
     path.write_text(json.dumps(model))
     s = synthetic.srtio3_supercell(6, sigma=0.05, seed=2)
-    _full_size_check(oracle_lib, str(path), model, s, "SrTiO3 6^3, scalar shape with the reference's 16 coupling terms")
+    _full_size_check(oracle_lib, str(path), model, s,
+                     f"SrTiO3 6^3, scalar shape, C={contract['channels']}, the reference's 16 coupling terms")
 
 
 def test_irregular_config_full_size(oracle_lib, medium):
