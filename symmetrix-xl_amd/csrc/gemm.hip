@@ -113,23 +113,36 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 5))
         }
         __syncthreads();
     }
+    // accumulator v of block j holds row 8 (v >> 2) + 4 (lane >> 5) + (v & 3),
+    // column j * 32 + (lane & 31): four runs of four consecutive rows, whose
+    // (node, row in node) is found once per run and then stepped
+    const int rpn = g.rows_per_node;
 #pragma unroll
-    for (int j = 0; j < kNB; ++j) {
-        const int col = col0 + wn * (kBN / kWN) + j * 32 + (lane & 31);
-        if (col >= N) continue;
+    for (int q = 0; q < 4; ++q) {
+        int row = row0 + wm * 32 + 8 * q + 4 * (lane >> 5);
+        int node = row / rpn;
+        int m = row - node * rpn;
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int row = row0 + wm * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        for (int u = 0; u < 4; ++u) {
             if (row < M) {
-                const int node = row / g.rows_per_node;
-                const int m = row - node * g.rows_per_node;
-                float value = acc[j][v];
-                if (g.bias.ptr)
-                    value += g.bias.ptr[g.bias.node_types[g.bias.node_base + node] * g.bias.type_stride +
-                                        m * g.bias.row_stride + col];
-                float* dst = g.c.ptr + node * g.c.node_stride + m * g.c.row_stride + col;
-                if (g.accumulate) value += *dst;
-                *dst = value;
+                const long long base = static_cast<long long>(node) * g.c.node_stride + m * g.c.row_stride;
+#pragma unroll
+                for (int j = 0; j < kNB; ++j) {
+                    const int col = col0 + wn * (kBN / kWN) + j * 32 + (lane & 31);
+                    if (col >= N) continue;
+                    float value = acc[j][4 * q + u];
+                    if (g.bias.ptr)
+                        value += g.bias.ptr[g.bias.node_types[g.bias.node_base + node] * g.bias.type_stride +
+                                            m * g.bias.row_stride + col];
+                    float* dst = g.c.ptr + base + col;
+                    if (g.accumulate) value += *dst;
+                    *dst = value;
+                }
+            }
+            ++row;
+            if (++m == rpn) {
+                m = 0;
+                ++node;
             }
         }
     }
