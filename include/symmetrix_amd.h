@@ -89,6 +89,19 @@ const char* sxl_last_error(void);
 int sxl_create(const char* model_path, const char* head, sxl_evaluator** out);
 void sxl_destroy(sxl_evaluator* evaluator);
 
+/* Runtime lifecycle.  Replace the module functions _init_kokkos,
+ * _finalize_kokkos, _kokkos_is_initialized, _kokkos_live_object_count and
+ * _kokkos_default_execution_space (symmetrix/source/cpp/tools_kokkos.cpp:522-534;
+ * libsymmetrix/source/tools_kokkos.cpp:44-99).  Creating an evaluator
+ * initializes the runtime; finalization fails while evaluators are alive and
+ * no evaluator can be created after it.  sxl_runtime_is_initialized returns
+ * 1 or 0; sxl_default_execution_space returns "HIP". */
+int sxl_runtime_initialize(void);
+int sxl_runtime_finalize(void);
+int sxl_runtime_is_initialized(void);
+int64_t sxl_live_evaluator_count(void);
+const char* sxl_default_execution_space(void);
+
 /* Model metadata: r_cut, l_max, L_max, ... properties (mace_kokkos.cpp:2762). */
 int sxl_model_info(const sxl_evaluator* evaluator, sxl_model_info_t* out);
 /* atomic_numbers / atomic_energies properties: num_elements entries. */

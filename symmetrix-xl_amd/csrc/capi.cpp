@@ -4,6 +4,7 @@
 #include <algorithm>
 #include <cmath>
 #include <memory>
+#include <mutex>
 #include <new>
 #include <stdexcept>
 #include <string>
@@ -63,6 +64,27 @@ int null_handle()
     return SXL_INVALID_ARGUMENT;
 }
 
+// Runtime lifecycle (reference libsymmetrix/source/tools_kokkos.cpp:44-99):
+// evaluators are counted while alive; finalization is refused while any is
+// alive and is final -- no evaluator can be constructed afterwards.
+std::mutex g_runtime_mutex;
+bool g_runtime_initialized = false;
+bool g_runtime_finalized = false;
+std::int64_t g_live_evaluators = 0;
+
+void initialize_runtime_locked()
+{
+    if (g_runtime_finalized) throw std::runtime_error("Cannot initialize the HIP runtime after finalization.");
+    if (g_runtime_initialized) return;
+    const hipError_t err = hipInit(0);
+    int devices = 0;
+    if (err != hipSuccess || hipGetDeviceCount(&devices) != hipSuccess || devices <= 0) {
+        (void)hipGetLastError();
+        throw std::runtime_error("HIP runtime initialization found no usable device.");
+    }
+    g_runtime_initialized = true;
+}
+
 }  // namespace
 
 extern "C" {
@@ -73,10 +95,61 @@ int sxl_create(const char* model_path, const char* head, sxl_evaluator** out)
 {
     if (!model_path || !out) return null_handle();
     *out = nullptr;
-    return guarded([&] { *out = new sxl_evaluator(model_path, head); });
+    return guarded([&] {
+        {
+            const std::scoped_lock lock(g_runtime_mutex);
+            if (g_runtime_finalized)
+                throw std::runtime_error("Cannot construct a Symmetrix evaluator after Kokkos finalization.");
+        }
+        auto ev = std::make_unique<sxl_evaluator>(model_path, head);
+        const std::scoped_lock lock(g_runtime_mutex);
+        g_runtime_initialized = true;
+        g_live_evaluators += 1;
+        *out = ev.release();
+    });
 }
 
-void sxl_destroy(sxl_evaluator* evaluator) { delete evaluator; }
+void sxl_destroy(sxl_evaluator* evaluator)
+{
+    if (!evaluator) return;
+    delete evaluator;
+    const std::scoped_lock lock(g_runtime_mutex);
+    g_live_evaluators -= 1;
+}
+
+int sxl_runtime_initialize(void)
+{
+    return guarded([] {
+        const std::scoped_lock lock(g_runtime_mutex);
+        initialize_runtime_locked();
+    });
+}
+
+int sxl_runtime_finalize(void)
+{
+    return guarded([] {
+        const std::scoped_lock lock(g_runtime_mutex);
+        if (g_live_evaluators != 0)
+            throw std::runtime_error("Cannot finalize Kokkos while " + std::to_string(g_live_evaluators) +
+                                     " Symmetrix evaluator object(s) are alive.");
+        g_runtime_initialized = false;
+        g_runtime_finalized = true;
+    });
+}
+
+int sxl_runtime_is_initialized(void)
+{
+    const std::scoped_lock lock(g_runtime_mutex);
+    return g_runtime_initialized ? 1 : 0;
+}
+
+int64_t sxl_live_evaluator_count(void)
+{
+    const std::scoped_lock lock(g_runtime_mutex);
+    return g_live_evaluators;
+}
+
+const char* sxl_default_execution_space(void) { return "HIP"; }
 
 int sxl_model_info(const sxl_evaluator* ev, sxl_model_info_t* out)
 {

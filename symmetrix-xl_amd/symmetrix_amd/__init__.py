@@ -10,7 +10,16 @@ models, FP32, one GPU).
 """
 
 from .calculator import Symmetrix, full_3x3_to_voigt_6_stress
-from .mace import MACEKokkosFloat, _kokkos_periodic_neighbor_graph, periodic_neighbor_graph
+from .mace import (
+    MACEKokkosFloat,
+    _finalize_kokkos,
+    _init_kokkos,
+    _kokkos_default_execution_space,
+    _kokkos_is_initialized,
+    _kokkos_live_object_count,
+    _kokkos_periodic_neighbor_graph,
+    periodic_neighbor_graph,
+)
 
 __all__ = [
     "MACEKokkosFloat",
@@ -18,4 +27,9 @@ __all__ = [
     "full_3x3_to_voigt_6_stress",
     "periodic_neighbor_graph",
     "_kokkos_periodic_neighbor_graph",
+    "_init_kokkos",
+    "_finalize_kokkos",
+    "_kokkos_is_initialized",
+    "_kokkos_live_object_count",
+    "_kokkos_default_execution_space",
 ]

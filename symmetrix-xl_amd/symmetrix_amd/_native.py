@@ -54,6 +54,11 @@ SIGNATURES = {
     "sxl_last_error": (ctypes.c_char_p, []),
     "sxl_create": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p)]),
     "sxl_destroy": (None, [ctypes.c_void_p]),
+    "sxl_runtime_initialize": (ctypes.c_int, []),
+    "sxl_runtime_finalize": (ctypes.c_int, []),
+    "sxl_runtime_is_initialized": (ctypes.c_int, []),
+    "sxl_live_evaluator_count": (ctypes.c_int64, []),
+    "sxl_default_execution_space": (ctypes.c_char_p, []),
     "sxl_model_info": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ModelInfo)]),
     "sxl_atomic_numbers": (ctypes.c_int, [ctypes.c_void_p, c_int_p]),
     "sxl_atomic_energies": (ctypes.c_int, [ctypes.c_void_p, c_double_p]),

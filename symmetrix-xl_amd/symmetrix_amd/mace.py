@@ -504,6 +504,32 @@ class MACEKokkosFloat:
         return {name: getattr(s, name) for name, _ in _native.Stats._fields_}
 
 
+# --- runtime lifecycle (reference tools_kokkos.cpp:522-534) ---------------------
+def _init_kokkos():
+    """Initialise the HIP runtime (reference ``_init_kokkos``); creating an
+    evaluator does this too."""
+    check(library().sxl_runtime_initialize())
+
+
+def _finalize_kokkos():
+    """Finalise the runtime (reference ``_finalize_kokkos``): RuntimeError
+    while evaluators are alive; no evaluator can be created afterwards."""
+    check(library().sxl_runtime_finalize())
+
+
+def _kokkos_is_initialized():
+    return bool(library().sxl_runtime_is_initialized())
+
+
+def _kokkos_live_object_count():
+    """Evaluator objects alive in this process."""
+    return int(library().sxl_live_evaluator_count())
+
+
+def _kokkos_default_execution_space():
+    return library().sxl_default_execution_space().decode()
+
+
 def periodic_neighbor_graph(positions, cell, inverse_cell, cutoff):
     """Periodic neighbour graph on the device in the reference's edge order
     (reference ``_kokkos_periodic_neighbor_graph``): dict of num_neigh,

@@ -103,3 +103,20 @@ def test_preparation_counts_are_reproducible(tiny):
     ev._prepare_factorized_graph(len(types), types, g["num_neigh"], g["sources"], types[g["sources"]])
     assert ev.factorized_prepared_graph_count == 3
     assert ev.factorized_preparation_fence_count == 2 * first + 2
+
+
+def test_live_evaluators_block_finalization(tiny):
+    # the reference counts live evaluators and refuses to finalize while any
+    # is alive (tools_kokkos.cpp:57-66); the runtime is not finalized here
+    import symmetrix_amd as s
+    from symmetrix_amd import MACEKokkosFloat
+
+    base = s._kokkos_live_object_count()
+    ev = MACEKokkosFloat(tiny[0])
+    assert s._kokkos_is_initialized()
+    assert s._kokkos_live_object_count() == base + 1
+    with pytest.raises(RuntimeError, match=r"Cannot finalize Kokkos while \d+ Symmetrix evaluator"):
+        s._finalize_kokkos()
+    ev.close()
+    assert s._kokkos_live_object_count() == base
+    assert s._kokkos_is_initialized()

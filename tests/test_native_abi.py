@@ -213,3 +213,39 @@ def test_null_arguments_are_rejected():
     lib = _native.library()
     assert lib.sxl_create(None, None, None) == 1
     assert lib.sxl_stats(None, None) == 1
+
+
+def test_runtime_lifecycle_without_a_device():
+    # the reference's module lifecycle (tools_kokkos.cpp:44-99), in a fresh
+    # process that never touches a device: finalization is final -- neither
+    # the runtime nor an evaluator can be created after it
+    import subprocess
+    import sys
+
+    code = """
+import sys
+sys.path.insert(0, {pkg!r})
+import symmetrix_amd as s
+assert s._kokkos_default_execution_space() == "HIP"
+assert not s._kokkos_is_initialized()
+assert s._kokkos_live_object_count() == 0
+s._finalize_kokkos()
+assert not s._kokkos_is_initialized()
+try:
+    s.MACEKokkosFloat({model!r})
+except RuntimeError as e:
+    assert "after Kokkos finalization" in str(e), e
+else:
+    raise AssertionError("constructed after finalization")
+try:
+    s._init_kokkos()
+except RuntimeError as e:
+    assert "after finalization" in str(e), e
+else:
+    raise AssertionError("initialized after finalization")
+assert s._kokkos_live_object_count() == 0
+print("lifecycle ok")
+""".format(pkg=os.path.join(ROOT, "symmetrix-xl_amd"), model=os.path.join(ROOT, "no_such_model.json"))
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stderr
+    assert "lifecycle ok" in out.stdout
