@@ -370,7 +370,8 @@ def main():
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py runs on one GPU only: this build has no multi-GPU path "
-              "(sharding is described in DESIGN.md); use --gpus 1", file=sys.stderr)
+              "(the evaluation would shard by spatial domain with halo exchanges of H1 "
+              "and its adjoint); use --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     if args.capacity_cells > 0:
