@@ -31,7 +31,8 @@ for p in (os.path.join(ROOT, "symmetrix-xl_amd"), ROOT):
         sys.path.insert(0, p)
 
 METRIC = "µs/atom per E+F+stress call (FP32, 1 MI355X) at 5k atoms; max atoms tiled"
-PUBLISHED_US_PER_ATOM = 1.922  # reference, RTX 5090, 5,000-atom SrTiO3
+PUBLISHED_US_PER_ATOM = 1.922  # reference, RTX 5090, 5,000-atom SrTiO3 (README.md:72-94)
+PUBLISHED_MD_US_PER_ATOM_STEP = 2.559  # reference LAMMPS pair style, RTX 5090, same system (README.md:101-104)
 FP32_PEAK_TFLOPS = 157.3       # MI355X published FP32 (vector with packed FP32, and matrix)
 FP32_NONPACKED_TFLOPS = 78.6   # one FMA per lane per cycle: the ceiling of non-packed FP32 VALU code
 HBM_PEAK_GBS = 8000.0
@@ -245,9 +246,22 @@ STAGE_BOUND = {
 
 
 # atomic masses (amu) of the SrTiO3 elements for the NVE run
-MASSES = {38: 87.62, 22: 47.867, 8: 15.999}
+# standard atomic weights (amu) of the elements the workloads use
+MASSES = {1: 1.008, 6: 12.011, 7: 14.007, 8: 15.999, 13: 26.982, 14: 28.085, 22: 47.867, 26: 55.845,
+          29: 63.546, 38: 87.62}
 EV_PER_A_AMU_TO_A_PER_FS2 = 9.648533212e-3  # 1 eV/(A amu) in A/fs^2
 KB_EV = 8.617333262e-5
+
+
+def thermal_start(structure, seed, kelvin=300.0):
+    """Masses (amu) and Maxwell-Boltzmann velocities (A/fs) at `kelvin`, zero
+    total momentum."""
+    m = np.array([MASSES[int(z)] for z in structure.numbers])
+    rng = np.random.default_rng(seed + 1)
+    # v in A/fs: sqrt(kT/m), kT/m in eV/amu times the unit factor gives (A/fs)^2
+    v = rng.normal(size=(len(m), 3)) * np.sqrt(KB_EV * kelvin * EV_PER_A_AMU_TO_A_PER_FS2 / m)[:, None]
+    v -= (m[:, None] * v).sum(0) / m.sum()
+    return m, v
 
 
 def capacity_run(args):
@@ -268,11 +282,7 @@ def capacity_run(args):
     if args.tile_receivers > 0:
         ev._set_dual_layer_workspace_receiver_limit_for_testing(args.tile_receivers)
     types = synthetic.node_types(s, ev.atomic_numbers)
-    m = np.array([MASSES[int(z)] for z in s.numbers])
-    rng = np.random.default_rng(args.seed + 1)
-    # v in A/fs: sqrt(kT/m), kT/m in eV/amu times the unit factor gives (A/fs)^2
-    v = rng.normal(size=(N, 3)) * np.sqrt(KB_EV * 300.0 * EV_PER_A_AMU_TO_A_PER_FS2 / m)[:, None]
-    v -= (m[:, None] * v).sum(0) / m.sum()
+    m, v = thermal_start(s, args.seed)
     print(f"[capacity] setup {time.perf_counter() - t_setup:.1f} s; running {args.md_steps} steps on the device",
           file=sys.stderr, flush=True)
     t_run = time.perf_counter()
@@ -343,6 +353,8 @@ def main():
     ap.add_argument("--capacity-cells", type=int, default=0, metavar="N",
                     help="tiled capacity run on SrTiO3 N^3 (5 N^3 atoms) instead of the 5k-atom benchmark")
     ap.add_argument("--md-steps", type=int, default=20)
+    ap.add_argument("--md-bench-steps", type=int, default=20,
+                    help="device NVE steps at the timed workload (0: skip)")
     ap.add_argument("--md-dt", type=float, default=1.0, help="fs")
     ap.add_argument("--tile-receivers", type=int, default=0, help="receivers per tile (0: planner)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -521,6 +533,32 @@ def main():
         }
         del calc
 
+    # MD at the timed workload: the device velocity-Verlet NVE driver (the
+    # `fix nve` update of the reference's LAMMPS runs), from 300 K, 1 fs;
+    # per-step wall time including the skin check (and any rebuild)
+    md = None
+    if args.md_bench_steps > 0:
+        ev_md = MACEKokkosFloat(model_path)
+        m, v = thermal_start(structure, args.seed)
+        res = ev_md._md_nve(synthetic.node_types(structure, ev_md.atomic_numbers), m, structure.positions, v,
+                            structure.cell, args.skin, args.md_dt, args.md_bench_steps)
+        steps_us = [t / N * 1e6 for t in res["step_seconds"]]
+        etot = res["potential_energy"] + res["kinetic_energy"]
+        md = {
+            "value": round(statistics.median(steps_us), 5),
+            "unit": "us/atom/step",
+            "mean": round(statistics.mean(steps_us), 5),
+            "steps": args.md_bench_steps,
+            "dt_fs": args.md_dt,
+            "neighbor_rebuilds": res["rebuilds"],
+            "max_energy_drift_per_atom_eV": round(float(np.max(np.abs(etot - etot[0]))) / N, 9),
+            "integrator": "device velocity-Verlet NVE (sxl_md_nve), 300 K start; the reference's LAMMPS "
+                          "pair-style step is 2.559 us/atom/step on an RTX 5090 (README.md:101-104)",
+            "vs_published": round(statistics.median(steps_us) / PUBLISHED_MD_US_PER_ATOM_STEP, 4),
+        }
+        ev_md.close()
+        del ev_md
+
     cpu = None
     parity = None
     if args.cpu_calls > 0:
@@ -581,6 +619,7 @@ def main():
         },
         "median_us_per_atom": round(median_us, 5),
         "host_boundary": host,
+        "md_nve": md,
         "parity": parity,
         "stage_ms": {k: round(v, 4) for k, v in stage_avg.items()},
         "stage_ms_source": "HIP events around every stage, 3 untimed calls after the warmup",
