@@ -30,7 +30,7 @@ REV_GROUPS = {(3, 2): [[0, 1], [2]]}
 # A pass holds its CG-contracted dPhi1 per (path, lm2, lm1) triple in
 # registers ("factored": two FMAs per triple and edge, no coefficient
 # operand) up to this many triples; the wide shape's passes hold 76 and 111
-# (211 VGPRs, no spills).  Beyond it a pass contracts per term with dPhi1 rows
+# (241 VGPRs, no spills).  Beyond it a pass contracts per term with dPhi1 rows
 # in registers.
 FACTORED_MAX_TRIPLES = 128
 
