@@ -513,10 +513,11 @@ void Evaluator::prepare_active_types(const std::vector<int>& node_types)
     }
     upload(r1_, r1, stream_, &staged_);
     upload(r0f_, r0f, stream_, &staged_);
-    // the second-interaction forward runs in 64-channel slices, one slice per
-    // XCD, when its coefficient table is far beyond one XCD's L2 (4 MiB)
+    // the second-interaction forward of a 256-channel model runs in 64-channel
+    // slices, one slice per XCD, when its coefficient table is far beyond one
+    // XCD's L2 (4 MiB)
     r1_slices_ = 1;
-    if ((C_ == 128 || C_ == 256) && r1.size() * sizeof(float) > kR1SliceTableBytes) r1_slices_ = C_ / 64;
+    if (C_ == 256 && r1.size() * sizeof(float) > kR1SliceTableBytes) r1_slices_ = C_ / 64;
     // density-normalisation splines per unordered pair: [pair_u][iv][4]
     auto density_table = [&](const RadialNetwork& net, DeviceBuffer& out) {
         std::vector<float> table(static_cast<std::size_t>(npairs) * NI * 4);

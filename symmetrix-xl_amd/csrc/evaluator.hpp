@@ -130,10 +130,12 @@ struct EvaluatorStats {
 // and the untiled workspace does not fit (reference mace_kokkos.hpp:542).
 constexpr int kDefaultTileReceivers = 32768;
 
-// Coefficient-table size above which the second-interaction forward runs in
-// channel slices.  Measured: the wide shape's 17.8 MB table (C = 256, 4
-// slices) 9.4 -> 6.9 ms on 30,000 water atoms; the medium shape's 5.2 MB
-// table (C = 128, 2 slices, mostly L2-resident already) 0.31 -> 0.38 ms.
+// Coefficient-table size above which the second-interaction forward of a
+// 256-channel model runs in 64-channel slices.  Measured: the wide shape's
+// 17.8 MB table (C = 256, 4 slices) 9.4 -> 6.9 ms on 30,000 water atoms.  At
+// C = 128 two slices lose whatever the table size: the medium shape's 5.2 MB
+// table 0.31 -> 0.38 ms, its 31 MB per-pair (Agnesi) tables 0.33 -> 0.39 ms,
+// the wide shape's 8.9 MB table at C = 128 3.2 -> 3.6 ms.
 constexpr std::size_t kR1SliceTableBytes = std::size_t(8) << 20;
 
 // Execution-plan report (reference execution_plan.hpp:32-50 and

@@ -89,6 +89,13 @@ PRESETS = {
         atomic_numbers=(38, 22, 8), channels=128, l_max=3, L_max=1,
         correlation=3, radial_hidden=(64, 64, 64), r_cut=6.0, avg_num_neighbors=70.0,
     ),
+    # Medium shape with the Agnesi distance transform: the radial tables are
+    # per unordered element pair (6 pairs on SrTiO3) instead of shared.
+    "medium_agnesi": ModelShape(
+        atomic_numbers=tuple(range(1, 90)), channels=128, l_max=3, L_max=1,
+        correlation=3, radial_hidden=(64, 64, 64), r_cut=6.0, avg_num_neighbors=70.0,
+        agnesi=True,
+    ),
     # Scalar hidden features (L_max = 0, 128x0e, lmax 3, correlation 3): the
     # shape of the reference's omat0-small and off23-small models, whose
     # second interaction has 4 paths and 16 coupling terms.
