@@ -767,7 +767,7 @@ std::size_t Evaluator::held_graph_bytes() const
         &node_types_, &first_, &receiver_, &source_, &tfirst_, &tedge_, &edge_pair_, &disp_, &positions_,
         &cell_dev_, &xyz_, &r_, &geo_positions_, &geo_edges_, &geo_shifts_, &A0_, &M0_, &H1_, &Phi1_, &A1_,
         &A1adj_, &direct_, &H1adj_, &msg_, &energies_, &forces_, &atom_forces_, &partials_, &totals_, &scratch_,
-        &scale1_, &dot1_, &M0s_, &run_source_, &run_start_, &run_length_, &node_order_, &m0_blocks_,
+        &scale1_, &dot1_, &M0s_, &run_source_, &run_start_, &run_length_, &node_order_, &m0_blocks_, &m0r_blocks_,
         &readout_blocks_, &tile_xyz_, &tile_r_, &tile_pair_, &tile_forces_, &tile_first_edge_dev_,
         &pgraph_.first, &pgraph_.sources, &pgraph_.shifts, &pgraph_.fractional_xyz, &pgraph_.fractional_positions};
     std::size_t total = 0;
@@ -896,8 +896,10 @@ void Evaluator::plan_node_blocks()
     for (int a = 0; a < na; ++a) ta[active_types_[a]] = a;
     std::vector<int> order;
     order.reserve(N);
-    std::vector<NodeBlock> m0b, rob;
+    std::vector<NodeBlock> m0b, m0rb, rob;
+    m0r_block_nodes_ = C_ <= 128 ? kM0ReverseBlockNodesNarrow : kM0BlockNodes;
     m0_block_offsets_.assign(tiles + 1, 0);
+    m0r_block_offsets_.assign(tiles + 1, 0);
     readout_block_offsets_.assign(tiles + 1, 0);
     std::vector<std::vector<int>> by_type(na);
     for (int t = 0; t < tiles; ++t) {
@@ -909,24 +911,30 @@ void Evaluator::plan_node_blocks()
             const int n = static_cast<int>(by_type[a].size());
             order.insert(order.end(), by_type[a].begin(), by_type[a].end());
             for (int b = 0; b < n; b += kM0BlockNodes) m0b.push_back({start + b, std::min(kM0BlockNodes, n - b), a, 0});
+            for (int b = 0; b < n; b += m0r_block_nodes_)
+                m0rb.push_back({start + b, std::min(m0r_block_nodes_, n - b), a, 0});
             for (int b = 0; b < n; b += kReadoutBlockNodes)
                 rob.push_back({start + b, std::min(kReadoutBlockNodes, n - b), a, 0});
         }
         m0_block_offsets_[t + 1] = static_cast<int>(m0b.size());
+        m0r_block_offsets_[t + 1] = static_cast<int>(m0rb.size());
         readout_block_offsets_[t + 1] = static_cast<int>(rob.size());
     }
     upload(node_order_, order, stream_, &staged_);
     upload(m0_blocks_, m0b, stream_, &staged_);
+    upload(m0r_blocks_, m0rb, stream_, &staged_);
     upload(readout_blocks_, rob, stream_, &staged_);
 }
 
-NodeBlocks Evaluator::node_blocks(const DeviceBuffer& blocks, const std::vector<int>& offsets, int tile) const
+NodeBlocks Evaluator::node_blocks(const DeviceBuffer& blocks, const std::vector<int>& offsets, int tile,
+                                  int block_nodes) const
 {
     NodeBlocks nb;
     nb.order = node_order_.as<int>();
     nb.blocks = blocks.as<NodeBlock>();
     nb.first = offsets[tile];
     nb.count = offsets[tile + 1] - offsets[tile];
+    nb.block_nodes = block_nodes;
     return nb;
 }
 
@@ -1698,7 +1706,7 @@ void Evaluator::evaluate()
         hip_check(launch_a0_forward(la, r0f_.as<float>(), A0_.as<float>(), s), "A0 forward");
         mark(kStageA0Forward, true);
         mark(kStageM0Forward, false);
-        hip_check(launch_m0_forward(la, p0, node_blocks(m0_blocks_, m0_block_offsets_, 0), A0_.as<float>(),
+        hip_check(launch_m0_forward(la, p0, node_blocks(m0_blocks_, m0_block_offsets_, 0, kM0BlockNodes), A0_.as<float>(),
                                     M0_.as<float>(), s),
                   "M0 forward");
         mark(kStageM0Forward, true);
@@ -1716,7 +1724,7 @@ void Evaluator::evaluate()
         mark(kStageA1Gemm, true);
         // readout and its reverse down to A1_adj
         ReadoutArgs ra;
-        ra.nodes = node_blocks(readout_blocks_, readout_block_offsets_, 0);
+        ra.nodes = node_blocks(readout_blocks_, readout_block_offsets_, 0, kReadoutBlockNodes);
         ra.local_base = 0;
         ra.m0_stride = nodeLM;
         ra.C = C_;
@@ -1771,7 +1779,7 @@ void Evaluator::evaluate()
         // A0_adj into the A1 buffer (no longer needed)
         float* A0adj = A1_.as<float>();
         mark(kStageM0Reverse, false);
-        hip_check(launch_m0_reverse(la, p0, node_blocks(m0_blocks_, m0_block_offsets_, 0), A0_.as<float>(), M0adj,
+        hip_check(launch_m0_reverse(la, p0, node_blocks(m0r_blocks_, m0r_block_offsets_, 0, m0r_block_nodes_), A0_.as<float>(), M0adj,
                                     A0adj, s),
                   "M0 reverse");
         mark(kStageM0Reverse, true);
@@ -1925,7 +1933,7 @@ void Evaluator::evaluate_tiled()
     for (int t = 0; t < num_tiles_; ++t) {
         tile(t, true);
         hip_check(launch_a0_forward(la, r0f_.as<float>(), A0_.as<float>(), s), "A0 forward");
-        hip_check(launch_m0_forward(la, p0, node_blocks(m0_blocks_, m0_block_offsets_, t), A0_.as<float>(),
+        hip_check(launch_m0_forward(la, p0, node_blocks(m0_blocks_, m0_block_offsets_, t, kM0BlockNodes), A0_.as<float>(),
                                     M0_.as<float>(), s),
                   "M0 forward");
         float* x = M0s + static_cast<std::size_t>(la.node_offset) * C_;
@@ -1966,7 +1974,7 @@ void Evaluator::evaluate_tiled()
         tile(t, false);
         hip_check(launch_r1_forward(la, r1_.as<float>(), cg_.as<float>(), H1, Phi1_.as<float>(), s), "R1 forward");
         gemm_a1(la.node_count, Phi1_.as<float>(), A1_.as<float>(), false, "A1 gemm");
-        ra.nodes = node_blocks(readout_blocks_, readout_block_offsets_, t);
+        ra.nodes = node_blocks(readout_blocks_, readout_block_offsets_, t, kReadoutBlockNodes);
         ra.local_base = la.local_base;
         hip_check(launch_readout(ra, s), "readout");
         gemm_a1(la.node_count, A1adj_.as<float>(), dPhi1, true, "A1 reverse gemm");
@@ -1984,7 +1992,7 @@ void Evaluator::evaluate_tiled()
                 "H1 reverse gemm");
         add_direct(la.node_count, la.node_offset, M0adj, s);
         hip_check(launch_a0_forward(la, r0f_.as<float>(), A0_.as<float>(), s), "A0 forward");
-        hip_check(launch_m0_reverse(la, p0, node_blocks(m0_blocks_, m0_block_offsets_, t), A0_.as<float>(), M0adj,
+        hip_check(launch_m0_reverse(la, p0, node_blocks(m0r_blocks_, m0r_block_offsets_, t, m0r_block_nodes_), A0_.as<float>(), M0adj,
                                     A0adj, s),
                   "M0 reverse");
         // the A0 reverse adds into the directed forces: this sweep's part starts at zero

@@ -296,7 +296,8 @@ private:
     void allocate_workspace();
     void plan_tiles();
     void plan_node_blocks();
-    NodeBlocks node_blocks(const DeviceBuffer& blocks, const std::vector<int>& offsets, int tile) const;
+    NodeBlocks node_blocks(const DeviceBuffer& blocks, const std::vector<int>& offsets, int tile,
+                           int block_nodes) const;
     void invalidate_graph();
     void evaluate();
     void evaluate_tiled();
@@ -419,8 +420,10 @@ private:
     // device NVE driver state: positions, velocities, masses, unit factor / mass, kinetic partials
     DeviceBuffer md_x_, md_v_, md_m_, md_inv_m_, md_partials_;
     // nodes grouped by (tile, active type) and their blocks for the node kernels
-    DeviceBuffer node_order_, m0_blocks_, readout_blocks_;
-    std::vector<int> m0_block_offsets_, readout_block_offsets_;  // [tiles + 1]
+    DeviceBuffer node_order_, m0_blocks_, m0r_blocks_, readout_blocks_;
+    // [tiles + 1] each; the M0 reverse has its own block size (m0r_block_nodes_)
+    std::vector<int> m0_block_offsets_, m0r_block_offsets_, readout_block_offsets_;
+    int m0r_block_nodes_ = kM0BlockNodes;
 
     bool profiling_ = false;
     unsigned profile_mask_ = 0;

@@ -96,8 +96,14 @@ struct NodeBlocks {
     const NodeBlock* blocks = nullptr;
     int first = 0;
     int count = 0;
+    int block_nodes = 0;  // most nodes in one block of the list
 };
 constexpr int kM0BlockNodes = 4;       // nodes per block of the M0 kernels
+// nodes per block of the M0 reverse at C <= 128: its blocks are two waves of
+// 200 VGPRs, and four nodes per block leave a 5,000-atom launch one and a
+// fraction waves per SIMD (measured: 66 -> 55 us at two nodes per block; at
+// C = 256 two nodes per block were slower)
+constexpr int kM0ReverseBlockNodesNarrow = 2;
 constexpr int kReadoutBlockNodes = 8;  // nodes per block of the readout kernel
 
 struct GemmRows {

@@ -657,6 +657,7 @@ hipError_t m0_forward_launch(const LayerArgs& a, const PolyArgs& p, const NodeBl
                              float* M0, hipStream_t s)
 {
     using P = PolyShape<LIN, LOUT, CORR>;
+    if (nb.block_nodes != kM0BlockNodes) return hipErrorInvalidValue;
     const int threads = node_threads(a.C);
     const size_t shmem = p.num_rem > 0 ? sizeof(float) * P::NIN * threads : 0;
     m0_forward_kernel<P, kM0BlockNodes><<<nb.count, threads, shmem, s>>>(a, p, nb, A0, M0), note_launch();
@@ -670,7 +671,15 @@ hipError_t m0_reverse_launch(const LayerArgs& a, const PolyArgs& p, const NodeBl
     using P = PolyShape<LIN, LOUT, CORR>;
     const int threads = node_threads(a.C);
     const size_t shmem = p.num_rem > 0 ? sizeof(float) * 2 * P::NIN * threads : 0;
-    m0_reverse_kernel<P, kM0BlockNodes><<<nb.count, threads, shmem, s>>>(a, p, nb, A0, M0_adj, A0_adj), note_launch();
+    // the kernel holds as many nodes as the list's largest block
+    if (nb.block_nodes == kM0ReverseBlockNodesNarrow)
+        m0_reverse_kernel<P, kM0ReverseBlockNodesNarrow><<<nb.count, threads, shmem, s>>>(a, p, nb, A0, M0_adj,
+                                                                                          A0_adj), note_launch();
+    else if (nb.block_nodes == kM0BlockNodes)
+        m0_reverse_kernel<P, kM0BlockNodes><<<nb.count, threads, shmem, s>>>(a, p, nb, A0, M0_adj, A0_adj),
+            note_launch();
+    else
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
@@ -678,6 +687,7 @@ template <int LIN, int CORR>
 hipError_t readout_launch(const ReadoutArgs& a, hipStream_t s)
 {
     using P = PolyShape<LIN, 0, CORR>;
+    if (a.nodes.block_nodes != kReadoutBlockNodes) return hipErrorInvalidValue;
     const int threads = std::max(node_threads(a.C), 64);
     const size_t NB = kReadoutBlockNodes;
     size_t floats = 3 * NB * threads + 2 * NB * kMaxHidden;
