@@ -277,6 +277,12 @@ Evaluator::Evaluator(const std::string& model_path, const std::string& head)
         throw std::runtime_error("no HIP device is available");
     }
     hip_check(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "stream create");
+    {
+        int device = 0;
+        hip_check(hipGetDevice(&device), "device query");
+        hip_check(hipDeviceGetAttribute(&compute_units_, hipDeviceAttributeMultiprocessorCount, device),
+                  "compute unit query");
+    }
     C_ = model_.channels;
     nlm_ = model_.num_lm;
     nLM_ = model_.num_LM;
@@ -897,7 +903,17 @@ void Evaluator::plan_node_blocks()
     std::vector<int> order;
     order.reserve(N);
     std::vector<NodeBlock> m0b, m0rb, rob;
-    m0r_block_nodes_ = C_ <= 128 ? kM0ReverseBlockNodesNarrow : kM0BlockNodes;
+    // narrower blocks for the two-wave-per-SIMD node kernels (M0 reverse,
+    // readout) of a launch that would otherwise fill the machine less than
+    // twice over: more workgroups, fewer registers, a shorter last round
+    const long long launch_nodes = std::min(N, T);
+    const int block_waves = (C_ + 63) / 64;  // node kernels: one thread per channel
+    const long long two_rounds = 2LL * 2 * 4 * std::max(compute_units_, 1);  // waves: 2 per SIMD, 4 SIMDs per CU
+    auto narrow = [&](int wide_nodes) {
+        return C_ <= 128 && (launch_nodes + wide_nodes - 1) / wide_nodes * block_waves < two_rounds;
+    };
+    m0r_block_nodes_ = narrow(kM0BlockNodes) ? kM0ReverseBlockNodesNarrow : kM0BlockNodes;
+    readout_block_nodes_ = narrow(kReadoutBlockNodes) ? kReadoutBlockNodesNarrow : kReadoutBlockNodes;
     m0_block_offsets_.assign(tiles + 1, 0);
     m0r_block_offsets_.assign(tiles + 1, 0);
     readout_block_offsets_.assign(tiles + 1, 0);
@@ -913,8 +929,8 @@ void Evaluator::plan_node_blocks()
             for (int b = 0; b < n; b += kM0BlockNodes) m0b.push_back({start + b, std::min(kM0BlockNodes, n - b), a, 0});
             for (int b = 0; b < n; b += m0r_block_nodes_)
                 m0rb.push_back({start + b, std::min(m0r_block_nodes_, n - b), a, 0});
-            for (int b = 0; b < n; b += kReadoutBlockNodes)
-                rob.push_back({start + b, std::min(kReadoutBlockNodes, n - b), a, 0});
+            for (int b = 0; b < n; b += readout_block_nodes_)
+                rob.push_back({start + b, std::min(readout_block_nodes_, n - b), a, 0});
         }
         m0_block_offsets_[t + 1] = static_cast<int>(m0b.size());
         m0r_block_offsets_[t + 1] = static_cast<int>(m0rb.size());
@@ -1724,7 +1740,7 @@ void Evaluator::evaluate()
         mark(kStageA1Gemm, true);
         // readout and its reverse down to A1_adj
         ReadoutArgs ra;
-        ra.nodes = node_blocks(readout_blocks_, readout_block_offsets_, 0, kReadoutBlockNodes);
+        ra.nodes = node_blocks(readout_blocks_, readout_block_offsets_, 0, readout_block_nodes_);
         ra.local_base = 0;
         ra.m0_stride = nodeLM;
         ra.C = C_;
@@ -1974,7 +1990,7 @@ void Evaluator::evaluate_tiled()
         tile(t, false);
         hip_check(launch_r1_forward(la, r1_.as<float>(), cg_.as<float>(), H1, Phi1_.as<float>(), s), "R1 forward");
         gemm_a1(la.node_count, Phi1_.as<float>(), A1_.as<float>(), false, "A1 gemm");
-        ra.nodes = node_blocks(readout_blocks_, readout_block_offsets_, t, kReadoutBlockNodes);
+        ra.nodes = node_blocks(readout_blocks_, readout_block_offsets_, t, readout_block_nodes_);
         ra.local_base = la.local_base;
         hip_check(launch_readout(ra, s), "readout");
         gemm_a1(la.node_count, A1adj_.as<float>(), dPhi1, true, "A1 reverse gemm");

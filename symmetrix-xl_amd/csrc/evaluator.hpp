@@ -424,6 +424,8 @@ private:
     // [tiles + 1] each; the M0 reverse has its own block size (m0r_block_nodes_)
     std::vector<int> m0_block_offsets_, m0r_block_offsets_, readout_block_offsets_;
     int m0r_block_nodes_ = kM0BlockNodes;
+    int readout_block_nodes_ = kReadoutBlockNodes;
+    int compute_units_ = 0;  // of the evaluator's device
 
     bool profiling_ = false;
     unsigned profile_mask_ = 0;

@@ -99,12 +99,17 @@ struct NodeBlocks {
     int block_nodes = 0;  // most nodes in one block of the list
 };
 constexpr int kM0BlockNodes = 4;       // nodes per block of the M0 kernels
-// nodes per block of the M0 reverse at C <= 128: its blocks are two waves of
-// 200 VGPRs, and four nodes per block leave a 5,000-atom launch one and a
-// fraction waves per SIMD (measured: 66 -> 55 us at two nodes per block; at
-// C = 256 two nodes per block were slower)
+// nodes per block of the M0 reverse at C <= 128 when the launch is small:
+// its blocks are two waves of 200 VGPRs, and four nodes per block leave a
+// 5,000-atom launch one and a fraction waves per SIMD (measured: 66 -> 55 us
+// at two nodes per block; 20,000 atoms: unchanged; C = 256: slower)
 constexpr int kM0ReverseBlockNodesNarrow = 2;
 constexpr int kReadoutBlockNodes = 8;  // nodes per block of the readout kernel
+// nodes per readout block at C <= 128 when the launch is small: eight per
+// block leave a 5,000-atom launch 625 workgroups of two waves (measured:
+// 83 -> 77 us at two per block; 20,000 atoms: 242 -> 252 us; C = 256 on
+// water: 0.77 -> 0.97 ms)
+constexpr int kReadoutBlockNodesNarrow = 2;
 
 struct GemmRows {
     const float* ptr = nullptr;

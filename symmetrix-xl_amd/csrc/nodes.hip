@@ -379,7 +379,7 @@ template <class P1, int NB>
 __global__ void __launch_bounds__(256) readout_kernel(ReadoutArgs a)
 {
     constexpr int NIN = P1::NIN;
-    constexpr int G = kReadoutGroup;
+    constexpr int G = NB < kReadoutGroup ? NB : kReadoutGroup;
     static_assert(NB % G == 0, "readout block must hold whole register groups");
     extern __shared__ float s_mem[];
     const int T = blockDim.x;  // >= C, a multiple of 64
@@ -687,12 +687,19 @@ template <int LIN, int CORR>
 hipError_t readout_launch(const ReadoutArgs& a, hipStream_t s)
 {
     using P = PolyShape<LIN, 0, CORR>;
-    if (a.nodes.block_nodes != kReadoutBlockNodes) return hipErrorInvalidValue;
     const int threads = std::max(node_threads(a.C), 64);
-    const size_t NB = kReadoutBlockNodes;
+    const size_t NB = static_cast<size_t>(a.nodes.block_nodes);
     size_t floats = 3 * NB * threads + 2 * NB * kMaxHidden;
     if (a.p1.num_rem > 0) floats += 2 * static_cast<size_t>(P::NIN) * threads;
-    readout_kernel<P, kReadoutBlockNodes><<<a.nodes.count, threads, sizeof(float) * floats, s>>>(a), note_launch();
+    // the kernel holds as many nodes as the list's largest block
+    if (NB == kReadoutBlockNodesNarrow)
+        readout_kernel<P, kReadoutBlockNodesNarrow><<<a.nodes.count, threads, sizeof(float) * floats, s>>>(a),
+            note_launch();
+    else if (NB == kReadoutBlockNodes)
+        readout_kernel<P, kReadoutBlockNodes><<<a.nodes.count, threads, sizeof(float) * floats, s>>>(a),
+            note_launch();
+    else
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
