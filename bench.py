@@ -443,13 +443,15 @@ def main():
 
     for _ in range(args.warmup):
         step()
-    # per-stage device times from an untimed profiled pass; the timed steps
-    # then record events around the dominant stage only
-    ev._set_profiling(True)
+    # per-stage device times: the median over 3 untimed profiled calls (one
+    # call stalled by the system must not pick the dominant stage); the timed
+    # steps then record events around the dominant stage only
+    samples = []
     for _ in range(3):
+        ev._set_profiling(True)
         step()
-    stages = ev._stage_times()
-    stage_avg = {k: (ms / c if c else 0.0) for k, (ms, c) in stages.items()}
+        samples.append({k: (ms / c if c else 0.0) for k, (ms, c) in ev._stage_times().items()})
+    stage_avg = {k: statistics.median(s[k] for s in samples) for k in samples[0]}
     dominant = max(stage_avg, key=stage_avg.get)
     ev._set_profiling(True, stages=[dominant])
     hip.synchronize()
@@ -622,7 +624,7 @@ def main():
         "md_nve": md,
         "parity": parity,
         "stage_ms": {k: round(v, 4) for k, v in stage_avg.items()},
-        "stage_ms_source": "HIP events around every stage, 3 untimed calls after the warmup",
+        "stage_ms_source": "HIP events around every stage, median of 3 untimed calls after the warmup",
         "essential_gflop_per_call": round(total_flops / 1e9, 3),
         "neighbor_rebuilds_timed": rebuilds,
         "roofline": roofline,
