@@ -103,6 +103,9 @@ int sxl_create(const char* model_path, const char* head, sxl_evaluator** out)
         }
         auto ev = std::make_unique<sxl_evaluator>(model_path, head);
         const std::scoped_lock lock(g_runtime_mutex);
+        // a finalization that ran while this evaluator was being built wins
+        if (g_runtime_finalized)
+            throw std::runtime_error("Cannot construct a Symmetrix evaluator after Kokkos finalization.");
         g_runtime_initialized = true;
         g_live_evaluators += 1;
         *out = ev.release();
