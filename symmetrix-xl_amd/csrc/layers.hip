@@ -23,6 +23,7 @@
 #include "device_math.hpp"
 #include "kernels.hpp"
 #include "r1_shapes.inc"
+#include "sh_grad.inc"
 
 namespace sxl {
 namespace {
@@ -1036,8 +1037,8 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
     constexpr int NLM = (LMAX + 1) * (LMAX + 1);
     constexpr int NL = LMAX + 1;
     __shared__ float s_Y[kTile][NLM];
-    __shared__ float s_dY[kTile][3][NLM];
     __shared__ float s_geo[kTile][4];
+    __shared__ float s_ir[kTile];  // 1 / r
     __shared__ int s_row[kTile];
     __shared__ int s_eid[kTile];
     __shared__ float s_f[kTile][kMaxWaves * kForcePartsA0][3];
@@ -1087,6 +1088,21 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
 #pragma unroll
         for (int lm = 0; lm < NLM; ++lm) adj[lm] /= sc;
     }
+    // the adjoint contracted with the harmonic gradients, once per receiver:
+    // sum_m adj[l, m] dP_lm/dr_k = sum_m' B[k][l - 1][m'] P_{l-1, m'}
+    float B[3][LMAX][2 * LMAX - 1];
+#pragma unroll
+    for (int d = 0; d < 3; ++d)
+#pragma unroll
+        for (int l = 1; l <= LMAX; ++l)
+#pragma unroll
+            for (int mp = 0; mp < 2 * l - 1; ++mp) {
+                float v = 0.0f;
+#pragma unroll
+                for (int m = 0; m < 2 * l + 1; ++m)
+                    if (kShGrad[d][l * l + m][mp] != 0.0f) v = fmaf(kShGrad[d][l * l + m][mp], adj[l * l + m], v);
+                B[d][l - 1][mp] = v;
+            }
     for (int base = e0; base < e1; base += kTile) {
         __syncthreads();
         if (threadIdx.x < 64) {
@@ -1097,9 +1113,10 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
             const int e = base + t;
             if (ts.active) {
                 const int sl = ts.slot;
-                edge_harmonics<LMAX, true>(g.xyz + 3 * static_cast<size_t>(e - g.edge_base), rr, s_Y[sl], s_dY[sl][0],
-                                           s_dY[sl][1], s_dY[sl][2], s_geo[sl]);
+                edge_harmonics<LMAX, false>(g.xyz + 3 * static_cast<size_t>(e - g.edge_base), rr, s_Y[sl], nullptr,
+                                            nullptr, nullptr, s_geo[sl]);
                 s_geo[sl][3] = ts.x;
+                s_ir[sl] = static_cast<float>(1.0 / rr);
                 s_row[sl] = ts.row;
                 s_eid[sl] = e;
                 s_dsc[sl] = a.d0.table ? dcoef * density_slope(a.d0.table, a.grid, g.edge_pair[e - g.edge_base] >> 16, rr) : 0.0f;
@@ -1120,28 +1137,42 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
 #pragma unroll
             for (int l = 0; l < NL; ++l) c[l] = load4(rs, voff, l * C * 16);
         };
+        // with P_lm(r) = r^l Y_lm, d/dr [R_l Y_lm] = r_hat (R_l' - l R_l / r) Y_lm
+        // + (R_l / r) sum_m' c_lm,m' Y_{l-1, m'}: the edge force is
+        // r_hat A + g with A = sum_l (R_l' - l R_l / r) sum_m adj Y and
+        // g_k = sum_l (R_l / r) sum_m' B[k][l - 1][m'] Y_{l-1, m'}
         auto edge_force = [&](int j, const float4v* cl) {
             const float x = uniform(s_geo[j][3]);
-            float yl[NL], ax[NL], ay[NL], az[NL];
+            const float ir = uniform(s_ir[j]);
+            float Y[NLM], yl[NL];
 #pragma unroll
-            for (int l = 0; l < NL; ++l) yl[l] = ax[l] = ay[l] = az[l] = 0.0f;
+            for (int lm = 0; lm < NLM; ++lm) Y[lm] = s_Y[j][lm];
 #pragma unroll
-            for (int lm = 0; lm < NLM; ++lm) {
-                const int l = kLmL[lm];
-                yl[l] = fmaf(s_Y[j][lm], adj[lm], yl[l]);
-                ax[l] = fmaf(s_dY[j][0][lm], adj[lm], ax[l]);
-                ay[l] = fmaf(s_dY[j][1][lm], adj[lm], ay[l]);
-                az[l] = fmaf(s_dY[j][2][lm], adj[lm], az[l]);
-            }
+            for (int l = 0; l < NL; ++l) yl[l] = 0.0f;
+#pragma unroll
+            for (int lm = 0; lm < NLM; ++lm) yl[kLmL[lm]] = fmaf(Y[lm], adj[lm], yl[kLmL[lm]]);
             float A = 0.0f, gx = 0.0f, gy = 0.0f, gz = 0.0f;
 #pragma unroll
             for (int l = 0; l < NL; ++l) {
                 float R, dR;
                 cubic_value_slope(cl[l], x, R, dR);
-                A = fmaf(dR, yl[l], A);
-                gx = fmaf(R, ax[l], gx);
-                gy = fmaf(R, ay[l], gy);
-                gz = fmaf(R, az[l], gz);
+                if (l == 0) {
+                    A = fmaf(dR, yl[0], A);
+                } else {
+                    A = fmaf(fmaf(-static_cast<float>(l) * ir, R, dR), yl[l], A);
+                    float ix = 0.0f, iy = 0.0f, iz = 0.0f;
+#pragma unroll
+                    for (int mp = 0; mp < 2 * l - 1; ++mp) {
+                        const float y = Y[(l - 1) * (l - 1) + mp];
+                        ix = fmaf(y, B[0][l - 1][mp], ix);
+                        iy = fmaf(y, B[1][l - 1][mp], iy);
+                        iz = fmaf(y, B[2][l - 1][mp], iz);
+                    }
+                    const float h = R * ir;
+                    gx = fmaf(h, ix, gx);
+                    gy = fmaf(h, iy, gy);
+                    gz = fmaf(h, iz, gz);
+                }
             }
             const float fx = partial_sum_dpp<kForcePartsA0>(fmaf(s_geo[j][0], A, gx));
             const float fy = partial_sum_dpp<kForcePartsA0>(fmaf(s_geo[j][1], A, gy));
