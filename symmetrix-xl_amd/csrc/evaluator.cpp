@@ -246,6 +246,29 @@ void DeviceBuffer::reserve(std::size_t bytes)
     ++thread_counters().allocations;
 }
 
+PinnedBuffer::~PinnedBuffer()
+{
+    if (ptr_) (void)hipHostFree(ptr_);
+}
+
+void PinnedBuffer::reserve(std::size_t bytes)
+{
+    if (bytes <= bytes_) return;
+    if (ptr_) (void)hipHostFree(ptr_);
+    ptr_ = nullptr;
+    bytes_ = 0;
+    void* p = nullptr;
+    const hipError_t err = hipHostMalloc(&p, bytes, hipHostMallocDefault);
+    if (err != hipSuccess) {
+        (void)hipGetLastError();
+        throw std::runtime_error("pinned host allocation of " + std::to_string(bytes) +
+                                 " bytes failed: " + hipGetErrorString(err));
+    }
+    ptr_ = p;
+    bytes_ = bytes;
+    ++thread_counters().allocations;
+}
+
 void Evaluator::account_preparation(const CallStart& start)
 {
     stats_.preparation_fences += static_cast<long long>(thread_counters().fences - start.counters.fences);
@@ -1491,10 +1514,22 @@ void Evaluator::compute_positions(std::uint64_t generation, const double* positi
     const CallStart start;
     require_geometry(generation);
     const int N = num_nodes_;
-    if (N > 0 && positions != positions_.as<double>())
-        hip_check(hipMemcpyAsync(positions_.as<double>(), positions, N * 3 * sizeof(double),
-                                 device_positions ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, stream_),
-                  "positions");
+    if (N > 0 && positions != positions_.as<double>()) {
+        const std::size_t bytes = static_cast<std::size_t>(N) * 3 * sizeof(double);
+        if (device_positions) {
+            hip_check(hipMemcpyAsync(positions_.as<double>(), positions, bytes, hipMemcpyDeviceToDevice, stream_),
+                      "positions");
+        } else {
+            // through pinned memory: the copy is DMA queued with the kernels
+            // (the previous evaluation's wait has drained the buffer)
+            pinned_positions_.reserve(bytes);
+            std::memcpy(pinned_positions_.as<double>(), positions, bytes);
+            hip_check(hipMemcpyAsync(positions_.as<double>(), pinned_positions_.as<double>(), bytes,
+                                     hipMemcpyHostToDevice, stream_),
+                      "positions");
+        }
+    }
+    results_to_host_ = !device_positions;
     for (int i = 0; i < kNumStages; ++i) stage_used_[i] = false;
     mark(kStageGeometry, false);
     const double* cell = cell_dev_.as<double>();
@@ -2109,6 +2144,7 @@ int Evaluator::md_nve(int num_atoms, const int* node_types, const double* masses
 // mace_kokkos_factorized_lifecycle.cpp:3078-3085).
 void Evaluator::finish_evaluation()
 {
+    host_results_ = false;
     invalid_edges_ = 0;
     fused_volume_ = 0.0;
     last_from_positions_ = check_geometry_;
@@ -2141,6 +2177,19 @@ void Evaluator::finish_evaluation()
                                  stream_),
                   "totals copy");
     }
+    const bool to_host = results_to_host_ && num_nodes_ > 0;
+    if (to_host) {
+        const std::size_t n = static_cast<std::size_t>(num_nodes_);
+        pinned_energies_.reserve(n * sizeof(double));
+        pinned_forces_.reserve(n * 3 * sizeof(double));
+        hip_check(hipMemcpyAsync(pinned_energies_.as<double>(), energies_.as<double>(), n * sizeof(double),
+                                 hipMemcpyDeviceToHost, stream_),
+                  "energies copy");
+        hip_check(hipMemcpyAsync(pinned_forces_.as<double>(), atom_forces_.as<double>(), n * 3 * sizeof(double),
+                                 hipMemcpyDeviceToHost, stream_),
+                  "forces copy");
+    }
+    results_to_host_ = false;
     wait("evaluation");
     if (tiled) {
         for (int q = 0; q < 9; ++q) host_virial_[q] = host_totals_[17 + q];
@@ -2155,6 +2204,7 @@ void Evaluator::finish_evaluation()
         evaluated_generation_ = 0;
         throw std::invalid_argument("Execution R1 prepared positions produced an invalid edge geometry.");
     }
+    host_results_ = to_host;
 }
 
 // Tiled plan: stress = (-sum_e f_e (x) xyz_e) / V on the host, also written
@@ -2210,6 +2260,10 @@ void Evaluator::synchronize() const { hip_check(host_fence(stream_), "synchroniz
 void Evaluator::node_energies(double* out) const
 {
     if (evaluated_generation_ != generation_) throw std::invalid_argument("no completed evaluation");
+    if (host_results_) {
+        std::memcpy(out, pinned_energies_.as<double>(), static_cast<std::size_t>(num_nodes_) * sizeof(double));
+        return;
+    }
     if (num_nodes_ > 0)
         hip_check(hipMemcpyAsync(out, energies_.as<double>(), num_nodes_ * sizeof(double), hipMemcpyDeviceToHost,
                                  stream_),
@@ -2236,6 +2290,10 @@ void Evaluator::atom_forces(std::uint64_t generation, double* out)
     check_generation(generation);
     if (evaluated_generation_ != generation_)
         throw std::invalid_argument("Atom-force reduction requires the current completed graph.");
+    if (host_results_) {
+        std::memcpy(out, pinned_forces_.as<double>(), static_cast<std::size_t>(num_nodes_) * 3 * sizeof(double));
+        return;
+    }
     if (num_nodes_ > 0)
         hip_check(hipMemcpyAsync(out, atom_forces_.as<double>(), num_nodes_ * 3 * sizeof(double),
                                  hipMemcpyDeviceToHost, stream_),

@@ -46,6 +46,23 @@ private:
     std::size_t bytes_ = 0;
 };
 
+// Pinned (page-locked) host memory, grow-only: copies between it and the
+// device are asynchronous DMA.
+class PinnedBuffer {
+public:
+    PinnedBuffer() = default;
+    PinnedBuffer(const PinnedBuffer&) = delete;
+    PinnedBuffer& operator=(const PinnedBuffer&) = delete;
+    ~PinnedBuffer();
+    void reserve(std::size_t bytes);  // grow-only
+    template <class T>
+    T* as() const { return static_cast<T*>(ptr_); }
+
+private:
+    void* ptr_ = nullptr;
+    std::size_t bytes_ = 0;
+};
+
 // Periodic neighbour graph on the device (reference
 // build_periodic_neighbor_graph_kokkos, neighbor_graph_kokkos.cpp:38-405).
 struct PeriodicGraph {
@@ -387,6 +404,13 @@ private:
     // [13] invalid-edge count; an evaluation from positions reduces energy and
     // stress (cell volume) in the same pass and fills it with one copy
     double host_totals_[32] = {};
+    // an evaluation from host positions also copies the node energies and
+    // atom forces to pinned host memory before its one wait, so reading them
+    // afterwards needs no device access (host_results_: they belong to the
+    // current evaluation)
+    PinnedBuffer pinned_positions_, pinned_energies_, pinned_forces_;
+    bool results_to_host_ = false;
+    bool host_results_ = false;
     void set_stress_from_virial(double volume);
     double fused_volume_ = 0.0;
     bool last_from_positions_ = false;

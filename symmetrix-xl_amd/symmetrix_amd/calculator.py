@@ -45,11 +45,16 @@ def topology_valid(cell, topology_cell, max_non_affine, cutoff, skin):
     at most ``max_non_affine`` (reference calculator.py:2872-2877): a pair
     within cutoff now was within contraction * (cutoff + 2 max_non_affine) in
     the build's cell, contraction = ||cell^-1 topology_cell||_2."""
-    try:
-        deformation = np.linalg.solve(np.asarray(cell, dtype=float), np.asarray(topology_cell, dtype=float))
-    except np.linalg.LinAlgError:
-        return False
-    contraction = float(np.linalg.norm(deformation, ord=2))
+    cell = np.asarray(cell, dtype=float)
+    topology_cell = np.asarray(topology_cell, dtype=float)
+    if np.array_equal(cell, topology_cell):
+        contraction = 1.0  # the identity deformation (the common case: no cell change)
+    else:
+        try:
+            deformation = np.linalg.solve(cell, topology_cell)
+        except np.linalg.LinAlgError:
+            return False
+        contraction = float(np.linalg.norm(deformation, ord=2))
     if not np.isfinite(contraction) or not np.isfinite(max_non_affine):
         return False
     return contraction * (cutoff + 2.0 * max_non_affine) <= cutoff + skin
