@@ -578,6 +578,42 @@ struct RevTrRanges {
 template <class RG>
 inline constexpr RevTrRanges<RG> kRevTrRanges{};
 
+// The harmonic part of a layer-1 edge force, g = sum_lm U_lm dY_lm/dr, is
+// tangential: Y_lm depends on the direction r_hat only, so r_hat . dY_lm/dr
+// = 0 for every lm.  Two Cartesian components therefore fix g.  The staging
+// keeps the gradient rows of the two axes other than `drop`, the axis where
+// |r_hat| is largest (|r_hat_drop| >= 1/sqrt(3)); the channels reduce only
+// those two components; the edge's thread forms the third as
+// -(r_a g_a + r_b g_b) / r_drop.  Rows of l = 0 are zero and left out: a
+// staged row holds lm = 1 .. NLM - 1 at index lm - 1 (16-byte aligned reads).
+template <int NLM>
+__device__ __forceinline__ void stage_tangent_rows(const float (&dY)[3][NLM], const float* u, float* row_a,
+                                                   float* row_b, int& drop)
+{
+    const float ax = fabsf(u[0]), ay = fabsf(u[1]), az = fabsf(u[2]);
+    drop = (az >= ax && az >= ay) ? 2 : (ay >= ax ? 1 : 0);
+#pragma unroll
+    for (int lm = 1; lm < NLM; ++lm) {
+        row_a[lm - 1] = drop == 0 ? dY[1][lm] : dY[0][lm];
+        row_b[lm - 1] = drop == 2 ? dY[1][lm] : dY[2][lm];
+    }
+}
+
+// +dE/dr of an edge from the channel sums of the radial coefficient A and of
+// the two kept harmonic components (ga on the lower kept axis, gb on the upper).
+__device__ __forceinline__ void tangent_force(double A, double ga, double gb, int drop, const float* u,
+                                              double (&f)[3])
+{
+    const double ux = u[0], uy = u[1], uz = u[2];
+    const double ua = drop == 0 ? uy : ux;
+    const double ub = drop == 2 ? uy : uz;
+    const double ud = drop == 0 ? ux : (drop == 1 ? uy : uz);
+    const double gd = -(ua * ga + ub * gb) / ud;
+    f[0] = fma(ux, A, drop == 0 ? gd : ga);
+    f[1] = fma(uy, A, drop == 0 ? ga : (drop == 1 ? gd : gb));
+    f[2] = fma(uz, A, drop == 2 ? gd : gb);
+}
+
 // ---------------------------------------------------------------------------
 // Layer 1 reverse.  Per receiver and channel, the CG contraction of dPhi1 is
 // taken once: G[p, lm2, lm1] = sum_{t in (p, lm2, lm1)} cg_t dPhi1[lme_t].
@@ -586,9 +622,11 @@ inline constexpr RevTrRanges<RG> kRevTrRanges{};
 //   msg[lm2]  = sum_p R_p s[p,lm2]                   -> H1 adjoint of the source
 //   A         = sum_p R'_p sum_lm2 H[lm2] s[p,lm2]
 //   U[lm1]    = sum_{p,lm2} R_p H[lm2] G[p,lm2,lm1]
-//   f_edge    = -sum_k (r_hat A + sum_lm1 dY[lm1] U[lm1])
-// When G does not fit the register budget (many triples) the terms are
-// contracted per edge instead, with dPhi1 in registers.
+//   f_edge    = -(r_hat A + sum_lm1 dY[lm1] U[lm1])
+// with the harmonic term reduced as two tangential components
+// (stage_tangent_rows).  When G does not fit the register budget (many
+// triples) the terms are contracted per edge instead, with dPhi1 in
+// registers.
 // ---------------------------------------------------------------------------
 template <class S>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S::NTR <= 40 ? 3 : 1)))
@@ -608,7 +646,8 @@ r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
     constexpr int NG = kFactored ? S::NTR : S::NLME;
     constexpr int NCGY = kFactored ? 1 : (NT + 3) / 4 * 4;
     __shared__ float s_Y[kTile][NLM];
-    __shared__ float s_dY[kTile][3][NLM];
+    __shared__ float s_dT[kTile][2][(NLM + 2) / 4 * 4];  // the two kept gradient rows (stage_tangent_rows)
+    __shared__ int s_drop[kTile];
     __shared__ float s_geo[kTile][4];  // r_hat, local spline coordinate
     __shared__ float s_cgY[kTile][NCGY];
     __shared__ int s_row[kTile];
@@ -658,8 +697,13 @@ r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
             const int e = base + t;
             if (ts.active) {
                 const int sl = ts.slot;
-                edge_harmonics<S::LMAX, true>(g.xyz + 3 * static_cast<size_t>(e - g.edge_base), rr, s_Y[sl], s_dY[sl][0],
-                                              s_dY[sl][1], s_dY[sl][2], s_geo[sl]);
+                float dY[3][NLM], u[3];
+                edge_harmonics<S::LMAX, true>(g.xyz + 3 * static_cast<size_t>(e - g.edge_base), rr, s_Y[sl], dY[0],
+                                              dY[1], dY[2], u);
+                stage_tangent_rows<NLM>(dY, u, s_dT[sl][0], s_dT[sl][1], s_drop[sl]);
+                s_geo[sl][0] = u[0];
+                s_geo[sl][1] = u[1];
+                s_geo[sl][2] = u[2];
                 s_geo[sl][3] = ts.x;
                 s_row[sl] = ts.row;
                 s_src[sl] = g.source[e];
@@ -743,22 +787,21 @@ r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
 #pragma unroll
                 for (int q = 0; q < NLMS; ++q) store1(m[q], ms, k * 4, q * C * 4);
             }
-            float gx = 0.0f, gy = 0.0f, gz = 0.0f;
+            float ga = 0.0f, gb = 0.0f;
 #pragma unroll
-            for (int lm = 0; lm < NLM; ++lm) {
-                gx = fmaf(s_dY[j][0][lm], U[lm], gx);
-                gy = fmaf(s_dY[j][1][lm], U[lm], gy);
-                gz = fmaf(s_dY[j][2][lm], U[lm], gz);
+            for (int lm = 1; lm < NLM; ++lm) {
+                ga = fmaf(s_dT[j][0][lm - 1], U[lm], ga);
+                gb = fmaf(s_dT[j][1][lm - 1], U[lm], gb);
             }
-            // partial sums of +dE/dxyz; the edge's thread negates their total
-            const float fx = partial_sum_dpp<kForceParts>(fmaf(s_geo[j][0], A, gx));
-            const float fy = partial_sum_dpp<kForceParts>(fmaf(s_geo[j][1], A, gy));
-            const float fz = partial_sum_dpp<kForceParts>(fmaf(s_geo[j][2], A, gz));
+            // partial sums of A and of the two kept harmonic components
+            const float pA = partial_sum_dpp<kForceParts>(A);
+            const float pa = partial_sum_dpp<kForceParts>(ga);
+            const float pb = partial_sum_dpp<kForceParts>(gb);
             if (holds_partial<kForceParts>(lane)) {
                 const int part = wave * kForceParts + lane / (64 / kForceParts);
-                s_f[j][part][0] = fx;
-                s_f[j][part][1] = fy;
-                s_f[j][part][2] = fz;
+                s_f[j][part][0] = pA;
+                s_f[j][part][1] = pa;
+                s_f[j][part][2] = pb;
             }
         };
         // Two row buffers used in turn (unrolled by two, so no register
@@ -779,9 +822,11 @@ r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
         __syncthreads();
         if (threadIdx.x < count) {
             const int t = threadIdx.x;
-            double f[3] = {0.0, 0.0, 0.0};
+            double p[3] = {0.0, 0.0, 0.0};
             for (int w = 0; w < nwaves * kForceParts; ++w)
-                for (int c = 0; c < 3; ++c) f[c] += static_cast<double>(s_f[t][w][c]);
+                for (int c = 0; c < 3; ++c) p[c] += static_cast<double>(s_f[t][w][c]);
+            double f[3];
+            tangent_force(p[0], p[1], p[2], s_drop[t], s_geo[t], f);
             double* out = forces + 3 * static_cast<size_t>(s_eid[t] - g.edge_base);
 #pragma unroll
             for (int c = 0; c < 3; ++c) out[c] = -f[c] + static_cast<double>(s_dsc[t] * s_geo[t][c]);
@@ -800,9 +845,10 @@ template <class S, int G>
 using RevGroup = R1RevGroup<S::LMAX, S::LLMAX, G>;
 
 template <int MAXT>
-struct RevTileLds {
+struct alignas(16) RevTileLds {
     float Y[kTile][16];
-    float dY[kTile][3][16];
+    float dT[kTile][2][16];  // the two kept gradient rows (stage_tangent_rows)
+    int drop[kTile];
     float geo[kTile][4];  // r_hat, local spline coordinate
     float cgY[kTile][MAXT];
     int row[kTile];
@@ -938,21 +984,21 @@ __device__ __forceinline__ void r1_reverse_pass(const LayerArgs& a, int i, bool 
 #pragma unroll
             for (int q = 0; q < RG::NH; ++q) store1(m[q], ms, k * 4, RG::h_lm2[q] * C * 4);
         }
-        float gx = 0.0f, gy = 0.0f, gz = 0.0f;
+        float ga = 0.0f, gb = 0.0f;
 #pragma unroll
-        for (int lm = 0; lm < NLM; ++lm) {
-            gx = fmaf(L.dY[j][0][lm], U[lm], gx);
-            gy = fmaf(L.dY[j][1][lm], U[lm], gy);
-            gz = fmaf(L.dY[j][2][lm], U[lm], gz);
+        for (int lm = 1; lm < NLM; ++lm) {
+            ga = fmaf(L.dT[j][0][lm - 1], U[lm], ga);
+            gb = fmaf(L.dT[j][1][lm - 1], U[lm], gb);
         }
-        const float fx = partial_sum_dpp<kForcePartsGrouped>(fmaf(L.geo[j][0], A, gx));
-        const float fy = partial_sum_dpp<kForcePartsGrouped>(fmaf(L.geo[j][1], A, gy));
-        const float fz = partial_sum_dpp<kForcePartsGrouped>(fmaf(L.geo[j][2], A, gz));
+        // partial sums of A and of the two kept harmonic components
+        const float pA = partial_sum_dpp<kForcePartsGrouped>(A);
+        const float pa = partial_sum_dpp<kForcePartsGrouped>(ga);
+        const float pb = partial_sum_dpp<kForcePartsGrouped>(gb);
         if (holds_partial<kForcePartsGrouped>(lane)) {
             const int part = wave * kForcePartsGrouped + lane / (64 / kForcePartsGrouped);
-            L.f[j][part][0] = first ? fx : L.f[j][part][0] + fx;
-            L.f[j][part][1] = first ? fy : L.f[j][part][1] + fy;
-            L.f[j][part][2] = first ? fz : L.f[j][part][2] + fz;
+            L.f[j][part][0] = first ? pA : L.f[j][part][0] + pA;
+            L.f[j][part][1] = first ? pa : L.f[j][part][1] + pa;
+            L.f[j][part][2] = first ? pb : L.f[j][part][2] + pb;
         }
     }
 }
@@ -991,8 +1037,14 @@ __global__ void __launch_bounds__(256) r1_reverse_grouped_kernel(LayerArgs a, co
             const int e = base + t;
             if (ts.active) {
                 const int sl = ts.slot;
-                edge_harmonics<S::LMAX, true>(g.xyz + 3 * static_cast<size_t>(e - g.edge_base), rr, L.Y[sl], L.dY[sl][0],
-                                              L.dY[sl][1], L.dY[sl][2], L.geo[sl]);
+                constexpr int NLM = (S::LMAX + 1) * (S::LMAX + 1);
+                float dY[3][NLM], u[3];
+                edge_harmonics<S::LMAX, true>(g.xyz + 3 * static_cast<size_t>(e - g.edge_base), rr, L.Y[sl], dY[0],
+                                              dY[1], dY[2], u);
+                stage_tangent_rows<NLM>(dY, u, L.dT[sl][0], L.dT[sl][1], L.drop[sl]);
+                L.geo[sl][0] = u[0];
+                L.geo[sl][1] = u[1];
+                L.geo[sl][2] = u[2];
                 L.geo[sl][3] = ts.x;
                 L.row[sl] = ts.row;
                 L.src[sl] = g.source[e];
@@ -1015,9 +1067,11 @@ __global__ void __launch_bounds__(256) r1_reverse_grouped_kernel(LayerArgs a, co
         __syncthreads();
         if (threadIdx.x < count) {
             const int t = threadIdx.x;
-            double f[3] = {0.0, 0.0, 0.0};
+            double p[3] = {0.0, 0.0, 0.0};
             for (int w = 0; w < nwaves * kForcePartsGrouped; ++w)
-                for (int c = 0; c < 3; ++c) f[c] += static_cast<double>(L.f[t][w][c]);
+                for (int c = 0; c < 3; ++c) p[c] += static_cast<double>(L.f[t][w][c]);
+            double f[3];
+            tangent_force(p[0], p[1], p[2], L.drop[t], L.geo[t], f);
             double* out = forces + 3 * static_cast<size_t>(L.eid[t] - g.edge_base);
 #pragma unroll
             for (int c = 0; c < 3; ++c) out[c] = -f[c] + static_cast<double>(L.dsc[t] * L.geo[t][c]);
