@@ -405,6 +405,14 @@ __device__ __forceinline__ void r1_forward_slots(const float4v (*s_W)[(S::NPL + 
         float RH[NPQ];
 #pragma unroll
         for (int pq = 0; pq < NPQ; ++pq) RH[pq] = cubic(c[S::pq_p[pq]], x) * H[S::pq_lm2[pq]];
+        if constexpr (S::NP <= kRowReusePaths) {
+            // RH is formed here, before the conditional refill: left to the
+            // compiler, the radial values sink below the branch, the refill
+            // then needs a second row buffer and every edge pays a register
+            // copy of the row at the loop latch
+#pragma unroll
+            for (int pq = 0; pq < NPQ; ++pq) asm volatile("" : : "v"(RH[pq]));
+        }
         const int jn = min(j + 1, hi - 1);
         // (the wide shapes' row registers leave no room for the branch: they
         // reload, an L1 hit)
