@@ -226,6 +226,54 @@ __device__ __forceinline__ bool holds_partial(int lane)
     return (lane & (64 / PARTS - 1)) == 64 / PARTS - 1;
 }
 
+// Wave sums of twelve values, f[c][d] = component c of item d, in 30 VALU
+// operations instead of 4-5 DPP steps per value.  v_permlane32_swap
+// exchanges the upper half of one register with the lower half of another,
+// so adding the pair sums each value over the two lane halves while the
+// halves take different values; v_permlane16_swap does the same for the odd
+// and even 16-lane rows.  After the two exchanges row r of out[c] holds
+// item r's component c summed over lanes congruent mod 16, and a row
+// reduction leaves item r's three wave sums in lane 16 r + 15.  The values
+// enter in the order v[4c + s(d)], s = (0, 2, 1, 3), which the row exchange
+// undoes.  Fixed combination order: run-to-run identical.
+//
+// Both results of a swap pass through an empty asm statement before they are
+// read as floats: this compiler (ROCm 7.2 clang) otherwise folds the float
+// view of the second result into the first and adds the first to itself.
+__device__ __forceinline__ float swap_pair_sum(unsigned lo, unsigned hi)
+{
+    asm volatile("" : "+v"(lo), "+v"(hi));
+    return __builtin_bit_cast(float, lo) + __builtin_bit_cast(float, hi);
+}
+
+__device__ __forceinline__ void wave_sum_3x4(const float (&f)[3][4], float (&out)[3])
+{
+    constexpr int s[4] = {0, 2, 1, 3};
+    float v[12];
+#pragma unroll
+    for (int c = 0; c < 3; ++c)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) v[4 * c + s[d]] = f[c][d];
+    float w[6];
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+        const auto x = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v[2 * i]),
+                                                        __builtin_bit_cast(unsigned, v[2 * i + 1]), false, false);
+        w[i] = swap_pair_sum(x[0], x[1]);
+    }
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        const auto x = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, w[2 * c]),
+                                                        __builtin_bit_cast(unsigned, w[2 * c + 1]), false, false);
+        float u = swap_pair_sum(x[0], x[1]);
+        u += dpp_moved<0xb1>(u);   // quad_perm [1,0,3,2]
+        u += dpp_moved<0x4e>(u);   // quad_perm [2,3,0,1]
+        u += dpp_moved<0x141>(u);  // row_half_mirror
+        u += dpp_moved<0x140>(u);  // row_mirror
+        out[c] = u;
+    }
+}
+
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 __device__ __forceinline__ float uniform(float v)
 {

@@ -30,10 +30,8 @@ namespace {
 
 constexpr int kMaxWaves = 4;  // 256 threads
 // partial sums per wave of an edge force component, stored in LDS and added
-// in double by the edge's thread (fewer DPP steps than a full reduction; the
-// layer-0 reverse keeps two to fit three workgroups' LDS per CU at 3 waves)
+// in double by the edge's thread (fewer DPP steps than a full reduction)
 constexpr int kForceParts = 4;
-constexpr int kForcePartsA0 = 2;
 // the path-group passes add into their partials once per pass: one per wave
 // (measured: four per wave made the wide shape's reverse 1 % slower)
 constexpr int kForcePartsGrouped = 1;
@@ -87,6 +85,37 @@ __device__ __forceinline__ void stream_ring(int count, Buf (&ring)[D], Fetch& fe
 }
 
 constexpr int kDepth = 4;  // edges in flight per wave in the layer-0 kernels
+
+// stream_ring (D = 4) for edge functions that yield three force components
+// per lane: use(j, buf, f0, f1, f2).  The components of each group of four
+// consecutive slots are summed over the wave together (wave_sum_3x4), and
+// lane 16 r + 15 passes slot j + r's three sums to store(j + r, sums).
+template <class Buf, class Fetch, class Use, class Store>
+__device__ __forceinline__ void stream_ring_sum3(int count, Buf (&ring)[4], Fetch& fetch, Use& use, Store& store)
+{
+    constexpr int D = 4;
+    const int r = (threadIdx.x & 63) >> 4;
+    const bool holder = (threadIdx.x & 15) == 15;
+#pragma unroll
+    for (int d = 0; d < D - 1; ++d)
+        if (d < count) fetch(d, ring[d]);
+    for (int j = 0; j < count; j += D) {
+        float f[3][D];
+#pragma unroll
+        for (int d = 0; d < D; ++d) f[0][d] = f[1][d] = f[2][d] = 0.0f;
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            const int jj = j + d;
+            if (jj < count) {
+                if (jj + D - 1 < count) fetch(jj + D - 1, ring[(d + D - 1) % D]);
+                use(jj, ring[d], f[0][d], f[1][d], f[2][d]);
+            }
+        }
+        float sums[3];
+        wave_sum_3x4(f, sums);
+        if (holder && j + r < count) store(j + r, sums);
+    }
+}
 
 struct TileSlot {
     bool active;
@@ -1091,7 +1120,7 @@ __global__ void __launch_bounds__(256) r1_reverse_grouped_kernel(LayerArgs a, co
 // Layer 0 reverse: f_ij += -sum_{lm,k} A0_adj[i,lm,k] (r_hat R0f' Y_lm + R0f dY_lm)
 // ---------------------------------------------------------------------------
 template <int LMAX>
-__global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const float* __restrict__ r0f,
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) a0_reverse_kernel(LayerArgs a, const float* __restrict__ r0f,
                                                           const float* __restrict__ A0,
                                                           const float* __restrict__ A0_adj,
                                                           double* __restrict__ forces)
@@ -1103,7 +1132,7 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
     __shared__ float s_ir[kTile];  // 1 / r
     __shared__ int s_row[kTile];
     __shared__ int s_eid[kTile];
-    __shared__ float s_f[kTile][kMaxWaves * kForcePartsA0][3];
+    __shared__ float s_f[kTile][kMaxWaves][3];  // wave sums (stream_ring_sum3)
     __shared__ float s_dsc[kTile];  // A0 density-scale force coefficient per active slot
     __shared__ int s_count;
 
@@ -1203,7 +1232,7 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
         // + (R_l / r) sum_m' c_lm,m' Y_{l-1, m'}: the edge force is
         // r_hat A + g with A = sum_l (R_l' - l R_l / r) sum_m adj Y and
         // g_k = sum_l (R_l / r) sum_m' B[k][l - 1][m'] Y_{l-1, m'}
-        auto edge_force = [&](int j, const float4v* cl) {
+        auto edge_force = [&](int j, const float4v* cl, float& fx, float& fy, float& fz) {
             const float x = uniform(s_geo[j][3]);
             const float ir = uniform(s_ir[j]);
             float Y[NLM], yl[NL];
@@ -1236,23 +1265,22 @@ __global__ void __launch_bounds__(256) a0_reverse_kernel(LayerArgs a, const floa
                     gz = fmaf(h, iz, gz);
                 }
             }
-            const float fx = partial_sum_dpp<kForcePartsA0>(fmaf(s_geo[j][0], A, gx));
-            const float fy = partial_sum_dpp<kForcePartsA0>(fmaf(s_geo[j][1], A, gy));
-            const float fz = partial_sum_dpp<kForcePartsA0>(fmaf(s_geo[j][2], A, gz));
-            if (holds_partial<kForcePartsA0>(lane)) {
-                const int part = wave * kForcePartsA0 + lane / (64 / kForcePartsA0);
-                s_f[j][part][0] = fx;
-                s_f[j][part][1] = fy;
-                s_f[j][part][2] = fz;
-            }
+            fx = fmaf(s_geo[j][0], A, gx);
+            fy = fmaf(s_geo[j][1], A, gy);
+            fz = fmaf(s_geo[j][2], A, gz);
+        };
+        auto store = [&](int j, const float (&sums)[3]) {
+            s_f[j][wave][0] = sums[0];
+            s_f[j][wave][1] = sums[1];
+            s_f[j][wave][2] = sums[2];
         };
         float4v ring[kDepth][NL];
-        stream_ring<kDepth>(count, ring, fetch, edge_force);
+        stream_ring_sum3(count, ring, fetch, edge_force, store);
         __syncthreads();
         if (threadIdx.x < count) {
             const int t = threadIdx.x;
             double f[3] = {0.0, 0.0, 0.0};
-            for (int w = 0; w < nwaves * kForcePartsA0; ++w)
+            for (int w = 0; w < nwaves; ++w)
                 for (int c = 0; c < 3; ++c) f[c] += static_cast<double>(s_f[t][w][c]);
             double* out = forces + 3 * static_cast<size_t>(s_eid[t] - g.edge_base);
 #pragma unroll
