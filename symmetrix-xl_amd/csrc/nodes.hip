@@ -59,41 +59,71 @@ __device__ __forceinline__ void load_chunk(__amdgpu_buffer_rsrc_t cs, int voff, 
     for (int j = 0; j < kChunk; ++j) c[j] = BASE + j < P::NT ? load1(cs, voff, (BASE + j) * C * 4) : 0.0f;
 }
 
+// The compiled tables list consecutive groups of terms of one output and
+// degree that share a lead: all of a monomial's indices but its free index
+// lz (la for degree 2, la and lb for degree 3).  A group is evaluated
+// nested: U = sum_t c_t x[lz_t], then out += lead * U with lead = x[la] or
+// x[la] x[lb] -- one FMA per term instead of a product and an FMA.  The
+// gradient of a group is dx[lz_t] += (lam lead) c_t per term and, once per
+// group, dx[la] += lam U (degree 2) or dx[la] += lam U x[lb] and
+// dx[lb] += lam U x[la] (degree 3).
+template <class P>
+struct PolyGroups {
+    static constexpr bool same(int s, int t)
+    {
+        return P::out[s] == P::out[t] && P::deg[s] == P::deg[t] && P::deg[t] >= 2 && P::la[s] == P::la[t] &&
+               (P::deg[t] == 2 || P::lb[s] == P::lb[t]);
+    }
+    static constexpr bool first(int t) { return t == 0 || !same(t - 1, t); }
+    static constexpr bool last(int t) { return t == P::NT - 1 || !same(t, t + 1); }
+};
+
 template <class P, int NB, int T>
-__device__ __forceinline__ void term_value(float c, const float (&x)[NB][P::NIN], float (&out)[NB][P::NOUT])
+__device__ __forceinline__ void term_value(float c, const float (&x)[NB][P::NIN], float (&out)[NB][P::NOUT],
+                                           float (&U)[NB])
 {
     if constexpr (T < P::NT) {
-        constexpr int d = P::deg[T], a0 = P::i0[T], a1 = P::i1[T], a2 = P::i2[T], o = P::out[T];
+        constexpr int d = P::deg[T], a0 = P::la[T], a1 = P::lb[T], z = P::lz[T], o = P::out[T];
+        constexpr bool f = PolyGroups<P>::first(T), l = PolyGroups<P>::last(T);
 #pragma unroll
         for (int n = 0; n < NB; ++n) {
-            float v = x[n][a0];
-            if constexpr (d > 1) v *= x[n][a1];
-            if constexpr (d > 2) v *= x[n][a2];
-            out[n][o] = fmaf(c, v, out[n][o]);
+            if constexpr (d == 1) {
+                out[n][o] = fmaf(c, x[n][a0], out[n][o]);
+            } else {
+                U[n] = f ? c * x[n][z] : fmaf(c, x[n][z], U[n]);
+                if constexpr (l) {
+                    const float lead = d == 2 ? x[n][a0] : x[n][a0] * x[n][a1];
+                    out[n][o] = fmaf(lead, U[n], out[n][o]);
+                }
+            }
         }
     }
 }
 
 template <class P, int NB, int T>
 __device__ __forceinline__ void term_gradient(float c, const float (&x)[NB][P::NIN], const float (&lam)[NB][P::NOUT],
-                                              float (&g)[NB][P::NIN])
+                                              float (&g)[NB][P::NIN], float (&U)[NB], float (&pl)[NB])
 {
     if constexpr (T < P::NT) {
-        constexpr int d = P::deg[T], a0 = P::i0[T], a1 = P::i1[T], a2 = P::i2[T], o = P::out[T];
+        constexpr int d = P::deg[T], a0 = P::la[T], a1 = P::lb[T], z = P::lz[T], o = P::out[T];
+        constexpr bool f = PolyGroups<P>::first(T), l = PolyGroups<P>::last(T);
 #pragma unroll
         for (int n = 0; n < NB; ++n) {
-            const float u = c * lam[n][o];
             if constexpr (d == 1) {
-                g[n][a0] += u;
-            } else if constexpr (d == 2) {
-                const float x0 = x[n][a0], x1 = x[n][a1];
-                g[n][a0] = fmaf(u, x1, g[n][a0]);
-                g[n][a1] = fmaf(u, x0, g[n][a1]);
+                g[n][a0] = fmaf(c, lam[n][o], g[n][a0]);
             } else {
-                const float x0 = x[n][a0], x1 = x[n][a1], x2 = x[n][a2];
-                g[n][a0] = fmaf(u, x1 * x2, g[n][a0]);
-                g[n][a1] = fmaf(u, x0 * x2, g[n][a1]);
-                g[n][a2] = fmaf(u, x0 * x1, g[n][a2]);
+                if constexpr (f) pl[n] = d == 2 ? lam[n][o] * x[n][a0] : lam[n][o] * (x[n][a0] * x[n][a1]);
+                U[n] = f ? c * x[n][z] : fmaf(c, x[n][z], U[n]);
+                g[n][z] = fmaf(pl[n], c, g[n][z]);
+                if constexpr (l) {
+                    const float q = lam[n][o] * U[n];
+                    if constexpr (d == 2) {
+                        g[n][a0] += q;
+                    } else {
+                        g[n][a0] = fmaf(q, x[n][a1], g[n][a0]);
+                        g[n][a1] = fmaf(q, x[n][a0], g[n][a1]);
+                    }
+                }
             }
         }
     }
@@ -101,43 +131,44 @@ __device__ __forceinline__ void term_gradient(float c, const float (&x)[NB][P::N
 
 template <class P, int NB, int BASE, int... J>
 __device__ __forceinline__ void value_chunk(const float (&c)[kChunk], const float (&x)[NB][P::NIN],
-                                            float (&out)[NB][P::NOUT], std::integer_sequence<int, J...>)
+                                            float (&out)[NB][P::NOUT], float (&U)[NB], std::integer_sequence<int, J...>)
 {
-    (term_value<P, NB, BASE + J>(c[J], x, out), ...);
+    (term_value<P, NB, BASE + J>(c[J], x, out, U), ...);
 }
 
 template <class P, int NB, int BASE, int... J>
 __device__ __forceinline__ void gradient_chunk(const float (&c)[kChunk], const float (&x)[NB][P::NIN],
                                                const float (&lam)[NB][P::NOUT], float (&g)[NB][P::NIN],
-                                               std::integer_sequence<int, J...>)
+                                               float (&U)[NB], float (&pl)[NB], std::integer_sequence<int, J...>)
 {
-    (term_gradient<P, NB, BASE + J>(c[J], x, lam, g), ...);
+    (term_gradient<P, NB, BASE + J>(c[J], x, lam, g, U, pl), ...);
 }
 
 template <class P, int NB, int BASE>
 __device__ __forceinline__ void core_value_from(__amdgpu_buffer_rsrc_t cs, int voff, int C, const float (&cur)[kChunk],
-                                                float (&x)[NB][P::NIN], float (&out)[NB][P::NOUT])
+                                                float (&x)[NB][P::NIN], float (&out)[NB][P::NOUT], float (&U)[NB])
 {
     if constexpr (BASE < P::NT) {
         float nxt[kChunk];
         if constexpr (BASE + kChunk < P::NT) load_chunk<P, BASE + kChunk>(cs, voff, C, nxt);
-        value_chunk<P, NB, BASE>(cur, x, out, std::make_integer_sequence<int, kChunk>{});
+        value_chunk<P, NB, BASE>(cur, x, out, U, std::make_integer_sequence<int, kChunk>{});
         chunk_boundary<NB, P::NIN>(x);
-        core_value_from<P, NB, BASE + kChunk>(cs, voff, C, nxt, x, out);
+        core_value_from<P, NB, BASE + kChunk>(cs, voff, C, nxt, x, out, U);
     }
 }
 
 template <class P, int NB, int BASE>
 __device__ __forceinline__ void core_gradient_from(__amdgpu_buffer_rsrc_t cs, int voff, int C,
                                                    const float (&cur)[kChunk], float (&x)[NB][P::NIN],
-                                                   const float (&lam)[NB][P::NOUT], float (&g)[NB][P::NIN])
+                                                   const float (&lam)[NB][P::NOUT], float (&g)[NB][P::NIN],
+                                                   float (&U)[NB], float (&pl)[NB])
 {
     if constexpr (BASE < P::NT) {
         float nxt[kChunk];
         if constexpr (BASE + kChunk < P::NT) load_chunk<P, BASE + kChunk>(cs, voff, C, nxt);
-        gradient_chunk<P, NB, BASE>(cur, x, lam, g, std::make_integer_sequence<int, kChunk>{});
+        gradient_chunk<P, NB, BASE>(cur, x, lam, g, U, pl, std::make_integer_sequence<int, kChunk>{});
         chunk_boundary<NB, P::NIN>(x);
-        core_gradient_from<P, NB, BASE + kChunk>(cs, voff, C, nxt, x, lam, g);
+        core_gradient_from<P, NB, BASE + kChunk>(cs, voff, C, nxt, x, lam, g, U, pl);
     }
 }
 
@@ -147,9 +178,9 @@ __device__ __forceinline__ void core_value(__amdgpu_buffer_rsrc_t cs, int voff, 
                                            float (&x)[NB][P::NIN], float (&out)[NB][P::NOUT])
 {
     if constexpr (P::NT > 0) {
-        float c[kChunk];
+        float c[kChunk], U[NB];
         load_chunk<P, 0>(cs, voff, C, c);
-        core_value_from<P, NB, 0>(cs, voff, C, c, x, out);
+        core_value_from<P, NB, 0>(cs, voff, C, c, x, out, U);
     }
 }
 
@@ -160,9 +191,9 @@ __device__ __forceinline__ void core_gradient(__amdgpu_buffer_rsrc_t cs, int vof
                                               float (&g)[NB][P::NIN])
 {
     if constexpr (P::NT > 0) {
-        float c[kChunk];
+        float c[kChunk], U[NB], pl[NB];
         load_chunk<P, 0>(cs, voff, C, c);
-        core_gradient_from<P, NB, 0>(cs, voff, C, c, x, lam, g);
+        core_gradient_from<P, NB, 0>(cs, voff, C, c, x, lam, g, U, pl);
     }
 }
 
