@@ -5,6 +5,7 @@
 #include <atomic>
 #include <chrono>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <limits>
 #include <map>
@@ -542,6 +543,50 @@ void Evaluator::prepare_active_types(const std::vector<int>& node_types)
     }
     upload(r1_, r1, stream_, &staged_);
     upload(r0f_, r0f, stream_, &staged_);
+    // the unfolded layer-0 table and its per-type factors (kA0FoldedTableBytes);
+    // SXL_A0_UNFOLDED=1 / 0 forces the choice (tests)
+    const char* force_unfolded = std::getenv("SXL_A0_UNFOLDED");
+    a0_unfold_ = force_unfolded && force_unfolded[0] ? force_unfolded[0] == '1'
+                                                     : r0f.size() * sizeof(float) > kA0FoldedTableBytes;
+    if (a0_unfold_) {
+        std::vector<float> r0u(static_cast<std::size_t>(npairs) * NI * 4 * NL * C_);
+        for (int pu = 0; pu < npairs; ++pu)
+            for (int iv = 0; iv < NI; ++iv)
+                for (int l = 0; l < NL; ++l)
+                    for (int k = 0; k < C_; ++k) {
+                        double c4[4];
+                        hermite(r0v[pu], r0d[pu], l * C_ + k, iv, c4);
+                        for (int q = 0; q < 4; ++q)
+                            r0u[(((static_cast<std::size_t>(pu) * NI + iv) * NL + l) * C_ + k) * 4 + q] =
+                                static_cast<float>(c4[q]);
+                    }
+        std::vector<float> h0(static_cast<std::size_t>(na) * C_);
+        std::vector<float> w(static_cast<std::size_t>(na) * NL * C_ * C_), wt(w.size());
+        for (int a = 0; a < na; ++a) {
+            for (int k = 0; k < C_; ++k)
+                h0[static_cast<std::size_t>(a) * C_ + k] =
+                    static_cast<float>(m.H0[static_cast<std::size_t>(types[a]) * C_ + k]);
+            for (int l = 0; l < NL; ++l) {
+                const double* W = m.A0W.data() + (static_cast<std::size_t>(types[a]) * NL + l) * C_ * C_;
+                const std::size_t base = (static_cast<std::size_t>(a) * NL + l) * C_ * C_;
+                for (int k = 0; k < C_; ++k)
+                    for (int ko = 0; ko < C_; ++ko) {
+                        const float v = static_cast<float>(W[static_cast<std::size_t>(k) * C_ + ko]);
+                        w[base + static_cast<std::size_t>(k) * C_ + ko] = v;   // reverse: out[k] += in[ko] w[k][ko]
+                        wt[base + static_cast<std::size_t>(ko) * C_ + k] = v;  // forward: out[ko] += in[k] wt[ko][k]
+                    }
+            }
+        }
+        upload(r0u_, r0u, stream_, &staged_);
+        upload(h0s_, h0, stream_, &staged_);
+        upload(a0w_, w, stream_, &staged_);
+        upload(a0wt_, wt, stream_, &staged_);
+    } else {
+        r0u_.release();
+        h0s_.release();
+        a0w_.release();
+        a0wt_.release();
+    }
     // the second-interaction forward of a 256-channel model runs in 64-channel
     // slices, one slice per XCD, when its coefficient table is far beyond one
     // XCD's L2 (4 MiB)
@@ -640,6 +685,10 @@ void Evaluator::allocate_workspace()
     else
         M0s_.release();
     A0_.reserve(NT * nlm_ * C_ * f);
+    if (a0_unfolded())
+        A0pre_.reserve(N * nlm_ * C_ * f);
+    else
+        A0pre_.release();
     M0_.reserve(NT * nLM_ * C_ * f);
     Phi1_.reserve(NT * nlme_ * C_ * f);
     A1_.reserve(NT * nlm_ * C_ * f);
@@ -795,7 +844,7 @@ std::size_t Evaluator::held_graph_bytes() const
     const DeviceBuffer* buffers[] = {
         &node_types_, &first_, &receiver_, &source_, &tfirst_, &tedge_, &edge_pair_, &disp_, &positions_,
         &cell_dev_, &xyz_, &r_, &geo_positions_, &geo_edges_, &geo_shifts_, &A0_, &M0_, &H1_, &Phi1_, &A1_,
-        &A1adj_, &direct_, &H1adj_, &msg_, &energies_, &forces_, &atom_forces_, &partials_, &totals_, &scratch_,
+        &A1adj_, &A0pre_, &direct_, &H1adj_, &msg_, &energies_, &forces_, &atom_forces_, &partials_, &totals_, &scratch_,
         &scale1_, &dot1_, &M0s_, &run_source_, &run_start_, &run_length_, &node_order_, &m0_blocks_, &m0r_blocks_,
         &readout_blocks_, &tile_xyz_, &tile_r_, &tile_pair_, &tile_forces_, &tile_first_edge_dev_,
         &pgraph_.first, &pgraph_.sources, &pgraph_.shifts, &pgraph_.fractional_xyz, &pgraph_.fractional_positions};
@@ -840,7 +889,9 @@ std::size_t Evaluator::graph_bytes_estimate(bool tiled) const
 // tile edge's geometry, pair code and directed force.
 std::size_t Evaluator::work_bytes_estimate(long long receivers, long long edges, bool tiled) const
 {
-    const std::size_t per_node = static_cast<std::size_t>(C_) * sizeof(float) * (3 * nlm_ + nLM_ + nlme_);
+    // the unfolded layer-0 path (untiled) keeps the sums before A0_W as well
+    const int pre = !tiled && a0_unfold_ ? nlm_ : 0;
+    const std::size_t per_node = static_cast<std::size_t>(C_) * sizeof(float) * (3 * nlm_ + pre + nLM_ + nlme_);
     std::size_t per_edge = static_cast<std::size_t>(nLM_) * C_ * sizeof(float);
     if (tiled) per_edge += 7 * sizeof(double) + sizeof(int);
     return per_node * static_cast<std::size_t>(std::max(receivers, 1LL)) +
@@ -941,6 +992,8 @@ void Evaluator::plan_node_blocks()
     m0r_block_offsets_.assign(tiles + 1, 0);
     readout_block_offsets_.assign(tiles + 1, 0);
     std::vector<std::vector<int>> by_type(na);
+    type_start_.assign(na, 0);
+    type_count_.assign(na, 0);
     for (int t = 0; t < tiles; ++t) {
         const int lo = t * T, hi = std::min(N, lo + T);
         for (auto& v : by_type) v.clear();
@@ -948,6 +1001,10 @@ void Evaluator::plan_node_blocks()
         for (int a = 0; a < na; ++a) {
             const int start = static_cast<int>(order.size());
             const int n = static_cast<int>(by_type[a].size());
+            if (tiles == 1) {
+                type_start_[a] = start;
+                type_count_[a] = n;
+            }
             order.insert(order.end(), by_type[a].begin(), by_type[a].end());
             for (int b = 0; b < n; b += kM0BlockNodes) m0b.push_back({start + b, std::min(kM0BlockNodes, n - b), a, 0});
             for (int b = 0; b < n; b += m0r_block_nodes_)
@@ -1684,6 +1741,37 @@ void Evaluator::add_direct(int nodes, int node_base, float* M0adj, hipStream_t s
     hip_check(launch_gemm_group(grp, s), "direct adjoint");
 }
 
+// A0 = A0_pre A0_W[type, l] (reverse: A0_pre_adj = A0_adj A0_W[type, l]^T)
+// per active type and l block over the untiled plan's nodes of that type
+// (node_order_ groups them), up to kMaxGemmGroup GEMMs per launch.
+void Evaluator::gemm_a0(const float* in, float* out, bool reverse)
+{
+    const int NL = model_.l_max + 1;
+    const long long node_stride = static_cast<long long>(nlm_) * C_;
+    const float* W = (reverse ? a0w_ : a0wt_).as<float>();
+    GemmGroup grp;
+    auto flush = [&] {
+        if (grp.count > 0) hip_check(launch_gemm_group(grp, stream_), reverse ? "A0 reverse gemm" : "A0 gemm");
+        grp = GemmGroup{};
+    };
+    for (std::size_t a = 0; a < active_types_.size(); ++a) {
+        if (type_count_[a] == 0) continue;
+        for (int l = 0; l < NL; ++l) {
+            if (grp.count == kMaxGemmGroup) flush();
+            GemmArgs& g = grp.g[grp.count++];
+            g.nodes = type_count_[a];
+            g.rows_per_node = 2 * l + 1;
+            g.K = C_;
+            g.Ncols = C_;
+            g.a = {in + static_cast<std::size_t>(l) * l * C_, node_stride, C_};
+            g.node_ids = node_order_.as<int>() + type_start_[a];
+            g.Bt = W + (a * NL + l) * static_cast<std::size_t>(C_) * C_;
+            g.c = {out + static_cast<std::size_t>(l) * l * C_, node_stride, C_};
+        }
+    }
+    flush();
+}
+
 // A1[l] = Phi1[l group] A1_W[l] (or, reverse, dPhi1[l group] = A1_adj[l]
 // A1_W[l]^T) for `nodes` consecutive tile-local nodes, one grouped launch.
 void Evaluator::gemm_a1(int nodes, const float* in, float* out, bool reverse, const char* what)
@@ -1754,7 +1842,14 @@ void Evaluator::evaluate()
     if (E > 0 || N > 0) {
         // layer 0: A0 (folded H0, A0_W), M0, H1
         mark(kStageA0Forward, false);
-        hip_check(launch_a0_forward(la, r0f_.as<float>(), A0_.as<float>(), s), "A0 forward");
+        if (a0_unfolded()) {
+            LayerArgs lu = la;
+            lu.h0 = h0s_.as<float>();
+            hip_check(launch_a0_forward(lu, r0u_.as<float>(), A0pre_.as<float>(), s), "A0 forward");
+            gemm_a0(A0pre_.as<float>(), A0_.as<float>(), false);
+        } else {
+            hip_check(launch_a0_forward(la, r0f_.as<float>(), A0_.as<float>(), s), "A0 forward");
+        }
         mark(kStageA0Forward, true);
         mark(kStageM0Forward, false);
         hip_check(launch_m0_forward(la, p0, node_blocks(m0_blocks_, m0_block_offsets_, 0, kM0BlockNodes), A0_.as<float>(),
@@ -1835,8 +1930,19 @@ void Evaluator::evaluate()
                   "M0 reverse");
         mark(kStageM0Reverse, true);
         mark(kStageA0Reverse, false);
-        hip_check(launch_a0_reverse(la, r0f_.as<float>(), A0_.as<float>(), A0adj, forces_.as<double>(), s),
-                  "A0 reverse");
+        if (a0_unfolded()) {
+            // the adjoint of the sums before A0_W, into the Phi1 buffer (dPhi1
+            // is consumed); A0_adj . A0 = A0pre_adj . A0pre for the density term
+            float* A0pre_adj = Phi1_.as<float>();
+            gemm_a0(A0adj, A0pre_adj, true);
+            LayerArgs lu = la;
+            lu.h0 = h0s_.as<float>();
+            hip_check(launch_a0_reverse(lu, r0u_.as<float>(), A0pre_.as<float>(), A0pre_adj, forces_.as<double>(), s),
+                      "A0 reverse");
+        } else {
+            hip_check(launch_a0_reverse(la, r0f_.as<float>(), A0_.as<float>(), A0adj, forces_.as<double>(), s),
+                      "A0 reverse");
+        }
         mark(kStageA0Reverse, true);
         launch_zbl_term(la, forces_.as<double>(), s);
     }

@@ -154,6 +154,12 @@ constexpr int kDefaultTileReceivers = 32768;
 // table 0.31 -> 0.38 ms, its 31 MB per-pair (Agnesi) tables 0.33 -> 0.39 ms,
 // the wide shape's 8.9 MB table at C = 128 3.2 -> 3.6 ms.
 constexpr std::size_t kR1SliceTableBytes = std::size_t(8) << 20;
+// The layer-0 table folds H0[source type] and A0_W[receiver type] per ordered
+// pair of active types (no extra work per edge).  Past this size (many
+// active types) the untiled plan uses the unfolded table instead -- one per
+// unordered radial table, resident in L2 -- with H0 applied per edge and A0_W
+// by per-type node GEMMs: the folded rows otherwise stream from HBM.
+constexpr std::size_t kA0FoldedTableBytes = std::size_t(64) << 20;
 
 // Execution-plan report (reference execution_plan.hpp:32-50 and
 // mace_kokkos_runtime.cpp:3843-3915): the candidate plans with their memory
@@ -322,6 +328,10 @@ private:
                  bool reverse, float* x_out, const char* what);
     void add_direct(int nodes, int node_base, float* M0adj, hipStream_t s);
     void gemm_a1(int nodes, const float* in, float* out, bool reverse, const char* what);
+    // A0 = A0_pre A0_W[type] per l block (reverse: A0_pre_adj = A0_adj A0_W^T),
+    // the untiled plan's nodes grouped by active type
+    void gemm_a0(const float* in, float* out, bool reverse);
+    bool a0_unfolded() const { return a0_unfold_ && tile_receivers_ == 0; }
     void reduce(double volume);
     // counts of the calling thread at the start of a preparation/evaluation
     struct CallStart {
@@ -348,6 +358,11 @@ private:
     DeviceBuffer h1w_, h1wt_, h2m1_, h2m1t_, q_, w1_, w2_, cg_;
     // pre_linear_up basis: P0 ([in][out]) and P0^T; residual tables [ne][num_LM][C]
     DeviceBuffer p0w_, p0wt_, residual_, residual_fused_;
+    // unfolded layer-0 table [pair_u][iv][l][k][q], H0 of the active types
+    // [active][C], A0_W per active type [active][l][k][k'] and transposed;
+    // A0_pre: the layer-0 sums before A0_W [N][nlm][C]
+    bool a0_unfold_ = false;
+    DeviceBuffer r0u_, h0s_, a0w_, a0wt_, A0pre_;
     std::vector<std::unique_ptr<DeviceBuffer>> a1w_, a1wt_;
     PolyLayout p0_layout_, p1_layout_;
     // density-normalisation splines [pair_u][interval][4] and ZBL pair tables [ordered active pair]
@@ -447,6 +462,9 @@ private:
     DeviceBuffer node_order_, m0_blocks_, m0r_blocks_, readout_blocks_;
     // [tiles + 1] each; the M0 reverse has its own block size (m0r_block_nodes_)
     std::vector<int> m0_block_offsets_, m0r_block_offsets_, readout_block_offsets_;
+    // untiled plan: each active type's nodes at node_order_[type_start_[a]
+    // .. + type_count_[a])
+    std::vector<int> type_start_, type_count_;
     int m0r_block_nodes_ = kM0BlockNodes;
     int readout_block_nodes_ = kReadoutBlockNodes;
     int compute_units_ = 0;  // of the evaluator's device

@@ -64,7 +64,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 5))
         if (r < M) {
             const int node = r / g.rows_per_node;
             const int m = r - node * g.rows_per_node;
-            arow[j] = g.a.ptr + node * g.a.node_stride + m * g.a.row_stride + lk;
+            const long long gn = g.node_ids ? g.node_ids[node] : node;
+            arow[j] = g.a.ptr + gn * g.a.node_stride + m * g.a.row_stride + lk;
         }
     }
     const float* brow[kBPasses];
@@ -125,7 +126,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 5))
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             if (row < M) {
-                const long long base = static_cast<long long>(node) * g.c.node_stride + m * g.c.row_stride;
+                const long long gn = g.node_ids ? g.node_ids[node] : node;
+                const long long base = gn * g.c.node_stride + m * g.c.row_stride;
 #pragma unroll
                 for (int j = 0; j < kNB; ++j) {
                     const int col = col0 + wn * (kBN / kWN) + j * 32 + (lane & 31);

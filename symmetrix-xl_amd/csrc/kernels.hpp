@@ -146,6 +146,9 @@ struct GemmArgs {
     GemmOut c;
     GemmBias bias;
     int accumulate = 0;
+    // GEMM node n is graph node node_ids[n] for the input and output rows
+    // (null: node n); the bias is not remapped
+    const int* node_ids = nullptr;
 };
 
 // Up to kMaxGemmGroup independent GEMMs (the irrep blocks of one stage) in
@@ -187,10 +190,16 @@ struct LayerArgs {
     // of all channels).  Set where the coefficient table outgrows one XCD's
     // L2: each XCD then reads only its slice's columns.
     int channel_slices = 1;
+    // Layer 0 with the unfolded table: rows per unordered pair table (no H0,
+    // no A0_W); each edge's radial values are scaled by
+    // h0[source's active type][k] and A0_W is applied to the node sums by
+    // GEMMs.  Null: the table folds H0 and A0_W per ordered pair.
+    const float* h0 = nullptr;  // [active types][C]
 };
 
 // Layer 0: A0[i] = sum_j R0f_{pair(i,j)}(r) Y(r_hat)   (H0 and A0_W folded in),
-// divided by the A0 density scale when the model has one
+// divided by the A0 density scale when the model has one; with a.h0 the
+// table is the unfolded one and A0 holds the sums before A0_W
 hipError_t launch_a0_forward(const LayerArgs& a, const float* r0f, float* A0, hipStream_t s);
 // M0 = P0(A0) per (node, LM, channel), over the nodes of the given blocks
 hipError_t launch_m0_forward(const LayerArgs& a, const PolyArgs& p0, const NodeBlocks& nb, const float* A0,

@@ -136,7 +136,7 @@ struct TileSlot {
 // (slot = lane prefix count) and skip the ranking.
 template <bool kOrdered, bool kSorted>
 __device__ __forceinline__ TileSlot compact_edge(const EdgeGraph& g, const SplineGrid& grid, int base, int n,
-                                                 int t, double& rr, int* count)
+                                                 int t, double& rr, int* count, bool pair_tables = false)
 {
     bool on = false;
     rr = 0.0;
@@ -150,7 +150,9 @@ __device__ __forceinline__ TileSlot compact_edge(const EdgeGraph& g, const Splin
         int iv;
         spline_point(rr, grid, iv, x);
         const int code = g.edge_pair[base + t - g.edge_base];
-        const int pair = kOrdered ? code & 0xffff : code >> 16;
+        // pair_tables: a layer-0 kernel on the unfolded table (rows per
+        // unordered pair table, as the second interaction's)
+        const int pair = kOrdered && !pair_tables ? code & 0xffff : code >> 16;
         row = pair * grid.intervals + iv;
     }
     const unsigned long long mask = __ballot(on);
@@ -213,7 +215,9 @@ __device__ __forceinline__ float density_scale(const DensityScale& d, const Edge
 // ---------------------------------------------------------------------------
 // Layer 0 forward: A0[i, lm, k] = sum_j R0f_{pair}(r_ij)[l, k] Y_lm(r_ij)
 // ---------------------------------------------------------------------------
-template <int LMAX>
+// kUnfolded: the table holds no H0 / A0_W (LayerArgs::h0); each edge's radial
+// values are scaled by H0 of its source's type, A0 receives the sums before A0_W.
+template <int LMAX, bool kUnfolded>
 __global__ void __launch_bounds__(256) a0_forward_kernel(LayerArgs a, const float* __restrict__ r0f,
                                                           float* __restrict__ A0)
 {
@@ -222,6 +226,7 @@ __global__ void __launch_bounds__(256) a0_forward_kernel(LayerArgs a, const floa
     __shared__ float s_Y[kTile][NLM];
     __shared__ float s_x[kTile];
     __shared__ int s_row[kTile];
+    __shared__ int s_h0row[kTile];  // kUnfolded: offset of the source type's H0 row
     __shared__ int s_gstart[kTile + 1];  // first slot of each run of equal rows
     __shared__ int s_count, s_groups;
 
@@ -246,7 +251,8 @@ __global__ void __launch_bounds__(256) a0_forward_kernel(LayerArgs a, const floa
         if (threadIdx.x < 64) {
             const int t = threadIdx.x;
             double rr;
-            const TileSlot ts = compact_edge<true, true>(g, a.grid, base, min(kTile, e1 - base), t, rr, &s_count);
+            const TileSlot ts =
+                compact_edge<true, true>(g, a.grid, base, min(kTile, e1 - base), t, rr, &s_count, kUnfolded);
             if (ts.active) {
                 const int e = base + t;
                 float Y[NLM], dir[3];
@@ -254,6 +260,8 @@ __global__ void __launch_bounds__(256) a0_forward_kernel(LayerArgs a, const floa
                                             nullptr, nullptr, dir);
                 s_x[ts.slot] = ts.x;
                 s_row[ts.slot] = ts.row;
+                if constexpr (kUnfolded)
+                    s_h0row[ts.slot] = (g.edge_pair[e - g.edge_base] & 0xffff) % g.num_active * C;
 #pragma unroll
                 for (int lm = 0; lm < NLM; ++lm) s_Y[ts.slot][lm] = Y[lm];
             }
@@ -290,6 +298,11 @@ __global__ void __launch_bounds__(256) a0_forward_kernel(LayerArgs a, const floa
                 float R[NL];
 #pragma unroll
                 for (int l = 0; l < NL; ++l) R[l] = cubic(c[l], x);
+                if constexpr (kUnfolded) {
+                    const float h = a.h0[uniform(s_h0row[j]) + min(k, C - 1)];
+#pragma unroll
+                    for (int l = 0; l < NL; ++l) R[l] *= h;
+                }
 #pragma unroll
                 for (int lm = 0; lm < NLM; ++lm) acc[lm] = fmaf(R[kLmL[lm]], s_Y[j][lm], acc[lm]);
             }
@@ -1119,7 +1132,7 @@ __global__ void __launch_bounds__(256) r1_reverse_grouped_kernel(LayerArgs a, co
 // ---------------------------------------------------------------------------
 // Layer 0 reverse: f_ij += -sum_{lm,k} A0_adj[i,lm,k] (r_hat R0f' Y_lm + R0f dY_lm)
 // ---------------------------------------------------------------------------
-template <int LMAX>
+template <int LMAX, bool kUnfolded>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) a0_reverse_kernel(LayerArgs a, const float* __restrict__ r0f,
                                                           const float* __restrict__ A0,
                                                           const float* __restrict__ A0_adj,
@@ -1131,6 +1144,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) a
     __shared__ float s_geo[kTile][4];
     __shared__ float s_ir[kTile];  // 1 / r
     __shared__ int s_row[kTile];
+    __shared__ int s_h0row[kTile];  // kUnfolded: offset of the source type's H0 row
     __shared__ int s_eid[kTile];
     __shared__ float s_f[kTile][kMaxWaves][3];  // wave sums (stream_ring_sum3)
     __shared__ float s_dsc[kTile];  // A0 density-scale force coefficient per active slot
@@ -1200,7 +1214,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) a
             const int t = threadIdx.x;
             double rr;
             const int n = min(kTile, e1 - base);
-            const TileSlot ts = compact_edge<true, false>(g, a.grid, base, n, t, rr, &s_count);
+            const TileSlot ts = compact_edge<true, false>(g, a.grid, base, n, t, rr, &s_count, kUnfolded);
             const int e = base + t;
             if (ts.active) {
                 const int sl = ts.slot;
@@ -1209,6 +1223,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) a
                 s_geo[sl][3] = ts.x;
                 s_ir[sl] = static_cast<float>(1.0 / rr);
                 s_row[sl] = ts.row;
+                if constexpr (kUnfolded) s_h0row[sl] = (g.edge_pair[e - g.edge_base] & 0xffff) % g.num_active * C;
                 s_eid[sl] = e;
                 s_dsc[sl] = a.d0.table ? dcoef * density_slope(a.d0.table, a.grid, g.edge_pair[e - g.edge_base] >> 16, rr) : 0.0f;
             } else if (t < n && a.d0.table) {
@@ -1268,6 +1283,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) a
             fx = fmaf(s_geo[j][0], A, gx);
             fy = fmaf(s_geo[j][1], A, gy);
             fz = fmaf(s_geo[j][2], A, gz);
+            if constexpr (kUnfolded) {
+                // the edge's terms are linear in its radial values: scale once
+                const float h = a.h0[uniform(s_h0row[j]) + min(k, C - 1)];
+                fx *= h;
+                fy *= h;
+                fz *= h;
+            }
         };
         auto store = [&](int j, const float (&sums)[3]) {
             s_f[j][wave][0] = sums[0];
@@ -1718,9 +1740,16 @@ hipError_t launch_a0_forward(const LayerArgs& a, const float* r0f, float* A0, hi
 {
     if (a.node_count <= 0) return hipSuccess;
     const int threads = node_threads(a.C);
+    const bool u = a.h0 != nullptr;
     switch (a.l_max) {
-    case 2: a0_forward_kernel<2><<<a.node_count, threads, 0, s>>>(a, r0f, A0), note_launch(); break;
-    case 3: a0_forward_kernel<3><<<a.node_count, threads, 0, s>>>(a, r0f, A0), note_launch(); break;
+    case 2:
+        if (u) a0_forward_kernel<2, true><<<a.node_count, threads, 0, s>>>(a, r0f, A0), note_launch();
+        else a0_forward_kernel<2, false><<<a.node_count, threads, 0, s>>>(a, r0f, A0), note_launch();
+        break;
+    case 3:
+        if (u) a0_forward_kernel<3, true><<<a.node_count, threads, 0, s>>>(a, r0f, A0), note_launch();
+        else a0_forward_kernel<3, false><<<a.node_count, threads, 0, s>>>(a, r0f, A0), note_launch();
+        break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -1731,9 +1760,16 @@ hipError_t launch_a0_reverse(const LayerArgs& a, const float* r0f, const float* 
 {
     if (a.node_count <= 0) return hipSuccess;
     const int threads = node_threads(a.C);
+    const bool u = a.h0 != nullptr;
     switch (a.l_max) {
-    case 2: a0_reverse_kernel<2><<<a.node_count, threads, 0, s>>>(a, r0f, A0, A0_adj, forces), note_launch(); break;
-    case 3: a0_reverse_kernel<3><<<a.node_count, threads, 0, s>>>(a, r0f, A0, A0_adj, forces), note_launch(); break;
+    case 2:
+        if (u) a0_reverse_kernel<2, true><<<a.node_count, threads, 0, s>>>(a, r0f, A0, A0_adj, forces), note_launch();
+        else a0_reverse_kernel<2, false><<<a.node_count, threads, 0, s>>>(a, r0f, A0, A0_adj, forces), note_launch();
+        break;
+    case 3:
+        if (u) a0_reverse_kernel<3, true><<<a.node_count, threads, 0, s>>>(a, r0f, A0, A0_adj, forces), note_launch();
+        else a0_reverse_kernel<3, false><<<a.node_count, threads, 0, s>>>(a, r0f, A0, A0_adj, forces), note_launch();
+        break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
