@@ -159,7 +159,10 @@ constexpr std::size_t kR1SliceTableBytes = std::size_t(8) << 20;
 // active types) the untiled plan uses the unfolded table instead -- one per
 // unordered radial table, resident in L2 -- with H0 applied per edge and A0_W
 // by per-type node GEMMs: the folded rows otherwise stream from HBM.
-constexpr std::size_t kA0FoldedTableBytes = std::size_t(64) << 20;
+// Measured on 20,000-atom irregular boxes (full calls, medium model): 4
+// types (33 MB folded) 6.64 ms folded / 6.88 unfolded, 6 types (75 MB)
+// 6.97 / 6.97-7.04, 8 types (134 MB) 7.31-7.37 / 6.97-7.07.
+constexpr std::size_t kA0FoldedTableBytes = std::size_t(100) << 20;
 
 // Execution-plan report (reference execution_plan.hpp:32-50 and
 // mace_kokkos_runtime.cpp:3843-3915): the candidate plans with their memory
