@@ -9,8 +9,8 @@
 // kMaxGemmGroup GEMMs, tiles numbered consecutively across the group).  A
 // 256-thread workgroup computes a 64 x 128 output tile with four waves of
 // v_mfma_f32_32x32x2f32 (each wave 32 x 64: two 32 x 32 blocks).  K is staged
-// through LDS in slices of 32, the next slice's global loads in flight while
-// the current one is multiplied.  Both operands are stored K-contiguous (the
+// through LDS in slices of 16 (64-row tiles) or 32 (32-row tiles), the next
+// slice's global loads in flight while the current one is multiplied.  Both operands are stored K-contiguous (the
 // weight matrix is passed transposed, Bt[n][k]) so one ds_read_b128 feeds four
 // MFMAs: lane half h supplies k = 8c + 4h + q to MFMA q of chunk c, the same
 // k for both operands, which sums every k of the chunk exactly once.
@@ -23,18 +23,25 @@ namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int kBN = 128, kBK = 32, kPad = 4;
+constexpr int kBN = 128, kPad = 4;
+constexpr int kKMultiple = 32;  // K must be a multiple of every slice length
 
 // kBM output rows per tile: 64 (four waves as 2 x 2, each 32 x 64: two MFMA
 // blocks) or, for launches too small to fill the chip, 32 (four waves side by
 // side, each 32 x 32: one block), which doubles the workgroups and halves
-// each one's chain of K slices.
+// each one's chain of K slices.  The 64-row tiles stage K in slices of 16:
+// 15 KB of LDS and 78 VGPRs, six workgroups per CU where slices of 32 (27 KB,
+// 96 VGPRs) allowed five and slices of 64 three; the 32-row tiles keep
+// slices of 32 at five.
 template <int kBM>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 5))) gemm_group_kernel(GemmGroup grp)
+__global__ void __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(kBM == 64 ? 6 : 5, kBM == 64 ? 6 : 5))) gemm_group_kernel(GemmGroup grp)
 {
     constexpr int kWN = kBM == 64 ? 2 : 4;       // waves along N
     constexpr int kNB = kBN / kWN / 32;          // 32 x 32 MFMA blocks per wave along N
+    constexpr int kBK = kBM == 64 ? 16 : 32;     // K slice
     static_assert(kBM == 64 || kBM == 32, "64- or 32-row tiles");
+    static_assert(kKMultiple % kBK == 0, "slice length divides the K multiple");
     __shared__ float As[kBM][kBK + kPad];
     __shared__ float Bs[kBN][kBK + kPad];
     const int b = blockIdx.x;
@@ -160,7 +167,7 @@ hipError_t launch_gemm_group(GemmGroup grp, hipStream_t stream)
         const GemmArgs& g = grp.g[i];
         const long long M = static_cast<long long>(g.nodes) * g.rows_per_node;
         if (M <= 0 || g.Ncols <= 0 || g.K <= 0) continue;
-        if (g.K % kBK != 0 || M > 0x7fffffff) return hipErrorInvalidValue;
+        if (g.K % kKMultiple != 0 || M > 0x7fffffff) return hipErrorInvalidValue;
         // float4 loads: row strides and bases must keep 16-byte alignment
         if (g.a.node_stride % 4 != 0 || g.a.row_stride % 4 != 0 ||
             reinterpret_cast<std::uintptr_t>(g.a.ptr) % 16 != 0 || reinterpret_cast<std::uintptr_t>(g.Bt) % 16 != 0)
@@ -179,7 +186,7 @@ hipError_t launch_gemm_group(GemmGroup grp, hipStream_t stream)
         return tiles;
     };
     // 64-row tiles unless they leave most compute units with at most one
-    // workgroup (256 CUs, five resident per CU)
+    // workgroup (256 CUs, five or six resident per CU)
     int tiles = number_tiles(64);
     if (tiles == 0) return hipSuccess;
     if (tiles < 2 * 256) {
