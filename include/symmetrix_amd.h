@@ -290,8 +290,7 @@ void sxl_neighbor_graph_free(sxl_graph* graph);
 
 /* No counterpart in the reference.  An allocation-free variant of
  * sxl_neighbor_graph_build for callers that cannot allocate device memory
- * (code under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc): the same kernels and the same, bit-identical, edge list, with
+ * (tight serving loops, harnesses that forbid hipMalloc): the same kernels and the same, bit-identical, edge list, with
  * the positions [N][3] and every output in the caller's device memory --
  * receiver_offsets [N+1], sources [edge_capacity], shifts and
  * fractional_xyz [edge_capacity][3] -- and the build's intermediate arrays
@@ -303,7 +302,9 @@ void sxl_neighbor_graph_free(sxl_graph* graph);
  * receives the edge count; when it exceeds edge_capacity the call returns a
  * length error and writes no output array (call again with larger arrays).
  * The work runs on `stream` (a hipStream_t; NULL: the default stream) and has
- * completed when the call returns.  All calls on one GPU share the library's
+ * completed when the call returns: the call reads the edge count back to the
+ * host and waits on the stream, so it cannot be recorded into a HIP graph
+ * (stream capture).  All calls on one GPU share the library's
  * array: calls that overlap on one GPU (other threads, other streams) race. */
 #define SXL_NOALLOC_MAX_ATOMS 131072
 #define SXL_NOALLOC_MAX_BINS 262144
