@@ -283,11 +283,30 @@ def capacity_run(args):
         ev._set_dual_layer_workspace_receiver_limit_for_testing(args.tile_receivers)
     types = synthetic.node_types(s, ev.atomic_numbers)
     m, v = thermal_start(s, args.seed)
+    lattice = None
+    if args.sigma == 0.0:
+        # a perfect lattice has one energy per atom at every size: the same
+        # model on a 3^3 cell (untiled, freed before the large run) is the
+        # size-independent check of the large tiled graph
+        small = synthetic.srtio3_supercell(3, sigma=0.0, seed=args.seed)
+        ref = MACEKokkosFloat(model_path)
+        gen = ref._prepare_periodic_factorized_graph(synthetic.node_types(small, ref.atomic_numbers), small.positions,
+                                                     small.cell, np.linalg.inv(small.cell),
+                                                     ref.r_cut + args.skin)["generation"]
+        ref._compute_prepared_factorized_positions(gen, small.positions)
+        lattice = {"reference_cells": 3, "reference_energy_per_atom": float(ref.node_energies.sum()) / len(small)}
+        ref.close()
+        del ref
     print(f"[capacity] setup {time.perf_counter() - t_setup:.1f} s; running {args.md_steps} steps on the device",
           file=sys.stderr, flush=True)
+
+    def progress(step, epot, ekin, seconds):
+        print(f"[capacity] step {step}: {seconds:.3f} s, E_tot {epot + ekin:.6f} eV", file=sys.stderr, flush=True)
+        return False
+
     t_run = time.perf_counter()
     try:
-        res = ev._md_nve(types, m, s.positions, v, s.cell, args.skin, args.md_dt, args.md_steps)
+        res = ev._md_nve(types, m, s.positions, v, s.cell, args.skin, args.md_dt, args.md_steps, progress=progress)
     except (OverflowError, MemoryError, RuntimeError, ValueError) as err:
         # refused before any evaluation (int32 edge limit, memory): say why
         print(json.dumps({
@@ -300,8 +319,13 @@ def capacity_run(args):
     t_run = time.perf_counter() - t_run
     times = list(res["step_seconds"])
     etot = res["potential_energy"] + res["kinetic_energy"]
-    for step, t in enumerate(times):
-        print(f"[capacity] step {step + 1}: {t:.3f} s, E_tot {etot[step + 1]:.6f} eV", file=sys.stderr, flush=True)
+    if lattice is not None:
+        lattice["energy_per_atom"] = float(res["potential_energy"][0]) / N
+        lattice["abs_difference"] = abs(lattice["energy_per_atom"] - lattice["reference_energy_per_atom"])
+        if args.md_steps == 0:  # forces of the perfect lattice itself
+            gen = ev._graph_size()[2]
+            lattice["max_abs_force"] = float(np.max(np.abs(ev._reduce_atom_forces(N, None, None, gen))))
+        print(f"[capacity] perfect-lattice check: {lattice}", file=sys.stderr, flush=True)
     st = ev.stats
     line = {
         "metric": "tiled capacity: atoms per MI355X and us/atom/step of a 20-step NVE run (FP32)",
@@ -314,6 +338,7 @@ def capacity_run(args):
         "max_energy_drift_per_atom_eV": round(float(np.max(np.abs(etot - etot[0]))) / N, 9),
         "neighbor_rebuilds": res["rebuilds"],
         "run_seconds_including_first_build": round(t_run, 2),
+        "perfect_lattice_check": lattice,
         "tile_receivers": st["tile_receivers"],
         "num_tiles": st["num_tiles"],
         "tiled_evaluations": st["tiled_evaluations"],

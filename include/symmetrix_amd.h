@@ -200,6 +200,11 @@ int sxl_compute_prepared_positions_device(sxl_evaluator* evaluator, uint64_t gen
  * Replaces _compute_prepared_factorized(generation, xyz, r)
  * (mace_kokkos.cpp:1817-1827). */
 int sxl_compute_prepared(sxl_evaluator* evaluator, uint64_t generation, const double* xyz, const double* r);
+/* The same with xyz and r in device memory (the reference's C++
+ * compute_prepared_factorized over device views, mace_kokkos.hpp:339-460);
+ * they are read during the call only. */
+int sxl_compute_prepared_device(sxl_evaluator* evaluator, uint64_t generation, const double* d_xyz,
+                                const double* d_r);
 
 /* One-shot: prepare the CSR graph and evaluate.  Replaces
  * compute_node_energies_forces(num_nodes, node_types, num_neigh,
@@ -257,6 +262,14 @@ int sxl_md_nve(sxl_evaluator* evaluator, int num_atoms, const int* node_types, c
                double* positions, double* velocities, const double* cell, const double* inverse_cell, double skin,
                double dt, int steps, double* potential_energy, double* kinetic_energy, double* step_seconds,
                int* rebuilds);
+/* Progress of sxl_md_nve, the thermo output of LAMMPS `fix nve` runs (no
+ * single reference counterpart): called on the calling thread after every
+ * step (1-based) with the step's potential and kinetic energy (eV; NaN when
+ * the run does not compute them) and its wall time (s); a nonzero return
+ * ends the run after that step.  NULL removes it. */
+typedef int (*sxl_md_progress_fn)(int step, double potential_energy, double kinetic_energy, double seconds,
+                                  void* user);
+int sxl_set_md_progress(sxl_evaluator* evaluator, sxl_md_progress_fn callback, void* user);
 
 /* node_energies property, N doubles (mace_kokkos.cpp:2086-2093). */
 int sxl_node_energies(const sxl_evaluator* evaluator, double* out, int num_nodes);

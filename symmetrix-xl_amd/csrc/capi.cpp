@@ -309,6 +309,12 @@ int sxl_compute_prepared(sxl_evaluator* ev, uint64_t generation, const double* x
     return guarded([&] { ev->impl.compute_xyz(generation, xyz, r, false); });
 }
 
+int sxl_compute_prepared_device(sxl_evaluator* ev, uint64_t generation, const double* d_xyz, const double* d_r)
+{
+    if (!ev || ((!d_xyz || !d_r) && ev->impl.num_edges() > 0)) return null_handle();
+    return guarded([&] { ev->impl.compute_xyz(generation, d_xyz, d_r, true); });
+}
+
 int sxl_compute_node_energies_forces(sxl_evaluator* ev, int num_nodes, const int* node_types, const int* num_neigh,
                                      const int* neigh_indices, const int* neigh_types, const double* xyz,
                                      const double* r)
@@ -363,6 +369,12 @@ int sxl_md_nve(sxl_evaluator* ev, int num_atoms, const int* node_types, const do
                                       dt, steps, potential_energy, kinetic_energy, step_seconds);
         if (rebuilds) *rebuilds = n;
     });
+}
+
+int sxl_set_md_progress(sxl_evaluator* ev, sxl_md_progress_fn callback, void* user)
+{
+    if (!ev) return null_handle();
+    return guarded([&] { ev->impl.set_md_progress(callback, user); });
 }
 
 int sxl_node_energies(const sxl_evaluator* ev, double* out, int num_nodes)

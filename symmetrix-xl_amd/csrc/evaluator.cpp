@@ -334,6 +334,12 @@ Evaluator::Evaluator(const std::string& model_path, const std::string& head)
     grid_.h = model_.spline_h;
     grid_.intervals = model_.spline_points - 1;
     grid_.r_cut = model_.r_cut;
+    // test hook: a lower edge-index ceiling makes small graphs take the
+    // paths of graphs past 2^31 - 1 edges
+    if (const char* limit = std::getenv("SXL_EDGE_INDEX_LIMIT"); limit && limit[0]) {
+        const long long v = std::atoll(limit);
+        if (v > 0 && v < edge_index_limit_) edge_index_limit_ = v;
+    }
     upload_static_tables();
     hip_check(host_fence(stream_), "model upload");
 }
@@ -704,8 +710,9 @@ void Evaluator::allocate_workspace()
     }
     energies_.reserve(N * sizeof(double));
     atom_forces_.reserve(N * 3 * sizeof(double));
-    partials_.reserve(static_cast<std::size_t>(reduce_totals_partials(num_nodes_, static_cast<int>(num_edges_))) *
-                      10 * sizeof(double));
+    // totals partials: nodes and edges of the graph (untiled) or of one tile
+    partials_.reserve(static_cast<std::size_t>(reduce_totals_partials(num_nodes_, static_cast<int>(ET))) * 10 *
+                      sizeof(double));
     // [0] energy, [1..9] stress, [12] max |disp|^2, [13] invalid edges,
     // [16..25] tiled plan: -sum f (x) xyz accumulated over the tiles
     totals_.reserve(32 * sizeof(double));
@@ -729,12 +736,30 @@ void Evaluator::allocate_workspace()
     }
 }
 
-// Execution plan of the prepared graph.  With fixed workspace allowed, the
-// graph is tiled when a receiver limit below N is set, or when the untiled
-// work arrays would not fit the free device memory (tiles of
-// kDefaultTileReceivers).  For a tiled plan: the edge range of each tile and
-// the runs of the source-major edge lists per tile (for the H1 adjoint).
-void Evaluator::plan_tiles()
+namespace {
+// Device memory the planner refuses to plan for: the estimate of the plan
+// exceeds everything the device could give this evaluator (std::bad_alloc,
+// so callers see an allocation error, with the planner's figures).
+class PlanMemoryError : public std::bad_alloc {
+public:
+    explicit PlanMemoryError(std::string message) : message_(std::move(message)) {}
+    const char* what() const noexcept override { return message_.c_str(); }
+
+private:
+    std::string message_;
+};
+}  // namespace
+
+// Execution plan of the graph being prepared, from its receiver offsets
+// (host_first_) before its edges are written.  The untiled plan indexes
+// edges graph-wide in int32 and takes at most edge_index_limit_ edges; the
+// tiled plan indexes them per tile.  With fixed workspace allowed, the graph
+// is tiled when a receiver limit below N is set, when the untiled work
+// arrays would not fit the memory budget, or when its edges exceed the
+// untiled plan's index (tiles of kDefaultTileReceivers by default).  A tiled
+// plan whose estimate exceeds all the memory the device could give is
+// refused here, before the edges are written.
+void Evaluator::select_plan()
 {
     tile_receivers_ = 0;
     num_tiles_ = 0;
@@ -748,32 +773,48 @@ void Evaluator::plan_tiles()
     ExecutionPlanReport rep;
     rep.requested_profile = plan_profile_;
     rep.selection_source = plan_debug_.empty() ? "native_request" : "debug_override";
-    const std::vector<int>& first = host_first_;
-    // candidate estimates: graph state + work arrays
-    const std::size_t graph_untiled = graph_bytes_estimate(false);
-    const std::size_t graph_tiled = graph_bytes_estimate(true);
-    const std::size_t untiled = graph_untiled + work_bytes_estimate(N, E, false);
+    const std::vector<long long>& first = host_first_;
     const int T = receiver_limit_ > 0 ? receiver_limit_ : kDefaultTileReceivers;
+    const int tiles = N > 0 ? static_cast<int>((static_cast<long long>(N) + T - 1) / T) : 0;
     long long tile_edges = 0;
     for (long long t0 = 0; t0 < N; t0 += T)
         tile_edges = std::max<long long>(tile_edges, first[std::min<long long>(N, t0 + T)] - first[t0]);
-    // runs of the source-major lists per tile: at least one per source with edges
-    const std::size_t tiled = graph_tiled + work_bytes_estimate(std::min(T, std::max(N, 1)), tile_edges, true) +
-                              3 * sizeof(int) * static_cast<std::size_t>(std::max(N, 1));
+    // runs (distinct sources per tile): counted by the device build's count
+    // pass or by count_tile_runs; otherwise at least one per node
+    long long runs = N;
+    if (static_cast<int>(tile_runs_.size()) == tiles && tiles > 0)
+        runs = std::accumulate(tile_runs_.begin(), tile_runs_.end(), 0LL);
+    const std::size_t untiled = graph_bytes_estimate(false, 0) + work_bytes_estimate(N, E, false);
+    const std::size_t tiled = graph_bytes_estimate(true, runs) +
+                              work_bytes_estimate(std::min(T, std::max(N, 1)), tile_edges, true);
     // memory budget: free device memory plus the graph and work memory this
     // evaluator holds now (the estimates count all of a plan's memory)
     std::size_t free_bytes = 0, total_bytes = 0;
     hip_check(hipMemGetInfo(&free_bytes, &total_bytes), "memory info");
     rep.available_bytes = free_bytes + held_graph_bytes();
+    // test hook: SXL_DEVICE_MEMORY_LIMIT (bytes) caps what the planner may use
+    if (const char* cap = std::getenv("SXL_DEVICE_MEMORY_LIMIT"); cap && cap[0]) {
+        const long long v = std::atoll(cap);
+        if (v > 0) rep.available_bytes = std::min<std::size_t>(rep.available_bytes, static_cast<std::size_t>(v));
+    }
     rep.reserve_bytes = rep.available_bytes / 10;
     const std::size_t budget = rep.available_bytes - rep.reserve_bytes;
     const bool tiled_permitted = allow_fixed_workspace_ || plan_debug_ == kTiled;
-    rep.candidates.push_back({kSpeed, true, untiled, untiled <= budget ? "estimated fit" : "exceeds advisory memory budget"});
+    const bool untiled_indexable = E <= edge_index_limit_;
+    const bool tiles_indexable = tile_edges <= edge_index_limit_;
+    const std::string over_index =
+        "the graph's " + std::to_string(E) + " edges exceed the untiled plan's 32-bit edge index";
+    rep.candidates.push_back({kSpeed, untiled_indexable, untiled,
+                              !untiled_indexable ? over_index
+                              : untiled <= budget ? "estimated fit"
+                                                  : "exceeds advisory memory budget"});
     rep.candidates.push_back(
-        {kTiled, tiled_permitted && N > T, tiled,
-         !tiled_permitted ? "fixed-workspace execution requires explicit opt-in via allow_fixed_workspace"
-         : N > T          ? "qualified"
-                          : "the graph fits in one tile of " + std::to_string(T) + " receivers"});
+        {kTiled, tiled_permitted && N > T && tiles_indexable, tiled,
+         !tiled_permitted  ? "fixed-workspace execution requires explicit opt-in via allow_fixed_workspace"
+         : !(N > T)        ? "the graph fits in one tile of " + std::to_string(T) + " receivers"
+         : !tiles_indexable ? "a tile of " + std::to_string(T) + " receivers has " + std::to_string(tile_edges) +
+                                  " edges, more than one tile's 32-bit edge index"
+                           : "qualified"});
 
     bool tile = false;
     if (plan_debug_ == kSpeed) {
@@ -784,6 +825,9 @@ void Evaluator::plan_tiles()
                                     : "debug override: the graph fits in one tile, untiled";
     } else if (plan_profile_ == "speed") {
         rep.selection_reason = "speed request selected the untiled plan";
+    } else if (!untiled_indexable && allow_fixed_workspace_ && N > T) {
+        tile = true;
+        rep.selection_reason = over_index + "; tiles of " + std::to_string(T) + " receivers";
     } else if (allow_fixed_workspace_ && receiver_limit_ > 0 && N > T) {
         tile = true;
         rep.selection_reason = "receiver limit " + std::to_string(T) + " set for the tiled plan";
@@ -798,43 +842,133 @@ void Evaluator::plan_tiles()
     }
     rep.selected_id = tile ? kTiled : kSpeed;
     rep.boundary_attempt = (tile ? tiled : untiled) > budget;
-    rep.state = "active";
+    rep.state = tile || untiled_indexable ? "active" : "refused";
     plan_report_ = rep;
-    if (!tile) return;
-
+    if (!tile) {
+        if (!untiled_indexable)
+            throw std::length_error("neighbor graph exceeds 32-bit edge indexing (" + std::to_string(E) +
+                                    " edges); fixed-workspace (tiled) execution indexes edges per tile");
+        return;
+    }
+    if (!tiles_indexable)
+        throw std::length_error("a receiver tile of " + std::to_string(T) + " receivers has " +
+                                std::to_string(tile_edges) +
+                                " edges, beyond 32-bit edge indexing; set a smaller workspace receiver limit");
+    if (tiled > rep.available_bytes) {
+        plan_report_.state = "refused";
+        throw PlanMemoryError("MACE tiled execution plan needs an estimated " + std::to_string(tiled) +
+                              " bytes of device memory for " + std::to_string(N) + " atoms and " +
+                              std::to_string(E) + " edges; the device can give " +
+                              std::to_string(rep.available_bytes) + " bytes");
+    }
     tile_receivers_ = T;
-    num_tiles_ = (N + T - 1) / T;
+    num_tiles_ = tiles;
     tile_first_edge_.resize(num_tiles_ + 1);
-    for (int t = 0; t <= num_tiles_; ++t) tile_first_edge_[t] = first[std::min<long long>(N, static_cast<long long>(t) * T)];
-    // runs: count per tile, scan on the host, fill (an edge's tile from the
-    // tiles' first edges)
-    std::vector<int> tfe(tile_first_edge_.begin(), tile_first_edge_.end());
-    upload(tile_first_edge_dev_, tfe, stream_, &staged_);
-    DeviceBuffer per_source, per_tile, offsets;
-    per_source.reserve(static_cast<std::size_t>(N) * sizeof(int));
-    per_tile.reserve(static_cast<std::size_t>(num_tiles_) * sizeof(int));
-    hip_check(hipMemsetAsync(per_tile.as<void>(), 0, num_tiles_ * sizeof(int), stream_), "memset");
-    hip_check(launch_tile_runs_count(N, tfirst_.as<int>(), tedge_.as<int>(), tile_first_edge_dev_.as<int>(),
-                                     num_tiles_, per_source.as<int>(), per_tile.as<int>(), stream_),
-              "tile runs");
-    std::vector<int> counts(num_tiles_);
-    hip_check(hipMemcpyAsync(counts.data(), per_tile.as<int>(), num_tiles_ * sizeof(int), hipMemcpyDeviceToHost,
-                             stream_),
-              "copy");
-    wait("sync");
-    tile_run_offsets_.assign(num_tiles_ + 1, 0);
-    for (int t = 0; t < num_tiles_; ++t) tile_run_offsets_[t + 1] = tile_run_offsets_[t] + counts[t];
-    const int runs = tile_run_offsets_[num_tiles_];
+    for (int t = 0; t <= num_tiles_; ++t)
+        tile_first_edge_[t] = first[std::min<long long>(N, static_cast<long long>(t) * T)];
+}
+
+// Distinct edge sources of each receiver tile of T receivers, from the
+// graph's sources on the device (caller graphs; the device build counts them
+// in its count pass).
+void Evaluator::count_tile_runs()
+{
+    const int N = num_nodes_;
+    const int T = receiver_limit_ > 0 ? receiver_limit_ : kDefaultTileReceivers;
+    const int tiles = static_cast<int>((static_cast<long long>(N) + T - 1) / T);
+    DeviceBuffer last_tile, counts;
+    last_tile.reserve(static_cast<std::size_t>(std::max(N, 1)) * sizeof(int));
+    counts.reserve(static_cast<std::size_t>(std::max(tiles, 1)) * sizeof(int));
+    hip_check(launch_fill_i32(last_tile.as<int>(), N, -1, stream_), "tile runs");
+    hip_check(launch_fill_i32(counts.as<int>(), tiles, 0, stream_), "tile runs");
+    for (int t = 0; t < tiles; ++t) {
+        const long long base = host_first_[static_cast<std::size_t>(t) * T];
+        const long long end = host_first_[std::min<long long>(N, static_cast<long long>(t + 1) * T)];
+        hip_check(launch_tile_runs_mark(static_cast<int>(end - base), source_.as<int>() + base, t,
+                                        last_tile.as<int>(), nullptr, nullptr, counts.as<int>() + t, stream_),
+                  "tile runs");
+    }
+    tile_runs_.assign(tiles, 0);
+    if (tiles > 0)
+        hip_check(hipMemcpyAsync(tile_runs_.data(), counts.as<int>(), tiles * sizeof(int), hipMemcpyDeviceToHost,
+                                 stream_),
+                  "copy");
+    wait("tile runs");
+}
+
+// Tiled plan, once the sources are on the device: tile-local receiver
+// offsets (first_), each tile's edges grouped by source with ascending
+// tile-local ids (tedge_, at the tile's first edge) and the runs (source,
+// start in the tile's list, length) of every tile.
+void Evaluator::build_tile_lists()
+{
+    const int N = num_nodes_;
+    const int T = tile_receivers_;
+    const int tiles = num_tiles_;
+    std::vector<int> local(static_cast<std::size_t>(N) + tiles);
+    for (int t = 0; t < tiles; ++t) {
+        const long long lo = static_cast<long long>(t) * T;
+        const int count = static_cast<int>(std::min<long long>(T, N - lo));
+        for (int j = 0; j <= count; ++j)
+            local[static_cast<std::size_t>(t) * (T + 1) + j] =
+                static_cast<int>(host_first_[lo + j] - tile_first_edge_[t]);
+    }
+    upload(first_, local, stream_, &staged_);
+    if (static_cast<int>(tile_runs_.size()) != tiles) count_tile_runs();
+    tile_run_offsets_.assign(tiles + 1, 0);
+    int max_runs = 0;
+    for (int t = 0; t < tiles; ++t) {
+        tile_run_offsets_[t + 1] = tile_run_offsets_[t] + tile_runs_[t];
+        max_runs = std::max(max_runs, tile_runs_[t]);
+    }
+    const int runs = tile_run_offsets_[tiles];
+    const long long E = num_edges_;
     run_source_.reserve(static_cast<std::size_t>(std::max(runs, 1)) * sizeof(int));
-    run_start_.reserve(static_cast<std::size_t>(std::max(runs, 1)) * sizeof(int));
+    run_start_.reserve((static_cast<std::size_t>(runs) + 1) * sizeof(int));
     run_length_.reserve(static_cast<std::size_t>(std::max(runs, 1)) * sizeof(int));
-    upload(offsets, tile_run_offsets_, stream_, &staged_);
-    hip_check(hipMemsetAsync(per_tile.as<void>(), 0, num_tiles_ * sizeof(int), stream_), "memset");
-    hip_check(launch_tile_runs_fill(N, tfirst_.as<int>(), tedge_.as<int>(), tile_first_edge_dev_.as<int>(),
-                                    num_tiles_, offsets.as<int>(), per_tile.as<int>(), run_source_.as<int>(),
-                                    run_start_.as<int>(), run_length_.as<int>(), stream_),
-              "tile runs");
-    wait("tile plan");
+    tedge_.reserve(static_cast<std::size_t>(std::max<long long>(E, 1)) * sizeof(int));
+    DeviceBuffer last_tile, run_of, counts, cursors, scan, scan_scratch;
+    last_tile.reserve(static_cast<std::size_t>(std::max(N, 1)) * sizeof(int));
+    run_of.reserve(static_cast<std::size_t>(std::max(N, 1)) * sizeof(int));
+    counts.reserve(static_cast<std::size_t>(std::max(tiles, 1)) * sizeof(int));
+    cursors.reserve(static_cast<std::size_t>(std::max(max_runs, 1)) * sizeof(int));
+    scan.reserve((static_cast<std::size_t>(max_runs) + 1) * sizeof(long long));
+    scan_scratch.reserve(scan_scratch_size(max_runs + 1) * sizeof(long long));
+    hip_check(launch_fill_i32(last_tile.as<int>(), N, -1, stream_), "tile lists");
+    hip_check(launch_fill_i32(counts.as<int>(), tiles, 0, stream_), "tile lists");
+    for (int t = 0; t < tiles; ++t) {
+        const long long base = tile_first_edge_[t];
+        const int n = static_cast<int>(tile_first_edge_[t + 1] - base);
+        const int nr = tile_runs_[t];
+        const int off = tile_run_offsets_[t];
+        const int* src = source_.as<int>() + base;
+        int* start = run_start_.as<int>() + off;
+        hip_check(launch_tile_runs_mark(n, src, t, last_tile.as<int>(), run_of.as<int>(),
+                                        run_source_.as<int>() + off, counts.as<int>() + t, stream_),
+                  "tile runs");
+        hip_check(launch_fill_i32(run_length_.as<int>() + off, nr, 0, stream_), "tile runs");
+        hip_check(launch_tile_runs_length(n, src, run_of.as<int>(), run_length_.as<int>() + off, stream_),
+                  "tile runs");
+        // starts: exclusive scan of the lengths, narrowed into run_start (its
+        // last entry, the tile's edge count, is the next tile's first start
+        // until that tile writes it)
+        hip_check(launch_exclusive_scan_i32(run_length_.as<int>() + off, nr, scan.as<long long>(),
+                                            scan_scratch.as<long long>(), stream_),
+                  "tile runs");
+        hip_check(launch_narrow_offsets(scan.as<long long>(), nr, start, nullptr, stream_), "tile runs");
+        hip_check(launch_fill_i32(cursors.as<int>(), nr, 0, stream_), "tile lists");
+        hip_check(launch_tile_list_fill(n, src, run_of.as<int>(), start, cursors.as<int>(), tedge_.as<int>() + base,
+                                        stream_),
+                  "tile lists");
+        hip_check(launch_sort_segments(nr, start, tedge_.as<int>() + base, stream_), "tile lists");
+    }
+    // every tile must have as many runs as its count said
+    std::vector<int> seen(tiles, 0);
+    if (tiles > 0)
+        hip_check(hipMemcpyAsync(seen.data(), counts.as<int>(), tiles * sizeof(int), hipMemcpyDeviceToHost, stream_),
+                  "copy");
+    wait("tile lists");
+    if (seen != tile_runs_) throw std::logic_error("tile run counts of the graph build and the tile lists differ");
 }
 
 // Device bytes this evaluator holds for graphs and their work arrays (not
@@ -846,7 +980,7 @@ std::size_t Evaluator::held_graph_bytes() const
         &cell_dev_, &xyz_, &r_, &geo_positions_, &geo_edges_, &geo_shifts_, &A0_, &M0_, &H1_, &Phi1_, &A1_,
         &A1adj_, &A0pre_, &direct_, &H1adj_, &msg_, &energies_, &forces_, &atom_forces_, &partials_, &totals_, &scratch_,
         &scale1_, &dot1_, &M0s_, &run_source_, &run_start_, &run_length_, &node_order_, &m0_blocks_, &m0r_blocks_,
-        &readout_blocks_, &tile_xyz_, &tile_r_, &tile_pair_, &tile_forces_, &tile_first_edge_dev_,
+        &readout_blocks_, &tile_xyz_, &tile_r_, &tile_pair_, &tile_forces_,
         &pgraph_.first, &pgraph_.sources, &pgraph_.shifts, &pgraph_.fractional_xyz, &pgraph_.fractional_positions};
     std::size_t total = 0;
     for (const DeviceBuffer* b : buffers) total += b->bytes();
@@ -854,33 +988,40 @@ std::size_t Evaluator::held_graph_bytes() const
 }
 
 // Device bytes of the graph-wide state of the prepared graph.  Both plans:
-// per edge the sources and the source-major list (and for a periodic graph
-// the cell shifts); per node types, offsets, energies, atom forces, H1 and
-// its adjoint, the direct adjoint, positions and displacements (periodic: the
-// build's offsets and fractional positions).  The untiled plan adds per edge
+// per edge the sources (and for a periodic graph the cell shifts, int8 or
+// int32); per node types, receiver offsets, the node order and blocks of
+// the node kernels, energies, atom forces, positions and displacements, H1
+// and its adjoint and the direct adjoint (periodic: the build's fractional
+// positions).  The untiled plan adds per edge the source-major list,
 // receivers, pair codes, geometry and directed forces (periodic: fractional
-// edge vectors); the tiled plan the scalar M0 block per node (and pair codes
-// per edge when a caller's neighbour types differ from its sources').
-std::size_t Evaluator::graph_bytes_estimate(bool tiled) const
+// edge vectors) and per node the source-major offsets; the tiled plan per
+// edge the tiles' source-grouped lists (and pair codes when a caller's
+// neighbour types differ from its sources'), per node the scalar M0 block,
+// and three ints per run.
+std::size_t Evaluator::graph_bytes_estimate(bool tiled, long long runs) const
 {
     const std::size_t N = num_nodes_, E = static_cast<std::size_t>(num_edges_);
-    std::size_t per_edge = 2 * sizeof(int);
-    std::size_t per_node = 4 * sizeof(int) + 4 * sizeof(double) + 2 * static_cast<std::size_t>(nLM_) * C_ * sizeof(float) +
-                           static_cast<std::size_t>(C_) * sizeof(float) + 6 * sizeof(double);
+    const std::size_t C = C_, f = sizeof(float);
+    std::size_t per_edge = sizeof(int);
+    std::size_t per_node = 7 * sizeof(int) + 10 * sizeof(double) + (2 * static_cast<std::size_t>(nLM_) + 1) * C * f;
     if (periodic_) {
-        per_edge += 3 * sizeof(int);
-        per_node += sizeof(int) + 3 * sizeof(double);
+        per_edge += 3 * static_cast<std::size_t>(pgraph_.shift_bytes);
+        per_node += 3 * sizeof(double);
     }
+    std::size_t extra = 0;
     if (!tiled) {
-        per_edge += 2 * sizeof(int) + 7 * sizeof(double);
+        per_edge += 3 * sizeof(int) + 7 * sizeof(double);
         if (periodic_) per_edge += 3 * sizeof(double);
+        per_node += sizeof(int);
     } else {
-        per_node += static_cast<std::size_t>(C_) * sizeof(float);
+        per_edge += sizeof(int);
+        per_node += C * f;
         if (!pair_from_types_) per_edge += sizeof(int);
+        extra += 3 * sizeof(int) * static_cast<std::size_t>(std::max(runs, 0LL));
     }
-    if (model_.A1_scaled) per_node += 2 * sizeof(float);
-    if (model_.pre_linear_up && !tiled) per_node += static_cast<std::size_t>(C_) * sizeof(float);
-    return per_edge * E + per_node * N;
+    if (model_.A1_scaled) per_node += 2 * f;
+    if (model_.pre_linear_up && !tiled) per_node += C * f;
+    return per_edge * E + per_node * N + extra;
 }
 
 // Device bytes of the work arrays for `receivers` receivers and `edges`
@@ -1056,83 +1197,99 @@ void Evaluator::set_workspace_receiver_limit(int receivers)
     receiver_limit_ = receivers;
 }
 
-// Shared tail of both graph preparations: source-major transpose, the
-// execution plan, and for the untiled plan the graph-wide receiver and pair
-// arrays (the tiled plan forms pair codes per tile), node blocks, workspace.
-void Evaluator::finish_graph(const int* host_neigh_types, const int* host_sources)
+// Per-edge state the tiled plan does not keep: released before its edges
+// are written, so a capacity graph never holds both.
+void Evaluator::release_untiled_edge_state()
+{
+    wait("synchronize");
+    receiver_.release();
+    tfirst_.release();
+    edge_pair_.release();
+    xyz_.release();
+    r_.release();
+    forces_.release();
+    msg_.release();
+    pgraph_.fractional_xyz.release();
+}
+
+// Pair codes of a caller's graph from its neighbour types (checked against
+// the model), and whether they follow from the node types.
+std::vector<int> Evaluator::caller_pairs(const int* host_neigh_types, const int* host_sources)
 {
     const int N = num_nodes_;
-    const int E = static_cast<int>(num_edges_);
-    // transpose: count -> scan -> fill -> sort each source segment ascending
-    // (its work arrays live until the preparation's final wait)
-    DeviceBuffer counts, offsets64;
-    {
+    std::vector<int> host_pairs(static_cast<std::size_t>(num_edges_));
+    std::vector<int> ta(model_.num_elements, -1);
+    for (std::size_t a = 0; a < active_types_.size(); ++a) ta[active_types_[a]] = static_cast<int>(a);
+    const int na = static_cast<int>(active_types_.size());
+    pair_from_types_ = true;
+    std::size_t e = 0;
+    for (int i = 0; i < N; ++i) {
+        const int a = ta[host_types_[i]];
+        for (long long j = host_first_[i]; j < host_first_[i + 1]; ++j, ++e) {
+            const int t = host_neigh_types[e];
+            if (t < 0 || t >= model_.num_elements) throw std::out_of_range("MACE radial type index is out of range.");
+            const int b = ta[t];
+            if (b < 0) throw std::runtime_error("MACE radial cache is not prepared for an active type.");
+            if (t != host_types_[host_sources[e]]) pair_from_types_ = false;
+            const int po = a * na + b;
+            const int pu = shared_pair_tables() ? 0 : a <= b ? a * (2 * na - a - 1) / 2 + b : b * (2 * na - b - 1) / 2 + a;
+            host_pairs[e] = po | (pu << 16);
+        }
+    }
+    return host_pairs;
+}
+
+// Shared tail of both graph preparations, once the plan is selected and the
+// sources are on the device.  Untiled: receiver offsets, source-major
+// transpose, receivers and pair codes graph-wide.  Tiled: the tile-local
+// offsets, source-grouped lists and runs (pair codes are formed per tile,
+// or kept graph-wide when a caller's neighbour types differ).  Then the node
+// blocks and the work arrays.
+void Evaluator::finish_graph(const std::vector<int>& host_pairs)
+{
+    const int N = num_nodes_;
+    const long long E = num_edges_;
+    if (tile_receivers_ == 0) {
+        run_source_.release();
+        run_start_.release();
+        run_length_.release();
+        const int Ei = static_cast<int>(E);  // the untiled plan's edges fit its 32-bit index
+        std::vector<int> first(host_first_.begin(), host_first_.end());
+        upload(first_, first, stream_, &staged_);
+        // transpose: count -> scan -> fill -> sort each source segment ascending
+        // (its work arrays live until the preparation's final wait)
+        DeviceBuffer counts, offsets64;
         counts.reserve((N + 1) * sizeof(int));
         offsets64.reserve((N + 1) * sizeof(long long));
         scratch_.reserve(scan_scratch_size(N + 1) * sizeof(long long));
         hip_check(hipMemsetAsync(counts.as<void>(), 0, (N + 1) * sizeof(int), stream_), "memset");
-        hip_check(launch_transpose_count(E, source_.as<int>(), counts.as<int>(), stream_), "transpose");
+        hip_check(launch_transpose_count(Ei, source_.as<int>(), counts.as<int>(), stream_), "transpose");
         hip_check(launch_exclusive_scan_i32(counts.as<int>(), N, offsets64.as<long long>(),
                                             scratch_.as<long long>(), stream_),
                   "scan");
         tfirst_.reserve((N + 1) * sizeof(int));
         hip_check(launch_narrow_offsets(offsets64.as<long long>(), N, tfirst_.as<int>(), nullptr, stream_),
                   "narrow");
-        tedge_.reserve(static_cast<std::size_t>(std::max(E, 1)) * sizeof(int));
+        tedge_.reserve(static_cast<std::size_t>(std::max(Ei, 1)) * sizeof(int));
         hip_check(hipMemsetAsync(counts.as<void>(), 0, (N + 1) * sizeof(int), stream_), "memset");
-        hip_check(launch_transpose_fill(E, source_.as<int>(), tfirst_.as<int>(), counts.as<int>(),
+        hip_check(launch_transpose_fill(Ei, source_.as<int>(), tfirst_.as<int>(), counts.as<int>(),
                                         tedge_.as<int>(), stream_),
                   "transpose fill");
         hip_check(launch_sort_segments(N, tfirst_.as<int>(), tedge_.as<int>(), stream_), "sort");
-    }
-    // caller-provided source types (prepare_graph): checked, and the pair
-    // codes formed on the host; they follow from the node types unless a
-    // neighbour type differs from its source's type
-    std::vector<int> host_pairs;
-    pair_from_types_ = true;
-    if (host_neigh_types) {
-        std::vector<int> ta(model_.num_elements, -1);
-        for (std::size_t a = 0; a < active_types_.size(); ++a) ta[active_types_[a]] = static_cast<int>(a);
-        const int na = static_cast<int>(active_types_.size());
-        host_pairs.resize(E);
-        std::size_t e = 0;
-        const std::vector<int>& first = host_first_;
-        for (int i = 0; i < N; ++i) {
-            const int a = ta[host_types_[i]];
-            for (int j = first[i]; j < first[i + 1]; ++j, ++e) {
-                const int t = host_neigh_types[e];
-                if (t < 0 || t >= model_.num_elements) throw std::out_of_range("MACE radial type index is out of range.");
-                const int b = ta[t];
-                if (b < 0) throw std::runtime_error("MACE radial cache is not prepared for an active type.");
-                if (t != host_types_[host_sources[e]]) pair_from_types_ = false;
-                const int po = a * na + b;
-                const int pu = shared_pair_tables() ? 0 : a <= b ? a * (2 * na - a - 1) / 2 + b : b * (2 * na - b - 1) / 2 + a;
-                host_pairs[e] = po | (pu << 16);
-            }
-        }
-    }
-    plan_tiles();
-    if (tile_receivers_ == 0) {
-        receiver_.reserve(static_cast<std::size_t>(std::max(E, 1)) * sizeof(int));
+        receiver_.reserve(static_cast<std::size_t>(std::max(Ei, 1)) * sizeof(int));
         hip_check(launch_receivers(N, first_.as<int>(), receiver_.as<int>(), stream_), "receivers");
-        if (host_neigh_types) {
+        if (!host_pairs.empty()) {
             upload(edge_pair_, host_pairs, stream_, &staged_);
         } else {
-            edge_pair_.reserve(static_cast<std::size_t>(std::max(E, 1)) * sizeof(int));
-            hip_check(launch_edge_pairs(E, receiver_.as<int>(), source_.as<int>(), node_types_.as<int>(),
+            edge_pair_.reserve(static_cast<std::size_t>(std::max(Ei, 1)) * sizeof(int));
+            hip_check(launch_edge_pairs(Ei, receiver_.as<int>(), source_.as<int>(), node_types_.as<int>(),
                                         type_active_.as<int>(), static_cast<int>(active_types_.size()),
                                         shared_pair_tables(), edge_pair_.as<int>(), stream_),
                       "edge pairs");
         }
     } else {
-        // graph-wide per-edge state of the untiled plan is not kept
-        wait("synchronize");
-        receiver_.release();
-        if (pair_from_types_)
-            edge_pair_.release();
-        else
-            upload(edge_pair_, host_pairs, stream_, &staged_);
-        if (periodic_) pgraph_.fractional_xyz.release();  // edges from cell shifts instead
+        if (!pair_from_types_) upload(edge_pair_, host_pairs, stream_, &staged_);
+        build_tile_lists();
     }
     plan_node_blocks();
     allocate_workspace();
@@ -1147,6 +1304,15 @@ void Evaluator::finish_graph(const int* host_neigh_types, const int* host_source
     stats_.num_tiles = num_tiles_;
 }
 
+// Tiles counted for the graph being prepared: only when a tiled plan could
+// be chosen (fixed workspace allowed or pinned, more nodes than one tile).
+bool Evaluator::tiles_possible(int num_nodes) const
+{
+    const int T = receiver_limit_ > 0 ? receiver_limit_ : kDefaultTileReceivers;
+    return (allow_fixed_workspace_ || plan_debug_ == "mh0-dual-layer-tiled-v1") && num_nodes > T &&
+           plan_debug_ != "mh0-direct-speed" && plan_profile_ != "speed";
+}
+
 std::uint64_t Evaluator::prepare_graph(int num_nodes, const int* node_types, const int* num_neigh,
                                        const int* neigh_indices, const int* neigh_types)
 {
@@ -1155,13 +1321,13 @@ std::uint64_t Evaluator::prepare_graph(int num_nodes, const int* node_types, con
         throw std::length_error("MACE graph atom count exceeds the 32-bit CSR limit.");
     std::vector<int> types(node_types, node_types + num_nodes);
     long long E = 0;
-    std::vector<int> first(num_nodes + 1, 0);
+    std::vector<long long> first(num_nodes + 1, 0);
     for (int i = 0; i < num_nodes; ++i) {
         if (num_neigh[i] < 0) throw std::invalid_argument("num_neigh must be non-negative.");
         E += num_neigh[i];
         if (E > std::numeric_limits<int>::max())
             throw std::length_error("MACE graph directed-edge count exceeds the 32-bit topology limit.");
-        first[i + 1] = static_cast<int>(E);
+        first[i + 1] = E;
     }
     for (long long e = 0; e < E; ++e)
         if (neigh_indices[e] < 0 || neigh_indices[e] >= num_nodes)
@@ -1174,15 +1340,19 @@ std::uint64_t Evaluator::prepare_graph(int num_nodes, const int* node_types, con
     num_nodes_ = num_nodes;
     num_edges_ = E;
     periodic_ = false;
-    upload(node_types_, types, stream_, &staged_);
-    upload(first_, first, stream_, &staged_);
     host_first_ = std::move(first);
+    upload(node_types_, types, stream_, &staged_);
     std::vector<int> src(neigh_indices, neigh_indices + E);
     upload(source_, src, stream_, &staged_);
     positions_.reserve(static_cast<std::size_t>(std::max(num_nodes, 1)) * 3 * sizeof(double));
     disp_.reserve(static_cast<std::size_t>(std::max(num_nodes, 1)) * 3 * sizeof(double));
     geometry_mode_ = kGeometryNone;
-    finish_graph(neigh_types, neigh_indices);
+    std::vector<int> pairs = caller_pairs(neigh_types, neigh_indices);
+    tile_runs_.clear();
+    if (tiles_possible(num_nodes)) count_tile_runs();
+    select_plan();
+    if (tile_receivers_ > 0) release_untiled_edge_state();
+    finish_graph(pairs);
     account_preparation(start);
     return generation_;
 }
@@ -1240,77 +1410,129 @@ NeighborPlan neighbor_plan(int num_nodes, const double* cell, const double* inve
 
 int neighbor_plan_bins(const NeighborPlan& plan) { return plan.bins[0] * plan.bins[1] * plan.bins[2]; }
 
-void build_periodic_graph(const double* d_positions, int num_nodes, const double* cell, const double* inverse_cell,
-                          double cutoff, hipStream_t stream, PeriodicGraph& out, std::vector<int>* host_first)
+void count_periodic_graph(const double* d_positions, int num_nodes, const double* cell, const double* inverse_cell,
+                          double cutoff, hipStream_t stream, DeviceBuffer& fractional_positions, PeriodicCount& c,
+                          int tile_receivers)
 {
-    const NeighborPlan plan = neighbor_plan(num_nodes, cell, inverse_cell, cutoff);
+    c.plan = neighbor_plan(num_nodes, cell, inverse_cell, cutoff);
+    const NeighborPlan& plan = c.plan;
     const int N = num_nodes;
     const int num_bins = neighbor_plan_bins(plan);
-    DeviceBuffer wp, wf, wrap, atom_bins, bin_sizes, bin_off64, bin_offsets, bin_atoms, counts, offsets, scratch;
+    DeviceBuffer bin_sizes, bin_off64, counts, scratch, small, last_tile;
     const std::size_t N3 = static_cast<std::size_t>(std::max(N, 1)) * 3;
-    out.fractional_positions.reserve(N3 * sizeof(double));
-    wp.reserve(N3 * sizeof(double));
-    wf.reserve(N3 * sizeof(double));
-    wrap.reserve(N3 * sizeof(int));
-    atom_bins.reserve(std::max(N, 1) * sizeof(int));
+    fractional_positions.reserve(N3 * sizeof(double));
+    c.wp.reserve(N3 * sizeof(double));
+    c.wf.reserve(N3 * sizeof(double));
+    c.wrap.reserve(N3 * sizeof(int));
+    c.atom_bins.reserve(std::max(N, 1) * sizeof(int));
     bin_sizes.reserve((num_bins + 1) * sizeof(int));
     bin_off64.reserve((num_bins + 1) * sizeof(long long));
-    bin_offsets.reserve((num_bins + 1) * sizeof(int));
-    bin_atoms.reserve(std::max(N, 1) * sizeof(int));
+    c.bin_offsets.reserve((num_bins + 1) * sizeof(int));
+    c.bin_atoms.reserve(std::max(N, 1) * sizeof(int));
     counts.reserve(std::max(N, 1) * sizeof(long long));
-    offsets.reserve((N + 1) * sizeof(long long));
+    c.offsets.reserve((static_cast<std::size_t>(N) + 1) * sizeof(long long));
     scratch.reserve(scan_scratch_size(std::max(num_bins, N) + 1) * sizeof(long long));
+    const int tiles = tile_receivers > 0 && N > 0 ? static_cast<int>((static_cast<long long>(N) + tile_receivers - 1) /
+                                                                     tile_receivers)
+                                                  : 0;
+    // small: [0] largest shift component, [1..tiles] distinct sources per tile
+    small.reserve((1 + static_cast<std::size_t>(tiles)) * sizeof(int));
+    hip_check(launch_fill_i32(small.as<int>(), 1 + tiles, 0, stream), "clear");
     hip_check(hipMemsetAsync(bin_sizes.as<void>(), 0, (num_bins + 1) * sizeof(int), stream), "memset");
-    hip_check(launch_neighbor_bins(plan, d_positions, out.fractional_positions.as<double>(), wp.as<double>(),
-                                   wf.as<double>(), wrap.as<int>(), atom_bins.as<int>(), bin_sizes.as<int>(), stream),
+    hip_check(launch_neighbor_bins(plan, d_positions, fractional_positions.as<double>(), c.wp.as<double>(),
+                                   c.wf.as<double>(), c.wrap.as<int>(), c.atom_bins.as<int>(), bin_sizes.as<int>(),
+                                   stream),
               "bins");
     hip_check(launch_exclusive_scan_i32(bin_sizes.as<int>(), num_bins, bin_off64.as<long long>(),
                                         scratch.as<long long>(), stream),
               "bin scan");
-    hip_check(launch_narrow_offsets(bin_off64.as<long long>(), num_bins, bin_offsets.as<int>(), nullptr, stream),
+    hip_check(launch_narrow_offsets(bin_off64.as<long long>(), num_bins, c.bin_offsets.as<int>(), nullptr, stream),
               "narrow");
     // cursors start at the bin offsets
-    hip_check(hipMemcpyAsync(bin_sizes.as<int>(), bin_offsets.as<int>(), num_bins * sizeof(int),
+    hip_check(hipMemcpyAsync(bin_sizes.as<int>(), c.bin_offsets.as<int>(), num_bins * sizeof(int),
                              hipMemcpyDeviceToDevice, stream),
               "cursors");
-    hip_check(launch_neighbor_fill_bins(plan, atom_bins.as<int>(), bin_offsets.as<int>(), bin_sizes.as<int>(),
-                                        bin_atoms.as<int>(), stream),
+    hip_check(launch_neighbor_fill_bins(plan, c.atom_bins.as<int>(), c.bin_offsets.as<int>(), bin_sizes.as<int>(),
+                                        c.bin_atoms.as<int>(), stream),
               "fill bins");
-    hip_check(launch_sort_segments(num_bins, bin_offsets.as<int>(), bin_atoms.as<int>(), stream), "sort bins");
-    hip_check(launch_neighbor_edges(plan, wp.as<double>(), wf.as<double>(), wrap.as<int>(), atom_bins.as<int>(),
-                                    bin_offsets.as<int>(), bin_atoms.as<int>(), nullptr, counts.as<long long>(),
-                                    nullptr, nullptr, nullptr, stream),
-              "count edges");
-    hip_check(launch_exclusive_scan_i64(counts.as<long long>(), N, offsets.as<long long>(), scratch.as<long long>(),
+    hip_check(launch_sort_segments(num_bins, c.bin_offsets.as<int>(), c.bin_atoms.as<int>(), stream), "sort bins");
+    EdgeOutputs o;
+    o.counts = counts.as<long long>();
+    o.max_shift = small.as<int>();
+    if (tiles > 0) {
+        // receiver tiles in order, each marking the sources it has seen
+        last_tile.reserve(std::max(N, 1) * sizeof(int));
+        hip_check(launch_fill_i32(last_tile.as<int>(), N, -1, stream), "clear");
+        o.last_tile = last_tile.as<int>();
+        for (int t = 0; t < tiles; ++t) {
+            o.tile = t;
+            o.tile_runs = small.as<int>() + 1 + t;
+            const int begin = t * tile_receivers;
+            hip_check(launch_neighbor_edges(plan, c.wp.as<double>(), c.wf.as<double>(), c.wrap.as<int>(),
+                                            c.atom_bins.as<int>(), c.bin_offsets.as<int>(), c.bin_atoms.as<int>(),
+                                            begin, std::min(tile_receivers, N - begin), o, stream),
+                      "count edges");
+        }
+    } else {
+        hip_check(launch_neighbor_edges(plan, c.wp.as<double>(), c.wf.as<double>(), c.wrap.as<int>(),
+                                        c.atom_bins.as<int>(), c.bin_offsets.as<int>(), c.bin_atoms.as<int>(), 0, N,
+                                        o, stream),
+                  "count edges");
+    }
+    hip_check(launch_exclusive_scan_i64(counts.as<long long>(), N, c.offsets.as<long long>(), scratch.as<long long>(),
                                         stream),
               "edge scan");
-    long long total = 0;
-    hip_check(hipMemcpyAsync(&total, offsets.as<long long>() + N, sizeof(long long), hipMemcpyDeviceToHost, stream),
+    c.host_first.resize(static_cast<std::size_t>(N) + 1);
+    hip_check(hipMemcpyAsync(c.host_first.data(), c.offsets.as<long long>(), (N + 1) * sizeof(long long),
+                             hipMemcpyDeviceToHost, stream),
+              "offsets copy");
+    std::vector<int> small_host(1 + tiles);
+    hip_check(hipMemcpyAsync(small_host.data(), small.as<int>(), (1 + tiles) * sizeof(int), hipMemcpyDeviceToHost,
+                             stream),
               "copy");
     hip_check(host_fence(stream), "edge count");
-    if (total > std::numeric_limits<int>::max())
-        throw std::length_error("neighbor graph exceeds 32-bit edge indexing");
-    const int E = static_cast<int>(total);
-    out.first.reserve((N + 1) * sizeof(int));
-    hip_check(launch_narrow_offsets(offsets.as<long long>(), N, out.first.as<int>(), nullptr, stream), "narrow");
-    out.sources.reserve(static_cast<std::size_t>(std::max(E, 1)) * sizeof(int));
-    // sizes in size_t: 3 E overflows 32 bits beyond ~1.43 G edges
-    out.shifts.reserve(static_cast<std::size_t>(std::max(E, 1)) * 3 * sizeof(int));
-    out.fractional_xyz.reserve(static_cast<std::size_t>(std::max(E, 1)) * 3 * sizeof(double));
-    hip_check(launch_neighbor_edges(plan, wp.as<double>(), wf.as<double>(), wrap.as<int>(), atom_bins.as<int>(),
-                                    bin_offsets.as<int>(), bin_atoms.as<int>(), offsets.as<long long>(), nullptr,
-                                    out.sources.as<int>(), out.shifts.as<int>(), out.fractional_xyz.as<double>(),
-                                    stream),
+    c.num_edges = c.host_first[N];
+    c.max_shift = small_host[0];
+    c.tile_receivers = tiles > 0 ? tile_receivers : 0;
+    c.tile_runs.assign(small_host.begin() + 1, small_host.end());
+}
+
+void fill_periodic_graph(const PeriodicCount& c, hipStream_t stream, int* sources, int* shifts, signed char* shifts8,
+                         double* fractional_xyz)
+{
+    EdgeOutputs o;
+    o.offsets = c.offsets.as<long long>();
+    o.sources = sources;
+    o.shifts = shifts;
+    o.shifts8 = shifts8;
+    o.frac = fractional_xyz;
+    hip_check(launch_neighbor_edges(c.plan, c.wp.as<double>(), c.wf.as<double>(), c.wrap.as<int>(),
+                                    c.atom_bins.as<int>(), c.bin_offsets.as<int>(), c.bin_atoms.as<int>(), 0,
+                                    c.plan.num_nodes, o, stream),
               "fill edges");
-    if (host_first) {
-        host_first->resize(static_cast<std::size_t>(N) + 1);
-        hip_check(hipMemcpyAsync(host_first->data(), out.first.as<int>(), (N + 1) * sizeof(int),
-                                 hipMemcpyDeviceToHost, stream),
-                  "offsets copy");
-    }
+}
+
+void build_periodic_graph(const double* d_positions, int num_nodes, const double* cell, const double* inverse_cell,
+                          double cutoff, hipStream_t stream, PeriodicGraph& out)
+{
+    PeriodicCount c;
+    count_periodic_graph(d_positions, num_nodes, cell, inverse_cell, cutoff, stream, out.fractional_positions, c, 0);
+    if (c.num_edges > std::numeric_limits<int>::max())
+        throw std::length_error("neighbor graph exceeds 32-bit edge indexing");
+    const int N = num_nodes;
+    const std::size_t E = static_cast<std::size_t>(std::max<long long>(c.num_edges, 1));
+    out.first.reserve((N + 1) * sizeof(int));
+    hip_check(launch_narrow_offsets(c.offsets.as<long long>(), N, out.first.as<int>(), nullptr, stream), "narrow");
+    out.sources.reserve(E * sizeof(int));
+    // sizes in size_t: 3 E overflows 32 bits beyond ~1.43 G edges
+    out.shifts.reserve(E * 3 * sizeof(int));
+    out.shift_bytes = 4;
+    out.fractional_xyz.reserve(E * 3 * sizeof(double));
+    fill_periodic_graph(c, stream, out.sources.as<int>(), out.shifts.as<int>(), nullptr,
+                        out.fractional_xyz.as<double>());
     hip_check(host_fence(stream), "graph build");
     out.num_nodes = N;
-    out.num_edges = E;
+    out.num_edges = c.num_edges;
 }
 
 std::uint64_t Evaluator::prepare_periodic_graph(int num_nodes, const int* node_types, const double* positions,
@@ -1331,24 +1553,42 @@ std::uint64_t Evaluator::prepare_periodic_graph(int num_nodes, const int* node_t
                                  device_positions ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, stream_),
                   "positions");
     disp_.reserve(static_cast<std::size_t>(std::max(N, 1)) * 3 * sizeof(double));
-    build_periodic_graph(positions_.as<double>(), N, cell, inverse_cell, cutoff, stream_, pgraph_, &host_first_);
-    const int E = static_cast<int>(pgraph_.num_edges);
-    first_.reserve((N + 1) * sizeof(int));
-    hip_check(hipMemcpyAsync(first_.as<int>(), pgraph_.first.as<int>(), (N + 1) * sizeof(int),
-                             hipMemcpyDeviceToDevice, stream_),
-              "copy");
-    // the build's source array becomes the graph's (no copy)
-    source_.swap(pgraph_.sources);
-    pgraph_.sources.release();
+    // count pass (with the distinct sources per tile when a tiled plan could
+    // be chosen), then the plan, then the edges it needs
+    auto count = std::make_unique<PeriodicCount>();
+    const int T = receiver_limit_ > 0 ? receiver_limit_ : kDefaultTileReceivers;
+    count_periodic_graph(positions_.as<double>(), N, cell, inverse_cell, cutoff, stream_,
+                         pgraph_.fractional_positions, *count, tiles_possible(N) ? T : 0);
     host_types_ = types;
     num_nodes_ = N;
-    num_edges_ = E;
+    num_edges_ = count->num_edges;
+    host_first_ = std::move(count->host_first);
+    tile_runs_ = count->tile_runs;
     periodic_ = true;
+    pair_from_types_ = true;
+    pgraph_.shift_bytes = count->max_shift <= 127 ? 1 : 4;
     std::memcpy(cell_, cell, sizeof(cell_));
     std::memcpy(inverse_cell_, inverse_cell, sizeof(inverse_cell_));
+    select_plan();
+    const bool tiled = tile_receivers_ > 0;
+    if (tiled) release_untiled_edge_state();
+    const std::size_t E = static_cast<std::size_t>(std::max<long long>(num_edges_, 1));
+    source_.reserve(E * sizeof(int));
+    pgraph_.shifts.reserve(E * 3 * static_cast<std::size_t>(pgraph_.shift_bytes));
+    // the untiled plan forms edge vectors from the build's fractional ones;
+    // the tiled plan forms them per tile from the shifts (bit for bit)
+    if (!tiled) pgraph_.fractional_xyz.reserve(E * 3 * sizeof(double));
+    fill_periodic_graph(*count, stream_, source_.as<int>(), pgraph_.shift_bytes == 4 ? pgraph_.shifts.as<int>() : nullptr,
+                        pgraph_.shift_bytes == 1 ? pgraph_.shifts.as<signed char>() : nullptr,
+                        tiled ? nullptr : pgraph_.fractional_xyz.as<double>());
+    pgraph_.first.release();
+    pgraph_.sources.release();
+    pgraph_.num_nodes = N;
+    pgraph_.num_edges = num_edges_;
     upload(node_types_, types, stream_, &staged_);
     upload_cell();
-    finish_graph(nullptr, nullptr);
+    finish_graph({});
+    count.reset();  // the count's work arrays (finish_graph has waited for the fill)
     // the build's fractional positions and edge vectors are the graph's geometry
     geometry_mode_ = kGeometryBuilt;
     geometry_generation_ = generation_;
@@ -1491,13 +1731,18 @@ GeometryRef Evaluator::geometry_ref() const
     GeometryRef g;
     if (geometry_mode_ == kGeometryBuilt) {
         // the build's fractional positions with its fractional edge vectors,
-        // or (tiled plan, which does not keep those) with its cell shifts
+        // or (tiled plan, which does not keep those) with its cell shifts,
+        // from which the same vectors are formed
         g.positions = pgraph_.fractional_positions.as<double>();
-        if (pgraph_.fractional_xyz.bytes() > 0)
+        if (pgraph_.fractional_xyz.bytes() > 0) {
             g.edges = pgraph_.fractional_xyz.as<double>();
-        else
+        } else if (pgraph_.shift_bytes == 1) {
+            g.shifts8 = pgraph_.shifts.as<signed char>();
+        } else {
             g.shifts = pgraph_.shifts.as<int>();
+        }
         g.fractional = 1;
+        g.built = 1;
         g.pbc = 7;
         return g;
     }
@@ -1524,45 +1769,65 @@ void Evaluator::graph_arrays(std::uint64_t generation, int* num_neigh, int* rece
     check_generation(generation);
     const int N = num_nodes_;
     const long long E = num_edges_;
-    std::vector<int> first(N + 1);
-    hip_check(hipMemcpyAsync(first.data(), first_.as<int>(), (N + 1) * sizeof(int), hipMemcpyDeviceToHost, stream_),
-              "copy");
+    // the arrays are int32 CSR: as the reference, graphs beyond it are not
+    // exported (symmetrix/source/symmetrix/calculator.py:88-104)
+    if (E > edge_index_limit_)
+        throw std::length_error("MACE graph directed-edge count exceeds the 32-bit topology limit.");
+    const std::size_t En = static_cast<std::size_t>(E);
     if (sources && E)
-        hip_check(hipMemcpyAsync(sources, source_.as<int>(), E * sizeof(int), hipMemcpyDeviceToHost, stream_), "copy");
-    if (periodic_) {
-        if (shifts && E)
-            hip_check(hipMemcpyAsync(shifts, pgraph_.shifts.as<int>(), E * 3 * sizeof(int), hipMemcpyDeviceToHost,
+        hip_check(hipMemcpyAsync(sources, source_.as<int>(), En * sizeof(int), hipMemcpyDeviceToHost, stream_), "copy");
+    std::vector<int> sh;
+    std::vector<int> src;
+    std::vector<double> frac;
+    const bool rebuild_frac = periodic_ && fractional_xyz && E && pgraph_.fractional_xyz.bytes() == 0;
+    if (periodic_ && E && (shifts || rebuild_frac)) {
+        if (pgraph_.shift_bytes == 1) {
+            std::vector<signed char> s8(3 * En);
+            hip_check(hipMemcpyAsync(s8.data(), pgraph_.shifts.as<signed char>(), 3 * En, hipMemcpyDeviceToHost,
                                      stream_),
                       "copy");
-        if (fractional_xyz && E && pgraph_.fractional_xyz.bytes() > 0)
-            hip_check(hipMemcpyAsync(fractional_xyz, pgraph_.fractional_xyz.as<double>(), E * 3 * sizeof(double),
+            hip_check(host_fence(stream_), "graph copy");
+            sh.assign(s8.begin(), s8.end());
+        } else {
+            sh.resize(3 * En);
+            hip_check(hipMemcpyAsync(sh.data(), pgraph_.shifts.as<int>(), 3 * En * sizeof(int),
                                      hipMemcpyDeviceToHost, stream_),
                       "copy");
+        }
     }
-    hip_check(host_fence(stream_), "graph copy");
-    if (receiver_offsets) std::copy(first.begin(), first.end(), receiver_offsets);
-    if (num_neigh)
-        for (int i = 0; i < N; ++i) num_neigh[i] = first[i + 1] - first[i];
-    if (periodic_ && fractional_xyz && E && pgraph_.fractional_xyz.bytes() == 0) {
-        // the tiled plan keeps the cell shifts only: the fractional edge
-        // vector is the fractional position difference plus the shift (equal
-        // to the build's value up to rounding)
-        std::vector<int> src(E), sh(3 * E);
-        std::vector<double> frac(3 * static_cast<std::size_t>(N));
-        hip_check(hipMemcpyAsync(src.data(), source_.as<int>(), E * sizeof(int), hipMemcpyDeviceToHost, stream_),
+    if (periodic_ && fractional_xyz && E && !rebuild_frac)
+        hip_check(hipMemcpyAsync(fractional_xyz, pgraph_.fractional_xyz.as<double>(), 3 * En * sizeof(double),
+                                 hipMemcpyDeviceToHost, stream_),
                   "copy");
-        hip_check(hipMemcpyAsync(sh.data(), pgraph_.shifts.as<int>(), E * 3 * sizeof(int), hipMemcpyDeviceToHost,
-                                 stream_),
+    if (rebuild_frac) {
+        src.resize(En);
+        frac.resize(3 * static_cast<std::size_t>(N));
+        hip_check(hipMemcpyAsync(src.data(), source_.as<int>(), En * sizeof(int), hipMemcpyDeviceToHost, stream_),
                   "copy");
         hip_check(hipMemcpyAsync(frac.data(), pgraph_.fractional_positions.as<double>(), N * 3 * sizeof(double),
                                  hipMemcpyDeviceToHost, stream_),
                   "copy");
-        hip_check(host_fence(stream_), "graph copy");
+    }
+    hip_check(host_fence(stream_), "graph copy");
+    if (receiver_offsets)
+        for (int i = 0; i <= N; ++i) receiver_offsets[i] = static_cast<int>(host_first_[i]);
+    if (num_neigh)
+        for (int i = 0; i < N; ++i) num_neigh[i] = static_cast<int>(host_first_[i + 1] - host_first_[i]);
+    if (shifts && periodic_ && E) std::copy(sh.begin(), sh.end(), shifts);
+    if (rebuild_frac) {
+        // the tiled plan keeps the cell shifts only: the fractional edge
+        // vector is formed as the build formed it (positions wrapped to
+        // [0, 1), their difference, plus the image), so it equals the
+        // build's value bit for bit
         for (int i = 0; i < N; ++i)
-            for (long long e = first[i]; e < first[i + 1]; ++e)
-                for (int a = 0; a < 3; ++a)
-                    fractional_xyz[3 * e + a] = frac[3 * static_cast<std::size_t>(src[e]) + a] -
-                                                frac[3 * static_cast<std::size_t>(i) + a] + sh[3 * e + a];
+            for (long long e = host_first_[i]; e < host_first_[i + 1]; ++e)
+                for (int a = 0; a < 3; ++a) {
+                    const double pj = frac[3 * static_cast<std::size_t>(src[e]) + a];
+                    const double pi = frac[3 * static_cast<std::size_t>(i) + a];
+                    const double fj = std::floor(pj), fi = std::floor(pi);
+                    const int image = sh[3 * e + a] + static_cast<int>(fj) - static_cast<int>(fi);
+                    fractional_xyz[3 * e + a] = ((pj - fj) - (pi - fi)) + static_cast<double>(image);
+                }
     }
 }
 
@@ -1612,18 +1877,31 @@ void Evaluator::compute_xyz(std::uint64_t generation, const double* xyz, const d
     const CallStart start;
     check_generation(generation);
     const long long E = num_edges_;
-    const hipMemcpyKind kind = device_arrays ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
-    // the tiled plan copies each tile's edges from these graph-wide arrays
-    xyz_.reserve(static_cast<std::size_t>(std::max<long long>(E, 1)) * 3 * sizeof(double));
-    r_.reserve(static_cast<std::size_t>(std::max<long long>(E, 1)) * sizeof(double));
-    if (E > 0) {
-        hip_check(hipMemcpyAsync(xyz_.as<double>(), xyz, E * 3 * sizeof(double), kind, stream_), "xyz");
-        hip_check(hipMemcpyAsync(r_.as<double>(), r, E * sizeof(double), kind, stream_), "r");
+    if (tile_receivers_ > 0) {
+        // the tiled plan copies each tile's slice of the caller's arrays into
+        // its arena during this call; nothing is kept graph-wide
+        explicit_xyz_ = xyz;
+        explicit_r_ = r;
+        explicit_device_ = device_arrays;
+    } else {
+        const hipMemcpyKind kind = device_arrays ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+        xyz_.reserve(static_cast<std::size_t>(std::max<long long>(E, 1)) * 3 * sizeof(double));
+        r_.reserve(static_cast<std::size_t>(std::max<long long>(E, 1)) * sizeof(double));
+        if (E > 0) {
+            hip_check(hipMemcpyAsync(xyz_.as<double>(), xyz, E * 3 * sizeof(double), kind, stream_), "xyz");
+            hip_check(hipMemcpyAsync(r_.as<double>(), r, E * sizeof(double), kind, stream_), "r");
+        }
     }
     for (int i = 0; i < kNumStages; ++i) stage_used_[i] = false;
     check_geometry_ = false;
     explicit_geometry_ = true;
-    evaluate();
+    try {
+        evaluate();
+    } catch (...) {
+        explicit_xyz_ = explicit_r_ = nullptr;
+        throw;
+    }
+    explicit_xyz_ = explicit_r_ = nullptr;
     account_evaluation(start);
 }
 
@@ -1994,22 +2272,18 @@ void Evaluator::evaluate_tiled()
 {
     const auto t0 = std::chrono::steady_clock::now();
     const int N = num_nodes_;
-    const int E = static_cast<int>(num_edges_);
     const int T = tile_receivers_;
     LayerArgs la;
     la.graph.num_nodes = N;
-    la.graph.num_edges = E;
     la.graph.node_types = node_types_.as<int>();
     la.graph.type_active = type_active_.as<int>();
     la.graph.num_active = static_cast<int>(active_types_.size());
-    la.graph.first = first_.as<int>();
     la.graph.receiver = nullptr;  // not kept by the tiled plan
-    la.graph.source = source_.as<int>();
-    la.graph.tfirst = tfirst_.as<int>();
-    la.graph.tedge = tedge_.as<int>();
+    la.graph.tfirst = nullptr;
     la.graph.edge_pair = tile_pair_.as<int>();
     la.graph.xyz = tile_xyz_.as<double>();
     la.graph.r = tile_r_.as<double>();
+    la.graph.edge_base = 0;  // every edge array is passed from the tile's first edge on
     la.grid = grid_;
     la.C = C_;
     la.l_max = model_.l_max;
@@ -2026,37 +2300,56 @@ void Evaluator::evaluate_tiled()
     double* virial = totals_.as<double>() + 16;  // [16] unused, [17..25] -sum f (x) xyz
     // the tile's geometry: the caller's edge vectors, or the prepared
     // geometry with the displacements of this evaluation
+    const bool in_arena = explicit_geometry_;
+    if (in_arena && num_edges_ > 0 && !(explicit_xyz_ && explicit_r_))
+        throw std::logic_error("tiled evaluation from edge vectors without the caller's arrays");
+    const GeometryRef ref = in_arena ? GeometryRef{} : geometry_ref();
     TileGeometry tg;
-    tg.first = first_.as<int>();
-    tg.source = source_.as<int>();
     tg.node_types = node_types_.as<int>();
     tg.type_active = type_active_.as<int>();
     tg.num_active = static_cast<int>(active_types_.size());
     tg.shared_tables = shared_pair_tables();
-    tg.pair_source = pair_from_types_ ? nullptr : edge_pair_.as<int>();
-    if (explicit_geometry_) {
-        tg.explicit_xyz = xyz_.as<double>();
-        tg.explicit_r = r_.as<double>();
-    } else {
-        tg.ref = geometry_ref();
-        tg.disp = disp_.as<double>();
-        tg.cell = cell_dev_.as<double>();
-    }
+    tg.in_arena = in_arena;
+    tg.disp = disp_.as<double>();
+    tg.cell = cell_dev_.as<double>();
     tg.r_cut = model_.r_cut;
     tg.xyz = tile_xyz_.as<double>();
     tg.r = tile_r_.as<double>();
     tg.edge_pair = tile_pair_.as<int>();
+    tg.edge_base = 0;
     auto tile = [&](int t, bool count_invalid) {
+        // tile-local offsets (first_ + t, indexed by graph receiver ids) and
+        // the graph-wide edge arrays from the tile's first edge on
+        const long long base = tile_first_edge_[t];
+        const long long tile_edges = tile_first_edge_[t + 1] - base;
         la.node_offset = t * T;
         la.node_count = std::min(T, N - t * T);
         la.local_base = la.node_offset;
-        la.graph.edge_base = tile_first_edge_[t];
+        la.graph.num_edges = static_cast<int>(tile_edges);
+        la.graph.first = first_.as<int>() + t;
+        la.graph.source = source_.as<int>() + base;
+        la.graph.tedge = tedge_.as<int>() + base;
         tg.node_begin = la.node_offset;
         tg.node_count = la.node_count;
-        tg.edge_base = la.graph.edge_base;
+        tg.first = la.graph.first;
+        tg.source = la.graph.source;
+        tg.pair_source = pair_from_types_ ? nullptr : edge_pair_.as<int>() + base;
+        tg.ref = ref;
+        if (ref.edges) tg.ref.edges = ref.edges + 3 * base;
+        if (ref.shifts) tg.ref.shifts = ref.shifts + 3 * base;
+        if (ref.shifts8) tg.ref.shifts8 = ref.shifts8 + 3 * base;
         tg.invalid = count_invalid && check_geometry_
                          ? reinterpret_cast<unsigned long long*>(totals_.as<double>() + 13)
                          : nullptr;
+        if (in_arena && tile_edges > 0) {
+            const hipMemcpyKind kind = explicit_device_ ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+            hip_check(hipMemcpyAsync(tile_xyz_.as<double>(), explicit_xyz_ + 3 * base,
+                                     static_cast<std::size_t>(tile_edges) * 3 * sizeof(double), kind, s),
+                      "tile xyz");
+            hip_check(hipMemcpyAsync(tile_r_.as<double>(), explicit_r_ + base,
+                                     static_cast<std::size_t>(tile_edges) * sizeof(double), kind, s),
+                      "tile r");
+        }
         hip_check(launch_tile_geometry(tg, s), "tile geometry");
     };
     auto runs_of = [&](int t) {
@@ -2070,8 +2363,8 @@ void Evaluator::evaluate_tiled()
     // the tile's directed forces into the atom forces and the virial
     auto fold = [&](int t) {
         const long long tile_edges = tile_first_edge_[t + 1] - tile_first_edge_[t];
-        hip_check(launch_fold_tile_forces(la.node_offset, la.node_count, first_.as<int>(), runs_of(t),
-                                          tedge_.as<int>(), la.graph.edge_base, forces, atom_forces, s),
+        hip_check(launch_fold_tile_forces(la.node_offset, la.node_count, la.graph.first, runs_of(t), la.graph.tedge,
+                                          0, forces, atom_forces, s),
                   "fold forces");
         if (tile_edges > 0) {
             const int np = reduce_totals_partials(0, static_cast<int>(tile_edges));
@@ -2232,11 +2525,18 @@ int Evaluator::md_nve(int num_atoms, const int* node_types, const double* masses
         }
         compute_positions(gen, xd, true);
         hip_check(launch_md_kick(N, vd, atom_forces_.as<double>(), md_inv_m_.as<double>(), dtf, stream_), "MD kick");
-        if (step_seconds) {
+        double seconds = 0.0;
+        if (step_seconds || md_progress_) {
             wait("MD step");
-            step_seconds[step - 1] = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+            seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+            if (step_seconds) step_seconds[step - 1] = seconds;
         }
         energies(step);
+        if (md_progress_) {
+            const double nan = std::numeric_limits<double>::quiet_NaN();
+            if (md_progress_(step, epot ? epot[step] : nan, ekin ? ekin[step] : nan, seconds, md_progress_user_) != 0)
+                break;
+        }
     }
     hip_check(hipMemcpyAsync(x, xd, bytes3, hipMemcpyDeviceToHost, stream_), "MD positions");
     hip_check(hipMemcpyAsync(v, vd, bytes3, hipMemcpyDeviceToHost, stream_), "MD velocities");

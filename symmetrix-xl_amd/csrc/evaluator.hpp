@@ -68,18 +68,42 @@ private:
 struct PeriodicGraph {
     int num_nodes = 0;
     long long num_edges = 0;
-    DeviceBuffer first;           // [N+1] int
+    DeviceBuffer first;           // [N+1] int (standalone builds)
     DeviceBuffer sources;         // [E] int
-    DeviceBuffer shifts;          // [E][3] int
-    DeviceBuffer fractional_xyz;  // [E][3] double
+    DeviceBuffer shifts;          // [E][3] int, or int8 when shift_bytes == 1
+    int shift_bytes = 4;
+    DeviceBuffer fractional_xyz;  // [E][3] double (may be absent)
     DeviceBuffer fractional_positions;  // [N][3] double: positions . inverse_cell at the build
 };
 
-// Builds the graph of N positions (device pointer) with the given cell.
+// Count pass of the periodic neighbour search: wrapped positions, sorted
+// cell bins, per-receiver edge counts and their int64 offsets (device and
+// host), the edge total, the largest |cell shift| component and, when
+// tile_receivers > 0, the number of distinct edge sources of each receiver
+// tile [t T, (t + 1) T).  The fill pass writes the edges from it.
+struct PeriodicCount {
+    NeighborPlan plan;
+    DeviceBuffer wp, wf, wrap, atom_bins, bin_offsets, bin_atoms, offsets;
+    long long num_edges = 0;
+    int max_shift = 0;
+    std::vector<long long> host_first;  // [N+1]
+    int tile_receivers = 0;
+    std::vector<int> tile_runs;         // [tiles]
+};
+void count_periodic_graph(const double* d_positions, int num_nodes, const double* cell, const double* inverse_cell,
+                          double cutoff, hipStream_t stream, DeviceBuffer& fractional_positions, PeriodicCount& c,
+                          int tile_receivers);
+// sources [E] int; shifts [E][3] as int32 (shifts) or int8 (shifts8, when
+// every component fits); fractional_xyz [E][3] when not null
+void fill_periodic_graph(const PeriodicCount& c, hipStream_t stream, int* sources, int* shifts, signed char* shifts8,
+                         double* fractional_xyz);
+
+// Builds the graph of N positions (device pointer) with the given cell
+// (int32 offsets and shifts, fractional edge vectors; at most 2^31 - 1 edges).
 // Validates inputs like the reference and throws on failure.
 void build_periodic_graph(const double* d_positions, int num_nodes, const double* cell,
                           const double* inverse_cell, double cutoff, hipStream_t stream,
-                          PeriodicGraph& out, std::vector<int>* host_first = nullptr);
+                          PeriodicGraph& out);
 void validate_periodic_inputs(int num_nodes, const double* cell, const double* inverse_cell,
                               double cutoff);
 // Bins and stencil reach of the cell-binned search (validates like the
@@ -122,7 +146,7 @@ std::size_t device_bytes_in_use();
 
 struct EvaluatorStats {
     int last_num_nodes = 0;
-    int last_num_edges = 0;
+    long long last_num_edges = 0;
     int active_edges = 0;
     double last_evaluation_ms = 0.0;
     int graph_builds = 0;
@@ -273,6 +297,15 @@ public:
     int md_nve(int num_atoms, const int* node_types, const double* masses, double* x, double* v,
                const double* cell, const double* inverse_cell, double skin, double dt, int steps, double* epot,
                double* ekin, double* step_seconds);
+    // Called on the host after each MD step (1-based) with its potential and
+    // kinetic energy (NaN when not computed) and wall time; a nonzero return
+    // stops the run after that step.  Null: none.
+    using StepCallback = int (*)(int step, double epot, double ekin, double seconds, void* user);
+    void set_md_progress(StepCallback callback, void* user)
+    {
+        md_progress_ = callback;
+        md_progress_user_ = user;
+    }
 
     // --- results -------------------------------------------------------------
     void node_energies(double* out) const;            // [N]
@@ -318,9 +351,17 @@ private:
     void check_generation(std::uint64_t generation) const;
     void prepare_active_types(const std::vector<int>& node_types);
     void upload_static_tables();
-    void finish_graph(const int* host_neigh_types, const int* host_sources);
+    void finish_graph(const std::vector<int>& host_pairs);
+    std::vector<int> caller_pairs(const int* host_neigh_types, const int* host_sources);
+    bool tiles_possible(int num_nodes) const;
     void allocate_workspace();
-    void plan_tiles();
+    // Execution plan of the graph being prepared from host_first_ and the
+    // edge count (before its edges are written), then the tiled plan's
+    // tile-local offsets, source-grouped lists and runs (after)
+    void select_plan();
+    void build_tile_lists();
+    void count_tile_runs();
+    void release_untiled_edge_state();
     void plan_node_blocks();
     NodeBlocks node_blocks(const DeviceBuffer& blocks, const std::vector<int>& offsets, int tile,
                            int block_nodes) const;
@@ -385,14 +426,23 @@ private:
     int num_nodes_ = 0;
     long long num_edges_ = 0;
     std::vector<int> host_types_;
-    std::vector<int> host_first_;  // CSR receiver offsets of the prepared graph, [N + 1]
+    std::vector<long long> host_first_;  // CSR receiver offsets of the prepared graph, [N + 1]
+    // edges a graph may have under the untiled plan, whose edge ids are int32
+    // (2^31 - 1; SXL_EDGE_INDEX_LIMIT lowers it, a test hook); the tiled plan
+    // indexes edges per tile and has no such limit
+    long long edge_index_limit_ = 2147483647LL;
     int r1_slices_ = 1;            // channel slices of the second-interaction forward
     // host copies of uploads in flight, released at the next wait()
     std::vector<std::vector<unsigned char>> staged_;
     double cell_[9] = {}, inverse_cell_[9] = {};
     PeriodicGraph pgraph_;
     // cell_dev_: cell (9) then inverse cell (9); disp_: [N][3] minimum-image
-    // displacements from the build's fractional positions in the current cell
+    // displacements from the build's fractional positions in the current cell.
+    // Untiled plan: first_ [N+1] receiver offsets, tfirst_ / tedge_ the
+    // source-major transpose.  Tiled plan: first_ holds tile-local offsets,
+    // tile t's receivers at [t (T + 1), t (T + 1) + count] (so first_ + t
+    // indexed by graph receiver ids), and tedge_ each tile's source-grouped
+    // list of tile-local edge ids at its first edge (no tfirst_).
     DeviceBuffer node_types_, first_, receiver_, source_, tfirst_, tedge_, edge_pair_, disp_, positions_,
         cell_dev_;
     bool check_geometry_ = false;          // evaluation from positions: invalid edges raise
@@ -438,29 +488,39 @@ private:
     int receiver_limit_ = 0;
     std::string plan_profile_ = "capacity", plan_debug_;
     ExecutionPlanReport plan_report_;
-    std::size_t graph_bytes_estimate(bool tiled) const;
+    std::size_t graph_bytes_estimate(bool tiled, long long runs) const;
     std::size_t held_graph_bytes() const;
     std::size_t work_bytes_estimate(long long receivers, long long edges, bool tiled) const;
     // tile arena: geometry, pair codes and directed forces of one tile's
     // edges (edge e at index e - first edge of the tile)
-    DeviceBuffer tile_xyz_, tile_r_, tile_pair_, tile_forces_, tile_first_edge_dev_;
+    DeviceBuffer tile_xyz_, tile_r_, tile_pair_, tile_forces_;
     // pair codes follow from the node types of receiver and source (false when
     // a caller's neighbour types differ: the tiled plan then keeps edge_pair_)
     bool pair_from_types_ = true;
-    // tiled plan: the last evaluation's edge vectors came from the caller
-    // (xyz_ / r_ kept graph-wide) rather than from the prepared geometry
+    // the last evaluation's edge vectors came from the caller rather than
+    // from the prepared geometry; the tiled plan copies each tile's slice of
+    // the caller's arrays (host or device, valid during that call) into the
+    // arena instead of keeping them graph-wide
     bool explicit_geometry_ = false;
+    const double* explicit_xyz_ = nullptr;
+    const double* explicit_r_ = nullptr;
+    bool explicit_device_ = false;
     // tiled plan: -sum_e f_e (x) xyz_e of the last evaluation (stress = this / V)
     double host_virial_[9] = {};
     int tile_receivers_ = 0;
     int num_tiles_ = 0;
     std::vector<long long> tile_first_edge_;  // [num_tiles + 1]
     std::vector<int> tile_run_offsets_;       // [num_tiles + 1]
+    // distinct edge sources per tile of the graph being prepared (from the
+    // count pass of a device build; empty: counted from the sources)
+    std::vector<int> tile_runs_;
     // M0s_: [N][C] scalar readout input x (M0 scalar block, or M0_scalar P0
     // (+ residual) in the pre_linear_up basis), graph-wide
     DeviceBuffer M0s_, run_source_, run_start_, run_length_;
     // device NVE driver state: positions, velocities, masses, unit factor / mass, kinetic partials
     DeviceBuffer md_x_, md_v_, md_m_, md_inv_m_, md_partials_;
+    StepCallback md_progress_ = nullptr;
+    void* md_progress_user_ = nullptr;
     // nodes grouped by (tile, active type) and their blocks for the node kernels
     DeviceBuffer node_order_, m0_blocks_, m0r_blocks_, readout_blocks_;
     // [tiles + 1] each; the M0 reverse has its own block size (m0r_block_nodes_)

@@ -77,20 +77,25 @@ __global__ void fill_bins_kernel(int n, const int* __restrict__ atom_bins, int* 
 // (dz -> dy -> dx), the atoms of a cell are tested 64 at a time, and the
 // accepted ones are placed by ballot and lane prefix count, so every
 // receiver's edges come out in the same order as one thread walking the
-// cells and their (sorted) atoms one by one.  The count pass (offsets null)
-// stores the number of edges; the fill pass writes them.
+// cells and their (sorted) atoms one by one.  A launch covers receivers
+// [receiver_begin, receiver_begin + receiver_count).  The count pass
+// (o.offsets null) stores the number of edges, the largest cell-shift
+// component, and with o.last_tile the number of distinct sources the launch
+// adds to tile o.tile (launches of consecutive tiles in stream order: a
+// source is new to the tile when it last appeared in an earlier one); the
+// fill pass writes the edges.
 constexpr int kEdgeThreads = 256;
 
 __global__ void __launch_bounds__(kEdgeThreads) edges_kernel(
     NeighborPlan p, const double* __restrict__ wp, const double* __restrict__ wf, const int* __restrict__ wrap,
     const int* __restrict__ atom_bins, const int* __restrict__ bin_offsets, const int* __restrict__ bin_atoms,
-    const long long* __restrict__ offsets, long long* __restrict__ counts, int* __restrict__ sources,
-    int* __restrict__ shifts, double* __restrict__ frac)
+    int receiver_begin, int receiver_count, EdgeOutputs o)
 {
     const int lane = threadIdx.x & 63;
-    const int receiver = blockIdx.x * (kEdgeThreads / 64) + (threadIdx.x >> 6);
-    if (receiver >= p.num_nodes) return;  // whole wave
-    const bool fill = offsets != nullptr;
+    const int local_receiver = blockIdx.x * (kEdgeThreads / 64) + (threadIdx.x >> 6);
+    if (local_receiver >= receiver_count) return;  // whole wave
+    const int receiver = receiver_begin + local_receiver;
+    const bool fill = o.offsets != nullptr;
     const int bx = p.bins[0], by = p.bins[1], bz = p.bins[2];
     const int receiver_bin = atom_bins[receiver];
     const int receiver_x = receiver_bin % bx;
@@ -98,9 +103,15 @@ __global__ void __launch_bounds__(kEdgeThreads) edges_kernel(
     const int receiver_z = static_cast<int>(static_cast<size_t>(receiver_bin) /
                                             (static_cast<size_t>(bx) * static_cast<size_t>(by)));
     long long local = 0;
-    const long long out0 = fill ? offsets[receiver] : 0;
+    const long long out0 = fill ? o.offsets[receiver] : 0;
+    int max_shift = 0;
+    int new_sources = 0;
+    int receiver_wrap[3];
     double rp[3];
-    for (int c = 0; c < 3; ++c) rp[c] = wp[3 * static_cast<size_t>(receiver) + c];
+    for (int c = 0; c < 3; ++c) {
+        rp[c] = wp[3 * static_cast<size_t>(receiver) + c];
+        receiver_wrap[c] = wrap[3 * static_cast<size_t>(receiver) + c];
+    }
     for (int dz = -p.reach[2]; dz <= p.reach[2]; ++dz) {
         const int raw_z = receiver_z + dz;
         const int shift_z = floor_div(raw_z, bz);
@@ -135,16 +146,30 @@ __global__ void __launch_bounds__(kEdgeThreads) edges_kernel(
                         }
                     }
                     const unsigned long long mask = __ballot(accept);
-                    if (fill && accept) {
-                        const int rank = __builtin_amdgcn_mbcnt_hi(
-                            static_cast<unsigned>(mask >> 32), __builtin_amdgcn_mbcnt_lo(static_cast<unsigned>(mask), 0));
-                        const size_t edge = static_cast<size_t>(out0 + local + rank);
-                        sources[edge] = source;
-                        for (int axis = 0; axis < 3; ++axis) {
-                            shifts[3 * edge + axis] = image[axis] - wrap[3 * static_cast<size_t>(source) + axis] +
-                                                      wrap[3 * static_cast<size_t>(receiver) + axis];
-                            frac[3 * edge + axis] = wf[3 * static_cast<size_t>(source) + axis] -
-                                                    wf[3 * static_cast<size_t>(receiver) + axis] + image[axis];
+                    if (accept) {
+                        int shift[3];
+                        for (int axis = 0; axis < 3; ++axis)
+                            shift[axis] = image[axis] - wrap[3 * static_cast<size_t>(source) + axis] +
+                                          receiver_wrap[axis];
+                        if (fill) {
+                            const int rank = __builtin_amdgcn_mbcnt_hi(
+                                static_cast<unsigned>(mask >> 32),
+                                __builtin_amdgcn_mbcnt_lo(static_cast<unsigned>(mask), 0));
+                            const size_t edge = static_cast<size_t>(out0 + local + rank);
+                            o.sources[edge] = source;
+                            for (int axis = 0; axis < 3; ++axis) {
+                                if (o.shifts8)
+                                    o.shifts8[3 * edge + axis] = static_cast<signed char>(shift[axis]);
+                                else
+                                    o.shifts[3 * edge + axis] = shift[axis];
+                                if (o.frac)
+                                    o.frac[3 * edge + axis] = wf[3 * static_cast<size_t>(source) + axis] -
+                                                              wf[3 * static_cast<size_t>(receiver) + axis] + image[axis];
+                            }
+                        } else {
+                            for (int axis = 0; axis < 3; ++axis)
+                                max_shift = max(max_shift, abs(shift[axis]));
+                            if (o.last_tile && atomicExch(o.last_tile + source, o.tile) != o.tile) ++new_sources;
                         }
                     }
                     local += __popcll(mask);
@@ -152,7 +177,17 @@ __global__ void __launch_bounds__(kEdgeThreads) edges_kernel(
             }
         }
     }
-    if (!fill && lane == 0) counts[receiver] = local;
+    if (!fill) {
+        for (int off = 32; off > 0; off >>= 1) {
+            max_shift = max(max_shift, __shfl_xor(max_shift, off, 64));
+            new_sources += __shfl_xor(new_sources, off, 64);
+        }
+        if (lane == 0) {
+            o.counts[receiver] = local;
+            if (o.max_shift && max_shift > 0) atomicMax(o.max_shift, max_shift);
+            if (o.last_tile && new_sources > 0) atomicAdd(o.tile_runs, new_sources);
+        }
+    }
 }
 
 // ---- scans ---------------------------------------------------------------
@@ -391,63 +426,48 @@ __global__ void edge_pairs_kernel(int E, const int* __restrict__ receiver, const
     edge_pair[e] = ordered | (unordered << 16);
 }
 
-// Runs of the source-major edge lists by receiver tile (tiles of T
-// consecutive receivers).  The list of each source is ascending in edge id,
-// so its receivers, and their tiles, are non-decreasing: one run per change.
-// Tile of edge e: the last tile whose first edge is <= e (tile_first_edge
-// holds num_tiles + 1 ascending offsets; empty tiles share an offset with the
-// next one, which is the one returned).
-__device__ __forceinline__ int tile_of_edge(int e, const int* __restrict__ tile_first_edge, int num_tiles)
+// Source-grouped edge list of one receiver tile.  The tile's launches run
+// after those of every earlier tile, so a source whose last_tile entry is
+// not this tile has not been seen in it yet: exactly one of its edges wins
+// the exchange and opens its run.
+__global__ void tile_runs_mark_kernel(int n, const int* __restrict__ sources, int tile, int* __restrict__ last_tile,
+                                      int* __restrict__ run_of, int* __restrict__ run_source,
+                                      int* __restrict__ run_count)
 {
-    int lo = 0, hi = num_tiles;  // answer in [lo, hi)
-    while (hi - lo > 1) {
-        const int mid = (lo + hi) / 2;
-        if (tile_first_edge[mid] <= e)
-            lo = mid;
-        else
-            hi = mid;
-    }
-    return lo;
-}
-
-__global__ void tile_runs_count_kernel(int n, const int* __restrict__ tfirst, const int* __restrict__ tedge,
-                                       const int* __restrict__ tile_first_edge, int num_tiles,
-                                       int* __restrict__ per_source, int* __restrict__ per_tile)
-{
-    const int src = blockIdx.x * blockDim.x + threadIdx.x;
-    if (src >= n) return;
-    int prev = -1, runs = 0;
-    for (int t = tfirst[src]; t < tfirst[src + 1]; ++t) {
-        const int tile = tile_of_edge(tedge[t], tile_first_edge, num_tiles);
-        if (tile != prev) {
-            ++runs;
-            atomicAdd(per_tile + tile, 1);
-            prev = tile;
+    const int l = blockIdx.x * blockDim.x + threadIdx.x;
+    if (l >= n) return;
+    const int src = sources[l];
+    if (atomicExch(last_tile + src, tile) != tile) {
+        const int k = atomicAdd(run_count, 1);
+        if (run_source) {  // null: count only
+            run_source[k] = src;
+            run_of[src] = k;
         }
     }
-    per_source[src] = runs;
 }
 
-__global__ void tile_runs_fill_kernel(int n, const int* __restrict__ tfirst, const int* __restrict__ tedge,
-                                      const int* __restrict__ tile_first_edge, int num_tiles,
-                                      const int* __restrict__ tile_offsets, int* __restrict__ cursors,
-                                      int* __restrict__ run_source, int* __restrict__ run_start,
-                                      int* __restrict__ run_length)
+__global__ void tile_runs_length_kernel(int n, const int* __restrict__ sources, const int* __restrict__ run_of,
+                                        int* __restrict__ run_length)
 {
-    const int src = blockIdx.x * blockDim.x + threadIdx.x;
-    if (src >= n) return;
-    const int t1 = tfirst[src + 1];
-    int t = tfirst[src];
-    while (t < t1) {
-        const int tile = tile_of_edge(tedge[t], tile_first_edge, num_tiles);
-        int u = t + 1;
-        while (u < t1 && tile_of_edge(tedge[u], tile_first_edge, num_tiles) == tile) ++u;
-        const int pos = tile_offsets[tile] + atomicAdd(cursors + tile, 1);
-        run_source[pos] = src;
-        run_start[pos] = t;
-        run_length[pos] = u - t;
-        t = u;
-    }
+    const int l = blockIdx.x * blockDim.x + threadIdx.x;
+    if (l >= n) return;
+    atomicAdd(run_length + run_of[sources[l]], 1);
+}
+
+__global__ void tile_list_fill_kernel(int n, const int* __restrict__ sources, const int* __restrict__ run_of,
+                                      const int* __restrict__ run_start, int* __restrict__ cursors,
+                                      int* __restrict__ list)
+{
+    const int l = blockIdx.x * blockDim.x + threadIdx.x;
+    if (l >= n) return;
+    const int k = run_of[sources[l]];
+    list[run_start[k] + atomicAdd(cursors + k, 1)] = l;
+}
+
+__global__ void fill_i32_range_kernel(int* __restrict__ out, long long n, int value)
+{
+    const long long i = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = value;
 }
 
 }  // namespace
@@ -486,14 +506,13 @@ hipError_t launch_neighbor_fill_bins(const NeighborPlan& p, const int* atom_bins
 hipError_t launch_neighbor_edges(const NeighborPlan& p, const double* wrapped_positions,
                                  const double* wrapped_fractional, const int* wrap_shifts,
                                  const int* atom_bins, const int* bin_offsets, const int* bin_atoms,
-                                 const long long* edge_offsets, long long* edge_counts, int* sources,
-                                 int* shifts, double* fractional_xyz, hipStream_t s)
+                                 int receiver_begin, int receiver_count, const EdgeOutputs& out, hipStream_t s)
 {
-    if (p.num_nodes <= 0) return hipSuccess;
+    if (receiver_count <= 0) return hipSuccess;
     constexpr int per_block = kEdgeThreads / 64;
-    edges_kernel<<<(p.num_nodes + per_block - 1) / per_block, kEdgeThreads, 0, s>>>(
-        p, wrapped_positions, wrapped_fractional, wrap_shifts, atom_bins, bin_offsets, bin_atoms,
-        edge_offsets, edge_counts, sources, shifts, fractional_xyz), note_launch();
+    edges_kernel<<<(receiver_count + per_block - 1) / per_block, kEdgeThreads, 0, s>>>(
+        p, wrapped_positions, wrapped_fractional, wrap_shifts, atom_bins, bin_offsets, bin_atoms, receiver_begin,
+        receiver_count, out), note_launch();
     return hipGetLastError();
 }
 
@@ -562,26 +581,39 @@ hipError_t launch_atom_displacements(int n, const double* positions, const Geome
     return hipGetLastError();
 }
 
-hipError_t launch_tile_runs_count(int num_nodes, const int* tfirst, const int* tedge, const int* tile_first_edge,
-                                  int num_tiles, int* runs_per_source, int* runs_per_tile, hipStream_t s)
+hipError_t launch_tile_runs_mark(int tile_edges, const int* sources, int tile, int* last_tile, int* run_of,
+                                 int* run_source, int* run_count, hipStream_t s)
 {
-    if (num_nodes <= 0) return hipSuccess;
-    tile_runs_count_kernel<<<(num_nodes + 255) / 256, 256, 0, s>>>(num_nodes, tfirst, tedge, tile_first_edge,
-                                                                   num_tiles, runs_per_source, runs_per_tile), note_launch();
+    if (tile_edges <= 0) return hipSuccess;
+    tile_runs_mark_kernel<<<(tile_edges + 255) / 256, 256, 0, s>>>(tile_edges, sources, tile, last_tile, run_of,
+                                                                  run_source, run_count), note_launch();
     return hipGetLastError();
 }
 
-hipError_t launch_tile_runs_fill(int num_nodes, const int* tfirst, const int* tedge, const int* tile_first_edge,
-                                 int num_tiles, const int* tile_offsets, int* tile_cursors, int* run_source,
-                                 int* run_start, int* run_length, hipStream_t s)
+hipError_t launch_tile_runs_length(int tile_edges, const int* sources, const int* run_of, int* run_length,
+                                   hipStream_t s)
 {
-    if (num_nodes <= 0) return hipSuccess;
-    tile_runs_fill_kernel<<<(num_nodes + 255) / 256, 256, 0, s>>>(num_nodes, tfirst, tedge, tile_first_edge,
-                                                                  num_tiles, tile_offsets, tile_cursors, run_source,
-                                                                  run_start, run_length), note_launch();
+    if (tile_edges <= 0) return hipSuccess;
+    tile_runs_length_kernel<<<(tile_edges + 255) / 256, 256, 0, s>>>(tile_edges, sources, run_of, run_length),
+        note_launch();
     return hipGetLastError();
 }
 
+hipError_t launch_tile_list_fill(int tile_edges, const int* sources, const int* run_of, const int* run_start,
+                                 int* cursors, int* list, hipStream_t s)
+{
+    if (tile_edges <= 0) return hipSuccess;
+    tile_list_fill_kernel<<<(tile_edges + 255) / 256, 256, 0, s>>>(tile_edges, sources, run_of, run_start, cursors,
+                                                                  list), note_launch();
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_i32(int* out, long long n, int value, hipStream_t s)
+{
+    if (n <= 0) return hipSuccess;
+    fill_i32_range_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, s>>>(out, n, value), note_launch();
+    return hipGetLastError();
+}
 
 // ---------------------------------------------------------------------------
 // Allocation-free neighbour graph (build_periodic_graph_noalloc).  The
@@ -719,9 +751,12 @@ void build_periodic_graph_noalloc(const double* d_positions, int num_nodes, cons
     launch_check(hipGetLastError(), "cursors");
     launch_check(launch_neighbor_fill_bins(plan, atom_bins, bin_offsets, bin_sizes, bin_atoms, s), "fill bins");
     launch_check(launch_sort_segments(B, bin_offsets, bin_atoms, s), "sort bins");
-    launch_check(launch_neighbor_edges(plan, wp, wf, wrap, atom_bins, bin_offsets, bin_atoms, nullptr, counts,
-                                       nullptr, nullptr, nullptr, s),
-                 "count edges");
+    {
+        EdgeOutputs o;
+        o.counts = counts;
+        launch_check(launch_neighbor_edges(plan, wp, wf, wrap, atom_bins, bin_offsets, bin_atoms, 0, N, o, s),
+                     "count edges");
+    }
     launch_check(launch_exclusive_scan_i64(counts, N, offsets, scan, s), "edge scan");
     long long total = 0;
     launch_check(hipMemcpyAsync(&total, offsets + N, sizeof(long long), hipMemcpyDeviceToHost, s), "edge count");
@@ -733,9 +768,15 @@ void build_periodic_graph_noalloc(const double* d_positions, int num_nodes, cons
         throw std::length_error("neighbor graph has " + std::to_string(total) + " edges, more than the capacity " +
                                 std::to_string(edge_capacity) + " of the output arrays");
     launch_check(launch_narrow_offsets(offsets, N, d_receiver_offsets, nullptr, s), "narrow");
-    launch_check(launch_neighbor_edges(plan, wp, wf, wrap, atom_bins, bin_offsets, bin_atoms, offsets, nullptr,
-                                       d_sources, d_shifts, d_fractional_xyz, s),
-                 "fill edges");
+    {
+        EdgeOutputs o;
+        o.offsets = offsets;
+        o.sources = d_sources;
+        o.shifts = d_shifts;
+        o.frac = d_fractional_xyz;
+        launch_check(launch_neighbor_edges(plan, wp, wf, wrap, atom_bins, bin_offsets, bin_atoms, 0, N, o, s),
+                     "fill edges");
+    }
     launch_check(host_fence(s), "neighbor graph");
 }
 

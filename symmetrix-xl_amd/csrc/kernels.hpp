@@ -56,8 +56,12 @@ struct EdgeGraph {
     const double* xyz = nullptr;       // [E][3]
     const double* r = nullptr;         // [E]
     // The per-edge arrays (edge_pair, xyz, r, and the directed forces and
-    // messages the kernels write) hold edge e at index e - edge_base: 0 when
-    // they span the whole graph, the tile's first edge in tiled execution.
+    // messages the kernels write) hold edge e at index e - edge_base.  The
+    // untiled plan passes graph-wide arrays (edge_base 0, edge ids below
+    // 2^31); the tiled plan passes tile-local receiver offsets, every
+    // graph-wide edge array from the tile's first edge on and the tile's
+    // source-grouped list as tedge, so edge ids are tile-local and edge_base
+    // is 0 there too.
     long long edge_base = 0;
 };
 
@@ -252,16 +256,25 @@ hipError_t launch_gather_messages(const LayerArgs& a, const float* msg, float* H
 struct TileRuns {
     int count = 0;
     const int* source = nullptr;
-    const int* start = nullptr;
+    const int* start = nullptr;   // into graph.tedge: the tile's source-grouped edge list
     const int* length = nullptr;
 };
-// (tile_first_edge [num_tiles + 1]: the first edge of each tile; an edge's
-// tile is found by binary search, so no per-edge receiver array is needed)
-hipError_t launch_tile_runs_count(int num_nodes, const int* tfirst, const int* tedge, const int* tile_first_edge,
-                                  int num_tiles, int* runs_per_source, int* runs_per_tile, hipStream_t s);
-hipError_t launch_tile_runs_fill(int num_nodes, const int* tfirst, const int* tedge, const int* tile_first_edge,
-                                 int num_tiles, const int* tile_offsets, int* tile_cursors, int* run_source,
-                                 int* run_start, int* run_length, hipStream_t s);
+// Source-grouped edge list of one receiver tile (built once per graph, tile
+// by tile in order): sources [E_t] are the tile's edge sources (tile-local
+// edge l at index l).  mark: each source seen for the first time in this
+// tile (last_tile [N] holds an earlier tile for it) becomes a run --
+// run_source[k] = source, run_of[source] = k (k from *run_count, which
+// starts at 0); lengths: run_length[run_of[source]] += 1 per edge (zeroed
+// first); fill: list[run_start[k] + j] = the tile-local edge ids of run k
+// (cursors zeroed first), in any order -- a segment sort makes them
+// ascending.  mark with run_source null only counts the runs.
+hipError_t launch_tile_runs_mark(int tile_edges, const int* sources, int tile, int* last_tile, int* run_of,
+                                 int* run_source, int* run_count, hipStream_t s);
+hipError_t launch_tile_runs_length(int tile_edges, const int* sources, const int* run_of, int* run_length,
+                                   hipStream_t s);
+hipError_t launch_tile_list_fill(int tile_edges, const int* sources, const int* run_of, const int* run_start,
+                                 int* cursors, int* list, hipStream_t s);
+hipError_t launch_fill_i32(int* out, long long n, int value, hipStream_t s);
 hipError_t launch_gather_tile_runs(const LayerArgs& a, const TileRuns& runs, const float* msg,
                                    float* H1_adj, hipStream_t s);
 // M0_adj[:, LM 0, :] += direct
@@ -302,8 +315,13 @@ hipError_t launch_zbl(int node_begin, int num_nodes, const int* first, long long
 struct GeometryRef {
     const double* positions = nullptr;  // [N][3] reference positions (fractional coordinates when fractional)
     const double* edges = nullptr;      // [E][3] reference edge vectors (fractional when fractional), or null
-    const int* shifts = nullptr;        // [E][3] integer cell shifts when edges is null
+    const int* shifts = nullptr;        // [E][3] integer cell shifts when edges is null, or
+    const signed char* shifts8 = nullptr;  // [E][3] the same in int8
     int fractional = 0;
+    // fractional positions and shifts of a graph built on the device: the
+    // edge vector is formed as the build formed its fractional edge vector
+    // (from the positions wrapped to [0, 1) and the image), bit for bit
+    int built = 0;
     int pbc = 7;                        // bit a set: lattice axis a is periodic
 };
 
@@ -317,11 +335,14 @@ hipError_t launch_edge_geometry(int num_edges, const int* receiver, const int* s
 
 // Tiled execution: the edges of receivers [node_begin, node_begin +
 // node_count) in the tile arena (edge e at index e - edge_base): xyz, r and
-// the pair code, from the caller's explicit edge vectors or from the
-// prepared geometry (ref) and the atoms' displacements; edges of zero or
-// non-finite length are set to (r_cut, 0, 0) and counted in *invalid (when
-// given).  Pair codes come from pair_source (a graph-wide table) or from the
-// active types of receiver and source.
+// the pair code, from the prepared geometry (ref) and the atoms'
+// displacements; edges of zero or non-finite length are set to (r_cut, 0, 0)
+// and counted in *invalid (when given).  With in_arena the caller's edge
+// vectors and lengths are already in the arena and only the pair codes are
+// formed.  Pair codes come from pair_source (a graph-wide table) or from the
+// active types of receiver and source.  The tiled plan passes every edge
+// array from the tile's first edge on and tile-local receiver offsets, so
+// edge_base is 0 and no index exceeds the tile.
 struct TileGeometry {
     int node_begin = 0, node_count = 0;
     long long edge_base = 0;
@@ -335,8 +356,7 @@ struct TileGeometry {
     GeometryRef ref;
     const double* disp = nullptr;
     const double* cell = nullptr;  // 9 doubles on the device
-    const double* explicit_xyz = nullptr;  // graph-wide [E][3] and [E], or null
-    const double* explicit_r = nullptr;
+    bool in_arena = false;
     double r_cut = 0.0;
     double* xyz = nullptr;
     double* r = nullptr;
@@ -379,11 +399,30 @@ hipError_t launch_neighbor_bins(const NeighborPlan& p, const double* positions, 
 hipError_t launch_neighbor_fill_bins(const NeighborPlan& p, const int* atom_bins,
                                      const int* bin_offsets, int* bin_cursors, int* bin_atoms,
                                      hipStream_t s);
+// Outputs of the neighbour search.  Count pass (offsets null): edges per
+// receiver, the largest |cell shift| component over the edges (atomicMax,
+// may be null) and, with last_tile ([N], -1 or an earlier tile for every
+// source before the first launch of `tile`), the number of distinct sources
+// the launch adds to the tile (atomicAdd into *tile_runs).  Fill pass: the
+// sources, the cell shifts (int32, or int8 when shifts8 is set) and, when
+// frac is set, the fractional edge vectors, at the receivers' offsets.
+struct EdgeOutputs {
+    const long long* offsets = nullptr;
+    long long* counts = nullptr;
+    int* max_shift = nullptr;
+    int* last_tile = nullptr;
+    int tile = 0;
+    int* tile_runs = nullptr;
+    int* sources = nullptr;
+    int* shifts = nullptr;
+    signed char* shifts8 = nullptr;
+    double* frac = nullptr;
+};
+// receivers [receiver_begin, receiver_begin + receiver_count)
 hipError_t launch_neighbor_edges(const NeighborPlan& p, const double* wrapped_positions,
                                  const double* wrapped_fractional, const int* wrap_shifts,
                                  const int* atom_bins, const int* bin_offsets, const int* bin_atoms,
-                                 const long long* edge_offsets, long long* edge_counts, int* sources,
-                                 int* shifts, double* fractional_xyz, hipStream_t s);
+                                 int receiver_begin, int receiver_count, const EdgeOutputs& out, hipStream_t s);
 
 // Exclusive scans (int -> int64 offsets), scratch of scan_scratch_size() int64
 std::size_t scan_scratch_size(int n);

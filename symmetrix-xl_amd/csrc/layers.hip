@@ -1433,6 +1433,59 @@ __global__ void add_direct_kernel(int nodes, int C, int nLM, const float* __rest
 // ---------------------------------------------------------------------------
 // geometry and reductions
 // ---------------------------------------------------------------------------
+// Cartesian vector of the fractional vector f in the cell (rows = lattice
+// vectors), with explicit fused operations so that every kernel forms it
+// with the same rounding.
+__device__ __forceinline__ void fractional_to_cartesian(const double f[3], const double* __restrict__ cell,
+                                                        double out[3])
+{
+    for (int c = 0; c < 3; ++c) out[c] = fma(f[2], cell[6 + c], fma(f[1], cell[3 + c], f[0] * cell[c]));
+}
+
+// Reference vector of edge e (receiver i, source j) of a prepared geometry.
+// A device-built graph (g.built) keeps its fractional positions and cell
+// shifts; its fractional edge vector is formed as the build formed it --
+// the positions wrapped to [0, 1) (p - floor(p)), their difference, plus the
+// image shift + floor(p_j) - floor(p_i) -- so it equals the build's stored
+// vector bit for bit.
+__device__ __forceinline__ void reference_edge(const GeometryRef& g, const double* __restrict__ cell, size_t e,
+                                               size_t i, size_t j, double ref[3])
+{
+    if (g.edges) {
+        const double* f = g.edges + 3 * e;
+        if (g.fractional) {
+            const double fv[3] = {f[0], f[1], f[2]};
+            fractional_to_cartesian(fv, cell, ref);
+        } else {
+            ref[0] = f[0], ref[1] = f[1], ref[2] = f[2];
+        }
+        return;
+    }
+    int sh[3];
+    for (int a = 0; a < 3; ++a) sh[a] = g.shifts8 ? static_cast<int>(g.shifts8[3 * e + a]) : g.shifts[3 * e + a];
+    const double* pj = g.positions + 3 * j;
+    const double* pi = g.positions + 3 * i;
+    if (g.built) {
+        double d[3];
+        for (int a = 0; a < 3; ++a) {
+            const double fj = floor(pj[a]), fi = floor(pi[a]);
+            const int image = sh[a] + static_cast<int>(fj) - static_cast<int>(fi);
+            d[a] = ((pj[a] - fj) - (pi[a] - fi)) + static_cast<double>(image);
+        }
+        fractional_to_cartesian(d, cell, ref);
+    } else if (g.fractional) {
+        double d[3];
+        for (int a = 0; a < 3; ++a) d[a] = pj[a] - pi[a] + static_cast<double>(sh[a]);
+        fractional_to_cartesian(d, cell, ref);
+    } else {
+        // single_layer_tiled_edge_geometry, mace_kokkos_factorized_lifecycle.cpp:1858-1866
+        for (int c = 0; c < 3; ++c) {
+            ref[c] = pj[c] - pi[c];
+            for (int a = 0; a < 3; ++a) ref[c] += static_cast<double>(sh[a]) * cell[3 * a + c];
+        }
+    }
+}
+
 __global__ void edge_geometry_kernel(int E, const int* __restrict__ receiver,
                                      const int* __restrict__ source, GeometryRef g,
                                      const double* __restrict__ disp, const double* __restrict__ cell,
@@ -1443,23 +1496,7 @@ __global__ void edge_geometry_kernel(int E, const int* __restrict__ receiver,
     if (e >= E) return;
     const size_t i = receiver[e], j = source[e];
     double ref[3];
-    if (g.edges) {
-        const double f0 = g.edges[3 * static_cast<size_t>(e)], f1 = g.edges[3 * static_cast<size_t>(e) + 1],
-                     f2 = g.edges[3 * static_cast<size_t>(e) + 2];
-        if (g.fractional) {
-            for (int c = 0; c < 3; ++c) ref[c] = f0 * cell[c] + f1 * cell[3 + c] + f2 * cell[6 + c];
-        } else {
-            ref[0] = f0, ref[1] = f1, ref[2] = f2;
-        }
-    } else {
-        // reference edge from the reference positions and the cell shift
-        // (single_layer_tiled_edge_geometry, mace_kokkos_factorized_lifecycle.cpp:1858-1866)
-        const int* sh = g.shifts + 3 * static_cast<size_t>(e);
-        for (int c = 0; c < 3; ++c) {
-            ref[c] = g.positions[3 * j + c] - g.positions[3 * i + c];
-            for (int axis = 0; axis < 3; ++axis) ref[c] += static_cast<double>(sh[axis]) * cell[3 * axis + c];
-        }
-    }
+    reference_edge(g, cell, static_cast<size_t>(e), i, j, ref);
     double v[3];
     for (int c = 0; c < 3; ++c) v[c] = ref[c] + disp[3 * j + c] - disp[3 * i + c];
     const double d2 = v[0] * v[0] + v[1] * v[1] + v[2] * v[2];
@@ -1610,9 +1647,10 @@ __global__ void __launch_bounds__(256) zbl_kernel(int node_begin, int N, const i
 
 // Tiled execution: the geometry of one tile's edges in the reused arena --
 // edge vector, length and pair code of edge e at index e - edge_base.  One
-// wave per receiver, lanes over its edges.  The vector is the caller's
-// (explicit) or the reference vector of the prepared geometry plus the
-// displacement difference, as edge_geometry_kernel forms it graph-wide.
+// wave per receiver, lanes over its edges.  The vector is the reference
+// vector of the prepared geometry plus the displacement difference, as
+// edge_geometry_kernel forms it graph-wide; with in_arena the caller's
+// vectors are already in place and only the pair codes are formed.
 __global__ void __launch_bounds__(256) tile_geometry_kernel(TileGeometry g)
 {
     const int lane = threadIdx.x & 63;
@@ -1620,41 +1658,13 @@ __global__ void __launch_bounds__(256) tile_geometry_kernel(TileGeometry g)
     if (local >= g.node_count) return;
     const int i = g.node_begin + local;
     const int a = g.type_active[g.node_types[i]];
-    const double* cell = g.cell;
     for (int e = g.first[i] + lane; e < g.first[i + 1]; e += 64) {
         const size_t le = static_cast<size_t>(e - g.edge_base);
         const size_t j = g.source[e];
-        double v[3];
-        if (g.explicit_xyz) {
-            for (int c = 0; c < 3; ++c) v[c] = g.explicit_xyz[3 * static_cast<size_t>(e) + c];
-            g.xyz[3 * le] = v[0];
-            g.xyz[3 * le + 1] = v[1];
-            g.xyz[3 * le + 2] = v[2];
-            g.r[le] = g.explicit_r[e];
-        } else {
+        if (!g.in_arena) {
             double ref[3];
-            if (g.ref.edges) {
-                const double* f = g.ref.edges + 3 * static_cast<size_t>(e);
-                if (g.ref.fractional) {
-                    for (int c = 0; c < 3; ++c) ref[c] = f[0] * cell[c] + f[1] * cell[3 + c] + f[2] * cell[6 + c];
-                } else {
-                    ref[0] = f[0], ref[1] = f[1], ref[2] = f[2];
-                }
-            } else {
-                const int* sh = g.ref.shifts + 3 * static_cast<size_t>(e);
-                const double* pj = g.ref.positions + 3 * j;
-                const double* pi = g.ref.positions + 3 * static_cast<size_t>(i);
-                if (g.ref.fractional) {
-                    double d[3];
-                    for (int axis = 0; axis < 3; ++axis) d[axis] = pj[axis] - pi[axis] + static_cast<double>(sh[axis]);
-                    for (int c = 0; c < 3; ++c) ref[c] = d[0] * cell[c] + d[1] * cell[3 + c] + d[2] * cell[6 + c];
-                } else {
-                    for (int c = 0; c < 3; ++c) {
-                        ref[c] = pj[c] - pi[c];
-                        for (int axis = 0; axis < 3; ++axis) ref[c] += static_cast<double>(sh[axis]) * cell[3 * axis + c];
-                    }
-                }
-            }
+            reference_edge(g.ref, g.cell, static_cast<size_t>(e), static_cast<size_t>(i), j, ref);
+            double v[3];
             for (int c = 0; c < 3; ++c) v[c] = ref[c] + g.disp[3 * j + c] - g.disp[3 * static_cast<size_t>(i) + c];
             const double d2 = v[0] * v[0] + v[1] * v[1] + v[2] * v[2];
             if (!(d2 > 0.0) || !(d2 < 1.0e300)) {
@@ -1889,7 +1899,8 @@ hipError_t launch_zbl(int node_begin, int num_nodes, const int* first, long long
 hipError_t launch_tile_geometry(const TileGeometry& g, hipStream_t s)
 {
     if (g.node_count <= 0) return hipSuccess;
-    if (!g.explicit_xyz && !g.ref.edges && !(g.ref.shifts && g.ref.positions)) return hipErrorInvalidValue;
+    if (!g.in_arena && !g.ref.edges && !((g.ref.shifts || g.ref.shifts8) && g.ref.positions))
+        return hipErrorInvalidValue;
     tile_geometry_kernel<<<(g.node_count + 3) / 4, 256, 0, s>>>(g), note_launch();
     return hipGetLastError();
 }
@@ -1919,7 +1930,7 @@ hipError_t launch_edge_geometry(int num_edges, const int* receiver, const int* s
                                 unsigned long long* invalid, hipStream_t s)
 {
     if (num_edges <= 0) return hipSuccess;
-    if (!ref.edges && !(ref.shifts && ref.positions)) return hipErrorInvalidValue;
+    if (!ref.edges && !((ref.shifts || ref.shifts8) && ref.positions)) return hipErrorInvalidValue;
     edge_geometry_kernel<<<(num_edges + 255) / 256, 256, 0, s>>>(num_edges, receiver, source, ref, displacements,
                                                                  cell, r_cut, xyz, r, invalid), note_launch();
     return hipGetLastError();

@@ -89,6 +89,7 @@ SIGNATURES = {
     "sxl_compute_prepared_positions": (ctypes.c_int, [ctypes.c_void_p, c_u64, c_double_p]),
     "sxl_compute_prepared_positions_device": (ctypes.c_int, [ctypes.c_void_p, c_u64, ctypes.c_void_p]),
     "sxl_compute_prepared": (ctypes.c_int, [ctypes.c_void_p, c_u64, c_double_p, c_double_p]),
+    "sxl_compute_prepared_device": (ctypes.c_int, [ctypes.c_void_p, c_u64, ctypes.c_void_p, ctypes.c_void_p]),
     "sxl_compute_node_energies_forces": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, c_int_p, c_int_p,
                                                         c_int_p, c_int_p, c_double_p, c_double_p]),
     "sxl_max_displacement": (ctypes.c_int, [ctypes.c_void_p, c_u64, ctypes.c_void_p, ctypes.c_int,
@@ -105,6 +106,7 @@ SIGNATURES = {
     "sxl_md_nve": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, c_int_p, c_double_p, c_double_p, c_double_p,
                                   c_double_p, c_double_p, ctypes.c_double, ctypes.c_double, ctypes.c_int,
                                   c_double_p, c_double_p, c_double_p, c_int_p]),
+    "sxl_set_md_progress": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
     "sxl_node_energies": (ctypes.c_int, [ctypes.c_void_p, c_double_p, ctypes.c_int]),
     "sxl_node_forces": (ctypes.c_int, [ctypes.c_void_p, c_double_p, c_i64]),
     "sxl_reduce_atom_forces": (ctypes.c_int, [ctypes.c_void_p, c_u64, c_double_p]),

@@ -18,6 +18,10 @@ import numpy as np
 from . import _native
 from ._native import c_double_p, c_i64, c_int_p, c_u64, check, library
 
+# sxl_md_progress_fn: int (int step, double epot, double ekin, double seconds, void* user)
+_PROGRESS_FN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_int, ctypes.c_double, ctypes.c_double, ctypes.c_double,
+                                ctypes.c_void_p)
+
 
 def _i32(a, n=None, name="array"):
     a = np.ascontiguousarray(a, dtype=np.int32).reshape(-1)
@@ -240,6 +244,13 @@ class MACEKokkosFloat:
                                              _p(rr, ctypes.c_double)))
         self._evaluated = True
 
+    def _compute_prepared_factorized_device(self, generation, xyz_ptr, r_ptr):
+        """As _compute_prepared_factorized with xyz [E][3] and r [E] doubles
+        in device memory (pointers), read during the call."""
+        check(library().sxl_compute_prepared_device(self._h, c_u64(int(generation)), ctypes.c_void_p(int(xyz_ptr)),
+                                                    ctypes.c_void_p(int(r_ptr))))
+        self._evaluated = True
+
     def compute_node_energies_forces(self, num_nodes, node_types, num_neigh, neigh_indices, neigh_types, xyz, r,
                                      execution_graph_generation=0):
         """Evaluate energies and directed forces (reference
@@ -321,13 +332,14 @@ class MACEKokkosFloat:
         self._evaluated = True
         return {"f": out.reshape(nall, 3), "energy": float(energy.value), "eatom": eatom, "virial": virial}
 
-    def _md_nve(self, node_types, masses, positions, velocities, cell, skin, dt, steps):
+    def _md_nve(self, node_types, masses, positions, velocities, cell, skin, dt, steps, progress=None):
         """Velocity-Verlet NVE run on the device (the `fix nve` update of the
         reference's LAMMPS capacity runs).  positions (A), velocities (A/fs),
         masses (amu), dt (fs).  Returns the final positions and velocities,
         the potential and kinetic energies (eV) at the start and after every
         step, each step's wall time and the number of neighbour-graph
-        rebuilds."""
+        rebuilds.  progress(step, epot, ekin, seconds), when given, is called
+        after every step; a true return ends the run after that step."""
         types = _i32(node_types, name="node_types")
         n = types.size
         m = _f64(masses, n, "masses")
@@ -340,11 +352,24 @@ class MACEKokkosFloat:
         ekin = np.zeros(max(steps, 0) + 1)
         seconds = np.zeros(max(steps, 1))
         rebuilds = ctypes.c_int(0)
-        check(library().sxl_md_nve(self._h, n, _p(types, ctypes.c_int), _p(m, ctypes.c_double),
-                                   _p(x, ctypes.c_double), _p(v, ctypes.c_double), _p(c, ctypes.c_double),
-                                   _p(inv, ctypes.c_double), float(skin), float(dt), steps,
-                                   _p(epot, ctypes.c_double), _p(ekin, ctypes.c_double),
-                                   _p(seconds, ctypes.c_double), ctypes.byref(rebuilds)))
+        callback = None
+        if progress is not None:
+            def relay(step, ep, ek, sec, _user):
+                try:
+                    return 1 if progress(int(step), float(ep), float(ek), float(sec)) else 0
+                except BaseException:  # an exception must not cross the C ABI: stop the run
+                    return 1
+            callback = _PROGRESS_FN(relay)
+            check(library().sxl_set_md_progress(self._h, ctypes.cast(callback, ctypes.c_void_p), None))
+        try:
+            check(library().sxl_md_nve(self._h, n, _p(types, ctypes.c_int), _p(m, ctypes.c_double),
+                                       _p(x, ctypes.c_double), _p(v, ctypes.c_double), _p(c, ctypes.c_double),
+                                       _p(inv, ctypes.c_double), float(skin), float(dt), steps,
+                                       _p(epot, ctypes.c_double), _p(ekin, ctypes.c_double),
+                                       _p(seconds, ctypes.c_double), ctypes.byref(rebuilds)))
+        finally:
+            if callback is not None:
+                check(library().sxl_set_md_progress(self._h, None, None))
         self._evaluated = True
         return {"positions": x.reshape(n, 3), "velocities": v.reshape(n, 3), "potential_energy": epot,
                 "kinetic_energy": ekin, "step_seconds": seconds[:max(steps, 0)], "rebuilds": int(rebuilds.value)}

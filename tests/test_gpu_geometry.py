@@ -10,6 +10,10 @@ equal the evaluation of the same graph from explicit edge vectors formed on
 the host (xyz = x[src] - x[recv] + shift . cell, r = |xyz|): energies and
 directed forces to FP64 rounding of the edge vectors (the device forms them
 from displacements, the host directly), far inside the north-star tolerances.
+Each case also runs under the tiled plan (tiles of a few receivers, which
+keeps no directed forces: energies and atom forces are compared), where the
+geometry is formed per tile from the same reference arrays and explicit edge
+vectors are copied into the tile arena per tile.
 """
 
 import json
@@ -39,12 +43,30 @@ def _caller_graph(model, s, cutoff):
     return types, g
 
 
+def _evaluator(path, limit):
+    from symmetrix_amd import MACEKokkosFloat
+
+    ev = MACEKokkosFloat(path)
+    if limit:
+        ev._set_allow_fixed_workspace(True)
+        ev._set_dual_layer_workspace_receiver_limit_for_testing(limit)
+    return ev
+
+
+def _results(ev, gen):
+    """Node energies and directed forces (untiled) or atom forces (tiled)."""
+    if ev.stats["tile_receivers"] > 0:
+        n = ev.stats["num_nodes"]
+        return ev.node_energies.copy(), np.asarray(ev._reduce_atom_forces(n, None, None, gen)).copy()
+    return ev.node_energies.copy(), ev.node_forces.copy()
+
+
 def _explicit(ev, gen, types, g, positions, cell):
     receivers = np.repeat(np.arange(len(types)), g["num_neigh"])
     xyz = positions[g["sources"]] - positions[receivers] + g["shifts"].astype(np.float64) @ cell
     r = np.linalg.norm(xyz, axis=1)
     ev._compute_prepared_factorized(gen, xyz, r)
-    return ev.node_energies.copy(), ev.node_forces.copy()
+    return _results(ev, gen)
 
 
 def _moved(s, seed, amount=0.08):
@@ -58,16 +80,17 @@ def _close(a, b):
     np.testing.assert_allclose(fa, fb, atol=1e-8, rtol=0)
 
 
+@pytest.mark.parametrize("limit", [None, 16])
 @pytest.mark.parametrize("kind", ["cartesian", "fractional", "shifts"])
-def test_caller_graph_geometry_equals_explicit_edge_vectors(tiny, kind):
-    from symmetrix_amd import MACEKokkosFloat, synthetic
+def test_caller_graph_geometry_equals_explicit_edge_vectors(tiny, kind, limit):
+    from symmetrix_amd import synthetic
 
     path, model = tiny
     s = synthetic.srtio3_supercell(3, sigma=0.05, seed=11)
     cutoff = model["r_cut"] + 0.5
     types, g = _caller_graph(model, s, cutoff)
     cell, inv = s.cell, np.linalg.inv(s.cell)
-    ev = MACEKokkosFloat(path)
+    ev = _evaluator(path, limit)
     ev._validate_graph_cardinality(len(types), len(types), len(g["sources"]))
     gen = ev._prepare_factorized_graph(len(types), types, g["num_neigh"], g["sources"], types[g["sources"]])
     pbc = np.ones(3, dtype=np.int32)
@@ -79,32 +102,34 @@ def test_caller_graph_geometry_equals_explicit_edge_vectors(tiny, kind):
         ev._prepare_factorized_fractional_geometry(gen, s.positions @ inv, g["fractional_xyz"], cell, inv, pbc)
     else:
         ev._prepare_factorized_shift_geometry(gen, s.positions, g["shifts"], cell, inv, pbc)
+    assert (ev.stats["tile_receivers"] > 0) == bool(limit)
     for seed in (1, 2):
         x = _moved(s, seed)
-        print(f"{kind} geometry, SrTiO3 3^3, displacement seed {seed}", flush=True)
+        print(f"{kind} geometry, SrTiO3 3^3, displacement seed {seed}, tile receivers {limit}", flush=True)
         ev._compute_prepared_factorized_positions(gen, x)
-        got = (ev.node_energies.copy(), ev.node_forces.copy())
+        got = _results(ev, gen)
         _close(got, _explicit(ev, gen, types, g, x, cell))
     # atoms moved by a lattice vector: the minimum-image displacement wraps
     x = _moved(s, 3)
     ev._compute_prepared_factorized_positions(gen, x)
-    base = (ev.node_energies.copy(), ev.node_forces.copy())
+    base = _results(ev, gen)
     x_wrapped = x.copy()
     x_wrapped[::7] += cell[0] - cell[2]
     ev._compute_prepared_factorized_positions(gen, x_wrapped)
-    _close((ev.node_energies.copy(), ev.node_forces.copy()), base)
+    _close(_results(ev, gen), base)
 
 
+@pytest.mark.parametrize("limit", [None, 16])
 @pytest.mark.parametrize("kind", ["fractional", "shifts"])
-def test_cell_update_follows_fractional_and_shift_geometry(tiny, kind):
-    from symmetrix_amd import MACEKokkosFloat, synthetic
+def test_cell_update_follows_fractional_and_shift_geometry(tiny, kind, limit):
+    from symmetrix_amd import synthetic
 
     path, model = tiny
     s = synthetic.srtio3_supercell(3, sigma=0.05, seed=12)
     cutoff = model["r_cut"] + 0.5
     types, g = _caller_graph(model, s, cutoff)
     cell, inv = s.cell, np.linalg.inv(s.cell)
-    ev = MACEKokkosFloat(path)
+    ev = _evaluator(path, limit)
     gen = ev._prepare_factorized_graph(len(types), types, g["num_neigh"], g["sources"], types[g["sources"]])
     pbc = np.ones(3, dtype=np.int32)
     if kind == "fractional":
@@ -116,10 +141,52 @@ def test_cell_update_follows_fractional_and_shift_geometry(tiny, kind):
     new_inv = np.linalg.inv(new_cell)
     ev._update_factorized_cell(gen, new_cell, new_inv)
     x = s.positions @ strain + np.random.default_rng(4).normal(scale=0.03, size=s.positions.shape)
-    print(f"{kind} geometry after a cell update", flush=True)
+    print(f"{kind} geometry after a cell update, tile receivers {limit}", flush=True)
     ev._compute_prepared_factorized_positions(gen, x)
-    got = (ev.node_energies.copy(), ev.node_forces.copy())
+    got = _results(ev, gen)
     _close(got, _explicit(ev, gen, types, g, x, new_cell))
+
+
+@pytest.mark.parametrize("device_arrays", [False, True])
+def test_tiled_neighbour_types_and_explicit_vectors_equal_untiled(tiny, device_arrays):
+    """A caller graph whose neighbour types differ from its sources' (the pair
+    codes are then kept graph-wide and read per tile), evaluated from
+    explicit edge vectors (host or device arrays, copied into the tile arena
+    per tile): the tiled plan equals the untiled one."""
+    from hip_memory import Hip
+    from symmetrix_amd import synthetic
+
+    path, model = tiny
+    s = synthetic.srtio3_supercell(3, sigma=0.05, seed=15)
+    types, g = _caller_graph(model, s, model["r_cut"] + 0.5)
+    elements = np.unique(types)
+    neigh_types = types[g["sources"]].copy()
+    # every fifth neighbour is read as the next active element
+    rank = np.searchsorted(elements, neigh_types[::5])
+    neigh_types[::5] = elements[(rank + 1) % elements.size]
+    receivers = np.repeat(np.arange(len(types)), g["num_neigh"])
+    xyz = s.positions[g["sources"]] - s.positions[receivers] + g["shifts"].astype(np.float64) @ s.cell
+    r = np.linalg.norm(xyz, axis=1)
+    out = {}
+    hip = Hip()
+    for limit in (None, 16):
+        ev = _evaluator(path, limit)
+        gen = ev._prepare_factorized_graph(len(types), types, g["num_neigh"], g["sources"], neigh_types)
+        assert (ev.stats["tile_receivers"] > 0) == bool(limit)
+        print(f"explicit edge vectors ({'device' if device_arrays else 'host'} arrays), tile receivers {limit}",
+              flush=True)
+        if device_arrays:
+            ev._compute_prepared_factorized_device(gen, hip.upload(xyz), hip.upload(r))
+        else:
+            ev._compute_prepared_factorized(gen, xyz, r)
+        e = ev.node_energies.copy()
+        f = np.asarray(ev._reduce_atom_forces(len(types), None, None, gen)).copy()
+        out[limit] = (e, f)
+    hip.free_all()
+    # the tiled plan sums each source's H1-adjoint messages per tile (FP32, in
+    # another order): atom forces agree to a few FP32 ulps of their size
+    np.testing.assert_allclose(out[16][0], out[None][0], atol=1e-9, rtol=0)
+    np.testing.assert_allclose(out[16][1], out[None][1], atol=1e-6, rtol=0)
 
 
 def test_open_boundary_cluster_with_cartesian_geometry(tiny):

@@ -111,3 +111,30 @@ def test_md_argument_validation(tiny):
         ev._md_nve(types, bad, s.positions, v0, s.cell, 0.5, 1.0, 3)
     with pytest.raises(ValueError, match="step count"):
         ev._md_nve(types, m, s.positions, v0, s.cell, 0.5, 1.0, -1)
+
+
+def test_md_progress_reports_every_step_and_can_stop_the_run(tiny):
+    from symmetrix_amd import MACEKokkosFloat, synthetic
+
+    path, model = tiny
+    s, m, v0 = _system(2, seed=24)
+    types = synthetic.node_types(s, model["atomic_numbers"])
+    full = MACEKokkosFloat(path)._md_nve(types, m, s.positions, v0, s.cell, 0.5, 1.0, 6)
+    seen = []
+
+    def progress(step, epot, ekin, seconds):
+        seen.append((step, epot, ekin, seconds))
+        return step == 4  # stop after the fourth step
+
+    print("MD with a progress callback stopping after step 4 of 6", flush=True)
+    ev = MACEKokkosFloat(path)
+    part = ev._md_nve(types, m, s.positions, v0, s.cell, 0.5, 1.0, 6, progress=progress)
+    assert [q[0] for q in seen] == [1, 2, 3, 4]
+    for step, epot, ekin, seconds in seen:
+        assert epot == full["potential_energy"][step] and ekin == full["kinetic_energy"][step]
+        assert seconds > 0.0
+    np.testing.assert_array_equal(part["potential_energy"][:5], full["potential_energy"][:5])
+    assert np.all(part["potential_energy"][5:] == 0.0)
+    # the callback is removed after the run: a plain run on the same evaluator works
+    again = ev._md_nve(types, m, s.positions, v0, s.cell, 0.5, 1.0, 2)
+    np.testing.assert_array_equal(again["potential_energy"], full["potential_energy"][:3])

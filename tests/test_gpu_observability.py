@@ -50,10 +50,10 @@ def test_repeat_evaluations_allocate_nothing_and_fence_once(tiny, tiled):
     st = ev.stats
     assert ev.factorized_prepared_graph_count == 1
     assert ev.factorized_prepared_evaluation_count == 0
-    # waits: the previous graph's work, the edge count read back, the built
-    # graph, the prepared graph; the tiled plan also reads back its tile runs
-    # and waits before dropping graph-wide per-edge arrays
-    assert ev.factorized_preparation_fence_count == (7 if tiled else 4), ev.factorized_preparation_fence_count
+    # waits: the previous graph's work, the edge counts read back (with the
+    # runs per tile), the prepared graph; the tiled plan also waits before
+    # dropping graph-wide per-edge arrays and checks its tile lists
+    assert ev.factorized_preparation_fence_count == (5 if tiled else 3), ev.factorized_preparation_fence_count
     assert ev.factorized_evaluation_fence_count == 0
     assert ev.factorized_last_graph_prepare_ms > 0.0
     assert (st["tile_receivers"] > 0) == tiled

@@ -98,9 +98,9 @@ def test_tiled_matches_untiled_at_tile_boundaries(tiny, cells, limit):
 
 
 def test_tiled_plan_keeps_no_graph_wide_edge_state(tiny):
-    """The tiled plan holds per edge only the sources, the cell shifts and the
-    source-major list (20 bytes); geometry, pair codes, directed forces and
-    messages live in the tile arena.  Its estimate matches the memory held,
+    """The tiled plan holds per edge only the sources, the cell shifts (int8)
+    and the tiles' source-grouped lists (11 bytes); geometry, pair codes,
+    directed forces and messages live in the tile arena.  Its estimate matches the memory held,
     and the per-atom footprint is a fraction of the untiled plan's."""
     from symmetrix_amd import MACEKokkosFloat, synthetic
 
