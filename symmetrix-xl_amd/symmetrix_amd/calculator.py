@@ -9,7 +9,13 @@ vectors in the current cell plus the atoms' minimum-image non-affine
 displacements, and the graph stays valid while
 ``||cell^-1 cell_build||_2 (cutoff + 2 max|non-affine|) <= cutoff + skin``
 (with an unchanged cell: no atom moved more than skin/2; atoms wrapped back
-into the cell count as not moved).  Every call evaluates at the current
+into the cell count as not moved).  A partly periodic cell (a slab or a wire,
+which the reference serves with a host neighbour list,
+``calculator.py:2934-2990``) is built on the device in a cell whose open axes
+are replaced by vectors orthogonal to the periodic ones and longer than the
+atoms' extent plus 2 (cutoff + skin), and evaluated through the graph's cell
+shifts with displacements wrapped along the periodic axes only; like the
+reference, it is rebuilt when the cell changes.  Every call evaluates at the current
 positions; energy is the FP64 sum of node energies, forces are reduced from
 the directed edge forces, stress is -(1/V) sum f (x) xyz in Voigt order
 (``calculator.py:3821-3894``).
@@ -22,7 +28,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from .mace import MACEKokkosFloat
+from .mace import MACEKokkosFloat, periodic_neighbor_graph
 
 
 def _arrays(atoms):
@@ -127,20 +133,42 @@ class Symmetrix:
         side = float(np.max(hi - lo)) + 2.0 * reach + 1.0
         return lo - reach, np.eye(3) * side
 
+    def _open_axes_cell(self, positions, cell, pbc):
+        """Build cell of a partly periodic system: the periodic lattice vectors
+        are kept; each open axis becomes a unit vector orthogonal to them (and
+        to the other open one) times the atoms' extent along it plus
+        2 (cutoff + skin) + 1, and the positions are offset into that box, so
+        no image across an open axis lies within cutoff + skin while the graph
+        is valid (atoms move at most skin/2 each before a rebuild)."""
+        reach = self.cutoff + self.neighbor_skin
+        periodic_vectors = np.array([cell[k] for k in range(3) if pbc[k]]).T
+        q, _ = np.linalg.qr(periodic_vectors, mode="complete")
+        directions = q[:, periodic_vectors.shape[1]:].T
+        build_cell = np.array(cell, dtype=float, copy=True)
+        offset = np.zeros(3)
+        for axis, d in zip([k for k in range(3) if not pbc[k]], directions):
+            projection = positions @ d if len(positions) else np.zeros(1)
+            lo, hi = float(projection.min()), float(projection.max())
+            build_cell[axis] = d * (hi - lo + 2.0 * reach + 1.0)
+            offset += d * (lo - reach)
+        return build_cell, offset
+
     def _geometry(self, atoms):
         positions, numbers, cell, pbc = _arrays(atoms)
-        if np.any(pbc) and not np.all(pbc):
-            raise NotImplementedError("mixed periodic boundary conditions are not supported")
-        return positions, numbers, cell, bool(np.all(pbc))
+        mode = "periodic" if np.all(pbc) else "open" if not np.any(pbc) else "mixed"
+        return positions, numbers, cell, pbc, mode
 
-    def _compatible(self, numbers, cell, periodic):
+    def _compatible(self, numbers, cell, pbc, mode):
         """Whether the cached graph may serve these atoms (same species in the
-        same order, same periodicity); a changed cell is moved to the device."""
+        same order, same periodicity); a changed cell is moved to the device
+        (a partly periodic cell that changed is rebuilt, as the reference's)."""
         c = self._cache
-        if c is None or c["periodic"] != periodic or len(numbers) != len(c["numbers"]) or \
+        if c is None or c["mode"] != mode or np.any(c["pbc"] != pbc) or len(numbers) != len(c["numbers"]) or \
                 np.any(numbers != c["numbers"]):
             return False
-        if periodic and not np.array_equal(cell, c["cell"]):
+        if mode == "mixed" and not np.array_equal(cell, c["cell"]):
+            return False
+        if mode == "periodic" and not np.array_equal(cell, c["cell"]):
             try:
                 inverse = np.linalg.inv(cell)
             except np.linalg.LinAlgError:
@@ -150,21 +178,39 @@ class Symmetrix:
             self.neighbor_cache_geometry_update_count += 1
         return True
 
-    def _still_valid(self, cell, periodic, moved):
-        if not periodic:
+    def _still_valid(self, cell, mode, moved):
+        if mode != "periodic":
             return moved <= 0.5 * self.neighbor_skin
         return topology_valid(cell, self._cache["topology_cell"], moved, self.cutoff, self.neighbor_skin)
 
-    def _build(self, positions, numbers, cell, periodic):
-        offset = np.zeros(3)
-        if not periodic:
-            offset, cell = self._isolated_box(positions)
+    def _build(self, positions, numbers, cell, pbc, mode):
         types = self._node_types(numbers)
-        info = self.evaluator._prepare_periodic_factorized_graph(
-            types, positions - offset, cell, np.linalg.inv(cell), self.cutoff + self.neighbor_skin)
-        self._cache = {"generation": info["generation"], "numbers": numbers.copy(), "periodic": periodic,
-                       "cell": cell.copy(), "topology_cell": cell.copy(), "offset": offset,
-                       "num_edges": info["num_edges"]}
+        reach = self.cutoff + self.neighbor_skin
+        offset = np.zeros(3)
+        if mode == "mixed":
+            # the device graph of the open-axes box, then evaluated from the
+            # caller's positions through its cell shifts (zero along the open
+            # axes), displacements wrapped along the periodic axes only
+            build_cell, shift_origin = self._open_axes_cell(positions, cell, pbc)
+            inverse = np.linalg.inv(build_cell)
+            g = periodic_neighbor_graph(positions - shift_origin, build_cell, inverse, reach)
+            if np.any(g["shifts"][:, ~pbc]):
+                raise RuntimeError("an edge crosses an open axis of the build cell")
+            ev = self.evaluator
+            gen = ev._prepare_factorized_graph(len(types), types, g["num_neigh"], g["sources"], types[g["sources"]])
+            ev._prepare_factorized_shift_geometry(gen, positions, g["shifts"], build_cell, inverse,
+                                                  pbc.astype(np.int32))
+            info = {"generation": gen, "num_edges": len(g["sources"])}
+            geometry_cell = build_cell
+        else:
+            geometry_cell = cell
+            if mode == "open":
+                offset, geometry_cell = self._isolated_box(positions)
+            info = self.evaluator._prepare_periodic_factorized_graph(
+                types, positions - offset, geometry_cell, np.linalg.inv(geometry_cell), reach)
+        self._cache = {"generation": info["generation"], "numbers": numbers.copy(), "mode": mode,
+                       "pbc": pbc.copy(), "cell": (cell if mode != "open" else geometry_cell).copy(),
+                       "topology_cell": geometry_cell.copy(), "offset": offset, "num_edges": info["num_edges"]}
         self.neighbor_cache_build_count += 1
         self.neighbor_cache_geometry_update_count += 1
 
@@ -175,24 +221,24 @@ class Symmetrix:
         one device pass; the rare failed check rebuilds and evaluates again.
         Returns the positions and cell the evaluator saw (isolated systems are
         shifted into their cached box) and the periodicity."""
-        positions, numbers, cell, periodic = self._geometry(atoms)
+        positions, numbers, cell, pbc, mode = self._geometry(atoms)
         ev = self.evaluator
-        if self._compatible(numbers, cell, periodic):
+        if self._compatible(numbers, cell, pbc, mode):
             c = self._cache
-            x = positions if periodic else positions - c["offset"]
+            x = positions - c["offset"]
             ev._compute_prepared_factorized_positions(c["generation"], x)
-            if self._still_valid(cell, periodic, ev._last_max_displacement()):
+            if self._still_valid(cell, mode, ev._last_max_displacement()):
                 self.neighbor_cache_reuse_count += 1
-                return x, c["cell"], periodic
-        self._build(positions, numbers, cell, periodic)
+                return x, c["cell"], mode
+        self._build(positions, numbers, cell, pbc, mode)
         c = self._cache
-        x = positions if periodic else positions - c["offset"]
+        x = positions - c["offset"]
         ev._compute_prepared_factorized_positions(c["generation"], x)
-        return x, c["cell"], periodic
+        return x, c["cell"], mode
 
     # ---- evaluation -----------------------------------------------------------------
     def calculate(self, atoms=None, properties=("energy", "forces", "stress"), system_changes=None):
-        positions, cell, periodic = self._evaluate(atoms)
+        positions, cell, mode = self._evaluate(atoms)
         gen = self._cache["generation"]
         ev = self.evaluator
         energy = ev._total_energy(gen)
@@ -202,8 +248,10 @@ class Symmetrix:
             "energies": ev.node_energies,
             "forces": ev._reduce_atom_forces(len(positions), execution_graph_generation=gen),
         }
-        if "stress" in properties and periodic:
-            volume = abs(float(np.linalg.det(cell)))
+        # stress of a periodic or partly periodic cell: -(1/V) sum f (x) xyz
+        # with the caller's cell volume (reference calculator.py:3878-3893)
+        volume = abs(float(np.linalg.det(cell))) if mode != "open" else 0.0
+        if "stress" in properties and volume > 0.0:
             results["stress"] = full_3x3_to_voigt_6_stress(ev._reduce_stress(volume, None, gen))
         self.results = results
         self.calculation_count += 1

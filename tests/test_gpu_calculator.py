@@ -197,3 +197,74 @@ def test_long_neighbour_cutoff_gives_the_same_results(tiny):
     assert abs(E1 - E0) / len(s) < E_TOL
     np.testing.assert_allclose(F1, F0, atol=F_TOL)
     np.testing.assert_allclose(S1, S0, atol=S_TOL)
+
+
+def _slab(pbc, vacuum=15.0, seed=31, tilt=0.0):
+    """SrTiO3 3 x 3 x 2 cells with vacuum added along the open axes (more than
+    cutoff + skin: no interaction across them), periodic along the others."""
+    from symmetrix_amd import synthetic
+
+    s = synthetic.srtio3_supercell(3, sigma=0.05, seed=seed)
+    a = synthetic.SRTIO3_A
+    keep = s.positions[:, 2] < 2.0 * a - 0.5 * a  # two of the three layers of cells
+    positions = s.positions[keep]
+    cell = s.cell.copy()
+    for axis in range(3):
+        if not pbc[axis]:
+            cell[axis] = cell[axis] / np.linalg.norm(cell[axis]) * (np.ptp(positions[:, axis]) + vacuum)
+    cell[1, 0] += tilt  # an oblique in-plane lattice
+    return synthetic.Structure(positions.copy(), s.numbers[keep].copy(), cell, tuple(bool(p) for p in pbc))
+
+
+@pytest.mark.parametrize("pbc,tiles", [((True, True, False), None), ((True, True, False), 16),
+                                       ((True, False, False), None), ((False, True, True), None)])
+def test_partly_periodic_cell_equals_the_periodic_box_and_oracle(oracle_lib, tiny, pbc, tiles):
+    from symmetrix_amd import Symmetrix
+
+    path, model = tiny
+    slab = _slab(pbc, tilt=0.3 if pbc[0] and pbc[1] else 0.0)
+    box = slab.copy()
+    box.pbc = (True, True, True)
+    print(f"pbc {pbc}: {len(slab)} atoms, vacuum along the open axes, tiles {tiles}", flush=True)
+    calc = Symmetrix(path, neighbor_skin=0.5, allow_fixed_workspace=tiles is not None)
+    if tiles:
+        calc.evaluator._set_dual_layer_workspace_receiver_limit_for_testing(tiles)
+    got = calc.calculate(slab)
+    assert (calc.evaluator.stats["tile_receivers"] > 0) == bool(tiles)
+    periodic = Symmetrix(path, neighbor_skin=0.5).calculate(box)
+    _close(got, periodic, len(slab))
+    _close(got, _oracle(oracle_lib, model, box), len(slab))
+
+
+def test_slab_reuses_its_graph_and_rebuilds_on_a_cell_change(oracle_lib, tiny):
+    from symmetrix_amd import Symmetrix
+
+    path, model = tiny
+    slab = _slab((True, True, False), seed=32)
+    calc = Symmetrix(path, neighbor_skin=0.5)
+    calc.calculate(slab)
+    rng = np.random.default_rng(5)
+    moved = slab.copy()
+    moved.positions = slab.positions + rng.normal(scale=0.05, size=slab.positions.shape)
+    moved.positions[[1, 9]] += slab.cell[0]  # whole periodic lattice vectors: not a move
+    print("slab: small moves and periodic wraps reuse the graph", flush=True)
+    got = calc.calculate(moved)
+    assert calc.neighbor_cache_build_count == 1 and calc.neighbor_cache_reuse_count == 1
+    _close(got, Symmetrix(path, neighbor_skin=0.5).calculate(moved), len(slab))
+    # an atom moved past skin/2 along the open axis: rebuilt
+    far = moved.copy()
+    far.positions[4, 2] += 0.4
+    got = calc.calculate(far)
+    assert calc.neighbor_cache_build_count == 2
+    _close(got, Symmetrix(path, neighbor_skin=0.5).calculate(far), len(slab))
+    # an in-plane strain: the partly periodic graph is rebuilt, as the reference's
+    strained = far.copy()
+    F = np.array([[1.01, 0.004, 0.0], [0.004, 0.995, 0.0], [0.0, 0.0, 1.0]])
+    strained.cell = far.cell @ F.T
+    strained.positions = far.positions @ F.T
+    print("slab: in-plane strain", flush=True)
+    got = calc.calculate(strained)
+    assert calc.neighbor_cache_build_count == 3
+    box = strained.copy()
+    box.pbc = (True, True, True)
+    _close(got, _oracle(oracle_lib, model, box), len(slab))
