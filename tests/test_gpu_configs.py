@@ -78,20 +78,23 @@ def test_headline_config_full_size(oracle_lib, medium):
     _full_size_check(oracle_lib, path, model, s, "SrTiO3 10^3, medium model (89 elements, 3 active)")
 
 
-def test_wide_model_with_reference_coupling_values(oracle_lib, tmp_path):
-    # the wide (3,2) shape with the coupling terms of the reference's own
-    # contract (tests/golden, from symmetrix/test/data/execution_contracts/
-    # jit_r1_mace_mp0b2_large_contract.json: 17 paths, 215 terms) in place of
-    # the generated ones
+@pytest.mark.parametrize("contract_name", ["jit_r1_mace_mp0b2_large_contract.json",
+                                           "jit_r1_mace_off23_large_contract.json"])
+def test_wide_model_with_reference_coupling_values(oracle_lib, tmp_path, contract_name):
+    # the wide (3,2) shape with the coupling terms and channel count of the
+    # reference's own contracts (tests/golden, from
+    # symmetrix/test/data/execution_contracts/: mp0b2-large, 128 channels, and
+    # off23-large, 224 channels -- an unsliced R1 forward over a 15.5 MB
+    # table; 17 paths, 215 terms each) in place of the generated ones
     import dataclasses
     import os
 
     from symmetrix_amd import synthetic
 
-    golden = os.path.join(os.path.dirname(__file__), "golden", "jit_r1_mace_mp0b2_large_contract.json")
+    golden = os.path.join(os.path.dirname(__file__), "golden", contract_name)
     with open(golden) as f:
         contract = json.load(f)
-    shape = dataclasses.replace(synthetic.PRESETS["wide"], channels=128)
+    shape = dataclasses.replace(synthetic.PRESETS["wide"], channels=contract["channels"])
     model = json.loads(synthetic.model_json(synthetic.random_mace_model(shape, seed=5)))
     assert [(l1, l2, lo) for l1, l2, lo in zip(model["Phi1_l1"], model["Phi1_l2"], model["Phi1_l"])] == [
         (p["edge_l"], p["source_l"], p["output_l"]) for p in contract["paths"]]
@@ -103,7 +106,8 @@ def test_wide_model_with_reference_coupling_values(oracle_lib, tmp_path):
     path = tmp_path / "wide_contract.json"
     path.write_text(json.dumps(model))
     s = synthetic.water_box(300, seed=2)
-    _full_size_check(oracle_lib, str(path), model, s, "water 300 H2O, wide shape with the reference's 215 coupling terms")
+    _full_size_check(oracle_lib, str(path), model, s,
+                     f"water 300 H2O, wide shape, C={contract['channels']}, the reference's 215 coupling terms")
 
 
 @pytest.mark.parametrize("contract_name", ["jit_r1_mace_omat0_small_contract.json",

@@ -196,3 +196,77 @@ def test_uncompiled_correlation_order_matches_oracle(oracle_lib, tmp_path):
     s = synthetic.srtio3_supercell(2, sigma=0.05, seed=5)
     print("l_max 3, correlation 2 (no compiled table), SrTiO3 2^3", flush=True)
     _check(oracle_lib, _write(tmp_path, "corr2", model), model, s)
+
+
+def _reference_m0_table(model, seed=7):
+    """The model's M0 polynomial with exactly the reference's own monomial lists
+    (tests/golden/standard_m0_contract.json, from libsymmetrix/source/
+    standard_m0.hpp:35-60: 422 terms, 94/118/92/118 per output component):
+    generated weights where the generated table has the term, random ones of
+    the same spread for the 12 others (in m = +-1 of the l = 1 output), which
+    no compiled slot holds and the runtime loop evaluates."""
+    import os
+
+    golden = os.path.join(os.path.dirname(__file__), "golden", "standard_m0_contract.json")
+    with open(golden) as f:
+        contract = json.load(f)
+    rng = np.random.default_rng(seed)
+    C = model["num_channels"]
+    extra = 0
+    for group in contract["monomial_groups"]:
+        LM = str(group["output_component"])
+        old = {tuple(m): j for j, m in enumerate(model["M0_monomials"][LM])}
+        terms = [list(t) for t in group["terms"]]
+        for a in range(model["num_elements"]):
+            w = model["M0_weights"][str(a)][LM]
+            spread = float(np.std(np.concatenate([np.asarray(w[str(k)]) for k in range(C)]))) or 1e-2
+            for k in range(C):
+                wk = w[str(k)]
+                w[str(k)] = [wk[old[tuple(t)]] if tuple(t) in old else float(rng.normal(scale=spread)) for t in terms]
+        extra += sum(1 for t in terms if tuple(t) not in old)
+        model["M0_monomials"][LM] = terms
+    assert sum(g["term_count"] for g in contract["monomial_groups"]) == 422 and extra == 12
+    return model
+
+
+def test_reference_m0_table_matches_oracle(oracle_lib, tmp_path):
+    from symmetrix_amd import synthetic
+
+    model = _reference_m0_table(_generated("medium3"))
+    path = _write(tmp_path, "medium3_reference_m0", model)
+    print("medium shape with the reference's 422-term M0 table, SrTiO3 3^3", flush=True)
+    _check(oracle_lib, path, model, synthetic.srtio3_supercell(3, sigma=0.05, seed=4))
+
+
+def test_reference_m0_table_stage_cost_at_the_headline_size(tmp_path):
+    """Stage times of the M0 kernels with the generated table (every term in a
+    compiled slot) and with the reference's table (12 terms in the runtime
+    loop) on the headline workload: the 89-element medium model on SrTiO3 10^3
+    (5,000 atoms), median of 5 profiled calls after 3 untimed."""
+    import statistics
+
+    from symmetrix_amd import MACEKokkosFloat, synthetic
+
+    s = synthetic.srtio3_supercell(10, sigma=0.05, seed=0)
+    generated = _generated("medium")
+    times = {}
+    for name, model in (("generated", generated), ("reference", _reference_m0_table(json.loads(json.dumps(generated))))):
+        path = _write(tmp_path, f"medium_{name}", model)
+        ev = MACEKokkosFloat(path)
+        types = synthetic.node_types(s, model["atomic_numbers"])
+        gen = ev._prepare_periodic_factorized_graph(types, s.positions, s.cell, np.linalg.inv(s.cell),
+                                                    model["r_cut"] + 0.5)["generation"]
+        for _ in range(3):
+            ev._compute_prepared_factorized_positions(gen, s.positions)
+        samples = []
+        for _ in range(5):
+            ev._set_profiling(True)
+            ev._compute_prepared_factorized_positions(gen, s.positions)
+            samples.append({k: ms / c if c else 0.0 for k, (ms, c) in ev._stage_times().items()})
+        ev._set_profiling(False)
+        times[name] = {k: statistics.median(x[k] for x in samples) for k in samples[0]}
+        total = sum(times[name].values())
+        print(f"  {name} M0 table: m0_forward {times[name]['m0_forward']:.4f} ms, m0_reverse "
+              f"{times[name]['m0_reverse']:.4f} ms, stages {total:.4f} ms", flush=True)
+    for stage in ("m0_forward", "m0_reverse"):
+        assert times["reference"][stage] > 0.0

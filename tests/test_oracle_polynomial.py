@@ -78,6 +78,7 @@ R1_CONTRACTS = [
     ("jit_r1_mace_mpa0_medium_contract.json", 3, 1, 86, 1e-12),
     ("jit_r1_contract.json", 3, 1, 86, 5e-8),
     ("jit_r1_mace_mp0b2_large_contract.json", 3, 2, 215, 1e-12),
+    ("jit_r1_mace_off23_large_contract.json", 3, 2, 215, 1e-12),
     ("jit_r1_mace_omat0_small_contract.json", 3, 0, 16, 1e-12),
     ("jit_r1_mace_off23_small_contract.json", 3, 0, 16, 1e-12),
     ("jit_r1_fixture_c4_e3_l0_contract.json", 0, 0, 1, 1e-12),
