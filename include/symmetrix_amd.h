@@ -113,6 +113,15 @@ int sxl_atomic_energies(const sxl_evaluator* evaluator, double* out);
  * neigh_types) (mace_kokkos.cpp:1561-1579). */
 int sxl_prepare_graph(sxl_evaluator* evaluator, int num_nodes, const int* node_types, const int* num_neigh,
                       const int* neigh_indices, const int* neigh_types, uint64_t* generation);
+/* The same with the four arrays in device memory.  Replaces the C++
+ * prepare_factorized_graph_device(num_nodes, node_types, num_neigh,
+ * neigh_indices, neigh_types) over Kokkos views
+ * (libsymmetrix/source/mace_kokkos.hpp:387-392): the node types and
+ * neighbour counts are read back (2 N ints); the neighbour arrays are
+ * checked and kept on the device. */
+int sxl_prepare_graph_device(sxl_evaluator* evaluator, int num_nodes, const int* d_node_types,
+                             const int* d_num_neigh, const int* d_neigh_indices, const int* d_neigh_types,
+                             uint64_t* generation);
 
 /* Periodic neighbour graph built on the device at `cutoff` (model cutoff plus
  * skin).  cell and inverse_cell are row-major 3x3 (rows are lattice vectors).
@@ -243,6 +252,27 @@ int sxl_max_displacement(sxl_evaluator* evaluator, uint64_t generation, const do
 int sxl_pair_compute(sxl_evaluator* evaluator, int inum, const int* ilist, const int* numneigh,
                      const int* const* firstneigh, int nall, const double* x, const int* type, const int* local_of,
                      int ntypes, const int* mace_types, double* f, double* energy, double* eatom, double* virial);
+
+/* The same on the device arrays of a LAMMPS KOKKOS pair style (GPU build):
+ * replaces PairSymmetrixMACEKokkos::compute_no_domain_decomposition
+ * (pair_symmetrix/pair_symmetrix_mace_kokkos.cpp:1010-1260), which runs on
+ * atomKK->k_x, k_list->d_ilist / d_numneigh / d_neighbors and k_f.  Every
+ * array is in device memory except mace_types [ntypes] (host) and the
+ * accumulators energy and virial [6] (host, may be null): ilist [inum],
+ * numneigh [nall], neighbors with neighbour slot jj of atom i at
+ * neighbors[i * neighbor_stride_atom + jj * neighbor_stride_slot] (masked with
+ * NEIGHMASK; a Kokkos LayoutRight view has strides (maxneighs, 1), LayoutLeft
+ * (1, rows)), x [nall][3], type [nall], local_of [nall], f [nall][3]
+ * (accumulated) and eatom [nall] (set for local atoms, may be null).  The
+ * list is filtered and mapped on the device and the graph prepared there;
+ * only the per-atom neighbour counts come to the host.  Forces are the
+ * evaluator's deterministic reduction of the directed forces (no atomics),
+ * so the results equal sxl_pair_compute's on the same list bit for bit.  The
+ * work runs on the evaluator's stream and has completed on return. */
+int sxl_pair_compute_device(sxl_evaluator* evaluator, int inum, const int* d_ilist, const int* d_numneigh,
+                            const int* d_neighbors, int64_t neighbor_stride_atom, int64_t neighbor_stride_slot,
+                            int nall, const double* d_x, const int* d_type, const int* d_local_of, int ntypes,
+                            const int* mace_types, double* d_f, double* energy, double* d_eatom, double* virial);
 
 /* Velocity-Verlet NVE molecular dynamics with positions, velocities and
  * forces resident on the device: the update of LAMMPS `fix nve` that the

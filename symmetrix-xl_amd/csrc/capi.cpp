@@ -196,6 +196,16 @@ int sxl_prepare_graph(sxl_evaluator* ev, int num_nodes, const int* node_types, c
     });
 }
 
+int sxl_prepare_graph_device(sxl_evaluator* ev, int num_nodes, const int* d_node_types, const int* d_num_neigh,
+                             const int* d_neigh_indices, const int* d_neigh_types, uint64_t* generation)
+{
+    if (!ev || !generation || (num_nodes > 0 && (!d_node_types || !d_num_neigh))) return null_handle();
+    return guarded([&] {
+        *generation =
+            ev->impl.prepare_graph_device(num_nodes, d_node_types, d_num_neigh, d_neigh_indices, d_neigh_types);
+    });
+}
+
 static int prepare_periodic(sxl_evaluator* ev, int num_nodes, const int* node_types, const double* positions,
                             bool device, const double* cell, const double* inverse_cell, double cutoff,
                             uint64_t* generation, int64_t* num_edges)
@@ -356,6 +366,35 @@ int sxl_pair_compute(sxl_evaluator* ev, int inum, const int* ilist, const int* n
         out.eatom = eatom;
         out.virial = virial;
         ev->pair.compute(ev->impl, in, out);
+    });
+}
+
+int sxl_pair_compute_device(sxl_evaluator* ev, int inum, const int* d_ilist, const int* d_numneigh,
+                            const int* d_neighbors, int64_t neighbor_stride_atom, int64_t neighbor_stride_slot,
+                            int nall, const double* d_x, const int* d_type, const int* d_local_of, int ntypes,
+                            const int* mace_types, double* d_f, double* energy, double* d_eatom, double* virial)
+{
+    if (!ev || !d_f) return null_handle();
+    return guarded([&] {
+        sxl::PairDeviceInput in;
+        in.inum = inum;
+        in.ilist = d_ilist;
+        in.numneigh = d_numneigh;
+        in.neighbors = d_neighbors;
+        in.stride_atom = neighbor_stride_atom;
+        in.stride_slot = neighbor_stride_slot;
+        in.nall = nall;
+        in.x = d_x;
+        in.type = d_type;
+        in.local_of = d_local_of;
+        in.ntypes = ntypes;
+        in.mace_types = mace_types;
+        sxl::PairOutput out;
+        out.f = d_f;
+        out.energy = energy;
+        out.eatom = d_eatom;
+        out.virial = virial;
+        ev->pair.compute_device(ev->impl, in, out);
     });
 }
 

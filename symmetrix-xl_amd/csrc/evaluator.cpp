@@ -1357,6 +1357,84 @@ std::uint64_t Evaluator::prepare_graph(int num_nodes, const int* node_types, con
     return generation_;
 }
 
+std::uint64_t Evaluator::prepare_graph_device(int num_nodes, const int* d_node_types, const int* d_num_neigh,
+                                              const int* d_neigh_indices, const int* d_neigh_types)
+{
+    const CallStart start;
+    if (num_nodes < 0 || num_nodes >= std::numeric_limits<int>::max())
+        throw std::length_error("MACE graph atom count exceeds the 32-bit CSR limit.");
+    // the per-node arrays come to the host (active types, node blocks, plan)
+    std::vector<int> types(num_nodes), counts(num_nodes);
+    if (num_nodes > 0) {
+        hip_check(hipMemcpyAsync(types.data(), d_node_types, num_nodes * sizeof(int), hipMemcpyDeviceToHost, stream_),
+                  "node types");
+        hip_check(hipMemcpyAsync(counts.data(), d_num_neigh, num_nodes * sizeof(int), hipMemcpyDeviceToHost, stream_),
+                  "num_neigh");
+    }
+    wait("graph arrays");
+    long long E = 0;
+    std::vector<long long> first(num_nodes + 1, 0);
+    for (int i = 0; i < num_nodes; ++i) {
+        if (counts[i] < 0) throw std::invalid_argument("num_neigh must be non-negative.");
+        E += counts[i];
+        if (E > std::numeric_limits<int>::max())
+            throw std::length_error("MACE graph directed-edge count exceeds the 32-bit topology limit.");
+        first[i + 1] = E;
+    }
+    for (int t : types)
+        if (t < 0 || t >= model_.num_elements) throw std::out_of_range("MACE radial type index is out of range.");
+    invalidate_graph();
+    prepare_active_types(types);
+    host_types_ = types;
+    num_nodes_ = num_nodes;
+    num_edges_ = E;
+    periodic_ = false;
+    host_first_ = std::move(first);
+    upload(node_types_, types, stream_, &staged_);
+    source_.reserve(static_cast<std::size_t>(std::max<long long>(E, 1)) * sizeof(int));
+    if (E > 0)
+        hip_check(hipMemcpyAsync(source_.as<int>(), d_neigh_indices, static_cast<std::size_t>(E) * sizeof(int),
+                                 hipMemcpyDeviceToDevice, stream_),
+                  "neighbour indices");
+    // neighbour indices and types checked on the device: out-of-range index,
+    // out-of-range type, inactive type, type differing from the source's
+    DeviceBuffer flags;
+    flags.reserve(4 * sizeof(unsigned long long));
+    hip_check(hipMemsetAsync(flags.as<void>(), 0, 4 * sizeof(unsigned long long), stream_), "memset");
+    hip_check(launch_check_neighbors(E, num_nodes, source_.as<int>(), d_neigh_types, node_types_.as<int>(),
+                                     type_active_.as<int>(), model_.num_elements, flags.as<unsigned long long>(),
+                                     stream_),
+              "neighbour check");
+    unsigned long long bad[4] = {};
+    hip_check(hipMemcpyAsync(bad, flags.as<void>(), sizeof(bad), hipMemcpyDeviceToHost, stream_), "copy");
+    wait("neighbour check");
+    if (bad[0]) throw std::out_of_range("neighbour index out of range.");
+    if (bad[1]) throw std::out_of_range("MACE radial type index is out of range.");
+    if (bad[2]) throw std::runtime_error("MACE radial cache is not prepared for an active type.");
+    positions_.reserve(static_cast<std::size_t>(std::max(num_nodes, 1)) * 3 * sizeof(double));
+    disp_.reserve(static_cast<std::size_t>(std::max(num_nodes, 1)) * 3 * sizeof(double));
+    geometry_mode_ = kGeometryNone;
+    std::vector<int> pairs;
+    pair_from_types_ = true;
+    if (bad[3]) {
+        // neighbour types that differ from their sources': pair codes on the host
+        std::vector<int> src(static_cast<std::size_t>(E)), ntypes(static_cast<std::size_t>(E));
+        hip_check(hipMemcpyAsync(src.data(), source_.as<int>(), E * sizeof(int), hipMemcpyDeviceToHost, stream_),
+                  "copy");
+        hip_check(hipMemcpyAsync(ntypes.data(), d_neigh_types, E * sizeof(int), hipMemcpyDeviceToHost, stream_),
+                  "copy");
+        wait("neighbour types");
+        pairs = caller_pairs(ntypes.data(), src.data());
+    }
+    tile_runs_.clear();
+    if (tiles_possible(num_nodes)) count_tile_runs();
+    select_plan();
+    if (tile_receivers_ > 0) release_untiled_edge_state();
+    finish_graph(pairs);
+    account_preparation(start);
+    return generation_;
+}
+
 void validate_periodic_inputs(int num_nodes, const double* cell, const double* inverse_cell, double cutoff)
 {
     if (!std::isfinite(cutoff) || !(cutoff > 0.0))

@@ -248,6 +248,12 @@ public:
     // e.g. a LAMMPS full list): neigh_types are model element indices.
     std::uint64_t prepare_graph(int num_nodes, const int* node_types, const int* num_neigh,
                                 const int* neigh_indices, const int* neigh_types);
+    // The same with every array in device memory (reference
+    // prepare_factorized_graph_device, mace_kokkos.hpp:387-392): the node
+    // types and counts are read back, the neighbour arrays checked and kept
+    // on the device.
+    std::uint64_t prepare_graph_device(int num_nodes, const int* d_node_types, const int* d_num_neigh,
+                                       const int* d_neigh_indices, const int* d_neigh_types);
     // Periodic graph built on the device with cutoff + skin.  Positions are
     // host or device pointers (device_positions).
     std::uint64_t prepare_periodic_graph(int num_nodes, const int* node_types, const double* positions,
@@ -315,6 +321,7 @@ public:
     double total_energy(std::uint64_t generation);
     // device pointers of the results (valid until the next call)
     const double* device_atom_forces() const { return atom_forces_.as<double>(); }
+    const double* device_node_energies() const { return energies_.as<double>(); }
     const double* device_totals() const { return totals_.as<double>(); }
     void synchronize() const;
 

@@ -470,7 +470,169 @@ __global__ void fill_i32_range_kernel(int* __restrict__ out, long long n, int va
     if (i < n) out[i] = value;
 }
 
+// ---- caller graphs on the device --------------------------------------------
+// flags[0] neighbour index out of range, [1] type out of range, [2] type not
+// active, [3] neighbour type differing from its source's type
+__global__ void check_neighbors_kernel(int E, int N, const int* __restrict__ source, const int* __restrict__ ntypes,
+                                       const int* __restrict__ node_types, const int* __restrict__ type_active,
+                                       int num_elements, unsigned long long* __restrict__ flags)
+{
+    const int e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    const int s = source[e], t = ntypes[e];
+    if (s < 0 || s >= N) {
+        atomicAdd(flags, 1ull);
+        return;
+    }
+    if (t < 0 || t >= num_elements) {
+        atomicAdd(flags + 1, 1ull);
+        return;
+    }
+    if (type_active[t] < 0) atomicAdd(flags + 2, 1ull);
+    if (t != node_types[s]) atomicAdd(flags + 3, 1ull);
+}
+
+// ---- LAMMPS KOKKOS neighbour lists (pair style on device arrays) -------------
+// flags: [0] ilist entry out of range or repeated, [1] neighbour index out of
+// range, [2] LAMMPS type out of range, [3] a neighbour's local atom is not in
+// ilist
+__global__ void pair_index_kernel(int inum, const int* __restrict__ ilist, int nall, int* __restrict__ ii_from_i,
+                                  unsigned* __restrict__ flags)
+{
+    const int ii = blockIdx.x * blockDim.x + threadIdx.x;
+    if (ii >= inum) return;
+    const int i = ilist[ii];
+    if (i < 0 || i >= nall || atomicExch(ii_from_i + i, ii) != -1) atomicOr(flags, 1u);
+}
+
+__device__ __forceinline__ int pair_neighbor(const PairList& p, int i, int jj)
+{
+    return p.neighbors[static_cast<long long>(i) * p.stride_atom + static_cast<long long>(jj) * p.stride_slot] &
+           kNeighMaskDevice;
+}
+
+// One wave per list entry ii: the neighbours within r_cut are counted, or
+// (offsets set) written in list order -- neighbour node, its element, the
+// edge vector x_j - x_i and its length -- by ballot and lane prefix count.
+// The length is formed as on the host (no fused operations in this file).
+__global__ void __launch_bounds__(256) pair_edges_kernel(PairList p, const int* __restrict__ ii_from_i,
+                                                         const long long* __restrict__ offsets,
+                                                         int* __restrict__ node_types, int* __restrict__ counts,
+                                                         int* __restrict__ neigh_indices, int* __restrict__ neigh_types,
+                                                         double* __restrict__ xyz, double* __restrict__ r,
+                                                         unsigned* __restrict__ flags)
+{
+    const int lane = threadIdx.x & 63;
+    const int ii = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (ii >= p.inum) return;  // whole wave
+    const int i = p.ilist[ii];
+    if (i < 0 || i >= p.nall) return;  // flagged by pair_index_kernel
+    const bool fill = offsets != nullptr;
+    const double xi = p.x[3 * static_cast<size_t>(i)], yi = p.x[3 * static_cast<size_t>(i) + 1],
+                 zi = p.x[3 * static_cast<size_t>(i) + 2];
+    const int n = p.numneigh[i];
+    long long out = fill ? offsets[ii] : 0;
+    int local = 0;
+    unsigned bad = 0;
+    for (int base = 0; base < n; base += 64) {
+        const int jj = base + lane;
+        bool accept = false;
+        int j = 0;
+        double dx = 0.0, dy = 0.0, dz = 0.0, r2 = 0.0;
+        if (jj < n) {
+            j = pair_neighbor(p, i, jj);
+            if (j < 0 || j >= p.nall) {
+                bad |= 2u;
+            } else {
+                dx = p.x[3 * static_cast<size_t>(j)] - xi;
+                dy = p.x[3 * static_cast<size_t>(j) + 1] - yi;
+                dz = p.x[3 * static_cast<size_t>(j) + 2] - zi;
+                r2 = dx * dx + dy * dy + dz * dz;
+                accept = r2 < p.r_cut_squared;
+            }
+        }
+        if (accept && !fill) {
+            const int jl = p.local_of[j];
+            if (jl < 0 || jl >= p.nall || ii_from_i[jl] < 0) bad |= 8u;
+            const int t = p.type[j];
+            if (t < 1 || t > p.ntypes) bad |= 4u;
+        }
+        const unsigned long long mask = __ballot(accept);
+        if (fill && accept) {
+            const int rank = __builtin_amdgcn_mbcnt_hi(static_cast<unsigned>(mask >> 32),
+                                                       __builtin_amdgcn_mbcnt_lo(static_cast<unsigned>(mask), 0));
+            const size_t e = static_cast<size_t>(out + local + rank);
+            neigh_indices[e] = ii_from_i[p.local_of[j]];
+            neigh_types[e] = p.mace_types[p.type[j] - 1];
+            xyz[3 * e] = dx;
+            xyz[3 * e + 1] = dy;
+            xyz[3 * e + 2] = dz;
+            r[e] = sqrt(r2);
+        }
+        local += __popcll(mask);
+    }
+    if (!fill) {
+        for (int off = 32; off > 0; off >>= 1) bad |= __shfl_xor(bad, off, 64);
+        if (lane == 0) {
+            counts[ii] = local;
+            const int t = p.type[i];
+            if (t < 1 || t > p.ntypes) bad |= 4u;
+            else node_types[ii] = p.mace_types[t - 1];
+            if (bad) atomicOr(flags, bad);
+        }
+    }
+}
+
+// f[ilist[ii]] += F[ii] (the node's reduced force) and eatom[ilist[ii]] = E[ii]
+__global__ void pair_scatter_kernel(int inum, const int* __restrict__ ilist, const double* __restrict__ node_forces,
+                                    const double* __restrict__ node_energies, double* __restrict__ f,
+                                    double* __restrict__ eatom)
+{
+    const int ii = blockIdx.x * blockDim.x + threadIdx.x;
+    if (ii >= inum) return;
+    const size_t i = ilist[ii];
+    for (int c = 0; c < 3; ++c) f[3 * i + c] += node_forces[3 * static_cast<size_t>(ii) + c];
+    if (eatom) eatom[i] = node_energies[ii];
+}
+
 }  // namespace
+
+hipError_t launch_check_neighbors(long long num_edges, int num_nodes, const int* source, const int* neigh_types,
+                                  const int* node_types, const int* type_active, int num_elements,
+                                  unsigned long long* flags, hipStream_t s)
+{
+    if (num_edges <= 0) return hipSuccess;
+    check_neighbors_kernel<<<static_cast<unsigned>((num_edges + 255) / 256), 256, 0, s>>>(
+        static_cast<int>(num_edges), num_nodes, source, neigh_types, node_types, type_active, num_elements, flags),
+        note_launch();
+    return hipGetLastError();
+}
+
+hipError_t launch_pair_index(int inum, const int* ilist, int nall, int* ii_from_i, unsigned* flags, hipStream_t s)
+{
+    if (inum <= 0) return hipSuccess;
+    pair_index_kernel<<<(inum + 255) / 256, 256, 0, s>>>(inum, ilist, nall, ii_from_i, flags), note_launch();
+    return hipGetLastError();
+}
+
+hipError_t launch_pair_edges(const PairList& p, const int* ii_from_i, const long long* offsets, int* node_types,
+                             int* counts, int* neigh_indices, int* neigh_types, double* xyz, double* r, unsigned* flags,
+                             hipStream_t s)
+{
+    if (p.inum <= 0) return hipSuccess;
+    pair_edges_kernel<<<(p.inum + 3) / 4, 256, 0, s>>>(p, ii_from_i, offsets, node_types, counts, neigh_indices,
+                                                       neigh_types, xyz, r, flags), note_launch();
+    return hipGetLastError();
+}
+
+hipError_t launch_pair_scatter(int inum, const int* ilist, const double* node_forces, const double* node_energies,
+                               double* f, double* eatom, hipStream_t s)
+{
+    if (inum <= 0) return hipSuccess;
+    pair_scatter_kernel<<<(inum + 255) / 256, 256, 0, s>>>(inum, ilist, node_forces, node_energies, f, eatom),
+        note_launch();
+    return hipGetLastError();
+}
 
 hipError_t launch_edge_pairs(int num_edges, const int* receiver, const int* source, const int* node_types,
                              const int* type_active, int num_active, bool shared_tables, int* edge_pair,

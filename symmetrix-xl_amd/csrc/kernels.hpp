@@ -275,6 +275,45 @@ hipError_t launch_tile_runs_length(int tile_edges, const int* sources, const int
 hipError_t launch_tile_list_fill(int tile_edges, const int* sources, const int* run_of, const int* run_start,
                                  int* cursors, int* list, hipStream_t s);
 hipError_t launch_fill_i32(int* out, long long n, int value, hipStream_t s);
+
+// A caller's neighbour arrays checked on the device: flags[0] += edges whose
+// source is outside [0, num_nodes), [1] whose type is outside the model,
+// [2] whose type is not active, [3] whose type differs from the source's.
+hipError_t launch_check_neighbors(long long num_edges, int num_nodes, const int* source, const int* neigh_types,
+                                  const int* node_types, const int* type_active, int num_elements,
+                                  unsigned long long* flags, hipStream_t s);
+
+// A LAMMPS KOKKOS full neighbour list in device memory (the pair style's
+// d_ilist, d_numneigh, d_neighbors, x, type; local_of[j] =
+// atom->map(atom->tag[j]) filled by the caller; mace_types a device copy of
+// the pair_coeff map): neighbour slot jj of atom i at neighbors[i stride_atom
+// + jj stride_slot], masked with NEIGHMASK.
+constexpr int kNeighMaskDevice = 0x1FFFFFFF;
+struct PairList {
+    int inum = 0;
+    const int* ilist = nullptr;
+    const int* numneigh = nullptr;
+    const int* neighbors = nullptr;
+    long long stride_atom = 0, stride_slot = 0;
+    int nall = 0;
+    const double* x = nullptr;
+    const int* type = nullptr;
+    const int* local_of = nullptr;
+    int ntypes = 0;
+    const int* mace_types = nullptr;
+    double r_cut_squared = 0.0;
+};
+// ii_from_i [nall] (filled with -1 first): ilist position of each listed atom
+hipError_t launch_pair_index(int inum, const int* ilist, int nall, int* ii_from_i, unsigned* flags, hipStream_t s);
+// count pass (offsets null): node_types and counts of neighbours within r_cut
+// per list entry, flags (bits: 1 ilist, 2 neighbour index, 4 type, 8 local
+// atom outside ilist); fill pass: the edges at offsets, in list order
+hipError_t launch_pair_edges(const PairList& p, const int* ii_from_i, const long long* offsets, int* node_types,
+                             int* counts, int* neigh_indices, int* neigh_types, double* xyz, double* r, unsigned* flags,
+                             hipStream_t s);
+// f[ilist[ii]] += node_forces[ii]; eatom[ilist[ii]] = node_energies[ii] (eatom may be null)
+hipError_t launch_pair_scatter(int inum, const int* ilist, const double* node_forces, const double* node_energies,
+                               double* f, double* eatom, hipStream_t s);
 hipError_t launch_gather_tile_runs(const LayerArgs& a, const TileRuns& runs, const float* msg,
                                    float* H1_adj, hipStream_t s);
 // M0_adj[:, LM 0, :] += direct

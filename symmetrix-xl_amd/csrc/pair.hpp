@@ -1,10 +1,14 @@
 // Single-rank LAMMPS pair-style driver over the evaluator: the counterpart of
 // PairSymmetrixMACE::compute_no_domain_decomposition
-// (pair_symmetrix/pair_symmetrix_mace.cpp:309-441).  A LAMMPS full neighbour
-// list over local and ghost atoms is filtered to r < r_cut, ghosts are mapped
-// to their local atoms (atom->map(atom->tag[j])), the receiver-major graph is
-// evaluated on the device, and the directed edge forces are folded into the
-// local atoms' forces and the global virial.
+// (pair_symmetrix/pair_symmetrix_mace.cpp:309-441) and, on device arrays, of
+// PairSymmetrixMACEKokkos::compute_no_domain_decomposition
+// (pair_symmetrix/pair_symmetrix_mace_kokkos.cpp:1010-1260).  A LAMMPS full
+// neighbour list over local and ghost atoms is filtered to r < r_cut, ghosts
+// are mapped to their local atoms (atom->map(atom->tag[j])), the
+// receiver-major graph is evaluated on the device, and its reduced node
+// forces (the sum of each atom's outgoing minus incoming directed forces),
+// energy and virial are added to the pair style's accumulators.  Both entries
+// use the same device reductions, so they give the same results bit for bit.
 #pragma once
 
 #include <vector>
@@ -29,20 +33,44 @@ struct PairInput {
     const int* mace_types = nullptr;       // [ntypes] model element index of LAMMPS type t + 1
 };
 
+// The same list in device memory (a LAMMPS KOKKOS list): neighbour slot jj
+// of atom i at neighbors[i stride_atom + jj stride_slot]; mace_types stays a
+// host array.
+struct PairDeviceInput {
+    int inum = 0;
+    const int* ilist = nullptr;
+    const int* numneigh = nullptr;
+    const int* neighbors = nullptr;
+    long long stride_atom = 0, stride_slot = 1;
+    int nall = 0;
+    const double* x = nullptr;
+    const int* type = nullptr;
+    const int* local_of = nullptr;
+    int ntypes = 0;
+    const int* mace_types = nullptr;
+};
+
 struct PairOutput {
-    double* f = nullptr;       // [nall][3], accumulated
-    double* energy = nullptr;  // global energy, accumulated (may be null)
-    double* eatom = nullptr;   // [nall] per-atom energy, set for local atoms (may be null)
-    double* virial = nullptr;  // [6] xx yy zz xy xz yz, accumulated (may be null)
+    double* f = nullptr;       // [nall][3], accumulated (device memory for the device entry)
+    double* energy = nullptr;  // global energy, accumulated (host, may be null)
+    double* eatom = nullptr;   // [nall] per-atom energy, set for local atoms (may be null; device for the device entry)
+    double* virial = nullptr;  // [6] xx yy zz xy xz yz, accumulated (host, may be null)
 };
 
 class PairDriver {
 public:
     void compute(Evaluator& ev, const PairInput& in, const PairOutput& out);
+    void compute_device(Evaluator& ev, const PairDeviceInput& in, const PairOutput& out);
 
 private:
-    std::vector<int> ii_from_i_, node_types_, num_neigh_, neigh_indices_, neigh_types_, node_i_, neigh_j_;
+    void check_types(const Evaluator& ev, int ntypes, const int* mace_types) const;
+    // energy and virial of the evaluated graph into the host accumulators
+    void totals(Evaluator& ev, std::uint64_t generation, const PairOutput& out);
+    std::vector<int> ii_from_i_, node_types_, num_neigh_, neigh_indices_, neigh_types_, node_i_;
     std::vector<double> xyz_, r_, node_energies_, node_forces_;
+    // device entry
+    DeviceBuffer d_mace_types_, d_ii_from_i_, d_node_types_, d_num_neigh_, d_offsets_, d_neigh_indices_,
+        d_neigh_types_, d_xyz_, d_r_, d_flags_;
 };
 
 }  // namespace sxl

@@ -103,6 +103,12 @@ SIGNATURES = {
     "sxl_pair_compute": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, c_int_p, c_int_p,
                                         ctypes.POINTER(c_int_p), ctypes.c_int, c_double_p, c_int_p, c_int_p,
                                         ctypes.c_int, c_int_p, c_double_p, c_double_p, c_double_p, c_double_p]),
+    "sxl_pair_compute_device": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                               ctypes.c_void_p, c_i64, c_i64, ctypes.c_int, ctypes.c_void_p,
+                                               ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, c_int_p,
+                                               ctypes.c_void_p, c_double_p, ctypes.c_void_p, c_double_p]),
+    "sxl_prepare_graph_device": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                                ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(c_u64)]),
     "sxl_md_nve": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, c_int_p, c_double_p, c_double_p, c_double_p,
                                   c_double_p, c_double_p, ctypes.c_double, ctypes.c_double, ctypes.c_int,
                                   c_double_p, c_double_p, c_double_p, c_int_p]),

@@ -118,6 +118,19 @@ class MACEKokkosFloat:
         self._evaluated = False
         return self._generation
 
+    def _prepare_factorized_graph_device(self, num_nodes, node_types_ptr, num_neigh_ptr, neigh_indices_ptr,
+                                         neigh_types_ptr):
+        """_prepare_factorized_graph with the four arrays in device memory
+        (pointers; reference prepare_factorized_graph_device)."""
+        gen = c_u64(0)
+        check(library().sxl_prepare_graph_device(self._h, int(num_nodes), ctypes.c_void_p(int(node_types_ptr)),
+                                                 ctypes.c_void_p(int(num_neigh_ptr)),
+                                                 ctypes.c_void_p(int(neigh_indices_ptr)),
+                                                 ctypes.c_void_p(int(neigh_types_ptr)), ctypes.byref(gen)))
+        self._generation = int(gen.value)
+        self._evaluated = False
+        return self._generation
+
     def _prepare_periodic_factorized_graph(self, node_types, positions, cell, inverse_cell, neighbor_cutoff):
         types = _i32(node_types)
         n = types.size
@@ -331,6 +344,23 @@ class MACEKokkosFloat:
                                          _p(virial, ctypes.c_double)))
         self._evaluated = True
         return {"f": out.reshape(nall, 3), "energy": float(energy.value), "eatom": eatom, "virial": virial}
+
+    def _pair_compute_device(self, inum, ilist_ptr, numneigh_ptr, neighbors_ptr, stride_atom, stride_slot, nall,
+                             x_ptr, type_ptr, local_of_ptr, mace_types, f_ptr, eatom_ptr=0):
+        """The LAMMPS KOKKOS pair style's compute on device arrays (pointers):
+        forces accumulated into f and per-atom energies set in eatom (when
+        given) on the device; returns the energy and the virial [6]."""
+        mt = _i32(mace_types, name="mace_types")
+        energy = ctypes.c_double(0.0)
+        virial = np.zeros(6)
+        check(library().sxl_pair_compute_device(
+            self._h, int(inum), ctypes.c_void_p(int(ilist_ptr)), ctypes.c_void_p(int(numneigh_ptr)),
+            ctypes.c_void_p(int(neighbors_ptr)), c_i64(int(stride_atom)), c_i64(int(stride_slot)), int(nall),
+            ctypes.c_void_p(int(x_ptr)), ctypes.c_void_p(int(type_ptr)), ctypes.c_void_p(int(local_of_ptr)),
+            mt.size, _p(mt, ctypes.c_int), ctypes.c_void_p(int(f_ptr)), ctypes.byref(energy),
+            ctypes.c_void_p(int(eatom_ptr)) if eatom_ptr else None, _p(virial, ctypes.c_double)))
+        self._evaluated = True
+        return {"energy": float(energy.value), "virial": virial}
 
     def _md_nve(self, node_types, masses, positions, velocities, cell, skin, dt, steps, progress=None):
         """Velocity-Verlet NVE run on the device (the `fix nve` update of the

@@ -105,3 +105,93 @@ def test_pair_style_accumulates_and_validates(tiny):
         ev._pair_compute(ilist, numneigh, firstneigh, x, atom_type, bad, mace_types)
     with pytest.raises(ValueError, match="outside the model"):
         ev._pair_compute(ilist, numneigh, firstneigh, x, atom_type, local_of, [0, 1, 99])
+
+
+def _kokkos_list(numneigh, firstneigh, layout):
+    """The list as a Kokkos 2-D neighbour view [nall][maxneigh]: LayoutRight
+    (strides maxneigh, 1) or LayoutLeft (strides 1, nall), padded with -1."""
+    nall = len(numneigh)
+    width = max(1, int(numneigh.max()))
+    table = np.full((nall, width), -1, dtype=np.int32)
+    for i, js in enumerate(firstneigh):
+        table[i, :len(js)] = js
+    if layout == "right":
+        return np.ascontiguousarray(table), width, 1
+    return np.ascontiguousarray(table.T), 1, nall
+
+
+@pytest.mark.parametrize("layout", ["right", "left"])
+def test_device_pair_entry_equals_the_host_entry_bit_for_bit(oracle_lib, tiny, layout):
+    from hip_memory import Hip
+    from symmetrix_amd import MACEKokkosFloat, synthetic
+
+    path, model = tiny
+    s = synthetic.srtio3_supercell(3, sigma=0.08, seed=33)
+    n = len(s)
+    ilist, numneigh, firstneigh, x, atom_type, local_of = lammps_lists(s, model["r_cut"] + 1.0, seed=3)
+    nall = len(x)
+    mace_types = [model["atomic_numbers"].index(z) for z in (38, 22, 8)]
+    prior = np.random.default_rng(1).normal(size=(nall, 3))
+    print(f"device pair entry ({layout} layout): {n} local + {nall - n} ghost atoms", flush=True)
+    host = MACEKokkosFloat(path)._pair_compute(ilist, numneigh, firstneigh, x, atom_type, local_of, mace_types,
+                                               f=prior.copy())
+    hip = Hip()
+    table, stride_atom, stride_slot = _kokkos_list(numneigh, firstneigh, layout)
+    d_f = hip.upload(prior)
+    d_eatom = hip.upload(np.full(nall, 7.0))
+    ev = MACEKokkosFloat(path)
+    dev = ev._pair_compute_device(n, hip.upload(ilist), hip.upload(numneigh), hip.upload(table), stride_atom,
+                                  stride_slot, nall, hip.upload(x), hip.upload(atom_type.astype(np.int32)),
+                                  hip.upload(local_of.astype(np.int32)), mace_types, d_f, d_eatom)
+    f = hip.download(d_f, (nall, 3), np.float64)
+    eatom = hip.download(d_eatom, nall, np.float64)
+    hip.free_all()
+    assert dev["energy"] == host["energy"]
+    np.testing.assert_array_equal(dev["virial"], host["virial"])
+    np.testing.assert_array_equal(f, host["f"])
+    np.testing.assert_array_equal(eatom[ilist], host["eatom"][ilist])
+    assert np.all(eatom[n:] == 7.0) and np.all(f[n:] == prior[n:])  # ghosts untouched
+
+    types = synthetic.node_types(s, model["atomic_numbers"])
+    orc = oracle_lib.MaceOracle(model, np.unique(types), "float32")
+    want = oracle_lib.evaluate(orc, s, model["r_cut"] + 0.5)
+    de = abs(dev["energy"] - want["energy"]) / n
+    df = float(np.max(np.abs(f[:n] - prior[:n] - want["forces"])))
+    print(f"  vs oracle: |dE|/atom={de:.3e} max|dF|={df:.3e}", flush=True)
+    assert de < E_TOL and df < F_TOL
+
+
+def test_device_pair_entry_validates_like_the_host_entry(tiny):
+    from hip_memory import Hip
+    from symmetrix_amd import MACEKokkosFloat, synthetic
+
+    path, model = tiny
+    s = synthetic.srtio3_supercell(2, sigma=0.05, seed=34)
+    ilist, numneigh, firstneigh, x, atom_type, local_of = lammps_lists(s, model["r_cut"])
+    nall = len(x)
+    mace_types = [model["atomic_numbers"].index(z) for z in (38, 22, 8)]
+    table, sa, ss = _kokkos_list(numneigh, firstneigh, "right")
+    hip = Hip()
+    ev = MACEKokkosFloat(path)
+
+    def call(local=local_of, types=mace_types, tab=table, ilist_=ilist):
+        return ev._pair_compute_device(len(s), hip.upload(ilist_), hip.upload(numneigh), hip.upload(tab), sa, ss,
+                                       nall, hip.upload(x), hip.upload(atom_type.astype(np.int32)),
+                                       hip.upload(local.astype(np.int32)), types, hip.alloc(nall * 24))
+
+    bad = local_of.copy()
+    bad[len(s):] = len(s)  # ghosts mapped to a ghost, not to their local atoms
+    with pytest.raises(ValueError, match="not in the local list"):
+        call(local=bad)
+    with pytest.raises(ValueError, match="outside the model"):
+        call(types=[0, 1, 99])
+    wild = table.copy()
+    wild[ilist[0], 0] = nall + 5
+    with pytest.raises(IndexError, match="neighbour index out of range"):
+        call(tab=wild)
+    twice = ilist.copy()
+    twice[1] = twice[0]
+    with pytest.raises(IndexError, match="ilist"):
+        call(ilist_=twice)
+    call()  # the evaluator is still usable
+    hip.free_all()
