@@ -600,3 +600,90 @@ def evaluate(oracle: MaceOracle, structure, cutoff, num_threads=0):
         "directed_forces": forces,
         "inputs": gi,
     }
+
+
+# ---------------------------------------------------------------------------
+# The R1 operator of the reference's plugin ABI, over its packets
+# (jit_hip_plugin_abi.h:37-85, 201-221; owners jit_codegen.py:884-1016
+# receiver, 1018-1110 source, 1314-1424 edge; spline helpers :2382-2497)
+# ---------------------------------------------------------------------------
+
+
+def hermite_pieces(values, derivs, h):
+    """Cubic pieces [intervals][4][functions] (c0 + c1 x + c2 x^2 + c3 x^3,
+    x in [0, h] from each interval's left knot) of knot values and
+    derivatives [functions][knots] (the Hermite form of
+    cubic_spline_set.cpp:20-29)."""
+    v = np.asarray(values, dtype=np.float64)
+    d = np.asarray(derivs, dtype=np.float64)
+    v0, v1, d0, d1 = v[:, :-1], v[:, 1:], d[:, :-1], d[:, 1:]
+    c2 = (3.0 * (v1 - v0) / h - 2.0 * d0 - d1) / h
+    c3 = (2.0 * (v0 - v1) / h + d0 + d1) / (h * h)
+    return np.stack([v0, d0, c2, c3], axis=0).transpose(2, 0, 1).copy()  # [intervals][4][fns]
+
+
+def plugin_spline(pieces, edge_type, radius, x0, h):
+    """Values and slopes [E][functions] of the packet's radial functions:
+    evaluation_point (interval clamped to the grid, x = 0 below, x = h above)
+    and the cubic piece of each edge's type (jit_codegen.py:2406-2497), in FP64."""
+    pieces = np.asarray(pieces, dtype=np.float64)  # [types][intervals][4][fns]
+    intervals = pieces.shape[1]
+    r = np.asarray(radius, dtype=np.float64)
+    iv = np.floor((r - x0) / h).astype(np.int64)
+    x = r - x0 - h * iv
+    low, high = iv < 0, iv >= intervals
+    iv = np.where(low, 0, np.where(high, intervals - 1, iv))
+    x = np.where(low, 0.0, np.where(high, h, x))
+    c = pieces[np.asarray(edge_type), iv]  # [E][4][fns]
+    xc = x[:, None]
+    value = c[:, 0] + c[:, 1] * xc + c[:, 2] * xc**2 + c[:, 3] * xc**3
+    slope = c[:, 1] + 2.0 * c[:, 2] * xc + 3.0 * c[:, 3] * xc**2
+    return value, slope
+
+
+def plugin_terms(contract):
+    """(path, lm1, lm2, lme, coefficient) of a contract's coupling terms; a
+    term's path is the one owning its row (rows run path by path,
+    (2 l1 + 1)(2 l2 + 1) per path)."""
+    row_path = []
+    for p, path in enumerate(contract["paths"]):
+        row_path += [p] * ((2 * path["edge_l"] + 1) * (2 * path["source_l"] + 1))
+    return [(row_path[t["row"]], t["lm1"], t["lm2"], t["lme"], t["coefficient"])
+            for t in contract["sparse_coupling"]["terms"]]
+
+
+def plugin_r1_forward(terms, channels, num_nodes, receivers, sources, active, R, Y, H, num_lme):
+    """Receiver owner: output[i][lme][k] = sum over the active edges of i of
+    sum_t cg_t R[e][p_t C + k] Y[e][lm1_t] H[src][lm2_t][k]."""
+    out = np.zeros((num_nodes, num_lme, channels))
+    e = np.flatnonzero(active)
+    for p, lm1, lm2, lme, cg in terms:
+        contrib = cg * R[e, p * channels:(p + 1) * channels] * Y[e, lm1][:, None] * H[sources[e], lm2]
+        np.add.at(out[:, lme], receivers[e], contrib)
+    return out
+
+
+def plugin_r1_source(terms, channels, num_nodes, num_lm2, receivers, sources, active, R, Y, A):
+    """Source owner: source_adjoint[s][lm2][k] = sum over the active edges
+    from s of sum_t cg_t R[e][p_t C + k] Y[e][lm1_t] A[recv][lme_t][k]."""
+    out = np.zeros((num_nodes, num_lm2, channels))
+    e = np.flatnonzero(active)
+    for p, lm1, lm2, lme, cg in terms:
+        contrib = cg * R[e, p * channels:(p + 1) * channels] * Y[e, lm1][:, None] * A[receivers[e], lme]
+        np.add.at(out[:, lm2], sources[e], contrib)
+    return out
+
+
+def plugin_r1_edge(terms, channels, receivers, sources, active, xyz, radius, R, dR, Y, dY, H, A):
+    """Edge owner: the directed force -dE/dxyz_e of E = <A, output> on each
+    active edge: -sum_k sum_t cg_t H[src][lm2_t][k] A[recv][lme_t][k]
+    (R'_p Y[lm1] r_hat + R_p grad Y[lm1]); dY [E][3][lm]."""
+    force = np.zeros((len(radius), 3))
+    e = np.flatnonzero(active)
+    u = xyz[e] / radius[e][:, None]
+    for p, lm1, lm2, lme, cg in terms:
+        w = cg * H[sources[e], lm2] * A[receivers[e], lme]  # [E][C]
+        radial = (w * dR[e, p * channels:(p + 1) * channels]).sum(1) * Y[e, lm1]
+        angular = (w * R[e, p * channels:(p + 1) * channels]).sum(1)
+        force[e] -= radial[:, None] * u + angular[:, None] * dY[e, :, lm1]
+    return force
