@@ -548,12 +548,15 @@ void Evaluator::prepare_active_types(const std::vector<int>& node_types)
         for (auto& t : pool) t.join();
     }
     upload(r1_, r1, stream_, &staged_);
-    upload(r0f_, r0f, stream_, &staged_);
+    // the layer-0 tables are kept on the host; place_layer0_tables() puts the
+    // one the selected plan reads on the device
+    host_r0f_ = std::move(r0f);
+    r0f_.release();
     // the unfolded layer-0 table and its per-type factors (kA0FoldedTableBytes);
     // SXL_A0_UNFOLDED=1 / 0 forces the choice (tests)
     const char* force_unfolded = std::getenv("SXL_A0_UNFOLDED");
     a0_unfold_ = force_unfolded && force_unfolded[0] ? force_unfolded[0] == '1'
-                                                     : r0f.size() * sizeof(float) > kA0FoldedTableBytes;
+                                                     : host_r0f_.size() * sizeof(float) > kA0FoldedTableBytes;
     if (a0_unfold_) {
         std::vector<float> r0u(static_cast<std::size_t>(npairs) * NI * 4 * NL * C_);
         for (int pu = 0; pu < npairs; ++pu)
@@ -583,16 +586,20 @@ void Evaluator::prepare_active_types(const std::vector<int>& node_types)
                     }
             }
         }
-        upload(r0u_, r0u, stream_, &staged_);
-        upload(h0s_, h0, stream_, &staged_);
-        upload(a0w_, w, stream_, &staged_);
-        upload(a0wt_, wt, stream_, &staged_);
+        host_r0u_ = std::move(r0u);
+        host_h0_ = std::move(h0);
+        host_a0w_ = std::move(w);
+        host_a0wt_ = std::move(wt);
     } else {
-        r0u_.release();
-        h0s_.release();
-        a0w_.release();
-        a0wt_.release();
+        host_r0u_.clear();
+        host_h0_.clear();
+        host_a0w_.clear();
+        host_a0wt_.clear();
     }
+    r0u_.release();
+    h0s_.release();
+    a0w_.release();
+    a0wt_.release();
     // the second-interaction forward of a 256-channel model runs in 64-channel
     // slices, one slice per XCD, when its coefficient table is far beyond one
     // XCD's L2 (4 MiB)
@@ -1239,6 +1246,28 @@ std::vector<int> Evaluator::caller_pairs(const int* host_neigh_types, const int*
     return host_pairs;
 }
 
+// The layer-0 table the selected plan reads on the device, the other one
+// released: the folded table for the tiled plan and for the untiled plan with
+// few active types, the unfolded table with H0 and A0_W otherwise.
+void Evaluator::place_layer0_tables()
+{
+    if (a0_unfolded()) {
+        r0f_.release();
+        if (r0u_.bytes() == 0) {
+            upload(r0u_, host_r0u_, stream_, &staged_);
+            upload(h0s_, host_h0_, stream_, &staged_);
+            upload(a0w_, host_a0w_, stream_, &staged_);
+            upload(a0wt_, host_a0wt_, stream_, &staged_);
+        }
+    } else {
+        r0u_.release();
+        h0s_.release();
+        a0w_.release();
+        a0wt_.release();
+        if (r0f_.bytes() == 0) upload(r0f_, host_r0f_, stream_, &staged_);
+    }
+}
+
 // Shared tail of both graph preparations, once the plan is selected and the
 // sources are on the device.  Untiled: receiver offsets, source-major
 // transpose, receivers and pair codes graph-wide.  Tiled: the tile-local
@@ -1249,6 +1278,7 @@ void Evaluator::finish_graph(const std::vector<int>& host_pairs)
 {
     const int N = num_nodes_;
     const long long E = num_edges_;
+    place_layer0_tables();
     if (tile_receivers_ == 0) {
         run_source_.release();
         run_start_.release();

@@ -414,6 +414,10 @@ private:
     // A0_pre: the layer-0 sums before A0_W [N][nlm][C]
     bool a0_unfold_ = false;
     DeviceBuffer r0u_, h0s_, a0w_, a0wt_, A0pre_;
+    // host copies of both layer-0 tables of the active types; only the one
+    // the selected plan reads is on the device (place_layer0_tables)
+    std::vector<float> host_r0f_, host_r0u_, host_h0_, host_a0w_, host_a0wt_;
+    void place_layer0_tables();
     std::vector<std::unique_ptr<DeviceBuffer>> a1w_, a1wt_;
     PolyLayout p0_layout_, p1_layout_;
     // density-normalisation splines [pair_u][interval][4] and ZBL pair tables [ordered active pair]
