@@ -600,7 +600,7 @@ void Evaluator::prepare_active_types(const std::vector<int>& node_types)
     h0s_.release();
     a0w_.release();
     a0wt_.release();
-    // the second-interaction forward of a 256-channel model runs in 64-channel
+    // the second interaction of a 256-channel model runs in 64-channel
     // slices, one slice per XCD, when its coefficient table is far beyond one
     // XCD's L2 (4 MiB)
     r1_slices_ = 1;
@@ -707,6 +707,10 @@ void Evaluator::allocate_workspace()
     A1_.reserve(NT * nlm_ * C_ * f);
     A1adj_.reserve(NT * nlm_ * C_ * f);
     msg_.reserve(ET * nLM_ * C_ * f);
+    if (r1_reverse_sliced(model_.l_max, model_.L_max, r1_slices_))
+        rpart_.reserve(ET * r1_slices_ * 3 * sizeof(double));
+    else
+        rpart_.release();
     // graph-wide
     H1_.reserve(N * nLM_ * C_ * f);
     H1adj_.reserve(N * nLM_ * C_ * f);
@@ -985,7 +989,7 @@ std::size_t Evaluator::held_graph_bytes() const
     const DeviceBuffer* buffers[] = {
         &node_types_, &first_, &receiver_, &source_, &tfirst_, &tedge_, &edge_pair_, &disp_, &positions_,
         &cell_dev_, &xyz_, &r_, &geo_positions_, &geo_edges_, &geo_shifts_, &A0_, &M0_, &H1_, &Phi1_, &A1_,
-        &A1adj_, &A0pre_, &direct_, &H1adj_, &msg_, &energies_, &forces_, &atom_forces_, &partials_, &totals_, &scratch_,
+        &A1adj_, &A0pre_, &direct_, &H1adj_, &msg_, &rpart_, &energies_, &forces_, &atom_forces_, &partials_, &totals_, &scratch_,
         &scale1_, &dot1_, &M0s_, &run_source_, &run_start_, &run_length_, &node_order_, &m0_blocks_, &m0r_blocks_,
         &readout_blocks_, &tile_xyz_, &tile_r_, &tile_pair_, &tile_forces_,
         &pgraph_.first, &pgraph_.sources, &pgraph_.shifts, &pgraph_.fractional_xyz, &pgraph_.fractional_positions};
@@ -1041,6 +1045,7 @@ std::size_t Evaluator::work_bytes_estimate(long long receivers, long long edges,
     const int pre = !tiled && a0_unfold_ ? nlm_ : 0;
     const std::size_t per_node = static_cast<std::size_t>(C_) * sizeof(float) * (3 * nlm_ + pre + nLM_ + nlme_);
     std::size_t per_edge = static_cast<std::size_t>(nLM_) * C_ * sizeof(float);
+    if (r1_reverse_sliced(model_.l_max, model_.L_max, r1_slices_)) per_edge += 3 * sizeof(double) * r1_slices_;
     if (tiled) per_edge += 7 * sizeof(double) + sizeof(int);
     return per_node * static_cast<std::size_t>(std::max(receivers, 1LL)) +
            per_edge * static_cast<std::size_t>(std::max(edges, 1LL));
@@ -1216,6 +1221,7 @@ void Evaluator::release_untiled_edge_state()
     r_.release();
     forces_.release();
     msg_.release();
+    rpart_.release();
     pgraph_.fractional_xyz.release();
 }
 
@@ -2296,7 +2302,7 @@ void Evaluator::evaluate()
         mark(kStageA1ReverseGemm, true);
         mark(kStageR1Reverse, false);
         hip_check(launch_r1_reverse(la, r1_.as<float>(), cg_.as<float>(), H1_.as<float>(), dPhi1,
-                                    forces_.as<double>(), msg_.as<float>(), s),
+                                    forces_.as<double>(), msg_.as<float>(), rpart_.as<double>(), s),
                   "R1 reverse");
         mark(kStageR1Reverse, true);
         mark(kStageGather, false);
@@ -2536,7 +2542,8 @@ void Evaluator::evaluate_tiled()
         ra.local_base = la.local_base;
         hip_check(launch_readout(ra, s), "readout");
         gemm_a1(la.node_count, A1adj_.as<float>(), dPhi1, true, "A1 reverse gemm");
-        hip_check(launch_r1_reverse(la, r1_.as<float>(), cg_.as<float>(), H1, dPhi1, forces, msg_.as<float>(), s),
+        hip_check(launch_r1_reverse(la, r1_.as<float>(), cg_.as<float>(), H1, dPhi1, forces, msg_.as<float>(),
+                                    rpart_.as<double>(), s),
                   "R1 reverse");
         hip_check(launch_gather_tile_runs(la, runs_of(t), msg_.as<float>(), H1adj, s), "H1 adjoint gather");
         fold(t);

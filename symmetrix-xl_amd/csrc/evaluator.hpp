@@ -442,7 +442,7 @@ private:
     // (2^31 - 1; SXL_EDGE_INDEX_LIMIT lowers it, a test hook); the tiled plan
     // indexes edges per tile and has no such limit
     long long edge_index_limit_ = 2147483647LL;
-    int r1_slices_ = 1;            // channel slices of the second-interaction forward
+    int r1_slices_ = 1;            // channel slices of the second interaction
     // host copies of uploads in flight, released at the next wait()
     std::vector<std::vector<unsigned char>> staged_;
     double cell_[9] = {}, inverse_cell_[9] = {};
@@ -472,7 +472,7 @@ private:
     void set_cell(const double* cell, const double* inverse_cell);
 
     // workspace
-    DeviceBuffer A0_, M0_, H1_, Phi1_, A1_, A1adj_, direct_, H1adj_, msg_, energies_, forces_,
+    DeviceBuffer A0_, M0_, H1_, Phi1_, A1_, A1adj_, direct_, H1adj_, msg_, rpart_, energies_, forces_,
         atom_forces_, partials_, totals_, scratch_;
     DeviceBuffer scale1_, dot1_;  // [N] A1 density scale and A1_adj . A1 (scaled models)
     void density_args(LayerArgs& la, ReadoutArgs* ra);

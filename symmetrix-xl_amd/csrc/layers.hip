@@ -894,7 +894,7 @@ r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
 template <class S, int G>
 using RevGroup = R1RevGroup<S::LMAX, S::LLMAX, G>;
 
-template <int MAXT>
+template <int MAXT, int NPART = kMaxWaves * kForcePartsGrouped>
 struct alignas(16) RevTileLds {
     float Y[kTile][16];
     float dT[kTile][2][16];  // the two kept gradient rows (stage_tangent_rows)
@@ -904,24 +904,23 @@ struct alignas(16) RevTileLds {
     int row[kTile];
     int src[kTile];
     int eid[kTile];
-    float f[kTile][kMaxWaves * kForcePartsGrouped][3];
+    float f[kTile][NPART][3];
     float dsc[kTile];
     int count;
 };
 
 
-template <class S, class RG, int MAXT>
-__device__ __forceinline__ void r1_reverse_pass(const LayerArgs& a, int i, bool first, int count,
+// Channel k of this thread; the wave's force partials go to L.f[.][part0 ..].
+template <class S, class RG, int MAXT, int NPART>
+__device__ __forceinline__ void r1_reverse_pass(const LayerArgs& a, int i, bool first, int count, int k, int part0,
                                                 const float* __restrict__ r1, const float* __restrict__ cg,
                                                 const float* __restrict__ H1, const float* __restrict__ dPhi1,
-                                                float* __restrict__ msg, RevTileLds<MAXT>& L)
+                                                float* __restrict__ msg, RevTileLds<MAXT, NPART>& L)
 {
     constexpr int NLM = (S::LMAX + 1) * (S::LMAX + 1);
     constexpr int NLMS = (S::LLMAX + 1) * (S::LLMAX + 1);
     constexpr int NG = RG::FACTORED ? RG::NTR : RG::NROW;
-    const int k = threadIdx.x;
     const int C = a.C;
-    const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     const int kk = min(k, C - 1);
     const int row_bytes = S::NP * C * 16;
@@ -1045,7 +1044,7 @@ __device__ __forceinline__ void r1_reverse_pass(const LayerArgs& a, int i, bool 
         const float pa = partial_sum_dpp<kForcePartsGrouped>(ga);
         const float pb = partial_sum_dpp<kForcePartsGrouped>(gb);
         if (holds_partial<kForcePartsGrouped>(lane)) {
-            const int part = wave * kForcePartsGrouped + lane / (64 / kForcePartsGrouped);
+            const int part = part0 + lane / (64 / kForcePartsGrouped);
             L.f[j][part][0] = first ? pA : L.f[j][part][0] + pA;
             L.f[j][part][1] = first ? pa : L.f[j][part][1] + pa;
             L.f[j][part][2] = first ? pb : L.f[j][part][2] + pb;
@@ -1059,6 +1058,43 @@ constexpr int rev_group_terms()
     int m = 1;
     ((m = !RevGroup<S, G>::FACTORED && RevGroup<S, G>::NT > m ? RevGroup<S, G>::NT : m), ...);
     return (m + 3) / 4 * 4;
+}
+
+// Wave 0 stages a tile of up to 64 of receiver i's edges from `base` for the
+// path-group passes; an edge beyond r_cut gets only the A1 density-scale
+// force term (reverse_A1_scaled visits every neighbour), passed to
+// out(edge, term) with term = 0 when the model has no A1 density scale.
+template <class S, int MAXT, int NPART, class Out>
+__device__ __forceinline__ void stage_reverse_tile(const LayerArgs& a, int base, int e1, float dcoef,
+                                                   RevTileLds<MAXT, NPART>& L, Out out)
+{
+    const EdgeGraph& g = a.graph;
+    const int t = threadIdx.x;
+    double rr;
+    const int n = min(kTile, e1 - base);
+    const TileSlot ts = compact_edge<false, false>(g, a.grid, base, n, t, rr, &L.count);
+    const int e = base + t;
+    if (ts.active) {
+        const int sl = ts.slot;
+        constexpr int NLM = (S::LMAX + 1) * (S::LMAX + 1);
+        float dY[3][NLM], u[3];
+        edge_harmonics<S::LMAX, true>(g.xyz + 3 * static_cast<size_t>(e - g.edge_base), rr, L.Y[sl], dY[0], dY[1],
+                                      dY[2], u);
+        stage_tangent_rows<NLM>(dY, u, L.dT[sl][0], L.dT[sl][1], L.drop[sl]);
+        L.geo[sl][0] = u[0];
+        L.geo[sl][1] = u[1];
+        L.geo[sl][2] = u[2];
+        L.geo[sl][3] = ts.x;
+        L.row[sl] = ts.row;
+        L.src[sl] = g.source[e];
+        L.eid[sl] = e;
+        L.dsc[sl] =
+            a.d1.table ? dcoef * density_slope(a.d1.table, a.grid, g.edge_pair[e - g.edge_base] >> 16, rr) : 0.0f;
+    } else if (t < n) {
+        float d = 0.0f;
+        if (a.d1.table) d = dcoef * density_slope(a.d1.table, a.grid, g.edge_pair[e - g.edge_base] >> 16, rr);
+        out(e, d, rr);
+    }
 }
 
 template <class S, int... G>
@@ -1079,41 +1115,18 @@ __global__ void __launch_bounds__(256) r1_reverse_grouped_kernel(LayerArgs a, co
     const int e0 = g.first[i], e1 = g.first[i + 1];
     for (int base = e0; base < e1; base += kTile) {
         __syncthreads();
-        if (threadIdx.x < 64) {
-            const int t = threadIdx.x;
-            double rr;
-            const int n = min(kTile, e1 - base);
-            const TileSlot ts = compact_edge<false, false>(g, a.grid, base, n, t, rr, &L.count);
-            const int e = base + t;
-            if (ts.active) {
-                const int sl = ts.slot;
-                constexpr int NLM = (S::LMAX + 1) * (S::LMAX + 1);
-                float dY[3][NLM], u[3];
-                edge_harmonics<S::LMAX, true>(g.xyz + 3 * static_cast<size_t>(e - g.edge_base), rr, L.Y[sl], dY[0],
-                                              dY[1], dY[2], u);
-                stage_tangent_rows<NLM>(dY, u, L.dT[sl][0], L.dT[sl][1], L.drop[sl]);
-                L.geo[sl][0] = u[0];
-                L.geo[sl][1] = u[1];
-                L.geo[sl][2] = u[2];
-                L.geo[sl][3] = ts.x;
-                L.row[sl] = ts.row;
-                L.src[sl] = g.source[e];
-                L.eid[sl] = e;
-                L.dsc[sl] = a.d1.table ? dcoef * density_slope(a.d1.table, a.grid, g.edge_pair[e - g.edge_base] >> 16, rr) : 0.0f;
-            } else if (t < n) {
-                // beyond r_cut: only the A1 density-scale term (reverse_A1_scaled visits every neighbour)
+        if (threadIdx.x < 64)
+            stage_reverse_tile<S>(a, base, e1, dcoef, L, [&](int e, float d, double rr) {
                 double* out = forces + 3 * static_cast<size_t>(e - g.edge_base);
-                float d = 0.0f;
-                if (a.d1.table) d = dcoef * density_slope(a.d1.table, a.grid, g.edge_pair[e - g.edge_base] >> 16, rr);
                 const double* x = g.xyz + 3 * static_cast<size_t>(e - g.edge_base);
-                out[0] = static_cast<double>(d * static_cast<float>(x[0] / rr));
-                out[1] = static_cast<double>(d * static_cast<float>(x[1] / rr));
-                out[2] = static_cast<double>(d * static_cast<float>(x[2] / rr));
-            }
-        }
+#pragma unroll
+                for (int c = 0; c < 3; ++c) out[c] = static_cast<double>(d * static_cast<float>(x[c] / rr));
+            });
         __syncthreads();
         const int count = uniform(L.count);
-        (r1_reverse_pass<S, RevGroup<S, G>, MAXT>(a, i, G == 0, count, r1, cg, H1, dPhi1, msg, L), ...);
+        (r1_reverse_pass<S, RevGroup<S, G>>(a, i, G == 0, count, threadIdx.x, (threadIdx.x >> 6) * kForcePartsGrouped,
+                                            r1, cg, H1, dPhi1, msg, L),
+         ...);
         __syncthreads();
         if (threadIdx.x < count) {
             const int t = threadIdx.x;
@@ -1127,6 +1140,75 @@ __global__ void __launch_bounds__(256) r1_reverse_grouped_kernel(LayerArgs a, co
             for (int c = 0; c < 3; ++c) out[c] = -f[c] + static_cast<double>(L.dsc[t] * L.geo[t][c]);
         }
     }
+}
+
+// Channel-sliced reverse (LayerArgs::channel_slices workgroups per receiver,
+// XCD-aligned like the sliced forward): a one-wave workgroup runs the
+// path-group passes of one 64-channel slice of a receiver, so each XCD's L2
+// holds only its slice's columns of the coefficient table.  The slice's part
+// of each directed force, a sum over its channels, goes to
+// part[edge][slice][3] (slice 0 adds the A1 density-scale term, the other
+// slices write zero for edges beyond r_cut); fold_slices_kernel adds the
+// parts in slice order.
+template <class S, int... G>
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2)))
+r1_reverse_sliced_kernel(LayerArgs a, const float* __restrict__ r1, const float* __restrict__ cg,
+                         const float* __restrict__ H1, const float* __restrict__ dPhi1, double* __restrict__ part,
+                         float* __restrict__ msg)
+{
+    constexpr int MAXT = rev_group_terms<S, G...>();
+    static_assert((S::LMAX + 1) * (S::LMAX + 1) <= 16, "harmonics beyond l = 3");
+    __shared__ RevTileLds<MAXT, kForcePartsGrouped> L;
+    int slice;
+    const int i = a.node_offset + xcd_slice_receiver(blockIdx.x, a.node_count, a.channel_slices, slice);
+    const int slices = a.channel_slices;
+    const int k = slice * 64 + static_cast<int>(threadIdx.x);  // < C: C = 64 slices
+    const EdgeGraph& g = a.graph;
+    const float dcoef = a.d1.table && slice == 0 ? a.d1.dot[i] / a.d1.scale[i] : 0.0f;
+    const int e0 = g.first[i], e1 = g.first[i + 1];
+    for (int base = e0; base < e1; base += kTile) {
+        __syncthreads();
+        stage_reverse_tile<S>(a, base, e1, dcoef, L, [&](int e, float d, double rr) {
+            double* out = part + 3 * (static_cast<size_t>(e - g.edge_base) * slices + slice);
+            const double* x = g.xyz + 3 * static_cast<size_t>(e - g.edge_base);
+#pragma unroll
+            for (int c = 0; c < 3; ++c) out[c] = static_cast<double>(d * static_cast<float>(x[c] / rr));
+        });
+        __syncthreads();
+        const int count = uniform(L.count);
+        (r1_reverse_pass<S, RevGroup<S, G>>(a, i, G == 0, count, k, 0, r1, cg, H1, dPhi1, msg, L), ...);
+        __syncthreads();
+        if (static_cast<int>(threadIdx.x) < count) {
+            const int t = threadIdx.x;
+            double p[3] = {0.0, 0.0, 0.0};
+            for (int w = 0; w < kForcePartsGrouped; ++w)
+                for (int c = 0; c < 3; ++c) p[c] += static_cast<double>(L.f[t][w][c]);
+            double f[3];
+            tangent_force(p[0], p[1], p[2], L.drop[t], L.geo[t], f);
+            double* out = part + 3 * (static_cast<size_t>(L.eid[t] - g.edge_base) * slices + slice);
+#pragma unroll
+            for (int c = 0; c < 3; ++c) out[c] = -f[c] + static_cast<double>(L.dsc[t] * L.geo[t][c]);
+        }
+    }
+}
+
+// forces[e] = part[e][0] + part[e][1] + ... (slice order), for the edges of
+// the launch's receivers (a grid over graph.num_edges, at least their count)
+__global__ void __launch_bounds__(256) fold_slices_kernel(LayerArgs a, const double* __restrict__ part,
+                                                          double* __restrict__ forces)
+{
+    const EdgeGraph& g = a.graph;
+    const int lo = g.first[a.node_offset] - g.edge_base;
+    const int hi = g.first[a.node_offset + a.node_count] - g.edge_base;
+    const int e = lo + static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x);
+    if (e >= hi) return;
+    const int slices = a.channel_slices;
+    const double* p = part + 3 * static_cast<size_t>(e) * slices;
+    double f[3] = {p[0], p[1], p[2]};
+    for (int q = 1; q < slices; ++q)
+        for (int c = 0; c < 3; ++c) f[c] += p[3 * q + c];
+    double* out = forces + 3 * static_cast<size_t>(e);
+    for (int c = 0; c < 3; ++c) out[c] = f[c];
 }
 
 // ---------------------------------------------------------------------------
@@ -1814,11 +1896,22 @@ hipError_t launch_r1_forward(const LayerArgs& a, const float* r1, const float* c
 static_assert(R1Groups<3, 2>::NREV == 2, "reverse pass list out of date");
 
 hipError_t launch_r1_reverse(const LayerArgs& a, const float* r1, const float* cg, const float* H1,
-                             const float* dPhi1, double* forces, float* msg, hipStream_t s)
+                             const float* dPhi1, double* forces, float* msg, double* part, hipStream_t s)
 {
     if (a.node_count <= 0) return hipSuccess;
     const int threads = node_threads(a.C);
     if (threads > 256) return hipErrorInvalidValue;
+    if (r1_reverse_sliced(a.l_max, a.L_max, a.channel_slices)) {
+        if (!part || a.C != 64 * a.channel_slices || (a.channel_slices != 2 && a.channel_slices != 4))
+            return hipErrorInvalidValue;
+        r1_reverse_sliced_kernel<R1Shape<3, 2>, 0, 1><<<a.node_count * a.channel_slices, 64, 0, s>>>(
+            a, r1, cg, H1, dPhi1, part, msg), note_launch();
+        const hipError_t err = hipGetLastError();
+        if (err != hipSuccess) return err;
+        if (a.graph.num_edges > 0)
+            fold_slices_kernel<<<(a.graph.num_edges + 255) / 256, 256, 0, s>>>(a, part, forces), note_launch();
+        return hipGetLastError();
+    }
     if (a.l_max == 2 && a.L_max == 1)
         r1_reverse_kernel<R1Shape<2, 1>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, dPhi1,
                                                                           forces, msg), note_launch();

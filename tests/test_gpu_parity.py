@@ -186,13 +186,20 @@ def test_medium_shape_parity(native, oracle_lib, medium3):
 
 
 def test_wide_shape_parity(native, oracle_lib, wide):
+    # C = 256 with a 17.8 MB coupling-radial table: the second interaction
+    # runs in four 64-channel slices (forward and reverse), the reverse's
+    # per-slice force parts added in slice order, so repeats agree bitwise
     from symmetrix_amd import Symmetrix, synthetic
 
     path, model = wide
     s = synthetic.water_box(num_molecules=60, seed=0)
     print(f"wide shape water ({len(s)} atoms)", flush=True)
-    got = Symmetrix(path).calculate(s)
+    calc = Symmetrix(path)
+    got = calc.calculate(s)
     _compare(got, _oracle_eval(oracle_lib, model, s), len(s))
+    again = calc.calculate(s.copy())
+    assert np.array_equal(got["forces"], again["forces"])
+    assert got["energy"] == again["energy"]
 
 
 def test_scalar_shape_parity(native, oracle_lib, tmp_path_factory):
