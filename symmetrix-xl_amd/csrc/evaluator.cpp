@@ -600,11 +600,21 @@ void Evaluator::prepare_active_types(const std::vector<int>& node_types)
     h0s_.release();
     a0w_.release();
     a0wt_.release();
-    // the second interaction of a 256-channel model runs in 64-channel
+    // the second-interaction forward of a 256-channel model runs in 64-channel
     // slices, one slice per XCD, when its coefficient table is far beyond one
-    // XCD's L2 (4 MiB)
+    // XCD's L2 (4 MiB), and so does the reverse of the (3, 2) shape
+    // (SXL_R1_REVERSE_SLICES = 1 or C / 64 forces the reverse's count: tests)
     r1_slices_ = 1;
     if (C_ == 256 && r1.size() * sizeof(float) > kR1SliceTableBytes) r1_slices_ = C_ / 64;
+    r1_rev_slices_ = r1_reverse_sliceable(model_.l_max, model_.L_max, C_, r1_slices_) ? r1_slices_ : 1;
+    if (const char* force = std::getenv("SXL_R1_REVERSE_SLICES"); force && force[0]) {
+        const int n = std::atoi(force);
+        if (!r1_reverse_sliceable(model_.l_max, model_.L_max, C_, n))
+            throw std::invalid_argument("SXL_R1_REVERSE_SLICES=" + std::string(force) +
+                                        " does not fit this model (1, or 64-channel slices of the l_max 3, L_max 2 "
+                                        "shape)");
+        r1_rev_slices_ = n;
+    }
     // density-normalisation splines per unordered pair: [pair_u][iv][4]
     auto density_table = [&](const RadialNetwork& net, DeviceBuffer& out) {
         std::vector<float> table(static_cast<std::size_t>(npairs) * NI * 4);
@@ -707,8 +717,8 @@ void Evaluator::allocate_workspace()
     A1_.reserve(NT * nlm_ * C_ * f);
     A1adj_.reserve(NT * nlm_ * C_ * f);
     msg_.reserve(ET * nLM_ * C_ * f);
-    if (r1_reverse_sliced(model_.l_max, model_.L_max, r1_slices_))
-        rpart_.reserve(ET * r1_slices_ * 3 * sizeof(double));
+    if (r1_rev_slices_ > 1)
+        rpart_.reserve(ET * r1_rev_slices_ * 3 * sizeof(double));
     else
         rpart_.release();
     // graph-wide
@@ -1045,7 +1055,7 @@ std::size_t Evaluator::work_bytes_estimate(long long receivers, long long edges,
     const int pre = !tiled && a0_unfold_ ? nlm_ : 0;
     const std::size_t per_node = static_cast<std::size_t>(C_) * sizeof(float) * (3 * nlm_ + pre + nLM_ + nlme_);
     std::size_t per_edge = static_cast<std::size_t>(nLM_) * C_ * sizeof(float);
-    if (r1_reverse_sliced(model_.l_max, model_.L_max, r1_slices_)) per_edge += 3 * sizeof(double) * r1_slices_;
+    if (r1_rev_slices_ > 1) per_edge += 3 * sizeof(double) * r1_rev_slices_;
     if (tiled) per_edge += 7 * sizeof(double) + sizeof(int);
     return per_node * static_cast<std::size_t>(std::max(receivers, 1LL)) +
            per_edge * static_cast<std::size_t>(std::max(edges, 1LL));
@@ -2222,6 +2232,7 @@ void Evaluator::evaluate()
     la.l_max = model_.l_max;
     la.L_max = model_.L_max;
     la.channel_slices = r1_slices_;
+    la.reverse_slices = r1_rev_slices_;
     la.node_offset = 0;
     la.node_count = N;
     density_args(la, nullptr);
@@ -2403,6 +2414,7 @@ void Evaluator::evaluate_tiled()
     la.l_max = model_.l_max;
     la.L_max = model_.L_max;
     la.channel_slices = r1_slices_;
+    la.reverse_slices = r1_rev_slices_;
     density_args(la, nullptr);
     la.type_order = node_order_.as<int>();
     hipStream_t s = stream_;

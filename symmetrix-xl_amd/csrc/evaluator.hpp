@@ -442,7 +442,8 @@ private:
     // (2^31 - 1; SXL_EDGE_INDEX_LIMIT lowers it, a test hook); the tiled plan
     // indexes edges per tile and has no such limit
     long long edge_index_limit_ = 2147483647LL;
-    int r1_slices_ = 1;            // channel slices of the second interaction
+    int r1_slices_ = 1;            // channel slices of the second-interaction forward
+    int r1_rev_slices_ = 1;        // and of its reverse
     // host copies of uploads in flight, released at the next wait()
     std::vector<std::vector<unsigned char>> staged_;
     double cell_[9] = {}, inverse_cell_[9] = {};

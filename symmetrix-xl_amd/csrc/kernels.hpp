@@ -189,12 +189,15 @@ struct LayerArgs {
     int local_base = 0;
     // receivers of this launch in element-type order (layer-0 kernels), or null
     const int* type_order = nullptr;
-    // Second interaction: workgroups per receiver, each over a slice of 64
-    // channels (1: one workgroup of all channels); the forward's 4 waves
-    // split the edges, the (3, 2) reverse runs one wave per slice.  Set
-    // where the coefficient table outgrows one XCD's L2: each XCD then reads
-    // only its slice's columns.
+    // Second-interaction forward: workgroups per receiver, each over a slice
+    // of 64 channels with its 4 waves splitting the edges (1: one workgroup
+    // of all channels).  Set where the coefficient table outgrows one XCD's
+    // L2: each XCD then reads only its slice's columns.
     int channel_slices = 1;
+    // Second-interaction reverse: one-wave workgroups per (receiver,
+    // 64-channel slice), block b on XCD b mod 8 running slice
+    // b mod reverse_slices (1: one workgroup of all channels).
+    int reverse_slices = 1;
     // Layer 0 with the unfolded table: rows per unordered pair table (no H0,
     // no A0_W); each edge's radial values are scaled by
     // h0[source's active type][k] and A0_W is applied to the node sums by
@@ -244,13 +247,13 @@ struct ReadoutArgs {
 hipError_t launch_readout(const ReadoutArgs& a, hipStream_t s);
 
 // Layer 1 reverse: directed forces (stored) and per-edge H1-adjoint messages.
-// With channel slices on the (3, 2) shape (r1_reverse_sliced) each slice's
+// With reverse_slices > 1 (the (3, 2) shape, C = 64 x slices) each slice's
 // part of the directed forces goes to `part` ([edges][slices][3] doubles,
 // indexed like `forces`) before they are added in slice order; otherwise
 // `part` is not read and may be null.
-inline bool r1_reverse_sliced(int l_max, int L_max, int channel_slices)
+inline bool r1_reverse_sliceable(int l_max, int L_max, int C, int slices)
 {
-    return channel_slices > 1 && l_max == 3 && L_max == 2;
+    return slices == 1 || (l_max == 3 && L_max == 2 && (slices == 2 || slices == 4) && C == 64 * slices);
 }
 hipError_t launch_r1_reverse(const LayerArgs& a, const float* r1, const float* cg, const float* H1,
                              const float* dPhi1, double* forces, float* msg, double* part, hipStream_t s);

@@ -1160,8 +1160,8 @@ r1_reverse_sliced_kernel(LayerArgs a, const float* __restrict__ r1, const float*
     static_assert((S::LMAX + 1) * (S::LMAX + 1) <= 16, "harmonics beyond l = 3");
     __shared__ RevTileLds<MAXT, kForcePartsGrouped> L;
     int slice;
-    const int i = a.node_offset + xcd_slice_receiver(blockIdx.x, a.node_count, a.channel_slices, slice);
-    const int slices = a.channel_slices;
+    const int i = a.node_offset + xcd_slice_receiver(blockIdx.x, a.node_count, a.reverse_slices, slice);
+    const int slices = a.reverse_slices;
     const int k = slice * 64 + static_cast<int>(threadIdx.x);  // < C: C = 64 slices
     const EdgeGraph& g = a.graph;
     const float dcoef = a.d1.table && slice == 0 ? a.d1.dot[i] / a.d1.scale[i] : 0.0f;
@@ -1202,7 +1202,7 @@ __global__ void __launch_bounds__(256) fold_slices_kernel(LayerArgs a, const dou
     const int hi = g.first[a.node_offset + a.node_count] - g.edge_base;
     const int e = lo + static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x);
     if (e >= hi) return;
-    const int slices = a.channel_slices;
+    const int slices = a.reverse_slices;
     const double* p = part + 3 * static_cast<size_t>(e) * slices;
     double f[3] = {p[0], p[1], p[2]};
     for (int q = 1; q < slices; ++q)
@@ -1901,10 +1901,9 @@ hipError_t launch_r1_reverse(const LayerArgs& a, const float* r1, const float* c
     if (a.node_count <= 0) return hipSuccess;
     const int threads = node_threads(a.C);
     if (threads > 256) return hipErrorInvalidValue;
-    if (r1_reverse_sliced(a.l_max, a.L_max, a.channel_slices)) {
-        if (!part || a.C != 64 * a.channel_slices || (a.channel_slices != 2 && a.channel_slices != 4))
-            return hipErrorInvalidValue;
-        r1_reverse_sliced_kernel<R1Shape<3, 2>, 0, 1><<<a.node_count * a.channel_slices, 64, 0, s>>>(
+    if (a.reverse_slices > 1) {
+        if (!part || !r1_reverse_sliceable(a.l_max, a.L_max, a.C, a.reverse_slices)) return hipErrorInvalidValue;
+        r1_reverse_sliced_kernel<R1Shape<3, 2>, 0, 1><<<a.node_count * a.reverse_slices, 64, 0, s>>>(
             a, r1, cg, H1, dPhi1, part, msg), note_launch();
         const hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;

@@ -202,6 +202,41 @@ def test_wide_shape_parity(native, oracle_lib, wide):
     assert got["energy"] == again["energy"]
 
 
+def test_wide_shape_sliced_reverse_equals_unsliced(native, wide, monkeypatch):
+    """The channel-sliced R1 reverse (four one-wave workgroups per receiver,
+    force parts added in slice order) against the one-workgroup grouped
+    reverse (SXL_R1_REVERSE_SLICES=1) on the same graph: node energies are
+    identical (the reverse does not touch them); directed forces, atom forces
+    and the virial differ only by FP64 summation order."""
+    from symmetrix_amd import MACEKokkosFloat, synthetic
+
+    path, model = wide
+    s = synthetic.water_box(num_molecules=60, seed=3)
+    types = synthetic.node_types(s, model["atomic_numbers"])
+
+    def run():
+        ev = MACEKokkosFloat(path)
+        gen = ev._prepare_periodic_factorized_graph(types, s.positions, s.cell, np.linalg.inv(s.cell),
+                                                    model["r_cut"] + 0.5)["generation"]
+        ev._compute_prepared_factorized_positions(gen, s.positions)
+        return (ev.node_energies.copy(), ev.node_forces.reshape(-1, 3).copy(),
+                ev._reduce_atom_forces(len(s), None, None, gen), ev._reduce_stress(s.volume, None, gen))
+
+    sliced = run()
+    monkeypatch.setenv("SXL_R1_REVERSE_SLICES", "1")
+    whole = run()
+    print(f"wide water ({len(s)} atoms): max|df_ij| = {np.max(np.abs(sliced[1] - whole[1])):.2e}", flush=True)
+    assert np.array_equal(sliced[0], whole[0])
+    scale = float(np.max(np.abs(whole[1])))
+    assert scale > 0.0
+    assert np.max(np.abs(sliced[1] - whole[1])) <= 1e-12 * scale
+    assert np.max(np.abs(sliced[2] - whole[2])) <= 1e-11 * scale
+    assert np.max(np.abs(sliced[3] - whole[3])) <= 1e-11 * max(1.0, float(np.max(np.abs(whole[3]))))
+    monkeypatch.setenv("SXL_R1_REVERSE_SLICES", "3")
+    with pytest.raises(ValueError, match="SXL_R1_REVERSE_SLICES"):
+        run()
+
+
 def test_scalar_shape_parity(native, oracle_lib, tmp_path_factory):
     # L_max = 0: scalar H1, 4 coupling paths (l, 0 -> l), 16 terms
     from symmetrix_amd import Symmetrix, synthetic
