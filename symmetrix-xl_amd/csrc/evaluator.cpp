@@ -1960,28 +1960,26 @@ void Evaluator::compute_positions(std::uint64_t generation, const double* positi
     const CallStart start;
     require_geometry(generation);
     const int N = num_nodes_;
-    if (N > 0 && positions != positions_.as<double>()) {
+    // device positions are read in place by the displacement kernel (nothing
+    // later in the evaluation reads them)
+    const double* src = device_positions ? positions : positions_.as<double>();
+    if (N > 0 && !device_positions) {
+        // through pinned memory: the copy is DMA queued with the kernels (the
+        // previous evaluation's wait has drained the buffer)
         const std::size_t bytes = static_cast<std::size_t>(N) * 3 * sizeof(double);
-        if (device_positions) {
-            hip_check(hipMemcpyAsync(positions_.as<double>(), positions, bytes, hipMemcpyDeviceToDevice, stream_),
-                      "positions");
-        } else {
-            // through pinned memory: the copy is DMA queued with the kernels
-            // (the previous evaluation's wait has drained the buffer)
-            pinned_positions_.reserve(bytes);
-            std::memcpy(pinned_positions_.as<double>(), positions, bytes);
-            hip_check(hipMemcpyAsync(positions_.as<double>(), pinned_positions_.as<double>(), bytes,
-                                     hipMemcpyHostToDevice, stream_),
-                      "positions");
-        }
+        pinned_positions_.reserve(bytes);
+        std::memcpy(pinned_positions_.as<double>(), positions, bytes);
+        hip_check(hipMemcpyAsync(positions_.as<double>(), pinned_positions_.as<double>(), bytes,
+                                 hipMemcpyHostToDevice, stream_),
+                  "positions");
     }
     results_to_host_ = !device_positions;
     for (int i = 0; i < kNumStages; ++i) stage_used_[i] = false;
     mark(kStageGeometry, false);
     const double* cell = cell_dev_.as<double>();
     const GeometryRef ref = geometry_ref();
-    hip_check(launch_atom_displacements(N, positions_.as<double>(), ref, cell, cell + 9, disp_.as<double>(),
-                                        totals_.as<double>() + 12, stream_),
+    hip_check(launch_atom_displacements(N, src, ref, cell, cell + 9, disp_.as<double>(), totals_.as<double>() + 12,
+                                        stream_),
               "displacements");
     // the tiled plan forms each tile's edges from the displacements per tile
     if (tile_receivers_ == 0)
