@@ -398,6 +398,20 @@ int sxl_model_heads_json(const sxl_evaluator* evaluator, char* buffer, int64_t c
  * is not larger than the length). */
 int sxl_execution_plan_json(const sxl_evaluator* evaluator, char* buffer, int64_t capacity, int64_t* length);
 
+/* Device memory by role and the plan's capacities of the prepared graph, as
+ * a JSON object of integers: graph_generation, num_nodes, num_edges, tiled,
+ * tile_receivers, num_tiles, max_tile_edges, tile_runs, run_bytes,
+ * graph_bytes, geometry_bytes, node_work_bytes, edge_work_bytes, phi1_bytes,
+ * message_bytes, readout_bytes, feature_bytes, reduction_bytes, table_bytes,
+ * device_free_bytes, device_total_bytes, a0_unfolded, r1_forward_slices,
+ * r1_reverse_slices.  The source of the reference's workspace and policy
+ * properties (phi1_workspace_bytes, readout_workspace_bytes,
+ * dual_layer_workspace_*, execution_planned_*, low_memory_*;
+ * symmetrix/source/cpp/mace_kokkos.cpp:517-630,
+ * libsymmetrix/source/mace_kokkos_runtime.cpp:2366-2511, 4093-4336).
+ * Buffer, capacity and length as for sxl_execution_plan_json. */
+int sxl_workspace_json(const sxl_evaluator* evaluator, char* buffer, int64_t capacity, int64_t* length);
+
 /* Tiled ("fixed workspace") execution for capacity runs: receivers are
  * processed in tiles with one reused work arena; graph-wide state is H1, its
  * adjoint and two per-node scalar blocks.  With allow != 0 the plan of the

@@ -553,6 +553,20 @@ int sxl_execution_plan_json(const sxl_evaluator* ev, char* buffer, int64_t capac
     });
 }
 
+int sxl_workspace_json(const sxl_evaluator* ev, char* buffer, int64_t capacity, int64_t* length)
+{
+    if (!ev || !length) return null_handle();
+    return guarded([&] {
+        const std::string text = ev->impl.workspace_json();
+        *length = static_cast<int64_t>(text.size());
+        if (!buffer) return;
+        if (capacity <= static_cast<int64_t>(text.size()))
+            throw std::length_error("workspace buffer is smaller than the report");
+        std::copy(text.begin(), text.end(), buffer);
+        buffer[text.size()] = '\0';
+    });
+}
+
 int sxl_set_workspace_receiver_limit(sxl_evaluator* ev, int receivers)
 {
     if (!ev) return null_handle();

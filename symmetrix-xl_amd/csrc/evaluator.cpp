@@ -1127,6 +1127,67 @@ std::string ExecutionPlanReport::json() const
     return out;
 }
 
+std::string Evaluator::workspace_json() const
+{
+    auto sum = [](std::initializer_list<const DeviceBuffer*> buffers) {
+        std::size_t total = 0;
+        for (const DeviceBuffer* b : buffers) total += b->bytes();
+        return total;
+    };
+    const bool tiled = tile_receivers_ > 0;
+    long long max_tile_edges = 0, runs = 0;
+    for (int t = 0; tiled && t < num_tiles_; ++t)
+        max_tile_edges = std::max(max_tile_edges, tile_first_edge_[t + 1] - tile_first_edge_[t]);
+    if (tiled && !tile_run_offsets_.empty()) runs = tile_run_offsets_.back();
+    std::size_t free_bytes = 0, total_bytes = 0;
+    if (hipMemGetInfo(&free_bytes, &total_bytes) != hipSuccess) free_bytes = total_bytes = 0;
+    const std::size_t node_work = sum({&A0_, &A0pre_, &M0_, &M0s_, &Phi1_, &A1_, &A1adj_, &scale1_, &dot1_});
+    const std::size_t edge_work = sum({&msg_, &rpart_, &forces_, &tile_forces_, &tile_xyz_, &tile_r_, &tile_pair_});
+    std::string out = "{";
+    auto field = [&](const char* k, long long v) {
+        if (out.size() > 1) out += ", ";
+        out += '"';
+        out += k;
+        out += "\": " + std::to_string(v);
+    };
+    // 0 when no graph is prepared or a setter has invalidated it
+    field("graph_generation", static_cast<long long>(prepared_generation_ == generation_ ? generation_ : 0));
+    field("num_nodes", num_nodes_);
+    field("num_edges", num_edges_);
+    field("tiled", tiled ? 1 : 0);
+    field("tile_receivers", tile_receivers_);
+    field("num_tiles", tiled ? num_tiles_ : 0);
+    field("max_tile_edges", max_tile_edges);
+    field("tile_runs", runs);
+    field("run_bytes", static_cast<long long>(sum({&run_source_, &run_start_, &run_length_})));
+    field("graph_bytes", static_cast<long long>(sum({&node_types_, &first_, &receiver_, &source_, &tfirst_, &tedge_,
+                                                     &edge_pair_, &run_source_, &run_start_, &run_length_,
+                                                     &node_order_, &m0_blocks_, &m0r_blocks_, &readout_blocks_,
+                                                     &pgraph_.first, &pgraph_.sources, &pgraph_.shifts,
+                                                     &pgraph_.fractional_xyz, &pgraph_.fractional_positions})));
+    field("geometry_bytes", static_cast<long long>(sum({&disp_, &positions_, &cell_dev_, &xyz_, &r_, &geo_positions_,
+                                                        &geo_edges_, &geo_shifts_, &tile_xyz_, &tile_r_})));
+    field("node_work_bytes", static_cast<long long>(node_work));
+    field("edge_work_bytes", static_cast<long long>(edge_work));
+    field("phi1_bytes", static_cast<long long>(Phi1_.bytes()));
+    field("message_bytes", static_cast<long long>(msg_.bytes()));
+    field("readout_bytes", static_cast<long long>(sum({&energies_, &direct_})));
+    field("feature_bytes", static_cast<long long>(sum({&H1_, &H1adj_, &atom_forces_})));
+    field("reduction_bytes", static_cast<long long>(sum({&partials_, &totals_, &scratch_})));
+    field("table_bytes", static_cast<long long>(sum({&type_active_, &r0f_, &r1_, &p0_coef_, &p0_packed_, &p0_offsets_,
+                                                     &p1_coef_, &p1_packed_, &p1_offsets_, &h2m0_, &h2m0t_, &e0_,
+                                                     &h1w_, &h1wt_, &h2m1_, &h2m1t_, &q_, &w1_, &w2_, &cg_, &p0w_,
+                                                     &p0wt_, &residual_, &residual_fused_, &r0u_, &h0s_, &a0w_,
+                                                     &a0wt_})));
+    field("device_free_bytes", static_cast<long long>(free_bytes));
+    field("device_total_bytes", static_cast<long long>(total_bytes));
+    field("a0_unfolded", a0_unfold_ ? 1 : 0);
+    field("r1_forward_slices", r1_slices_);
+    field("r1_reverse_slices", r1_rev_slices_);
+    out += "}";
+    return out;
+}
+
 // Nodes of each tile (the whole graph untiled) grouped by active type, in
 // ascending node order within a type, cut into blocks for the node kernels.
 void Evaluator::plan_node_blocks()
@@ -1341,6 +1402,7 @@ void Evaluator::finish_graph(const std::vector<int>& host_pairs)
     allocate_workspace();
     wait("graph preparation");
     ++generation_;
+    prepared_generation_ = generation_;
     evaluated_generation_ = 0;
     reduced_ = false;
     stats_.graph_builds += 1;

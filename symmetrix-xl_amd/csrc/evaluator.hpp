@@ -343,6 +343,9 @@ public:
     void set_execution_plan_request(const std::string& algorithm, const std::string& profile,
                                     const std::string& debug_plan);
     const ExecutionPlanReport& execution_plan_report() const { return plan_report_; }
+    // Device bytes by role and the plan's capacities, as a JSON object (the
+    // workspace and policy properties of the Python class are read from it).
+    std::string workspace_json() const;
 
     // Per-stage device time (ms) accumulated over profiled evaluations.
     void set_profiling(bool enable);
@@ -432,6 +435,7 @@ private:
 
     // graph
     std::uint64_t generation_ = 0;
+    std::uint64_t prepared_generation_ = 0;  // generation_ right after the last successful preparation
     std::uint64_t evaluated_generation_ = 0;
     bool periodic_ = false;
     int num_nodes_ = 0;

@@ -558,6 +558,272 @@ class MACEKokkosFloat:
         check(library().sxl_stats(self._h, ctypes.byref(s)))
         return {name: getattr(s, name) for name, _ in _native.Stats._fields_}
 
+    # --- workspace and policy properties (reference mace_kokkos.cpp:459-723;
+    # accessors libsymmetrix/source/mace_kokkos_runtime.cpp:2366-2511,
+    # 3919-3937, 4093-4390).  Each reports what this evaluator holds for the
+    # prepared graph; subsystems it does not have (JIT plugins, stored
+    # harmonics) report their inactive value.
+    def _workspace(self):
+        length = c_i64(0)
+        check(library().sxl_workspace_json(self._h, None, 0, ctypes.byref(length)))
+        buf = ctypes.create_string_buffer(int(length.value) + 1)
+        check(library().sxl_workspace_json(self._h, buf, len(buf), ctypes.byref(length)))
+        return json.loads(buf.value.decode())
+
+    def _candidate_bytes(self, plan_id):
+        for c in self.execution_plan_report["candidates"]:
+            if c["id"] == plan_id:
+                return int(c["estimated_bytes"])
+        return 0
+
+    @property
+    def factorized_graph_generation(self):
+        """Generation of the prepared graph (0: none)."""
+        return self._workspace()["graph_generation"]
+
+    @property
+    def factorized_ready(self):
+        return self._workspace()["graph_generation"] != 0
+
+    @property
+    def factorized_tiled_ready(self):
+        w = self._workspace()
+        return w["graph_generation"] != 0 and bool(w["tiled"])
+
+    @property
+    def factorized_fallback_evaluation_count(self):
+        """Evaluations that left the native kernels: none (there is no fallback path)."""
+        return 0
+
+    @property
+    def factorized_schedule_build_count(self):
+        """Node-block and tile schedules built: one per prepared graph."""
+        return self.stats["graph_builds"]
+
+    @property
+    def factorized_source_owned_reverse(self):
+        """The R1 reverse is receiver-owned (per-edge H1-adjoint messages
+        gathered per source)."""
+        return False
+
+    @property
+    def factorized_jit_ready(self):
+        """No JIT plugin is loaded by the evaluator (the R1 plugin ABI is a
+        separate ahead-of-time library)."""
+        return False
+
+    @property
+    def factorized_jit_launch_count(self):
+        return 0
+
+    @property
+    def factorized_jit_forward_launch_count(self):
+        return 0
+
+    @property
+    def factorized_jit_reverse_launch_count(self):
+        return 0
+
+    @property
+    def factorized_workspace_bytes(self):
+        """Device bytes of the evaluation's work arrays (node and edge work,
+        features, reductions) for the prepared graph."""
+        w = self._workspace()
+        return w["node_work_bytes"] + w["edge_work_bytes"] + w["feature_bytes"] + w["reduction_bytes"]
+
+    @property
+    def factorized_graph_device_capacity_bytes(self):
+        return self._workspace()["graph_bytes"]
+
+    @property
+    def phi1_workspace_bytes(self):
+        """Bytes of Phi1 (its adjoint reuses the buffer)."""
+        return self._workspace()["phi1_bytes"]
+
+    @property
+    def phi1_policy(self):
+        """"receiver-local" under the tiled plan (Phi1 per tile), else "retained"."""
+        return "receiver-local" if self._workspace()["tiled"] else "retained"
+
+    @property
+    def readout_workspace_bytes(self):
+        """Bytes the readout writes besides the A1 adjoint: node energies and
+        the direct scalar adjoint."""
+        return self._workspace()["readout_bytes"]
+
+    @property
+    def readout_policy(self):
+        """"fused": one kernel computes the readout and its adjoint per node
+        block; nothing of the forward is kept for the reverse."""
+        return "fused"
+
+    @property
+    def edge_geometry_policy(self):
+        """Edge vectors and lengths held as float64 (the reference's
+        "cartesian-f64-v1" layout)."""
+        return "cartesian-f64-v1"
+
+    @property
+    def compact_edge_geometry_bytes(self):
+        return 0
+
+    @property
+    def execution_geometry_workspace_bytes(self):
+        return self._workspace()["geometry_bytes"]
+
+    @property
+    def harmonic_value_bytes(self):
+        """Harmonics are formed per edge tile in LDS; no array holds them."""
+        return 0
+
+    @property
+    def harmonic_gradient_bytes(self):
+        return 0
+
+    @property
+    def shuffled_coordinate_bytes(self):
+        return 0
+
+    @property
+    def scalar_size_bytes(self):
+        return 4
+
+    @property
+    def dual_layer_workspace_planned_receivers(self):
+        return self._workspace()["tile_receivers"]
+
+    @property
+    def dual_layer_workspace_active_receivers(self):
+        return self._workspace()["tile_receivers"]
+
+    @property
+    def dual_layer_workspace_planned_edges(self):
+        """Edges of the largest tile (the arena's edge capacity)."""
+        return self._workspace()["max_tile_edges"]
+
+    @property
+    def dual_layer_workspace_active_edges(self):
+        return self._workspace()["max_tile_edges"]
+
+    @property
+    def dual_layer_workspace_batch_count(self):
+        """Receiver tiles of the prepared graph (0 untiled)."""
+        return self._workspace()["num_tiles"]
+
+    @property
+    def dual_layer_workspace_bytes(self):
+        """The tiled plan's reused arena: per-receiver work arrays and per-edge
+        geometry, pair codes, directed forces and messages (0 untiled)."""
+        w = self._workspace()
+        return w["node_work_bytes"] + w["edge_work_bytes"] if w["tiled"] else 0
+
+    @property
+    def dual_layer_workspace_bytes_per_receiver(self):
+        w = self._workspace()
+        return w["node_work_bytes"] // w["tile_receivers"] if w["tiled"] else 0
+
+    @property
+    def dual_layer_workspace_bytes_per_edge(self):
+        w = self._workspace()
+        return w["edge_work_bytes"] // max(w["max_tile_edges"], 1) if w["tiled"] else 0
+
+    @property
+    def dual_layer_schedule_bytes(self):
+        """Bytes of the tiles' (source, start, length) runs."""
+        return self._workspace()["run_bytes"]
+
+    @property
+    def dual_layer_source_segment_count(self):
+        """(source, tile) runs of the tiled plan's source-grouped edge lists."""
+        return self._workspace()["tile_runs"]
+
+    @property
+    def execution_active_receiver_count(self):
+        return self._workspace()["num_nodes"]
+
+    @property
+    def execution_active_feature_node_count(self):
+        return self._workspace()["num_nodes"]
+
+    @property
+    def execution_active_edge_count(self):
+        return self._workspace()["num_edges"]
+
+    @property
+    def execution_planned_receiver_capacity(self):
+        w = self._workspace()
+        return w["tile_receivers"] if w["tiled"] else w["num_nodes"]
+
+    @property
+    def execution_planned_feature_node_capacity(self):
+        return self._workspace()["num_nodes"]
+
+    @property
+    def execution_planned_edge_capacity(self):
+        w = self._workspace()
+        return w["max_tile_edges"] if w["tiled"] else w["num_edges"]
+
+    @property
+    def execution_planned_capacity_bytes(self):
+        """The selected plan's memory estimate."""
+        return self._candidate_bytes(self.execution_plan_report["selected_id"])
+
+    @property
+    def execution_capacity_selection_reason(self):
+        return self.execution_plan_report["selection_reason"]
+
+    @property
+    def low_memory(self):
+        """The prepared graph runs the tiled (capacity) plan."""
+        return bool(self._workspace()["tiled"])
+
+    @property
+    def low_memory_requested(self):
+        return self.execution_plan_report["requested_profile"] == "capacity" and self.allow_fixed_workspace
+
+    @property
+    def low_memory_policy(self):
+        """"disabled" (tiles not allowed), "pending" (no graph), "capacity"
+        (tiled plan) or "speed" (untiled plan)."""
+        if not self.low_memory_requested:
+            return "disabled"
+        w = self._workspace()
+        if w["graph_generation"] == 0:
+            return "pending"
+        return "capacity" if w["tiled"] else "speed"
+
+    @property
+    def low_memory_selection_reason(self):
+        return self.execution_plan_report["selection_reason"]
+
+    @property
+    def low_memory_device_free_bytes(self):
+        return self._workspace()["device_free_bytes"]
+
+    @property
+    def low_memory_device_total_bytes(self):
+        return self._workspace()["device_total_bytes"]
+
+    @property
+    def low_memory_available_bytes(self):
+        return int(self.execution_plan_report["available_bytes"])
+
+    @property
+    def low_memory_reserve_bytes(self):
+        return int(self.execution_plan_report["reserve_bytes"])
+
+    @property
+    def low_memory_speed_estimated_bytes(self):
+        return self._candidate_bytes("mh0-direct-speed")
+
+    @property
+    def low_memory_capacity_estimated_bytes(self):
+        return self._candidate_bytes("mh0-dual-layer-tiled-v1")
+
+    @property
+    def low_memory_selected_estimated_bytes(self):
+        return self.execution_planned_capacity_bytes
+
 
 # --- runtime lifecycle (reference tools_kokkos.cpp:522-534) ---------------------
 def _init_kokkos():

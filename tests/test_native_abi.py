@@ -249,3 +249,31 @@ print("lifecycle ok")
     out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
     assert out.returncode == 0, out.stderr
     assert "lifecycle ok" in out.stdout
+
+
+def test_reference_workspace_and_policy_properties_exist():
+    """The reference's read-only workspace and policy properties that this
+    evaluator reports (symmetrix/source/cpp/mace_kokkos.cpp:459-723) are
+    properties of MACEKokkosFloat; their values are checked on the GPU."""
+    from symmetrix_amd import MACEKokkosFloat
+
+    names = """factorized_graph_generation factorized_ready factorized_tiled_ready
+        factorized_fallback_evaluation_count factorized_schedule_build_count factorized_source_owned_reverse
+        factorized_jit_ready factorized_jit_launch_count factorized_jit_forward_launch_count
+        factorized_jit_reverse_launch_count factorized_workspace_bytes factorized_graph_device_capacity_bytes
+        phi1_workspace_bytes phi1_policy readout_workspace_bytes readout_policy edge_geometry_policy
+        compact_edge_geometry_bytes execution_geometry_workspace_bytes harmonic_value_bytes
+        harmonic_gradient_bytes shuffled_coordinate_bytes scalar_size_bytes
+        dual_layer_workspace_planned_receivers dual_layer_workspace_active_receivers
+        dual_layer_workspace_planned_edges dual_layer_workspace_active_edges dual_layer_workspace_batch_count
+        dual_layer_workspace_bytes dual_layer_workspace_bytes_per_receiver dual_layer_workspace_bytes_per_edge
+        dual_layer_schedule_bytes dual_layer_source_segment_count dual_layer_tiled_evaluation_count
+        execution_active_receiver_count execution_active_feature_node_count execution_active_edge_count
+        execution_planned_receiver_capacity execution_planned_feature_node_capacity
+        execution_planned_edge_capacity execution_planned_capacity_bytes execution_capacity_selection_reason
+        low_memory low_memory_requested low_memory_policy low_memory_selection_reason
+        low_memory_device_free_bytes low_memory_device_total_bytes low_memory_available_bytes
+        low_memory_reserve_bytes low_memory_speed_estimated_bytes low_memory_capacity_estimated_bytes
+        low_memory_selected_estimated_bytes""".split()
+    for name in names:
+        assert isinstance(getattr(MACEKokkosFloat, name, None), property), name
