@@ -724,7 +724,13 @@ void Evaluator::allocate_workspace()
     // graph-wide
     H1_.reserve(N * nLM_ * C_ * f);
     H1adj_.reserve(N * nLM_ * C_ * f);
-    direct_.reserve(N * C_ * f);
+    // the tiled plan writes the readout's direct adjoint over the scalar M0
+    // block (M0s_): the readout reads a node's block before it writes that
+    // node's adjoint, and nothing reads the block afterwards
+    if (tiled)
+        direct_.release();
+    else
+        direct_.reserve(N * C_ * f);
     if (model_.A1_scaled) {
         scale1_.reserve(N * f);
         dot1_.reserve(N * f);
@@ -1017,8 +1023,8 @@ std::size_t Evaluator::held_graph_bytes() const
 // receivers, pair codes, geometry and directed forces (periodic: fractional
 // edge vectors) and per node the source-major offsets; the tiled plan per
 // edge the tiles' source-grouped lists (and pair codes when a caller's
-// neighbour types differ from its sources'), per node the scalar M0 block,
-// and three ints per run.
+// neighbour types differ from its sources') and three ints per run; its
+// scalar M0 block shares the direct adjoint's array.
 std::size_t Evaluator::graph_bytes_estimate(bool tiled, long long runs) const
 {
     const std::size_t N = num_nodes_, E = static_cast<std::size_t>(num_edges_);
@@ -1036,7 +1042,6 @@ std::size_t Evaluator::graph_bytes_estimate(bool tiled, long long runs) const
         per_node += sizeof(int);
     } else {
         per_edge += sizeof(int);
-        per_node += C * f;
         if (!pair_from_types_) per_edge += sizeof(int);
         extra += 3 * sizeof(int) * static_cast<std::size_t>(std::max(runs, 0LL));
     }
@@ -2185,7 +2190,7 @@ void Evaluator::gemm_h1(int nodes, int node_base, const float* in, long long in_
 // add_h1_affine_direct_adjoint, mace_kokkos_h1_phi1.cpp:296-345).
 void Evaluator::add_direct(int nodes, int node_base, float* M0adj, hipStream_t s)
 {
-    const float* direct = direct_.as<float>() + static_cast<std::size_t>(node_base) * C_;
+    const float* direct = (tile_receivers_ > 0 ? M0s_ : direct_).as<float>() + static_cast<std::size_t>(node_base) * C_;
     if (!model_.pre_linear_up) {
         hip_check(launch_add_direct(nodes, C_, nLM_, direct, M0adj, s), "direct adjoint");
         return;
@@ -2602,7 +2607,7 @@ void Evaluator::evaluate_tiled()
     ra.scale = static_cast<float>(model_.readout_scale);
     ra.E0 = e0_.as<double>();
     ra.energies = energies_.as<double>();
-    ra.direct = direct_.as<float>();
+    ra.direct = M0s;  // over each node's scalar block, once the readout has read it
     ra.A1_adj = A1adj_.as<float>();
     density_args(la, &ra);
     float* dPhi1 = Phi1_.as<float>();
