@@ -151,6 +151,19 @@ public:
         return generation;
     }
 
+    // the same from device arrays (the reference's Kokkos::View overload,
+    // mace_kokkos.hpp:339-460): node_types, num_neigh [num_nodes],
+    // neigh_indices, neigh_types [sum of num_neigh] in device memory
+    std::uint64_t prepare_factorized_graph_device(int num_nodes, const int* d_node_types, const int* d_num_neigh,
+                                                  const int* d_neigh_indices, const int* d_neigh_types)
+    {
+        detail::require(num_nodes >= 0, "num_nodes must be non-negative.");
+        std::uint64_t generation = 0;
+        detail::check(sxl_prepare_graph_device(handle_, num_nodes, d_node_types, d_num_neigh, d_neigh_indices,
+                                               d_neigh_types, &generation));
+        return generation;
+    }
+
     // prepare_periodic_factorized_graph(node_types, positions, cell, inverse_cell, neighbor_cutoff)
     //   -> {generation, num_edges}
     std::pair<std::uint64_t, std::size_t> prepare_periodic_factorized_graph(std::span<const int> node_types,
@@ -250,6 +263,19 @@ public:
         evaluated(graph_generation);
     }
 
+    // the same two evaluations from device arrays: xyz [3 E], r [E] or
+    // positions [3 N] in device memory (results stay on the device until read)
+    void compute_prepared_factorized_device(std::uint64_t graph_generation, const double* d_xyz, const double* d_r)
+    {
+        detail::check(sxl_compute_prepared_device(handle_, graph_generation, d_xyz, d_r));
+        evaluated(graph_generation);
+    }
+    void compute_prepared_factorized_positions_device(std::uint64_t graph_generation, const double* d_positions)
+    {
+        detail::check(sxl_compute_prepared_positions_device(handle_, graph_generation, d_positions));
+        evaluated(graph_generation);
+    }
+
     // compute_node_energies_forces(num_nodes, node_types, num_neigh, neigh_indices,
     //                              neigh_types, xyz, r, execution_graph_generation = 0)
     void compute_node_energies_forces(int num_nodes, std::span<const int> node_types, std::span<const int> num_neigh,
@@ -300,6 +326,14 @@ public:
     {
         return detail::json_text([this](char* b, std::int64_t c, std::int64_t* n) {
             return sxl_execution_plan_json(handle_, b, c, n);
+        });
+    }
+
+    // device memory by role and the plan's capacities (sxl_workspace_json)
+    std::string workspace_json() const
+    {
+        return detail::json_text([this](char* b, std::int64_t c, std::int64_t* n) {
+            return sxl_workspace_json(handle_, b, c, n);
         });
     }
 

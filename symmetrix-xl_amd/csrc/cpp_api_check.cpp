@@ -65,6 +65,11 @@ int run(const std::string& model, const std::string& head, const std::string& in
     const double energy = ev.total_energy(generation);
     const std::vector<double>& energies = ev.node_energies();
     const std::vector<double>& directed = ev.node_forces();
+    // the workspace report names the prepared graph
+    if (ev.workspace_json().find("\"graph_generation\": " + std::to_string(generation)) == std::string::npos) {
+        std::cerr << "workspace_json: generation " << generation << " missing\n";
+        return 3;
+    }
 
     std::ofstream out(out_path, std::ios::binary);
     write_values(out, &energy, 1);
