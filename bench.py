@@ -186,6 +186,17 @@ def cpu_model_name():
     return "unknown"
 
 
+def host_has_x86_64_v3():
+    """AVX2, FMA, BMI2 and MOVBE on this host: the oracle's vectorised timing
+    build (oracle/liboracle_timed.so) runs here."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            flags = f.read()
+    except OSError:
+        return False
+    return all(f" {flag}" in flags for flag in ("avx2", "fma", "bmi2", "movbe"))
+
+
 def cpu_baseline(model_path, structure, cutoff, cpus, calls, warmup, single_thread=True):
     """The oracle's OpenMP restatement of the reference CPU path on this
     host, run like the reference's OpenMP qualification
@@ -193,9 +204,12 @@ def cpu_baseline(model_path, structure, cutoff, cpus, calls, warmup, single_thre
     physical core, threads bound close to cores (OMP_PROC_BIND=close,
     OMP_PLACES=cores, set before the OpenMP runtime loads) and the process
     pinned to those cores; `warmup` untimed calls, then the median of `calls`
-    complete calls (compute + atom-force and stress reductions).  Also
-    returns the result of the last call (energy, atom forces, stress) for the
-    parity check of the GPU result."""
+    complete calls (compute + atom-force and stress reductions).  The timed
+    calls run the oracle's vectorised build (oracle/liboracle_timed.so, where
+    the host has x86-64-v3); one more, untimed call of the checker build gives
+    the result (energy, atom forces, stress) for the parity check of the GPU
+    result.  Returns the median, the times, the single-thread time, that
+    result and whether the vectorised build was timed."""
     os.environ.setdefault("OMP_PROC_BIND", "close")
     os.environ.setdefault("OMP_PLACES", "cores")
     from oracle import oracle
@@ -204,14 +218,16 @@ def cpu_baseline(model_path, structure, cutoff, cpus, calls, warmup, single_thre
     with open(model_path) as f:
         model = json.load(f)
     types = synthetic.node_types(structure, model["atomic_numbers"])
-    orc = oracle.MaceOracle(model, np.unique(types), "float32")
+    vectorised = host_has_x86_64_v3()
+    timed = oracle.MaceOracle(model, np.unique(types), "float32", timed=vectorised)
+    checker = oracle.MaceOracle(model, np.unique(types), "float32")
     gi = oracle.graph_inputs(structure, cutoff, model["atomic_numbers"])
     volume = structure.volume
     threads = len(cpus)
     previous = os.sched_getaffinity(0)
     os.sched_setaffinity(0, cpus)
     try:
-        def call(n_threads):
+        def call(n_threads, orc=timed):
             e, f = orc.compute(gi["node_types"], gi["num_neigh"], gi["neigh_indices"], gi["neigh_types"],
                                gi["xyz"], gi["r"], n_threads)
             forces, stress = oracle.reduce(gi["num_neigh"], gi["neigh_indices"], f, gi["xyz"], volume)
@@ -222,16 +238,17 @@ def cpu_baseline(model_path, structure, cutoff, cpus, calls, warmup, single_thre
         times = []
         for _ in range(calls):
             t0 = time.perf_counter()
-            result = call(threads)
+            call(threads)
             times.append(time.perf_counter() - t0)
         single = None
         if single_thread:
             t0 = time.perf_counter()
             call(1)
             single = (time.perf_counter() - t0) / len(structure) * 1e6
+        result = call(threads, checker)
     finally:
         os.sched_setaffinity(0, previous)
-    return statistics.median(times) / len(structure) * 1e6, times, single, result
+    return statistics.median(times) / len(structure) * 1e6, times, single, result, vectorised
 
 
 # Bound and peak of each stage's kernels: the node linears run on the FP32
@@ -601,7 +618,7 @@ def main():
         cpus = physical_core_cpus()
         if args.cpu_threads > 0:
             cpus = cpus[: args.cpu_threads]
-        us, times, us1, (ref_energy, ref_forces, ref_stress) = cpu_baseline(
+        us, times, us1, (ref_energy, ref_forces, ref_stress), vectorised = cpu_baseline(
             model_path, structure, cutoff, cpus, args.cpu_calls, args.cpu_warmup,
             single_thread=args.workload == "srtio3")
         cpu = {
@@ -612,7 +629,10 @@ def main():
             "cpu_model": cpu_model_name(),
             "sample": f"full {N}-atom workload, {args.cpu_warmup} untimed + median of {args.cpu_calls} calls of "
                       f"the oracle (reference-algorithm CPU restatement, reference binary unavailable: "
-                      f"compute + reductions, neighbour list reused), one thread per physical core on "
+                      f"compute + reductions, neighbour list reused; "
+                      + ("its x86-64-v3 -ffast-math build, oracle/liboracle_timed.so"
+                         if vectorised else "its checker build, oracle/liboracle.so")
+                      + f"), one thread per physical core on "
                       f"{len(cpus)} cores (OMP_PROC_BIND=close, OMP_PLACES=cores, pinned), "
                       f"{sum(times):.1f} s timed" + ("; one more call on 1 thread" if us1 is not None else ""),
             "single_thread_value": None if us1 is None else round(us1, 3),

@@ -28,18 +28,19 @@ import subprocess
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB = None
+_LIBS = {}
 
 
 def build() -> str:
-    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    subprocess.run(["make", "-s", "-C", _HERE, "all"], check=True)
     return os.path.join(_HERE, "liboracle.so")
 
 
-def _lib():
-    global _LIB
-    if _LIB is None:
-        path = os.path.join(_HERE, "liboracle.so")
+def _lib(timed=False):
+    """The checker build, or with timed=True the vectorised build of the same
+    source that bench.py's CPU baseline times (never the checker)."""
+    if timed not in _LIBS:
+        path = os.path.join(_HERE, "liboracle_timed.so" if timed else "liboracle.so")
         if not os.path.exists(path):
             build()
         lib = ctypes.CDLL(path)
@@ -50,8 +51,8 @@ def _lib():
             getattr(lib, name).argtypes = [ctypes.c_void_p]
         for name in ("oracle_mace_destroy_f32", "oracle_mace_destroy_f64"):
             getattr(lib, name).argtypes = [ctypes.c_void_p]
-        _LIB = lib
-    return _LIB
+        _LIBS[timed] = lib
+    return _LIBS[timed]
 
 
 def _ptr(a, ctype):
@@ -313,7 +314,7 @@ def _monomial_arrays(monomial_lists):
 class MaceOracle:
     """CPU restatement of MACECPU for one model and a set of active types."""
 
-    def __init__(self, model: dict, active_types, precision="float32"):
+    def __init__(self, model: dict, active_types, precision="float32", timed=False):
         mode = model.get("h1_affine_mode")
         if model.get("symmetrix_format_version") != 4 or mode not in ("m0_composite", "pre_linear_up"):
             raise NotImplementedError("the oracle restates format-4 models (m0_composite or pre_linear_up basis)")
@@ -441,7 +442,8 @@ class MaceOracle:
         if a1s:
             spec.a1s_values = arr(np.stack(a1sv))
             spec.a1s_derivs = arr(np.stack(a1sd))
-        lib = _lib()
+        lib = _lib(timed)
+        self._lib = lib
         suffix = "f32" if precision == "float32" else "f64"
         self._destroy = getattr(lib, f"oracle_mace_destroy_{suffix}")
         self._compute = getattr(lib, f"oracle_mace_compute_{suffix}")
@@ -473,7 +475,7 @@ class MaceOracle:
             _ptr(xyz, ctypes.c_double), _ptr(r, ctypes.c_double), _ptr(energies, ctypes.c_double),
             _ptr(forces, ctypes.c_double), ctypes.c_int(num_threads))
         if status != 0:
-            raise RuntimeError(_lib().oracle_mace_last_error().decode())
+            raise RuntimeError(self._lib.oracle_mace_last_error().decode())
         return energies, forces
 
 
