@@ -1007,7 +1007,7 @@ std::size_t Evaluator::held_graph_bytes() const
         &cell_dev_, &xyz_, &r_, &geo_positions_, &geo_edges_, &geo_shifts_, &A0_, &M0_, &H1_, &Phi1_, &A1_,
         &A1adj_, &A0pre_, &direct_, &H1adj_, &msg_, &rpart_, &energies_, &forces_, &atom_forces_, &partials_, &totals_, &scratch_,
         &scale1_, &dot1_, &M0s_, &run_source_, &run_start_, &run_length_, &node_order_, &m0_blocks_, &m0r_blocks_,
-        &readout_blocks_, &tile_xyz_, &tile_r_, &tile_pair_, &tile_forces_,
+        &readout_blocks_, &edge_tiles_, &edge_tiles_l0_, &tile_xyz_, &tile_r_, &tile_pair_, &tile_forces_,
         &pgraph_.first, &pgraph_.sources, &pgraph_.shifts, &pgraph_.fractional_xyz, &pgraph_.fractional_positions};
     std::size_t total = 0;
     for (const DeviceBuffer* b : buffers) total += b->bytes();
@@ -1040,6 +1040,8 @@ std::size_t Evaluator::graph_bytes_estimate(bool tiled, long long runs) const
         per_edge += 3 * sizeof(int) + 7 * sizeof(double);
         if (periodic_) per_edge += 3 * sizeof(double);
         per_node += sizeof(int);
+        // the two edge-tile lists: two ints per tile, at most N + E / 64 tiles
+        extra += 4 * sizeof(int) * (N + E / kEdgeTile);
     } else {
         per_edge += sizeof(int);
         if (!pair_from_types_) per_edge += sizeof(int);
@@ -1246,6 +1248,36 @@ void Evaluator::plan_node_blocks()
         readout_block_offsets_[t + 1] = static_cast<int>(rob.size());
     }
     upload(node_order_, order, stream_, &staged_);
+    // untiled plan with fewer receiver waves than SIMDs: the reverse edge
+    // kernels, which need no per-receiver reduction, run a receiver's 64-edge
+    // tiles as workgroups of their own (135 atoms: 379 -> 344 us per call;
+    // 5,000 atoms, where the receivers fill the machine five times over,
+    // repeating each receiver's set-up per tile costs 1.745 -> 1.865 ms).
+    // SXL_EDGE_TILE_LAUNCH=1 / 0 forces the choice (tests).
+    num_edge_tiles_ = 0;
+    edge_tiles_.release();
+    edge_tiles_l0_.release();
+    const char* tile_launch = std::getenv("SXL_EDGE_TILE_LAUNCH");
+    const long long receiver_waves = static_cast<long long>(N) * ((C_ + 63) / 64);
+    const bool edge_tile_launch = tile_launch && tile_launch[0]
+                                      ? tile_launch[0] == '1'
+                                      : receiver_waves <= 4LL * std::max(compute_units_, 1);
+    if (tile_receivers_ == 0 && N > 0 && edge_tile_launch) {
+        std::vector<int> natural, layer0;
+        auto add = [&](std::vector<int>& list, int i) {
+            for (long long e = host_first_[i]; e < host_first_[i + 1]; e += kEdgeTile) {
+                list.push_back(i);
+                list.push_back(static_cast<int>(e));
+            }
+        };
+        for (int i = 0; i < N; ++i) add(natural, i);
+        for (int i : order) add(layer0, i);
+        num_edge_tiles_ = static_cast<int>(natural.size() / 2);
+        if (num_edge_tiles_ > 0) {
+            upload(edge_tiles_, natural, stream_, &staged_);
+            upload(edge_tiles_l0_, layer0, stream_, &staged_);
+        }
+    }
     upload(m0_blocks_, m0b, stream_, &staged_);
     upload(m0r_blocks_, m0rb, stream_, &staged_);
     upload(readout_blocks_, rob, stream_, &staged_);
@@ -2300,6 +2332,11 @@ void Evaluator::evaluate()
     la.reverse_slices = r1_rev_slices_;
     la.node_offset = 0;
     la.node_count = N;
+    if (num_edge_tiles_ > 0) {
+        la.edge_tiles = edge_tiles_.as<int>();
+        la.edge_tiles_layer0 = edge_tiles_l0_.as<int>();
+        la.num_edge_tiles = num_edge_tiles_;
+    }
     density_args(la, nullptr);
     la.type_order = node_order_.as<int>();
     hipStream_t s = stream_;

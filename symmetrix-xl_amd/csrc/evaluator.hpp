@@ -539,6 +539,11 @@ private:
     void* md_progress_user_ = nullptr;
     // nodes grouped by (tile, active type) and their blocks for the node kernels
     DeviceBuffer node_order_, m0_blocks_, m0r_blocks_, readout_blocks_;
+    // untiled plan: (receiver, first edge) of every 64-edge tile of the
+    // receivers' edge lists, in receiver order and in the layer-0 order
+    // (LayerArgs::edge_tiles); empty when SXL_EDGE_TILE_LAUNCH=0
+    DeviceBuffer edge_tiles_, edge_tiles_l0_;
+    int num_edge_tiles_ = 0;
     // [tiles + 1] each; the M0 reverse has its own block size (m0r_block_nodes_)
     std::vector<int> m0_block_offsets_, m0r_block_offsets_, readout_block_offsets_;
     // untiled plan: each active type's nodes at node_order_[type_start_[a]

@@ -61,6 +61,27 @@ __device__ __forceinline__ int layer0_receiver(const LayerArgs& a)
 // coefficient load costs no vector address arithmetic.
 // ---------------------------------------------------------------------------
 constexpr int kTile = 64;
+static_assert(kTile == kEdgeTile, "edge-tile launches cut receivers at the kernels' tile size");
+
+// The receiver and edge range of this workgroup: with an edge-tile list
+// (LayerArgs::edge_tiles) one tile of at most kTile edges, else all the
+// receiver's edges.  `xcd` spreads consecutive entries over the XCDs in
+// contiguous runs (receiver order); without it entry b is block b (the
+// layer-0 type order).
+__device__ __forceinline__ void block_edges(const LayerArgs& a, const int* tiles, bool xcd, int receiver, int& i,
+                                            int& e0, int& e1)
+{
+    if (tiles) {
+        const int b = xcd ? xcd_contiguous(blockIdx.x, a.num_edge_tiles) : static_cast<int>(blockIdx.x);
+        i = tiles[2 * b];
+        e0 = tiles[2 * b + 1];
+        e1 = min(e0 + kTile, a.graph.first[i + 1]);
+    } else {
+        i = receiver;
+        e0 = a.graph.first[i];
+        e1 = a.graph.first[i + 1];
+    }
+}
 
 // Streams the active slots 0..count-1 of a tile through a ring of D row
 // buffers: the coefficient rows of the next D - 1 edges are in flight while
@@ -707,7 +728,8 @@ r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
     __shared__ float s_dsc[kTile];  // A1 density-scale force coefficient per active slot
     __shared__ int s_count;
 
-    const int i = receiver_of_block(a);
+    int i, e0, e1;
+    block_edges(a, a.edge_tiles, true, a.edge_tiles ? 0 : receiver_of_block(a), i, e0, e1);
     const int k = threadIdx.x;
     const int C = a.C;
     const int wave = threadIdx.x >> 6;
@@ -736,7 +758,6 @@ r1_reverse_kernel(LayerArgs a, const float* __restrict__ r1,
             for (int q = 0; q < S::NLME; ++q) G[q] = in[q * C];
         }
     }
-    const int e0 = g.first[i], e1 = g.first[i + 1];
     for (int base = e0; base < e1; base += kTile) {
         __syncthreads();
         if (threadIdx.x < 64) {
@@ -1232,7 +1253,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) a
     __shared__ float s_dsc[kTile];  // A0 density-scale force coefficient per active slot
     __shared__ int s_count;
 
-    const int i = layer0_receiver(a);
+    int i, t0, t1;  // the receiver and the edges of this workgroup
+    block_edges(a, a.edge_tiles_layer0, false, a.edge_tiles_layer0 ? 0 : layer0_receiver(a), i, t0, t1);
     const int k = threadIdx.x;
     const int C = a.C;
     const int wave = threadIdx.x >> 6;
@@ -1250,7 +1272,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) a
 #pragma unroll
         for (int lm = 0; lm < NLM; ++lm) adj[lm] = 0.0f;
     }
-    const int e0 = g.first[i], e1 = g.first[i + 1];
+    const int e0 = g.first[i], e1 = g.first[i + 1];  // all the receiver's edges (density scale)
     // reverse_A0_scaled: dcoef = (A0_adj . A0) / s for the edge terms, adj /= s
     float dcoef = 0.0f;
     if (a.d0.table) {
@@ -1290,12 +1312,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) a
                     if (kShGrad[d][l * l + m][mp] != 0.0f) v = fmaf(kShGrad[d][l * l + m][mp], adj[l * l + m], v);
                 B[d][l - 1][mp] = v;
             }
-    for (int base = e0; base < e1; base += kTile) {
+    for (int base = t0; base < t1; base += kTile) {
         __syncthreads();
         if (threadIdx.x < 64) {
             const int t = threadIdx.x;
             double rr;
-            const int n = min(kTile, e1 - base);
+            const int n = min(kTile, t1 - base);
             const TileSlot ts = compact_edge<true, false>(g, a.grid, base, n, t, rr, &s_count, kUnfolded);
             const int e = base + t;
             if (ts.active) {
@@ -1847,20 +1869,32 @@ hipError_t launch_a0_forward(const LayerArgs& a, const float* r0f, float* A0, hi
     return hipGetLastError();
 }
 
+// Workgroups of an edge kernel: one per edge tile with a tile list (the
+// whole graph only), else one per receiver.
+static int edge_blocks(const LayerArgs& a, const int* tiles, bool& ok)
+{
+    ok = !tiles || (a.node_offset == 0 && a.local_base == 0 && a.node_count == a.graph.num_nodes);
+    return tiles ? a.num_edge_tiles : a.node_count;
+}
+
 hipError_t launch_a0_reverse(const LayerArgs& a, const float* r0f, const float* A0, const float* A0_adj,
                              double* forces, hipStream_t s)
 {
     if (a.node_count <= 0) return hipSuccess;
     const int threads = node_threads(a.C);
     const bool u = a.h0 != nullptr;
+    bool ok;
+    const int blocks = edge_blocks(a, a.edge_tiles_layer0, ok);
+    if (!ok) return hipErrorInvalidValue;
+    if (blocks <= 0) return hipSuccess;
     switch (a.l_max) {
     case 2:
-        if (u) a0_reverse_kernel<2, true><<<a.node_count, threads, 0, s>>>(a, r0f, A0, A0_adj, forces), note_launch();
-        else a0_reverse_kernel<2, false><<<a.node_count, threads, 0, s>>>(a, r0f, A0, A0_adj, forces), note_launch();
+        if (u) a0_reverse_kernel<2, true><<<blocks, threads, 0, s>>>(a, r0f, A0, A0_adj, forces), note_launch();
+        else a0_reverse_kernel<2, false><<<blocks, threads, 0, s>>>(a, r0f, A0, A0_adj, forces), note_launch();
         break;
     case 3:
-        if (u) a0_reverse_kernel<3, true><<<a.node_count, threads, 0, s>>>(a, r0f, A0, A0_adj, forces), note_launch();
-        else a0_reverse_kernel<3, false><<<a.node_count, threads, 0, s>>>(a, r0f, A0, A0_adj, forces), note_launch();
+        if (u) a0_reverse_kernel<3, true><<<blocks, threads, 0, s>>>(a, r0f, A0, A0_adj, forces), note_launch();
+        else a0_reverse_kernel<3, false><<<blocks, threads, 0, s>>>(a, r0f, A0, A0_adj, forces), note_launch();
         break;
     default: return hipErrorInvalidValue;
     }
@@ -1911,18 +1945,28 @@ hipError_t launch_r1_reverse(const LayerArgs& a, const float* r1, const float* c
             fold_slices_kernel<<<(a.graph.num_edges + 255) / 256, 256, 0, s>>>(a, part, forces), note_launch();
         return hipGetLastError();
     }
-    if (a.l_max == 2 && a.L_max == 1)
-        r1_reverse_kernel<R1Shape<2, 1>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, dPhi1,
-                                                                          forces, msg), note_launch();
-    else if (a.l_max == 3 && a.L_max == 1)
-        r1_reverse_kernel<R1Shape<3, 1>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, dPhi1,
-                                                                          forces, msg), note_launch();
-    else if (a.l_max == 3 && a.L_max == 2)
-        r1_reverse_grouped_kernel<R1Shape<3, 2>, 0, 1><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, dPhi1,
+    // the single-pass kernels take edge tiles; the (3, 2) path-group kernel
+    // runs one workgroup per receiver
+    bool ok;
+    const int blocks = edge_blocks(a, a.edge_tiles, ok);
+    if (!ok) return hipErrorInvalidValue;
+    if (a.l_max == 3 && a.L_max == 2) {
+        LayerArgs ar = a;
+        ar.edge_tiles = nullptr;
+        r1_reverse_grouped_kernel<R1Shape<3, 2>, 0, 1><<<a.node_count, threads, 0, s>>>(ar, r1, cg, H1, dPhi1,
                                                                                        forces, msg), note_launch();
+        return hipGetLastError();
+    }
+    if (blocks <= 0) return hipSuccess;
+    if (a.l_max == 2 && a.L_max == 1)
+        r1_reverse_kernel<R1Shape<2, 1>><<<blocks, threads, 0, s>>>(a, r1, cg, H1, dPhi1, forces, msg),
+            note_launch();
+    else if (a.l_max == 3 && a.L_max == 1)
+        r1_reverse_kernel<R1Shape<3, 1>><<<blocks, threads, 0, s>>>(a, r1, cg, H1, dPhi1, forces, msg),
+            note_launch();
     else if (a.l_max == 3 && a.L_max == 0)
-        r1_reverse_kernel<R1Shape<3, 0>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, dPhi1,
-                                                                          forces, msg), note_launch();
+        r1_reverse_kernel<R1Shape<3, 0>><<<blocks, threads, 0, s>>>(a, r1, cg, H1, dPhi1, forces, msg),
+            note_launch();
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
