@@ -370,6 +370,18 @@ int sxl_set_profiling(sxl_evaluator* evaluator, int enable);
 /* Profile only the stages whose bit is set in mask (bit i = stage i; 0 turns
  * profiling off): two events per profiled stage and evaluation. */
 int sxl_set_profiling_stages(sxl_evaluator* evaluator, uint32_t mask);
+/* HIP graph replay of evaluations from positions (sxl_compute_prepared_positions
+ * and its device form) under the untiled plan: with enable != 0 the kernels of
+ * such an evaluation, from the positions copy to the energy and stress
+ * reduction, are captured into a HIP graph on the first call for a graph
+ * generation, positions array and cell, and later calls replay it with one
+ * launch (the result copies and the wait stay outside the graph); a new
+ * graph, cell, reference geometry or positions array recaptures, profiling
+ * evaluates eagerly.  For small graphs, whose evaluation is bound by the
+ * host's kernel launches.  No reference counterpart (the reference runs
+ * Kokkos kernels eagerly); off by default. */
+int sxl_set_graph_replay(sxl_evaluator* evaluator, int enable);
+int sxl_graph_replay(const sxl_evaluator* evaluator, int* enabled);
 int sxl_num_stages(void);
 const char* sxl_stage_name(int stage);
 int sxl_stage_times(const sxl_evaluator* evaluator, double* ms, int* counts);

@@ -676,6 +676,18 @@ int sxl_set_profiling(sxl_evaluator* ev, int enable)
     return guarded([&] { ev->impl.set_profiling(enable != 0); });
 }
 
+int sxl_set_graph_replay(sxl_evaluator* ev, int enable)
+{
+    if (!ev) return null_handle();
+    return guarded([&] { ev->impl.set_graph_replay(enable != 0); });
+}
+
+int sxl_graph_replay(const sxl_evaluator* ev, int* enabled)
+{
+    if (!ev || !enabled) return null_handle();
+    return guarded([&] { *enabled = ev->impl.graph_replay() ? 1 : 0; });
+}
+
 int sxl_num_stages(void) { return sxl::kNumStages; }
 
 const char* sxl_stage_name(int stage) { return sxl::stage_name(stage); }

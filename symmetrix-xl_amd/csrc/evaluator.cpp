@@ -379,6 +379,7 @@ void Evaluator::mark(int stage, bool end)
 Evaluator::~Evaluator()
 {
     if (stream_) (void)host_fence(stream_);
+    release_replay();
     for (auto& e : events_) (void)hipEventDestroy(e);
     // buffers free themselves; the stream goes last
     A0_.release();
@@ -1298,6 +1299,7 @@ NodeBlocks Evaluator::node_blocks(const DeviceBuffer& blocks, const std::vector<
 void Evaluator::invalidate_graph()
 {
     wait("synchronize");
+    release_replay();
     ++generation_;
     evaluated_generation_ = 0;
     reduced_ = false;
@@ -1833,6 +1835,7 @@ void Evaluator::upload_cell()
 // reuses the graph while it still covers the cutoff.
 void Evaluator::set_cell(const double* cell, const double* inverse_cell)
 {
+    release_replay();  // the captured totals kernel holds the old volume
     std::memcpy(cell_, cell, sizeof(cell_));
     std::memcpy(inverse_cell_, inverse_cell, sizeof(inverse_cell_));
     upload_cell();
@@ -1884,6 +1887,7 @@ void Evaluator::prepare_geometry(std::uint64_t generation, const double* referen
                                  std::size_t num_positions, const double* reference_xyz, std::size_t num_xyz,
                                  const double* cell, const double* inverse_cell, const int* pbc, bool fractional)
 {
+    release_replay();  // the captured geometry kernels hold the old reference geometry
     if (fractional) {
         if (!(pbc[0] && pbc[1] && pbc[2]))
             throw std::invalid_argument("Fractional Execution R1 geometry requires a fully periodic cell.");
@@ -1916,6 +1920,7 @@ void Evaluator::prepare_shift_geometry(std::uint64_t generation, const double* r
                                        std::size_t num_positions, const int* shifts, std::size_t num_shifts,
                                        const double* cell, const double* inverse_cell, const int* pbc)
 {
+    release_replay();  // the captured geometry kernels hold the old reference geometry
     if (generation == 0 || generation != generation_)
         throw std::invalid_argument("Shift geometry requires the current prepared graph token.");
     const std::size_t N = num_nodes_, E = static_cast<std::size_t>(num_edges_);
@@ -2054,26 +2059,13 @@ void Evaluator::graph_arrays(std::uint64_t generation, int* num_neigh, int* rece
     }
 }
 
-void Evaluator::compute_positions(std::uint64_t generation, const double* positions, bool device_positions)
+void Evaluator::enqueue_positions(const double* src, bool device_positions)
 {
-    const CallStart start;
-    require_geometry(generation);
     const int N = num_nodes_;
-    // device positions are read in place by the displacement kernel (nothing
-    // later in the evaluation reads them)
-    const double* src = device_positions ? positions : positions_.as<double>();
-    if (N > 0 && !device_positions) {
-        // through pinned memory: the copy is DMA queued with the kernels (the
-        // previous evaluation's wait has drained the buffer)
-        const std::size_t bytes = static_cast<std::size_t>(N) * 3 * sizeof(double);
-        pinned_positions_.reserve(bytes);
-        std::memcpy(pinned_positions_.as<double>(), positions, bytes);
-        hip_check(hipMemcpyAsync(positions_.as<double>(), pinned_positions_.as<double>(), bytes,
-                                 hipMemcpyHostToDevice, stream_),
+    if (N > 0 && !device_positions)
+        hip_check(hipMemcpyAsync(positions_.as<double>(), pinned_positions_.as<double>(),
+                                 static_cast<std::size_t>(N) * 3 * sizeof(double), hipMemcpyHostToDevice, stream_),
                   "positions");
-    }
-    results_to_host_ = !device_positions;
-    for (int i = 0; i < kNumStages; ++i) stage_used_[i] = false;
     mark(kStageGeometry, false);
     const double* cell = cell_dev_.as<double>();
     const GeometryRef ref = geometry_ref();
@@ -2087,9 +2079,89 @@ void Evaluator::compute_positions(std::uint64_t generation, const double* positi
                                        reinterpret_cast<unsigned long long*>(totals_.as<double>() + 13), stream_),
                   "edge geometry");
     mark(kStageGeometry, true);
+}
+
+bool Evaluator::ReplayKey::operator==(const ReplayKey& o) const
+{
+    if (generation != o.generation || positions != o.positions || device != o.device) return false;
+    for (int q = 0; q < 9; ++q)
+        if (cell[q] != o.cell[q]) return false;
+    return true;
+}
+
+void Evaluator::release_replay()
+{
+    if (replay_exec_) (void)hipGraphExecDestroy(replay_exec_);
+    if (replay_graph_) (void)hipGraphDestroy(replay_graph_);
+    replay_exec_ = nullptr;
+    replay_graph_ = nullptr;
+    replay_key_ = ReplayKey{};
+    replay_launches_ = 0;
+}
+
+void Evaluator::set_graph_replay(bool enable)
+{
+    if (!enable) release_replay();
+    graph_replay_ = enable;
+}
+
+void Evaluator::compute_positions(std::uint64_t generation, const double* positions, bool device_positions)
+{
+    const CallStart start;
+    require_geometry(generation);
+    const int N = num_nodes_;
+    // device positions are read in place by the displacement kernel (nothing
+    // later in the evaluation reads them); host positions are staged through
+    // pinned memory, whose copy is DMA queued with the kernels (the previous
+    // evaluation's wait has drained the buffer)
+    const double* src = device_positions ? positions : positions_.as<double>();
+    if (N > 0 && !device_positions) {
+        const std::size_t bytes = static_cast<std::size_t>(N) * 3 * sizeof(double);
+        pinned_positions_.reserve(bytes);
+        std::memcpy(pinned_positions_.as<double>(), positions, bytes);
+    }
+    results_to_host_ = !device_positions;
+    for (int i = 0; i < kNumStages; ++i) stage_used_[i] = false;
     check_geometry_ = true;
     explicit_geometry_ = false;
-    evaluate();
+    if (graph_replay_ && tile_receivers_ == 0 && !profiling_ && N > 0) {
+        const auto t0 = std::chrono::steady_clock::now();
+        ReplayKey key;
+        key.generation = generation_;
+        key.positions = device_positions ? positions : pinned_positions_.as<double>();
+        key.device = device_positions;
+        std::copy(cell_, cell_ + 9, key.cell);
+        if (!replay_exec_ || !(key == replay_key_)) {
+            release_replay();
+            const std::uint64_t before = thread_counters().launches;
+            hip_check(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "graph capture");
+            hipGraph_t graph = nullptr;
+            try {
+                enqueue_positions(src, device_positions);
+                enqueue_evaluation();
+                enqueue_totals();
+            } catch (...) {
+                (void)hipStreamEndCapture(stream_, &graph);
+                if (graph) (void)hipGraphDestroy(graph);
+                (void)hipGetLastError();
+                throw;
+            }
+            hip_check(hipStreamEndCapture(stream_, &graph), "graph capture");
+            replay_graph_ = graph;
+            hip_check(hipGraphInstantiate(&replay_exec_, replay_graph_, nullptr, nullptr, 0), "graph instantiate");
+            replay_key_ = key;
+            // the captured launches ran no kernel: counted at each replay
+            replay_launches_ = static_cast<long long>(thread_counters().launches - before);
+            thread_counters().launches = before;
+        }
+        hip_check(hipGraphLaunch(replay_exec_, stream_), "graph launch");
+        thread_counters().launches += static_cast<std::uint64_t>(replay_launches_);
+        complete_evaluation();
+        after_evaluation(t0);
+    } else {
+        enqueue_positions(src, device_positions);
+        evaluate();
+    }
     account_evaluation(start);
 }
 
@@ -2308,6 +2380,37 @@ void Evaluator::evaluate()
         return;
     }
     const auto t0 = std::chrono::steady_clock::now();
+    enqueue_evaluation();
+    // the evaluation (and any copy from caller-owned host arrays) has completed
+    // when this returns
+    finish_evaluation();
+    after_evaluation(t0);
+}
+
+// Per-stage times, the evaluated generation and the call's statistics once
+// an untiled evaluation has completed.
+void Evaluator::after_evaluation(std::chrono::steady_clock::time_point t0)
+{
+    if (profiling_)
+        for (int i = 0; i < kNumStages; ++i) {
+            if (!stage_used_[i]) continue;
+            float ms = 0.0f;
+            hip_check(hipEventElapsedTime(&ms, events_[2 * i], events_[2 * i + 1]), "event time");
+            stage_ms_[i] += ms;
+            stage_count_[i] += 1;
+        }
+    evaluated_generation_ = generation_;
+    reduced_ = fused_volume_ > 0.0;
+    reduced_volume_ = fused_volume_;
+    stats_.evaluations += 1;
+    stats_.last_evaluation_ms =
+        std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+}
+
+// The untiled evaluation's kernels, from the layer-0 edge pass to the atom
+// forces, on the evaluator's stream (no host wait).
+void Evaluator::enqueue_evaluation()
+{
     const int N = num_nodes_;
     const int E = static_cast<int>(num_edges_);
     LayerArgs la;
@@ -2456,23 +2559,6 @@ void Evaluator::evaluate()
                                  atom_forces_.as<double>(), s),
               "atom forces");
     mark(kStageAtomForces, true);
-    // the evaluation (and any copy from caller-owned host arrays) has completed
-    // when this returns
-    finish_evaluation();
-    if (profiling_)
-        for (int i = 0; i < kNumStages; ++i) {
-            if (!stage_used_[i]) continue;
-            float ms = 0.0f;
-            hip_check(hipEventElapsedTime(&ms, events_[2 * i], events_[2 * i + 1]), "event time");
-            stage_ms_[i] += ms;
-            stage_count_[i] += 1;
-        }
-    evaluated_generation_ = generation_;
-    reduced_ = fused_volume_ > 0.0;
-    reduced_volume_ = fused_volume_;
-    stats_.evaluations += 1;
-    stats_.last_evaluation_ms =
-        std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
 }
 
 // Tiled evaluation (reference compute_dual_layer_tiled,
@@ -2777,37 +2863,61 @@ int Evaluator::md_nve(int num_atoms, const int* node_types, const double* masses
 // edge geometry held an edge of zero or non-finite length (reference
 // validate_prepared_factorized_positions_geometry,
 // mace_kokkos_factorized_lifecycle.cpp:3078-3085).
+// Volume of the current cell (0 for a non-finite determinant).
+double Evaluator::cell_volume() const
+{
+    const double* c = cell_;
+    const double v = std::abs(c[0] * (c[4] * c[8] - c[5] * c[7]) - c[1] * (c[3] * c[8] - c[5] * c[6]) +
+                              c[2] * (c[3] * c[7] - c[4] * c[6]));
+    return std::isfinite(v) ? v : 0.0;
+}
+
+// The totals kernels of an evaluation: the energy over the nodes and, for
+// an untiled evaluation from positions in a cell of positive volume, the
+// stress for that cell in the same pass (no host wait; part of a captured
+// replay graph).
+void Evaluator::enqueue_totals()
+{
+    const double volume = cell_volume();
+    if (tile_receivers_ > 0) {
+        // the energy over the nodes; the virial was accumulated tile by tile
+        const int np = reduce_totals_partials(num_nodes_, 0);
+        hip_check(launch_reduce_totals(num_nodes_, 0, energies_.as<double>(), nullptr, nullptr, 1.0,
+                                       partials_.as<double>(), np, totals_.as<double>(), stream_),
+                  "totals");
+    } else if (check_geometry_ && volume > 0.0) {
+        const int np = reduce_totals_partials(num_nodes_, static_cast<int>(num_edges_));
+        hip_check(launch_reduce_totals(num_nodes_, static_cast<int>(num_edges_), energies_.as<double>(),
+                                       forces_.as<double>(), xyz_.as<double>(), 1.0 / volume,
+                                       partials_.as<double>(), np, totals_.as<double>(), stream_),
+                  "totals");
+    }
+}
+
 void Evaluator::finish_evaluation()
+{
+    enqueue_totals();
+    complete_evaluation();
+}
+
+// Copies the totals (with the displacement maximum and the invalid-edge
+// count) and, for host callers, the node energies and atom forces back, waits
+// for the stream and checks the evaluation's edges.
+void Evaluator::complete_evaluation()
 {
     host_results_ = false;
     invalid_edges_ = 0;
     fused_volume_ = 0.0;
     last_from_positions_ = check_geometry_;
     const bool tiled = tile_receivers_ > 0;
-    // energy and stress for the current cell in the same pass, copied back
-    // with the displacement maximum and the invalid-edge count
-    const double* c = cell_;
-    const double volume = std::abs(c[0] * (c[4] * c[8] - c[5] * c[7]) - c[1] * (c[3] * c[8] - c[5] * c[6]) +
-                                   c[2] * (c[3] * c[7] - c[4] * c[6]));
-    const bool fuse = check_geometry_ && std::isfinite(volume) && volume > 0.0;
+    const double volume = cell_volume();
+    const bool fuse = check_geometry_ && volume > 0.0;
     if (tiled) {
-        // the energy over the nodes; the virial was accumulated tile by tile
-        const int np = reduce_totals_partials(num_nodes_, 0);
-        hip_check(launch_reduce_totals(num_nodes_, 0, energies_.as<double>(), nullptr, nullptr, 1.0,
-                                       partials_.as<double>(), np, totals_.as<double>(), stream_),
-                  "totals");
         hip_check(hipMemcpyAsync(host_totals_, totals_.as<double>(), 26 * sizeof(double), hipMemcpyDeviceToHost,
                                  stream_),
                   "totals copy");
     } else if (check_geometry_) {
-        if (fuse) {
-            const int np = reduce_totals_partials(num_nodes_, static_cast<int>(num_edges_));
-            hip_check(launch_reduce_totals(num_nodes_, static_cast<int>(num_edges_), energies_.as<double>(),
-                                           forces_.as<double>(), xyz_.as<double>(), 1.0 / volume,
-                                           partials_.as<double>(), np, totals_.as<double>(), stream_),
-                      "totals");
-            fused_volume_ = volume;
-        }
+        if (fuse) fused_volume_ = volume;
         hip_check(hipMemcpyAsync(host_totals_, totals_.as<double>(), 14 * sizeof(double), hipMemcpyDeviceToHost,
                                  stream_),
                   "totals copy");

@@ -348,6 +348,11 @@ public:
     std::string workspace_json() const;
 
     // Per-stage device time (ms) accumulated over profiled evaluations.
+    // Replay untiled evaluations from positions as one HIP graph launch
+    // (captured on the first call for a graph generation, positions array
+    // and cell; recaptured when one of them changes).  Off by default.
+    void set_graph_replay(bool enable);
+    bool graph_replay() const { return graph_replay_; }
     void set_profiling(bool enable);
     // profile only the stages whose bit is set in mask (bit i = stage i)
     void set_profiling_stages(unsigned mask);
@@ -465,6 +470,30 @@ private:
     unsigned long long invalid_edges_ = 0;
     void upload_cell();
     void finish_evaluation();
+    void enqueue_evaluation();
+    void enqueue_totals();
+    void complete_evaluation();
+    void after_evaluation(std::chrono::steady_clock::time_point t0);
+    double cell_volume() const;
+    // the geometry kernels of an evaluation from positions (src: device
+    // positions, or positions_ after the staged host copy)
+    void enqueue_positions(const double* src, bool device_positions);
+    // HIP graph replay of untiled evaluations from positions: the kernels
+    // from the positions copy to the totals are captured once per (graph
+    // generation, positions array, cell) and replayed with one launch
+    bool graph_replay_ = false;
+    hipGraph_t replay_graph_ = nullptr;
+    hipGraphExec_t replay_exec_ = nullptr;
+    struct ReplayKey {
+        std::uint64_t generation = 0;
+        const double* positions = nullptr;
+        bool device = false;
+        double cell[9] = {};
+        bool operator==(const ReplayKey& o) const;
+    };
+    ReplayKey replay_key_;
+    long long replay_launches_ = 0;  // kernels in the captured graph
+    void release_replay();
     DeviceBuffer xyz_, r_;
     // reference geometry for evaluations from positions (see prepare_geometry)
     enum GeometryMode { kGeometryNone = 0, kGeometryBuilt, kGeometryCartesian, kGeometryFractional, kGeometryShifts };

@@ -365,6 +365,11 @@ __global__ void __launch_bounds__(kSortThreads) sort_segments_kernel(int nseg, c
 // with any periodic axis, f = delta cell^-1, f -= floor(f + 1/2) on the
 // periodic axes, disp = f cell; without, disp = delta.  out[0] collects
 // max |disp|^2 (as ordered bits; non-finite: infinite).
+__global__ void clear_pair_kernel(unsigned long long* __restrict__ out)
+{
+    if (threadIdx.x < 2) out[threadIdx.x] = 0ull;
+}
+
 __global__ void atom_displacements_kernel(int n, const double* __restrict__ pos, GeometryRef g,
                                           const double* __restrict__ cell,
                                           const double* __restrict__ inverse_cell, double* __restrict__ disp,
@@ -734,8 +739,11 @@ hipError_t launch_sort_segments(int num_segments, const int* offsets, int* value
 hipError_t launch_atom_displacements(int n, const double* positions, const GeometryRef& ref, const double* cell,
                                      const double* inverse_cell, double* displacements, double* out, hipStream_t s)
 {
-    // out[0]: max |disp|^2, out[1]: invalid-edge count of the edge geometry that follows
-    hipError_t err = hipMemsetAsync(out, 0, 2 * sizeof(double), s);
+    // out[0]: max |disp|^2, out[1]: invalid-edge count of the edge geometry
+    // that follows; cleared by a kernel, not a memset, so the sequence can be
+    // captured into a replayed HIP graph
+    clear_pair_kernel<<<1, 64, 0, s>>>(reinterpret_cast<unsigned long long*>(out)), note_launch();
+    hipError_t err = hipGetLastError();
     if (err != hipSuccess || n <= 0) return err;
     const int blocks = std::min((n + 255) / 256, 1024);
     atom_displacements_kernel<<<blocks, 256, 0, s>>>(n, positions, ref, cell, inverse_cell, displacements,

@@ -101,6 +101,8 @@ SIGNATURES = {
     "sxl_model_heads_json": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_char_p, c_i64, ctypes.POINTER(c_i64)]),
     "sxl_execution_plan_json": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_char_p, c_i64, ctypes.POINTER(c_i64)]),
     "sxl_workspace_json": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_char_p, c_i64, ctypes.POINTER(c_i64)]),
+    "sxl_set_graph_replay": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
+    "sxl_graph_replay": (ctypes.c_int, [ctypes.c_void_p, c_int_p]),
     "sxl_pair_compute": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, c_int_p, c_int_p,
                                         ctypes.POINTER(c_int_p), ctypes.c_int, c_double_p, c_int_p, c_int_p,
                                         ctypes.c_int, c_int_p, c_double_p, c_double_p, c_double_p, c_double_p]),

@@ -505,6 +505,17 @@ class MACEKokkosFloat:
         check(library().sxl_allow_fixed_workspace(self._h, ctypes.byref(v)))
         return bool(v.value)
 
+    def _set_graph_replay(self, enabled=True):
+        """Replay untiled evaluations from positions as one HIP graph launch
+        (captured per graph generation, positions array and cell)."""
+        check(library().sxl_set_graph_replay(self._h, 1 if enabled else 0))
+
+    @property
+    def graph_replay(self):
+        v = ctypes.c_int(0)
+        check(library().sxl_graph_replay(self._h, ctypes.byref(v)))
+        return bool(v.value)
+
     def _set_dual_layer_workspace_receiver_limit_for_testing(self, receivers):
         """Receivers per tile of the tiled plan; invalidates the prepared
         graph.  Non-positive limits raise ValueError like the reference."""
