@@ -1190,7 +1190,7 @@ std::string Evaluator::workspace_json() const
     field("device_free_bytes", static_cast<long long>(free_bytes));
     field("device_total_bytes", static_cast<long long>(total_bytes));
     field("a0_unfolded", a0_unfold_ ? 1 : 0);
-    field("r1_forward_slices", r1_slices_);
+    field("r1_forward_slices", tile_receivers_ > 0 ? r1_slices_ : r1_graph_slices_);
     field("r1_reverse_slices", r1_rev_slices_);
     out += "}";
     return out;
@@ -1263,6 +1263,13 @@ void Evaluator::plan_node_blocks()
     const bool edge_tile_launch = tile_launch && tile_launch[0]
                                       ? tile_launch[0] == '1'
                                       : receiver_waves <= 4LL * std::max(compute_units_, 1);
+    // the same small graphs run the second-interaction forward of the
+    // (3, 1) and (3, 2) shapes in 64-channel slices whose four waves split
+    // each receiver's edges
+    r1_graph_slices_ = r1_slices_;
+    if (tile_receivers_ == 0 && receiver_waves <= 4LL * std::max(compute_units_, 1) && model_.l_max == 3 &&
+        (model_.L_max == 1 || model_.L_max == 2) && (C_ == 128 || C_ == 256))
+        r1_graph_slices_ = C_ / 64;
     if (tile_receivers_ == 0 && N > 0 && edge_tile_launch) {
         std::vector<int> natural, layer0;
         auto add = [&](std::vector<int>& list, int i) {
@@ -2431,7 +2438,7 @@ void Evaluator::enqueue_evaluation()
     la.C = C_;
     la.l_max = model_.l_max;
     la.L_max = model_.L_max;
-    la.channel_slices = r1_slices_;
+    la.channel_slices = r1_graph_slices_;
     la.reverse_slices = r1_rev_slices_;
     la.node_offset = 0;
     la.node_count = N;

@@ -452,6 +452,7 @@ private:
     // indexes edges per tile and has no such limit
     long long edge_index_limit_ = 2147483647LL;
     int r1_slices_ = 1;            // channel slices of the second-interaction forward
+    int r1_graph_slices_ = 1;      // and for the prepared graph (small untiled graphs slice more)
     int r1_rev_slices_ = 1;        // and of its reverse
     // host copies of uploads in flight, released at the next wait()
     std::vector<std::vector<unsigned char>> staged_;
