@@ -89,6 +89,7 @@ CompiledPoly compiled_poly(int lin, int lout, int corr)
     case 323: return compiled_from<PolyShape<3, 2, 3>>();
     case 202: return compiled_from<PolyShape<2, 0, 2>>();
     case 303: return compiled_from<PolyShape<3, 0, 3>>();
+    case 222: return compiled_from<PolyShape<2, 2, 2>>();
     default: return {};
     }
 }
@@ -184,6 +185,24 @@ struct ShapeInfo {
     int nlme;
     std::vector<int> num_e, lme_off;
 };
+
+// Calls f with the compiled R1 shape of (l_max, L_max), or throws.
+template <class F>
+void with_r1_shape(int l_max, int L_max, F&& f)
+{
+    switch (l_max * 10 + L_max) {
+    case 21: f(R1Shape<2, 1>{}); return;
+    case 31: f(R1Shape<3, 1>{}); return;
+    case 32: f(R1Shape<3, 2>{}); return;
+    case 30: f(R1Shape<3, 0>{}); return;
+    case 20: f(R1Shape<2, 0>{}); return;
+    case 22: f(R1Shape<2, 2>{}); return;
+    default:
+        throw std::invalid_argument("no compiled kernels for (l_max, L_max) = (" + std::to_string(l_max) + ", " +
+                                    std::to_string(L_max) +
+                                    "); compiled shapes: (2,0), (2,1), (2,2), (3,0), (3,1), (3,2)");
+    }
+}
 
 template <class S>
 ShapeInfo shape_info()
@@ -311,18 +330,7 @@ Evaluator::Evaluator(const std::string& model_path, const std::string& head)
     nlm_ = model_.num_lm;
     nLM_ = model_.num_LM;
     ShapeInfo info;
-    if (model_.l_max == 2 && model_.L_max == 1)
-        info = shape_info<R1Shape<2, 1>>();
-    else if (model_.l_max == 3 && model_.L_max == 1)
-        info = shape_info<R1Shape<3, 1>>();
-    else if (model_.l_max == 3 && model_.L_max == 2)
-        info = shape_info<R1Shape<3, 2>>();
-    else if (model_.l_max == 3 && model_.L_max == 0)
-        info = shape_info<R1Shape<3, 0>>();
-    else
-        throw std::invalid_argument("no compiled kernels for (l_max, L_max) = (" +
-                                    std::to_string(model_.l_max) + ", " + std::to_string(model_.L_max) +
-                                    "); compiled shapes: (2,1), (3,1), (3,2), (3,0)");
+    with_r1_shape(model_.l_max, model_.L_max, [&](auto shape) { info = shape_info<decltype(shape)>(); });
     nlme_ = info.nlme;
     num_e_ = info.num_e;
     lme_off_ = info.lme_off;
@@ -419,14 +427,7 @@ void Evaluator::upload_static_tables()
     upload(w1_, to_float(m.readout_w1.data(), m.readout_w1.size()), stream_);
     upload(w2_, to_float(m.readout_w2.data(), m.readout_w2.size()), stream_);
     std::vector<float> cg;
-    if (m.l_max == 2 && m.L_max == 1)
-        cg = shape_cg<R1Shape<2, 1>>(m);
-    else if (m.l_max == 3 && m.L_max == 1)
-        cg = shape_cg<R1Shape<3, 1>>(m);
-    else if (m.l_max == 3 && m.L_max == 0)
-        cg = shape_cg<R1Shape<3, 0>>(m);
-    else
-        cg = shape_cg<R1Shape<3, 2>>(m);
+    with_r1_shape(m.l_max, m.L_max, [&](auto shape) { cg = shape_cg<decltype(shape)>(m); });
     upload(cg_, cg, stream_);
     p0_layout_ = poly_layout(m.l_max, m.L_max, m.m0_offsets, m.m0_degree, m.m0_index);
     upload(p0_offsets_, p0_layout_.rem_offsets, stream_);

@@ -17,7 +17,7 @@ sys.path.insert(0, os.path.dirname(HERE))
 
 from symmetrix_amd import irreps  # noqa: E402
 
-SHAPES = [(2, 1), (3, 1), (3, 2), (3, 0)]
+SHAPES = [(2, 1), (3, 1), (3, 2), (3, 0), (2, 0), (2, 2)]
 # Shapes whose per-channel reverse state does not fit the register file in
 # one pass run the second-interaction reverse in passes over disjoint path
 # groups by source l2: each pass owns its message rows and edge forces add up

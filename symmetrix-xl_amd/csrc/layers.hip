@@ -1921,6 +1921,10 @@ hipError_t launch_r1_forward(const LayerArgs& a, const float* r1, const float* c
         r1_forward_sliced_kernel<R1Shape<3, 2>><<<blocks, 256, 0, s>>>(a, r1, cg, H1, Phi1), note_launch();
     else if (a.l_max == 3 && a.L_max == 0)
         r1_forward_kernel<R1Shape<3, 0>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, Phi1), note_launch();
+    else if (a.l_max == 2 && a.L_max == 0)
+        r1_forward_kernel<R1Shape<2, 0>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, Phi1), note_launch();
+    else if (a.l_max == 2 && a.L_max == 2)
+        r1_forward_kernel<R1Shape<2, 2>><<<a.node_count, threads, 0, s>>>(a, r1, cg, H1, Phi1), note_launch();
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
@@ -1966,6 +1970,12 @@ hipError_t launch_r1_reverse(const LayerArgs& a, const float* r1, const float* c
             note_launch();
     else if (a.l_max == 3 && a.L_max == 0)
         r1_reverse_kernel<R1Shape<3, 0>><<<blocks, threads, 0, s>>>(a, r1, cg, H1, dPhi1, forces, msg),
+            note_launch();
+    else if (a.l_max == 2 && a.L_max == 0)
+        r1_reverse_kernel<R1Shape<2, 0>><<<blocks, threads, 0, s>>>(a, r1, cg, H1, dPhi1, forces, msg),
+            note_launch();
+    else if (a.l_max == 2 && a.L_max == 2)
+        r1_reverse_kernel<R1Shape<2, 2>><<<blocks, threads, 0, s>>>(a, r1, cg, H1, dPhi1, forces, msg),
             note_launch();
     else
         return hipErrorInvalidValue;

@@ -750,6 +750,10 @@ hipError_t launch_m0_forward(const LayerArgs& a, const PolyArgs& p0, const NodeB
     case 310: return m0_forward_launch<3, 1, 0>(a, p0, nb, A0, M0, s);
     case 320: return m0_forward_launch<3, 2, 0>(a, p0, nb, A0, M0, s);
     case 300: return m0_forward_launch<3, 0, 0>(a, p0, nb, A0, M0, s);
+    case 202: return m0_forward_launch<2, 0, 2>(a, p0, nb, A0, M0, s);
+    case 200: return m0_forward_launch<2, 0, 0>(a, p0, nb, A0, M0, s);
+    case 222: return m0_forward_launch<2, 2, 2>(a, p0, nb, A0, M0, s);
+    case 220: return m0_forward_launch<2, 2, 0>(a, p0, nb, A0, M0, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -768,6 +772,10 @@ hipError_t launch_m0_reverse(const LayerArgs& a, const PolyArgs& p0, const NodeB
     case 310: return m0_reverse_launch<3, 1, 0>(a, p0, nb, A0, M0_adj, A0_adj, s);
     case 320: return m0_reverse_launch<3, 2, 0>(a, p0, nb, A0, M0_adj, A0_adj, s);
     case 300: return m0_reverse_launch<3, 0, 0>(a, p0, nb, A0, M0_adj, A0_adj, s);
+    case 202: return m0_reverse_launch<2, 0, 2>(a, p0, nb, A0, M0_adj, A0_adj, s);
+    case 200: return m0_reverse_launch<2, 0, 0>(a, p0, nb, A0, M0_adj, A0_adj, s);
+    case 222: return m0_reverse_launch<2, 2, 2>(a, p0, nb, A0, M0_adj, A0_adj, s);
+    case 220: return m0_reverse_launch<2, 2, 0>(a, p0, nb, A0, M0_adj, A0_adj, s);
     default: return hipErrorInvalidValue;
     }
 }
