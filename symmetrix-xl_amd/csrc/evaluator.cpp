@@ -1042,8 +1042,8 @@ std::size_t Evaluator::graph_bytes_estimate(bool tiled, long long runs) const
         per_edge += 3 * sizeof(int) + 7 * sizeof(double);
         if (periodic_) per_edge += 3 * sizeof(double);
         per_node += sizeof(int);
-        // the two edge-tile lists: two ints per tile, at most N + E / 64 tiles
-        extra += 4 * sizeof(int) * (N + E / kEdgeTile);
+        // the two edge-tile lists: two ints per tile, at most N + E / 16 tiles
+        extra += 4 * sizeof(int) * (N + E / kMinEdgeTile);
     } else {
         per_edge += sizeof(int);
         if (!pair_from_types_) per_edge += sizeof(int);
@@ -1250,31 +1250,39 @@ void Evaluator::plan_node_blocks()
         readout_block_offsets_[t + 1] = static_cast<int>(rob.size());
     }
     upload(node_order_, order, stream_, &staged_);
-    // untiled plan with fewer receiver waves than SIMDs: the reverse edge
-    // kernels, which need no per-receiver reduction, run a receiver's 64-edge
-    // tiles as workgroups of their own (135 atoms: 379 -> 344 us per call;
-    // 5,000 atoms, where the receivers fill the machine five times over,
-    // repeating each receiver's set-up per tile costs 1.745 -> 1.865 ms).
-    // SXL_EDGE_TILE_LAUNCH=1 / 0 forces the choice (tests).
+    // untiled plan with at most ten receiver waves per compute unit: the
+    // reverse edge kernels, which need no per-receiver reduction, run each
+    // receiver's edges in 16-edge tiles, each tile a workgroup of its own
+    // (medium shape, per call: 135 atoms 317 -> 266 us, 625 atoms 434 ->
+    // 400 us, 1,080 atoms 536 -> 511 us; 1,715 atoms 705 -> 715 us and 5,000
+    // atoms 1.64 -> 1.77 ms, where the receivers already fill the machine and
+    // each tile repeats its receiver's set-up; 32- and 64-edge tiles gain
+    // less at every size).  SXL_EDGE_TILE_LAUNCH=1 / 0 forces the choice and
+    // SXL_EDGE_TILE=16 / 32 / 64 the tile (tests).
     num_edge_tiles_ = 0;
     edge_tiles_.release();
     edge_tiles_l0_.release();
     const char* tile_launch = std::getenv("SXL_EDGE_TILE_LAUNCH");
     const long long receiver_waves = static_cast<long long>(N) * ((C_ + 63) / 64);
-    const bool edge_tile_launch = tile_launch && tile_launch[0]
-                                      ? tile_launch[0] == '1'
-                                      : receiver_waves <= 4LL * std::max(compute_units_, 1);
-    // the same small graphs run the second-interaction forward of the
-    // (3, 1) and (3, 2) shapes in 64-channel slices whose four waves split
-    // each receiver's edges
+    const long long cus = std::max(compute_units_, 1);
+    const bool edge_tile_launch =
+        tile_launch && tile_launch[0] ? tile_launch[0] == '1' : receiver_waves <= 10LL * cus;
+    // graphs with at most one receiver wave per SIMD run the second-interaction
+    // forward of the (3, 1) and (3, 2) shapes in 64-channel slices whose four
+    // waves split each receiver's edges
     r1_graph_slices_ = r1_slices_;
-    if (tile_receivers_ == 0 && receiver_waves <= 4LL * std::max(compute_units_, 1) && model_.l_max == 3 &&
+    if (tile_receivers_ == 0 && receiver_waves <= 4LL * cus && model_.l_max == 3 &&
         (model_.L_max == 1 || model_.L_max == 2) && (C_ == 128 || C_ == 256))
         r1_graph_slices_ = C_ / 64;
+    edge_tile_ = kMinEdgeTile;
+    if (const char* t = std::getenv("SXL_EDGE_TILE"); t && t[0]) {
+        const int v = std::atoi(t);
+        if (v == 16 || v == 32 || v == 64) edge_tile_ = v;
+    }
     if (tile_receivers_ == 0 && N > 0 && edge_tile_launch) {
         std::vector<int> natural, layer0;
         auto add = [&](std::vector<int>& list, int i) {
-            for (long long e = host_first_[i]; e < host_first_[i + 1]; e += kEdgeTile) {
+            for (long long e = host_first_[i]; e < host_first_[i + 1]; e += edge_tile_) {
                 list.push_back(i);
                 list.push_back(static_cast<int>(e));
             }
@@ -2447,6 +2455,7 @@ void Evaluator::enqueue_evaluation()
         la.edge_tiles = edge_tiles_.as<int>();
         la.edge_tiles_layer0 = edge_tiles_l0_.as<int>();
         la.num_edge_tiles = num_edge_tiles_;
+        la.edge_tile = edge_tile_;
     }
     density_args(la, nullptr);
     la.type_order = node_order_.as<int>();

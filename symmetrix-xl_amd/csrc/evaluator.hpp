@@ -574,6 +574,7 @@ private:
     // (LayerArgs::edge_tiles); empty when SXL_EDGE_TILE_LAUNCH=0
     DeviceBuffer edge_tiles_, edge_tiles_l0_;
     int num_edge_tiles_ = 0;
+    int edge_tile_ = kEdgeTile;  // edges per tile-list entry
     // [tiles + 1] each; the M0 reverse has its own block size (m0r_block_nodes_)
     std::vector<int> m0_block_offsets_, m0r_block_offsets_, readout_block_offsets_;
     // untiled plan: each active type's nodes at node_order_[type_start_[a]

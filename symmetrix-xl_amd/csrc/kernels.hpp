@@ -201,14 +201,15 @@ struct LayerArgs {
     // Edge-tile launches of the unsliced R1 reverse and the A0 reverse (their
     // per-receiver state is read-only and their outputs are per edge): one
     // workgroup per (receiver, first edge) entry, the receiver's edges from
-    // there for at most 64 (kEdgeTile) edges, entries in receiver order
-    // (edge_tiles) or in the layer-0 receiver order (edge_tiles_layer0).
-    // Null: one workgroup per receiver over all its edges.  The tiles start
-    // where a receiver's own 64-edge tiles do, so the results are the same
-    // bit for bit.
+    // there for at most edge_tile edges (16, 32 or kEdgeTile = 64), entries
+    // in receiver order (edge_tiles) or in the layer-0 receiver order
+    // (edge_tiles_layer0).  Null: one workgroup per receiver over all its
+    // edges.  Each edge's force and message are reduced over the channels
+    // alone, whichever tile holds it, so the results are the same bit for bit.
     const int* edge_tiles = nullptr;         // [num_edge_tiles][2]
     const int* edge_tiles_layer0 = nullptr;  // [num_edge_tiles][2]
     int num_edge_tiles = 0;
+    int edge_tile = 64;
     // Layer 0 with the unfolded table: rows per unordered pair table (no H0,
     // no A0_W); each edge's radial values are scaled by
     // h0[source's active type][k] and A0_W is applied to the node sums by
@@ -257,7 +258,8 @@ struct ReadoutArgs {
 };
 hipError_t launch_readout(const ReadoutArgs& a, hipStream_t s);
 
-constexpr int kEdgeTile = 64;  // edges per tile of the edge kernels
+constexpr int kEdgeTile = 64;     // edges per tile of the edge kernels
+constexpr int kMinEdgeTile = 16;  // smallest edge tile of a tile-list launch
 
 // Layer 1 reverse: directed forces (stored) and per-edge H1-adjoint messages.
 // With reverse_slices > 1 (the (3, 2) shape, C = 64 x slices) each slice's

@@ -64,8 +64,8 @@ constexpr int kTile = 64;
 static_assert(kTile == kEdgeTile, "edge-tile launches cut receivers at the kernels' tile size");
 
 // The receiver and edge range of this workgroup: with an edge-tile list
-// (LayerArgs::edge_tiles) one tile of at most kTile edges, else all the
-// receiver's edges.  `xcd` spreads consecutive entries over the XCDs in
+// (LayerArgs::edge_tiles) one tile of at most edge_tile (<= kTile) edges,
+// else all the receiver's edges.  `xcd` spreads consecutive entries over the XCDs in
 // contiguous runs (receiver order); without it entry b is block b (the
 // layer-0 type order).
 __device__ __forceinline__ void block_edges(const LayerArgs& a, const int* tiles, bool xcd, int receiver, int& i,
@@ -75,7 +75,7 @@ __device__ __forceinline__ void block_edges(const LayerArgs& a, const int* tiles
         const int b = xcd ? xcd_contiguous(blockIdx.x, a.num_edge_tiles) : static_cast<int>(blockIdx.x);
         i = tiles[2 * b];
         e0 = tiles[2 * b + 1];
-        e1 = min(e0 + kTile, a.graph.first[i + 1]);
+        e1 = min(e0 + a.edge_tile, a.graph.first[i + 1]);
     } else {
         i = receiver;
         e0 = a.graph.first[i];
@@ -1873,7 +1873,8 @@ hipError_t launch_a0_forward(const LayerArgs& a, const float* r0f, float* A0, hi
 // whole graph only), else one per receiver.
 static int edge_blocks(const LayerArgs& a, const int* tiles, bool& ok)
 {
-    ok = !tiles || (a.node_offset == 0 && a.local_base == 0 && a.node_count == a.graph.num_nodes);
+    ok = !tiles || (a.node_offset == 0 && a.local_base == 0 && a.node_count == a.graph.num_nodes &&
+                    a.edge_tile > 0 && a.edge_tile <= kTile);
     return tiles ? a.num_edge_tiles : a.node_count;
 }
 

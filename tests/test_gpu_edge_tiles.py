@@ -1,13 +1,14 @@
 """Edge-tile launches of the reverse edge kernels (the R1 reverse of the
-single-pass shapes and the A0 reverse): one workgroup per 64-edge tile of a
-receiver instead of one per receiver, chosen when the receivers' waves do
-not fill the SIMDs once (SXL_EDGE_TILE_LAUNCH=1 / 0 forces it).  The tiles
-start where a receiver's own tiles do and neither kernel reduces over a
-receiver's edges, so node energies, directed forces, atom forces and stress
+single-pass shapes and the A0 reverse): one workgroup per 16-, 32- or 64-edge
+tile of a receiver instead of one per receiver, chosen for graphs of at most
+ten receiver waves per compute unit (SXL_EDGE_TILE_LAUNCH=1 / 0 forces it,
+SXL_EDGE_TILE the tile).  Neither kernel reduces over a receiver's edges:
+each edge's force and message are sums over the channels alone, whichever
+tile holds it, so node energies, directed forces, atom forces and stress
 equal the one-workgroup-per-receiver launches bit for bit: on the medium
 shape, with every model option (A0/A1 density terms, ZBL, Agnesi,
 pre_linear_up, residual), on the unfolded layer-0 path, on the scalar shape,
-and with receivers of 0, 1, 64 and 65 edges."""
+and with receivers of 0, 1, 15, 16, 17, 63, 64, 65 and 129 edges."""
 
 import dataclasses
 import json
@@ -49,8 +50,9 @@ def _assert_identical(a, b):
         assert np.array_equal(x, y)
 
 
+@pytest.mark.parametrize("tile", [16, 64])
 @pytest.mark.parametrize("case", ["medium3", "all_options", "unfolded", "scalar"])
-def test_edge_tile_launch_equals_receiver_launch(tmp_path, monkeypatch, case):
+def test_edge_tile_launch_equals_receiver_launch(tmp_path, monkeypatch, case, tile):
     from symmetrix_amd import synthetic
 
     if case == "all_options":
@@ -61,6 +63,7 @@ def test_edge_tile_launch_equals_receiver_launch(tmp_path, monkeypatch, case):
     if case == "unfolded":
         monkeypatch.setenv("SXL_A0_UNFOLDED", "1")
     monkeypatch.setenv("SXL_EDGE_TILE_LAUNCH", "1")
+    monkeypatch.setenv("SXL_EDGE_TILE", str(tile))
     s = synthetic.srtio3_supercell(3, sigma=0.05, seed=7)
     n = len(s)
     ev, gen = _periodic(path, model, s)
@@ -69,17 +72,20 @@ def test_edge_tile_launch_equals_receiver_launch(tmp_path, monkeypatch, case):
     monkeypatch.setenv("SXL_EDGE_TILE_LAUNCH", "0")
     ev0, gen0 = _periodic(path, model, s)
     whole = _results(ev0, gen0, n, s.volume)
-    print(f"{case}: {n} atoms, {tiles} edges; max |dF| {np.max(np.abs(tiled[2] - whole[2])):.1e}", flush=True)
+    print(f"{case}, {tile}-edge tiles: {n} atoms, {tiles} edges; max |dF| {np.max(np.abs(tiled[2] - whole[2])):.1e}",
+          flush=True)
     _assert_identical(tiled, whole)
 
 
-def test_edge_tiles_at_tile_boundaries(tmp_path, monkeypatch):
-    """A caller graph whose receivers have 0, 1, 63, 64, 65 and 129 edges."""
+@pytest.mark.parametrize("tile", [16, 32, 64])
+def test_edge_tiles_at_tile_boundaries(tmp_path, monkeypatch, tile):
+    """A caller graph whose receivers have 0, 1, 15, 16, 17, 63, 64, 65 and
+    129 edges."""
     from symmetrix_amd import MACEKokkosFloat
 
     path, model = _model(tmp_path, "medium3")
     rng = np.random.default_rng(3)
-    degrees = [0, 1, 63, 64, 65, 129, 5, 0, 64]
+    degrees = [0, 1, 63, 64, 65, 129, 5, 0, 64, 15, 16, 17, 32, 33]
     n = 140
     num_neigh = np.zeros(n, dtype=np.int32)
     num_neigh[:len(degrees)] = degrees
@@ -91,6 +97,7 @@ def test_edge_tiles_at_tile_boundaries(tmp_path, monkeypatch):
     r = np.linalg.norm(xyz, axis=1)
 
     monkeypatch.setenv("SXL_EDGE_TILE_LAUNCH", "1")
+    monkeypatch.setenv("SXL_EDGE_TILE", str(tile))
 
     def run():
         ev = MACEKokkosFloat(path)
@@ -101,5 +108,5 @@ def test_edge_tiles_at_tile_boundaries(tmp_path, monkeypatch):
     tiled = run()
     monkeypatch.setenv("SXL_EDGE_TILE_LAUNCH", "0")
     whole = run()
-    print(f"caller graph: {n} receivers, {len(sources)} edges", flush=True)
+    print(f"caller graph, {tile}-edge tiles: {n} receivers, {len(sources)} edges", flush=True)
     _assert_identical(tiled, whole)
