@@ -416,7 +416,9 @@ int sxl_execution_plan_json(const sxl_evaluator* evaluator, char* buffer, int64_
  * graph_bytes, geometry_bytes, node_work_bytes, edge_work_bytes, phi1_bytes,
  * message_bytes, readout_bytes, feature_bytes, reduction_bytes, table_bytes,
  * device_free_bytes, device_total_bytes, a0_unfolded, r1_forward_slices,
- * r1_reverse_slices.  The source of the reference's workspace and policy
+ * r1_reverse_slices, a0_forward_slices, edge_tile (edges per tile of the
+ * reverse edge kernels' tile launches, 0 without).  The source of the
+ * reference's workspace and policy
  * properties (phi1_workspace_bytes, readout_workspace_bytes,
  * dual_layer_workspace_*, execution_planned_*, low_memory_*;
  * symmetrix/source/cpp/mace_kokkos.cpp:517-630,

@@ -1193,6 +1193,8 @@ std::string Evaluator::workspace_json() const
     field("a0_unfolded", a0_unfold_ ? 1 : 0);
     field("r1_forward_slices", tile_receivers_ > 0 ? r1_slices_ : r1_graph_slices_);
     field("r1_reverse_slices", r1_rev_slices_);
+    field("a0_forward_slices", tile_receivers_ > 0 ? 1 : a0_graph_slices_);
+    field("edge_tile", num_edge_tiles_ > 0 ? edge_tile_ : 0);
     out += "}";
     return out;
 }
@@ -1268,12 +1270,18 @@ void Evaluator::plan_node_blocks()
     const bool edge_tile_launch =
         tile_launch && tile_launch[0] ? tile_launch[0] == '1' : receiver_waves <= 10LL * cus;
     // graphs with at most one receiver wave per SIMD run the second-interaction
-    // forward of the (3, 1) and (3, 2) shapes in 64-channel slices whose four
-    // waves split each receiver's edges
+    // forward of the (3, 1) and (3, 2) shapes and the layer-0 forward in
+    // 64-channel slices whose four waves split each receiver's edges (layer 0,
+    // medium shape: 135 atoms 267 -> 252 us per call; 625 atoms 401 -> 403 us,
+    // 1,080 atoms 512 -> 520 us when forced).  SXL_A0_FORWARD_SLICES=1 / 0
+    // forces the layer-0 choice (tests).
+    const bool small_graph = tile_receivers_ == 0 && receiver_waves <= 4LL * cus && (C_ == 128 || C_ == 256);
     r1_graph_slices_ = r1_slices_;
-    if (tile_receivers_ == 0 && receiver_waves <= 4LL * cus && model_.l_max == 3 &&
-        (model_.L_max == 1 || model_.L_max == 2) && (C_ == 128 || C_ == 256))
-        r1_graph_slices_ = C_ / 64;
+    if (small_graph && model_.l_max == 3 && (model_.L_max == 1 || model_.L_max == 2)) r1_graph_slices_ = C_ / 64;
+    bool a0_sliced = small_graph;
+    if (const char* t = std::getenv("SXL_A0_FORWARD_SLICES"); t && t[0])
+        a0_sliced = t[0] == '1' && tile_receivers_ == 0 && (C_ == 128 || C_ == 256);
+    a0_graph_slices_ = a0_sliced ? C_ / 64 : 1;
     edge_tile_ = kMinEdgeTile;
     if (const char* t = std::getenv("SXL_EDGE_TILE"); t && t[0]) {
         const int v = std::atoi(t);
@@ -2449,6 +2457,7 @@ void Evaluator::enqueue_evaluation()
     la.L_max = model_.L_max;
     la.channel_slices = r1_graph_slices_;
     la.reverse_slices = r1_rev_slices_;
+    la.a0_slices = a0_graph_slices_;
     la.node_offset = 0;
     la.node_count = N;
     if (num_edge_tiles_ > 0) {

@@ -575,6 +575,7 @@ private:
     DeviceBuffer edge_tiles_, edge_tiles_l0_;
     int num_edge_tiles_ = 0;
     int edge_tile_ = kEdgeTile;  // edges per tile-list entry
+    int a0_graph_slices_ = 1;    // layer-0 forward slices of the untiled plan (LayerArgs::a0_slices)
     // [tiles + 1] each; the M0 reverse has its own block size (m0r_block_nodes_)
     std::vector<int> m0_block_offsets_, m0r_block_offsets_, readout_block_offsets_;
     // untiled plan: each active type's nodes at node_order_[type_start_[a]

@@ -194,6 +194,10 @@ struct LayerArgs {
     // of all channels).  Set where the coefficient table outgrows one XCD's
     // L2: each XCD then reads only its slice's columns.
     int channel_slices = 1;
+    // Layer-0 forward: workgroups per receiver, each over a slice of 64
+    // channels with its 4 waves splitting the edges (1: one workgroup of all
+    // channels); set for graphs whose receivers leave SIMDs idle.
+    int a0_slices = 1;
     // Second-interaction reverse: one-wave workgroups per (receiver,
     // 64-channel slice), block b on XCD b mod 8 running slice
     // b mod reverse_slices (1: one workgroup of all channels).

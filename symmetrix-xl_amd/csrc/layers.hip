@@ -344,6 +344,142 @@ __global__ void __launch_bounds__(256) a0_forward_kernel(LayerArgs a, const floa
     }
 }
 
+// Channel-sliced layer-0 forward for graphs whose receivers leave SIMDs idle
+// (LayerArgs::a0_slices = C / 64 workgroups per receiver): a workgroup runs
+// one 64-channel slice of a receiver; each of its 4 waves takes a contiguous
+// quarter of the receiver's edges and stages and consumes its own tiles of
+// kWaveTile edges (sorted by spline row, one row load per run of equal rows,
+// no workgroup barrier in the edge loop); the waves' partial sums are added
+// at the end in a fixed order, (w0 + w2) + (w1 + w3).
+template <int LMAX, bool kUnfolded>
+__global__ void __launch_bounds__(256) a0_forward_sliced_kernel(LayerArgs a, const float* __restrict__ r0f,
+                                                                 float* __restrict__ A0)
+{
+    constexpr int NLM = (LMAX + 1) * (LMAX + 1);
+    constexpr int NL = LMAX + 1;
+    constexpr int kWT = 16;  // edges per wave tile
+    __shared__ float s_Y[kMaxWaves][kWT][NLM];
+    __shared__ float s_x[kMaxWaves][kWT];
+    __shared__ int s_row[kMaxWaves][kWT];
+    __shared__ int s_h0row[kMaxWaves][kWT];
+    __shared__ int s_gstart[kMaxWaves][kWT + 1];
+    __shared__ int s_count[kMaxWaves], s_groups[kMaxWaves];
+    __shared__ float s_red[2][NLM][64];
+    __shared__ float s_scale;
+
+    int slice;
+    const int r = xcd_slice_receiver(blockIdx.x, a.node_count, a.a0_slices, slice);
+    const int i = a.type_order ? a.type_order[a.node_offset + r] : a.node_offset + r;
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int C = a.C;
+    const int k = slice * 64 + lane;  // < C: C = 64 slices
+    const EdgeGraph& g = a.graph;
+    const int row_bytes = NL * C * 16;
+    if (a.d0.table && wave == 0) {
+        const float sc = density_scale(a.d0, g, a.grid, g.first[i], g.first[i + 1]);
+        if (lane == 0) s_scale = sc;
+    }
+    float acc[NLM];
+#pragma unroll
+    for (int lm = 0; lm < NLM; ++lm) acc[lm] = 0.0f;
+    const int e0 = g.first[i], n = g.first[i + 1] - e0;
+    const int lo = e0 + (n * wave) / kMaxWaves, hi = e0 + (n * (wave + 1)) / kMaxWaves;
+    for (int base = lo; base < hi; base += kWT) {
+        // the wave's previous tile is consumed before its slots are rewritten
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        {
+            double rr;
+            const TileSlot ts = compact_edge<true, true>(g, a.grid, base, min(kWT, hi - base), lane, rr,
+                                                         &s_count[wave], kUnfolded);
+            if (ts.active) {
+                const int e = base + lane;
+                float Y[NLM], dir[3];
+                edge_harmonics<LMAX, false>(g.xyz + 3 * static_cast<size_t>(e - g.edge_base), rr, Y, nullptr,
+                                            nullptr, nullptr, dir);
+                s_x[wave][ts.slot] = ts.x;
+                s_row[wave][ts.slot] = ts.row;
+                if constexpr (kUnfolded)
+                    s_h0row[wave][ts.slot] = (g.edge_pair[e - g.edge_base] & 0xffff) % g.num_active * C;
+#pragma unroll
+                for (int lm = 0; lm < NLM; ++lm) s_Y[wave][ts.slot][lm] = Y[lm];
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            // runs of equal rows among the (row-sorted) slots
+            const int count = uniform(s_count[wave]);
+            const bool start = lane < count && (lane == 0 || s_row[wave][lane] != s_row[wave][lane - 1]);
+            const unsigned long long starts = __ballot(start);
+            const int gi = __builtin_amdgcn_mbcnt_hi(static_cast<unsigned>(starts >> 32),
+                                                     __builtin_amdgcn_mbcnt_lo(static_cast<unsigned>(starts), 0));
+            if (start) s_gstart[wave][gi] = lane;
+            if (lane == 0) {
+                s_groups[wave] = __popcll(starts);
+                s_gstart[wave][__popcll(starts)] = count;
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int groups = uniform(s_groups[wave]);
+        auto fetch = [&](int gi, float4v* c) {
+            const int row = uniform(s_row[wave][uniform(s_gstart[wave][gi])]);
+            const auto rs = buffer_rsrc(r0f + static_cast<size_t>(row) * NL * C * 4, row_bytes);
+#pragma unroll
+            for (int l = 0; l < NL; ++l) c[l] = load4(rs, k * 16, l * C * 16);
+        };
+        auto accumulate = [&](int gi, const float4v* c) {
+            const int j1 = uniform(s_gstart[wave][gi + 1]);
+            for (int j = uniform(s_gstart[wave][gi]); j < j1; ++j) {
+                const float x = uniform(s_x[wave][j]);
+                float R[NL];
+#pragma unroll
+                for (int l = 0; l < NL; ++l) R[l] = cubic(c[l], x);
+                if constexpr (kUnfolded) {
+                    const float h = a.h0[uniform(s_h0row[wave][j]) + k];
+#pragma unroll
+                    for (int l = 0; l < NL; ++l) R[l] *= h;
+                }
+#pragma unroll
+                for (int lm = 0; lm < NLM; ++lm) acc[lm] = fmaf(R[kLmL[lm]], s_Y[wave][j][lm], acc[lm]);
+            }
+        };
+        float4v ring[kDepth][NL];
+        stream_ring<kDepth>(groups, ring, fetch, accumulate);
+    }
+    __syncthreads();
+    if (wave >= 2) {
+#pragma unroll
+        for (int lm = 0; lm < NLM; ++lm) s_red[wave - 2][lm][lane] = acc[lm];
+    }
+    __syncthreads();
+    if (wave < 2) {
+#pragma unroll
+        for (int lm = 0; lm < NLM; ++lm) acc[lm] += s_red[wave][lm][lane];
+    }
+    __syncthreads();
+    if (wave == 1) {
+#pragma unroll
+        for (int lm = 0; lm < NLM; ++lm) s_red[0][lm][lane] = acc[lm];
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int lm = 0; lm < NLM; ++lm) acc[lm] += s_red[0][lm][lane];
+        if (a.d0.table) {
+            const float sc = s_scale;
+#pragma unroll
+            for (int lm = 0; lm < NLM; ++lm) acc[lm] /= sc;
+        }
+        float* out = A0 + static_cast<size_t>(i - a.local_base) * NLM * C + k;
+#pragma unroll
+        for (int lm = 0; lm < NLM; ++lm) out[lm * C] = acc[lm];
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Layer 1 forward: Phi1[i, lme, k] = sum_j sum_t cg_t Y_{lm1_t} R1_{p_t}(r)[k] H1[src, lm2_t, k]
 //
@@ -1855,6 +1991,22 @@ hipError_t launch_a0_forward(const LayerArgs& a, const float* r0f, float* A0, hi
     if (a.node_count <= 0) return hipSuccess;
     const int threads = node_threads(a.C);
     const bool u = a.h0 != nullptr;
+    if (a.a0_slices > 1) {
+        if ((a.a0_slices != 2 && a.a0_slices != 4) || a.C != 64 * a.a0_slices) return hipErrorInvalidValue;
+        const int blocks = a.node_count * a.a0_slices;
+        switch (a.l_max) {
+        case 2:
+            if (u) a0_forward_sliced_kernel<2, true><<<blocks, 256, 0, s>>>(a, r0f, A0), note_launch();
+            else a0_forward_sliced_kernel<2, false><<<blocks, 256, 0, s>>>(a, r0f, A0), note_launch();
+            break;
+        case 3:
+            if (u) a0_forward_sliced_kernel<3, true><<<blocks, 256, 0, s>>>(a, r0f, A0), note_launch();
+            else a0_forward_sliced_kernel<3, false><<<blocks, 256, 0, s>>>(a, r0f, A0), note_launch();
+            break;
+        default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
     switch (a.l_max) {
     case 2:
         if (u) a0_forward_kernel<2, true><<<a.node_count, threads, 0, s>>>(a, r0f, A0), note_launch();
