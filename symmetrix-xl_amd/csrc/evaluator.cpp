@@ -1223,6 +1223,15 @@ void Evaluator::plan_node_blocks()
     };
     m0r_block_nodes_ = narrow(kM0BlockNodes) ? kM0ReverseBlockNodesNarrow : kM0BlockNodes;
     readout_block_nodes_ = narrow(kReadoutBlockNodes) ? kReadoutBlockNodesNarrow : kReadoutBlockNodes;
+    // one node per block where the launch has at most one wave per SIMD:
+    // the blocks' serial chains set the time there (medium shape, per call:
+    // 135 atoms 255 -> 246 us, 320 atoms 297 -> 292 us; M0 forward and
+    // reverse 12 -> 9 us each at 135 atoms, readout 25 -> 23 us; 1,080 atoms
+    // 511 -> 526 us).  SXL_NODE_BLOCK=1 / 0 forces the choice (tests).
+    bool one_node = launch_nodes * block_waves <= 4LL * std::max(compute_units_, 1);
+    if (const char* v = std::getenv("SXL_NODE_BLOCK"); v && v[0]) one_node = v[0] == '1';
+    m0_block_nodes_ = kM0BlockNodes;
+    if (one_node) m0_block_nodes_ = m0r_block_nodes_ = readout_block_nodes_ = 1;
     m0_block_offsets_.assign(tiles + 1, 0);
     m0r_block_offsets_.assign(tiles + 1, 0);
     readout_block_offsets_.assign(tiles + 1, 0);
@@ -1241,7 +1250,8 @@ void Evaluator::plan_node_blocks()
                 type_count_[a] = n;
             }
             order.insert(order.end(), by_type[a].begin(), by_type[a].end());
-            for (int b = 0; b < n; b += kM0BlockNodes) m0b.push_back({start + b, std::min(kM0BlockNodes, n - b), a, 0});
+            for (int b = 0; b < n; b += m0_block_nodes_)
+                m0b.push_back({start + b, std::min(m0_block_nodes_, n - b), a, 0});
             for (int b = 0; b < n; b += m0r_block_nodes_)
                 m0rb.push_back({start + b, std::min(m0r_block_nodes_, n - b), a, 0});
             for (int b = 0; b < n; b += readout_block_nodes_)
@@ -2486,7 +2496,7 @@ void Evaluator::enqueue_evaluation()
         }
         mark(kStageA0Forward, true);
         mark(kStageM0Forward, false);
-        hip_check(launch_m0_forward(la, p0, node_blocks(m0_blocks_, m0_block_offsets_, 0, kM0BlockNodes), A0_.as<float>(),
+        hip_check(launch_m0_forward(la, p0, node_blocks(m0_blocks_, m0_block_offsets_, 0, m0_block_nodes_), A0_.as<float>(),
                                     M0_.as<float>(), s),
                   "M0 forward");
         mark(kStageM0Forward, true);
@@ -2723,7 +2733,7 @@ void Evaluator::evaluate_tiled()
     for (int t = 0; t < num_tiles_; ++t) {
         tile(t, true);
         hip_check(launch_a0_forward(la, r0f_.as<float>(), A0_.as<float>(), s), "A0 forward");
-        hip_check(launch_m0_forward(la, p0, node_blocks(m0_blocks_, m0_block_offsets_, t, kM0BlockNodes), A0_.as<float>(),
+        hip_check(launch_m0_forward(la, p0, node_blocks(m0_blocks_, m0_block_offsets_, t, m0_block_nodes_), A0_.as<float>(),
                                     M0_.as<float>(), s),
                   "M0 forward");
         float* x = M0s + static_cast<std::size_t>(la.node_offset) * C_;

@@ -581,6 +581,7 @@ private:
     // untiled plan: each active type's nodes at node_order_[type_start_[a]
     // .. + type_count_[a])
     std::vector<int> type_start_, type_count_;
+    int m0_block_nodes_ = kM0BlockNodes;
     int m0r_block_nodes_ = kM0BlockNodes;
     int readout_block_nodes_ = kReadoutBlockNodes;
     int compute_units_ = 0;  // of the evaluator's device

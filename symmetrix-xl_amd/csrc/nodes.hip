@@ -688,10 +688,14 @@ hipError_t m0_forward_launch(const LayerArgs& a, const PolyArgs& p, const NodeBl
                              float* M0, hipStream_t s)
 {
     using P = PolyShape<LIN, LOUT, CORR>;
-    if (nb.block_nodes != kM0BlockNodes) return hipErrorInvalidValue;
+    if (nb.block_nodes < 1 || nb.block_nodes > kM0BlockNodes) return hipErrorInvalidValue;
     const int threads = node_threads(a.C);
     const size_t shmem = p.num_rem > 0 ? sizeof(float) * P::NIN * threads : 0;
-    m0_forward_kernel<P, kM0BlockNodes><<<nb.count, threads, shmem, s>>>(a, p, nb, A0, M0), note_launch();
+    // the kernel holds at least as many nodes as the list's largest block
+    if (nb.block_nodes == 1)
+        m0_forward_kernel<P, 1><<<nb.count, threads, shmem, s>>>(a, p, nb, A0, M0), note_launch();
+    else
+        m0_forward_kernel<P, kM0BlockNodes><<<nb.count, threads, shmem, s>>>(a, p, nb, A0, M0), note_launch();
     return hipGetLastError();
 }
 
@@ -702,11 +706,13 @@ hipError_t m0_reverse_launch(const LayerArgs& a, const PolyArgs& p, const NodeBl
     using P = PolyShape<LIN, LOUT, CORR>;
     const int threads = node_threads(a.C);
     const size_t shmem = p.num_rem > 0 ? sizeof(float) * 2 * P::NIN * threads : 0;
-    // the kernel holds as many nodes as the list's largest block
-    if (nb.block_nodes == kM0ReverseBlockNodesNarrow)
+    // the kernel holds at least as many nodes as the list's largest block
+    if (nb.block_nodes == 1)
+        m0_reverse_kernel<P, 1><<<nb.count, threads, shmem, s>>>(a, p, nb, A0, M0_adj, A0_adj), note_launch();
+    else if (nb.block_nodes > 1 && nb.block_nodes <= kM0ReverseBlockNodesNarrow)
         m0_reverse_kernel<P, kM0ReverseBlockNodesNarrow><<<nb.count, threads, shmem, s>>>(a, p, nb, A0, M0_adj,
                                                                                           A0_adj), note_launch();
-    else if (nb.block_nodes == kM0BlockNodes)
+    else if (nb.block_nodes > kM0ReverseBlockNodesNarrow && nb.block_nodes <= kM0BlockNodes)
         m0_reverse_kernel<P, kM0BlockNodes><<<nb.count, threads, shmem, s>>>(a, p, nb, A0, M0_adj, A0_adj),
             note_launch();
     else
@@ -719,18 +725,21 @@ hipError_t readout_launch(const ReadoutArgs& a, hipStream_t s)
 {
     using P = PolyShape<LIN, 0, CORR>;
     const int threads = std::max(node_threads(a.C), 64);
-    const size_t NB = static_cast<size_t>(a.nodes.block_nodes);
+    // the kernel holds at least as many nodes as the list's largest block;
+    // its LDS is laid out for the kernel's capacity
+    const int most = a.nodes.block_nodes;
+    if (most < 1 || most > kReadoutBlockNodes) return hipErrorInvalidValue;
+    const size_t NB = most == 1 ? 1 : most <= kReadoutBlockNodesNarrow ? kReadoutBlockNodesNarrow : kReadoutBlockNodes;
     size_t floats = 3 * NB * threads + 2 * NB * kMaxHidden;
     if (a.p1.num_rem > 0) floats += 2 * static_cast<size_t>(P::NIN) * threads;
-    // the kernel holds as many nodes as the list's largest block
-    if (NB == kReadoutBlockNodesNarrow)
+    if (NB == 1)
+        readout_kernel<P, 1><<<a.nodes.count, threads, sizeof(float) * floats, s>>>(a), note_launch();
+    else if (NB == kReadoutBlockNodesNarrow)
         readout_kernel<P, kReadoutBlockNodesNarrow><<<a.nodes.count, threads, sizeof(float) * floats, s>>>(a),
             note_launch();
-    else if (NB == kReadoutBlockNodes)
+    else
         readout_kernel<P, kReadoutBlockNodes><<<a.nodes.count, threads, sizeof(float) * floats, s>>>(a),
             note_launch();
-    else
-        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 

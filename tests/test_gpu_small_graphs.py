@@ -1,9 +1,10 @@
 """Launch shapes of small graphs, whose receivers would leave most SIMDs idle
 with one workgroup per receiver: the layer-0 forward in 64-channel slices
 whose four waves split each receiver's edges (LayerArgs::a0_slices, chosen
-at up to one receiver wave per SIMD; SXL_A0_FORWARD_SLICES=1 / 0 forces it)
-and the reverse edge kernels in 16-edge tiles (up to ten receiver waves per
-compute unit).  The sliced layer-0 forward sums a receiver's edges in
+at up to one receiver wave per SIMD; SXL_A0_FORWARD_SLICES=1 / 0 forces it),
+the reverse edge kernels in 16-edge tiles (up to ten receiver waves per
+compute unit) and the node kernels in one-node workgroups (up to one wave per
+SIMD).  The sliced layer-0 forward sums a receiver's edges in
 another order than the one-workgroup kernel, so it is checked against the
 CPU oracle (FP32 tolerances) on the medium shape, with every model option
 (A0 density term, ZBL, Agnesi, pre_linear_up, residual), on the unfolded
@@ -95,3 +96,28 @@ def test_sliced_layer0_forward_matches_oracle(oracle_lib, tmp_path, monkeypatch,
     assert de < E_TOL and df < F_TOL and ds < S_TOL
     scale = max(1.0, float(np.max(np.abs(whole["energies"]))))
     assert dn < 1e-5 * scale and dw < 1e-4
+
+
+@pytest.mark.parametrize("case", ["tiny", "medium3", "all_options", "wide"])
+def test_one_node_blocks_equal_wider_blocks(tmp_path, monkeypatch, case):
+    """The node kernels (M0 forward and reverse, readout) of launches with at
+    most one wave per SIMD run one node per workgroup (SXL_NODE_BLOCK=1 / 0
+    forces it); each node's terms are evaluated alone in either form, so the
+    results are the same bit for bit."""
+    from symmetrix_amd import synthetic
+
+    if case == "all_options":
+        path, model = _model(tmp_path, "medium3", zbl=True, density=("A0", "A1"), agnesi=True,
+                             h1_basis="pre_linear_up", residual=True)
+    else:
+        path, model = _model(tmp_path, case)
+    s = synthetic.water_box(num_molecules=45, seed=3) if case == "wide" else \
+        synthetic.srtio3_supercell(3, sigma=0.05, seed=3)
+    monkeypatch.setenv("SXL_NODE_BLOCK", "1")
+    one = _evaluate(path, model, s)
+    monkeypatch.setenv("SXL_NODE_BLOCK", "0")
+    wide = _evaluate(path, model, s)
+    print(f"{case}: {len(s)} atoms; max |dE_i| {np.max(np.abs(one['energies'] - wide['energies'])):.1e}",
+          flush=True)
+    for key in ("energies", "forces", "stress"):
+        assert np.array_equal(one[key], wide[key])
