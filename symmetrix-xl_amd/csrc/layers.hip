@@ -1316,13 +1316,23 @@ r1_reverse_sliced_kernel(LayerArgs a, const float* __restrict__ r1, const float*
     constexpr int MAXT = rev_group_terms<S, G...>();
     static_assert((S::LMAX + 1) * (S::LMAX + 1) <= 16, "harmonics beyond l = 3");
     __shared__ RevTileLds<MAXT, kForcePartsGrouped> L;
-    int slice;
-    const int i = a.node_offset + xcd_slice_receiver(blockIdx.x, a.node_count, a.reverse_slices, slice);
+    // (receiver or edge tile, slice) of this workgroup: slice b mod slices on
+    // XCD b mod 8, receivers (or edge tiles) in contiguous runs per XCD
+    int slice, i, e0, e1;
+    if (a.edge_tiles) {
+        const int t = xcd_slice_receiver(blockIdx.x, a.num_edge_tiles, a.reverse_slices, slice);
+        i = a.edge_tiles[2 * t];
+        e0 = a.edge_tiles[2 * t + 1];
+        e1 = min(e0 + a.edge_tile, a.graph.first[i + 1]);
+    } else {
+        i = a.node_offset + xcd_slice_receiver(blockIdx.x, a.node_count, a.reverse_slices, slice);
+        e0 = a.graph.first[i];
+        e1 = a.graph.first[i + 1];
+    }
     const int slices = a.reverse_slices;
     const int k = slice * 64 + static_cast<int>(threadIdx.x);  // < C: C = 64 slices
     const EdgeGraph& g = a.graph;
     const float dcoef = a.d1.table && slice == 0 ? a.d1.dot[i] / a.d1.scale[i] : 0.0f;
-    const int e0 = g.first[i], e1 = g.first[i + 1];
     for (int base = e0; base < e1; base += kTile) {
         __syncthreads();
         stage_reverse_tile<S>(a, base, e1, dcoef, L, [&](int e, float d, double rr) {
@@ -2094,8 +2104,13 @@ hipError_t launch_r1_reverse(const LayerArgs& a, const float* r1, const float* c
     if (threads > 256) return hipErrorInvalidValue;
     if (a.reverse_slices > 1) {
         if (!part || !r1_reverse_sliceable(a.l_max, a.L_max, a.C, a.reverse_slices)) return hipErrorInvalidValue;
-        r1_reverse_sliced_kernel<R1Shape<3, 2>, 0, 1><<<a.node_count * a.reverse_slices, 64, 0, s>>>(
-            a, r1, cg, H1, dPhi1, part, msg), note_launch();
+        // one-wave workgroups per (receiver or edge tile, slice)
+        bool ok;
+        const int units = edge_blocks(a, a.edge_tiles, ok);
+        if (!ok) return hipErrorInvalidValue;
+        if (units > 0)
+            r1_reverse_sliced_kernel<R1Shape<3, 2>, 0, 1><<<units * a.reverse_slices, 64, 0, s>>>(
+                a, r1, cg, H1, dPhi1, part, msg), note_launch();
         const hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
         if (a.graph.num_edges > 0)

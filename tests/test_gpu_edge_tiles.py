@@ -1,5 +1,6 @@
 """Edge-tile launches of the reverse edge kernels (the R1 reverse of the
-single-pass shapes and the A0 reverse): one workgroup per 16-, 32- or 64-edge
+single-pass shapes, the channel-sliced R1 reverse of the wide shape and the
+A0 reverse): one workgroup per 16-, 32- or 64-edge
 tile of a receiver instead of one per receiver, chosen for graphs of at most
 ten receiver waves per compute unit (SXL_EDGE_TILE_LAUNCH=1 / 0 forces it,
 SXL_EDGE_TILE the tile).  Neither kernel reduces over a receiver's edges:
@@ -8,7 +9,8 @@ tile holds it, so node energies, directed forces, atom forces and stress
 equal the one-workgroup-per-receiver launches bit for bit: on the medium
 shape, with every model option (A0/A1 density terms, ZBL, Agnesi,
 pre_linear_up, residual), on the unfolded layer-0 path, on the scalar shape,
-and with receivers of 0, 1, 15, 16, 17, 63, 64, 65 and 129 edges."""
+on the wide shape (per-slice force parts) and with receivers of 0, 1, 15,
+16, 17, 63, 64, 65 and 129 edges."""
 
 import dataclasses
 import json
@@ -51,20 +53,25 @@ def _assert_identical(a, b):
 
 
 @pytest.mark.parametrize("tile", [16, 64])
-@pytest.mark.parametrize("case", ["medium3", "all_options", "unfolded", "scalar"])
+@pytest.mark.parametrize("case", ["medium3", "all_options", "unfolded", "scalar", "wide"])
 def test_edge_tile_launch_equals_receiver_launch(tmp_path, monkeypatch, case, tile):
     from symmetrix_amd import synthetic
 
     if case == "all_options":
         path, model = _model(tmp_path, "medium3", zbl=True, density=("A0", "A1"), agnesi=True,
                              h1_basis="pre_linear_up", residual=True)
+    elif case == "wide":
+        # A1 density term: the channel-sliced reverse's slice 0 carries the
+        # density-scale force of every edge
+        path, model = _model(tmp_path, "wide", density=("A1",))
     else:
         path, model = _model(tmp_path, "scalar" if case == "scalar" else "medium3")
     if case == "unfolded":
         monkeypatch.setenv("SXL_A0_UNFOLDED", "1")
     monkeypatch.setenv("SXL_EDGE_TILE_LAUNCH", "1")
     monkeypatch.setenv("SXL_EDGE_TILE", str(tile))
-    s = synthetic.srtio3_supercell(3, sigma=0.05, seed=7)
+    s = synthetic.water_box(num_molecules=45, seed=7) if case == "wide" else \
+        synthetic.srtio3_supercell(3, sigma=0.05, seed=7)
     n = len(s)
     ev, gen = _periodic(path, model, s)
     tiles = ev.stats["num_edges"]  # edges > 64 per receiver at this cutoff: several tiles each
