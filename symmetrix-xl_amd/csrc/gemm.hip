@@ -8,12 +8,16 @@
 // All irrep blocks of one stage run in one launch (a group of up to
 // kMaxGemmGroup GEMMs, tiles numbered consecutively across the group).  A
 // 256-thread workgroup computes a 64 x 128 output tile with four waves of
-// v_mfma_f32_32x32x2f32 (each wave 32 x 64: two 32 x 32 blocks).  K is staged
-// through LDS in slices of 16 (64-row tiles) or 32 (32-row tiles), the next
-// slice's global loads in flight while the current one is multiplied.  Both operands are stored K-contiguous (the
-// weight matrix is passed transposed, Bt[n][k]) so one ds_read_b128 feeds four
-// MFMAs: lane half h supplies k = 8c + 4h + q to MFMA q of chunk c, the same
-// k for both operands, which sums every k of the chunk exactly once.
+// v_mfma_f32_32x32x2f32 (each wave 32 x 64: two 32 x 32 blocks), or, in
+// launches too small to fill the chip, a 16 x 128 tile with four waves of
+// v_mfma_f32_16x16x4f32 (each wave 16 x 32).  K is staged through LDS in
+// slices of 16 (64-row tiles) or 32 (16-row tiles), the next slice's global
+// loads in flight while the current one is multiplied.  Both operands are
+// stored K-contiguous (the weight matrix is passed transposed, Bt[n][k]) so
+// one ds_read_b128 feeds four MFMAs: lane group h supplies k = 8c + 4h + q
+// (32 x 32 blocks, two groups) or k = 16c + 4h + q (16 x 16 blocks, four
+// groups) to MFMA q of chunk c, the same k for both operands, which sums
+// every k of the chunk exactly once.
 #include <hip/hip_runtime.h>
 
 #include "kernels.hpp"
@@ -26,21 +30,18 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 constexpr int kBN = 128, kPad = 4;
 constexpr int kKMultiple = 32;  // K must be a multiple of every slice length
 
-// kBM output rows per tile: 64 (four waves as 2 x 2, each 32 x 64: two MFMA
-// blocks) or, for launches too small to fill the chip, 32 (four waves side by
-// side, each 32 x 32: one block), which doubles the workgroups and halves
-// each one's chain of K slices.  The 64-row tiles stage K in slices of 16:
-// 15 KB of LDS and 78 VGPRs, six workgroups per CU where slices of 32 (27 KB,
-// 96 VGPRs) allowed five and slices of 64 three; the 32-row tiles keep
-// slices of 32 at five.
-template <int kBM>
-__global__ void __launch_bounds__(256)
-__attribute__((amdgpu_waves_per_eu(kBM == 64 ? 6 : 5, kBM == 64 ? 6 : 5))) gemm_group_kernel(GemmGroup grp)
+// 64-row tiles: four waves as 2 x 2, each 32 x 64 (two MFMA blocks), K
+// staged in slices of 16: 15 KB of LDS and 78 VGPRs, six workgroups per CU
+// where slices of 32 (27 KB, 96 VGPRs) allowed five and slices of 64 three.
+// (Launches too small to fill the chip take the 16-row kernel below; a
+// 32-row form of this kernel, four waves of one 32 x 32 block each, ran
+// slower than the 16-row one at every size measured.)
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 6))) gemm_group_kernel(GemmGroup grp)
 {
-    constexpr int kWN = kBM == 64 ? 2 : 4;       // waves along N
+    constexpr int kBM = 64;
+    constexpr int kWN = 2;                       // waves along N
     constexpr int kNB = kBN / kWN / 32;          // 32 x 32 MFMA blocks per wave along N
-    constexpr int kBK = kBM == 64 ? 16 : 32;     // K slice
-    static_assert(kBM == 64 || kBM == 32, "64- or 32-row tiles");
+    constexpr int kBK = 16;                      // K slice
     static_assert(kKMultiple % kBK == 0, "slice length divides the K multiple");
     __shared__ float As[kBM][kBK + kPad];
     __shared__ float Bs[kBN][kBK + kPad];
@@ -157,6 +158,122 @@ __attribute__((amdgpu_waves_per_eu(kBM == 64 ? 6 : 5, kBM == 64 ? 6 : 5))) gemm_
     }
 }
 
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// 16-row tiles for launches that leave most SIMDs idle even with 32-row
+// tiles (small graphs), where each wave's chain of MFMAs sets the time: four
+// waves side by side, each 16 x 32 (two blocks of v_mfma_f32_16x16x4f32:
+// half the MFMA chain of a 32-row tile's wave), twice the workgroups, K
+// staged through LDS in slices of 32.  Lane group h = lane >> 4 supplies
+// k = c + 4h + q to MFMA q of chunk c (16 k), the same k for both operands,
+// so one ds_read_b128 per operand feeds four MFMAs and every k of the chunk
+// is summed exactly once.
+__global__ void __launch_bounds__(256) gemm_group16_kernel(GemmGroup grp)
+{
+    constexpr int kBM = 16, kBK = 32, kWN = 4;
+    constexpr int kNB = kBN / kWN / 16;  // 16 x 16 blocks per wave along N
+    __shared__ float As[kBM][kBK + kPad];
+    __shared__ float Bs[kBN][kBK + kPad];
+    const int b = blockIdx.x;
+    int item = 0;
+    while (item + 1 < grp.count && b >= grp.tile_start[item + 1]) ++item;
+    const GemmArgs& g = grp.g[item];
+    const int M = g.nodes * g.rows_per_node;
+    const int K = g.K, N = g.Ncols;
+    const int local = b - grp.tile_start[item];
+    const int tiles_m = (M + kBM - 1) / kBM;
+    const int row0 = (local % tiles_m) * kBM;
+    const int col0 = (local / tiles_m) * kBN;
+    const int t = threadIdx.x;
+    const int lane = t & 63, wn = t >> 6;
+
+    // global -> register staging: 8 threads per row (one float4 each), 32
+    // rows per pass: A (16 rows) by the first 128 threads, Bt in 4 passes
+    constexpr int kThreadsPerRow = kBK / 4, kRowsPerPass = 256 / kThreadsPerRow;
+    constexpr int kBPasses = kBN / kRowsPerPass;
+    const int lr = t / kThreadsPerRow, lk = (t % kThreadsPerRow) * 4;
+    const float* arow = nullptr;
+    if (lr < kBM && row0 + lr < M) {
+        const int r = row0 + lr;
+        const int node = r / g.rows_per_node;
+        const int m = r - node * g.rows_per_node;
+        const long long gn = g.node_ids ? g.node_ids[node] : node;
+        arow = g.a.ptr + gn * g.a.node_stride + m * g.a.row_stride + lk;
+    }
+    const float* brow[kBPasses];
+#pragma unroll
+    for (int j = 0; j < kBPasses; ++j) {
+        const int n = col0 + lr + kRowsPerPass * j;
+        brow[j] = n < N ? g.Bt + static_cast<size_t>(n) * K + lk : nullptr;
+    }
+    float4 ra, rb[kBPasses];
+    auto fetch = [&](int k0) {
+        ra = arow ? *reinterpret_cast<const float4*>(arow + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int j = 0; j < kBPasses; ++j)
+            rb[j] = brow[j] ? *reinterpret_cast<const float4*>(brow[j] + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+    };
+
+    floatx4 acc[kNB];
+#pragma unroll
+    for (int j = 0; j < kNB; ++j)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[j][v] = 0.0f;
+
+    fetch(0);
+    const int kq = 4 * (lane >> 4);
+    for (int k0 = 0; k0 < K; k0 += kBK) {
+        if (lr < kBM) *reinterpret_cast<float4*>(&As[lr][lk]) = ra;
+#pragma unroll
+        for (int j = 0; j < kBPasses; ++j) *reinterpret_cast<float4*>(&Bs[lr + kRowsPerPass * j][lk]) = rb[j];
+        __syncthreads();
+        if (k0 + kBK < K) fetch(k0 + kBK);
+#pragma unroll
+        for (int c = 0; c < kBK; c += 16) {
+            const float4 a4 = *reinterpret_cast<const float4*>(&As[lane & 15][c + kq]);
+#pragma unroll
+            for (int j = 0; j < kNB; ++j) {
+                const float4 b4 = *reinterpret_cast<const float4*>(&Bs[wn * 32 + j * 16 + (lane & 15)][c + kq]);
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.x, b4.x, acc[j], 0, 0, 0);
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.y, b4.y, acc[j], 0, 0, 0);
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.z, b4.z, acc[j], 0, 0, 0);
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.w, b4.w, acc[j], 0, 0, 0);
+            }
+        }
+        __syncthreads();
+    }
+    // accumulator v of block j holds row 4 (lane >> 4) + v, column
+    // j * 16 + (lane & 15): one run of four consecutive rows
+    const int rpn = g.rows_per_node;
+    int row = row0 + 4 * (lane >> 4);
+    int node = row / rpn;
+    int m = row - node * rpn;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        if (row < M) {
+            const long long gn = g.node_ids ? g.node_ids[node] : node;
+            const long long base = gn * g.c.node_stride + m * g.c.row_stride;
+#pragma unroll
+            for (int j = 0; j < kNB; ++j) {
+                const int col = col0 + wn * 32 + j * 16 + (lane & 15);
+                if (col >= N) continue;
+                float value = acc[j][u];
+                if (g.bias.ptr)
+                    value += g.bias.ptr[g.bias.node_types[g.bias.node_base + node] * g.bias.type_stride +
+                                        m * g.bias.row_stride + col];
+                float* dst = g.c.ptr + base + col;
+                if (g.accumulate) value += *dst;
+                *dst = value;
+            }
+        }
+        ++row;
+        if (++m == rpn) {
+            m = 0;
+            ++node;
+        }
+    }
+}
+
 }  // namespace
 
 hipError_t launch_gemm_group(GemmGroup grp, hipStream_t stream)
@@ -186,14 +303,16 @@ hipError_t launch_gemm_group(GemmGroup grp, hipStream_t stream)
         return tiles;
     };
     // 64-row tiles unless they leave most compute units with at most one
-    // workgroup (256 CUs, five or six resident per CU)
+    // workgroup (256 CUs, five or six resident per CU); then 16-row tiles
+    // (medium shape, per call, against 32-row tiles: 135 atoms 247 -> 232 us,
+    // 625 atoms 396 -> 388-392 us, 2,560 and 5,000 atoms unchanged)
     int tiles = number_tiles(64);
     if (tiles == 0) return hipSuccess;
     if (tiles < 2 * 256) {
-        tiles = number_tiles(32);
-        gemm_group_kernel<32><<<tiles, 256, 0, stream>>>(grp), note_launch();
+        tiles = number_tiles(16);
+        gemm_group16_kernel<<<tiles, 256, 0, stream>>>(grp), note_launch();
     } else {
-        gemm_group_kernel<64><<<tiles, 256, 0, stream>>>(grp), note_launch();
+        gemm_group_kernel<<<tiles, 256, 0, stream>>>(grp), note_launch();
     }
     return hipGetLastError();
 }
