@@ -176,14 +176,22 @@ def physical_core_cpus(limit=16):
 
 
 def cpu_model_name():
+    """The host CPU as /proc/cpuinfo names it, with its family / model /
+    stepping numbers (a virtualised host may report only "AMD EPYC"; the
+    numbers still tell the generation) and the logical CPU count."""
+    fields = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if not line.strip():
+                    break  # the first processor's block is enough
+                key, _, value = line.partition(":")
+                fields[key.strip()] = value.strip()
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    name = fields.get("model name", "unknown")
+    ids = ", ".join(f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping") if k in fields)
+    return f"{name} ({ids}; {os.cpu_count()} logical CPUs)" if ids else name
 
 
 def host_has_x86_64_v3():
