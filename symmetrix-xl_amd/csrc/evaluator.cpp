@@ -2819,8 +2819,12 @@ constexpr double kForceToAcceleration = 9.648533212e-3;
 // Velocity-Verlet NVE (the LAMMPS `fix nve` update the reference's capacity
 // runs use with pair_style symmetrix/mace): per step v += dt/2 a, x += dt v,
 // forces at the new positions, v += dt/2 a.  Every array stays on the
-// device; the host reads three scalars per step (max displacement, potential
-// and kinetic energy).
+// device.  A step waits on the host once: the evaluation at the new
+// positions runs on the current graph, the second half kick (into the other
+// velocity buffer) and the kinetic energy are queued behind it, and the
+// displacement the evaluation measured decides afterwards whether the graph
+// still held; if not (a rebuild step) the graph is rebuilt and the
+// evaluation and kick run again from the kept velocities.
 int Evaluator::md_nve(int num_atoms, const int* node_types, const double* masses, double* x, double* v,
                       const double* cell, const double* inverse_cell, double skin, double dt, int steps,
                       double* epot, double* ekin, double* step_seconds)
@@ -2838,6 +2842,7 @@ int Evaluator::md_nve(int num_atoms, const int* node_types, const double* masses
     const std::size_t bytes3 = static_cast<std::size_t>(N) * 3 * sizeof(double);
     md_x_.reserve(bytes3);
     md_v_.reserve(bytes3);
+    md_v2_.reserve(bytes3);
     hip_check(hipMemcpyAsync(md_x_.as<double>(), x, bytes3, hipMemcpyHostToDevice, stream_), "MD positions");
     hip_check(hipMemcpyAsync(md_v_.as<double>(), v, bytes3, hipMemcpyHostToDevice, stream_), "MD velocities");
     upload(md_m_, m, stream_, &staged_);
@@ -2845,44 +2850,55 @@ int Evaluator::md_nve(int num_atoms, const int* node_types, const double* masses
     const int np = md_kinetic_partials(N);
     md_partials_.reserve(static_cast<std::size_t>(np) * sizeof(double));
     double* xd = md_x_.as<double>();
-    double* vd = md_v_.as<double>();
+    double* vd = md_v_.as<double>();      // velocities at the start of the step
+    double* vnext = md_v2_.as<double>();  // after the step's second half kick
     const double cutoff = model_.r_cut + skin;
+    // the kinetic energy of `vel`, queued on the stream: m |v|^2 lands in
+    // totals_[14] and host_totals_[14]
+    auto queue_kinetic = [&](const double* vel) {
+        hip_check(launch_md_kinetic(N, vel, md_m_.as<double>(), md_partials_.as<double>(), np,
+                                    totals_.as<double>() + 14, stream_),
+                  "kinetic energy");
+        hip_check(hipMemcpyAsync(host_totals_ + 14, totals_.as<double>() + 14, sizeof(double), hipMemcpyDeviceToHost,
+                                 stream_),
+                  "copy");
+    };
+    struct EpilogueGuard {
+        std::function<void()>& slot;
+        ~EpilogueGuard() { slot = nullptr; }
+    } guard{epilogue_};
 
     std::uint64_t gen = prepare_periodic_graph(N, node_types, xd, true, cell, inverse_cell, cutoff);
     int rebuilds = 0;
-    auto energies = [&](int step) {
-        if (epot) epot[step] = total_energy(gen);
-        if (ekin) {
-            hip_check(launch_md_kinetic(N, vd, md_m_.as<double>(), md_partials_.as<double>(), np,
-                                        totals_.as<double>() + 14, stream_),
-                      "kinetic energy");
-            double mv2 = 0.0;
-            hip_check(hipMemcpyAsync(&mv2, totals_.as<double>() + 14, sizeof(double), hipMemcpyDeviceToHost, stream_),
-                      "copy");
-            wait("kinetic energy");
-            ekin[step] = 0.5 * mv2 / kForceToAcceleration;
-        }
-    };
+    epilogue_ = [&] { queue_kinetic(vd); };
     compute_positions(gen, xd, true);
-    energies(0);
+    epilogue_ = nullptr;
+    if (epot) epot[0] = total_energy(gen);
+    if (ekin) ekin[0] = 0.5 * host_totals_[14] / kForceToAcceleration;
     const double dtf = 0.5 * dt;
     for (int step = 1; step <= steps; ++step) {
         const auto t0 = std::chrono::steady_clock::now();
         hip_check(launch_md_kick_drift(N, xd, vd, atom_forces_.as<double>(), md_inv_m_.as<double>(), dtf, dt, stream_),
                   "MD drift");
-        if (!(max_displacement(gen, xd, true) <= 0.5 * skin)) {
+        epilogue_ = [&] {
+            hip_check(launch_md_kick(N, vd, vnext, atom_forces_.as<double>(), md_inv_m_.as<double>(), dtf, stream_),
+                      "MD kick");
+            if (ekin) queue_kinetic(vnext);
+        };
+        compute_positions(gen, xd, true);
+        if (!(last_max_displacement() <= 0.5 * skin)) {
+            // the graph no longer covers every pair within the cutoff: rebuild
+            // and evaluate again (vd still holds the half-kicked velocities)
             gen = prepare_periodic_graph(N, node_types, xd, true, cell, inverse_cell, cutoff);
             ++rebuilds;
+            compute_positions(gen, xd, true);
         }
-        compute_positions(gen, xd, true);
-        hip_check(launch_md_kick(N, vd, atom_forces_.as<double>(), md_inv_m_.as<double>(), dtf, stream_), "MD kick");
-        double seconds = 0.0;
-        if (step_seconds || md_progress_) {
-            wait("MD step");
-            seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
-            if (step_seconds) step_seconds[step - 1] = seconds;
-        }
-        energies(step);
+        epilogue_ = nullptr;
+        std::swap(vd, vnext);
+        double seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+        if (step_seconds) step_seconds[step - 1] = seconds;
+        if (epot) epot[step] = total_energy(gen);
+        if (ekin) ekin[step] = 0.5 * host_totals_[14] / kForceToAcceleration;
         if (md_progress_) {
             const double nan = std::numeric_limits<double>::quiet_NaN();
             if (md_progress_(step, epot ? epot[step] : nan, ekin ? ekin[step] : nan, seconds, md_progress_user_) != 0)
@@ -2941,6 +2957,7 @@ void Evaluator::finish_evaluation()
 // for the stream and checks the evaluation's edges.
 void Evaluator::complete_evaluation()
 {
+    if (epilogue_) epilogue_();
     host_results_ = false;
     invalid_edges_ = 0;
     fused_volume_ = 0.0;
