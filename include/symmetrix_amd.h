@@ -274,6 +274,31 @@ int sxl_pair_compute_device(sxl_evaluator* evaluator, int inum, const int* d_ili
                             int nall, const double* d_x, const int* d_type, const int* d_local_of, int ntypes,
                             const int* mace_types, double* d_f, double* energy, double* d_eatom, double* virial);
 
+/* The KOKKOS pair style's prepared execution (the reference's path when the
+ * model runs prepared graphs: pair_symmetrix/pair_symmetrix_mace_kokkos.cpp:
+ * 1043-1160, its rebuild_topology condition and the stable edge set).
+ * Arrays and accumulators as for sxl_pair_compute_device, except that every
+ * listed pair becomes an edge: one at r >= r_cut is scaled to length r_cut
+ * and contributes nothing.  With neighbor_ago = 0 (LAMMPS neighbor->ago: the
+ * list was rebuilt this step), on the first call, when inum or nall changed
+ * or when the evaluator prepared another graph in between, the graph is
+ * rebuilt from the list; otherwise the list must be the previous call's and
+ * only the edge vectors are formed from x before the prepared graph is
+ * evaluated again (no host round trip for the topology).  An entry whose
+ * neighbour count differs from the prepared graph's is an invalid-argument
+ * error.  *rebuilt (may be null) is set to 1 when the graph was rebuilt.
+ * Results match sxl_pair_compute_device's on the same list and positions to
+ * FP32 rounding: the scaled pairs are inactive in every kernel but change
+ * which of a receiver's edges share a kernel tile, so sums run in another
+ * order; models with density-normalised layers also take every graph
+ * neighbour into their density sums, as the reference's prepared execution
+ * does.  Results are run-to-run identical. */
+int sxl_pair_compute_device_prepared(sxl_evaluator* evaluator, int neighbor_ago, int inum, const int* d_ilist,
+                                     const int* d_numneigh, const int* d_neighbors, int64_t neighbor_stride_atom,
+                                     int64_t neighbor_stride_slot, int nall, const double* d_x, const int* d_type,
+                                     const int* d_local_of, int ntypes, const int* mace_types, double* d_f,
+                                     double* energy, double* d_eatom, double* virial, int* rebuilt);
+
 /* Velocity-Verlet NVE molecular dynamics with positions, velocities and
  * forces resident on the device: the update of LAMMPS `fix nve` that the
  * reference's capacity runs apply with pair_style symmetrix/mace

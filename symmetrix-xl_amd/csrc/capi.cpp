@@ -398,6 +398,38 @@ int sxl_pair_compute_device(sxl_evaluator* ev, int inum, const int* d_ilist, con
     });
 }
 
+int sxl_pair_compute_device_prepared(sxl_evaluator* ev, int neighbor_ago, int inum, const int* d_ilist,
+                                     const int* d_numneigh, const int* d_neighbors, int64_t neighbor_stride_atom,
+                                     int64_t neighbor_stride_slot, int nall, const double* d_x, const int* d_type,
+                                     const int* d_local_of, int ntypes, const int* mace_types, double* d_f,
+                                     double* energy, double* d_eatom, double* virial, int* rebuilt)
+{
+    if (!ev || !d_f) return null_handle();
+    return guarded([&] {
+        sxl::PairDeviceInput in;
+        in.inum = inum;
+        in.ilist = d_ilist;
+        in.numneigh = d_numneigh;
+        in.neighbors = d_neighbors;
+        in.stride_atom = neighbor_stride_atom;
+        in.stride_slot = neighbor_stride_slot;
+        in.nall = nall;
+        in.x = d_x;
+        in.type = d_type;
+        in.local_of = d_local_of;
+        in.ntypes = ntypes;
+        in.mace_types = mace_types;
+        sxl::PairOutput out;
+        out.f = d_f;
+        out.energy = energy;
+        out.eatom = d_eatom;
+        out.virial = virial;
+        bool r = false;
+        ev->pair.compute_device_prepared(ev->impl, neighbor_ago, in, out, &r);
+        if (rebuilt) *rebuilt = r ? 1 : 0;
+    });
+}
+
 int sxl_md_nve(sxl_evaluator* ev, int num_atoms, const int* node_types, const double* masses, double* positions,
                double* velocities, const double* cell, const double* inverse_cell, double skin, double dt, int steps,
                double* potential_energy, double* kinetic_energy, double* step_seconds, int* rebuilds)

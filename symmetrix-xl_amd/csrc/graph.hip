@@ -516,10 +516,14 @@ __device__ __forceinline__ int pair_neighbor(const PairList& p, int i, int jj)
            kNeighMaskDevice;
 }
 
-// One wave per list entry ii: the neighbours within r_cut are counted, or
-// (offsets set) written in list order -- neighbour node, its element, the
-// edge vector x_j - x_i and its length -- by ballot and lane prefix count.
-// The length is formed as on the host (no fused operations in this file).
+// One wave per list entry ii: the neighbours within r_cut (stable: all
+// listed neighbours) are counted, or (offsets set) written in list order --
+// neighbour node, its element, the edge vector x_j - x_i and its length -- by
+// ballot and lane prefix count.  The length is formed as on the host (no
+// fused operations in this file).  A stable fill scales an edge at
+// r >= r_cut to length r_cut (reference pair_symmetrix_mace_kokkos.cpp:
+// 1134-1150) and, for a geometry update (neigh_indices null), writes only
+// within the entry's edges from offsets and flags a count that differs.
 __global__ void __launch_bounds__(256) pair_edges_kernel(PairList p, const int* __restrict__ ii_from_i,
                                                          const long long* __restrict__ offsets,
                                                          int* __restrict__ node_types, int* __restrict__ counts,
@@ -533,10 +537,12 @@ __global__ void __launch_bounds__(256) pair_edges_kernel(PairList p, const int* 
     const int i = p.ilist[ii];
     if (i < 0 || i >= p.nall) return;  // flagged by pair_index_kernel
     const bool fill = offsets != nullptr;
+    const bool geometry_only = fill && neigh_indices == nullptr;
     const double xi = p.x[3 * static_cast<size_t>(i)], yi = p.x[3 * static_cast<size_t>(i) + 1],
                  zi = p.x[3 * static_cast<size_t>(i) + 2];
     const int n = p.numneigh[i];
     long long out = fill ? offsets[ii] : 0;
+    const long long room = geometry_only ? offsets[ii + 1] - out : 0;  // the entry's edges at the last rebuild
     int local = 0;
     unsigned bad = 0;
     for (int base = 0; base < n; base += 64) {
@@ -553,7 +559,7 @@ __global__ void __launch_bounds__(256) pair_edges_kernel(PairList p, const int* 
                 dy = p.x[3 * static_cast<size_t>(j) + 1] - yi;
                 dz = p.x[3 * static_cast<size_t>(j) + 2] - zi;
                 r2 = dx * dx + dy * dy + dz * dz;
-                accept = r2 < p.r_cut_squared;
+                accept = p.stable || r2 < p.r_cut_squared;
             }
         }
         if (accept && !fill) {
@@ -566,15 +572,32 @@ __global__ void __launch_bounds__(256) pair_edges_kernel(PairList p, const int* 
         if (fill && accept) {
             const int rank = __builtin_amdgcn_mbcnt_hi(static_cast<unsigned>(mask >> 32),
                                                        __builtin_amdgcn_mbcnt_lo(static_cast<unsigned>(mask), 0));
-            const size_t e = static_cast<size_t>(out + local + rank);
-            neigh_indices[e] = ii_from_i[p.local_of[j]];
-            neigh_types[e] = p.mace_types[p.type[j] - 1];
-            xyz[3 * e] = dx;
-            xyz[3 * e + 1] = dy;
-            xyz[3 * e + 2] = dz;
-            r[e] = sqrt(r2);
+            if (!geometry_only || local + rank < room) {
+                const size_t e = static_cast<size_t>(out + local + rank);
+                if (!geometry_only) {
+                    neigh_indices[e] = ii_from_i[p.local_of[j]];
+                    neigh_types[e] = p.mace_types[p.type[j] - 1];
+                }
+                double len = sqrt(r2);
+                if (p.stable && !(r2 < p.r_cut_squared)) {
+                    const double scale = p.r_cut / len;
+                    dx *= scale;
+                    dy *= scale;
+                    dz *= scale;
+                    len = p.r_cut;
+                }
+                xyz[3 * e] = dx;
+                xyz[3 * e + 1] = dy;
+                xyz[3 * e + 2] = dz;
+                r[e] = len;
+            }
         }
         local += __popcll(mask);
+    }
+    if (geometry_only) {
+        for (int off = 32; off > 0; off >>= 1) bad |= __shfl_xor(bad, off, 64);
+        if (local != room) bad |= 16u;
+        if (lane == 0 && bad) atomicOr(flags, bad);
     }
     if (!fill) {
         for (int off = 32; off > 0; off >>= 1) bad |= __shfl_xor(bad, off, 64);

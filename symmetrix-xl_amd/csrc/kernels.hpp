@@ -333,12 +333,20 @@ struct PairList {
     int ntypes = 0;
     const int* mace_types = nullptr;
     double r_cut_squared = 0.0;
+    // Stable topology (the reference's prepared execution): every listed
+    // neighbour becomes an edge; one at r >= r_cut is scaled to length r_cut
+    // (inactive in every edge kernel).  With neigh_indices null the fill pass
+    // writes only xyz and r (a geometry update of an unchanged list) and flags
+    // 16 when an entry's neighbour count differs from its offsets.
+    int stable = 0;
+    double r_cut = 0.0;
 };
 // ii_from_i [nall] (filled with -1 first): ilist position of each listed atom
 hipError_t launch_pair_index(int inum, const int* ilist, int nall, int* ii_from_i, unsigned* flags, hipStream_t s);
 // count pass (offsets null): node_types and counts of neighbours within r_cut
-// per list entry, flags (bits: 1 ilist, 2 neighbour index, 4 type, 8 local
-// atom outside ilist); fill pass: the edges at offsets, in list order
+// (stable: of every listed neighbour) per list entry, flags (bits: 1 ilist,
+// 2 neighbour index, 4 type, 8 local atom outside ilist); fill pass: the
+// edges at offsets, in list order
 hipError_t launch_pair_edges(const PairList& p, const int* ii_from_i, const long long* offsets, int* node_types,
                              int* counts, int* neigh_indices, int* neigh_types, double* xyz, double* r, unsigned* flags,
                              hipStream_t s);

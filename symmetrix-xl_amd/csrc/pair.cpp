@@ -121,31 +121,22 @@ void PairDriver::compute(Evaluator& ev, const PairInput& in, const PairOutput& o
     totals(ev, g, out);
 }
 
-void PairDriver::compute_device(Evaluator& ev, const PairDeviceInput& in, const PairOutput& out)
+// The list as a PairList over the device arrays (mace_types copied to the
+// device on the evaluator's stream).
+PairList PairDriver::device_list(Evaluator& ev, const PairDeviceInput& in, bool stable)
 {
     if (in.inum < 0 || in.nall < in.inum) throw std::invalid_argument("pair list has invalid atom counts");
-    if (!out.f) throw std::invalid_argument("pair compute requires a force array");
-    if (in.inum == 0) return;
     if (!in.ilist || !in.numneigh || !in.neighbors || !in.x || !in.type || !in.local_of || !in.mace_types)
         throw std::invalid_argument("pair list arrays must not be null");
     if (in.ntypes < 1) throw std::invalid_argument("pair compute requires the pair_coeff type map");
     check_types(ev, in.ntypes, in.mace_types);
-    hipStream_t s = ev.stream();
-    const int n = in.inum;
     std::vector<int> map(in.mace_types, in.mace_types + in.ntypes);
     d_mace_types_.reserve(map.size() * sizeof(int));
-    hip_check(hipMemcpyAsync(d_mace_types_.as<int>(), map.data(), map.size() * sizeof(int), hipMemcpyHostToDevice, s),
+    hip_check(hipMemcpyAsync(d_mace_types_.as<int>(), map.data(), map.size() * sizeof(int), hipMemcpyHostToDevice,
+                             ev.stream()),
               "type map");
-    d_ii_from_i_.reserve(static_cast<std::size_t>(in.nall) * sizeof(int));
-    d_node_types_.reserve(static_cast<std::size_t>(n) * sizeof(int));
-    d_num_neigh_.reserve(static_cast<std::size_t>(n) * sizeof(int));
-    d_offsets_.reserve((static_cast<std::size_t>(n) + 1) * sizeof(long long));
-    d_flags_.reserve(sizeof(unsigned));
-    hip_check(hipMemsetAsync(d_flags_.as<void>(), 0, sizeof(unsigned), s), "memset");
-    hip_check(launch_fill_i32(d_ii_from_i_.as<int>(), in.nall, -1, s), "list index");
-    hip_check(launch_pair_index(n, in.ilist, in.nall, d_ii_from_i_.as<int>(), d_flags_.as<unsigned>(), s), "list index");
     PairList p;
-    p.inum = n;
+    p.inum = in.inum;
     p.ilist = in.ilist;
     p.numneigh = in.numneigh;
     p.neighbors = in.neighbors;
@@ -158,6 +149,26 @@ void PairDriver::compute_device(Evaluator& ev, const PairDeviceInput& in, const 
     p.ntypes = in.ntypes;
     p.mace_types = d_mace_types_.as<int>();
     p.r_cut_squared = ev.model().r_cut * ev.model().r_cut;
+    p.r_cut = ev.model().r_cut;
+    p.stable = stable ? 1 : 0;
+    return p;
+}
+
+// Filters and maps the list on the device and prepares its graph: the
+// per-atom neighbour counts come to the host once.  Leaves the edge vectors
+// in d_xyz_ / d_r_ and returns the graph's generation.
+std::uint64_t PairDriver::prepare_device_graph(Evaluator& ev, const PairList& p)
+{
+    hipStream_t s = ev.stream();
+    const int n = p.inum;
+    d_ii_from_i_.reserve(static_cast<std::size_t>(p.nall) * sizeof(int));
+    d_node_types_.reserve(static_cast<std::size_t>(n) * sizeof(int));
+    d_num_neigh_.reserve(static_cast<std::size_t>(n) * sizeof(int));
+    d_offsets_.reserve((static_cast<std::size_t>(n) + 1) * sizeof(long long));
+    d_flags_.reserve(sizeof(unsigned));
+    hip_check(hipMemsetAsync(d_flags_.as<void>(), 0, sizeof(unsigned), s), "memset");
+    hip_check(launch_fill_i32(d_ii_from_i_.as<int>(), p.nall, -1, s), "list index");
+    hip_check(launch_pair_index(n, p.ilist, p.nall, d_ii_from_i_.as<int>(), d_flags_.as<unsigned>(), s), "list index");
     hip_check(launch_pair_edges(p, d_ii_from_i_.as<int>(), nullptr, d_node_types_.as<int>(), d_num_neigh_.as<int>(),
                                 nullptr, nullptr, nullptr, nullptr, d_flags_.as<unsigned>(), s),
               "list count");
@@ -188,13 +199,72 @@ void PairDriver::compute_device(Evaluator& ev, const PairDeviceInput& in, const 
                                 d_neigh_indices_.as<int>(), d_neigh_types_.as<int>(), d_xyz_.as<double>(),
                                 d_r_.as<double>(), nullptr, s),
               "list edges");
+    // prepare_graph_device waits on the stream, so the host offsets outlive their copy
     const std::uint64_t g = ev.prepare_graph_device(n, d_node_types_.as<int>(), d_num_neigh_.as<int>(),
                                                     d_neigh_indices_.as<int>(), d_neigh_types_.as<int>());
+    return g;
+}
+
+// Evaluates the graph g on the edge vectors in d_xyz_ / d_r_ and adds the
+// results to the pair style's accumulators.
+void PairDriver::evaluate_device(Evaluator& ev, std::uint64_t g, const PairDeviceInput& in, const PairOutput& out)
+{
     ev.compute_xyz(g, d_xyz_.as<double>(), d_r_.as<double>(), true);
-    hip_check(launch_pair_scatter(n, in.ilist, ev.device_atom_forces(), ev.device_node_energies(), out.f, out.eatom, s),
+    hip_check(launch_pair_scatter(in.inum, in.ilist, ev.device_atom_forces(), ev.device_node_energies(), out.f,
+                                  out.eatom, ev.stream()),
               "pair forces");
     totals(ev, g, out);
     ev.synchronize();  // the forces and energies are in place on return
+}
+
+void PairDriver::compute_device(Evaluator& ev, const PairDeviceInput& in, const PairOutput& out)
+{
+    if (in.inum < 0 || in.nall < in.inum) throw std::invalid_argument("pair list has invalid atom counts");
+    if (!out.f) throw std::invalid_argument("pair compute requires a force array");
+    if (in.inum == 0) return;
+    const PairList p = device_list(ev, in, false);
+    const std::uint64_t g = prepare_device_graph(ev, p);
+    prepared_generation_ = 0;  // the stable entry's graph is replaced
+    evaluate_device(ev, g, in, out);
+}
+
+void PairDriver::compute_device_prepared(Evaluator& ev, int neighbor_ago, const PairDeviceInput& in,
+                                         const PairOutput& out, bool* rebuilt)
+{
+    if (rebuilt) *rebuilt = false;
+    if (in.inum < 0 || in.nall < in.inum) throw std::invalid_argument("pair list has invalid atom counts");
+    if (!out.f) throw std::invalid_argument("pair compute requires a force array");
+    if (in.inum == 0) return;
+    const PairList p = device_list(ev, in, true);
+    const bool rebuild = neighbor_ago == 0 || prepared_generation_ == 0 || ev.generation() != prepared_generation_ ||
+                         in.inum != prepared_inum_ || in.nall != prepared_nall_;
+    if (rebuild) {
+        prepared_generation_ = 0;
+        const std::uint64_t g = prepare_device_graph(ev, p);
+        prepared_generation_ = g;
+        prepared_inum_ = in.inum;
+        prepared_nall_ = in.nall;
+        ++graph_rebuilds_;
+        if (rebuilt) *rebuilt = true;
+    } else {
+        // an unchanged list (LAMMPS neighbor->ago > 0): only the edge vectors
+        hipStream_t s = ev.stream();
+        hip_check(hipMemsetAsync(d_flags_.as<void>(), 0, sizeof(unsigned), s), "memset");
+        hip_check(launch_pair_edges(p, nullptr, d_offsets_.as<long long>(), nullptr, nullptr, nullptr, nullptr,
+                                    d_xyz_.as<double>(), d_r_.as<double>(), d_flags_.as<unsigned>(), s),
+                  "list geometry");
+        flags_host_.reserve(sizeof(unsigned));
+        hip_check(hipMemcpyAsync(flags_host_.as<unsigned>(), d_flags_.as<void>(), sizeof(unsigned),
+                                 hipMemcpyDeviceToHost, s),
+                  "copy");
+        ++geometry_updates_;
+    }
+    evaluate_device(ev, prepared_generation_, in, out);
+    if (!rebuild && *flags_host_.as<unsigned>() != 0) {
+        prepared_generation_ = 0;
+        throw std::invalid_argument(
+            "the neighbour list changed without a rebuild (neighbor_ago > 0 requires the list of the last call)");
+    }
 }
 
 }  // namespace sxl

@@ -61,11 +61,28 @@ class PairDriver {
 public:
     void compute(Evaluator& ev, const PairInput& in, const PairOutput& out);
     void compute_device(Evaluator& ev, const PairDeviceInput& in, const PairOutput& out);
+    // The reference Kokkos pair style's prepared execution
+    // (pair_symmetrix_mace_kokkos.cpp:1043-1160): every listed pair is an
+    // edge (those at r >= r_cut scaled to length r_cut, contributing
+    // nothing), and while the list is unchanged (neighbor_ago > 0, same atom
+    // counts, the evaluator still on this graph) only the edge vectors are
+    // updated and the prepared graph is evaluated again.
+    void compute_device_prepared(Evaluator& ev, int neighbor_ago, const PairDeviceInput& in, const PairOutput& out,
+                                 bool* rebuilt);
+    long long graph_rebuilds() const { return graph_rebuilds_; }
+    long long geometry_updates() const { return geometry_updates_; }
 
 private:
     void check_types(const Evaluator& ev, int ntypes, const int* mace_types) const;
     // energy and virial of the evaluated graph into the host accumulators
     void totals(Evaluator& ev, std::uint64_t generation, const PairOutput& out);
+    PairList device_list(Evaluator& ev, const PairDeviceInput& in, bool stable);
+    std::uint64_t prepare_device_graph(Evaluator& ev, const PairList& p);
+    void evaluate_device(Evaluator& ev, std::uint64_t generation, const PairDeviceInput& in, const PairOutput& out);
+    std::uint64_t prepared_generation_ = 0;
+    int prepared_inum_ = 0, prepared_nall_ = 0;
+    long long graph_rebuilds_ = 0, geometry_updates_ = 0;
+    PinnedBuffer flags_host_;
     std::vector<int> ii_from_i_, node_types_, num_neigh_, neigh_indices_, neigh_types_, node_i_;
     std::vector<double> xyz_, r_, node_energies_, node_forces_;
     // device entry

@@ -110,6 +110,11 @@ SIGNATURES = {
                                                ctypes.c_void_p, c_i64, c_i64, ctypes.c_int, ctypes.c_void_p,
                                                ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, c_int_p,
                                                ctypes.c_void_p, c_double_p, ctypes.c_void_p, c_double_p]),
+    "sxl_pair_compute_device_prepared": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                                        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, c_i64,
+                                                        c_i64, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                                        ctypes.c_void_p, ctypes.c_int, c_int_p, ctypes.c_void_p,
+                                                        c_double_p, ctypes.c_void_p, c_double_p, c_int_p]),
     "sxl_prepare_graph_device": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
                                                 ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(c_u64)]),
     "sxl_md_nve": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, c_int_p, c_double_p, c_double_p, c_double_p,

@@ -362,6 +362,28 @@ class MACEKokkosFloat:
         self._evaluated = True
         return {"energy": float(energy.value), "virial": virial}
 
+    def _pair_compute_device_prepared(self, neighbor_ago, inum, ilist_ptr, numneigh_ptr, neighbors_ptr, stride_atom,
+                                      stride_slot, nall, x_ptr, type_ptr, local_of_ptr, mace_types, f_ptr,
+                                      eatom_ptr=0):
+        """The LAMMPS KOKKOS pair style's prepared execution on device arrays:
+        every listed pair an edge (those beyond r_cut scaled to it), the graph
+        rebuilt when neighbor_ago is 0 (or the list's counts changed) and
+        otherwise only the edge vectors updated.  Returns the energy, the
+        virial [6] and whether the graph was rebuilt."""
+        mt = _i32(mace_types, name="mace_types")
+        energy = ctypes.c_double(0.0)
+        virial = np.zeros(6)
+        rebuilt = ctypes.c_int(0)
+        check(library().sxl_pair_compute_device_prepared(
+            self._h, int(neighbor_ago), int(inum), ctypes.c_void_p(int(ilist_ptr)), ctypes.c_void_p(int(numneigh_ptr)),
+            ctypes.c_void_p(int(neighbors_ptr)), c_i64(int(stride_atom)), c_i64(int(stride_slot)), int(nall),
+            ctypes.c_void_p(int(x_ptr)), ctypes.c_void_p(int(type_ptr)), ctypes.c_void_p(int(local_of_ptr)),
+            mt.size, _p(mt, ctypes.c_int), ctypes.c_void_p(int(f_ptr)), ctypes.byref(energy),
+            ctypes.c_void_p(int(eatom_ptr)) if eatom_ptr else None, _p(virial, ctypes.c_double),
+            ctypes.byref(rebuilt)))
+        self._evaluated = True
+        return {"energy": float(energy.value), "virial": virial, "rebuilt": bool(rebuilt.value)}
+
     def _md_nve(self, node_types, masses, positions, velocities, cell, skin, dt, steps, progress=None):
         """Velocity-Verlet NVE run on the device (the `fix nve` update of the
         reference's LAMMPS capacity runs).  positions (A), velocities (A/fs),

@@ -195,3 +195,66 @@ def test_device_pair_entry_validates_like_the_host_entry(tiny):
         call(ilist_=twice)
     call()  # the evaluator is still usable
     hip.free_all()
+
+
+def test_prepared_device_pair_entry_reuses_its_graph(tiny):
+    """The KOKKOS pair style's prepared execution
+    (pair_symmetrix_mace_kokkos.cpp:1043-1160): every listed pair an edge,
+    those beyond r_cut scaled to it (inactive), the graph rebuilt only when
+    neighbor_ago is 0.  With the list of the previous call and moved atoms
+    it updates only the edge vectors and matches the filtering entry on the
+    same list and positions to FP32 rounding (the scaled pairs change which
+    of a receiver's edges share a kernel tile, so the sums run in another
+    order); a list that changed without a rebuild is refused, and the next
+    call rebuilds."""
+    from hip_memory import Hip
+    from symmetrix_amd import MACEKokkosFloat, synthetic
+
+    path, model = tiny
+    s = synthetic.srtio3_supercell(3, sigma=0.05, seed=41)
+    n = len(s)
+    ilist, numneigh, firstneigh, x, atom_type, local_of = lammps_lists(s, model["r_cut"] + 1.0, seed=5)
+    nall = len(x)
+    mace_types = [model["atomic_numbers"].index(z) for z in (38, 22, 8)]
+    table, stride_atom, stride_slot = _kokkos_list(numneigh, firstneigh, "right")
+    hip = Hip()
+    d_ilist, d_table = hip.upload(ilist), hip.upload(table)
+    d_type, d_local = hip.upload(atom_type.astype(np.int32)), hip.upload(local_of.astype(np.int32))
+    prepared, filtering = MACEKokkosFloat(path), MACEKokkosFloat(path)
+    delta = np.random.default_rng(2).normal(scale=0.03, size=(n, 3))
+    within = [int(np.sum(np.linalg.norm(x[js & 0x1FFFFFFF] - x[i], axis=1) < model["r_cut"]))
+              for i, js in enumerate(firstneigh[:n])]
+    print(f"prepared pair entry: {n} local atoms, {int(numneigh.sum())} list entries, {sum(within)} within r_cut",
+          flush=True)
+
+    def both(xs, ago, counts=numneigh):
+        d_x, d_nn = hip.upload(xs), hip.upload(counts)
+        d_fp, d_ff = hip.upload(np.zeros((nall, 3))), hip.upload(np.zeros((nall, 3)))
+        d_ep, d_ef = hip.upload(np.zeros(nall)), hip.upload(np.zeros(nall))
+        a = prepared._pair_compute_device_prepared(ago, n, d_ilist, d_nn, d_table, stride_atom, stride_slot, nall,
+                                                   d_x, d_type, d_local, mace_types, d_fp, d_ep)
+        b = filtering._pair_compute_device(n, d_ilist, d_nn, d_table, stride_atom, stride_slot, nall, d_x, d_type,
+                                           d_local, mace_types, d_ff, d_ef)
+        a.update(f=hip.download(d_fp, (nall, 3), np.float64), eatom=hip.download(d_ep, nall, np.float64))
+        b.update(f=hip.download(d_ff, (nall, 3), np.float64), eatom=hip.download(d_ef, nall, np.float64))
+        return a, b
+
+    for step, ago in enumerate([0, 1, 2, 3]):
+        xs = x + step * delta[local_of]  # ghosts move with their local atoms
+        a, b = both(xs, ago)
+        print(f"  step {step} (ago {ago}): rebuilt {a['rebuilt']}, E {a['energy']:.8f}", flush=True)
+        assert a["rebuilt"] == (ago == 0)
+        print(f"    vs filtering entry: |dE| {abs(a['energy'] - b['energy']):.1e}, "
+              f"max|dF| {np.max(np.abs(a['f'] - b['f'])):.1e}, max|dW| {np.max(np.abs(a['virial'] - b['virial'])):.1e}",
+              flush=True)
+        assert abs(a["energy"] - b["energy"]) < 1e-8 * n
+        np.testing.assert_allclose(a["virial"], b["virial"], rtol=0, atol=1e-6)
+        np.testing.assert_allclose(a["f"], b["f"], rtol=0, atol=1e-6)
+        np.testing.assert_allclose(a["eatom"], b["eatom"], rtol=0, atol=1e-6)
+    shorter = numneigh.copy()
+    shorter[ilist[0]] -= 1
+    with pytest.raises(ValueError, match="neighbour list changed"):
+        both(x, 4, shorter)
+    a, _ = both(x, 5)
+    assert a["rebuilt"]
+    hip.free_all()
