@@ -41,17 +41,29 @@ def _system(n, seed, temperature=300.0):
     return s, m, v
 
 
-def test_device_md_matches_host_velocity_verlet(tiny):
+@pytest.mark.parametrize("tile_receivers", [None, 40])
+def test_device_md_matches_host_velocity_verlet(tiny, tile_receivers):
+    """Untiled, and under the tiled plan (tiles of 40 receivers): the device
+    driver evaluates on the current graph, then reads the displacement that
+    evaluation measured and rebuilds and evaluates again past skin/2, which
+    gives the host loop's trajectory (check first, then evaluate)."""
     from symmetrix_amd import MACEKokkosFloat, synthetic
+
+    def evaluator():
+        ev = MACEKokkosFloat(path)
+        if tile_receivers:
+            ev._set_allow_fixed_workspace(True)
+            ev._set_dual_layer_workspace_receiver_limit_for_testing(tile_receivers)
+        return ev
 
     path, model = tiny
     s, m, v0 = _system(3, seed=21, temperature=600.0)
     types = synthetic.node_types(s, model["atomic_numbers"])
     skin, dt, steps = 0.1, 2.0, 12   # small skin: the run rebuilds its graph
-    print(f"device MD vs host loop: {len(s)} atoms, {steps} steps", flush=True)
-    dev = MACEKokkosFloat(path)._md_nve(types, m, s.positions, v0, s.cell, skin, dt, steps)
+    print(f"device MD vs host loop: {len(s)} atoms, {steps} steps, tile receivers {tile_receivers}", flush=True)
+    dev = evaluator()._md_nve(types, m, s.positions, v0, s.cell, skin, dt, steps)
 
-    ev = MACEKokkosFloat(path)
+    ev = evaluator()
     inv_cell = np.linalg.inv(s.cell)
     cutoff = model["r_cut"] + skin
     x, v = s.positions.copy(), v0.copy()
@@ -72,6 +84,8 @@ def test_device_md_matches_host_velocity_verlet(tiny):
         f = ev._reduce_atom_forces(len(s), None, None, gen)
         v = v + dtf * f * inv_m
         epot.append(ev._total_energy(gen))
+    if tile_receivers:
+        assert ev.stats["tile_receivers"] == tile_receivers
     print(f"  rebuilds device {dev['rebuilds']} host {rebuilds}", flush=True)
     assert rebuilds >= 1 and dev["rebuilds"] == rebuilds
     np.testing.assert_array_equal(dev["positions"], x)
