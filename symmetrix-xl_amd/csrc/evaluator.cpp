@@ -2820,11 +2820,12 @@ constexpr double kForceToAcceleration = 9.648533212e-3;
 // runs use with pair_style symmetrix/mace): per step v += dt/2 a, x += dt v,
 // forces at the new positions, v += dt/2 a.  Every array stays on the
 // device.  A step waits on the host once: the evaluation at the new
-// positions runs on the current graph, the second half kick (into the other
-// velocity buffer) and the kinetic energy are queued behind it, and the
-// displacement the evaluation measured decides afterwards whether the graph
-// still held; if not (a rebuild step) the graph is rebuilt and the
-// evaluation and kick run again from the kept velocities.
+// positions runs on the current graph, the second half kick and the kinetic
+// energy are queued behind it, and the squared displacement the evaluation
+// measured decides whether the graph still held, on the device (the kick
+// applies only if it did) and on the host afterwards with the same
+// comparison; if not (a rebuild step) the graph is rebuilt and the
+// evaluation and kick run again on the unkicked velocities.
 int Evaluator::md_nve(int num_atoms, const int* node_types, const double* masses, double* x, double* v,
                       const double* cell, const double* inverse_cell, double skin, double dt, int steps,
                       double* epot, double* ekin, double* step_seconds)
@@ -2842,7 +2843,6 @@ int Evaluator::md_nve(int num_atoms, const int* node_types, const double* masses
     const std::size_t bytes3 = static_cast<std::size_t>(N) * 3 * sizeof(double);
     md_x_.reserve(bytes3);
     md_v_.reserve(bytes3);
-    md_v2_.reserve(bytes3);
     hip_check(hipMemcpyAsync(md_x_.as<double>(), x, bytes3, hipMemcpyHostToDevice, stream_), "MD positions");
     hip_check(hipMemcpyAsync(md_v_.as<double>(), v, bytes3, hipMemcpyHostToDevice, stream_), "MD velocities");
     upload(md_m_, m, stream_, &staged_);
@@ -2850,9 +2850,11 @@ int Evaluator::md_nve(int num_atoms, const int* node_types, const double* masses
     const int np = md_kinetic_partials(N);
     md_partials_.reserve(static_cast<std::size_t>(np) * sizeof(double));
     double* xd = md_x_.as<double>();
-    double* vd = md_v_.as<double>();      // velocities at the start of the step
-    double* vnext = md_v2_.as<double>();  // after the step's second half kick
+    double* vd = md_v_.as<double>();
     const double cutoff = model_.r_cut + skin;
+    // the graph holds while every atom moved at most skin/2 since its build:
+    // squared displacement (totals_[12]) <= (skin/2)^2
+    const double limit2 = (0.5 * skin) * (0.5 * skin);
     // the kinetic energy of `vel`, queued on the stream: m |v|^2 lands in
     // totals_[14] and host_totals_[14]
     auto queue_kinetic = [&](const double* vel) {
@@ -2881,20 +2883,20 @@ int Evaluator::md_nve(int num_atoms, const int* node_types, const double* masses
         hip_check(launch_md_kick_drift(N, xd, vd, atom_forces_.as<double>(), md_inv_m_.as<double>(), dtf, dt, stream_),
                   "MD drift");
         epilogue_ = [&] {
-            hip_check(launch_md_kick(N, vd, vnext, atom_forces_.as<double>(), md_inv_m_.as<double>(), dtf, stream_),
+            hip_check(launch_md_kick(N, vd, atom_forces_.as<double>(), md_inv_m_.as<double>(), dtf,
+                                     totals_.as<double>() + 12, limit2, stream_),
                       "MD kick");
-            if (ekin) queue_kinetic(vnext);
+            if (ekin) queue_kinetic(vd);
         };
         compute_positions(gen, xd, true);
-        if (!(last_max_displacement() <= 0.5 * skin)) {
-            // the graph no longer covers every pair within the cutoff: rebuild
-            // and evaluate again (vd still holds the half-kicked velocities)
+        if (!(host_totals_[12] <= limit2)) {
+            // the graph no longer covers every pair within the cutoff (the
+            // kick did not apply): rebuild and evaluate again
             gen = prepare_periodic_graph(N, node_types, xd, true, cell, inverse_cell, cutoff);
             ++rebuilds;
             compute_positions(gen, xd, true);
         }
         epilogue_ = nullptr;
-        std::swap(vd, vnext);
         double seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
         if (step_seconds) step_seconds[step - 1] = seconds;
         if (epot) epot[step] = total_energy(gen);

@@ -565,7 +565,7 @@ private:
     // (+ residual) in the pre_linear_up basis), graph-wide
     DeviceBuffer M0s_, run_source_, run_start_, run_length_;
     // device NVE driver state: positions, velocities, masses, unit factor / mass, kinetic partials
-    DeviceBuffer md_x_, md_v_, md_v2_, md_m_, md_inv_m_, md_partials_;
+    DeviceBuffer md_x_, md_v_, md_m_, md_inv_m_, md_partials_;
     // Work queued behind an evaluation from positions and before its one
     // host wait (the MD driver's kick and kinetic energy); null otherwise.
     std::function<void()> epilogue_;

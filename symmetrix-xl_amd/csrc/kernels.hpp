@@ -521,8 +521,9 @@ hipError_t launch_sort_segments(int num_segments, const int* offsets, int* value
 // [N][3] doubles, inv_m [N] (unit factor / mass), m [N] masses.
 hipError_t launch_md_kick_drift(int num_atoms, double* x, double* v, const double* f, const double* inv_m,
                                 double dtf, double dt, hipStream_t s);
-hipError_t launch_md_kick(int num_atoms, const double* v_in, double* v_out, const double* f, const double* inv_m,
-                          double dtf, hipStream_t s);
+// v += dtf f inv_m; with a gate, only when *gate <= gate_limit (device value)
+hipError_t launch_md_kick(int num_atoms, double* v, const double* f, const double* inv_m, double dtf,
+                          const double* gate, double gate_limit, hipStream_t s);
 // out[0] = sum m |v|^2 over the atoms (deterministic two-stage sum)
 int md_kinetic_partials(int num_atoms);
 hipError_t launch_md_kinetic(int num_atoms, const double* v, const double* m, double* partials, int num_partials,

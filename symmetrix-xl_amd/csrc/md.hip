@@ -30,13 +30,16 @@ __global__ void kick_drift_kernel(int n, double* __restrict__ x, double* __restr
     x[i] = x[i] + dt * vi;
 }
 
-// v_out = v_in + dtf f inv_m (v_out may be v_in)
-__global__ void kick_kernel(int n, const double* v_in, double* v_out, const double* __restrict__ f,
-                            const double* __restrict__ inv_m, double dtf)
+// v += dtf f inv_m, unless a gate is given and *gate <= gate_limit fails
+// (the evaluation whose forces f holds ran on a graph that no longer held)
+__global__ void kick_kernel(int n, double* __restrict__ v, const double* __restrict__ f,
+                            const double* __restrict__ inv_m, double dtf, const double* __restrict__ gate,
+                            double gate_limit)
 {
     const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i >= static_cast<size_t>(n) * 3) return;
-    v_out[i] = v_in[i] + dtf * f[i] * inv_m[i / 3];
+    if (gate && !(*gate <= gate_limit)) return;
+    v[i] = v[i] + dtf * f[i] * inv_m[i / 3];
 }
 
 // partials[b] = sum over block b's atoms of m |v|^2 (fixed order per block)
@@ -92,11 +95,11 @@ hipError_t launch_md_kick_drift(int num_atoms, double* x, double* v, const doubl
     return hipGetLastError();
 }
 
-hipError_t launch_md_kick(int num_atoms, const double* v_in, double* v_out, const double* f, const double* inv_m,
-                          double dtf, hipStream_t s)
+hipError_t launch_md_kick(int num_atoms, double* v, const double* f, const double* inv_m, double dtf,
+                          const double* gate, double gate_limit, hipStream_t s)
 {
     if (num_atoms <= 0) return hipSuccess;
-    kick_kernel<<<blocks_for(3LL * num_atoms), kMdThreads, 0, s>>>(num_atoms, v_in, v_out, f, inv_m, dtf),
+    kick_kernel<<<blocks_for(3LL * num_atoms), kMdThreads, 0, s>>>(num_atoms, v, f, inv_m, dtf, gate, gate_limit),
         note_launch();
     return hipGetLastError();
 }
