@@ -2234,6 +2234,11 @@ void Evaluator::compute_xyz(std::uint64_t generation, const double* xyz, const d
 
 double Evaluator::max_displacement(std::uint64_t generation, const double* positions, bool device_positions)
 {
+    return std::sqrt(max_displacement_squared(generation, positions, device_positions));
+}
+
+double Evaluator::max_displacement_squared(std::uint64_t generation, const double* positions, bool device_positions)
+{
     require_geometry(generation);
     const int N = num_nodes_;
     if (N > 0 && positions != positions_.as<double>())
@@ -2248,7 +2253,7 @@ double Evaluator::max_displacement(std::uint64_t generation, const double* posit
     hip_check(hipMemcpyAsync(&d2, totals_.as<double>() + 12, sizeof(double), hipMemcpyDeviceToHost, stream_),
               "copy");
     wait("displacement");
-    return std::sqrt(d2);
+    return d2;
 }
 
 // Density-normalisation arguments of the layer and readout kernels.
@@ -2819,13 +2824,17 @@ constexpr double kForceToAcceleration = 9.648533212e-3;
 // Velocity-Verlet NVE (the LAMMPS `fix nve` update the reference's capacity
 // runs use with pair_style symmetrix/mace): per step v += dt/2 a, x += dt v,
 // forces at the new positions, v += dt/2 a.  Every array stays on the
-// device.  A step waits on the host once: the evaluation at the new
-// positions runs on the current graph, the second half kick and the kinetic
-// energy are queued behind it, and the squared displacement the evaluation
-// measured decides whether the graph still held, on the device (the kick
-// applies only if it did) and on the host afterwards with the same
-// comparison; if not (a rebuild step) the graph is rebuilt and the
-// evaluation and kick run again on the unkicked velocities.
+// device.  The second half kick and the kinetic energy are queued behind
+// the evaluation at the new positions, and the squared displacement that
+// evaluation measured decides whether the graph still held, on the device
+// (the kick applies only if it did) and on the host afterwards with the same
+// comparison; if not, the graph is rebuilt and the evaluation and kick run
+// again on the unkicked velocities.  While the displacement since the build
+// plus twice its largest growth per step so far stays below skin/2, a step
+// evaluates on the graph directly and waits on the host once; otherwise
+// (the first step, the steps near a rebuild) the displacement is checked
+// before the evaluation, so an evaluation is rarely run on a graph that no
+// longer holds (which would cost a whole evaluation at capacity sizes).
 int Evaluator::md_nve(int num_atoms, const int* node_types, const double* masses, double* x, double* v,
                       const double* cell, const double* inverse_cell, double skin, double dt, int steps,
                       double* epot, double* ekin, double* step_seconds)
@@ -2878,10 +2887,21 @@ int Evaluator::md_nve(int num_atoms, const int* node_types, const double* masses
     if (epot) epot[0] = total_energy(gen);
     if (ekin) ekin[0] = 0.5 * host_totals_[14] / kForceToAcceleration;
     const double dtf = 0.5 * dt;
+    double disp = 0.0;      // displacement since the graph's build after the last evaluation
+    double growth = -1.0;   // largest growth of it in one step (negative: none seen yet)
     for (int step = 1; step <= steps; ++step) {
         const auto t0 = std::chrono::steady_clock::now();
         hip_check(launch_md_kick_drift(N, xd, vd, atom_forces_.as<double>(), md_inv_m_.as<double>(), dtf, dt, stream_),
                   "MD drift");
+        bool rebuilt = false;
+        if (!(growth >= 0.0 && disp + 2.0 * growth < 0.5 * skin)) {
+            // near a rebuild (or no growth seen yet): check before evaluating
+            if (!(max_displacement_squared(gen, xd, true) <= limit2)) {
+                gen = prepare_periodic_graph(N, node_types, xd, true, cell, inverse_cell, cutoff);
+                ++rebuilds;
+                rebuilt = true;
+            }
+        }
         epilogue_ = [&] {
             hip_check(launch_md_kick(N, vd, atom_forces_.as<double>(), md_inv_m_.as<double>(), dtf,
                                      totals_.as<double>() + 12, limit2, stream_),
@@ -2894,9 +2914,13 @@ int Evaluator::md_nve(int num_atoms, const int* node_types, const double* masses
             // kick did not apply): rebuild and evaluate again
             gen = prepare_periodic_graph(N, node_types, xd, true, cell, inverse_cell, cutoff);
             ++rebuilds;
+            rebuilt = true;
             compute_positions(gen, xd, true);
         }
         epilogue_ = nullptr;
+        const double now = std::sqrt(host_totals_[12]);
+        if (!rebuilt) growth = std::max(growth, now - disp);
+        disp = now;
         double seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
         if (step_seconds) step_seconds[step - 1] = seconds;
         if (epot) epot[step] = total_energy(gen);

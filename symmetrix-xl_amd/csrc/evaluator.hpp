@@ -292,6 +292,7 @@ public:
     // Largest displacement (Angstrom) of positions from those of the last
     // periodic graph build, on the device (for neighbour-list skin reuse).
     double max_displacement(std::uint64_t generation, const double* positions, bool device_positions);
+    double max_displacement_squared(std::uint64_t generation, const double* positions, bool device_positions);
 
     // --- device NVE molecular dynamics -----------------------------------------
     // Velocity-Verlet NVE run of `steps` steps of dt (fs) with positions,
