@@ -306,6 +306,14 @@ __device__ __forceinline__ void store1(float v, __amdgpu_buffer_rsrc_t r, int vo
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned int, v), r, voffset, soffset, 0);
 }
 
+// Non-temporal (streaming) store: cache-policy NT, for data written once and
+// read once much later by another kernel, far more than the L2s hold.
+constexpr int kCachePolicyNT = 2;
+__device__ __forceinline__ void store1_stream(float v, __amdgpu_buffer_rsrc_t r, int voffset, int soffset)
+{
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned int, v), r, voffset, soffset, kCachePolicyNT);
+}
+
 // Cubic of one interval, c = (c0, c1, c2, c3) in local coordinate x.
 __device__ __forceinline__ float cubic(const float4v& c, float x)
 {
