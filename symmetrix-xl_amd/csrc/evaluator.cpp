@@ -110,9 +110,10 @@ long long term_key(int out, int deg, int i0, int i1, int i2)
 // runtime remainder, grouped by output in JSON order.  Compiled slots that
 // the JSON does not use keep a zero coefficient.
 PolyLayout poly_layout(int lin, int lout, const std::vector<int>& offsets, const std::vector<int>& degree,
-                       const std::vector<int>& index)
+                       const std::vector<int>& index, bool quad)
 {
     PolyLayout L;
+    L.quad = quad;
     const int nout = static_cast<int>(offsets.size()) - 1;
     const int T = offsets.back();
     int corr = 0;
@@ -139,16 +140,17 @@ PolyLayout poly_layout(int lin, int lout, const std::vector<int>& offsets, const
     }
     L.core = cp.nt > 0 ? corr : 0;
     L.core_terms = cp.nt;
+    const int core_slots = quad ? compiled_slots(cp.nt) : cp.nt;
     L.rem_offsets.push_back(0);
     for (int o = 0; o < nout; ++o) {
         for (int j = offsets[o]; j < offsets[o + 1]; ++j) {
             if (L.slot[j] >= 0) continue;
-            L.slot[j] = cp.nt + static_cast<int>(L.rem_packed.size());
+            L.slot[j] = core_slots + static_cast<int>(L.rem_packed.size());
             L.rem_packed.push_back(pack_term(degree[j], index.data() + 3 * static_cast<std::size_t>(j)));
         }
         L.rem_offsets.push_back(static_cast<int>(L.rem_packed.size()));
     }
-    L.stride = cp.nt + static_cast<int>(L.rem_packed.size());
+    L.stride = core_slots + static_cast<int>(L.rem_packed.size());
     return L;
 }
 
@@ -429,11 +431,11 @@ void Evaluator::upload_static_tables()
     std::vector<float> cg;
     with_r1_shape(m.l_max, m.L_max, [&](auto shape) { cg = shape_cg<decltype(shape)>(m); });
     upload(cg_, cg, stream_);
-    p0_layout_ = poly_layout(m.l_max, m.L_max, m.m0_offsets, m.m0_degree, m.m0_index);
+    p0_layout_ = poly_layout(m.l_max, m.L_max, m.m0_offsets, m.m0_degree, m.m0_index, true);
     upload(p0_offsets_, p0_layout_.rem_offsets, stream_);
     upload(p0_packed_, p0_layout_.rem_packed, stream_);
     const std::vector<int> off1 = {0, static_cast<int>(m.m1_degree.size())};
-    p1_layout_ = poly_layout(m.l_max, 0, off1, m.m1_degree, m.m1_index);
+    p1_layout_ = poly_layout(m.l_max, 0, off1, m.m1_degree, m.m1_index, false);
     upload(p1_offsets_, p1_layout_.rem_offsets, stream_);
     upload(p1_packed_, p1_layout_.rem_packed, stream_);
 }
@@ -656,15 +658,21 @@ void Evaluator::prepare_active_types(const std::vector<int>& node_types)
     upload(type_active_, type_active, stream_, &staged_);
     std::vector<float> p0c, p1c, h2m0, h2m0t;
     std::vector<double> e0;
-    // coefficients [active][slot][C] on the slots of the polynomial layouts
+    // coefficients per active type on the slots of the polynomial layouts:
+    // [slot][C], or for a quad layout the compiled slots in runs of four per
+    // channel ([slot / 4][C][4], one 16-byte load per lane for four terms)
     auto place = [&](const PolyLayout& L, const std::vector<double>& coef, int t, std::vector<float>& out) {
         const std::size_t T = L.slot.size();
         const std::size_t base = out.size();
         out.resize(base + static_cast<std::size_t>(L.stride) * C_, 0.0f);
-        for (std::size_t j = 0; j < T; ++j)
-            for (int k = 0; k < C_; ++k)
-                out[base + static_cast<std::size_t>(L.slot[j]) * C_ + k] =
-                    static_cast<float>(coef[(static_cast<std::size_t>(t) * T + j) * C_ + k]);
+        for (std::size_t j = 0; j < T; ++j) {
+            const std::size_t s = static_cast<std::size_t>(L.slot[j]);
+            for (int k = 0; k < C_; ++k) {
+                const std::size_t at =
+                    L.quad && static_cast<int>(s) < L.core_terms ? (s / 4 * C_ + k) * 4 + s % 4 : s * C_ + k;
+                out[base + at] = static_cast<float>(coef[(static_cast<std::size_t>(t) * T + j) * C_ + k]);
+            }
+        }
     };
     for (int a = 0; a < na; ++a) {
         const int t = types[a];

@@ -133,14 +133,15 @@ std::size_t noalloc_scratch_bytes();
 // coefficient slots (see PolyArgs): JSON term j -> slot[j].
 struct PolyLayout {
     int core = 0;        // correlation order of the compiled table used, 0 = none
-    int core_terms = 0;  // compiled slots
+    int core_terms = 0;  // compiled terms
+    bool quad = false;   // compiled slots in runs of four per channel ([slot / 4][C][4])
     int stride = 0;      // slots per active type
     std::vector<int> slot;
     std::vector<int> rem_offsets;  // [outputs + 1]
     std::vector<int> rem_packed;
 };
 PolyLayout poly_layout(int input_lmax, int output_lmax, const std::vector<int>& offsets,
-                       const std::vector<int>& degree, const std::vector<int>& index);
+                       const std::vector<int>& degree, const std::vector<int>& index, bool quad);
 
 // Bytes of device memory held by this library's buffers (all evaluators).
 std::size_t device_bytes_in_use();

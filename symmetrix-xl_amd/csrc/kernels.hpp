@@ -83,8 +83,15 @@ struct PolyArgs {
     int num_rem = 0;                   // remainder terms
     const int* rem_offsets = nullptr;  // [outputs+1] remainder terms grouped by output
     const int* rem_packed = nullptr;   // [num_rem] deg | i0<<4 | i1<<10 | i2<<16
-    const float* coef = nullptr;       // [active_type][stride][C], compiled slots first
+    const float* coef = nullptr;       // [active_type][stride][C] floats: compiled slots first, then the
+                                       // remainder slots [slot][C]; the M0 table holds its compiled slots
+                                       // in runs of four per channel ([slot / 4][C][4], padded to a
+                                       // multiple of four slots), the readout table [slot][C]
 };
+
+// Slots of the compiled terms of an M0 coefficient block: the term count
+// padded to whole runs of four.
+constexpr int compiled_slots(int terms) { return (terms + 3) / 4 * 4; }
 
 // Nodes grouped by active type: each block holds up to a fixed number of
 // nodes of one type, so that a thread applies each coefficient it loads to

@@ -52,11 +52,36 @@ __device__ __forceinline__ void chunk_boundary(float (&x)[NB][NIN])
         for (int v = 0; v < NIN; ++v) asm volatile("" : "+v"(x[n][v]));
 }
 
-template <class P, int BASE>
+// kQuad: the compiled coefficients lie in runs of four terms per channel
+// ([slot / 4][C][4]), one 16-byte load per lane bringing four terms; else one
+// [slot][C] row per term.  voff is the lane's byte offset in a [slot][C] row
+// (kk * 4).  The M0 kernels take the runs of four (medium shape: forward
+// 32.6 -> 24 us, reverse 51 -> 43 us); the readout keeps a row per term, as
+// its eight-node blocks (graphs of many receivers) then need 256 VGPRs and
+// run at one wave per SIMD (0.81 -> 1.30 ms on water) or spill at two
+// (0.81 -> 0.82 ms), and its two-node blocks gain nothing.
+template <class P, int BASE, bool kQuad>
 __device__ __forceinline__ void load_chunk(__amdgpu_buffer_rsrc_t cs, int voff, int C, float (&c)[kChunk])
 {
+    static_assert(BASE % 4 == 0 && kChunk % 4 == 0);
+    if constexpr (!kQuad) {
 #pragma unroll
-    for (int j = 0; j < kChunk; ++j) c[j] = BASE + j < P::NT ? load1(cs, voff, (BASE + j) * C * 4) : 0.0f;
+        for (int j = 0; j < kChunk; ++j) c[j] = BASE + j < P::NT ? load1(cs, voff, (BASE + j) * C * 4) : 0.0f;
+        return;
+    }
+#pragma unroll
+    for (int u = 0; u < kChunk / 4; ++u) {
+        if (BASE + 4 * u < P::NT) {
+            const float4v q = load4(cs, 4 * voff, (BASE / 4 + u) * C * 16);
+            c[4 * u] = q.x;
+            c[4 * u + 1] = q.y;
+            c[4 * u + 2] = q.z;
+            c[4 * u + 3] = q.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) c[4 * u + j] = 0.0f;
+        }
+    }
 }
 
 // The compiled tables list consecutive groups of terms of one output and
@@ -144,20 +169,20 @@ __device__ __forceinline__ void gradient_chunk(const float (&c)[kChunk], const f
     (term_gradient<P, NB, BASE + J>(c[J], x, lam, g, U, pl), ...);
 }
 
-template <class P, int NB, int BASE>
+template <class P, int NB, int BASE, bool kQuad>
 __device__ __forceinline__ void core_value_from(__amdgpu_buffer_rsrc_t cs, int voff, int C, const float (&cur)[kChunk],
                                                 float (&x)[NB][P::NIN], float (&out)[NB][P::NOUT], float (&U)[NB])
 {
     if constexpr (BASE < P::NT) {
         float nxt[kChunk];
-        if constexpr (BASE + kChunk < P::NT) load_chunk<P, BASE + kChunk>(cs, voff, C, nxt);
+        if constexpr (BASE + kChunk < P::NT) load_chunk<P, BASE + kChunk, kQuad>(cs, voff, C, nxt);
         value_chunk<P, NB, BASE>(cur, x, out, U, std::make_integer_sequence<int, kChunk>{});
         chunk_boundary<NB, P::NIN>(x);
-        core_value_from<P, NB, BASE + kChunk>(cs, voff, C, nxt, x, out, U);
+        core_value_from<P, NB, BASE + kChunk, kQuad>(cs, voff, C, nxt, x, out, U);
     }
 }
 
-template <class P, int NB, int BASE>
+template <class P, int NB, int BASE, bool kQuad>
 __device__ __forceinline__ void core_gradient_from(__amdgpu_buffer_rsrc_t cs, int voff, int C,
                                                    const float (&cur)[kChunk], float (&x)[NB][P::NIN],
                                                    const float (&lam)[NB][P::NOUT], float (&g)[NB][P::NIN],
@@ -165,35 +190,35 @@ __device__ __forceinline__ void core_gradient_from(__amdgpu_buffer_rsrc_t cs, in
 {
     if constexpr (BASE < P::NT) {
         float nxt[kChunk];
-        if constexpr (BASE + kChunk < P::NT) load_chunk<P, BASE + kChunk>(cs, voff, C, nxt);
+        if constexpr (BASE + kChunk < P::NT) load_chunk<P, BASE + kChunk, kQuad>(cs, voff, C, nxt);
         gradient_chunk<P, NB, BASE>(cur, x, lam, g, U, pl, std::make_integer_sequence<int, kChunk>{});
         chunk_boundary<NB, P::NIN>(x);
-        core_gradient_from<P, NB, BASE + kChunk>(cs, voff, C, nxt, x, lam, g, U, pl);
+        core_gradient_from<P, NB, BASE + kChunk, kQuad>(cs, voff, C, nxt, x, lam, g, U, pl);
     }
 }
 
 // out[n][o] += sum over compiled terms t of output o: c_t prod x[n][i]
-template <class P, int NB>
+template <class P, int NB, bool kQuad>
 __device__ __forceinline__ void core_value(__amdgpu_buffer_rsrc_t cs, int voff, int C,
                                            float (&x)[NB][P::NIN], float (&out)[NB][P::NOUT])
 {
     if constexpr (P::NT > 0) {
         float c[kChunk], U[NB];
-        load_chunk<P, 0>(cs, voff, C, c);
-        core_value_from<P, NB, 0>(cs, voff, C, c, x, out, U);
+        load_chunk<P, 0, kQuad>(cs, voff, C, c);
+        core_value_from<P, NB, 0, kQuad>(cs, voff, C, c, x, out, U);
     }
 }
 
 // g[n][i] += sum over compiled terms t: c_t lam[n][out_t] d(prod x[n])/dx_i
-template <class P, int NB>
+template <class P, int NB, bool kQuad>
 __device__ __forceinline__ void core_gradient(__amdgpu_buffer_rsrc_t cs, int voff, int C,
                                               float (&x)[NB][P::NIN], const float (&lam)[NB][P::NOUT],
                                               float (&g)[NB][P::NIN])
 {
     if constexpr (P::NT > 0) {
         float c[kChunk], U[NB], pl[NB];
-        load_chunk<P, 0>(cs, voff, C, c);
-        core_gradient_from<P, NB, 0>(cs, voff, C, c, x, lam, g, U, pl);
+        load_chunk<P, 0, kQuad>(cs, voff, C, c);
+        core_gradient_from<P, NB, 0, kQuad>(cs, voff, C, c, x, lam, g, U, pl);
     }
 }
 
@@ -202,7 +227,7 @@ __device__ __forceinline__ void core_gradient(__amdgpu_buffer_rsrc_t cs, int vof
 // ---------------------------------------------------------------------------
 template <int NOUT>
 __device__ __forceinline__ void rem_value(const PolyArgs& p, __amdgpu_buffer_rsrc_t cs, int voff, int C,
-                                          int core_terms, const float* xc, int xs, float (&f)[NOUT])
+                                          int first_rem, const float* xc, int xs, float (&f)[NOUT])
 {
 #pragma unroll
     for (int o = 0; o < NOUT; ++o)
@@ -212,13 +237,13 @@ __device__ __forceinline__ void rem_value(const PolyArgs& p, __amdgpu_buffer_rsr
             float v = xc[((pk >> 4) & 63) * xs];
             if (d > 1) v *= xc[((pk >> 10) & 63) * xs];
             if (d > 2) v *= xc[((pk >> 16) & 63) * xs];
-            f[o] = fmaf(load1(cs, voff, (core_terms + t) * C * 4), v, f[o]);
+            f[o] = fmaf(load1(cs, voff, (first_rem + t) * C * 4), v, f[o]);
         }
 }
 
 template <int NOUT>
 __device__ __forceinline__ void rem_gradient(const PolyArgs& p, __amdgpu_buffer_rsrc_t cs, int voff, int C,
-                                             int core_terms, const float* xc, float* gc, int xs,
+                                             int first_rem, const float* xc, float* gc, int xs,
                                              const float (&lam)[NOUT])
 {
 #pragma unroll
@@ -227,7 +252,7 @@ __device__ __forceinline__ void rem_gradient(const PolyArgs& p, __amdgpu_buffer_
             const int pk = p.rem_packed[t];
             const int d = pk & 15;
             const int a0 = ((pk >> 4) & 63) * xs, a1 = ((pk >> 10) & 63) * xs, a2 = ((pk >> 16) & 63) * xs;
-            const float u = load1(cs, voff, (core_terms + t) * C * 4) * lam[o];
+            const float u = load1(cs, voff, (first_rem + t) * C * 4) * lam[o];
             if (d == 1) {
                 gc[a0] += u;
             } else if (d == 2) {
@@ -243,8 +268,12 @@ __device__ __forceinline__ void rem_gradient(const PolyArgs& p, __amdgpu_buffer_
         }
 }
 
+// First remainder slot of a coefficient block.
+template <class P, bool kQuad>
+constexpr int first_rem_slot() { return kQuad ? compiled_slots(P::NT) : P::NT; }
+
 // Forward remainder of the NB nodes held in registers (LDS column of NIN floats).
-template <class P, int NB>
+template <class P, int NB, bool kQuad>
 __device__ __forceinline__ void rem_value_nodes(const PolyArgs& p, __amdgpu_buffer_rsrc_t cs, int voff, int C,
                                                 float* xc, int xs, const float (&x)[NB][P::NIN],
                                                 float (&out)[NB][P::NOUT])
@@ -253,11 +282,11 @@ __device__ __forceinline__ void rem_value_nodes(const PolyArgs& p, __amdgpu_buff
     for (int n = 0; n < NB; ++n) {
 #pragma unroll
         for (int v = 0; v < P::NIN; ++v) xc[v * xs] = x[n][v];
-        rem_value<P::NOUT>(p, cs, voff, C, P::NT, xc, xs, out[n]);
+        rem_value<P::NOUT>(p, cs, voff, C, first_rem_slot<P, kQuad>(), xc, xs, out[n]);
     }
 }
 
-template <class P, int NB>
+template <class P, int NB, bool kQuad>
 __device__ __forceinline__ void rem_gradient_nodes(const PolyArgs& p, __amdgpu_buffer_rsrc_t cs, int voff, int C,
                                                    float* xc, float* gc, int xs, const float (&x)[NB][P::NIN],
                                                    const float (&lam)[NB][P::NOUT], float (&g)[NB][P::NIN])
@@ -269,7 +298,7 @@ __device__ __forceinline__ void rem_gradient_nodes(const PolyArgs& p, __amdgpu_b
             xc[v * xs] = x[n][v];
             gc[v * xs] = 0.0f;
         }
-        rem_gradient<P::NOUT>(p, cs, voff, C, P::NT, xc, gc, xs, lam[n]);
+        rem_gradient<P::NOUT>(p, cs, voff, C, first_rem_slot<P, kQuad>(), xc, gc, xs, lam[n]);
 #pragma unroll
         for (int v = 0; v < P::NIN; ++v) g[n][v] += gc[v * xs];
     }
@@ -303,8 +332,8 @@ __global__ void __launch_bounds__(256) m0_forward_kernel(LayerArgs a, PolyArgs p
 #pragma unroll
         for (int o = 0; o < NOUT; ++o) out[n][o] = 0.0f;
     const auto cs = buffer_rsrc(p.coef + static_cast<size_t>(blk.type) * p.stride * C, p.stride * C * 4);
-    core_value<P, NB>(cs, kk * 4, C, x, out);
-    if (p.num_rem > 0) rem_value_nodes<P, NB>(p, cs, kk * 4, C, s_mem + k, blockDim.x, x, out);
+    core_value<P, NB, true>(cs, kk * 4, C, x, out);
+    if (p.num_rem > 0) rem_value_nodes<P, NB, true>(p, cs, kk * 4, C, s_mem + k, blockDim.x, x, out);
     if (k < C) {
 #pragma unroll
         for (int n = 0; n < NB; ++n) {
@@ -345,9 +374,9 @@ __global__ void __launch_bounds__(256) m0_reverse_kernel(LayerArgs a, PolyArgs p
         for (int o = 0; o < NOUT; ++o) lam[n][o] = node[n] >= 0 ? la[o * C] : 0.0f;
     }
     const auto cs = buffer_rsrc(p.coef + static_cast<size_t>(blk.type) * p.stride * C, p.stride * C * 4);
-    core_gradient<P, NB>(cs, kk * 4, C, x, lam, g);
+    core_gradient<P, NB, true>(cs, kk * 4, C, x, lam, g);
     if (p.num_rem > 0)
-        rem_gradient_nodes<P, NB>(p, cs, kk * 4, C, s_mem + k, s_mem + NIN * blockDim.x + k, blockDim.x, x,
+        rem_gradient_nodes<P, NB, true>(p, cs, kk * 4, C, s_mem + k, s_mem + NIN * blockDim.x + k, blockDim.x, x,
                                   lam, g);
     if (k < C) {
 #pragma unroll
@@ -454,8 +483,8 @@ __global__ void __launch_bounds__(256) readout_kernel(ReadoutArgs a)
             }
             m1[n][0] = 0.0f;
         }
-        core_value<P1, G>(cs, voff, C, x, m1);
-        if (a.p1.num_rem > 0) rem_value_nodes<P1, G>(a.p1, cs, voff, C, s_rem + k, T, x, m1);
+        core_value<P1, G, false>(cs, voff, C, x, m1);
+        if (a.p1.num_rem > 0) rem_value_nodes<P1, G, false>(a.p1, cs, voff, C, s_rem + k, T, x, m1);
 #pragma unroll
         for (int n = 0; n < G; ++n) {
             const int i = node[g0 + n];
@@ -646,9 +675,9 @@ __global__ void __launch_bounds__(256) readout_kernel(ReadoutArgs a)
             }
             lam[n][0] = m1adj[g0 + n];
         }
-        core_gradient<P1, G>(cs, voff, C, x, lam, g);
+        core_gradient<P1, G, false>(cs, voff, C, x, lam, g);
         if (a.p1.num_rem > 0)
-            rem_gradient_nodes<P1, G>(a.p1, cs, voff, C, s_rem + k, s_rem + NIN * T + k, T, x, lam, g);
+            rem_gradient_nodes<P1, G, false>(a.p1, cs, voff, C, s_rem + k, s_rem + NIN * T + k, T, x, lam, g);
         if (a.a1_scale) {
 #pragma unroll
             for (int n = 0; n < G; ++n) {
