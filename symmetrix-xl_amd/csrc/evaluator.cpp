@@ -63,6 +63,18 @@ std::vector<float> transpose(const double* p, int rows, int cols)
     return out;
 }
 
+// A row-major [rows][cols] matrix read one row per step, a column per lane,
+// in runs of four rows per column: [rows / 4][cols][4] (rows a multiple of 4)
+std::vector<float> runs4(const std::vector<float>& m, int rows, int cols)
+{
+    if (rows % 4 != 0) throw std::invalid_argument("runs of four rows need a row count divisible by 4");
+    std::vector<float> out(m.size());
+    for (int r = 0; r < rows; ++r)
+        for (int c = 0; c < cols; ++c)
+            out[(static_cast<std::size_t>(r / 4) * cols + c) * 4 + r % 4] = m[static_cast<std::size_t>(r) * cols + c];
+    return out;
+}
+
 // Monomial -> packed (deg | i0 << 4 | i1 << 10 | i2 << 16)
 int pack_term(int degree, const int* index)
 {
@@ -423,8 +435,8 @@ void Evaluator::upload_static_tables()
         upload(residual_, to_float(m.residual.data(), m.residual.size()), stream_);
         upload(residual_fused_, to_float(m.residual_fused.data(), m.residual_fused.size()), stream_);
     }
-    upload(h2m1_, to_float(m.H2M1.data(), m.H2M1.size()), stream_);
-    upload(h2m1t_, transpose(m.H2M1.data(), C_, C_), stream_);
+    upload(h2m1_, runs4(to_float(m.H2M1.data(), m.H2M1.size()), C_, C_), stream_);
+    upload(h2m1t_, runs4(transpose(m.H2M1.data(), C_, C_), C_, C_), stream_);
     upload(q_, to_float(m.readout_q.data(), m.readout_q.size()), stream_);
     upload(w1_, to_float(m.readout_w1.data(), m.readout_w1.size()), stream_);
     upload(w2_, to_float(m.readout_w2.data(), m.readout_w2.size()), stream_);
@@ -678,10 +690,11 @@ void Evaluator::prepare_active_types(const std::vector<int>& node_types)
         const int t = types[a];
         place(p0_layout_, m.m0_coef, t, p0c);
         place(p1_layout_, m.m1_coef, t, p1c);
-        auto hm = to_float(m.H2M0.data() + static_cast<std::size_t>(t) * C_ * C_,
-                           static_cast<std::size_t>(C_) * C_);
+        auto hm = runs4(to_float(m.H2M0.data() + static_cast<std::size_t>(t) * C_ * C_,
+                                 static_cast<std::size_t>(C_) * C_),
+                        C_, C_);
         h2m0.insert(h2m0.end(), hm.begin(), hm.end());
-        auto hmt = transpose(m.H2M0.data() + static_cast<std::size_t>(t) * C_ * C_, C_, C_);
+        auto hmt = runs4(transpose(m.H2M0.data() + static_cast<std::size_t>(t) * C_ * C_, C_, C_), C_, C_);
         h2m0t.insert(h2m0t.end(), hmt.begin(), hmt.end());
         e0.push_back(m.atomic_energies[t]);
     }

@@ -254,10 +254,12 @@ struct ReadoutArgs {
     float* a1_dot = nullptr;          // [N] A1_adj . A1 per node (scaled model)
     const float* M0 = nullptr;      // scalar block (LM 0) of node i at M0 + i * m0_stride
     PolyArgs p1;
-    const float* H2M0 = nullptr;    // [active][C][C]  ([in][out])
-    const float* H2M0T = nullptr;   // [active][C][C]  ([out][in])
-    const float* H2M1 = nullptr;    // [C][C]  ([in][out])
-    const float* H2M1T = nullptr;   // [C][C]  ([out][in])
+    // the H2 weights in runs of four of the streamed index per lane index
+    // (runs4: [in / 4][out][4] for a matrix read as [in][out])
+    const float* H2M0 = nullptr;    // [active] runs4 of [in][out]
+    const float* H2M0T = nullptr;   // [active] runs4 of [out][in]
+    const float* H2M1 = nullptr;    // runs4 of [in][out]
+    const float* H2M1T = nullptr;   // runs4 of [out][in]
     const float* q = nullptr;       // [C]
     const float* W1 = nullptr;      // [hidden][C]
     const float* W2 = nullptr;      // [hidden]

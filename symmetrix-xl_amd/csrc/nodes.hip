@@ -501,14 +501,14 @@ __global__ void __launch_bounds__(256) readout_kernel(ReadoutArgs a)
         float h2[NB];
 #pragma unroll
         for (int n = 0; n < NB; ++n) h2[n] = 0.0f;
-        const float* Tm = a.H2M0 + static_cast<size_t>(blk.type) * C * C + k;
-        const float* Wm = a.H2M1 + k;
+        // weights in runs of four inputs per output ([in / 4][out][4]): two
+        // 16-byte loads per lane and block of four inputs
+        const float4* Tm = reinterpret_cast<const float4*>(a.H2M0 + static_cast<size_t>(blk.type) * C * C) + k;
+        const float4* Wm = reinterpret_cast<const float4*>(a.H2M1) + k;
         auto load = [&](int b, float (&w)[8]) {
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                w[u] = Tm[static_cast<size_t>(4 * b + u) * C];
-                w[4 + u] = Wm[static_cast<size_t>(4 * b + u) * C];
-            }
+            const float4 t = Tm[static_cast<size_t>(b) * C], m = Wm[static_cast<size_t>(b) * C];
+            w[0] = t.x, w[1] = t.y, w[2] = t.z, w[3] = t.w;
+            w[4] = m.x, w[5] = m.y, w[6] = m.z, w[7] = m.w;
         };
         auto use = [&](int b, const float (&w)[8]) {
             const int in = 4 * b;
@@ -618,14 +618,12 @@ __global__ void __launch_bounds__(256) readout_kernel(ReadoutArgs a)
         const float qk = a.q[k];
 #pragma unroll
         for (int n = 0; n < NB; ++n) d[n] = qk;
-        const float* Tt = a.H2M0T + static_cast<size_t>(blk.type) * C * C + k;
-        const float* Wt = a.H2M1T + k;
+        const float4* Tt = reinterpret_cast<const float4*>(a.H2M0T + static_cast<size_t>(blk.type) * C * C) + k;
+        const float4* Wt = reinterpret_cast<const float4*>(a.H2M1T) + k;
         auto load = [&](int b, float (&w)[8]) {
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                w[u] = Tt[static_cast<size_t>(4 * b + u) * C];
-                w[4 + u] = Wt[static_cast<size_t>(4 * b + u) * C];
-            }
+            const float4 t = Tt[static_cast<size_t>(b) * C], m = Wt[static_cast<size_t>(b) * C];
+            w[0] = t.x, w[1] = t.y, w[2] = t.z, w[3] = t.w;
+            w[4] = m.x, w[5] = m.y, w[6] = m.z, w[7] = m.w;
         };
         auto use = [&](int b, const float (&w)[8]) {
             const int o = 4 * b;
