@@ -1234,8 +1234,9 @@ void Evaluator::plan_node_blocks()
     order.reserve(N);
     std::vector<NodeBlock> m0b, m0rb, rob;
     // narrower blocks for the two-wave-per-SIMD node kernels (M0 reverse,
-    // readout) of a launch that would otherwise fill the machine less than
-    // twice over: more workgroups, fewer registers, a shorter last round
+    // readout, eight-node M0 forward) of a launch that would otherwise fill
+    // the machine less than twice over: more workgroups, fewer registers, a
+    // shorter last round
     const long long launch_nodes = std::min(N, T);
     const int block_waves = (C_ + 63) / 64;  // node kernels: one thread per channel
     const long long two_rounds = 2LL * 2 * 4 * std::max(compute_units_, 1);  // waves: 2 per SIMD, 4 SIMDs per CU
@@ -1251,7 +1252,7 @@ void Evaluator::plan_node_blocks()
     // 511 -> 526 us).  SXL_NODE_BLOCK=1 / 0 forces the choice (tests).
     bool one_node = launch_nodes * block_waves <= 4LL * std::max(compute_units_, 1);
     if (const char* v = std::getenv("SXL_NODE_BLOCK"); v && v[0]) one_node = v[0] == '1';
-    m0_block_nodes_ = kM0BlockNodes;
+    m0_block_nodes_ = narrow(kM0ForwardBlockNodesWide) ? kM0BlockNodes : kM0ForwardBlockNodesWide;
     if (one_node) m0_block_nodes_ = m0r_block_nodes_ = readout_block_nodes_ = 1;
     m0_block_offsets_.assign(tiles + 1, 0);
     m0r_block_offsets_.assign(tiles + 1, 0);

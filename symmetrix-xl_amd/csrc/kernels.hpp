@@ -110,6 +110,11 @@ struct NodeBlocks {
     int block_nodes = 0;  // most nodes in one block of the list
 };
 constexpr int kM0BlockNodes = 4;       // nodes per block of the M0 kernels
+// nodes per block of the M0 forward on launches that fill the machine twice
+// over even so (the readout's rule): each coefficient load serves eight nodes
+// (two waves per SIMD at 210-250 VGPRs; measured: water 0.45 -> 0.33 ms,
+// 20,000 atoms 80 -> 74 us; 5,000 atoms 23.6 -> 26.0 us, hence four there)
+constexpr int kM0ForwardBlockNodesWide = 8;
 // nodes per block of the M0 reverse at C <= 128 when the launch is small:
 // its blocks are two waves of 200 VGPRs, and four nodes per block leave a
 // 5,000-atom launch one and a fraction waves per SIMD (measured: 66 -> 55 us

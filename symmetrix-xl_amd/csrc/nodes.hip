@@ -715,14 +715,17 @@ hipError_t m0_forward_launch(const LayerArgs& a, const PolyArgs& p, const NodeBl
                              float* M0, hipStream_t s)
 {
     using P = PolyShape<LIN, LOUT, CORR>;
-    if (nb.block_nodes < 1 || nb.block_nodes > kM0BlockNodes) return hipErrorInvalidValue;
+    if (nb.block_nodes < 1 || nb.block_nodes > kM0ForwardBlockNodesWide) return hipErrorInvalidValue;
     const int threads = node_threads(a.C);
     const size_t shmem = p.num_rem > 0 ? sizeof(float) * P::NIN * threads : 0;
     // the kernel holds at least as many nodes as the list's largest block
     if (nb.block_nodes == 1)
         m0_forward_kernel<P, 1><<<nb.count, threads, shmem, s>>>(a, p, nb, A0, M0), note_launch();
-    else
+    else if (nb.block_nodes <= kM0BlockNodes)
         m0_forward_kernel<P, kM0BlockNodes><<<nb.count, threads, shmem, s>>>(a, p, nb, A0, M0), note_launch();
+    else
+        m0_forward_kernel<P, kM0ForwardBlockNodesWide><<<nb.count, threads, shmem, s>>>(a, p, nb, A0, M0),
+            note_launch();
     return hipGetLastError();
 }
 

@@ -98,21 +98,25 @@ def test_sliced_layer0_forward_matches_oracle(oracle_lib, tmp_path, monkeypatch,
     assert dn < 1e-5 * scale and dw < 1e-4
 
 
-@pytest.mark.parametrize("case", ["tiny", "medium3", "all_options", "wide"])
+@pytest.mark.parametrize("case", ["tiny", "medium3", "all_options", "wide", "wide300"])
 def test_one_node_blocks_equal_wider_blocks(tmp_path, monkeypatch, case):
     """The node kernels (M0 forward and reverse, readout) of launches with at
     most one wave per SIMD run one node per workgroup (SXL_NODE_BLOCK=1 / 0
     forces it); each node's terms are evaluated alone in either form, so the
-    results are the same bit for bit."""
+    results are the same bit for bit.  wide300: the wide shape on 300 atoms,
+    whose wider blocks are the eight-node M0 forward and readout blocks of
+    large graphs."""
     from symmetrix_amd import synthetic
 
     if case == "all_options":
         path, model = _model(tmp_path, "medium3", zbl=True, density=("A0", "A1"), agnesi=True,
                              h1_basis="pre_linear_up", residual=True)
     else:
-        path, model = _model(tmp_path, case)
-    s = synthetic.water_box(num_molecules=45, seed=3) if case == "wide" else \
-        synthetic.srtio3_supercell(3, sigma=0.05, seed=3)
+        path, model = _model(tmp_path, "wide" if case == "wide300" else case)
+    if case.startswith("wide"):
+        s = synthetic.water_box(num_molecules=100 if case == "wide300" else 45, seed=3)
+    else:
+        s = synthetic.srtio3_supercell(3, sigma=0.05, seed=3)
     monkeypatch.setenv("SXL_NODE_BLOCK", "1")
     one = _evaluate(path, model, s)
     monkeypatch.setenv("SXL_NODE_BLOCK", "0")
